@@ -1,0 +1,162 @@
+// cyfa_abi.hip -- extern "C" entry points of libcyfa_hip.so (declared in
+// include/cyfa_abi.h). Validates arguments, maps them onto the kernel
+// parameter blocks and launches on the caller's stream. No device memory is
+// allocated here; the caller supplies every buffer, including the workspace.
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "cyfa_abi.h"
+#include "cyfa_internal.h"
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_error, sizeof(g_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(CYFA_ERR_LAUNCH, "%s: kernel launch failed: %s", what, hipGetErrorString(e));
+    return CYFA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cyfa_abi_version(void) { return CYFA_ABI_VERSION; }
+
+const char* cyfa_last_error(void) { return g_error; }
+
+size_t cyfa_chunk_workspace_bytes(int B, int T, int H, int K, int V, int M, int C) {
+    (void)M;
+    (void)C;
+    if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0) return 0;
+    return cyfa::workspace_layout(B, T, H, K, V).total;
+}
+
+int cyfa_readout_table(const float* readout, float* table, int H, int M, void* hip_stream) {
+    if (M != 128) return fail(CYFA_ERR_UNSUPPORTED, "cyfa_readout_table: num_slots must be 128, got %d", M);
+    if (H <= 0) return fail(CYFA_ERR_VALUE, "cyfa_readout_table: H must be positive, got %d", H);
+    if (!readout || !table) return fail(CYFA_ERR_VALUE, "cyfa_readout_table: null pointer");
+    cyfa::launch_readout_table(readout, table, H, (hipStream_t)hip_stream);
+    return check_launch("cyfa_readout_table");
+}
+
+int cyfa_decode_step(const CyfaDecodeArgs* a, void* hip_stream) {
+    if (!a) return fail(CYFA_ERR_VALUE, "cyfa_decode_step: null args");
+    if (a->M != 128) return fail(CYFA_ERR_UNSUPPORTED, "cyfa_decode_step: num_slots must be 128, got %d", a->M);
+    if (!((a->K == 128 || a->K == 256) && (a->V == 128 || a->V == 256)))
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_decode_step: head dims K=%d V=%d not in {128, 256}", a->K, a->V);
+    if (a->B <= 0 || a->H <= 0) return fail(CYFA_ERR_VALUE, "cyfa_decode_step: B=%d H=%d must be positive", a->B, a->H);
+    if (!a->q || !a->k || !a->v || !a->g || !a->delta || !a->beta || !a->table || !a->q_norm_weight ||
+        !a->k_norm_weight || !a->o || !a->hk_out || !a->hv_out || !a->clock_out)
+        return fail(CYFA_ERR_VALUE, "cyfa_decode_step: null required pointer");
+    const bool has_in = a->hk_in != nullptr;
+    if (has_in != (a->hv_in != nullptr) || has_in != (a->clock_in != nullptr))
+        return fail(CYFA_ERR_VALUE, "cyfa_decode_step: hk_in, hv_in and clock_in must be all set or all null");
+    if (!aligned(a->v, 8) || !aligned(a->table, 16) || !aligned(a->hk_out, 16) || !aligned(a->hv_out, 16) ||
+        (has_in && (!aligned(a->hk_in, 16) || !aligned(a->hv_in, 16))))
+        return fail(CYFA_ERR_ALIGN, "cyfa_decode_step: states/table need 16-byte and v 8-byte alignment");
+    cyfa::DecodeParams p;
+    p.B = a->B;
+    p.H = a->H;
+    p.q = (const __bf16*)a->q;
+    p.k = (const __bf16*)a->k;
+    p.v = (const __bf16*)a->v;
+    p.g = a->g;
+    p.delta = a->delta;
+    p.beta = a->beta;
+    p.table = a->table;
+    p.q_w = a->q_norm_weight;
+    p.k_w = a->k_norm_weight;
+    p.q_eps = a->q_norm_eps;
+    p.k_eps = a->k_norm_eps;
+    p.scale = a->scale;
+    p.hk_in = a->hk_in;
+    p.hv_in = a->hv_in;
+    p.clock_in = a->clock_in;
+    p.o = (__bf16*)a->o;
+    p.hk_out = a->hk_out;
+    p.hv_out = a->hv_out;
+    p.clock_out = a->clock_out;
+    if (cyfa::launch_decode_step(p, a->K, a->V, (hipStream_t)hip_stream) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_decode_step: no kernel for K=%d V=%d", a->K, a->V);
+    return check_launch("cyfa_decode_step");
+}
+
+int cyfa_chunk_fwd(const CyfaChunkArgs* a, void* hip_stream) {
+    if (!a) return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd: null args");
+    if (a->M != 128) return fail(CYFA_ERR_UNSUPPORTED, "cyfa_chunk_fwd: num_slots must be 128, got %d", a->M);
+    if (a->C != 64) return fail(CYFA_ERR_UNSUPPORTED, "cyfa_chunk_fwd: chunk_size must be 64, got %d", a->C);
+    if (a->K != 256 || a->V != 256)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_chunk_fwd: head dims K=%d V=%d, the prefill kernels need 256", a->K,
+                    a->V);
+    if (a->B <= 0 || a->T <= 0 || a->H <= 0)
+        return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd: B=%d T=%d H=%d must be positive", a->B, a->T, a->H);
+    if (!a->q || !a->k || !a->v || !a->g || !a->delta || !a->beta || !a->table || !a->q_norm_weight ||
+        !a->k_norm_weight || !a->o)
+        return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd: null required pointer");
+    const bool has_h0 = a->h0_k != nullptr;
+    if (has_h0 != (a->h0_v != nullptr) || has_h0 != (a->clock0 != nullptr))
+        return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd: h0_k, h0_v and clock0 must be all set or all null");
+    const bool has_out = a->hk != nullptr;
+    if (has_out != (a->hv != nullptr) || has_out != (a->clock != nullptr))
+        return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd: hk, hv and clock must be all set or all null");
+    if (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16) || !aligned(a->o, 16) ||
+        !aligned(a->q_norm_weight, 16) || !aligned(a->k_norm_weight, 16) ||
+        (has_h0 && (!aligned(a->h0_k, 16) || !aligned(a->h0_v, 16))))
+        return fail(CYFA_ERR_ALIGN, "cyfa_chunk_fwd: q/k/v/o, norm weights and states need 16-byte alignment");
+    const cyfa::WorkspaceLayout ws = cyfa::workspace_layout(a->B, a->T, a->H, a->K, a->V);
+    if (!a->workspace || a->workspace_bytes < ws.total)
+        return fail(CYFA_ERR_WORKSPACE, "cyfa_chunk_fwd: workspace of %zu bytes needed, got %zu", ws.total,
+                    a->workspace ? a->workspace_bytes : (size_t)0);
+    if (!aligned(a->workspace, 256)) return fail(CYFA_ERR_ALIGN, "cyfa_chunk_fwd: workspace needs 256-byte alignment");
+
+    cyfa::PrefillParams p;
+    p.B = a->B;
+    p.T = a->T;
+    p.H = a->H;
+    p.K = a->K;
+    p.V = a->V;
+    p.N = (a->T + 63) / 64;
+    p.Tp = p.N * 64;
+    cyfa::choose_segments(p.B * p.H, p.N, &p.P, &p.L);
+    p.q = (const __bf16*)a->q;
+    p.k = (const __bf16*)a->k;
+    p.v = (const __bf16*)a->v;
+    p.g = a->g;
+    p.delta = a->delta;
+    p.beta = a->beta;
+    p.table = a->table;
+    p.q_w = a->q_norm_weight;
+    p.k_w = a->k_norm_weight;
+    p.q_eps = a->q_norm_eps;
+    p.k_eps = a->k_norm_eps;
+    p.scale = a->scale;
+    p.h0_k = a->h0_k;
+    p.h0_v = a->h0_v;
+    p.clock0 = a->clock0;
+    p.o = (__bf16*)a->o;
+    p.hk = a->hk;
+    p.hv = a->hv;
+    p.clock = a->clock;
+    char* base = (char*)a->workspace;
+    p.lam = (float*)(base + ws.lam);
+    p.seg = (float*)(base + ws.seg);
+    p.seg_decay = (float*)(base + ws.seg_decay);
+    p.omega = (__bf16*)(base + ws.omega);
+    cyfa::launch_prefill(p, (hipStream_t)hip_stream);
+    return check_launch("cyfa_chunk_fwd");
+}
+
+}  // extern "C"

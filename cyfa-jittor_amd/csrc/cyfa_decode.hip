@@ -1,0 +1,254 @@
+// cyfa_decode.hip -- fused constant-memory CyFA decode step for gfx950.
+//
+// One 1024-thread workgroup per (batch, head). The step is HBM-bound: it
+// streams the fp32 key state hk [K, M] and value state hv [M, V] in and out
+// once (512 KiB per (b, h) for K = V = 256). Both states are issued as
+// coalesced float4 loads at kernel entry, so the value-state stream is in
+// flight while the key-state update, the query and the slot readout run.
+//
+// Math (ops/fused_recurrent.py:57-188): q_hat = bf16(q rs_q w_q) * scale,
+// k_hat = bf16(k rs_k w_k); lam = clock + delta; alpha = e^g;
+// w = bf16(beta U(-lam) b); hk' = alpha hk + k_hat (x) w; raw = hk'^T q_hat;
+// z = U(lam) raw; p = softmax(table z); u = table^T p; weights = U(-lam) u;
+// hv' = alpha hv + w (x) v; o = bf16(hv'^T weights).
+// The readout is evaluated in fp32 (the reference rounds z, the table and p
+// to bf16 here); the write vector and the normalised q/k keep the reference's
+// bf16 rounding so decode and the chunkwise prefill see identical operands.
+#include "cyfa_device.h"
+#include "cyfa_internal.h"
+
+namespace cyfa {
+
+template <int K, int V>
+__global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
+    constexpr int NT = 1024;
+    constexpr int KJ = K / 32;      // float4 of hk per thread (row has 32 float4)
+    constexpr int VQ = V / 4;       // float4 per hv row
+    constexpr int VROWS = NT / VQ;  // hv rows covered per sweep
+    constexpr int VJ = kSlots / VROWS;
+    constexpr int NW = NT / 64;
+    const int bh = blockIdx.x, h = bh % p.H, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+
+    __shared__ float s_q[K], s_k[K], s_w[kSlots], s_raw[kSlots], s_z[kSlots];
+    __shared__ float s_p[kSlots], s_om[kSlots], s_c[kPairs], s_s[kPairs];
+    __shared__ float s_part[NW][V > kSlots ? V : kSlots];
+    __shared__ float s_red[2][NW];
+
+    const bool has_state = p.hk_in != nullptr;
+    const float4* hk_in = reinterpret_cast<const float4*>(p.hk_in + (size_t)bh * K * kSlots);
+    const float4* hv_in = reinterpret_cast<const float4*>(p.hv_in + (size_t)bh * kSlots * V);
+    float4* hk_out = reinterpret_cast<float4*>(p.hk_out + (size_t)bh * K * kSlots);
+    float4* hv_out = reinterpret_cast<float4*>(p.hv_out + (size_t)bh * kSlots * V);
+
+    // Issue both state streams first; everything below overlaps with them.
+    float4 hk_r[KJ], hv_r[VJ];
+    if (has_state) {
+#pragma unroll
+        for (int j = 0; j < KJ; j++) hk_r[j] = hk_in[tid + NT * j];
+#pragma unroll
+        for (int j = 0; j < VJ; j++) hv_r[j] = hv_in[tid + NT * j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < KJ; j++) hk_r[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < VJ; j++) hv_r[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+
+    // q/k RMS statistics (ops/fused_recurrent.py:62-89).
+    float qv = 0.f, kv = 0.f;
+    if (tid < K) {
+        qv = (float)p.q[(size_t)bh * K + tid];
+        kv = (float)p.k[(size_t)bh * K + tid];
+    }
+    const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
+    if (lane == 0 && wave < K / 64) {
+        s_red[0][wave] = sq;
+        s_red[1][wave] = sk;
+    }
+    const float clock = has_state ? p.clock_in[bh] : 0.f;
+    const float lam = clock + p.delta[bh];
+    const float decay = expf(p.g[bh]);
+    const float beta = p.beta[bh];
+    if (tid < kPairs) {
+        float s, c;
+        phase_sincos(lam, tid, s, c);
+        const float a = beta * pair_scale(tid);
+        s_w[2 * tid] = bf16_round(a * c);
+        s_w[2 * tid + 1] = bf16_round(-a * s);
+        s_c[tid] = c;
+        s_s[tid] = s;
+    }
+    __syncthreads();
+    float tq = 0.f, tk = 0.f;
+#pragma unroll
+    for (int i = 0; i < K / 64; i++) {
+        tq += s_red[0][i];
+        tk += s_red[1][i];
+    }
+    if (tid < K) {
+        const float rq = rsqrtf(tq / K + p.q_eps), rk = rsqrtf(tk / K + p.k_eps);
+        s_q[tid] = bf16_round(qv * rq * p.q_w[tid]) * p.scale;
+        s_k[tid] = bf16_round(kv * rk * p.k_w[tid]);
+    }
+    __syncthreads();
+    if (tid == 0) p.clock_out[bh] = lam;  // after every thread has read clock_in
+
+    // Key state: hk' = alpha hk + k_hat (x) w ; raw = hk'^T q_hat.
+    {
+        const int m4 = (tid & 31) * 4;
+        const float w0 = s_w[m4], w1 = s_w[m4 + 1], w2 = s_w[m4 + 2], w3 = s_w[m4 + 3];
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+        for (int j = 0; j < KJ; j++) {
+            const int d = (tid >> 5) + 32 * j;
+            const float kd = s_k[d], qd = s_q[d];
+            float4 n = hk_r[j];
+            n.x = fmaf(n.x, decay, kd * w0);
+            n.y = fmaf(n.y, decay, kd * w1);
+            n.z = fmaf(n.z, decay, kd * w2);
+            n.w = fmaf(n.w, decay, kd * w3);
+            hk_out[tid + NT * j] = n;
+            a0 = fmaf(n.x, qd, a0);
+            a1 = fmaf(n.y, qd, a1);
+            a2 = fmaf(n.z, qd, a2);
+            a3 = fmaf(n.w, qd, a3);
+        }
+        a0 += __shfl_xor(a0, 32);
+        a1 += __shfl_xor(a1, 32);
+        a2 += __shfl_xor(a2, 32);
+        a3 += __shfl_xor(a3, 32);
+        if (lane < 32) {
+            s_part[wave][m4] = a0;
+            s_part[wave][m4 + 1] = a1;
+            s_part[wave][m4 + 2] = a2;
+            s_part[wave][m4 + 3] = a3;
+        }
+    }
+    __syncthreads();
+    if (tid < kSlots) {
+        float r = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) r += s_part[w][tid];
+        s_raw[tid] = r;
+    }
+    __syncthreads();
+
+    // Slot readout (ops/fused_recurrent.py:114-175), fp32.
+    if (tid < kPairs) {
+        const float c = s_c[tid], s = s_s[tid];
+        const float e = s_raw[2 * tid], o = s_raw[2 * tid + 1];
+        s_z[2 * tid] = c * e - s * o;
+        s_z[2 * tid + 1] = s * e + c * o;
+    }
+    __syncthreads();
+    const float* tb = p.table + (size_t)h * kActive * kSlots;
+    {
+        const int r = tid >> 3, part = tid & 7;
+        float lg = 0.f;
+        if (r < kActive) {
+            const float4* row = reinterpret_cast<const float4*>(tb + r * kSlots + part * 16);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 t = row[i];
+                const int m = part * 16 + 4 * i;
+                lg += t.x * s_z[m] + t.y * s_z[m + 1] + t.z * s_z[m + 2] + t.w * s_z[m + 3];
+            }
+        }
+        lg += __shfl_xor(lg, 1);
+        lg += __shfl_xor(lg, 2);
+        lg += __shfl_xor(lg, 4);
+        if (part == 0) s_p[r] = r < kActive ? lg : -INFINITY;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const float a = s_p[lane], b = s_p[lane + 64];
+        const float mx = wave_max(fmaxf(a, b));
+        const float ea = expf(a - mx);
+        const float eb = (lane + 64 < kActive) ? expf(b - mx) : 0.f;
+        const float inv = 1.f / wave_sum(ea + eb);
+        s_p[lane] = ea * inv;
+        s_p[lane + 64] = eb * inv;
+    }
+    __syncthreads();
+    {
+        const int m = tid & (kSlots - 1), part = tid >> 7;  // 8 parts of 16 slots
+        float u = 0.f;
+        const int r1 = part * 16 + 16 < kActive ? part * 16 + 16 : kActive;
+        for (int r = part * 16; r < r1; r++) u = fmaf(s_p[r], tb[r * kSlots + m], u);
+        s_part[part][m] = u;
+    }
+    __syncthreads();
+    if (tid < kPairs) {
+        float ue = 0.f, uo = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            ue += s_part[q][2 * tid];
+            uo += s_part[q][2 * tid + 1];
+        }
+        const float c = s_c[tid], s = s_s[tid];
+        s_om[2 * tid] = c * ue + s * uo;
+        s_om[2 * tid + 1] = -s * ue + c * uo;
+    }
+    __syncthreads();
+
+    // Value state: hv' = alpha hv + w (x) v ; o = hv'^T weights.
+    {
+        const int v4 = (tid % VQ) * 4, r0 = tid / VQ;
+        const bf16x4 vb = *reinterpret_cast<const bf16x4*>(p.v + (size_t)bh * V + v4);
+        const float v0 = (float)vb[0], v1 = (float)vb[1], v2 = (float)vb[2], v3 = (float)vb[3];
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+        for (int j = 0; j < VJ; j++) {
+            const int m = r0 + VROWS * j;
+            const float wm = s_w[m], om = s_om[m];
+            float4 n = hv_r[j];
+            n.x = fmaf(n.x, decay, wm * v0);
+            n.y = fmaf(n.y, decay, wm * v1);
+            n.z = fmaf(n.z, decay, wm * v2);
+            n.w = fmaf(n.w, decay, wm * v3);
+            hv_out[tid + NT * j] = n;
+            a0 = fmaf(n.x, om, a0);
+            a1 = fmaf(n.y, om, a1);
+            a2 = fmaf(n.z, om, a2);
+            a3 = fmaf(n.w, om, a3);
+        }
+        if (VQ == 32) {  // two rows of the sweep share a wave
+            a0 += __shfl_xor(a0, 32);
+            a1 += __shfl_xor(a1, 32);
+            a2 += __shfl_xor(a2, 32);
+            a3 += __shfl_xor(a3, 32);
+        }
+        __syncthreads();  // s_part reuse
+        if (VQ == 64 || lane < 32) {
+            s_part[wave][v4] = a0;
+            s_part[wave][v4 + 1] = a1;
+            s_part[wave][v4 + 2] = a2;
+            s_part[wave][v4 + 3] = a3;
+        }
+    }
+    __syncthreads();
+    if (tid < V) {
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) s += s_part[w][tid];
+        p.o[(size_t)bh * V + tid] = (bf16_t)s;
+    }
+}
+
+int launch_decode_step(const DecodeParams& p, int K, int V, hipStream_t stream) {
+    dim3 grid(p.B * p.H), block(1024);
+    if (K == 256 && V == 256)
+        hipLaunchKernelGGL((decode_step_kernel<256, 256>), grid, block, 0, stream, p);
+    else if (K == 128 && V == 128)
+        hipLaunchKernelGGL((decode_step_kernel<128, 128>), grid, block, 0, stream, p);
+    else if (K == 256 && V == 128)
+        hipLaunchKernelGGL((decode_step_kernel<256, 128>), grid, block, 0, stream, p);
+    else if (K == 128 && V == 256)
+        hipLaunchKernelGGL((decode_step_kernel<128, 256>), grid, block, 0, stream, p);
+    else
+        return -1;
+    return 0;
+}
+
+}  // namespace cyfa

@@ -1,0 +1,105 @@
+// cyfa_device.h -- device-side helpers shared by the CyFA gfx950 kernels.
+//
+// Vector types for the CDNA4 MFMA builtins, bf16/fp16 conversions (hardware
+// round-to-nearest-even conversions on gfx950), the integer range-reduced
+// clock phase and wavefront reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cyfa {
+
+constexpr int kSlots = 128;   // stored slot coordinates M
+constexpr int kActive = 127;  // active slots R = M - 1
+constexpr int kPairs = 64;    // Fourier pairs M / 2
+constexpr int kChunk = 64;    // tokens per chunk
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float bf16_round(float x) { return (float)(bf16_t)x; }
+
+// Load 8 consecutive bf16 (16 bytes, 16-byte aligned) and widen to fp32.
+__device__ __forceinline__ void load_bf16x8(const bf16_t* p, float out[8]) {
+    bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+    for (int i = 0; i < 8; i++) out[i] = (float)v[i];
+}
+
+// Clock phase of Fourier pair `pair` at clock lam, with the integer range
+// reduction of the reference (ops/utils.py:649-661):
+//   wi = floor(lam) mod R (non-negative); coord = ((wi * pair) mod R) + frac(lam) * pair,
+//   wrapped into (-R/2, R/2]; theta = coord * 2 pi / R.
+// The integer part keeps |theta| <= pi exact for any clock value, so the phase
+// stays accurate when lam grows to 1e4 and beyond.
+__device__ __forceinline__ float clock_phase(float lam, int pair) {
+    const float whole = floorf(lam);
+    const float frac = lam - whole;
+    int wi = (int)whole % kActive;
+    if (wi < 0) wi += kActive;
+    float coord = (float)((wi * pair) % kActive) + frac * (float)pair;
+    if (coord > 0.5f * kActive) coord -= (float)kActive;
+    return coord * 0.049473900056532176f;  // 2 pi / 127
+}
+
+// The same reduced phase in revolutions (coord / R, in (-1/2, 1/2]) evaluated
+// with the hardware sine/cosine (v_sin_f32 / v_cos_f32 take revolutions).
+// The argument is already reduced exactly, so no further range reduction is
+// needed.
+__device__ __forceinline__ void phase_sincos(float lam, int pair, float& s, float& c) {
+    const float whole = floorf(lam);
+    const float frac = lam - whole;
+    int wi = (int)whole % kActive;
+    if (wi < 0) wi += kActive;
+    float coord = (float)((wi * pair) % kActive) + frac * (float)pair;
+    if (coord > 0.5f * kActive) coord -= (float)kActive;
+    const float rev = coord * (1.0f / kActive);
+    s = __builtin_amdgcn_sinf(rev);
+    c = __builtin_amdgcn_cosf(rev);
+}
+
+__device__ __forceinline__ f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mfma_f16(const f16x8& a, const f16x8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// s_p of the real-DFT basis: (1/R)^1/2 for pair 0, (2/R)^1/2 otherwise.
+__device__ __forceinline__ float pair_scale(int pair) {
+    return pair == 0 ? 0.088735650941611332f : 0.12549115289319523f;
+}
+
+// Write-vector pair (w[2p], w[2p+1]) = beta s_p (cos theta_p, -sin theta_p)
+// (ops/utils.py:664-702), before rounding.
+__device__ __forceinline__ void write_pair(float lam, float beta, int pair, float& we, float& wo) {
+    float s, c;
+    phase_sincos(lam, pair, s, c);
+    const float a = beta * pair_scale(pair);
+    we = a * c;
+    wo = -a * s;
+}
+
+template <int W = 64>
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) x += __shfl_xor(x, o, W);
+    return x;
+}
+
+template <int W = 64>
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, W));
+    return x;
+}
+
+}  // namespace cyfa

@@ -1,0 +1,53 @@
+// cyfa_internal.h -- kernel parameter blocks and launchers shared between the
+// C-ABI layer (cyfa_abi.hip) and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+namespace cyfa {
+
+struct DecodeParams {
+    int B, H;
+    const __bf16 *q, *k, *v;
+    const float *g, *delta, *beta, *table, *q_w, *k_w;
+    float q_eps, k_eps, scale;
+    const float *hk_in, *hv_in, *clock_in;
+    __bf16* o;
+    float *hk_out, *hv_out, *clock_out;
+};
+
+// Prefill: T is split into N = ceil(T / 64) chunks and every (batch, head)
+// sequence into P segments of L consecutive chunks. Segments run in parallel;
+// their start states come from an affine carry over segment-local states.
+struct PrefillParams {
+    int B, T, H, K, V;
+    int N, Tp;  // chunks, padded length N * 64
+    int P, L;   // segments per sequence, chunks per segment
+    const __bf16 *q, *k, *v;
+    const float *g, *delta, *beta;
+    const float* table;  // f32 [H, 127, 128]
+    const float *q_w, *k_w;
+    float q_eps, k_eps, scale;
+    const float *h0_k, *h0_v, *clock0;
+    __bf16* o;
+    float *hk, *hv, *clock;
+    // workspace
+    float* lam;        // [B*H, Tp] clock per token
+    float* seg;        // [B*H, P, K*128 + 128*V] segment-local states, then segment start states
+    float* seg_decay;  // [B*H, P] product of alpha over each segment
+    __bf16* omega;     // [B*H, Tp, 128] slot weights between the two passes
+};
+
+struct WorkspaceLayout {
+    size_t lam, seg, seg_decay, omega, total;
+};
+
+void choose_segments(int BH, int N, int* P, int* L);
+WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V);
+
+int launch_decode_step(const DecodeParams& p, int K, int V, hipStream_t stream);
+int launch_prefill(const PrefillParams& p, hipStream_t stream);
+int launch_readout_table(const float* readout, float* table, int H, hipStream_t stream);
+
+}  // namespace cyfa

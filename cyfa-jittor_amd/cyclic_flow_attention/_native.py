@@ -1,0 +1,149 @@
+"""ctypes binding of libcyfa_hip.so (C ABI declared in include/cyfa_abi.h).
+
+PyTorch-ROCm tensors are the only device container: callers pass tensors,
+this module passes their data pointers and the current HIP stream to the
+library. There is no fallback: if the library is missing, or no GPU is
+visible, every entry point raises.
+"""
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(os.environ.get("CYFA_LIB", Path(__file__).with_name("libcyfa_hip.so")))
+ABI_VERSION = 1
+
+CYFA_OK = 0
+CYFA_ERR_VALUE = -1
+CYFA_ERR_UNSUPPORTED = -2
+CYFA_ERR_ALIGN = -3
+CYFA_ERR_WORKSPACE = -4
+CYFA_ERR_LAUNCH = -5
+
+_c_int, _c_float, _c_void_p, _c_size_t = ctypes.c_int, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
+
+
+class CyfaChunkArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", _c_int), ("T", _c_int), ("H", _c_int), ("K", _c_int), ("V", _c_int), ("M", _c_int), ("C", _c_int),
+        ("q", _c_void_p), ("k", _c_void_p), ("v", _c_void_p),
+        ("g", _c_void_p), ("delta", _c_void_p), ("beta", _c_void_p),
+        ("table", _c_void_p), ("q_norm_weight", _c_void_p), ("k_norm_weight", _c_void_p),
+        ("q_norm_eps", _c_float), ("k_norm_eps", _c_float), ("scale", _c_float),
+        ("h0_k", _c_void_p), ("h0_v", _c_void_p), ("clock0", _c_void_p),
+        ("o", _c_void_p), ("hk", _c_void_p), ("hv", _c_void_p), ("clock", _c_void_p),
+        ("workspace", _c_void_p), ("workspace_bytes", _c_size_t),
+    ]
+
+
+class CyfaDecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", _c_int), ("H", _c_int), ("K", _c_int), ("V", _c_int), ("M", _c_int),
+        ("q", _c_void_p), ("k", _c_void_p), ("v", _c_void_p),
+        ("g", _c_void_p), ("delta", _c_void_p), ("beta", _c_void_p),
+        ("table", _c_void_p), ("q_norm_weight", _c_void_p), ("k_norm_weight", _c_void_p),
+        ("q_norm_eps", _c_float), ("k_norm_eps", _c_float), ("scale", _c_float),
+        ("hk_in", _c_void_p), ("hv_in", _c_void_p), ("clock_in", _c_void_p),
+        ("o", _c_void_p), ("hk_out", _c_void_p), ("hv_out", _c_void_p), ("clock_out", _c_void_p),
+    ]
+
+
+# Every symbol include/cyfa_abi.h declares, with its ctypes signature.
+SIGNATURES = {
+    "cyfa_chunk_fwd": (_c_int, [ctypes.POINTER(CyfaChunkArgs), _c_void_p]),
+    "cyfa_chunk_workspace_bytes": (_c_size_t, [_c_int] * 7),
+    "cyfa_decode_step": (_c_int, [ctypes.POINTER(CyfaDecodeArgs), _c_void_p]),
+    "cyfa_readout_table": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "cyfa_last_error": (ctypes.c_char_p, []),
+    "cyfa_abi_version": (_c_int, []),
+}
+
+_lib = None
+
+
+def load_library(path=None):
+    """Load and type the shared library (no GPU needed). Raises if missing."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(
+            f"CyFA HIP library not found at {p}; build it with `python cyfa-jittor_amd/build_native.py`"
+        )
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    version = lib.cyfa_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"{p} has ABI version {version}, expected {ABI_VERSION}; rebuild it")
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _raise(code, what):
+    msg = load_library().cyfa_last_error().decode(errors="replace") or what
+    if code == CYFA_ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    if code in (CYFA_ERR_VALUE, CYFA_ERR_ALIGN, CYFA_ERR_WORKSPACE):
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def ptr(t):
+    """Device pointer of a tensor, or None (NULL) for None."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_device(*tensors):
+    """All tensors must live on one HIP device; returns it."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError("CyFA HIP ops need tensors on a GPU device (got %s)" % t.device)
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError("CyFA HIP ops need all tensors on one device")
+    if dev is None:
+        raise ValueError("no device tensor given")
+    return dev
+
+
+def chunk_workspace_bytes(B, T, H, K, V, M=128, C=64):
+    return int(load_library().cyfa_chunk_workspace_bytes(B, T, H, K, V, M, C))
+
+
+def chunk_fwd(args: CyfaChunkArgs, device):
+    rc = load_library().cyfa_chunk_fwd(ctypes.byref(args), stream_handle(device))
+    if rc != CYFA_OK:
+        _raise(rc, "cyfa_chunk_fwd failed")
+
+
+def decode_step(args: CyfaDecodeArgs, device):
+    rc = load_library().cyfa_decode_step(ctypes.byref(args), stream_handle(device))
+    if rc != CYFA_OK:
+        _raise(rc, "cyfa_decode_step failed")
+
+
+def readout_table(readout: torch.Tensor) -> torch.Tensor:
+    """table = readout @ Phi on the GPU: readout f32 [H, R, R] -> [H, R, R+1]."""
+    dev = require_device(readout)
+    H, R = readout.shape[0], readout.shape[-1]
+    src = readout.detach().to(torch.float32).contiguous()
+    table = torch.empty(H, R, R + 1, dtype=torch.float32, device=dev)
+    rc = load_library().cyfa_readout_table(ptr(src), ptr(table), H, R + 1, stream_handle(dev))
+    if rc != CYFA_OK:
+        _raise(rc, "cyfa_readout_table failed")
+    return table

@@ -1,0 +1,127 @@
+"""CyFA decoder blocks and causal language model (PyTorch host code).
+
+Mirrors models/cyfa/modeling_cyfa.py:13-133 of Chyxx/CyFA-Jittor v0.1.2:
+pre-norm attention + SwiGLU MLP blocks, torch-checkpoint-compatible parameter
+names, and the bf16 precision policy of ``to_bfloat16``.
+"""
+
+import math
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from ...layers.cyfa import CyclicFlowAttention, RMSNorm
+
+
+def mlp_width(config):
+    return config.intermediate_size or 256 * math.ceil(int(config.hidden_size * config.hidden_ratio * 2 / 3) / 256)
+
+
+class GatedMLP(nn.Module):
+    def __init__(self, config):
+        super().__init__()
+        mid = mlp_width(config)
+        self.gate_proj = nn.Linear(config.hidden_size, mid, bias=False)
+        self.up_proj = nn.Linear(config.hidden_size, mid, bias=False)
+        self.down_proj = nn.Linear(mid, config.hidden_size, bias=False)
+
+    def forward(self, x):
+        g = self.gate_proj(x)
+        u = self.up_proj(x)
+        return self.down_proj((F.silu(g.float()) * u.float()).to(x.dtype))
+
+
+class CyFABlock(nn.Module):
+    def __init__(self, config):
+        super().__init__()
+        self.attn_norm = RMSNorm(config.hidden_size, config.norm_eps)
+        self.attn = CyclicFlowAttention(
+            hidden_size=config.hidden_size,
+            num_heads=config.num_heads,
+            head_dim=config.head_dim,
+            expand_k=config.expand_k,
+            expand_v=config.expand_v,
+            num_slots=config.num_slots,
+            use_short_conv=config.use_short_conv,
+            conv_size=config.conv_size,
+            conv_bias=config.conv_bias,
+            norm_eps=config.norm_eps,
+            chunk_size=config.chunk_size,
+        )
+        self.mlp_norm = RMSNorm(config.hidden_size, config.norm_eps)
+        self.mlp = GatedMLP(config)
+
+    def forward(self, x, cache=None, use_cache=False, attention_mask=None):
+        y, cache = self.attn(self.attn_norm(x), cache, use_cache, attention_mask)
+        residual = x + y
+        return residual + self.mlp(self.mlp_norm(residual)), cache
+
+
+class CyclicFlowAttentionModel(nn.Module):
+    def __init__(self, config):
+        super().__init__()
+        self.embeddings = nn.Embedding(config.vocab_size, config.hidden_size)
+        self.layers = nn.ModuleList([CyFABlock(config) for _ in range(config.num_hidden_layers)])
+        self.norm = RMSNorm(config.hidden_size, config.norm_eps)
+
+    def forward(self, input_ids, cache=None, use_cache=False, attention_mask=None):
+        x = self.embeddings(input_ids)
+        new = []
+        for i, layer in enumerate(self.layers):
+            x, s = layer(x, None if cache is None else cache[i], use_cache, attention_mask)
+            new.append(s)
+        return self.norm(x), (new if use_cache else None)
+
+
+# Parameters that stay fp32 under to_bfloat16 (modeling_cyfa.py:110-116).
+FP32_PARAMETERS = ("norm.weight", "readout", "A_log", "dt_bias")
+
+
+class CyclicFlowAttentionForCausalLM(nn.Module):
+    """CyFA causal language model with Torch-checkpoint-compatible parameter names."""
+
+    def __init__(self, config):
+        super().__init__()
+        self.config = config
+        self.model = CyclicFlowAttentionModel(config)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        if config.tie_word_embeddings:
+            self.lm_head.weight = self.model.embeddings.weight
+
+    def forward(self, input_ids, labels=None, cache=None, use_cache=False, attention_mask=None):
+        hidden, cache = self.model(input_ids, cache, use_cache, attention_mask)
+        logits = self.lm_head(hidden)
+        loss = None
+        if labels is not None:
+            loss = F.cross_entropy(
+                logits[:, :-1].float().reshape(-1, self.config.vocab_size),
+                labels[:, 1:].reshape(-1),
+                ignore_index=-100,
+            )
+        return {"logits": logits, "loss": loss, "cache": cache}
+
+    def to_bfloat16(self):
+        for name, p in self.named_parameters():
+            if not any(s in name for s in FP32_PARAMETERS):
+                p.data = p.data.to(torch.bfloat16)
+        return self
+
+    @torch.no_grad()
+    def generate(self, input_ids, max_new_tokens=32, eos_token_id=None):
+        """Greedy decoding with the constant-size state (modeling_cyfa.py:142-158).
+
+        The argmax stays on the device; tokens are copied to the host once at
+        the end (the reference synchronises every step)."""
+        self.eval()
+        tokens = [input_ids]
+        cache = None
+        current = input_ids
+        for _ in range(max_new_tokens):
+            result = self(current, cache=cache, use_cache=True)
+            cache = result["cache"]
+            current = result["logits"][:, -1:].argmax(-1)
+            tokens.append(current)
+            if eos_token_id is not None and bool((current == eos_token_id).all()):
+                break
+        return torch.cat(tokens, dim=1)

@@ -1,0 +1,93 @@
+"""Chunkwise CyFA prefill on the gfx950 HIP path.
+
+Keeps the reference's signature, argument meaning and error behaviour
+(ops/chunk.py:164-353 of Chyxx/CyFA-Jittor v0.1.2); the whole computation --
+q/k RMS norm, clock scan, write vector, both ScalarGatedLA passes, the fused
+slot readout and the final states -- runs inside ``cyfa_chunk_fwd`` of
+libcyfa_hip.so. Forward only: the reference's autograd adjoints are out of
+scope here, so gradients raise.
+"""
+
+import torch
+
+from .. import _native
+from .utils import check_forward_only, readout_table
+
+
+def chunk_cyfa(
+    q,
+    k,
+    v,
+    g,
+    delta,
+    beta,
+    readout,
+    q_norm_weight,
+    k_norm_weight,
+    q_norm_eps=1e-6,
+    k_norm_eps=1e-6,
+    scale=None,
+    initial_state=None,
+    output_final_state=False,
+    cu_seqlens=None,
+    checkpoint_level=0,
+    chunk_size=64,
+):
+    """Chunkwise Cyclic Flow Attention.
+
+    Inputs q, k and v use [batch, time, heads, channels]; g, delta and beta use
+    [batch, time, heads]. The readout has [heads, slots-1, slots-1]. Returns
+    the output (bf16, [batch, time, heads, V]) and, when requested,
+    (key_state [B,H,K,M], value_state [B,H,M,V], clock [B,H]), all fp32.
+    """
+    if cu_seqlens is not None:
+        raise NotImplementedError("packed layout requires native segment dispatch")
+    if checkpoint_level != 0:
+        raise NotImplementedError("only saved-activation training is implemented")
+    state_in = tuple(initial_state) if initial_state is not None else ()
+    check_forward_only("chunk_cyfa", (q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight) + state_in)
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    M = readout.shape[-1] + 1
+    if tuple(k.shape) != (B, T, H, K) or tuple(v.shape[:3]) != (B, T, H):
+        raise ValueError(f"q/k/v shapes disagree: {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
+    for name, x in (("g", g), ("delta", delta), ("beta", beta)):
+        if tuple(x.shape) != (B, T, H):
+            raise ValueError(f"{name} must have shape {(B, T, H)}, got {tuple(x.shape)}")
+    for name, x in (("q", q), ("k", k), ("v", v)):
+        if x.dtype != torch.bfloat16:
+            raise NotImplementedError(f"the HIP prefill computes in bfloat16; {name} is {x.dtype}")
+    dev = _native.require_device(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, *state_in)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    g, delta, beta = (x.to(torch.float32).contiguous() for x in (g, delta, beta))
+    qw = q_norm_weight.to(torch.float32).contiguous()
+    kw = k_norm_weight.to(torch.float32).contiguous()
+    table = readout_table(readout)
+    if initial_state is not None:
+        h0k, h0v, c0 = (x.to(torch.float32).contiguous() for x in initial_state)
+        if tuple(h0k.shape) != (B, H, K, M) or tuple(h0v.shape) != (B, H, M, V) or tuple(c0.shape) != (B, H):
+            raise ValueError("initial_state must be (hk [B,H,K,M], hv [B,H,M,V], clock [B,H])")
+    else:
+        h0k = h0v = c0 = None
+    o = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=dev)
+    if output_final_state:
+        hk = torch.empty(B, H, K, M, dtype=torch.float32, device=dev)
+        hv = torch.empty(B, H, M, V, dtype=torch.float32, device=dev)
+        clock = torch.empty(B, H, dtype=torch.float32, device=dev)
+    else:
+        hk = hv = clock = None
+    ws_bytes = _native.chunk_workspace_bytes(B, T, H, K, V, M, chunk_size)
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    args = _native.CyfaChunkArgs(
+        B=B, T=T, H=H, K=K, V=V, M=M, C=chunk_size,
+        q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(),
+        g=g.data_ptr(), delta=delta.data_ptr(), beta=beta.data_ptr(),
+        table=table.data_ptr(), q_norm_weight=qw.data_ptr(), k_norm_weight=kw.data_ptr(),
+        q_norm_eps=float(q_norm_eps), k_norm_eps=float(k_norm_eps),
+        scale=float(K**-0.5 if scale is None else scale),
+        h0_k=_native.ptr(h0k), h0_v=_native.ptr(h0v), clock0=_native.ptr(c0),
+        o=o.data_ptr(), hk=_native.ptr(hk), hv=_native.ptr(hv), clock=_native.ptr(clock),
+        workspace=workspace.data_ptr(), workspace_bytes=ws_bytes,
+    )
+    _native.chunk_fwd(args, dev)
+    return o, ((hk, hv, clock) if output_final_state else None)

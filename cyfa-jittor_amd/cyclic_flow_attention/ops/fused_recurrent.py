@@ -1,0 +1,95 @@
+"""Constant-state autoregressive CyFA decoding on the gfx950 HIP path.
+
+Keeps the reference's signature, checks and return convention
+(ops/fused_recurrent.py:10-200 of Chyxx/CyFA-Jittor v0.1.2). One call runs one
+fused HBM-streaming kernel, ``cyfa_decode_step`` of libcyfa_hip.so.
+"""
+
+import torch
+
+from .. import _native
+from .utils import readout_table
+
+
+def fused_recurrent_cyfa(
+    q,
+    k,
+    v,
+    g,
+    delta,
+    beta,
+    readout,
+    q_norm_weight,
+    k_norm_weight,
+    q_norm_eps=1e-6,
+    k_norm_eps=1e-6,
+    scale=None,
+    initial_state=None,
+    output_final_state=False,
+    cu_seqlens=None,
+    *,
+    table=None,
+    inplace=False,
+):
+    """Decode one token using constant-size key, value and clock states.
+
+    Uses the same input layout and return convention as chunk_cyfa. The new
+    states are returned as new tensors; ``inplace=True`` (an extension) updates
+    the given initial_state tensors instead and returns them. ``table`` (an
+    extension) passes a precomputed readout @ Phi to skip rebuilding it.
+    """
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    M = readout.shape[-1] + 1
+    tracked = (q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight)
+    if initial_state is not None:
+        tracked = tracked + tuple(initial_state)
+    if torch.is_grad_enabled() and any(isinstance(x, torch.Tensor) and x.requires_grad for x in tracked):
+        raise ValueError(
+            "fused_recurrent_cyfa is inference-only; use torch.no_grad() or chunk_cyfa for gradients"
+        )
+    if T != 1 or cu_seqlens is not None:
+        raise NotImplementedError("native fused decode currently needs dense T=1")
+    if M > 256 or K > 1024 or V > 1024:
+        raise ValueError("decode shape exceeds block limits")
+    for name, x in (("q", q), ("k", k), ("v", v)):
+        if x.dtype != torch.bfloat16:
+            raise NotImplementedError(f"the HIP decode step computes in bfloat16; {name} is {x.dtype}")
+    dev = _native.require_device(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    g, delta, beta = (x.to(torch.float32).contiguous() for x in (g, delta, beta))
+    qw = q_norm_weight.to(torch.float32).contiguous()
+    kw = k_norm_weight.to(torch.float32).contiguous()
+    if table is None:
+        table = readout_table(readout)
+    if initial_state is not None:
+        hk_in, hv_in, c_in = initial_state
+        if tuple(hk_in.shape) != (B, H, K, M) or tuple(hv_in.shape) != (B, H, M, V) or tuple(c_in.shape) != (B, H):
+            raise ValueError("initial_state must be (hk [B,H,K,M], hv [B,H,M,V], clock [B,H])")
+        if inplace:
+            for x in (hk_in, hv_in, c_in):
+                if x.dtype != torch.float32 or not x.is_contiguous():
+                    raise ValueError("inplace decode needs contiguous fp32 state tensors")
+        else:
+            hk_in, hv_in, c_in = (x.to(torch.float32).contiguous() for x in (hk_in, hv_in, c_in))
+    else:
+        hk_in = hv_in = c_in = None
+    if inplace and initial_state is not None:
+        hk_out, hv_out, c_out = hk_in, hv_in, c_in
+    else:
+        hk_out = torch.empty(B, H, K, M, dtype=torch.float32, device=dev)
+        hv_out = torch.empty(B, H, M, V, dtype=torch.float32, device=dev)
+        c_out = torch.empty(B, H, dtype=torch.float32, device=dev)
+    o = torch.empty(B, 1, H, V, dtype=torch.bfloat16, device=dev)
+    args = _native.CyfaDecodeArgs(
+        B=B, H=H, K=K, V=V, M=M,
+        q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(),
+        g=g.data_ptr(), delta=delta.data_ptr(), beta=beta.data_ptr(),
+        table=table.data_ptr(), q_norm_weight=qw.data_ptr(), k_norm_weight=kw.data_ptr(),
+        q_norm_eps=float(q_norm_eps), k_norm_eps=float(k_norm_eps),
+        scale=float(K**-0.5 if scale is None else scale),
+        hk_in=_native.ptr(hk_in), hv_in=_native.ptr(hv_in), clock_in=_native.ptr(c_in),
+        o=o.data_ptr(), hk_out=hk_out.data_ptr(), hv_out=hv_out.data_ptr(), clock_out=c_out.data_ptr(),
+    )
+    _native.decode_step(args, dev)
+    return o, ((hk_out, hv_out, c_out) if output_final_state else None)

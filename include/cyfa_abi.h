@@ -1,0 +1,114 @@
+/*
+ * cyfa_abi.h -- C ABI of the MI355X (gfx950) CyFA attention hot path.
+ *
+ * One shared library (libcyfa_hip.so) exports these entry points. Callers pass
+ * plain device pointers and sizes; the library never allocates device memory
+ * on the hot path and enqueues all work on the caller's HIP stream. Return 0 on
+ * success or a negative CYFA_ERR_* code; cyfa_last_error() returns a
+ * thread-local message for the last failing call on the calling thread.
+ *
+ * Each entry point names the reference interface it replaces (paths relative
+ * to the Chyxx/CyFA-Jittor v0.1.2 tree). In the reference those interfaces are
+ * Python functions that emit inline CUDA through Jittor's jt.code operator;
+ * here the Python host code (cyclic_flow_attention/ops/chunk.py and
+ * ops/fused_recurrent.py) binds these
+ * symbols with ctypes.
+ *
+ * Tensor layouts (row-major, contiguous):
+ *   q, k   bf16 [B, T, H, K]        v, o    bf16 [B, T, H, V]
+ *   g, delta, beta  f32 [B, T, H]   (g = natural log of the decay alpha)
+ *   table  f32 [H, M-1, M]          (readout @ Phi, see cyfa_readout_table)
+ *   hk     f32 [B, H, K, M]         hv      f32 [B, H, M, V]   clock f32 [B, H]
+ */
+#ifndef CYFA_ABI_H
+#define CYFA_ABI_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CYFA_ABI_VERSION 1
+
+enum {
+    CYFA_OK = 0,
+    CYFA_ERR_VALUE = -1,       /* bad shape / argument     -> Python ValueError */
+    CYFA_ERR_UNSUPPORTED = -2, /* valid but not implemented -> NotImplementedError */
+    CYFA_ERR_ALIGN = -3,       /* pointer misaligned        -> ValueError */
+    CYFA_ERR_WORKSPACE = -4,   /* workspace missing / small -> ValueError */
+    CYFA_ERR_LAUNCH = -5       /* HIP launch failure        -> RuntimeError */
+};
+
+/* Arguments of one chunkwise prefill call. Nullable pointers are marked. */
+typedef struct CyfaChunkArgs {
+    int B, T, H, K, V, M, C;      /* M = num_slots (128); C = chunk size (64) */
+    const void *q, *k, *v;        /* bf16, see layouts above */
+    const float *g, *delta, *beta;
+    const float *table;           /* f32 [H, M-1, M] */
+    const float *q_norm_weight;   /* f32 [K] */
+    const float *k_norm_weight;   /* f32 [K] */
+    float q_norm_eps, k_norm_eps;
+    float scale;                  /* pass-1 scale; the reference default is K^-1/2 */
+    const float *h0_k;            /* nullable: initial key state   [B,H,K,M] */
+    const float *h0_v;            /* nullable: initial value state [B,H,M,V] */
+    const float *clock0;          /* nullable: initial clock       [B,H] */
+    void *o;                      /* bf16 output [B,T,H,V] */
+    float *hk, *hv, *clock;       /* nullable: final states (all three or none) */
+    void *workspace;              /* device scratch, >= cyfa_chunk_workspace_bytes() */
+    size_t workspace_bytes;
+} CyfaChunkArgs;
+
+/* Chunkwise two-pass CyFA forward: clock scan, write vector, pass-1
+ * ScalarGatedLA with the fused slot-softmax readout, pass-2 ScalarGatedLA and
+ * the final states. Replaces chunk_cyfa (ops/chunk.py:164-353) together with
+ * the kernels it launches: clock_cumsum / clock_total (ops/utils.py:229-348),
+ * phase_write (ops/utils.py:543-766), head_rmsnorm / query_rms_stats
+ * (ops/qk_norm.py:64-297), head_gates / head_layout (ops/utils.py:351-492),
+ * local_log2_cumsum (ops/utils.py:495-520), state_forward
+ * (ops/chunk_h.py:10-339), first_readout (ops/chunk_readout.py:624-1136) and
+ * output_forward (ops/chunk_o.py:10-613). Zero padding of T to a multiple of
+ * C (ops/chunk.py:198-207) is handled inside the kernels. */
+int cyfa_chunk_fwd(const CyfaChunkArgs *args, void *hip_stream);
+
+/* Workspace bytes cyfa_chunk_fwd needs for these dimensions (the reference
+ * allocates the equivalent intermediates through Jittor, ops/chunk.py:244-336). */
+size_t cyfa_chunk_workspace_bytes(int B, int T, int H, int K, int V, int M, int C);
+
+/* Arguments of one decode step (T == 1). */
+typedef struct CyfaDecodeArgs {
+    int B, H, K, V, M;
+    const void *q, *k, *v;        /* bf16 [B,1,H,K|V] */
+    const float *g, *delta, *beta;/* f32 [B,1,H] */
+    const float *table;           /* f32 [H, M-1, M] */
+    const float *q_norm_weight, *k_norm_weight;
+    float q_norm_eps, k_norm_eps, scale;
+    const float *hk_in, *hv_in, *clock_in; /* nullable (all or none): zero state */
+    void *o;                      /* bf16 [B,1,H,V] */
+    float *hk_out, *hv_out, *clock_out;    /* required; may alias the inputs */
+} CyfaDecodeArgs;
+
+/* One fused constant-memory decode step: q/k RMS norm, clock and write
+ * vector, key-state update and query, slot readout, value-state update and
+ * output, in one HBM-streaming kernel. Replaces fused_recurrent_cyfa and its
+ * decode kernel (ops/fused_recurrent.py:10-200). Updating in place
+ * (hk_out == hk_in, ...) is allowed. */
+int cyfa_decode_step(const CyfaDecodeArgs *args, void *hip_stream);
+
+/* table[h] = readout[h] @ Phi, with Phi the real-DFT slot basis [M-1, M].
+ * Replaces _basis + jt.matmul (ops/chunk.py:82-103, 281;
+ * ops/fused_recurrent.py:53). readout f32 [H, M-1, M-1]; table f32 [H, M-1, M]. */
+int cyfa_readout_table(const float *readout, float *table, int H, int M, void *hip_stream);
+
+/* Thread-local message of the last failing call (never NULL). No reference
+ * counterpart: Jittor reports kernel errors as C++ exceptions. */
+const char *cyfa_last_error(void);
+
+/* CYFA_ABI_VERSION of the loaded library. No reference counterpart. */
+int cyfa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CYFA_ABI_H */

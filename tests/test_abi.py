@@ -1,0 +1,93 @@
+"""The C-ABI library loads, exports every symbol include/cyfa_abi.h declares,
+and its ctypes mirror has the C struct layout. No GPU compute is issued: only
+host-side entry points (version, workspace size, argument validation that
+fails before any HIP call) are called."""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+import torch
+
+from cyclic_flow_attention import _native
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "cyfa_abi.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:const\s+)?\w+\s*\*?\s*(cyfa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.load_library()
+    names = declared_functions()
+    assert set(names) == set(_native.SIGNATURES), names
+    for name in names:
+        assert hasattr(lib, name), name
+    assert lib.cyfa_abi_version() == _native.ABI_VERSION
+
+
+def _c_layout(tmp_path, struct, fields):
+    src = tmp_path / "layout.c"
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "cyfa_abi.h"', "int main(void) {",
+             f'printf("%zu\\n", sizeof({struct}));']
+    lines += [f'printf("%zu\\n", offsetof({struct}, {f}));' for f in fields]
+    lines += ["return 0; }"]
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    return [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+
+
+@pytest.mark.parametrize("cls,name", [(_native.CyfaChunkArgs, "CyfaChunkArgs"),
+                                      (_native.CyfaDecodeArgs, "CyfaDecodeArgs")])
+def test_struct_layout_matches_header(tmp_path, cls, name):
+    fields = [f for f, _ in cls._fields_]
+    got = [ctypes.sizeof(cls)] + [getattr(cls, f).offset for f in fields]
+    assert got == _c_layout(tmp_path, name, fields)
+
+
+def test_workspace_size_is_host_side():
+    n = _native.chunk_workspace_bytes(8, 2048, 4, 256, 256)
+    # clock [B*H*T] f32 + segment states + slot weights [B*H*T*128] bf16, at least
+    assert n >= 8 * 4 * 2048 * (4 + 256)
+    assert _native.chunk_workspace_bytes(1, 1, 1, 256, 256) > 0
+
+
+def test_unsupported_shapes_fail_before_launch():
+    lib = _native.load_library()
+    args = _native.CyfaChunkArgs(B=1, T=64, H=1, K=256, V=256, M=64, C=64)
+    assert lib.cyfa_chunk_fwd(ctypes.byref(args), None) == _native.CYFA_ERR_UNSUPPORTED
+    assert b"num_slots" in lib.cyfa_last_error()
+    args.M, args.C = 128, 32
+    assert lib.cyfa_chunk_fwd(ctypes.byref(args), None) == _native.CYFA_ERR_UNSUPPORTED
+    args.C = 64
+    assert lib.cyfa_chunk_fwd(ctypes.byref(args), None) == _native.CYFA_ERR_VALUE  # null pointers
+    dargs = _native.CyfaDecodeArgs(B=1, H=1, K=512, V=256, M=128)
+    assert lib.cyfa_decode_step(ctypes.byref(dargs), None) == _native.CYFA_ERR_UNSUPPORTED
+    assert lib.cyfa_readout_table(None, None, 1, 64, None) == _native.CYFA_ERR_UNSUPPORTED
+
+
+def test_python_ops_reject_like_the_reference():
+    from cyclic_flow_attention.ops import chunk_cyfa, fused_recurrent_cyfa
+
+    q = torch.zeros(1, 2, 1, 256, dtype=torch.bfloat16)
+    g = torch.zeros(1, 2, 1)
+    ro = torch.eye(127)[None]
+    w = torch.ones(256)
+    with pytest.raises(NotImplementedError):
+        chunk_cyfa(q, q, q, g, g, g, ro, w, w, cu_seqlens=torch.tensor([0, 2]))
+    with pytest.raises(NotImplementedError):
+        chunk_cyfa(q, q, q, g, g, g, ro, w, w, checkpoint_level=1)
+    with pytest.raises(NotImplementedError):
+        fused_recurrent_cyfa(q, q, q, g, g, g, ro, w, w)  # T != 1
+    q1 = q[:, :1].clone().requires_grad_(False)
+    g1 = g[:, :1]
+    with pytest.raises(ValueError):
+        fused_recurrent_cyfa(q1, q1, q1, g1.clone().requires_grad_(True), g1, g1, ro, w, w)
+    with pytest.raises(ValueError):
+        chunk_cyfa(q, q, q, g, g, g, ro, w, w)  # CPU tensors: the HIP path has no CPU fallback
