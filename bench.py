@@ -1,0 +1,281 @@
+#!/usr/bin/env python
+"""CyFA-400M bf16 on one MI355X: prefill tok/s (B=8, T=2048) and decode tok/s (B=64).
+
+Workload (BASELINE.json metric; configs 3 and 4):
+  prefill  CyFA-400M forward over B=8 x T=2048 uniform random token ids with
+           use_cache=True (full logits, as the reference's model forward);
+           one step = one prefill pass.  value = total prefill tokens / second.
+  decode   B=64: a 2048-token prompt processed chunkwise (untimed), then
+           greedy decode steps with the fused constant-memory decode kernel;
+           argmax stays on the device. Reported under "decode".
+Weights are seeded N(0, 0.02) random init (no checkpoints offline).
+
+roofline: HIP events around every cyfa_chunk_fwd / cyfa_decode_step launch in
+the timed region give the average device duration per launch;
+  prefill attention: 377 088 algorithmic FLOP per token*head / duration vs the
+                     2.5 PFLOP/s dense bf16 MFMA peak;
+  decode:            524 288 bytes of fp32 state per (batch, head) per layer
+                     launch / duration vs 8 TB/s HBM.
+cpu_baseline: the CPU oracle (the restatement of the reference path; the
+reference itself has no CPU path) timed on this host, bounded sample.
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (str(ROOT), str(ROOT / "cyfa-jittor_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"]
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+FLOP_PER_TOKEN_HEAD = 377_088      # pass 1 + readout + pass 2, causal-exact
+STATE_BYTES_PER_BH = 524_288       # fp32 hk + hv, read and written, K = V = 256
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10, help="timed prefill steps")
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--decode-warmup", type=int, default=4)
+    ap.add_argument("--batch", type=int, default=8)
+    ap.add_argument("--seq-len", type=int, default=2048)
+    ap.add_argument("--decode-batch", type=int, default=64)
+    ap.add_argument("--config", default="cyclic_flow_attention_400m.json")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_threads():
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def build_model(cfg_name, device):
+    import torch
+
+    from cyclic_flow_attention.utils import initialize_model, read_config
+
+    config = read_config(cfg_name)
+    model = initialize_model(config, std=0.02, seed=0).to(device).eval()
+    return config, model
+
+
+def time_prefill(model, ids, steps, warmup):
+    import torch
+
+    from cyclic_flow_attention import _native
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            model(ids, use_cache=True)
+        torch.cuda.synchronize()
+        with _native.LaunchTimer() as timer:
+            start = time.perf_counter()
+            for _ in range(steps):
+                out = model(ids, use_cache=True)
+            torch.cuda.synchronize()
+            elapsed = time.perf_counter() - start
+        del out
+    return elapsed, timer.results().get("cyfa_chunk_fwd", [])
+
+
+def time_decode(model, prompt, steps, warmup):
+    import torch
+
+    from cyclic_flow_attention import _native
+
+    with torch.no_grad():
+        hidden, cache = model.model(prompt, use_cache=True)
+        tok = model.lm_head(hidden[:, -1]).argmax(-1)
+        del hidden
+        for _ in range(warmup):
+            out = model(tok[:, None], cache=cache, use_cache=True)
+            cache = out["cache"]
+            tok = out["logits"][:, -1].argmax(-1)
+        torch.cuda.synchronize()
+        with _native.LaunchTimer() as timer:
+            start = time.perf_counter()
+            for _ in range(steps):
+                out = model(tok[:, None], cache=cache, use_cache=True)
+                cache = out["cache"]
+                tok = out["logits"][:, -1].argmax(-1)
+            torch.cuda.synchronize()
+            elapsed = time.perf_counter() - start
+    return elapsed, timer.results().get("cyfa_decode_step", [])
+
+
+def cpu_baseline_prefill(model, config, seq_len):
+    """Oracle forward (float32, reference rounding points) of one whole
+    sequence of the prefill batch on the host cores."""
+    import torch
+
+    from oracle import model_oracle
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    params = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    cfg = {k: getattr(config, k) for k in config.__dataclass_fields__}
+    gen = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, config.vocab_size, (1, seq_len), generator=gen)
+    with torch.no_grad():
+        model_oracle.causal_lm(params, cfg, ids[:, :64], mode="mirror")  # warm-up
+        start = time.perf_counter()
+        model_oracle.causal_lm(params, cfg, ids, use_cache=True, mode="mirror")
+        elapsed = time.perf_counter() - start
+    return {
+        "value": round(seq_len / elapsed, 2),
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"CPU oracle (float32, bf16 rounding points) full 400M forward, B=1 x T={seq_len} "
+                  f"(one of the prefill batch's sequences), {elapsed:.1f} s",
+    }
+
+
+def cpu_baseline_decode(model, config, batch, steps=2):
+    """Oracle decode steps on the host, from a zero state (same per-step work)."""
+    import torch
+
+    from oracle import model_oracle
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    params = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    cfg = {k: getattr(config, k) for k in config.__dataclass_fields__}
+    gen = torch.Generator().manual_seed(2)
+    ids = torch.randint(0, config.vocab_size, (batch, 1), generator=gen)
+    cache = None
+    with torch.no_grad():
+        _, cache = model_oracle.causal_lm(params, cfg, ids, cache=None, use_cache=True, mode="mirror")
+        start = time.perf_counter()
+        for _ in range(steps):
+            logits, cache = model_oracle.causal_lm(params, cfg, ids, cache=cache, use_cache=True, mode="mirror")
+            ids = logits[:, -1].argmax(-1, keepdim=True)
+        elapsed = time.perf_counter() - start
+    return {
+        "value": round(batch * steps / elapsed, 2),
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"CPU oracle (float32) {steps} decode steps of the 400M model at B={batch}, {elapsed:.1f} s",
+    }
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU: the CyFA hot path shards over (batch, head) "
+                                   "with no exchange inside the op; run with --gpus 1"}), flush=True)
+        return 2
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    log(f"device {torch.cuda.get_device_name(dev)}")
+    config, model = build_model(args.config, dev)
+    H = config.num_heads
+    gen = torch.Generator().manual_seed(0)
+    ids = torch.randint(0, config.vocab_size, (args.batch, args.seq_len), generator=gen).to(dev)
+
+    log(f"prefill B={args.batch} T={args.seq_len}: warmup {args.warmup}, timed {args.steps}")
+    elapsed, op_ms = time_prefill(model, ids, args.steps, args.warmup)
+    tokens = args.batch * args.seq_len * args.steps
+    value = tokens / elapsed
+    op_avg = statistics.fmean(op_ms) if op_ms else float("nan")
+    flop = FLOP_PER_TOKEN_HEAD * args.batch * args.seq_len * H
+    achieved = flop / (op_avg * 1e-3) / 1e12
+    log(f"prefill {value:,.0f} tok/s; attention op {op_avg:.3f} ms/launch over {len(op_ms)} launches "
+        f"= {achieved:.1f} TFLOP/s")
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: uniform random token ids; seeded N(0, 0.02) random-init CyFA-400M weights",
+        "config": {
+            "workload": f"CyFA-400M prefill B={args.batch} x T={args.seq_len} (config 3) as value; "
+                        f"decode B={args.decode_batch} after a {args.seq_len}-token prompt (config 4) under 'decode'",
+            "global_batch": args.batch,
+            "seq_len": args.seq_len,
+            "parallelism": "single-gpu",
+        },
+        "roofline": {
+            "kernel": "cyfa_chunk_fwd (clock, segment states, carry, pass 1 + readout, pass 2)",
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+            "launch_ms": round(op_avg, 4),
+            "flop_per_launch": flop,
+        },
+    }
+
+    if not args.no_decode:
+        prompt = torch.randint(0, config.vocab_size, (args.decode_batch, args.seq_len), generator=gen).to(dev)
+        log(f"decode B={args.decode_batch}: prompt {args.seq_len}, warmup {args.decode_warmup}, "
+            f"timed {args.decode_steps}")
+        d_elapsed, dec_ms = time_decode(model, prompt, args.decode_steps, args.decode_warmup)
+        d_value = args.decode_batch * args.decode_steps / d_elapsed
+        d_avg = statistics.fmean(dec_ms) if dec_ms else float("nan")
+        d_bytes = STATE_BYTES_PER_BH * args.decode_batch * H
+        d_gbs = d_bytes / (d_avg * 1e-3) / 1e9
+        log(f"decode {d_value:,.0f} tok/s; decode kernel {d_avg * 1e3:.1f} us/launch = {d_gbs:,.0f} GB/s")
+        result["decode"] = {
+            "value": round(d_value, 1),
+            "unit": "tok/s",
+            "batch": args.decode_batch,
+            "steps": args.decode_steps,
+            "ms_per_step": round(d_elapsed / args.decode_steps * 1e3, 3),
+            "roofline": {
+                "kernel": "cyfa_decode_step",
+                "bound": "hbm",
+                "achieved": round(d_gbs, 1),
+                "peak": PEAK_HBM_GBS,
+                "unit": "GB/s",
+                "frac": round(d_gbs / PEAK_HBM_GBS, 4),
+                "traffic": None,
+                "launch_us": round(d_avg * 1e3, 2),
+                "bytes_per_launch": d_bytes,
+            },
+        }
+        del prompt
+
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle) ...")
+        result["cpu_baseline"] = cpu_baseline_prefill(model, config, args.seq_len)
+        log(f"cpu prefill {result['cpu_baseline']['value']} tok/s")
+        if "decode" in result:
+            result["decode"]["cpu_baseline"] = cpu_baseline_decode(model, config, args.decode_batch)
+            log(f"cpu decode {result['decode']['cpu_baseline']['value']} tok/s")
+
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

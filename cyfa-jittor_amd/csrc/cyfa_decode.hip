@@ -72,7 +72,7 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     const float beta = p.beta[bh];
     if (tid < kPairs) {
         float s, c;
-        phase_sincos(lam, tid, s, c);
+        pair_sincos(reduced_clock(lam), tid, s, c);
         const float a = beta * pair_scale(tid);
         s_w[2 * tid] = bf16_round(a * c);
         s_w[2 * tid + 1] = bf16_round(-a * s);

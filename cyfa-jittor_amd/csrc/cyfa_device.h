@@ -65,6 +65,19 @@ __device__ __forceinline__ void phase_sincos(float lam, int pair, float& s, floa
     c = __builtin_amdgcn_cosf(rev);
 }
 
+// Clock reduced once per token: lam' = (lam mod R) / R. The phase of pair p
+// in revolutions is then p * lam' (the same angle, modulo 2 pi, as the
+// reference's integer reduction above; p * lam' < 64 revolutions so one fp32
+// product keeps the angle to ~2.5e-5 rad), and the sine / cosine of pair p
+// cost one multiply and one transcendental each.
+__device__ __forceinline__ float reduced_clock(float lam) { return fmodf(lam, (float)kActive) * (1.0f / kActive); }
+
+__device__ __forceinline__ void pair_sincos(float lamr, int pair, float& s, float& c) {
+    const float rev = (float)pair * lamr;
+    s = __builtin_amdgcn_sinf(rev);
+    c = __builtin_amdgcn_cosf(rev);
+}
+
 __device__ __forceinline__ f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -79,13 +92,22 @@ __device__ __forceinline__ float pair_scale(int pair) {
 }
 
 // Write-vector pair (w[2p], w[2p+1]) = beta s_p (cos theta_p, -sin theta_p)
-// (ops/utils.py:664-702), before rounding.
-__device__ __forceinline__ void write_pair(float lam, float beta, int pair, float& we, float& wo) {
+// (ops/utils.py:664-702), before rounding; lamr = reduced_clock(lam).
+__device__ __forceinline__ void write_pair(float lamr, float beta, int pair, float& we, float& wo) {
     float s, c;
-    phase_sincos(lam, pair, s, c);
+    pair_sincos(lamr, pair, s, c);
     const float a = beta * pair_scale(pair);
     we = a * c;
     wo = -a * s;
+}
+
+// Write-vector element m alone: beta s_p cos(theta_p) for even m,
+// -beta s_p sin(theta_p) for odd m (one transcendental).
+__device__ __forceinline__ float write_coord(float lamr, float beta, int m) {
+    const int pair = m >> 1;
+    const float rev = (float)pair * lamr;
+    const float a = beta * pair_scale(pair);
+    return (m & 1) ? -a * __builtin_amdgcn_sinf(rev) : a * __builtin_amdgcn_cosf(rev);
 }
 
 template <int W = 64>

@@ -13,10 +13,14 @@
 //                        readout epilogue -> slot weights (bf16).
 //   5. pass2_kernel      the same sweep for the value state [128 x 256] with
 //                        query = slot weights, key = w, value = v -> o (bf16).
-// All GEMM-shaped work runs on v_mfma_f32_16x16x32_{bf16,f16} with fp32
-// accumulation; 64-token chunks are staged in LDS. The sweep keeps each
-// segment's state on chip from the first to the last chunk; only segment
-// boundary states (one per L chunks) touch HBM.
+// The sweep kernels run 8 waves (512 threads); each wave holds 1/8 of the fp32
+// state as MFMA accumulators, and the global loads of chunk n + 1 are issued
+// into registers before chunk n computes. All GEMM-shaped work runs on
+// v_mfma_f32_16x16x32_{bf16,f16} with fp32 accumulation. Every 64-token tile
+// (q_hat, k_hat, w, v, slot weights) is staged once in LDS, token-major; the
+// operands that contract over tokens are read with the gfx950 LDS transpose
+// read. The sweep keeps each segment's state on chip from its first to its
+// last chunk; only segment boundary states (one per L chunks) touch HBM.
 //
 // Lane conventions of the 16x16x32 MFMA (wave64, lane l, lr = l & 15, lg = l >> 4):
 //   A[row][k]: row = lr, k = 8 lg + j (j = 0..7)     B[k][col]: col = lr, k = 8 lg + j
@@ -40,83 +44,197 @@ constexpr int SEG_K = KD * kSlots;  // key-state elements
 constexpr int SEG_V = kSlots * VD;  // value-state elements
 constexpr int SEG = SEG_K + SEG_V;
 
-constexpr int QS = KD + 8;    // row stride (elements) of a 64 x 256 bf16 tile
-constexpr int TS = 64 + 8;    // row stride of a [rows x 64 tokens] bf16 tile
-constexpr int ZS = 128 + 8;   // row stride of a 64 x 128 16-bit tile / table
-constexpr int RS = 128 + 4;   // row stride of a 64 x 128 fp32 tile
+// Row strides (elements) of the LDS tiles. The 16-bit strides are 8 dwords
+// modulo the 64 LDS banks, so the four rows a transpose read touches per
+// 16-lane block fall on disjoint banks.
+constexpr int RS256 = 256 + 16;  // 64 x 256 bf16 tiles
+constexpr int RS128 = 128 + 16;  // 64 x 128 16-bit tiles and the 128 x 128 table
+constexpr int TS = 64 + 8;       // 64 x 64 score tile
+constexpr int FS = 128 + 4;      // 64 x 128 fp32 tile
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ size_t tok_index(const PrefillParams& p, int b, int t, int h) {
     return ((size_t)b * p.T + t) * p.H + h;
 }
 
-// Gates of chunk [t0, t0 + 64) into LDS: clock, beta and the in-chunk
-// inclusive cumsum of g in log2 units (ops/utils.py:495-520). Wave 0 only.
-__device__ __forceinline__ void stage_gates(const PrefillParams& p, int b, int h, int bh, int t0,
-                                            float* sLam, float* sBeta, float* sGam) {
+// Chunk gates, split into an issue step (global loads into registers, wave 0,
+// lane = token) and a commit step (in-chunk scan of g in log2 units,
+// ops/utils.py:495-520, and the LDS writes), so that the loads of chunk n + 1
+// can be in flight while chunk n computes. LDS per token: sLam = reduced clock
+// (lam mod 127) / 127, sBeta, sGam = G_t, sGam[64 + t] = 2^G_t and
+// sGam[128 + t] = 2^(G_last - G_t).
+struct GateRegs {
+    float g, beta, lam;
+};
+
+__device__ __forceinline__ GateRegs issue_gates(const PrefillParams& p, int b, int h, int bh, int t0) {
+    GateRegs r{0.f, 0.f, 0.f};
     const int tid = threadIdx.x;
     if (tid < 64) {
         const int t = t0 + tid;
-        float g = 0.f, be = 0.f;
-        if (t < p.T) {
-            const size_t i = tok_index(p, b, t, h);
-            g = p.g[i];
-            be = p.beta[i];
-        }
-        float x = g;
+        const size_t i = tok_index(p, b, t < p.T ? t : p.T - 1, h);
+        r.g = p.g[i];
+        r.beta = p.beta[i];
+        r.lam = p.lam[(size_t)bh * p.Tp + t];
+    }
+    return r;
+}
+
+__device__ __forceinline__ void commit_gates(const PrefillParams& p, int t0, const GateRegs& r, float* sLam,
+                                             float* sBeta, float* sGam) {
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        const bool valid = t0 + tid < p.T;
+        float x = valid ? r.g : 0.f;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const float y = __shfl_up(x, o, 64);
             if (tid >= o) x += y;
         }
-        sGam[tid] = x * kLog2e;
-        sBeta[tid] = be;
-        sLam[tid] = p.lam[(size_t)bh * p.Tp + t];
+        const float gam = x * kLog2e;
+        const float last = __shfl(gam, 63, 64);
+        sGam[tid] = gam;
+        sBeta[tid] = valid ? r.beta : 0.f;
+        sLam[tid] = reduced_clock(r.lam);
+        sGam[64 + tid] = exp2f(gam);          // 2^G_t
+        sGam[128 + tid] = exp2f(last - gam);  // 2^(G_last - G_t)
     }
 }
 
-// Load row t of a [B, T, H, 256] bf16 tensor in A/B-fragment order (8 k-steps
-// of 32) and RMS-normalise it: x_hat = bf16(x rsqrt(mean x^2 + eps) w)
-// (ops/qk_norm.py:64-107, 206-233). Rows past T are zero. The four lanes
-// sharing lr hold the whole row; their partial sums are combined by shuffles.
-__device__ __forceinline__ void load_norm_row(const PrefillParams& p, const bf16_t* x, const float* wn, float eps,
-                                              int b, int h, int t, bf16x8 frag[8]) {
-    const int lg = (threadIdx.x & 63) >> 4;
-    float v[8][8];
-    float ss = 0.f;
-    const bool valid = t < p.T;
-    const bf16_t* row = x + tok_index(p, b, valid ? t : 0, h) * KD;
+// LDS transpose read (ds_read_b64_tr_b16). Within each 16-lane block of a
+// wave, source lane i supplies the address of four consecutive 16-bit
+// elements D[i][0..3] and result lane i receives {D[4e + (i >> 2)][i & 3]},
+// e = 0..3. load_tr arranges the source addresses so that two such reads
+// return the MFMA fragment of the transpose of a row-major tile:
+//   lane (lr, lg) element j = X[s0 + 8 lg + j][c0 + lr],   j = 0..7,
+// i.e. the A operand A[row = c0 + lr][k = s0 + 8 lg + j] or the B operand
+// B[k = s0 + 8 lg + j][col = c0 + lr] of a tile stored token-major.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef s16x4 __attribute__((address_space(3))) lds_s16x4;
+
+__device__ __forceinline__ s16x8 load_tr(const void* X, int ld, int s0, int c0) {
+    const int l = threadIdx.x & 63, g = l >> 4, i = l & 15;
+    const short* p = reinterpret_cast<const short*>(X) + (s0 + 8 * g + (i >> 2)) * ld + c0 + 4 * (i & 3);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(const_cast<short*>(p)));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(const_cast<short*>(p + 4 * ld)));
+    s16x8 r;
+    r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+    r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+    return r;
+}
+
+__device__ __forceinline__ bf16x8 load_tr_bf16(const bf16_t* X, int ld, int s0, int c0) {
+    return __builtin_bit_cast(bf16x8, load_tr(X, ld, s0, c0));
+}
+
+__device__ __forceinline__ f16x8 load_tr_f16(const f16_t* X, int ld, int s0, int c0) {
+    return __builtin_bit_cast(f16x8, load_tr(X, ld, s0, c0));
+}
+
+// Row fragment: lane (lr, lg) gets X[r0 + lr][k0 + 8 lg .. + 8] (A operand, or
+// B operand of a product that contracts over X's columns).
+template <typename V8, typename T>
+__device__ __forceinline__ V8 load_row(const T* X, int ld, int r0, int k0) {
+    const int l = threadIdx.x & 63;
+    return *reinterpret_cast<const V8*>(X + (r0 + (l & 15)) * ld + k0 + 8 * (l >> 4));
+}
+
+// Rows [t0, t0 + 64) of a [B, T, H, 256] bf16 tensor, four 16-byte loads per
+// thread of a 512-thread block: row (tid >> 5) + 16 it, columns 8 (tid & 31) .. + 8.
+// Rows past T are clamped to T - 1 (and zeroed when stored).
+__device__ __forceinline__ void issue_rows(const PrefillParams& p, const bf16_t* x, int b, int h, int t0, bf16x8 raw[4]) {
+    const int tid = threadIdx.x;
 #pragma unroll
-    for (int ks = 0; ks < 8; ks++) {
-        if (valid) {
-            load_bf16x8(row + 32 * ks + 8 * lg, v[ks]);
-        } else {
+    for (int it = 0; it < 4; it++) {
+        const int t = t0 + (tid >> 5) + 16 * it;
+        raw[it] = *reinterpret_cast<const bf16x8*>(x + tok_index(p, b, t < p.T ? t : p.T - 1, h) * KD + 8 * (tid & 31));
+    }
+}
+
+// RMS-normalise those rows and store them row-major into dst [64][RS256]:
+// x_hat = bf16(x rsqrt(mean x^2 + eps) w) (ops/qk_norm.py:64-107, 206-233).
+// A row's 32 chunks live in one half-wave; wn is the weight in LDS.
+__device__ __forceinline__ void norm_store_rows(const PrefillParams& p, int t0, const bf16x8 raw[4], const float* wn,
+                                                float eps, bf16_t* dst) {
+    const int tid = threadIdx.x, c8 = 8 * (tid & 31);
+    const float4 w0 = *reinterpret_cast<const float4*>(wn + c8);
+    const float4 w1 = *reinterpret_cast<const float4*>(wn + c8 + 4);
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-            for (int j = 0; j < 8; j++) v[ks][j] = 0.f;
+    for (int it = 0; it < 4; it++) {
+        const int r = (tid >> 5) + 16 * it;
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float v = (float)raw[it][j];
+            ss = fmaf(v, v, ss);
         }
+        ss = wave_sum<32>(ss);
+        const float rs = t0 + r < p.T ? rsqrtf(ss * (1.f / KD) + eps) : 0.f;
+        bf16x8 o;
 #pragma unroll
-        for (int j = 0; j < 8; j++) ss = fmaf(v[ks][j], v[ks][j], ss);
-    }
-    ss += __shfl_xor(ss, 16);
-    ss += __shfl_xor(ss, 32);
-    const float rs = rsqrtf(ss * (1.f / KD) + eps);
-#pragma unroll
-    for (int ks = 0; ks < 8; ks++) {
-        const float4 w0 = *reinterpret_cast<const float4*>(wn + 32 * ks + 8 * lg);
-        const float4 w1 = *reinterpret_cast<const float4*>(wn + 32 * ks + 8 * lg + 4);
-        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-        for (int j = 0; j < 8; j++) frag[ks][j] = (bf16_t)(v[ks][j] * rs * wv[j]);
+        for (int j = 0; j < 8; j++) o[j] = (bf16_t)((float)raw[it][j] * rs * wv[j]);
+        *reinterpret_cast<bf16x8*>(dst + r * RS256 + c8) = o;
     }
 }
 
-// Write-vector element w[s][m] (ops/utils.py:664-702), rounded to bf16.
-__device__ __forceinline__ bf16_t write_elem(float lam, float beta, int m) {
-    float sn, cs;
-    const int pair = m >> 1;
-    phase_sincos(lam, pair, sn, cs);
-    const float a = beta * pair_scale(pair);
-    return (bf16_t)((m & 1) ? -a * sn : a * cs);
+// Store rows of v (no normalisation), zero past T.
+__device__ __forceinline__ void store_rows(const PrefillParams& p, int t0, const bf16x8 raw[4], bf16_t* dst) {
+    const int tid = threadIdx.x, c8 = 8 * (tid & 31);
+#pragma unroll
+    for (int it = 0; it < 4; it++) {
+        const int r = (tid >> 5) + 16 * it;
+        bf16x8 o = raw[it];
+        if (t0 + r >= p.T) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) o[j] = (bf16_t)0.f;
+        }
+        *reinterpret_cast<bf16x8*>(dst + r * RS256 + c8) = o;
+    }
+}
+
+// Slot-weight rows [t0, t0 + 64) of the pass-1 output: two 16-byte loads per thread.
+__device__ __forceinline__ void issue_omega(const PrefillParams& p, int bh, int t0, bf16x8 om[2]) {
+    const bf16_t* src = p.omega + ((size_t)bh * p.Tp + t0) * kSlots;
+#pragma unroll
+    for (int it = 0; it < 2; it++) {
+        const int idx = threadIdx.x + 512 * it, r = idx >> 4, c8 = (idx & 15) * 8;
+        om[it] = *reinterpret_cast<const bf16x8*>(src + r * kSlots + c8);
+    }
+}
+
+// Write vector of the chunk, w [64 tokens][128] bf16 row-major (ops/utils.py:664-702):
+// 4096 pairs over 512 threads.
+__device__ __forceinline__ void store_write_rows(const float* sLam, const float* sBeta, bf16_t* dst) {
+#pragma unroll
+    for (int it = 0; it < 8; it++) {
+        const int idx = threadIdx.x + 512 * it, s = idx >> 6, pr = idx & 63;
+        float we, wo;
+        write_pair(sLam[s], sBeta[s], pr, we, wo);
+        bf16_t* d = dst + s * RS128 + 2 * pr;
+        d[0] = (bf16_t)we;
+        d[1] = (bf16_t)wo;
+    }
+}
+
+// Write-vector element w[s][m] (ops/utils.py:664-702), rounded to bf16;
+// lamr is the token's reduced clock.
+__device__ __forceinline__ bf16_t write_elem(float lamr, float beta, int m) { return (bf16_t)write_coord(lamr, beta, m); }
+
+// Masked, decayed score tile for key block sb and query block tb, from an
+// accumulated q.k block: P[t][s] = bf16(2^(G_t - G_s) q_t.k_s) for s <= t, else 0
+// (ops/chunk_o.py:240-250).
+__device__ __forceinline__ void store_scores(const f32x4& sc, int tb, int sb, const float* sGam, bf16_t* sP) {
+    const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
+    const int s = 16 * sb + lr;
+    const float gs = sGam[s];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int t = 16 * tb + 4 * lg + i;
+        const float v = s <= t ? sc[i] * exp2f(sGam[t] - gs) : 0.f;
+        sP[t * TS + s] = (bf16_t)v;
+    }
 }
 
 __device__ __forceinline__ bf16x8 cat4(const bf16x4& lo, const bf16x4& hi) {
@@ -183,138 +301,119 @@ __global__ __launch_bounds__(256) void clock_kernel(PrefillParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// 2. Segment-local end states (zero start). grid = (B*H*(P-1), 2): y = pass.
-constexpr int SEGK_LDS = KD * TS * 2;               // sKt
-constexpr int SEGV_LDS = kSlots * TS * 2 + VD * TS * 2;  // sWt + sVt
-constexpr int SEG_LDS = (SEGK_LDS > SEGV_LDS ? SEGK_LDS : SEGV_LDS) + 3 * 64 * 4;
+// 2. Segment-local end states from a zero start. grid = (B*H*(P-1), 2), y = pass;
+// 512 threads. Pass 0: wave w owns key-state columns [16 w, 16 w + 16)
+// (acc[db] = S[16 db + 4 lg + i][16 w + lr]). Pass 1: wave w owns value-state
+// columns [32 w, 32 w + 32) (acc[mb][cb] = S[16 mb + 4 lg + i][32 w + 16 cb + lr]).
+constexpr int SG_K = 0;                     // pass 0: bf16 [64][RS256] k_hat rows
+constexpr int SG_W = 0;                     // pass 1: bf16 [64][RS128] w rows
+constexpr int SG_V = 64 * RS128 * 2;        // pass 1: bf16 [64][RS256] v rows
+constexpr int SG_G = SG_V + 64 * RS256 * 2; // f32 [5][64] gates
+constexpr int SG_NW = SG_G + 5 * 64 * 4;    // f32 [256] k norm weight
+constexpr int SG_LDS = SG_NW + KD * 4;
+static_assert(64 * RS256 * 2 <= SG_G, "k tile overlaps the gates");
 
-__global__ __launch_bounds__(256) void segment_state_kernel(PrefillParams p) {
-    __shared__ __align__(16) unsigned char smem[SEG_LDS];
+__global__ __launch_bounds__(512) void segment_state_kernel(PrefillParams p) {
+    __shared__ __align__(16) unsigned char smem[SG_LDS];
+    float* sLam = reinterpret_cast<float*>(smem + SG_G);
+    float* sBeta = sLam + 64;
+    float* sGam = sBeta + 64;
+    float* sNw = reinterpret_cast<float*>(smem + SG_NW);
     const int P1 = p.P - 1;
     const int bh = blockIdx.x / P1, j = blockIdx.x % P1, pass = blockIdx.y;
     const int b = bh / p.H, h = bh % p.H;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 15, lg = lane >> 4;
-    float* sLam = reinterpret_cast<float*>(smem + SEG_LDS - 3 * 64 * 4);
-    float* sBeta = sLam + 64;
-    float* sGam = sBeta + 64;
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
     float* out = p.seg + ((size_t)bh * p.P + j) * SEG;
-    float logdecay = 0.f;
+    if (tid < KD) sNw[tid] = p.k_w[tid];
 
     if (pass == 0) {
-        bf16_t* sKt = reinterpret_cast<bf16_t*>(smem);
-        f32x4 acc[16][2];
+        bf16_t* sK = reinterpret_cast<bf16_t*>(smem + SG_K);
+        f32x4 acc[16];
 #pragma unroll
-        for (int db = 0; db < 16; db++)
-#pragma unroll
-            for (int mb = 0; mb < 2; mb++) acc[db][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int db = 0; db < 16; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        bf16x8 kraw[4];
+        issue_rows(p, p.k, b, h, n0 * 64, kraw);
+        GateRegs gr = issue_gates(p, b, h, bh, n0 * 64);
+        float logdecay = 0.f;
+        __syncthreads();
         for (int n = n0; n < n1; n++) {
             const int t0 = n * 64;
-            stage_gates(p, b, h, bh, t0, sLam, sBeta, sGam);
-            bf16x8 kf[8];
-            load_norm_row(p, p.k, p.k_w, p.k_eps, b, h, t0 + 16 * w + lr, kf);
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++)
-#pragma unroll
-                for (int jj = 0; jj < 8; jj++) sKt[(32 * ks + 8 * lg + jj) * TS + 16 * w + lr] = kf[ks][jj];
+            commit_gates(p, t0, gr, sLam, sBeta, sGam);
+            norm_store_rows(p, t0, kraw, sNw, p.k_eps, sK);
+            if (n + 1 < n1) {
+                issue_rows(p, p.k, b, h, t0 + 64, kraw);
+                gr = issue_gates(p, b, h, bh, t0 + 64);
+            }
             __syncthreads();
-            const float last = sGam[63];
-            logdecay += last;
-            bf16x8 wt[2][2];
+            logdecay += sGam[63];
+            bf16x8 wt[2];
+            {
+                const int m = 16 * w + lr;
 #pragma unroll
-            for (int ss = 0; ss < 2; ss++)
-#pragma unroll
-                for (int mb = 0; mb < 2; mb++) {
-                    const int m = 32 * w + 16 * mb + lr;
+                for (int ss = 0; ss < 2; ss++)
 #pragma unroll
                     for (int jj = 0; jj < 8; jj++) {
                         const int s = 32 * ss + 8 * lg + jj;
-                        const float wv = (float)write_elem(sLam[s], sBeta[s], m);
-                        wt[ss][mb][jj] = (bf16_t)(wv * exp2f(last - sGam[s]));
+                        wt[ss][jj] = (bf16_t)((float)write_elem(sLam[s], sBeta[s], m) * sGam[128 + s]);
                     }
-                }
-            const float dec = exp2f(last);
+            }
+            const float dec = sGam[64 + 63];
+#pragma unroll
+            for (int db = 0; db < 16; db++) acc[db] *= dec;
 #pragma unroll
             for (int db = 0; db < 16; db++)
 #pragma unroll
-                for (int mb = 0; mb < 2; mb++) acc[db][mb] *= dec;
-#pragma unroll
-            for (int db = 0; db < 16; db++)
-#pragma unroll
-                for (int ss = 0; ss < 2; ss++) {
-                    const bf16x8 a = *reinterpret_cast<const bf16x8*>(sKt + (16 * db + lr) * TS + 32 * ss + 8 * lg);
-#pragma unroll
-                    for (int mb = 0; mb < 2; mb++) acc[db][mb] = mfma_bf16(a, wt[ss][mb], acc[db][mb]);
-                }
+                for (int ss = 0; ss < 2; ss++)
+                    acc[db] = mfma_bf16(load_tr_bf16(sK, RS256, 32 * ss, 16 * db), wt[ss], acc[db]);
             __syncthreads();
         }
 #pragma unroll
         for (int db = 0; db < 16; db++)
 #pragma unroll
-            for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) out[(16 * db + 4 * lg + i) * kSlots + 32 * w + 16 * mb + lr] = acc[db][mb][i];
+            for (int i = 0; i < 4; i++) out[(16 * db + 4 * lg + i) * kSlots + 16 * w + lr] = acc[db][i];
         if (tid == 0) p.seg_decay[bh * p.P + j] = exp2f(logdecay);
     } else {
-        bf16_t* sWt = reinterpret_cast<bf16_t*>(smem);
-        bf16_t* sVt = sWt + kSlots * TS;
-        f32x4 acc[8][4];
+        bf16_t* sW = reinterpret_cast<bf16_t*>(smem + SG_W);
+        bf16_t* sV = reinterpret_cast<bf16_t*>(smem + SG_V);
+        f32x4 acc[8][2];
 #pragma unroll
         for (int mb = 0; mb < 8; mb++)
 #pragma unroll
-            for (int cb = 0; cb < 4; cb++) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int cb = 0; cb < 2; cb++) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        bf16x8 vraw[4];
+        issue_rows(p, p.v, b, h, n0 * 64, vraw);
+        GateRegs gr = issue_gates(p, b, h, bh, n0 * 64);
         for (int n = n0; n < n1; n++) {
             const int t0 = n * 64;
-            stage_gates(p, b, h, bh, t0, sLam, sBeta, sGam);
-            __syncthreads();
-            // w^T [128 x 64] for all slots: 4096 pairs / 256 threads.
-#pragma unroll 4
-            for (int it = 0; it < 16; it++) {
-                const int idx = tid + 256 * it, s = idx >> 6, pr = idx & 63;
-                float we, wo;
-                write_pair(sLam[s], sBeta[s], pr, we, wo);
-                sWt[(2 * pr) * TS + s] = (bf16_t)we;
-                sWt[(2 * pr + 1) * TS + s] = (bf16_t)wo;
-            }
-            // v^T for this wave's 64 value columns.
-#pragma unroll
-            for (int it = 0; it < 8; it++) {
-                const int q = lane + 64 * it, s = q >> 3, c8 = (q & 7) * 8;
-                const int t = t0 + s;
-                bf16x8 vv;
-                if (t < p.T) {
-                    vv = *reinterpret_cast<const bf16x8*>(p.v + tok_index(p, b, t, h) * VD + 64 * w + c8);
-                } else {
-#pragma unroll
-                    for (int jj = 0; jj < 8; jj++) vv[jj] = (bf16_t)0.f;
-                }
-#pragma unroll
-                for (int jj = 0; jj < 8; jj++) sVt[(64 * w + c8 + jj) * TS + s] = vv[jj];
+            commit_gates(p, t0, gr, sLam, sBeta, sGam);
+            store_rows(p, t0, vraw, sV);
+            if (n + 1 < n1) {
+                issue_rows(p, p.v, b, h, t0 + 64, vraw);
+                gr = issue_gates(p, b, h, bh, t0 + 64);
             }
             __syncthreads();
-            const float last = sGam[63];
-            const float dec = exp2f(last);
+            store_write_rows(sLam, sBeta, sW);
+            __syncthreads();
+            const float dec = sGam[64 + 63];
 #pragma unroll
             for (int mb = 0; mb < 8; mb++)
 #pragma unroll
-                for (int cb = 0; cb < 4; cb++) acc[mb][cb] *= dec;
+                for (int cb = 0; cb < 2; cb++) acc[mb][cb] *= dec;
 #pragma unroll
             for (int ss = 0; ss < 2; ss++) {
-                float f[8];
+                bf16x8 vt[2];
 #pragma unroll
-                for (int jj = 0; jj < 8; jj++) f[jj] = exp2f(last - sGam[32 * ss + 8 * lg + jj]);
-                bf16x8 vt[4];
+                for (int cb = 0; cb < 2; cb++) {
+                    const bf16x8 vb = load_tr_bf16(sV, RS256, 32 * ss, 32 * w + 16 * cb);
 #pragma unroll
-                for (int cb = 0; cb < 4; cb++) {
-                    const bf16x8 raw = *reinterpret_cast<const bf16x8*>(sVt + (64 * w + 16 * cb + lr) * TS + 32 * ss + 8 * lg);
-#pragma unroll
-                    for (int jj = 0; jj < 8; jj++) vt[cb][jj] = (bf16_t)((float)raw[jj] * f[jj]);
+                    for (int jj = 0; jj < 8; jj++) vt[cb][jj] = (bf16_t)((float)vb[jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
                 }
 #pragma unroll
                 for (int mb = 0; mb < 8; mb++) {
-                    const bf16x8 a = *reinterpret_cast<const bf16x8*>(sWt + (16 * mb + lr) * TS + 32 * ss + 8 * lg);
+                    const bf16x8 a = load_tr_bf16(sW, RS128, 32 * ss, 16 * mb);
 #pragma unroll
-                    for (int cb = 0; cb < 4; cb++) acc[mb][cb] = mfma_bf16(a, vt[cb], acc[mb][cb]);
+                    for (int cb = 0; cb < 2; cb++) acc[mb][cb] = mfma_bf16(a, vt[cb], acc[mb][cb]);
                 }
             }
             __syncthreads();
@@ -323,9 +422,9 @@ __global__ __launch_bounds__(256) void segment_state_kernel(PrefillParams p) {
 #pragma unroll
         for (int mb = 0; mb < 8; mb++)
 #pragma unroll
-            for (int cb = 0; cb < 4; cb++)
+            for (int cb = 0; cb < 2; cb++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) outv[(16 * mb + 4 * lg + i) * VD + 64 * w + 16 * cb + lr] = acc[mb][cb][i];
+                for (int i = 0; i < 4; i++) outv[(16 * mb + 4 * lg + i) * VD + 32 * w + 16 * cb + lr] = acc[mb][cb][i];
     }
 }
 
@@ -358,267 +457,240 @@ __global__ __launch_bounds__(256) void carry_kernel(PrefillParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// 4. Pass 1 (key state) + fused slot readout. grid = B*H*P, 256 threads.
-constexpr int P1_Q = 0;                         // bf16 [64][QS] q_hat; later z, then p (f16 [64][ZS])
-constexpr int P1_KT = P1_Q + 64 * QS * 2;       // bf16 [256][TS] k_hat^T; later raw f32 [64][RS], then omega staging
-constexpr int P1_P = P1_KT + KD * TS * 2;       // bf16 [64][TS] masked scores
-constexpr int P1_TAB = P1_P + 64 * TS * 2;      // f16 [128][ZS] table rows r
-constexpr int P1_TABT = P1_TAB + 128 * ZS * 2;  // f16 [128][ZS] table^T rows m
-constexpr int P1_G = P1_TABT + 128 * ZS * 2;    // f32 [3][64] gates
-constexpr int P1_LDS = P1_G + 3 * 64 * 4;
-static_assert(64 * RS * 4 <= KD * TS * 2, "raw tile must fit in the k^T tile");
-static_assert(64 * ZS * 2 <= 64 * QS * 2, "z/p must fit in the q tile");
+// 4. Pass 1 (key state) + fused slot readout. grid = B*H*P, 512 threads.
+// Wave w owns key-state columns [16 w, 16 w + 16): acc[db] = S[16 db + 4 lg + i][16 w + lr].
+// Scores: wave w covers key block sb = w & 3 and query blocks 2 hi, 2 hi + 1
+// (hi = w >> 2). Readout: wave w covers query block sb and slot / coordinate
+// blocks 4 hi .. 4 hi + 3.
+constexpr int P1_Q = 0;                          // bf16 [64][RS256] q_hat rows; later z, then p (f16 [64][RS128])
+constexpr int P1_K = P1_Q + 64 * RS256 * 2;      // bf16 [64][RS256] k_hat rows; later raw f32 [64][FS], then weights
+constexpr int P1_P = P1_K + 64 * RS256 * 2;      // bf16 [64][TS] masked scores
+constexpr int P1_TAB = P1_P + 64 * TS * 2;       // f16 [128][RS128] readout table rows r (row 127 zero)
+constexpr int P1_RED = P1_TAB + 128 * RS128 * 2; // f32 [2][64][2] softmax row partials
+constexpr int P1_G = P1_RED + 2 * 64 * 2 * 4;    // f32 [5][64] gates
+constexpr int P1_NW = P1_G + 5 * 64 * 4;         // f32 [2][256] q and k norm weights
+constexpr int P1_LDS = P1_NW + 2 * KD * 4;
+static_assert(64 * FS * 4 <= 64 * RS256 * 2, "raw tile must fit in the k tile");
 static_assert(P1_LDS <= 160 * 1024, "pass-1 LDS exceeds gfx950 LDS");
 
-__global__ __launch_bounds__(256) void pass1_kernel(PrefillParams p) {
+__global__ __launch_bounds__(512) void pass1_kernel(PrefillParams p) {
     __shared__ __align__(16) unsigned char smem[P1_LDS];
     bf16_t* sQ = reinterpret_cast<bf16_t*>(smem + P1_Q);
-    f16_t* sZ = reinterpret_cast<f16_t*>(smem + P1_Q);                       // z, then p
-    bf16_t* sOm = reinterpret_cast<bf16_t*>(smem + P1_KT);                   // omega staging (raw is dead by then)
-    bf16_t* sKt = reinterpret_cast<bf16_t*>(smem + P1_KT);
-    float* sRaw = reinterpret_cast<float*>(smem + P1_KT);
+    f16_t* sZ = reinterpret_cast<f16_t*>(smem + P1_Q);
+    bf16_t* sK = reinterpret_cast<bf16_t*>(smem + P1_K);
+    float* sRaw = reinterpret_cast<float*>(smem + P1_K);
+    bf16_t* sOm = reinterpret_cast<bf16_t*>(smem + P1_K);
     bf16_t* sP = reinterpret_cast<bf16_t*>(smem + P1_P);
     f16_t* sTab = reinterpret_cast<f16_t*>(smem + P1_TAB);
-    f16_t* sTabT = reinterpret_cast<f16_t*>(smem + P1_TABT);
+    float* sRed = reinterpret_cast<float*>(smem + P1_RED);
     float* sLam = reinterpret_cast<float*>(smem + P1_G);
     float* sBeta = sLam + 64;
     float* sGam = sBeta + 64;
+    float* sQw = reinterpret_cast<float*>(smem + P1_NW);
+    float* sKw = sQw + KD;
 
     const int bh = blockIdx.x / p.P, j = blockIdx.x % p.P;
     const int b = bh / p.H, h = bh % p.H;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    const int sb = w & 3, hi = w >> 2;
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
-
-    // Readout table of head h in fp16, both orientations; row / column 127 zero.
+    if (tid < KD) {
+        sQw[tid] = p.q_w[tid];
+        sKw[tid] = p.k_w[tid];
+    }
     {
         const float* tb = p.table + (size_t)h * kActive * kSlots;
-        for (int idx = tid; idx < 128 * 128; idx += 256) {
+        for (int idx = tid; idx < 128 * 128; idx += 512) {
             const int r = idx >> 7, m = idx & 127;
-            const f16_t v = (f16_t)(r < kActive ? tb[r * kSlots + m] : 0.f);
-            sTab[r * ZS + m] = v;
-            sTabT[m * ZS + r] = v;
+            sTab[r * RS128 + m] = (f16_t)(r < kActive ? tb[r * kSlots + m] : 0.f);
         }
     }
-
-    // Segment start state: acc[db][mb] holds S[16 db + 4 lg + i][32 w + 16 mb + lr].
-    f32x4 acc[16][2];
+    f32x4 acc[16];
     {
         const float* s0 = p.P > 1 ? p.seg + ((size_t)bh * p.P + j) * SEG
                                   : (p.h0_k ? p.h0_k + (size_t)bh * SEG_K : nullptr);
+        if (s0) {
 #pragma unroll
-        for (int db = 0; db < 16; db++)
+            for (int db = 0; db < 16; db++)
 #pragma unroll
-            for (int mb = 0; mb < 2; mb++)
+                for (int i = 0; i < 4; i++) acc[db][i] = s0[(16 * db + 4 * lg + i) * kSlots + 16 * w + lr];
+        } else {
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    acc[db][mb][i] = s0 ? s0[(16 * db + 4 * lg + i) * kSlots + 32 * w + 16 * mb + lr] : 0.f;
+            for (int db = 0; db < 16; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
     }
+    bf16x8 qraw[4], kraw[4];
+    issue_rows(p, p.q, b, h, n0 * 64, qraw);
+    issue_rows(p, p.k, b, h, n0 * 64, kraw);
+    GateRegs gr = issue_gates(p, b, h, bh, n0 * 64);
+    __syncthreads();  // norm weights and table staged
 
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
-        stage_gates(p, b, h, bh, t0, sLam, sBeta, sGam);
-        // q_hat rows of this wave -> LDS (row-major); k_hat rows -> registers + LDS (transposed).
-        {
-            bf16x8 qf[8];
-            load_norm_row(p, p.q, p.q_w, p.q_eps, b, h, t0 + 16 * w + lr, qf);
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++)
-                *reinterpret_cast<bf16x8*>(sQ + (16 * w + lr) * QS + 32 * ks + 8 * lg) = qf[ks];
+        commit_gates(p, t0, gr, sLam, sBeta, sGam);
+        norm_store_rows(p, t0, qraw, sQw, p.q_eps, sQ);
+        norm_store_rows(p, t0, kraw, sKw, p.k_eps, sK);
+        if (n + 1 < n1) {
+            issue_rows(p, p.q, b, h, t0 + 64, qraw);
+            issue_rows(p, p.k, b, h, t0 + 64, kraw);
+            gr = issue_gates(p, b, h, bh, t0 + 64);
         }
-        bf16x8 kf[8];
-        load_norm_row(p, p.k, p.k_w, p.k_eps, b, h, t0 + 16 * w + lr, kf);
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++)
-#pragma unroll
-            for (int jj = 0; jj < 8; jj++) sKt[(32 * ks + 8 * lg + jj) * TS + 16 * w + lr] = kf[ks][jj];
         __syncthreads();
 
-        const float last = sGam[63];
-        // Write vector (B operand, this wave's 32 slot columns), raw and decayed.
-        bf16x8 wf[2][2], wt[2][2];
+        // Write vector (B operand) for this wave's 16 slot columns, raw and decayed.
+        bf16x8 wf[2], wt[2];
+        {
+            const int m = 16 * w + lr;
 #pragma unroll
-        for (int ss = 0; ss < 2; ss++)
-#pragma unroll
-            for (int mb = 0; mb < 2; mb++) {
-                const int m = 32 * w + 16 * mb + lr;
+            for (int ss = 0; ss < 2; ss++)
 #pragma unroll
                 for (int jj = 0; jj < 8; jj++) {
                     const int s = 32 * ss + 8 * lg + jj;
                     const bf16_t wb = write_elem(sLam[s], sBeta[s], m);
-                    wf[ss][mb][jj] = wb;
-                    wt[ss][mb][jj] = (bf16_t)((float)wb * exp2f(last - sGam[s]));
+                    wf[ss][jj] = wb;
+                    wt[ss][jj] = (bf16_t)((float)wb * sGam[128 + s]);
                 }
-            }
-
-        // Scores for key columns s in [16 w, 16 w + 16), all 64 query rows.
+        }
+        // Masked, decayed scores P[t][s] for key block sb and query blocks 2 hi, 2 hi + 1.
         {
-            f32x4 sc[4];
+            f32x4 sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int tb = 0; tb < 4; tb++) sc[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++)
-#pragma unroll
-                for (int tb = 0; tb < 4; tb++) {
-                    const bf16x8 a = *reinterpret_cast<const bf16x8*>(sQ + (16 * tb + lr) * QS + 32 * ks + 8 * lg);
-                    sc[tb] = mfma_bf16(a, kf[ks], sc[tb]);
-                }
-            const int s = 16 * w + lr;
-            const float gs = sGam[s];
-#pragma unroll
-            for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int t = 16 * tb + 4 * lg + i;
-                    const float v = s <= t ? sc[tb][i] * exp2f(sGam[t] - gs) : 0.f;
-                    sP[t * TS + s] = (bf16_t)v;
-                }
+            for (int ks = 0; ks < 8; ks++) {
+                const bf16x8 kb = load_row<bf16x8>(sK, RS256, 16 * sb, 32 * ks);
+                sc0 = mfma_bf16(load_row<bf16x8>(sQ, RS256, 32 * hi, 32 * ks), kb, sc0);
+                sc1 = mfma_bf16(load_row<bf16x8>(sQ, RS256, 32 * hi + 16, 32 * ks), kb, sc1);
+            }
+            store_scores(sc0, 2 * hi, sb, sGam, sP);
+            store_scores(sc1, 2 * hi + 1, sb, sGam, sP);
         }
         __syncthreads();
 
-        // raw = scale (2^G_t q S_n + P w) for this wave's 32 slot columns.
-        f32x4 out[4][2];
+        // raw = scale (2^G_t q S_n + P w) for this wave's 16 slot columns.
+        f32x4 out[4];
 #pragma unroll
-        for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-            for (int mb = 0; mb < 2; mb++) out[tb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int tb = 0; tb < 4; tb++) out[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
-            bf16x8 bs[2];
+            const bf16x8 bs = state_as_b(acc[2 * ks], acc[2 * ks + 1]);
 #pragma unroll
-            for (int mb = 0; mb < 2; mb++) bs[mb] = state_as_b(acc[2 * ks][mb], acc[2 * ks + 1][mb]);
-#pragma unroll
-            for (int tb = 0; tb < 4; tb++) {
-                const bf16x8 a = load_query_perm(sQ + (16 * tb + lr) * QS + 32 * ks, lg);
-#pragma unroll
-                for (int mb = 0; mb < 2; mb++) out[tb][mb] = mfma_bf16(a, bs[mb], out[tb][mb]);
-            }
+            for (int tb = 0; tb < 4; tb++)
+                out[tb] = mfma_bf16(load_query_perm(sQ + (16 * tb + lr) * RS256 + 32 * ks, lg), bs, out[tb]);
         }
 #pragma unroll
         for (int tb = 0; tb < 4; tb++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float f = exp2f(sGam[16 * tb + 4 * lg + i]);
-#pragma unroll
-                for (int mb = 0; mb < 2; mb++) out[tb][mb][i] *= f;
-            }
+            for (int i = 0; i < 4; i++) out[tb][i] *= sGam[64 + 16 * tb + 4 * lg + i];
 #pragma unroll
         for (int ss = 0; ss < 2; ss++)
 #pragma unroll
-            for (int tb = 0; tb < 4; tb++) {
-                const bf16x8 a = *reinterpret_cast<const bf16x8*>(sP + (16 * tb + lr) * TS + 32 * ss + 8 * lg);
-#pragma unroll
-                for (int mb = 0; mb < 2; mb++) out[tb][mb] = mfma_bf16(a, wf[ss][mb], out[tb][mb]);
-            }
-
-        // State update: S = 2^G_last S + k_hat^T bf16(2^(G_last - G_s) w).
+            for (int tb = 0; tb < 4; tb++)
+                out[tb] = mfma_bf16(load_row<bf16x8>(sP, TS, 16 * tb, 32 * ss), wf[ss], out[tb]);
+        // State update: S = 2^G_last S + k_hat^T bf16(2^(G_last - G_s) w); the
+        // k_hat^T fragments come straight from the row-major k tile.
         {
-            const float dec = exp2f(last);
+            const float dec = sGam[64 + 63];
+#pragma unroll
+            for (int db = 0; db < 16; db++) acc[db] *= dec;
 #pragma unroll
             for (int db = 0; db < 16; db++)
 #pragma unroll
-                for (int mb = 0; mb < 2; mb++) acc[db][mb] *= dec;
-#pragma unroll
-            for (int db = 0; db < 16; db++)
-#pragma unroll
-                for (int ss = 0; ss < 2; ss++) {
-                    const bf16x8 a = *reinterpret_cast<const bf16x8*>(sKt + (16 * db + lr) * TS + 32 * ss + 8 * lg);
-#pragma unroll
-                    for (int mb = 0; mb < 2; mb++) acc[db][mb] = mfma_bf16(a, wt[ss][mb], acc[db][mb]);
-                }
+                for (int ss = 0; ss < 2; ss++)
+                    acc[db] = mfma_bf16(load_tr_bf16(sK, RS256, 32 * ss, 16 * db), wt[ss], acc[db]);
         }
-        __syncthreads();  // k^T and q tiles are dead from here on
-
+        __syncthreads();  // q and k tiles are dead from here on
 #pragma unroll
         for (int tb = 0; tb < 4; tb++)
 #pragma unroll
-            for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    sRaw[(16 * tb + 4 * lg + i) * RS + 32 * w + 16 * mb + lr] = out[tb][mb][i] * p.scale;
+            for (int i = 0; i < 4; i++) sRaw[(16 * tb + 4 * lg + i) * FS + 16 * w + lr] = out[tb][i] * p.scale;
         __syncthreads();
 
-        // Readout (ops/chunk_readout.py:797-909): z = U(lam) raw in fp16.
-#pragma unroll 4
-        for (int it = 0; it < 16; it++) {
-            const int idx = tid + 256 * it, t = idx >> 6, pr = idx & 63;
-            const float e = sRaw[t * RS + 2 * pr], o = sRaw[t * RS + 2 * pr + 1];
+        // Readout (ops/chunk_readout.py:797-909): z = U(lam) raw, in fp16.
+#pragma unroll
+        for (int it = 0; it < 8; it++) {
+            const int idx = tid + 512 * it, t = idx >> 6, pr = idx & 63;
+            const float2 eo = *reinterpret_cast<const float2*>(sRaw + t * FS + 2 * pr);
             float sn, cs;
-            phase_sincos(sLam[t], pr, sn, cs);
-            sZ[t * ZS + 2 * pr] = (f16_t)(cs * e - sn * o);
-            sZ[t * ZS + 2 * pr + 1] = (f16_t)(sn * e + cs * o);
+            pair_sincos(sLam[t], pr, sn, cs);
+            f16_t* d = sZ + t * RS128 + 2 * pr;
+            d[0] = (f16_t)(cs * eo.x - sn * eo.y);
+            d[1] = (f16_t)(sn * eo.x + cs * eo.y);
         }
         __syncthreads();
-        // logits = z table^T for this wave's 16 rows; softmax over the 127 active slots.
-        {
-            f32x4 lgt[8];
+        // logits = z table^T for query block sb and slots 64 hi .. 64 hi + 63;
+        // softmax over the 127 active slots, row max / sum combined across the
+        // two waves of a query block through LDS.
+        f32x4 lgt[4];
 #pragma unroll
-            for (int rb = 0; rb < 8; rb++) lgt[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int u = 0; u < 4; u++) lgt[u] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                const f16x8 a = *reinterpret_cast<const f16x8*>(sZ + (16 * w + lr) * ZS + 32 * ks + 8 * lg);
+        for (int ks = 0; ks < 4; ks++) {
+            const f16x8 a = load_row<f16x8>(sZ, RS128, 16 * sb, 32 * ks);
 #pragma unroll
-                for (int rb = 0; rb < 8; rb++) {
-                    const f16x8 bt = *reinterpret_cast<const f16x8*>(sTab + (16 * rb + lr) * ZS + 32 * ks + 8 * lg);
-                    lgt[rb] = mfma_f16(a, bt, lgt[rb]);
-                }
-            }
-            __syncthreads();  // every wave has consumed its z rows before p overwrites them
+            for (int u = 0; u < 4; u++) lgt[u] = mfma_f16(a, load_row<f16x8>(sTab, RS128, 16 * (4 * hi + u), 32 * ks), lgt[u]);
+        }
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float mx = -INFINITY;
+        for (int i = 0; i < 4; i++) {
+            float mx = -INFINITY;
 #pragma unroll
-                for (int rb = 0; rb < 8; rb++)
-                    if (16 * rb + lr < kActive) mx = fmaxf(mx, lgt[rb][i]);
-                mx = wave_max<16>(mx);
-                float e[8], sum = 0.f;
-#pragma unroll
-                for (int rb = 0; rb < 8; rb++) {
-                    e[rb] = 16 * rb + lr < kActive ? __expf(lgt[rb][i] - mx) : 0.f;
-                    sum += e[rb];
-                }
-                sum = wave_sum<16>(sum);
-                const float inv = 1.f / sum;
-                const int t = 16 * w + 4 * lg + i;
-#pragma unroll
-                for (int rb = 0; rb < 8; rb++) sZ[t * ZS + 16 * rb + lr] = (f16_t)(e[rb] * inv);
-            }
+            for (int u = 0; u < 4; u++)
+                if (16 * (4 * hi + u) + lr < kActive) mx = fmaxf(mx, lgt[u][i]);
+            mx = wave_max<16>(mx);
+            if (lr == 0) sRed[(16 * sb + 4 * lg + i) * 2 + hi] = mx;
         }
         __syncthreads();
-        // u = p table, weights = U(-lam) u -> bf16.
-        {
-            f32x4 uu[8];
 #pragma unroll
-            for (int mb = 0; mb < 8; mb++) uu[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < 4; i++) {
+            const int t = 16 * sb + 4 * lg + i;
+            const float mx = fmaxf(sRed[t * 2], sRed[t * 2 + 1]);
+            float sum = 0.f;
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                lgt[u][i] = 16 * (4 * hi + u) + lr < kActive ? __expf(lgt[u][i] - mx) : 0.f;
+                sum += lgt[u][i];
+            }
+            sum = wave_sum<16>(sum);
+            if (lr == 0) sRed[128 + t * 2 + hi] = sum;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 16 * sb + 4 * lg + i;
+            const float inv = 1.f / (sRed[128 + t * 2] + sRed[128 + t * 2 + 1]);
+#pragma unroll
+            for (int u = 0; u < 4; u++) sZ[t * RS128 + 16 * (4 * hi + u) + lr] = (f16_t)(lgt[u][i] * inv);
+        }
+        __syncthreads();
+        // u = p table (table^T fragments by transpose reads), weights = U(-lam) u.
+        {
+            f32x4 uu[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) uu[u] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int rs = 0; rs < 4; rs++) {
-                const f16x8 a = *reinterpret_cast<const f16x8*>(sZ + (16 * w + lr) * ZS + 32 * rs + 8 * lg);
+                const f16x8 a = load_row<f16x8>(sZ, RS128, 16 * sb, 32 * rs);
 #pragma unroll
-                for (int mb = 0; mb < 8; mb++) {
-                    const f16x8 bt = *reinterpret_cast<const f16x8*>(sTabT + (16 * mb + lr) * ZS + 32 * rs + 8 * lg);
-                    uu[mb] = mfma_f16(a, bt, uu[mb]);
-                }
+                for (int u = 0; u < 4; u++) uu[u] = mfma_f16(a, load_tr_f16(sTab, RS128, 32 * rs, 16 * (4 * hi + u)), uu[u]);
             }
 #pragma unroll
-            for (int mb = 0; mb < 8; mb++)
+            for (int u = 0; u < 4; u++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int t = 16 * w + 4 * lg + i, m = 16 * mb + lr;
-                    const float mine = uu[mb][i];
+                    const int t = 16 * sb + 4 * lg + i, m = 16 * (4 * hi + u) + lr;
+                    const float mine = uu[u][i];
                     const float other = __shfl_xor(mine, 1);
                     float sn, cs;
-                    phase_sincos(sLam[t], m >> 1, sn, cs);
+                    pair_sincos(sLam[t], m >> 1, sn, cs);
                     const float e = (m & 1) ? other : mine, o = (m & 1) ? mine : other;
-                    const float om = (m & 1) ? (-sn * e + cs * o) : (cs * e + sn * o);
-                    sOm[t * ZS + m] = (bf16_t)om;
+                    sOm[t * RS128 + m] = (bf16_t)((m & 1) ? (-sn * e + cs * o) : (cs * e + sn * o));
                 }
         }
         __syncthreads();
         {
             bf16_t* dst = p.omega + ((size_t)bh * p.Tp + t0) * kSlots;
 #pragma unroll
-            for (int it = 0; it < 4; it++) {
-                const int idx = tid + 256 * it, r = idx >> 4, c8 = (idx & 15) * 8;
-                *reinterpret_cast<bf16x8*>(dst + r * kSlots + c8) = *reinterpret_cast<const bf16x8*>(sOm + r * ZS + c8);
+            for (int it = 0; it < 2; it++) {
+                const int idx = tid + 512 * it, r = idx >> 4, c8 = (idx & 15) * 8;
+                *reinterpret_cast<bf16x8*>(dst + r * kSlots + c8) = *reinterpret_cast<const bf16x8*>(sOm + r * RS128 + c8);
             }
         }
         __syncthreads();
@@ -629,29 +701,26 @@ __global__ __launch_bounds__(256) void pass1_kernel(PrefillParams p) {
 #pragma unroll
         for (int db = 0; db < 16; db++)
 #pragma unroll
-            for (int mb = 0; mb < 2; mb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) dst[(16 * db + 4 * lg + i) * kSlots + 32 * w + 16 * mb + lr] = acc[db][mb][i];
+            for (int i = 0; i < 4; i++) dst[(16 * db + 4 * lg + i) * kSlots + 16 * w + lr] = acc[db][i];
     }
 }
 
 // ---------------------------------------------------------------------------
-// 5. Pass 2 (value state). grid = B*H*P, 256 threads. Wave w owns value columns
-// [64 w, 64 w + 64); acc[mb][cb] holds S[16 mb + 4 lg + i][64 w + 16 cb + lr].
-constexpr int P2_OM = 0;                         // bf16 [64][ZS] slot weights (query)
-constexpr int P2_WT = P2_OM + 64 * ZS * 2;       // bf16 [128][TS] w^T
-constexpr int P2_VT = P2_WT + kSlots * TS * 2;   // bf16 [256][TS] v^T; later o staging [64][QS]
-constexpr int P2_P = P2_VT + VD * TS * 2;        // bf16 [64][TS] masked scores
-constexpr int P2_G = P2_P + 64 * TS * 2;
-constexpr int P2_LDS = P2_G + 3 * 64 * 4;
-static_assert(64 * QS * 2 <= VD * TS * 2, "o staging must fit in the v^T tile");
+// 5. Pass 2 (value state). grid = B*H*P, 512 threads. Wave w owns value columns
+// [32 w, 32 w + 32): acc[mb][cb] = S[16 mb + 4 lg + i][32 w + 16 cb + lr].
+constexpr int P2_OM = 0;                          // bf16 [64][RS128] slot weights (query)
+constexpr int P2_W = P2_OM + 64 * RS128 * 2;      // bf16 [64][RS128] w rows (key)
+constexpr int P2_V = P2_W + 64 * RS128 * 2;       // bf16 [64][RS256] v rows; later o staging
+constexpr int P2_P = P2_V + 64 * RS256 * 2;       // bf16 [64][TS] masked scores
+constexpr int P2_G = P2_P + 64 * TS * 2;          // f32 [5][64] gates
+constexpr int P2_LDS = P2_G + 5 * 64 * 4;
 
-__global__ __launch_bounds__(256) void pass2_kernel(PrefillParams p) {
+__global__ __launch_bounds__(512) void pass2_kernel(PrefillParams p) {
     __shared__ __align__(16) unsigned char smem[P2_LDS];
     bf16_t* sOmq = reinterpret_cast<bf16_t*>(smem + P2_OM);
-    bf16_t* sWt = reinterpret_cast<bf16_t*>(smem + P2_WT);
-    bf16_t* sVt = reinterpret_cast<bf16_t*>(smem + P2_VT);
-    bf16_t* sO = reinterpret_cast<bf16_t*>(smem + P2_VT);
+    bf16_t* sW = reinterpret_cast<bf16_t*>(smem + P2_W);
+    bf16_t* sV = reinterpret_cast<bf16_t*>(smem + P2_V);
+    bf16_t* sO = reinterpret_cast<bf16_t*>(smem + P2_V);
     bf16_t* sP = reinterpret_cast<bf16_t*>(smem + P2_P);
     float* sLam = reinterpret_cast<float*>(smem + P2_G);
     float* sBeta = sLam + 64;
@@ -660,163 +729,129 @@ __global__ __launch_bounds__(256) void pass2_kernel(PrefillParams p) {
     const int bh = blockIdx.x / p.P, j = blockIdx.x % p.P;
     const int b = bh / p.H, h = bh % p.H;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    const int sb = w & 3, hi = w >> 2;
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
 
-    f32x4 acc[8][4];
+    f32x4 acc[8][2];
     {
         const float* s0 = p.P > 1 ? p.seg + ((size_t)bh * p.P + j) * SEG + SEG_K
                                   : (p.h0_v ? p.h0_v + (size_t)bh * SEG_V : nullptr);
+        if (s0) {
 #pragma unroll
-        for (int mb = 0; mb < 8; mb++)
+            for (int mb = 0; mb < 8; mb++)
 #pragma unroll
-            for (int cb = 0; cb < 4; cb++)
+                for (int cb = 0; cb < 2; cb++)
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    acc[mb][cb][i] = s0 ? s0[(16 * mb + 4 * lg + i) * VD + 64 * w + 16 * cb + lr] : 0.f;
+                    for (int i = 0; i < 4; i++)
+                        acc[mb][cb][i] = s0[(16 * mb + 4 * lg + i) * VD + 32 * w + 16 * cb + lr];
+        } else {
+#pragma unroll
+            for (int mb = 0; mb < 8; mb++)
+#pragma unroll
+                for (int cb = 0; cb < 2; cb++) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
     }
+    bf16x8 vraw[4], om[2];
+    issue_rows(p, p.v, b, h, n0 * 64, vraw);
+    issue_omega(p, bh, n0 * 64, om);
+    GateRegs gr = issue_gates(p, b, h, bh, n0 * 64);
 
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
-        stage_gates(p, b, h, bh, t0, sLam, sBeta, sGam);
-        {
-            const bf16_t* src = p.omega + ((size_t)bh * p.Tp + t0) * kSlots;
+        commit_gates(p, t0, gr, sLam, sBeta, sGam);
 #pragma unroll
-            for (int it = 0; it < 4; it++) {
-                const int idx = tid + 256 * it, r = idx >> 4, c8 = (idx & 15) * 8;
-                *reinterpret_cast<bf16x8*>(sOmq + r * ZS + c8) = *reinterpret_cast<const bf16x8*>(src + r * kSlots + c8);
-            }
+        for (int it = 0; it < 2; it++) {
+            const int idx = tid + 512 * it, r = idx >> 4, c8 = (idx & 15) * 8;
+            *reinterpret_cast<bf16x8*>(sOmq + r * RS128 + c8) = om[it];
         }
-#pragma unroll
-        for (int it = 0; it < 8; it++) {
-            const int q = lane + 64 * it, s = q >> 3, c8 = (q & 7) * 8;
-            const int t = t0 + s;
-            bf16x8 vv;
-            if (t < p.T) {
-                vv = *reinterpret_cast<const bf16x8*>(p.v + tok_index(p, b, t, h) * VD + 64 * w + c8);
-            } else {
-#pragma unroll
-                for (int jj = 0; jj < 8; jj++) vv[jj] = (bf16_t)0.f;
-            }
-#pragma unroll
-            for (int jj = 0; jj < 8; jj++) sVt[(64 * w + c8 + jj) * TS + s] = vv[jj];
+        store_rows(p, t0, vraw, sV);
+        if (n + 1 < n1) {
+            issue_rows(p, p.v, b, h, t0 + 64, vraw);
+            issue_omega(p, bh, t0 + 64, om);
+            gr = issue_gates(p, b, h, bh, t0 + 64);
         }
         __syncthreads();
-        // Key fragments (the write vector) for key rows s in [16 w, 16 w + 16), and w^T in LDS.
-        bf16x8 wq[4];
+        store_write_rows(sLam, sBeta, sW);
+        __syncthreads();
         {
-            const int s = 16 * w + lr;
-            const float lam = sLam[s], be = sBeta[s];
+            f32x4 sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-                for (int jj = 0; jj < 8; jj += 2) {
-                    const int m = 32 * ks + 8 * lg + jj;
-                    float we, wo;
-                    write_pair(lam, be, m >> 1, we, wo);
-                    wq[ks][jj] = (bf16_t)we;
-                    wq[ks][jj + 1] = (bf16_t)wo;
-                    sWt[m * TS + s] = wq[ks][jj];
-                    sWt[(m + 1) * TS + s] = wq[ks][jj + 1];
-                }
-        }
-        {
-            f32x4 sc[4];
-#pragma unroll
-            for (int tb = 0; tb < 4; tb++) sc[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-                for (int tb = 0; tb < 4; tb++) {
-                    const bf16x8 a = *reinterpret_cast<const bf16x8*>(sOmq + (16 * tb + lr) * ZS + 32 * ks + 8 * lg);
-                    sc[tb] = mfma_bf16(a, wq[ks], sc[tb]);
-                }
-            const int s = 16 * w + lr;
-            const float gs = sGam[s];
-#pragma unroll
-            for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int t = 16 * tb + 4 * lg + i;
-                    const float v = s <= t ? sc[tb][i] * exp2f(sGam[t] - gs) : 0.f;
-                    sP[t * TS + s] = (bf16_t)v;
-                }
+            for (int ks = 0; ks < 4; ks++) {
+                const bf16x8 wb = load_row<bf16x8>(sW, RS128, 16 * sb, 32 * ks);
+                sc0 = mfma_bf16(load_row<bf16x8>(sOmq, RS128, 32 * hi, 32 * ks), wb, sc0);
+                sc1 = mfma_bf16(load_row<bf16x8>(sOmq, RS128, 32 * hi + 16, 32 * ks), wb, sc1);
+            }
+            store_scores(sc0, 2 * hi, sb, sGam, sP);
+            store_scores(sc1, 2 * hi + 1, sb, sGam, sP);
         }
         __syncthreads();
 
-        f32x4 out[4][4];
+        f32x4 out[4][2];
 #pragma unroll
         for (int tb = 0; tb < 4; tb++)
 #pragma unroll
-            for (int cb = 0; cb < 4; cb++) out[tb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int cb = 0; cb < 2; cb++) out[tb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            bf16x8 bs[4];
-#pragma unroll
-            for (int cb = 0; cb < 4; cb++) bs[cb] = state_as_b(acc[2 * ks][cb], acc[2 * ks + 1][cb]);
+            const bf16x8 bs0 = state_as_b(acc[2 * ks][0], acc[2 * ks + 1][0]);
+            const bf16x8 bs1 = state_as_b(acc[2 * ks][1], acc[2 * ks + 1][1]);
 #pragma unroll
             for (int tb = 0; tb < 4; tb++) {
-                const bf16x8 a = load_query_perm(sOmq + (16 * tb + lr) * ZS + 32 * ks, lg);
-#pragma unroll
-                for (int cb = 0; cb < 4; cb++) out[tb][cb] = mfma_bf16(a, bs[cb], out[tb][cb]);
+                const bf16x8 a = load_query_perm(sOmq + (16 * tb + lr) * RS128 + 32 * ks, lg);
+                out[tb][0] = mfma_bf16(a, bs0, out[tb][0]);
+                out[tb][1] = mfma_bf16(a, bs1, out[tb][1]);
             }
         }
 #pragma unroll
         for (int tb = 0; tb < 4; tb++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float f = exp2f(sGam[16 * tb + 4 * lg + i]);
-#pragma unroll
-                for (int cb = 0; cb < 4; cb++) out[tb][cb][i] *= f;
+                const float f = sGam[64 + 16 * tb + 4 * lg + i];
+                out[tb][0][i] *= f;
+                out[tb][1][i] *= f;
             }
-        const float last = sGam[63];
+        const float dec = sGam[64 + 63];
+#pragma unroll
+        for (int mb = 0; mb < 8; mb++)
+#pragma unroll
+            for (int cb = 0; cb < 2; cb++) acc[mb][cb] *= dec;
 #pragma unroll
         for (int ss = 0; ss < 2; ss++) {
-            float f[8];
+            bf16x8 vb[2], vt[2];
 #pragma unroll
-            for (int jj = 0; jj < 8; jj++) f[jj] = exp2f(last - sGam[32 * ss + 8 * lg + jj]);
-            bf16x8 vb[4], vt[4];
+            for (int cb = 0; cb < 2; cb++) {
+                vb[cb] = load_tr_bf16(sV, RS256, 32 * ss, 32 * w + 16 * cb);
 #pragma unroll
-            for (int cb = 0; cb < 4; cb++) {
-                vb[cb] = *reinterpret_cast<const bf16x8*>(sVt + (64 * w + 16 * cb + lr) * TS + 32 * ss + 8 * lg);
-#pragma unroll
-                for (int jj = 0; jj < 8; jj++) vt[cb][jj] = (bf16_t)((float)vb[cb][jj] * f[jj]);
+                for (int jj = 0; jj < 8; jj++) vt[cb][jj] = (bf16_t)((float)vb[cb][jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
             }
 #pragma unroll
             for (int tb = 0; tb < 4; tb++) {
-                const bf16x8 a = *reinterpret_cast<const bf16x8*>(sP + (16 * tb + lr) * TS + 32 * ss + 8 * lg);
-#pragma unroll
-                for (int cb = 0; cb < 4; cb++) out[tb][cb] = mfma_bf16(a, vb[cb], out[tb][cb]);
-            }
-            if (ss == 0) {
-                const float dec = exp2f(last);
-#pragma unroll
-                for (int mb = 0; mb < 8; mb++)
-#pragma unroll
-                    for (int cb = 0; cb < 4; cb++) acc[mb][cb] *= dec;
+                const bf16x8 a = load_row<bf16x8>(sP, TS, 16 * tb, 32 * ss);
+                out[tb][0] = mfma_bf16(a, vb[0], out[tb][0]);
+                out[tb][1] = mfma_bf16(a, vb[1], out[tb][1]);
             }
 #pragma unroll
             for (int mb = 0; mb < 8; mb++) {
-                const bf16x8 a = *reinterpret_cast<const bf16x8*>(sWt + (16 * mb + lr) * TS + 32 * ss + 8 * lg);
-#pragma unroll
-                for (int cb = 0; cb < 4; cb++) acc[mb][cb] = mfma_bf16(a, vt[cb], acc[mb][cb]);
+                const bf16x8 a = load_tr_bf16(sW, RS128, 32 * ss, 16 * mb);
+                acc[mb][0] = mfma_bf16(a, vt[0], acc[mb][0]);
+                acc[mb][1] = mfma_bf16(a, vt[1], acc[mb][1]);
             }
         }
-        __syncthreads();  // v^T is dead; reuse it for the output tile
+        __syncthreads();  // v is dead; reuse it for the output tile
 #pragma unroll
         for (int tb = 0; tb < 4; tb++)
 #pragma unroll
-            for (int cb = 0; cb < 4; cb++)
+            for (int cb = 0; cb < 2; cb++)
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    sO[(16 * tb + 4 * lg + i) * QS + 64 * w + 16 * cb + lr] = (bf16_t)out[tb][cb][i];
+                    sO[(16 * tb + 4 * lg + i) * RS256 + 32 * w + 16 * cb + lr] = (bf16_t)out[tb][cb][i];
         __syncthreads();
 #pragma unroll
-        for (int it = 0; it < 8; it++) {
-            const int idx = tid + 256 * it, r = idx >> 5, c8 = (idx & 31) * 8;
-            const int t = t0 + r;
-            if (t < p.T)
-                *reinterpret_cast<bf16x8*>(p.o + tok_index(p, b, t, h) * VD + c8) =
-                    *reinterpret_cast<const bf16x8*>(sO + r * QS + c8);
+        for (int it = 0; it < 4; it++) {
+            const int idx = tid + 512 * it, r = idx >> 5, c8 = (idx & 31) * 8;
+            if (t0 + r < p.T)
+                *reinterpret_cast<bf16x8*>(p.o + tok_index(p, b, t0 + r, h) * VD + c8) =
+                    *reinterpret_cast<const bf16x8*>(sO + r * RS256 + c8);
         }
         __syncthreads();
     }
@@ -826,9 +861,9 @@ __global__ __launch_bounds__(256) void pass2_kernel(PrefillParams p) {
 #pragma unroll
         for (int mb = 0; mb < 8; mb++)
 #pragma unroll
-            for (int cb = 0; cb < 4; cb++)
+            for (int cb = 0; cb < 2; cb++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) dst[(16 * mb + 4 * lg + i) * VD + 64 * w + 16 * cb + lr] = acc[mb][cb][i];
+                for (int i = 0; i < 4; i++) dst[(16 * mb + 4 * lg + i) * VD + 32 * w + 16 * cb + lr] = acc[mb][cb][i];
     }
 }
 
@@ -892,11 +927,11 @@ int launch_prefill(const PrefillParams& p, hipStream_t stream) {
     const int BH = p.B * p.H;
     hipLaunchKernelGGL(clock_kernel, dim3(BH), dim3(256), 0, stream, p);
     if (p.P > 1) {
-        hipLaunchKernelGGL(segment_state_kernel, dim3(BH * (p.P - 1), 2), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL(segment_state_kernel, dim3(BH * (p.P - 1), 2), dim3(512), 0, stream, p);
         hipLaunchKernelGGL(carry_kernel, dim3(BH, SEG / 1024), dim3(256), 0, stream, p);
     }
-    hipLaunchKernelGGL(pass1_kernel, dim3(BH * p.P), dim3(256), 0, stream, p);
-    hipLaunchKernelGGL(pass2_kernel, dim3(BH * p.P), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(pass1_kernel, dim3(BH * p.P), dim3(512), 0, stream, p);
+    hipLaunchKernelGGL(pass2_kernel, dim3(BH * p.P), dim3(512), 0, stream, p);
     return 0;
 }
 

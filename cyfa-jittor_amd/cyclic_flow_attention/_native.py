@@ -125,14 +125,58 @@ def chunk_workspace_bytes(B, T, H, K, V, M=128, C=64):
     return int(load_library().cyfa_chunk_workspace_bytes(B, T, H, K, V, M, C))
 
 
+class LaunchTimer:
+    """Records HIP events around every library launch while active.
+
+    Events are recorded on the stream the kernels are enqueued on (torch's
+    current stream), so ``results()`` gives per-call device durations without
+    a host sync per call."""
+
+    def __init__(self):
+        self.records = []
+
+    def __enter__(self):
+        _TIMERS.append(self)
+        return self
+
+    def __exit__(self, *exc):
+        _TIMERS.remove(self)
+
+    def results(self):
+        """{entry point: [milliseconds per call]} (synchronises the device)."""
+        torch.cuda.synchronize()
+        out = {}
+        for name, start, end in self.records:
+            out.setdefault(name, []).append(start.elapsed_time(end))
+        return out
+
+
+_TIMERS = []
+
+
+def _timed(name, fn):
+    if not _TIMERS:
+        return fn()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    rc = fn()
+    end.record()
+    for t in _TIMERS:
+        t.records.append((name, start, end))
+    return rc
+
+
 def chunk_fwd(args: CyfaChunkArgs, device):
-    rc = load_library().cyfa_chunk_fwd(ctypes.byref(args), stream_handle(device))
+    lib = load_library()
+    rc = _timed("cyfa_chunk_fwd", lambda: lib.cyfa_chunk_fwd(ctypes.byref(args), stream_handle(device)))
     if rc != CYFA_OK:
         _raise(rc, "cyfa_chunk_fwd failed")
 
 
 def decode_step(args: CyfaDecodeArgs, device):
-    rc = load_library().cyfa_decode_step(ctypes.byref(args), stream_handle(device))
+    lib = load_library()
+    rc = _timed("cyfa_decode_step", lambda: lib.cyfa_decode_step(ctypes.byref(args), stream_handle(device)))
     if rc != CYFA_OK:
         _raise(rc, "cyfa_decode_step failed")
 
