@@ -53,6 +53,9 @@ def parse():
     ap.add_argument("--config", default="cyclic_flow_attention_400m.json")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="run one fp32 copy kernel (out = 1.0 * in) of this many MiB before the prefill, "
+                         "as the known-size reference for HBM byte counters")
     return ap.parse_args()
 
 
@@ -192,6 +195,15 @@ def main():
     H = config.num_heads
     gen = torch.Generator().manual_seed(0)
     ids = torch.randint(0, config.vocab_size, (args.batch, args.seq_len), generator=gen).to(dev)
+
+    if args.calibration_copy_mib:
+        n = args.calibration_copy_mib * (1 << 20) // 4
+        src = torch.randn(n, device=dev)
+        dst = torch.empty_like(src)
+        torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {args.calibration_copy_mib} MiB read + {args.calibration_copy_mib} MiB written")
+        del src, dst
 
     log(f"prefill B={args.batch} T={args.seq_len}: warmup {args.warmup}, timed {args.steps}")
     elapsed, op_ms = time_prefill(model, ids, args.steps, args.warmup)
