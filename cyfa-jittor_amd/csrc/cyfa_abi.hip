@@ -154,6 +154,7 @@ int cyfa_chunk_fwd(const CyfaChunkArgs* a, void* hip_stream) {
     p.lam = (float*)(base + ws.lam);
     p.seg = (float*)(base + ws.seg);
     p.seg_decay = (float*)(base + ws.seg_decay);
+    p.raw = (__bf16*)(base + ws.raw);
     p.omega = (__bf16*)(base + ws.omega);
     cyfa::launch_prefill(p, (hipStream_t)hip_stream);
     return check_launch("cyfa_chunk_fwd");

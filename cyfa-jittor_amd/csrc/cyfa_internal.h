@@ -36,11 +36,12 @@ struct PrefillParams {
     float* lam;        // [B*H, Tp] clock per token
     float* seg;        // [B*H, P, K*128 + 128*V] segment-local states, then segment start states
     float* seg_decay;  // [B*H, P] product of alpha over each segment
+    __bf16* raw;       // [2, B*H, Tp, 128] pass-1 output of each 128-wide key half
     __bf16* omega;     // [B*H, Tp, 128] slot weights between the two passes
 };
 
 struct WorkspaceLayout {
-    size_t lam, seg, seg_decay, omega, total;
+    size_t lam, seg, seg_decay, raw, omega, total;
 };
 
 void choose_segments(int BH, int N, int* P, int* L);

@@ -1,34 +1,42 @@
 // cyfa_prefill.hip -- chunkwise two-pass CyFA prefill for gfx950 (K = V = 256, M = 128).
 //
 // Pipeline for one call (all kernels on the caller's stream):
-//   1. clock_kernel      lam_t = clock0 + sum_{s<=t} delta_s, final clock.
-//   2. segment_state     (only when a sequence is split into P > 1 segments)
-//                        segment-local end states of both passes from a zero
-//                        start, and the product of alpha over each segment.
-//   3. carry_kernel      affine carry over segments: S_in[j+1] = a_j S_in[j] + U_j.
-//   4. pass1_kernel      per segment, sweep its 64-token chunks with the fp32 key
-//                        state [256 x 128] held in registers: raw = scale (2^G q S
-//                        + P w), P = mask 2^(G_t-G_s) q k^T; state update
-//                        S = 2^G_last S + k^T bf16(2^(G_last-G_s) w); fused slot
-//                        readout epilogue -> slot weights (bf16).
-//   5. pass2_kernel      the same sweep for the value state [128 x 256] with
-//                        query = slot weights, key = w, value = v -> o (bf16).
-// The sweep kernels run 8 waves (512 threads); each wave holds 1/8 of the fp32
-// state as MFMA accumulators, and the global loads of chunk n + 1 are issued
-// into registers before chunk n computes. All GEMM-shaped work runs on
-// v_mfma_f32_16x16x32_{bf16,f16} with fp32 accumulation. Every 64-token tile
-// (q_hat, k_hat, w, v, slot weights) is staged once in LDS, token-major; the
-// operands that contract over tokens are read with the gfx950 LDS transpose
-// read. The sweep keeps each segment's state on chip from its first to its
-// last chunk; only segment boundary states (one per L chunks) touch HBM.
+//   1. clock_kernel     lam_t = clock0 + sum_{s<=t} delta_s, final clock.
+//   2. segment_state    (only when a sequence is split into P > 1 segments)
+//                       segment-local end states of both passes from a zero
+//                       start, and the product of alpha over each segment.
+//   3. carry_kernel     affine carry over segments: S_in[j+1] = a_j S_in[j] + U_j.
+//   4. pass1_kernel     per (segment, 128-wide key half): sweep the segment's
+//                       64-token chunks with that half of the fp32 key state
+//                       [128 x 128] held in registers and write the half's
+//                       pass-1 output scale (2^G q S + P w) as bf16.
+//   5. readout_kernel   raw = sum of the two halves; z = U(lam) raw;
+//                       p = softmax(table z); u = table^T p; slot weights
+//                       bf16(U(-lam) u) (ops/chunk_readout.py:797-909).
+//   6. pass2_kernel     per (segment, 128-wide value half): the same sweep for
+//                       that half of the value state [128 x 128] with query =
+//                       slot weights, key = w, value = v -> o (bf16).
+// Splitting pass 1 over the key dimension follows the reference, which forms
+// the pass-1 output as two 128-wide key slices, each scaled and rounded to
+// bf16, and sums them (ops/chunk_o.py:240-250, 369-374). Splitting pass 2 over
+// the value dimension is exact. Each sweep workgroup (8 waves) then needs
+// under 80 KB of LDS and 128 registers per lane, so two independent
+// workgroups share a CU and hide each other's LDS, barrier and global-load
+// latency. All GEMM-shaped work runs on v_mfma_f32_16x16x32_{bf16,f16} with
+// fp32 accumulation; 64-token tiles are staged once in LDS, token-major, and
+// operands that contract over tokens use the gfx950 LDS transpose read. A
+// segment's state stays on chip from its first to its last chunk; only
+// segment boundary states (one per L chunks) touch HBM.
 //
 // Lane conventions of the 16x16x32 MFMA (wave64, lane l, lr = l & 15, lg = l >> 4):
 //   A[row][k]: row = lr, k = 8 lg + j (j = 0..7)     B[k][col]: col = lr, k = 8 lg + j
 //   C[row][col]: col = lr, row = 4 lg + i (i = 0..3)
-// A state block pair held as C (rows 32 ks .. 32 ks + 31) is used directly as the
-// B operand of the query product by pairing element j < 4 with row 32 ks + 4 lg + j
-// and j >= 4 with row 32 ks + 16 + 4 lg + (j - 4); the query fragment is read
-// with the same k order.
+// A pair of state blocks held as C (rows 32 ks .. 32 ks + 31) serves directly as
+// the A operand of a product that contracts over those rows, with element j < 4
+// taken from row 32 ks + 4 lg + j and j >= 4 from row 32 ks + 16 + 4 lg + (j - 4);
+// the other operand is read in the same k order. The sweeps compute their
+// outputs transposed (output coordinate = C row, token = C column), so each lane
+// ends with four consecutive output coordinates of one token.
 #include <stdlib.h>
 
 #include "cyfa_device.h"
@@ -40,43 +48,119 @@ namespace {
 
 constexpr int KD = 256;             // key / query dim of pass 1
 constexpr int VD = 256;             // value dim of pass 2
+constexpr int HALF = 128;           // key / value columns per sweep workgroup
 constexpr int SEG_K = KD * kSlots;  // key-state elements
 constexpr int SEG_V = kSlots * VD;  // value-state elements
 constexpr int SEG = SEG_K + SEG_V;
 
-// Row strides (elements) of the LDS tiles. The 16-bit strides are 8 dwords
-// modulo the 64 LDS banks, so the four rows a transpose read touches per
-// 16-lane block fall on disjoint banks.
-constexpr int RS256 = 256 + 16;  // 64 x 256 bf16 tiles
-constexpr int RS128 = 128 + 16;  // 64 x 128 16-bit tiles and the 128 x 128 table
-constexpr int TS = 64 + 8;       // 64 x 64 score tile
-constexpr int FS = 128 + 4;      // 64 x 128 fp32 tile
+// Row strides (16-bit elements) of the LDS tiles: 8 dwords past a multiple of
+// the 64 banks, so the rows a transpose read touches per 16-lane block fall on
+// disjoint banks.
+constexpr int RS = 128 + 16;  // 64 x 128 tiles and the 128 x 128 table
+constexpr int TS = 64 + 8;    // 64 x 64 score tile
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ size_t tok_index(const PrefillParams& p, int b, int t, int h) {
     return ((size_t)b * p.T + t) * p.H + h;
 }
 
-// Chunk gates, split into an issue step (global loads into registers, wave 0,
-// lane = token) and a commit step (in-chunk scan of g in log2 units,
-// ops/utils.py:495-520, and the LDS writes), so that the loads of chunk n + 1
-// can be in flight while chunk n computes. LDS per token: sLam = reduced clock
-// (lam mod 127) / 127, sBeta, sGam = G_t, sGam[64 + t] = 2^G_t and
-// sGam[128 + t] = 2^(G_last - G_t).
+// Keeps the scheduler from hoisting the LDS fragment loads of later MFMA steps
+// above this point (which would raise register pressure past the 128-register
+// budget of two workgroups per CU).
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// Global memory in the sweeps goes through buffer instructions: a 128-bit
+// resource per stream in scalar registers and one 32-bit byte offset per lane,
+// which keeps the address arithmetic out of the vector register budget.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, size_t bytes) {
+    const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
+
+__device__ __forceinline__ bf16x8 ld_b128(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+__device__ __forceinline__ float ld_f32(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+__device__ __forceinline__ void st_b64(rsrc_t r, uint32_t off, uint32_t soff, bf16x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, off, soff, 0);
+}
+
+// The streams of one (batch, head) sequence: q, k, v, o rows of 512 bytes
+// H * 512 bytes apart, g / beta H * 4 bytes apart, lam contiguous.
+struct Seq {
+    rsrc_t q, k, v, o, g, beta, lam;
+    uint32_t row16, row4;
+};
+
+__device__ __forceinline__ Seq make_seq(const PrefillParams& p, int b, int h, int bh) {
+    const size_t first = (size_t)b * p.T * p.H + h;              // token row of (b, 0, h)
+    const size_t span = ((size_t)(p.T - 1) * p.H + 1);           // rows up to (b, T - 1, h)
+    Seq s;
+    s.q = make_rsrc(p.q + first * KD, span * KD * 2);
+    s.k = make_rsrc(p.k + first * KD, span * KD * 2);
+    s.v = make_rsrc(p.v + first * VD, span * VD * 2);
+    s.o = make_rsrc(p.o + first * VD, span * VD * 2);
+    s.g = make_rsrc(p.g + first, span * 4);
+    s.beta = make_rsrc(p.beta + first, span * 4);
+    s.lam = make_rsrc(p.lam + (size_t)bh * p.Tp, (size_t)p.Tp * 4);
+    s.row16 = (uint32_t)p.H * KD * 2;
+    s.row4 = (uint32_t)p.H * 4;
+    return s;
+}
+
+// Sweep workgroups come in pairs (the two halves of one segment). Workgroup
+// ids are dealt round-robin to the 8 XCDs, so the pair is placed 8 ids apart:
+// both halves run on the same XCD at about the same time and the second read
+// of the shared q / k rows hits that XCD's L2.
+struct SweepBlock {
+    int unit, half;
+};
+
+__device__ __forceinline__ SweepBlock sweep_block() {
+    const int bid = blockIdx.x;
+    return {((bid >> 4) << 3) | (bid & 7), (bid >> 3) & 1};
+}
+
+int sweep_grid(int units) { return (units + 7) / 8 * 16; }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over the 8 lanes of an aligned octet: quad_perm [1,0,3,2], [2,3,0,1],
+// then row_half_mirror (lane i of the octet reads lane 7 - i).
+__device__ __forceinline__ float octet_sum(float x) {
+    x += dpp<0xB1>(x);
+    x += dpp<0x4E>(x);
+    x += dpp<0x141>(x);
+    return x;
+}
+
+// Chunk gates, loaded by every wave with lane = token (issue) and scanned /
+// staged in LDS by wave 0 (commit): the in-chunk scan of g in log2 units
+// (ops/utils.py:495-520). LDS per token: sLam = reduced clock (lam mod 127) /
+// 127, sBeta, sGam = G_t, sGam[64 + t] = 2^G_t, sGam[128 + t] = 2^(G_last - G_t).
 struct GateRegs {
     float g, beta, lam;
 };
 
-__device__ __forceinline__ GateRegs issue_gates(const PrefillParams& p, int b, int h, int bh, int t0) {
-    GateRegs r{0.f, 0.f, 0.f};
-    const int tid = threadIdx.x;
-    if (tid < 64) {
-        const int t = t0 + tid;
-        const size_t i = tok_index(p, b, t < p.T ? t : p.T - 1, h);
-        r.g = p.g[i];
-        r.beta = p.beta[i];
-        r.lam = p.lam[(size_t)bh * p.Tp + t];
-    }
+__device__ __forceinline__ GateRegs issue_gates(const Seq& sq, int T, int t0) {
+    const int t = t0 + (threadIdx.x & 63);
+    const uint32_t off = (uint32_t)(t < T ? t : T - 1) * sq.row4;
+    GateRegs r;
+    r.g = ld_f32(sq.g, off);
+    r.beta = ld_f32(sq.beta, off);
+    r.lam = ld_f32(sq.lam, (uint32_t)t * 4);
     return r;
 }
 
@@ -140,81 +224,93 @@ __device__ __forceinline__ V8 load_row(const T* X, int ld, int r0, int k0) {
     return *reinterpret_cast<const V8*>(X + (r0 + (l & 15)) * ld + k0 + 8 * (l >> 4));
 }
 
-// Rows [t0, t0 + 64) of a [B, T, H, 256] bf16 tensor, four 16-byte loads per
-// thread of a 512-thread block: row (tid >> 5) + 16 it, columns 8 (tid & 31) .. + 8.
-// Rows past T are clamped to T - 1 (and zeroed when stored).
-__device__ __forceinline__ void issue_rows(const PrefillParams& p, const bf16_t* x, int b, int h, int t0, bf16x8 raw[4]) {
-    const int tid = threadIdx.x;
+// Full 256-wide rows [t0, t0 + 64) of a [B, T, H, 256] bf16 tensor for a
+// 512-thread block: thread tid holds row tid >> 3, columns 8 c + 64 it
+// (c = tid & 7, it = 0..3). Rows past T are clamped to T - 1 (zeroed when stored).
+__device__ __forceinline__ void issue_full_rows(const Seq& sq, rsrc_t x, int T, int t0, bf16x8 raw[4]) {
+    const int t = t0 + (threadIdx.x >> 3);
+    const uint32_t off = (uint32_t)(t < T ? t : T - 1) * sq.row16 + 16 * (threadIdx.x & 7);
 #pragma unroll
-    for (int it = 0; it < 4; it++) {
-        const int t = t0 + (tid >> 5) + 16 * it;
-        raw[it] = *reinterpret_cast<const bf16x8*>(x + tok_index(p, b, t < p.T ? t : p.T - 1, h) * KD + 8 * (tid & 31));
-    }
+    for (int it = 0; it < 4; it++) raw[it] = ld_b128(x, off + 128 * it);
 }
 
-// RMS-normalise those rows and store them row-major into dst [64][RS256]:
-// x_hat = bf16(x rsqrt(mean x^2 + eps) w) (ops/qk_norm.py:64-107, 206-233).
-// A row's 32 chunks live in one half-wave; wn is the weight in LDS.
-__device__ __forceinline__ void norm_store_rows(const PrefillParams& p, int t0, const bf16x8 raw[4], const float* wn,
-                                                float eps, bf16_t* dst) {
-    const int tid = threadIdx.x, c8 = 8 * (tid & 31);
-    const float4 w0 = *reinterpret_cast<const float4*>(wn + c8);
-    const float4 w1 = *reinterpret_cast<const float4*>(wn + c8 + 4);
-    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+// x_hat = bf16(x rsqrt(mean x^2 + eps) w) over the full row (ops/qk_norm.py:64-107,
+// 206-233); the columns of half y are stored into dst [64][RS] (zero past T).
+// wn is the half's norm weight in LDS.
+__device__ __forceinline__ void norm_store_half(const PrefillParams& p, int t0, const bf16x8 raw[4], const float* wn,
+                                                float eps, int y, bf16_t* dst) {
+    const int r = threadIdx.x >> 3, c = threadIdx.x & 7;
+    float ss = 0.f;
 #pragma unroll
-    for (int it = 0; it < 4; it++) {
-        const int r = (tid >> 5) + 16 * it;
-        float ss = 0.f;
+    for (int it = 0; it < 4; it++)
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const float v = (float)raw[it][j];
             ss = fmaf(v, v, ss);
         }
-        ss = wave_sum<32>(ss);
-        const float rs = t0 + r < p.T ? rsqrtf(ss * (1.f / KD) + eps) : 0.f;
+    ss = octet_sum(ss);
+    const float rs = t0 + r < p.T ? rsqrtf(ss * (1.f / KD) + eps) : 0.f;
+#pragma unroll
+    for (int h2 = 0; h2 < 2; h2++) {
+        const bf16x8 x = y ? raw[2 + h2] : raw[h2];
+        const int col = 8 * c + 64 * h2;
+        const float4 w0 = *reinterpret_cast<const float4*>(wn + col);
+        const float4 w1 = *reinterpret_cast<const float4*>(wn + col + 4);
+        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
         bf16x8 o;
 #pragma unroll
-        for (int j = 0; j < 8; j++) o[j] = (bf16_t)((float)raw[it][j] * rs * wv[j]);
-        *reinterpret_cast<bf16x8*>(dst + r * RS256 + c8) = o;
+        for (int j = 0; j < 8; j++) o[j] = (bf16_t)((float)x[j] * rs * wv[j]);
+        *reinterpret_cast<bf16x8*>(dst + r * RS + col) = o;
     }
 }
 
-// Store rows of v (no normalisation), zero past T.
-__device__ __forceinline__ void store_rows(const PrefillParams& p, int t0, const bf16x8 raw[4], bf16_t* dst) {
-    const int tid = threadIdx.x, c8 = 8 * (tid & 31);
+// Columns [128 y, 128 y + 128) of rows [t0, t0 + 64) of a [B, T, H, 256] bf16
+// tensor: thread tid holds row tid >> 3, columns 128 y + 8 c + 64 it (it = 0, 1).
+__device__ __forceinline__ void issue_half_rows(const Seq& sq, rsrc_t x, int T, int t0, int y, bf16x8 raw[2]) {
+    const int t = t0 + (threadIdx.x >> 3);
+    const uint32_t off = (uint32_t)(t < T ? t : T - 1) * sq.row16 + 2 * HALF * y + 16 * (threadIdx.x & 7);
 #pragma unroll
-    for (int it = 0; it < 4; it++) {
-        const int r = (tid >> 5) + 16 * it;
+    for (int it = 0; it < 2; it++) raw[it] = ld_b128(x, off + 128 * it);
+}
+
+// Slot-weight rows [t0, t0 + 64) of the readout output (256-byte rows), same
+// thread mapping.
+__device__ __forceinline__ void issue_omega(rsrc_t om_rows, int t0, bf16x8 om[2]) {
+    const uint32_t off = (uint32_t)(t0 + (threadIdx.x >> 3)) * (kSlots * 2) + 16 * (threadIdx.x & 7);
+#pragma unroll
+    for (int it = 0; it < 2; it++) om[it] = ld_b128(om_rows, off + 128 * it);
+}
+
+// Store 64 x 128 rows held with that mapping into dst [64][RS]; rows at or past
+// `valid` are zeroed.
+__device__ __forceinline__ void store_half_rows(const bf16x8 raw[2], int valid, bf16_t* dst) {
+    const int r = threadIdx.x >> 3, c = threadIdx.x & 7;
+#pragma unroll
+    for (int it = 0; it < 2; it++) {
         bf16x8 o = raw[it];
-        if (t0 + r >= p.T) {
+        if (r >= valid) {
 #pragma unroll
             for (int j = 0; j < 8; j++) o[j] = (bf16_t)0.f;
         }
-        *reinterpret_cast<bf16x8*>(dst + r * RS256 + c8) = o;
+        *reinterpret_cast<bf16x8*>(dst + r * RS + 8 * c + 64 * it) = o;
     }
 }
 
-// Slot-weight rows [t0, t0 + 64) of the pass-1 output: two 16-byte loads per thread.
-__device__ __forceinline__ void issue_omega(const PrefillParams& p, int bh, int t0, bf16x8 om[2]) {
-    const bf16_t* src = p.omega + ((size_t)bh * p.Tp + t0) * kSlots;
-#pragma unroll
-    for (int it = 0; it < 2; it++) {
-        const int idx = threadIdx.x + 512 * it, r = idx >> 4, c8 = (idx & 15) * 8;
-        om[it] = *reinterpret_cast<const bf16x8*>(src + r * kSlots + c8);
-    }
-}
-
-// Write vector of the chunk, w [64 tokens][128] bf16 row-major (ops/utils.py:664-702):
-// 4096 pairs over 512 threads.
-__device__ __forceinline__ void store_write_rows(const float* sLam, const float* sBeta, bf16_t* dst) {
+// Write vector of the chunk, w [64 tokens][128] bf16 row-major (ops/utils.py:664-702),
+// from the gate registers (lane = token): wave w covers tokens w + 8 it, lane = pair.
+__device__ __forceinline__ void store_write_tile(const GateRegs& gr, int valid, bf16_t* dst) {
+    const int lane = threadIdx.x & 63, w = wave_id();
+    const float lamr = reduced_clock(gr.lam);
+    const float beta = lane < valid ? gr.beta : 0.f;
 #pragma unroll
     for (int it = 0; it < 8; it++) {
-        const int idx = threadIdx.x + 512 * it, s = idx >> 6, pr = idx & 63;
+        const int s = w + 8 * it;
+        const float ls = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lamr), s));
+        const float bs = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, beta), s));
         float we, wo;
-        write_pair(sLam[s], sBeta[s], pr, we, wo);
-        bf16_t* d = dst + s * RS128 + 2 * pr;
-        d[0] = (bf16_t)we;
-        d[1] = (bf16_t)wo;
+        write_pair(ls, bs, lane, we, wo);
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<bf16x2*>(dst + s * RS + 2 * lane) = bf16x2{(bf16_t)we, (bf16_t)wo};
     }
 }
 
@@ -237,6 +333,17 @@ __device__ __forceinline__ void store_scores(const f32x4& sc, int tb, int sb, co
     }
 }
 
+// The 10 causal 16 x 16 score blocks (query block tb >= key block sb): wave w
+// takes blocks w and w + 8.
+__device__ __forceinline__ void score_block(int blk, int& tb, int& sb) {
+    tb = blk < 1 ? 0 : blk < 3 ? 1 : blk < 6 ? 2 : 3;
+    sb = blk - tb * (tb + 1) / 2;
+}
+
+__device__ __forceinline__ void zero_scores(bf16_t* sP) {
+    for (int idx = threadIdx.x; idx < 64 * TS / 2; idx += blockDim.x) reinterpret_cast<uint32_t*>(sP)[idx] = 0u;
+}
+
 __device__ __forceinline__ bf16x8 cat4(const bf16x4& lo, const bf16x4& hi) {
     bf16x8 r;
     r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
@@ -244,14 +351,17 @@ __device__ __forceinline__ bf16x8 cat4(const bf16x4& lo, const bf16x4& hi) {
     return r;
 }
 
-// Query fragment for the state product, in the k order of a C-block pair.
-__device__ __forceinline__ bf16x8 load_query_perm(const bf16_t* row_ks, int lg) {
+// Row fragment in the k order of a C-block pair: elements row[4 lg .. + 4] and
+// row[16 + 4 lg .. + 4] of a 32-wide k step.
+__device__ __forceinline__ bf16x8 load_row_perm(const bf16_t* row_ks, int lg) {
     const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row_ks + 4 * lg);
     const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row_ks + 16 + 4 * lg);
     return cat4(lo, hi);
 }
 
-__device__ __forceinline__ bf16x8 state_as_b(const f32x4& top, const f32x4& bottom) {
+// A C-block pair of the fp32 state as a bf16 operand (the reference emits the
+// per-chunk states in bf16, ops/chunk_h.py:238-327).
+__device__ __forceinline__ bf16x8 state_frag(const f32x4& top, const f32x4& bottom) {
     bf16x8 r;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -259,6 +369,10 @@ __device__ __forceinline__ bf16x8 state_as_b(const f32x4& top, const f32x4& bott
         r[4 + i] = (bf16_t)bottom[i];
     }
     return r;
+}
+
+__device__ __forceinline__ bf16x4 to_bf16x4(const f32x4& x, float s) {
+    return bf16x4{(bf16_t)(x[0] * s), (bf16_t)(x[1] * s), (bf16_t)(x[2] * s), (bf16_t)(x[3] * s)};
 }
 
 // ---------------------------------------------------------------------------
@@ -301,120 +415,101 @@ __global__ __launch_bounds__(256) void clock_kernel(PrefillParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// 2. Segment-local end states from a zero start. grid = (B*H*(P-1), 2), y = pass;
-// 512 threads. Pass 0: wave w owns key-state columns [16 w, 16 w + 16)
-// (acc[db] = S[16 db + 4 lg + i][16 w + lr]). Pass 1: wave w owns value-state
-// columns [32 w, 32 w + 32) (acc[mb][cb] = S[16 mb + 4 lg + i][32 w + 16 cb + lr]).
-constexpr int SG_K = 0;                     // pass 0: bf16 [64][RS256] k_hat rows
-constexpr int SG_W = 0;                     // pass 1: bf16 [64][RS128] w rows
-constexpr int SG_V = 64 * RS128 * 2;        // pass 1: bf16 [64][RS256] v rows
-constexpr int SG_G = SG_V + 64 * RS256 * 2; // f32 [5][64] gates
-constexpr int SG_NW = SG_G + 5 * 64 * 4;    // f32 [256] k norm weight
-constexpr int SG_LDS = SG_NW + KD * 4;
-static_assert(64 * RS256 * 2 <= SG_G, "k tile overlaps the gates");
+// 2. Segment-local end states from a zero start. grid = (B*H*(P-1), 4), 512
+// threads. y = 0, 1: key-state rows [128 y, 128 y + 128); wave w owns columns
+// [16 w, 16 w + 16): acc[kb] = S[128 y + 16 kb + 4 lg + i][16 w + lr].
+// y = 2, 3: value-state columns [128 (y-2), + 128); wave w owns 16 of them:
+// acc[mb] = S[16 mb + 4 lg + i][128 (y-2) + 16 w + lr].
+constexpr int SG_A = 0;                   // bf16 [64][RS]: k_hat half (key) or w (value)
+constexpr int SG_B = SG_A + 64 * RS * 2;  // bf16 [64][RS]: v half (value)
+constexpr int SG_G = SG_B + 64 * RS * 2;  // f32 [5][64] gates
+constexpr int SG_NW = SG_G + 5 * 64 * 4;  // f32 [128] k norm weight (half)
+constexpr int SG_LDS = SG_NW + HALF * 4;
 
-__global__ __launch_bounds__(512) void segment_state_kernel(PrefillParams p) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void segment_state_kernel(PrefillParams p) {
     __shared__ __align__(16) unsigned char smem[SG_LDS];
+    bf16_t* sA = reinterpret_cast<bf16_t*>(smem + SG_A);
+    bf16_t* sB = reinterpret_cast<bf16_t*>(smem + SG_B);
     float* sLam = reinterpret_cast<float*>(smem + SG_G);
     float* sBeta = sLam + 64;
     float* sGam = sBeta + 64;
     float* sNw = reinterpret_cast<float*>(smem + SG_NW);
     const int P1 = p.P - 1;
-    const int bh = blockIdx.x / P1, j = blockIdx.x % P1, pass = blockIdx.y;
+    const int bh = blockIdx.x / P1, j = blockIdx.x % P1, part = blockIdx.y;
     const int b = bh / p.H, h = bh % p.H;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), lr = lane & 15, lg = lane >> 4;
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
     float* out = p.seg + ((size_t)bh * p.P + j) * SEG;
-    if (tid < KD) sNw[tid] = p.k_w[tid];
-
-    if (pass == 0) {
-        bf16_t* sK = reinterpret_cast<bf16_t*>(smem + SG_K);
-        f32x4 acc[16];
+    f32x4 acc[8];
 #pragma unroll
-        for (int db = 0; db < 16; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int x = 0; x < 8; x++) acc[x] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const Seq sq = make_seq(p, b, h, bh);
+    GateRegs gr = issue_gates(sq, p.T, n0 * 64);
+
+    if (part < 2) {
+        const int y = part;
+        if (tid < HALF) sNw[tid] = p.k_w[HALF * y + tid];
         bf16x8 kraw[4];
-        issue_rows(p, p.k, b, h, n0 * 64, kraw);
-        GateRegs gr = issue_gates(p, b, h, bh, n0 * 64);
+        issue_full_rows(sq, sq.k, p.T, n0 * 64, kraw);
         float logdecay = 0.f;
         __syncthreads();
         for (int n = n0; n < n1; n++) {
             const int t0 = n * 64;
             commit_gates(p, t0, gr, sLam, sBeta, sGam);
-            norm_store_rows(p, t0, kraw, sNw, p.k_eps, sK);
+            norm_store_half(p, t0, kraw, sNw, p.k_eps, y, sA);
             if (n + 1 < n1) {
-                issue_rows(p, p.k, b, h, t0 + 64, kraw);
-                gr = issue_gates(p, b, h, bh, t0 + 64);
+                issue_full_rows(sq, sq.k, p.T, t0 + 64, kraw);
+                gr = issue_gates(sq, p.T, t0 + 64);
             }
             __syncthreads();
             logdecay += sGam[63];
             bf16x8 wt[2];
-            {
-                const int m = 16 * w + lr;
 #pragma unroll
-                for (int ss = 0; ss < 2; ss++)
+            for (int ss = 0; ss < 2; ss++)
 #pragma unroll
-                    for (int jj = 0; jj < 8; jj++) {
-                        const int s = 32 * ss + 8 * lg + jj;
-                        wt[ss][jj] = (bf16_t)((float)write_elem(sLam[s], sBeta[s], m) * sGam[128 + s]);
-                    }
-            }
+                for (int jj = 0; jj < 8; jj++) {
+                    const int s = 32 * ss + 8 * lg + jj;
+                    wt[ss][jj] = (bf16_t)((float)write_elem(sLam[s], sBeta[s], 16 * w + lr) * sGam[128 + s]);
+                }
             const float dec = sGam[64 + 63];
 #pragma unroll
-            for (int db = 0; db < 16; db++) acc[db] *= dec;
+            for (int kb = 0; kb < 8; kb++) acc[kb] *= dec;
 #pragma unroll
-            for (int db = 0; db < 16; db++)
+            for (int ss = 0; ss < 2; ss++)
 #pragma unroll
-                for (int ss = 0; ss < 2; ss++)
-                    acc[db] = mfma_bf16(load_tr_bf16(sK, RS256, 32 * ss, 16 * db), wt[ss], acc[db]);
+                for (int kb = 0; kb < 8; kb++) acc[kb] = mfma_bf16(load_tr_bf16(sA, RS, 32 * ss, 16 * kb), wt[ss], acc[kb]);
             __syncthreads();
         }
 #pragma unroll
-        for (int db = 0; db < 16; db++)
+        for (int kb = 0; kb < 8; kb++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) out[(16 * db + 4 * lg + i) * kSlots + 16 * w + lr] = acc[db][i];
-        if (tid == 0) p.seg_decay[bh * p.P + j] = exp2f(logdecay);
+            for (int i = 0; i < 4; i++) out[(HALF * y + 16 * kb + 4 * lg + i) * kSlots + 16 * w + lr] = acc[kb][i];
+        if (y == 0 && tid == 0) p.seg_decay[bh * p.P + j] = exp2f(logdecay);
     } else {
-        bf16_t* sW = reinterpret_cast<bf16_t*>(smem + SG_W);
-        bf16_t* sV = reinterpret_cast<bf16_t*>(smem + SG_V);
-        f32x4 acc[8][2];
-#pragma unroll
-        for (int mb = 0; mb < 8; mb++)
-#pragma unroll
-            for (int cb = 0; cb < 2; cb++) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        bf16x8 vraw[4];
-        issue_rows(p, p.v, b, h, n0 * 64, vraw);
-        GateRegs gr = issue_gates(p, b, h, bh, n0 * 64);
+        const int y = part - 2;
+        bf16x8 vraw[2];
+        issue_half_rows(sq, sq.v, p.T, n0 * 64, y, vraw);
         for (int n = n0; n < n1; n++) {
             const int t0 = n * 64;
             commit_gates(p, t0, gr, sLam, sBeta, sGam);
-            store_rows(p, t0, vraw, sV);
+            store_write_tile(gr, p.T - t0, sA);
+            store_half_rows(vraw, p.T - t0, sB);
             if (n + 1 < n1) {
-                issue_rows(p, p.v, b, h, t0 + 64, vraw);
-                gr = issue_gates(p, b, h, bh, t0 + 64);
+                issue_half_rows(sq, sq.v, p.T, t0 + 64, y, vraw);
+                gr = issue_gates(sq, p.T, t0 + 64);
             }
-            __syncthreads();
-            store_write_rows(sLam, sBeta, sW);
             __syncthreads();
             const float dec = sGam[64 + 63];
 #pragma unroll
-            for (int mb = 0; mb < 8; mb++)
-#pragma unroll
-                for (int cb = 0; cb < 2; cb++) acc[mb][cb] *= dec;
+            for (int mb = 0; mb < 8; mb++) acc[mb] *= dec;
 #pragma unroll
             for (int ss = 0; ss < 2; ss++) {
-                bf16x8 vt[2];
+                const bf16x8 vb = load_tr_bf16(sB, RS, 32 * ss, 16 * w);
+                bf16x8 vt;
 #pragma unroll
-                for (int cb = 0; cb < 2; cb++) {
-                    const bf16x8 vb = load_tr_bf16(sV, RS256, 32 * ss, 32 * w + 16 * cb);
+                for (int jj = 0; jj < 8; jj++) vt[jj] = (bf16_t)((float)vb[jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
 #pragma unroll
-                    for (int jj = 0; jj < 8; jj++) vt[cb][jj] = (bf16_t)((float)vb[jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
-                }
-#pragma unroll
-                for (int mb = 0; mb < 8; mb++) {
-                    const bf16x8 a = load_tr_bf16(sW, RS128, 32 * ss, 16 * mb);
-#pragma unroll
-                    for (int cb = 0; cb < 2; cb++) acc[mb][cb] = mfma_bf16(a, vt[cb], acc[mb][cb]);
-                }
+                for (int mb = 0; mb < 8; mb++) acc[mb] = mfma_bf16(load_tr_bf16(sA, RS, 32 * ss, 16 * mb), vt, acc[mb]);
             }
             __syncthreads();
         }
@@ -422,9 +517,7 @@ __global__ __launch_bounds__(512) void segment_state_kernel(PrefillParams p) {
 #pragma unroll
         for (int mb = 0; mb < 8; mb++)
 #pragma unroll
-            for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) outv[(16 * mb + 4 * lg + i) * VD + 32 * w + 16 * cb + lr] = acc[mb][cb][i];
+            for (int i = 0; i < 4; i++) outv[(16 * mb + 4 * lg + i) * VD + HALF * y + 16 * w + lr] = acc[mb][i];
     }
 }
 
@@ -457,282 +550,314 @@ __global__ __launch_bounds__(256) void carry_kernel(PrefillParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// 4. Pass 1 (key state) + fused slot readout. grid = B*H*P, 512 threads.
-// Wave w owns key-state columns [16 w, 16 w + 16): acc[db] = S[16 db + 4 lg + i][16 w + lr].
-// Scores: wave w covers key block sb = w & 3 and query blocks 2 hi, 2 hi + 1
-// (hi = w >> 2). Readout: wave w covers query block sb and slot / coordinate
-// blocks 4 hi .. 4 hi + 3.
-constexpr int P1_Q = 0;                          // bf16 [64][RS256] q_hat rows; later z, then p (f16 [64][RS128])
-constexpr int P1_K = P1_Q + 64 * RS256 * 2;      // bf16 [64][RS256] k_hat rows; later raw f32 [64][FS], then weights
-constexpr int P1_P = P1_K + 64 * RS256 * 2;      // bf16 [64][TS] masked scores
-constexpr int P1_TAB = P1_P + 64 * TS * 2;       // f16 [128][RS128] readout table rows r (row 127 zero)
-constexpr int P1_RED = P1_TAB + 128 * RS128 * 2; // f32 [2][64][2] softmax row partials
-constexpr int P1_G = P1_RED + 2 * 64 * 2 * 4;    // f32 [5][64] gates
-constexpr int P1_NW = P1_G + 5 * 64 * 4;         // f32 [2][256] q and k norm weights
-constexpr int P1_LDS = P1_NW + 2 * KD * 4;
-static_assert(64 * FS * 4 <= 64 * RS256 * 2, "raw tile must fit in the k tile");
-static_assert(P1_LDS <= 160 * 1024, "pass-1 LDS exceeds gfx950 LDS");
+// 4. Pass 1 (key state), one key half per workgroup. grid = sweep_grid(B*H*P),
+// 512 threads. Wave w owns key-state columns [16 w, 16 w + 16) of rows
+// [128 y, 128 y + 128): acc[kb] = S[128 y + 16 kb + 4 lg + i][16 w + lr], and
+// the same 16 output coordinates: out[tb] = raw^T[16 w + 4 lg + i][16 tb + lr].
+constexpr int P1_Q = 0;                       // bf16 [64][RS] q_hat (half)
+constexpr int P1_K = P1_Q + 64 * RS * 2;      // bf16 [64][RS] k_hat (half)
+constexpr int P1_W = P1_K + 64 * RS * 2;      // bf16 [64][RS] w
+constexpr int P1_P = P1_W + 64 * RS * 2;      // bf16 [64][TS] masked scores
+constexpr int P1_G = P1_P + 64 * TS * 2;      // f32 [5][64] gates
+constexpr int P1_NW = P1_G + 5 * 64 * 4;      // f32 [2][128] q and k norm weights (half)
+constexpr int P1_LDS = P1_NW + 2 * HALF * 4;
+static_assert(2 * P1_LDS <= 160 * 1024, "two pass-1 workgroups must fit in one CU's LDS");
 
-__global__ __launch_bounds__(512) void pass1_kernel(PrefillParams p) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void pass1_kernel(PrefillParams p) {
     __shared__ __align__(16) unsigned char smem[P1_LDS];
     bf16_t* sQ = reinterpret_cast<bf16_t*>(smem + P1_Q);
-    f16_t* sZ = reinterpret_cast<f16_t*>(smem + P1_Q);
     bf16_t* sK = reinterpret_cast<bf16_t*>(smem + P1_K);
-    float* sRaw = reinterpret_cast<float*>(smem + P1_K);
-    bf16_t* sOm = reinterpret_cast<bf16_t*>(smem + P1_K);
+    bf16_t* sW = reinterpret_cast<bf16_t*>(smem + P1_W);
     bf16_t* sP = reinterpret_cast<bf16_t*>(smem + P1_P);
-    f16_t* sTab = reinterpret_cast<f16_t*>(smem + P1_TAB);
-    float* sRed = reinterpret_cast<float*>(smem + P1_RED);
     float* sLam = reinterpret_cast<float*>(smem + P1_G);
     float* sBeta = sLam + 64;
     float* sGam = sBeta + 64;
     float* sQw = reinterpret_cast<float*>(smem + P1_NW);
-    float* sKw = sQw + KD;
+    float* sKw = sQw + HALF;
 
-    const int bh = blockIdx.x / p.P, j = blockIdx.x % p.P;
+    const SweepBlock sw = sweep_block();
+    if (sw.unit >= p.B * p.H * p.P) return;
+    const int bh = sw.unit / p.P, j = sw.unit % p.P, y = sw.half;
     const int b = bh / p.H, h = bh % p.H;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 15, lg = lane >> 4;
-    const int sb = w & 3, hi = w >> 2;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), lr = lane & 15, lg = lane >> 4;
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
-    if (tid < KD) {
-        sQw[tid] = p.q_w[tid];
-        sKw[tid] = p.k_w[tid];
+    if (tid < HALF) {
+        sQw[tid] = p.q_w[HALF * y + tid];
+        sKw[tid] = p.k_w[HALF * y + tid];
     }
-    {
-        const float* tb = p.table + (size_t)h * kActive * kSlots;
-        for (int idx = tid; idx < 128 * 128; idx += 512) {
-            const int r = idx >> 7, m = idx & 127;
-            sTab[r * RS128 + m] = (f16_t)(r < kActive ? tb[r * kSlots + m] : 0.f);
-        }
-    }
-    f32x4 acc[16];
+    zero_scores(sP);  // the two blocks above the diagonal that the intra product reads stay zero
+    f32x4 acc[8];
     {
         const float* s0 = p.P > 1 ? p.seg + ((size_t)bh * p.P + j) * SEG
                                   : (p.h0_k ? p.h0_k + (size_t)bh * SEG_K : nullptr);
         if (s0) {
 #pragma unroll
-            for (int db = 0; db < 16; db++)
+            for (int kb = 0; kb < 8; kb++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[db][i] = s0[(16 * db + 4 * lg + i) * kSlots + 16 * w + lr];
+                for (int i = 0; i < 4; i++) acc[kb][i] = s0[(HALF * y + 16 * kb + 4 * lg + i) * kSlots + 16 * w + lr];
         } else {
 #pragma unroll
-            for (int db = 0; db < 16; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int kb = 0; kb < 8; kb++) acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
     }
+    const Seq sq = make_seq(p, b, h, bh);
+    const rsrc_t rraw = make_rsrc(p.raw + ((size_t)y * p.B * p.H + bh) * p.Tp * kSlots, (size_t)p.Tp * kSlots * 2);
+    const uint32_t raw_lane = (uint32_t)lr * (kSlots * 2) + 2 * (16 * w + 4 * lg);
     bf16x8 qraw[4], kraw[4];
-    issue_rows(p, p.q, b, h, n0 * 64, qraw);
-    issue_rows(p, p.k, b, h, n0 * 64, kraw);
-    GateRegs gr = issue_gates(p, b, h, bh, n0 * 64);
-    __syncthreads();  // norm weights and table staged
+    issue_full_rows(sq, sq.q, p.T, n0 * 64, qraw);
+    issue_full_rows(sq, sq.k, p.T, n0 * 64, kraw);
+    GateRegs gr = issue_gates(sq, p.T, n0 * 64);
+    __syncthreads();  // norm weights staged, score tile zeroed
 
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
         commit_gates(p, t0, gr, sLam, sBeta, sGam);
-        norm_store_rows(p, t0, qraw, sQw, p.q_eps, sQ);
-        norm_store_rows(p, t0, kraw, sKw, p.k_eps, sK);
+        store_write_tile(gr, p.T - t0, sW);
+        norm_store_half(p, t0, qraw, sQw, p.q_eps, y, sQ);
+        norm_store_half(p, t0, kraw, sKw, p.k_eps, y, sK);
+        sched_fence();  // the next chunk's loads reuse these registers
         if (n + 1 < n1) {
-            issue_rows(p, p.q, b, h, t0 + 64, qraw);
-            issue_rows(p, p.k, b, h, t0 + 64, kraw);
-            gr = issue_gates(p, b, h, bh, t0 + 64);
+            issue_full_rows(sq, sq.q, p.T, t0 + 64, qraw);
+            issue_full_rows(sq, sq.k, p.T, t0 + 64, kraw);
+            gr = issue_gates(sq, p.T, t0 + 64);
         }
         __syncthreads();
 
-        // Write vector (B operand) for this wave's 16 slot columns, raw and decayed.
-        bf16x8 wf[2], wt[2];
-        {
-            const int m = 16 * w + lr;
+        // Masked, decayed scores of this half's key slice.
+        for (int blk = w; blk < 10; blk += 8) {
+            int tb, sb;
+            score_block(blk, tb, sb);
+            f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ss = 0; ss < 2; ss++)
-#pragma unroll
-                for (int jj = 0; jj < 8; jj++) {
-                    const int s = 32 * ss + 8 * lg + jj;
-                    const bf16_t wb = write_elem(sLam[s], sBeta[s], m);
-                    wf[ss][jj] = wb;
-                    wt[ss][jj] = (bf16_t)((float)wb * sGam[128 + s]);
-                }
+            for (int ks = 0; ks < 4; ks++)
+                sc = mfma_bf16(load_row<bf16x8>(sQ, RS, 16 * tb, 32 * ks), load_row<bf16x8>(sK, RS, 16 * sb, 32 * ks), sc);
+            store_scores(sc, tb, sb, sGam, sP);
         }
-        // Masked, decayed scores P[t][s] for key block sb and query blocks 2 hi, 2 hi + 1.
-        {
-            f32x4 sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
-                const bf16x8 kb = load_row<bf16x8>(sK, RS256, 16 * sb, 32 * ks);
-                sc0 = mfma_bf16(load_row<bf16x8>(sQ, RS256, 32 * hi, 32 * ks), kb, sc0);
-                sc1 = mfma_bf16(load_row<bf16x8>(sQ, RS256, 32 * hi + 16, 32 * ks), kb, sc1);
-            }
-            store_scores(sc0, 2 * hi, sb, sGam, sP);
-            store_scores(sc1, 2 * hi + 1, sb, sGam, sP);
-        }
-        __syncthreads();
-
-        // raw = scale (2^G_t q S_n + P w) for this wave's 16 slot columns.
+        // raw^T = 2^G_t S_n^T q_t over this half's key rows.
         f32x4 out[4];
 #pragma unroll
         for (int tb = 0; tb < 4; tb++) out[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-            const bf16x8 bs = state_as_b(acc[2 * ks], acc[2 * ks + 1]);
-#pragma unroll
-            for (int tb = 0; tb < 4; tb++)
-                out[tb] = mfma_bf16(load_query_perm(sQ + (16 * tb + lr) * RS256 + 32 * ks, lg), bs, out[tb]);
-        }
-#pragma unroll
-        for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) out[tb][i] *= sGam[64 + 16 * tb + 4 * lg + i];
-#pragma unroll
-        for (int ss = 0; ss < 2; ss++)
-#pragma unroll
-            for (int tb = 0; tb < 4; tb++)
-                out[tb] = mfma_bf16(load_row<bf16x8>(sP, TS, 16 * tb, 32 * ss), wf[ss], out[tb]);
-        // State update: S = 2^G_last S + k_hat^T bf16(2^(G_last - G_s) w); the
-        // k_hat^T fragments come straight from the row-major k tile.
-        {
-            const float dec = sGam[64 + 63];
-#pragma unroll
-            for (int db = 0; db < 16; db++) acc[db] *= dec;
-#pragma unroll
-            for (int db = 0; db < 16; db++)
-#pragma unroll
-                for (int ss = 0; ss < 2; ss++)
-                    acc[db] = mfma_bf16(load_tr_bf16(sK, RS256, 32 * ss, 16 * db), wt[ss], acc[db]);
-        }
-        __syncthreads();  // q and k tiles are dead from here on
-#pragma unroll
-        for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) sRaw[(16 * tb + 4 * lg + i) * FS + 16 * w + lr] = out[tb][i] * p.scale;
-        __syncthreads();
-
-        // Readout (ops/chunk_readout.py:797-909): z = U(lam) raw, in fp16.
-#pragma unroll
-        for (int it = 0; it < 8; it++) {
-            const int idx = tid + 512 * it, t = idx >> 6, pr = idx & 63;
-            const float2 eo = *reinterpret_cast<const float2*>(sRaw + t * FS + 2 * pr);
-            float sn, cs;
-            pair_sincos(sLam[t], pr, sn, cs);
-            f16_t* d = sZ + t * RS128 + 2 * pr;
-            d[0] = (f16_t)(cs * eo.x - sn * eo.y);
-            d[1] = (f16_t)(sn * eo.x + cs * eo.y);
-        }
-        __syncthreads();
-        // logits = z table^T for query block sb and slots 64 hi .. 64 hi + 63;
-        // softmax over the 127 active slots, row max / sum combined across the
-        // two waves of a query block through LDS.
-        f32x4 lgt[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) lgt[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            const f16x8 a = load_row<f16x8>(sZ, RS128, 16 * sb, 32 * ks);
+            const bf16x8 a = state_frag(acc[2 * ks], acc[2 * ks + 1]);
 #pragma unroll
-            for (int u = 0; u < 4; u++) lgt[u] = mfma_f16(a, load_row<f16x8>(sTab, RS128, 16 * (4 * hi + u), 32 * ks), lgt[u]);
+            for (int tb = 0; tb < 4; tb++)
+                out[tb] = mfma_bf16(a, load_row_perm(sQ + (16 * tb + lr) * RS + 32 * ks, lg), out[tb]);
+            sched_fence();
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float mx = -INFINITY;
+        for (int tb = 0; tb < 4; tb++) out[tb] *= sGam[64 + 16 * tb + lr];
+        __syncthreads();  // scores complete
+
+        // raw^T += w^T P^T; the blocks of P above the diagonal are zero.
+        // wf[ss][jj] = w[32 ss + 8 lg + jj][16 w + lr].
+        bf16x8 wf[2];
 #pragma unroll
-            for (int u = 0; u < 4; u++)
-                if (16 * (4 * hi + u) + lr < kActive) mx = fmaxf(mx, lgt[u][i]);
-            mx = wave_max<16>(mx);
-            if (lr == 0) sRed[(16 * sb + 4 * lg + i) * 2 + hi] = mx;
+        for (int ss = 0; ss < 2; ss++) wf[ss] = load_tr_bf16(sW, RS, 32 * ss, 16 * w);
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+            for (int ss = 0; ss <= (tb >> 1); ss++)
+                out[tb] = mfma_bf16(wf[ss], load_row<bf16x8>(sP, TS, 16 * tb, 32 * ss), out[tb]);
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++)
+            st_b64(rraw, raw_lane, (uint32_t)(t0 + 16 * tb) * (kSlots * 2), to_bf16x4(out[tb], p.scale));
+        // State update: S = 2^G_last S + k_hat^T bf16(2^(G_last - G_s) w).
+        const float dec = sGam[64 + 63];
+#pragma unroll
+        for (int kb = 0; kb < 8; kb++) acc[kb] *= dec;
+#pragma unroll
+        for (int ss = 0; ss < 2; ss++) {
+            bf16x8 wt;
+#pragma unroll
+            for (int jj = 0; jj < 8; jj++) wt[jj] = (bf16_t)((float)wf[ss][jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
+#pragma unroll
+            for (int kb = 0; kb < 8; kb++) acc[kb] = mfma_bf16(load_tr_bf16(sK, RS, 32 * ss, 16 * kb), wt, acc[kb]);
+            sched_fence();
         }
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = 16 * sb + 4 * lg + i;
-            const float mx = fmaxf(sRed[t * 2], sRed[t * 2 + 1]);
-            float sum = 0.f;
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                lgt[u][i] = 16 * (4 * hi + u) + lr < kActive ? __expf(lgt[u][i] - mx) : 0.f;
-                sum += lgt[u][i];
-            }
-            sum = wave_sum<16>(sum);
-            if (lr == 0) sRed[128 + t * 2 + hi] = sum;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = 16 * sb + 4 * lg + i;
-            const float inv = 1.f / (sRed[128 + t * 2] + sRed[128 + t * 2 + 1]);
-#pragma unroll
-            for (int u = 0; u < 4; u++) sZ[t * RS128 + 16 * (4 * hi + u) + lr] = (f16_t)(lgt[u][i] * inv);
-        }
-        __syncthreads();
-        // u = p table (table^T fragments by transpose reads), weights = U(-lam) u.
-        {
-            f32x4 uu[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) uu[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int rs = 0; rs < 4; rs++) {
-                const f16x8 a = load_row<f16x8>(sZ, RS128, 16 * sb, 32 * rs);
-#pragma unroll
-                for (int u = 0; u < 4; u++) uu[u] = mfma_f16(a, load_tr_f16(sTab, RS128, 32 * rs, 16 * (4 * hi + u)), uu[u]);
-            }
-#pragma unroll
-            for (int u = 0; u < 4; u++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int t = 16 * sb + 4 * lg + i, m = 16 * (4 * hi + u) + lr;
-                    const float mine = uu[u][i];
-                    const float other = __shfl_xor(mine, 1);
-                    float sn, cs;
-                    pair_sincos(sLam[t], m >> 1, sn, cs);
-                    const float e = (m & 1) ? other : mine, o = (m & 1) ? mine : other;
-                    sOm[t * RS128 + m] = (bf16_t)((m & 1) ? (-sn * e + cs * o) : (cs * e + sn * o));
-                }
-        }
-        __syncthreads();
-        {
-            bf16_t* dst = p.omega + ((size_t)bh * p.Tp + t0) * kSlots;
-#pragma unroll
-            for (int it = 0; it < 2; it++) {
-                const int idx = tid + 512 * it, r = idx >> 4, c8 = (idx & 15) * 8;
-                *reinterpret_cast<bf16x8*>(dst + r * kSlots + c8) = *reinterpret_cast<const bf16x8*>(sOm + r * RS128 + c8);
-            }
-        }
-        __syncthreads();
+        __syncthreads();  // tiles are overwritten by the next chunk
     }
 
     if (j == p.P - 1 && p.hk) {
         float* dst = p.hk + (size_t)bh * SEG_K;
 #pragma unroll
-        for (int db = 0; db < 16; db++)
+        for (int kb = 0; kb < 8; kb++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) dst[(16 * db + 4 * lg + i) * kSlots + 16 * w + lr] = acc[db][i];
+            for (int i = 0; i < 4; i++) dst[(HALF * y + 16 * kb + 4 * lg + i) * kSlots + 16 * w + lr] = acc[kb][i];
     }
 }
 
 // ---------------------------------------------------------------------------
-// 5. Pass 2 (value state). grid = B*H*P, 512 threads. Wave w owns value columns
-// [32 w, 32 w + 32): acc[mb][cb] = S[16 mb + 4 lg + i][32 w + 16 cb + lr].
-constexpr int P2_OM = 0;                          // bf16 [64][RS128] slot weights (query)
-constexpr int P2_W = P2_OM + 64 * RS128 * 2;      // bf16 [64][RS128] w rows (key)
-constexpr int P2_V = P2_W + 64 * RS128 * 2;       // bf16 [64][RS256] v rows; later o staging
-constexpr int P2_P = P2_V + 64 * RS256 * 2;       // bf16 [64][TS] masked scores
-constexpr int P2_G = P2_P + 64 * TS * 2;          // f32 [5][64] gates
-constexpr int P2_LDS = P2_G + 5 * 64 * 4;
+// 5. Slot readout (ops/chunk_readout.py:797-909), fp16 MFMA with fp32
+// accumulation. grid = H * G, 512 threads; the workgroup stages its head's
+// table once and each wave then runs 16-token tasks on its own: lane (lr, lg)
+// works on token lr of the task.
+//   z_t = U(lam_t) raw_t                              (B operand, registers)
+//   L^T[r][t] = table[r] . z_t                        (C rows r = 16 rb + 4 lg + i)
+//   p_t = softmax over r < 127 of L^T[:, t]           (in registers + 2 shuffles)
+//   u^T[m][t] = sum_r table[r][m] p_t[r]              (p_t as the B operand straight
+//                                                      from the C layout)
+//   weights_t = bf16(U(-lam_t) u_t)
+// The second product reads the table through transpose reads of a copy whose
+// rows are stored in the k order of a C-block pair.
+constexpr int RO_A = 0;                    // f16 [128][RS] table rows r (row 127 zero)
+constexpr int RO_B = RO_A + 128 * RS * 2;  // f16 [128][RS] table rows in C-pair order
+constexpr int RO_LDS = RO_B + 128 * RS * 2;
+static_assert(2 * RO_LDS <= 160 * 1024, "two readout workgroups must fit in one CU's LDS");
 
-__global__ __launch_bounds__(512) void pass2_kernel(PrefillParams p) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void readout_kernel(PrefillParams p) {
+    __shared__ __align__(16) unsigned char smem[RO_LDS];
+    f16_t* sTA = reinterpret_cast<f16_t*>(smem + RO_A);
+    f16_t* sTB = reinterpret_cast<f16_t*>(smem + RO_B);
+    const int h = blockIdx.x % p.H, grp = blockIdx.x / p.H, ngrp = gridDim.x / p.H;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), lr = lane & 15, lg = lane >> 4;
+    {
+        const float* tb = p.table + (size_t)h * kActive * kSlots;
+        for (int idx = tid; idx < 128 * 32; idx += 512) {
+            const int r = idx >> 5, m4 = (idx & 31) * 4;
+            const float4 v = r < kActive ? *reinterpret_cast<const float4*>(tb + r * kSlots + m4)
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+            const f16x4 hv = f16x4{(f16_t)v.x, (f16_t)v.y, (f16_t)v.z, (f16_t)v.w};
+            *reinterpret_cast<f16x4*>(sTA + r * RS + m4) = hv;
+            // row r sits at k position 8 lg + j of its 32-row group, where
+            // r % 32 = 4 lg + j (j < 4) or 16 + 4 lg + (j - 4) (j >= 4)
+            const int rl = r & 31;
+            const int pos = rl < 16 ? 8 * (rl >> 2) + (rl & 3) : 8 * ((rl - 16) >> 2) + 4 + (rl & 3);
+            *reinterpret_cast<f16x4*>(sTB + ((r & ~31) + pos) * RS + m4) = hv;
+        }
+    }
+    __syncthreads();
+
+    const int blocks = p.Tp / 16, tasks = p.B * blocks;
+    const size_t plane = (size_t)p.B * p.H * p.Tp * kSlots;
+    for (int task = grp * 8 + w; task < tasks; task += ngrp * 8) {
+        const int b = task / blocks, t = 16 * (task % blocks) + lr;
+        const int bh = b * p.H + h;
+        const size_t row = ((size_t)bh * p.Tp + t) * kSlots;
+        bf16x8 ra[4], rb[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            ra[ks] = *reinterpret_cast<const bf16x8*>(p.raw + row + 32 * ks + 8 * lg);
+            rb[ks] = *reinterpret_cast<const bf16x8*>(p.raw + plane + row + 32 * ks + 8 * lg);
+        }
+        const float lamr = reduced_clock(p.lam[(size_t)bh * p.Tp + t]);
+        // z fragments: element j = z_t[32 ks + 8 lg + j].
+        f16x8 zf[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float e = (float)ra[ks][2 * q] + (float)rb[ks][2 * q];
+                const float o = (float)ra[ks][2 * q + 1] + (float)rb[ks][2 * q + 1];
+                float sn, cs;
+                pair_sincos(lamr, 16 * ks + 4 * lg + q, sn, cs);
+                zf[ks][2 * q] = (f16_t)(cs * e - sn * o);
+                zf[ks][2 * q + 1] = (f16_t)(sn * e + cs * o);
+            }
+        f32x4 L[8];
+#pragma unroll
+        for (int rb8 = 0; rb8 < 8; rb8++) L[rb8] = f32x4{0.f, 0.f, 0.f, 0.f};
+        sched_fence();
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+#pragma unroll
+            for (int rb8 = 0; rb8 < 8; rb8++)
+                L[rb8] = mfma_f16(load_row<f16x8>(sTA, RS, 16 * rb8, 32 * ks), zf[ks], L[rb8]);
+            sched_fence();
+        }
+        if (lg == 3) L[7][3] = -INFINITY;  // slot r = 127 is not active
+        float mx = -INFINITY;
+#pragma unroll
+        for (int rb8 = 0; rb8 < 8; rb8++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) mx = fmaxf(mx, L[rb8][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        float sum = 0.f;
+#pragma unroll
+        for (int rb8 = 0; rb8 < 8; rb8++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                L[rb8][i] = __expf(L[rb8][i] - mx);
+                sum += L[rb8][i];
+            }
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+        const float inv = 1.f / sum;
+        f16x8 pf[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                pf[ks][i] = (f16_t)(L[2 * ks][i] * inv);
+                pf[ks][4 + i] = (f16_t)(L[2 * ks + 1][i] * inv);
+            }
+        f32x4 U[8];
+#pragma unroll
+        for (int mb = 0; mb < 8; mb++) U[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        sched_fence();
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+#pragma unroll
+            for (int mb = 0; mb < 8; mb++) U[mb] = mfma_f16(load_tr_f16(sTB, RS, 32 * ks, 16 * mb), pf[ks], U[mb]);
+            sched_fence();
+        }
+        // Lane holds u_t[16 mb + 4 lg + i]: pairs 8 mb + 2 lg + q, q = 0, 1.
+        bf16_t* dst = p.omega + row;
+#pragma unroll
+        for (int mb = 0; mb < 8; mb++) {
+            bf16x4 o;
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                float sn, cs;
+                pair_sincos(lamr, 8 * mb + 2 * lg + q, sn, cs);
+                const float ue = U[mb][2 * q], uo = U[mb][2 * q + 1];
+                o[2 * q] = (bf16_t)(cs * ue + sn * uo);
+                o[2 * q + 1] = (bf16_t)(cs * uo - sn * ue);
+            }
+            *reinterpret_cast<bf16x4*>(dst + 16 * mb + 4 * lg) = o;
+        }
+    }
+}
+
+int readout_groups(int B, int Tp, int H) {
+    const int iters = (B * Tp / 16 + 7) / 8;  // 8 tasks per workgroup iteration
+    int g = (512 + H - 1) / H;                // about two workgroups per CU
+    if (g > iters) g = iters;
+    return g < 1 ? 1 : g;
+}
+
+// ---------------------------------------------------------------------------
+// 6. Pass 2 (value state), one value half per workgroup. grid = sweep_grid(B*H*P),
+// 512 threads. Wave w owns value columns 128 y + 16 w + [0, 16):
+// acc[mb] = S[16 mb + 4 lg + i][128 y + 16 w + lr], and the same 16 output
+// coordinates: out[tb] = o^T[128 y + 16 w + 4 lg + i][16 tb + lr].
+constexpr int P2_OM = 0;                   // bf16 [64][RS] slot weights (query)
+constexpr int P2_W = P2_OM + 64 * RS * 2;  // bf16 [64][RS] w (key)
+constexpr int P2_V = P2_W + 64 * RS * 2;   // bf16 [64][RS] v (half)
+constexpr int P2_P = P2_V + 64 * RS * 2;   // bf16 [64][TS] masked scores
+constexpr int P2_G = P2_P + 64 * TS * 2;   // f32 [5][64] gates
+constexpr int P2_LDS = P2_G + 5 * 64 * 4;
+static_assert(2 * P2_LDS <= 160 * 1024, "two pass-2 workgroups must fit in one CU's LDS");
+
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void pass2_kernel(PrefillParams p) {
     __shared__ __align__(16) unsigned char smem[P2_LDS];
-    bf16_t* sOmq = reinterpret_cast<bf16_t*>(smem + P2_OM);
+    bf16_t* sOm = reinterpret_cast<bf16_t*>(smem + P2_OM);
     bf16_t* sW = reinterpret_cast<bf16_t*>(smem + P2_W);
     bf16_t* sV = reinterpret_cast<bf16_t*>(smem + P2_V);
-    bf16_t* sO = reinterpret_cast<bf16_t*>(smem + P2_V);
     bf16_t* sP = reinterpret_cast<bf16_t*>(smem + P2_P);
     float* sLam = reinterpret_cast<float*>(smem + P2_G);
     float* sBeta = sLam + 64;
     float* sGam = sBeta + 64;
 
-    const int bh = blockIdx.x / p.P, j = blockIdx.x % p.P;
+    const SweepBlock sw = sweep_block();
+    if (sw.unit >= p.B * p.H * p.P) return;
+    const int bh = sw.unit / p.P, j = sw.unit % p.P, y = sw.half;
     const int b = bh / p.H, h = bh % p.H;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 15, lg = lane >> 4;
-    const int sb = w & 3, hi = w >> 2;
+    const int lane = threadIdx.x & 63, w = wave_id(), lr = lane & 15, lg = lane >> 4;
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
-
-    f32x4 acc[8][2];
+    zero_scores(sP);
+    f32x4 acc[8];
     {
         const float* s0 = p.P > 1 ? p.seg + ((size_t)bh * p.P + j) * SEG + SEG_K
                                   : (p.h0_v ? p.h0_v + (size_t)bh * SEG_V : nullptr);
@@ -740,118 +865,81 @@ __global__ __launch_bounds__(512) void pass2_kernel(PrefillParams p) {
 #pragma unroll
             for (int mb = 0; mb < 8; mb++)
 #pragma unroll
-                for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        acc[mb][cb][i] = s0[(16 * mb + 4 * lg + i) * VD + 32 * w + 16 * cb + lr];
+                for (int i = 0; i < 4; i++) acc[mb][i] = s0[(16 * mb + 4 * lg + i) * VD + HALF * y + 16 * w + lr];
         } else {
 #pragma unroll
-            for (int mb = 0; mb < 8; mb++)
-#pragma unroll
-                for (int cb = 0; cb < 2; cb++) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int mb = 0; mb < 8; mb++) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
     }
-    bf16x8 vraw[4], om[2];
-    issue_rows(p, p.v, b, h, n0 * 64, vraw);
-    issue_omega(p, bh, n0 * 64, om);
-    GateRegs gr = issue_gates(p, b, h, bh, n0 * 64);
+    const Seq sq = make_seq(p, b, h, bh);
+    const rsrc_t rom = make_rsrc(p.omega + (size_t)bh * p.Tp * kSlots, (size_t)p.Tp * kSlots * 2);
+    const uint32_t o_lane = (uint32_t)lr * sq.row16 + 2 * (HALF * y + 16 * w + 4 * lg);
+    bf16x8 vraw[2], om[2];
+    issue_half_rows(sq, sq.v, p.T, n0 * 64, y, vraw);
+    issue_omega(rom, n0 * 64, om);
+    GateRegs gr = issue_gates(sq, p.T, n0 * 64);
 
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
         commit_gates(p, t0, gr, sLam, sBeta, sGam);
-#pragma unroll
-        for (int it = 0; it < 2; it++) {
-            const int idx = tid + 512 * it, r = idx >> 4, c8 = (idx & 15) * 8;
-            *reinterpret_cast<bf16x8*>(sOmq + r * RS128 + c8) = om[it];
-        }
-        store_rows(p, t0, vraw, sV);
+        store_write_tile(gr, p.T - t0, sW);
+        store_half_rows(om, 64, sOm);
+        store_half_rows(vraw, p.T - t0, sV);
         if (n + 1 < n1) {
-            issue_rows(p, p.v, b, h, t0 + 64, vraw);
-            issue_omega(p, bh, t0 + 64, om);
-            gr = issue_gates(p, b, h, bh, t0 + 64);
-        }
-        __syncthreads();
-        store_write_rows(sLam, sBeta, sW);
-        __syncthreads();
-        {
-            f32x4 sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                const bf16x8 wb = load_row<bf16x8>(sW, RS128, 16 * sb, 32 * ks);
-                sc0 = mfma_bf16(load_row<bf16x8>(sOmq, RS128, 32 * hi, 32 * ks), wb, sc0);
-                sc1 = mfma_bf16(load_row<bf16x8>(sOmq, RS128, 32 * hi + 16, 32 * ks), wb, sc1);
-            }
-            store_scores(sc0, 2 * hi, sb, sGam, sP);
-            store_scores(sc1, 2 * hi + 1, sb, sGam, sP);
+            issue_half_rows(sq, sq.v, p.T, t0 + 64, y, vraw);
+            issue_omega(rom, t0 + 64, om);
+            gr = issue_gates(sq, p.T, t0 + 64);
         }
         __syncthreads();
 
-        f32x4 out[4][2];
+        for (int blk = w; blk < 10; blk += 8) {
+            int tb, sb;
+            score_block(blk, tb, sb);
+            f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int tb = 0; tb < 4; tb++)
+            for (int ks = 0; ks < 4; ks++)
+                sc = mfma_bf16(load_row<bf16x8>(sOm, RS, 16 * tb, 32 * ks), load_row<bf16x8>(sW, RS, 16 * sb, 32 * ks), sc);
+            store_scores(sc, tb, sb, sGam, sP);
+        }
+        // o^T = 2^G_t S_n^T weights_t.
+        f32x4 out[4];
 #pragma unroll
-            for (int cb = 0; cb < 2; cb++) out[tb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int tb = 0; tb < 4; tb++) out[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            const bf16x8 bs0 = state_as_b(acc[2 * ks][0], acc[2 * ks + 1][0]);
-            const bf16x8 bs1 = state_as_b(acc[2 * ks][1], acc[2 * ks + 1][1]);
+            const bf16x8 a = state_frag(acc[2 * ks], acc[2 * ks + 1]);
 #pragma unroll
-            for (int tb = 0; tb < 4; tb++) {
-                const bf16x8 a = load_query_perm(sOmq + (16 * tb + lr) * RS128 + 32 * ks, lg);
-                out[tb][0] = mfma_bf16(a, bs0, out[tb][0]);
-                out[tb][1] = mfma_bf16(a, bs1, out[tb][1]);
-            }
+            for (int tb = 0; tb < 4; tb++)
+                out[tb] = mfma_bf16(a, load_row_perm(sOm + (16 * tb + lr) * RS + 32 * ks, lg), out[tb]);
         }
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++) out[tb] *= sGam[64 + 16 * tb + lr];
+        __syncthreads();  // scores complete
+
+        // o^T += v^T P^T.
+        bf16x8 vb[2];
+#pragma unroll
+        for (int ss = 0; ss < 2; ss++) vb[ss] = load_tr_bf16(sV, RS, 32 * ss, 16 * w);
 #pragma unroll
         for (int tb = 0; tb < 4; tb++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float f = sGam[64 + 16 * tb + 4 * lg + i];
-                out[tb][0][i] *= f;
-                out[tb][1][i] *= f;
-            }
+            for (int ss = 0; ss <= (tb >> 1); ss++)
+                out[tb] = mfma_bf16(vb[ss], load_row<bf16x8>(sP, TS, 16 * tb, 32 * ss), out[tb]);
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++) {
+            if (t0 + 16 * tb + lr < p.T) st_b64(sq.o, o_lane, (uint32_t)(t0 + 16 * tb) * sq.row16, to_bf16x4(out[tb], 1.f));
+        }
+        // State update: S = 2^G_last S + w^T bf16(2^(G_last - G_s) v).
         const float dec = sGam[64 + 63];
 #pragma unroll
-        for (int mb = 0; mb < 8; mb++)
-#pragma unroll
-            for (int cb = 0; cb < 2; cb++) acc[mb][cb] *= dec;
+        for (int mb = 0; mb < 8; mb++) acc[mb] *= dec;
 #pragma unroll
         for (int ss = 0; ss < 2; ss++) {
-            bf16x8 vb[2], vt[2];
+            bf16x8 vt;
 #pragma unroll
-            for (int cb = 0; cb < 2; cb++) {
-                vb[cb] = load_tr_bf16(sV, RS256, 32 * ss, 32 * w + 16 * cb);
+            for (int jj = 0; jj < 8; jj++) vt[jj] = (bf16_t)((float)vb[ss][jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
 #pragma unroll
-                for (int jj = 0; jj < 8; jj++) vt[cb][jj] = (bf16_t)((float)vb[cb][jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
-            }
-#pragma unroll
-            for (int tb = 0; tb < 4; tb++) {
-                const bf16x8 a = load_row<bf16x8>(sP, TS, 16 * tb, 32 * ss);
-                out[tb][0] = mfma_bf16(a, vb[0], out[tb][0]);
-                out[tb][1] = mfma_bf16(a, vb[1], out[tb][1]);
-            }
-#pragma unroll
-            for (int mb = 0; mb < 8; mb++) {
-                const bf16x8 a = load_tr_bf16(sW, RS128, 32 * ss, 16 * mb);
-                acc[mb][0] = mfma_bf16(a, vt[0], acc[mb][0]);
-                acc[mb][1] = mfma_bf16(a, vt[1], acc[mb][1]);
-            }
-        }
-        __syncthreads();  // v is dead; reuse it for the output tile
-#pragma unroll
-        for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-            for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    sO[(16 * tb + 4 * lg + i) * RS256 + 32 * w + 16 * cb + lr] = (bf16_t)out[tb][cb][i];
-        __syncthreads();
-#pragma unroll
-        for (int it = 0; it < 4; it++) {
-            const int idx = tid + 512 * it, r = idx >> 5, c8 = (idx & 31) * 8;
-            if (t0 + r < p.T)
-                *reinterpret_cast<bf16x8*>(p.o + tok_index(p, b, t0 + r, h) * VD + c8) =
-                    *reinterpret_cast<const bf16x8*>(sO + r * RS256 + c8);
+            for (int mb = 0; mb < 8; mb++) acc[mb] = mfma_bf16(load_tr_bf16(sW, RS, 32 * ss, 16 * mb), vt, acc[mb]);
         }
         __syncthreads();
     }
@@ -861,9 +949,7 @@ __global__ __launch_bounds__(512) void pass2_kernel(PrefillParams p) {
 #pragma unroll
         for (int mb = 0; mb < 8; mb++)
 #pragma unroll
-            for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) dst[(16 * mb + 4 * lg + i) * VD + 32 * w + 16 * cb + lr] = acc[mb][cb][i];
+            for (int i = 0; i < 4; i++) dst[(16 * mb + 4 * lg + i) * VD + HALF * y + 16 * w + lr] = acc[mb][i];
     }
 }
 
@@ -891,8 +977,9 @@ __global__ __launch_bounds__(128) void readout_table_kernel(const float* readout
 }  // namespace
 
 void choose_segments(int BH, int N, int* P, int* L) {
-    // Aim for about one workgroup per CU (256 CUs) in the sweeps.
-    // CYFA_SEGMENT_CHUNKS=<L> fixes the chunks per segment (tests, tuning).
+    // Two sweep workgroups (key / value halves) per segment: aim for about two
+    // workgroups per CU (256 CUs). CYFA_SEGMENT_CHUNKS=<L> fixes the chunks per
+    // segment (tests, tuning).
     int target = (256 + BH - 1) / BH;
     if (target < 1) target = 1;
     if (target > N) target = N;
@@ -918,7 +1005,8 @@ WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V) {
     w.seg = align256(w.lam + BH * Tp * sizeof(float));
     const size_t seg_bytes = P > 1 ? BH * P * (size_t)(K * kSlots + kSlots * V) * sizeof(float) : 0;
     w.seg_decay = align256(w.seg + seg_bytes);
-    w.omega = align256(w.seg_decay + BH * P * sizeof(float));
+    w.raw = align256(w.seg_decay + BH * P * sizeof(float));
+    w.omega = align256(w.raw + 2 * BH * Tp * kSlots * 2);
     w.total = align256(w.omega + BH * Tp * kSlots * 2);
     return w;
 }
@@ -927,11 +1015,12 @@ int launch_prefill(const PrefillParams& p, hipStream_t stream) {
     const int BH = p.B * p.H;
     hipLaunchKernelGGL(clock_kernel, dim3(BH), dim3(256), 0, stream, p);
     if (p.P > 1) {
-        hipLaunchKernelGGL(segment_state_kernel, dim3(BH * (p.P - 1), 2), dim3(512), 0, stream, p);
+        hipLaunchKernelGGL(segment_state_kernel, dim3(BH * (p.P - 1), 4), dim3(512), 0, stream, p);
         hipLaunchKernelGGL(carry_kernel, dim3(BH, SEG / 1024), dim3(256), 0, stream, p);
     }
-    hipLaunchKernelGGL(pass1_kernel, dim3(BH * p.P), dim3(512), 0, stream, p);
-    hipLaunchKernelGGL(pass2_kernel, dim3(BH * p.P), dim3(512), 0, stream, p);
+    hipLaunchKernelGGL(pass1_kernel, dim3(sweep_grid(BH * p.P)), dim3(512), 0, stream, p);
+    hipLaunchKernelGGL(readout_kernel, dim3(p.H * readout_groups(p.B, p.Tp, p.H)), dim3(512), 0, stream, p);
+    hipLaunchKernelGGL(pass2_kernel, dim3(sweep_grid(BH * p.P)), dim3(512), 0, stream, p);
     return 0;
 }
 
