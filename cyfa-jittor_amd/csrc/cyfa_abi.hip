@@ -2,6 +2,7 @@
 // include/cyfa_abi.h). Validates arguments, maps them onto the kernel
 // parameter blocks and launches on the caller's stream. No device memory is
 // allocated here; the caller supplies every buffer, including the workspace.
+#include <math.h>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -106,6 +107,8 @@ int cyfa_chunk_fwd(const CyfaChunkArgs* a, void* hip_stream) {
     if (!a->q || !a->k || !a->v || !a->g || !a->delta || !a->beta || !a->table || !a->q_norm_weight ||
         !a->k_norm_weight || !a->o)
         return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd: null required pointer");
+    if (!(a->scale > 0.f) || !isfinite(a->scale))
+        return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd: scale must be positive and finite, got %g", (double)a->scale);
     const bool has_h0 = a->h0_k != nullptr;
     if (has_h0 != (a->h0_v != nullptr) || has_h0 != (a->clock0 != nullptr))
         return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd: h0_k, h0_v and clock0 must be all set or all null");
@@ -143,6 +146,7 @@ int cyfa_chunk_fwd(const CyfaChunkArgs* a, void* hip_stream) {
     p.q_eps = a->q_norm_eps;
     p.k_eps = a->k_norm_eps;
     p.scale = a->scale;
+    p.log2_scale = log2f(a->scale);
     p.h0_k = a->h0_k;
     p.h0_v = a->h0_v;
     p.clock0 = a->clock0;
@@ -152,6 +156,7 @@ int cyfa_chunk_fwd(const CyfaChunkArgs* a, void* hip_stream) {
     p.clock = a->clock;
     char* base = (char*)a->workspace;
     p.lam = (float*)(base + ws.lam);
+    p.gam = (float*)(base + ws.gam);
     p.seg = (float*)(base + ws.seg);
     p.seg_decay = (float*)(base + ws.seg_decay);
     p.raw = (__bf16*)(base + ws.raw);

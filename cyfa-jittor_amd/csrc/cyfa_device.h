@@ -69,8 +69,21 @@ __device__ __forceinline__ void phase_sincos(float lam, int pair, float& s, floa
 // in revolutions is then p * lam' (the same angle, modulo 2 pi, as the
 // reference's integer reduction above; p * lam' < 64 revolutions so one fp32
 // product keeps the angle to ~2.5e-5 rad), and the sine / cosine of pair p
-// cost one multiply and one transcendental each.
-__device__ __forceinline__ float reduced_clock(float lam) { return fmodf(lam, (float)kActive) * (1.0f / kActive); }
+// cost one multiply and one transcendental each. lam - R floor(lam / R) is
+// formed with one fma, which is exact (the result is a multiple of lam's ulp
+// below 2 R); the quotient estimate may be off by one, which the two
+// corrections undo.
+__device__ __forceinline__ float reduced_clock(float lam) {
+    const float q = floorf(lam * (1.0f / kActive));
+    float r = fmaf(-(float)kActive, q, lam);
+    r = r < 0.f ? r + (float)kActive : r;
+    r = r >= (float)kActive ? r - (float)kActive : r;
+    return r * (1.0f / kActive);
+}
+
+// 2^x with the hardware exponential (v_exp_f32); results below the normal
+// range flush to zero, which is what every caller wants for decay factors.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ void pair_sincos(float lamr, int pair, float& s, float& c) {
     const float rev = (float)pair * lamr;

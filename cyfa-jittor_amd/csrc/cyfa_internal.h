@@ -29,11 +29,13 @@ struct PrefillParams {
     const float* table;  // f32 [H, 127, 128]
     const float *q_w, *k_w;
     float q_eps, k_eps, scale;
+    float log2_scale;  // log2(scale), formed on the host (exact for powers of two)
     const float *h0_k, *h0_v, *clock0;
     __bf16* o;
     float *hk, *hv, *clock;
     // workspace
-    float* lam;        // [B*H, Tp] clock per token
+    float* lam;        // [B*H, Tp] reduced clock per token, (lam mod 127) / 127
+    float* gam;        // [B*H, Tp] in-chunk inclusive scan of g, log2 units
     float* seg;        // [B*H, P, K*128 + 128*V] segment-local states, then segment start states
     float* seg_decay;  // [B*H, P] product of alpha over each segment
     __bf16* raw;       // [2, B*H, Tp, 128] pass-1 output of each 128-wide key half
@@ -41,7 +43,7 @@ struct PrefillParams {
 };
 
 struct WorkspaceLayout {
-    size_t lam, seg, seg_decay, raw, omega, total;
+    size_t lam, gam, seg, seg_decay, raw, omega, total;
 };
 
 void choose_segments(int BH, int N, int* P, int* L);

@@ -95,9 +95,10 @@ __device__ __forceinline__ void st_b64(rsrc_t r, uint32_t off, uint32_t soff, bf
 }
 
 // The streams of one (batch, head) sequence: q, k, v, o rows of 512 bytes
-// H * 512 bytes apart, g / beta H * 4 bytes apart, lam contiguous.
+// H * 512 bytes apart, beta H * 4 bytes apart, the per-token reduced clock
+// and decay scan of the workspace contiguous.
 struct Seq {
-    rsrc_t q, k, v, o, g, beta, lam;
+    rsrc_t q, k, v, o, beta, lam, gam;
     uint32_t row16, row4;
 };
 
@@ -109,12 +110,22 @@ __device__ __forceinline__ Seq make_seq(const PrefillParams& p, int b, int h, in
     s.k = make_rsrc(p.k + first * KD, span * KD * 2);
     s.v = make_rsrc(p.v + first * VD, span * VD * 2);
     s.o = make_rsrc(p.o + first * VD, span * VD * 2);
-    s.g = make_rsrc(p.g + first, span * 4);
     s.beta = make_rsrc(p.beta + first, span * 4);
     s.lam = make_rsrc(p.lam + (size_t)bh * p.Tp, (size_t)p.Tp * 4);
+    s.gam = make_rsrc(p.gam + (size_t)bh * p.Tp, (size_t)p.Tp * 4);
     s.row16 = (uint32_t)p.H * KD * 2;
     s.row4 = (uint32_t)p.H * 4;
     return s;
+}
+
+// Segment states in the workspace are kept in the register order of the
+// sweeps: the float4 that lane `lane` of wave w holds as accumulator block x
+// (key-state row block kb or value-state row block mb) of half y sits at
+// float offset frag_offset(y, w, x, lane), so a wave loads or stores a block
+// as one contiguous 1 KiB run. The key state fills [0, SEG_K), the value state
+// [SEG_K, SEG).
+__host__ __device__ constexpr int frag_offset(int y, int w, int x, int lane) {
+    return (((y * 8 + w) * 8 + x) * 64 + lane) * 4;
 }
 
 // Sweep workgroups come in pairs (the two halves of one segment). Workgroup
@@ -146,42 +157,38 @@ __device__ __forceinline__ float octet_sum(float x) {
     return x;
 }
 
-// Chunk gates, loaded by every wave with lane = token (issue) and scanned /
-// staged in LDS by wave 0 (commit): the in-chunk scan of g in log2 units
-// (ops/utils.py:495-520). LDS per token: sLam = reduced clock (lam mod 127) /
-// 127, sBeta, sGam = G_t, sGam[64 + t] = 2^G_t, sGam[128 + t] = 2^(G_last - G_t).
+// Chunk gates, loaded by every wave with lane = token (issue) and staged in
+// LDS by wave 0 (commit). The clock kernel has already formed the reduced
+// clock lamr_t and the in-chunk decay scan G_t (log2 units, ops/utils.py:495-520).
+// LDS per token: sLam = lamr, sBeta, sGam = G_t, sGam[64 + t] = 2^G_t,
+// sGam[128 + t] = 2^(G_last - G_t).
 struct GateRegs {
-    float g, beta, lam;
+    float beta, lamr, gam;
 };
 
 __device__ __forceinline__ GateRegs issue_gates(const Seq& sq, int T, int t0) {
     const int t = t0 + (threadIdx.x & 63);
-    const uint32_t off = (uint32_t)(t < T ? t : T - 1) * sq.row4;
     GateRegs r;
-    r.g = ld_f32(sq.g, off);
-    r.beta = ld_f32(sq.beta, off);
-    r.lam = ld_f32(sq.lam, (uint32_t)t * 4);
+    r.beta = ld_f32(sq.beta, (uint32_t)(t < T ? t : T - 1) * sq.row4);
+    r.lamr = ld_f32(sq.lam, (uint32_t)t * 4);
+    r.gam = ld_f32(sq.gam, (uint32_t)t * 4);
     return r;
+}
+
+__device__ __forceinline__ float chunk_last_gam(const GateRegs& r) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r.gam), 63));
 }
 
 __device__ __forceinline__ void commit_gates(const PrefillParams& p, int t0, const GateRegs& r, float* sLam,
                                              float* sBeta, float* sGam) {
     const int tid = threadIdx.x;
     if (tid < 64) {
-        const bool valid = t0 + tid < p.T;
-        float x = valid ? r.g : 0.f;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const float y = __shfl_up(x, o, 64);
-            if (tid >= o) x += y;
-        }
-        const float gam = x * kLog2e;
-        const float last = __shfl(gam, 63, 64);
-        sGam[tid] = gam;
-        sBeta[tid] = valid ? r.beta : 0.f;
-        sLam[tid] = reduced_clock(r.lam);
-        sGam[64 + tid] = exp2f(gam);          // 2^G_t
-        sGam[128 + tid] = exp2f(last - gam);  // 2^(G_last - G_t)
+        const float last = chunk_last_gam(r);
+        sGam[tid] = r.gam;
+        sBeta[tid] = t0 + tid < p.T ? r.beta : 0.f;
+        sLam[tid] = r.lamr;
+        sGam[64 + tid] = fast_exp2(r.gam);          // 2^G_t
+        sGam[128 + tid] = fast_exp2(last - r.gam);  // 2^(G_last - G_t)
     }
 }
 
@@ -225,41 +232,48 @@ __device__ __forceinline__ V8 load_row(const T* X, int ld, int r0, int k0) {
 }
 
 // Full 256-wide rows [t0, t0 + 64) of a [B, T, H, 256] bf16 tensor for a
-// 512-thread block: thread tid holds row tid >> 3, columns 8 c + 64 it
-// (c = tid & 7, it = 0..3). Rows past T are clamped to T - 1 (zeroed when stored).
-__device__ __forceinline__ void issue_full_rows(const Seq& sq, rsrc_t x, int T, int t0, bf16x8 raw[4]) {
+// 512-thread block: thread tid holds row tid >> 3, columns 128 y + 8 c + 64 it
+// of its own half y (raw[it], it = 0, 1) and the same columns of the other half
+// (raw[2 + it]), c = tid & 7. Rows past T are clamped to T - 1 (zeroed when stored).
+__device__ __forceinline__ void issue_full_rows(const Seq& sq, rsrc_t x, int T, int t0, int y, bf16x8 raw[4]) {
     const int t = t0 + (threadIdx.x >> 3);
     const uint32_t off = (uint32_t)(t < T ? t : T - 1) * sq.row16 + 16 * (threadIdx.x & 7);
+    const uint32_t own = 2 * HALF * y, other = 2 * HALF * (1 - y);
 #pragma unroll
-    for (int it = 0; it < 4; it++) raw[it] = ld_b128(x, off + 128 * it);
+    for (int it = 0; it < 2; it++) {
+        raw[it] = ld_b128(x, off + own + 128 * it);
+        raw[2 + it] = ld_b128(x, off + other + 128 * it);
+    }
 }
 
 // x_hat = bf16(x rsqrt(mean x^2 + eps) w) over the full row (ops/qk_norm.py:64-107,
-// 206-233); the columns of half y are stored into dst [64][RS] (zero past T).
-// wn is the half's norm weight in LDS.
+// 206-233); the own-half columns are stored into dst [64][RS] (zero past T).
+// wn is the half's norm weight in LDS. The sum of squares uses the bf16 dot
+// product (two elements per instruction, fp32 accumulation).
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ void norm_store_half(const PrefillParams& p, int t0, const bf16x8 raw[4], const float* wn,
-                                                float eps, int y, bf16_t* dst) {
+                                                float eps, bf16_t* dst) {
     const int r = threadIdx.x >> 3, c = threadIdx.x & 7;
     float ss = 0.f;
 #pragma unroll
     for (int it = 0; it < 4; it++)
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float v = (float)raw[it][j];
-            ss = fmaf(v, v, ss);
+        for (int j = 0; j < 4; j++) {
+            const bf16x2 x2 = {raw[it][2 * j], raw[it][2 * j + 1]};
+            ss = __builtin_amdgcn_fdot2_f32_bf16(x2, x2, ss, false);
         }
     ss = octet_sum(ss);
     const float rs = t0 + r < p.T ? rsqrtf(ss * (1.f / KD) + eps) : 0.f;
 #pragma unroll
     for (int h2 = 0; h2 < 2; h2++) {
-        const bf16x8 x = y ? raw[2 + h2] : raw[h2];
         const int col = 8 * c + 64 * h2;
         const float4 w0 = *reinterpret_cast<const float4*>(wn + col);
         const float4 w1 = *reinterpret_cast<const float4*>(wn + col + 4);
         const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
         bf16x8 o;
 #pragma unroll
-        for (int j = 0; j < 8; j++) o[j] = (bf16_t)((float)x[j] * rs * wv[j]);
+        for (int j = 0; j < 8; j++) o[j] = (bf16_t)((float)raw[h2][j] * (rs * wv[j]));
         *reinterpret_cast<bf16x8*>(dst + r * RS + col) = o;
     }
 }
@@ -297,40 +311,28 @@ __device__ __forceinline__ void store_half_rows(const bf16x8 raw[2], int valid, 
 }
 
 // Write vector of the chunk, w [64 tokens][128] bf16 row-major (ops/utils.py:664-702),
-// from the gate registers (lane = token): wave w covers tokens w + 8 it, lane = pair.
+// from the gate registers: lane = token, wave w covers pairs 8 w .. 8 w + 7.
+// The hardware gives (cos, sin) of pair 8 w and of pair 1; the next pairs
+// follow by complex multiplication, i.e. rotation by theta (seven steps add
+// about 1e-6 to a result rounded to bf16).
 __device__ __forceinline__ void store_write_tile(const GateRegs& gr, int valid, bf16_t* dst) {
     const int lane = threadIdx.x & 63, w = wave_id();
-    const float lamr = reduced_clock(gr.lam);
     const float beta = lane < valid ? gr.beta : 0.f;
+    float s1, c1, sn, cs;
+    pair_sincos(gr.lamr, 1, s1, c1);
+    pair_sincos(gr.lamr, 8 * w, sn, cs);
+    bf16x8 o[2];
 #pragma unroll
-    for (int it = 0; it < 8; it++) {
-        const int s = w + 8 * it;
-        const float ls = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lamr), s));
-        const float bs = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, beta), s));
-        float we, wo;
-        write_pair(ls, bs, lane, we, wo);
-        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-        *reinterpret_cast<bf16x2*>(dst + s * RS + 2 * lane) = bf16x2{(bf16_t)we, (bf16_t)wo};
+    for (int q = 0; q < 8; q++) {
+        const float a = beta * pair_scale(8 * w + q);
+        o[q >> 2][2 * (q & 3)] = (bf16_t)(a * cs);
+        o[q >> 2][2 * (q & 3) + 1] = (bf16_t)(-a * sn);
+        const float cn = cs * c1 - sn * s1;
+        sn = sn * c1 + cs * s1;
+        cs = cn;
     }
-}
-
-// Write-vector element w[s][m] (ops/utils.py:664-702), rounded to bf16;
-// lamr is the token's reduced clock.
-__device__ __forceinline__ bf16_t write_elem(float lamr, float beta, int m) { return (bf16_t)write_coord(lamr, beta, m); }
-
-// Masked, decayed score tile for key block sb and query block tb, from an
-// accumulated q.k block: P[t][s] = bf16(2^(G_t - G_s) q_t.k_s) for s <= t, else 0
-// (ops/chunk_o.py:240-250).
-__device__ __forceinline__ void store_scores(const f32x4& sc, int tb, int sb, const float* sGam, bf16_t* sP) {
-    const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
-    const int s = 16 * sb + lr;
-    const float gs = sGam[s];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int t = 16 * tb + 4 * lg + i;
-        const float v = s <= t ? sc[i] * exp2f(sGam[t] - gs) : 0.f;
-        sP[t * TS + s] = (bf16_t)v;
-    }
+    *reinterpret_cast<bf16x8*>(dst + lane * RS + 16 * w) = o[0];
+    *reinterpret_cast<bf16x8*>(dst + lane * RS + 16 * w + 8) = o[1];
 }
 
 // The 10 causal 16 x 16 score blocks (query block tb >= key block sb): wave w
@@ -338,6 +340,40 @@ __device__ __forceinline__ void store_scores(const f32x4& sc, int tb, int sb, co
 __device__ __forceinline__ void score_block(int blk, int& tb, int& sb) {
     tb = blk < 1 ? 0 : blk < 3 ? 1 : blk < 6 ? 2 : 3;
     sb = blk - tb * (tb + 1) / 2;
+}
+
+// Block blk (query block tb >= key block sb) of the masked, decayed scores of
+// a query tile X and key tile Y ([64][RS], 128-wide contraction), into sP:
+// P[t][s] = bf16(2^(G_t - G_s) c x_t . y_s) for s <= t, else 0 (ops/chunk_o.py:240-250),
+// c = 2^log2_scale the output scale of the pass (exact for the default
+// scale 1/16: scaling a bf16 value by a power of two commutes with rounding).
+// The block is computed transposed (C rows = keys, columns = queries), so a
+// lane holds four consecutive keys of one query and writes them in one store.
+__device__ __forceinline__ void score_tile(const bf16_t* X, const bf16_t* Y, int blk, const float* sGam, float log2_scale,
+                                           bf16_t* sP) {
+    const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
+    int tb, sb;
+    score_block(blk, tb, sb);
+    bf16x8 a[4], b[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        a[ks] = load_row<bf16x8>(Y, RS, 16 * sb, 32 * ks);
+        b[ks] = load_row<bf16x8>(X, RS, 16 * tb, 32 * ks);
+    }
+    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) sc = mfma_bf16(a[ks], b[ks], sc);
+    const int t = 16 * tb + lr, s0 = 16 * sb + 4 * lg;
+    const float gt = sGam[t] + log2_scale;
+    const float4 gs = *reinterpret_cast<const float4*>(sGam + s0);
+    const float gsv[4] = {gs.x, gs.y, gs.z, gs.w};
+    bf16x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float v = sc[i] * fast_exp2(gt - gsv[i]);
+        o[i] = (bf16_t)(s0 + i <= t ? v : 0.f);
+    }
+    *reinterpret_cast<bf16x4*>(sP + t * TS + s0) = o;
 }
 
 __device__ __forceinline__ void zero_scores(bf16_t* sP) {
@@ -376,18 +412,32 @@ __device__ __forceinline__ bf16x4 to_bf16x4(const f32x4& x, float s) {
 }
 
 // ---------------------------------------------------------------------------
-// 1. Clock scan.
-__global__ __launch_bounds__(256) void clock_kernel(PrefillParams p) {
+// 1. Clock scan and in-chunk decay scan. One block (512 threads) per (batch,
+// head), 2048 tokens per step, four consecutive tokens per thread:
+//   lam[t] = reduced_clock(clock0 + sum_{s<=t} delta_s)   (double carry across steps)
+//   gam[t] = log2(e) sum_{chunk start <= s <= t} g_s       (ops/utils.py:495-520)
+// The 16 threads of a 64-token chunk form one DPP row.
+template <int CTRL>
+__device__ __forceinline__ float dpp_shift(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+constexpr int CLOCK_THREADS = 512;
+
+__global__ __launch_bounds__(CLOCK_THREADS) void clock_kernel(PrefillParams p) {
+    constexpr int NW = CLOCK_THREADS / 64;
     const int bh = blockIdx.x, b = bh / p.H, h = bh % p.H;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    __shared__ float s_tot[4];
+    __shared__ float s_tot[NW];
     double carry = p.clock0 ? (double)p.clock0[bh] : 0.0;
-    for (int t0 = 0; t0 < p.Tp; t0 += 1024) {
-        float d[4];
+    for (int t0 = 0; t0 < p.Tp; t0 += 4 * CLOCK_THREADS) {
+        float d[4], gg[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int t = t0 + 4 * tid + j;
-            d[j] = t < p.T ? p.delta[tok_index(p, b, t, h)] : 0.f;
+            const bool valid = t < p.T;
+            d[j] = valid ? p.delta[tok_index(p, b, t, h)] : 0.f;
+            gg[j] = valid ? p.g[tok_index(p, b, t, h)] : 0.f;
         }
         const float s1 = d[0] + d[1], s2 = s1 + d[2], s3 = s2 + d[3];
         const float pre[4] = {d[0], s1, s2, s3};
@@ -397,16 +447,31 @@ __global__ __launch_bounds__(256) void clock_kernel(PrefillParams p) {
             const float y = __shfl_up(x, o, 64);
             if (lane >= o) x += y;
         }
+        // in-chunk inclusive scan of g over the row's 16 threads (row_shr 1, 2, 4, 8)
+        const float g1 = gg[0] + gg[1], g2 = g1 + gg[2], g3 = g2 + gg[3];
+        float xs = g3;
+        xs += dpp_shift<0x111>(xs);
+        xs += dpp_shift<0x112>(xs);
+        xs += dpp_shift<0x114>(xs);
+        xs += dpp_shift<0x118>(xs);
+        const float gex = xs - g3;
+        const float gpre[4] = {gg[0], g1, g2, g3};
         if (lane == 63) s_tot[wave] = x;
         __syncthreads();
-        float before = 0.f;
-        for (int w = 0; w < wave; w++) before += s_tot[w];
-        const float tile = s_tot[0] + s_tot[1] + s_tot[2] + s_tot[3];
+        float before = 0.f, tile = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            before += w < wave ? s_tot[w] : 0.f;
+            tile += s_tot[w];
+        }
         const float excl = before + x - s3;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int t = t0 + 4 * tid + j;
-            if (t < p.Tp) p.lam[(size_t)bh * p.Tp + t] = (float)(carry + (double)(excl + pre[j]));
+            if (t < p.Tp) {
+                p.lam[(size_t)bh * p.Tp + t] = reduced_clock((float)(carry + (double)(excl + pre[j])));
+                p.gam[(size_t)bh * p.Tp + t] = (gex + gpre[j]) * kLog2e;
+            }
         }
         carry += (double)tile;
         __syncthreads();
@@ -421,7 +486,7 @@ __global__ __launch_bounds__(256) void clock_kernel(PrefillParams p) {
 // y = 2, 3: value-state columns [128 (y-2), + 128); wave w owns 16 of them:
 // acc[mb] = S[16 mb + 4 lg + i][128 (y-2) + 16 w + lr].
 constexpr int SG_A = 0;                   // bf16 [64][RS]: k_hat half (key) or w (value)
-constexpr int SG_B = SG_A + 64 * RS * 2;  // bf16 [64][RS]: v half (value)
+constexpr int SG_B = SG_A + 64 * RS * 2;  // bf16 [64][RS]: w (key) or v half (value)
 constexpr int SG_G = SG_B + 64 * RS * 2;  // f32 [5][64] gates
 constexpr int SG_NW = SG_G + 5 * 64 * 4;  // f32 [128] k norm weight (half)
 constexpr int SG_LDS = SG_NW + HALF * 4;
@@ -450,27 +515,27 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
         const int y = part;
         if (tid < HALF) sNw[tid] = p.k_w[HALF * y + tid];
         bf16x8 kraw[4];
-        issue_full_rows(sq, sq.k, p.T, n0 * 64, kraw);
+        issue_full_rows(sq, sq.k, p.T, n0 * 64, y, kraw);
         float logdecay = 0.f;
         __syncthreads();
         for (int n = n0; n < n1; n++) {
             const int t0 = n * 64;
             commit_gates(p, t0, gr, sLam, sBeta, sGam);
-            norm_store_half(p, t0, kraw, sNw, p.k_eps, y, sA);
+            store_write_tile(gr, p.T - t0, sB);
+            norm_store_half(p, t0, kraw, sNw, p.k_eps, sA);
             if (n + 1 < n1) {
-                issue_full_rows(sq, sq.k, p.T, t0 + 64, kraw);
+                issue_full_rows(sq, sq.k, p.T, t0 + 64, y, kraw);
                 gr = issue_gates(sq, p.T, t0 + 64);
             }
             __syncthreads();
             logdecay += sGam[63];
             bf16x8 wt[2];
 #pragma unroll
-            for (int ss = 0; ss < 2; ss++)
+            for (int ss = 0; ss < 2; ss++) {
+                const bf16x8 wf = load_tr_bf16(sB, RS, 32 * ss, 16 * w);
 #pragma unroll
-                for (int jj = 0; jj < 8; jj++) {
-                    const int s = 32 * ss + 8 * lg + jj;
-                    wt[ss][jj] = (bf16_t)((float)write_elem(sLam[s], sBeta[s], 16 * w + lr) * sGam[128 + s]);
-                }
+                for (int jj = 0; jj < 8; jj++) wt[ss][jj] = (bf16_t)((float)wf[jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
+            }
             const float dec = sGam[64 + 63];
 #pragma unroll
             for (int kb = 0; kb < 8; kb++) acc[kb] *= dec;
@@ -481,9 +546,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
             __syncthreads();
         }
 #pragma unroll
-        for (int kb = 0; kb < 8; kb++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) out[(HALF * y + 16 * kb + 4 * lg + i) * kSlots + 16 * w + lr] = acc[kb][i];
+        for (int kb = 0; kb < 8; kb++) *reinterpret_cast<f32x4*>(out + frag_offset(y, w, kb, lane)) = acc[kb];
         if (y == 0 && tid == 0) p.seg_decay[bh * p.P + j] = exp2f(logdecay);
     } else {
         const int y = part - 2;
@@ -515,9 +578,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
         }
         float* outv = out + SEG_K;
 #pragma unroll
-        for (int mb = 0; mb < 8; mb++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) outv[(16 * mb + 4 * lg + i) * VD + HALF * y + 16 * w + lr] = acc[mb][i];
+        for (int mb = 0; mb < 8; mb++) *reinterpret_cast<f32x4*>(outv + frag_offset(y, w, mb, lane)) = acc[mb];
     }
 }
 
@@ -528,10 +589,20 @@ __global__ __launch_bounds__(256) void carry_kernel(PrefillParams p) {
     const int bh = blockIdx.x;
     const int e = (blockIdx.y * 256 + threadIdx.x) * 4;
     float4 S = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (e < SEG_K) {
-        if (p.h0_k) S = *reinterpret_cast<const float4*>(p.h0_k + (size_t)bh * SEG_K + e);
-    } else {
-        if (p.h0_v) S = *reinterpret_cast<const float4*>(p.h0_v + (size_t)bh * SEG_V + (e - SEG_K));
+    {
+        // e is a register-order offset; find the four row-major elements it holds.
+        const bool key = e < SEG_K;
+        const int f = (key ? e : e - SEG_K) >> 2;
+        const int lane = f & 63, x = (f >> 6) & 7, w = (f >> 9) & 7, y = f >> 12;
+        const int lr = lane & 15, lg = lane >> 4;
+        const float* h0 = key ? p.h0_k : p.h0_v;
+        if (h0) {
+            const int ld = key ? kSlots : VD;
+            const int row = key ? HALF * y + 16 * x + 4 * lg : 16 * x + 4 * lg;
+            const int col = key ? 16 * w + lr : HALF * y + 16 * w + lr;
+            const float* src = h0 + (size_t)bh * (key ? SEG_K : SEG_V) + row * ld + col;
+            S = make_float4(src[0], src[ld], src[2 * ld], src[3 * ld]);
+        }
     }
     for (int j = 0; j < p.P; j++) {
         float4* slot = reinterpret_cast<float4*>(p.seg + ((size_t)bh * p.P + j) * SEG + e);
@@ -580,6 +651,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void p
     const int bh = sw.unit / p.P, j = sw.unit % p.P, y = sw.half;
     const int b = bh / p.H, h = bh % p.H;
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), lr = lane & 15, lg = lane >> 4;
+    const float log2_scale = p.log2_scale;
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
     if (tid < HALF) {
         sQw[tid] = p.q_w[HALF * y + tid];
@@ -588,13 +660,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void p
     zero_scores(sP);  // the two blocks above the diagonal that the intra product reads stay zero
     f32x4 acc[8];
     {
-        const float* s0 = p.P > 1 ? p.seg + ((size_t)bh * p.P + j) * SEG
-                                  : (p.h0_k ? p.h0_k + (size_t)bh * SEG_K : nullptr);
-        if (s0) {
+        const float* h0 = p.h0_k ? p.h0_k + (size_t)bh * SEG_K : nullptr;
+        if (p.P > 1) {
+            const float* s0 = p.seg + ((size_t)bh * p.P + j) * SEG;
+#pragma unroll
+            for (int kb = 0; kb < 8; kb++) acc[kb] = *reinterpret_cast<const f32x4*>(s0 + frag_offset(y, w, kb, lane));
+        } else if (h0) {
 #pragma unroll
             for (int kb = 0; kb < 8; kb++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[kb][i] = s0[(HALF * y + 16 * kb + 4 * lg + i) * kSlots + 16 * w + lr];
+                for (int i = 0; i < 4; i++) acc[kb][i] = h0[(HALF * y + 16 * kb + 4 * lg + i) * kSlots + 16 * w + lr];
         } else {
 #pragma unroll
             for (int kb = 0; kb < 8; kb++) acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -604,8 +679,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void p
     const rsrc_t rraw = make_rsrc(p.raw + ((size_t)y * p.B * p.H + bh) * p.Tp * kSlots, (size_t)p.Tp * kSlots * 2);
     const uint32_t raw_lane = (uint32_t)lr * (kSlots * 2) + 2 * (16 * w + 4 * lg);
     bf16x8 qraw[4], kraw[4];
-    issue_full_rows(sq, sq.q, p.T, n0 * 64, qraw);
-    issue_full_rows(sq, sq.k, p.T, n0 * 64, kraw);
+    issue_full_rows(sq, sq.q, p.T, n0 * 64, y, qraw);
+    issue_full_rows(sq, sq.k, p.T, n0 * 64, y, kraw);
     GateRegs gr = issue_gates(sq, p.T, n0 * 64);
     __syncthreads();  // norm weights staged, score tile zeroed
 
@@ -613,26 +688,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void p
         const int t0 = n * 64;
         commit_gates(p, t0, gr, sLam, sBeta, sGam);
         store_write_tile(gr, p.T - t0, sW);
-        norm_store_half(p, t0, qraw, sQw, p.q_eps, y, sQ);
-        norm_store_half(p, t0, kraw, sKw, p.k_eps, y, sK);
+        norm_store_half(p, t0, qraw, sQw, p.q_eps, sQ);
+        norm_store_half(p, t0, kraw, sKw, p.k_eps, sK);
         sched_fence();  // the next chunk's loads reuse these registers
         if (n + 1 < n1) {
-            issue_full_rows(sq, sq.q, p.T, t0 + 64, qraw);
-            issue_full_rows(sq, sq.k, p.T, t0 + 64, kraw);
+            issue_full_rows(sq, sq.q, p.T, t0 + 64, y, qraw);
+            issue_full_rows(sq, sq.k, p.T, t0 + 64, y, kraw);
             gr = issue_gates(sq, p.T, t0 + 64);
         }
         __syncthreads();
 
         // Masked, decayed scores of this half's key slice.
-        for (int blk = w; blk < 10; blk += 8) {
-            int tb, sb;
-            score_block(blk, tb, sb);
-            f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-                sc = mfma_bf16(load_row<bf16x8>(sQ, RS, 16 * tb, 32 * ks), load_row<bf16x8>(sK, RS, 16 * sb, 32 * ks), sc);
-            store_scores(sc, tb, sb, sGam, sP);
-        }
+        score_tile(sQ, sK, w, sGam, log2_scale, sP);
+        if (w < 2) score_tile(sQ, sK, w + 8, sGam, log2_scale, sP);
         // raw^T = 2^G_t S_n^T q_t over this half's key rows.
         f32x4 out[4];
 #pragma unroll
@@ -646,10 +714,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void p
             sched_fence();
         }
 #pragma unroll
-        for (int tb = 0; tb < 4; tb++) out[tb] *= sGam[64 + 16 * tb + lr];
+        for (int tb = 0; tb < 4; tb++) out[tb] *= sGam[64 + 16 * tb + lr] * p.scale;
         __syncthreads();  // scores complete
 
-        // raw^T += w^T P^T; the blocks of P above the diagonal are zero.
+        // raw^T += w^T P^T (P carries the scale); the blocks of P above the diagonal are zero.
         // wf[ss][jj] = w[32 ss + 8 lg + jj][16 w + lr].
         bf16x8 wf[2];
 #pragma unroll
@@ -661,7 +729,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void p
                 out[tb] = mfma_bf16(wf[ss], load_row<bf16x8>(sP, TS, 16 * tb, 32 * ss), out[tb]);
 #pragma unroll
         for (int tb = 0; tb < 4; tb++)
-            st_b64(rraw, raw_lane, (uint32_t)(t0 + 16 * tb) * (kSlots * 2), to_bf16x4(out[tb], p.scale));
+            st_b64(rraw, raw_lane, (uint32_t)(t0 + 16 * tb) * (kSlots * 2), to_bf16x4(out[tb], 1.f));
         // State update: S = 2^G_last S + k_hat^T bf16(2^(G_last - G_s) w).
         const float dec = sGam[64 + 63];
 #pragma unroll
@@ -730,17 +798,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void r
 
     const int blocks = p.Tp / 16, tasks = p.B * blocks;
     const size_t plane = (size_t)p.B * p.H * p.Tp * kSlots;
-    for (int task = grp * 8 + w; task < tasks; task += ngrp * 8) {
+    // raw rows of the wave's next task are loaded while the current one computes
+    bf16x8 ra[4], rb[4];
+    float lam_next = 0.f;
+    auto issue = [&](int task) {
         const int b = task / blocks, t = 16 * (task % blocks) + lr;
-        const int bh = b * p.H + h;
-        const size_t row = ((size_t)bh * p.Tp + t) * kSlots;
-        bf16x8 ra[4], rb[4];
+        const size_t row = ((size_t)(b * p.H + h) * p.Tp + t) * kSlots;
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             ra[ks] = *reinterpret_cast<const bf16x8*>(p.raw + row + 32 * ks + 8 * lg);
             rb[ks] = *reinterpret_cast<const bf16x8*>(p.raw + plane + row + 32 * ks + 8 * lg);
         }
-        const float lamr = reduced_clock(p.lam[(size_t)bh * p.Tp + t]);
+        lam_next = p.lam[(size_t)(b * p.H + h) * p.Tp + t];
+    };
+    int task = grp * 8 + w;
+    if (task < tasks) issue(task);
+    for (; task < tasks; task += ngrp * 8) {
+        const int b = task / blocks, t = 16 * (task % blocks) + lr;
+        const int bh = b * p.H + h;
+        const size_t row = ((size_t)bh * p.Tp + t) * kSlots;
+        const float lamr = lam_next;
         // z fragments: element j = z_t[32 ks + 8 lg + j].
         f16x8 zf[4];
 #pragma unroll
@@ -754,6 +831,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void r
                 zf[ks][2 * q] = (f16_t)(cs * e - sn * o);
                 zf[ks][2 * q + 1] = (f16_t)(sn * e + cs * o);
             }
+        if (task + ngrp * 8 < tasks) issue(task + ngrp * 8);
         f32x4 L[8];
 #pragma unroll
         for (int rb8 = 0; rb8 < 8; rb8++) L[rb8] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -859,13 +937,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void p
     zero_scores(sP);
     f32x4 acc[8];
     {
-        const float* s0 = p.P > 1 ? p.seg + ((size_t)bh * p.P + j) * SEG + SEG_K
-                                  : (p.h0_v ? p.h0_v + (size_t)bh * SEG_V : nullptr);
-        if (s0) {
+        const float* h0 = p.h0_v ? p.h0_v + (size_t)bh * SEG_V : nullptr;
+        if (p.P > 1) {
+            const float* s0 = p.seg + ((size_t)bh * p.P + j) * SEG + SEG_K;
+#pragma unroll
+            for (int mb = 0; mb < 8; mb++) acc[mb] = *reinterpret_cast<const f32x4*>(s0 + frag_offset(y, w, mb, lane));
+        } else if (h0) {
 #pragma unroll
             for (int mb = 0; mb < 8; mb++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[mb][i] = s0[(16 * mb + 4 * lg + i) * VD + HALF * y + 16 * w + lr];
+                for (int i = 0; i < 4; i++) acc[mb][i] = h0[(16 * mb + 4 * lg + i) * VD + HALF * y + 16 * w + lr];
         } else {
 #pragma unroll
             for (int mb = 0; mb < 8; mb++) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -892,15 +973,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void p
         }
         __syncthreads();
 
-        for (int blk = w; blk < 10; blk += 8) {
-            int tb, sb;
-            score_block(blk, tb, sb);
-            f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-                sc = mfma_bf16(load_row<bf16x8>(sOm, RS, 16 * tb, 32 * ks), load_row<bf16x8>(sW, RS, 16 * sb, 32 * ks), sc);
-            store_scores(sc, tb, sb, sGam, sP);
-        }
+        score_tile(sOm, sW, w, sGam, 0.f, sP);
+        if (w < 2) score_tile(sOm, sW, w + 8, sGam, 0.f, sP);
         // o^T = 2^G_t S_n^T weights_t.
         f32x4 out[4];
 #pragma unroll
@@ -1002,7 +1076,8 @@ WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V) {
     choose_segments(B * H, N, &P, &L);
     const size_t BH = (size_t)B * H;
     w.lam = 0;
-    w.seg = align256(w.lam + BH * Tp * sizeof(float));
+    w.gam = align256(w.lam + BH * Tp * sizeof(float));
+    w.seg = align256(w.gam + BH * Tp * sizeof(float));
     const size_t seg_bytes = P > 1 ? BH * P * (size_t)(K * kSlots + kSlots * V) * sizeof(float) : 0;
     w.seg_decay = align256(w.seg + seg_bytes);
     w.raw = align256(w.seg_decay + BH * P * sizeof(float));
@@ -1013,7 +1088,7 @@ WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V) {
 
 int launch_prefill(const PrefillParams& p, hipStream_t stream) {
     const int BH = p.B * p.H;
-    hipLaunchKernelGGL(clock_kernel, dim3(BH), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(clock_kernel, dim3(BH), dim3(CLOCK_THREADS), 0, stream, p);
     if (p.P > 1) {
         hipLaunchKernelGGL(segment_state_kernel, dim3(BH * (p.P - 1), 4), dim3(512), 0, stream, p);
         hipLaunchKernelGGL(carry_kernel, dim3(BH, SEG / 1024), dim3(256), 0, stream, p);
