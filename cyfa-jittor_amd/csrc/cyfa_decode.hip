@@ -3,8 +3,10 @@
 // One 1024-thread workgroup per (batch, head). The step is HBM-bound: it
 // streams the fp32 key state hk [K, M] and value state hv [M, V] in and out
 // once (512 KiB per (b, h) for K = V = 256). Both states are issued as
-// coalesced float4 loads at kernel entry, so the value-state stream is in
-// flight while the key-state update, the query and the slot readout run.
+// coalesced float4 loads at kernel entry. Both updated states are written
+// before the slot readout runs (the value-state update does not depend on the
+// readout; the updated hv stays in registers for o = hv'^T weights), so the
+// write stream drains while the readout computes.
 //
 // Math (ops/fused_recurrent.py:57-188): q_hat = bf16(q rs_q w_q) * scale,
 // k_hat = bf16(k rs_k w_k); lam = clock + delta; alpha = e^g;
@@ -125,6 +127,23 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
             s_part[wave][m4 + 3] = a3;
         }
     }
+    // Value state: hv' = alpha hv + w (x) v, written now; kept in hv_r for o.
+    {
+        const int v4 = (tid % VQ) * 4, r0 = tid / VQ;
+        const bf16x4 vb = *reinterpret_cast<const bf16x4*>(p.v + (size_t)bh * V + v4);
+        const float v0 = (float)vb[0], v1 = (float)vb[1], v2 = (float)vb[2], v3 = (float)vb[3];
+#pragma unroll
+        for (int j = 0; j < VJ; j++) {
+            const float wm = s_w[r0 + VROWS * j];
+            float4 n = hv_r[j];
+            n.x = fmaf(n.x, decay, wm * v0);
+            n.y = fmaf(n.y, decay, wm * v1);
+            n.z = fmaf(n.z, decay, wm * v2);
+            n.w = fmaf(n.w, decay, wm * v3);
+            hv_out[tid + NT * j] = n;
+            hv_r[j] = n;
+        }
+    }
     __syncthreads();
     if (tid < kSlots) {
         float r = 0.f;
@@ -192,26 +211,17 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     }
     __syncthreads();
 
-    // Value state: hv' = alpha hv + w (x) v ; o = hv'^T weights.
+    // o = hv'^T weights, from the updated value state kept in registers.
     {
         const int v4 = (tid % VQ) * 4, r0 = tid / VQ;
-        const bf16x4 vb = *reinterpret_cast<const bf16x4*>(p.v + (size_t)bh * V + v4);
-        const float v0 = (float)vb[0], v1 = (float)vb[1], v2 = (float)vb[2], v3 = (float)vb[3];
         float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
         for (int j = 0; j < VJ; j++) {
-            const int m = r0 + VROWS * j;
-            const float wm = s_w[m], om = s_om[m];
-            float4 n = hv_r[j];
-            n.x = fmaf(n.x, decay, wm * v0);
-            n.y = fmaf(n.y, decay, wm * v1);
-            n.z = fmaf(n.z, decay, wm * v2);
-            n.w = fmaf(n.w, decay, wm * v3);
-            hv_out[tid + NT * j] = n;
-            a0 = fmaf(n.x, om, a0);
-            a1 = fmaf(n.y, om, a1);
-            a2 = fmaf(n.z, om, a2);
-            a3 = fmaf(n.w, om, a3);
+            const float om = s_om[r0 + VROWS * j];
+            a0 = fmaf(hv_r[j].x, om, a0);
+            a1 = fmaf(hv_r[j].y, om, a1);
+            a2 = fmaf(hv_r[j].z, om, a2);
+            a3 = fmaf(hv_r[j].w, om, a3);
         }
         if (VQ == 32) {  // two rows of the sweep share a wave
             a0 += __shfl_xor(a0, 32);
@@ -219,7 +229,6 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
             a2 += __shfl_xor(a2, 32);
             a3 += __shfl_xor(a3, 32);
         }
-        __syncthreads();  // s_part reuse
         if (VQ == 64 || lane < 32) {
             s_part[wave][v4] = a0;
             s_part[wave][v4 + 1] = a1;
