@@ -165,4 +165,80 @@ int cyfa_chunk_fwd(const CyfaChunkArgs* a, void* hip_stream) {
     return check_launch("cyfa_chunk_fwd");
 }
 
+int cyfa_rms_norm(const CyfaNormArgs* a, void* hip_stream) {
+    if (!a) return fail(CYFA_ERR_VALUE, "cyfa_rms_norm: null args");
+    if (a->rows < 0 || a->D <= 0) return fail(CYFA_ERR_VALUE, "cyfa_rms_norm: rows=%d D=%d", a->rows, a->D);
+    if (a->D % 256 != 0 || a->D > 2048 || (a->D / 256 & (a->D / 256 - 1)) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_rms_norm: D=%d must be 256, 512, 1024 or 2048", a->D);
+    if (!a->x || !a->weight || !a->out || (a->residual && !a->sum_out))
+        return fail(CYFA_ERR_VALUE, "cyfa_rms_norm: null required pointer");
+    if (!aligned(a->x, 8) || !aligned(a->out, 8) || !aligned(a->weight, 16) || (a->residual && !aligned(a->residual, 8)) ||
+        (a->sum_out && !aligned(a->sum_out, 8)) || (a->gate && !aligned(a->gate, 8)))
+        return fail(CYFA_ERR_ALIGN, "cyfa_rms_norm: bf16 rows need 8-byte and the weight 16-byte alignment");
+    if (a->rows == 0) return CYFA_OK;
+    cyfa::NormParams p;
+    p.rows = a->rows;
+    p.D = a->D;
+    p.x = (const __bf16*)a->x;
+    p.residual = (const __bf16*)a->residual;
+    p.sum_out = (__bf16*)a->sum_out;
+    p.weight = a->weight;
+    p.gate = (const __bf16*)a->gate;
+    p.eps = a->eps;
+    p.prescale = a->prescale;
+    p.out = (__bf16*)a->out;
+    cyfa::launch_rms_norm(p, (hipStream_t)hip_stream);
+    return check_launch("cyfa_rms_norm");
+}
+
+int cyfa_short_conv(const CyfaConvArgs* a, void* hip_stream) {
+    if (!a) return fail(CYFA_ERR_VALUE, "cyfa_short_conv: null args");
+    if (a->B < 0 || a->T < 0 || a->D <= 0 || a->split <= 0)
+        return fail(CYFA_ERR_VALUE, "cyfa_short_conv: B=%d T=%d D=%d split=%d", a->B, a->T, a->D, a->split);
+    if (a->W < 2 || a->W > 4) return fail(CYFA_ERR_UNSUPPORTED, "cyfa_short_conv: width %d not in 2..4", a->W);
+    if (a->D % 8 != 0 || a->split % 8 != 0 || a->D % a->split != 0 || a->D / a->split > 3)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_short_conv: D=%d split=%d (multiples of 8, at most 3 outputs)", a->D,
+                    a->split);
+    if (!a->x || !a->weight) return fail(CYFA_ERR_VALUE, "cyfa_short_conv: null required pointer");
+    for (int i = 0; i < a->D / a->split; i++)
+        if (!a->out[i] || !aligned(a->out[i], 16)) return fail(CYFA_ERR_ALIGN, "cyfa_short_conv: output %d null or misaligned", i);
+    if (!aligned(a->x, 16) || a->x_row % 8 != 0 || (a->cache && (!aligned(a->cache, 16) || a->cache_row % 8 || a->cache_batch % 8)))
+        return fail(CYFA_ERR_ALIGN, "cyfa_short_conv: inputs need 16-byte aligned rows");
+    if (a->B == 0 || a->T == 0) return CYFA_OK;
+    cyfa::ConvParams p;
+    p.B = a->B;
+    p.T = a->T;
+    p.D = a->D;
+    p.W = a->W;
+    p.x = (const __bf16*)a->x;
+    p.x_row = a->x_row;
+    p.cache = (const __bf16*)a->cache;
+    p.cache_row = a->cache_row;
+    p.cache_batch = a->cache_batch;
+    p.weight = (const __bf16*)a->weight;
+    p.bias = (const __bf16*)a->bias;
+    for (int i = 0; i < 3; i++) p.out[i] = (__bf16*)a->out[i];
+    p.split = a->split;
+    cyfa::launch_short_conv(p, (hipStream_t)hip_stream);
+    return check_launch("cyfa_short_conv");
+}
+
+int cyfa_silu_mul(const void* gu, void* out, int rows, int F, void* hip_stream) {
+    if (!gu || !out || rows < 0 || F <= 0) return fail(CYFA_ERR_VALUE, "cyfa_silu_mul: bad arguments");
+    if (F % 8 != 0) return fail(CYFA_ERR_UNSUPPORTED, "cyfa_silu_mul: F=%d must be a multiple of 8", F);
+    if (!aligned(gu, 16) || !aligned(out, 16)) return fail(CYFA_ERR_ALIGN, "cyfa_silu_mul: 16-byte alignment needed");
+    if (rows == 0) return CYFA_OK;
+    cyfa::launch_silu_mul((const __bf16*)gu, (__bf16*)out, rows, F, (hipStream_t)hip_stream);
+    return check_launch("cyfa_silu_mul");
+}
+
+int cyfa_gates(const void* abd, const float* dt_bias, const float* A_log, float* g, float* beta, float* delta, int rows,
+               int H, void* hip_stream) {
+    if (!abd || !dt_bias || !A_log || !g || !beta || !delta || rows < 0 || H <= 0)
+        return fail(CYFA_ERR_VALUE, "cyfa_gates: bad arguments");
+    if (rows == 0) return CYFA_OK;
+    cyfa::launch_gates((const __bf16*)abd, dt_bias, A_log, g, beta, delta, rows, H, (hipStream_t)hip_stream);
+    return check_launch("cyfa_gates");
+}
+
 }  // extern "C"

@@ -42,6 +42,28 @@ struct PrefillParams {
     __bf16* omega;     // [B*H, Tp, 128] slot weights between the two passes
 };
 
+// Layer-side kernels (cyfa_layer.hip).
+struct NormParams {
+    int rows, D;
+    const __bf16 *x, *residual;  // residual nullable
+    __bf16* sum_out;             // receives bf16(x + residual) when residual is set
+    const float* weight;         // fp32 [D]
+    const __bf16* gate;          // nullable, [rows, D]
+    float eps, prescale;
+    __bf16* out;
+};
+
+struct ConvParams {
+    int B, T, D, W;
+    const __bf16* x;
+    long long x_row;             // elements between time rows of x
+    const __bf16* cache;         // nullable: [B, W-1, D] view
+    long long cache_row, cache_batch;
+    const __bf16 *weight, *bias; // [D, W], nullable [D]
+    __bf16* out[3];              // channel c -> out[c / split][(b*T + t)*split + c % split]
+    int split;
+};
+
 struct WorkspaceLayout {
     size_t lam, gam, seg, seg_decay, raw, omega, total;
 };
@@ -52,5 +74,10 @@ WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V);
 int launch_decode_step(const DecodeParams& p, int K, int V, hipStream_t stream);
 int launch_prefill(const PrefillParams& p, hipStream_t stream);
 int launch_readout_table(const float* readout, float* table, int H, hipStream_t stream);
+int launch_rms_norm(const NormParams& p, hipStream_t stream);
+int launch_short_conv(const ConvParams& p, hipStream_t stream);
+int launch_silu_mul(const __bf16* gu, __bf16* out, int rows, int F, hipStream_t stream);
+int launch_gates(const __bf16* abd, const float* dt_bias, const float* A_log, float* g, float* beta, float* delta,
+                 int rows, int H, hipStream_t stream);
 
 }  // namespace cyfa

@@ -1,0 +1,197 @@
+// cyfa_layer.hip -- the layer-side kernels either side of the CyFA op for gfx950:
+// fused residual add + RMSNorm (+ sigmoid gate), the causal depthwise short
+// convolution, the gate activations and the SwiGLU product. All are
+// HBM-streaming elementwise / row kernels; each reads its inputs once and
+// writes its outputs once, in bf16 with fp32 arithmetic.
+#include "cyfa_device.h"
+#include "cyfa_internal.h"
+
+namespace cyfa {
+
+namespace {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + expf(-x)); }
+
+// One wave per row; lane covers columns 4 lane + 256 j.
+// (layers/cyfa.py:62-135 and modeling_cyfa.py:48-51)
+//   s   = residual ? bf16(x + residual) : x      (sum_out receives s)
+//   xs  = prescale != 1 ? bf16(s * prescale) : s
+//   out = bf16(xs * rsqrt(mean xs^2 + eps) * weight * (gate ? sigmoid(gate) : 1))
+template <int J>
+__global__ __launch_bounds__(256) void rms_norm_kernel(NormParams p) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= p.rows) return;
+    const size_t base = (size_t)row * p.D;
+    float v[J][4];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int d = 4 * lane + 256 * j;
+        const bf16x4 x = *reinterpret_cast<const bf16x4*>(p.x + base + d);
+        if (p.residual) {
+            const bf16x4 r = *reinterpret_cast<const bf16x4*>(p.residual + base + d);
+            bf16x4 s;
+#pragma unroll
+            for (int i = 0; i < 4; i++) s[i] = (bf16_t)((float)x[i] + (float)r[i]);
+            *reinterpret_cast<bf16x4*>(p.sum_out + base + d) = s;
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[j][i] = (float)s[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[j][i] = (float)x[i];
+        }
+        if (p.prescale != 1.f) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[j][i] = bf16_round(v[j][i] * p.prescale);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) ss = fmaf(v[j][i], v[j][i], ss);
+    }
+    ss = wave_sum(ss);
+    const float rs = rsqrtf(ss / (float)p.D + p.eps);
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int d = 4 * lane + 256 * j;
+        const float4 w = *reinterpret_cast<const float4*>(p.weight + d);
+        float y[4] = {v[j][0] * rs * w.x, v[j][1] * rs * w.y, v[j][2] * rs * w.z, v[j][3] * rs * w.w};
+        if (p.gate) {
+            const bf16x4 g = *reinterpret_cast<const bf16x4*>(p.gate + base + d);
+#pragma unroll
+            for (int i = 0; i < 4; i++) y[i] *= sigmoidf((float)g[i]);
+        }
+        *reinterpret_cast<bf16x4*>(p.out + base + d) = bf16x4{(bf16_t)y[0], (bf16_t)y[1], (bf16_t)y[2], (bf16_t)y[3]};
+    }
+}
+
+// Causal depthwise convolution over time (layers/cyfa.py:138-233):
+//   y[b, t, c] = bias[c] + sum_{w < W} weight[c, w] * X[b, t + w - (W - 1), c]
+// where X[b, i] is x[b, i] for i >= 0, cache[b, W - 1 + i] for i < 0 when a
+// cache is given, else 0. Thread = 8 channels x a run of CONV_RUN tokens,
+// sliding the W-row window through registers; channel c goes to output
+// c / split, column c % split.
+constexpr int CONV_RUN = 32;
+
+template <int W>
+__global__ __launch_bounds__(256) void short_conv_kernel(ConvParams p) {
+    const int c8 = (blockIdx.x * 256 + threadIdx.x) * 8;
+    if (c8 >= p.D) return;
+    const int b = blockIdx.y, t0 = blockIdx.z * CONV_RUN;
+    float wt[W][8], bias[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+#pragma unroll
+        for (int w = 0; w < W; w++) wt[w][i] = (float)p.weight[(size_t)(c8 + i) * W + w];
+        bias[i] = p.bias ? (float)p.bias[c8 + i] : 0.f;
+    }
+    auto row = [&](int i) -> bf16x8 {
+        if (i >= 0) return *reinterpret_cast<const bf16x8*>(p.x + ((size_t)b * p.T + i) * p.x_row + c8);
+        if (p.cache)
+            return *reinterpret_cast<const bf16x8*>(p.cache + (size_t)b * p.cache_batch + (size_t)(W - 1 + i) * p.cache_row + c8);
+        bf16x8 z;
+#pragma unroll
+        for (int k = 0; k < 8; k++) z[k] = (bf16_t)0.f;
+        return z;
+    };
+    float win[W][8];
+#pragma unroll
+    for (int w = 0; w < W - 1; w++) {
+        const bf16x8 r = row(t0 + w - (W - 1));
+#pragma unroll
+        for (int i = 0; i < 8; i++) win[w][i] = (float)r[i];
+    }
+    const int out_i = c8 / p.split, col = c8 % p.split;
+    bf16_t* out = p.out[out_i];
+    const int t1 = t0 + CONV_RUN < p.T ? t0 + CONV_RUN : p.T;
+    for (int t = t0; t < t1; t++) {
+        const bf16x8 r = row(t);
+#pragma unroll
+        for (int i = 0; i < 8; i++) win[W - 1][i] = (float)r[i];
+        bf16x8 y;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float acc = win[0][i] * wt[0][i];
+#pragma unroll
+            for (int w = 1; w < W; w++) acc = fmaf(win[w][i], wt[w][i], acc);
+            y[i] = (bf16_t)(acc + bias[i]);
+        }
+        *reinterpret_cast<bf16x8*>(out + ((size_t)b * p.T + t) * p.split + col) = y;
+#pragma unroll
+        for (int w = 0; w < W - 1; w++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) win[w][i] = win[w + 1][i];
+    }
+}
+
+// SwiGLU product (modeling_cyfa.py:22-27): out = bf16(g sigmoid(g) u) for
+// gu = [g | u] rows of 2F bf16.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const bf16_t* gu, bf16_t* out, int rows, int F) {
+    const size_t i8 = ((size_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (i8 >= (size_t)rows * F) return;
+    const size_t r = i8 / F, c = i8 % F;
+    const bf16x8 g = *reinterpret_cast<const bf16x8*>(gu + r * 2 * F + c);
+    const bf16x8 u = *reinterpret_cast<const bf16x8*>(gu + r * 2 * F + F + c);
+    bf16x8 y;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float gf = (float)g[i];
+        y[i] = (bf16_t)(gf * sigmoidf(gf) * (float)u[i]);
+    }
+    *reinterpret_cast<bf16x8*>(out + i8) = y;
+}
+
+// Gate activations (layers/cyfa.py:323-326) from abd = [a | b | d] rows of 3H
+// bf16 (the b / d biases already added): g = -exp(A_log) softplus(a + dt_bias),
+// beta = sigmoid(b), delta = sigmoid(d), all fp32 [rows, H].
+__global__ __launch_bounds__(256) void gates_kernel(const bf16_t* abd, const float* dt_bias, const float* A_log, float* g,
+                                                    float* beta, float* delta, int rows, int H) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * H) return;
+    const int r = i / H, h = i % H;
+    const float a = (float)abd[(size_t)r * 3 * H + h] + dt_bias[h];
+    const float sp = a > 20.f ? a : log1pf(expf(a));
+    g[i] = -expf(A_log[h]) * sp;
+    beta[i] = sigmoidf((float)abd[(size_t)r * 3 * H + H + h]);
+    delta[i] = sigmoidf((float)abd[(size_t)r * 3 * H + 2 * H + h]);
+}
+
+}  // namespace
+
+int launch_rms_norm(const NormParams& p, hipStream_t stream) {
+    const dim3 grid((p.rows + 3) / 4), block(256);
+    switch (p.D / 256) {
+        case 1: hipLaunchKernelGGL(rms_norm_kernel<1>, grid, block, 0, stream, p); break;
+        case 2: hipLaunchKernelGGL(rms_norm_kernel<2>, grid, block, 0, stream, p); break;
+        case 4: hipLaunchKernelGGL(rms_norm_kernel<4>, grid, block, 0, stream, p); break;
+        case 8: hipLaunchKernelGGL(rms_norm_kernel<8>, grid, block, 0, stream, p); break;
+        default: return -1;
+    }
+    return 0;
+}
+
+int launch_short_conv(const ConvParams& p, hipStream_t stream) {
+    const dim3 grid((p.D / 8 + 255) / 256, p.B, (p.T + CONV_RUN - 1) / CONV_RUN), block(256);
+    switch (p.W) {
+        case 2: hipLaunchKernelGGL(short_conv_kernel<2>, grid, block, 0, stream, p); break;
+        case 3: hipLaunchKernelGGL(short_conv_kernel<3>, grid, block, 0, stream, p); break;
+        case 4: hipLaunchKernelGGL(short_conv_kernel<4>, grid, block, 0, stream, p); break;
+        default: return -1;
+    }
+    return 0;
+}
+
+int launch_silu_mul(const bf16_t* gu, bf16_t* out, int rows, int F, hipStream_t stream) {
+    const size_t n8 = (size_t)rows * F / 8;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, stream, gu, out, rows, F);
+    return 0;
+}
+
+int launch_gates(const bf16_t* abd, const float* dt_bias, const float* A_log, float* g, float* beta, float* delta,
+                 int rows, int H, hipStream_t stream) {
+    hipLaunchKernelGGL(gates_kernel, dim3((rows * H + 255) / 256), dim3(256), 0, stream, abd, dt_bias, A_log, g, beta,
+                       delta, rows, H);
+    return 0;
+}
+
+}  // namespace cyfa

@@ -50,12 +50,37 @@ class CyfaDecodeArgs(ctypes.Structure):
     ]
 
 
+class CyfaNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("rows", _c_int), ("D", _c_int),
+        ("x", _c_void_p), ("residual", _c_void_p), ("sum_out", _c_void_p),
+        ("weight", _c_void_p), ("gate", _c_void_p),
+        ("eps", _c_float), ("prescale", _c_float),
+        ("out", _c_void_p),
+    ]
+
+
+class CyfaConvArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", _c_int), ("T", _c_int), ("D", _c_int), ("W", _c_int),
+        ("x", _c_void_p), ("x_row", ctypes.c_longlong),
+        ("cache", _c_void_p), ("cache_row", ctypes.c_longlong), ("cache_batch", ctypes.c_longlong),
+        ("weight", _c_void_p), ("bias", _c_void_p),
+        ("out", _c_void_p * 3), ("split", _c_int),
+    ]
+
+
 # Every symbol include/cyfa_abi.h declares, with its ctypes signature.
 SIGNATURES = {
     "cyfa_chunk_fwd": (_c_int, [ctypes.POINTER(CyfaChunkArgs), _c_void_p]),
     "cyfa_chunk_workspace_bytes": (_c_size_t, [_c_int] * 7),
     "cyfa_decode_step": (_c_int, [ctypes.POINTER(CyfaDecodeArgs), _c_void_p]),
     "cyfa_readout_table": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "cyfa_rms_norm": (_c_int, [ctypes.POINTER(CyfaNormArgs), _c_void_p]),
+    "cyfa_short_conv": (_c_int, [ctypes.POINTER(CyfaConvArgs), _c_void_p]),
+    "cyfa_silu_mul": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "cyfa_gates": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int,
+                            _c_void_p]),
     "cyfa_last_error": (ctypes.c_char_p, []),
     "cyfa_abi_version": (_c_int, []),
 }
@@ -191,3 +216,79 @@ def readout_table(readout: torch.Tensor) -> torch.Tensor:
     if rc != CYFA_OK:
         _raise(rc, "cyfa_readout_table failed")
     return table
+
+
+def _check(rc, what):
+    if rc != CYFA_OK:
+        _raise(rc, what + " failed")
+
+
+def rms_norm(x, weight, eps, gate=None, residual=None, prescale=1.0):
+    """Fused (residual add +) RMSNorm (+ sigmoid gate) over the last dim of bf16 x.
+
+    Returns out, or (sum, out) when residual is given (sum = bf16(x + residual))."""
+    dev = require_device(x, weight, gate, residual)
+    D = x.shape[-1]
+    x = x.contiguous()
+    w = weight.detach().to(torch.float32).contiguous()
+    out = torch.empty_like(x)
+    total = None
+    if residual is not None:
+        residual = residual.contiguous()
+        total = torch.empty_like(x)
+    if gate is not None:
+        gate = gate.contiguous()
+    args = CyfaNormArgs(rows=x.numel() // D, D=D, x=ptr(x), residual=ptr(residual), sum_out=ptr(total),
+                        weight=ptr(w), gate=ptr(gate), eps=float(eps), prescale=float(prescale), out=ptr(out))
+    _check(load_library().cyfa_rms_norm(ctypes.byref(args), stream_handle(dev)), "cyfa_rms_norm")
+    return out if residual is None else (total, out)
+
+
+def short_conv(x, weight, bias=None, cache=None, split=None):
+    """Causal depthwise convolution over time of x [B, T, D] (rows may be strided).
+
+    weight [D, W] bf16, cache an optional [B, W-1, D] view. The D channels are
+    written to D // split contiguous [B, T, split] tensors (split defaults to D)."""
+    dev = require_device(x, weight, bias, cache)
+    B, T, D = x.shape
+    W = weight.shape[-1]
+    split = D if split is None else split
+    if x.stride(-1) != 1 or x.stride(0) != T * x.stride(1):
+        x = x.contiguous()
+    outs = [torch.empty(B, T, split, dtype=x.dtype, device=dev) for _ in range(D // split)]
+    w = weight.reshape(D, W).contiguous()
+    if cache is not None and cache.stride(-1) != 1:
+        cache = cache.contiguous()
+    args = CyfaConvArgs(B=B, T=T, D=D, W=W, x=ptr(x), x_row=x.stride(1),
+                        cache=ptr(cache), cache_row=0 if cache is None else cache.stride(1),
+                        cache_batch=0 if cache is None else cache.stride(0),
+                        weight=ptr(w), bias=ptr(None if bias is None else bias.contiguous()), split=split)
+    for i, o in enumerate(outs):
+        args.out[i] = o.data_ptr()
+    _check(load_library().cyfa_short_conv(ctypes.byref(args), stream_handle(dev)), "cyfa_short_conv")
+    return outs
+
+
+def silu_mul(gu):
+    """bf16(g * sigmoid(g) * u) for gu = [..., 2F] holding [g | u]."""
+    dev = require_device(gu)
+    gu = gu.contiguous()
+    F2 = gu.shape[-1]
+    out = torch.empty(*gu.shape[:-1], F2 // 2, dtype=gu.dtype, device=dev)
+    _check(load_library().cyfa_silu_mul(ptr(gu), ptr(out), gu.numel() // F2, F2 // 2, stream_handle(dev)),
+           "cyfa_silu_mul")
+    return out
+
+
+def gates(abd, dt_bias, A_log):
+    """(g, beta, delta) fp32 [..., H] from the fused a|b|d projection [..., 3H]."""
+    dev = require_device(abd, dt_bias, A_log)
+    abd = abd.contiguous()
+    H = abd.shape[-1] // 3
+    shape = tuple(abd.shape[:-1]) + (H,)
+    g, beta, delta = (torch.empty(shape, dtype=torch.float32, device=dev) for _ in range(3))
+    db = dt_bias.detach().to(torch.float32).contiguous()
+    al = A_log.detach().to(torch.float32).contiguous()
+    _check(load_library().cyfa_gates(ptr(abd), ptr(db), ptr(al), ptr(g), ptr(beta), ptr(delta),
+                                      abd.numel() // (3 * H), H, stream_handle(dev)), "cyfa_gates")
+    return g, beta, delta

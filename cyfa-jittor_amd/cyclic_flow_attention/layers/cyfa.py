@@ -7,6 +7,12 @@ arguments, parameter names (torch-checkpoint compatible), the
 Projections run as torch (hipBLASLt) GEMMs in bf16 with fp32 accumulation;
 the attention itself is ``ops.chunk_cyfa`` (prefill) or
 ``ops.fused_recurrent_cyfa`` (one-token decode), both HIP kernels.
+
+Like the reference, which switches to its inference kernels for bf16 CUDA
+tensors without gradients (layers/cyfa.py:66-73, 148-155), bf16 GPU inference
+takes a fused path: one q|k|v projection and one short-convolution launch
+for the three tensors, one a|b|d projection with a fused gate kernel, and the
+gated o_norm as one HIP kernel. Other inputs take the general torch path.
 """
 
 import math
@@ -15,8 +21,29 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from .. import _native
 from ..ops import chunk_cyfa, fused_recurrent_cyfa
 from ..ops.utils import readout_table
+
+
+def inference_fast_path(x):
+    """bf16 GPU inference without gradients (the reference's `_inference` condition)."""
+    return x.is_cuda and x.dtype == torch.bfloat16 and not torch.is_grad_enabled()
+
+
+class FusedWeight:
+    """Concatenation of parameters along dim 0, rebuilt when any of them changes."""
+
+    def __init__(self):
+        self.key = None
+        self.value = None
+
+    def get(self, *tensors):
+        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in tensors)
+        if key != self.key:
+            self.value = torch.cat([t.detach() for t in tensors], dim=0)
+            self.key = key
+        return self.value
 
 
 class RMSNorm(nn.Module):
@@ -27,12 +54,27 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(dim))
         self.eps = eps
 
-    def forward(self, x, gate=None):
+    def forward(self, x, gate=None, *, prescale=1.0, residual=None):
+        """norm(x) [* sigmoid(gate)]. Keyword extensions used by the fused
+        inference path: ``prescale`` normalises bf16(x * prescale) (the layer's
+        o * (num_slots - 1)); ``residual`` first forms s = x + residual and
+        returns (s, norm(s))."""
+        D = x.shape[-1]
+        if (inference_fast_path(x) and D % 256 == 0 and D // 256 in (1, 2, 4, 8)
+                and (gate is None or gate.dtype == torch.bfloat16)
+                and (residual is None or residual.dtype == torch.bfloat16)):
+            return _native.rms_norm(x, self.weight, self.eps, gate, residual, prescale)
+        total = None
+        if residual is not None:
+            x = total = x + residual
+        if prescale != 1.0:
+            x = x * prescale
         xf = x.float()
         y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps) * self.weight.float()
         if gate is not None:
             y = y * torch.sigmoid(gate.float())
-        return y.to(x.dtype)
+        y = y.to(x.dtype)
+        return y if residual is None else (total, y)
 
     execute = forward
 
@@ -54,6 +96,11 @@ class ShortConvolution(nn.Module):
     def forward(self, x, cache=None, lengths=None):
         B, T, D = x.shape
         W = self.width
+        if inference_fast_path(x) and lengths is None and 2 <= W <= 4 and D % 8 == 0:
+            y = _native.short_conv(x, self.weight.reshape(D, W).to(x.dtype),
+                                   None if self.bias is None else self.bias.to(x.dtype),
+                                   None if cache is None else cache.to(x.dtype))[0]
+            return y, conv_cache_tail(x, cache, W)
         history = x if cache is None else torch.cat([cache.to(x.dtype), x], dim=1)
         offset = W - 1 if cache is None else 0
         padded = F.pad(history, (0, 0, offset, 0)) if offset else history
@@ -76,6 +123,16 @@ class ShortConvolution(nn.Module):
         return y.contiguous(), new_cache
 
     execute = forward
+
+
+def conv_cache_tail(x, cache, W):
+    """The last W - 1 rows of cat(cache, x) over time (layers/cyfa.py:172-174)."""
+    B, T, D = x.shape
+    if T >= W - 1:
+        return x[:, T - (W - 1):].contiguous()
+    if cache is None:  # positions before the start read as zeros (layers/cyfa.py:175-182)
+        cache = torch.zeros(B, W - 1, D, dtype=x.dtype, device=x.device)
+    return torch.cat([cache.to(x.dtype)[:, T:], x], dim=1)
 
 
 class CyclicFlowAttention(nn.Module):
@@ -133,6 +190,10 @@ class CyclicFlowAttention(nn.Module):
         self.o_proj = nn.Linear(self.value_dim, hidden_size, bias=False)
         self._table_key = None
         self._table = None
+        self._qkv_weight = FusedWeight()
+        self._conv_weight = FusedWeight()
+        self._abd_weight = FusedWeight()
+        self._abd_bias = FusedWeight()
 
     def readout_table(self):
         """readout @ Phi, cached while the readout parameter is unchanged."""
@@ -143,6 +204,9 @@ class CyclicFlowAttention(nn.Module):
         return self._table
 
     def forward(self, x, cache=None, use_cache=False, attention_mask=None):
+        if (inference_fast_path(x) and attention_mask is None and self.use_short_conv
+                and 2 <= self.q_conv1d.width <= 4 and self.q_conv1d.bias is None):
+            return self._forward_fused(x, cache, use_cache)
         B, T, _ = x.shape
         H = self.num_heads
         q, k, v = self.q_proj(x), self.k_proj(x), self.v_proj(x)
@@ -187,9 +251,54 @@ class CyclicFlowAttention(nn.Module):
         if not self.training and T == 1 and not torch.is_grad_enabled():
             o, state = fused_recurrent_cyfa(**kwargs, table=self.readout_table())
         else:
-            o, state = chunk_cyfa(**kwargs, chunk_size=self.chunk_size)
+            o, state = chunk_cyfa(**kwargs, chunk_size=self.chunk_size,
+                                  table=None if torch.is_grad_enabled() else self.readout_table())
         gate = self.g_proj(x).reshape(B, T, H, self.head_v_dim)
         o = self.o_norm(o * (self.num_slots - 1), gate).reshape(B, T, self.value_dim)
+        o = self.o_proj(o)
+        new_cache = {"recurrent_state": state, "conv_state": (cq, ck, cv)} if use_cache else None
+        return o, new_cache
+
+    def _forward_fused(self, x, cache, use_cache):
+        """bf16 inference: the same math as forward with fused launches."""
+        B, T, _ = x.shape
+        H, Dk, Dv = self.num_heads, self.key_dim, self.value_dim
+        W = self.q_conv1d.width
+        qkv = F.linear(x, self._qkv_weight.get(self.q_proj.weight, self.k_proj.weight, self.v_proj.weight))
+        conv_cache = None if cache is None else cache.get("conv_state")
+        cat_cache = None if conv_cache is None else torch.cat([c.to(x.dtype) for c in conv_cache], dim=-1)
+        wconv = self._conv_weight.get(self.q_conv1d.weight, self.k_conv1d.weight, self.v_conv1d.weight)
+        if Dk == Dv:
+            q, k, v = _native.short_conv(qkv, wconv.reshape(-1, W).to(x.dtype), None, cat_cache, split=Dk)
+        else:
+            (y,) = _native.short_conv(qkv, wconv.reshape(-1, W).to(x.dtype), None, cat_cache)
+            q, k, v = y[..., :Dk].contiguous(), y[..., Dk:2 * Dk].contiguous(), y[..., 2 * Dk:].contiguous()
+        tail = conv_cache_tail(qkv, cat_cache, W)
+        cq, ck, cv = tail[..., :Dk].contiguous(), tail[..., Dk:2 * Dk].contiguous(), tail[..., 2 * Dk:].contiguous()
+        abd = F.linear(x, self._abd_weight.get(self.a_proj.weight, self.b_proj.weight, self.d_proj.weight),
+                       self._abd_bias.get(torch.zeros_like(self.b_proj.bias), self.b_proj.bias, self.d_proj.bias))
+        g, beta, delta = _native.gates(abd, self.dt_bias, self.A_log)
+        kwargs = dict(
+            q=q.view(B, T, H, self.head_k_dim),
+            k=k.view(B, T, H, self.head_k_dim),
+            v=v.view(B, T, H, self.head_v_dim),
+            g=g,
+            delta=delta,
+            beta=beta,
+            readout=self.readout,
+            q_norm_weight=self.q_norm.weight.float(),
+            k_norm_weight=self.k_norm.weight.float(),
+            q_norm_eps=self.q_norm.eps,
+            k_norm_eps=self.k_norm.eps,
+            initial_state=None if cache is None else cache["recurrent_state"],
+            output_final_state=use_cache,
+        )
+        if not self.training and T == 1:
+            o, state = fused_recurrent_cyfa(**kwargs, table=self.readout_table())
+        else:
+            o, state = chunk_cyfa(**kwargs, chunk_size=self.chunk_size, table=self.readout_table())
+        gate = self.g_proj(x).view(B, T, H, self.head_v_dim)
+        o = self.o_norm(o, gate, prescale=float(self.num_slots - 1)).view(B, T, Dv)
         o = self.o_proj(o)
         new_cache = {"recurrent_state": state, "conv_state": (cq, ck, cv)} if use_cache else None
         return o, new_cache

@@ -11,7 +11,8 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from ...layers.cyfa import CyclicFlowAttention, RMSNorm
+from ... import _native
+from ...layers.cyfa import CyclicFlowAttention, FusedWeight, RMSNorm, inference_fast_path
 
 
 def mlp_width(config):
@@ -25,8 +26,13 @@ class GatedMLP(nn.Module):
         self.gate_proj = nn.Linear(config.hidden_size, mid, bias=False)
         self.up_proj = nn.Linear(config.hidden_size, mid, bias=False)
         self.down_proj = nn.Linear(mid, config.hidden_size, bias=False)
+        self._gate_up = FusedWeight()
 
     def forward(self, x):
+        if inference_fast_path(x) and self.gate_proj.weight.shape[0] % 8 == 0:
+            # one [gate | up] GEMM and the fused SwiGLU kernel
+            gu = F.linear(x, self._gate_up.get(self.gate_proj.weight, self.up_proj.weight))
+            return self.down_proj(_native.silu_mul(gu))
         g = self.gate_proj(x)
         u = self.up_proj(x)
         return self.down_proj((F.silu(g.float()) * u.float()).to(x.dtype))
@@ -68,10 +74,26 @@ class CyclicFlowAttentionModel(nn.Module):
     def forward(self, input_ids, cache=None, use_cache=False, attention_mask=None):
         x = self.embeddings(input_ids)
         new = []
+        if not inference_fast_path(x):
+            for i, layer in enumerate(self.layers):
+                x, s = layer(x, None if cache is None else cache[i], use_cache, attention_mask)
+                new.append(s)
+            return self.norm(x), (new if use_cache else None)
+        # bf16 inference: each residual add runs inside the following norm
+        # kernel (x + y and residual + mlp, as CyFABlock.forward, bit for bit).
+        pending = None
         for i, layer in enumerate(self.layers):
-            x, s = layer(x, None if cache is None else cache[i], use_cache, attention_mask)
+            h = layer.attn_norm(x) if pending is None else None
+            if pending is not None:
+                x, h = layer.attn_norm(pending, residual=x)
+            y, s = layer.attn(h, None if cache is None else cache[i], use_cache, attention_mask)
+            x, m = layer.mlp_norm(y, residual=x)
+            pending = layer.mlp(m)
             new.append(s)
-        return self.norm(x), (new if use_cache else None)
+        if pending is None:
+            return self.norm(x), (new if use_cache else None)
+        _, out = self.norm(pending, residual=x)
+        return out, (new if use_cache else None)
 
 
 # Parameters that stay fp32 under to_bfloat16 (modeling_cyfa.py:110-116).

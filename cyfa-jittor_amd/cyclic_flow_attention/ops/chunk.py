@@ -32,6 +32,8 @@ def chunk_cyfa(
     cu_seqlens=None,
     checkpoint_level=0,
     chunk_size=64,
+    *,
+    table=None,
 ):
     """Chunkwise Cyclic Flow Attention.
 
@@ -39,6 +41,8 @@ def chunk_cyfa(
     [batch, time, heads]. The readout has [heads, slots-1, slots-1]. Returns
     the output (bf16, [batch, time, heads, V]) and, when requested,
     (key_state [B,H,K,M], value_state [B,H,M,V], clock [B,H]), all fp32.
+    ``table`` (keyword only, not in the reference signature) is a precomputed
+    readout @ Phi [H, M-1, M] fp32; when None it is formed from ``readout``.
     """
     if cu_seqlens is not None:
         raise NotImplementedError("packed layout requires native segment dispatch")
@@ -62,7 +66,11 @@ def chunk_cyfa(
     g, delta, beta = (x.to(torch.float32).contiguous() for x in (g, delta, beta))
     qw = q_norm_weight.to(torch.float32).contiguous()
     kw = k_norm_weight.to(torch.float32).contiguous()
-    table = readout_table(readout)
+    if table is None:
+        table = readout_table(readout)
+    elif tuple(table.shape) != (H, M - 1, M) or table.dtype != torch.float32:
+        raise ValueError(f"table must be float32 [{H}, {M - 1}, {M}], got {tuple(table.shape)} {table.dtype}")
+    table = table.contiguous()
     if initial_state is not None:
         h0k, h0v, c0 = (x.to(torch.float32).contiguous() for x in initial_state)
         if tuple(h0k.shape) != (B, H, K, M) or tuple(h0v.shape) != (B, H, M, V) or tuple(c0.shape) != (B, H):

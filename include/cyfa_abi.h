@@ -100,6 +100,62 @@ int cyfa_decode_step(const CyfaDecodeArgs *args, void *hip_stream);
  * ops/fused_recurrent.py:53). readout f32 [H, M-1, M-1]; table f32 [H, M-1, M]. */
 int cyfa_readout_table(const float *readout, float *table, int H, int M, void *hip_stream);
 
+/* ---- Layer-side kernels around the op (layers/cyfa.py, modeling_cyfa.py) ---- */
+
+/* Arguments of one RMSNorm over rows of D bf16 values (D a multiple of 256, at
+ * most 2048). The residual add of the surrounding block is fused in front:
+ *   s   = residual ? bf16(x + residual) : x           (written to sum_out)
+ *   xs  = prescale != 1 ? bf16(s * prescale) : s
+ *   out = bf16(xs * rsqrt(mean(xs^2) + eps) * weight * (gate ? sigmoid(gate) : 1)) */
+typedef struct CyfaNormArgs {
+    int rows, D;
+    const void *x;                /* bf16 [rows, D] */
+    const void *residual;         /* nullable bf16 [rows, D] */
+    void *sum_out;                /* bf16 [rows, D]; required when residual is set */
+    const float *weight;          /* f32 [D] */
+    const void *gate;             /* nullable bf16 [rows, D] */
+    float eps, prescale;
+    void *out;                    /* bf16 [rows, D] */
+} CyfaNormArgs;
+
+/* Replaces RMSNorm.execute / RMSNorm._inference (layers/cyfa.py:62-135; the
+ * gated form is the o_norm(o * (num_slots - 1), gate) of layers/cyfa.py:351)
+ * and the residual adds of CyFABlock.execute (modeling_cyfa.py:48-51). */
+int cyfa_rms_norm(const CyfaNormArgs *args, void *hip_stream);
+
+/* Arguments of one causal depthwise convolution over time of B x T rows of D
+ * bf16 channels (D a multiple of 8, W in 2..4):
+ *   y[b,t,c] = bias[c] + sum_{w<W} weight[c,w] * X[b, t + w - (W-1), c],
+ * X[b,i] = x[b,i] for i >= 0, else cache[b, W-1+i] (or 0 without a cache).
+ * Channel c is written to out[c / split] at column c % split, so one launch
+ * can convolve a fused q|k|v projection into three tensors. */
+typedef struct CyfaConvArgs {
+    int B, T, D, W;
+    const void *x;                /* bf16, element (b,t,c) at x[(b*T + t)*x_row + c] */
+    long long x_row;
+    const void *cache;            /* nullable bf16, (b,i,c) at cache[b*cache_batch + i*cache_row + c] */
+    long long cache_row, cache_batch;
+    const void *weight;           /* bf16 [D, W] */
+    const void *bias;             /* nullable bf16 [D] */
+    void *out[3];                 /* bf16 [B, T, split] each; D / split of them used */
+    int split;
+} CyfaConvArgs;
+
+/* Replaces ShortConvolution.execute / _inference (layers/cyfa.py:138-233); the
+ * new cache (the last W-1 inputs) stays a view of the input in the caller. */
+int cyfa_short_conv(const CyfaConvArgs *args, void *hip_stream);
+
+/* out[r, c] = bf16(g sigmoid(g) u), g = gu[r, c], u = gu[r, F + c]; F a
+ * multiple of 8. Replaces the activation of GatedMLP.execute
+ * (modeling_cyfa.py:22-27). */
+int cyfa_silu_mul(const void *gu, void *out, int rows, int F, void *hip_stream);
+
+/* Gate activations from the fused a|b|d projection abd [rows, 3H] bf16 (b and
+ * d biases included): g = -exp(A_log) softplus(a + dt_bias), beta =
+ * sigmoid(b), delta = sigmoid(d), f32 [rows, H]. Replaces layers/cyfa.py:323-326. */
+int cyfa_gates(const void *abd, const float *dt_bias, const float *A_log, float *g, float *beta, float *delta,
+               int rows, int H, void *hip_stream);
+
 /* Thread-local message of the last failing call (never NULL). No reference
  * counterpart: Jittor reports kernel errors as C++ exceptions. */
 const char *cyfa_last_error(void);

@@ -7,7 +7,11 @@ so that the product model and the oracle consume identical weights.
 ``mode="exact"`` computes in float64 with no bfloat16 casts; ``mode="mirror"``
 computes in float32 and casts to bfloat16 wherever the reference's bf16
 inference path does (``.cast(x.dtype)`` points of layers/cyfa.py and
-modeling_cyfa.py).
+modeling_cyfa.py). ``op_mode`` (default: ``mode``) sets the mode of the
+attention op alone: ``mode="mirror", op_mode="exact"`` is the reference's bf16
+layer plumbing around an exact (float64) CyFA op, the fp32-or-better
+reference a bf16 layer is compared with (a float64 plumbing would round the
+clock increments differently from any bf16 layer and let the clock drift).
 """
 
 import math
@@ -80,11 +84,12 @@ def short_conv(x, weight, bias=None, cache=None, lengths=None, mode="exact"):
 
 
 def attention_layer(p, pre, x, cfg, cache=None, use_cache=False, attention_mask=None, mode="exact",
-                    chunk_size=64):
+                    chunk_size=64, op_mode=None, cast_output=True):
     """CyclicFlowAttention.execute (layers/cyfa.py:299-357).
 
     p: state dict; pre: name prefix such as "model.layers.0.attn.";
     cfg: dict with hidden_size, num_heads, head_dim, num_slots, norm_eps.
+    cast_output=False leaves the layer output (o_proj) in the working precision.
     """
     dt = _dt(mode)
     B, T, _ = x.shape
@@ -127,7 +132,7 @@ def attention_layer(p, pre, x, cfg, cache=None, use_cache=False, attention_mask=
         q_norm_eps=eps, k_norm_eps=eps,
         initial_state=None if cache is None else cache["recurrent_state"],
         output_final_state=use_cache,
-        mode=mode,
+        mode=op_mode or mode,
     )
     if T == 1 and cache is not None:
         o, state = ops.fused_recurrent_cyfa(**kwargs)
@@ -137,7 +142,7 @@ def attention_layer(p, pre, x, cfg, cache=None, use_cache=False, attention_mask=
                   p[pre + "g_proj.1.bias"], mode).reshape(B, T, H, Dv)
     scaled = _cast(o.to(dt) * (cfg["num_slots"] - 1), mode)
     o = rms_norm(scaled, p[pre + "o_norm.weight"], eps, gate, mode).reshape(B, T, H * Dv)
-    y = linear(o, p[pre + "o_proj.weight"], mode=mode)
+    y = linear(o, p[pre + "o_proj.weight"], mode=mode if cast_output else "exact")
     new_cache = {"recurrent_state": state, "conv_state": (cq, ck, cv)} if use_cache else None
     return y, new_cache
 
@@ -158,7 +163,7 @@ def gated_mlp(p, pre, x, mode="exact"):
 
 
 def causal_lm(p, cfg, input_ids, cache=None, use_cache=False, attention_mask=None, mode="exact",
-              chunk_size=64):
+              chunk_size=64, op_mode=None):
     """CyclicFlowAttentionForCausalLM.execute without the loss
     (models/cyfa/modeling_cyfa.py:49-108). Returns (logits, cache)."""
     dt = _dt(mode)
@@ -169,7 +174,7 @@ def causal_lm(p, cfg, input_ids, cache=None, use_cache=False, attention_mask=Non
         pre = f"model.layers.{i}."
         h = rms_norm(x, p[pre + "attn_norm.weight"], eps, mode=mode)
         y, c = attention_layer(p, pre + "attn.", h, cfg, None if cache is None else cache[i], use_cache,
-                               attention_mask, mode, chunk_size)
+                               attention_mask, mode, chunk_size, op_mode)
         r = _cast(x + y, mode)
         x = _cast(r + gated_mlp(p, pre + "mlp.", rms_norm(r, p[pre + "mlp_norm.weight"], eps, mode=mode), mode),
                   mode)

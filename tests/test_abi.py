@@ -44,7 +44,9 @@ def _c_layout(tmp_path, struct, fields):
 
 
 @pytest.mark.parametrize("cls,name", [(_native.CyfaChunkArgs, "CyfaChunkArgs"),
-                                      (_native.CyfaDecodeArgs, "CyfaDecodeArgs")])
+                                      (_native.CyfaDecodeArgs, "CyfaDecodeArgs"),
+                                      (_native.CyfaNormArgs, "CyfaNormArgs"),
+                                      (_native.CyfaConvArgs, "CyfaConvArgs")])
 def test_struct_layout_matches_header(tmp_path, cls, name):
     fields = [f for f, _ in cls._fields_]
     got = [ctypes.sizeof(cls)] + [getattr(cls, f).offset for f in fields]
@@ -91,3 +93,17 @@ def test_python_ops_reject_like_the_reference():
         fused_recurrent_cyfa(q1, q1, q1, g1.clone().requires_grad_(True), g1, g1, ro, w, w)
     with pytest.raises(ValueError):
         chunk_cyfa(q, q, q, g, g, g, ro, w, w)  # CPU tensors: the HIP path has no CPU fallback
+
+
+def test_layer_entry_points_validate_before_launch():
+    lib = _native.load_library()
+    n = _native.CyfaNormArgs(rows=4, D=384)
+    assert lib.cyfa_rms_norm(ctypes.byref(n), None) == _native.CYFA_ERR_UNSUPPORTED
+    n.D = 256
+    assert lib.cyfa_rms_norm(ctypes.byref(n), None) == _native.CYFA_ERR_VALUE  # null pointers
+    c = _native.CyfaConvArgs(B=1, T=4, D=64, W=5, split=64)
+    assert lib.cyfa_short_conv(ctypes.byref(c), None) == _native.CYFA_ERR_UNSUPPORTED
+    c.W, c.split = 4, 12
+    assert lib.cyfa_short_conv(ctypes.byref(c), None) == _native.CYFA_ERR_UNSUPPORTED
+    assert lib.cyfa_silu_mul(None, None, 1, 8, None) == _native.CYFA_ERR_VALUE
+    assert lib.cyfa_gates(None, None, None, None, None, None, 1, 4, None) == _native.CYFA_ERR_VALUE

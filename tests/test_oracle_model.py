@@ -1,0 +1,123 @@
+"""Pins of the oracle's layer / block / model plumbing (oracle/model_oracle.py).
+
+Each piece is checked against a library routine that computes the same
+textbook operation by another route (torch.nn.functional), or against an
+invariant the reference relies on: prefix + continuation equals the full
+sequence (tests/test_inference.py:20-34 of the reference), and right padding
+is neutral (tests/test_inference.py:56-65).
+"""
+
+import torch
+import torch.nn.functional as F
+
+from oracle import model_oracle as MO
+
+D64 = torch.float64
+
+
+def _layer_params(hidden=64, H=1, Dh=32, seed=0):
+    """A small random state dict with the reference's parameter names."""
+    gen = torch.Generator().manual_seed(seed)
+    r = lambda *s, std=0.1: std * torch.randn(*s, dtype=D64, generator=gen)
+    pre = "attn."
+    p = {
+        pre + "q_proj.weight": r(H * Dh, hidden), pre + "k_proj.weight": r(H * Dh, hidden),
+        pre + "v_proj.weight": r(H * Dh, hidden), pre + "a_proj.weight": r(H, hidden),
+        pre + "b_proj.weight": r(H, hidden), pre + "b_proj.bias": r(H),
+        pre + "d_proj.weight": r(H, hidden), pre + "d_proj.bias": r(H),
+        pre + "dt_bias": r(H), pre + "A_log": r(H).abs().log(),
+        pre + "readout": torch.eye(127, dtype=D64).expand(H, 127, 127) + r(H, 127, 127, std=0.05),
+        pre + "q_norm.weight": 1 + r(Dh), pre + "k_norm.weight": 1 + r(Dh),
+        pre + "q_conv1d.weight": r(H * Dh, 1, 4, std=0.5), pre + "k_conv1d.weight": r(H * Dh, 1, 4, std=0.5),
+        pre + "v_conv1d.weight": r(H * Dh, 1, 4, std=0.5),
+        pre + "g_proj.0.weight": r(Dh, hidden), pre + "g_proj.1.weight": r(H * Dh, Dh),
+        pre + "g_proj.1.bias": r(H * Dh), pre + "o_norm.weight": 1 + r(Dh),
+        pre + "o_proj.weight": r(hidden, H * Dh),
+    }
+    cfg = dict(hidden_size=hidden, num_heads=H, head_dim=Dh, num_slots=128, norm_eps=1e-6, use_short_conv=True)
+    return p, pre, cfg
+
+
+def test_linear_and_rms_norm_match_library_routines():
+    gen = torch.Generator().manual_seed(1)
+    x = torch.randn(3, 5, 16, dtype=D64, generator=gen)
+    w = torch.randn(8, 16, dtype=D64, generator=gen)
+    b = torch.randn(8, dtype=D64, generator=gen)
+    torch.testing.assert_close(MO.linear(x, w, b), F.linear(x, w, b))
+    nw = torch.rand(16, dtype=D64, generator=gen) + 0.5
+    gate = torch.randn(3, 5, 16, dtype=D64, generator=gen)
+    ref = F.rms_norm(x, (16,), nw, eps=1e-6) * torch.sigmoid(gate)
+    torch.testing.assert_close(MO.rms_norm(x, nw, 1e-6, gate), ref)
+
+
+def test_short_conv_matches_conv1d_and_continues_from_its_cache():
+    gen = torch.Generator().manual_seed(2)
+    B, T, D, W = 2, 11, 6, 4
+    x = torch.randn(B, T, D, dtype=D64, generator=gen)
+    w = torch.randn(D, 1, W, dtype=D64, generator=gen)
+    bias = torch.randn(D, dtype=D64, generator=gen)
+    y, cache = MO.short_conv(x, w, bias)
+    ref = F.conv1d(F.pad(x.transpose(1, 2), (W - 1, 0)), w, bias, groups=D).transpose(1, 2)
+    torch.testing.assert_close(y, ref)
+    torch.testing.assert_close(cache, x[:, -(W - 1):])
+    # split the sequence: the cache carries the history exactly
+    y1, c1 = MO.short_conv(x[:, :7], w, bias)
+    y2, c2 = MO.short_conv(x[:, 7:], w, bias, cache=c1)
+    torch.testing.assert_close(torch.cat([y1, y2], 1), y)
+    torch.testing.assert_close(c2, cache)
+    # a length-aware cache of right-padded rows equals the cache of the unpadded prefix
+    lengths = torch.tensor([T, 5])
+    _, cl = MO.short_conv(x, w, bias, lengths=lengths)
+    _, c5 = MO.short_conv(x[1:, :5], w, bias)
+    torch.testing.assert_close(cl[1:], c5)
+
+
+def test_attention_layer_prefix_then_decode_equals_full_sequence():
+    p, pre, cfg = _layer_params()
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(1, 70, cfg["hidden_size"], dtype=D64, generator=gen)
+    full, _ = MO.attention_layer(p, pre, x, cfg, use_cache=True)
+    y, cache = MO.attention_layer(p, pre, x[:, :64], cfg, use_cache=True)
+    outs = [y]
+    for t in range(64, 70):
+        y, cache = MO.attention_layer(p, pre, x[:, t:t + 1], cfg, cache=cache, use_cache=True)
+        outs.append(y)
+    torch.testing.assert_close(torch.cat(outs, 1), full, atol=1e-10, rtol=0)
+
+
+def test_attention_layer_right_padding_is_neutral():
+    p, pre, cfg = _layer_params(seed=4)
+    gen = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 40, cfg["hidden_size"], dtype=D64, generator=gen)
+    mask = torch.ones(2, 40, dtype=torch.long)
+    mask[1, 25:] = 0
+    y, cache = MO.attention_layer(p, pre, x, cfg, use_cache=True, attention_mask=mask)
+    y1, cache1 = MO.attention_layer(p, pre, x[1:, :25], cfg, use_cache=True)
+    torch.testing.assert_close(y[1:, :25], y1, atol=1e-10, rtol=0)
+    for a, b in zip(cache["recurrent_state"], cache1["recurrent_state"]):
+        torch.testing.assert_close(a[1:], b, atol=1e-10, rtol=0)
+    for a, b in zip(cache["conv_state"], cache1["conv_state"]):
+        torch.testing.assert_close(a[1:], b, atol=0, rtol=0)
+
+
+def test_causal_lm_prefix_then_decode_equals_full_forward():
+    p, pre, cfg = _layer_params(seed=6)
+    gen = torch.Generator().manual_seed(7)
+    V, hidden = 50, cfg["hidden_size"]
+    lm = {"model.layers.0." + k: v for k, v in p.items()}
+    lm["model.embeddings.weight"] = torch.randn(V, hidden, dtype=D64, generator=gen)
+    lm["model.layers.0.attn_norm.weight"] = 1 + 0.1 * torch.randn(hidden, dtype=D64, generator=gen)
+    lm["model.layers.0.mlp_norm.weight"] = 1 + 0.1 * torch.randn(hidden, dtype=D64, generator=gen)
+    for name, shape in (("gate_proj", (96, hidden)), ("up_proj", (96, hidden)), ("down_proj", (hidden, 96))):
+        lm[f"model.layers.0.mlp.{name}.weight"] = 0.1 * torch.randn(*shape, dtype=D64, generator=gen)
+    lm["model.norm.weight"] = torch.ones(hidden, dtype=D64)
+    lm["lm_head.weight"] = 0.1 * torch.randn(V, hidden, dtype=D64, generator=gen)
+    cfg = dict(cfg, num_hidden_layers=1, vocab_size=V, intermediate_size=96)
+    ids = torch.randint(0, V, (1, 68), generator=gen)
+    full, _ = MO.causal_lm(lm, cfg, ids)
+    logits, cache = MO.causal_lm(lm, cfg, ids[:, :64], use_cache=True)
+    outs = [logits]
+    for t in range(64, 68):
+        logits, cache = MO.causal_lm(lm, cfg, ids[:, t:t + 1], cache=cache, use_cache=True)
+        outs.append(logits)
+    torch.testing.assert_close(torch.cat(outs, 1), full, atol=1e-10, rtol=0)
