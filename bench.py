@@ -6,12 +6,15 @@ Workload (BASELINE.json metric; configs 3 and 4):
            use_cache=True (full logits, as the reference's model forward);
            one step = one prefill pass.  value = total prefill tokens / second.
   decode   B=64: a 2048-token prompt processed chunkwise (untimed), then
-           greedy decode steps with the fused constant-memory decode kernel;
-           argmax stays on the device. Reported under "decode".
+           greedy decode steps with the fused constant-memory decode kernel,
+           each step one replay of the HIP-graph captured 24-layer step
+           (argmax on the device). Reported under "decode".
 Weights are seeded N(0, 0.02) random init (no checkpoints offline).
 
-roofline: HIP events around every cyfa_chunk_fwd / cyfa_decode_step launch in
-the timed region give the average device duration per launch;
+roofline: HIP events around every cyfa_chunk_fwd launch in the timed prefill
+region give its average device duration; the decode kernel's duration comes
+from HIP events around replays of a graph of in-place decode launches at the
+decode shape (B=64, H=4), free of host launch gaps;
   prefill attention: 377 088 algorithmic FLOP per token*head / duration vs the
                      2.5 PFLOP/s dense bf16 MFMA peak;
   decode:            524 288 bytes of fp32 state per (batch, head) per layer
@@ -97,28 +100,69 @@ def time_prefill(model, ids, steps, warmup):
 
 
 def time_decode(model, prompt, steps, warmup):
+    """Greedy decode after a chunkwise prompt; one step = one replay of the
+    HIP-graph captured 24-layer decode step (argmax on the device)."""
     import torch
-
-    from cyclic_flow_attention import _native
 
     with torch.no_grad():
         hidden, cache = model.model(prompt, use_cache=True)
-        tok = model.lm_head(hidden[:, -1]).argmax(-1)
+        tok = model.lm_head(hidden[:, -1:]).argmax(-1)
         del hidden
+        dec = model.graphed_decoder(cache, tok)
+        del cache
         for _ in range(warmup):
-            out = model(tok[:, None], cache=cache, use_cache=True)
-            cache = out["cache"]
-            tok = out["logits"][:, -1].argmax(-1)
+            dec.step()
         torch.cuda.synchronize()
-        with _native.LaunchTimer() as timer:
-            start = time.perf_counter()
-            for _ in range(steps):
-                out = model(tok[:, None], cache=cache, use_cache=True)
-                cache = out["cache"]
-                tok = out["logits"][:, -1].argmax(-1)
-            torch.cuda.synchronize()
-            elapsed = time.perf_counter() - start
-    return elapsed, timer.results().get("cyfa_decode_step", [])
+        start = time.perf_counter()
+        for _ in range(steps):
+            dec.step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - start
+    return elapsed
+
+
+def decode_kernel_ms(batch, heads, reps=20, replays=5):
+    """Average device time of one fused decode launch at the decode shape.
+
+    `reps` in-place launches are captured in one HIP graph and the graph is
+    replayed between two HIP events on the launch stream, so host launch gaps
+    do not enter the figure."""
+    import torch
+
+    from cyclic_flow_attention.ops import fused_recurrent_cyfa
+    from cyclic_flow_attention.ops.utils import readout_table
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(5)
+    x = dict(q=torch.randn(batch, 1, heads, 256, generator=gen).bfloat16(),
+             k=torch.randn(batch, 1, heads, 256, generator=gen).bfloat16(),
+             v=torch.randn(batch, 1, heads, 256, generator=gen).bfloat16(),
+             g=torch.nn.functional.logsigmoid(torch.randn(batch, 1, heads, generator=gen) + 3),
+             delta=torch.sigmoid(torch.randn(batch, 1, heads, generator=gen)),
+             beta=torch.sigmoid(torch.randn(batch, 1, heads, generator=gen)),
+             readout=torch.eye(127).expand(heads, 127, 127).clone(),
+             q_norm_weight=torch.ones(256), k_norm_weight=torch.ones(256))
+    x = {k: v.to(dev) for k, v in x.items()}
+    table = readout_table(x["readout"])
+    state = (torch.randn(batch, heads, 256, 128, device=dev), torch.randn(batch, heads, 128, 256, device=dev),
+             torch.rand(batch, heads, device=dev))
+    with torch.no_grad():
+        fused_recurrent_cyfa(**x, initial_state=state, output_final_state=True, table=table, inplace=True)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fused_recurrent_cyfa(**x, initial_state=state, output_final_state=True, table=table, inplace=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(replays):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+    return start.elapsed_time(end) / (reps * replays)
 
 
 def cpu_baseline_prefill(model, config, seq_len):
@@ -251,9 +295,9 @@ def main():
         prompt = torch.randint(0, config.vocab_size, (args.decode_batch, args.seq_len), generator=gen).to(dev)
         log(f"decode B={args.decode_batch}: prompt {args.seq_len}, warmup {args.decode_warmup}, "
             f"timed {args.decode_steps}")
-        d_elapsed, dec_ms = time_decode(model, prompt, args.decode_steps, args.decode_warmup)
+        d_elapsed = time_decode(model, prompt, args.decode_steps, args.decode_warmup)
         d_value = args.decode_batch * args.decode_steps / d_elapsed
-        d_avg = statistics.fmean(dec_ms) if dec_ms else float("nan")
+        d_avg = decode_kernel_ms(args.decode_batch, H)
         d_bytes = STATE_BYTES_PER_BH * args.decode_batch * H
         d_gbs = d_bytes / (d_avg * 1e-3) / 1e9
         log(f"decode {d_value:,.0f} tok/s; decode kernel {d_avg * 1e3:.1f} us/launch = {d_gbs:,.0f} GB/s")

@@ -194,6 +194,10 @@ class CyclicFlowAttention(nn.Module):
         self._conv_weight = FusedWeight()
         self._abd_weight = FusedWeight()
         self._abd_bias = FusedWeight()
+        self._a_bias_zero = None  # a_proj has no bias: zeros in the fused a|b|d bias
+        # When set, one-token steps update the cache's recurrent states in place
+        # (the graphed decode loop); otherwise new state tensors are returned.
+        self.decode_in_place = False
 
     def readout_table(self):
         """readout @ Phi, cached while the readout parameter is unchanged."""
@@ -275,8 +279,11 @@ class CyclicFlowAttention(nn.Module):
             q, k, v = y[..., :Dk].contiguous(), y[..., Dk:2 * Dk].contiguous(), y[..., 2 * Dk:].contiguous()
         tail = conv_cache_tail(qkv, cat_cache, W)
         cq, ck, cv = tail[..., :Dk].contiguous(), tail[..., Dk:2 * Dk].contiguous(), tail[..., 2 * Dk:].contiguous()
+        if self._a_bias_zero is None or self._a_bias_zero.dtype != self.b_proj.bias.dtype \
+                or self._a_bias_zero.device != self.b_proj.bias.device:
+            self._a_bias_zero = torch.zeros_like(self.b_proj.bias.detach())
         abd = F.linear(x, self._abd_weight.get(self.a_proj.weight, self.b_proj.weight, self.d_proj.weight),
-                       self._abd_bias.get(torch.zeros_like(self.b_proj.bias), self.b_proj.bias, self.d_proj.bias))
+                       self._abd_bias.get(self._a_bias_zero, self.b_proj.bias, self.d_proj.bias))
         g, beta, delta = _native.gates(abd, self.dt_bias, self.A_log)
         kwargs = dict(
             q=q.view(B, T, H, self.head_k_dim),
@@ -294,7 +301,8 @@ class CyclicFlowAttention(nn.Module):
             output_final_state=use_cache,
         )
         if not self.training and T == 1:
-            o, state = fused_recurrent_cyfa(**kwargs, table=self.readout_table())
+            o, state = fused_recurrent_cyfa(**kwargs, table=self.readout_table(),
+                                            inplace=self.decode_in_place and cache is not None)
         else:
             o, state = chunk_cyfa(**kwargs, chunk_size=self.chunk_size, table=self.readout_table())
         gate = self.g_proj(x).view(B, T, H, self.head_v_dim)

@@ -130,6 +130,11 @@ class CyclicFlowAttentionForCausalLM(nn.Module):
         return self
 
     @torch.no_grad()
+    def graphed_decoder(self, cache, tokens):
+        """A GraphedDecodeStep continuing from a prefill cache and the last tokens [B, 1]."""
+        return GraphedDecodeStep(self, cache, tokens)
+
+    @torch.no_grad()
     def generate(self, input_ids, max_new_tokens=32, eos_token_id=None):
         """Greedy decoding with the constant-size state (modeling_cyfa.py:142-158).
 
@@ -147,3 +152,61 @@ class CyclicFlowAttentionForCausalLM(nn.Module):
             if eos_token_id is not None and bool((current == eos_token_id).all()):
                 break
         return torch.cat(tokens, dim=1)
+
+
+class GraphedDecodeStep:
+    """One greedy decode step of the whole model, captured once as a HIP graph.
+
+    The step reads the token buffer, runs every layer's one-token path (the
+    fused decode kernel updates each layer's recurrent state in place), writes
+    the conv histories back into the cache buffers, and stores the argmax token
+    in the token buffer for the next replay. ``step()`` replays it and returns
+    the token buffer [B, 1] (valid until the next replay). The reference runs
+    the same step as separate launches with a host sync per token
+    (generation.py:23-62).
+    """
+
+    def __init__(self, model, cache, tokens):
+        if not torch.cuda.is_available() or not tokens.is_cuda:
+            raise ValueError("graphed decoding needs the model and tokens on a GPU")
+        self.model = model
+        self.tokens = tokens.detach().clone()
+        self.cache = [
+            {"recurrent_state": tuple(t.clone() for t in c["recurrent_state"]),
+             "conv_state": tuple(t.clone() for t in c["conv_state"])}
+            for c in cache
+        ]
+        layers = [blk.attn for blk in model.model.layers]
+        for attn in layers:
+            attn.decode_in_place = True
+        try:
+            # one eager step on a copy warms up library handles and kernel selection
+            scratch = [
+                {"recurrent_state": tuple(t.clone() for t in c["recurrent_state"]),
+                 "conv_state": tuple(t.clone() for t in c["conv_state"])}
+                for c in self.cache
+            ]
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                model(self.tokens.clone(), cache=scratch, use_cache=True)
+            torch.cuda.current_stream().wait_stream(side)
+            del scratch
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph):
+                out = model(self.tokens, cache=self.cache, use_cache=True)
+                for dst, src in zip(self.cache, out["cache"]):
+                    for a, b in zip(dst["recurrent_state"], src["recurrent_state"]):
+                        if a.data_ptr() != b.data_ptr():
+                            a.copy_(b)
+                    for a, b in zip(dst["conv_state"], src["conv_state"]):
+                        a.copy_(b)
+                self.logits = out["logits"]
+                self.tokens.copy_(out["logits"][:, -1:].argmax(-1))
+        finally:
+            for attn in layers:
+                attn.decode_in_place = False
+
+    def step(self):
+        self.graph.replay()
+        return self.tokens

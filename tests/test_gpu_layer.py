@@ -209,3 +209,25 @@ def test_greedy_tokens_match_oracle(name, layers, prompt):
                                      op_mode="exact")
         last = logits[0, -1]
     print(f"{name}: {64 - ties} of 64 greedy tokens equal the oracle's argmax, {ties} near-ties")
+
+
+@pytest.mark.parametrize("name,layers,B", [("tiny.json", None, 2), ("cyclic_flow_attention_400m.json", 2, 4)])
+def test_graphed_decode_matches_eager(name, layers, B):
+    """Replays of the HIP-graph captured decode step equal eager steps bit for
+    bit, replay after replay, with unrelated eager GPU work in between."""
+    model, _, cfg = _model(name, seed=5, layers=layers)
+    ids = torch.randint(0, cfg["vocab_size"], (B, 70), generator=torch.Generator().manual_seed(6)).to(DEV)
+    with torch.no_grad():
+        out = model(ids, use_cache=True)
+        tok = out["logits"][:, -1:].argmax(-1)
+        dec = model.graphed_decoder(out["cache"], tok)
+        cache = out["cache"]
+        for step in range(6):
+            eager = model(tok, cache=cache, use_cache=True)
+            cache = eager["cache"]
+            tok = eager["logits"][:, -1:].argmax(-1)
+            got = dec.step()
+            assert torch.equal(dec.logits, eager["logits"]), f"step {step}: logits differ"
+            assert torch.equal(got, tok), f"step {step}: tokens differ"
+            torch.randn(256, 256, device=DEV).matmul(torch.randn(256, 256, device=DEV))  # unrelated work
+            torch.cuda.synchronize()
