@@ -202,8 +202,11 @@ int cyfa_short_conv(const CyfaConvArgs* a, void* hip_stream) {
     if (!a->x || !a->weight) return fail(CYFA_ERR_VALUE, "cyfa_short_conv: null required pointer");
     for (int i = 0; i < a->D / a->split; i++)
         if (!a->out[i] || !aligned(a->out[i], 16)) return fail(CYFA_ERR_ALIGN, "cyfa_short_conv: output %d null or misaligned", i);
-    if (!aligned(a->x, 16) || a->x_row % 8 != 0 || (a->cache && (!aligned(a->cache, 16) || a->cache_row % 8 || a->cache_batch % 8)))
+    if (!aligned(a->x, 16) || a->x_row % 8 != 0 || (a->cache && (!aligned(a->cache, 16) || a->cache_row % 8 || a->cache_batch % 8)) ||
+        (a->cache_out && (!aligned(a->cache_out, 16) || a->cache_out_row % 8 || a->cache_out_batch % 8)))
         return fail(CYFA_ERR_ALIGN, "cyfa_short_conv: inputs need 16-byte aligned rows");
+    if (a->cache_out && a->cache_out == a->cache && a->T > 32)
+        return fail(CYFA_ERR_VALUE, "cyfa_short_conv: in-place cache update needs T <= 32, got %d", a->T);
     if (a->B == 0 || a->T == 0) return CYFA_OK;
     cyfa::ConvParams p;
     p.B = a->B;
@@ -219,6 +222,9 @@ int cyfa_short_conv(const CyfaConvArgs* a, void* hip_stream) {
     p.bias = (const __bf16*)a->bias;
     for (int i = 0; i < 3; i++) p.out[i] = (__bf16*)a->out[i];
     p.split = a->split;
+    p.cache_out = (__bf16*)a->cache_out;
+    p.cache_out_row = a->cache_out_row;
+    p.cache_out_batch = a->cache_out_batch;
     cyfa::launch_short_conv(p, (hipStream_t)hip_stream);
     return check_launch("cyfa_short_conv");
 }

@@ -62,6 +62,8 @@ struct ConvParams {
     const __bf16 *weight, *bias; // [D, W], nullable [D]
     __bf16* out[3];              // channel c -> out[c / split][(b*T + t)*split + c % split]
     int split;
+    __bf16* cache_out;           // nullable: the last W-1 rows of X, cache addressing
+    long long cache_out_row, cache_out_batch;
 };
 
 struct WorkspaceLayout {

@@ -70,7 +70,9 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormParams p) {
 // where X[b, i] is x[b, i] for i >= 0, cache[b, W - 1 + i] for i < 0 when a
 // cache is given, else 0. Thread = 8 channels x a run of CONV_RUN tokens,
 // sliding the W-row window through registers; channel c goes to output
-// c / split, column c % split.
+// c / split, column c % split. The thread of the last run writes its window,
+// the last W - 1 rows of X, to cache_out (layers/cyfa.py:172-182); with a
+// single run it has read its cache rows before, so the update may be in place.
 constexpr int CONV_RUN = 32;
 
 template <int W>
@@ -121,6 +123,15 @@ __global__ __launch_bounds__(256) void short_conv_kernel(ConvParams p) {
         for (int w = 0; w < W - 1; w++)
 #pragma unroll
             for (int i = 0; i < 8; i++) win[w][i] = win[w + 1][i];
+    }
+    if (p.cache_out && t1 == p.T) {
+#pragma unroll
+        for (int w = 0; w < W - 1; w++) {
+            bf16x8 r;
+#pragma unroll
+            for (int i = 0; i < 8; i++) r[i] = (bf16_t)win[w][i];
+            *reinterpret_cast<bf16x8*>(p.cache_out + (size_t)b * p.cache_out_batch + (size_t)w * p.cache_out_row + c8) = r;
+        }
     }
 }
 

@@ -67,6 +67,7 @@ class CyfaConvArgs(ctypes.Structure):
         ("cache", _c_void_p), ("cache_row", ctypes.c_longlong), ("cache_batch", ctypes.c_longlong),
         ("weight", _c_void_p), ("bias", _c_void_p),
         ("out", _c_void_p * 3), ("split", _c_int),
+        ("cache_out", _c_void_p), ("cache_out_row", ctypes.c_longlong), ("cache_out_batch", ctypes.c_longlong),
     ]
 
 
@@ -244,11 +245,13 @@ def rms_norm(x, weight, eps, gate=None, residual=None, prescale=1.0):
     return out if residual is None else (total, out)
 
 
-def short_conv(x, weight, bias=None, cache=None, split=None):
+def short_conv(x, weight, bias=None, cache=None, split=None, cache_out=None):
     """Causal depthwise convolution over time of x [B, T, D] (rows may be strided).
 
     weight [D, W] bf16, cache an optional [B, W-1, D] view. The D channels are
-    written to D // split contiguous [B, T, split] tensors (split defaults to D)."""
+    written to D // split contiguous [B, T, split] tensors (split defaults to D).
+    ``cache_out`` [B, W-1, D] (channel stride 1) receives the last W-1 rows of
+    cat(cache, x); it may be ``cache`` itself when T <= 32."""
     dev = require_device(x, weight, bias, cache)
     B, T, D = x.shape
     W = weight.shape[-1]
@@ -262,7 +265,9 @@ def short_conv(x, weight, bias=None, cache=None, split=None):
     args = CyfaConvArgs(B=B, T=T, D=D, W=W, x=ptr(x), x_row=x.stride(1),
                         cache=ptr(cache), cache_row=0 if cache is None else cache.stride(1),
                         cache_batch=0 if cache is None else cache.stride(0),
-                        weight=ptr(w), bias=ptr(None if bias is None else bias.contiguous()), split=split)
+                        weight=ptr(w), bias=ptr(None if bias is None else bias.contiguous()), split=split,
+                        cache_out=ptr(cache_out), cache_out_row=0 if cache_out is None else cache_out.stride(1),
+                        cache_out_batch=0 if cache_out is None else cache_out.stride(0))
     for i, o in enumerate(outs):
         args.out[i] = o.data_ptr()
     _check(load_library().cyfa_short_conv(ctypes.byref(args), stream_handle(dev)), "cyfa_short_conv")

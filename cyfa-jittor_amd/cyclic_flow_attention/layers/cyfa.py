@@ -125,6 +125,24 @@ class ShortConvolution(nn.Module):
     execute = forward
 
 
+def shared_conv_cache(conv_state):
+    """The [B, W-1, Dq+Dk+Dv] buffer the three conv caches are channel slices
+    of, when they are (as the fused path creates them); else None."""
+    cq, ck, cv = conv_state
+    base = cq._base if cq._base is not None else None
+    if base is None or ck._base is not base or cv._base is not base or base.dim() != 3:
+        return None
+    if cq.data_ptr() != base.data_ptr() or base.stride(-1) != 1:
+        return None
+    Dq, Dk = cq.shape[-1], ck.shape[-1]
+    item = base.element_size()
+    if ck.data_ptr() != cq.data_ptr() + Dq * item or cv.data_ptr() != ck.data_ptr() + Dk * item:
+        return None
+    if base.shape[-1] != Dq + Dk + cv.shape[-1] or base.shape[:2] != cq.shape[:2]:
+        return None
+    return base
+
+
 def conv_cache_tail(x, cache, W):
     """The last W - 1 rows of cat(cache, x) over time (layers/cyfa.py:172-174)."""
     B, T, D = x.shape
@@ -270,15 +288,23 @@ class CyclicFlowAttention(nn.Module):
         W = self.q_conv1d.width
         qkv = F.linear(x, self._qkv_weight.get(self.q_proj.weight, self.k_proj.weight, self.v_proj.weight))
         conv_cache = None if cache is None else cache.get("conv_state")
-        cat_cache = None if conv_cache is None else torch.cat([c.to(x.dtype) for c in conv_cache], dim=-1)
+        cat_cache = None
+        if conv_cache is not None:
+            cat_cache = shared_conv_cache(conv_cache)
+            if cat_cache is None or cat_cache.dtype != x.dtype:
+                cat_cache = torch.cat([c.to(x.dtype) for c in conv_cache], dim=-1)
+        # the new caches are channel slices of one buffer the conv kernel writes
+        # (the cache itself when a graphed decode step updates in place)
+        in_place = self.decode_in_place and cat_cache is not None and T <= 32
+        tail = cat_cache if in_place else torch.empty(B, W - 1, qkv.shape[-1], dtype=x.dtype, device=x.device)
         wconv = self._conv_weight.get(self.q_conv1d.weight, self.k_conv1d.weight, self.v_conv1d.weight)
         if Dk == Dv:
-            q, k, v = _native.short_conv(qkv, wconv.reshape(-1, W).to(x.dtype), None, cat_cache, split=Dk)
+            q, k, v = _native.short_conv(qkv, wconv.reshape(-1, W).to(x.dtype), None, cat_cache, split=Dk,
+                                         cache_out=tail)
         else:
-            (y,) = _native.short_conv(qkv, wconv.reshape(-1, W).to(x.dtype), None, cat_cache)
+            (y,) = _native.short_conv(qkv, wconv.reshape(-1, W).to(x.dtype), None, cat_cache, cache_out=tail)
             q, k, v = y[..., :Dk].contiguous(), y[..., Dk:2 * Dk].contiguous(), y[..., 2 * Dk:].contiguous()
-        tail = conv_cache_tail(qkv, cat_cache, W)
-        cq, ck, cv = tail[..., :Dk].contiguous(), tail[..., Dk:2 * Dk].contiguous(), tail[..., 2 * Dk:].contiguous()
+        cq, ck, cv = tail[..., :Dk], tail[..., Dk:2 * Dk], tail[..., 2 * Dk:]
         if self._a_bias_zero is None or self._a_bias_zero.dtype != self.b_proj.bias.dtype \
                 or self._a_bias_zero.device != self.b_proj.bias.device:
             self._a_bias_zero = torch.zeros_like(self.b_proj.bias.detach())

@@ -154,6 +154,18 @@ class CyclicFlowAttentionForCausalLM(nn.Module):
         return torch.cat(tokens, dim=1)
 
 
+def _clone_cache(c):
+    """Copy of one layer's cache; the three conv caches become channel slices
+    of one buffer, the layout the fused conv kernel updates in place."""
+    conv = torch.cat([t for t in c["conv_state"]], dim=-1)
+    sizes = [t.shape[-1] for t in c["conv_state"]]
+    views, start = [], 0
+    for n in sizes:
+        views.append(conv[..., start:start + n])
+        start += n
+    return {"recurrent_state": tuple(t.clone() for t in c["recurrent_state"]), "conv_state": tuple(views)}
+
+
 class GraphedDecodeStep:
     """One greedy decode step of the whole model, captured once as a HIP graph.
 
@@ -171,21 +183,13 @@ class GraphedDecodeStep:
             raise ValueError("graphed decoding needs the model and tokens on a GPU")
         self.model = model
         self.tokens = tokens.detach().clone()
-        self.cache = [
-            {"recurrent_state": tuple(t.clone() for t in c["recurrent_state"]),
-             "conv_state": tuple(t.clone() for t in c["conv_state"])}
-            for c in cache
-        ]
+        self.cache = [_clone_cache(c) for c in cache]
         layers = [blk.attn for blk in model.model.layers]
         for attn in layers:
             attn.decode_in_place = True
         try:
             # one eager step on a copy warms up library handles and kernel selection
-            scratch = [
-                {"recurrent_state": tuple(t.clone() for t in c["recurrent_state"]),
-                 "conv_state": tuple(t.clone() for t in c["conv_state"])}
-                for c in self.cache
-            ]
+            scratch = [_clone_cache(c) for c in self.cache]
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(side):
@@ -200,7 +204,8 @@ class GraphedDecodeStep:
                         if a.data_ptr() != b.data_ptr():
                             a.copy_(b)
                     for a, b in zip(dst["conv_state"], src["conv_state"]):
-                        a.copy_(b)
+                        if a.data_ptr() != b.data_ptr():
+                            a.copy_(b)
                 self.logits = out["logits"]
                 self.tokens.copy_(out["logits"][:, -1:].argmax(-1))
         finally:

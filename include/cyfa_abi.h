@@ -128,7 +128,9 @@ int cyfa_rms_norm(const CyfaNormArgs *args, void *hip_stream);
  *   y[b,t,c] = bias[c] + sum_{w<W} weight[c,w] * X[b, t + w - (W-1), c],
  * X[b,i] = x[b,i] for i >= 0, else cache[b, W-1+i] (or 0 without a cache).
  * Channel c is written to out[c / split] at column c % split, so one launch
- * can convolve a fused q|k|v projection into three tensors. */
+ * can convolve a fused q|k|v projection into three tensors. When cache_out is
+ * set it receives the new cache, X[b, T-(W-1) .. T-1] (layers/cyfa.py:172-182);
+ * it may be the cache itself when T <= 32. */
 typedef struct CyfaConvArgs {
     int B, T, D, W;
     const void *x;                /* bf16, element (b,t,c) at x[(b*T + t)*x_row + c] */
@@ -139,6 +141,8 @@ typedef struct CyfaConvArgs {
     const void *bias;             /* nullable bf16 [D] */
     void *out[3];                 /* bf16 [B, T, split] each; D / split of them used */
     int split;
+    void *cache_out;              /* nullable bf16, same addressing as cache with cache_out_row / _batch */
+    long long cache_out_row, cache_out_batch;
 } CyfaConvArgs;
 
 /* Replaces ShortConvolution.execute / _inference (layers/cyfa.py:138-233); the
