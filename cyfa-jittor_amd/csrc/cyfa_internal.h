@@ -19,7 +19,7 @@ struct DecodeParams {
 
 // Prefill: T is split into N = ceil(T / 64) chunks and every (batch, head)
 // sequence into P segments of L consecutive chunks. Segments run in parallel;
-// their start states come from an affine carry over segment-local states.
+// each forms its start state from the segment-local end states before it.
 struct PrefillParams {
     int B, T, H, K, V;
     int N, Tp;  // chunks, padded length N * 64
@@ -36,7 +36,7 @@ struct PrefillParams {
     // workspace
     float* lam;        // [B*H, Tp] reduced clock per token, (lam mod 127) / 127
     float* gam;        // [B*H, Tp] in-chunk inclusive scan of g, log2 units
-    float* seg;        // [B*H, P, K*128 + 128*V] segment-local states, then segment start states
+    float* seg;        // [B*H, P-1, K*128 + 128*V] segment-local end states (register order)
     float* seg_decay;  // [B*H, P] product of alpha over each segment
     __bf16* raw;       // [2, B*H, Tp, 128] pass-1 output of each 128-wide key half
     __bf16* omega;     // [B*H, Tp, 128] slot weights between the two passes

@@ -3,29 +3,31 @@
 // Pipeline for one call (all kernels on the caller's stream):
 //   1. clock_kernel     lam_t = clock0 + sum_{s<=t} delta_s, final clock.
 //   2. segment_state    (only when a sequence is split into P > 1 segments)
-//                       segment-local end states of both passes from a zero
-//                       start, and the product of alpha over each segment.
-//   3. carry_kernel     affine carry over segments: S_in[j+1] = a_j S_in[j] + U_j.
-//   4. pass1_kernel     per (segment, 128-wide key half): sweep the segment's
-//                       64-token chunks with that half of the fp32 key state
-//                       [128 x 128] held in registers and write the half's
-//                       pass-1 output scale (2^G q S + P w) as bf16.
-//   5. readout_kernel   raw = sum of the two halves; z = U(lam) raw;
+//                       segment-local end states E_j of both passes from a
+//                       zero start, and the product a_j of alpha over each
+//                       segment.
+//   3. pass1_kernel     per segment: start from the carried state
+//                       S_j = sum_{i<j} (prod_{i<l<j} a_l) E_i + (prod_{l<j} a_l) h0,
+//                       then sweep the segment's 64-token chunks with
+//                       the fp32 key state [256 x 128] held in registers and
+//                       write each 128-wide key half's pass-1 output scale
+//                       (2^G q S + P w) as bf16.
+//   4. readout_kernel   raw = sum of the two halves; z = U(lam) raw;
 //                       p = softmax(table z); u = table^T p; slot weights
 //                       bf16(U(-lam) u) (ops/chunk_readout.py:797-909).
-//   6. pass2_kernel     per (segment, 128-wide value half): the same sweep for
-//                       that half of the value state [128 x 128] with query =
-//                       slot weights, key = w, value = v -> o (bf16).
-// Splitting pass 1 over the key dimension follows the reference, which forms
-// the pass-1 output as two 128-wide key slices, each scaled and rounded to
-// bf16, and sums them (ops/chunk_o.py:240-250, 369-374). Splitting pass 2 over
-// the value dimension is exact. Each sweep workgroup (8 waves) then needs
-// under 80 KB of LDS and 128 registers per lane, so two independent
-// workgroups share a CU and hide each other's LDS, barrier and global-load
-// latency. All GEMM-shaped work runs on v_mfma_f32_16x16x32_{bf16,f16} with
-// fp32 accumulation; 64-token tiles are staged once in LDS, token-major, and
-// operands that contract over tokens use the gfx950 LDS transpose read. A
-// segment's state stays on chip from its first to its last chunk; only
+//   5. pass2_kernel     per segment: the same carry and sweep for the value state
+//                       [128 x 256] with query = slot weights, key = w,
+//                       value = v -> o (bf16).
+// The pass-1 output is formed as two 128-wide key slices, each scaled and
+// rounded to bf16, and summed, as the reference does (ops/chunk_o.py:240-250,
+// 369-374). A sweep workgroup has 8 waves, one per 32 state columns of a
+// 128-row half (pass 1) or per 32 value columns (pass 2); each wave holds its
+// 128 x 32 block of the fp32 state (64 registers per lane) from the first to
+// the last chunk of the segment. Each 64-token chunk is loaded from HBM once,
+// normalised once and staged once in LDS, token-major; every fragment a wave
+// reads from LDS feeds two MFMAs (its two 16-column blocks). All GEMM-shaped
+// work runs on v_mfma_f32_16x16x32_{bf16,f16} with fp32 accumulation, and
+// operands that contract over tokens use the gfx950 LDS transpose read. Only
 // segment boundary states (one per L chunks) touch HBM.
 //
 // Lane conventions of the 16x16x32 MFMA (wave64, lane l, lr = l & 15, lg = l >> 4):
@@ -57,6 +59,7 @@ constexpr int SEG = SEG_K + SEG_V;
 // the 64 banks, so the rows a transpose read touches per 16-lane block fall on
 // disjoint banks.
 constexpr int RS = 128 + 16;  // 64 x 128 tiles and the 128 x 128 table
+constexpr int RF = 256 + 16;  // 64 x 256 tiles
 constexpr int TS = 64 + 8;    // 64 x 64 score tile
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -70,6 +73,19 @@ __device__ __forceinline__ size_t tok_index(const PrefillParams& p, int b, int t
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// Sweep and segment-state grids are (H, B, segments): the coordinates come
+// straight from the block ids. (A quotient such as blockIdx.x / P is formed in
+// vector registers, and the buffer resources derived from it would then be
+// wrapped in a waterfall loop at every access.)
+struct SegCoord {
+    int bh, j, b, h;
+};
+
+__device__ __forceinline__ SegCoord seg_coord(int H, int j) {
+    const int b = blockIdx.y, h = blockIdx.x;
+    return {b * H + h, j, b, h};
+}
 
 // Global memory in the sweeps goes through buffer instructions: a 128-bit
 // resource per stream in scalar registers and one 32-bit byte offset per lane,
@@ -119,29 +135,15 @@ __device__ __forceinline__ Seq make_seq(const PrefillParams& p, int b, int h, in
 }
 
 // Segment states in the workspace are kept in the register order of the
-// sweeps: the float4 that lane `lane` of wave w holds as accumulator block x
-// (key-state row block kb or value-state row block mb) of half y sits at
-// float offset frag_offset(y, w, x, lane), so a wave loads or stores a block
-// as one contiguous 1 KiB run. The key state fills [0, SEG_K), the value state
-// [SEG_K, SEG).
-__host__ __device__ constexpr int frag_offset(int y, int w, int x, int lane) {
-    return (((y * 8 + w) * 8 + x) * 64 + lane) * 4;
+// sweeps: the float4 that lane `lane` of wave w holds as accumulator block
+// (x, c) sits at float offset frag_offset(w, x, c, lane), so a wave loads or
+// stores a block as one contiguous 1 KiB run. Wave w, x = 0..7, c = 0..1 holds
+//   key state   S[128 (w >> 2) + 16 x + 4 lg + i][32 (w & 3) + 16 c + lr]
+//   value state S[16 x + 4 lg + i][32 w + 16 c + lr].
+// The key state fills [0, SEG_K), the value state [SEG_K, SEG).
+__host__ __device__ constexpr int frag_offset(int w, int x, int c, int lane) {
+    return (((w * 8 + x) * 2 + c) * 64 + lane) * 4;
 }
-
-// Sweep workgroups come in pairs (the two halves of one segment). Workgroup
-// ids are dealt round-robin to the 8 XCDs, so the pair is placed 8 ids apart:
-// both halves run on the same XCD at about the same time and the second read
-// of the shared q / k rows hits that XCD's L2.
-struct SweepBlock {
-    int unit, half;
-};
-
-__device__ __forceinline__ SweepBlock sweep_block() {
-    const int bid = blockIdx.x;
-    return {((bid >> 4) << 3) | (bid & 7), (bid >> 3) & 1};
-}
-
-int sweep_grid(int units) { return (units + 7) / 8 * 16; }
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
@@ -232,59 +234,61 @@ __device__ __forceinline__ V8 load_row(const T* X, int ld, int r0, int k0) {
 }
 
 // Full 256-wide rows [t0, t0 + 64) of a [B, T, H, 256] bf16 tensor for a
-// 512-thread block: thread tid holds row tid >> 3, columns 128 y + 8 c + 64 it
-// of its own half y (raw[it], it = 0, 1) and the same columns of the other half
-// (raw[2 + it]), c = tid & 7. Rows past T are clamped to T - 1 (zeroed when stored).
-__device__ __forceinline__ void issue_full_rows(const Seq& sq, rsrc_t x, int T, int t0, int y, bf16x8 raw[4]) {
+// 512-thread block: thread tid holds row tid >> 3, columns 64 q + 8 c .. + 8 in
+// raw[q] (q = 0..3, c = tid & 7). Rows past T are clamped to T - 1 (zeroed when
+// stored).
+__device__ __forceinline__ void issue_rows(const Seq& sq, rsrc_t x, int T, int t0, bf16x8 raw[4]) {
     const int t = t0 + (threadIdx.x >> 3);
     const uint32_t off = (uint32_t)(t < T ? t : T - 1) * sq.row16 + 16 * (threadIdx.x & 7);
-    const uint32_t own = 2 * HALF * y, other = 2 * HALF * (1 - y);
 #pragma unroll
-    for (int it = 0; it < 2; it++) {
-        raw[it] = ld_b128(x, off + own + 128 * it);
-        raw[2 + it] = ld_b128(x, off + other + 128 * it);
-    }
+    for (int q = 0; q < 4; q++) raw[q] = ld_b128(x, off + 128 * q);
 }
 
 // x_hat = bf16(x rsqrt(mean x^2 + eps) w) over the full row (ops/qk_norm.py:64-107,
-// 206-233); the own-half columns are stored into dst [64][RS] (zero past T).
-// wn is the half's norm weight in LDS. The sum of squares uses the bf16 dot
-// product (two elements per instruction, fp32 accumulation).
+// 206-233), stored into dst [64][RF] (zero past T). wn is the norm weight in
+// LDS. The sum of squares uses the bf16 dot product (two elements per
+// instruction, fp32 accumulation) and the 8 threads of a row meet by DPP.
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ void norm_store_half(const PrefillParams& p, int t0, const bf16x8 raw[4], const float* wn,
+__device__ __forceinline__ void norm_store_rows(const PrefillParams& p, int t0, const bf16x8 raw[4], const float* wn,
                                                 float eps, bf16_t* dst) {
     const int r = threadIdx.x >> 3, c = threadIdx.x & 7;
     float ss = 0.f;
 #pragma unroll
-    for (int it = 0; it < 4; it++)
+    for (int q = 0; q < 4; q++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const bf16x2 x2 = {raw[it][2 * j], raw[it][2 * j + 1]};
+            const bf16x2 x2 = {raw[q][2 * j], raw[q][2 * j + 1]};
             ss = __builtin_amdgcn_fdot2_f32_bf16(x2, x2, ss, false);
         }
     ss = octet_sum(ss);
     const float rs = t0 + r < p.T ? rsqrtf(ss * (1.f / KD) + eps) : 0.f;
 #pragma unroll
-    for (int h2 = 0; h2 < 2; h2++) {
-        const int col = 8 * c + 64 * h2;
+    for (int q = 0; q < 4; q++) {
+        const int col = 64 * q + 8 * c;
         const float4 w0 = *reinterpret_cast<const float4*>(wn + col);
         const float4 w1 = *reinterpret_cast<const float4*>(wn + col + 4);
         const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
         bf16x8 o;
 #pragma unroll
-        for (int j = 0; j < 8; j++) o[j] = (bf16_t)((float)raw[h2][j] * (rs * wv[j]));
-        *reinterpret_cast<bf16x8*>(dst + r * RS + col) = o;
+        for (int j = 0; j < 8; j++) o[j] = (bf16_t)((float)raw[q][j] * (rs * wv[j]));
+        *reinterpret_cast<bf16x8*>(dst + r * RF + col) = o;
     }
 }
 
-// Columns [128 y, 128 y + 128) of rows [t0, t0 + 64) of a [B, T, H, 256] bf16
-// tensor: thread tid holds row tid >> 3, columns 128 y + 8 c + 64 it (it = 0, 1).
-__device__ __forceinline__ void issue_half_rows(const Seq& sq, rsrc_t x, int T, int t0, int y, bf16x8 raw[2]) {
-    const int t = t0 + (threadIdx.x >> 3);
-    const uint32_t off = (uint32_t)(t < T ? t : T - 1) * sq.row16 + 2 * HALF * y + 16 * (threadIdx.x & 7);
+// Store 64 x 256 rows held with the issue_rows mapping into dst [64][RF]; rows
+// at or past `valid` are zeroed.
+__device__ __forceinline__ void store_rows(const bf16x8 raw[4], int valid, bf16_t* dst) {
+    const int r = threadIdx.x >> 3, c = threadIdx.x & 7;
 #pragma unroll
-    for (int it = 0; it < 2; it++) raw[it] = ld_b128(x, off + 128 * it);
+    for (int q = 0; q < 4; q++) {
+        bf16x8 o = raw[q];
+        if (r >= valid) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) o[j] = (bf16_t)0.f;
+        }
+        *reinterpret_cast<bf16x8*>(dst + r * RF + 64 * q + 8 * c) = o;
+    }
 }
 
 // Slot-weight rows [t0, t0 + 64) of the readout output (256-byte rows), same
@@ -343,22 +347,22 @@ __device__ __forceinline__ void score_block(int blk, int& tb, int& sb) {
 }
 
 // Block blk (query block tb >= key block sb) of the masked, decayed scores of
-// a query tile X and key tile Y ([64][RS], 128-wide contraction), into sP:
+// a query tile X and key tile Y (64 rows ld apart, 128-wide contraction), into sP:
 // P[t][s] = bf16(2^(G_t - G_s) c x_t . y_s) for s <= t, else 0 (ops/chunk_o.py:240-250),
 // c = 2^log2_scale the output scale of the pass (exact for the default
 // scale 1/16: scaling a bf16 value by a power of two commutes with rounding).
 // The block is computed transposed (C rows = keys, columns = queries), so a
 // lane holds four consecutive keys of one query and writes them in one store.
-__device__ __forceinline__ void score_tile(const bf16_t* X, const bf16_t* Y, int blk, const float* sGam, float log2_scale,
-                                           bf16_t* sP) {
+__device__ __forceinline__ void score_tile(const bf16_t* X, const bf16_t* Y, int ld, int blk, const float* sGam,
+                                           float log2_scale, bf16_t* sP) {
     const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
     int tb, sb;
     score_block(blk, tb, sb);
     bf16x8 a[4], b[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
-        a[ks] = load_row<bf16x8>(Y, RS, 16 * sb, 32 * ks);
-        b[ks] = load_row<bf16x8>(X, RS, 16 * tb, 32 * ks);
+        a[ks] = load_row<bf16x8>(Y, ld, 16 * sb, 32 * ks);
+        b[ks] = load_row<bf16x8>(X, ld, 16 * tb, 32 * ks);
     }
     f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -376,8 +380,8 @@ __device__ __forceinline__ void score_tile(const bf16_t* X, const bf16_t* Y, int
     *reinterpret_cast<bf16x4*>(sP + t * TS + s0) = o;
 }
 
-__device__ __forceinline__ void zero_scores(bf16_t* sP) {
-    for (int idx = threadIdx.x; idx < 64 * TS / 2; idx += blockDim.x) reinterpret_cast<uint32_t*>(sP)[idx] = 0u;
+__device__ __forceinline__ void zero_scores(bf16_t* sP, int tiles) {
+    for (int idx = threadIdx.x; idx < tiles * 64 * TS / 2; idx += blockDim.x) reinterpret_cast<uint32_t*>(sP)[idx] = 0u;
 }
 
 __device__ __forceinline__ bf16x8 cat4(const bf16x4& lo, const bf16x4& hi) {
@@ -480,16 +484,15 @@ __global__ __launch_bounds__(CLOCK_THREADS) void clock_kernel(PrefillParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// 2. Segment-local end states from a zero start. grid = (B*H*(P-1), 4), 512
-// threads. y = 0, 1: key-state rows [128 y, 128 y + 128); wave w owns columns
-// [16 w, 16 w + 16): acc[kb] = S[128 y + 16 kb + 4 lg + i][16 w + lr].
-// y = 2, 3: value-state columns [128 (y-2), + 128); wave w owns 16 of them:
-// acc[mb] = S[16 mb + 4 lg + i][128 (y-2) + 16 w + lr].
-constexpr int SG_A = 0;                   // bf16 [64][RS]: k_hat half (key) or w (value)
-constexpr int SG_B = SG_A + 64 * RS * 2;  // bf16 [64][RS]: w (key) or v half (value)
+// 2. Segment-local end states from a zero start. grid = (H, B, 2 (P-1)), 512
+// threads, blockIdx.z = 2 j + part; state blocks as in frag_offset. part 0: key state, rows 128 y ..,
+// y = w >> 2, columns 32 (w & 3) ..; part 1: value state, columns 32 w ...
+constexpr int SG_A = 0;                   // bf16 [64][RF]: k_hat (key) or v (value)
+constexpr int SG_B = SG_A + 64 * RF * 2;  // bf16 [64][RS]: w
 constexpr int SG_G = SG_B + 64 * RS * 2;  // f32 [5][64] gates
-constexpr int SG_NW = SG_G + 5 * 64 * 4;  // f32 [128] k norm weight (half)
-constexpr int SG_LDS = SG_NW + HALF * 4;
+constexpr int SG_NW = SG_G + 5 * 64 * 4;  // f32 [256] k norm weight
+constexpr int SG_LDS = SG_NW + KD * 4;
+static_assert(2 * SG_LDS <= 160 * 1024, "two segment-state workgroups must fit in one CU's LDS");
 
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void segment_state_kernel(PrefillParams p) {
     __shared__ __align__(16) unsigned char smem[SG_LDS];
@@ -499,142 +502,133 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
     float* sBeta = sLam + 64;
     float* sGam = sBeta + 64;
     float* sNw = reinterpret_cast<float*>(smem + SG_NW);
-    const int P1 = p.P - 1;
-    const int bh = blockIdx.x / P1, j = blockIdx.x % P1, part = blockIdx.y;
-    const int b = bh / p.H, h = bh % p.H;
-    const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), lr = lane & 15, lg = lane >> 4;
+    const SegCoord cd = seg_coord(p.H, blockIdx.z >> 1);
+    const int bh = cd.bh, j = cd.j, b = cd.b, h = cd.h, key = (blockIdx.z & 1) == 0;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), lg = lane >> 4;
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
-    float* out = p.seg + ((size_t)bh * p.P + j) * SEG;
-    f32x4 acc[8];
+    // key: A rows of the update are k_hat columns 128 y + 16 x, B = w columns 32 (w & 3) + 16 c;
+    // value: A rows are w columns 16 x, B = v columns 32 w + 16 c.
+    const int a_col = key ? HALF * (w >> 2) : 0, a_ld = key ? RF : RS;
+    const int b_col = key ? 32 * (w & 3) : 32 * w;
+    const bf16_t* sArow = key ? sA : sB;
+    const bf16_t* sBcol = key ? sB : sA;
+    const int b_ld = key ? RS : RF;
+    f32x4 acc[8][2];
 #pragma unroll
-    for (int x = 0; x < 8; x++) acc[x] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int x = 0; x < 8; x++) acc[x][0] = acc[x][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     const Seq sq = make_seq(p, b, h, bh);
     GateRegs gr = issue_gates(sq, p.T, n0 * 64);
-
-    if (part < 2) {
-        const int y = part;
-        if (tid < HALF) sNw[tid] = p.k_w[HALF * y + tid];
-        bf16x8 kraw[4];
-        issue_full_rows(sq, sq.k, p.T, n0 * 64, y, kraw);
-        float logdecay = 0.f;
+    bf16x8 raw[4];
+    issue_rows(sq, key ? sq.k : sq.v, p.T, n0 * 64, raw);
+    if (key && tid < KD) sNw[tid] = p.k_w[tid];
+    float logdecay = 0.f;
+    __syncthreads();
+    for (int n = n0; n < n1; n++) {
+        const int t0 = n * 64;
+        commit_gates(p, t0, gr, sLam, sBeta, sGam);
+        store_write_tile(gr, p.T - t0, sB);
+        if (key)
+            norm_store_rows(p, t0, raw, sNw, p.k_eps, sA);
+        else
+            store_rows(raw, p.T - t0, sA);
+        if (n + 1 < n1) {
+            issue_rows(sq, key ? sq.k : sq.v, p.T, t0 + 64, raw);
+            gr = issue_gates(sq, p.T, t0 + 64);
+        }
         __syncthreads();
-        for (int n = n0; n < n1; n++) {
-            const int t0 = n * 64;
-            commit_gates(p, t0, gr, sLam, sBeta, sGam);
-            store_write_tile(gr, p.T - t0, sB);
-            norm_store_half(p, t0, kraw, sNw, p.k_eps, sA);
-            if (n + 1 < n1) {
-                issue_full_rows(sq, sq.k, p.T, t0 + 64, y, kraw);
-                gr = issue_gates(sq, p.T, t0 + 64);
-            }
-            __syncthreads();
-            logdecay += sGam[63];
-            bf16x8 wt[2];
+        logdecay += sGam[63];
+        const float dec = sGam[64 + 63];
 #pragma unroll
-            for (int ss = 0; ss < 2; ss++) {
-                const bf16x8 wf = load_tr_bf16(sB, RS, 32 * ss, 16 * w);
-#pragma unroll
-                for (int jj = 0; jj < 8; jj++) wt[ss][jj] = (bf16_t)((float)wf[jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
-            }
-            const float dec = sGam[64 + 63];
-#pragma unroll
-            for (int kb = 0; kb < 8; kb++) acc[kb] *= dec;
-#pragma unroll
-            for (int ss = 0; ss < 2; ss++)
-#pragma unroll
-                for (int kb = 0; kb < 8; kb++) acc[kb] = mfma_bf16(load_tr_bf16(sA, RS, 32 * ss, 16 * kb), wt[ss], acc[kb]);
-            __syncthreads();
+        for (int x = 0; x < 8; x++) {
+            acc[x][0] *= dec;
+            acc[x][1] *= dec;
         }
+        // S += A^T bf16(2^(G_last - G_s) B): bt[c][jj] = B[32 ss + 8 lg + jj][b_col + 16 c + lr] scaled.
 #pragma unroll
-        for (int kb = 0; kb < 8; kb++) *reinterpret_cast<f32x4*>(out + frag_offset(y, w, kb, lane)) = acc[kb];
-        if (y == 0 && tid == 0) p.seg_decay[bh * p.P + j] = exp2f(logdecay);
-    } else {
-        const int y = part - 2;
-        bf16x8 vraw[2];
-        issue_half_rows(sq, sq.v, p.T, n0 * 64, y, vraw);
-        for (int n = n0; n < n1; n++) {
-            const int t0 = n * 64;
-            commit_gates(p, t0, gr, sLam, sBeta, sGam);
-            store_write_tile(gr, p.T - t0, sA);
-            store_half_rows(vraw, p.T - t0, sB);
-            if (n + 1 < n1) {
-                issue_half_rows(sq, sq.v, p.T, t0 + 64, y, vraw);
-                gr = issue_gates(sq, p.T, t0 + 64);
+        for (int ss = 0; ss < 2; ss++) {
+            bf16x8 bt[2];
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const bf16x8 f = load_tr_bf16(sBcol, b_ld, 32 * ss, b_col + 16 * c);
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++) bt[c][jj] = (bf16_t)((float)f[jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
             }
-            __syncthreads();
-            const float dec = sGam[64 + 63];
 #pragma unroll
-            for (int mb = 0; mb < 8; mb++) acc[mb] *= dec;
-#pragma unroll
-            for (int ss = 0; ss < 2; ss++) {
-                const bf16x8 vb = load_tr_bf16(sB, RS, 32 * ss, 16 * w);
-                bf16x8 vt;
-#pragma unroll
-                for (int jj = 0; jj < 8; jj++) vt[jj] = (bf16_t)((float)vb[jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
-#pragma unroll
-                for (int mb = 0; mb < 8; mb++) acc[mb] = mfma_bf16(load_tr_bf16(sA, RS, 32 * ss, 16 * mb), vt, acc[mb]);
+            for (int x = 0; x < 8; x++) {
+                const bf16x8 af = load_tr_bf16(sArow, a_ld, 32 * ss, a_col + 16 * x);
+                acc[x][0] = mfma_bf16(af, bt[0], acc[x][0]);
+                acc[x][1] = mfma_bf16(af, bt[1], acc[x][1]);
+                if (x & 1) sched_fence();
             }
-            __syncthreads();
         }
-        float* outv = out + SEG_K;
+        __syncthreads();
+    }
+    float* out = p.seg + ((size_t)bh * (p.P - 1) + j) * SEG + (key ? 0 : SEG_K);
 #pragma unroll
-        for (int mb = 0; mb < 8; mb++) *reinterpret_cast<f32x4*>(outv + frag_offset(y, w, mb, lane)) = acc[mb];
+    for (int x = 0; x < 8; x++)
+#pragma unroll
+        for (int c = 0; c < 2; c++) *reinterpret_cast<f32x4*>(out + frag_offset(w, x, c, lane)) = acc[x][c];
+    if (key && tid == 0) p.seg_decay[bh * p.P + j] = exp2f(logdecay);
+}
+
+// ---------------------------------------------------------------------------
+// Start state of segment j, in register order (the affine carry over
+// segments S_{i+1} = a_i S_i + E_i, unrolled):
+//   S_j = sum_{i<j} (prod_{i<l<j} a_l) E_i + (prod_{l<j} a_l) h0.
+// base selects the key (0) or value (SEG_K) part of the stored states; h0 is
+// row-major and nullable, h0_index(x, c, i) gives the element of acc[x][c][i].
+// The segment workgroups of one sequence have block ids H * B apart; when
+// H * B is a multiple of 8 they are dealt to the same XCD, and most E_i reads
+// hit that XCD's L2.
+template <typename H0Index>
+__device__ __forceinline__ void load_start_state(const PrefillParams& p, int bh, int j, int base, const float* h0,
+                                                 H0Index h0_index, f32x4 acc[8][2]) {
+    const int lane = threadIdx.x & 63, w = wave_id();
+#pragma unroll
+    for (int x = 0; x < 8; x++) acc[x][0] = acc[x][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float a = 1.f;
+    const float* seg = p.seg + (size_t)bh * (p.P - 1) * SEG + base;
+    for (int i = j - 1; i >= 0; i--) {
+        const float* e = seg + (size_t)i * SEG;
+        f32x4 v[8][2];
+#pragma unroll
+        for (int x = 0; x < 8; x++)
+#pragma unroll
+            for (int c = 0; c < 2; c++) v[x][c] = *reinterpret_cast<const f32x4*>(e + frag_offset(w, x, c, lane));
+#pragma unroll
+        for (int x = 0; x < 8; x++)
+#pragma unroll
+            for (int c = 0; c < 2; c++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) acc[x][c][q] = fmaf(a, v[x][c][q], acc[x][c][q]);
+        a *= p.seg_decay[bh * p.P + i];
+    }
+    if (h0) {
+#pragma unroll
+        for (int x = 0; x < 8; x++)
+#pragma unroll
+            for (int c = 0; c < 2; c++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) acc[x][c][q] = fmaf(a, h0[h0_index(x, c, q)], acc[x][c][q]);
     }
 }
 
 // ---------------------------------------------------------------------------
-// 3. Carry over segments, in place: slot j receives the start state of
-// segment j. grid = (B*H, SEG / 1024).
-__global__ __launch_bounds__(256) void carry_kernel(PrefillParams p) {
-    const int bh = blockIdx.x;
-    const int e = (blockIdx.y * 256 + threadIdx.x) * 4;
-    float4 S = make_float4(0.f, 0.f, 0.f, 0.f);
-    {
-        // e is a register-order offset; find the four row-major elements it holds.
-        const bool key = e < SEG_K;
-        const int f = (key ? e : e - SEG_K) >> 2;
-        const int lane = f & 63, x = (f >> 6) & 7, w = (f >> 9) & 7, y = f >> 12;
-        const int lr = lane & 15, lg = lane >> 4;
-        const float* h0 = key ? p.h0_k : p.h0_v;
-        if (h0) {
-            const int ld = key ? kSlots : VD;
-            const int row = key ? HALF * y + 16 * x + 4 * lg : 16 * x + 4 * lg;
-            const int col = key ? 16 * w + lr : HALF * y + 16 * w + lr;
-            const float* src = h0 + (size_t)bh * (key ? SEG_K : SEG_V) + row * ld + col;
-            S = make_float4(src[0], src[ld], src[2 * ld], src[3 * ld]);
-        }
-    }
-    for (int j = 0; j < p.P; j++) {
-        float4* slot = reinterpret_cast<float4*>(p.seg + ((size_t)bh * p.P + j) * SEG + e);
-        if (j + 1 < p.P) {
-            const float4 U = *slot;
-            const float a = p.seg_decay[bh * p.P + j];
-            *slot = S;
-            S.x = fmaf(a, S.x, U.x);
-            S.y = fmaf(a, S.y, U.y);
-            S.z = fmaf(a, S.z, U.z);
-            S.w = fmaf(a, S.w, U.w);
-        } else {
-            *slot = S;
-        }
-    }
-}
+// 4. Pass 1 (key state), one segment per workgroup. grid = (H, B, P), 512 threads.
+// Wave w works on key half y = w >> 2 and state columns [32 mq, 32 mq + 32),
+// mq = w & 3: acc[kb][c] = S[128 y + 16 kb + 4 lg + i][32 mq + 16 c + lr], and
+// the same 32 output coordinates of half y:
+// out[tb][c] = raw_y^T[32 mq + 16 c + 4 lg + i][16 tb + lr].
+constexpr int P1_Q = 0;                       // bf16 [64][RF] q_hat
+constexpr int P1_K = P1_Q + 64 * RF * 2;      // bf16 [64][RF] k_hat
+constexpr int P1_W = P1_K + 64 * RF * 2;      // bf16 [64][RS] w
+constexpr int P1_P = P1_W + 64 * RS * 2;      // bf16 [2][64][TS] masked scores of each half
+constexpr int P1_G = P1_P + 2 * 64 * TS * 2;  // f32 [5][64] gates
+constexpr int P1_NW = P1_G + 5 * 64 * 4;      // f32 [2][256] q and k norm weights
+constexpr int P1_LDS = P1_NW + 2 * KD * 4;
+static_assert(P1_LDS <= 160 * 1024, "pass-1 workgroup must fit in one CU's LDS");
 
-// ---------------------------------------------------------------------------
-// 4. Pass 1 (key state), one key half per workgroup. grid = sweep_grid(B*H*P),
-// 512 threads. Wave w owns key-state columns [16 w, 16 w + 16) of rows
-// [128 y, 128 y + 128): acc[kb] = S[128 y + 16 kb + 4 lg + i][16 w + lr], and
-// the same 16 output coordinates: out[tb] = raw^T[16 w + 4 lg + i][16 tb + lr].
-constexpr int P1_Q = 0;                       // bf16 [64][RS] q_hat (half)
-constexpr int P1_K = P1_Q + 64 * RS * 2;      // bf16 [64][RS] k_hat (half)
-constexpr int P1_W = P1_K + 64 * RS * 2;      // bf16 [64][RS] w
-constexpr int P1_P = P1_W + 64 * RS * 2;      // bf16 [64][TS] masked scores
-constexpr int P1_G = P1_P + 64 * TS * 2;      // f32 [5][64] gates
-constexpr int P1_NW = P1_G + 5 * 64 * 4;      // f32 [2][128] q and k norm weights (half)
-constexpr int P1_LDS = P1_NW + 2 * HALF * 4;
-static_assert(2 * P1_LDS <= 160 * 1024, "two pass-1 workgroups must fit in one CU's LDS");
-
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void pass1_kernel(PrefillParams p) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void pass1_kernel(PrefillParams p) {
     __shared__ __align__(16) unsigned char smem[P1_LDS];
     bf16_t* sQ = reinterpret_cast<bf16_t*>(smem + P1_Q);
     bf16_t* sK = reinterpret_cast<bf16_t*>(smem + P1_K);
@@ -644,103 +638,116 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void p
     float* sBeta = sLam + 64;
     float* sGam = sBeta + 64;
     float* sQw = reinterpret_cast<float*>(smem + P1_NW);
-    float* sKw = sQw + HALF;
+    float* sKw = sQw + KD;
 
-    const SweepBlock sw = sweep_block();
-    if (sw.unit >= p.B * p.H * p.P) return;
-    const int bh = sw.unit / p.P, j = sw.unit % p.P, y = sw.half;
-    const int b = bh / p.H, h = bh % p.H;
+    const SegCoord cd = seg_coord(p.H, blockIdx.z);
+    const int bh = cd.bh, j = cd.j, b = cd.b, h = cd.h;
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), lr = lane & 15, lg = lane >> 4;
+    const int y = w >> 2, mq = w & 3;
     const float log2_scale = p.log2_scale;
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
-    if (tid < HALF) {
-        sQw[tid] = p.q_w[HALF * y + tid];
-        sKw[tid] = p.k_w[HALF * y + tid];
+    if (tid < KD) {
+        sQw[tid] = p.q_w[tid];
+        sKw[tid] = p.k_w[tid];
     }
-    zero_scores(sP);  // the two blocks above the diagonal that the intra product reads stay zero
-    f32x4 acc[8];
-    {
-        const float* h0 = p.h0_k ? p.h0_k + (size_t)bh * SEG_K : nullptr;
-        if (p.P > 1) {
-            const float* s0 = p.seg + ((size_t)bh * p.P + j) * SEG;
-#pragma unroll
-            for (int kb = 0; kb < 8; kb++) acc[kb] = *reinterpret_cast<const f32x4*>(s0 + frag_offset(y, w, kb, lane));
-        } else if (h0) {
-#pragma unroll
-            for (int kb = 0; kb < 8; kb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[kb][i] = h0[(HALF * y + 16 * kb + 4 * lg + i) * kSlots + 16 * w + lr];
-        } else {
-#pragma unroll
-            for (int kb = 0; kb < 8; kb++) acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-    }
+    zero_scores(sP, 2);  // the two blocks above the diagonal that the intra product reads stay zero
+    bf16_t* sPy = sP + y * 64 * TS;
+    f32x4 acc[8][2];
+    load_start_state(p, bh, j, 0, p.h0_k ? p.h0_k + (size_t)bh * SEG_K : nullptr,
+                     [&](int kb, int c, int i) { return (HALF * y + 16 * kb + 4 * lg + i) * kSlots + 32 * mq + 16 * c + lr; },
+                     acc);
     const Seq sq = make_seq(p, b, h, bh);
     const rsrc_t rraw = make_rsrc(p.raw + ((size_t)y * p.B * p.H + bh) * p.Tp * kSlots, (size_t)p.Tp * kSlots * 2);
-    const uint32_t raw_lane = (uint32_t)lr * (kSlots * 2) + 2 * (16 * w + 4 * lg);
+    const uint32_t raw_lane = (uint32_t)lr * (kSlots * 2) + 2 * (32 * mq + 4 * lg);
     bf16x8 qraw[4], kraw[4];
-    issue_full_rows(sq, sq.q, p.T, n0 * 64, y, qraw);
-    issue_full_rows(sq, sq.k, p.T, n0 * 64, y, kraw);
+    issue_rows(sq, sq.q, p.T, n0 * 64, qraw);
+    issue_rows(sq, sq.k, p.T, n0 * 64, kraw);
     GateRegs gr = issue_gates(sq, p.T, n0 * 64);
-    __syncthreads();  // norm weights staged, score tile zeroed
+    __syncthreads();  // norm weights staged, score tiles zeroed
 
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
         commit_gates(p, t0, gr, sLam, sBeta, sGam);
         store_write_tile(gr, p.T - t0, sW);
-        norm_store_half(p, t0, qraw, sQw, p.q_eps, sQ);
-        norm_store_half(p, t0, kraw, sKw, p.k_eps, sK);
+        norm_store_rows(p, t0, qraw, sQw, p.q_eps, sQ);
+        norm_store_rows(p, t0, kraw, sKw, p.k_eps, sK);
         sched_fence();  // the next chunk's loads reuse these registers
         if (n + 1 < n1) {
-            issue_full_rows(sq, sq.q, p.T, t0 + 64, y, qraw);
-            issue_full_rows(sq, sq.k, p.T, t0 + 64, y, kraw);
+            issue_rows(sq, sq.q, p.T, t0 + 64, qraw);
+            issue_rows(sq, sq.k, p.T, t0 + 64, kraw);
             gr = issue_gates(sq, p.T, t0 + 64);
         }
         __syncthreads();
 
-        // Masked, decayed scores of this half's key slice.
-        score_tile(sQ, sK, w, sGam, log2_scale, sP);
-        if (w < 2) score_tile(sQ, sK, w + 8, sGam, log2_scale, sP);
-        // raw^T = 2^G_t S_n^T q_t over this half's key rows.
-        f32x4 out[4];
+        // Masked, decayed scores of this half's key slice: blocks mq, mq + 4 (and mq + 8).
+        score_tile(sQ + HALF * y, sK + HALF * y, RF, mq, sGam, log2_scale, sPy);
+        score_tile(sQ + HALF * y, sK + HALF * y, RF, mq + 4, sGam, log2_scale, sPy);
+        if (mq < 2) score_tile(sQ + HALF * y, sK + HALF * y, RF, mq + 8, sGam, log2_scale, sPy);
+        // raw_y^T = 2^G_t S_n^T q_t over this half's key rows.
+        f32x4 out[4][2];
 #pragma unroll
-        for (int tb = 0; tb < 4; tb++) out[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int tb = 0; tb < 4; tb++) out[tb][0] = out[tb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            const bf16x8 a = state_frag(acc[2 * ks], acc[2 * ks + 1]);
+            const bf16x8 a0 = state_frag(acc[2 * ks][0], acc[2 * ks + 1][0]);
+            const bf16x8 a1 = state_frag(acc[2 * ks][1], acc[2 * ks + 1][1]);
 #pragma unroll
-            for (int tb = 0; tb < 4; tb++)
-                out[tb] = mfma_bf16(a, load_row_perm(sQ + (16 * tb + lr) * RS + 32 * ks, lg), out[tb]);
+            for (int tb = 0; tb < 4; tb++) {
+                const bf16x8 bq = load_row_perm(sQ + (16 * tb + lr) * RF + HALF * y + 32 * ks, lg);
+                out[tb][0] = mfma_bf16(a0, bq, out[tb][0]);
+                out[tb][1] = mfma_bf16(a1, bq, out[tb][1]);
+            }
             sched_fence();
         }
 #pragma unroll
-        for (int tb = 0; tb < 4; tb++) out[tb] *= sGam[64 + 16 * tb + lr] * p.scale;
+        for (int tb = 0; tb < 4; tb++) {
+            const float sc = sGam[64 + 16 * tb + lr] * p.scale;
+            out[tb][0] *= sc;
+            out[tb][1] *= sc;
+        }
         __syncthreads();  // scores complete
 
-        // raw^T += w^T P^T (P carries the scale); the blocks of P above the diagonal are zero.
-        // wf[ss][jj] = w[32 ss + 8 lg + jj][16 w + lr].
-        bf16x8 wf[2];
+        // raw_y^T += w^T P_y^T (P carries the scale); the blocks of P above the diagonal are zero.
+        // wf[c][ss][jj] = w[32 ss + 8 lg + jj][32 mq + 16 c + lr].
+        bf16x8 wf[2][2];
 #pragma unroll
-        for (int ss = 0; ss < 2; ss++) wf[ss] = load_tr_bf16(sW, RS, 32 * ss, 16 * w);
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int ss = 0; ss < 2; ss++) wf[c][ss] = load_tr_bf16(sW, RS, 32 * ss, 32 * mq + 16 * c);
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+            for (int ss = 0; ss <= (tb >> 1); ss++) {
+                const bf16x8 pf = load_row<bf16x8>(sPy, TS, 16 * tb, 32 * ss);
+                out[tb][0] = mfma_bf16(wf[0][ss], pf, out[tb][0]);
+                out[tb][1] = mfma_bf16(wf[1][ss], pf, out[tb][1]);
+            }
 #pragma unroll
         for (int tb = 0; tb < 4; tb++)
 #pragma unroll
-            for (int ss = 0; ss <= (tb >> 1); ss++)
-                out[tb] = mfma_bf16(wf[ss], load_row<bf16x8>(sP, TS, 16 * tb, 32 * ss), out[tb]);
-#pragma unroll
-        for (int tb = 0; tb < 4; tb++)
-            st_b64(rraw, raw_lane, (uint32_t)(t0 + 16 * tb) * (kSlots * 2), to_bf16x4(out[tb], 1.f));
+            for (int c = 0; c < 2; c++)
+                st_b64(rraw, raw_lane + 32 * c, (uint32_t)(t0 + 16 * tb) * (kSlots * 2), to_bf16x4(out[tb][c], 1.f));
         // State update: S = 2^G_last S + k_hat^T bf16(2^(G_last - G_s) w).
         const float dec = sGam[64 + 63];
 #pragma unroll
-        for (int kb = 0; kb < 8; kb++) acc[kb] *= dec;
+        for (int kb = 0; kb < 8; kb++) {
+            acc[kb][0] *= dec;
+            acc[kb][1] *= dec;
+        }
 #pragma unroll
         for (int ss = 0; ss < 2; ss++) {
-            bf16x8 wt;
+            bf16x8 wt[2];
 #pragma unroll
-            for (int jj = 0; jj < 8; jj++) wt[jj] = (bf16_t)((float)wf[ss][jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
+            for (int c = 0; c < 2; c++)
 #pragma unroll
-            for (int kb = 0; kb < 8; kb++) acc[kb] = mfma_bf16(load_tr_bf16(sK, RS, 32 * ss, 16 * kb), wt, acc[kb]);
+                for (int jj = 0; jj < 8; jj++)
+                    wt[c][jj] = (bf16_t)((float)wf[c][ss][jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
+#pragma unroll
+            for (int kb = 0; kb < 8; kb++) {
+                const bf16x8 kf = load_tr_bf16(sK, RF, 32 * ss, HALF * y + 16 * kb);
+                acc[kb][0] = mfma_bf16(kf, wt[0], acc[kb][0]);
+                acc[kb][1] = mfma_bf16(kf, wt[1], acc[kb][1]);
+            }
             sched_fence();
         }
         __syncthreads();  // tiles are overwritten by the next chunk
@@ -751,7 +758,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void p
 #pragma unroll
         for (int kb = 0; kb < 8; kb++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) dst[(HALF * y + 16 * kb + 4 * lg + i) * kSlots + 16 * w + lr] = acc[kb][i];
+            for (int c = 0; c < 2; c++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    dst[(HALF * y + 16 * kb + 4 * lg + i) * kSlots + 32 * mq + 16 * c + lr] = acc[kb][c][i];
     }
 }
 
@@ -906,19 +916,19 @@ int readout_groups(int B, int Tp, int H) {
 }
 
 // ---------------------------------------------------------------------------
-// 6. Pass 2 (value state), one value half per workgroup. grid = sweep_grid(B*H*P),
-// 512 threads. Wave w owns value columns 128 y + 16 w + [0, 16):
-// acc[mb] = S[16 mb + 4 lg + i][128 y + 16 w + lr], and the same 16 output
-// coordinates: out[tb] = o^T[128 y + 16 w + 4 lg + i][16 tb + lr].
+// 6. Pass 2 (value state), one segment per workgroup. grid = (H, B, P), 512
+// threads. Wave w owns value columns [32 w, 32 w + 32):
+// acc[mb][c] = S[16 mb + 4 lg + i][32 w + 16 c + lr], and the same 32 output
+// coordinates: out[tb][c] = o^T[32 w + 16 c + 4 lg + i][16 tb + lr].
 constexpr int P2_OM = 0;                   // bf16 [64][RS] slot weights (query)
 constexpr int P2_W = P2_OM + 64 * RS * 2;  // bf16 [64][RS] w (key)
-constexpr int P2_V = P2_W + 64 * RS * 2;   // bf16 [64][RS] v (half)
-constexpr int P2_P = P2_V + 64 * RS * 2;   // bf16 [64][TS] masked scores
+constexpr int P2_V = P2_W + 64 * RS * 2;   // bf16 [64][RF] v
+constexpr int P2_P = P2_V + 64 * RF * 2;   // bf16 [64][TS] masked scores
 constexpr int P2_G = P2_P + 64 * TS * 2;   // f32 [5][64] gates
 constexpr int P2_LDS = P2_G + 5 * 64 * 4;
-static_assert(2 * P2_LDS <= 160 * 1024, "two pass-2 workgroups must fit in one CU's LDS");
+static_assert(P2_LDS <= 160 * 1024, "pass-2 workgroup must fit in one CU's LDS");
 
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void pass2_kernel(PrefillParams p) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void pass2_kernel(PrefillParams p) {
     __shared__ __align__(16) unsigned char smem[P2_LDS];
     bf16_t* sOm = reinterpret_cast<bf16_t*>(smem + P2_OM);
     bf16_t* sW = reinterpret_cast<bf16_t*>(smem + P2_W);
@@ -928,35 +938,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void p
     float* sBeta = sLam + 64;
     float* sGam = sBeta + 64;
 
-    const SweepBlock sw = sweep_block();
-    if (sw.unit >= p.B * p.H * p.P) return;
-    const int bh = sw.unit / p.P, j = sw.unit % p.P, y = sw.half;
-    const int b = bh / p.H, h = bh % p.H;
+    const SegCoord cd = seg_coord(p.H, blockIdx.z);
+    const int bh = cd.bh, j = cd.j, b = cd.b, h = cd.h;
     const int lane = threadIdx.x & 63, w = wave_id(), lr = lane & 15, lg = lane >> 4;
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
-    zero_scores(sP);
-    f32x4 acc[8];
-    {
-        const float* h0 = p.h0_v ? p.h0_v + (size_t)bh * SEG_V : nullptr;
-        if (p.P > 1) {
-            const float* s0 = p.seg + ((size_t)bh * p.P + j) * SEG + SEG_K;
-#pragma unroll
-            for (int mb = 0; mb < 8; mb++) acc[mb] = *reinterpret_cast<const f32x4*>(s0 + frag_offset(y, w, mb, lane));
-        } else if (h0) {
-#pragma unroll
-            for (int mb = 0; mb < 8; mb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[mb][i] = h0[(16 * mb + 4 * lg + i) * VD + HALF * y + 16 * w + lr];
-        } else {
-#pragma unroll
-            for (int mb = 0; mb < 8; mb++) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-    }
+    zero_scores(sP, 1);
+    f32x4 acc[8][2];
+    load_start_state(p, bh, j, SEG_K, p.h0_v ? p.h0_v + (size_t)bh * SEG_V : nullptr,
+                     [&](int mb, int c, int i) { return (16 * mb + 4 * lg + i) * VD + 32 * w + 16 * c + lr; }, acc);
     const Seq sq = make_seq(p, b, h, bh);
     const rsrc_t rom = make_rsrc(p.omega + (size_t)bh * p.Tp * kSlots, (size_t)p.Tp * kSlots * 2);
-    const uint32_t o_lane = (uint32_t)lr * sq.row16 + 2 * (HALF * y + 16 * w + 4 * lg);
-    bf16x8 vraw[2], om[2];
-    issue_half_rows(sq, sq.v, p.T, n0 * 64, y, vraw);
+    const uint32_t o_lane = (uint32_t)lr * sq.row16 + 2 * (32 * w + 4 * lg);
+    bf16x8 vraw[4], om[2];
+    issue_rows(sq, sq.v, p.T, n0 * 64, vraw);
     issue_omega(rom, n0 * 64, om);
     GateRegs gr = issue_gates(sq, p.T, n0 * 64);
 
@@ -965,55 +959,85 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void p
         commit_gates(p, t0, gr, sLam, sBeta, sGam);
         store_write_tile(gr, p.T - t0, sW);
         store_half_rows(om, 64, sOm);
-        store_half_rows(vraw, p.T - t0, sV);
+        store_rows(vraw, p.T - t0, sV);
+        sched_fence();
         if (n + 1 < n1) {
-            issue_half_rows(sq, sq.v, p.T, t0 + 64, y, vraw);
+            issue_rows(sq, sq.v, p.T, t0 + 64, vraw);
             issue_omega(rom, t0 + 64, om);
             gr = issue_gates(sq, p.T, t0 + 64);
         }
         __syncthreads();
 
-        score_tile(sOm, sW, w, sGam, 0.f, sP);
-        if (w < 2) score_tile(sOm, sW, w + 8, sGam, 0.f, sP);
+        score_tile(sOm, sW, RS, w, sGam, 0.f, sP);
+        if (w < 2) score_tile(sOm, sW, RS, w + 8, sGam, 0.f, sP);
         // o^T = 2^G_t S_n^T weights_t.
-        f32x4 out[4];
+        f32x4 out[4][2];
 #pragma unroll
-        for (int tb = 0; tb < 4; tb++) out[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int tb = 0; tb < 4; tb++) out[tb][0] = out[tb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            const bf16x8 a = state_frag(acc[2 * ks], acc[2 * ks + 1]);
+            const bf16x8 a0 = state_frag(acc[2 * ks][0], acc[2 * ks + 1][0]);
+            const bf16x8 a1 = state_frag(acc[2 * ks][1], acc[2 * ks + 1][1]);
 #pragma unroll
-            for (int tb = 0; tb < 4; tb++)
-                out[tb] = mfma_bf16(a, load_row_perm(sOm + (16 * tb + lr) * RS + 32 * ks, lg), out[tb]);
+            for (int tb = 0; tb < 4; tb++) {
+                const bf16x8 bo = load_row_perm(sOm + (16 * tb + lr) * RS + 32 * ks, lg);
+                out[tb][0] = mfma_bf16(a0, bo, out[tb][0]);
+                out[tb][1] = mfma_bf16(a1, bo, out[tb][1]);
+            }
+            sched_fence();
         }
 #pragma unroll
-        for (int tb = 0; tb < 4; tb++) out[tb] *= sGam[64 + 16 * tb + lr];
+        for (int tb = 0; tb < 4; tb++) {
+            const float sc = sGam[64 + 16 * tb + lr];
+            out[tb][0] *= sc;
+            out[tb][1] *= sc;
+        }
         __syncthreads();  // scores complete
 
-        // o^T += v^T P^T.
-        bf16x8 vb[2];
+        // o^T += v^T P^T. vb[c][ss][jj] = v[32 ss + 8 lg + jj][32 w + 16 c + lr].
+        bf16x8 vb[2][2];
 #pragma unroll
-        for (int ss = 0; ss < 2; ss++) vb[ss] = load_tr_bf16(sV, RS, 32 * ss, 16 * w);
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int ss = 0; ss < 2; ss++) vb[c][ss] = load_tr_bf16(sV, RF, 32 * ss, 32 * w + 16 * c);
 #pragma unroll
         for (int tb = 0; tb < 4; tb++)
 #pragma unroll
-            for (int ss = 0; ss <= (tb >> 1); ss++)
-                out[tb] = mfma_bf16(vb[ss], load_row<bf16x8>(sP, TS, 16 * tb, 32 * ss), out[tb]);
+            for (int ss = 0; ss <= (tb >> 1); ss++) {
+                const bf16x8 pf = load_row<bf16x8>(sP, TS, 16 * tb, 32 * ss);
+                out[tb][0] = mfma_bf16(vb[0][ss], pf, out[tb][0]);
+                out[tb][1] = mfma_bf16(vb[1][ss], pf, out[tb][1]);
+            }
 #pragma unroll
         for (int tb = 0; tb < 4; tb++) {
-            if (t0 + 16 * tb + lr < p.T) st_b64(sq.o, o_lane, (uint32_t)(t0 + 16 * tb) * sq.row16, to_bf16x4(out[tb], 1.f));
+            if (t0 + 16 * tb + lr < p.T) {
+#pragma unroll
+                for (int c = 0; c < 2; c++)
+                    st_b64(sq.o, o_lane + 32 * c, (uint32_t)(t0 + 16 * tb) * sq.row16, to_bf16x4(out[tb][c], 1.f));
+            }
         }
         // State update: S = 2^G_last S + w^T bf16(2^(G_last - G_s) v).
         const float dec = sGam[64 + 63];
 #pragma unroll
-        for (int mb = 0; mb < 8; mb++) acc[mb] *= dec;
+        for (int mb = 0; mb < 8; mb++) {
+            acc[mb][0] *= dec;
+            acc[mb][1] *= dec;
+        }
 #pragma unroll
         for (int ss = 0; ss < 2; ss++) {
-            bf16x8 vt;
+            bf16x8 vt[2];
 #pragma unroll
-            for (int jj = 0; jj < 8; jj++) vt[jj] = (bf16_t)((float)vb[ss][jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
+            for (int c = 0; c < 2; c++)
 #pragma unroll
-            for (int mb = 0; mb < 8; mb++) acc[mb] = mfma_bf16(load_tr_bf16(sW, RS, 32 * ss, 16 * mb), vt, acc[mb]);
+                for (int jj = 0; jj < 8; jj++)
+                    vt[c][jj] = (bf16_t)((float)vb[c][ss][jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
+#pragma unroll
+            for (int mb = 0; mb < 8; mb++) {
+                const bf16x8 wk = load_tr_bf16(sW, RS, 32 * ss, 16 * mb);
+                acc[mb][0] = mfma_bf16(wk, vt[0], acc[mb][0]);
+                acc[mb][1] = mfma_bf16(wk, vt[1], acc[mb][1]);
+            }
+            sched_fence();
         }
         __syncthreads();
     }
@@ -1023,7 +1047,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void p
 #pragma unroll
         for (int mb = 0; mb < 8; mb++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) dst[(16 * mb + 4 * lg + i) * VD + HALF * y + 16 * w + lr] = acc[mb][i];
+            for (int c = 0; c < 2; c++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) dst[(16 * mb + 4 * lg + i) * VD + 32 * w + 16 * c + lr] = acc[mb][c][i];
     }
 }
 
@@ -1051,9 +1077,8 @@ __global__ __launch_bounds__(128) void readout_table_kernel(const float* readout
 }  // namespace
 
 void choose_segments(int BH, int N, int* P, int* L) {
-    // Two sweep workgroups (key / value halves) per segment: aim for about two
-    // workgroups per CU (256 CUs). CYFA_SEGMENT_CHUNKS=<L> fixes the chunks per
-    // segment (tests, tuning).
+    // One sweep workgroup per segment: aim for one workgroup per CU (256 CUs).
+    // CYFA_SEGMENT_CHUNKS=<L> fixes the chunks per segment (tests, tuning).
     int target = (256 + BH - 1) / BH;
     if (target < 1) target = 1;
     if (target > N) target = N;
@@ -1078,7 +1103,7 @@ WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V) {
     w.lam = 0;
     w.gam = align256(w.lam + BH * Tp * sizeof(float));
     w.seg = align256(w.gam + BH * Tp * sizeof(float));
-    const size_t seg_bytes = P > 1 ? BH * P * (size_t)(K * kSlots + kSlots * V) * sizeof(float) : 0;
+    const size_t seg_bytes = P > 1 ? BH * (P - 1) * (size_t)(K * kSlots + kSlots * V) * sizeof(float) : 0;
     w.seg_decay = align256(w.seg + seg_bytes);
     w.raw = align256(w.seg_decay + BH * P * sizeof(float));
     w.omega = align256(w.raw + 2 * BH * Tp * kSlots * 2);
@@ -1089,13 +1114,10 @@ WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V) {
 int launch_prefill(const PrefillParams& p, hipStream_t stream) {
     const int BH = p.B * p.H;
     hipLaunchKernelGGL(clock_kernel, dim3(BH), dim3(CLOCK_THREADS), 0, stream, p);
-    if (p.P > 1) {
-        hipLaunchKernelGGL(segment_state_kernel, dim3(BH * (p.P - 1), 4), dim3(512), 0, stream, p);
-        hipLaunchKernelGGL(carry_kernel, dim3(BH, SEG / 1024), dim3(256), 0, stream, p);
-    }
-    hipLaunchKernelGGL(pass1_kernel, dim3(sweep_grid(BH * p.P)), dim3(512), 0, stream, p);
+    if (p.P > 1) hipLaunchKernelGGL(segment_state_kernel, dim3(p.H, p.B, 2 * (p.P - 1)), dim3(512), 0, stream, p);
+    hipLaunchKernelGGL(pass1_kernel, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
     hipLaunchKernelGGL(readout_kernel, dim3(p.H * readout_groups(p.B, p.Tp, p.H)), dim3(512), 0, stream, p);
-    hipLaunchKernelGGL(pass2_kernel, dim3(sweep_grid(BH * p.P)), dim3(512), 0, stream, p);
+    hipLaunchKernelGGL(pass2_kernel, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
     return 0;
 }
 

@@ -111,7 +111,7 @@ CHUNK_CASES = [
     (1, 63, 1, True, None),
     (1, 130, 2, True, "1"),
     (1, 512, 2, True, "3"),      # segments of 3 chunks, last one shorter
-    (2, 512, 2, True, "100"),    # one segment: no carry kernels
+    (2, 512, 2, True, "100"),    # one segment: no segment-state kernel
     (16, 1024, 4, False, None),  # 64 sequences, 4 chunks per segment
 ]
 
