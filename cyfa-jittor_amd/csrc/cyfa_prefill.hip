@@ -41,6 +41,8 @@
 // ends with four consecutive output coordinates of one token.
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "cyfa_device.h"
 #include "cyfa_internal.h"
 
@@ -55,12 +57,31 @@ constexpr int SEG_K = KD * kSlots;  // key-state elements
 constexpr int SEG_V = kSlots * VD;  // value-state elements
 constexpr int SEG = SEG_K + SEG_V;
 
-// Row strides (16-bit elements) of the LDS tiles: 8 dwords past a multiple of
-// the 64 banks, so the rows a transpose read touches per 16-lane block fall on
-// disjoint banks.
-constexpr int RS = 128 + 16;  // 64 x 128 tiles and the 128 x 128 table
-constexpr int RF = 256 + 16;  // 64 x 256 tiles
-constexpr int TS = 64 + 8;    // 64 x 64 score tile
+// LDS tile layouts. Element (r, e) of a tile sits at Tile<LD, XA>::off(r, e):
+// rows LD elements apart, and in rows with bit 3 set the 16-byte unit index
+// e >> 3 is XORed with XA. The layouts were chosen by measuring
+// SQ_LDS_BANK_CONFLICT on gfx950 for each access pattern of the sweeps:
+//   padded rows (LD = 256 + 16, 128 + 16)  row reads and staging stores
+//                                          conflict-free; transpose reads 2-way
+//   LD = 256 + 32 / 128 + 32 with XA = 2   row reads, transpose reads and
+//                                          staging stores conflict-free
+template <int LD, int XA>
+struct Tile {
+    static constexpr int ld = LD;
+    static constexpr int bytes = 64 * LD * 2;  // 64 rows of 16-bit elements
+    static_assert(XA < 4, "the XOR stays inside a 32-element block");
+    // The XOR only touches the unit index within a 32-element block, so
+    // whole blocks (e & ~31) add as plain offsets.
+    __device__ static __forceinline__ int off(int r, int e) {
+        return r * LD + (e & ~31) + (((((e & 31) >> 3) ^ (XA * ((r >> 3) & 1)))) << 3) + (e & 7);
+    }
+};
+using TileQ = Tile<256 + 16, 0>;  // q_hat: row reads only
+using TileF = Tile<256 + 32, 2>;  // k_hat, v: row and transpose reads
+using TileW = Tile<128 + 32, 2>;  // w: row and transpose reads
+using TileO = Tile<128 + 16, 0>;  // slot weights: row reads only
+using TileP = Tile<64 + 8, 2>;    // 64 x 64 masked scores
+constexpr int RS = 128 + 16;      // readout table rows
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ size_t tok_index(const PrefillParams& p, int b, int t, int h) {
@@ -137,13 +158,18 @@ __device__ __forceinline__ Seq make_seq(const PrefillParams& p, int b, int h, in
 // Segment states in the workspace are kept in the register order of the
 // sweeps: the float4 that lane `lane` of wave w holds as accumulator block
 // (x, c) sits at float offset frag_offset(w, x, c, lane), so a wave loads or
-// stores a block as one contiguous 1 KiB run. Wave w, x = 0..7, c = 0..1 holds
-//   key state   S[128 (w >> 2) + 16 x + 4 lg + i][32 (w & 3) + 16 c + lr]
-//   value state S[16 x + 4 lg + i][32 w + 16 c + lr].
+// stores a block as one contiguous 1 KiB run. Wave w, x = 0..7, c = 0..1,
+// element i holds (see load_tr_perm for the row order)
+//   key state   S[128 (w >> 2) + state_row(x, lg, i)][32 (w & 3) + 16 c + lr]
+//   value state S[state_row(x, lg, i)][32 w + 16 c + lr].
 // The key state fills [0, SEG_K), the value state [SEG_K, SEG).
 __host__ __device__ constexpr int frag_offset(int w, int x, int c, int lane) {
     return (((w * 8 + x) * 2 + c) * 64 + lane) * 4;
 }
+
+// Row (within a 128-row half) of element i of state block x in a lane of row
+// group lg.
+__host__ __device__ constexpr int state_row(int x, int lg, int i) { return 32 * (x >> 1) + 8 * lg + 4 * (x & 1) + i; }
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
@@ -206,9 +232,7 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef s16x4 __attribute__((address_space(3))) lds_s16x4;
 
-__device__ __forceinline__ s16x8 load_tr(const void* X, int ld, int s0, int c0) {
-    const int l = threadIdx.x & 63, g = l >> 4, i = l & 15;
-    const short* p = reinterpret_cast<const short*>(X) + (s0 + 8 * g + (i >> 2)) * ld + c0 + 4 * (i & 3);
+__device__ __forceinline__ s16x8 tr_pair(const short* p, int ld) {
     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(const_cast<short*>(p)));
     const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(const_cast<short*>(p + 4 * ld)));
     s16x8 r;
@@ -217,18 +241,44 @@ __device__ __forceinline__ s16x8 load_tr(const void* X, int ld, int s0, int c0) 
     return r;
 }
 
-__device__ __forceinline__ bf16x8 load_tr_bf16(const bf16_t* X, int ld, int s0, int c0) {
-    return __builtin_bit_cast(bf16x8, load_tr(X, ld, s0, c0));
+// s0 is a multiple of 8, so rows r and r + 4 of a lane share the XOR of r >> 3.
+template <class L>
+__device__ __forceinline__ bf16x8 load_tr(const bf16_t* X, int s0, int c0) {
+    const int l = threadIdx.x & 63, g = l >> 4, i = l & 15;
+    const short* p = reinterpret_cast<const short*>(X) + L::off(s0 + 8 * g + (i >> 2), c0 + 4 * (i & 3));
+    return __builtin_bit_cast(bf16x8, tr_pair(p, L::ld));
+}
+
+// The same read with the columns of a 32-column block taken in the order
+//   lane (lr, lg) element j = X[s0 + 8 lg + j][c0 + 8 (lr >> 2) + 4 h + (lr & 3)]
+// (c0 a multiple of 32, h = 0, 1). As the A operand of the state update it
+// leaves the C rows 4 lg + i of state block 2 b + h holding key (or slot)
+// index 32 b + 8 lg + 4 h + i, so that a C-block pair is the A operand of the
+// product over those indices in their natural order: element j of lane lg is
+// index 32 b + 8 lg + j, and the other operand is a plain row fragment.
+template <class L>
+__device__ __forceinline__ bf16x8 load_tr_perm(const bf16_t* X, int s0, int c0, int h) {
+    const int l = threadIdx.x & 63, g = l >> 4, i = l & 15;
+    const short* p = reinterpret_cast<const short*>(X) + L::off(s0 + 8 * g + (i >> 2), c0 + 8 * (i & 3) + 4 * h);
+    return __builtin_bit_cast(bf16x8, tr_pair(p, L::ld));
 }
 
 __device__ __forceinline__ f16x8 load_tr_f16(const f16_t* X, int ld, int s0, int c0) {
-    return __builtin_bit_cast(f16x8, load_tr(X, ld, s0, c0));
+    const int l = threadIdx.x & 63, g = l >> 4, i = l & 15;
+    const short* p = reinterpret_cast<const short*>(X) + (s0 + 8 * g + (i >> 2)) * ld + c0 + 4 * (i & 3);
+    return __builtin_bit_cast(f16x8, tr_pair(p, ld));
 }
 
 // Row fragment: lane (lr, lg) gets X[r0 + lr][k0 + 8 lg .. + 8] (A operand, or
-// B operand of a product that contracts over X's columns).
+// B operand of a product that contracts over X's columns); k0 a multiple of 8.
+template <class L, typename V8 = bf16x8, typename T>
+__device__ __forceinline__ V8 load_row(const T* X, int r0, int k0) {
+    const int l = threadIdx.x & 63;
+    return *reinterpret_cast<const V8*>(X + L::off(r0 + (l & 15), k0 + 8 * (l >> 4)));
+}
+
 template <typename V8, typename T>
-__device__ __forceinline__ V8 load_row(const T* X, int ld, int r0, int k0) {
+__device__ __forceinline__ V8 load_row_ld(const T* X, int ld, int r0, int k0) {
     const int l = threadIdx.x & 63;
     return *reinterpret_cast<const V8*>(X + (r0 + (l & 15)) * ld + k0 + 8 * (l >> 4));
 }
@@ -245,11 +295,12 @@ __device__ __forceinline__ void issue_rows(const Seq& sq, rsrc_t x, int T, int t
 }
 
 // x_hat = bf16(x rsqrt(mean x^2 + eps) w) over the full row (ops/qk_norm.py:64-107,
-// 206-233), stored into dst [64][RF] (zero past T). wn is the norm weight in
+// 206-233), stored into the tile dst (zero past T). wn is the norm weight in
 // LDS. The sum of squares uses the bf16 dot product (two elements per
 // instruction, fp32 accumulation) and the 8 threads of a row meet by DPP.
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
+template <class L>
 __device__ __forceinline__ void norm_store_rows(const PrefillParams& p, int t0, const bf16x8 raw[4], const float* wn,
                                                 float eps, bf16_t* dst) {
     const int r = threadIdx.x >> 3, c = threadIdx.x & 7;
@@ -272,12 +323,13 @@ __device__ __forceinline__ void norm_store_rows(const PrefillParams& p, int t0, 
         bf16x8 o;
 #pragma unroll
         for (int j = 0; j < 8; j++) o[j] = (bf16_t)((float)raw[q][j] * (rs * wv[j]));
-        *reinterpret_cast<bf16x8*>(dst + r * RF + col) = o;
+        *reinterpret_cast<bf16x8*>(dst + L::off(r, col)) = o;
     }
 }
 
-// Store 64 x 256 rows held with the issue_rows mapping into dst [64][RF]; rows
+// Store 64 x 256 rows held with the issue_rows mapping into the tile dst; rows
 // at or past `valid` are zeroed.
+template <class L>
 __device__ __forceinline__ void store_rows(const bf16x8 raw[4], int valid, bf16_t* dst) {
     const int r = threadIdx.x >> 3, c = threadIdx.x & 7;
 #pragma unroll
@@ -287,7 +339,7 @@ __device__ __forceinline__ void store_rows(const bf16x8 raw[4], int valid, bf16_
 #pragma unroll
             for (int j = 0; j < 8; j++) o[j] = (bf16_t)0.f;
         }
-        *reinterpret_cast<bf16x8*>(dst + r * RF + 64 * q + 8 * c) = o;
+        *reinterpret_cast<bf16x8*>(dst + L::off(r, 64 * q + 8 * c)) = o;
     }
 }
 
@@ -299,8 +351,8 @@ __device__ __forceinline__ void issue_omega(rsrc_t om_rows, int t0, bf16x8 om[2]
     for (int it = 0; it < 2; it++) om[it] = ld_b128(om_rows, off + 128 * it);
 }
 
-// Store 64 x 128 rows held with that mapping into dst [64][RS]; rows at or past
-// `valid` are zeroed.
+// Store 64 x 128 rows held with that mapping into the TileO tile dst; rows at
+// or past `valid` are zeroed.
 __device__ __forceinline__ void store_half_rows(const bf16x8 raw[2], int valid, bf16_t* dst) {
     const int r = threadIdx.x >> 3, c = threadIdx.x & 7;
 #pragma unroll
@@ -310,7 +362,7 @@ __device__ __forceinline__ void store_half_rows(const bf16x8 raw[2], int valid, 
 #pragma unroll
             for (int j = 0; j < 8; j++) o[j] = (bf16_t)0.f;
         }
-        *reinterpret_cast<bf16x8*>(dst + r * RS + 8 * c + 64 * it) = o;
+        *reinterpret_cast<bf16x8*>(dst + TileO::off(r, 8 * c + 64 * it)) = o;
     }
 }
 
@@ -319,6 +371,7 @@ __device__ __forceinline__ void store_half_rows(const bf16x8 raw[2], int valid, 
 // The hardware gives (cos, sin) of pair 8 w and of pair 1; the next pairs
 // follow by complex multiplication, i.e. rotation by theta (seven steps add
 // about 1e-6 to a result rounded to bf16).
+template <class L>
 __device__ __forceinline__ void store_write_tile(const GateRegs& gr, int valid, bf16_t* dst) {
     const int lane = threadIdx.x & 63, w = wave_id();
     const float beta = lane < valid ? gr.beta : 0.f;
@@ -335,8 +388,8 @@ __device__ __forceinline__ void store_write_tile(const GateRegs& gr, int valid, 
         sn = sn * c1 + cs * s1;
         cs = cn;
     }
-    *reinterpret_cast<bf16x8*>(dst + lane * RS + 16 * w) = o[0];
-    *reinterpret_cast<bf16x8*>(dst + lane * RS + 16 * w + 8) = o[1];
+    *reinterpret_cast<bf16x8*>(dst + L::off(lane, 16 * w)) = o[0];
+    *reinterpret_cast<bf16x8*>(dst + L::off(lane, 16 * w + 8)) = o[1];
 }
 
 // The 10 causal 16 x 16 score blocks (query block tb >= key block sb): wave w
@@ -347,13 +400,15 @@ __device__ __forceinline__ void score_block(int blk, int& tb, int& sb) {
 }
 
 // Block blk (query block tb >= key block sb) of the masked, decayed scores of
-// a query tile X and key tile Y (64 rows ld apart, 128-wide contraction), into sP:
+// a query tile X and key tile Y (columns xc / yc onward, 128-wide
+// contraction), into the TileP tile sP:
 // P[t][s] = bf16(2^(G_t - G_s) c x_t . y_s) for s <= t, else 0 (ops/chunk_o.py:240-250),
 // c = 2^log2_scale the output scale of the pass (exact for the default
 // scale 1/16: scaling a bf16 value by a power of two commutes with rounding).
 // The block is computed transposed (C rows = keys, columns = queries), so a
 // lane holds four consecutive keys of one query and writes them in one store.
-__device__ __forceinline__ void score_tile(const bf16_t* X, const bf16_t* Y, int ld, int blk, const float* sGam,
+template <class LX, class LY>
+__device__ __forceinline__ void score_tile(const bf16_t* X, int xc, const bf16_t* Y, int yc, int blk, const float* sGam,
                                            float log2_scale, bf16_t* sP) {
     const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
     int tb, sb;
@@ -361,8 +416,8 @@ __device__ __forceinline__ void score_tile(const bf16_t* X, const bf16_t* Y, int
     bf16x8 a[4], b[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
-        a[ks] = load_row<bf16x8>(Y, ld, 16 * sb, 32 * ks);
-        b[ks] = load_row<bf16x8>(X, ld, 16 * tb, 32 * ks);
+        a[ks] = load_row<LY>(Y, 16 * sb, yc + 32 * ks);
+        b[ks] = load_row<LX>(X, 16 * tb, xc + 32 * ks);
     }
     f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -377,26 +432,11 @@ __device__ __forceinline__ void score_tile(const bf16_t* X, const bf16_t* Y, int
         const float v = sc[i] * fast_exp2(gt - gsv[i]);
         o[i] = (bf16_t)(s0 + i <= t ? v : 0.f);
     }
-    *reinterpret_cast<bf16x4*>(sP + t * TS + s0) = o;
+    *reinterpret_cast<bf16x4*>(sP + TileP::off(t, s0)) = o;
 }
 
 __device__ __forceinline__ void zero_scores(bf16_t* sP, int tiles) {
-    for (int idx = threadIdx.x; idx < tiles * 64 * TS / 2; idx += blockDim.x) reinterpret_cast<uint32_t*>(sP)[idx] = 0u;
-}
-
-__device__ __forceinline__ bf16x8 cat4(const bf16x4& lo, const bf16x4& hi) {
-    bf16x8 r;
-    r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
-    r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
-    return r;
-}
-
-// Row fragment in the k order of a C-block pair: elements row[4 lg .. + 4] and
-// row[16 + 4 lg .. + 4] of a 32-wide k step.
-__device__ __forceinline__ bf16x8 load_row_perm(const bf16_t* row_ks, int lg) {
-    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row_ks + 4 * lg);
-    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row_ks + 16 + 4 * lg);
-    return cat4(lo, hi);
+    for (int idx = threadIdx.x; idx < tiles * TileP::bytes / 4; idx += blockDim.x) reinterpret_cast<uint32_t*>(sP)[idx] = 0u;
 }
 
 // A C-block pair of the fp32 state as a bf16 operand (the reference emits the
@@ -487,52 +527,52 @@ __global__ __launch_bounds__(CLOCK_THREADS) void clock_kernel(PrefillParams p) {
 // 2. Segment-local end states from a zero start. grid = (H, B, 2 (P-1)), 512
 // threads, blockIdx.z = 2 j + part; state blocks as in frag_offset. part 0: key state, rows 128 y ..,
 // y = w >> 2, columns 32 (w & 3) ..; part 1: value state, columns 32 w ...
-constexpr int SG_A = 0;                   // bf16 [64][RF]: k_hat (key) or v (value)
-constexpr int SG_B = SG_A + 64 * RF * 2;  // bf16 [64][RS]: w
-constexpr int SG_G = SG_B + 64 * RS * 2;  // f32 [5][64] gates
-constexpr int SG_NW = SG_G + 5 * 64 * 4;  // f32 [256] k norm weight
+constexpr int SG_A = 0;                     // k_hat (key) or v (value), TileF
+constexpr int SG_B = SG_A + TileF::bytes;  // w, TileW
+constexpr int SG_G = SG_B + TileW::bytes;  // f32 [5][64] gates
+constexpr int SG_NW = SG_G + 5 * 64 * 4;   // f32 [256] k norm weight
 constexpr int SG_LDS = SG_NW + KD * 4;
 static_assert(2 * SG_LDS <= 160 * 1024, "two segment-state workgroups must fit in one CU's LDS");
 
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void segment_state_kernel(PrefillParams p) {
-    __shared__ __align__(16) unsigned char smem[SG_LDS];
+// key: S += k_hat^T w', A = k_hat columns (this wave's half), B = w columns 32 (w & 3) ..;
+// value: S += w^T v', A = w columns, B = v columns 32 w ...
+template <bool KEY>
+__device__ __forceinline__ void segment_state_body(const PrefillParams& p, int bh, int j, int b, int h,
+                                                   unsigned char* smem) {
     bf16_t* sA = reinterpret_cast<bf16_t*>(smem + SG_A);
     bf16_t* sB = reinterpret_cast<bf16_t*>(smem + SG_B);
     float* sLam = reinterpret_cast<float*>(smem + SG_G);
     float* sBeta = sLam + 64;
     float* sGam = sBeta + 64;
     float* sNw = reinterpret_cast<float*>(smem + SG_NW);
-    const SegCoord cd = seg_coord(p.H, blockIdx.z >> 1);
-    const int bh = cd.bh, j = cd.j, b = cd.b, h = cd.h, key = (blockIdx.z & 1) == 0;
+    using LA = typename std::conditional<KEY, TileF, TileW>::type;
+    using LB = typename std::conditional<KEY, TileW, TileF>::type;
+    const bf16_t* sArow = KEY ? sA : sB;
+    const bf16_t* sBcol = KEY ? sB : sA;
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), lg = lane >> 4;
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
-    // key: A rows of the update are k_hat columns 128 y + 16 x, B = w columns 32 (w & 3) + 16 c;
-    // value: A rows are w columns 16 x, B = v columns 32 w + 16 c.
-    const int a_col = key ? HALF * (w >> 2) : 0, a_ld = key ? RF : RS;
-    const int b_col = key ? 32 * (w & 3) : 32 * w;
-    const bf16_t* sArow = key ? sA : sB;
-    const bf16_t* sBcol = key ? sB : sA;
-    const int b_ld = key ? RS : RF;
+    const int a_col = KEY ? HALF * (w >> 2) : 0;
+    const int b_col = KEY ? 32 * (w & 3) : 32 * w;
     f32x4 acc[8][2];
 #pragma unroll
     for (int x = 0; x < 8; x++) acc[x][0] = acc[x][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     const Seq sq = make_seq(p, b, h, bh);
     GateRegs gr = issue_gates(sq, p.T, n0 * 64);
     bf16x8 raw[4];
-    issue_rows(sq, key ? sq.k : sq.v, p.T, n0 * 64, raw);
-    if (key && tid < KD) sNw[tid] = p.k_w[tid];
+    issue_rows(sq, KEY ? sq.k : sq.v, p.T, n0 * 64, raw);
+    if (KEY && tid < KD) sNw[tid] = p.k_w[tid];
     float logdecay = 0.f;
     __syncthreads();
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
         commit_gates(p, t0, gr, sLam, sBeta, sGam);
-        store_write_tile(gr, p.T - t0, sB);
-        if (key)
-            norm_store_rows(p, t0, raw, sNw, p.k_eps, sA);
+        store_write_tile<TileW>(gr, p.T - t0, sB);
+        if (KEY)
+            norm_store_rows<TileF>(p, t0, raw, sNw, p.k_eps, sA);
         else
-            store_rows(raw, p.T - t0, sA);
+            store_rows<TileF>(raw, p.T - t0, sA);
         if (n + 1 < n1) {
-            issue_rows(sq, key ? sq.k : sq.v, p.T, t0 + 64, raw);
+            issue_rows(sq, KEY ? sq.k : sq.v, p.T, t0 + 64, raw);
             gr = issue_gates(sq, p.T, t0 + 64);
         }
         __syncthreads();
@@ -549,13 +589,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
             bf16x8 bt[2];
 #pragma unroll
             for (int c = 0; c < 2; c++) {
-                const bf16x8 f = load_tr_bf16(sBcol, b_ld, 32 * ss, b_col + 16 * c);
+                const bf16x8 f = load_tr<LB>(sBcol, 32 * ss, b_col + 16 * c);
 #pragma unroll
                 for (int jj = 0; jj < 8; jj++) bt[c][jj] = (bf16_t)((float)f[jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
             }
+            sched_fence();
 #pragma unroll
             for (int x = 0; x < 8; x++) {
-                const bf16x8 af = load_tr_bf16(sArow, a_ld, 32 * ss, a_col + 16 * x);
+                const bf16x8 af = load_tr_perm<LA>(sArow, 32 * ss, a_col + 32 * (x >> 1), x & 1);
                 acc[x][0] = mfma_bf16(af, bt[0], acc[x][0]);
                 acc[x][1] = mfma_bf16(af, bt[1], acc[x][1]);
                 if (x & 1) sched_fence();
@@ -563,12 +604,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
         }
         __syncthreads();
     }
-    float* out = p.seg + ((size_t)bh * (p.P - 1) + j) * SEG + (key ? 0 : SEG_K);
+    float* out = p.seg + ((size_t)bh * (p.P - 1) + j) * SEG + (KEY ? 0 : SEG_K);
 #pragma unroll
     for (int x = 0; x < 8; x++)
 #pragma unroll
         for (int c = 0; c < 2; c++) *reinterpret_cast<f32x4*>(out + frag_offset(w, x, c, lane)) = acc[x][c];
-    if (key && tid == 0) p.seg_decay[bh * p.P + j] = exp2f(logdecay);
+    if (KEY && tid == 0) p.seg_decay[bh * p.P + j] = exp2f(logdecay);
+}
+
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void segment_state_kernel(PrefillParams p) {
+    __shared__ __align__(16) unsigned char smem[SG_LDS];
+    const SegCoord cd = seg_coord(p.H, blockIdx.z >> 1);
+    if ((blockIdx.z & 1) == 0)
+        segment_state_body<true>(p, cd.bh, cd.j, cd.b, cd.h, smem);
+    else
+        segment_state_body<false>(p, cd.bh, cd.j, cd.b, cd.h, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -616,14 +666,14 @@ __device__ __forceinline__ void load_start_state(const PrefillParams& p, int bh,
 // ---------------------------------------------------------------------------
 // 4. Pass 1 (key state), one segment per workgroup. grid = (H, B, P), 512 threads.
 // Wave w works on key half y = w >> 2 and state columns [32 mq, 32 mq + 32),
-// mq = w & 3: acc[kb][c] = S[128 y + 16 kb + 4 lg + i][32 mq + 16 c + lr], and
-// the same 32 output coordinates of half y:
+// mq = w & 3: acc[kb][c] = S[128 y + state_row(kb, lg, i)][32 mq + 16 c + lr],
+// and the same 32 output coordinates of half y:
 // out[tb][c] = raw_y^T[32 mq + 16 c + 4 lg + i][16 tb + lr].
-constexpr int P1_Q = 0;                       // bf16 [64][RF] q_hat
-constexpr int P1_K = P1_Q + 64 * RF * 2;      // bf16 [64][RF] k_hat
-constexpr int P1_W = P1_K + 64 * RF * 2;      // bf16 [64][RS] w
-constexpr int P1_P = P1_W + 64 * RS * 2;      // bf16 [2][64][TS] masked scores of each half
-constexpr int P1_G = P1_P + 2 * 64 * TS * 2;  // f32 [5][64] gates
+constexpr int P1_Q = 0;                        // q_hat, TileQ
+constexpr int P1_K = P1_Q + TileQ::bytes;      // k_hat, TileF
+constexpr int P1_W = P1_K + TileF::bytes;      // w, TileW
+constexpr int P1_P = P1_W + TileW::bytes;      // masked scores of each half, 2 x TileP
+constexpr int P1_G = P1_P + 2 * TileP::bytes;  // f32 [5][64] gates
 constexpr int P1_NW = P1_G + 5 * 64 * 4;      // f32 [2][256] q and k norm weights
 constexpr int P1_LDS = P1_NW + 2 * KD * 4;
 static_assert(P1_LDS <= 160 * 1024, "pass-1 workgroup must fit in one CU's LDS");
@@ -651,10 +701,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         sKw[tid] = p.k_w[tid];
     }
     zero_scores(sP, 2);  // the two blocks above the diagonal that the intra product reads stay zero
-    bf16_t* sPy = sP + y * 64 * TS;
+    bf16_t* sPy = sP + y * (TileP::bytes / 2);
     f32x4 acc[8][2];
     load_start_state(p, bh, j, 0, p.h0_k ? p.h0_k + (size_t)bh * SEG_K : nullptr,
-                     [&](int kb, int c, int i) { return (HALF * y + 16 * kb + 4 * lg + i) * kSlots + 32 * mq + 16 * c + lr; },
+                     [&](int kb, int c, int i) { return (HALF * y + state_row(kb, lg, i)) * kSlots + 32 * mq + 16 * c + lr; },
                      acc);
     const Seq sq = make_seq(p, b, h, bh);
     const rsrc_t rraw = make_rsrc(p.raw + ((size_t)y * p.B * p.H + bh) * p.Tp * kSlots, (size_t)p.Tp * kSlots * 2);
@@ -668,9 +718,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
         commit_gates(p, t0, gr, sLam, sBeta, sGam);
-        store_write_tile(gr, p.T - t0, sW);
-        norm_store_rows(p, t0, qraw, sQw, p.q_eps, sQ);
-        norm_store_rows(p, t0, kraw, sKw, p.k_eps, sK);
+        store_write_tile<TileW>(gr, p.T - t0, sW);
+        norm_store_rows<TileQ>(p, t0, qraw, sQw, p.q_eps, sQ);
+        norm_store_rows<TileF>(p, t0, kraw, sKw, p.k_eps, sK);
         sched_fence();  // the next chunk's loads reuse these registers
         if (n + 1 < n1) {
             issue_rows(sq, sq.q, p.T, t0 + 64, qraw);
@@ -680,9 +730,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         __syncthreads();
 
         // Masked, decayed scores of this half's key slice: blocks mq, mq + 4 (and mq + 8).
-        score_tile(sQ + HALF * y, sK + HALF * y, RF, mq, sGam, log2_scale, sPy);
-        score_tile(sQ + HALF * y, sK + HALF * y, RF, mq + 4, sGam, log2_scale, sPy);
-        if (mq < 2) score_tile(sQ + HALF * y, sK + HALF * y, RF, mq + 8, sGam, log2_scale, sPy);
+        score_tile<TileQ, TileF>(sQ, HALF * y, sK, HALF * y, mq, sGam, log2_scale, sPy);
+        score_tile<TileQ, TileF>(sQ, HALF * y, sK, HALF * y, mq + 4, sGam, log2_scale, sPy);
+        if (mq < 2) score_tile<TileQ, TileF>(sQ, HALF * y, sK, HALF * y, mq + 8, sGam, log2_scale, sPy);
         // raw_y^T = 2^G_t S_n^T q_t over this half's key rows.
         f32x4 out[4][2];
 #pragma unroll
@@ -693,7 +743,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
             const bf16x8 a1 = state_frag(acc[2 * ks][1], acc[2 * ks + 1][1]);
 #pragma unroll
             for (int tb = 0; tb < 4; tb++) {
-                const bf16x8 bq = load_row_perm(sQ + (16 * tb + lr) * RF + HALF * y + 32 * ks, lg);
+                const bf16x8 bq = load_row<TileQ>(sQ, 16 * tb, HALF * y + 32 * ks);
                 out[tb][0] = mfma_bf16(a0, bq, out[tb][0]);
                 out[tb][1] = mfma_bf16(a1, bq, out[tb][1]);
             }
@@ -713,12 +763,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
         for (int c = 0; c < 2; c++)
 #pragma unroll
-            for (int ss = 0; ss < 2; ss++) wf[c][ss] = load_tr_bf16(sW, RS, 32 * ss, 32 * mq + 16 * c);
+            for (int ss = 0; ss < 2; ss++) wf[c][ss] = load_tr<TileW>(sW, 32 * ss, 32 * mq + 16 * c);
 #pragma unroll
         for (int tb = 0; tb < 4; tb++)
 #pragma unroll
             for (int ss = 0; ss <= (tb >> 1); ss++) {
-                const bf16x8 pf = load_row<bf16x8>(sPy, TS, 16 * tb, 32 * ss);
+                const bf16x8 pf = load_row<TileP>(sPy, 16 * tb, 32 * ss);
                 out[tb][0] = mfma_bf16(wf[0][ss], pf, out[tb][0]);
                 out[tb][1] = mfma_bf16(wf[1][ss], pf, out[tb][1]);
             }
@@ -744,7 +794,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
                     wt[c][jj] = (bf16_t)((float)wf[c][ss][jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
 #pragma unroll
             for (int kb = 0; kb < 8; kb++) {
-                const bf16x8 kf = load_tr_bf16(sK, RF, 32 * ss, HALF * y + 16 * kb);
+                const bf16x8 kf = load_tr_perm<TileF>(sK, 32 * ss, HALF * y + 32 * (kb >> 1), kb & 1);
                 acc[kb][0] = mfma_bf16(kf, wt[0], acc[kb][0]);
                 acc[kb][1] = mfma_bf16(kf, wt[1], acc[kb][1]);
             }
@@ -761,7 +811,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
             for (int c = 0; c < 2; c++)
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    dst[(HALF * y + 16 * kb + 4 * lg + i) * kSlots + 32 * mq + 16 * c + lr] = acc[kb][c][i];
+                    dst[(HALF * y + state_row(kb, lg, i)) * kSlots + 32 * mq + 16 * c + lr] = acc[kb][c][i];
     }
 }
 
@@ -850,7 +900,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void r
         for (int ks = 0; ks < 4; ks++) {
 #pragma unroll
             for (int rb8 = 0; rb8 < 8; rb8++)
-                L[rb8] = mfma_f16(load_row<f16x8>(sTA, RS, 16 * rb8, 32 * ks), zf[ks], L[rb8]);
+                L[rb8] = mfma_f16(load_row_ld<f16x8>(sTA, RS, 16 * rb8, 32 * ks), zf[ks], L[rb8]);
             sched_fence();
         }
         if (lg == 3) L[7][3] = -INFINITY;  // slot r = 127 is not active
@@ -918,13 +968,13 @@ int readout_groups(int B, int Tp, int H) {
 // ---------------------------------------------------------------------------
 // 6. Pass 2 (value state), one segment per workgroup. grid = (H, B, P), 512
 // threads. Wave w owns value columns [32 w, 32 w + 32):
-// acc[mb][c] = S[16 mb + 4 lg + i][32 w + 16 c + lr], and the same 32 output
+// acc[mb][c] = S[state_row(mb, lg, i)][32 w + 16 c + lr], and the same 32 output
 // coordinates: out[tb][c] = o^T[32 w + 16 c + 4 lg + i][16 tb + lr].
-constexpr int P2_OM = 0;                   // bf16 [64][RS] slot weights (query)
-constexpr int P2_W = P2_OM + 64 * RS * 2;  // bf16 [64][RS] w (key)
-constexpr int P2_V = P2_W + 64 * RS * 2;   // bf16 [64][RF] v
-constexpr int P2_P = P2_V + 64 * RF * 2;   // bf16 [64][TS] masked scores
-constexpr int P2_G = P2_P + 64 * TS * 2;   // f32 [5][64] gates
+constexpr int P2_OM = 0;                     // slot weights (query), TileO
+constexpr int P2_W = P2_OM + TileO::bytes;   // w (key), TileW
+constexpr int P2_V = P2_W + TileW::bytes;    // v, TileF
+constexpr int P2_P = P2_V + TileF::bytes;    // masked scores, TileP
+constexpr int P2_G = P2_P + TileP::bytes;    // f32 [5][64] gates
 constexpr int P2_LDS = P2_G + 5 * 64 * 4;
 static_assert(P2_LDS <= 160 * 1024, "pass-2 workgroup must fit in one CU's LDS");
 
@@ -945,7 +995,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     zero_scores(sP, 1);
     f32x4 acc[8][2];
     load_start_state(p, bh, j, SEG_K, p.h0_v ? p.h0_v + (size_t)bh * SEG_V : nullptr,
-                     [&](int mb, int c, int i) { return (16 * mb + 4 * lg + i) * VD + 32 * w + 16 * c + lr; }, acc);
+                     [&](int mb, int c, int i) { return state_row(mb, lg, i) * VD + 32 * w + 16 * c + lr; }, acc);
     const Seq sq = make_seq(p, b, h, bh);
     const rsrc_t rom = make_rsrc(p.omega + (size_t)bh * p.Tp * kSlots, (size_t)p.Tp * kSlots * 2);
     const uint32_t o_lane = (uint32_t)lr * sq.row16 + 2 * (32 * w + 4 * lg);
@@ -957,9 +1007,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
         commit_gates(p, t0, gr, sLam, sBeta, sGam);
-        store_write_tile(gr, p.T - t0, sW);
+        store_write_tile<TileW>(gr, p.T - t0, sW);
         store_half_rows(om, 64, sOm);
-        store_rows(vraw, p.T - t0, sV);
+        store_rows<TileF>(vraw, p.T - t0, sV);
         sched_fence();
         if (n + 1 < n1) {
             issue_rows(sq, sq.v, p.T, t0 + 64, vraw);
@@ -968,8 +1018,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         }
         __syncthreads();
 
-        score_tile(sOm, sW, RS, w, sGam, 0.f, sP);
-        if (w < 2) score_tile(sOm, sW, RS, w + 8, sGam, 0.f, sP);
+        score_tile<TileO, TileW>(sOm, 0, sW, 0, w, sGam, 0.f, sP);
+        if (w < 2) score_tile<TileO, TileW>(sOm, 0, sW, 0, w + 8, sGam, 0.f, sP);
         // o^T = 2^G_t S_n^T weights_t.
         f32x4 out[4][2];
 #pragma unroll
@@ -980,7 +1030,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
             const bf16x8 a1 = state_frag(acc[2 * ks][1], acc[2 * ks + 1][1]);
 #pragma unroll
             for (int tb = 0; tb < 4; tb++) {
-                const bf16x8 bo = load_row_perm(sOm + (16 * tb + lr) * RS + 32 * ks, lg);
+                const bf16x8 bo = load_row<TileO>(sOm, 16 * tb, 32 * ks);
                 out[tb][0] = mfma_bf16(a0, bo, out[tb][0]);
                 out[tb][1] = mfma_bf16(a1, bo, out[tb][1]);
             }
@@ -999,12 +1049,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
         for (int c = 0; c < 2; c++)
 #pragma unroll
-            for (int ss = 0; ss < 2; ss++) vb[c][ss] = load_tr_bf16(sV, RF, 32 * ss, 32 * w + 16 * c);
+            for (int ss = 0; ss < 2; ss++) vb[c][ss] = load_tr<TileF>(sV, 32 * ss, 32 * w + 16 * c);
 #pragma unroll
         for (int tb = 0; tb < 4; tb++)
 #pragma unroll
             for (int ss = 0; ss <= (tb >> 1); ss++) {
-                const bf16x8 pf = load_row<bf16x8>(sP, TS, 16 * tb, 32 * ss);
+                const bf16x8 pf = load_row<TileP>(sP, 16 * tb, 32 * ss);
                 out[tb][0] = mfma_bf16(vb[0][ss], pf, out[tb][0]);
                 out[tb][1] = mfma_bf16(vb[1][ss], pf, out[tb][1]);
             }
@@ -1033,7 +1083,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
                     vt[c][jj] = (bf16_t)((float)vb[c][ss][jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
 #pragma unroll
             for (int mb = 0; mb < 8; mb++) {
-                const bf16x8 wk = load_tr_bf16(sW, RS, 32 * ss, 16 * mb);
+                const bf16x8 wk = load_tr_perm<TileW>(sW, 32 * ss, 32 * (mb >> 1), mb & 1);
                 acc[mb][0] = mfma_bf16(wk, vt[0], acc[mb][0]);
                 acc[mb][1] = mfma_bf16(wk, vt[1], acc[mb][1]);
             }
@@ -1049,7 +1099,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
             for (int c = 0; c < 2; c++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) dst[(16 * mb + 4 * lg + i) * VD + 32 * w + 16 * c + lr] = acc[mb][c][i];
+                for (int i = 0; i < 4; i++) dst[state_row(mb, lg, i) * VD + 32 * w + 16 * c + lr] = acc[mb][c][i];
     }
 }
 
