@@ -157,7 +157,8 @@ int cyfa_chunk_fwd(const CyfaChunkArgs* a, void* hip_stream) {
     char* base = (char*)a->workspace;
     p.lam = (float*)(base + ws.lam);
     p.gam = (float*)(base + ws.gam);
-    p.seg = (float*)(base + ws.seg);
+    p.seg = (_Float16*)(base + ws.seg);
+    p.seg_exp = (int*)(base + ws.seg_exp);
     p.seg_decay = (float*)(base + ws.seg_decay);
     p.raw = (__bf16*)(base + ws.raw);
     p.omega = (__bf16*)(base + ws.omega);

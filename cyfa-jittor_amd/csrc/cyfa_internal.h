@@ -36,7 +36,9 @@ struct PrefillParams {
     // workspace
     float* lam;        // [B*H, Tp] reduced clock per token, (lam mod 127) / 127
     float* gam;        // [B*H, Tp] in-chunk inclusive scan of g, log2 units
-    float* seg;        // [B*H, P-1, K*128 + 128*V] segment-local end states (register order)
+    _Float16* seg;     // [B*H, P-1, K*128 + 128*V] segment-local end states (register order),
+                       // each wave's block scaled by 2^-seg_exp
+    int* seg_exp;      // [B*H, P-1, 2, 8] power-of-two exponent per (key / value part, wave)
     float* seg_decay;  // [B*H, P] product of alpha over each segment
     __bf16* raw;       // [2, B*H, Tp, 128] pass-1 output of each 128-wide key half
     __bf16* omega;     // [B*H, Tp, 128] slot weights between the two passes
@@ -67,7 +69,7 @@ struct ConvParams {
 };
 
 struct WorkspaceLayout {
-    size_t lam, gam, seg, seg_decay, raw, omega, total;
+    size_t lam, gam, seg, seg_exp, seg_decay, raw, omega, total;
 };
 
 void choose_segments(int BH, int N, int* P, int* L);

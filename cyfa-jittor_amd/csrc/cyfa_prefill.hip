@@ -156,9 +156,9 @@ __device__ __forceinline__ Seq make_seq(const PrefillParams& p, int b, int h, in
 }
 
 // Segment states in the workspace are kept in the register order of the
-// sweeps: the float4 that lane `lane` of wave w holds as accumulator block
-// (x, c) sits at float offset frag_offset(w, x, c, lane), so a wave loads or
-// stores a block as one contiguous 1 KiB run. Wave w, x = 0..7, c = 0..1,
+// sweeps: the four values that lane `lane` of wave w holds as accumulator
+// block (x, c) sit at element offset frag_offset(w, x, c, lane), so a wave
+// loads or stores a block as one contiguous run. Wave w, x = 0..7, c = 0..1,
 // element i holds (see load_tr_perm for the row order)
 //   key state   S[128 (w >> 2) + state_row(x, lg, i)][32 (w & 3) + 16 c + lr]
 //   value state S[state_row(x, lg, i)][32 w + 16 c + lr].
@@ -207,18 +207,40 @@ __device__ __forceinline__ float chunk_last_gam(const GateRegs& r) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r.gam), 63));
 }
 
+// inv: 1 / sigma of the state after this chunk's update (see StateScale).
 __device__ __forceinline__ void commit_gates(const PrefillParams& p, int t0, const GateRegs& r, float* sLam,
-                                             float* sBeta, float* sGam) {
+                                             float* sBeta, float* sGam, float inv) {
     const int tid = threadIdx.x;
     if (tid < 64) {
         const float last = chunk_last_gam(r);
         sGam[tid] = r.gam;
         sBeta[tid] = t0 + tid < p.T ? r.beta : 0.f;
         sLam[tid] = r.lamr;
-        sGam[64 + tid] = fast_exp2(r.gam);          // 2^G_t
-        sGam[128 + tid] = fast_exp2(last - r.gam);  // 2^(G_last - G_t)
+        sGam[64 + tid] = fast_exp2(r.gam);                // 2^G_t
+        sGam[128 + tid] = fast_exp2(last - r.gam) * inv;  // 2^(G_last - G_t) / sigma'
     }
 }
+
+// The sweeps hold the fp32 state as S = sigma * acc with sigma uniform over the
+// workgroup. The chunk update S' = 2^G_last S + A^T bf16(2^(G_last - G_s) B)
+// becomes acc' = acc + A^T bf16(2^(G_last - G_s) / sigma' B) with
+// sigma' = 2^G_last sigma: the decay costs one scalar product per chunk instead
+// of a multiply per accumulator, and sigma folds into the per-token factors
+// that already scale the update's values and the inter-chunk output. When
+// sigma' would fall below 2^-64 it is multiplied into acc instead and reset to
+// 1 (so |acc| stays within 2^64 |S|).
+struct StateScale {
+    float sig = 1.f;   // sigma of the state the chunk starts from
+    float next = 1.f;  // sigma after the chunk's update
+    float fold = 1.f;  // multiplied into acc before the update (1 unless renormalising)
+    __device__ __forceinline__ void begin_chunk(float last_gam) {
+        const float s = sig * fast_exp2(last_gam);
+        const bool renorm = s < 0x1p-64f;
+        fold = renorm ? s : 1.f;
+        next = renorm ? 1.f : s;
+    }
+    __device__ __forceinline__ float inv() const { return 1.f / next; }
+};
 
 // LDS transpose read (ds_read_b64_tr_b16). Within each 16-lane block of a
 // wave, source lane i supplies the address of four consecutive 16-bit
@@ -312,18 +334,22 @@ __device__ __forceinline__ void norm_store_rows(const PrefillParams& p, int t0, 
             const bf16x2 x2 = {raw[q][2 * j], raw[q][2 * j + 1]};
             ss = __builtin_amdgcn_fdot2_f32_bf16(x2, x2, ss, false);
         }
+    float4 wq[4][2];  // all weight reads in flight at once
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        wq[q][0] = *reinterpret_cast<const float4*>(wn + 64 * q + 8 * c);
+        wq[q][1] = *reinterpret_cast<const float4*>(wn + 64 * q + 8 * c + 4);
+    }
     ss = octet_sum(ss);
     const float rs = t0 + r < p.T ? rsqrtf(ss * (1.f / KD) + eps) : 0.f;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-        const int col = 64 * q + 8 * c;
-        const float4 w0 = *reinterpret_cast<const float4*>(wn + col);
-        const float4 w1 = *reinterpret_cast<const float4*>(wn + col + 4);
-        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        const float wv[8] = {wq[q][0].x, wq[q][0].y, wq[q][0].z, wq[q][0].w,
+                             wq[q][1].x, wq[q][1].y, wq[q][1].z, wq[q][1].w};
         bf16x8 o;
 #pragma unroll
         for (int j = 0; j < 8; j++) o[j] = (bf16_t)((float)raw[q][j] * (rs * wv[j]));
-        *reinterpret_cast<bf16x8*>(dst + L::off(r, col)) = o;
+        *reinterpret_cast<bf16x8*>(dst + L::off(r, 64 * q + 8 * c)) = o;
     }
 }
 
@@ -562,28 +588,31 @@ __device__ __forceinline__ void segment_state_body(const PrefillParams& p, int b
     issue_rows(sq, KEY ? sq.k : sq.v, p.T, n0 * 64, raw);
     if (KEY && tid < KD) sNw[tid] = p.k_w[tid];
     float logdecay = 0.f;
+    StateScale sc;
     __syncthreads();
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
-        commit_gates(p, t0, gr, sLam, sBeta, sGam);
+        sc.begin_chunk(chunk_last_gam(gr));
+        commit_gates(p, t0, gr, sLam, sBeta, sGam, sc.inv());
         store_write_tile<TileW>(gr, p.T - t0, sB);
         if (KEY)
             norm_store_rows<TileF>(p, t0, raw, sNw, p.k_eps, sA);
         else
             store_rows<TileF>(raw, p.T - t0, sA);
+        __syncthreads();
         if (n + 1 < n1) {
             issue_rows(sq, KEY ? sq.k : sq.v, p.T, t0 + 64, raw);
             gr = issue_gates(sq, p.T, t0 + 64);
         }
-        __syncthreads();
         logdecay += sGam[63];
-        const float dec = sGam[64 + 63];
+        if (sc.fold != 1.f) {
 #pragma unroll
-        for (int x = 0; x < 8; x++) {
-            acc[x][0] *= dec;
-            acc[x][1] *= dec;
+            for (int x = 0; x < 8; x++) {
+                acc[x][0] *= sc.fold;
+                acc[x][1] *= sc.fold;
+            }
         }
-        // S += A^T bf16(2^(G_last - G_s) B): bt[c][jj] = B[32 ss + 8 lg + jj][b_col + 16 c + lr] scaled.
+        // acc += A^T bf16(2^(G_last - G_s) / sigma' B): bt[c][jj] = B[32 ss + 8 lg + jj][b_col + 16 c + lr] scaled.
 #pragma unroll
         for (int ss = 0; ss < 2; ss++) {
             bf16x8 bt[2];
@@ -602,13 +631,36 @@ __device__ __forceinline__ void segment_state_body(const PrefillParams& p, int b
                 if (x & 1) sched_fence();
             }
         }
+        sc.sig = sc.next;
         __syncthreads();
     }
-    float* out = p.seg + ((size_t)bh * (p.P - 1) + j) * SEG + (KEY ? 0 : SEG_K);
+    // E = sigma acc in fp16, scaled by 2^-e so that the wave's largest |E| is
+    // below 2^15 (fp16 keeps 11 bits, four times finer than the bf16 rounding
+    // the state gets before each inter-chunk product).
+    float m = 0.f;
 #pragma unroll
     for (int x = 0; x < 8; x++)
 #pragma unroll
-        for (int c = 0; c < 2; c++) *reinterpret_cast<f32x4*>(out + frag_offset(w, x, c, lane)) = acc[x][c];
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) m = fmaxf(m, fabsf(acc[x][c][i]));
+    m = wave_max(m) * sc.sig;
+    int e = 0;
+    if (m > 0.f && m < INFINITY) {
+        frexpf(m, &e);  // m < 2^e
+        e -= 15;
+    }
+    const float f = ldexpf(sc.sig, -e);
+    const size_t slot = (size_t)bh * (p.P - 1) + j;
+    _Float16* out = p.seg + slot * SEG + (KEY ? 0 : SEG_K);
+#pragma unroll
+    for (int x = 0; x < 8; x++)
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const f32x4 v = acc[x][c] * f;
+            *reinterpret_cast<f16x4*>(out + frag_offset(w, x, c, lane)) = f16x4{(f16_t)v[0], (f16_t)v[1], (f16_t)v[2], (f16_t)v[3]};
+        }
+    if (lane == 0) p.seg_exp[(slot * 2 + (KEY ? 0 : 1)) * 8 + w] = e;
     if (KEY && tid == 0) p.seg_decay[bh * p.P + j] = exp2f(logdecay);
 }
 
@@ -625,32 +677,33 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
 // Start state of segment j, in register order (the affine carry over
 // segments S_{i+1} = a_i S_i + E_i, unrolled):
 //   S_j = sum_{i<j} (prod_{i<l<j} a_l) E_i + (prod_{l<j} a_l) h0.
-// base selects the key (0) or value (SEG_K) part of the stored states; h0 is
+// part selects the key (0) or value (1) part of the stored states; h0 is
 // row-major and nullable, h0_index(x, c, i) gives the element of acc[x][c][i].
 // The segment workgroups of one sequence have block ids H * B apart; when
 // H * B is a multiple of 8 they are dealt to the same XCD, and most E_i reads
 // hit that XCD's L2.
 template <typename H0Index>
-__device__ __forceinline__ void load_start_state(const PrefillParams& p, int bh, int j, int base, const float* h0,
+__device__ __forceinline__ void load_start_state(const PrefillParams& p, int bh, int j, int part, const float* h0,
                                                  H0Index h0_index, f32x4 acc[8][2]) {
     const int lane = threadIdx.x & 63, w = wave_id();
 #pragma unroll
     for (int x = 0; x < 8; x++) acc[x][0] = acc[x][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     float a = 1.f;
-    const float* seg = p.seg + (size_t)bh * (p.P - 1) * SEG + base;
     for (int i = j - 1; i >= 0; i--) {
-        const float* e = seg + (size_t)i * SEG;
-        f32x4 v[8][2];
+        const size_t slot = (size_t)bh * (p.P - 1) + i;
+        const _Float16* e = p.seg + slot * SEG + part * SEG_K;
+        const float ai = ldexpf(a, p.seg_exp[(slot * 2 + part) * 8 + w]);
+        f16x4 v[8][2];
 #pragma unroll
         for (int x = 0; x < 8; x++)
 #pragma unroll
-            for (int c = 0; c < 2; c++) v[x][c] = *reinterpret_cast<const f32x4*>(e + frag_offset(w, x, c, lane));
+            for (int c = 0; c < 2; c++) v[x][c] = *reinterpret_cast<const f16x4*>(e + frag_offset(w, x, c, lane));
 #pragma unroll
         for (int x = 0; x < 8; x++)
 #pragma unroll
             for (int c = 0; c < 2; c++)
 #pragma unroll
-                for (int q = 0; q < 4; q++) acc[x][c][q] = fmaf(a, v[x][c][q], acc[x][c][q]);
+                for (int q = 0; q < 4; q++) acc[x][c][q] = fmaf(ai, (float)v[x][c][q], acc[x][c][q]);
         a *= p.seg_decay[bh * p.P + i];
     }
     if (h0) {
@@ -713,21 +766,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     issue_rows(sq, sq.q, p.T, n0 * 64, qraw);
     issue_rows(sq, sq.k, p.T, n0 * 64, kraw);
     GateRegs gr = issue_gates(sq, p.T, n0 * 64);
+    StateScale sc;
     __syncthreads();  // norm weights staged, score tiles zeroed
 
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
-        commit_gates(p, t0, gr, sLam, sBeta, sGam);
+        sc.begin_chunk(chunk_last_gam(gr));
+        commit_gates(p, t0, gr, sLam, sBeta, sGam, sc.inv());
         store_write_tile<TileW>(gr, p.T - t0, sW);
         norm_store_rows<TileQ>(p, t0, qraw, sQw, p.q_eps, sQ);
         norm_store_rows<TileF>(p, t0, kraw, sKw, p.k_eps, sK);
-        sched_fence();  // the next chunk's loads reuse these registers
-        if (n + 1 < n1) {
-            issue_rows(sq, sq.q, p.T, t0 + 64, qraw);
-            issue_rows(sq, sq.k, p.T, t0 + 64, kraw);
-            gr = issue_gates(sq, p.T, t0 + 64);
-        }
         __syncthreads();
+        // The next chunk's loads are spread over the phases (q here, k and the
+        // gates after the scores) so that no wave waits at a barrier for the
+        // CU's memory pipeline to accept them.
+        if (n + 1 < n1) issue_rows(sq, sq.q, p.T, t0 + 64, qraw);
 
         // Masked, decayed scores of this half's key slice: blocks mq, mq + 4 (and mq + 8).
         score_tile<TileQ, TileF>(sQ, HALF * y, sK, HALF * y, mq, sGam, log2_scale, sPy);
@@ -747,15 +800,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
                 out[tb][0] = mfma_bf16(a0, bq, out[tb][0]);
                 out[tb][1] = mfma_bf16(a1, bq, out[tb][1]);
             }
-            sched_fence();
         }
+        const float osc = p.scale * sc.sig;
 #pragma unroll
         for (int tb = 0; tb < 4; tb++) {
-            const float sc = sGam[64 + 16 * tb + lr] * p.scale;
-            out[tb][0] *= sc;
-            out[tb][1] *= sc;
+            const float f = sGam[64 + 16 * tb + lr] * osc;
+            out[tb][0] *= f;
+            out[tb][1] *= f;
         }
         __syncthreads();  // scores complete
+        if (n + 1 < n1) {
+            issue_rows(sq, sq.k, p.T, t0 + 64, kraw);
+            gr = issue_gates(sq, p.T, t0 + 64);
+        }
 
         // raw_y^T += w^T P_y^T (P carries the scale); the blocks of P above the diagonal are zero.
         // wf[c][ss][jj] = w[32 ss + 8 lg + jj][32 mq + 16 c + lr].
@@ -777,12 +834,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
             for (int c = 0; c < 2; c++)
                 st_b64(rraw, raw_lane + 32 * c, (uint32_t)(t0 + 16 * tb) * (kSlots * 2), to_bf16x4(out[tb][c], 1.f));
-        // State update: S = 2^G_last S + k_hat^T bf16(2^(G_last - G_s) w).
-        const float dec = sGam[64 + 63];
+        // State update: S = 2^G_last S + k_hat^T bf16(2^(G_last - G_s) w), as
+        // acc += k_hat^T bf16(2^(G_last - G_s) / sigma' w).
+        if (sc.fold != 1.f) {
 #pragma unroll
-        for (int kb = 0; kb < 8; kb++) {
-            acc[kb][0] *= dec;
-            acc[kb][1] *= dec;
+            for (int kb = 0; kb < 8; kb++) {
+                acc[kb][0] *= sc.fold;
+                acc[kb][1] *= sc.fold;
+            }
         }
 #pragma unroll
         for (int ss = 0; ss < 2; ss++) {
@@ -798,8 +857,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
                 acc[kb][0] = mfma_bf16(kf, wt[0], acc[kb][0]);
                 acc[kb][1] = mfma_bf16(kf, wt[1], acc[kb][1]);
             }
-            sched_fence();
         }
+        sc.sig = sc.next;
         __syncthreads();  // tiles are overwritten by the next chunk
     }
 
@@ -811,7 +870,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
             for (int c = 0; c < 2; c++)
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    dst[(HALF * y + state_row(kb, lg, i)) * kSlots + 32 * mq + 16 * c + lr] = acc[kb][c][i];
+                    dst[(HALF * y + state_row(kb, lg, i)) * kSlots + 32 * mq + 16 * c + lr] = acc[kb][c][i] * sc.sig;
     }
 }
 
@@ -994,7 +1053,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
     zero_scores(sP, 1);
     f32x4 acc[8][2];
-    load_start_state(p, bh, j, SEG_K, p.h0_v ? p.h0_v + (size_t)bh * SEG_V : nullptr,
+    load_start_state(p, bh, j, 1, p.h0_v ? p.h0_v + (size_t)bh * SEG_V : nullptr,
                      [&](int mb, int c, int i) { return state_row(mb, lg, i) * VD + 32 * w + 16 * c + lr; }, acc);
     const Seq sq = make_seq(p, b, h, bh);
     const rsrc_t rom = make_rsrc(p.omega + (size_t)bh * p.Tp * kSlots, (size_t)p.Tp * kSlots * 2);
@@ -1003,20 +1062,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     issue_rows(sq, sq.v, p.T, n0 * 64, vraw);
     issue_omega(rom, n0 * 64, om);
     GateRegs gr = issue_gates(sq, p.T, n0 * 64);
+    StateScale sc;
 
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
-        commit_gates(p, t0, gr, sLam, sBeta, sGam);
+        sc.begin_chunk(chunk_last_gam(gr));
+        commit_gates(p, t0, gr, sLam, sBeta, sGam, sc.inv());
         store_write_tile<TileW>(gr, p.T - t0, sW);
         store_half_rows(om, 64, sOm);
         store_rows<TileF>(vraw, p.T - t0, sV);
-        sched_fence();
-        if (n + 1 < n1) {
-            issue_rows(sq, sq.v, p.T, t0 + 64, vraw);
-            issue_omega(rom, t0 + 64, om);
-            gr = issue_gates(sq, p.T, t0 + 64);
-        }
         __syncthreads();
+        // The next chunk's loads are spread over the phases (see pass 1).
+        if (n + 1 < n1) issue_omega(rom, t0 + 64, om);
 
         score_tile<TileO, TileW>(sOm, 0, sW, 0, w, sGam, 0.f, sP);
         if (w < 2) score_tile<TileO, TileW>(sOm, 0, sW, 0, w + 8, sGam, 0.f, sP);
@@ -1034,15 +1091,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
                 out[tb][0] = mfma_bf16(a0, bo, out[tb][0]);
                 out[tb][1] = mfma_bf16(a1, bo, out[tb][1]);
             }
-            sched_fence();
         }
 #pragma unroll
         for (int tb = 0; tb < 4; tb++) {
-            const float sc = sGam[64 + 16 * tb + lr];
-            out[tb][0] *= sc;
-            out[tb][1] *= sc;
+            const float f = sGam[64 + 16 * tb + lr] * sc.sig;
+            out[tb][0] *= f;
+            out[tb][1] *= f;
         }
         __syncthreads();  // scores complete
+        if (n + 1 < n1) {
+            issue_rows(sq, sq.v, p.T, t0 + 64, vraw);
+            gr = issue_gates(sq, p.T, t0 + 64);
+        }
 
         // o^T += v^T P^T. vb[c][ss][jj] = v[32 ss + 8 lg + jj][32 w + 16 c + lr].
         bf16x8 vb[2][2];
@@ -1066,12 +1126,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
                     st_b64(sq.o, o_lane + 32 * c, (uint32_t)(t0 + 16 * tb) * sq.row16, to_bf16x4(out[tb][c], 1.f));
             }
         }
-        // State update: S = 2^G_last S + w^T bf16(2^(G_last - G_s) v).
-        const float dec = sGam[64 + 63];
+        // State update: S = 2^G_last S + w^T bf16(2^(G_last - G_s) v), as
+        // acc += w^T bf16(2^(G_last - G_s) / sigma' v).
+        if (sc.fold != 1.f) {
 #pragma unroll
-        for (int mb = 0; mb < 8; mb++) {
-            acc[mb][0] *= dec;
-            acc[mb][1] *= dec;
+            for (int mb = 0; mb < 8; mb++) {
+                acc[mb][0] *= sc.fold;
+                acc[mb][1] *= sc.fold;
+            }
         }
 #pragma unroll
         for (int ss = 0; ss < 2; ss++) {
@@ -1087,8 +1149,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
                 acc[mb][0] = mfma_bf16(wk, vt[0], acc[mb][0]);
                 acc[mb][1] = mfma_bf16(wk, vt[1], acc[mb][1]);
             }
-            sched_fence();
         }
+        sc.sig = sc.next;
         __syncthreads();
     }
 
@@ -1099,7 +1161,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
             for (int c = 0; c < 2; c++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) dst[state_row(mb, lg, i) * VD + 32 * w + 16 * c + lr] = acc[mb][c][i];
+                for (int i = 0; i < 4; i++) dst[state_row(mb, lg, i) * VD + 32 * w + 16 * c + lr] = acc[mb][c][i] * sc.sig;
     }
 }
 
@@ -1153,8 +1215,9 @@ WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V) {
     w.lam = 0;
     w.gam = align256(w.lam + BH * Tp * sizeof(float));
     w.seg = align256(w.gam + BH * Tp * sizeof(float));
-    const size_t seg_bytes = P > 1 ? BH * (P - 1) * (size_t)(K * kSlots + kSlots * V) * sizeof(float) : 0;
-    w.seg_decay = align256(w.seg + seg_bytes);
+    const size_t nseg = P > 1 ? BH * (P - 1) : 0;
+    w.seg_exp = align256(w.seg + nseg * (size_t)(K * kSlots + kSlots * V) * sizeof(_Float16));
+    w.seg_decay = align256(w.seg_exp + nseg * 16 * sizeof(int));
     w.raw = align256(w.seg_decay + BH * P * sizeof(float));
     w.omega = align256(w.raw + 2 * BH * Tp * kSlots * 2);
     w.total = align256(w.omega + BH * Tp * kSlots * 2);
