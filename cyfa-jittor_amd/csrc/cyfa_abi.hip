@@ -160,7 +160,6 @@ int cyfa_chunk_fwd(const CyfaChunkArgs* a, void* hip_stream) {
     p.seg = (_Float16*)(base + ws.seg);
     p.seg_exp = (int*)(base + ws.seg_exp);
     p.seg_decay = (float*)(base + ws.seg_decay);
-    p.raw = (__bf16*)(base + ws.raw);
     p.omega = (__bf16*)(base + ws.omega);
     cyfa::launch_prefill(p, (hipStream_t)hip_stream);
     return check_launch("cyfa_chunk_fwd");

@@ -40,7 +40,6 @@ struct PrefillParams {
                        // each wave's block scaled by 2^-seg_exp
     int* seg_exp;      // [B*H, P-1, 2, 8] power-of-two exponent per (key / value part, wave)
     float* seg_decay;  // [B*H, P] product of alpha over each segment
-    __bf16* raw;       // [2, B*H, Tp, 128] pass-1 output of each 128-wide key half
     __bf16* omega;     // [B*H, Tp, 128] slot weights between the two passes
 };
 
@@ -69,7 +68,7 @@ struct ConvParams {
 };
 
 struct WorkspaceLayout {
-    size_t lam, gam, seg, seg_exp, seg_decay, raw, omega, total;
+    size_t lam, gam, seg, seg_exp, seg_decay, omega, total;
 };
 
 void choose_segments(int BH, int N, int* P, int* L);

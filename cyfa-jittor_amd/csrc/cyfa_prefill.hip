@@ -8,14 +8,14 @@
 //                       segment.
 //   3. pass1_kernel     per segment: start from the carried state
 //                       S_j = sum_{i<j} (prod_{i<l<j} a_l) E_i + (prod_{l<j} a_l) h0,
-//                       then sweep the segment's 64-token chunks with
-//                       the fp32 key state [256 x 128] held in registers and
-//                       write each 128-wide key half's pass-1 output scale
-//                       (2^G q S + P w) as bf16.
-//   4. readout_kernel   raw = sum of the two halves; z = U(lam) raw;
-//                       p = softmax(table z); u = table^T p; slot weights
-//                       bf16(U(-lam) u) (ops/chunk_readout.py:797-909).
-//   5. pass2_kernel     per segment: the same carry and sweep for the value state
+//                       then sweep the segment's 64-token chunks with the
+//                       fp32 key state [256 x 128] held in registers; each
+//                       chunk's pass-1 output (2^G q S + P w per 128-wide key
+//                       half, bf16) goes through LDS into the slot readout
+//                       z = U(lam) raw; p = softmax(table z); u = table^T p;
+//                       slot weights bf16(U(-lam) u) (ops/chunk_readout.py:797-909),
+//                       which are written for pass 2.
+//   4. pass2_kernel     per segment: the same carry and sweep for the value state
 //                       [128 x 256] with query = slot weights, key = w,
 //                       value = v -> o (bf16).
 // The pass-1 output is formed as two 128-wide key slices, each scaled and
@@ -285,10 +285,21 @@ __device__ __forceinline__ bf16x8 load_tr_perm(const bf16_t* X, int s0, int c0, 
     return __builtin_bit_cast(bf16x8, tr_pair(p, L::ld));
 }
 
-__device__ __forceinline__ f16x8 load_tr_f16(const f16_t* X, int ld, int s0, int c0) {
+// Transpose read of a row-major f16 tile with the rows of a 32-row block taken
+// in the k order of a C-block pair:
+//   lane (lr, lg) element j = X[r0 + 4 lg + j][c0 + lr]             (j < 4)
+//                             X[r0 + 16 + 4 lg + (j - 4)][c0 + lr]  (j >= 4)
+// i.e. the A operand A[row = c0 + lr][k] of a product whose other operand is a
+// C-block pair (rows r0 .. r0 + 31) used directly as the B operand.
+__device__ __forceinline__ f16x8 load_tr_pair_f16(const f16_t* X, int ld, int r0, int c0) {
     const int l = threadIdx.x & 63, g = l >> 4, i = l & 15;
-    const short* p = reinterpret_cast<const short*>(X) + (s0 + 8 * g + (i >> 2)) * ld + c0 + 4 * (i & 3);
-    return __builtin_bit_cast(f16x8, tr_pair(p, ld));
+    const short* p = reinterpret_cast<const short*>(X) + (r0 + 4 * g + (i >> 2)) * ld + c0 + 4 * (i & 3);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(const_cast<short*>(p)));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(const_cast<short*>(p + 16 * ld)));
+    s16x8 r;
+    r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+    r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+    return __builtin_bit_cast(f16x8, r);
 }
 
 // Row fragment: lane (lr, lg) gets X[r0 + lr][k0 + 8 lg .. + 8] (A operand, or
@@ -717,7 +728,104 @@ __device__ __forceinline__ void load_start_state(const PrefillParams& p, int bh,
 }
 
 // ---------------------------------------------------------------------------
-// 4. Pass 1 (key state), one segment per workgroup. grid = (H, B, P), 512 threads.
+// Slot readout of 16 tokens (ops/chunk_readout.py:797-909), fp16 MFMA with
+// fp32 accumulation; lane (lr, lg) works on token lr. The two 128-wide key
+// halves of the pass-1 output (bf16, rows RR apart) come from LDS, the table
+// (f16 [128][RS], row 127 zero) too.
+//   z_t = U(lam_t) (raw0_t + raw1_t)                 (B operand, registers)
+//   L^T[r][t] = table[r] . z_t                       (C rows r = 16 rb + 4 lg + i)
+//   p_t = softmax over r < 127 of L^T[:, t]          (in registers + 2 shuffles)
+//   u^T[m][t] = sum_r table[r][m] p_t[r]             (p_t as the B operand straight
+//                                                     from the C layout)
+//   weights_t = bf16(U(-lam_t) u_t)                  (four consecutive m per store)
+constexpr int RR = 128 + 8;  // row stride of the pass-1 output tiles in LDS
+
+__device__ __forceinline__ void readout_tokens(const bf16_t* sR0, const bf16_t* sR1, const f16_t* sTab, float lamr,
+                                               bf16_t* dst) {
+    const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+    // z fragments: element j = z_t[32 ks + 8 lg + j].
+    f16x8 zf[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        const bf16x8 ra = *reinterpret_cast<const bf16x8*>(sR0 + lr * RR + 32 * ks + 8 * lg);
+        const bf16x8 rb = *reinterpret_cast<const bf16x8*>(sR1 + lr * RR + 32 * ks + 8 * lg);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float e = (float)ra[2 * q] + (float)rb[2 * q];
+            const float o = (float)ra[2 * q + 1] + (float)rb[2 * q + 1];
+            float sn, cs;
+            pair_sincos(lamr, 16 * ks + 4 * lg + q, sn, cs);
+            zf[ks][2 * q] = (f16_t)(cs * e - sn * o);
+            zf[ks][2 * q + 1] = (f16_t)(sn * e + cs * o);
+        }
+    }
+    f32x4 L[8];
+#pragma unroll
+    for (int rb8 = 0; rb8 < 8; rb8++) L[rb8] = f32x4{0.f, 0.f, 0.f, 0.f};
+    sched_fence();
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+#pragma unroll
+        for (int rb8 = 0; rb8 < 8; rb8++)
+            L[rb8] = mfma_f16(load_row_ld<f16x8>(sTab, RS, 16 * rb8, 32 * ks), zf[ks], L[rb8]);
+        sched_fence();
+    }
+    if (lg == 3) L[7][3] = -INFINITY;  // slot r = 127 is not active
+    float mx = -INFINITY;
+#pragma unroll
+    for (int rb8 = 0; rb8 < 8; rb8++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) mx = fmaxf(mx, L[rb8][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    float sum = 0.f;
+#pragma unroll
+    for (int rb8 = 0; rb8 < 8; rb8++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            L[rb8][i] = __expf(L[rb8][i] - mx);
+            sum += L[rb8][i];
+        }
+    sum += __shfl_xor(sum, 16);
+    sum += __shfl_xor(sum, 32);
+    const float inv = 1.f / sum;
+    f16x8 pf[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            pf[ks][i] = (f16_t)(L[2 * ks][i] * inv);
+            pf[ks][4 + i] = (f16_t)(L[2 * ks + 1][i] * inv);
+        }
+    f32x4 U[8];
+#pragma unroll
+    for (int mb = 0; mb < 8; mb++) U[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    sched_fence();
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+#pragma unroll
+        for (int mb = 0; mb < 8; mb++) U[mb] = mfma_f16(load_tr_pair_f16(sTab, RS, 32 * ks, 16 * mb), pf[ks], U[mb]);
+        sched_fence();
+    }
+    // Lane holds u_t[16 mb + 4 lg + i]: pairs 8 mb + 2 lg + q, q = 0, 1.
+#pragma unroll
+    for (int mb = 0; mb < 8; mb++) {
+        bf16x4 o;
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            float sn, cs;
+            pair_sincos(lamr, 8 * mb + 2 * lg + q, sn, cs);
+            const float ue = U[mb][2 * q], uo = U[mb][2 * q + 1];
+            o[2 * q] = (bf16_t)(cs * ue + sn * uo);
+            o[2 * q + 1] = (bf16_t)(cs * uo - sn * ue);
+        }
+        *reinterpret_cast<bf16x4*>(dst + 16 * mb + 4 * lg) = o;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 4. Pass 1 (key state) and the slot readout, one segment per workgroup.
+// grid = (H, B, P), 512 threads.
 // Wave w works on key half y = w >> 2 and state columns [32 mq, 32 mq + 32),
 // mq = w & 3: acc[kb][c] = S[128 y + state_row(kb, lg, i)][32 mq + 16 c + lr],
 // and the same 32 output coordinates of half y:
@@ -728,7 +836,9 @@ constexpr int P1_W = P1_K + TileF::bytes;      // w, TileW
 constexpr int P1_P = P1_W + TileW::bytes;      // masked scores of each half, 2 x TileP
 constexpr int P1_G = P1_P + 2 * TileP::bytes;  // f32 [5][64] gates
 constexpr int P1_NW = P1_G + 5 * 64 * 4;      // f32 [2][256] q and k norm weights
-constexpr int P1_LDS = P1_NW + 2 * KD * 4;
+constexpr int P1_T = P1_NW + 2 * KD * 4;       // f16 [128][RS] readout table of the head (row 127 zero)
+constexpr int P1_LDS = P1_T + 128 * RS * 2;
+static_assert(2 * 64 * RR * 2 <= TileQ::bytes, "the two pass-1 output tiles fit in the q_hat tile");
 static_assert(P1_LDS <= 160 * 1024, "pass-1 workgroup must fit in one CU's LDS");
 
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void pass1_kernel(PrefillParams p) {
@@ -742,6 +852,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     float* sGam = sBeta + 64;
     float* sQw = reinterpret_cast<float*>(smem + P1_NW);
     float* sKw = sQw + KD;
+    f16_t* sTab = reinterpret_cast<f16_t*>(smem + P1_T);
+    // After the scores and the inter-chunk product the q_hat tile is free; it
+    // then holds the chunk's pass-1 output of both key halves for the readout.
+    bf16_t* sR0 = sQ;
+    bf16_t* sR1 = sQ + 64 * RR;
 
     const SegCoord cd = seg_coord(p.H, blockIdx.z);
     const int bh = cd.bh, j = cd.j, b = cd.b, h = cd.h;
@@ -753,6 +868,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         sQw[tid] = p.q_w[tid];
         sKw[tid] = p.k_w[tid];
     }
+    {
+        const float* tb = p.table + (size_t)h * kActive * kSlots;
+        for (int idx = tid; idx < 128 * 32; idx += 512) {
+            const int r = idx >> 5, m4 = (idx & 31) * 4;
+            const float4 v = r < kActive ? *reinterpret_cast<const float4*>(tb + r * kSlots + m4)
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+            *reinterpret_cast<f16x4*>(sTab + r * RS + m4) = f16x4{(f16_t)v.x, (f16_t)v.y, (f16_t)v.z, (f16_t)v.w};
+        }
+    }
     zero_scores(sP, 2);  // the two blocks above the diagonal that the intra product reads stay zero
     bf16_t* sPy = sP + y * (TileP::bytes / 2);
     f32x4 acc[8][2];
@@ -760,8 +884,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
                      [&](int kb, int c, int i) { return (HALF * y + state_row(kb, lg, i)) * kSlots + 32 * mq + 16 * c + lr; },
                      acc);
     const Seq sq = make_seq(p, b, h, bh);
-    const rsrc_t rraw = make_rsrc(p.raw + ((size_t)y * p.B * p.H + bh) * p.Tp * kSlots, (size_t)p.Tp * kSlots * 2);
-    const uint32_t raw_lane = (uint32_t)lr * (kSlots * 2) + 2 * (32 * mq + 4 * lg);
     bf16x8 qraw[4], kraw[4];
     issue_rows(sq, sq.q, p.T, n0 * 64, qraw);
     issue_rows(sq, sq.k, p.T, n0 * 64, kraw);
@@ -829,11 +951,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
                 out[tb][0] = mfma_bf16(wf[0][ss], pf, out[tb][0]);
                 out[tb][1] = mfma_bf16(wf[1][ss], pf, out[tb][1]);
             }
+        // The half's output, rounded to bf16 (ops/chunk_o.py:369-374), into LDS.
+        bf16_t* sRy = y == 0 ? sR0 : sR1;
 #pragma unroll
         for (int tb = 0; tb < 4; tb++)
 #pragma unroll
             for (int c = 0; c < 2; c++)
-                st_b64(rraw, raw_lane + 32 * c, (uint32_t)(t0 + 16 * tb) * (kSlots * 2), to_bf16x4(out[tb][c], 1.f));
+                *reinterpret_cast<bf16x4*>(sRy + (16 * tb + lr) * RR + 32 * mq + 16 * c + 4 * lg) = to_bf16x4(out[tb][c], 1.f);
         // State update: S = 2^G_last S + k_hat^T bf16(2^(G_last - G_s) w), as
         // acc += k_hat^T bf16(2^(G_last - G_s) / sigma' w).
         if (sc.fold != 1.f) {
@@ -859,6 +983,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
             }
         }
         sc.sig = sc.next;
+        __syncthreads();  // output tiles complete
+        // Slot readout of the chunk: wave mq of the first half takes tokens 16 mq .. 16 mq + 15.
+        if (y == 0)
+            readout_tokens(sR0 + 16 * mq * RR, sR1 + 16 * mq * RR, sTab, sLam[16 * mq + lr],
+                           p.omega + ((size_t)bh * p.Tp + t0 + 16 * mq + lr) * kSlots);
         __syncthreads();  // tiles are overwritten by the next chunk
     }
 
@@ -875,157 +1004,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 }
 
 // ---------------------------------------------------------------------------
-// 5. Slot readout (ops/chunk_readout.py:797-909), fp16 MFMA with fp32
-// accumulation. grid = H * G, 512 threads; the workgroup stages its head's
-// table once and each wave then runs 16-token tasks on its own: lane (lr, lg)
-// works on token lr of the task.
-//   z_t = U(lam_t) raw_t                              (B operand, registers)
-//   L^T[r][t] = table[r] . z_t                        (C rows r = 16 rb + 4 lg + i)
-//   p_t = softmax over r < 127 of L^T[:, t]           (in registers + 2 shuffles)
-//   u^T[m][t] = sum_r table[r][m] p_t[r]              (p_t as the B operand straight
-//                                                      from the C layout)
-//   weights_t = bf16(U(-lam_t) u_t)
-// The second product reads the table through transpose reads of a copy whose
-// rows are stored in the k order of a C-block pair.
-constexpr int RO_A = 0;                    // f16 [128][RS] table rows r (row 127 zero)
-constexpr int RO_B = RO_A + 128 * RS * 2;  // f16 [128][RS] table rows in C-pair order
-constexpr int RO_LDS = RO_B + 128 * RS * 2;
-static_assert(2 * RO_LDS <= 160 * 1024, "two readout workgroups must fit in one CU's LDS");
-
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void readout_kernel(PrefillParams p) {
-    __shared__ __align__(16) unsigned char smem[RO_LDS];
-    f16_t* sTA = reinterpret_cast<f16_t*>(smem + RO_A);
-    f16_t* sTB = reinterpret_cast<f16_t*>(smem + RO_B);
-    const int h = blockIdx.x % p.H, grp = blockIdx.x / p.H, ngrp = gridDim.x / p.H;
-    const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), lr = lane & 15, lg = lane >> 4;
-    {
-        const float* tb = p.table + (size_t)h * kActive * kSlots;
-        for (int idx = tid; idx < 128 * 32; idx += 512) {
-            const int r = idx >> 5, m4 = (idx & 31) * 4;
-            const float4 v = r < kActive ? *reinterpret_cast<const float4*>(tb + r * kSlots + m4)
-                                         : make_float4(0.f, 0.f, 0.f, 0.f);
-            const f16x4 hv = f16x4{(f16_t)v.x, (f16_t)v.y, (f16_t)v.z, (f16_t)v.w};
-            *reinterpret_cast<f16x4*>(sTA + r * RS + m4) = hv;
-            // row r sits at k position 8 lg + j of its 32-row group, where
-            // r % 32 = 4 lg + j (j < 4) or 16 + 4 lg + (j - 4) (j >= 4)
-            const int rl = r & 31;
-            const int pos = rl < 16 ? 8 * (rl >> 2) + (rl & 3) : 8 * ((rl - 16) >> 2) + 4 + (rl & 3);
-            *reinterpret_cast<f16x4*>(sTB + ((r & ~31) + pos) * RS + m4) = hv;
-        }
-    }
-    __syncthreads();
-
-    const int blocks = p.Tp / 16, tasks = p.B * blocks;
-    const size_t plane = (size_t)p.B * p.H * p.Tp * kSlots;
-    // raw rows of the wave's next task are loaded while the current one computes
-    bf16x8 ra[4], rb[4];
-    float lam_next = 0.f;
-    auto issue = [&](int task) {
-        const int b = task / blocks, t = 16 * (task % blocks) + lr;
-        const size_t row = ((size_t)(b * p.H + h) * p.Tp + t) * kSlots;
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            ra[ks] = *reinterpret_cast<const bf16x8*>(p.raw + row + 32 * ks + 8 * lg);
-            rb[ks] = *reinterpret_cast<const bf16x8*>(p.raw + plane + row + 32 * ks + 8 * lg);
-        }
-        lam_next = p.lam[(size_t)(b * p.H + h) * p.Tp + t];
-    };
-    int task = grp * 8 + w;
-    if (task < tasks) issue(task);
-    for (; task < tasks; task += ngrp * 8) {
-        const int b = task / blocks, t = 16 * (task % blocks) + lr;
-        const int bh = b * p.H + h;
-        const size_t row = ((size_t)bh * p.Tp + t) * kSlots;
-        const float lamr = lam_next;
-        // z fragments: element j = z_t[32 ks + 8 lg + j].
-        f16x8 zf[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float e = (float)ra[ks][2 * q] + (float)rb[ks][2 * q];
-                const float o = (float)ra[ks][2 * q + 1] + (float)rb[ks][2 * q + 1];
-                float sn, cs;
-                pair_sincos(lamr, 16 * ks + 4 * lg + q, sn, cs);
-                zf[ks][2 * q] = (f16_t)(cs * e - sn * o);
-                zf[ks][2 * q + 1] = (f16_t)(sn * e + cs * o);
-            }
-        if (task + ngrp * 8 < tasks) issue(task + ngrp * 8);
-        f32x4 L[8];
-#pragma unroll
-        for (int rb8 = 0; rb8 < 8; rb8++) L[rb8] = f32x4{0.f, 0.f, 0.f, 0.f};
-        sched_fence();
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-#pragma unroll
-            for (int rb8 = 0; rb8 < 8; rb8++)
-                L[rb8] = mfma_f16(load_row_ld<f16x8>(sTA, RS, 16 * rb8, 32 * ks), zf[ks], L[rb8]);
-            sched_fence();
-        }
-        if (lg == 3) L[7][3] = -INFINITY;  // slot r = 127 is not active
-        float mx = -INFINITY;
-#pragma unroll
-        for (int rb8 = 0; rb8 < 8; rb8++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) mx = fmaxf(mx, L[rb8][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        float sum = 0.f;
-#pragma unroll
-        for (int rb8 = 0; rb8 < 8; rb8++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                L[rb8][i] = __expf(L[rb8][i] - mx);
-                sum += L[rb8][i];
-            }
-        sum += __shfl_xor(sum, 16);
-        sum += __shfl_xor(sum, 32);
-        const float inv = 1.f / sum;
-        f16x8 pf[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                pf[ks][i] = (f16_t)(L[2 * ks][i] * inv);
-                pf[ks][4 + i] = (f16_t)(L[2 * ks + 1][i] * inv);
-            }
-        f32x4 U[8];
-#pragma unroll
-        for (int mb = 0; mb < 8; mb++) U[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        sched_fence();
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-#pragma unroll
-            for (int mb = 0; mb < 8; mb++) U[mb] = mfma_f16(load_tr_f16(sTB, RS, 32 * ks, 16 * mb), pf[ks], U[mb]);
-            sched_fence();
-        }
-        // Lane holds u_t[16 mb + 4 lg + i]: pairs 8 mb + 2 lg + q, q = 0, 1.
-        bf16_t* dst = p.omega + row;
-#pragma unroll
-        for (int mb = 0; mb < 8; mb++) {
-            bf16x4 o;
-#pragma unroll
-            for (int q = 0; q < 2; q++) {
-                float sn, cs;
-                pair_sincos(lamr, 8 * mb + 2 * lg + q, sn, cs);
-                const float ue = U[mb][2 * q], uo = U[mb][2 * q + 1];
-                o[2 * q] = (bf16_t)(cs * ue + sn * uo);
-                o[2 * q + 1] = (bf16_t)(cs * uo - sn * ue);
-            }
-            *reinterpret_cast<bf16x4*>(dst + 16 * mb + 4 * lg) = o;
-        }
-    }
-}
-
-int readout_groups(int B, int Tp, int H) {
-    const int iters = (B * Tp / 16 + 7) / 8;  // 8 tasks per workgroup iteration
-    int g = (512 + H - 1) / H;                // about two workgroups per CU
-    if (g > iters) g = iters;
-    return g < 1 ? 1 : g;
-}
-
-// ---------------------------------------------------------------------------
-// 6. Pass 2 (value state), one segment per workgroup. grid = (H, B, P), 512
+// 5. Pass 2 (value state), one segment per workgroup. grid = (H, B, P), 512
 // threads. Wave w owns value columns [32 w, 32 w + 32):
 // acc[mb][c] = S[state_row(mb, lg, i)][32 w + 16 c + lr], and the same 32 output
 // coordinates: out[tb][c] = o^T[32 w + 16 c + 4 lg + i][16 tb + lr].
@@ -1218,8 +1197,7 @@ WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V) {
     const size_t nseg = P > 1 ? BH * (P - 1) : 0;
     w.seg_exp = align256(w.seg + nseg * (size_t)(K * kSlots + kSlots * V) * sizeof(_Float16));
     w.seg_decay = align256(w.seg_exp + nseg * 16 * sizeof(int));
-    w.raw = align256(w.seg_decay + BH * P * sizeof(float));
-    w.omega = align256(w.raw + 2 * BH * Tp * kSlots * 2);
+    w.omega = align256(w.seg_decay + BH * P * sizeof(float));
     w.total = align256(w.omega + BH * Tp * kSlots * 2);
     return w;
 }
@@ -1229,7 +1207,6 @@ int launch_prefill(const PrefillParams& p, hipStream_t stream) {
     hipLaunchKernelGGL(clock_kernel, dim3(BH), dim3(CLOCK_THREADS), 0, stream, p);
     if (p.P > 1) hipLaunchKernelGGL(segment_state_kernel, dim3(p.H, p.B, 2 * (p.P - 1)), dim3(512), 0, stream, p);
     hipLaunchKernelGGL(pass1_kernel, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
-    hipLaunchKernelGGL(readout_kernel, dim3(p.H * readout_groups(p.B, p.Tp, p.H)), dim3(512), 0, stream, p);
     hipLaunchKernelGGL(pass2_kernel, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
     return 0;
 }

@@ -134,6 +134,45 @@ def test_chunk_matches_oracle(B, T, H, state, seg, monkeypatch):
     _check_states(st, rst, "chunk")
 
 
+@pytest.mark.parametrize("case", ["strong_decay", "extreme_decay", "large_values"])
+def test_chunk_state_scale_paths(case, monkeypatch):
+    """Paths of the sweeps' state bookkeeping that mild gates never reach.
+
+    strong_decay: about 2^-23 of decay per chunk, so the per-workgroup state
+    scale falls below 2^-64 every few chunks and is multiplied into the fp32
+    accumulators; extreme_decay: the chunk decay underflows to zero in fp32
+    (the state restarts from the chunk's own update, as the oracle's 2^-185
+    factor makes it); large_values: value magnitudes of 3e4 drive the
+    segment-local value states past the fp16 range, so they are stored with a
+    power-of-two scale. Outputs and value states are compared after dividing
+    by the value scale (the tolerance is absolute in max-abs)."""
+    from cyclic_flow_attention.ops import chunk_cyfa
+
+    monkeypatch.setenv("CYFA_SEGMENT_CHUNKS", "2")
+    B, T, H = 2, 640, 2
+    x, init = _inputs(B, T, H, seed=31, state=True)
+    gen = torch.Generator().manual_seed(32)
+    scale = 1.0
+    if case == "strong_decay":
+        x["g"] = -0.25 - 0.05 * torch.rand(B, T, H, generator=gen)
+    elif case == "extreme_decay":
+        x["g"] = -3.0 - torch.rand(B, T, H, generator=gen)
+    else:
+        scale = 3e4
+        x["v"] = (x["v"].float() * scale).bfloat16()
+        init = (init[0], init[1] * scale, init[2])
+    xg, ig = _gpu(x, init)
+    xd, idd = _oracle(x, init)
+    with torch.no_grad():
+        o, st = chunk_cyfa(**xg, initial_state=ig, output_final_state=True)
+    torch.cuda.synchronize()
+    ro, rst = O.chunk_cyfa(**xd, initial_state=idd, output_final_state=True)
+    assert torch.isfinite(o.float()).all()
+    assert_close(o.double().cpu() / scale, ro / scale, what=f"state paths {case} o")
+    assert_close(st[0], rst[0], what=f"state paths {case} hk")
+    assert_close(st[1].double().cpu() / scale, rst[1] / scale, what=f"state paths {case} hv")
+
+
 def test_chunk_long_clock_range_reduction():
     """Clock values around 1.2e4 (the config-5 regime) keep their phase accuracy."""
     from cyclic_flow_attention.ops import chunk_cyfa
