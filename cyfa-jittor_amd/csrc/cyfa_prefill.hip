@@ -208,16 +208,17 @@ __device__ __forceinline__ float chunk_last_gam(const GateRegs& r) {
 }
 
 // inv: 1 / sigma of the state after this chunk's update (see StateScale).
+// Written by the wave whose index is `leader`.
 __device__ __forceinline__ void commit_gates(const PrefillParams& p, int t0, const GateRegs& r, float* sLam,
-                                             float* sBeta, float* sGam, float inv) {
-    const int tid = threadIdx.x;
-    if (tid < 64) {
+                                             float* sBeta, float* sGam, float inv, int leader = 0) {
+    const int lane = threadIdx.x & 63;
+    if (wave_id() == leader) {
         const float last = chunk_last_gam(r);
-        sGam[tid] = r.gam;
-        sBeta[tid] = t0 + tid < p.T ? r.beta : 0.f;
-        sLam[tid] = r.lamr;
-        sGam[64 + tid] = fast_exp2(r.gam);                // 2^G_t
-        sGam[128 + tid] = fast_exp2(last - r.gam) * inv;  // 2^(G_last - G_t) / sigma'
+        sGam[lane] = r.gam;
+        sBeta[lane] = t0 + lane < p.T ? r.beta : 0.f;
+        sLam[lane] = r.lamr;
+        sGam[64 + lane] = fast_exp2(r.gam);                // 2^G_t
+        sGam[128 + lane] = fast_exp2(last - r.gam) * inv;  // 2^(G_last - G_t) / sigma'
     }
 }
 
@@ -380,6 +381,51 @@ __device__ __forceinline__ void store_rows(const bf16x8 raw[4], int valid, bf16_
     }
 }
 
+// The same rows for a 256-thread group: thread u (0..255) holds row u >> 2,
+// columns 64 (u & 3) + 8 j .. + 8 in raw[j] (j = 0..7).
+__device__ __forceinline__ void issue_rows_q(const Seq& sq, rsrc_t x, int T, int t0, int u, bf16x8 raw[8]) {
+    const int t = t0 + (u >> 2);
+    const uint32_t off = (uint32_t)(t < T ? t : T - 1) * sq.row16 + 128 * (u & 3);
+#pragma unroll
+    for (int j = 0; j < 8; j++) raw[j] = ld_b128(x, off + 16 * j);
+}
+
+// norm_store_rows for that mapping (the 4 threads of a row meet by DPP).
+template <class L>
+__device__ __forceinline__ void norm_store_rows_q(const PrefillParams& p, int t0, int u, const bf16x8 raw[8],
+                                                  const float* wn, float eps, bf16_t* dst) {
+    const int r = u >> 2, c0 = 64 * (u & 3);
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const bf16x2 x2 = {raw[j][2 * e], raw[j][2 * e + 1]};
+            ss = __builtin_amdgcn_fdot2_f32_bf16(x2, x2, ss, false);
+        }
+    ss += dpp<0xB1>(ss);
+    ss += dpp<0x4E>(ss);
+    const float rs = t0 + r < p.T ? rsqrtf(ss * (1.f / KD) + eps) : 0.f;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {  // weights read four groups at a time
+        float4 wq[4][2];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            wq[j][0] = *reinterpret_cast<const float4*>(wn + c0 + 32 * h + 8 * j);
+            wq[j][1] = *reinterpret_cast<const float4*>(wn + c0 + 32 * h + 8 * j + 4);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float wv[8] = {wq[j][0].x, wq[j][0].y, wq[j][0].z, wq[j][0].w,
+                                 wq[j][1].x, wq[j][1].y, wq[j][1].z, wq[j][1].w};
+            bf16x8 o;
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[e] = (bf16_t)((float)raw[4 * h + j][e] * (rs * wv[e]));
+            *reinterpret_cast<bf16x8*>(dst + L::off(r, c0 + 32 * h + 8 * j)) = o;
+        }
+    }
+}
+
 // Slot-weight rows [t0, t0 + 64) of the readout output (256-byte rows), same
 // thread mapping.
 __device__ __forceinline__ void issue_omega(rsrc_t om_rows, int t0, bf16x8 om[2]) {
@@ -408,25 +454,35 @@ __device__ __forceinline__ void store_half_rows(const bf16x8 raw[2], int valid, 
 // The hardware gives (cos, sin) of pair 8 w and of pair 1; the next pairs
 // follow by complex multiplication, i.e. rotation by theta (seven steps add
 // about 1e-6 to a result rounded to bf16).
-template <class L>
-__device__ __forceinline__ void store_write_tile(const GateRegs& gr, int valid, bf16_t* dst) {
-    const int lane = threadIdx.x & 63, w = wave_id();
+// NW waves share the tile (wave g of the group covers pairs 64 / NW g ..).
+template <class L, int NW = 8>
+__device__ __forceinline__ void store_write_tile(const GateRegs& gr, int valid, bf16_t* dst, int g) {
+    constexpr int NP = 64 / NW;  // pairs per wave
+    const int lane = threadIdx.x & 63;
     const float beta = lane < valid ? gr.beta : 0.f;
     float s1, c1, sn, cs;
     pair_sincos(gr.lamr, 1, s1, c1);
-    pair_sincos(gr.lamr, 8 * w, sn, cs);
-    bf16x8 o[2];
+    pair_sincos(gr.lamr, NP * g, sn, cs);
 #pragma unroll
-    for (int q = 0; q < 8; q++) {
-        const float a = beta * pair_scale(8 * w + q);
-        o[q >> 2][2 * (q & 3)] = (bf16_t)(a * cs);
-        o[q >> 2][2 * (q & 3) + 1] = (bf16_t)(-a * sn);
-        const float cn = cs * c1 - sn * s1;
-        sn = sn * c1 + cs * s1;
-        cs = cn;
+    for (int h = 0; h < NP / 8; h++) {
+        bf16x8 o[2];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const float a = beta * pair_scale(NP * g + 8 * h + q);
+            o[q >> 2][2 * (q & 3)] = (bf16_t)(a * cs);
+            o[q >> 2][2 * (q & 3) + 1] = (bf16_t)(-a * sn);
+            const float cn = cs * c1 - sn * s1;
+            sn = sn * c1 + cs * s1;
+            cs = cn;
+        }
+        *reinterpret_cast<bf16x8*>(dst + L::off(lane, 2 * NP * g + 16 * h)) = o[0];
+        *reinterpret_cast<bf16x8*>(dst + L::off(lane, 2 * NP * g + 16 * h + 8)) = o[1];
     }
-    *reinterpret_cast<bf16x8*>(dst + L::off(lane, 16 * w)) = o[0];
-    *reinterpret_cast<bf16x8*>(dst + L::off(lane, 16 * w + 8)) = o[1];
+}
+
+template <class L>
+__device__ __forceinline__ void store_write_tile(const GateRegs& gr, int valid, bf16_t* dst) {
+    store_write_tile<L, 8>(gr, valid, dst, wave_id());
 }
 
 // The 10 causal 16 x 16 score blocks (query block tb >= key block sb): wave w
@@ -884,21 +940,33 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
                      [&](int kb, int c, int i) { return (HALF * y + state_row(kb, lg, i)) * kSlots + 32 * mq + 16 * c + lr; },
                      acc);
     const Seq sq = make_seq(p, b, h, bh);
-    bf16x8 qraw[4], kraw[4];
+    // Staging is split between the halves: every wave normalises its share of
+    // q at the top of a chunk; the waves of the second half (u = tid - 256)
+    // load and stage k_hat, the write-vector tile and the gates of the next
+    // chunk while the first half runs the chunk's slot readout.
+    const int u = tid - 256;
+    bf16x8 qraw[4], kraw[8];
+    GateRegs gr{};
     issue_rows(sq, sq.q, p.T, n0 * 64, qraw);
-    issue_rows(sq, sq.k, p.T, n0 * 64, kraw);
-    GateRegs gr = issue_gates(sq, p.T, n0 * 64);
+    if (y == 1) {
+        issue_rows_q(sq, sq.k, p.T, n0 * 64, u, kraw);
+        gr = issue_gates(sq, p.T, n0 * 64);
+    }
     StateScale sc;
-    __syncthreads();  // norm weights staged, score tiles zeroed
+    __syncthreads();  // norm weights and table staged, score tiles zeroed
+    if (y == 1) {
+        sc.begin_chunk(chunk_last_gam(gr));
+        commit_gates(p, n0 * 64, gr, sLam, sBeta, sGam, sc.inv(), 4);
+        store_write_tile<TileW, 4>(gr, p.T - n0 * 64, sW, mq);
+        norm_store_rows_q<TileF>(p, n0 * 64, u, kraw, sKw, p.k_eps, sK);
+    }
 
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
-        sc.begin_chunk(chunk_last_gam(gr));
-        commit_gates(p, t0, gr, sLam, sBeta, sGam, sc.inv());
-        store_write_tile<TileW>(gr, p.T - t0, sW);
         norm_store_rows<TileQ>(p, t0, qraw, sQw, p.q_eps, sQ);
-        norm_store_rows<TileF>(p, t0, kraw, sKw, p.k_eps, sK);
         __syncthreads();
+        // The second half has taken this chunk's scale step while staging it.
+        if (y == 0) sc.begin_chunk(sGam[63]);
         // The next chunk's loads are spread over the phases (q here, k and the
         // gates after the scores) so that no wave waits at a barrier for the
         // CU's memory pipeline to accept them.
@@ -931,10 +999,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
             out[tb][1] *= f;
         }
         __syncthreads();  // scores complete
-        if (n + 1 < n1) {
-            issue_rows(sq, sq.k, p.T, t0 + 64, kraw);
-            gr = issue_gates(sq, p.T, t0 + 64);
-        }
 
         // raw_y^T += w^T P_y^T (P carries the scale); the blocks of P above the diagonal are zero.
         // wf[c][ss][jj] = w[32 ss + 8 lg + jj][32 mq + 16 c + lr].
@@ -983,11 +1047,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
             }
         }
         sc.sig = sc.next;
-        __syncthreads();  // output tiles complete
-        // Slot readout of the chunk: wave mq of the first half takes tokens 16 mq .. 16 mq + 15.
-        if (y == 0)
-            readout_tokens(sR0 + 16 * mq * RR, sR1 + 16 * mq * RR, sTab, sLam[16 * mq + lr],
+        const float lamr = sLam[16 * mq + lr];
+        __syncthreads();  // output tiles complete; k_hat, w and the gates of this chunk are done with
+        if (y == 0) {
+            // Slot readout of the chunk: wave mq takes tokens 16 mq .. 16 mq + 15.
+            readout_tokens(sR0 + 16 * mq * RR, sR1 + 16 * mq * RR, sTab, lamr,
                            p.omega + ((size_t)bh * p.Tp + t0 + 16 * mq + lr) * kSlots);
+        } else if (n + 1 < n1) {
+            // The readout outlasts these loads; their latency is hidden behind it.
+            issue_rows_q(sq, sq.k, p.T, t0 + 64, u, kraw);
+            gr = issue_gates(sq, p.T, t0 + 64);
+            sc.begin_chunk(chunk_last_gam(gr));
+            commit_gates(p, t0 + 64, gr, sLam, sBeta, sGam, sc.inv(), 4);
+            store_write_tile<TileW, 4>(gr, p.T - t0 - 64, sW, mq);
+            norm_store_rows_q<TileF>(p, t0 + 64, u, kraw, sKw, p.k_eps, sK);
+        }
         __syncthreads();  // tiles are overwritten by the next chunk
     }
 
