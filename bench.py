@@ -44,7 +44,7 @@ STATE_BYTES_PER_BH = 524_288       # fp32 hk + hv, read and written, K = V = 256
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
 # scaled by a 1 GiB copy kernel (profiles/cyfa_chunk_fwd_cfg3_prefill.md,
 # profiles/cyfa_decode_step_cfg4.md); they apply to the default shapes.
-TRAFFIC_PREFILL_BYTES = 578.2e6    # one cyfa_chunk_fwd at B=8, T=2048, H=4
+TRAFFIC_PREFILL_BYTES = 302.2e6    # one cyfa_chunk_fwd at B=8, T=2048, H=4
 TRAFFIC_DECODE_BYTES = 135.5e6     # one decode launch at B=64, H=4
 
 
@@ -297,7 +297,7 @@ def main():
             "parallelism": "single-gpu",
         },
         "roofline": {
-            "kernel": "cyfa_chunk_fwd (clock, segment states, carry, pass 1 + readout, pass 2)",
+            "kernel": "cyfa_chunk_fwd (clock, segment states, pass 1 with the slot readout, pass 2)",
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,
