@@ -1,12 +1,13 @@
 // cyfa_prefill.hip -- chunkwise two-pass CyFA prefill for gfx950 (K = V = 256, M = 128).
 //
 // Pipeline for one call (all kernels on the caller's stream):
-//   1. clock_kernel     lam_t = clock0 + sum_{s<=t} delta_s, final clock.
-//   2. segment_state    (only when a sequence is split into P > 1 segments)
-//                       segment-local end states E_j of both passes from a
-//                       zero start, and the product a_j of alpha over each
+//   1. segment_state    the clock lam_t = clock0 + sum_{s<=t} delta_s and the
+//                       in-chunk decay scan of every token, the final clock,
+//                       and (when a sequence is split into P > 1 segments)
+//                       the segment-local end states E_j of both passes from
+//                       a zero start and the product a_j of alpha over each
 //                       segment.
-//   3. pass1_kernel     per segment: start from the carried state
+//   2. pass1_kernel     per segment: start from the carried state
 //                       S_j = sum_{i<j} (prod_{i<l<j} a_l) E_i + (prod_{l<j} a_l) h0,
 //                       then sweep the segment's 64-token chunks with the
 //                       fp32 key state [256 x 128] held in registers; each
@@ -15,7 +16,7 @@
 //                       z = U(lam) raw; p = softmax(table z); u = table^T p;
 //                       slot weights bf16(U(-lam) u) (ops/chunk_readout.py:797-909),
 //                       which are written for pass 2.
-//   4. pass2_kernel     per segment: the same carry and sweep for the value state
+//   3. pass2_kernel     per segment: the same carry and sweep for the value state
 //                       [128 x 256] with query = slot weights, key = w,
 //                       value = v -> o (bf16).
 // The pass-1 output is formed as two 128-wide key slices, each scaled and
@@ -135,7 +136,7 @@ __device__ __forceinline__ void st_b64(rsrc_t r, uint32_t off, uint32_t soff, bf
 // H * 512 bytes apart, beta H * 4 bytes apart, the per-token reduced clock
 // and decay scan of the workspace contiguous.
 struct Seq {
-    rsrc_t q, k, v, o, beta, lam, gam;
+    rsrc_t q, k, v, o, beta, delta, g, lam, gam;
     uint32_t row16, row4;
 };
 
@@ -148,6 +149,8 @@ __device__ __forceinline__ Seq make_seq(const PrefillParams& p, int b, int h, in
     s.v = make_rsrc(p.v + first * VD, span * VD * 2);
     s.o = make_rsrc(p.o + first * VD, span * VD * 2);
     s.beta = make_rsrc(p.beta + first, span * 4);
+    s.delta = make_rsrc(p.delta + first, span * 4);
+    s.g = make_rsrc(p.g + first, span * 4);
     s.lam = make_rsrc(p.lam + (size_t)bh * p.Tp, (size_t)p.Tp * 4);
     s.gam = make_rsrc(p.gam + (size_t)bh * p.Tp, (size_t)p.Tp * 4);
     s.row16 = (uint32_t)p.H * KD * 2;
@@ -549,25 +552,85 @@ __device__ __forceinline__ bf16x4 to_bf16x4(const f32x4& x, float s) {
 }
 
 // ---------------------------------------------------------------------------
-// 1. Clock scan and in-chunk decay scan. One block (512 threads) per (batch,
-// head), 2048 tokens per step, four consecutive tokens per thread:
-//   lam[t] = reduced_clock(clock0 + sum_{s<=t} delta_s)   (double carry across steps)
-//   gam[t] = log2(e) sum_{chunk start <= s <= t} g_s       (ops/utils.py:495-520)
-// The 16 threads of a 64-token chunk form one DPP row.
+// Clock and in-chunk decay scan (ops/utils.py:229-348, 495-520):
+//   lam[t] = reduced_clock(clock0 + sum_{s<=t} delta_s)
+//   gam[t] = log2(e) sum_{chunk start <= s <= t} g_s
+// They are formed inside segment_state: every workgroup starts from the
+// clock before its first chunk (a double sum over the earlier tokens) and
+// carries it in double from chunk to chunk; the state workgroups scan each
+// chunk with lane = token, and one extra workgroup per sequence covers the
+// last segment (all of the sequence when P = 1) and writes the final clock.
 template <int CTRL>
 __device__ __forceinline__ float dpp_shift(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
 
-constexpr int CLOCK_THREADS = 512;
+// clock0 + sum_{s < t_end} delta_s, summed in double by the workgroup (512
+// threads) in a fixed order, so every workgroup of a sequence gets the same bits.
+__device__ __forceinline__ double clock_before(const PrefillParams& p, int b, int h, int bh, int t_end) {
+    __shared__ double part[8];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    double acc = 0.0;
+    const int te = min(t_end, p.T);
+    for (int t = tid; t < te; t += 512) acc += (double)p.delta[tok_index(p, b, t, h)];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (lane == 0) part[w] = acc;
+    __syncthreads();
+    double tot = p.clock0 ? (double)p.clock0[bh] : 0.0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) tot += part[i];
+    __syncthreads();
+    return tot;
+}
 
-__global__ __launch_bounds__(CLOCK_THREADS) void clock_kernel(PrefillParams p) {
-    constexpr int NW = CLOCK_THREADS / 64;
-    const int bh = blockIdx.x, b = bh / p.H, h = bh % p.H;
+// Raw gate inputs of one chunk, lane = token (loads only; see finish_gates).
+struct GateIn {
+    float d, g, beta;
+};
+
+__device__ __forceinline__ GateIn load_gate_inputs(const Seq& sq, int T, int t0) {
+    const int t = t0 + (threadIdx.x & 63);
+    const uint32_t off = (uint32_t)(t < T ? t : T - 1) * sq.row4;
+    GateIn r;
+    r.d = t < T ? ld_f32(sq.delta, off) : 0.f;
+    r.g = t < T ? ld_f32(sq.g, off) : 0.f;
+    r.beta = ld_f32(sq.beta, off);
+    return r;
+}
+
+// Inclusive scan over the 64 lanes of a wave by DPP: row_shr 1, 2, 4, 8 within
+// each 16-lane row, then row_bcast 15 (rows 1, 3) and row_bcast 31 (rows 2, 3).
+__device__ __forceinline__ float wave_scan(float x) {
+    x += dpp_shift<0x111>(x);
+    x += dpp_shift<0x112>(x);
+    x += dpp_shift<0x114>(x);
+    x += dpp_shift<0x118>(x);
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x142, 0xA, 0xF, false));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x143, 0xC, 0xF, false));
+    return x;
+}
+
+// Inclusive scans over the chunk's 64 lanes; clock advances by the chunk's sum of delta.
+__device__ __forceinline__ GateRegs finish_gates(const GateIn& r, double& clock) {
+    const float sd = wave_scan(r.d), sg = wave_scan(r.g);
+    GateRegs out;
+    out.beta = r.beta;
+    out.lamr = reduced_clock((float)(clock + (double)sd));
+    out.gam = sg * kLog2e;
+    clock += (double)__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sd), 63));
+    return out;
+}
+
+// The clock of tokens [t_begin, Tp) from the clock `carry` before t_begin
+// (t_begin a multiple of 64), 2048 tokens per step, four consecutive tokens
+// per thread; writes lam / gam and the final clock. The 16 threads of a
+// 64-token chunk form one DPP row.
+__device__ __forceinline__ void clock_scan(const PrefillParams& p, int bh, int b, int h, int t_begin, double carry) {
+    constexpr int NW = 8;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     __shared__ float s_tot[NW];
-    double carry = p.clock0 ? (double)p.clock0[bh] : 0.0;
-    for (int t0 = 0; t0 < p.Tp; t0 += 4 * CLOCK_THREADS) {
+    for (int t0 = t_begin; t0 < p.Tp; t0 += 4 * 512) {
         float d[4], gg[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -617,7 +680,7 @@ __global__ __launch_bounds__(CLOCK_THREADS) void clock_kernel(PrefillParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// 2. Segment-local end states from a zero start. grid = (H, B, 2 (P-1)), 512
+// 1. Segment-local end states from a zero start. grid = (H, B, 2 (P-1)), 512
 // threads, blockIdx.z = 2 j + part; state blocks as in frag_offset. part 0: key state, rows 128 y ..,
 // y = w >> 2, columns 32 (w & 3) ..; part 1: value state, columns 32 w ...
 constexpr int SG_A = 0;                     // k_hat (key) or v (value), TileF
@@ -650,15 +713,21 @@ __device__ __forceinline__ void segment_state_body(const PrefillParams& p, int b
 #pragma unroll
     for (int x = 0; x < 8; x++) acc[x][0] = acc[x][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     const Seq sq = make_seq(p, b, h, bh);
-    GateRegs gr = issue_gates(sq, p.T, n0 * 64);
+    GateIn gin = load_gate_inputs(sq, p.T, n0 * 64);
     bf16x8 raw[4];
     issue_rows(sq, KEY ? sq.k : sq.v, p.T, n0 * 64, raw);
     if (KEY && tid < KD) sNw[tid] = p.k_w[tid];
+    double clock = clock_before(p, b, h, bh, n0 * 64);  // its loads overlap the ones above
     float logdecay = 0.f;
     StateScale sc;
     __syncthreads();
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
+        const GateRegs gr = finish_gates(gin, clock);
+        if (KEY && w == 0) {  // the sweeps read the key part's copy
+            p.lam[(size_t)bh * p.Tp + t0 + lane] = gr.lamr;
+            p.gam[(size_t)bh * p.Tp + t0 + lane] = gr.gam;
+        }
         sc.begin_chunk(chunk_last_gam(gr));
         commit_gates(p, t0, gr, sLam, sBeta, sGam, sc.inv());
         store_write_tile<TileW>(gr, p.T - t0, sB);
@@ -669,7 +738,7 @@ __device__ __forceinline__ void segment_state_body(const PrefillParams& p, int b
         __syncthreads();
         if (n + 1 < n1) {
             issue_rows(sq, KEY ? sq.k : sq.v, p.T, t0 + 64, raw);
-            gr = issue_gates(sq, p.T, t0 + 64);
+            gin = load_gate_inputs(sq, p.T, t0 + 64);
         }
         logdecay += sGam[63];
         if (sc.fold != 1.f) {
@@ -733,8 +802,15 @@ __device__ __forceinline__ void segment_state_body(const PrefillParams& p, int b
 
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void segment_state_kernel(PrefillParams p) {
     __shared__ __align__(16) unsigned char smem[SG_LDS];
-    const SegCoord cd = seg_coord(p.H, blockIdx.z >> 1);
-    if ((blockIdx.z & 1) == 0)
+    const int z = blockIdx.z;
+    if (z == 2 * (p.P - 1)) {  // clock of the last segment
+        const SegCoord cd = seg_coord(p.H, p.P - 1);
+        const int t_begin = (p.P - 1) * p.L * 64;
+        clock_scan(p, cd.bh, cd.b, cd.h, t_begin, clock_before(p, cd.b, cd.h, cd.bh, t_begin));
+        return;
+    }
+    const SegCoord cd = seg_coord(p.H, z >> 1);
+    if ((z & 1) == 0)
         segment_state_body<true>(p, cd.bh, cd.j, cd.b, cd.h, smem);
     else
         segment_state_body<false>(p, cd.bh, cd.j, cd.b, cd.h, smem);
@@ -880,7 +956,7 @@ __device__ __forceinline__ void readout_tokens(const bf16_t* sR0, const bf16_t* 
 }
 
 // ---------------------------------------------------------------------------
-// 4. Pass 1 (key state) and the slot readout, one segment per workgroup.
+// 2. Pass 1 (key state) and the slot readout, one segment per workgroup.
 // grid = (H, B, P), 512 threads.
 // Wave w works on key half y = w >> 2 and state columns [32 mq, 32 mq + 32),
 // mq = w & 3: acc[kb][c] = S[128 y + state_row(kb, lg, i)][32 mq + 16 c + lr],
@@ -1078,7 +1154,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 }
 
 // ---------------------------------------------------------------------------
-// 5. Pass 2 (value state), one segment per workgroup. grid = (H, B, P), 512
+// 3. Pass 2 (value state), one segment per workgroup. grid = (H, B, P), 512
 // threads. Wave w owns value columns [32 w, 32 w + 32):
 // acc[mb][c] = S[state_row(mb, lg, i)][32 w + 16 c + lr], and the same 32 output
 // coordinates: out[tb][c] = o^T[32 w + 16 c + 4 lg + i][16 tb + lr].
@@ -1277,9 +1353,7 @@ WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V) {
 }
 
 int launch_prefill(const PrefillParams& p, hipStream_t stream) {
-    const int BH = p.B * p.H;
-    hipLaunchKernelGGL(clock_kernel, dim3(BH), dim3(CLOCK_THREADS), 0, stream, p);
-    if (p.P > 1) hipLaunchKernelGGL(segment_state_kernel, dim3(p.H, p.B, 2 * (p.P - 1)), dim3(512), 0, stream, p);
+    hipLaunchKernelGGL(segment_state_kernel, dim3(p.H, p.B, 2 * (p.P - 1) + 1), dim3(512), 0, stream, p);
     hipLaunchKernelGGL(pass1_kernel, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
     hipLaunchKernelGGL(pass2_kernel, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
     return 0;
