@@ -63,6 +63,11 @@ def parse():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--decode-kernel-only", action="store_true",
                     help="only time the fused decode kernel at the decode shape (for hardware-counter runs)")
+    ap.add_argument("--no-tuned-gemms", action="store_true",
+                    help="leave the library GEMMs on their default solutions")
+    ap.add_argument("--tune-gemms", metavar="FILE",
+                    help="time the GEMM solutions of every shape this run executes and write the "
+                         "selections to FILE (TunableOp results; see cyclic_flow_attention/gemm_tuning.py)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="run one fp32 copy kernel (out = 1.0 * in) of this many MiB before the prefill, "
                          "as the known-size reference for HBM byte counters")
@@ -253,6 +258,14 @@ def main():
         log(f"decode kernel: 24 launches at B={args.decode_batch}, H=4, one state each")
         return 0
     log(f"device {torch.cuda.get_device_name(dev)}")
+    from cyclic_flow_attention import gemm_tuning
+
+    if args.tune_gemms:
+        gemm_tuning.tune_gemms(args.tune_gemms)
+        log(f"GEMM solutions: tuning, selections to {args.tune_gemms}")
+    elif not args.no_tuned_gemms:
+        used = gemm_tuning.use_tuned_gemms()
+        log(f"GEMM solutions: {'TunableOp selections ' + str(gemm_tuning.DEFAULT_FILE.name) if used else 'library defaults'}")
     config, model = build_model(args.config, dev)
     H = config.num_heads
     gen = torch.Generator().manual_seed(0)
