@@ -159,16 +159,15 @@ __device__ __forceinline__ Seq make_seq(const PrefillParams& p, int b, int h, in
 }
 
 // Segment states in the workspace are kept in the register order of the
-// sweeps: the four values that lane `lane` of wave w holds as accumulator
-// block (x, c) sit at element offset frag_offset(w, x, c, lane), so a wave
-// loads or stores a block as one contiguous run. Wave w, x = 0..7, c = 0..1,
-// element i holds (see load_tr_perm for the row order)
+// sweeps: the eight values that lane `lane` of wave w holds as accumulator
+// blocks (x, 0) and (x, 1) sit at element offset frag_offset(w, x, lane) (16
+// bytes per lane), so a wave loads or stores a block pair as one contiguous
+// 1 KiB run. Element 4 c + i of the run holds (see load_tr_perm for the row
+// order)
 //   key state   S[128 (w >> 2) + state_row(x, lg, i)][32 (w & 3) + 16 c + lr]
 //   value state S[state_row(x, lg, i)][32 w + 16 c + lr].
 // The key state fills [0, SEG_K), the value state [SEG_K, SEG).
-__host__ __device__ constexpr int frag_offset(int w, int x, int c, int lane) {
-    return (((w * 8 + x) * 2 + c) * 64 + lane) * 4;
-}
+__host__ __device__ constexpr int frag_offset(int w, int x, int lane) { return ((w * 8 + x) * 64 + lane) * 8; }
 
 // Row (within a 128-row half) of element i of state block x in a lane of row
 // group lg.
@@ -790,12 +789,14 @@ __device__ __forceinline__ void segment_state_body(const PrefillParams& p, int b
     const size_t slot = (size_t)bh * (p.P - 1) + j;
     _Float16* out = p.seg + slot * SEG + (KEY ? 0 : SEG_K);
 #pragma unroll
-    for (int x = 0; x < 8; x++)
+    for (int x = 0; x < 8; x++) {
+        f16x8 v;
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-            const f32x4 v = acc[x][c] * f;
-            *reinterpret_cast<f16x4*>(out + frag_offset(w, x, c, lane)) = f16x4{(f16_t)v[0], (f16_t)v[1], (f16_t)v[2], (f16_t)v[3]};
-        }
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[4 * c + i] = (f16_t)(acc[x][c][i] * f);
+        *reinterpret_cast<f16x8*>(out + frag_offset(w, x, lane)) = v;
+    }
     if (lane == 0) p.seg_exp[(slot * 2 + (KEY ? 0 : 1)) * 8 + w] = e;
     if (KEY && tid == 0) p.seg_decay[bh * p.P + j] = exp2f(logdecay);
 }
@@ -831,23 +832,33 @@ __device__ __forceinline__ void load_start_state(const PrefillParams& p, int bh,
     const int lane = threadIdx.x & 63, w = wave_id();
 #pragma unroll
     for (int x = 0; x < 8; x++) acc[x][0] = acc[x][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float a = 1.f;
-    for (int i = j - 1; i >= 0; i--) {
-        const size_t slot = (size_t)bh * (p.P - 1) + i;
-        const _Float16* e = p.seg + slot * SEG + part * SEG_K;
-        const float ai = ldexpf(a, p.seg_exp[(slot * 2 + part) * 8 + w]);
-        f16x4 v[8][2];
+    const _Float16* seg = p.seg + (size_t)bh * (p.P - 1) * SEG + part * SEG_K;
+    const int* seg_exp = p.seg_exp + (size_t)bh * (p.P - 1) * 16 + part * 8 + w;
+    // E_i for i = j - 1 down to 0; the loads of E_{i-1} are in flight while E_i is added.
+    f16x8 v[8];
+    if (j > 0) {
 #pragma unroll
         for (int x = 0; x < 8; x++)
+            v[x] = *reinterpret_cast<const f16x8*>(seg + (size_t)(j - 1) * SEG + frag_offset(w, x, lane));
+    }
+    float a = 1.f;
+    for (int i = j - 1; i >= 0; i--) {
+        f16x8 nv[8];
+        if (i > 0) {
 #pragma unroll
-            for (int c = 0; c < 2; c++) v[x][c] = *reinterpret_cast<const f16x4*>(e + frag_offset(w, x, c, lane));
+            for (int x = 0; x < 8; x++)
+                nv[x] = *reinterpret_cast<const f16x8*>(seg + (size_t)(i - 1) * SEG + frag_offset(w, x, lane));
+        }
+        const float ai = ldexpf(a, seg_exp[i * 16]);
 #pragma unroll
         for (int x = 0; x < 8; x++)
 #pragma unroll
             for (int c = 0; c < 2; c++)
 #pragma unroll
-                for (int q = 0; q < 4; q++) acc[x][c][q] = fmaf(ai, (float)v[x][c][q], acc[x][c][q]);
+                for (int q = 0; q < 4; q++) acc[x][c][q] = fmaf(ai, (float)v[x][4 * c + q], acc[x][c][q]);
         a *= p.seg_decay[bh * p.P + i];
+#pragma unroll
+        for (int x = 0; x < 8; x++) v[x] = nv[x];
     }
     if (h0) {
 #pragma unroll
@@ -1000,21 +1011,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         sQw[tid] = p.q_w[tid];
         sKw[tid] = p.k_w[tid];
     }
-    {
-        const float* tb = p.table + (size_t)h * kActive * kSlots;
-        for (int idx = tid; idx < 128 * 32; idx += 512) {
-            const int r = idx >> 5, m4 = (idx & 31) * 4;
-            const float4 v = r < kActive ? *reinterpret_cast<const float4*>(tb + r * kSlots + m4)
-                                         : make_float4(0.f, 0.f, 0.f, 0.f);
-            *reinterpret_cast<f16x4*>(sTab + r * RS + m4) = f16x4{(f16_t)v.x, (f16_t)v.y, (f16_t)v.z, (f16_t)v.w};
-        }
-    }
-    zero_scores(sP, 2);  // the two blocks above the diagonal that the intra product reads stay zero
-    bf16_t* sPy = sP + y * (TileP::bytes / 2);
-    f32x4 acc[8][2];
-    load_start_state(p, bh, j, 0, p.h0_k ? p.h0_k + (size_t)bh * SEG_K : nullptr,
-                     [&](int kb, int c, int i) { return (HALF * y + state_row(kb, lg, i)) * kSlots + 32 * mq + 16 * c + lr; },
-                     acc);
     const Seq sq = make_seq(p, b, h, bh);
     // Staging is split between the halves: every wave normalises its share of
     // q at the top of a chunk; the waves of the second half (u = tid - 256)
@@ -1023,11 +1019,34 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     const int u = tid - 256;
     bf16x8 qraw[4], kraw[8];
     GateRegs gr{};
+    // The first chunk's loads and the table's are issued before the start
+    // state is summed, so that their latency overlaps it.
     issue_rows(sq, sq.q, p.T, n0 * 64, qraw);
     if (y == 1) {
         issue_rows_q(sq, sq.k, p.T, n0 * 64, u, kraw);
         gr = issue_gates(sq, p.T, n0 * 64);
     }
+    {
+        const float* tb = p.table + (size_t)h * kActive * kSlots;
+        float4 tv[8];
+#pragma unroll
+        for (int it = 0; it < 8; it++) {
+            const int idx = tid + 512 * it, r = idx >> 5, m4 = (idx & 31) * 4;
+            tv[it] = r < kActive ? *reinterpret_cast<const float4*>(tb + r * kSlots + m4) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int it = 0; it < 8; it++) {
+            const int idx = tid + 512 * it, r = idx >> 5, m4 = (idx & 31) * 4;
+            *reinterpret_cast<f16x4*>(sTab + r * RS + m4) =
+                f16x4{(f16_t)tv[it].x, (f16_t)tv[it].y, (f16_t)tv[it].z, (f16_t)tv[it].w};
+        }
+    }
+    zero_scores(sP, 2);  // the two blocks above the diagonal that the intra product reads stay zero
+    bf16_t* sPy = sP + y * (TileP::bytes / 2);
+    f32x4 acc[8][2];
+    load_start_state(p, bh, j, 0, p.h0_k ? p.h0_k + (size_t)bh * SEG_K : nullptr,
+                     [&](int kb, int c, int i) { return (HALF * y + state_row(kb, lg, i)) * kSlots + 32 * mq + 16 * c + lr; },
+                     acc);
     StateScale sc;
     __syncthreads();  // norm weights and table staged, score tiles zeroed
     if (y == 1) {
@@ -1180,17 +1199,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     const int bh = cd.bh, j = cd.j, b = cd.b, h = cd.h;
     const int lane = threadIdx.x & 63, w = wave_id(), lr = lane & 15, lg = lane >> 4;
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
-    zero_scores(sP, 1);
-    f32x4 acc[8][2];
-    load_start_state(p, bh, j, 1, p.h0_v ? p.h0_v + (size_t)bh * SEG_V : nullptr,
-                     [&](int mb, int c, int i) { return state_row(mb, lg, i) * VD + 32 * w + 16 * c + lr; }, acc);
     const Seq sq = make_seq(p, b, h, bh);
     const rsrc_t rom = make_rsrc(p.omega + (size_t)bh * p.Tp * kSlots, (size_t)p.Tp * kSlots * 2);
     const uint32_t o_lane = (uint32_t)lr * sq.row16 + 2 * (32 * w + 4 * lg);
+    // The first chunk's loads are issued before the start state is summed.
     bf16x8 vraw[4], om[2];
     issue_rows(sq, sq.v, p.T, n0 * 64, vraw);
     issue_omega(rom, n0 * 64, om);
     GateRegs gr = issue_gates(sq, p.T, n0 * 64);
+    zero_scores(sP, 1);
+    f32x4 acc[8][2];
+    load_start_state(p, bh, j, 1, p.h0_v ? p.h0_v + (size_t)bh * SEG_V : nullptr,
+                     [&](int mb, int c, int i) { return state_row(mb, lg, i) * VD + 32 * w + 16 * c + lr; }, acc);
     StateScale sc;
 
     for (int n = n0; n < n1; n++) {
