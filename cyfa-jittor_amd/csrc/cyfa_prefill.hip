@@ -886,6 +886,20 @@ constexpr int RR = 128 + 8;  // row stride of the pass-1 output tiles in LDS
 __device__ __forceinline__ void readout_tokens(const bf16_t* sR0, const bf16_t* sR1, const f16_t* sTab, float lamr,
                                                bf16_t* dst) {
     const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
+    // Phases: the hardware gives (cos, sin) of pairs 1, 8, 16 and of the
+    // lane's first pair of each group; the others follow by rotation (complex
+    // multiplication), at most six steps for z and eight for the weights,
+    // each adding about 1e-7 to values that are rounded to fp16 / bf16.
+    float s1, c1, s16, c16;
+    pair_sincos(lamr, 1, s1, c1);
+    pair_sincos(lamr, 16, s16, c16);
+    float zs[4], zc[4];  // pairs 4 lg + q, then 16 ks + 4 lg + q
+    pair_sincos(lamr, 4 * lg, zs[0], zc[0]);
+#pragma unroll
+    for (int q = 1; q < 4; q++) {
+        zc[q] = zc[q - 1] * c1 - zs[q - 1] * s1;
+        zs[q] = zs[q - 1] * c1 + zc[q - 1] * s1;
+    }
     // z fragments: element j = z_t[32 ks + 8 lg + j].
     f16x8 zf[4];
 #pragma unroll
@@ -896,10 +910,13 @@ __device__ __forceinline__ void readout_tokens(const bf16_t* sR0, const bf16_t* 
         for (int q = 0; q < 4; q++) {
             const float e = (float)ra[2 * q] + (float)rb[2 * q];
             const float o = (float)ra[2 * q + 1] + (float)rb[2 * q + 1];
-            float sn, cs;
-            pair_sincos(lamr, 16 * ks + 4 * lg + q, sn, cs);
+            const float sn = zs[q], cs = zc[q];
             zf[ks][2 * q] = (f16_t)(cs * e - sn * o);
             zf[ks][2 * q + 1] = (f16_t)(sn * e + cs * o);
+            if (ks < 3) {
+                zc[q] = cs * c16 - sn * s16;
+                zs[q] = sn * c16 + cs * s16;
+            }
         }
     }
     f32x4 L[8];
@@ -951,16 +968,24 @@ __device__ __forceinline__ void readout_tokens(const bf16_t* sR0, const bf16_t* 
         sched_fence();
     }
     // Lane holds u_t[16 mb + 4 lg + i]: pairs 8 mb + 2 lg + q, q = 0, 1.
+    float s8, c8, ws[2], wc[2];
+    pair_sincos(lamr, 8, s8, c8);
+    pair_sincos(lamr, 2 * lg, ws[0], wc[0]);
+    wc[1] = wc[0] * c1 - ws[0] * s1;
+    ws[1] = ws[0] * c1 + wc[0] * s1;
 #pragma unroll
     for (int mb = 0; mb < 8; mb++) {
         bf16x4 o;
 #pragma unroll
         for (int q = 0; q < 2; q++) {
-            float sn, cs;
-            pair_sincos(lamr, 8 * mb + 2 * lg + q, sn, cs);
+            const float sn = ws[q], cs = wc[q];
             const float ue = U[mb][2 * q], uo = U[mb][2 * q + 1];
             o[2 * q] = (bf16_t)(cs * ue + sn * uo);
             o[2 * q + 1] = (bf16_t)(cs * uo - sn * ue);
+            if (mb < 7) {
+                wc[q] = cs * c8 - sn * s8;
+                ws[q] = sn * c8 + cs * s8;
+            }
         }
         *reinterpret_cast<bf16x4*>(dst + 16 * mb + 4 * lg) = o;
     }
