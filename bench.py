@@ -11,8 +11,9 @@ Workload (BASELINE.json metric; configs 3 and 4):
            (argmax on the device). Reported under "decode".
 Weights are seeded N(0, 0.02) random init (no checkpoints offline).
 
-roofline: HIP events around every cyfa_chunk_fwd launch in the timed prefill
-region give its average device duration; the decode kernel's duration comes
+roofline: HIP events around every prefill attention launch in the timed
+prefill region (cyfa_chunk_fwd_normed: the op with the layer's gated output
+norm in its last kernel) give its average device duration; the decode kernel's duration comes
 from HIP events around replays of a graph of in-place decode launches at the
 decode shape (B=64, H=4), free of host launch gaps;
   prefill attention: 377 088 algorithmic FLOP per token*head / duration vs the
@@ -108,7 +109,8 @@ def time_prefill(model, ids, steps, warmup):
             torch.cuda.synchronize()
             elapsed = time.perf_counter() - start
         del out
-    return elapsed, timer.results().get("cyfa_chunk_fwd", [])
+    res = timer.results()
+    return elapsed, res.get("cyfa_chunk_fwd_normed", []) + res.get("cyfa_chunk_fwd", [])
 
 
 def time_decode(model, prompt, steps, warmup):
@@ -310,7 +312,8 @@ def main():
             "parallelism": "single-gpu",
         },
         "roofline": {
-            "kernel": "cyfa_chunk_fwd (clock, segment states, pass 1 with the slot readout, pass 2)",
+            "kernel": "cyfa_chunk_fwd_normed (segment states, pass 1 with the slot readout, "
+                      "pass 2 with the gated output norm); FLOP of the attention op only",
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,

@@ -95,7 +95,9 @@ int cyfa_decode_step(const CyfaDecodeArgs* a, void* hip_stream) {
     return check_launch("cyfa_decode_step");
 }
 
-int cyfa_chunk_fwd(const CyfaChunkArgs* a, void* hip_stream) {
+namespace {
+
+int chunk_fwd(const CyfaChunkArgs* a, const CyfaOutNormArgs* on, void* hip_stream) {
     if (!a) return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd: null args");
     if (a->M != 128) return fail(CYFA_ERR_UNSUPPORTED, "cyfa_chunk_fwd: num_slots must be 128, got %d", a->M);
     if (a->C != 64) return fail(CYFA_ERR_UNSUPPORTED, "cyfa_chunk_fwd: chunk_size must be 64, got %d", a->C);
@@ -124,6 +126,14 @@ int cyfa_chunk_fwd(const CyfaChunkArgs* a, void* hip_stream) {
         return fail(CYFA_ERR_WORKSPACE, "cyfa_chunk_fwd: workspace of %zu bytes needed, got %zu", ws.total,
                     a->workspace ? a->workspace_bytes : (size_t)0);
     if (!aligned(a->workspace, 256)) return fail(CYFA_ERR_ALIGN, "cyfa_chunk_fwd: workspace needs 256-byte alignment");
+    if (on) {
+        if (!on->weight || !on->gate) return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd_normed: null weight or gate");
+        if (!aligned(on->weight, 16) || !aligned(on->gate, 16))
+            return fail(CYFA_ERR_ALIGN, "cyfa_chunk_fwd_normed: weight and gate need 16-byte alignment");
+        if (!(on->eps >= 0.f) || !isfinite(on->eps) || !isfinite(on->prescale))
+            return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd_normed: eps=%g prescale=%g", (double)on->eps,
+                        (double)on->prescale);
+    }
 
     cyfa::PrefillParams p;
     p.B = a->B;
@@ -154,6 +164,10 @@ int cyfa_chunk_fwd(const CyfaChunkArgs* a, void* hip_stream) {
     p.hk = a->hk;
     p.hv = a->hv;
     p.clock = a->clock;
+    p.on_w = on ? on->weight : nullptr;
+    p.on_gate = on ? (const __bf16*)on->gate : nullptr;
+    p.on_eps = on ? on->eps : 0.f;
+    p.on_prescale = on ? on->prescale : 1.f;
     char* base = (char*)a->workspace;
     p.lam = (float*)(base + ws.lam);
     p.gam = (float*)(base + ws.gam);
@@ -162,7 +176,16 @@ int cyfa_chunk_fwd(const CyfaChunkArgs* a, void* hip_stream) {
     p.seg_decay = (float*)(base + ws.seg_decay);
     p.omega = (__bf16*)(base + ws.omega);
     cyfa::launch_prefill(p, (hipStream_t)hip_stream);
-    return check_launch("cyfa_chunk_fwd");
+    return check_launch(on ? "cyfa_chunk_fwd_normed" : "cyfa_chunk_fwd");
+}
+
+}  // namespace
+
+int cyfa_chunk_fwd(const CyfaChunkArgs* a, void* hip_stream) { return chunk_fwd(a, nullptr, hip_stream); }
+
+int cyfa_chunk_fwd_normed(const CyfaChunkArgs* a, const CyfaOutNormArgs* norm, void* hip_stream) {
+    if (!norm) return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd_normed: null norm args");
+    return chunk_fwd(a, norm, hip_stream);
 }
 
 int cyfa_rms_norm(const CyfaNormArgs* a, void* hip_stream) {

@@ -123,6 +123,13 @@ __device__ __forceinline__ float write_coord(float lamr, float beta, int m) {
     return (m & 1) ? -a * __builtin_amdgcn_sinf(rev) : a * __builtin_amdgcn_cosf(rev);
 }
 
+// 1 / (1 + e^-x) with the hardware exponential and reciprocal (v_exp_f32,
+// v_rcp_f32, each within 1 ulp): a relative error of a few 1e-7, far below the
+// bf16 rounding of every result it feeds. Saturates to 0 / 1 for large |x|.
+__device__ __forceinline__ float sigmoidf(float x) {
+    return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
+
 template <int W = 64>
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll

@@ -33,6 +33,11 @@ struct PrefillParams {
     const float *h0_k, *h0_v, *clock0;
     __bf16* o;
     float *hk, *hv, *clock;
+    // Optional gated output norm applied to o in the pass-2 epilogue (on_w null: none):
+    //   xs = bf16(bf16(o) * on_prescale); o = bf16(xs * rsqrt(mean_V xs^2 + on_eps) * on_w * sigmoid(on_gate))
+    const float* on_w;       // f32 [V]
+    const __bf16* on_gate;   // bf16 [B, T, H, V]
+    float on_eps, on_prescale;
     // workspace
     float* lam;        // [B*H, Tp] reduced clock per token, (lam mod 127) / 127
     float* gam;        // [B*H, Tp] in-chunk inclusive scan of g, log2 units

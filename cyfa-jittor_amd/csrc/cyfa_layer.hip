@@ -12,8 +12,6 @@ namespace {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + expf(-x)); }
-
 // One wave per row; lane covers columns 4 lane + 256 j.
 // (layers/cyfa.py:62-135 and modeling_cyfa.py:48-51)
 //   s   = residual ? bf16(x + residual) : x      (sum_out receives s)

@@ -128,6 +128,10 @@ __device__ __forceinline__ float ld_f32(rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 
+__device__ __forceinline__ bf16x4 ld_b64(rsrc_t r, uint32_t off, uint32_t soff) {
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(r, off, soff, 0));
+}
+
 __device__ __forceinline__ void st_b64(rsrc_t r, uint32_t off, uint32_t soff, bf16x4 v) {
     __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, off, soff, 0);
 }
@@ -140,14 +144,21 @@ struct Seq {
     uint32_t row16, row4;
 };
 
+// The 256-wide rows (b, t, h), t < T, of a [B, T, H, 256] bf16 tensor, row t at byte t * H * 512.
+__device__ __forceinline__ rsrc_t rows_rsrc(const PrefillParams& p, int b, int h, const bf16_t* x) {
+    const size_t first = (size_t)b * p.T * p.H + h;     // token row of (b, 0, h)
+    const size_t span = ((size_t)(p.T - 1) * p.H + 1);  // rows up to (b, T - 1, h)
+    return make_rsrc(x + first * 256, span * 256 * 2);
+}
+
 __device__ __forceinline__ Seq make_seq(const PrefillParams& p, int b, int h, int bh) {
-    const size_t first = (size_t)b * p.T * p.H + h;              // token row of (b, 0, h)
-    const size_t span = ((size_t)(p.T - 1) * p.H + 1);           // rows up to (b, T - 1, h)
+    const size_t first = (size_t)b * p.T * p.H + h;
+    const size_t span = ((size_t)(p.T - 1) * p.H + 1);
     Seq s;
-    s.q = make_rsrc(p.q + first * KD, span * KD * 2);
-    s.k = make_rsrc(p.k + first * KD, span * KD * 2);
-    s.v = make_rsrc(p.v + first * VD, span * VD * 2);
-    s.o = make_rsrc(p.o + first * VD, span * VD * 2);
+    s.q = rows_rsrc(p, b, h, p.q);
+    s.k = rows_rsrc(p, b, h, p.k);
+    s.v = rows_rsrc(p, b, h, p.v);
+    s.o = rows_rsrc(p, b, h, p.o);
     s.beta = make_rsrc(p.beta + first, span * 4);
     s.delta = make_rsrc(p.delta + first, span * 4);
     s.g = make_rsrc(p.g + first, span * 4);
@@ -1207,9 +1218,16 @@ constexpr int P2_W = P2_OM + TileO::bytes;   // w (key), TileW
 constexpr int P2_V = P2_W + TileW::bytes;    // v, TileF
 constexpr int P2_P = P2_V + TileF::bytes;    // masked scores, TileP
 constexpr int P2_G = P2_P + TileP::bytes;    // f32 [5][64] gates
-constexpr int P2_LDS = P2_G + 5 * 64 * 4;
+constexpr int P2_N = P2_G + 5 * 64 * 4;      // output norm: f32 [64][8] partial sums of squares, f32 [256] weight
+constexpr int P2_LDS = P2_N + (64 * 8 + VD) * 4;
 static_assert(P2_LDS <= 160 * 1024, "pass-2 workgroup must fit in one CU's LDS");
 
+// NORM: the gated output norm (on_w, on_gate) is applied before o is stored.
+// Each lane's eight coordinates of a token are rounded and scaled (xs), their
+// squares summed over the lane's row group and written per wave to LDS; the
+// per-token totals are read back after the chunk's last barrier, where the
+// normalised, gated output is stored.
+template <bool NORM>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void pass2_kernel(PrefillParams p) {
     __shared__ __align__(16) unsigned char smem[P2_LDS];
     bf16_t* sOm = reinterpret_cast<bf16_t*>(smem + P2_OM);
@@ -1219,11 +1237,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     float* sLam = reinterpret_cast<float*>(smem + P2_G);
     float* sBeta = sLam + 64;
     float* sGam = sBeta + 64;
+    float* sNs = reinterpret_cast<float*>(smem + P2_N);  // [token][wave]
+    float* sNw = sNs + 64 * 8;
 
     const SegCoord cd = seg_coord(p.H, blockIdx.z);
     const int bh = cd.bh, j = cd.j, b = cd.b, h = cd.h;
     const int lane = threadIdx.x & 63, w = wave_id(), lr = lane & 15, lg = lane >> 4;
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
+    if (NORM && threadIdx.x < VD) sNw[threadIdx.x] = p.on_w[threadIdx.x];
     const Seq sq = make_seq(p, b, h, bh);
     const rsrc_t rom = make_rsrc(p.omega + (size_t)bh * p.Tp * kSlots, (size_t)p.Tp * kSlots * 2);
     const uint32_t o_lane = (uint32_t)lr * sq.row16 + 2 * (32 * w + 4 * lg);
@@ -1277,6 +1298,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
             issue_rows(sq, sq.v, p.T, t0 + 64, vraw);
             gr = issue_gates(sq, p.T, t0 + 64);
         }
+        bf16x4 gate[4][2];  // gate of the output coordinates of this lane (NORM)
+        if constexpr (NORM) {
+            const rsrc_t rg = rows_rsrc(p, b, h, p.on_gate);
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+                for (int c = 0; c < 2; c++) gate[tb][c] = ld_b64(rg, o_lane + 32 * c, (uint32_t)(t0 + 16 * tb) * sq.row16);
+        }
 
         // o^T += v^T P^T. vb[c][ss][jj] = v[32 ss + 8 lg + jj][32 w + 16 c + lr].
         bf16x8 vb[2][2];
@@ -1292,12 +1321,33 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
                 out[tb][0] = mfma_bf16(vb[0][ss], pf, out[tb][0]);
                 out[tb][1] = mfma_bf16(vb[1][ss], pf, out[tb][1]);
             }
+        bf16x4 xs[4][2];  // NORM: bf16(bf16(o) * prescale)
+        if constexpr (NORM) {
 #pragma unroll
-        for (int tb = 0; tb < 4; tb++) {
-            if (t0 + 16 * tb + lr < p.T) {
+            for (int tb = 0; tb < 4; tb++) {
+                float ss = 0.f;
 #pragma unroll
-                for (int c = 0; c < 2; c++)
-                    st_b64(sq.o, o_lane + 32 * c, (uint32_t)(t0 + 16 * tb) * sq.row16, to_bf16x4(out[tb][c], 1.f));
+                for (int c = 0; c < 2; c++) {
+                    const bf16x4 o4 = to_bf16x4(out[tb][c], 1.f);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        xs[tb][c][i] = (bf16_t)((float)o4[i] * p.on_prescale);
+                        const float x = (float)xs[tb][c][i];
+                        ss = fmaf(x, x, ss);
+                    }
+                }
+                ss += __shfl_xor(ss, 16);
+                ss += __shfl_xor(ss, 32);
+                if (lg == 0) sNs[(16 * tb + lr) * 8 + w] = ss;
+            }
+        } else {
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++) {
+                if (t0 + 16 * tb + lr < p.T) {
+#pragma unroll
+                    for (int c = 0; c < 2; c++)
+                        st_b64(sq.o, o_lane + 32 * c, (uint32_t)(t0 + 16 * tb) * sq.row16, to_bf16x4(out[tb][c], 1.f));
+                }
             }
         }
         // State update: S = 2^G_last S + w^T bf16(2^(G_last - G_s) v), as
@@ -1326,6 +1376,27 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         }
         sc.sig = sc.next;
         __syncthreads();
+        if constexpr (NORM) {
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++) {
+                const float4 s0 = *reinterpret_cast<const float4*>(sNs + (16 * tb + lr) * 8);
+                const float4 s1 = *reinterpret_cast<const float4*>(sNs + (16 * tb + lr) * 8 + 4);
+                const float tot = ((s0.x + s0.y) + (s0.z + s0.w)) + ((s1.x + s1.y) + (s1.z + s1.w));
+                const float rs = rsqrtf(tot * (1.f / VD) + p.on_eps);
+                if (t0 + 16 * tb + lr < p.T) {
+#pragma unroll
+                    for (int c = 0; c < 2; c++) {
+                        const float4 wv = *reinterpret_cast<const float4*>(sNw + 32 * w + 16 * c + 4 * lg);
+                        const float wa[4] = {wv.x, wv.y, wv.z, wv.w};
+                        bf16x4 y;
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            y[i] = (bf16_t)((float)xs[tb][c][i] * rs * wa[i] * sigmoidf((float)gate[tb][c][i]));
+                        st_b64(sq.o, o_lane + 32 * c, (uint32_t)(t0 + 16 * tb) * sq.row16, y);
+                    }
+                }
+            }
+        }
     }
 
     if (j == p.P - 1 && p.hv) {
@@ -1400,7 +1471,10 @@ WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V) {
 int launch_prefill(const PrefillParams& p, hipStream_t stream) {
     hipLaunchKernelGGL(segment_state_kernel, dim3(p.H, p.B, 2 * (p.P - 1) + 1), dim3(512), 0, stream, p);
     hipLaunchKernelGGL(pass1_kernel, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
-    hipLaunchKernelGGL(pass2_kernel, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
+    if (p.on_w)
+        hipLaunchKernelGGL(pass2_kernel<true>, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
+    else
+        hipLaunchKernelGGL(pass2_kernel<false>, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
     return 0;
 }
 

@@ -38,6 +38,10 @@ class CyfaChunkArgs(ctypes.Structure):
     ]
 
 
+class CyfaOutNormArgs(ctypes.Structure):
+    _fields_ = [("weight", _c_void_p), ("gate", _c_void_p), ("eps", _c_float), ("prescale", _c_float)]
+
+
 class CyfaDecodeArgs(ctypes.Structure):
     _fields_ = [
         ("B", _c_int), ("H", _c_int), ("K", _c_int), ("V", _c_int), ("M", _c_int),
@@ -74,6 +78,7 @@ class CyfaConvArgs(ctypes.Structure):
 # Every symbol include/cyfa_abi.h declares, with its ctypes signature.
 SIGNATURES = {
     "cyfa_chunk_fwd": (_c_int, [ctypes.POINTER(CyfaChunkArgs), _c_void_p]),
+    "cyfa_chunk_fwd_normed": (_c_int, [ctypes.POINTER(CyfaChunkArgs), ctypes.POINTER(CyfaOutNormArgs), _c_void_p]),
     "cyfa_chunk_workspace_bytes": (_c_size_t, [_c_int] * 7),
     "cyfa_decode_step": (_c_int, [ctypes.POINTER(CyfaDecodeArgs), _c_void_p]),
     "cyfa_readout_table": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
@@ -198,6 +203,14 @@ def chunk_fwd(args: CyfaChunkArgs, device):
     rc = _timed("cyfa_chunk_fwd", lambda: lib.cyfa_chunk_fwd(ctypes.byref(args), stream_handle(device)))
     if rc != CYFA_OK:
         _raise(rc, "cyfa_chunk_fwd failed")
+
+
+def chunk_fwd_normed(args: CyfaChunkArgs, norm: CyfaOutNormArgs, device):
+    lib = load_library()
+    rc = _timed("cyfa_chunk_fwd_normed",
+                lambda: lib.cyfa_chunk_fwd_normed(ctypes.byref(args), ctypes.byref(norm), stream_handle(device)))
+    if rc != CYFA_OK:
+        _raise(rc, "cyfa_chunk_fwd_normed failed")
 
 
 def decode_step(args: CyfaDecodeArgs, device):

@@ -326,13 +326,17 @@ class CyclicFlowAttention(nn.Module):
             initial_state=None if cache is None else cache["recurrent_state"],
             output_final_state=use_cache,
         )
+        gate = self.g_proj(x).view(B, T, H, self.head_v_dim)
         if not self.training and T == 1:
             o, state = fused_recurrent_cyfa(**kwargs, table=self.readout_table(),
                                             inplace=self.decode_in_place and cache is not None)
+            o = self.o_norm(o, gate, prescale=float(self.num_slots - 1)).view(B, T, Dv)
         else:
-            o, state = chunk_cyfa(**kwargs, chunk_size=self.chunk_size, table=self.readout_table())
-        gate = self.g_proj(x).view(B, T, H, self.head_v_dim)
-        o = self.o_norm(o, gate, prescale=float(self.num_slots - 1)).view(B, T, Dv)
+            # the gated output norm runs in the prefill's last kernel
+            o, state = chunk_cyfa(**kwargs, chunk_size=self.chunk_size, table=self.readout_table(),
+                                  output_norm=(self.o_norm.weight, gate, self.o_norm.eps,
+                                               float(self.num_slots - 1)))
+            o = o.view(B, T, Dv)
         o = self.o_proj(o)
         new_cache = {"recurrent_state": state, "conv_state": (cq, ck, cv)} if use_cache else None
         return o, new_cache

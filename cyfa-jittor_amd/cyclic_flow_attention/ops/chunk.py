@@ -34,6 +34,7 @@ def chunk_cyfa(
     chunk_size=64,
     *,
     table=None,
+    output_norm=None,
 ):
     """Chunkwise Cyclic Flow Attention.
 
@@ -43,6 +44,10 @@ def chunk_cyfa(
     (key_state [B,H,K,M], value_state [B,H,M,V], clock [B,H]), all fp32.
     ``table`` (keyword only, not in the reference signature) is a precomputed
     readout @ Phi [H, M-1, M] fp32; when None it is formed from ``readout``.
+    ``output_norm`` (keyword only, an extension) is ``(weight [V], gate
+    [B, T, H, V] bf16, eps, prescale)``: the layer's gated output norm
+    bf16(xs rsqrt(mean xs^2 + eps) weight sigmoid(gate)), xs = bf16(o prescale),
+    is then applied inside the kernels and its result returned in place of o.
     """
     if cu_seqlens is not None:
         raise NotImplementedError("packed layout requires native segment dispatch")
@@ -97,5 +102,19 @@ def chunk_cyfa(
         o=o.data_ptr(), hk=_native.ptr(hk), hv=_native.ptr(hv), clock=_native.ptr(clock),
         workspace=workspace.data_ptr(), workspace_bytes=ws_bytes,
     )
-    _native.chunk_fwd(args, dev)
+    if output_norm is None:
+        _native.chunk_fwd(args, dev)
+    else:
+        on_w, on_gate, on_eps, on_prescale = output_norm
+        on_w = on_w.detach().to(torch.float32).contiguous()
+        if tuple(on_w.shape) != (V,):
+            raise ValueError(f"output_norm weight must have shape ({V},), got {tuple(on_w.shape)}")
+        on_gate = on_gate.reshape(B, T, H, V)
+        if on_gate.dtype != torch.bfloat16:
+            raise NotImplementedError(f"output_norm gate must be bfloat16, got {on_gate.dtype}")
+        on_gate = on_gate.contiguous()
+        _native.require_device(on_w, on_gate)
+        norm = _native.CyfaOutNormArgs(weight=on_w.data_ptr(), gate=on_gate.data_ptr(), eps=float(on_eps),
+                                       prescale=float(on_prescale))
+        _native.chunk_fwd_normed(args, norm, dev)
     return o, ((hk, hv, clock) if output_final_state else None)

@@ -71,6 +71,22 @@ typedef struct CyfaChunkArgs {
  * C (ops/chunk.py:198-207) is handled inside the kernels. */
 int cyfa_chunk_fwd(const CyfaChunkArgs *args, void *hip_stream);
 
+/* Gated output norm of the layer (the o_norm(o * (num_slots - 1), gate) of
+ * layers/cyfa.py:349-350, the same arithmetic as cyfa_rms_norm with D = V):
+ *   xs = bf16(o * prescale);  o' = bf16(xs * rsqrt(mean(xs^2) + eps) * weight * sigmoid(gate)) */
+typedef struct CyfaOutNormArgs {
+    const float *weight;          /* f32 [V] */
+    const void *gate;             /* bf16 [B,T,H,V] */
+    float eps, prescale;
+} CyfaOutNormArgs;
+
+/* cyfa_chunk_fwd followed by the layer's gated output norm, applied in the
+ * pass-2 epilogue before o is written, so that o' is written once and o never
+ * reaches HBM. Replaces chunk_cyfa (ops/chunk.py:164-353) together with the
+ * RMSNorm.execute call on its output (layers/cyfa.py:62-135, 349-350). args->o
+ * receives o'. */
+int cyfa_chunk_fwd_normed(const CyfaChunkArgs *args, const CyfaOutNormArgs *norm, void *hip_stream);
+
 /* Workspace bytes cyfa_chunk_fwd needs for these dimensions (the reference
  * allocates the equivalent intermediates through Jittor, ops/chunk.py:244-336). */
 size_t cyfa_chunk_workspace_bytes(int B, int T, int H, int K, int V, int M, int C);
@@ -119,7 +135,7 @@ typedef struct CyfaNormArgs {
 } CyfaNormArgs;
 
 /* Replaces RMSNorm.execute / RMSNorm._inference (layers/cyfa.py:62-135; the
- * gated form is the o_norm(o * (num_slots - 1), gate) of layers/cyfa.py:351)
+ * gated form is the o_norm(o * (num_slots - 1), gate) of layers/cyfa.py:350)
  * and the residual adds of CyFABlock.execute (modeling_cyfa.py:48-51). */
 int cyfa_rms_norm(const CyfaNormArgs *args, void *hip_stream);
 

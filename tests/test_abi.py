@@ -45,6 +45,7 @@ def _c_layout(tmp_path, struct, fields):
 
 @pytest.mark.parametrize("cls,name", [(_native.CyfaChunkArgs, "CyfaChunkArgs"),
                                       (_native.CyfaDecodeArgs, "CyfaDecodeArgs"),
+                                      (_native.CyfaOutNormArgs, "CyfaOutNormArgs"),
                                       (_native.CyfaNormArgs, "CyfaNormArgs"),
                                       (_native.CyfaConvArgs, "CyfaConvArgs")])
 def test_struct_layout_matches_header(tmp_path, cls, name):

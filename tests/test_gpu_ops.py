@@ -226,3 +226,34 @@ def test_prefix_chunk_then_decode():
     assert_close(torch.cat(outs, 1), full[:, 64:].float(), what="prefix+decode o")
     for a, b, n in zip(st, stf, ("hk", "hv", "clock")):
         assert_close(a, b.double(), what=f"prefix+decode {n}")
+
+
+@pytest.mark.parametrize("B,T,H,seg", [(1, 130, 2, "1"), (2, 333, 2, None), (1, 2048, 4, None)])
+def test_chunk_output_norm_equals_separate_norm(B, T, H, seg, monkeypatch):
+    """The gated output norm in the pass-2 epilogue (cyfa_chunk_fwd_normed)
+    against cyfa_chunk_fwd followed by cyfa_rms_norm on the same inputs: the
+    same roundings, so results differ only where the per-token sum of squares,
+    added in another order, moves a value across a bf16 rounding boundary."""
+    from cyclic_flow_attention import _native
+    from cyclic_flow_attention.ops import chunk_cyfa
+
+    if seg is not None:
+        monkeypatch.setenv("CYFA_SEGMENT_CHUNKS", seg)
+    x, init = _inputs(B, T, H, seed=5 * T + B, state=True)
+    xg, ig = _gpu(x, init)
+    gen = torch.Generator().manual_seed(T)
+    gate = (2 * torch.randn(B, T, H, 256, generator=gen)).bfloat16().to(DEV)
+    weight = (1 + 0.2 * torch.randn(256, generator=gen)).to(DEV)
+    with torch.no_grad():
+        o, st = chunk_cyfa(**xg, initial_state=ig, output_final_state=True)
+        ref = _native.rms_norm(o, weight, 1e-6, gate, prescale=127.0)
+        on, stn = chunk_cyfa(**xg, initial_state=ig, output_final_state=True,
+                             output_norm=(weight, gate, 1e-6, 127.0))
+    torch.cuda.synchronize()
+    for a, b in zip(st, stn):
+        assert torch.equal(a, b)
+    a, b = on.float(), ref.float()
+    ulp = torch.ldexp(torch.ones_like(b), torch.frexp(b)[1] - 8)  # one bf16 ulp of the reference value
+    diff = (a - b).abs()
+    assert (diff <= ulp).all(), f"max diff {diff.max().item()}"
+    assert (diff > 0).float().mean().item() < 1e-2
