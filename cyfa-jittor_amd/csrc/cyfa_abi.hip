@@ -188,6 +188,57 @@ int cyfa_chunk_fwd_normed(const CyfaChunkArgs* a, const CyfaOutNormArgs* norm, v
     return chunk_fwd(a, norm, hip_stream);
 }
 
+size_t cyfa_scalar_la_workspace_bytes(int B, int T, int H, int K, int V) {
+    if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0) return 0;
+    return cyfa::sla_workspace_layout(B, T, H, K, V).total;
+}
+
+int cyfa_scalar_la(const CyfaSlaArgs* a, void* hip_stream) {
+    if (!a) return fail(CYFA_ERR_VALUE, "cyfa_scalar_la: null args");
+    if (!((a->K == 256 && a->V == 128) || (a->K == 128 && a->V == 256)))
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_scalar_la: (K, V) = (%d, %d), supported are (256, 128) and (128, 256)",
+                    a->K, a->V);
+    if (a->B <= 0 || a->T <= 0 || a->H <= 0 || a->T % 64 != 0)
+        return fail(CYFA_ERR_VALUE, "cyfa_scalar_la: B=%d H=%d must be positive and T=%d a positive multiple of 64",
+                    a->B, a->H, a->T);
+    if (!a->q || !a->k || !a->v || !a->g || !a->o) return fail(CYFA_ERR_VALUE, "cyfa_scalar_la: null required pointer");
+    if (!isfinite(a->scale)) return fail(CYFA_ERR_VALUE, "cyfa_scalar_la: scale must be finite, got %g", (double)a->scale);
+    if (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16) || !aligned(a->o, 16))
+        return fail(CYFA_ERR_ALIGN, "cyfa_scalar_la: q/k/v/o need 16-byte alignment");
+    if (!aligned(a->g, 4) || (a->initial && !aligned(a->initial, 4)) || (a->final_state && !aligned(a->final_state, 4)))
+        return fail(CYFA_ERR_ALIGN, "cyfa_scalar_la: g and the states need 4-byte alignment");
+    const cyfa::SlaWorkspaceLayout ws = cyfa::sla_workspace_layout(a->B, a->T, a->H, a->K, a->V);
+    if (!a->workspace || a->workspace_bytes < ws.total)
+        return fail(CYFA_ERR_WORKSPACE, "cyfa_scalar_la: workspace of %zu bytes needed, got %zu", ws.total,
+                    a->workspace ? a->workspace_bytes : (size_t)0);
+    if (!aligned(a->workspace, 256)) return fail(CYFA_ERR_ALIGN, "cyfa_scalar_la: workspace needs 256-byte alignment");
+    cyfa::SlaParams p;
+    p.B = a->B;
+    p.T = a->T;
+    p.H = a->H;
+    p.K = a->K;
+    p.V = a->V;
+    p.N = a->T / 64;
+    cyfa::choose_segments(p.B * p.H, p.N, &p.P, &p.L);
+    p.q = (const __bf16*)a->q;
+    p.k = (const __bf16*)a->k;
+    p.v = (const __bf16*)a->v;
+    p.g = a->g;
+    p.h0 = a->initial;
+    p.scale = a->scale;
+    p.v_bth = a->v_bth != 0;
+    p.o_bth = a->output_bth != 0;
+    p.raw_output = a->raw_output != 0;
+    p.o = a->o;
+    p.hfinal = a->final_state;
+    char* base = (char*)a->workspace;
+    p.seg = (_Float16*)(base + ws.seg);
+    p.seg_exp = (int*)(base + ws.seg_exp);
+    p.seg_decay = (float*)(base + ws.seg_decay);
+    cyfa::launch_scalar_la(p, (hipStream_t)hip_stream);
+    return check_launch("cyfa_scalar_la");
+}
+
 int cyfa_rms_norm(const CyfaNormArgs* a, void* hip_stream) {
     if (!a) return fail(CYFA_ERR_VALUE, "cyfa_rms_norm: null args");
     if (a->rows < 0 || a->D <= 0) return fail(CYFA_ERR_VALUE, "cyfa_rms_norm: rows=%d D=%d", a->rows, a->D);

@@ -48,6 +48,32 @@ struct PrefillParams {
     __bf16* omega;     // [B*H, Tp, 128] slot weights between the two passes
 };
 
+// Isolated ScalarGatedLA, one pass (scalar_la): every operand read from memory.
+// (K, V) is (256, 128) or (128, 256); T is a multiple of 64. Segments as in
+// the prefill, with one state part per segment.
+struct SlaParams {
+    int B, T, H, K, V;
+    int N, P, L;
+    const __bf16 *q, *k, *v;  // q, k [B, H, T, K]; v [B, H, T, V] or [B, T, H, V] (v_bth)
+    const float* g;           // [B, H, T] natural-log decay
+    const float* h0;          // nullable [B, H, K, V]
+    float scale;
+    int v_bth, o_bth, raw_output;
+    void* o;                  // [B, H, T, V] or [B, T, H, V] (o_bth); f32 if raw_output else bf16
+    float* hfinal;            // nullable [B, H, K, V]
+    // workspace
+    _Float16* seg;     // [B*H, P-1, K*V] segment-local end states (register order)
+    int* seg_exp;      // [B*H, P-1, 8]
+    float* seg_decay;  // [B*H, P]
+};
+
+struct SlaWorkspaceLayout {
+    size_t seg, seg_exp, seg_decay, total;
+};
+
+SlaWorkspaceLayout sla_workspace_layout(int B, int T, int H, int K, int V);
+int launch_scalar_la(const SlaParams& p, hipStream_t stream);
+
 // Layer-side kernels (cyfa_layer.hip).
 struct NormParams {
     int rows, D;

@@ -114,6 +114,7 @@ __device__ __forceinline__ SegCoord seg_coord(int H, int j) {
 // which keeps the address arithmetic out of the vector register budget.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, size_t bytes) {
     const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
@@ -222,13 +223,13 @@ __device__ __forceinline__ float chunk_last_gam(const GateRegs& r) {
 
 // inv: 1 / sigma of the state after this chunk's update (see StateScale).
 // Written by the wave whose index is `leader`.
-__device__ __forceinline__ void commit_gates(const PrefillParams& p, int t0, const GateRegs& r, float* sLam,
-                                             float* sBeta, float* sGam, float inv, int leader = 0) {
+__device__ __forceinline__ void commit_gates(int T, int t0, const GateRegs& r, float* sLam, float* sBeta, float* sGam,
+                                             float inv, int leader = 0) {
     const int lane = threadIdx.x & 63;
     if (wave_id() == leader) {
         const float last = chunk_last_gam(r);
         sGam[lane] = r.gam;
-        sBeta[lane] = t0 + lane < p.T ? r.beta : 0.f;
+        sBeta[lane] = t0 + lane < T ? r.beta : 0.f;
         sLam[lane] = r.lamr;
         sGam[64 + lane] = fast_exp2(r.gam);                // 2^G_t
         sGam[128 + lane] = fast_exp2(last - r.gam) * inv;  // 2^(G_last - G_t) / sigma'
@@ -334,11 +335,15 @@ __device__ __forceinline__ V8 load_row_ld(const T* X, int ld, int r0, int k0) {
 // 512-thread block: thread tid holds row tid >> 3, columns 64 q + 8 c .. + 8 in
 // raw[q] (q = 0..3, c = tid & 7). Rows past T are clamped to T - 1 (zeroed when
 // stored).
-__device__ __forceinline__ void issue_rows(const Seq& sq, rsrc_t x, int T, int t0, bf16x8 raw[4]) {
+__device__ __forceinline__ void issue_rows_stride(rsrc_t x, uint32_t row_bytes, int T, int t0, bf16x8 raw[4]) {
     const int t = t0 + (threadIdx.x >> 3);
-    const uint32_t off = (uint32_t)(t < T ? t : T - 1) * sq.row16 + 16 * (threadIdx.x & 7);
+    const uint32_t off = (uint32_t)(t < T ? t : T - 1) * row_bytes + 16 * (threadIdx.x & 7);
 #pragma unroll
     for (int q = 0; q < 4; q++) raw[q] = ld_b128(x, off + 128 * q);
+}
+
+__device__ __forceinline__ void issue_rows(const Seq& sq, rsrc_t x, int T, int t0, bf16x8 raw[4]) {
+    issue_rows_stride(x, sq.row16, T, t0, raw);
 }
 
 // x_hat = bf16(x rsqrt(mean x^2 + eps) w) over the full row (ops/qk_norm.py:64-107,
@@ -439,16 +444,22 @@ __device__ __forceinline__ void norm_store_rows_q(const PrefillParams& p, int t0
     }
 }
 
-// Slot-weight rows [t0, t0 + 64) of the readout output (256-byte rows), same
-// thread mapping.
-__device__ __forceinline__ void issue_omega(rsrc_t om_rows, int t0, bf16x8 om[2]) {
-    const uint32_t off = (uint32_t)(t0 + (threadIdx.x >> 3)) * (kSlots * 2) + 16 * (threadIdx.x & 7);
+// 128-wide rows [t0, t0 + 64) (row r at byte r * row_bytes): thread tid holds
+// row tid >> 3, columns 8 c + 64 it .. + 8 in raw[it] (c = tid & 7).
+__device__ __forceinline__ void issue_half_rows(rsrc_t x, uint32_t row_bytes, int t0, bf16x8 raw[2]) {
+    const uint32_t off = (uint32_t)(t0 + (threadIdx.x >> 3)) * row_bytes + 16 * (threadIdx.x & 7);
 #pragma unroll
-    for (int it = 0; it < 2; it++) om[it] = ld_b128(om_rows, off + 128 * it);
+    for (int it = 0; it < 2; it++) raw[it] = ld_b128(x, off + 128 * it);
 }
 
-// Store 64 x 128 rows held with that mapping into the TileO tile dst; rows at
-// or past `valid` are zeroed.
+// Slot-weight rows of the readout output (256-byte rows).
+__device__ __forceinline__ void issue_omega(rsrc_t om_rows, int t0, bf16x8 om[2]) {
+    issue_half_rows(om_rows, kSlots * 2, t0, om);
+}
+
+// Store 64 x 128 rows held with that mapping into the tile dst (layout L);
+// rows at or past `valid` are zeroed.
+template <class L = TileO>
 __device__ __forceinline__ void store_half_rows(const bf16x8 raw[2], int valid, bf16_t* dst) {
     const int r = threadIdx.x >> 3, c = threadIdx.x & 7;
 #pragma unroll
@@ -458,7 +469,7 @@ __device__ __forceinline__ void store_half_rows(const bf16x8 raw[2], int valid, 
 #pragma unroll
             for (int j = 0; j < 8; j++) o[j] = (bf16_t)0.f;
         }
-        *reinterpret_cast<bf16x8*>(dst + TileO::off(r, 8 * c + 64 * it)) = o;
+        *reinterpret_cast<bf16x8*>(dst + L::off(r, 8 * c + 64 * it)) = o;
     }
 }
 
@@ -689,6 +700,67 @@ __device__ __forceinline__ void clock_scan(const PrefillParams& p, int bh, int b
     if (p.clock && tid == 0) p.clock[bh] = (float)carry;
 }
 
+// One chunk's update of a segment sweep's state block: acc += A^T bf16(2^(G_last
+// - G_s) / sigma' B) for the 64 tokens staged in LDS (A rows from column a_col
+// of tile sArow, B columns from column b_col of tile sBcol, both token-major;
+// sGam[128 + s] = 2^(G_last - G_s) / sigma').
+// bt[c][jj] = B[32 ss + 8 lg + jj][b_col + 16 c + lr], scaled.
+template <class LA, class LB>
+__device__ __forceinline__ void chunk_state_update(const bf16_t* sArow, int a_col, const bf16_t* sBcol, int b_col,
+                                                   const float* sGam, f32x4 acc[8][2]) {
+    const int lg = (threadIdx.x & 63) >> 4;
+#pragma unroll
+    for (int ss = 0; ss < 2; ss++) {
+        bf16x8 bt[2];
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const bf16x8 f = load_tr<LB>(sBcol, 32 * ss, b_col + 16 * c);
+#pragma unroll
+            for (int jj = 0; jj < 8; jj++) bt[c][jj] = (bf16_t)((float)f[jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
+        }
+        sched_fence();
+#pragma unroll
+        for (int x = 0; x < 8; x++) {
+            const bf16x8 af = load_tr_perm<LA>(sArow, 32 * ss, a_col + 32 * (x >> 1), x & 1);
+            acc[x][0] = mfma_bf16(af, bt[0], acc[x][0]);
+            acc[x][1] = mfma_bf16(af, bt[1], acc[x][1]);
+            if (x & 1) sched_fence();
+        }
+    }
+}
+
+// Segment-local end state E = sigma acc of this wave's block, in fp16 at
+// out + frag_offset(w, .., lane), scaled by 2^-e so that the wave's largest |E|
+// is below 2^15 (fp16 keeps 11 bits, four times finer than the bf16 rounding
+// the state gets before each inter-chunk product); e goes to exp_out[w].
+__device__ __forceinline__ void store_segment_state(const f32x4 acc[8][2], float sig, _Float16* out, int* exp_out) {
+    const int lane = threadIdx.x & 63, w = wave_id();
+    float m = 0.f;
+#pragma unroll
+    for (int x = 0; x < 8; x++)
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) m = fmaxf(m, fabsf(acc[x][c][i]));
+    m = wave_max(m) * sig;
+    int e = 0;
+    if (m > 0.f && m < INFINITY) {
+        frexpf(m, &e);  // m < 2^e
+        e -= 15;
+    }
+    const float f = ldexpf(sig, -e);
+#pragma unroll
+    for (int x = 0; x < 8; x++) {
+        f16x8 v;
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[4 * c + i] = (f16_t)(acc[x][c][i] * f);
+        *reinterpret_cast<f16x8*>(out + frag_offset(w, x, lane)) = v;
+    }
+    if (lane == 0) exp_out[w] = e;
+}
+
 // ---------------------------------------------------------------------------
 // 1. Segment-local end states from a zero start. grid = (H, B, 2 (P-1)), 512
 // threads, blockIdx.z = 2 j + part; state blocks as in frag_offset. part 0: key state, rows 128 y ..,
@@ -715,7 +787,7 @@ __device__ __forceinline__ void segment_state_body(const PrefillParams& p, int b
     using LB = typename std::conditional<KEY, TileW, TileF>::type;
     const bf16_t* sArow = KEY ? sA : sB;
     const bf16_t* sBcol = KEY ? sB : sA;
-    const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), lg = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
     const int a_col = KEY ? HALF * (w >> 2) : 0;
     const int b_col = KEY ? 32 * (w & 3) : 32 * w;
@@ -739,7 +811,7 @@ __device__ __forceinline__ void segment_state_body(const PrefillParams& p, int b
             p.gam[(size_t)bh * p.Tp + t0 + lane] = gr.gam;
         }
         sc.begin_chunk(chunk_last_gam(gr));
-        commit_gates(p, t0, gr, sLam, sBeta, sGam, sc.inv());
+        commit_gates(p.T, t0, gr, sLam, sBeta, sGam, sc.inv());
         store_write_tile<TileW>(gr, p.T - t0, sB);
         if (KEY)
             norm_store_rows<TileF>(p, t0, raw, sNw, p.k_eps, sA);
@@ -758,57 +830,12 @@ __device__ __forceinline__ void segment_state_body(const PrefillParams& p, int b
                 acc[x][1] *= sc.fold;
             }
         }
-        // acc += A^T bf16(2^(G_last - G_s) / sigma' B): bt[c][jj] = B[32 ss + 8 lg + jj][b_col + 16 c + lr] scaled.
-#pragma unroll
-        for (int ss = 0; ss < 2; ss++) {
-            bf16x8 bt[2];
-#pragma unroll
-            for (int c = 0; c < 2; c++) {
-                const bf16x8 f = load_tr<LB>(sBcol, 32 * ss, b_col + 16 * c);
-#pragma unroll
-                for (int jj = 0; jj < 8; jj++) bt[c][jj] = (bf16_t)((float)f[jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
-            }
-            sched_fence();
-#pragma unroll
-            for (int x = 0; x < 8; x++) {
-                const bf16x8 af = load_tr_perm<LA>(sArow, 32 * ss, a_col + 32 * (x >> 1), x & 1);
-                acc[x][0] = mfma_bf16(af, bt[0], acc[x][0]);
-                acc[x][1] = mfma_bf16(af, bt[1], acc[x][1]);
-                if (x & 1) sched_fence();
-            }
-        }
+        chunk_state_update<LA, LB>(sArow, a_col, sBcol, b_col, sGam, acc);
         sc.sig = sc.next;
         __syncthreads();
     }
-    // E = sigma acc in fp16, scaled by 2^-e so that the wave's largest |E| is
-    // below 2^15 (fp16 keeps 11 bits, four times finer than the bf16 rounding
-    // the state gets before each inter-chunk product).
-    float m = 0.f;
-#pragma unroll
-    for (int x = 0; x < 8; x++)
-#pragma unroll
-        for (int c = 0; c < 2; c++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) m = fmaxf(m, fabsf(acc[x][c][i]));
-    m = wave_max(m) * sc.sig;
-    int e = 0;
-    if (m > 0.f && m < INFINITY) {
-        frexpf(m, &e);  // m < 2^e
-        e -= 15;
-    }
-    const float f = ldexpf(sc.sig, -e);
     const size_t slot = (size_t)bh * (p.P - 1) + j;
-    _Float16* out = p.seg + slot * SEG + (KEY ? 0 : SEG_K);
-#pragma unroll
-    for (int x = 0; x < 8; x++) {
-        f16x8 v;
-#pragma unroll
-        for (int c = 0; c < 2; c++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) v[4 * c + i] = (f16_t)(acc[x][c][i] * f);
-        *reinterpret_cast<f16x8*>(out + frag_offset(w, x, lane)) = v;
-    }
-    if (lane == 0) p.seg_exp[(slot * 2 + (KEY ? 0 : 1)) * 8 + w] = e;
+    store_segment_state(acc, sc.sig, p.seg + slot * SEG + (KEY ? 0 : SEG_K), p.seg_exp + (slot * 2 + (KEY ? 0 : 1)) * 8);
     if (KEY && tid == 0) p.seg_decay[bh * p.P + j] = exp2f(logdecay);
 }
 
@@ -837,20 +864,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
 // The segment workgroups of one sequence have block ids H * B apart; when
 // H * B is a multiple of 8 they are dealt to the same XCD, and most E_i reads
 // hit that XCD's L2.
+// seg: E_0 of this sequence and part (E_i at seg + i * seg_stride elements);
+// seg_exp: its wave exponents (E_i's at seg_exp + i * exp_stride); decay: a_0.
 template <typename H0Index>
-__device__ __forceinline__ void load_start_state(const PrefillParams& p, int bh, int j, int part, const float* h0,
+__device__ __forceinline__ void load_start_state(const _Float16* seg, size_t seg_stride, const int* seg_exp,
+                                                 int exp_stride, const float* decay, int j, const float* h0,
                                                  H0Index h0_index, f32x4 acc[8][2]) {
     const int lane = threadIdx.x & 63, w = wave_id();
 #pragma unroll
     for (int x = 0; x < 8; x++) acc[x][0] = acc[x][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const _Float16* seg = p.seg + (size_t)bh * (p.P - 1) * SEG + part * SEG_K;
-    const int* seg_exp = p.seg_exp + (size_t)bh * (p.P - 1) * 16 + part * 8 + w;
+    seg_exp += w;
     // E_i for i = j - 1 down to 0; the loads of E_{i-1} are in flight while E_i is added.
     f16x8 v[8];
     if (j > 0) {
 #pragma unroll
         for (int x = 0; x < 8; x++)
-            v[x] = *reinterpret_cast<const f16x8*>(seg + (size_t)(j - 1) * SEG + frag_offset(w, x, lane));
+            v[x] = *reinterpret_cast<const f16x8*>(seg + (size_t)(j - 1) * seg_stride + frag_offset(w, x, lane));
     }
     float a = 1.f;
     for (int i = j - 1; i >= 0; i--) {
@@ -858,16 +887,16 @@ __device__ __forceinline__ void load_start_state(const PrefillParams& p, int bh,
         if (i > 0) {
 #pragma unroll
             for (int x = 0; x < 8; x++)
-                nv[x] = *reinterpret_cast<const f16x8*>(seg + (size_t)(i - 1) * SEG + frag_offset(w, x, lane));
+                nv[x] = *reinterpret_cast<const f16x8*>(seg + (size_t)(i - 1) * seg_stride + frag_offset(w, x, lane));
         }
-        const float ai = ldexpf(a, seg_exp[i * 16]);
+        const float ai = ldexpf(a, seg_exp[i * exp_stride]);
 #pragma unroll
         for (int x = 0; x < 8; x++)
 #pragma unroll
             for (int c = 0; c < 2; c++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) acc[x][c][q] = fmaf(ai, (float)v[x][4 * c + q], acc[x][c][q]);
-        a *= p.seg_decay[bh * p.P + i];
+        a *= decay[i];
 #pragma unroll
         for (int x = 0; x < 8; x++) v[x] = nv[x];
     }
@@ -879,6 +908,15 @@ __device__ __forceinline__ void load_start_state(const PrefillParams& p, int bh,
 #pragma unroll
                 for (int q = 0; q < 4; q++) acc[x][c][q] = fmaf(a, h0[h0_index(x, c, q)], acc[x][c][q]);
     }
+}
+
+// The same for the two parts of a prefill call's segment states.
+template <typename H0Index>
+__device__ __forceinline__ void load_start_state(const PrefillParams& p, int bh, int j, int part, const float* h0,
+                                                 H0Index h0_index, f32x4 acc[8][2]) {
+    load_start_state(p.seg + (size_t)bh * (p.P - 1) * SEG + part * SEG_K, SEG,
+                     p.seg_exp + (size_t)bh * (p.P - 1) * 16 + part * 8, 16, p.seg_decay + bh * p.P, j, h0, h0_index,
+                     acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -1087,7 +1125,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     __syncthreads();  // norm weights and table staged, score tiles zeroed
     if (y == 1) {
         sc.begin_chunk(chunk_last_gam(gr));
-        commit_gates(p, n0 * 64, gr, sLam, sBeta, sGam, sc.inv(), 4);
+        commit_gates(p.T, n0 * 64, gr, sLam, sBeta, sGam, sc.inv(), 4);
         store_write_tile<TileW, 4>(gr, p.T - n0 * 64, sW, mq);
         norm_store_rows_q<TileF>(p, n0 * 64, u, kraw, sKw, p.k_eps, sK);
     }
@@ -1189,7 +1227,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
             issue_rows_q(sq, sq.k, p.T, t0 + 64, u, kraw);
             gr = issue_gates(sq, p.T, t0 + 64);
             sc.begin_chunk(chunk_last_gam(gr));
-            commit_gates(p, t0 + 64, gr, sLam, sBeta, sGam, sc.inv(), 4);
+            commit_gates(p.T, t0 + 64, gr, sLam, sBeta, sGam, sc.inv(), 4);
             store_write_tile<TileW, 4>(gr, p.T - t0 - 64, sW, mq);
             norm_store_rows_q<TileF>(p, t0 + 64, u, kraw, sKw, p.k_eps, sK);
         }
@@ -1262,7 +1300,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
         sc.begin_chunk(chunk_last_gam(gr));
-        commit_gates(p, t0, gr, sLam, sBeta, sGam, sc.inv());
+        commit_gates(p.T, t0, gr, sLam, sBeta, sGam, sc.inv());
         store_write_tile<TileW>(gr, p.T - t0, sW);
         store_half_rows(om, 64, sOm);
         store_rows<TileF>(vraw, p.T - t0, sV);
@@ -1431,6 +1469,424 @@ __global__ __launch_bounds__(128) void readout_table_kernel(const float* readout
     table[(size_t)hr * kSlots + m] = acc;
 }
 
+// ---------------------------------------------------------------------------
+// 4. Isolated ScalarGatedLA: one pass of scalar_la (ops/chunk.py:30-79 over
+// state_forward, ops/chunk_h.py:10-339, and output_forward, ops/chunk_o.py:177-613)
+//   S_{n+1} = 2^G_last S_n + k^T bf16(2^(G_last - G_s) v)
+//   o_t = scale (2^G_t q_t S_n + sum_{s <= t} bf16(2^(G_t - G_s) q_t . k_s) v_s)
+// with q, k, v and g read from memory and the in-chunk decay scan G formed on
+// the fly. Shape A: K = 256, V = 128 (the pass-1 shape; the output is formed
+// per 128-wide key slice, each slice scaled and rounded to bf16, and the slices
+// summed, as the reference's raw output accumulates them, ops/chunk_o.py:240-250);
+// shape B: K = 128, V = 256 (the pass-2 shape). Segments as in the prefill:
+// segment-local end states, then one sweep per segment from its carried start.
+
+// The streams of one (batch, head) sequence; row strides in bytes.
+struct SlaSeq {
+    rsrc_t q, k, v, o, g;
+    uint32_t rk, rv, ro;
+};
+
+__device__ __forceinline__ SlaSeq make_sla_seq(const SlaParams& p, int b, int h) {
+    const size_t bh = (size_t)b * p.H + h;
+    const size_t bth = (size_t)b * p.T * p.H + h;        // row (b, 0, h) of a [B, T, H, .] tensor
+    const size_t span = (size_t)(p.T - 1) * p.H + 1;     // its rows up to (b, T - 1, h)
+    SlaSeq s;
+    s.q = make_rsrc(p.q + bh * p.T * p.K, (size_t)p.T * p.K * 2);
+    s.k = make_rsrc(p.k + bh * p.T * p.K, (size_t)p.T * p.K * 2);
+    s.rk = p.K * 2;
+    s.v = p.v_bth ? make_rsrc(p.v + bth * p.V, span * p.V * 2) : make_rsrc(p.v + bh * p.T * p.V, (size_t)p.T * p.V * 2);
+    s.rv = (p.v_bth ? p.H : 1) * p.V * 2;
+    const size_t osz = p.raw_output ? 4 : 2;
+    char* o = reinterpret_cast<char*>(p.o);
+    s.o = p.o_bth ? make_rsrc(o + bth * p.V * osz, span * p.V * osz) : make_rsrc(o + bh * p.T * p.V * osz, (size_t)p.T * p.V * osz);
+    s.ro = (p.o_bth ? p.H : 1) * p.V * (uint32_t)osz;
+    s.g = make_rsrc(p.g + bh * p.T, (size_t)p.T * 4);
+    return s;
+}
+
+// G_t = log2(e) * (in-chunk inclusive sum of g) from the raw gate, lane = token
+// (ops/utils.py:495-520).
+__device__ __forceinline__ GateRegs sla_gates(float graw) {
+    GateRegs r;
+    r.beta = 0.f;
+    r.lamr = 0.f;
+    r.gam = wave_scan(graw) * kLog2e;
+    return r;
+}
+
+__device__ __forceinline__ void st_b128(rsrc_t r, uint32_t off, uint32_t soff, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, soff, 0);
+}
+
+// Segment-local end states, grid (H, B, P - 1), 512 threads; the state blocks of
+// the waves as in the prefill's key (shape A) or value (shape B) part.
+template <bool SA>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void sla_segment_kernel(SlaParams p) {
+    __shared__ __align__(16) unsigned char smem[SG_NW];
+    bf16_t* sF = reinterpret_cast<bf16_t*>(smem + SG_A);  // the 256-wide operand: k (A) or v (B), TileF
+    bf16_t* sH = reinterpret_cast<bf16_t*>(smem + SG_B);  // the 128-wide operand: v (A) or k (B), TileW
+    float* sLam = reinterpret_cast<float*>(smem + SG_G);
+    float* sBeta = sLam + 64;
+    float* sGam = sBeta + 64;
+    using LA = typename std::conditional<SA, TileF, TileW>::type;
+    using LB = typename std::conditional<SA, TileW, TileF>::type;
+    const bf16_t* sArow = SA ? sF : sH;
+    const bf16_t* sBcol = SA ? sH : sF;
+    const int h = blockIdx.x, b = blockIdx.y, j = blockIdx.z, bh = b * p.H + h;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+    const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
+    const int a_col = SA ? HALF * (w >> 2) : 0;
+    const int b_col = SA ? 32 * (w & 3) : 32 * w;
+    const SlaSeq sq = make_sla_seq(p, b, h);
+    const rsrc_t xf = SA ? sq.k : sq.v, xh = SA ? sq.v : sq.k;
+    const uint32_t rf = SA ? sq.rk : sq.rv, rh = SA ? sq.rv : sq.rk;
+    f32x4 acc[8][2];
+#pragma unroll
+    for (int x = 0; x < 8; x++) acc[x][0] = acc[x][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    bf16x8 fraw[4], hraw[2];
+    issue_rows_stride(xf, rf, p.T, n0 * 64, fraw);
+    issue_half_rows(xh, rh, n0 * 64, hraw);
+    float graw = ld_f32(sq.g, (uint32_t)(n0 * 64 + lane) * 4);
+    float logdecay = 0.f;
+    StateScale sc;
+    for (int n = n0; n < n1; n++) {
+        const int t0 = n * 64;
+        const GateRegs gr = sla_gates(graw);
+        sc.begin_chunk(chunk_last_gam(gr));
+        commit_gates(p.T, t0, gr, sLam, sBeta, sGam, sc.inv());
+        store_rows<TileF>(fraw, 64, sF);
+        store_half_rows<TileW>(hraw, 64, sH);
+        __syncthreads();
+        if (n + 1 < n1) {
+            issue_rows_stride(xf, rf, p.T, t0 + 64, fraw);
+            issue_half_rows(xh, rh, t0 + 64, hraw);
+            graw = ld_f32(sq.g, (uint32_t)(t0 + 64 + lane) * 4);
+        }
+        logdecay += sGam[63];
+        if (sc.fold != 1.f) {
+#pragma unroll
+            for (int x = 0; x < 8; x++) {
+                acc[x][0] *= sc.fold;
+                acc[x][1] *= sc.fold;
+            }
+        }
+        chunk_state_update<LA, LB>(sArow, a_col, sBcol, b_col, sGam, acc);
+        sc.sig = sc.next;
+        __syncthreads();
+    }
+    const size_t slot = (size_t)bh * (p.P - 1) + j;
+    store_segment_state(acc, sc.sig, p.seg + slot * (KD * HALF), p.seg_exp + slot * 8);
+    if (tid == 0) p.seg_decay[bh * p.P + j] = exp2f(logdecay);
+}
+
+// Start state of segment j of a scalar_la sequence (one part per segment).
+template <typename H0Index>
+__device__ __forceinline__ void sla_start_state(const SlaParams& p, int bh, int j, H0Index h0_index, f32x4 acc[8][2]) {
+    load_start_state(p.seg + (size_t)bh * (p.P - 1) * (KD * HALF), KD * HALF, p.seg_exp + (size_t)bh * (p.P - 1) * 8, 8,
+                     p.seg_decay + bh * p.P, j, p.h0 ? p.h0 + (size_t)bh * (KD * HALF) : nullptr, h0_index, acc);
+}
+
+// Shape A sweep (K = 256, V = 128), grid (H, B, P), 512 threads. Wave w works
+// on key slice y = w >> 2 and state columns [32 mq, 32 mq + 32), mq = w & 3, as
+// pass 1 does; each slice's output, bf16(scale x), goes through LDS and the
+// two slices are summed per token.
+constexpr int SA_Q = 0;                        // q, TileQ
+constexpr int SA_K = SA_Q + TileQ::bytes;      // k, TileF
+constexpr int SA_V = SA_K + TileF::bytes;      // v, TileW
+constexpr int SA_P = SA_V + TileW::bytes;      // masked scores of each slice, 2 x TileP
+constexpr int SA_G = SA_P + 2 * TileP::bytes;  // f32 [5][64] gates
+constexpr int SA_LDS = SA_G + 5 * 64 * 4;
+static_assert(SA_LDS <= 160 * 1024, "scalar_la workgroup must fit in one CU's LDS");
+
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void sla_sweep_a_kernel(SlaParams p) {
+    __shared__ __align__(16) unsigned char smem[SA_LDS];
+    bf16_t* sQ = reinterpret_cast<bf16_t*>(smem + SA_Q);
+    bf16_t* sK = reinterpret_cast<bf16_t*>(smem + SA_K);
+    bf16_t* sW = reinterpret_cast<bf16_t*>(smem + SA_V);
+    bf16_t* sP = reinterpret_cast<bf16_t*>(smem + SA_P);
+    float* sLam = reinterpret_cast<float*>(smem + SA_G);
+    float* sBeta = sLam + 64;
+    float* sGam = sBeta + 64;
+    bf16_t* sR0 = sQ;  // the slices' outputs, after the q tile is done with
+    bf16_t* sR1 = sQ + 64 * RR;
+    const int h = blockIdx.x, b = blockIdx.y, j = blockIdx.z, bh = b * p.H + h;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_id(), lr = lane & 15, lg = lane >> 4;
+    const int y = w >> 2, mq = w & 3;
+    const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
+    const SlaSeq sq = make_sla_seq(p, b, h);
+    bf16x8 qraw[4], kraw[4], vraw[2];
+    issue_rows_stride(sq.q, sq.rk, p.T, n0 * 64, qraw);
+    issue_rows_stride(sq.k, sq.rk, p.T, n0 * 64, kraw);
+    issue_half_rows(sq.v, sq.rv, n0 * 64, vraw);
+    float graw = ld_f32(sq.g, (uint32_t)(n0 * 64 + lane) * 4);
+    zero_scores(sP, 2);
+    bf16_t* sPy = sP + y * (TileP::bytes / 2);
+    f32x4 acc[8][2];
+    sla_start_state(p, bh, j,
+                    [&](int kb, int c, int i) { return (HALF * y + state_row(kb, lg, i)) * HALF + 32 * mq + 16 * c + lr; },
+                    acc);
+    StateScale sc;
+    // combine mapping: token r, columns [16 cq, 16 cq + 16)
+    const int r = tid >> 3, cq = tid & 7;
+    const bool raw = p.raw_output != 0;
+    for (int n = n0; n < n1; n++) {
+        const int t0 = n * 64;
+        const GateRegs gr = sla_gates(graw);
+        sc.begin_chunk(chunk_last_gam(gr));
+        commit_gates(p.T, t0, gr, sLam, sBeta, sGam, sc.inv());
+        store_rows<TileQ>(qraw, 64, sQ);
+        store_rows<TileF>(kraw, 64, sK);
+        store_half_rows<TileW>(vraw, 64, sW);
+        __syncthreads();
+        if (n + 1 < n1) {
+            issue_rows_stride(sq.q, sq.rk, p.T, t0 + 64, qraw);
+            graw = ld_f32(sq.g, (uint32_t)(t0 + 64 + lane) * 4);
+        }
+        // Masked, decayed scores of this slice (unscaled): blocks mq, mq + 4 (and mq + 8).
+        score_tile<TileQ, TileF>(sQ, HALF * y, sK, HALF * y, mq, sGam, 0.f, sPy);
+        score_tile<TileQ, TileF>(sQ, HALF * y, sK, HALF * y, mq + 4, sGam, 0.f, sPy);
+        if (mq < 2) score_tile<TileQ, TileF>(sQ, HALF * y, sK, HALF * y, mq + 8, sGam, 0.f, sPy);
+        // x_y^T = 2^G_t S_n^T q_t over this slice's key rows.
+        f32x4 out[4][2];
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++) out[tb][0] = out[tb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const bf16x8 a0 = state_frag(acc[2 * ks][0], acc[2 * ks + 1][0]);
+            const bf16x8 a1 = state_frag(acc[2 * ks][1], acc[2 * ks + 1][1]);
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++) {
+                const bf16x8 bq = load_row<TileQ>(sQ, 16 * tb, HALF * y + 32 * ks);
+                out[tb][0] = mfma_bf16(a0, bq, out[tb][0]);
+                out[tb][1] = mfma_bf16(a1, bq, out[tb][1]);
+            }
+        }
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++) {
+            const float f = sGam[64 + 16 * tb + lr] * sc.sig;
+            out[tb][0] *= f;
+            out[tb][1] *= f;
+        }
+        __syncthreads();  // scores complete, q tile done with
+        if (n + 1 < n1) {
+            issue_rows_stride(sq.k, sq.rk, p.T, t0 + 64, kraw);
+            issue_half_rows(sq.v, sq.rv, t0 + 64, vraw);
+        }
+        // x_y^T += v^T P_y^T; wf[c][ss][jj] = v[32 ss + 8 lg + jj][32 mq + 16 c + lr].
+        bf16x8 wf[2][2];
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int ss = 0; ss < 2; ss++) wf[c][ss] = load_tr<TileW>(sW, 32 * ss, 32 * mq + 16 * c);
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+            for (int ss = 0; ss <= (tb >> 1); ss++) {
+                const bf16x8 pf = load_row<TileP>(sPy, 16 * tb, 32 * ss);
+                out[tb][0] = mfma_bf16(wf[0][ss], pf, out[tb][0]);
+                out[tb][1] = mfma_bf16(wf[1][ss], pf, out[tb][1]);
+            }
+        bf16_t* sRy = y == 0 ? sR0 : sR1;
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+            for (int c = 0; c < 2; c++)
+                *reinterpret_cast<bf16x4*>(sRy + (16 * tb + lr) * RR + 32 * mq + 16 * c + 4 * lg) =
+                    to_bf16x4(out[tb][c], p.scale);
+        // S = 2^G_last S + k^T bf16(2^(G_last - G_s) v), as acc += k^T bf16(2^(G_last - G_s) / sigma' v).
+        if (sc.fold != 1.f) {
+#pragma unroll
+            for (int kb = 0; kb < 8; kb++) {
+                acc[kb][0] *= sc.fold;
+                acc[kb][1] *= sc.fold;
+            }
+        }
+#pragma unroll
+        for (int ss = 0; ss < 2; ss++) {
+            bf16x8 wt[2];
+#pragma unroll
+            for (int c = 0; c < 2; c++)
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++)
+                    wt[c][jj] = (bf16_t)((float)wf[c][ss][jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
+#pragma unroll
+            for (int kb = 0; kb < 8; kb++) {
+                const bf16x8 kf = load_tr_perm<TileF>(sK, 32 * ss, HALF * y + 32 * (kb >> 1), kb & 1);
+                acc[kb][0] = mfma_bf16(kf, wt[0], acc[kb][0]);
+                acc[kb][1] = mfma_bf16(kf, wt[1], acc[kb][1]);
+            }
+        }
+        sc.sig = sc.next;
+        __syncthreads();  // both slices' outputs complete
+        {
+            float x[16];
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const bf16x8 a = *reinterpret_cast<const bf16x8*>(sR0 + r * RR + 16 * cq + 8 * hh);
+                const bf16x8 c2 = *reinterpret_cast<const bf16x8*>(sR1 + r * RR + 16 * cq + 8 * hh);
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[8 * hh + e] = (float)a[e] + (float)c2[e];
+            }
+            const uint32_t soff = (uint32_t)(t0 + r) * sq.ro;
+            if (raw) {
+#pragma unroll
+                for (int q4 = 0; q4 < 4; q4++)
+                    st_b128(sq.o, 4 * (16 * cq + 4 * q4), soff, f32x4{x[4 * q4], x[4 * q4 + 1], x[4 * q4 + 2], x[4 * q4 + 3]});
+            } else {
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++) {
+                    bf16x8 o8;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) o8[e] = (bf16_t)x[8 * hh + e];
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o8), sq.o, 2 * (16 * cq + 8 * hh), soff, 0);
+                }
+            }
+        }
+        __syncthreads();  // tiles are overwritten by the next chunk
+    }
+    if (j == p.P - 1 && p.hfinal) {
+        float* dst = p.hfinal + (size_t)bh * (KD * HALF);
+#pragma unroll
+        for (int kb = 0; kb < 8; kb++)
+#pragma unroll
+            for (int c = 0; c < 2; c++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    dst[(HALF * y + state_row(kb, lg, i)) * HALF + 32 * mq + 16 * c + lr] = acc[kb][c][i] * sc.sig;
+    }
+}
+
+// Shape B sweep (K = 128, V = 256), grid (H, B, P), 512 threads; wave w owns
+// value columns [32 w, 32 w + 32) as pass 2 does.
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void sla_sweep_b_kernel(SlaParams p) {
+    __shared__ __align__(16) unsigned char smem[P2_N];
+    bf16_t* sQh = reinterpret_cast<bf16_t*>(smem + P2_OM);  // q, TileO
+    bf16_t* sK = reinterpret_cast<bf16_t*>(smem + P2_W);    // k, TileW
+    bf16_t* sV = reinterpret_cast<bf16_t*>(smem + P2_V);    // v, TileF
+    bf16_t* sP = reinterpret_cast<bf16_t*>(smem + P2_P);
+    float* sLam = reinterpret_cast<float*>(smem + P2_G);
+    float* sBeta = sLam + 64;
+    float* sGam = sBeta + 64;
+    const int h = blockIdx.x, b = blockIdx.y, j = blockIdx.z, bh = b * p.H + h;
+    const int lane = threadIdx.x & 63, w = wave_id(), lr = lane & 15, lg = lane >> 4;
+    const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
+    const SlaSeq sq = make_sla_seq(p, b, h);
+    const bool raw = p.raw_output != 0;
+    const uint32_t osz = raw ? 4 : 2;
+    const uint32_t o_lane = (uint32_t)lr * sq.ro + osz * (32 * w + 4 * lg);
+    bf16x8 vraw[4], qraw[2], kraw[2];
+    issue_rows_stride(sq.v, sq.rv, p.T, n0 * 64, vraw);
+    issue_half_rows(sq.q, sq.rk, n0 * 64, qraw);
+    issue_half_rows(sq.k, sq.rk, n0 * 64, kraw);
+    float graw = ld_f32(sq.g, (uint32_t)(n0 * 64 + lane) * 4);
+    zero_scores(sP, 1);
+    f32x4 acc[8][2];
+    sla_start_state(p, bh, j, [&](int mb, int c, int i) { return state_row(mb, lg, i) * VD + 32 * w + 16 * c + lr; },
+                    acc);
+    StateScale sc;
+    for (int n = n0; n < n1; n++) {
+        const int t0 = n * 64;
+        const GateRegs gr = sla_gates(graw);
+        sc.begin_chunk(chunk_last_gam(gr));
+        commit_gates(p.T, t0, gr, sLam, sBeta, sGam, sc.inv());
+        store_half_rows<TileO>(qraw, 64, sQh);
+        store_half_rows<TileW>(kraw, 64, sK);
+        store_rows<TileF>(vraw, 64, sV);
+        __syncthreads();
+        if (n + 1 < n1) {
+            issue_half_rows(sq.q, sq.rk, t0 + 64, qraw);
+            issue_half_rows(sq.k, sq.rk, t0 + 64, kraw);
+            graw = ld_f32(sq.g, (uint32_t)(t0 + 64 + lane) * 4);
+        }
+        score_tile<TileO, TileW>(sQh, 0, sK, 0, w, sGam, 0.f, sP);
+        if (w < 2) score_tile<TileO, TileW>(sQh, 0, sK, 0, w + 8, sGam, 0.f, sP);
+        // o^T = 2^G_t S_n^T q_t.
+        f32x4 out[4][2];
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++) out[tb][0] = out[tb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const bf16x8 a0 = state_frag(acc[2 * ks][0], acc[2 * ks + 1][0]);
+            const bf16x8 a1 = state_frag(acc[2 * ks][1], acc[2 * ks + 1][1]);
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++) {
+                const bf16x8 bo = load_row<TileO>(sQh, 16 * tb, 32 * ks);
+                out[tb][0] = mfma_bf16(a0, bo, out[tb][0]);
+                out[tb][1] = mfma_bf16(a1, bo, out[tb][1]);
+            }
+        }
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++) {
+            const float f = sGam[64 + 16 * tb + lr] * sc.sig;
+            out[tb][0] *= f;
+            out[tb][1] *= f;
+        }
+        __syncthreads();  // scores complete
+        if (n + 1 < n1) issue_rows_stride(sq.v, sq.rv, p.T, t0 + 64, vraw);
+        // o^T += v^T P^T. vb[c][ss][jj] = v[32 ss + 8 lg + jj][32 w + 16 c + lr].
+        bf16x8 vb[2][2];
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int ss = 0; ss < 2; ss++) vb[c][ss] = load_tr<TileF>(sV, 32 * ss, 32 * w + 16 * c);
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+            for (int ss = 0; ss <= (tb >> 1); ss++) {
+                const bf16x8 pf = load_row<TileP>(sP, 16 * tb, 32 * ss);
+                out[tb][0] = mfma_bf16(vb[0][ss], pf, out[tb][0]);
+                out[tb][1] = mfma_bf16(vb[1][ss], pf, out[tb][1]);
+            }
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++) {
+            const uint32_t soff = (uint32_t)(t0 + 16 * tb) * sq.ro;
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const bf16x4 o4 = to_bf16x4(out[tb][c], p.scale);
+                if (raw)
+                    st_b128(sq.o, o_lane + osz * 16 * c, soff, f32x4{(float)o4[0], (float)o4[1], (float)o4[2], (float)o4[3]});
+                else
+                    st_b64(sq.o, o_lane + osz * 16 * c, soff, o4);
+            }
+        }
+        // S = 2^G_last S + k^T bf16(2^(G_last - G_s) v), as acc += k^T bf16(2^(G_last - G_s) / sigma' v).
+        if (sc.fold != 1.f) {
+#pragma unroll
+            for (int mb = 0; mb < 8; mb++) {
+                acc[mb][0] *= sc.fold;
+                acc[mb][1] *= sc.fold;
+            }
+        }
+#pragma unroll
+        for (int ss = 0; ss < 2; ss++) {
+            bf16x8 vt[2];
+#pragma unroll
+            for (int c = 0; c < 2; c++)
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++)
+                    vt[c][jj] = (bf16_t)((float)vb[c][ss][jj] * sGam[128 + 32 * ss + 8 * lg + jj]);
+#pragma unroll
+            for (int mb = 0; mb < 8; mb++) {
+                const bf16x8 kk = load_tr_perm<TileW>(sK, 32 * ss, 32 * (mb >> 1), mb & 1);
+                acc[mb][0] = mfma_bf16(kk, vt[0], acc[mb][0]);
+                acc[mb][1] = mfma_bf16(kk, vt[1], acc[mb][1]);
+            }
+        }
+        sc.sig = sc.next;
+        __syncthreads();
+    }
+    if (j == p.P - 1 && p.hfinal) {
+        float* dst = p.hfinal + (size_t)bh * (HALF * VD);
+#pragma unroll
+        for (int mb = 0; mb < 8; mb++)
+#pragma unroll
+            for (int c = 0; c < 2; c++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) dst[state_row(mb, lg, i) * VD + 32 * w + 16 * c + lr] = acc[mb][c][i] * sc.sig;
+    }
+}
+
 }  // namespace
 
 void choose_segments(int BH, int N, int* P, int* L) {
@@ -1475,6 +1931,35 @@ int launch_prefill(const PrefillParams& p, hipStream_t stream) {
         hipLaunchKernelGGL(pass2_kernel<true>, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
     else
         hipLaunchKernelGGL(pass2_kernel<false>, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
+    return 0;
+}
+
+SlaWorkspaceLayout sla_workspace_layout(int B, int T, int H, int K, int V) {
+    SlaWorkspaceLayout w;
+    const int N = (T + kChunk - 1) / kChunk;
+    int P, L;
+    choose_segments(B * H, N, &P, &L);
+    const size_t BH = (size_t)B * H;
+    const size_t nseg = P > 1 ? BH * (P - 1) : 0;
+    w.seg = 0;
+    w.seg_exp = align256(w.seg + nseg * (size_t)K * V * sizeof(_Float16));
+    w.seg_decay = align256(w.seg_exp + nseg * 8 * sizeof(int));
+    w.total = align256(w.seg_decay + BH * P * sizeof(float));
+    return w;
+}
+
+int launch_scalar_la(const SlaParams& p, hipStream_t stream) {
+    const bool a = p.K == KD;
+    if (p.P > 1) {
+        if (a)
+            hipLaunchKernelGGL(sla_segment_kernel<true>, dim3(p.H, p.B, p.P - 1), dim3(512), 0, stream, p);
+        else
+            hipLaunchKernelGGL(sla_segment_kernel<false>, dim3(p.H, p.B, p.P - 1), dim3(512), 0, stream, p);
+    }
+    if (a)
+        hipLaunchKernelGGL(sla_sweep_a_kernel, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
+    else
+        hipLaunchKernelGGL(sla_sweep_b_kernel, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
     return 0;
 }
 

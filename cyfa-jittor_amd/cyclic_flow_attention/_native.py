@@ -42,6 +42,16 @@ class CyfaOutNormArgs(ctypes.Structure):
     _fields_ = [("weight", _c_void_p), ("gate", _c_void_p), ("eps", _c_float), ("prescale", _c_float)]
 
 
+class CyfaSlaArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", _c_int), ("T", _c_int), ("H", _c_int), ("K", _c_int), ("V", _c_int),
+        ("q", _c_void_p), ("k", _c_void_p), ("v", _c_void_p), ("g", _c_void_p), ("initial", _c_void_p),
+        ("scale", _c_float), ("raw_output", _c_int), ("output_bth", _c_int), ("v_bth", _c_int),
+        ("o", _c_void_p), ("final_state", _c_void_p),
+        ("workspace", _c_void_p), ("workspace_bytes", _c_size_t),
+    ]
+
+
 class CyfaDecodeArgs(ctypes.Structure):
     _fields_ = [
         ("B", _c_int), ("H", _c_int), ("K", _c_int), ("V", _c_int), ("M", _c_int),
@@ -80,6 +90,8 @@ SIGNATURES = {
     "cyfa_chunk_fwd": (_c_int, [ctypes.POINTER(CyfaChunkArgs), _c_void_p]),
     "cyfa_chunk_fwd_normed": (_c_int, [ctypes.POINTER(CyfaChunkArgs), ctypes.POINTER(CyfaOutNormArgs), _c_void_p]),
     "cyfa_chunk_workspace_bytes": (_c_size_t, [_c_int] * 7),
+    "cyfa_scalar_la": (_c_int, [ctypes.POINTER(CyfaSlaArgs), _c_void_p]),
+    "cyfa_scalar_la_workspace_bytes": (_c_size_t, [_c_int] * 5),
     "cyfa_decode_step": (_c_int, [ctypes.POINTER(CyfaDecodeArgs), _c_void_p]),
     "cyfa_readout_table": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "cyfa_rms_norm": (_c_int, [ctypes.POINTER(CyfaNormArgs), _c_void_p]),
@@ -211,6 +223,17 @@ def chunk_fwd_normed(args: CyfaChunkArgs, norm: CyfaOutNormArgs, device):
                 lambda: lib.cyfa_chunk_fwd_normed(ctypes.byref(args), ctypes.byref(norm), stream_handle(device)))
     if rc != CYFA_OK:
         _raise(rc, "cyfa_chunk_fwd_normed failed")
+
+
+def scalar_la_workspace_bytes(B, T, H, K, V):
+    return int(load_library().cyfa_scalar_la_workspace_bytes(B, T, H, K, V))
+
+
+def scalar_la(args: CyfaSlaArgs, device):
+    lib = load_library()
+    rc = _timed("cyfa_scalar_la", lambda: lib.cyfa_scalar_la(ctypes.byref(args), stream_handle(device)))
+    if rc != CYFA_OK:
+        _raise(rc, "cyfa_scalar_la failed")
 
 
 def decode_step(args: CyfaDecodeArgs, device):

@@ -118,3 +118,54 @@ def chunk_cyfa(
                                        prescale=float(on_prescale))
         _native.chunk_fwd_normed(args, norm, dev)
     return o, ((hk, hv, clock) if output_final_state else None)
+
+
+def scalar_la(q, k, v, g, initial, scale=1.0, raw_output=False, output_bth=False, v_bth=False):
+    """One chunkwise scalar-gated linear-attention pass (ops/chunk.py:74-79 of
+    the reference, ``ScalarAttention`` at ops/chunk.py:30-71), on the HIP path.
+
+    q, k [B, H, T, K] bf16; v [B, H, T, V] bf16 ([B, T, H, V] when ``v_bth``);
+    g [B, H, T] natural-log decay; initial [B, H, K, V] fp32 or None (zero
+    state). (K, V) is (256, 128) or (128, 256) and T a multiple of 64. Returns
+    (o, final): o is [B, H, T, V] ([B, T, H, V] when ``output_bth``), fp32 when
+    ``raw_output`` (the sum of the per-128-wide-key-slice outputs, each rounded
+    to bf16 after the scale) and bf16 otherwise; final is the fp32 state.
+    Forward only.
+    """
+    state_in = (initial,) if initial is not None else ()
+    check_forward_only("scalar_la", (q, k, v, g) + state_in)
+    if q.dim() != 4 or k.shape != q.shape:
+        raise ValueError(f"q and k must be [B, H, T, K] of one shape, got {tuple(q.shape)} {tuple(k.shape)}")
+    B, H, T, K = q.shape
+    V = v.shape[-1]
+    want_v = (B, T, H, V) if v_bth else (B, H, T, V)
+    if tuple(v.shape) != want_v:
+        raise ValueError(f"v must have shape {want_v}, got {tuple(v.shape)}")
+    if tuple(g.shape) != (B, H, T):
+        raise ValueError(f"g must have shape {(B, H, T)}, got {tuple(g.shape)}")
+    if T % 64 != 0:
+        raise ValueError(f"scalar_la needs T to be a multiple of 64, got {T}")
+    for name, x in (("q", q), ("k", k), ("v", v)):
+        if x.dtype != torch.bfloat16:
+            raise NotImplementedError(f"scalar_la computes in bfloat16; {name} is {x.dtype}")
+    dev = _native.require_device(q, k, v, g, *state_in)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    g = g.to(torch.float32).contiguous()
+    h0 = None
+    if initial is not None:
+        h0 = initial.to(torch.float32).contiguous()
+        if tuple(h0.shape) != (B, H, K, V):
+            raise ValueError(f"initial must have shape {(B, H, K, V)}, got {tuple(h0.shape)}")
+    shape = (B, T, H, V) if output_bth else (B, H, T, V)
+    o = torch.empty(shape, dtype=torch.float32 if raw_output else torch.bfloat16, device=dev)
+    final = torch.empty(B, H, K, V, dtype=torch.float32, device=dev)
+    ws_bytes = _native.scalar_la_workspace_bytes(B, T, H, K, V)
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    args = _native.CyfaSlaArgs(
+        B=B, T=T, H=H, K=K, V=V, q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), g=g.data_ptr(),
+        initial=_native.ptr(h0), scale=float(scale), raw_output=int(bool(raw_output)),
+        output_bth=int(bool(output_bth)), v_bth=int(bool(v_bth)), o=o.data_ptr(), final_state=final.data_ptr(),
+        workspace=workspace.data_ptr(), workspace_bytes=ws_bytes,
+    )
+    _native.scalar_la(args, dev)
+    return o, final

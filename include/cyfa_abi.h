@@ -91,6 +91,37 @@ int cyfa_chunk_fwd_normed(const CyfaChunkArgs *args, const CyfaOutNormArgs *norm
  * allocates the equivalent intermediates through Jittor, ops/chunk.py:244-336). */
 size_t cyfa_chunk_workspace_bytes(int B, int T, int H, int K, int V, int M, int C);
 
+/* Arguments of one isolated ScalarGatedLA pass. (K, V) is (256, 128), the
+ * pass-1 shape, or (128, 256), the pass-2 shape; T is a multiple of 64. */
+typedef struct CyfaSlaArgs {
+    int B, T, H, K, V;
+    const void *q, *k;            /* bf16 [B,H,T,K] */
+    const void *v;                /* bf16 [B,H,T,V], or [B,T,H,V] when v_bth */
+    const float *g;               /* f32 [B,H,T], natural log of the per-token decay */
+    const float *initial;         /* nullable f32 [B,H,K,V] (zero state) */
+    float scale;
+    int raw_output, output_bth, v_bth;
+    void *o;                      /* [B,H,T,V], or [B,T,H,V] when output_bth;
+                                     f32 when raw_output, else bf16 */
+    float *final_state;           /* nullable f32 [B,H,K,V] */
+    void *workspace;              /* device scratch, >= cyfa_scalar_la_workspace_bytes() */
+    size_t workspace_bytes;
+} CyfaSlaArgs;
+
+/* One chunkwise scalar-gated linear-attention pass,
+ *   S_{n+1} = 2^G_last S_n + k^T bf16(2^(G_last - G_s) v),
+ *   o_t = scale (2^G_t q_t S_n + sum_{s<=t} bf16(2^(G_t - G_s) q_t.k_s) v_s),
+ * G the in-chunk cumulative sum of g in log2 units, S_0 = initial. The output
+ * is formed per 128-wide key slice, each slice rounded to bf16 after the scale,
+ * and the slices summed (in f32 when raw_output, else rounded once more to
+ * bf16). Replaces scalar_la / ScalarAttention (ops/chunk.py:30-79) with
+ * state_forward (ops/chunk_h.py:10-339), local_log2_cumsum
+ * (ops/utils.py:495-520) and output_forward (ops/chunk_o.py:177-613). */
+int cyfa_scalar_la(const CyfaSlaArgs *args, void *hip_stream);
+
+/* Workspace bytes cyfa_scalar_la needs for these dimensions. */
+size_t cyfa_scalar_la_workspace_bytes(int B, int T, int H, int K, int V);
+
 /* Arguments of one decode step (T == 1). */
 typedef struct CyfaDecodeArgs {
     int B, H, K, V, M;

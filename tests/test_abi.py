@@ -46,6 +46,7 @@ def _c_layout(tmp_path, struct, fields):
 @pytest.mark.parametrize("cls,name", [(_native.CyfaChunkArgs, "CyfaChunkArgs"),
                                       (_native.CyfaDecodeArgs, "CyfaDecodeArgs"),
                                       (_native.CyfaOutNormArgs, "CyfaOutNormArgs"),
+                                      (_native.CyfaSlaArgs, "CyfaSlaArgs"),
                                       (_native.CyfaNormArgs, "CyfaNormArgs"),
                                       (_native.CyfaConvArgs, "CyfaConvArgs")])
 def test_struct_layout_matches_header(tmp_path, cls, name):
@@ -108,3 +109,24 @@ def test_layer_entry_points_validate_before_launch():
     assert lib.cyfa_short_conv(ctypes.byref(c), None) == _native.CYFA_ERR_UNSUPPORTED
     assert lib.cyfa_silu_mul(None, None, 1, 8, None) == _native.CYFA_ERR_VALUE
     assert lib.cyfa_gates(None, None, None, None, None, None, 1, 4, None) == _native.CYFA_ERR_VALUE
+
+
+def test_scalar_la_validates_before_launch():
+    from cyclic_flow_attention.ops.chunk import scalar_la
+
+    lib = _native.load_library()
+    a = _native.CyfaSlaArgs(B=1, T=64, H=1, K=256, V=256)
+    assert lib.cyfa_scalar_la(ctypes.byref(a), None) == _native.CYFA_ERR_UNSUPPORTED
+    a.V, a.T = 128, 100
+    assert lib.cyfa_scalar_la(ctypes.byref(a), None) == _native.CYFA_ERR_VALUE  # T not a multiple of 64
+    a.T = 128
+    assert lib.cyfa_scalar_la(ctypes.byref(a), None) == _native.CYFA_ERR_VALUE  # null pointers
+    assert _native.scalar_la_workspace_bytes(8, 4096, 4, 256, 128) > 0
+    q = torch.zeros(1, 1, 64, 128, dtype=torch.bfloat16)
+    g = torch.zeros(1, 1, 64)
+    with pytest.raises(ValueError):
+        scalar_la(q, q, torch.zeros(1, 1, 64, 256, dtype=torch.bfloat16), g, None)  # CPU tensors
+    with pytest.raises(ValueError):
+        scalar_la(q, q, torch.zeros(1, 1, 32, 256, dtype=torch.bfloat16), g, None)  # v shape
+    with pytest.raises(NotImplementedError):
+        scalar_la(q, q, torch.zeros(1, 1, 64, 256), g, None)  # fp32 v
