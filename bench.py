@@ -20,6 +20,11 @@ decode shape (B=64, H=4), free of host launch gaps;
                      2.5 PFLOP/s dense bf16 MFMA peak;
   decode:            524 288 bytes of fp32 state per (batch, head) per layer
                      launch / duration vs 8 TB/s HBM.
+isolated_pass: configuration 2 (B=8, H=4, T=4096), one scalar_la pass at each
+pass shape ((K, V) = (256, 128) and (128, 256)), q, k, v ~ N(0, 1) bf16 with q, k
+L2-normalised, log alpha = logsigmoid(N(3, 1)); HIP events around each launch;
+156 032 FLOP per token*head per pass against the bf16 MFMA peak and the
+algorithmic bytes (q, k, v, g in, o out) against 8 TB/s.
 cpu_baseline: the CPU oracle (the restatement of the reference path; the
 reference itself has no CPU path) timed on this host, bounded sample.
 """
@@ -42,6 +47,7 @@ PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 FLOP_PER_TOKEN_HEAD = 377_088      # pass 1 + readout + pass 2, causal-exact
 STATE_BYTES_PER_BH = 524_288       # fp32 hk + hv, read and written, K = V = 256
+FLOP_PER_TOKEN_HEAD_PASS = 156_032  # one ScalarGatedLA pass, causal-exact
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
 # scaled by a 1 GiB copy kernel (profiles/cyfa_chunk_fwd_cfg3_prefill.md,
 # profiles/cyfa_decode_step_cfg4.md); they apply to the default shapes.
@@ -62,6 +68,10 @@ def parse():
     ap.add_argument("--config", default="cyclic_flow_attention_400m.json")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-isolated", action="store_true", help="skip the configuration-2 scalar_la timings")
+    ap.add_argument("--long-context", action="store_true",
+                    help="also run configuration 5: CyFA-1.4B, B=1, a 16384-token prefill, then 512 greedy "
+                         "decode steps (reported under 'long_context')")
     ap.add_argument("--decode-kernel-only", action="store_true",
                     help="only time the fused decode kernel at the decode shape (for hardware-counter runs)")
     ap.add_argument("--no-tuned-gemms", action="store_true",
@@ -111,6 +121,32 @@ def time_prefill(model, ids, steps, warmup):
         del out
     res = timer.results()
     return elapsed, res.get("cyfa_chunk_fwd_normed", []) + res.get("cyfa_chunk_fwd", [])
+
+
+def time_isolated_pass(K, V, B=8, H=4, T=4096, reps=20, warmup=3):
+    """Average device duration (ms) of one scalar_la launch at configuration 2."""
+    import torch
+
+    from cyclic_flow_attention import _native
+    from cyclic_flow_attention.ops.chunk import scalar_la
+
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    q = torch.nn.functional.normalize(torch.randn(B, H, T, K, device="cuda", generator=gen), dim=-1).bfloat16()
+    k = torch.nn.functional.normalize(torch.randn(B, H, T, K, device="cuda", generator=gen), dim=-1).bfloat16()
+    v = torch.randn(B, H, T, V, device="cuda", generator=gen).bfloat16()
+    g = torch.nn.functional.logsigmoid(torch.randn(B, H, T, device="cuda", generator=gen) + 3)
+    raw = K == 256  # the pass-1 shape returns the raw fp32 sum of the slices
+    scale = K ** -0.5 if K == 256 else 1.0
+    with torch.no_grad():
+        for _ in range(warmup):
+            scalar_la(q, k, v, g, None, scale, raw)
+        torch.cuda.synchronize()
+        with _native.LaunchTimer() as timer:
+            for _ in range(reps):
+                scalar_la(q, k, v, g, None, scale, raw)
+            ms = timer.results().get("cyfa_scalar_la", [])
+    per_th = 2 * K + 2 * K + 2 * V + 4 + (4 if raw else 2) * V  # q, k, v, g read; o written
+    return statistics.fmean(ms), per_th * B * H * T, FLOP_PER_TOKEN_HEAD_PASS * B * H * T
 
 
 def time_decode(model, prompt, steps, warmup):
@@ -355,6 +391,22 @@ def main():
         }
         del prompt
 
+    if not args.no_isolated:
+        iso = {"workload": "scalar_la, configuration 2: B=8, H=4, T=4096, zero initial state"}
+        for name, (K, V) in (("pass1_shape", (256, 128)), ("pass2_shape", (128, 256))):
+            ms, nbytes, flop = time_isolated_pass(K, V)
+            tflops = flop / (ms * 1e-3) / 1e12
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            iso[name] = {
+                "K": K, "V": V, "launch_us": round(ms * 1e3, 2),
+                "mfma": {"achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tflops / PEAK_BF16_TFLOPS, 4)},
+                "hbm": {"achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                        "frac": round(gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": nbytes},
+            }
+            log(f"scalar_la K={K} V={V}: {ms * 1e3:.1f} us/launch = {tflops:.1f} TFLOP/s, {gbs:,.0f} GB/s algorithmic")
+        result["isolated_pass"] = iso
+
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle) ...")
         result["cpu_baseline"] = cpu_baseline_prefill(model, config, args.seq_len)
@@ -362,6 +414,24 @@ def main():
         if "decode" in result:
             result["decode"]["cpu_baseline"] = cpu_baseline_decode(model, config, args.decode_batch)
             log(f"cpu decode {result['decode']['cpu_baseline']['value']} tok/s")
+
+    if args.long_context:
+        del model
+        torch.cuda.empty_cache()
+        lc_config, lc_model = build_model("cyclic_flow_attention_1_4b.json", dev)
+        T5 = 16384
+        lc_ids = torch.randint(0, lc_config.vocab_size, (1, T5), generator=gen).to(dev)
+        log(f"long context: CyFA-1.4B prefill B=1 T={T5}")
+        lc_elapsed, _ = time_prefill(lc_model, lc_ids, 2, 1)
+        log(f"long context: decode B=1, 512 steps after the {T5}-token prompt")
+        lc_dec = time_decode(lc_model, lc_ids, 512, 4)
+        result["long_context"] = {
+            "workload": f"configuration 5: CyFA-1.4B, B=1, {T5}-token prefill, then 512 greedy decode steps",
+            "prefill": {"value": round(2 * T5 / lc_elapsed, 1), "unit": "tok/s", "ms_per_step": round(lc_elapsed / 2 * 1e3, 3)},
+            "decode": {"value": round(512 / lc_dec, 1), "unit": "tok/s", "ms_per_step": round(lc_dec / 512 * 1e3, 4)},
+        }
+        log(f"long context: prefill {2 * T5 / lc_elapsed:,.0f} tok/s, decode {512 / lc_dec:,.1f} tok/s")
+        del lc_model
 
     print(json.dumps(result), flush=True)
     return 0

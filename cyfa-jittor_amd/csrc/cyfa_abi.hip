@@ -239,6 +239,30 @@ int cyfa_scalar_la(const CyfaSlaArgs* a, void* hip_stream) {
     return check_launch("cyfa_scalar_la");
 }
 
+int cyfa_linear_rows(const CyfaLinearArgs* a, void* hip_stream) {
+    if (!a) return fail(CYFA_ERR_VALUE, "cyfa_linear_rows: null args");
+    if (a->M < 1 || a->M > 64 || a->N < 1 || a->K < 32 || a->K % 32 != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_linear_rows: M=%d N=%d K=%d (needs 1 <= M <= 64, K a multiple of 32)",
+                    a->M, a->N, a->K);
+    if (!a->x || !a->weight || !a->y) return fail(CYFA_ERR_VALUE, "cyfa_linear_rows: null required pointer");
+    if (a->ldx < a->K || a->ldx % 8 != 0 || a->ldy < a->N)
+        return fail(CYFA_ERR_VALUE, "cyfa_linear_rows: ldx=%lld ldy=%lld", a->ldx, a->ldy);
+    if (!aligned(a->x, 16) || !aligned(a->weight, 16) || !aligned(a->y, 2) || (a->bias && !aligned(a->bias, 2)))
+        return fail(CYFA_ERR_ALIGN, "cyfa_linear_rows: x and weight need 16-byte alignment");
+    cyfa::LinearParams p;
+    p.M = a->M;
+    p.N = a->N;
+    p.K = a->K;
+    p.x = (const __bf16*)a->x;
+    p.ldx = a->ldx;
+    p.w = (const __bf16*)a->weight;
+    p.bias = (const __bf16*)a->bias;
+    p.y = (__bf16*)a->y;
+    p.ldy = a->ldy;
+    cyfa::launch_linear_rows(p, (hipStream_t)hip_stream);
+    return check_launch("cyfa_linear_rows");
+}
+
 int cyfa_rms_norm(const CyfaNormArgs* a, void* hip_stream) {
     if (!a) return fail(CYFA_ERR_VALUE, "cyfa_rms_norm: null args");
     if (a->rows < 0 || a->D <= 0) return fail(CYFA_ERR_VALUE, "cyfa_rms_norm: rows=%d D=%d", a->rows, a->D);
@@ -312,12 +336,12 @@ int cyfa_silu_mul(const void* gu, void* out, int rows, int F, void* hip_stream) 
     return check_launch("cyfa_silu_mul");
 }
 
-int cyfa_gates(const void* abd, const float* dt_bias, const float* A_log, float* g, float* beta, float* delta, int rows,
-               int H, void* hip_stream) {
-    if (!abd || !dt_bias || !A_log || !g || !beta || !delta || rows < 0 || H <= 0)
+int cyfa_gates(const void* abd, long long abd_row, const float* dt_bias, const float* A_log, float* g, float* beta,
+               float* delta, int rows, int H, void* hip_stream) {
+    if (!abd || !dt_bias || !A_log || !g || !beta || !delta || rows < 0 || H <= 0 || abd_row < 3LL * H)
         return fail(CYFA_ERR_VALUE, "cyfa_gates: bad arguments");
     if (rows == 0) return CYFA_OK;
-    cyfa::launch_gates((const __bf16*)abd, dt_bias, A_log, g, beta, delta, rows, H, (hipStream_t)hip_stream);
+    cyfa::launch_gates((const __bf16*)abd, abd_row, dt_bias, A_log, g, beta, delta, rows, H, (hipStream_t)hip_stream);
     return check_launch("cyfa_gates");
 }
 

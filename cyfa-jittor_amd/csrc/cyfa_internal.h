@@ -108,10 +108,22 @@ WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V);
 int launch_decode_step(const DecodeParams& p, int K, int V, hipStream_t stream);
 int launch_prefill(const PrefillParams& p, hipStream_t stream);
 int launch_readout_table(const float* readout, float* table, int H, hipStream_t stream);
+// y = x W^T (+ bias) for at most 64 rows of x (the one-token decode step's projections).
+struct LinearParams {
+    int M, N, K;
+    const __bf16* x;     // [M, K], rows ldx elements apart
+    long long ldx;
+    const __bf16* w;     // [N, K] row-major (torch Linear weight)
+    const __bf16* bias;  // nullable [N]
+    __bf16* y;           // [M, N], rows ldy elements apart
+    long long ldy;
+};
+
 int launch_rms_norm(const NormParams& p, hipStream_t stream);
+int launch_linear_rows(const LinearParams& p, hipStream_t stream);
 int launch_short_conv(const ConvParams& p, hipStream_t stream);
 int launch_silu_mul(const __bf16* gu, __bf16* out, int rows, int F, hipStream_t stream);
-int launch_gates(const __bf16* abd, const float* dt_bias, const float* A_log, float* g, float* beta, float* delta,
-                 int rows, int H, hipStream_t stream);
+int launch_gates(const __bf16* abd, long long abd_row, const float* dt_bias, const float* A_log, float* g, float* beta,
+                 float* delta, int rows, int H, hipStream_t stream);
 
 }  // namespace cyfa

@@ -63,6 +63,93 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormParams p) {
     }
 }
 
+// y[m][n] = bias[n] + sum_k x[m][k] W[n][k] for M <= 64 rows (the nn.Linear /
+// F.linear calls of the one-token decode step, layers/cyfa.py and
+// modeling_cyfa.py). At these shapes the weight read is the whole cost: a
+// library GEMM tiles M into large blocks and leaves most of the chip idle,
+// while here every workgroup streams a 32-column slice of W once, with all
+// of its loads in flight. Workgroup = 8 waves over one 32-column slice; wave w
+// takes the 32-deep k-steps w, w + 8, ... of all MT row tiles of 16, on
+// v_mfma_f32_16x16x32_bf16 (A = x rows, B = W rows read straight from global
+// memory: lane (lr, lg) loads 8 consecutive k of row lr). The eight partial
+// tiles are summed in LDS in wave order, so results do not depend on timing.
+// Rows of x at or past M and rows of W at or past N read as zero (buffer
+// bounds).
+typedef __amdgpu_buffer_rsrc_t lin_rsrc_t;
+
+__device__ __forceinline__ lin_rsrc_t lin_rsrc(const void* base, size_t bytes) {
+    const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
+
+__device__ __forceinline__ bf16x8 lin_ld(lin_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+template <int MT>
+__global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
+    __shared__ float part[8][MT * 16][33];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lr = lane & 15, lg = lane >> 4;
+    const int n0 = blockIdx.x * 32;
+    const lin_rsrc_t rx = lin_rsrc(p.x, ((size_t)(p.M - 1) * p.ldx + p.K) * 2);
+    const lin_rsrc_t rw = lin_rsrc(p.w + (size_t)n0 * p.K, (size_t)min(32, p.N - n0) * p.K * 2);
+    // the bias of this thread's outputs, loaded with the operands
+    float bias[MT];
+#pragma unroll
+    for (int r = 0; r < MT; r++) {
+        const int n = n0 + ((threadIdx.x + 512 * r) & 31);
+        bias[r] = p.bias && n < p.N ? (float)p.bias[n] : 0.f;
+    }
+    f32x4 acc[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Wave w takes a contiguous run of 32-deep k-steps, so that its loads of a
+    // row cover whole cache lines; up to four k-steps' loads are in flight at once.
+    const int steps = p.K / 32, per = (steps + 7) / 8;
+    const int s0 = min(steps, w * per), s1 = min(steps, s0 + per);
+    const uint32_t wrow = (uint32_t)lr * p.K * 2, xrow = (uint32_t)lr * (uint32_t)p.ldx * 2;
+    const uint32_t xstride = (uint32_t)(16 * p.ldx * 2);
+    for (int s = s0; s < s1; s += 4) {
+        bf16x8 wf[4][2], xf[4][MT];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if (s + u < s1) {
+                const uint32_t kb = (uint32_t)(32 * (s + u) + 8 * lg) * 2;
+#pragma unroll
+                for (int c = 0; c < 2; c++) wf[u][c] = lin_ld(rw, wrow + (uint32_t)(16 * c) * p.K * 2 + kb);
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) xf[u][mt] = lin_ld(rx, xrow + mt * xstride + kb);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if (s + u < s1) {
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                    for (int c = 0; c < 2; c++)
+                        acc[mt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[u][mt], wf[u][c], acc[mt][c], 0, 0, 0);
+            }
+        }
+    }
+    // acc[mt][c][i] = partial y[16 mt + 4 lg + i][n0 + 16 c + lr]
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) part[w][16 * mt + 4 * lg + i][16 * c + lr] = acc[mt][c][i];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < MT; r++) {
+        const int idx = threadIdx.x + 512 * r, m = idx >> 5, n = idx & 31;
+        float s = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < 8; ww++) s += part[ww][m][n];
+        if (m < p.M && n0 + n < p.N) p.y[(size_t)m * p.ldy + n0 + n] = (bf16_t)(s + bias[r]);
+    }
+}
+
 // Causal depthwise convolution over time (layers/cyfa.py:138-233):
 //   y[b, t, c] = bias[c] + sum_{w < W} weight[c, w] * X[b, t + w - (W - 1), c]
 // where X[b, i] is x[b, i] for i >= 0, cache[b, W - 1 + i] for i < 0 when a
@@ -153,16 +240,18 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const bf16_t* gu, bf16_t*
 // Gate activations (layers/cyfa.py:323-326) from abd = [a | b | d] rows of 3H
 // bf16 (the b / d biases already added): g = -exp(A_log) softplus(a + dt_bias),
 // beta = sigmoid(b), delta = sigmoid(d), all fp32 [rows, H].
-__global__ __launch_bounds__(256) void gates_kernel(const bf16_t* abd, const float* dt_bias, const float* A_log, float* g,
-                                                    float* beta, float* delta, int rows, int H) {
+__global__ __launch_bounds__(256) void gates_kernel(const bf16_t* abd, long long abd_row, const float* dt_bias,
+                                                    const float* A_log, float* g, float* beta, float* delta, int rows,
+                                                    int H) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= rows * H) return;
     const int r = i / H, h = i % H;
-    const float a = (float)abd[(size_t)r * 3 * H + h] + dt_bias[h];
+    const bf16_t* row = abd + (size_t)r * abd_row;
+    const float a = (float)row[h] + dt_bias[h];
     const float sp = a > 20.f ? a : log1pf(expf(a));
     g[i] = -expf(A_log[h]) * sp;
-    beta[i] = sigmoidf((float)abd[(size_t)r * 3 * H + H + h]);
-    delta[i] = sigmoidf((float)abd[(size_t)r * 3 * H + 2 * H + h]);
+    beta[i] = sigmoidf((float)row[H + h]);
+    delta[i] = sigmoidf((float)row[2 * H + h]);
 }
 
 }  // namespace
@@ -174,6 +263,18 @@ int launch_rms_norm(const NormParams& p, hipStream_t stream) {
         case 2: hipLaunchKernelGGL(rms_norm_kernel<2>, grid, block, 0, stream, p); break;
         case 4: hipLaunchKernelGGL(rms_norm_kernel<4>, grid, block, 0, stream, p); break;
         case 8: hipLaunchKernelGGL(rms_norm_kernel<8>, grid, block, 0, stream, p); break;
+        default: return -1;
+    }
+    return 0;
+}
+
+int launch_linear_rows(const LinearParams& p, hipStream_t stream) {
+    const dim3 grid((p.N + 31) / 32), block(512);
+    switch ((p.M + 15) / 16) {
+        case 1: hipLaunchKernelGGL(linear_rows_kernel<1>, grid, block, 0, stream, p); break;
+        case 2: hipLaunchKernelGGL(linear_rows_kernel<2>, grid, block, 0, stream, p); break;
+        case 3: hipLaunchKernelGGL(linear_rows_kernel<3>, grid, block, 0, stream, p); break;
+        case 4: hipLaunchKernelGGL(linear_rows_kernel<4>, grid, block, 0, stream, p); break;
         default: return -1;
     }
     return 0;
@@ -196,10 +297,10 @@ int launch_silu_mul(const bf16_t* gu, bf16_t* out, int rows, int F, hipStream_t 
     return 0;
 }
 
-int launch_gates(const bf16_t* abd, const float* dt_bias, const float* A_log, float* g, float* beta, float* delta,
-                 int rows, int H, hipStream_t stream) {
-    hipLaunchKernelGGL(gates_kernel, dim3((rows * H + 255) / 256), dim3(256), 0, stream, abd, dt_bias, A_log, g, beta,
-                       delta, rows, H);
+int launch_gates(const bf16_t* abd, long long abd_row, const float* dt_bias, const float* A_log, float* g, float* beta,
+                 float* delta, int rows, int H, hipStream_t stream) {
+    hipLaunchKernelGGL(gates_kernel, dim3((rows * H + 255) / 256), dim3(256), 0, stream, abd, abd_row, dt_bias, A_log, g,
+                       beta, delta, rows, H);
     return 0;
 }
 

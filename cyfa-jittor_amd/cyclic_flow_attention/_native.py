@@ -11,6 +11,7 @@ import os
 from pathlib import Path
 
 import torch
+import torch.nn.functional as F
 
 LIB_PATH = Path(os.environ.get("CYFA_LIB", Path(__file__).with_name("libcyfa_hip.so")))
 ABI_VERSION = 1
@@ -74,6 +75,14 @@ class CyfaNormArgs(ctypes.Structure):
     ]
 
 
+class CyfaLinearArgs(ctypes.Structure):
+    _fields_ = [
+        ("M", _c_int), ("N", _c_int), ("K", _c_int),
+        ("x", _c_void_p), ("ldx", ctypes.c_longlong), ("weight", _c_void_p), ("bias", _c_void_p),
+        ("y", _c_void_p), ("ldy", ctypes.c_longlong),
+    ]
+
+
 class CyfaConvArgs(ctypes.Structure):
     _fields_ = [
         ("B", _c_int), ("T", _c_int), ("D", _c_int), ("W", _c_int),
@@ -96,9 +105,10 @@ SIGNATURES = {
     "cyfa_readout_table": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "cyfa_rms_norm": (_c_int, [ctypes.POINTER(CyfaNormArgs), _c_void_p]),
     "cyfa_short_conv": (_c_int, [ctypes.POINTER(CyfaConvArgs), _c_void_p]),
+    "cyfa_linear_rows": (_c_int, [ctypes.POINTER(CyfaLinearArgs), _c_void_p]),
     "cyfa_silu_mul": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
-    "cyfa_gates": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int,
-                            _c_void_p]),
+    "cyfa_gates": (_c_int, [_c_void_p, ctypes.c_longlong, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                            _c_int, _c_int, _c_void_p]),
     "cyfa_last_error": (ctypes.c_char_p, []),
     "cyfa_abi_version": (_c_int, []),
 }
@@ -281,6 +291,46 @@ def rms_norm(x, weight, eps, gate=None, residual=None, prescale=1.0):
     return out if residual is None else (total, out)
 
 
+LINEAR_ROWS_MAX = 64
+
+
+def linear(x, weight, bias=None, out_cols=None):
+    """x W^T (+ bias), bf16, like F.linear. Calls with at most 64 rows (the
+    one-token decode step) run on cyfa_linear_rows, which streams W once
+    across the whole chip; larger calls go to the library GEMM. ``out_cols``
+    (>= N) pads the output rows, so that column slices of the result start
+    16-byte aligned."""
+    K = weight.shape[-1]
+    N = weight.shape[0]
+    width = K
+    if x.shape[-1] != width:
+        raise ValueError(f"linear: x has {x.shape[-1]} columns, the weight needs {width}")
+    rows = x.numel() // width if width else 0
+    if (rows == 0 or rows > LINEAR_ROWS_MAX or K % 32 or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16
+            or (bias is not None and bias.dtype != torch.bfloat16) or not x.is_cuda
+            or (torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad))):
+        return F.linear(x, weight, bias)
+    require_device(x, weight, bias)
+    x2 = x.reshape(rows, width)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    w = weight.detach()
+    if not w.is_contiguous():
+        w = w.contiguous()
+    ldy = max(N, out_cols or N)
+    y = torch.empty(rows, ldy, dtype=torch.bfloat16, device=x.device)
+    args = CyfaLinearArgs(M=rows, N=N, K=K, x=x2.data_ptr(), ldx=x2.stride(0), weight=w.data_ptr(),
+                          bias=ptr(None if bias is None else bias.detach().contiguous()), y=y.data_ptr(), ldy=ldy)
+    _check(load_library().cyfa_linear_rows(ctypes.byref(args), stream_handle(x.device)), "cyfa_linear_rows")
+    lead = tuple(x.shape[:-1])
+    if not lead:
+        return y.view(-1)[:N]
+    strides = [ldy, 1]  # rows ldy apart, whatever the sizes of the leading dims
+    for i in range(len(lead) - 2, -1, -1):
+        strides.insert(0, strides[0] * lead[i + 1])
+    return y.as_strided(lead + (N,), tuple(strides))
+
+
 def short_conv(x, weight, bias=None, cache=None, split=None, cache_out=None):
     """Causal depthwise convolution over time of x [B, T, D] (rows may be strided).
 
@@ -324,12 +374,15 @@ def silu_mul(gu):
 def gates(abd, dt_bias, A_log):
     """(g, beta, delta) fp32 [..., H] from the fused a|b|d projection [..., 3H]."""
     dev = require_device(abd, dt_bias, A_log)
-    abd = abd.contiguous()
     H = abd.shape[-1] // 3
+    rows = abd.numel() // (3 * H)
+    flat = abd.reshape(rows, 3 * H) if abd.dim() > 1 else abd.reshape(1, 3 * H)
+    if flat.stride(-1) != 1:
+        flat = flat.contiguous()
     shape = tuple(abd.shape[:-1]) + (H,)
     g, beta, delta = (torch.empty(shape, dtype=torch.float32, device=dev) for _ in range(3))
     db = dt_bias.detach().to(torch.float32).contiguous()
     al = A_log.detach().to(torch.float32).contiguous()
-    _check(load_library().cyfa_gates(ptr(abd), ptr(db), ptr(al), ptr(g), ptr(beta), ptr(delta),
-                                      abd.numel() // (3 * H), H, stream_handle(dev)), "cyfa_gates")
+    _check(load_library().cyfa_gates(ptr(flat), flat.stride(0), ptr(db), ptr(al), ptr(g), ptr(beta), ptr(delta),
+                                      rows, H, stream_handle(dev)), "cyfa_gates")
     return g, beta, delta

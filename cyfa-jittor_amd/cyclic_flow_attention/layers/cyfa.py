@@ -4,15 +4,19 @@ Mirrors layers/cyfa.py:236-357 of Chyxx/CyFA-Jittor v0.1.2: constructor
 arguments, parameter names (torch-checkpoint compatible), the
 ``y, cache = layer(x)`` contract and the cache layout
 {"recurrent_state": (hk, hv, clock), "conv_state": (cq, ck, cv)}.
-Projections run as torch (hipBLASLt) GEMMs in bf16 with fp32 accumulation;
-the attention itself is ``ops.chunk_cyfa`` (prefill) or
-``ops.fused_recurrent_cyfa`` (one-token decode), both HIP kernels.
+Projections run as torch (hipBLASLt) GEMMs in bf16 with fp32 accumulation,
+except calls of at most 64 rows (decode steps) on the fused path, which run
+on the HIP kernel behind ``_native.linear``; the attention itself is
+``ops.chunk_cyfa`` (prefill) or ``ops.fused_recurrent_cyfa`` (one-token
+decode), both HIP kernels.
 
 Like the reference, which switches to its inference kernels for bf16 CUDA
 tensors without gradients (layers/cyfa.py:66-73, 148-155), bf16 GPU inference
 takes a fused path: one q|k|v projection and one short-convolution launch
 for the three tensors, one a|b|d projection with a fused gate kernel, and the
-gated o_norm as one HIP kernel. Other inputs take the general torch path.
+gated o_norm inside the prefill's last kernel (a separate HIP kernel after a
+decode step). Decode steps of at most 64 rows form q|k|v, g_proj[0] and a|b|d
+in one projection launch. Other inputs take the general torch path.
 """
 
 import math
@@ -213,6 +217,10 @@ class CyclicFlowAttention(nn.Module):
         self._abd_weight = FusedWeight()
         self._abd_bias = FusedWeight()
         self._a_bias_zero = None  # a_proj has no bias: zeros in the fused a|b|d bias
+        # decode steps: one [q | k | v | g_proj[0] | a | b | d] projection
+        self._in_weight = FusedWeight()
+        self._in_bias = FusedWeight()
+        self._in_bias_zero = None
         # When set, one-token steps update the cache's recurrent states in place
         # (the graphed decode loop); otherwise new state tensors are returned.
         self.decode_in_place = False
@@ -286,7 +294,26 @@ class CyclicFlowAttention(nn.Module):
         B, T, _ = x.shape
         H, Dk, Dv = self.num_heads, self.key_dim, self.value_dim
         W = self.q_conv1d.width
-        qkv = F.linear(x, self._qkv_weight.get(self.q_proj.weight, self.k_proj.weight, self.v_proj.weight))
+        g0, g1 = self.g_proj
+        if self._a_bias_zero is None or self._a_bias_zero.dtype != self.b_proj.bias.dtype \
+                or self._a_bias_zero.device != self.b_proj.bias.device:
+            self._a_bias_zero = torch.zeros_like(self.b_proj.bias.detach())
+        abd_bias = self._abd_bias.get(self._a_bias_zero, self.b_proj.bias, self.d_proj.bias)
+        if B * T <= _native.LINEAR_ROWS_MAX:
+            # one launch for the q|k|v, g_proj[0] and a|b|d projections; the
+            # outputs are column slices of one buffer with 16-byte aligned rows
+            D3, Dg = 2 * Dk + Dv, g0.weight.shape[0]
+            if self._in_bias_zero is None or self._in_bias_zero.shape[0] != D3 + Dg \
+                    or self._in_bias_zero.dtype != abd_bias.dtype or self._in_bias_zero.device != abd_bias.device:
+                self._in_bias_zero = torch.zeros(D3 + Dg, dtype=abd_bias.dtype, device=abd_bias.device)
+            w_in = self._in_weight.get(self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, g0.weight,
+                                       self.a_proj.weight, self.b_proj.weight, self.d_proj.weight)
+            b_in = self._in_bias.get(self._in_bias_zero, abd_bias)
+            y_in = _native.linear(x, w_in, b_in, out_cols=(D3 + Dg + 3 * H + 7) // 8 * 8)
+            qkv, g0_out, abd = y_in[..., :D3], y_in[..., D3:D3 + Dg], y_in[..., D3 + Dg:]
+        else:
+            qkv = _native.linear(x, self._qkv_weight.get(self.q_proj.weight, self.k_proj.weight, self.v_proj.weight))
+            g0_out = abd = None
         conv_cache = None if cache is None else cache.get("conv_state")
         cat_cache = None
         if conv_cache is not None:
@@ -305,11 +332,9 @@ class CyclicFlowAttention(nn.Module):
             (y,) = _native.short_conv(qkv, wconv.reshape(-1, W).to(x.dtype), None, cat_cache, cache_out=tail)
             q, k, v = y[..., :Dk].contiguous(), y[..., Dk:2 * Dk].contiguous(), y[..., 2 * Dk:].contiguous()
         cq, ck, cv = tail[..., :Dk], tail[..., Dk:2 * Dk], tail[..., 2 * Dk:]
-        if self._a_bias_zero is None or self._a_bias_zero.dtype != self.b_proj.bias.dtype \
-                or self._a_bias_zero.device != self.b_proj.bias.device:
-            self._a_bias_zero = torch.zeros_like(self.b_proj.bias.detach())
-        abd = F.linear(x, self._abd_weight.get(self.a_proj.weight, self.b_proj.weight, self.d_proj.weight),
-                       self._abd_bias.get(self._a_bias_zero, self.b_proj.bias, self.d_proj.bias))
+        if abd is None:
+            abd = _native.linear(x, self._abd_weight.get(self.a_proj.weight, self.b_proj.weight, self.d_proj.weight),
+                                 abd_bias)
         g, beta, delta = _native.gates(abd, self.dt_bias, self.A_log)
         kwargs = dict(
             q=q.view(B, T, H, self.head_k_dim),
@@ -326,7 +351,9 @@ class CyclicFlowAttention(nn.Module):
             initial_state=None if cache is None else cache["recurrent_state"],
             output_final_state=use_cache,
         )
-        gate = self.g_proj(x).view(B, T, H, self.head_v_dim)
+        if g0_out is None:
+            g0_out = _native.linear(x, g0.weight)
+        gate = _native.linear(g0_out, g1.weight, g1.bias).view(B, T, H, self.head_v_dim)
         if not self.training and T == 1:
             o, state = fused_recurrent_cyfa(**kwargs, table=self.readout_table(),
                                             inplace=self.decode_in_place and cache is not None)
@@ -337,7 +364,7 @@ class CyclicFlowAttention(nn.Module):
                                   output_norm=(self.o_norm.weight, gate, self.o_norm.eps,
                                                float(self.num_slots - 1)))
             o = o.view(B, T, Dv)
-        o = self.o_proj(o)
+        o = _native.linear(o, self.o_proj.weight)
         new_cache = {"recurrent_state": state, "conv_state": (cq, ck, cv)} if use_cache else None
         return o, new_cache
 

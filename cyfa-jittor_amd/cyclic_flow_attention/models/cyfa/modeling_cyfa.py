@@ -31,8 +31,8 @@ class GatedMLP(nn.Module):
     def forward(self, x):
         if inference_fast_path(x) and self.gate_proj.weight.shape[0] % 8 == 0:
             # one [gate | up] GEMM and the fused SwiGLU kernel
-            gu = F.linear(x, self._gate_up.get(self.gate_proj.weight, self.up_proj.weight))
-            return self.down_proj(_native.silu_mul(gu))
+            gu = _native.linear(x, self._gate_up.get(self.gate_proj.weight, self.up_proj.weight))
+            return _native.linear(_native.silu_mul(gu), self.down_proj.weight)
         g = self.gate_proj(x)
         u = self.up_proj(x)
         return self.down_proj((F.silu(g.float()) * u.float()).to(x.dtype))
@@ -113,7 +113,10 @@ class CyclicFlowAttentionForCausalLM(nn.Module):
 
     def forward(self, input_ids, labels=None, cache=None, use_cache=False, attention_mask=None):
         hidden, cache = self.model(input_ids, cache, use_cache, attention_mask)
-        logits = self.lm_head(hidden)
+        if inference_fast_path(hidden):
+            logits = _native.linear(hidden, self.lm_head.weight)
+        else:
+            logits = self.lm_head(hidden)
         loss = None
         if labels is not None:
             loss = F.cross_entropy(

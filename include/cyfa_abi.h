@@ -170,6 +170,26 @@ typedef struct CyfaNormArgs {
  * and the residual adds of CyFABlock.execute (modeling_cyfa.py:48-51). */
 int cyfa_rms_norm(const CyfaNormArgs *args, void *hip_stream);
 
+/* Arguments of one projection y = x W^T (+ bias) over at most 64 rows of x
+ * (1 <= M <= 64; K a positive multiple of 32). */
+typedef struct CyfaLinearArgs {
+    int M, N, K;
+    const void *x;                /* bf16 [M, K], rows ldx elements apart (ldx >= K, ldx % 8 == 0) */
+    long long ldx;
+    const void *weight;           /* bf16 [N, K] row-major (torch Linear weight) */
+    const void *bias;             /* nullable bf16 [N] */
+    void *y;                      /* bf16 [M, N], rows ldy elements apart */
+    long long ldy;
+} CyfaLinearArgs;
+
+/* Replaces the Linear / BiasLinear projections (layers/cyfa.py:15-58) of the
+ * one-token decode step when it has at most 64 rows: the q/k/v, a/b/d, g and
+ * o projections of CyclicFlowAttention.execute (layers/cyfa.py:302, 323-326,
+ * 349, 351), the GatedMLP projections (models/cyfa/modeling_cyfa.py:13-28) and
+ * the lm_head (models/cyfa/modeling_cyfa.py:80, 100). fp32 accumulation, one bf16
+ * rounding. */
+int cyfa_linear_rows(const CyfaLinearArgs *args, void *hip_stream);
+
 /* Arguments of one causal depthwise convolution over time of B x T rows of D
  * bf16 channels (D a multiple of 8, W in 2..4):
  *   y[b,t,c] = bias[c] + sum_{w<W} weight[c,w] * X[b, t + w - (W-1), c],
@@ -201,11 +221,12 @@ int cyfa_short_conv(const CyfaConvArgs *args, void *hip_stream);
  * (modeling_cyfa.py:22-27). */
 int cyfa_silu_mul(const void *gu, void *out, int rows, int F, void *hip_stream);
 
-/* Gate activations from the fused a|b|d projection abd [rows, 3H] bf16 (b and
- * d biases included): g = -exp(A_log) softplus(a + dt_bias), beta =
- * sigmoid(b), delta = sigmoid(d), f32 [rows, H]. Replaces layers/cyfa.py:323-326. */
-int cyfa_gates(const void *abd, const float *dt_bias, const float *A_log, float *g, float *beta, float *delta,
-               int rows, int H, void *hip_stream);
+/* Gate activations from the fused a|b|d projection abd [rows, 3H] bf16 (rows
+ * abd_row elements apart; b and d biases included): g = -exp(A_log)
+ * softplus(a + dt_bias), beta = sigmoid(b), delta = sigmoid(d), f32 [rows, H].
+ * Replaces layers/cyfa.py:323-326. */
+int cyfa_gates(const void *abd, long long abd_row, const float *dt_bias, const float *A_log, float *g, float *beta,
+               float *delta, int rows, int H, void *hip_stream);
 
 /* Thread-local message of the last failing call (never NULL). No reference
  * counterpart: Jittor reports kernel errors as C++ exceptions. */

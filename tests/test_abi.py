@@ -48,7 +48,8 @@ def _c_layout(tmp_path, struct, fields):
                                       (_native.CyfaOutNormArgs, "CyfaOutNormArgs"),
                                       (_native.CyfaSlaArgs, "CyfaSlaArgs"),
                                       (_native.CyfaNormArgs, "CyfaNormArgs"),
-                                      (_native.CyfaConvArgs, "CyfaConvArgs")])
+                                      (_native.CyfaConvArgs, "CyfaConvArgs"),
+                                      (_native.CyfaLinearArgs, "CyfaLinearArgs")])
 def test_struct_layout_matches_header(tmp_path, cls, name):
     fields = [f for f, _ in cls._fields_]
     got = [ctypes.sizeof(cls)] + [getattr(cls, f).offset for f in fields]
@@ -108,7 +109,7 @@ def test_layer_entry_points_validate_before_launch():
     c.W, c.split = 4, 12
     assert lib.cyfa_short_conv(ctypes.byref(c), None) == _native.CYFA_ERR_UNSUPPORTED
     assert lib.cyfa_silu_mul(None, None, 1, 8, None) == _native.CYFA_ERR_VALUE
-    assert lib.cyfa_gates(None, None, None, None, None, None, 1, 4, None) == _native.CYFA_ERR_VALUE
+    assert lib.cyfa_gates(None, 12, None, None, None, None, None, 1, 4, None) == _native.CYFA_ERR_VALUE
 
 
 def test_scalar_la_validates_before_launch():

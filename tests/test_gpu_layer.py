@@ -231,3 +231,29 @@ def test_graphed_decode_matches_eager(name, layers, B):
             assert torch.equal(got, tok), f"step {step}: tokens differ"
             torch.randn(256, 256, device=DEV).matmul(torch.randn(256, 256, device=DEV))  # unrelated work
             torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("M,N,K,bias,ldx", [(1, 3072, 1024, False, 1024), (64, 12, 1024, True, 1024),
+                                            (17, 256, 1024, False, 1024), (64, 1024, 256, True, 256),
+                                            (33, 1024, 2816, False, 2816), (64, 32000, 1024, False, 1024),
+                                            (5, 100, 64, True, 3 * 64)])
+def test_linear_rows_kernel(M, N, K, bias, ldx):
+    """cyfa_linear_rows against x W^T + b in float64: one bf16 rounding of an
+    fp32 sum (bound: half a bf16 ulp of the result plus the fp32 summation
+    error, K 2^-24 sum |x||w|, with a factor of two to spare)."""
+    from cyclic_flow_attention import _native
+
+    gen = torch.Generator().manual_seed(M * N + K)
+    xs = torch.randn(M, ldx, generator=gen).bfloat16()
+    x = xs[:, :K]  # rows ldx apart
+    w = (0.05 * torch.randn(N, K, generator=gen)).bfloat16()
+    b = torch.randn(N, generator=gen).bfloat16() if bias else None
+    with torch.no_grad():
+        y = _native.linear(xs.to(DEV)[:, :K], w.to(DEV), None if b is None else b.to(DEV))
+    torch.cuda.synchronize()
+    assert y.shape == (M, N) and y.dtype == torch.bfloat16
+    ref = x.double() @ w.double().T + (0 if b is None else b.double())
+    bound = 2 * (BF16_ULP / 2 * ref.abs() + K * 2.0 ** -24 * (x.double().abs() @ w.double().abs().T)) + 1e-30
+    err = (y.cpu().double() - ref).abs()
+    assert (err <= bound).all(), f"max err {err.max().item()} vs bound {bound[err.argmax() // N, err.argmax() % N].item()}"
+

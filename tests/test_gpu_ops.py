@@ -257,3 +257,36 @@ def test_chunk_output_norm_equals_separate_norm(B, T, H, seg, monkeypatch):
     diff = (a - b).abs()
     assert (diff <= ulp).all(), f"max diff {diff.max().item()}"
     assert (diff > 0).float().mean().item() < 1e-2
+
+
+def test_config5_long_carry_prefill_then_decode():
+    """Configuration 5's attention shape: B=1, H=8, a 16384-token chunkwise
+    prefill (the clock reaches about 8200, 32 segments carry the state) followed
+    by 16 fused decode steps from the prefill's states, both against the oracle."""
+    from cyclic_flow_attention.ops import chunk_cyfa, fused_recurrent_cyfa
+
+    T, steps = 16384, 16
+    x, _ = _inputs(1, T + steps, 8, seed=5)
+    xg, _ = _gpu(x, None)
+    xd, _ = _oracle(x, None)
+    seq = ("q", "k", "v", "g", "delta", "beta")
+    pre_g = {k: (v[:, :T] if k in seq else v) for k, v in xg.items()}
+    pre_d = {k: (v[:, :T] if k in seq else v) for k, v in xd.items()}
+    with torch.no_grad():
+        o, st = chunk_cyfa(**pre_g, output_final_state=True)
+        outs = []
+        for t in range(T, T + steps):
+            step = {k: (v[:, t:t + 1] if k in seq else v) for k, v in xg.items()}
+            od, st = fused_recurrent_cyfa(**step, initial_state=st, output_final_state=True)
+            outs.append(od)
+    torch.cuda.synchronize()
+    ro, rst = O.chunk_cyfa(**pre_d, output_final_state=True)
+    assert_close(o, ro, what="config 5 prefill o")
+    routs = []
+    for t in range(T, T + steps):
+        step = {k: (v[:, t:t + 1] if k in seq else v) for k, v in xd.items()}
+        r1, rst_next = O.fused_recurrent_cyfa(**step, initial_state=rst, output_final_state=True)
+        routs.append(r1)
+        rst = rst_next
+    assert_close(torch.cat(outs, 1), torch.cat(routs, 1), what="config 5 decode o")
+    _check_states(st, rst, "config 5")
