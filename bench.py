@@ -51,7 +51,7 @@ FLOP_PER_TOKEN_HEAD_PASS = 156_032  # one ScalarGatedLA pass, causal-exact
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
 # scaled by a 1 GiB copy kernel (profiles/cyfa_chunk_fwd_cfg3_prefill.md,
 # profiles/cyfa_decode_step_cfg4.md); they apply to the default shapes.
-TRAFFIC_PREFILL_BYTES = 302.2e6    # one cyfa_chunk_fwd at B=8, T=2048, H=4
+TRAFFIC_PREFILL_BYTES = 343.2e6    # one cyfa_chunk_fwd_normed at B=8, T=2048, H=4
 TRAFFIC_DECODE_BYTES = 135.5e6     # one decode launch at B=64, H=4
 
 
