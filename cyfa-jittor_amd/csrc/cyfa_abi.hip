@@ -53,22 +53,41 @@ int cyfa_readout_table(const float* readout, float* table, int H, int M, void* h
     return check_launch("cyfa_readout_table");
 }
 
-int cyfa_decode_step(const CyfaDecodeArgs* a, void* hip_stream) {
+namespace {
+
+int decode_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* ly, void* hip_stream) {
     if (!a) return fail(CYFA_ERR_VALUE, "cyfa_decode_step: null args");
     if (a->M != 128) return fail(CYFA_ERR_UNSUPPORTED, "cyfa_decode_step: num_slots must be 128, got %d", a->M);
     if (!((a->K == 128 || a->K == 256) && (a->V == 128 || a->V == 256)))
         return fail(CYFA_ERR_UNSUPPORTED, "cyfa_decode_step: head dims K=%d V=%d not in {128, 256}", a->K, a->V);
     if (a->B <= 0 || a->H <= 0) return fail(CYFA_ERR_VALUE, "cyfa_decode_step: B=%d H=%d must be positive", a->B, a->H);
-    if (!a->q || !a->k || !a->v || !a->g || !a->delta || !a->beta || !a->table || !a->q_norm_weight ||
+    if ((!ly && (!a->q || !a->k || !a->v || !a->g || !a->delta || !a->beta)) || !a->table || !a->q_norm_weight ||
         !a->k_norm_weight || !a->o || !a->hk_out || !a->hv_out || !a->clock_out)
         return fail(CYFA_ERR_VALUE, "cyfa_decode_step: null required pointer");
+    if (ly) {
+        if (a->K != 256 || a->V != 256)
+            return fail(CYFA_ERR_UNSUPPORTED, "cyfa_decode_layer_step: head dims K=%d V=%d, the layer step needs 256",
+                        a->K, a->V);
+        if (!ly->qkv || !ly->conv_cache_out || !ly->conv_weight || !ly->abd || !ly->dt_bias || !ly->A_log ||
+            !ly->gate || !ly->norm_weight)
+            return fail(CYFA_ERR_VALUE, "cyfa_decode_layer_step: null required pointer");
+        const long long D = 3LL * a->H * 256;
+        if (ly->qkv_row < D || ly->abd_row < 3LL * a->H || ly->gate_row < (long long)a->H * 256 || ly->gate_row % 4 ||
+            ly->cache_row < D || ly->cache_batch < 3 * ly->cache_row)
+            return fail(CYFA_ERR_VALUE, "cyfa_decode_layer_step: row strides too small");
+        if (!aligned(ly->gate, 8) || !aligned(ly->norm_weight, 16))
+            return fail(CYFA_ERR_ALIGN, "cyfa_decode_layer_step: gate needs 8-byte and norm_weight 16-byte alignment");
+        if (!(ly->norm_eps >= 0.f) || !isfinite(ly->norm_prescale))
+            return fail(CYFA_ERR_VALUE, "cyfa_decode_layer_step: norm_eps=%g prescale=%g", (double)ly->norm_eps,
+                        (double)ly->norm_prescale);
+    }
     const bool has_in = a->hk_in != nullptr;
     if (has_in != (a->hv_in != nullptr) || has_in != (a->clock_in != nullptr))
         return fail(CYFA_ERR_VALUE, "cyfa_decode_step: hk_in, hv_in and clock_in must be all set or all null");
-    if (!aligned(a->v, 8) || !aligned(a->table, 16) || !aligned(a->hk_out, 16) || !aligned(a->hv_out, 16) ||
+    if ((!ly && !aligned(a->v, 8)) || !aligned(a->table, 16) || !aligned(a->hk_out, 16) || !aligned(a->hv_out, 16) ||
         (has_in && (!aligned(a->hk_in, 16) || !aligned(a->hv_in, 16))))
         return fail(CYFA_ERR_ALIGN, "cyfa_decode_step: states/table need 16-byte and v 8-byte alignment");
-    cyfa::DecodeParams p;
+    cyfa::DecodeParams p{};
     p.B = a->B;
     p.H = a->H;
     p.q = (const __bf16*)a->q;
@@ -90,9 +109,36 @@ int cyfa_decode_step(const CyfaDecodeArgs* a, void* hip_stream) {
     p.hk_out = a->hk_out;
     p.hv_out = a->hv_out;
     p.clock_out = a->clock_out;
+    if (ly) {
+        p.qkv = (const __bf16*)ly->qkv;
+        p.qkv_row = ly->qkv_row;
+        p.cache_in = (const __bf16*)ly->conv_cache;
+        p.cache_out = (__bf16*)ly->conv_cache_out;
+        p.cache_row = ly->cache_row;
+        p.cache_batch = ly->cache_batch;
+        p.conv_w = (const __bf16*)ly->conv_weight;
+        p.abd = (const __bf16*)ly->abd;
+        p.abd_row = ly->abd_row;
+        p.dt_bias = ly->dt_bias;
+        p.A_log = ly->A_log;
+        p.gate = (const __bf16*)ly->gate;
+        p.gate_row = ly->gate_row;
+        p.on_w = ly->norm_weight;
+        p.on_eps = ly->norm_eps;
+        p.on_prescale = ly->norm_prescale;
+    }
     if (cyfa::launch_decode_step(p, a->K, a->V, (hipStream_t)hip_stream) != 0)
         return fail(CYFA_ERR_UNSUPPORTED, "cyfa_decode_step: no kernel for K=%d V=%d", a->K, a->V);
-    return check_launch("cyfa_decode_step");
+    return check_launch(ly ? "cyfa_decode_layer_step" : "cyfa_decode_step");
+}
+
+}  // namespace
+
+int cyfa_decode_step(const CyfaDecodeArgs* a, void* hip_stream) { return decode_step(a, nullptr, hip_stream); }
+
+int cyfa_decode_layer_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* layer, void* hip_stream) {
+    if (!layer) return fail(CYFA_ERR_VALUE, "cyfa_decode_layer_step: null layer args");
+    return decode_step(a, layer, hip_stream);
 }
 
 namespace {
@@ -135,7 +181,7 @@ int chunk_fwd(const CyfaChunkArgs* a, const CyfaOutNormArgs* on, void* hip_strea
                         (double)on->prescale);
     }
 
-    cyfa::PrefillParams p;
+    cyfa::PrefillParams p{};
     p.B = a->B;
     p.T = a->T;
     p.H = a->H;
@@ -212,7 +258,7 @@ int cyfa_scalar_la(const CyfaSlaArgs* a, void* hip_stream) {
         return fail(CYFA_ERR_WORKSPACE, "cyfa_scalar_la: workspace of %zu bytes needed, got %zu", ws.total,
                     a->workspace ? a->workspace_bytes : (size_t)0);
     if (!aligned(a->workspace, 256)) return fail(CYFA_ERR_ALIGN, "cyfa_scalar_la: workspace needs 256-byte alignment");
-    cyfa::SlaParams p;
+    cyfa::SlaParams p{};
     p.B = a->B;
     p.T = a->T;
     p.H = a->H;

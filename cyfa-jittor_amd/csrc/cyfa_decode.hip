@@ -32,7 +32,14 @@ __device__ __forceinline__ void stream_store(float4* p, const float4& v) {
     __builtin_nontemporal_store(__builtin_bit_cast(f32x4, v), reinterpret_cast<f32x4*>(p));
 }
 
-template <int K, int V>
+// LAYER: the layer's one-token step around the op in the same kernel. The
+// width-4 causal short convolution of the projection row (layers/cyfa.py:138-233,
+// the arithmetic of short_conv_kernel) gives this head's q, k and v and the new
+// conv cache; the gate activations (layers/cyfa.py:323-326, as gates_kernel)
+// come from the a|b|d row; and o goes through the gated output norm
+// o_norm(o * prescale, gate) (layers/cyfa.py:349-350, as rms_norm_kernel<1>:
+// wave 0 holds four consecutive values per lane) before it is stored.
+template <int K, int V, bool LAYER>
 __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     constexpr int NT = 1024;
     constexpr int KJ = K / 32;      // float4 of hk per thread (row has 32 float4)
@@ -47,6 +54,7 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     __shared__ float s_p[kSlots], s_om[kSlots], s_c[kPairs], s_s[kPairs];
     __shared__ float s_part[NW][V > kSlots ? V : kSlots];
     __shared__ float s_red[2][NW];
+    __shared__ float s_v[LAYER ? V : 1];
 
     const bool has_state = p.hk_in != nullptr;
     const float4* hk_in = reinterpret_cast<const float4*>(p.hk_in + (size_t)bh * K * kSlots);
@@ -70,9 +78,43 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
 
     // q/k RMS statistics (ops/fused_recurrent.py:62-89).
     float qv = 0.f, kv = 0.f;
-    if (tid < K) {
-        qv = (float)p.q[(size_t)bh * K + tid];
-        kv = (float)p.k[(size_t)bh * K + tid];
+    float g_in, delta_in, beta_in;
+    if (LAYER) {
+        const int b = bh / p.H;
+        const int HK = p.H * K;
+        auto conv = [&](int ch) -> float {
+            float win[4];
+#pragma unroll
+            for (int w = 0; w < 3; w++)
+                win[w] = p.cache_in ? (float)p.cache_in[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch] : 0.f;
+            win[3] = (float)p.qkv[(size_t)b * p.qkv_row + ch];
+            float acc = win[0] * (float)p.conv_w[(size_t)ch * 4];
+#pragma unroll
+            for (int w = 1; w < 4; w++) acc = fmaf(win[w], (float)p.conv_w[(size_t)ch * 4 + w], acc);
+#pragma unroll
+            for (int w = 0; w < 3; w++)
+                p.cache_out[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch] = (bf16_t)win[w + 1];
+            return bf16_round(acc);
+        };
+        if (tid < K) {
+            qv = conv(h * K + tid);
+            kv = conv(HK + h * K + tid);
+        }
+        if (tid < V) s_v[tid] = conv(2 * HK + h * V + tid);
+        const bf16_t* row = p.abd + (size_t)b * p.abd_row;
+        const float a = (float)row[h] + p.dt_bias[h];
+        const float sp = a > 20.f ? a : log1pf(expf(a));
+        g_in = -expf(p.A_log[h]) * sp;
+        beta_in = sigmoidf((float)row[p.H + h]);
+        delta_in = sigmoidf((float)row[2 * p.H + h]);
+    } else {
+        if (tid < K) {
+            qv = (float)p.q[(size_t)bh * K + tid];
+            kv = (float)p.k[(size_t)bh * K + tid];
+        }
+        g_in = p.g[bh];
+        delta_in = p.delta[bh];
+        beta_in = p.beta[bh];
     }
     const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
     if (lane == 0 && wave < K / 64) {
@@ -80,9 +122,9 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
         s_red[1][wave] = sk;
     }
     const float clock = has_state ? p.clock_in[bh] : 0.f;
-    const float lam = clock + p.delta[bh];
-    const float decay = expf(p.g[bh]);
-    const float beta = p.beta[bh];
+    const float lam = clock + delta_in;
+    const float decay = expf(g_in);
+    const float beta = beta_in;
     if (tid < kPairs) {
         float s, c;
         pair_sincos(reduced_clock(lam), tid, s, c);
@@ -141,8 +183,19 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     // Value state: hv' = alpha hv + w (x) v, written now; kept in hv_r for o.
     {
         const int v4 = (tid % VQ) * 4, r0 = tid / VQ;
-        const bf16x4 vb = *reinterpret_cast<const bf16x4*>(p.v + (size_t)bh * V + v4);
-        const float v0 = (float)vb[0], v1 = (float)vb[1], v2 = (float)vb[2], v3 = (float)vb[3];
+        float v0, v1, v2, v3;
+        if (LAYER) {
+            v0 = s_v[v4];
+            v1 = s_v[v4 + 1];
+            v2 = s_v[v4 + 2];
+            v3 = s_v[v4 + 3];
+        } else {
+            const bf16x4 vb = *reinterpret_cast<const bf16x4*>(p.v + (size_t)bh * V + v4);
+            v0 = (float)vb[0];
+            v1 = (float)vb[1];
+            v2 = (float)vb[2];
+            v3 = (float)vb[3];
+        }
 #pragma unroll
         for (int j = 0; j < VJ; j++) {
             const float wm = s_w[r0 + VROWS * j];
@@ -248,24 +301,66 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
         }
     }
     __syncthreads();
+    if (!LAYER) {
+        if (tid < V) {
+            float s = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) s += s_part[w][tid];
+            p.o[(size_t)bh * V + tid] = (bf16_t)s;
+        }
+        return;
+    }
     if (tid < V) {
         float s = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; w++) s += s_part[w][tid];
-        p.o[(size_t)bh * V + tid] = (bf16_t)s;
+        s_v[tid] = (float)(bf16_t)s;  // o as the op would store it
+    }
+    __syncthreads();
+    if (wave == 0) {
+        constexpr int J = (V + 255) / 256;  // four consecutive values per lane and 256-wide block (V = 256)
+        const int b = bh / p.H;
+        float xs[J][4];
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < J; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float x = s_v[4 * lane + 256 * j + i];
+                if (p.on_prescale != 1.f) x = bf16_round(x * p.on_prescale);
+                xs[j][i] = x;
+                ss = fmaf(x, x, ss);
+            }
+        ss = wave_sum(ss);
+        const float rs = rsqrtf(ss / (float)V + p.on_eps);
+        const bf16_t* gt = p.gate + (size_t)b * p.gate_row + (size_t)h * V;
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            const int d0 = 4 * lane + 256 * j;
+            const float4 w = *reinterpret_cast<const float4*>(p.on_w + d0);
+            const bf16x4 g4 = *reinterpret_cast<const bf16x4*>(gt + d0);
+            const float wa[4] = {w.x, w.y, w.z, w.w};
+            bf16x4 y;
+#pragma unroll
+            for (int i = 0; i < 4; i++) y[i] = (bf16_t)(xs[j][i] * rs * wa[i] * sigmoidf((float)g4[i]));
+            *reinterpret_cast<bf16x4*>(p.o + (size_t)bh * V + d0) = y;
+        }
     }
 }
 
 int launch_decode_step(const DecodeParams& p, int K, int V, hipStream_t stream) {
     dim3 grid(p.B * p.H), block(1024);
-    if (K == 256 && V == 256)
-        hipLaunchKernelGGL((decode_step_kernel<256, 256>), grid, block, 0, stream, p);
+    if (p.qkv) {  // the layer step: K = V = 256 only
+        if (K != 256 || V != 256) return -1;
+        hipLaunchKernelGGL((decode_step_kernel<256, 256, true>), grid, block, 0, stream, p);
+    } else if (K == 256 && V == 256)
+        hipLaunchKernelGGL((decode_step_kernel<256, 256, false>), grid, block, 0, stream, p);
     else if (K == 128 && V == 128)
-        hipLaunchKernelGGL((decode_step_kernel<128, 128>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((decode_step_kernel<128, 128, false>), grid, block, 0, stream, p);
     else if (K == 256 && V == 128)
-        hipLaunchKernelGGL((decode_step_kernel<256, 128>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((decode_step_kernel<256, 128, false>), grid, block, 0, stream, p);
     else if (K == 128 && V == 256)
-        hipLaunchKernelGGL((decode_step_kernel<128, 256>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((decode_step_kernel<128, 256, false>), grid, block, 0, stream, p);
     else
         return -1;
     return 0;

@@ -15,6 +15,22 @@ struct DecodeParams {
     const float *hk_in, *hv_in, *clock_in;
     __bf16* o;
     float *hk_out, *hv_out, *clock_out;
+    // Layer step (decode_step_kernel<.., true>): q, k, v come from the width-4
+    // short convolution of the projection row qkv, the gates from abd, and o
+    // receives the gated output norm instead of the op's output.
+    const __bf16* qkv;       // row b at qkv + b * qkv_row: q (H K) | k (H K) | v (H V)
+    long long qkv_row;
+    const __bf16* cache_in;  // nullable: [B, 3, 2 H K + H V] rows cache_row, batches cache_batch
+    __bf16* cache_out;       // the new cache, same addressing (may be cache_in)
+    long long cache_row, cache_batch;
+    const __bf16* conv_w;    // [2 H K + H V, 4]
+    const __bf16* abd;       // row b at abd + b * abd_row: a (H) | b (H) | d (H)
+    long long abd_row;
+    const float *dt_bias, *A_log;
+    const __bf16* gate;      // row b at gate + b * gate_row: [H V]
+    long long gate_row;
+    const float* on_w;       // [V]
+    float on_eps, on_prescale;
 };
 
 // Prefill: T is split into N = ceil(T / 64) chunks and every (batch, head)

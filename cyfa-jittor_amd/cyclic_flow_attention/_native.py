@@ -65,6 +65,17 @@ class CyfaDecodeArgs(ctypes.Structure):
     ]
 
 
+class CyfaDecodeLayerArgs(ctypes.Structure):
+    _fields_ = [
+        ("qkv", _c_void_p), ("qkv_row", ctypes.c_longlong),
+        ("conv_cache", _c_void_p), ("conv_cache_out", _c_void_p),
+        ("cache_row", ctypes.c_longlong), ("cache_batch", ctypes.c_longlong),
+        ("conv_weight", _c_void_p), ("abd", _c_void_p), ("abd_row", ctypes.c_longlong),
+        ("dt_bias", _c_void_p), ("A_log", _c_void_p), ("gate", _c_void_p), ("gate_row", ctypes.c_longlong),
+        ("norm_weight", _c_void_p), ("norm_eps", _c_float), ("norm_prescale", _c_float),
+    ]
+
+
 class CyfaNormArgs(ctypes.Structure):
     _fields_ = [
         ("rows", _c_int), ("D", _c_int),
@@ -102,6 +113,7 @@ SIGNATURES = {
     "cyfa_scalar_la": (_c_int, [ctypes.POINTER(CyfaSlaArgs), _c_void_p]),
     "cyfa_scalar_la_workspace_bytes": (_c_size_t, [_c_int] * 5),
     "cyfa_decode_step": (_c_int, [ctypes.POINTER(CyfaDecodeArgs), _c_void_p]),
+    "cyfa_decode_layer_step": (_c_int, [ctypes.POINTER(CyfaDecodeArgs), ctypes.POINTER(CyfaDecodeLayerArgs), _c_void_p]),
     "cyfa_readout_table": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "cyfa_rms_norm": (_c_int, [ctypes.POINTER(CyfaNormArgs), _c_void_p]),
     "cyfa_short_conv": (_c_int, [ctypes.POINTER(CyfaConvArgs), _c_void_p]),
@@ -251,6 +263,14 @@ def decode_step(args: CyfaDecodeArgs, device):
     rc = _timed("cyfa_decode_step", lambda: lib.cyfa_decode_step(ctypes.byref(args), stream_handle(device)))
     if rc != CYFA_OK:
         _raise(rc, "cyfa_decode_step failed")
+
+
+def decode_layer_step(args: CyfaDecodeArgs, layer: CyfaDecodeLayerArgs, device):
+    lib = load_library()
+    rc = _timed("cyfa_decode_layer_step",
+                lambda: lib.cyfa_decode_layer_step(ctypes.byref(args), ctypes.byref(layer), stream_handle(device)))
+    if rc != CYFA_OK:
+        _raise(rc, "cyfa_decode_layer_step failed")
 
 
 def readout_table(readout: torch.Tensor) -> torch.Tensor:

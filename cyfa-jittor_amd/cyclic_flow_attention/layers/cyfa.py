@@ -27,6 +27,7 @@ from torch import nn
 
 from .. import _native
 from ..ops import chunk_cyfa, fused_recurrent_cyfa
+from ..ops.fused_recurrent import decode_layer_step
 from ..ops.utils import readout_table
 
 
@@ -325,6 +326,27 @@ class CyclicFlowAttention(nn.Module):
         in_place = self.decode_in_place and cat_cache is not None and T <= 32
         tail = cat_cache if in_place else torch.empty(B, W - 1, qkv.shape[-1], dtype=x.dtype, device=x.device)
         wconv = self._conv_weight.get(self.q_conv1d.weight, self.k_conv1d.weight, self.v_conv1d.weight)
+        if (not self.training and T == 1 and W == 4 and self.head_k_dim == 256 and self.head_v_dim == 256
+                and all(c.bias is None for c in (self.q_conv1d, self.k_conv1d, self.v_conv1d))
+                and (cat_cache is None or cat_cache.stride() == tail.stride())):
+            # one-token step: short convolution, gates, the decode op and the
+            # gated output norm in one kernel
+            if abd is None:
+                abd = _native.linear(x, self._abd_weight.get(self.a_proj.weight, self.b_proj.weight,
+                                                              self.d_proj.weight), abd_bias)
+            if g0_out is None:
+                g0_out = _native.linear(x, g0.weight)
+            gate = _native.linear(g0_out, g1.weight, g1.bias)
+            o, state = decode_layer_step(
+                qkv, cat_cache, tail, wconv.reshape(-1, W).to(x.dtype), abd, self.dt_bias, self.A_log, gate,
+                self.o_norm.weight, self.o_norm.eps, float(self.num_slots - 1), self.readout_table(),
+                self.q_norm.weight, self.k_norm.weight, self.q_norm.eps, self.k_norm.eps, H,
+                initial_state=None if cache is None else cache["recurrent_state"], output_final_state=use_cache,
+                inplace=self.decode_in_place and cache is not None)
+            o = _native.linear(o.view(B, T, Dv), self.o_proj.weight)
+            cq, ck, cv = tail[..., :Dk], tail[..., Dk:2 * Dk], tail[..., 2 * Dk:]
+            new_cache = {"recurrent_state": state, "conv_state": (cq, ck, cv)} if use_cache else None
+            return o, new_cache
         if Dk == Dv:
             q, k, v = _native.short_conv(qkv, wconv.reshape(-1, W).to(x.dtype), None, cat_cache, split=Dk,
                                          cache_out=tail)

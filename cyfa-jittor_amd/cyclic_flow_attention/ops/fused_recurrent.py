@@ -93,3 +93,64 @@ def fused_recurrent_cyfa(
     )
     _native.decode_step(args, dev)
     return o, ((hk_out, hv_out, c_out) if output_final_state else None)
+
+
+def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias, A_log, gate, norm_weight, norm_eps,
+                      norm_prescale, table, q_norm_weight, k_norm_weight, q_norm_eps, k_norm_eps, num_heads,
+                      initial_state=None, output_final_state=False, inplace=False):
+    """The layer's one-token step around the op in one kernel (cyfa_decode_layer_step).
+
+    qkv [B, 1, 3 H 256] is the projection before the short convolution (rows
+    may be strided), conv_cache / conv_cache_out [B, 3, 3 H 256] the conv
+    history in and out (conv_cache may be None; conv_cache_out may be
+    conv_cache), conv_weight [3 H 256, 4], abd [B, 1, 3H] the a|b|d projection
+    with its biases, gate [B, 1, H 256]. Returns (o', states) with o' the gated
+    output norm o_norm(o * norm_prescale, gate) of the op's output, [B, 1, H, 256],
+    and the states as fused_recurrent_cyfa returns them.
+    """
+    B = qkv.shape[0]
+    H, K, V, M = num_heads, 256, 256, table.shape[-1]
+    dev = _native.require_device(qkv, conv_cache_out, conv_weight, abd, gate, table)
+    D = 2 * H * K + H * V
+    if qkv.shape[-1] != D or qkv.stride(-1) != 1 or conv_weight.shape != (D, 4) or not conv_weight.is_contiguous():
+        raise ValueError("decode_layer_step: qkv must have 3 H 256 unit-stride columns and conv_weight [3 H 256, 4]")
+    if conv_cache is not None and conv_cache.stride() != conv_cache_out.stride():
+        raise ValueError("decode_layer_step: conv_cache and conv_cache_out must share their layout")
+    qw = q_norm_weight.to(torch.float32).contiguous()
+    kw = k_norm_weight.to(torch.float32).contiguous()
+    db = dt_bias.detach().to(torch.float32).contiguous()
+    al = A_log.detach().to(torch.float32).contiguous()
+    nw = norm_weight.detach().to(torch.float32).contiguous()
+    if initial_state is not None:
+        hk_in, hv_in, c_in = initial_state
+        if inplace:
+            for x in (hk_in, hv_in, c_in):
+                if x.dtype != torch.float32 or not x.is_contiguous():
+                    raise ValueError("inplace decode needs contiguous fp32 state tensors")
+        else:
+            hk_in, hv_in, c_in = (x.to(torch.float32).contiguous() for x in (hk_in, hv_in, c_in))
+    else:
+        hk_in = hv_in = c_in = None
+    if inplace and initial_state is not None:
+        hk_out, hv_out, c_out = hk_in, hv_in, c_in
+    else:
+        hk_out = torch.empty(B, H, K, M, dtype=torch.float32, device=dev)
+        hv_out = torch.empty(B, H, M, V, dtype=torch.float32, device=dev)
+        c_out = torch.empty(B, H, dtype=torch.float32, device=dev)
+    o = torch.empty(B, 1, H, V, dtype=torch.bfloat16, device=dev)
+    args = _native.CyfaDecodeArgs(
+        B=B, H=H, K=K, V=V, M=M, table=table.data_ptr(), q_norm_weight=qw.data_ptr(), k_norm_weight=kw.data_ptr(),
+        q_norm_eps=float(q_norm_eps), k_norm_eps=float(k_norm_eps), scale=float(K ** -0.5),
+        hk_in=_native.ptr(hk_in), hv_in=_native.ptr(hv_in), clock_in=_native.ptr(c_in),
+        o=o.data_ptr(), hk_out=hk_out.data_ptr(), hv_out=hv_out.data_ptr(), clock_out=c_out.data_ptr(),
+    )
+    layer = _native.CyfaDecodeLayerArgs(
+        qkv=qkv.data_ptr(), qkv_row=qkv.stride(0), conv_cache=_native.ptr(conv_cache),
+        conv_cache_out=conv_cache_out.data_ptr(), cache_row=conv_cache_out.stride(1),
+        cache_batch=conv_cache_out.stride(0), conv_weight=conv_weight.data_ptr(), abd=abd.data_ptr(),
+        abd_row=abd.stride(0), dt_bias=db.data_ptr(), A_log=al.data_ptr(), gate=gate.data_ptr(),
+        gate_row=gate.stride(0), norm_weight=nw.data_ptr(), norm_eps=float(norm_eps),
+        norm_prescale=float(norm_prescale),
+    )
+    _native.decode_layer_step(args, layer, dev)
+    return o, ((hk_out, hv_out, c_out) if output_final_state else None)

@@ -142,6 +142,35 @@ typedef struct CyfaDecodeArgs {
  * (hk_out == hk_in, ...) is allowed. */
 int cyfa_decode_step(const CyfaDecodeArgs *args, void *hip_stream);
 
+/* The rest of the layer's one-token step, for the decode loop (K = V = 256,
+ * conv width 4, no conv bias). */
+typedef struct CyfaDecodeLayerArgs {
+    const void *qkv;              /* bf16 projection rows [B, qkv_row] before the convolution:
+                                     q (H K) | k (H K) | v (H V) */
+    long long qkv_row;
+    const void *conv_cache;       /* nullable bf16 [B, 3, 3 H 256] (zero history) */
+    void *conv_cache_out;         /* bf16, same addressing; may be conv_cache (updated in place) */
+    long long cache_row, cache_batch;
+    const void *conv_weight;      /* bf16 [3 H 256, 4] */
+    const void *abd;              /* bf16 rows [B, abd_row]: a | b | d (H each), b and d biases added */
+    long long abd_row;
+    const float *dt_bias, *A_log; /* f32 [H] */
+    const void *gate;             /* bf16 rows [B, gate_row]: [H 256], 8-byte aligned */
+    long long gate_row;
+    const float *norm_weight;     /* f32 [256] */
+    float norm_eps, norm_prescale;
+} CyfaDecodeLayerArgs;
+
+/* cyfa_decode_step with the layer around it in the same kernel: q, k and v
+ * from the width-4 causal short convolution of the projection row and the new
+ * conv cache (ShortConvolution, layers/cyfa.py:138-233), the gate activations
+ * from the a|b|d row (layers/cyfa.py:323-326), and args->o receives the gated
+ * output norm o_norm(o * prescale, gate) (layers/cyfa.py:349-350) instead of
+ * o. args->q, k, v, g, delta and beta are not read. Replaces those steps of
+ * CyclicFlowAttention.execute for a one-token step together with
+ * fused_recurrent_cyfa (ops/fused_recurrent.py:10-200). */
+int cyfa_decode_layer_step(const CyfaDecodeArgs *args, const CyfaDecodeLayerArgs *layer, void *hip_stream);
+
 /* table[h] = readout[h] @ Phi, with Phi the real-DFT slot basis [M-1, M].
  * Replaces _basis + jt.matmul (ops/chunk.py:82-103, 281;
  * ops/fused_recurrent.py:53). readout f32 [H, M-1, M-1]; table f32 [H, M-1, M]. */

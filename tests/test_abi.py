@@ -47,6 +47,7 @@ def _c_layout(tmp_path, struct, fields):
                                       (_native.CyfaDecodeArgs, "CyfaDecodeArgs"),
                                       (_native.CyfaOutNormArgs, "CyfaOutNormArgs"),
                                       (_native.CyfaSlaArgs, "CyfaSlaArgs"),
+                                      (_native.CyfaDecodeLayerArgs, "CyfaDecodeLayerArgs"),
                                       (_native.CyfaNormArgs, "CyfaNormArgs"),
                                       (_native.CyfaConvArgs, "CyfaConvArgs"),
                                       (_native.CyfaLinearArgs, "CyfaLinearArgs")])

@@ -257,3 +257,55 @@ def test_linear_rows_kernel(M, N, K, bias, ldx):
     err = (y.cpu().double() - ref).abs()
     assert (err <= bound).all(), f"max err {err.max().item()} vs bound {bound[err.argmax() // N, err.argmax() % N].item()}"
 
+
+
+@pytest.mark.parametrize("B,state,inplace", [(3, True, False), (2, False, False), (4, True, True)])
+def test_decode_layer_step_equals_separate_kernels(B, state, inplace):
+    """cyfa_decode_layer_step (short convolution, gates, decode op and gated
+    output norm in one kernel) against the four separate kernels on the same
+    inputs: the same arithmetic in the same order, so outputs, states and the
+    new conv cache are bit-identical."""
+    from cyclic_flow_attention import _native
+    from cyclic_flow_attention.ops import fused_recurrent_cyfa
+    from cyclic_flow_attention.ops.fused_recurrent import decode_layer_step
+
+    H, D = 4, 3 * 4 * 256
+    gen = torch.Generator().manual_seed(B + 10 * state + 100 * inplace)
+    qkv_rows = torch.randn(B, 1, D + 40, generator=gen).bfloat16().to(DEV)
+    qkv = qkv_rows[..., :D]  # rows D + 40 apart
+    cache = (0.5 * torch.randn(B, 3, D, generator=gen)).bfloat16().to(DEV) if state else None
+    wconv = (0.3 * torch.randn(D, 4, generator=gen)).bfloat16().to(DEV)
+    abd = torch.randn(B, 1, 3 * H, generator=gen).bfloat16().to(DEV)
+    dt_bias, A_log = torch.randn(H, generator=gen).to(DEV), torch.randn(H, generator=gen).to(DEV)
+    gate = torch.randn(B, 1, H * 256, generator=gen).bfloat16().to(DEV)
+    nw = (1 + 0.1 * torch.randn(256, generator=gen)).to(DEV)
+    qw, kw = (1 + 0.1 * torch.randn(256, generator=gen)).to(DEV), (1 + 0.1 * torch.randn(256, generator=gen)).to(DEV)
+    readout = (torch.eye(127).expand(H, 127, 127) + 0.05 * torch.randn(H, 127, 127, generator=gen)).to(DEV)
+    init = None
+    if state:
+        init = (0.3 * torch.randn(B, H, 256, 128, generator=gen).to(DEV),
+                0.3 * torch.randn(B, H, 128, 256, generator=gen).to(DEV), 50 * torch.rand(B, H, generator=gen).to(DEV))
+    table = _native.readout_table(readout)
+    with torch.no_grad():
+        # separate kernels
+        tail_ref = torch.empty(B, 3, D, dtype=torch.bfloat16, device=DEV)
+        q, k, v = _native.short_conv(qkv, wconv, None, cache, split=H * 256, cache_out=tail_ref)
+        g, beta, delta = _native.gates(abd, dt_bias, A_log)
+        o, st = fused_recurrent_cyfa(q.view(B, 1, H, 256), k.view(B, 1, H, 256), v.view(B, 1, H, 256), g, delta, beta,
+                                     readout, qw, kw, initial_state=None if init is None else tuple(t.clone() for t in init),
+                                     output_final_state=True, table=table)
+        ref = _native.rms_norm(o.view(B, 1, H, 256), nw, 1e-6, gate.view(B, 1, H, 256), prescale=127.0)
+        # one kernel
+        cache_in = None if cache is None else cache.clone()
+        tail = cache_in if (inplace and cache_in is not None) else torch.empty(B, 3, D, dtype=torch.bfloat16, device=DEV)
+        st_in = None if init is None else tuple(t.clone() for t in init)
+        got, st2 = decode_layer_step(qkv, cache_in, tail, wconv, abd, dt_bias, A_log, gate, nw, 1e-6, 127.0, table, qw,
+                                     kw, 1e-6, 1e-6, H, initial_state=st_in, output_final_state=True,
+                                     inplace=inplace and st_in is not None)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    assert torch.equal(tail, tail_ref)
+    for a, b in zip(st2, st):
+        assert torch.equal(a, b)
+    if inplace and st_in is not None:
+        assert st2[0].data_ptr() == st_in[0].data_ptr()
