@@ -291,7 +291,9 @@ int cyfa_linear_rows(const CyfaLinearArgs* a, void* hip_stream) {
         return fail(CYFA_ERR_UNSUPPORTED, "cyfa_linear_rows: M=%d N=%d K=%d (needs 1 <= M <= 64, K a multiple of 32)",
                     a->M, a->N, a->K);
     if (!a->x || !a->weight || !a->y) return fail(CYFA_ERR_VALUE, "cyfa_linear_rows: null required pointer");
-    if (a->ldx < a->K || a->ldx % 8 != 0 || a->ldy < a->N)
+    if (a->swiglu && (a->bias || a->N % 32 != 0))
+        return fail(CYFA_ERR_VALUE, "cyfa_linear_rows: swiglu needs N a multiple of 32 and no bias");
+    if (a->ldx < a->K || a->ldx % 8 != 0 || a->ldy < (a->swiglu ? a->N / 2 : a->N))
         return fail(CYFA_ERR_VALUE, "cyfa_linear_rows: ldx=%lld ldy=%lld", a->ldx, a->ldy);
     if (!aligned(a->x, 16) || !aligned(a->weight, 16) || !aligned(a->y, 2) || (a->bias && !aligned(a->bias, 2)))
         return fail(CYFA_ERR_ALIGN, "cyfa_linear_rows: x and weight need 16-byte alignment");
@@ -305,6 +307,7 @@ int cyfa_linear_rows(const CyfaLinearArgs* a, void* hip_stream) {
     p.bias = (const __bf16*)a->bias;
     p.y = (__bf16*)a->y;
     p.ldy = a->ldy;
+    p.swiglu = a->swiglu != 0;
     cyfa::launch_linear_rows(p, (hipStream_t)hip_stream);
     return check_launch("cyfa_linear_rows");
 }

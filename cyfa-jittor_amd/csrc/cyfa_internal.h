@@ -131,8 +131,10 @@ struct LinearParams {
     long long ldx;
     const __bf16* w;     // [N, K] row-major (torch Linear weight)
     const __bf16* bias;  // nullable [N]
-    __bf16* y;           // [M, N], rows ldy elements apart
+    __bf16* y;           // [M, N], rows ldy elements apart ([M, N / 2] with swiglu)
     long long ldy;
+    int swiglu;          // W rows interleaved per 32: 16 gate rows, then the matching 16 up rows;
+                         // y = bf16(g sigmoid(g) u) of the bf16-rounded g and u
 };
 
 int launch_rms_norm(const NormParams& p, hipStream_t stream);

@@ -140,6 +140,20 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
 #pragma unroll
             for (int i = 0; i < 4; i++) part[w][16 * mt + 4 * lg + i][16 * c + lr] = acc[mt][c][i];
     __syncthreads();
+    if (p.swiglu) {  // the SwiGLU product of the slice's 16 gate and 16 up columns
+        for (int idx = threadIdx.x; idx < MT * 16 * 16; idx += 512) {
+            const int m = idx >> 4, f = idx & 15;
+            float sg = 0.f, su = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < 8; ww++) {
+                sg += part[ww][m][f];
+                su += part[ww][m][16 + f];
+            }
+            const float gf = (float)(bf16_t)sg, uf = (float)(bf16_t)su;
+            if (m < p.M && n0 + f < p.N) p.y[(size_t)m * p.ldy + n0 / 2 + f] = (bf16_t)(gf * sigmoidf(gf) * uf);
+        }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < MT; r++) {
         const int idx = threadIdx.x + 512 * r, m = idx >> 5, n = idx & 31;

@@ -90,7 +90,7 @@ class CyfaLinearArgs(ctypes.Structure):
     _fields_ = [
         ("M", _c_int), ("N", _c_int), ("K", _c_int),
         ("x", _c_void_p), ("ldx", ctypes.c_longlong), ("weight", _c_void_p), ("bias", _c_void_p),
-        ("y", _c_void_p), ("ldy", ctypes.c_longlong),
+        ("y", _c_void_p), ("ldy", ctypes.c_longlong), ("swiglu", _c_int),
     ]
 
 
@@ -349,6 +349,35 @@ def linear(x, weight, bias=None, out_cols=None):
     for i in range(len(lead) - 2, -1, -1):
         strides.insert(0, strides[0] * lead[i + 1])
     return y.as_strided(lead + (N,), tuple(strides))
+
+
+def interleave_gate_up(gate_weight, up_weight):
+    """[F, K] gate and up weights -> [2F, K] in groups of 32 rows (16 gate rows,
+    then the matching 16 up rows), the layout linear_swiglu reads."""
+    F_, K = gate_weight.shape
+    if F_ % 16:
+        raise ValueError("interleave_gate_up: the MLP width must be a multiple of 16")
+    return torch.cat([gate_weight.reshape(F_ // 16, 16, K), up_weight.reshape(F_ // 16, 16, K)], 1).reshape(2 * F_, K)
+
+
+def linear_swiglu(x, w_interleaved):
+    """bf16(g sigmoid(g) u) of g = x W_gate^T, u = x W_up^T (each rounded to
+    bf16), for at most 64 rows, in one cyfa_linear_rows launch; w_interleaved
+    comes from interleave_gate_up."""
+    K = w_interleaved.shape[-1]
+    N = w_interleaved.shape[0]
+    rows = x.numel() // K
+    require_device(x, w_interleaved)
+    if rows == 0 or rows > LINEAR_ROWS_MAX or K % 32 or N % 32 or x.shape[-1] != K:
+        raise ValueError(f"linear_swiglu: {rows} rows of {x.shape[-1]} columns against a [{N}, {K}] weight")
+    x2 = x.reshape(rows, K)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    y = torch.empty(rows, N // 2, dtype=torch.bfloat16, device=x.device)
+    args = CyfaLinearArgs(M=rows, N=N, K=K, x=x2.data_ptr(), ldx=x2.stride(0), weight=w_interleaved.data_ptr(),
+                          bias=None, y=y.data_ptr(), ldy=N // 2, swiglu=1)
+    _check(load_library().cyfa_linear_rows(ctypes.byref(args), stream_handle(x.device)), "cyfa_linear_rows")
+    return y.view(*x.shape[:-1], N // 2)
 
 
 def short_conv(x, weight, bias=None, cache=None, split=None, cache_out=None):

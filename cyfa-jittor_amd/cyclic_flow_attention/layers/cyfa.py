@@ -43,10 +43,12 @@ class FusedWeight:
         self.key = None
         self.value = None
 
-    def get(self, *tensors):
+    def get(self, *tensors, build=None):
+        """torch.cat(tensors) along dim 0, or build(*tensors) when given."""
         key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in tensors)
         if key != self.key:
-            self.value = torch.cat([t.detach() for t in tensors], dim=0)
+            parts = [t.detach() for t in tensors]
+            self.value = build(*parts) if build is not None else torch.cat(parts, dim=0)
             self.key = key
         return self.value
 

@@ -27,8 +27,15 @@ class GatedMLP(nn.Module):
         self.up_proj = nn.Linear(config.hidden_size, mid, bias=False)
         self.down_proj = nn.Linear(mid, config.hidden_size, bias=False)
         self._gate_up = FusedWeight()
+        self._gate_up_il = FusedWeight()
 
     def forward(self, x):
+        rows = x.numel() // x.shape[-1]
+        if (inference_fast_path(x) and rows <= _native.LINEAR_ROWS_MAX and self.gate_proj.weight.shape[0] % 16 == 0
+                and x.shape[-1] % 32 == 0):
+            # decode steps: the SwiGLU product in the gate|up projection's epilogue
+            w = self._gate_up_il.get(self.gate_proj.weight, self.up_proj.weight, build=_native.interleave_gate_up)
+            return _native.linear(_native.linear_swiglu(x, w), self.down_proj.weight)
         if inference_fast_path(x) and self.gate_proj.weight.shape[0] % 8 == 0:
             # one [gate | up] GEMM and the fused SwiGLU kernel
             gu = _native.linear(x, self._gate_up.get(self.gate_proj.weight, self.up_proj.weight))

@@ -200,15 +200,20 @@ typedef struct CyfaNormArgs {
 int cyfa_rms_norm(const CyfaNormArgs *args, void *hip_stream);
 
 /* Arguments of one projection y = x W^T (+ bias) over at most 64 rows of x
- * (1 <= M <= 64; K a positive multiple of 32). */
+ * (1 <= M <= 64; K a positive multiple of 32). With swiglu set (no bias, N a
+ * multiple of 32), the rows of W come in groups of 32: 16 rows of the gate
+ * projection, then the matching 16 rows of the up projection, and y [M, N/2]
+ * receives the SwiGLU product bf16(g sigmoid(g) u) of the bf16-rounded g and u
+ * (GatedMLP, models/cyfa/modeling_cyfa.py:22-27). */
 typedef struct CyfaLinearArgs {
     int M, N, K;
     const void *x;                /* bf16 [M, K], rows ldx elements apart (ldx >= K, ldx % 8 == 0) */
     long long ldx;
     const void *weight;           /* bf16 [N, K] row-major (torch Linear weight) */
     const void *bias;             /* nullable bf16 [N] */
-    void *y;                      /* bf16 [M, N], rows ldy elements apart */
+    void *y;                      /* bf16 [M, N] ([M, N/2] with swiglu), rows ldy elements apart */
     long long ldy;
+    int swiglu;
 } CyfaLinearArgs;
 
 /* Replaces the Linear / BiasLinear projections (layers/cyfa.py:15-58) of the

@@ -309,3 +309,22 @@ def test_decode_layer_step_equals_separate_kernels(B, state, inplace):
         assert torch.equal(a, b)
     if inplace and st_in is not None:
         assert st2[0].data_ptr() == st_in[0].data_ptr()
+
+
+@pytest.mark.parametrize("M", [1, 37, 64])
+def test_linear_swiglu_equals_projection_then_silu_mul(M):
+    """The SwiGLU epilogue of cyfa_linear_rows (interleaved gate|up weight)
+    equals the [gate | up] projection followed by silu_mul, bit for bit: every
+    output column is the same fixed-order sum and the same roundings."""
+    from cyclic_flow_attention import _native
+
+    gen = torch.Generator().manual_seed(M)
+    F_, K = 2816, 1024
+    x = torch.randn(M, K, generator=gen).bfloat16().to(DEV)
+    wg = (0.05 * torch.randn(F_, K, generator=gen)).bfloat16().to(DEV)
+    wu = (0.05 * torch.randn(F_, K, generator=gen)).bfloat16().to(DEV)
+    with torch.no_grad():
+        ref = _native.silu_mul(_native.linear(x, torch.cat([wg, wu], 0)))
+        got = _native.linear_swiglu(x, _native.interleave_gate_up(wg, wu))
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
