@@ -22,23 +22,33 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormParams p) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= p.rows) return;
     const size_t base = (size_t)row * p.D;
+    // Every load of the row is issued before the first one is used: x, the
+    // residual, the weight and the gate.
+    bf16x4 xr[J], rr[J], gr[J];
+    float4 wr[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int d = 4 * lane + 256 * j;
+        xr[j] = *reinterpret_cast<const bf16x4*>(p.x + base + d);
+        if (p.residual) rr[j] = *reinterpret_cast<const bf16x4*>(p.residual + base + d);
+        wr[j] = *reinterpret_cast<const float4*>(p.weight + d);
+        if (p.gate) gr[j] = *reinterpret_cast<const bf16x4*>(p.gate + base + d);
+    }
     float v[J][4];
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < J; j++) {
         const int d = 4 * lane + 256 * j;
-        const bf16x4 x = *reinterpret_cast<const bf16x4*>(p.x + base + d);
         if (p.residual) {
-            const bf16x4 r = *reinterpret_cast<const bf16x4*>(p.residual + base + d);
             bf16x4 s;
 #pragma unroll
-            for (int i = 0; i < 4; i++) s[i] = (bf16_t)((float)x[i] + (float)r[i]);
+            for (int i = 0; i < 4; i++) s[i] = (bf16_t)((float)xr[j][i] + (float)rr[j][i]);
             *reinterpret_cast<bf16x4*>(p.sum_out + base + d) = s;
 #pragma unroll
             for (int i = 0; i < 4; i++) v[j][i] = (float)s[i];
         } else {
 #pragma unroll
-            for (int i = 0; i < 4; i++) v[j][i] = (float)x[i];
+            for (int i = 0; i < 4; i++) v[j][i] = (float)xr[j][i];
         }
         if (p.prescale != 1.f) {
 #pragma unroll
@@ -52,12 +62,11 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormParams p) {
 #pragma unroll
     for (int j = 0; j < J; j++) {
         const int d = 4 * lane + 256 * j;
-        const float4 w = *reinterpret_cast<const float4*>(p.weight + d);
+        const float4 w = wr[j];
         float y[4] = {v[j][0] * rs * w.x, v[j][1] * rs * w.y, v[j][2] * rs * w.z, v[j][3] * rs * w.w};
         if (p.gate) {
-            const bf16x4 g = *reinterpret_cast<const bf16x4*>(p.gate + base + d);
 #pragma unroll
-            for (int i = 0; i < 4; i++) y[i] *= sigmoidf((float)g[i]);
+            for (int i = 0; i < 4; i++) y[i] *= sigmoidf((float)gr[j][i]);
         }
         *reinterpret_cast<bf16x4*>(p.out + base + d) = bf16x4{(bf16_t)y[0], (bf16_t)y[1], (bf16_t)y[2], (bf16_t)y[3]};
     }
@@ -205,23 +214,35 @@ __global__ __launch_bounds__(256) void short_conv_kernel(ConvParams p) {
     const int out_i = c8 / p.split, col = c8 % p.split;
     bf16_t* out = p.out[out_i];
     const int t1 = t0 + CONV_RUN < p.T ? t0 + CONV_RUN : p.T;
-    for (int t = t0; t < t1; t++) {
-        const bf16x8 r = row(t);
+    // Eight rows at a time: their loads are all in flight before the first is used.
+    constexpr int U = 8;
+    for (int tb = t0; tb < t1; tb += U) {
+        bf16x8 rows[U];
+        const bf16_t* src = p.x + ((size_t)b * p.T + tb) * p.x_row + c8;  // rows tb.. are never before the start
+        const int n = t1 - tb;
 #pragma unroll
-        for (int i = 0; i < 8; i++) win[W - 1][i] = (float)r[i];
-        bf16x8 y;
+        for (int u = 0; u < U; u++)
+            rows[u] = *reinterpret_cast<const bf16x8*>(src + (size_t)(u < n ? u : 0) * p.x_row);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            float acc = win[0][i] * wt[0][i];
+        for (int u = 0; u < U; u++) {
+            if (tb + u < t1) {
 #pragma unroll
-            for (int w = 1; w < W; w++) acc = fmaf(win[w][i], wt[w][i], acc);
-            y[i] = (bf16_t)(acc + bias[i]);
+                for (int i = 0; i < 8; i++) win[W - 1][i] = (float)rows[u][i];
+                bf16x8 y;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    float acc = win[0][i] * wt[0][i];
+#pragma unroll
+                    for (int w = 1; w < W; w++) acc = fmaf(win[w][i], wt[w][i], acc);
+                    y[i] = (bf16_t)(acc + bias[i]);
+                }
+                *reinterpret_cast<bf16x8*>(out + ((size_t)b * p.T + tb + u) * p.split + col) = y;
+#pragma unroll
+                for (int w = 0; w < W - 1; w++)
+#pragma unroll
+                    for (int i = 0; i < 8; i++) win[w][i] = win[w + 1][i];
+            }
         }
-        *reinterpret_cast<bf16x8*>(out + ((size_t)b * p.T + t) * p.split + col) = y;
-#pragma unroll
-        for (int w = 0; w < W - 1; w++)
-#pragma unroll
-            for (int i = 0; i < 8; i++) win[w][i] = win[w + 1][i];
     }
     if (p.cache_out && t1 == p.T) {
 #pragma unroll
