@@ -14,9 +14,10 @@ Like the reference, which switches to its inference kernels for bf16 CUDA
 tensors without gradients (layers/cyfa.py:66-73, 148-155), bf16 GPU inference
 takes a fused path: one q|k|v projection and one short-convolution launch
 for the three tensors, one a|b|d projection with a fused gate kernel, and the
-gated o_norm inside the prefill's last kernel (a separate HIP kernel after a
-decode step). Decode steps of at most 64 rows form q|k|v, g_proj[0] and a|b|d
-in one projection launch. Other inputs take the general torch path.
+gated o_norm inside the prefill's last kernel. Decode steps of at most 64 rows
+form q|k|v, g_proj[0] and a|b|d in one projection launch, and a one-token step
+runs the convolution, the gates, the op and the gated o_norm as one HIP kernel.
+Other inputs take the general torch path.
 """
 
 import math
