@@ -62,7 +62,28 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     float4* hk_out = reinterpret_cast<float4*>(p.hk_out + (size_t)bh * K * kSlots);
     float4* hv_out = reinterpret_cast<float4*>(p.hv_out + (size_t)bh * kSlots * V);
 
-    // Issue both state streams first; everything below overlaps with them.
+    // Layer step: the short-convolution inputs of this thread's channels (the
+    // q and k channel tid, the v channel tid) are loaded ahead of the state
+    // streams, so they arrive first. win[c][0..2] = cache rows, win[c][3] = x.
+    float cwin[3][4], cwt[3][4];
+    if (LAYER) {
+        const int b = bh / p.H, HK = p.H * K;
+        const int ch[3] = {h * K + tid, HK + h * K + tid, 2 * HK + h * V + tid};
+#pragma unroll
+        for (int c = 0; c < 3; c++) {
+            if (tid < (c < 2 ? K : V)) {
+#pragma unroll
+                for (int w = 0; w < 3; w++)
+                    cwin[c][w] = p.cache_in ? (float)p.cache_in[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch[c]]
+                                            : 0.f;
+                cwin[c][3] = (float)p.qkv[(size_t)b * p.qkv_row + ch[c]];
+#pragma unroll
+                for (int w = 0; w < 4; w++) cwt[c][w] = (float)p.conv_w[(size_t)ch[c] * 4 + w];
+            }
+        }
+    }
+
+    // Issue both state streams; everything below overlaps with them.
     float4 hk_r[KJ], hv_r[VJ];
     if (has_state) {
 #pragma unroll
@@ -82,25 +103,21 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     if (LAYER) {
         const int b = bh / p.H;
         const int HK = p.H * K;
-        auto conv = [&](int ch) -> float {
-            float win[4];
+        // The arithmetic of short_conv_kernel; the new cache is the last three rows of the window.
+        auto conv = [&](int c, int ch) -> float {
+            float acc = cwin[c][0] * cwt[c][0];
+#pragma unroll
+            for (int w = 1; w < 4; w++) acc = fmaf(cwin[c][w], cwt[c][w], acc);
 #pragma unroll
             for (int w = 0; w < 3; w++)
-                win[w] = p.cache_in ? (float)p.cache_in[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch] : 0.f;
-            win[3] = (float)p.qkv[(size_t)b * p.qkv_row + ch];
-            float acc = win[0] * (float)p.conv_w[(size_t)ch * 4];
-#pragma unroll
-            for (int w = 1; w < 4; w++) acc = fmaf(win[w], (float)p.conv_w[(size_t)ch * 4 + w], acc);
-#pragma unroll
-            for (int w = 0; w < 3; w++)
-                p.cache_out[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch] = (bf16_t)win[w + 1];
+                p.cache_out[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch] = (bf16_t)cwin[c][w + 1];
             return bf16_round(acc);
         };
         if (tid < K) {
-            qv = conv(h * K + tid);
-            kv = conv(HK + h * K + tid);
+            qv = conv(0, h * K + tid);
+            kv = conv(1, HK + h * K + tid);
         }
-        if (tid < V) s_v[tid] = conv(2 * HK + h * V + tid);
+        if (tid < V) s_v[tid] = conv(2, 2 * HK + h * V + tid);
         const bf16_t* row = p.abd + (size_t)b * p.abd_row;
         const float a = (float)row[h] + p.dt_bias[h];
         const float sp = a > 20.f ? a : log1pf(expf(a));
