@@ -308,7 +308,8 @@ int cyfa_linear_rows(const CyfaLinearArgs* a, void* hip_stream) {
     p.y = (__bf16*)a->y;
     p.ldy = a->ldy;
     p.swiglu = a->swiglu != 0;
-    cyfa::launch_linear_rows(p, (hipStream_t)hip_stream);
+    if (cyfa::launch_linear_rows(p, (hipStream_t)hip_stream) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_linear_rows: M=%d outside 1..64", a->M);
     return check_launch("cyfa_linear_rows");
 }
 

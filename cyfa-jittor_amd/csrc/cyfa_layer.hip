@@ -74,14 +74,16 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormParams p) {
 
 // y[m][n] = bias[n] + sum_k x[m][k] W[n][k] for M <= 64 rows (the nn.Linear /
 // F.linear calls of the one-token decode step, layers/cyfa.py and
-// modeling_cyfa.py). At these shapes the weight read is the whole cost: a
-// library GEMM tiles M into large blocks and leaves most of the chip idle,
-// while here every workgroup streams a 32-column slice of W once, with all
-// of its loads in flight. Workgroup = 8 waves over one 32-column slice; wave w
-// takes the 32-deep k-steps w, w + 8, ... of all MT row tiles of 16, on
+// modeling_cyfa.py). At these shapes a library GEMM tiles M into large blocks
+// and leaves most of the chip idle. Here a workgroup of 8 waves computes one
+// tile of RT x 16 rows by CT x 16 columns over the whole of K, on
 // v_mfma_f32_16x16x32_bf16 (A = x rows, B = W rows read straight from global
-// memory: lane (lr, lg) loads 8 consecutive k of row lr). The eight partial
-// tiles are summed in LDS in wave order, so results do not depend on timing.
+// memory: lane (lr, lg) loads 8 consecutive k of row lr). Wave w takes a
+// contiguous run of the 32-deep k-steps, so its loads of a row cover whole
+// cache lines, with the loads of several steps in flight; the eight partial
+// tiles are summed in LDS in wave order. Every output element is therefore
+// summed in the same order whatever the tile shape, so the launcher may pick
+// the shape per call (launch_linear_rows) without changing a bit of y.
 // Rows of x at or past M and rows of W at or past N read as zero (buffer
 // bounds).
 typedef __amdgpu_buffer_rsrc_t lin_rsrc_t;
@@ -95,62 +97,66 @@ __device__ __forceinline__ bf16x8 lin_ld(lin_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
-template <int MT>
+template <int RT, int CT>
 __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
-    __shared__ float part[8][MT * 16][33];
+    constexpr int TM = 16 * RT, TN = 16 * CT, OUT = TM * TN, R = (OUT + 511) / 512;
+    // k-steps whose loads are in flight together: about 24 loads per lane
+    constexpr int U = RT + CT <= 3 ? 8 : RT + CT <= 4 ? 6 : 4;
+    __shared__ float part[8][TM][TN + 1];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lr = lane & 15, lg = lane >> 4;
-    const int n0 = blockIdx.x * 32;
-    const lin_rsrc_t rx = lin_rsrc(p.x, ((size_t)(p.M - 1) * p.ldx + p.K) * 2);
-    const lin_rsrc_t rw = lin_rsrc(p.w + (size_t)n0 * p.K, (size_t)min(32, p.N - n0) * p.K * 2);
+    const int n0 = blockIdx.x * TN, m0 = blockIdx.y * TM;
+    const int mrows = min(TM, p.M - m0);
+    const lin_rsrc_t rx = lin_rsrc(p.x + (size_t)m0 * p.ldx, ((size_t)(mrows - 1) * p.ldx + p.K) * 2);
+    const lin_rsrc_t rw = lin_rsrc(p.w + (size_t)n0 * p.K, (size_t)min(TN, p.N - n0) * p.K * 2);
     // the bias of this thread's outputs, loaded with the operands
-    float bias[MT];
+    float bias[R];
 #pragma unroll
-    for (int r = 0; r < MT; r++) {
-        const int n = n0 + ((threadIdx.x + 512 * r) & 31);
+    for (int r = 0; r < R; r++) {
+        const int n = n0 + ((threadIdx.x + 512 * r) % TN);
         bias[r] = p.bias && n < p.N ? (float)p.bias[n] : 0.f;
     }
-    f32x4 acc[MT][2];
+    f32x4 acc[RT][CT];
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // Wave w takes a contiguous run of 32-deep k-steps, so that its loads of a
-    // row cover whole cache lines; up to four k-steps' loads are in flight at once.
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int c = 0; c < CT; c++) acc[rt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int steps = p.K / 32, per = (steps + 7) / 8;
     const int s0 = min(steps, w * per), s1 = min(steps, s0 + per);
     const uint32_t wrow = (uint32_t)lr * p.K * 2, xrow = (uint32_t)lr * (uint32_t)p.ldx * 2;
-    const uint32_t xstride = (uint32_t)(16 * p.ldx * 2);
-    for (int s = s0; s < s1; s += 4) {
-        bf16x8 wf[4][2], xf[4][MT];
+    const uint32_t xstride = (uint32_t)(16 * p.ldx * 2), wstride = (uint32_t)(16 * p.K * 2);
+    for (int s = s0; s < s1; s += U) {
+        bf16x8 wf[U][CT], xf[U][RT];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < U; u++) {
             if (s + u < s1) {
                 const uint32_t kb = (uint32_t)(32 * (s + u) + 8 * lg) * 2;
 #pragma unroll
-                for (int c = 0; c < 2; c++) wf[u][c] = lin_ld(rw, wrow + (uint32_t)(16 * c) * p.K * 2 + kb);
+                for (int c = 0; c < CT; c++) wf[u][c] = lin_ld(rw, wrow + c * wstride + kb);
 #pragma unroll
-                for (int mt = 0; mt < MT; mt++) xf[u][mt] = lin_ld(rx, xrow + mt * xstride + kb);
+                for (int rt = 0; rt < RT; rt++) xf[u][rt] = lin_ld(rx, xrow + rt * xstride + kb);
             }
         }
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < U; u++) {
             if (s + u < s1) {
 #pragma unroll
-                for (int mt = 0; mt < MT; mt++)
+                for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-                    for (int c = 0; c < 2; c++)
-                        acc[mt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[u][mt], wf[u][c], acc[mt][c], 0, 0, 0);
+                    for (int c = 0; c < CT; c++)
+                        acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[u][rt], wf[u][c], acc[rt][c], 0, 0, 0);
             }
         }
     }
-    // acc[mt][c][i] = partial y[16 mt + 4 lg + i][n0 + 16 c + lr]
+    // acc[rt][c][i] = partial y[m0 + 16 rt + 4 lg + i][n0 + 16 c + lr]
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++)
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-        for (int c = 0; c < 2; c++)
+        for (int c = 0; c < CT; c++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) part[w][16 * mt + 4 * lg + i][16 * c + lr] = acc[mt][c][i];
+            for (int i = 0; i < 4; i++) part[w][16 * rt + 4 * lg + i][16 * c + lr] = acc[rt][c][i];
     __syncthreads();
-    if (p.swiglu) {  // the SwiGLU product of the slice's 16 gate and 16 up columns
-        for (int idx = threadIdx.x; idx < MT * 16 * 16; idx += 512) {
+    if (CT == 2 && p.swiglu) {  // the SwiGLU product of the tile's 16 gate and 16 up columns
+        for (int idx = threadIdx.x; idx < TM * 16; idx += 512) {
             const int m = idx >> 4, f = idx & 15;
             float sg = 0.f, su = 0.f;
 #pragma unroll
@@ -159,17 +165,20 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
                 su += part[ww][m][16 + f];
             }
             const float gf = (float)(bf16_t)sg, uf = (float)(bf16_t)su;
-            if (m < p.M && n0 + f < p.N) p.y[(size_t)m * p.ldy + n0 / 2 + f] = (bf16_t)(gf * sigmoidf(gf) * uf);
+            if (m < mrows && n0 + f < p.N)
+                p.y[(size_t)(m0 + m) * p.ldy + n0 / 2 + f] = (bf16_t)(gf * sigmoidf(gf) * uf);
         }
         return;
     }
 #pragma unroll
-    for (int r = 0; r < MT; r++) {
-        const int idx = threadIdx.x + 512 * r, m = idx >> 5, n = idx & 31;
-        float s = 0.f;
+    for (int r = 0; r < R; r++) {
+        const int idx = threadIdx.x + 512 * r, m = idx / TN, n = idx % TN;
+        if (idx < OUT) {
+            float s = 0.f;
 #pragma unroll
-        for (int ww = 0; ww < 8; ww++) s += part[ww][m][n];
-        if (m < p.M && n0 + n < p.N) p.y[(size_t)m * p.ldy + n0 + n] = (bf16_t)(s + bias[r]);
+            for (int ww = 0; ww < 8; ww++) s += part[ww][m][n];
+            if (m < mrows && n0 + n < p.N) p.y[(size_t)(m0 + m) * p.ldy + n0 + n] = (bf16_t)(s + bias[r]);
+        }
     }
 }
 
@@ -303,16 +312,49 @@ int launch_rms_norm(const NormParams& p, hipStream_t stream) {
     return 0;
 }
 
-int launch_linear_rows(const LinearParams& p, hipStream_t stream) {
-    const dim3 grid((p.N + 31) / 32), block(512);
-    switch ((p.M + 15) / 16) {
-        case 1: hipLaunchKernelGGL(linear_rows_kernel<1>, grid, block, 0, stream, p); break;
-        case 2: hipLaunchKernelGGL(linear_rows_kernel<2>, grid, block, 0, stream, p); break;
-        case 3: hipLaunchKernelGGL(linear_rows_kernel<3>, grid, block, 0, stream, p); break;
-        case 4: hipLaunchKernelGGL(linear_rows_kernel<4>, grid, block, 0, stream, p); break;
-        default: return -1;
+// The tile shape of linear_rows_kernel for one call. Each workgroup reads
+// 16 (RT + CT) rows of K (RT x 16 rows of x and CT x 16 rows of W), and at
+// these sizes a CU's read rate, not the chip's, is the limit; one workgroup
+// fits a CU at a time, so the workgroups past the first 256 run in further
+// rounds. Pick the shape with the least bytes read per CU over all rounds
+// (on MI355X: 28 -> 35 k tok/s for the 400M decode step at B=64 against a
+// fixed 4 x 2 tile). The SwiGLU epilogue needs CT = 2, the 16 gate and 16 up
+// columns of one interleaved group.
+static void linear_tile(int M, int N, bool swiglu, int& rt_out, int& ct_out) {
+    static const int shapes[][2] = {{4, 2}, {2, 4}, {4, 1}, {2, 2}, {1, 4}, {2, 1}, {1, 2}, {1, 1}};
+    long long best = -1;
+    rt_out = 4;
+    ct_out = 2;
+    for (const auto& sh : shapes) {
+        const int rt = sh[0], ct = sh[1];
+        if (swiglu && ct != 2) continue;
+        const long long groups = (long long)((M + 16 * rt - 1) / (16 * rt)) * ((N + 16 * ct - 1) / (16 * ct));
+        const long long cost = (groups + 255) / 256 * (rt + ct);
+        if (best < 0 || cost < best) {
+            best = cost;
+            rt_out = rt;
+            ct_out = ct;
+        }
     }
-    return 0;
+}
+
+int launch_linear_rows(const LinearParams& p, hipStream_t stream) {
+    if (p.M < 1 || p.M > 64) return -1;
+    int rt, ct;
+    linear_tile(p.M, p.N, p.swiglu != 0, rt, ct);
+    const dim3 grid((p.N + 16 * ct - 1) / (16 * ct), (p.M + 16 * rt - 1) / (16 * rt)), block(512);
+#define CYFA_LINEAR(RT_, CT_) \
+    if (rt == RT_ && ct == CT_) { hipLaunchKernelGGL((linear_rows_kernel<RT_, CT_>), grid, block, 0, stream, p); return 0; }
+    CYFA_LINEAR(4, 2)
+    CYFA_LINEAR(2, 4)
+    CYFA_LINEAR(4, 1)
+    CYFA_LINEAR(2, 2)
+    CYFA_LINEAR(1, 4)
+    CYFA_LINEAR(2, 1)
+    CYFA_LINEAR(1, 2)
+    CYFA_LINEAR(1, 1)
+#undef CYFA_LINEAR
+    return -1;
 }
 
 int launch_short_conv(const ConvParams& p, hipStream_t stream) {

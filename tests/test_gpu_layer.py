@@ -236,7 +236,8 @@ def test_graphed_decode_matches_eager(name, layers, B):
 @pytest.mark.parametrize("M,N,K,bias,ldx", [(1, 3072, 1024, False, 1024), (64, 12, 1024, True, 1024),
                                             (17, 256, 1024, False, 1024), (64, 1024, 256, True, 256),
                                             (33, 1024, 2816, False, 2816), (64, 32000, 1024, False, 1024),
-                                            (5, 100, 64, True, 3 * 64)])
+                                            (5, 100, 64, True, 3 * 64), (64, 3340, 1024, True, 1024),
+                                            (64, 1024, 2816, False, 2816), (40, 5000, 512, True, 512)])
 def test_linear_rows_kernel(M, N, K, bias, ldx):
     """cyfa_linear_rows against x W^T + b in float64: one bf16 rounding of an
     fp32 sum (bound: half a bf16 ulp of the result plus the fp32 summation
@@ -257,6 +258,24 @@ def test_linear_rows_kernel(M, N, K, bias, ldx):
     err = (y.cpu().double() - ref).abs()
     assert (err <= bound).all(), f"max err {err.max().item()} vs bound {bound[err.argmax() // N, err.argmax() % N].item()}"
 
+
+@pytest.mark.parametrize("N,K", [(32000, 1024), (3340, 1024), (5000, 512)])
+def test_linear_rows_tile_shape_does_not_change_bits(N, K):
+    """The launcher picks the workgroup tile per call (64 rows and 1 row get
+    different tiles at these N); every output is the same fixed-order sum in
+    any tile, so a row's result does not depend on the other rows."""
+    from cyclic_flow_attention import _native
+
+    gen = torch.Generator().manual_seed(N + K)
+    x = torch.randn(64, K, generator=gen).bfloat16().to(DEV)
+    w = (0.05 * torch.randn(N, K, generator=gen)).bfloat16().to(DEV)
+    b = torch.randn(N, generator=gen).bfloat16().to(DEV)
+    with torch.no_grad():
+        full = _native.linear(x, w, b)
+        rows = [_native.linear(x[m:m + 1], w, b) for m in (0, 17, 63)]
+    torch.cuda.synchronize()
+    for m, y in zip((0, 17, 63), rows):
+        assert torch.equal(y[0], full[m]), f"row {m}"
 
 
 @pytest.mark.parametrize("B,state,inplace", [(3, True, False), (2, False, False), (4, True, True)])
