@@ -285,19 +285,21 @@ int cyfa_scalar_la(const CyfaSlaArgs* a, void* hip_stream) {
     return check_launch("cyfa_scalar_la");
 }
 
-int cyfa_linear_rows(const CyfaLinearArgs* a, void* hip_stream) {
-    if (!a) return fail(CYFA_ERR_VALUE, "cyfa_linear_rows: null args");
+static int linear_params(const CyfaLinearArgs* a, const char* name, cyfa::LinearParams& p) {
+    if (!a) return fail(CYFA_ERR_VALUE, "%s: null args", name);
     if (a->M < 1 || a->M > 64 || a->N < 1 || a->K < 32 || a->K % 32 != 0)
-        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_linear_rows: M=%d N=%d K=%d (needs 1 <= M <= 64, K a multiple of 32)",
-                    a->M, a->N, a->K);
-    if (!a->x || !a->weight || !a->y) return fail(CYFA_ERR_VALUE, "cyfa_linear_rows: null required pointer");
+        return fail(CYFA_ERR_UNSUPPORTED, "%s: M=%d N=%d K=%d (needs 1 <= M <= 64, K a multiple of 32)", name, a->M,
+                    a->N, a->K);
+    if (!a->x || !a->weight || !a->y) return fail(CYFA_ERR_VALUE, "%s: null required pointer", name);
     if (a->swiglu && (a->bias || a->N % 32 != 0))
-        return fail(CYFA_ERR_VALUE, "cyfa_linear_rows: swiglu needs N a multiple of 32 and no bias");
+        return fail(CYFA_ERR_VALUE, "%s: swiglu needs N a multiple of 32 and no bias", name);
     if (a->ldx < a->K || a->ldx % 8 != 0 || a->ldy < (a->swiglu ? a->N / 2 : a->N))
-        return fail(CYFA_ERR_VALUE, "cyfa_linear_rows: ldx=%lld ldy=%lld", a->ldx, a->ldy);
+        return fail(CYFA_ERR_VALUE, "%s: ldx=%lld ldy=%lld", name, a->ldx, a->ldy);
     if (!aligned(a->x, 16) || !aligned(a->weight, 16) || !aligned(a->y, 2) || (a->bias && !aligned(a->bias, 2)))
-        return fail(CYFA_ERR_ALIGN, "cyfa_linear_rows: x and weight need 16-byte alignment");
-    cyfa::LinearParams p;
+        return fail(CYFA_ERR_ALIGN, "%s: x and weight need 16-byte alignment", name);
+    if (a->residual && (a->swiglu || a->ldr < a->N || !aligned(a->residual, 2)))
+        return fail(CYFA_ERR_VALUE, "%s: residual needs no swiglu and ldr >= N (ldr=%lld)", name, a->ldr);
+    p = cyfa::LinearParams{};
     p.M = a->M;
     p.N = a->N;
     p.K = a->K;
@@ -308,9 +310,41 @@ int cyfa_linear_rows(const CyfaLinearArgs* a, void* hip_stream) {
     p.y = (__bf16*)a->y;
     p.ldy = a->ldy;
     p.swiglu = a->swiglu != 0;
+    p.add = (const __bf16*)a->residual;
+    p.ld_add = a->ldr;
+    return CYFA_OK;
+}
+
+int cyfa_linear_rows(const CyfaLinearArgs* a, void* hip_stream) {
+    cyfa::LinearParams p;
+    if (int rc = linear_params(a, "cyfa_linear_rows", p)) return rc;
     if (cyfa::launch_linear_rows(p, (hipStream_t)hip_stream) != 0)
-        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_linear_rows: M=%d outside 1..64", a->M);
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_linear_rows: no tile for M=%d N=%d K=%d", a->M, a->N, a->K);
     return check_launch("cyfa_linear_rows");
+}
+
+int cyfa_norm_linear_rows(const CyfaLinearArgs* a, const CyfaRowNormArgs* n, void* hip_stream) {
+    cyfa::LinearParams p;
+    if (int rc = linear_params(a, "cyfa_norm_linear_rows", p)) return rc;
+    if (!n || !n->weight) return fail(CYFA_ERR_VALUE, "cyfa_norm_linear_rows: null norm args or weight");
+    if (a->K > cyfa::LINEAR_NORM_MAX_K)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_norm_linear_rows: K=%d above %d", a->K, cyfa::LINEAR_NORM_MAX_K);
+    if (!aligned(n->weight, 16)) return fail(CYFA_ERR_ALIGN, "cyfa_norm_linear_rows: norm weight needs 16-byte alignment");
+    if (n->residual) {
+        if (!n->sum_out) return fail(CYFA_ERR_VALUE, "cyfa_norm_linear_rows: residual without sum_out");
+        if (n->ldr < a->K || n->ldr % 8 != 0)
+            return fail(CYFA_ERR_VALUE, "cyfa_norm_linear_rows: ldr=%lld", n->ldr);
+        if (!aligned(n->residual, 16) || !aligned(n->sum_out, 16))
+            return fail(CYFA_ERR_ALIGN, "cyfa_norm_linear_rows: residual and sum_out need 16-byte alignment");
+    }
+    p.norm_weight = n->weight;
+    p.norm_eps = n->eps;
+    p.norm_residual = (const __bf16*)n->residual;
+    p.norm_sum_out = n->residual ? (__bf16*)n->sum_out : nullptr;
+    p.ldr = n->ldr;
+    if (cyfa::launch_linear_rows(p, (hipStream_t)hip_stream) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_norm_linear_rows: no tile for M=%d N=%d K=%d", a->M, a->N, a->K);
+    return check_launch("cyfa_norm_linear_rows");
 }
 
 int cyfa_rms_norm(const CyfaNormArgs* a, void* hip_stream) {

@@ -135,7 +135,19 @@ struct LinearParams {
     long long ldy;
     int swiglu;          // W rows interleaved per 32: 16 gate rows, then the matching 16 up rows;
                          // y = bf16(g sigmoid(g) u) of the bf16-rounded g and u
+    const __bf16* add;   // nullable [M, N], rows ld_add apart: y = bf16(add + bf16(x W^T + bias)); no swiglu
+    long long ld_add;
+    // Optional RMS norm of the x rows before the product (over all K columns):
+    //   s = norm_residual ? bf16(x + residual) : x   (norm_sum_out receives s)
+    //   the product reads bf16(s * rsqrt(mean(s^2) + norm_eps) * norm_weight)
+    const float* norm_weight;     // nullable: x is used as given
+    const __bf16* norm_residual;  // nullable [M, K], rows ldr elements apart
+    __bf16* norm_sum_out;         // [M, K], rows ldr apart; set with norm_residual; aliases no input
+    long long ldr;
+    float norm_eps;
 };
+
+constexpr int LINEAR_NORM_MAX_K = 2048;
 
 int launch_rms_norm(const NormParams& p, hipStream_t stream);
 int launch_linear_rows(const LinearParams& p, hipStream_t stream);

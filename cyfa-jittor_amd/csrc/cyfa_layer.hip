@@ -97,23 +97,74 @@ __device__ __forceinline__ bf16x8 lin_ld(lin_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
-template <int RT, int CT>
+// k-steps whose loads a wave has in flight together: about 24 loads per lane
+__host__ __device__ constexpr int lin_batch(int rt, int ct) { return rt + ct <= 3 ? 8 : rt + ct <= 4 ? 6 : 4; }
+
+template <int U, int RT, int CT>
+__device__ __forceinline__ void lin_issue_w(lin_rsrc_t rw, int s, int s1, uint32_t wrow, uint32_t wstride, int lg,
+                                           bf16x8 (&wf)[U][CT]) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        if (s + u < s1) {
+            const uint32_t kb = (uint32_t)(32 * (s + u) + 8 * lg) * 2;
+#pragma unroll
+            for (int c = 0; c < CT; c++) wf[u][c] = lin_ld(rw, wrow + c * wstride + kb);
+        }
+    }
+}
+
+template <int U, int RT>
+__device__ __forceinline__ void lin_issue_x(lin_rsrc_t rx, int s, int s1, uint32_t xrow, uint32_t xstride, int lg,
+                                            bf16x8 (&xf)[U][RT]) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        if (s + u < s1) {
+            const uint32_t kb = (uint32_t)(32 * (s + u) + 8 * lg) * 2;
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) xf[u][rt] = lin_ld(rx, xrow + rt * xstride + kb);
+        }
+    }
+}
+
+template <int U, int RT, int CT>
+__device__ __forceinline__ void lin_mfma(int s, int s1, const bf16x8 (&wf)[U][CT], const bf16x8 (&xf)[U][RT],
+                                         f32x4 (&acc)[RT][CT]) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        if (s + u < s1) {
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int c = 0; c < CT; c++)
+                    acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[u][rt], wf[u][c], acc[rt][c], 0, 0, 0);
+        }
+    }
+}
+
+template <int RT, int CT, bool NORM>
 __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
     constexpr int TM = 16 * RT, TN = 16 * CT, OUT = TM * TN, R = (OUT + 511) / 512;
-    // k-steps whose loads are in flight together: about 24 loads per lane
-    constexpr int U = RT + CT <= 3 ? 8 : RT + CT <= 4 ? 6 : 4;
+    constexpr int U = lin_batch(RT, CT);
     __shared__ float part[8][TM][TN + 1];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lr = lane & 15, lg = lane >> 4;
+    __shared__ float sq[NORM ? 8 : 1][NORM ? TM : 1];
+    __shared__ float4 snw[NORM ? LINEAR_NORM_MAX_K / 4 : 1];
+    // The wave index comes from a scalar register, so the k-run bounds and
+    // every `s + u < s1` test are uniform branches. Under a lane-divergent
+    // test the compiler may leave an MFMA to run with an empty exec mask,
+    // which on gfx950 still accumulated the stale operand registers.
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lr = lane & 15,
+              lg = lane >> 4;
     const int n0 = blockIdx.x * TN, m0 = blockIdx.y * TM;
     const int mrows = min(TM, p.M - m0);
     const lin_rsrc_t rx = lin_rsrc(p.x + (size_t)m0 * p.ldx, ((size_t)(mrows - 1) * p.ldx + p.K) * 2);
     const lin_rsrc_t rw = lin_rsrc(p.w + (size_t)n0 * p.K, (size_t)min(TN, p.N - n0) * p.K * 2);
-    // the bias of this thread's outputs, loaded with the operands
-    float bias[R];
+    // the bias and the residual of this thread's outputs, loaded with the operands
+    float bias[R], add[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        const int n = n0 + ((threadIdx.x + 512 * r) % TN);
+        const int idx = threadIdx.x + 512 * r, n = n0 + idx % TN, m = idx / TN;
         bias[r] = p.bias && n < p.N ? (float)p.bias[n] : 0.f;
+        add[r] = p.add && n < p.N && idx < OUT && m < mrows ? (float)p.add[(size_t)(m0 + m) * p.ld_add + n] : 0.f;
     }
     f32x4 acc[RT][CT];
 #pragma unroll
@@ -124,28 +175,77 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
     const int s0 = min(steps, w * per), s1 = min(steps, s0 + per);
     const uint32_t wrow = (uint32_t)lr * p.K * 2, xrow = (uint32_t)lr * (uint32_t)p.ldx * 2;
     const uint32_t xstride = (uint32_t)(16 * p.ldx * 2), wstride = (uint32_t)(16 * p.K * 2);
-    for (int s = s0; s < s1; s += U) {
-        bf16x8 wf[U][CT], xf[U][RT];
+    bf16x8 wf[U][CT], xf[U][RT];
+    if constexpr (!NORM) {
+        for (int s = s0; s < s1; s += U) {
+            lin_issue_w<U, RT, CT>(rw, s, s1, wrow, wstride, lg, wf);
+            lin_issue_x<U, RT>(rx, s, s1, xrow, xstride, lg, xf);
+            lin_mfma<U, RT, CT>(s, s1, wf, xf, acc);
+        }
+    } else {
+        // The row norm (the launcher guarantees one batch: K <= 256 U). Lane
+        // (lr, lg) holds 8 columns of row 16 rt + lr per k-step, the same
+        // columns in every tile shape. Its sum of squares runs over its
+        // k-steps in order, then over the row's four lanes (xor 16, xor 32)
+        // and the eight waves in wave order.
+        const bool res = p.norm_residual != nullptr;
+        lin_issue_w<U, RT, CT>(rw, s0, s1, wrow, wstride, lg, wf);
+        lin_issue_x<U, RT>(rx, s0, s1, xrow, xstride, lg, xf);
+        if (res) {
+            const lin_rsrc_t rr =
+                lin_rsrc(p.norm_residual + (size_t)m0 * p.ldr, ((size_t)(mrows - 1) * p.ldr + p.K) * 2);
+            bf16x8 rf[U][RT];
+            lin_issue_x<U, RT>(rr, s0, s1, (uint32_t)lr * (uint32_t)p.ldr * 2, (uint32_t)(16 * p.ldr * 2), lg, rf);
+            // s = bf16(x + residual); the first column of workgroups writes it out
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            if (s + u < s1) {
-                const uint32_t kb = (uint32_t)(32 * (s + u) + 8 * lg) * 2;
+            for (int u = 0; u < U; u++) {
+                if (s0 + u < s1) {
 #pragma unroll
-                for (int c = 0; c < CT; c++) wf[u][c] = lin_ld(rw, wrow + c * wstride + kb);
+                    for (int rt = 0; rt < RT; rt++) {
 #pragma unroll
-                for (int rt = 0; rt < RT; rt++) xf[u][rt] = lin_ld(rx, xrow + rt * xstride + kb);
+                        for (int e = 0; e < 8; e++) xf[u][rt][e] = (bf16_t)((float)xf[u][rt][e] + (float)rf[u][rt][e]);
+                        if (blockIdx.x == 0 && 16 * rt + lr < mrows)
+                            *reinterpret_cast<bf16x8*>(p.norm_sum_out + (size_t)(m0 + 16 * rt + lr) * p.ldr +
+                                                       32 * (s0 + u) + 8 * lg) = xf[u][rt];
+                    }
+                }
             }
         }
+        for (int i = threadIdx.x; 4 * i < p.K; i += 512) snw[i] = reinterpret_cast<const float4*>(p.norm_weight)[i];
+        float ss[RT];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            if (s + u < s1) {
+        for (int rt = 0; rt < RT; rt++) {
+            ss[rt] = 0.f;
 #pragma unroll
-                for (int rt = 0; rt < RT; rt++)
+            for (int u = 0; u < U; u++) {
+                if (s0 + u < s1) {
 #pragma unroll
-                    for (int c = 0; c < CT; c++)
-                        acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[u][rt], wf[u][c], acc[rt][c], 0, 0, 0);
+                    for (int e = 0; e < 8; e++) ss[rt] = fmaf((float)xf[u][rt][e], (float)xf[u][rt][e], ss[rt]);
+                }
+            }
+            ss[rt] += __shfl_xor(ss[rt], 16);
+            ss[rt] += __shfl_xor(ss[rt], 32);
+            if (lg == 0) sq[w][16 * rt + lr] = ss[rt];
+        }
+        __syncthreads();
+        // bf16(s * rs * weight), as rms_norm_kernel rounds it
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            float t = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < 8; ww++) t += sq[ww][16 * rt + lr];
+            const float rs = rsqrtf(t / (float)p.K + p.norm_eps);
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                if (s0 + u < s1) {
+                    const float4 a = snw[(32 * (s0 + u) + 8 * lg) / 4], b = snw[(32 * (s0 + u) + 8 * lg) / 4 + 1];
+                    const float wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                    for (int e = 0; e < 8; e++) xf[u][rt][e] = (bf16_t)((float)xf[u][rt][e] * rs * wv[e]);
+                }
             }
         }
+        lin_mfma<U, RT, CT>(s0, s1, wf, xf, acc);
     }
     // acc[rt][c][i] = partial y[m0 + 16 rt + 4 lg + i][n0 + 16 c + lr]
 #pragma unroll
@@ -177,7 +277,9 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
             float s = 0.f;
 #pragma unroll
             for (int ww = 0; ww < 8; ww++) s += part[ww][m][n];
-            if (m < mrows && n0 + n < p.N) p.y[(size_t)(m0 + m) * p.ldy + n0 + n] = (bf16_t)(s + bias[r]);
+            float v = s + bias[r];
+            if (p.add) v = (float)(bf16_t)v + add[r];  // the block's residual add, x + bf16(y)
+            if (m < mrows && n0 + n < p.N) p.y[(size_t)(m0 + m) * p.ldy + n0 + n] = (bf16_t)v;
         }
     }
 }
@@ -319,8 +421,9 @@ int launch_rms_norm(const NormParams& p, hipStream_t stream) {
 // rounds. Pick the shape with the least bytes read per CU over all rounds
 // (on MI355X: 28 -> 35 k tok/s for the 400M decode step at B=64 against a
 // fixed 4 x 2 tile). The SwiGLU epilogue needs CT = 2, the 16 gate and 16 up
-// columns of one interleaved group.
-static void linear_tile(int M, int N, bool swiglu, int& rt_out, int& ct_out) {
+// columns of one interleaved group; the row norm needs each wave's k-steps in
+// one batch of loads (K <= 256 lin_batch). False when no shape qualifies.
+static bool linear_tile(int M, int N, bool swiglu, int norm_k, int& rt_out, int& ct_out) {
     static const int shapes[][2] = {{4, 2}, {2, 4}, {4, 1}, {2, 2}, {1, 4}, {2, 1}, {1, 2}, {1, 1}};
     long long best = -1;
     rt_out = 4;
@@ -328,6 +431,7 @@ static void linear_tile(int M, int N, bool swiglu, int& rt_out, int& ct_out) {
     for (const auto& sh : shapes) {
         const int rt = sh[0], ct = sh[1];
         if (swiglu && ct != 2) continue;
+        if (norm_k > 256 * lin_batch(rt, ct)) continue;  // the norm needs all of a row in one batch
         const long long groups = (long long)((M + 16 * rt - 1) / (16 * rt)) * ((N + 16 * ct - 1) / (16 * ct));
         const long long cost = (groups + 255) / 256 * (rt + ct);
         if (best < 0 || cost < best) {
@@ -336,15 +440,23 @@ static void linear_tile(int M, int N, bool swiglu, int& rt_out, int& ct_out) {
             ct_out = ct;
         }
     }
+    return best >= 0;
 }
 
 int launch_linear_rows(const LinearParams& p, hipStream_t stream) {
-    if (p.M < 1 || p.M > 64) return -1;
+    if (p.M < 1 || p.M > 64 || (p.norm_weight && p.K > LINEAR_NORM_MAX_K)) return -1;
     int rt, ct;
-    linear_tile(p.M, p.N, p.swiglu != 0, rt, ct);
+    if (!linear_tile(p.M, p.N, p.swiglu != 0, p.norm_weight ? p.K : 0, rt, ct)) return -1;
     const dim3 grid((p.N + 16 * ct - 1) / (16 * ct), (p.M + 16 * rt - 1) / (16 * rt)), block(512);
-#define CYFA_LINEAR(RT_, CT_) \
-    if (rt == RT_ && ct == CT_) { hipLaunchKernelGGL((linear_rows_kernel<RT_, CT_>), grid, block, 0, stream, p); return 0; }
+    const bool norm = p.norm_weight != nullptr;
+#define CYFA_LINEAR(RT_, CT_)                                                                                  \
+    if (rt == RT_ && ct == CT_) {                                                                              \
+        if (norm)                                                                                              \
+            hipLaunchKernelGGL((linear_rows_kernel<RT_, CT_, true>), grid, block, 0, stream, p);              \
+        else                                                                                                   \
+            hipLaunchKernelGGL((linear_rows_kernel<RT_, CT_, false>), grid, block, 0, stream, p);             \
+        return 0;                                                                                              \
+    }
     CYFA_LINEAR(4, 2)
     CYFA_LINEAR(2, 4)
     CYFA_LINEAR(4, 1)

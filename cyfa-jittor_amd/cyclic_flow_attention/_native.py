@@ -14,7 +14,7 @@ import torch
 import torch.nn.functional as F
 
 LIB_PATH = Path(os.environ.get("CYFA_LIB", Path(__file__).with_name("libcyfa_hip.so")))
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 CYFA_OK = 0
 CYFA_ERR_VALUE = -1
@@ -91,6 +91,14 @@ class CyfaLinearArgs(ctypes.Structure):
         ("M", _c_int), ("N", _c_int), ("K", _c_int),
         ("x", _c_void_p), ("ldx", ctypes.c_longlong), ("weight", _c_void_p), ("bias", _c_void_p),
         ("y", _c_void_p), ("ldy", ctypes.c_longlong), ("swiglu", _c_int),
+        ("residual", _c_void_p), ("ldr", ctypes.c_longlong),
+    ]
+
+
+class CyfaRowNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("weight", _c_void_p), ("eps", ctypes.c_float), ("residual", _c_void_p), ("sum_out", _c_void_p),
+        ("ldr", ctypes.c_longlong),
     ]
 
 
@@ -118,6 +126,7 @@ SIGNATURES = {
     "cyfa_rms_norm": (_c_int, [ctypes.POINTER(CyfaNormArgs), _c_void_p]),
     "cyfa_short_conv": (_c_int, [ctypes.POINTER(CyfaConvArgs), _c_void_p]),
     "cyfa_linear_rows": (_c_int, [ctypes.POINTER(CyfaLinearArgs), _c_void_p]),
+    "cyfa_norm_linear_rows": (_c_int, [ctypes.POINTER(CyfaLinearArgs), ctypes.POINTER(CyfaRowNormArgs), _c_void_p]),
     "cyfa_silu_mul": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "cyfa_gates": (_c_int, [_c_void_p, ctypes.c_longlong, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                             _c_int, _c_int, _c_void_p]),
@@ -314,9 +323,10 @@ def rms_norm(x, weight, eps, gate=None, residual=None, prescale=1.0):
 LINEAR_ROWS_MAX = 64
 
 
-def linear(x, weight, bias=None, out_cols=None):
-    """x W^T (+ bias), bf16, like F.linear. Calls with at most 64 rows (the
-    one-token decode step) run on cyfa_linear_rows, which streams W once
+def linear(x, weight, bias=None, out_cols=None, residual=None):
+    """x W^T (+ bias), bf16, like F.linear; with ``residual``, the block's
+    residual add residual + bf16(x W^T + bias). Calls with at most 64 rows
+    (the one-token decode step) run on cyfa_linear_rows, which streams W once
     across the whole chip; larger calls go to the library GEMM. ``out_cols``
     (>= N) pads the output rows, so that column slices of the result start
     16-byte aligned."""
@@ -328,9 +338,15 @@ def linear(x, weight, bias=None, out_cols=None):
     rows = x.numel() // width if width else 0
     if (rows == 0 or rows > LINEAR_ROWS_MAX or K % 32 or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16
             or (bias is not None and bias.dtype != torch.bfloat16) or not x.is_cuda
+            or (residual is not None and residual.dtype != torch.bfloat16)
             or (torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad))):
-        return F.linear(x, weight, bias)
-    require_device(x, weight, bias)
+        y = F.linear(x, weight, bias)
+        return y if residual is None else residual + y
+    require_device(x, weight, bias, residual)
+    if residual is not None:
+        residual = residual.reshape(rows, N)
+        if residual.stride(-1) != 1:
+            residual = residual.contiguous()
     x2 = x.reshape(rows, width)
     if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
         x2 = x2.contiguous()
@@ -340,7 +356,8 @@ def linear(x, weight, bias=None, out_cols=None):
     ldy = max(N, out_cols or N)
     y = torch.empty(rows, ldy, dtype=torch.bfloat16, device=x.device)
     args = CyfaLinearArgs(M=rows, N=N, K=K, x=x2.data_ptr(), ldx=x2.stride(0), weight=w.data_ptr(),
-                          bias=ptr(None if bias is None else bias.detach().contiguous()), y=y.data_ptr(), ldy=ldy)
+                          bias=ptr(None if bias is None else bias.detach().contiguous()), y=y.data_ptr(), ldy=ldy,
+                          residual=ptr(residual), ldr=0 if residual is None else residual.stride(0))
     _check(load_library().cyfa_linear_rows(ctypes.byref(args), stream_handle(x.device)), "cyfa_linear_rows")
     lead = tuple(x.shape[:-1])
     if not lead:
@@ -349,6 +366,65 @@ def linear(x, weight, bias=None, out_cols=None):
     for i in range(len(lead) - 2, -1, -1):
         strides.insert(0, strides[0] * lead[i + 1])
     return y.as_strided(lead + (N,), tuple(strides))
+
+
+LINEAR_NORM_MAX_K = 2048
+
+
+def norm_linear(x, norm_weight, eps, weight, bias=None, residual=None, out_cols=None, swiglu=False):
+    """The block's pre-norm and its first projection in one cyfa_norm_linear_rows
+    launch, for at most 64 bf16 rows of K <= 2048 columns:
+    s = bf16(x + residual) (x itself without a residual), h = rms_norm(s), and
+    y = linear(h, weight, bias) (linear_swiglu(h, weight) with ``swiglu``).
+    Returns (s, y). Other shapes run rms_norm and the projection separately.
+    h may differ from rms_norm's in the last bit: the sum of squares runs in
+    another order."""
+    K = weight.shape[-1]
+    N = weight.shape[0]
+    if x.shape[-1] != K:
+        raise ValueError(f"norm_linear: x has {x.shape[-1]} columns, the weight needs {K}")
+    rows = x.numel() // K if K else 0
+    if (rows == 0 or rows > LINEAR_ROWS_MAX or K % 32 or K > LINEAR_NORM_MAX_K or x.dtype != torch.bfloat16
+            or weight.dtype != torch.bfloat16 or (bias is not None and bias.dtype != torch.bfloat16)
+            or (residual is not None and residual.dtype != torch.bfloat16) or not x.is_cuda
+            or (swiglu and (bias is not None or N % 32)) or torch.is_grad_enabled()):
+        if residual is None:
+            s, h = x, rms_norm(x, norm_weight, eps)
+        else:
+            s, h = rms_norm(x, norm_weight, eps, residual=residual)
+        return s, (linear_swiglu(h, weight) if swiglu else linear(h, weight, bias, out_cols))
+    require_device(x, weight, bias, residual)
+    x2 = x.reshape(rows, K)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    w = weight.detach()
+    if not w.is_contiguous():
+        w = w.contiguous()
+    nw = norm_weight.detach().to(torch.float32).contiguous()
+    s = x
+    r2 = total = None
+    if residual is not None:
+        r2 = residual.reshape(rows, K).contiguous()
+        if r2.data_ptr() % 16:
+            r2 = r2.clone()
+        total = torch.empty(rows, K, dtype=torch.bfloat16, device=x.device)
+        s = total.view(x.shape)
+    out_w = N // 2 if swiglu else N
+    ldy = max(out_w, out_cols or out_w)
+    y = torch.empty(rows, ldy, dtype=torch.bfloat16, device=x.device)
+    args = CyfaLinearArgs(M=rows, N=N, K=K, x=x2.data_ptr(), ldx=x2.stride(0), weight=w.data_ptr(),
+                          bias=ptr(None if bias is None else bias.detach().contiguous()), y=y.data_ptr(), ldy=ldy,
+                          swiglu=1 if swiglu else 0)
+    nargs = CyfaRowNormArgs(weight=nw.data_ptr(), eps=float(eps), residual=ptr(r2), sum_out=ptr(total), ldr=K)
+    _check(load_library().cyfa_norm_linear_rows(ctypes.byref(args), ctypes.byref(nargs), stream_handle(x.device)),
+           "cyfa_norm_linear_rows")
+    lead = tuple(x.shape[:-1])
+    if not lead:
+        return s, y.view(-1)[:out_w]
+    strides = [ldy, 1]  # rows ldy apart, whatever the sizes of the leading dims
+    for i in range(len(lead) - 2, -1, -1):
+        strides.insert(0, strides[0] * lead[i + 1])
+    return s, y.as_strided(lead + (out_w,), tuple(strides))
 
 
 def interleave_gate_up(gate_weight, up_weight):

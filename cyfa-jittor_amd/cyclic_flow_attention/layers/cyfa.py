@@ -237,9 +237,12 @@ class CyclicFlowAttention(nn.Module):
             self._table_key = key
         return self._table
 
+    def _fused_ok(self, x, attention_mask):
+        return (inference_fast_path(x) and attention_mask is None and self.use_short_conv
+                and 2 <= self.q_conv1d.width <= 4 and self.q_conv1d.bias is None)
+
     def forward(self, x, cache=None, use_cache=False, attention_mask=None):
-        if (inference_fast_path(x) and attention_mask is None and self.use_short_conv
-                and 2 <= self.q_conv1d.width <= 4 and self.q_conv1d.bias is None):
+        if self._fused_ok(x, attention_mask):
             return self._forward_fused(x, cache, use_cache)
         B, T, _ = x.shape
         H = self.num_heads
@@ -293,9 +296,27 @@ class CyclicFlowAttention(nn.Module):
         new_cache = {"recurrent_state": state, "conv_state": (cq, ck, cv)} if use_cache else None
         return o, new_cache
 
-    def _forward_fused(self, x, cache, use_cache):
-        """bf16 inference: the same math as forward with fused launches."""
+    def forward_block(self, x, norm, cache=None, use_cache=False):
+        """The attention half of a decoder block, x + self(norm(x), cache,
+        use_cache) (CyFABlock.execute, models/cyfa/modeling_cyfa.py:48-51), for
+        the decoder's bf16 inference loop. Returns (x + o, new_cache). A decode
+        step with at most 64 rows runs the norm inside the input projection and
+        the residual add inside o_proj."""
+        if self._fused_ok(x, None):
+            return self._forward_fused(x, cache, use_cache, prenorm=norm)
+        o, new_cache = self(norm(x), cache, use_cache)
+        return x + o, new_cache
+
+    def _forward_fused(self, x, cache, use_cache, prenorm=None):
+        """bf16 inference: the same math as forward with fused launches. With
+        ``prenorm`` (the block's norm), x is the block input and the result is
+        (x + o, new_cache), as forward_block."""
         B, T, _ = x.shape
+        block_in = None
+        if prenorm is not None:
+            block_in = x
+            if B * T > _native.LINEAR_ROWS_MAX:
+                x, prenorm = prenorm(x), None
         H, Dk, Dv = self.num_heads, self.key_dim, self.value_dim
         W = self.q_conv1d.width
         g0, g1 = self.g_proj
@@ -313,7 +334,11 @@ class CyclicFlowAttention(nn.Module):
             w_in = self._in_weight.get(self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, g0.weight,
                                        self.a_proj.weight, self.b_proj.weight, self.d_proj.weight)
             b_in = self._in_bias.get(self._in_bias_zero, abd_bias)
-            y_in = _native.linear(x, w_in, b_in, out_cols=(D3 + Dg + 3 * H + 7) // 8 * 8)
+            if prenorm is not None:
+                _, y_in = _native.norm_linear(x, prenorm.weight, prenorm.eps, w_in, b_in,
+                                              out_cols=(D3 + Dg + 3 * H + 7) // 8 * 8)
+            else:
+                y_in = _native.linear(x, w_in, b_in, out_cols=(D3 + Dg + 3 * H + 7) // 8 * 8)
             qkv, g0_out, abd = y_in[..., :D3], y_in[..., D3:D3 + Dg], y_in[..., D3 + Dg:]
         else:
             qkv = _native.linear(x, self._qkv_weight.get(self.q_proj.weight, self.k_proj.weight, self.v_proj.weight))
@@ -346,7 +371,7 @@ class CyclicFlowAttention(nn.Module):
                 self.q_norm.weight, self.k_norm.weight, self.q_norm.eps, self.k_norm.eps, H,
                 initial_state=None if cache is None else cache["recurrent_state"], output_final_state=use_cache,
                 inplace=self.decode_in_place and cache is not None)
-            o = _native.linear(o.view(B, T, Dv), self.o_proj.weight)
+            o = _native.linear(o.view(B, T, Dv), self.o_proj.weight, residual=block_in)
             cq, ck, cv = tail[..., :Dk], tail[..., Dk:2 * Dk], tail[..., 2 * Dk:]
             new_cache = {"recurrent_state": state, "conv_state": (cq, ck, cv)} if use_cache else None
             return o, new_cache
@@ -389,7 +414,7 @@ class CyclicFlowAttention(nn.Module):
                                   output_norm=(self.o_norm.weight, gate, self.o_norm.eps,
                                                float(self.num_slots - 1)))
             o = o.view(B, T, Dv)
-        o = _native.linear(o, self.o_proj.weight)
+        o = _native.linear(o, self.o_proj.weight, residual=block_in)
         new_cache = {"recurrent_state": state, "conv_state": (cq, ck, cv)} if use_cache else None
         return o, new_cache
 

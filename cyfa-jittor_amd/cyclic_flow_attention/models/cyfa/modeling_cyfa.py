@@ -44,6 +44,18 @@ class GatedMLP(nn.Module):
         u = self.up_proj(x)
         return self.down_proj((F.silu(g.float()) * u.float()).to(x.dtype))
 
+    def forward_block(self, x, norm):
+        """The MLP half of a decoder block, x + self(norm(x)). A decode step with
+        at most 64 rows runs the norm inside the gate|up projection and the
+        residual add inside down_proj."""
+        rows = x.numel() // x.shape[-1]
+        if (inference_fast_path(x) and rows <= _native.LINEAR_ROWS_MAX and self.gate_proj.weight.shape[0] % 16 == 0
+                and x.shape[-1] % 32 == 0):
+            w = self._gate_up_il.get(self.gate_proj.weight, self.up_proj.weight, build=_native.interleave_gate_up)
+            _, h = _native.norm_linear(x, norm.weight, norm.eps, w, swiglu=True)
+            return _native.linear(h, self.down_proj.weight, residual=x)
+        return x + self(norm(x))
+
 
 class CyFABlock(nn.Module):
     def __init__(self, config):
@@ -86,8 +98,17 @@ class CyclicFlowAttentionModel(nn.Module):
                 x, s = layer(x, None if cache is None else cache[i], use_cache, attention_mask)
                 new.append(s)
             return self.norm(x), (new if use_cache else None)
-        # bf16 inference: each residual add runs inside the following norm
-        # kernel (x + y and residual + mlp, as CyFABlock.forward, bit for bit).
+        if x.numel() // x.shape[-1] <= _native.LINEAR_ROWS_MAX and attention_mask is None:
+            # bf16 decode steps: each pre-norm runs inside the projection after
+            # it, each residual add inside the projection before it (x + y, as
+            # CyFABlock.forward, bit for bit)
+            for i, layer in enumerate(self.layers):
+                x, s = layer.attn.forward_block(x, layer.attn_norm, None if cache is None else cache[i], use_cache)
+                x = layer.mlp.forward_block(x, layer.mlp_norm)
+                new.append(s)
+            return self.norm(x), (new if use_cache else None)
+        # bf16 prefill: each residual add runs inside the following norm kernel
+        # (x + y and residual + mlp, as CyFABlock.forward, bit for bit)
         pending = None
         for i, layer in enumerate(self.layers):
             h = layer.attn_norm(x) if pending is None else None

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define CYFA_ABI_VERSION 1
+#define CYFA_ABI_VERSION 2
 
 enum {
     CYFA_OK = 0,
@@ -204,7 +204,9 @@ int cyfa_rms_norm(const CyfaNormArgs *args, void *hip_stream);
  * multiple of 32), the rows of W come in groups of 32: 16 rows of the gate
  * projection, then the matching 16 rows of the up projection, and y [M, N/2]
  * receives the SwiGLU product bf16(g sigmoid(g) u) of the bf16-rounded g and u
- * (GatedMLP, models/cyfa/modeling_cyfa.py:22-27). */
+ * (GatedMLP, models/cyfa/modeling_cyfa.py:22-27). With residual set, y is the
+ * block's residual add around the projection (CyFABlock.execute,
+ * models/cyfa/modeling_cyfa.py:48-51). */
 typedef struct CyfaLinearArgs {
     int M, N, K;
     const void *x;                /* bf16 [M, K], rows ldx elements apart (ldx >= K, ldx % 8 == 0) */
@@ -214,6 +216,9 @@ typedef struct CyfaLinearArgs {
     void *y;                      /* bf16 [M, N] ([M, N/2] with swiglu), rows ldy elements apart */
     long long ldy;
     int swiglu;
+    const void *residual;         /* nullable bf16 [M, N], rows ldr apart: y = bf16(residual + bf16(x W^T + b));
+                                     not with swiglu; may be y itself */
+    long long ldr;
 } CyfaLinearArgs;
 
 /* Replaces the Linear / BiasLinear projections (layers/cyfa.py:15-58) of the
@@ -223,6 +228,26 @@ typedef struct CyfaLinearArgs {
  * the lm_head (models/cyfa/modeling_cyfa.py:80, 100). fp32 accumulation, one bf16
  * rounding. */
 int cyfa_linear_rows(const CyfaLinearArgs *args, void *hip_stream);
+
+/* The RMS norm in front of a projection (K <= 2048 columns):
+ *   s  = residual ? bf16(x + residual) : x        (sum_out receives s)
+ *   xs = bf16(s * rsqrt(mean(s^2) + eps) * weight)
+ * and the projection reads xs in place of x. */
+typedef struct CyfaRowNormArgs {
+    const float *weight;          /* f32 [K], 16-byte aligned */
+    float eps;
+    const void *residual;         /* nullable bf16 [M, K], rows ldr elements apart */
+    void *sum_out;                /* bf16 [M, K], rows ldr apart; required with residual; aliases no input */
+    long long ldr;
+} CyfaRowNormArgs;
+
+/* Replaces the pre-norm in front of the first projection of each block of a
+ * decode step: attn_norm (with the residual add x + attn(...)) before the q/k/v,
+ * g and a/b/d projections, and mlp_norm before the GatedMLP gate/up projection
+ * (CyFABlock.execute, models/cyfa/modeling_cyfa.py:48-51; RMSNorm,
+ * layers/cyfa.py:62-135). The norm's sum of squares runs in another order than
+ * cyfa_rms_norm's, so xs may differ from it in the last bit. */
+int cyfa_norm_linear_rows(const CyfaLinearArgs *args, const CyfaRowNormArgs *norm, void *hip_stream);
 
 /* Arguments of one causal depthwise convolution over time of B x T rows of D
  * bf16 channels (D a multiple of 8, W in 2..4):

@@ -50,7 +50,8 @@ def _c_layout(tmp_path, struct, fields):
                                       (_native.CyfaDecodeLayerArgs, "CyfaDecodeLayerArgs"),
                                       (_native.CyfaNormArgs, "CyfaNormArgs"),
                                       (_native.CyfaConvArgs, "CyfaConvArgs"),
-                                      (_native.CyfaLinearArgs, "CyfaLinearArgs")])
+                                      (_native.CyfaLinearArgs, "CyfaLinearArgs"),
+                                      (_native.CyfaRowNormArgs, "CyfaRowNormArgs")])
 def test_struct_layout_matches_header(tmp_path, cls, name):
     fields = [f for f, _ in cls._fields_]
     got = [ctypes.sizeof(cls)] + [getattr(cls, f).offset for f in fields]
@@ -111,6 +112,18 @@ def test_layer_entry_points_validate_before_launch():
     assert lib.cyfa_short_conv(ctypes.byref(c), None) == _native.CYFA_ERR_UNSUPPORTED
     assert lib.cyfa_silu_mul(None, None, 1, 8, None) == _native.CYFA_ERR_VALUE
     assert lib.cyfa_gates(None, 12, None, None, None, None, None, 1, 4, None) == _native.CYFA_ERR_VALUE
+    # the fused pre-norm: checked before anything is launched (the pointers are never dereferenced)
+    a = _native.CyfaLinearArgs(M=4, N=64, K=4096, x=0x10000, ldx=4096, weight=0x20000, y=0x30000, ldy=64)
+    nrm = _native.CyfaRowNormArgs(weight=0x40000, eps=1e-6)
+    assert lib.cyfa_norm_linear_rows(ctypes.byref(a), ctypes.byref(nrm), None) == _native.CYFA_ERR_UNSUPPORTED
+    a.K = a.ldx = 1024
+    assert lib.cyfa_norm_linear_rows(ctypes.byref(a), None, None) == _native.CYFA_ERR_VALUE
+    nrm.residual, nrm.ldr = 0x50000, 1024
+    assert lib.cyfa_norm_linear_rows(ctypes.byref(a), ctypes.byref(nrm), None) == _native.CYFA_ERR_VALUE  # no sum_out
+    nrm.sum_out, nrm.ldr = 0x60000, 1000
+    assert lib.cyfa_norm_linear_rows(ctypes.byref(a), ctypes.byref(nrm), None) == _native.CYFA_ERR_VALUE  # ldr
+    nrm.ldr, nrm.weight = 1024, 0x40004
+    assert lib.cyfa_norm_linear_rows(ctypes.byref(a), ctypes.byref(nrm), None) == _native.CYFA_ERR_ALIGN
 
 
 def test_scalar_la_validates_before_launch():

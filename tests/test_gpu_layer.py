@@ -278,6 +278,69 @@ def test_linear_rows_tile_shape_does_not_change_bits(N, K):
         assert torch.equal(y[0], full[m]), f"row {m}"
 
 
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1024, 1024), (64, 1024, 2816), (17, 3340, 256)])
+def test_linear_rows_residual_add(M, N, K):
+    """The residual-add epilogue of cyfa_linear_rows (the block's x + o_proj(o)
+    and x + down(h)) equals the projection followed by a bf16 add, bit for bit."""
+    from cyclic_flow_attention import _native
+
+    gen = torch.Generator().manual_seed(M + N + K)
+    x = torch.randn(M, K, generator=gen).bfloat16().to(DEV)
+    w = (0.05 * torch.randn(N, K, generator=gen)).bfloat16().to(DEV)
+    b = torch.randn(N, generator=gen).bfloat16().to(DEV)
+    r = torch.randn(M, N + 8, generator=gen).bfloat16().to(DEV)[:, :N]  # rows N + 8 apart
+    with torch.no_grad():
+        got = _native.linear(x, w, b, residual=r)
+        ref = r + _native.linear(x, w, b)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("M,residual,swiglu,K", [(1, False, False, 1024), (37, True, False, 1024),
+                                                 (64, True, False, 1024), (64, True, True, 1024),
+                                                 (5, True, True, 2048), (64, False, False, 512)])
+def test_norm_linear_rows(M, residual, swiglu, K):
+    """cyfa_norm_linear_rows (the pre-norm inside the projection): s equals the
+    separate residual add bit for bit; y against the norm and the projection
+    in float64, with the bound of one bf16 rounding of each normalised input
+    and of the result plus the fp32 summation error (factor two to spare); and
+    y equals rms_norm followed by linear except where the norm's sum of squares,
+    added in another order, moves an input across a bf16 rounding boundary."""
+    from cyclic_flow_attention import _native
+
+    gen = torch.Generator().manual_seed(M * 7 + K + 3 * residual + swiglu)
+    N = 2 * 1408 if swiglu else 3340
+    x = torch.randn(M, K, generator=gen).bfloat16()
+    r = torch.randn(M, K, generator=gen).bfloat16() if residual else None
+    nw = 1.0 + 0.1 * torch.randn(K, generator=gen)
+    w = (0.05 * torch.randn(N, K, generator=gen)).bfloat16()
+    b = None if swiglu else torch.randn(N, generator=gen).bfloat16()
+    d = lambda t: None if t is None else t.to(DEV)  # noqa: E731
+    with torch.no_grad():
+        s, y = _native.norm_linear(d(x), d(nw), 1e-6, d(w), d(b), residual=d(r), swiglu=swiglu)
+        if residual:
+            s_ref, h_ref = _native.rms_norm(d(x), d(nw), 1e-6, residual=d(r))
+        else:
+            s_ref, h_ref = d(x), _native.rms_norm(d(x), d(nw), 1e-6)
+        y_ref = _native.linear_swiglu(h_ref, d(w)) if swiglu else _native.linear(h_ref, d(w), d(b))
+    torch.cuda.synchronize()
+    assert torch.equal(s, s_ref)
+    assert y.shape == y_ref.shape and not y.isnan().any()
+    if not swiglu:
+        s64 = s.cpu().double()
+        h64 = s64 * torch.rsqrt(s64.pow(2).mean(-1, keepdim=True) + 1e-6) * nw.double()
+        y64 = h64 @ w.double().T + b.double()
+        mag = h64.abs() @ w.double().abs().T
+        bound = 2 * (BF16_ULP / 2 * (y64.abs() + mag) + K * 2.0 ** -24 * mag) + 1e-30
+        err = (y.cpu().double() - y64).abs()
+        assert (err <= bound).all(), f"max err {err.max().item()}"
+    # one input moved by an ulp changes about a tenth of its row's outputs
+    rows = int((y != y_ref).reshape(M, -1).any(-1).sum())
+    assert rows <= max(1, M // 10), f"{rows} of {M} rows differ from rms_norm + linear"
+
+
 @pytest.mark.parametrize("B,state,inplace", [(3, True, False), (2, False, False), (4, True, True)])
 def test_decode_layer_step_equals_separate_kernels(B, state, inplace):
     """cyfa_decode_layer_step (short convolution, gates, decode op and gated
