@@ -98,7 +98,7 @@ __device__ __forceinline__ bf16x8 lin_ld(lin_rsrc_t r, uint32_t off) {
 }
 
 // k-steps whose loads a wave has in flight together: about 24 loads per lane
-__host__ __device__ constexpr int lin_batch(int rt, int ct) { return rt + ct <= 3 ? 8 : rt + ct <= 4 ? 6 : 4; }
+__host__ __device__ constexpr int lin_batch(int rt, int ct) { return rt + ct <= 2 ? 12 : rt + ct <= 3 ? 8 : rt + ct <= 4 ? 6 : 4; }
 
 template <int U, int RT, int CT>
 __device__ __forceinline__ void lin_issue_w(lin_rsrc_t rw, int s, int s1, uint32_t wrow, uint32_t wstride, int lg,
