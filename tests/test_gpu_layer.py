@@ -410,3 +410,39 @@ def test_linear_swiglu_equals_projection_then_silu_mul(M):
         got = _native.linear_swiglu(x, _native.interleave_gate_up(wg, wu))
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
+
+
+def test_padded_generation_matches_individual_prompts():
+    """generate_batch over right-padded prompts gives each prompt's own greedy
+    continuation (the reference's tests/test_inference.py:56-65)."""
+    from cyclic_flow_attention.generation import generate, generate_batch
+
+    model, _, _ = _model("tiny.json", seed=0)
+    prompts = [[10, 20, 30], list(range(4, 67))]
+    expected = [generate(model, ids, max_new_tokens=8) for ids in prompts]
+    actual = generate_batch(model, prompts, max_new_tokens=8)
+    assert actual == expected
+    with pytest.raises(ValueError):
+        generate_batch(model, [[1], []])
+
+
+def test_checkpoint_round_trip_and_seeded_sampling(tmp_path):
+    """A saved and reloaded model gives the same logits, and sampling with a
+    seed repeats (the reference's tests/test_inference.py:20-53)."""
+    from cyclic_flow_attention.generation import generate
+    from cyclic_flow_attention.utils import load_model, save_model
+
+    model, _, _ = _model("tiny.json", seed=1)
+    ids = (torch.arange(65)[None] + 32).to(DEV)
+    with torch.no_grad():
+        reference = model(ids)["logits"]
+    save_model(model, tmp_path)
+    loaded, _ = load_model(tmp_path)
+    loaded = loaded.to(DEV).eval()
+    with torch.no_grad():
+        assert torch.equal(loaded(ids)["logits"], reference)
+    first = generate(loaded, [32, 33], 4, temperature=0.8, top_p=0.9, seed=5)
+    second = generate(loaded, [32, 33], 4, temperature=0.8, top_p=0.9, seed=5)
+    assert first == second and len(first) == 4
+    with pytest.raises(ValueError):
+        generate(loaded, [32], 4, top_p=0.0)
