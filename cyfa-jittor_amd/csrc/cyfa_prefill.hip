@@ -1305,6 +1305,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         store_half_rows(om, 64, sOm);
         store_rows<TileF>(vraw, p.T - t0, sV);
         __syncthreads();
+        // NORM: this chunk's gate for the lane's output coordinates, issued
+        // before the next chunk's loads, so that waiting for it in the
+        // epilogue does not wait for them (loads complete in order).
+        bf16x4 gate[4][2];
+        if constexpr (NORM) {
+            const rsrc_t rg = rows_rsrc(p, b, h, p.on_gate);
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+                for (int c = 0; c < 2; c++) gate[tb][c] = ld_b64(rg, o_lane + 32 * c, (uint32_t)(t0 + 16 * tb) * sq.row16);
+        }
         // The next chunk's loads are spread over the phases (see pass 1).
         if (n + 1 < n1) issue_omega(rom, t0 + 64, om);
 
@@ -1336,14 +1347,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
             issue_rows(sq, sq.v, p.T, t0 + 64, vraw);
             gr = issue_gates(sq, p.T, t0 + 64);
         }
-        bf16x4 gate[4][2];  // gate of the output coordinates of this lane (NORM)
-        if constexpr (NORM) {
-            const rsrc_t rg = rows_rsrc(p, b, h, p.on_gate);
-#pragma unroll
-            for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-                for (int c = 0; c < 2; c++) gate[tb][c] = ld_b64(rg, o_lane + 32 * c, (uint32_t)(t0 + 16 * tb) * sq.row16);
-        }
 
         // o^T += v^T P^T. vb[c][ss][jj] = v[32 ss + 8 lg + jj][32 w + 16 c + lr].
         bf16x8 vb[2][2];
@@ -1361,9 +1364,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
             }
         bf16x4 xs[4][2];  // NORM: bf16(bf16(o) * prescale)
         if constexpr (NORM) {
+            float ss[4];
 #pragma unroll
             for (int tb = 0; tb < 4; tb++) {
-                float ss = 0.f;
+                ss[tb] = 0.f;
 #pragma unroll
                 for (int c = 0; c < 2; c++) {
                     const bf16x4 o4 = to_bf16x4(out[tb][c], 1.f);
@@ -1371,12 +1375,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
                     for (int i = 0; i < 4; i++) {
                         xs[tb][c][i] = (bf16_t)((float)o4[i] * p.on_prescale);
                         const float x = (float)xs[tb][c][i];
-                        ss = fmaf(x, x, ss);
+                        ss[tb] = fmaf(x, x, ss[tb]);
                     }
                 }
-                ss += __shfl_xor(ss, 16);
-                ss += __shfl_xor(ss, 32);
-                if (lg == 0) sNs[(16 * tb + lr) * 8 + w] = ss;
+            }
+            // the four tiles' exchanges issued together (their latencies overlap)
+            float sh[4];
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++) sh[tb] = __shfl_xor(ss[tb], 16);
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++) ss[tb] += sh[tb];
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++) sh[tb] = __shfl_xor(ss[tb], 32);
+#pragma unroll
+            for (int tb = 0; tb < 4; tb++) {
+                ss[tb] += sh[tb];
+                if (lg == 0) sNs[(16 * tb + lr) * 8 + w] = ss[tb];
             }
         } else {
 #pragma unroll
