@@ -49,7 +49,8 @@ int cyfa_readout_table(const float* readout, float* table, int H, int M, void* h
     if (M != 128) return fail(CYFA_ERR_UNSUPPORTED, "cyfa_readout_table: num_slots must be 128, got %d", M);
     if (H <= 0) return fail(CYFA_ERR_VALUE, "cyfa_readout_table: H must be positive, got %d", H);
     if (!readout || !table) return fail(CYFA_ERR_VALUE, "cyfa_readout_table: null pointer");
-    cyfa::launch_readout_table(readout, table, H, (hipStream_t)hip_stream);
+    if (cyfa::launch_readout_table(readout, table, H, (hipStream_t)hip_stream) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_readout_table: launch refused");
     return check_launch("cyfa_readout_table");
 }
 
@@ -221,7 +222,8 @@ int chunk_fwd(const CyfaChunkArgs* a, const CyfaOutNormArgs* on, void* hip_strea
     p.seg_exp = (int*)(base + ws.seg_exp);
     p.seg_decay = (float*)(base + ws.seg_decay);
     p.omega = (__bf16*)(base + ws.omega);
-    cyfa::launch_prefill(p, (hipStream_t)hip_stream);
+    if (cyfa::launch_prefill(p, (hipStream_t)hip_stream) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_chunk_fwd: launch refused");
     return check_launch(on ? "cyfa_chunk_fwd_normed" : "cyfa_chunk_fwd");
 }
 
@@ -281,7 +283,8 @@ int cyfa_scalar_la(const CyfaSlaArgs* a, void* hip_stream) {
     p.seg = (_Float16*)(base + ws.seg);
     p.seg_exp = (int*)(base + ws.seg_exp);
     p.seg_decay = (float*)(base + ws.seg_decay);
-    cyfa::launch_scalar_la(p, (hipStream_t)hip_stream);
+    if (cyfa::launch_scalar_la(p, (hipStream_t)hip_stream) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_scalar_la: launch refused");
     return check_launch("cyfa_scalar_la");
 }
 
@@ -369,7 +372,8 @@ int cyfa_rms_norm(const CyfaNormArgs* a, void* hip_stream) {
     p.eps = a->eps;
     p.prescale = a->prescale;
     p.out = (__bf16*)a->out;
-    cyfa::launch_rms_norm(p, (hipStream_t)hip_stream);
+    if (cyfa::launch_rms_norm(p, (hipStream_t)hip_stream) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_rms_norm: D=%d", a->D);
     return check_launch("cyfa_rms_norm");
 }
 
@@ -407,7 +411,8 @@ int cyfa_short_conv(const CyfaConvArgs* a, void* hip_stream) {
     p.cache_out = (__bf16*)a->cache_out;
     p.cache_out_row = a->cache_out_row;
     p.cache_out_batch = a->cache_out_batch;
-    cyfa::launch_short_conv(p, (hipStream_t)hip_stream);
+    if (cyfa::launch_short_conv(p, (hipStream_t)hip_stream) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_short_conv: W=%d", a->W);
     return check_launch("cyfa_short_conv");
 }
 
@@ -416,7 +421,8 @@ int cyfa_silu_mul(const void* gu, void* out, int rows, int F, void* hip_stream) 
     if (F % 8 != 0) return fail(CYFA_ERR_UNSUPPORTED, "cyfa_silu_mul: F=%d must be a multiple of 8", F);
     if (!aligned(gu, 16) || !aligned(out, 16)) return fail(CYFA_ERR_ALIGN, "cyfa_silu_mul: 16-byte alignment needed");
     if (rows == 0) return CYFA_OK;
-    cyfa::launch_silu_mul((const __bf16*)gu, (__bf16*)out, rows, F, (hipStream_t)hip_stream);
+    if (cyfa::launch_silu_mul((const __bf16*)gu, (__bf16*)out, rows, F, (hipStream_t)hip_stream) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_silu_mul: launch refused");
     return check_launch("cyfa_silu_mul");
 }
 
@@ -425,7 +431,8 @@ int cyfa_gates(const void* abd, long long abd_row, const float* dt_bias, const f
     if (!abd || !dt_bias || !A_log || !g || !beta || !delta || rows < 0 || H <= 0 || abd_row < 3LL * H)
         return fail(CYFA_ERR_VALUE, "cyfa_gates: bad arguments");
     if (rows == 0) return CYFA_OK;
-    cyfa::launch_gates((const __bf16*)abd, abd_row, dt_bias, A_log, g, beta, delta, rows, H, (hipStream_t)hip_stream);
+    if (cyfa::launch_gates((const __bf16*)abd, abd_row, dt_bias, A_log, g, beta, delta, rows, H, (hipStream_t)hip_stream) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_gates: launch refused");
     return check_launch("cyfa_gates");
 }
 
