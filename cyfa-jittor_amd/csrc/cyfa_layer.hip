@@ -188,14 +188,21 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
         // columns in every tile shape. Its sum of squares runs over its
         // k-steps in order, then over the row's four lanes (xor 16, xor 32)
         // and the eight waves in wave order.
+        // x (and the residual) first, then the norm weight, then W: loads
+        // complete in order, so the norm waits for x alone while W streams in.
         const bool res = p.norm_residual != nullptr;
-        lin_issue_w<U, RT, CT>(rw, s0, s1, wrow, wstride, lg, wf);
         lin_issue_x<U, RT>(rx, s0, s1, xrow, xstride, lg, xf);
+        bf16x8 rf[U][RT];
         if (res) {
             const lin_rsrc_t rr =
                 lin_rsrc(p.norm_residual + (size_t)m0 * p.ldr, ((size_t)(mrows - 1) * p.ldr + p.K) * 2);
-            bf16x8 rf[U][RT];
             lin_issue_x<U, RT>(rr, s0, s1, (uint32_t)lr * (uint32_t)p.ldr * 2, (uint32_t)(16 * p.ldr * 2), lg, rf);
+        }
+        const bool has_nw = 4 * (int)threadIdx.x < p.K;  // K <= 2048: one float4 per thread at most
+        float4 nwv = float4{0.f, 0.f, 0.f, 0.f};
+        if (has_nw) nwv = reinterpret_cast<const float4*>(p.norm_weight)[threadIdx.x];
+        lin_issue_w<U, RT, CT>(rw, s0, s1, wrow, wstride, lg, wf);
+        if (res) {
             // s = bf16(x + residual); the first column of workgroups writes it out
 #pragma unroll
             for (int u = 0; u < U; u++) {
@@ -211,7 +218,7 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
                 }
             }
         }
-        for (int i = threadIdx.x; 4 * i < p.K; i += 512) snw[i] = reinterpret_cast<const float4*>(p.norm_weight)[i];
+        if (has_nw) snw[threadIdx.x] = nwv;
         float ss[RT];
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
