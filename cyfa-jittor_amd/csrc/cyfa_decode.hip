@@ -55,6 +55,7 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     __shared__ float s_part[NW][V > kSlots ? V : kSlots];
     __shared__ float s_red[2][NW];
     __shared__ float s_v[LAYER ? V : 1];
+    __shared__ __align__(16) float s_tab[kActive * kSlots];  // this head's readout table
 
     const bool has_state = p.hk_in != nullptr;
     const float4* hk_in = reinterpret_cast<const float4*>(p.hk_in + (size_t)bh * K * kSlots);
@@ -82,6 +83,29 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
             }
         }
     }
+
+    // Layer step: wave 0's norm weight and gate for the output norm at the
+    // end, loaded now so that their latency is not the kernel's last step.
+    constexpr int OJ = (V + 255) / 256;  // four consecutive values per lane and 256-wide block
+    float4 on_w4[OJ];
+    bf16x4 on_g4[OJ];
+    if (LAYER && wave == 0) {
+        const bf16_t* gt = p.gate + (size_t)(bh / p.H) * p.gate_row + (size_t)h * V;
+#pragma unroll
+        for (int j = 0; j < OJ; j++) {
+            on_w4[j] = *reinterpret_cast<const float4*>(p.on_w + 4 * lane + 256 * j);
+            on_g4[j] = *reinterpret_cast<const bf16x4*>(gt + 4 * lane + 256 * j);
+        }
+    }
+
+    // The readout table (L2-resident, 64 KB per head) is read into registers
+    // ahead of the state streams and staged in LDS during the prologue, so the
+    // readout after the state writes finds it on chip.
+    constexpr int TQ = kActive * kSlots / 4;  // float4 of the table: 3 per thread, 4 for the first 992
+    static_assert(NT == 1024 && TQ > 3 * NT && TQ <= 4 * NT, "table staging covers the table");
+    const float4* tb4 = reinterpret_cast<const float4*>(p.table + (size_t)h * kActive * kSlots);
+    const float4 tab0 = tb4[tid], tab1 = tb4[tid + NT], tab2 = tb4[tid + 2 * NT];
+    const float4 tab3 = tid + 3 * NT < TQ ? tb4[tid + 3 * NT] : float4{0.f, 0.f, 0.f, 0.f};
 
     // Issue both state streams; everything below overlaps with them.
     float4 hk_r[KJ], hv_r[VJ];
@@ -137,6 +161,13 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     if (lane == 0 && wave < K / 64) {
         s_red[0][wave] = sq;
         s_red[1][wave] = sk;
+    }
+    {
+        float4* st4 = reinterpret_cast<float4*>(s_tab);
+        st4[tid] = tab0;
+        st4[tid + NT] = tab1;
+        st4[tid + 2 * NT] = tab2;
+        if (tid + 3 * NT < TQ) st4[tid + 3 * NT] = tab3;
     }
     const float clock = has_state ? p.clock_in[bh] : 0.f;
     const float lam = clock + delta_in;
@@ -242,7 +273,7 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
         s_z[2 * tid + 1] = s * e + c * o;
     }
     __syncthreads();
-    const float* tb = p.table + (size_t)h * kActive * kSlots;
+    const float* tb = s_tab;
     {
         const int r = tid >> 3, part = tid & 7;
         float lg = 0.f;
@@ -335,8 +366,7 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     }
     __syncthreads();
     if (wave == 0) {
-        constexpr int J = (V + 255) / 256;  // four consecutive values per lane and 256-wide block (V = 256)
-        const int b = bh / p.H;
+        constexpr int J = OJ;
         float xs[J][4];
         float ss = 0.f;
 #pragma unroll
@@ -350,12 +380,11 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
             }
         ss = wave_sum(ss);
         const float rs = rsqrtf(ss / (float)V + p.on_eps);
-        const bf16_t* gt = p.gate + (size_t)b * p.gate_row + (size_t)h * V;
 #pragma unroll
         for (int j = 0; j < J; j++) {
             const int d0 = 4 * lane + 256 * j;
-            const float4 w = *reinterpret_cast<const float4*>(p.on_w + d0);
-            const bf16x4 g4 = *reinterpret_cast<const bf16x4*>(gt + d0);
+            const float4 w = on_w4[j];
+            const bf16x4 g4 = on_g4[j];
             const float wa[4] = {w.x, w.y, w.z, w.w};
             bf16x4 y;
 #pragma unroll
