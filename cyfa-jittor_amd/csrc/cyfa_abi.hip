@@ -76,8 +76,9 @@ int decode_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* ly, void* hi
         if (ly->qkv_row < D || ly->abd_row < 3LL * a->H || ly->gate_row < (long long)a->H * 256 || ly->gate_row % 4 ||
             ly->cache_row < D || ly->cache_batch < 3 * ly->cache_row)
             return fail(CYFA_ERR_VALUE, "cyfa_decode_layer_step: row strides too small");
-        if (!aligned(ly->gate, 8) || !aligned(ly->norm_weight, 16))
-            return fail(CYFA_ERR_ALIGN, "cyfa_decode_layer_step: gate needs 8-byte and norm_weight 16-byte alignment");
+        if (!aligned(ly->gate, 8) || !aligned(ly->conv_weight, 8) || !aligned(ly->norm_weight, 16))
+            return fail(CYFA_ERR_ALIGN,
+                        "cyfa_decode_layer_step: gate and conv_weight need 8-byte, norm_weight 16-byte alignment");
         if (!(ly->norm_eps >= 0.f) || !isfinite(ly->norm_prescale))
             return fail(CYFA_ERR_VALUE, "cyfa_decode_layer_step: norm_eps=%g prescale=%g", (double)ly->norm_eps,
                         (double)ly->norm_prescale);

@@ -78,8 +78,9 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
                     cwin[c][w] = p.cache_in ? (float)p.cache_in[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch[c]]
                                             : 0.f;
                 cwin[c][3] = (float)p.qkv[(size_t)b * p.qkv_row + ch[c]];
+                const bf16x4 wt = *reinterpret_cast<const bf16x4*>(p.conv_w + (size_t)ch[c] * 4);  // one 8-byte load
 #pragma unroll
-                for (int w = 0; w < 4; w++) cwt[c][w] = (float)p.conv_w[(size_t)ch[c] * 4 + w];
+                for (int w = 0; w < 4; w++) cwt[c][w] = (float)wt[w];
             }
         }
     }

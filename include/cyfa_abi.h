@@ -151,7 +151,7 @@ typedef struct CyfaDecodeLayerArgs {
     const void *conv_cache;       /* nullable bf16 [B, 3, 3 H 256] (zero history) */
     void *conv_cache_out;         /* bf16, same addressing; may be conv_cache (updated in place) */
     long long cache_row, cache_batch;
-    const void *conv_weight;      /* bf16 [3 H 256, 4] */
+    const void *conv_weight;      /* bf16 [3 H 256, 4], 8-byte aligned */
     const void *abd;              /* bf16 rows [B, abd_row]: a | b | d (H each), b and d biases added */
     long long abd_row;
     const float *dt_bias, *A_log; /* f32 [H] */
