@@ -121,3 +121,39 @@ def test_causal_lm_prefix_then_decode_equals_full_forward():
         logits, cache = MO.causal_lm(lm, cfg, ids[:, t:t + 1], cache=cache, use_cache=True)
         outs.append(logits)
     torch.testing.assert_close(torch.cat(outs, 1), full, atol=1e-10, rtol=0)
+
+
+def test_gated_mlp_against_a_scalar_loop_and_its_special_cases():
+    """GatedMLP (models/cyfa/modeling_cyfa.py:13-27) in exact mode against a
+    brute-force float64 loop over scalars with math.exp, on a tiny input, and
+    the cases the formula fixes: zero up projection gives zero, a gate of zero
+    gives zero (silu(0) = 0), and swapping the gate and up weights changes the
+    result (silu is not symmetric)."""
+    import math
+
+    gen = torch.Generator().manual_seed(11)
+    d, f, rows = 5, 7, 3
+    p = {
+        "m.gate_proj.weight": torch.randn(f, d, generator=gen, dtype=torch.float64),
+        "m.up_proj.weight": torch.randn(f, d, generator=gen, dtype=torch.float64),
+        "m.down_proj.weight": torch.randn(d, f, generator=gen, dtype=torch.float64),
+    }
+    x = torch.randn(rows, d, generator=gen, dtype=torch.float64)
+    got = MO.gated_mlp(p, "m.", x, mode="exact").double()
+    wg, wu, wd = (p[f"m.{n}_proj.weight"].tolist() for n in ("gate", "up", "down"))
+    for r in range(rows):
+        xr = x[r].tolist()
+        h = []
+        for j in range(f):
+            g = sum(wg[j][c] * xr[c] for c in range(d))
+            u = sum(wu[j][c] * xr[c] for c in range(d))
+            h.append(g / (1.0 + math.exp(-g)) * u)
+        for o in range(d):
+            want = sum(wd[o][j] * h[j] for j in range(f))
+            assert abs(got[r, o].item() - want) <= 1e-12 * (1 + abs(want))
+    zero_up = dict(p, **{"m.up_proj.weight": torch.zeros(f, d, dtype=torch.float64)})
+    assert torch.equal(MO.gated_mlp(zero_up, "m.", x, mode="exact").double(), torch.zeros(rows, d, dtype=torch.float64))
+    zero_gate = dict(p, **{"m.gate_proj.weight": torch.zeros(f, d, dtype=torch.float64)})
+    assert MO.gated_mlp(zero_gate, "m.", x, mode="exact").abs().max().item() == 0.0
+    swapped = dict(p, **{"m.gate_proj.weight": p["m.up_proj.weight"], "m.up_proj.weight": p["m.gate_proj.weight"]})
+    assert (MO.gated_mlp(swapped, "m.", x, mode="exact").double() - got).abs().max().item() > 1e-3
