@@ -806,7 +806,9 @@ __device__ __forceinline__ void segment_state_body(const PrefillParams& p, int b
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
         const GateRegs gr = finish_gates(gin, clock);
-        if (KEY && w == 0) {  // the sweeps read the key part's copy
+        // Both parts form the same clock and decay scan; the value part, whose
+        // chunks are shorter (no k_hat norm), writes them for the sweeps.
+        if (!KEY && w == 0) {
             p.lam[(size_t)bh * p.Tp + t0 + lane] = gr.lamr;
             p.gam[(size_t)bh * p.Tp + t0 + lane] = gr.gam;
         }
