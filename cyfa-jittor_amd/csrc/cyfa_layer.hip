@@ -149,9 +149,10 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
     __shared__ float sq[NORM ? 8 : 1][NORM ? TM : 1];
     __shared__ float4 snw[NORM ? LINEAR_NORM_MAX_K / 4 : 1];
     // The wave index comes from a scalar register, so the k-run bounds and
-    // every `s + u < s1` test are uniform branches. Under a lane-divergent
-    // test the compiler may leave an MFMA to run with an empty exec mask,
-    // which on gfx950 still accumulated the stale operand registers.
+    // every `s + u < s1` test are uniform branches. With a lane-divergent test
+    // the compiler left one MFMA of the fused-norm variant to run under an
+    // empty exec mask instead of branching around it, and outputs of that
+    // build picked up stale operand registers (NaNs on MI355X).
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lr = lane & 15,
               lg = lane >> 4;
     const int n0 = blockIdx.x * TN, m0 = blockIdx.y * TM;
