@@ -432,13 +432,14 @@ int launch_rms_norm(const NormParams& p, hipStream_t stream) {
 // columns of one interleaved group; the row norm needs each wave's k-steps in
 // one batch of loads (K <= 256 lin_batch). False when no shape qualifies.
 static bool linear_tile(int M, int N, bool swiglu, int norm_k, int& rt_out, int& ct_out) {
-    static const int shapes[][2] = {{4, 2}, {2, 4}, {4, 1}, {2, 2}, {1, 4}, {2, 1}, {1, 2}, {1, 1}};
+    static const int shapes[][2] = {{4, 4}, {4, 2}, {2, 4}, {4, 1}, {2, 2}, {1, 4}, {2, 1}, {1, 2}, {1, 1}};
     long long best = -1;
     rt_out = 4;
     ct_out = 2;
     for (const auto& sh : shapes) {
         const int rt = sh[0], ct = sh[1];
         if (swiglu && ct != 2) continue;
+        if (norm_k && rt * ct > 8) continue;  // no fused-norm build of the 64 x 64 tile (its registers would spill)
         if (norm_k > 256 * lin_batch(rt, ct)) continue;  // the norm needs all of a row in one batch
         const long long groups = (long long)((M + 16 * rt - 1) / (16 * rt)) * ((N + 16 * ct - 1) / (16 * ct));
         const long long cost = (groups + 255) / 256 * (rt + ct);
@@ -464,6 +465,10 @@ int launch_linear_rows(const LinearParams& p, hipStream_t stream) {
         else                                                                                                   \
             hipLaunchKernelGGL((linear_rows_kernel<RT_, CT_, false>), grid, block, 0, stream, p);             \
         return 0;                                                                                              \
+    }
+    if (rt == 4 && ct == 4 && !norm) {  // the lm_head's tile at 64 rows (N = 32000: 500 workgroups)
+        hipLaunchKernelGGL((linear_rows_kernel<4, 4, false>), grid, block, 0, stream, p);
+        return 0;
     }
     CYFA_LINEAR(4, 2)
     CYFA_LINEAR(2, 4)
