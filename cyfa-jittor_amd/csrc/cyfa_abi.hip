@@ -427,6 +427,16 @@ int cyfa_silu_mul(const void* gu, void* out, int rows, int F, void* hip_stream) 
     return check_launch("cyfa_silu_mul");
 }
 
+int cyfa_argmax_rows(const void* x, long long ldx, int rows, int n, long long* out, void* hip_stream) {
+    if (!x || !out || rows < 0 || n <= 0 || ldx < n || ldx % 8 != 0)
+        return fail(CYFA_ERR_VALUE, "cyfa_argmax_rows: rows=%d n=%d ldx=%lld", rows, n, ldx);
+    if (!aligned(x, 16) || !aligned(out, 8)) return fail(CYFA_ERR_ALIGN, "cyfa_argmax_rows: x needs 16-byte alignment");
+    if (rows == 0) return CYFA_OK;
+    if (cyfa::launch_argmax_rows((const __bf16*)x, ldx, rows, n, out, (hipStream_t)hip_stream) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_argmax_rows: launch refused");
+    return check_launch("cyfa_argmax_rows");
+}
+
 int cyfa_gates(const void* abd, long long abd_row, const float* dt_bias, const float* A_log, float* g, float* beta,
                float* delta, int rows, int H, void* hip_stream) {
     if (!abd || !dt_bias || !A_log || !g || !beta || !delta || rows < 0 || H <= 0 || abd_row < 3LL * H)

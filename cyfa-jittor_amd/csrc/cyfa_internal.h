@@ -153,6 +153,7 @@ int launch_rms_norm(const NormParams& p, hipStream_t stream);
 int launch_linear_rows(const LinearParams& p, hipStream_t stream);
 int launch_short_conv(const ConvParams& p, hipStream_t stream);
 int launch_silu_mul(const __bf16* gu, __bf16* out, int rows, int F, hipStream_t stream);
+int launch_argmax_rows(const __bf16* x, long long ldx, int rows, int n, long long* out, hipStream_t stream);
 int launch_gates(const __bf16* abd, long long abd_row, const float* dt_bias, const float* A_log, float* g, float* beta,
                  float* delta, int rows, int H, hipStream_t stream);
 

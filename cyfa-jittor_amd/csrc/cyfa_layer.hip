@@ -391,6 +391,74 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const bf16_t* gu, bf16_t*
     *reinterpret_cast<bf16x8*>(out + i8) = y;
 }
 
+// Row-wise argmax of bf16 logits with torch.argmax's result: the index of the
+// first maximum, NaN counting as larger than any number. One workgroup per row;
+// each thread keeps the best (value, index) of its strided elements, then the
+// workgroup reduces with the same order.
+__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
+    const bool vn = v != v, bn = bv != bv;
+    if (vn != bn) return vn;
+    if (!vn && v != bv) return v > bv;
+    return i < bi;
+}
+
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const bf16_t* x, long long ldx, int n, long long* out) {
+    constexpr int NT = 1024, DEPTH = 4;  // four 16-byte loads per thread in flight
+    const bf16_t* xr = x + (size_t)blockIdx.x * ldx;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int base = 0; base < n; base += 8 * NT * DEPTH) {
+        bf16x8 v[DEPTH];
+#pragma unroll
+        for (int d = 0; d < DEPTH; d++) {
+            const int i0 = base + 8 * (threadIdx.x + NT * d);
+            if (i0 + 8 <= n) v[d] = *reinterpret_cast<const bf16x8*>(xr + i0);
+        }
+#pragma unroll
+        for (int d = 0; d < DEPTH; d++) {
+            const int i0 = base + 8 * (threadIdx.x + NT * d);
+            if (i0 + 8 <= n) {
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    if (argmax_better((float)v[d][e], i0 + e, bv, bi)) {
+                        bv = (float)v[d][e];
+                        bi = i0 + e;
+                    }
+            } else {
+                for (int i = i0; i < n && i < i0 + 8; i++)
+                    if (argmax_better((float)xr[i], i, bv, bi)) {
+                        bv = (float)xr[i];
+                        bi = i;
+                    }
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (argmax_better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    __shared__ float sv[NT / 64];
+    __shared__ int si[NT / 64];
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < NT / 64; w++)
+            if (argmax_better(sv[w], si[w], bv, bi)) {
+                bv = sv[w];
+                bi = si[w];
+            }
+        out[blockIdx.x] = bi;
+    }
+}
+
 // Gate activations (layers/cyfa.py:323-326) from abd = [a | b | d] rows of 3H
 // bf16 (the b / d biases already added): g = -exp(A_log) softplus(a + dt_bias),
 // beta = sigmoid(b), delta = sigmoid(d), all fp32 [rows, H].
@@ -496,6 +564,11 @@ int launch_short_conv(const ConvParams& p, hipStream_t stream) {
 int launch_silu_mul(const bf16_t* gu, bf16_t* out, int rows, int F, hipStream_t stream) {
     const size_t n8 = (size_t)rows * F / 8;
     hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, stream, gu, out, rows, F);
+    return 0;
+}
+
+int launch_argmax_rows(const bf16_t* x, long long ldx, int rows, int n, long long* out, hipStream_t stream) {
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(1024), 0, stream, x, ldx, n, out);
     return 0;
 }
 

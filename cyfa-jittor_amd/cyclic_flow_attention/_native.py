@@ -128,6 +128,7 @@ SIGNATURES = {
     "cyfa_linear_rows": (_c_int, [ctypes.POINTER(CyfaLinearArgs), _c_void_p]),
     "cyfa_norm_linear_rows": (_c_int, [ctypes.POINTER(CyfaLinearArgs), ctypes.POINTER(CyfaRowNormArgs), _c_void_p]),
     "cyfa_silu_mul": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "cyfa_argmax_rows": (_c_int, [_c_void_p, ctypes.c_longlong, _c_int, _c_int, _c_void_p, _c_void_p]),
     "cyfa_gates": (_c_int, [_c_void_p, ctypes.c_longlong, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                             _c_int, _c_int, _c_void_p]),
     "cyfa_last_error": (ctypes.c_char_p, []),
@@ -425,6 +426,22 @@ def norm_linear(x, norm_weight, eps, weight, bias=None, residual=None, out_cols=
     for i in range(len(lead) - 2, -1, -1):
         strides.insert(0, strides[0] * lead[i + 1])
     return s, y.as_strided(lead + (out_w,), tuple(strides))
+
+
+def argmax_rows(x):
+    """x.argmax(-1) for a bf16 CUDA tensor [..., n] (the first maximum, NaN
+    largest, as torch.argmax), one cyfa_argmax_rows launch; int64 [...]."""
+    require_device(x)
+    if x.dtype != torch.bfloat16:
+        raise ValueError("argmax_rows: bf16 input expected")
+    n = x.shape[-1]
+    x2 = x.reshape(-1, n)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    out = torch.empty(x2.shape[0], dtype=torch.int64, device=x.device)
+    _check(load_library().cyfa_argmax_rows(x2.data_ptr(), x2.stride(0), x2.shape[0], n, out.data_ptr(),
+                                           stream_handle(x.device)), "cyfa_argmax_rows")
+    return out.view(x.shape[:-1])
 
 
 def interleave_gate_up(gate_weight, up_weight):

@@ -241,7 +241,8 @@ class GraphedDecodeStep:
                         if a.data_ptr() != b.data_ptr():
                             a.copy_(b)
                 self.logits = out["logits"]
-                self.tokens.copy_(out["logits"][:, -1:].argmax(-1))
+                last = out["logits"][:, -1:]
+                self.tokens.copy_(_native.argmax_rows(last) if inference_fast_path(last) else last.argmax(-1))
         finally:
             for attn in layers:
                 attn.decode_in_place = False

@@ -199,6 +199,12 @@ typedef struct CyfaNormArgs {
  * and the residual adds of CyFABlock.execute (modeling_cyfa.py:48-51). */
 int cyfa_rms_norm(const CyfaNormArgs *args, void *hip_stream);
 
+/* Row-wise argmax of bf16 rows x[r * ldx .. + n) into out[r] (int64), with
+ * torch.argmax's result: the index of the first maximum, NaN counting as the
+ * largest value. Replaces the greedy token choice of a decode step
+ * (logits.argmax, models/cyfa/modeling_cyfa.py:142-158; generation.py:43). */
+int cyfa_argmax_rows(const void *x, long long ldx, int rows, int n, long long *out, void *hip_stream);
+
 /* Arguments of one projection y = x W^T (+ bias) over at most 64 rows of x
  * (1 <= M <= 64; K a positive multiple of 32). With swiglu set (no bias, N a
  * multiple of 32), the rows of W come in groups of 32: 16 rows of the gate

@@ -446,3 +446,22 @@ def test_checkpoint_round_trip_and_seeded_sampling(tmp_path):
     assert first == second and len(first) == 4
     with pytest.raises(ValueError):
         generate(loaded, [32], 4, top_p=0.0)
+
+
+def test_argmax_rows_equals_torch_argmax():
+    """cyfa_argmax_rows gives torch.argmax's index: the first of tied maxima,
+    NaN largest, an all -inf row at 0, and rows that end off a multiple of 8."""
+    from cyclic_flow_attention import _native
+
+    gen = torch.Generator().manual_seed(9)
+    x = (torch.randint(-20, 20, (7, 32000), generator=gen) / 4).bfloat16()  # many ties
+    x[3, 12345] = float("nan")
+    x[4, 77] = float("nan")
+    x[4, 5] = float("nan")
+    x[5] = float("-inf")
+    xd = x.to(DEV)
+    got = _native.argmax_rows(xd)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), xd.argmax(-1).cpu())
+    y = torch.randn(5, 104, generator=gen).bfloat16().to(DEV)[:, :100]  # rows 104 apart, 100 wide
+    assert torch.equal(_native.argmax_rows(y).cpu(), y.argmax(-1).cpu())
