@@ -111,6 +111,9 @@ def test_layer_entry_points_validate_before_launch():
     c.W, c.split = 4, 12
     assert lib.cyfa_short_conv(ctypes.byref(c), None) == _native.CYFA_ERR_UNSUPPORTED
     assert lib.cyfa_silu_mul(None, None, 1, 8, None) == _native.CYFA_ERR_VALUE
+    assert lib.cyfa_argmax_rows(None, 8, 1, 8, None, None) == _native.CYFA_ERR_VALUE
+    assert lib.cyfa_argmax_rows(0x10000, 100, 1, 100, 0x20000, None) == _native.CYFA_ERR_VALUE  # ldx % 8
+    assert lib.cyfa_argmax_rows(0x10002, 104, 1, 100, 0x20000, None) == _native.CYFA_ERR_ALIGN
     assert lib.cyfa_gates(None, 12, None, None, None, None, None, 1, 4, None) == _native.CYFA_ERR_VALUE
     # the fused pre-norm: checked before anything is launched (the pointers are never dereferenced)
     a = _native.CyfaLinearArgs(M=4, N=64, K=4096, x=0x10000, ldx=4096, weight=0x20000, y=0x30000, ldy=64)
