@@ -157,6 +157,10 @@ int chunk_fwd(const CyfaChunkArgs* a, const CyfaOutNormArgs* on, void* hip_strea
     if (!a->q || !a->k || !a->v || !a->g || !a->delta || !a->beta || !a->table || !a->q_norm_weight ||
         !a->k_norm_weight || !a->o)
         return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd: null required pointer");
+    // The kernels address a sequence's rows with 32-bit byte offsets.
+    if ((size_t)a->T * a->H * a->K * 2 > cyfa::MAX_SPAN_BYTES)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_chunk_fwd: T * H * K * 2 = %zu bytes per sequence exceeds 2^32 - 1",
+                    (size_t)a->T * a->H * a->K * 2);
     if (!(a->scale > 0.f) || !isfinite(a->scale))
         return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd: scale must be positive and finite, got %g", (double)a->scale);
     const bool has_h0 = a->h0_k != nullptr;
@@ -223,6 +227,7 @@ int chunk_fwd(const CyfaChunkArgs* a, const CyfaOutNormArgs* on, void* hip_strea
     p.seg_exp = (int*)(base + ws.seg_exp);
     p.seg_decay = (float*)(base + ws.seg_decay);
     p.omega = (__bf16*)(base + ws.omega);
+    p.tab_exp = (int*)(base + ws.tab_exp);
     if (cyfa::launch_prefill(p, (hipStream_t)hip_stream) != 0)
         return fail(CYFA_ERR_UNSUPPORTED, "cyfa_chunk_fwd: launch refused");
     return check_launch(on ? "cyfa_chunk_fwd_normed" : "cyfa_chunk_fwd");
@@ -251,6 +256,15 @@ int cyfa_scalar_la(const CyfaSlaArgs* a, void* hip_stream) {
         return fail(CYFA_ERR_VALUE, "cyfa_scalar_la: B=%d H=%d must be positive and T=%d a positive multiple of 64",
                     a->B, a->H, a->T);
     if (!a->q || !a->k || !a->v || !a->g || !a->o) return fail(CYFA_ERR_VALUE, "cyfa_scalar_la: null required pointer");
+    {  // the kernels address a sequence's rows with 32-bit byte offsets
+        const size_t T = (size_t)a->T, osz = a->raw_output ? 4 : 2;
+        const size_t span_k = T * a->K * 2;
+        const size_t span_v = T * (a->v_bth ? a->H : 1) * a->V * 2;
+        const size_t span_o = T * (a->output_bth ? a->H : 1) * a->V * osz;
+        const size_t span = span_k > span_v ? (span_k > span_o ? span_k : span_o) : (span_v > span_o ? span_v : span_o);
+        if (span > cyfa::MAX_SPAN_BYTES)
+            return fail(CYFA_ERR_UNSUPPORTED, "cyfa_scalar_la: a sequence spans %zu bytes, above 2^32 - 1", span);
+    }
     if (!isfinite(a->scale)) return fail(CYFA_ERR_VALUE, "cyfa_scalar_la: scale must be finite, got %g", (double)a->scale);
     if (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16) || !aligned(a->o, 16))
         return fail(CYFA_ERR_ALIGN, "cyfa_scalar_la: q/k/v/o need 16-byte alignment");

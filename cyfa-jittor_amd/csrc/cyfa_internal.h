@@ -62,6 +62,7 @@ struct PrefillParams {
     int* seg_exp;      // [B*H, P-1, 2, 8] power-of-two exponent per (key / value part, wave)
     float* seg_decay;  // [B*H, P] product of alpha over each segment
     __bf16* omega;     // [B*H, Tp, 128] slot weights between the two passes
+    int* tab_exp;      // [B*H] power-of-two exponent e of the head's readout table: max |table| 2^-e < 2^14
 };
 
 // Isolated ScalarGatedLA, one pass (scalar_la): every operand read from memory.
@@ -115,9 +116,15 @@ struct ConvParams {
 };
 
 struct WorkspaceLayout {
-    size_t lam, gam, seg, seg_exp, seg_decay, omega, total;
+    size_t lam, gam, seg, seg_exp, seg_decay, omega, tab_exp, total;
 };
 
+// Largest byte span of one sequence's rows that the kernels' 32-bit buffer
+// offsets can address.
+constexpr size_t MAX_SPAN_BYTES = 0xffffffffull;
+
+// Compute units of the current device (256 when no device is visible).
+int device_cu_count();
 void choose_segments(int BH, int N, int* P, int* L);
 WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V);
 

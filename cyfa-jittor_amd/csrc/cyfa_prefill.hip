@@ -841,11 +841,43 @@ __device__ __forceinline__ void segment_state_body(const PrefillParams& p, int b
     if (KEY && tid == 0) p.seg_decay[bh * p.P + j] = exp2f(logdecay);
 }
 
+// Power-of-two exponent e of head h's readout table with max |table| 2^-e in
+// [2^13, 2^14) (0 for an all-zero or non-finite table): pass 1 stages the
+// table in fp16 as table 2^-e, so any finite table keeps fp16's full
+// precision and range.
+__device__ __forceinline__ void table_exponent(const PrefillParams& p, int h, int bh) {
+    __shared__ float part[8];
+    const int tid = threadIdx.x;
+    const float4* tb4 = reinterpret_cast<const float4*>(p.table + (size_t)h * kActive * kSlots);
+    constexpr int NQ = kActive * kSlots / 4;
+    float m = 0.f;
+    for (int i = tid; i < NQ; i += 512) {
+        const float4 t = tb4[i];
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
+    }
+    m = wave_max(m);
+    if ((tid & 63) == 0) part[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) {
+        float mx = part[0];
+#pragma unroll
+        for (int i = 1; i < 8; i++) mx = fmaxf(mx, part[i]);
+        int e = 0;
+        if (mx > 0.f && mx < INFINITY) {
+            frexpf(mx, &e);  // mx < 2^e
+            e -= 14;
+        }
+        p.tab_exp[bh] = e;
+    }
+    __syncthreads();
+}
+
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void segment_state_kernel(PrefillParams p) {
     __shared__ __align__(16) unsigned char smem[SG_LDS];
     const int z = blockIdx.z;
-    if (z == 2 * (p.P - 1)) {  // clock of the last segment
+    if (z == 2 * (p.P - 1)) {  // clock of the last segment and the table's exponent
         const SegCoord cd = seg_coord(p.H, p.P - 1);
+        table_exponent(p, cd.h, cd.bh);
         const int t_begin = (p.P - 1) * p.L * 64;
         clock_scan(p, cd.bh, cd.b, cd.h, t_begin, clock_before(p, cd.b, cd.h, cd.bh, t_begin));
         return;
@@ -925,17 +957,22 @@ __device__ __forceinline__ void load_start_state(const PrefillParams& p, int bh,
 // Slot readout of 16 tokens (ops/chunk_readout.py:797-909), fp16 MFMA with
 // fp32 accumulation; lane (lr, lg) works on token lr. The two 128-wide key
 // halves of the pass-1 output (bf16, rows RR apart) come from LDS, the table
-// (f16 [128][RS], row 127 zero) too.
-//   z_t = U(lam_t) (raw0_t + raw1_t)                 (B operand, registers)
+// (f16 [128][RS], row 127 zero, staged as table 2^-et) too.
+//   z_t = U(lam_t) (raw0_t + raw1_t) 2^-ez_t          (B operand, registers)
 //   L^T[r][t] = table[r] . z_t                       (C rows r = 16 rb + 4 lg + i)
-//   p_t = softmax over r < 127 of L^T[:, t]          (in registers + 2 shuffles)
+//   p_t = softmax over r < 127 of L^T[:, t] 2^(et + ez_t)
+//                                                    (in registers + 2 shuffles)
 //   u^T[m][t] = sum_r table[r][m] p_t[r]             (p_t as the B operand straight
 //                                                     from the C layout)
-//   weights_t = bf16(U(-lam_t) u_t)                  (four consecutive m per store)
+//   weights_t = bf16(U(-lam_t) u_t 2^et)             (four consecutive m per store)
+// ez_t is a power of two per token with max |z_t| 2^-ez_t < 2^15, so the fp16
+// operand never overflows however large the pass-1 output grows (coherent
+// keys over long contexts); the scales are undone on the fp32 logits and on
+// the weights, and powers of two commute with every rounding in between.
 constexpr int RR = 128 + 8;  // row stride of the pass-1 output tiles in LDS
 
 __device__ __forceinline__ void readout_tokens(const bf16_t* sR0, const bf16_t* sR1, const f16_t* sTab, float lamr,
-                                               bf16_t* dst) {
+                                               float tab_scale, bf16_t* dst) {
     const int lane = threadIdx.x & 63, lr = lane & 15, lg = lane >> 4;
     // Phases: the hardware gives (cos, sin) of pairs 1, 8, 16 and of the
     // lane's first pair of each group; the others follow by rotation (complex
@@ -946,21 +983,44 @@ __device__ __forceinline__ void readout_tokens(const bf16_t* sR0, const bf16_t* 
     pair_sincos(lamr, 16, s16, c16);
     float zs[4], zc[4];  // pairs 4 lg + q, then 16 ks + 4 lg + q
     pair_sincos(lamr, 4 * lg, zs[0], zc[0]);
-#pragma unroll
-    for (int q = 1; q < 4; q++) {
-        zc[q] = zc[q - 1] * c1 - zs[q - 1] * s1;
-        zs[q] = zs[q - 1] * c1 + zc[q - 1] * s1;
-    }
-    // z fragments: element j = z_t[32 ks + 8 lg + j].
-    f16x8 zf[4];
+    // raw0 + raw1, element 2 q (+1) of fragment ks = coordinate 32 ks + 8 lg + 2 q (+1)
+    float re[4][4], ro[4][4];
+    float m = 0.f;
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
         const bf16x8 ra = *reinterpret_cast<const bf16x8*>(sR0 + lr * RR + 32 * ks + 8 * lg);
         const bf16x8 rb = *reinterpret_cast<const bf16x8*>(sR1 + lr * RR + 32 * ks + 8 * lg);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const float e = (float)ra[2 * q] + (float)rb[2 * q];
-            const float o = (float)ra[2 * q + 1] + (float)rb[2 * q + 1];
+            re[ks][q] = (float)ra[2 * q] + (float)rb[2 * q];
+            ro[ks][q] = (float)ra[2 * q + 1] + (float)rb[2 * q + 1];
+            m = fmaxf(m, fmaxf(fabsf(re[ks][q]), fabsf(ro[ks][q])));
+        }
+    }
+    // The token's largest raw coordinate (its 128 values are spread over the
+    // four row groups); a rotated pair is at most sqrt(2) times larger.
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    int ez = 0;
+    if (m > 0.f && m < INFINITY) {
+        frexpf(m, &ez);  // m < 2^ez
+        ez -= 14;
+    }
+    const float zscale = ldexpf(1.f, -ez);
+    zs[0] *= zscale;
+    zc[0] *= zscale;
+#pragma unroll
+    for (int q = 1; q < 4; q++) {
+        zc[q] = zc[q - 1] * c1 - zs[q - 1] * s1;
+        zs[q] = zs[q - 1] * c1 + zc[q - 1] * s1;
+    }
+    // z fragments: element j = z_t[32 ks + 8 lg + j] 2^-ez.
+    f16x8 zf[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float e = re[ks][q], o = ro[ks][q];
             const float sn = zs[q], cs = zc[q];
             zf[ks][2 * q] = (f16_t)(cs * e - sn * o);
             zf[ks][2 * q + 1] = (f16_t)(sn * e + cs * o);
@@ -989,12 +1049,14 @@ __device__ __forceinline__ void readout_tokens(const bf16_t* sR0, const bf16_t* 
         for (int i = 0; i < 4; i++) mx = fmaxf(mx, L[rb8][i]);
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
+    // e^(logit - max) with logit = L 2^(et + ez): one exponential per slot
+    const float lsc = kLog2e * tab_scale * ldexpf(1.f, ez);
     float sum = 0.f;
 #pragma unroll
     for (int rb8 = 0; rb8 < 8; rb8++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            L[rb8][i] = __expf(L[rb8][i] - mx);
+            L[rb8][i] = fast_exp2((L[rb8][i] - mx) * lsc);
             sum += L[rb8][i];
         }
     sum += __shfl_xor(sum, 16);
@@ -1018,10 +1080,12 @@ __device__ __forceinline__ void readout_tokens(const bf16_t* sR0, const bf16_t* 
         for (int mb = 0; mb < 8; mb++) U[mb] = mfma_f16(load_tr_pair_f16(sTab, RS, 32 * ks, 16 * mb), pf[ks], U[mb]);
         sched_fence();
     }
-    // Lane holds u_t[16 mb + 4 lg + i]: pairs 8 mb + 2 lg + q, q = 0, 1.
+    // Lane holds u_t[16 mb + 4 lg + i] 2^-et: pairs 8 mb + 2 lg + q, q = 0, 1.
     float s8, c8, ws[2], wc[2];
     pair_sincos(lamr, 8, s8, c8);
     pair_sincos(lamr, 2 * lg, ws[0], wc[0]);
+    ws[0] *= tab_scale;
+    wc[0] *= tab_scale;
     wc[1] = wc[0] * c1 - ws[0] * s1;
     ws[1] = ws[0] * c1 + wc[0] * s1;
 #pragma unroll
@@ -1102,8 +1166,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         issue_rows_q(sq, sq.k, p.T, n0 * 64, u, kraw);
         gr = issue_gates(sq, p.T, n0 * 64);
     }
+    // The table goes to LDS in fp16 as table 2^-et (et from segment_state:
+    // max |table| 2^-et < 2^14); the readout undoes the factor.
+    const int et = p.tab_exp[bh];
+    const float tab_scale = ldexpf(1.f, et);
     {
         const float* tb = p.table + (size_t)h * kActive * kSlots;
+        const float ts = ldexpf(1.f, -et);
         float4 tv[8];
 #pragma unroll
         for (int it = 0; it < 8; it++) {
@@ -1114,7 +1183,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         for (int it = 0; it < 8; it++) {
             const int idx = tid + 512 * it, r = idx >> 5, m4 = (idx & 31) * 4;
             *reinterpret_cast<f16x4*>(sTab + r * RS + m4) =
-                f16x4{(f16_t)tv[it].x, (f16_t)tv[it].y, (f16_t)tv[it].z, (f16_t)tv[it].w};
+                f16x4{(f16_t)(tv[it].x * ts), (f16_t)(tv[it].y * ts), (f16_t)(tv[it].z * ts), (f16_t)(tv[it].w * ts)};
         }
     }
     zero_scores(sP, 2);  // the two blocks above the diagonal that the intra product reads stay zero
@@ -1222,7 +1291,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         __syncthreads();  // output tiles complete; k_hat, w and the gates of this chunk are done with
         if (y == 0) {
             // Slot readout of the chunk: wave mq takes tokens 16 mq .. 16 mq + 15.
-            readout_tokens(sR0 + 16 * mq * RR, sR1 + 16 * mq * RR, sTab, lamr,
+            readout_tokens(sR0 + 16 * mq * RR, sR1 + 16 * mq * RR, sTab, lamr, tab_scale,
                            p.omega + ((size_t)bh * p.Tp + t0 + 16 * mq + lr) * kSlots);
         } else if (n + 1 < n1) {
             // The readout outlasts these loads; their latency is hidden behind it.
@@ -1310,13 +1379,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
         // NORM: this chunk's gate for the lane's output coordinates, issued
         // before the next chunk's loads, so that waiting for it in the
         // epilogue does not wait for them (loads complete in order).
+        // Rows past T are clamped to T - 1 inside the per-lane offset: the
+        // buffer's range check covers the lane offset only, not the scalar
+        // offset, so a row index never goes into the scalar offset of a load.
         bf16x4 gate[4][2];
         if constexpr (NORM) {
             const rsrc_t rg = rows_rsrc(p, b, h, p.on_gate);
 #pragma unroll
-            for (int tb = 0; tb < 4; tb++)
+            for (int tb = 0; tb < 4; tb++) {
+                const int tg = min(t0 + 16 * tb + lr, p.T - 1);
+                const uint32_t off = (uint32_t)tg * sq.row16 + 2 * (32 * w + 4 * lg);
 #pragma unroll
-                for (int c = 0; c < 2; c++) gate[tb][c] = ld_b64(rg, o_lane + 32 * c, (uint32_t)(t0 + 16 * tb) * sq.row16);
+                for (int c = 0; c < 2; c++) gate[tb][c] = ld_b64(rg, off + 32 * c, 0);
+            }
         }
         // The next chunk's loads are spread over the phases (see pass 1).
         if (n + 1 < n1) issue_omega(rom, t0 + 64, om);
@@ -1905,10 +1980,30 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
 
 }  // namespace
 
+int device_cu_count() {
+    constexpr int kMaxDevices = 64;
+    static int cached[kMaxDevices];  // 0 = not queried yet; every writer stores the same value
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();  // no device: clear the error, use the MI355X count
+        return 256;
+    }
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+            (void)hipGetLastError();
+            n = 256;
+        }
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 void choose_segments(int BH, int N, int* P, int* L) {
-    // One sweep workgroup per segment: aim for one workgroup per CU (256 CUs).
+    // One sweep workgroup per segment: aim for one workgroup per CU.
     // CYFA_SEGMENT_CHUNKS=<L> fixes the chunks per segment (tests, tuning).
-    int target = (256 + BH - 1) / BH;
+    const int cus = device_cu_count();
+    int target = (cus + BH - 1) / BH;
     if (target < 1) target = 1;
     if (target > N) target = N;
     int l = (N + target - 1) / target;
@@ -1936,7 +2031,8 @@ WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V) {
     w.seg_exp = align256(w.seg + nseg * (size_t)(K * kSlots + kSlots * V) * sizeof(_Float16));
     w.seg_decay = align256(w.seg_exp + nseg * 16 * sizeof(int));
     w.omega = align256(w.seg_decay + BH * P * sizeof(float));
-    w.total = align256(w.omega + BH * Tp * kSlots * 2);
+    w.tab_exp = align256(w.omega + BH * Tp * kSlots * 2);
+    w.total = align256(w.tab_exp + BH * sizeof(int));
     return w;
 }
 

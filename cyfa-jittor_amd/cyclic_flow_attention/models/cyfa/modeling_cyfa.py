@@ -139,6 +139,22 @@ class CyclicFlowAttentionForCausalLM(nn.Module):
         if config.tie_word_embeddings:
             self.lm_head.weight = self.model.embeddings.weight
 
+    @classmethod
+    def from_pretrained(cls, path):
+        """The bf16 model of a local checkpoint directory (config.json and
+        *.safetensors, loaded strictly; models/cyfa/modeling_cyfa.py:85-89)."""
+        from ...utils import load_model
+
+        return load_model(path)[0]
+
+    def save_pretrained(self, directory, tokenizer=None):
+        """config.json and model.safetensors under ``directory`` (and the
+        tokenizer's files and special-token ids when one is given;
+        models/cyfa/modeling_cyfa.py:91-94)."""
+        from ...utils import save_model
+
+        save_model(self, directory, tokenizer)
+
     def forward(self, input_ids, labels=None, cache=None, use_cache=False, attention_mask=None):
         # The final norm stays a launch of its own: inside the lm_head
         # projection each of its 1000 workgroups would normalise the rows again

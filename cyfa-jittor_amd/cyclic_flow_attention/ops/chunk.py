@@ -11,7 +11,7 @@ scope here, so gradients raise.
 import torch
 
 from .. import _native
-from .utils import check_forward_only, readout_table
+from .utils import check_forward_only, check_table, readout_table
 
 
 def chunk_cyfa(
@@ -66,16 +66,15 @@ def chunk_cyfa(
     for name, x in (("q", q), ("k", k), ("v", v)):
         if x.dtype != torch.bfloat16:
             raise NotImplementedError(f"the HIP prefill computes in bfloat16; {name} is {x.dtype}")
-    dev = _native.require_device(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, *state_in)
+    dev = _native.require_device(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, table, *state_in)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     g, delta, beta = (x.to(torch.float32).contiguous() for x in (g, delta, beta))
     qw = q_norm_weight.to(torch.float32).contiguous()
     kw = k_norm_weight.to(torch.float32).contiguous()
     if table is None:
         table = readout_table(readout)
-    elif tuple(table.shape) != (H, M - 1, M) or table.dtype != torch.float32:
-        raise ValueError(f"table must be float32 [{H}, {M - 1}, {M}], got {tuple(table.shape)} {table.dtype}")
-    table = table.contiguous()
+    else:
+        check_table(table, H, M)
     if initial_state is not None:
         h0k, h0v, c0 = (x.to(torch.float32).contiguous() for x in initial_state)
         if tuple(h0k.shape) != (B, H, K, M) or tuple(h0v.shape) != (B, H, M, V) or tuple(c0.shape) != (B, H):
@@ -90,7 +89,7 @@ def chunk_cyfa(
     else:
         hk = hv = clock = None
     ws_bytes = _native.chunk_workspace_bytes(B, T, H, K, V, M, chunk_size)
-    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)  # alive until the launch
     args = _native.CyfaChunkArgs(
         B=B, T=T, H=H, K=K, V=V, M=M, C=chunk_size,
         q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(),
@@ -100,7 +99,7 @@ def chunk_cyfa(
         scale=float(K**-0.5 if scale is None else scale),
         h0_k=_native.ptr(h0k), h0_v=_native.ptr(h0v), clock0=_native.ptr(c0),
         o=o.data_ptr(), hk=_native.ptr(hk), hv=_native.ptr(hv), clock=_native.ptr(clock),
-        workspace=workspace.data_ptr(), workspace_bytes=ws_bytes,
+        workspace=_native.ptr(workspace), workspace_bytes=ws_bytes,
     )
     if output_norm is None:
         _native.chunk_fwd(args, dev)

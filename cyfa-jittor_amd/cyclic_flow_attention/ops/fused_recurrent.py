@@ -8,7 +8,7 @@ fused HBM-streaming kernel, ``cyfa_decode_step`` of libcyfa_hip.so.
 import torch
 
 from .. import _native
-from .utils import readout_table
+from .utils import check_table, readout_table
 
 
 def fused_recurrent_cyfa(
@@ -55,13 +55,16 @@ def fused_recurrent_cyfa(
     for name, x in (("q", q), ("k", k), ("v", v)):
         if x.dtype != torch.bfloat16:
             raise NotImplementedError(f"the HIP decode step computes in bfloat16; {name} is {x.dtype}")
-    dev = _native.require_device(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight)
+    state_in = tuple(initial_state) if initial_state is not None else ()
+    dev = _native.require_device(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, table, *state_in)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     g, delta, beta = (x.to(torch.float32).contiguous() for x in (g, delta, beta))
     qw = q_norm_weight.to(torch.float32).contiguous()
     kw = k_norm_weight.to(torch.float32).contiguous()
     if table is None:
         table = readout_table(readout)
+    else:
+        check_table(table, H, M)
     if initial_state is not None:
         hk_in, hv_in, c_in = initial_state
         if tuple(hk_in.shape) != (B, H, K, M) or tuple(hv_in.shape) != (B, H, M, V) or tuple(c_in.shape) != (B, H):
@@ -110,10 +113,23 @@ def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias
     """
     B = qkv.shape[0]
     H, K, V, M = num_heads, 256, 256, table.shape[-1]
-    dev = _native.require_device(qkv, conv_cache_out, conv_weight, abd, gate, table)
+    state_in = tuple(initial_state) if initial_state is not None else ()
+    dev = _native.require_device(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias, A_log, gate, norm_weight,
+                                 table, q_norm_weight, k_norm_weight, *state_in)
     D = 2 * H * K + H * V
     if qkv.shape[-1] != D or qkv.stride(-1) != 1 or conv_weight.shape != (D, 4) or not conv_weight.is_contiguous():
         raise ValueError("decode_layer_step: qkv must have 3 H 256 unit-stride columns and conv_weight [3 H 256, 4]")
+    for name, x in (("qkv", qkv), ("abd", abd), ("gate", gate), ("conv_weight", conv_weight),
+                    ("conv_cache_out", conv_cache_out)):
+        if x.dtype != torch.bfloat16 or x.stride(-1) != 1:
+            raise ValueError(f"decode_layer_step: {name} must be bfloat16 with unit last-dim stride")
+    if abd.shape[-1] != 3 * H or gate.shape[-1] != H * V:
+        raise ValueError(f"decode_layer_step: abd needs {3 * H} and gate {H * V} columns")
+    if conv_cache_out.dim() != 3 or tuple(conv_cache_out.shape) != (B, 3, D):
+        raise ValueError(f"decode_layer_step: conv_cache_out must be [{B}, 3, {D}]")
+    check_table(table, H, M)
+    if conv_cache is not None and (conv_cache.dtype != torch.bfloat16 or conv_cache.shape != conv_cache_out.shape):
+        raise ValueError("decode_layer_step: conv_cache must be bfloat16 of conv_cache_out's shape")
     if conv_cache is not None and conv_cache.stride() != conv_cache_out.stride():
         raise ValueError("decode_layer_step: conv_cache and conv_cache_out must share their layout")
     qw = q_norm_weight.to(torch.float32).contiguous()
@@ -123,6 +139,8 @@ def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias
     nw = norm_weight.detach().to(torch.float32).contiguous()
     if initial_state is not None:
         hk_in, hv_in, c_in = initial_state
+        if tuple(hk_in.shape) != (B, H, K, M) or tuple(hv_in.shape) != (B, H, M, V) or tuple(c_in.shape) != (B, H):
+            raise ValueError("initial_state must be (hk [B,H,K,M], hv [B,H,M,V], clock [B,H])")
         if inplace:
             for x in (hk_in, hv_in, c_in):
                 if x.dtype != torch.float32 or not x.is_contiguous():

@@ -17,3 +17,11 @@ def check_forward_only(name, tensors):
 def readout_table(readout):
     """table = readout @ Phi, [H, M-1, M] fp32 (ops/chunk.py:82-103, 281)."""
     return _native.readout_table(readout)
+
+
+def check_table(table, H, M):
+    """A precomputed readout table must be contiguous float32 [H, M-1, M]."""
+    if tuple(table.shape) != (H, M - 1, M) or table.dtype != torch.float32 or not table.is_contiguous():
+        raise ValueError(
+            f"table must be contiguous float32 [{H}, {M - 1}, {M}], got {tuple(table.shape)} {table.dtype}"
+        )

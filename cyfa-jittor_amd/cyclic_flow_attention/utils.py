@@ -155,16 +155,22 @@ def save_safetensors(tensors, path):
     os.replace(tmp, path)
 
 
-def save_model(model, directory):
+def save_model(model, directory, tokenizer=None):
     """config.json (the config fields plus model_type and architectures) and
     model.safetensors with the torch-checkpoint parameter names
-    (utils.py:163-177)."""
+    (utils.py:163-177). With a tokenizer, config.json also records its
+    ``eos_id`` / ``bos_id`` as eos_token_id / bos_token_id and the
+    tokenizer writes its own files into the directory (``tokenizer.save``)."""
     directory = Path(directory)
     directory.mkdir(parents=True, exist_ok=True)
     config = dataclasses.asdict(model.config)
     config.update(model_type="cyclic_flow_attention", architectures=["CyclicFlowAttentionForCausalLM"])
+    if tokenizer is not None:
+        config.update(eos_token_id=tokenizer.eos_id, bos_token_id=tokenizer.bos_id)
     (directory / "config.json").write_text(json.dumps(config, indent=2) + "\n")
     save_safetensors(model.state_dict(), directory / "model.safetensors")
+    if tokenizer is not None:
+        tokenizer.save(directory)
 
 
 def load_model(path):

@@ -83,6 +83,27 @@ def short_conv(x, weight, bias=None, cache=None, lengths=None, mode="exact"):
     return _cast(y, mode), new_cache
 
 
+def gate_activations(a, b, d, dt_bias, A_log, mode="exact"):
+    """Gate activations of layers/cyfa.py:323-326 from the three projections
+    (a, b, d: [..., H], the b and d biases included):
+    g = -exp(A_log) softplus(a + dt_bias) (natural log of the decay),
+    beta = sigmoid(b), delta = sigmoid(d). Returns (g, beta, delta)."""
+    dt = _dt(mode)
+    g = -torch.exp(A_log.to(dt)) * torch.nn.functional.softplus(a.to(dt) + dt_bias.to(dt))
+    return g, torch.sigmoid(b.to(dt)), torch.sigmoid(d.to(dt))
+
+
+def layer_gates(p, pre, xin, mode="exact"):
+    """(g, delta, beta) of the layer for the normed input xin: the a, b and d
+    projections (layers/cyfa.py:323-326; a_proj has no bias, b_proj and
+    d_proj have one) through gate_activations."""
+    a = linear(xin, p[pre + "a_proj.weight"], mode=mode)
+    b = linear(xin, p[pre + "b_proj.weight"], p[pre + "b_proj.bias"], mode)
+    d = linear(xin, p[pre + "d_proj.weight"], p[pre + "d_proj.bias"], mode)
+    g, beta, delta = gate_activations(a, b, d, p[pre + "dt_bias"], p[pre + "A_log"], mode)
+    return g, delta, beta
+
+
 def attention_layer(p, pre, x, cfg, cache=None, use_cache=False, attention_mask=None, mode="exact",
                     chunk_size=64, op_mode=None, cast_output=True):
     """CyclicFlowAttention.execute (layers/cyfa.py:299-357).
@@ -116,10 +137,7 @@ def attention_layer(p, pre, x, cfg, cache=None, use_cache=False, attention_mask=
     q = q.reshape(B, T, H, Dk)
     k = k.reshape(B, T, H, Dk)
     v = v.reshape(B, T, H, Dv)
-    a = linear(xin, p[pre + "a_proj.weight"], mode=mode).to(dt) + p[pre + "dt_bias"].to(dt)
-    g = -torch.exp(p[pre + "A_log"].to(dt)) * torch.nn.functional.softplus(a)
-    delta = torch.sigmoid(linear(xin, p[pre + "d_proj.weight"], p[pre + "d_proj.bias"], mode).to(dt))
-    beta = torch.sigmoid(linear(xin, p[pre + "b_proj.weight"], p[pre + "b_proj.bias"], mode).to(dt))
+    g, delta, beta = layer_gates(p, pre, xin, mode)
     if attention_mask is not None:
         valid = attention_mask.to(torch.bool)[..., None]
         zero = torch.zeros((), dtype=dt)

@@ -148,3 +148,48 @@ def test_scalar_la_validates_before_launch():
         scalar_la(q, q, torch.zeros(1, 1, 32, 256, dtype=torch.bfloat16), g, None)  # v shape
     with pytest.raises(NotImplementedError):
         scalar_la(q, q, torch.zeros(1, 1, 64, 256), g, None)  # fp32 v
+
+
+def test_sequence_spans_beyond_32_bit_offsets_are_refused():
+    """The kernels address one sequence's rows with 32-bit byte offsets, so
+    calls whose per-sequence span reaches 2^32 bytes return
+    CYFA_ERR_UNSUPPORTED before anything is launched (the pointers are never
+    dereferenced)."""
+    lib = _native.load_library()
+    ptrs = dict(q=0x10000, k=0x20000, v=0x30000, g=0x40000, delta=0x50000, beta=0x60000, table=0x70000,
+                q_norm_weight=0x80000, k_norm_weight=0x90000, o=0xa0000)
+    # T * H * 512 = 2^32 exactly: one byte past the largest offset
+    args = _native.CyfaChunkArgs(B=1, T=1 << 21, H=4, K=256, V=256, M=128, C=64, scale=0.0625, **ptrs)
+    assert lib.cyfa_chunk_fwd(ctypes.byref(args), None) == _native.CYFA_ERR_UNSUPPORTED
+    assert b"2^32" in lib.cyfa_last_error()
+    args.T = (1 << 21) - 1  # below the limit: passes the span check, then fails on the missing workspace
+    assert lib.cyfa_chunk_fwd(ctypes.byref(args), None) == _native.CYFA_ERR_WORKSPACE
+    s = _native.CyfaSlaArgs(B=1, T=1 << 16, H=128, K=128, V=256, q=0x10000, k=0x20000, v=0x30000, g=0x40000,
+                            o=0x50000, scale=1.0, v_bth=1)
+    assert lib.cyfa_scalar_la(ctypes.byref(s), None) == _native.CYFA_ERR_UNSUPPORTED  # v rows span 2^32 bytes
+    s.v_bth = 0
+    assert lib.cyfa_scalar_la(ctypes.byref(s), None) == _native.CYFA_ERR_WORKSPACE
+    s.output_bth, s.raw_output = 1, 1
+    assert lib.cyfa_scalar_la(ctypes.byref(s), None) == _native.CYFA_ERR_UNSUPPORTED  # f32 o rows: 2^33 bytes
+
+
+def test_decode_wrappers_check_every_tensor_before_launch():
+    """Every tensor argument of the decode wrappers is checked for its device
+    before any launch (CPU tensors raise ValueError), and a precomputed table
+    must be float32 [H, M-1, M]."""
+    from cyclic_flow_attention.ops import fused_recurrent_cyfa
+    from cyclic_flow_attention.ops.utils import check_table
+
+    q = torch.zeros(1, 1, 1, 256, dtype=torch.bfloat16)
+    g = torch.zeros(1, 1, 1)
+    ro = torch.eye(127)[None]
+    w = torch.ones(256)
+    state = (torch.zeros(1, 1, 256, 128), torch.zeros(1, 1, 128, 256), torch.zeros(1, 1))
+    with pytest.raises(ValueError):
+        fused_recurrent_cyfa(q, q, q, g, g, g, ro, w, w, initial_state=state)
+    with pytest.raises(ValueError):
+        check_table(torch.zeros(1, 127, 128, dtype=torch.bfloat16), 1, 128)
+    with pytest.raises(ValueError):
+        check_table(torch.zeros(2, 127, 128), 1, 128)
+    check_table(torch.zeros(1, 127, 128), 1, 128)
+

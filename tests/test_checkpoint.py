@@ -92,3 +92,31 @@ def test_load_checkpoint_errors_like_the_reference(tmp_path):
         load_checkpoint(model, tmp_path)  # shape mismatch
     with pytest.raises(FileNotFoundError):
         load_model(tmp_path / "absent")
+
+
+def test_causal_lm_from_pretrained_and_save_pretrained(tmp_path):
+    """The reference's model-class API (models/cyfa/modeling_cyfa.py:85-94):
+    save_pretrained writes the checkpoint directory, from_pretrained loads it
+    back bit for bit; a tokenizer adds its special-token ids to config.json
+    and saves its own files."""
+    from cyclic_flow_attention.models.cyfa import CyclicFlowAttentionForCausalLM
+
+    class _Tok:
+        eos_id, bos_id = 2, 1
+
+        def save(self, directory):
+            (directory / "tokenizer.model").write_bytes(b"tok")
+
+    model = _tiny()
+    model.save_pretrained(tmp_path / "a")
+    loaded = CyclicFlowAttentionForCausalLM.from_pretrained(tmp_path / "a")
+    assert isinstance(loaded, CyclicFlowAttentionForCausalLM)
+    for name, value in model.state_dict().items():
+        other = loaded.state_dict()[name]
+        assert other.dtype == value.dtype and torch.equal(other.float(), value.float()), name
+    model.save_pretrained(tmp_path / "b", tokenizer=_Tok())
+    cfg = json.loads((tmp_path / "b" / "config.json").read_text())
+    assert (cfg["eos_token_id"], cfg["bos_token_id"]) == (2, 1)
+    assert (tmp_path / "b" / "tokenizer.model").read_bytes() == b"tok"
+    with pytest.raises(FileNotFoundError):
+        CyclicFlowAttentionForCausalLM.from_pretrained(tmp_path / "missing")

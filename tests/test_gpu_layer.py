@@ -90,10 +90,11 @@ def test_silu_mul_and_gate_kernels():
     A_log = torch.randn(H, generator=gen)
     gg, beta, delta = (t.cpu().double() for t in _native.gates(abd.to(DEV), dt_bias.to(DEV), A_log.to(DEV)))
     a = abd.double()
-    ref_g = -torch.exp(A_log.double()) * F.softplus(a[..., :H] + dt_bias.double())
+    ref_g, ref_beta, ref_delta = MO.gate_activations(a[..., :H], a[..., H:2 * H], a[..., 2 * H:], dt_bias.double(),
+                                                     A_log.double())
     torch.testing.assert_close(gg, ref_g, rtol=1e-5, atol=1e-6)
-    torch.testing.assert_close(beta, torch.sigmoid(a[..., H:2 * H]), rtol=1e-5, atol=1e-6)
-    torch.testing.assert_close(delta, torch.sigmoid(a[..., 2 * H:]), rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(beta, ref_beta, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(delta, ref_delta, rtol=1e-5, atol=1e-6)
 
 
 def _layer(hidden=1024, H=4, seed=0):
@@ -209,6 +210,7 @@ def test_greedy_tokens_match_oracle(name, layers, prompt):
                                      op_mode="exact")
         last = logits[0, -1]
     print(f"{name}: {64 - ties} of 64 greedy tokens equal the oracle's argmax, {ties} near-ties")
+    assert ties <= 16, f"{ties} of 64 steps were near-ties"
 
 
 @pytest.mark.parametrize("name,layers,B", [("tiny.json", None, 2), ("cyclic_flow_attention_400m.json", 2, 4)])
@@ -341,7 +343,7 @@ def test_norm_linear_rows(M, residual, swiglu, K):
     assert rows <= max(1, M // 10), f"{rows} of {M} rows differ from rms_norm + linear"
 
 
-@pytest.mark.parametrize("B,state,inplace", [(3, True, False), (2, False, False), (4, True, True)])
+@pytest.mark.parametrize("B,state,inplace", [(3, True, False), (2, False, False), (4, True, True), (64, True, True)])
 def test_decode_layer_step_equals_separate_kernels(B, state, inplace):
     """cyfa_decode_layer_step (short convolution, gates, decode op and gated
     output norm in one kernel) against the four separate kernels on the same

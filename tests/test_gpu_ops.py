@@ -73,7 +73,8 @@ def test_readout_table_matches_oracle():
 
 
 @pytest.mark.parametrize("B,H,K,V,state", [(3, 2, 256, 256, True), (2, 4, 256, 256, False),
-                                           (1, 1, 128, 128, True), (2, 2, 256, 128, True)])
+                                           (1, 1, 128, 128, True), (2, 2, 256, 128, True),
+                                           (64, 4, 256, 256, True)])  # configuration 4: 256 workgroups
 def test_decode_step_matches_oracle(B, H, K, V, state):
     from cyclic_flow_attention.ops import fused_recurrent_cyfa
 
@@ -113,6 +114,7 @@ CHUNK_CASES = [
     (1, 512, 2, True, "3"),      # segments of 3 chunks, last one shorter
     (2, 512, 2, True, "100"),    # one segment: no segment-state kernel
     (16, 1024, 4, False, None),  # 64 sequences, 4 chunks per segment
+    (8, 2048, 4, True, None),    # configuration 3's attention shape: 8 segments of 4 chunks
 ]
 
 
@@ -290,3 +292,57 @@ def test_config5_long_carry_prefill_then_decode():
         rst = rst_next
     assert_close(torch.cat(outs, 1), torch.cat(routs, 1), what="config 5 decode o")
     _check_states(st, rst, "config 5")
+
+
+def test_readout_range_guard_coherent_long_context():
+    """Coherent q/k, alpha ~ 1 and a slowly moving clock over 16384 tokens
+    drive the pass-1 output past the fp16 range for about two thirds of the
+    tokens (tests/coherent_inputs.py; a CPU test checks that). The fused
+    readout scales z per token and the table per head by powers of two, so the
+    prefill stays finite and matches the oracle; a decode step continuing from
+    its states (fp32 readout) agrees as well. The table's entries (~1e-4) sit
+    at the edge of the fp16 normal range, which the per-head table scale
+    covers. Outputs are compared relative to their RMS (they grow with T);
+    the max-abs bound is the larger of the north-star 2e-2 and 1.5x the
+    reference's own bf16 rounding (oracle mirror mode) on the same inputs
+    (~0.057 of the RMS here)."""
+    from cyclic_flow_attention.ops import chunk_cyfa, fused_recurrent_cyfa
+
+    from coherent_inputs import coherent_inputs
+
+    T = 16384
+    x = coherent_inputs(T=T + 1)
+    seq = ("q", "k", "v", "g", "delta", "beta")
+    pre = {n: (t[:, :T] if n in seq else t) for n, t in x.items()}
+    last = {n: (t[:, T:] if n in seq else t) for n, t in x.items()}
+    with torch.no_grad():
+        o, st = chunk_cyfa(**{n: t.to(DEV) for n, t in pre.items()}, output_final_state=True)
+        od, _ = fused_recurrent_cyfa(**{n: t.to(DEV) for n, t in last.items()}, initial_state=st,
+                                     output_final_state=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o.float()).all() and torch.isfinite(od.float()).all()
+    pre_d = {n: t.double() for n, t in pre.items()}
+    ro, rst = O.chunk_cyfa(**pre_d, output_final_state=True)
+    rm, _ = O.chunk_cyfa(**pre_d, mode="mirror")
+    rod, _ = O.fused_recurrent_cyfa(**{n: t.double() for n, t in last.items()}, initial_state=rst,
+                                    output_final_state=True)
+    rms = ro.pow(2).mean().sqrt()
+    own = (rm / rms - ro / rms).abs().max().item()
+    assert_close(o.double().cpu() / rms, ro / rms, max_abs=max(2e-2, 1.5 * own), what="range guard o")
+    for a, b, n in zip(st[:2], rst[:2], ("hk", "hv")):
+        assert_close(a, b, max_abs=float("inf"), what=f"range guard {n}")
+    drms = rod.pow(2).mean().sqrt()
+    assert_close(od.double().cpu() / drms, rod / drms, what="range guard decode o")
+
+
+def test_decode_refuses_host_tensors_before_launch():
+    """A CPU initial state, or a precomputed table of the wrong dtype, raises
+    ValueError before any launch (the kernel would otherwise read host memory)."""
+    from cyclic_flow_attention.ops import fused_recurrent_cyfa
+
+    x, init = _inputs(1, 1, 2, seed=3, state=True)
+    xg, _ = _gpu(x, None)
+    with pytest.raises(ValueError):
+        fused_recurrent_cyfa(**xg, initial_state=init)
+    with pytest.raises(ValueError):
+        fused_recurrent_cyfa(**xg, table=torch.zeros(2, 127, 128, dtype=torch.bfloat16, device=DEV))

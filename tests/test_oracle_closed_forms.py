@@ -142,3 +142,21 @@ def test_slot_readout_identity_at_zero_clock():
     weights = O.slot_readout(raw, torch.zeros(1, 1, 4, dtype=torch.float64), phi[None])
     p = torch.softmax(raw @ phi.T, dim=-1)
     torch.testing.assert_close(weights, p @ phi, atol=1e-14, rtol=0)
+
+
+def test_coherent_inputs_drive_the_readout_past_fp16():
+    """The GPU range test's inputs (tests/coherent_inputs.py) really push the
+    readout input z beyond the fp16 range: unscaled fp16 z would be infinite
+    for most tokens and the softmax would return NaN, while the reference's
+    own bf16 rounding of z and the table stays finite and close to exact."""
+    from coherent_inputs import coherent_inputs, pass1_output
+
+    x = coherent_inputs(T=16384)
+    raw, z = pass1_output(x)
+    over = (z.abs().amax(-1) > 65504).double().mean().item()
+    assert over > 0.5, over
+    table = O.readout_table(x["readout"].double())
+    logits = torch.einsum("bhtm,hrm->bhtr", z.to(torch.float16).double(), table)
+    assert torch.isnan(torch.softmax(logits, -1)).any()
+    logits_bf16 = torch.einsum("bhtm,hrm->bhtr", z.to(torch.bfloat16).double(), table)
+    assert torch.isfinite(torch.softmax(logits_bf16, -1)).all()

@@ -7,6 +7,8 @@ sequence (tests/test_inference.py:20-34 of the reference), and right padding
 is neutral (tests/test_inference.py:56-65).
 """
 
+import math
+
 import torch
 import torch.nn.functional as F
 
@@ -157,3 +159,66 @@ def test_gated_mlp_against_a_scalar_loop_and_its_special_cases():
     assert MO.gated_mlp(zero_gate, "m.", x, mode="exact").abs().max().item() == 0.0
     swapped = dict(p, **{"m.gate_proj.weight": p["m.up_proj.weight"], "m.up_proj.weight": p["m.gate_proj.weight"]})
     assert (MO.gated_mlp(swapped, "m.", x, mode="exact").double() - got).abs().max().item() > 1e-3
+
+
+def test_gate_activations_special_cases():
+    """g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b), delta =
+    sigmoid(d) (layers/cyfa.py:323-326), pinned by scalar closed forms:
+    a = 0 gives -exp(A_log) log(1 + exp(dt_bias)); a -> -inf gives g -> 0-
+    (no decay); a large gives -exp(A_log) (a + dt_bias); beta and delta are
+    the logistic function of their own projection only."""
+    A_log = torch.tensor([0.0, math.log(3.0), -1.5], dtype=D64)
+    dt_bias = torch.tensor([0.0, -2.0, 1.25], dtype=D64)
+    zero = torch.zeros(1, 3, dtype=D64)
+    g, beta, delta = MO.gate_activations(zero, zero, zero, dt_bias, A_log)
+    for h in range(3):
+        want = -math.exp(float(A_log[h])) * math.log1p(math.exp(float(dt_bias[h])))
+        assert abs(float(g[0, h]) - want) < 1e-15
+    assert abs(float(g[0, 0]) + math.log(2.0)) < 1e-15  # A_log = dt_bias = 0: -log 2
+    torch.testing.assert_close(beta, torch.full_like(beta, 0.5), rtol=0, atol=0)
+    big = torch.full((1, 3), 60.0, dtype=D64)
+    g_hi, _, _ = MO.gate_activations(big, zero, zero, dt_bias, A_log)
+    g_lo, _, _ = MO.gate_activations(-big, zero, zero, dt_bias, A_log)
+    for h in range(3):
+        assert abs(float(g_hi[0, h]) + math.exp(float(A_log[h])) * (60.0 + float(dt_bias[h]))) < 1e-9
+        assert -1e-20 < float(g_lo[0, h]) < 0.0
+    b = torch.tensor([[-3.0, 0.7, 9.0]], dtype=D64)
+    d = torch.tensor([[2.0, -0.4, -7.5]], dtype=D64)
+    _, beta, delta = MO.gate_activations(zero, b, d, dt_bias, A_log)
+    for h in range(3):
+        assert abs(float(beta[0, h]) - 1 / (1 + math.exp(-float(b[0, h])))) < 1e-15
+        assert abs(float(delta[0, h]) - 1 / (1 + math.exp(-float(d[0, h])))) < 1e-15
+
+
+def test_layer_gates_wire_each_projection_to_its_gate():
+    """With zero a/b/d projection weights the layer's gates are constants of
+    the biases alone: g from dt_bias and A_log, beta = sigmoid(b_proj.bias),
+    delta = sigmoid(d_proj.bias), with distinct biases so that a swapped
+    projection or a missing bias fails. A nonzero a_proj then moves g only."""
+    p, pre, cfg = _layer_params(H=2)
+    H, hidden = 2, cfg["hidden_size"]
+    for n in ("a_proj", "b_proj", "d_proj"):
+        p[pre + n + ".weight"] = torch.zeros(H, hidden, dtype=D64)
+    p[pre + "b_proj.bias"] = torch.tensor([0.3, -1.1], dtype=D64)
+    p[pre + "d_proj.bias"] = torch.tensor([-2.2, 0.9], dtype=D64)
+    p[pre + "dt_bias"] = torch.tensor([-0.5, 0.75], dtype=D64)
+    p[pre + "A_log"] = torch.tensor([0.2, -0.3], dtype=D64)
+    x = torch.randn(2, 5, hidden, dtype=D64, generator=torch.Generator().manual_seed(11))
+    g, delta, beta = MO.layer_gates(p, pre, x)
+    assert g.shape == delta.shape == beta.shape == (2, 5, H)
+    for h in range(H):
+        want_g = -math.exp(float(p[pre + "A_log"][h])) * math.log1p(math.exp(float(p[pre + "dt_bias"][h])))
+        want_b = 1 / (1 + math.exp(-float(p[pre + "b_proj.bias"][h])))
+        want_d = 1 / (1 + math.exp(-float(p[pre + "d_proj.bias"][h])))
+        assert (g[..., h] - want_g).abs().max() < 1e-15
+        assert (beta[..., h] - want_b).abs().max() < 1e-15
+        assert (delta[..., h] - want_d).abs().max() < 1e-15
+    p[pre + "a_proj.weight"] = torch.randn(H, hidden, dtype=D64, generator=torch.Generator().manual_seed(12))
+    g2, delta2, beta2 = MO.layer_gates(p, pre, x)
+    assert (g2 - g).abs().max() > 1e-3
+    assert torch.equal(delta2, delta) and torch.equal(beta2, beta)
+    a = x @ p[pre + "a_proj.weight"].T
+    for (bi, t, h) in ((0, 0, 0), (1, 4, 1), (0, 2, 1)):
+        z = float(a[bi, t, h]) + float(p[pre + "dt_bias"][h])
+        want = -math.exp(float(p[pre + "A_log"][h])) * math.log1p(math.exp(z))
+        assert abs(float(g2[bi, t, h]) - want) < 1e-12
