@@ -7,8 +7,17 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "cyfa_abi.h"
 #include "cyfa_internal.h"
+
+// Scratch of cyfa_chunk_fwd_noalloc: a device array each GPU holds from the
+// library's load until the process ends. In host code `scratch` names a
+// host-side stand-in, not device memory; its device address is resolved once
+// per device with hipGetSymbolAddress (scratch_base) and only that address
+// is handed to kernels.
+static __device__ __align__(256) unsigned char scratch[CYFA_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -27,6 +36,33 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 int check_launch(const char* what) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(CYFA_ERR_LAUNCH, "%s: kernel launch failed: %s", what, hipGetErrorString(e));
+    return CYFA_OK;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_base[kMaxDevices];  // device address of `scratch` per device, resolved on first use
+
+// Device address of the current device's scratch array (resolved once per
+// device, with that device current).
+int scratch_base(void** out, const char* what) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        return fail(CYFA_ERR_LAUNCH, "%s: no current HIP device", what);
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_base[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return fail(CYFA_ERR_LAUNCH, "%s: hipGetSymbolAddress of the scratch array failed on device %d: %s", what,
+                        dev, hipGetErrorString(e));
+        }
+        g_scratch_base[dev] = p;
+    }
+    *out = g_scratch_base[dev];
     return CYFA_OK;
 }
 
@@ -145,7 +181,9 @@ int cyfa_decode_layer_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* l
 
 namespace {
 
-int chunk_fwd(const CyfaChunkArgs* a, const CyfaOutNormArgs* on, void* hip_stream) {
+// use_scratch: the workspace is the device's scratch array (args->workspace
+// and args->workspace_bytes are ignored).
+int chunk_fwd(const CyfaChunkArgs* a, const CyfaOutNormArgs* on, void* hip_stream, bool use_scratch = false) {
     if (!a) return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd: null args");
     if (a->M != 128) return fail(CYFA_ERR_UNSUPPORTED, "cyfa_chunk_fwd: num_slots must be 128, got %d", a->M);
     if (a->C != 64) return fail(CYFA_ERR_UNSUPPORTED, "cyfa_chunk_fwd: chunk_size must be 64, got %d", a->C);
@@ -174,10 +212,19 @@ int chunk_fwd(const CyfaChunkArgs* a, const CyfaOutNormArgs* on, void* hip_strea
         (has_h0 && (!aligned(a->h0_k, 16) || !aligned(a->h0_v, 16))))
         return fail(CYFA_ERR_ALIGN, "cyfa_chunk_fwd: q/k/v/o, norm weights and states need 16-byte alignment");
     const cyfa::WorkspaceLayout ws = cyfa::workspace_layout(a->B, a->T, a->H, a->K, a->V);
-    if (!a->workspace || a->workspace_bytes < ws.total)
-        return fail(CYFA_ERR_WORKSPACE, "cyfa_chunk_fwd: workspace of %zu bytes needed, got %zu", ws.total,
-                    a->workspace ? a->workspace_bytes : (size_t)0);
-    if (!aligned(a->workspace, 256)) return fail(CYFA_ERR_ALIGN, "cyfa_chunk_fwd: workspace needs 256-byte alignment");
+    void* workspace = a->workspace;
+    if (use_scratch) {
+        if (ws.total > CYFA_NOALLOC_SCRATCH_BYTES)
+            return fail(CYFA_ERR_UNSUPPORTED,
+                        "cyfa_chunk_fwd_noalloc: B=%d T=%d H=%d needs %zu bytes of scratch; the array holds %llu "
+                        "(call cyfa_chunk_fwd with a workspace instead)",
+                        a->B, a->T, a->H, ws.total, (unsigned long long)CYFA_NOALLOC_SCRATCH_BYTES);
+    } else {
+        if (!workspace || a->workspace_bytes < ws.total)
+            return fail(CYFA_ERR_WORKSPACE, "cyfa_chunk_fwd: workspace of %zu bytes needed, got %zu", ws.total,
+                        workspace ? a->workspace_bytes : (size_t)0);
+        if (!aligned(workspace, 256)) return fail(CYFA_ERR_ALIGN, "cyfa_chunk_fwd: workspace needs 256-byte alignment");
+    }
     if (on) {
         if (!on->weight || !on->gate) return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd_normed: null weight or gate");
         if (!aligned(on->weight, 16) || !aligned(on->gate, 16))
@@ -220,7 +267,10 @@ int chunk_fwd(const CyfaChunkArgs* a, const CyfaOutNormArgs* on, void* hip_strea
     p.on_gate = on ? (const __bf16*)on->gate : nullptr;
     p.on_eps = on ? on->eps : 0.f;
     p.on_prescale = on ? on->prescale : 1.f;
-    char* base = (char*)a->workspace;
+    if (use_scratch) {
+        if (int rc = scratch_base(&workspace, "cyfa_chunk_fwd_noalloc")) return rc;
+    }
+    char* base = (char*)workspace;
     p.lam = (float*)(base + ws.lam);
     p.gam = (float*)(base + ws.gam);
     p.seg = (_Float16*)(base + ws.seg);
@@ -240,6 +290,10 @@ int cyfa_chunk_fwd(const CyfaChunkArgs* a, void* hip_stream) { return chunk_fwd(
 int cyfa_chunk_fwd_normed(const CyfaChunkArgs* a, const CyfaOutNormArgs* norm, void* hip_stream) {
     if (!norm) return fail(CYFA_ERR_VALUE, "cyfa_chunk_fwd_normed: null norm args");
     return chunk_fwd(a, norm, hip_stream);
+}
+
+int cyfa_chunk_fwd_noalloc(const CyfaChunkArgs* a, const CyfaOutNormArgs* norm, void* hip_stream) {
+    return chunk_fwd(a, norm, hip_stream, true);
 }
 
 size_t cyfa_scalar_la_workspace_bytes(int B, int T, int H, int K, int V) {

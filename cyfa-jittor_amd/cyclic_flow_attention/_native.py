@@ -117,6 +117,7 @@ class CyfaConvArgs(ctypes.Structure):
 SIGNATURES = {
     "cyfa_chunk_fwd": (_c_int, [ctypes.POINTER(CyfaChunkArgs), _c_void_p]),
     "cyfa_chunk_fwd_normed": (_c_int, [ctypes.POINTER(CyfaChunkArgs), ctypes.POINTER(CyfaOutNormArgs), _c_void_p]),
+    "cyfa_chunk_fwd_noalloc": (_c_int, [ctypes.POINTER(CyfaChunkArgs), ctypes.POINTER(CyfaOutNormArgs), _c_void_p]),
     "cyfa_chunk_workspace_bytes": (_c_size_t, [_c_int] * 7),
     "cyfa_scalar_la": (_c_int, [ctypes.POINTER(CyfaSlaArgs), _c_void_p]),
     "cyfa_scalar_la_workspace_bytes": (_c_size_t, [_c_int] * 5),
@@ -255,6 +256,20 @@ def chunk_fwd_normed(args: CyfaChunkArgs, norm: CyfaOutNormArgs, device):
                 lambda: lib.cyfa_chunk_fwd_normed(ctypes.byref(args), ctypes.byref(norm), stream_handle(device)))
     if rc != CYFA_OK:
         _raise(rc, "cyfa_chunk_fwd_normed failed")
+
+
+NOALLOC_SCRATCH_BYTES = 80 << 20  # CYFA_NOALLOC_SCRATCH_BYTES
+
+
+def chunk_fwd_noalloc(args: CyfaChunkArgs, norm, device):
+    """cyfa_chunk_fwd_noalloc: the op with the library's per-device scratch
+    array as its workspace (norm: CyfaOutNormArgs or None)."""
+    lib = load_library()
+    ref = None if norm is None else ctypes.byref(norm)
+    rc = _timed("cyfa_chunk_fwd_noalloc", lambda: lib.cyfa_chunk_fwd_noalloc(ctypes.byref(args), ref,
+                                                                              stream_handle(device)))
+    if rc != CYFA_OK:
+        _raise(rc, "cyfa_chunk_fwd_noalloc failed")
 
 
 def scalar_la_workspace_bytes(B, T, H, K, V):

@@ -35,6 +35,7 @@ def chunk_cyfa(
     *,
     table=None,
     output_norm=None,
+    no_alloc=False,
 ):
     """Chunkwise Cyclic Flow Attention.
 
@@ -48,6 +49,9 @@ def chunk_cyfa(
     [B, T, H, V] bf16, eps, prescale)``: the layer's gated output norm
     bf16(xs rsqrt(mean xs^2 + eps) weight sigmoid(gate)), xs = bf16(o prescale),
     is then applied inside the kernels and its result returned in place of o.
+    ``no_alloc`` (keyword only, an extension) runs cyfa_chunk_fwd_noalloc: the
+    intermediates live in the library's per-device scratch array instead of
+    a workspace allocated here (calls on one GPU must not overlap).
     """
     if cu_seqlens is not None:
         raise NotImplementedError("packed layout requires native segment dispatch")
@@ -88,8 +92,11 @@ def chunk_cyfa(
         clock = torch.empty(B, H, dtype=torch.float32, device=dev)
     else:
         hk = hv = clock = None
-    ws_bytes = _native.chunk_workspace_bytes(B, T, H, K, V, M, chunk_size)
-    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)  # alive until the launch
+    if no_alloc:
+        ws_bytes, workspace = 0, None
+    else:
+        ws_bytes = _native.chunk_workspace_bytes(B, T, H, K, V, M, chunk_size)
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)  # alive until the launch
     args = _native.CyfaChunkArgs(
         B=B, T=T, H=H, K=K, V=V, M=M, C=chunk_size,
         q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(),
@@ -102,7 +109,10 @@ def chunk_cyfa(
         workspace=_native.ptr(workspace), workspace_bytes=ws_bytes,
     )
     if output_norm is None:
-        _native.chunk_fwd(args, dev)
+        if no_alloc:
+            _native.chunk_fwd_noalloc(args, None, dev)
+        else:
+            _native.chunk_fwd(args, dev)
     else:
         on_w, on_gate, on_eps, on_prescale = output_norm
         on_w = on_w.detach().to(torch.float32).contiguous()
@@ -115,7 +125,10 @@ def chunk_cyfa(
         _native.require_device(on_w, on_gate)
         norm = _native.CyfaOutNormArgs(weight=on_w.data_ptr(), gate=on_gate.data_ptr(), eps=float(on_eps),
                                        prescale=float(on_prescale))
-        _native.chunk_fwd_normed(args, norm, dev)
+        if no_alloc:
+            _native.chunk_fwd_noalloc(args, norm, dev)
+        else:
+            _native.chunk_fwd_normed(args, norm, dev)
     return o, ((hk, hv, clock) if output_final_state else None)
 
 

@@ -87,6 +87,27 @@ typedef struct CyfaOutNormArgs {
  * receives o'. */
 int cyfa_chunk_fwd_normed(const CyfaChunkArgs *args, const CyfaOutNormArgs *norm, void *hip_stream);
 
+/* Size of the device scratch array behind cyfa_chunk_fwd_noalloc: 80 MiB,
+ * enough for the workspace of configurations up to B * H * T = 131072
+ * token-heads (e.g. B=8, T=2048, H=4 needs 44.5 MiB; B=1, T=16384, H=8 needs
+ * 64 MiB). */
+#define CYFA_NOALLOC_SCRATCH_BYTES (80ull << 20)
+
+/* cyfa_chunk_fwd (norm == NULL) or cyfa_chunk_fwd_normed (norm set) that
+ * allocates nothing and takes no workspace: args->workspace and
+ * args->workspace_bytes are ignored, and the intermediates live in a device
+ * array of CYFA_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds
+ * until the process ends (its address is resolved on the first call on each
+ * device). For callers that cannot allocate device memory: code under HIP
+ * graph capture, serving loops that forbid allocation. No counterpart in the
+ * reference. Calls whose workspace would exceed the array return
+ * CYFA_ERR_UNSUPPORTED. Every call on one GPU uses that GPU's one array, so
+ * calls that overlap on one GPU (different streams, or different threads
+ * without ordering) race and give wrong results; calls in one stream are
+ * ordered and safe. Every intermediate a call reads is written earlier in the
+ * same call, so nothing in the array needs clearing between calls. */
+int cyfa_chunk_fwd_noalloc(const CyfaChunkArgs *args, const CyfaOutNormArgs *norm, void *hip_stream);
+
 /* Workspace bytes cyfa_chunk_fwd needs for these dimensions (the reference
  * allocates the equivalent intermediates through Jittor, ops/chunk.py:244-336). */
 size_t cyfa_chunk_workspace_bytes(int B, int T, int H, int K, int V, int M, int C);

@@ -193,3 +193,16 @@ def test_decode_wrappers_check_every_tensor_before_launch():
         check_table(torch.zeros(2, 127, 128), 1, 128)
     check_table(torch.zeros(1, 127, 128), 1, 128)
 
+
+def test_noalloc_entry_point_refuses_oversize_before_launch():
+    """cyfa_chunk_fwd_noalloc checks its workspace against the scratch array
+    before touching the device: B=64, T=2048, H=4 needs 132 MiB (> 80 MiB)."""
+    lib = _native.load_library()
+    ptrs = dict(q=0x10000, k=0x20000, v=0x30000, g=0x40000, delta=0x50000, beta=0x60000, table=0x70000,
+                q_norm_weight=0x80000, k_norm_weight=0x90000, o=0xa0000)
+    args = _native.CyfaChunkArgs(B=64, T=2048, H=4, K=256, V=256, M=128, C=64, scale=0.0625, **ptrs)
+    assert _native.chunk_workspace_bytes(64, 2048, 4, 256, 256) > _native.NOALLOC_SCRATCH_BYTES
+    assert lib.cyfa_chunk_fwd_noalloc(ctypes.byref(args), None, None) == _native.CYFA_ERR_UNSUPPORTED
+    assert b"scratch" in lib.cyfa_last_error()
+    assert _native.chunk_workspace_bytes(8, 2048, 4, 256, 256) <= _native.NOALLOC_SCRATCH_BYTES
+    assert _native.chunk_workspace_bytes(1, 16384, 8, 256, 256) <= _native.NOALLOC_SCRATCH_BYTES
