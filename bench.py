@@ -14,19 +14,27 @@ Weights are seeded N(0, 0.02) random init (no checkpoints offline).
 roofline: HIP events around every prefill attention launch in the timed
 prefill region (cyfa_chunk_fwd_normed: the op with the layer's gated output
 norm in its last kernel) give its average device duration; the decode kernel's duration comes
-from HIP events around replays of a graph of in-place decode launches at the
-decode shape (B=64, H=4), free of host launch gaps;
+from HIP events around replays of a graph of in-place launches at the decode
+shape (B=64, H=4), free of host launch gaps;
   prefill attention: 377 088 algorithmic FLOP per token*head / duration vs the
-                     2.5 PFLOP/s dense bf16 MFMA peak;
-  decode:            524 288 bytes of fp32 state per (batch, head) per layer
-                     launch / duration vs 8 TB/s HBM.
+                     2.5 PFLOP/s dense bf16 MFMA peak, and (roofline.hbm) 2 572
+                     algorithmic bytes per token*head (q, k, v, o, the output
+                     norm's gate in bf16, three f32 gates) vs 8 TB/s;
+  decode:            524 288 bytes of fp32 state per (batch, head) per launch of
+                     cyfa_decode_layer_step, the kernel of the model's graphed
+                     decode step, vs 8 TB/s (decode.op_kernel: the same for
+                     cyfa_decode_step, fused_recurrent_cyfa alone).
 isolated_pass: configuration 2 (B=8, H=4, T=4096), one scalar_la pass at each
 pass shape ((K, V) = (256, 128) and (128, 256)), q, k, v ~ N(0, 1) bf16 with q, k
 L2-normalised, log alpha = logsigmoid(N(3, 1)); HIP events around each launch;
 156 032 FLOP per token*head per pass against the bf16 MFMA peak and the
 algorithmic bytes (q, k, v, g in, o out) against 8 TB/s.
+long_context: configuration 5 (CyFA-1.4B, B=1, a 16384-token prefill, 512
+greedy decode steps) with the op's and the decode layer kernel's fractions.
 cpu_baseline: the CPU oracle (the restatement of the reference path; the
-reference itself has no CPU path) timed on this host, bounded sample.
+reference itself has no CPU path) timed on this host, bounded sample, median
+of three after a warm-up, with the GPU's logits of the same sequence compared
+against the oracle's.
 """
 
 import argparse
@@ -48,11 +56,16 @@ PEAK_HBM_GBS = 8000.0
 FLOP_PER_TOKEN_HEAD = 377_088      # pass 1 + readout + pass 2, causal-exact
 STATE_BYTES_PER_BH = 524_288       # fp32 hk + hv, read and written, K = V = 256
 FLOP_PER_TOKEN_HEAD_PASS = 156_032  # one ScalarGatedLA pass, causal-exact
+# Algorithmic HBM bytes of the prefill op per token*head: q, k, v and o in bf16
+# (4 x 512) and the three f32 gates (12), plus the gated output norm's bf16 gate
+# input (512) that the model's normed launch reads.
+BYTES_PER_TOKEN_HEAD = 2 * 256 * 4 + 12 + 2 * 256
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
 # scaled by a 1 GiB copy kernel (profiles/cyfa_chunk_fwd_cfg3_prefill.md,
 # profiles/cyfa_decode_step_cfg4.md); they apply to the default shapes.
 TRAFFIC_PREFILL_BYTES = 343.2e6    # one cyfa_chunk_fwd_normed at B=8, T=2048, H=4
 TRAFFIC_DECODE_BYTES = 135.5e6     # one decode launch at B=64, H=4
+TRAFFIC_LAYER_STEP_BYTES = None    # one cyfa_decode_layer_step at B=64, H=4 (not yet counted)
 
 
 def parse():
@@ -69,8 +82,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-isolated", action="store_true", help="skip the configuration-2 scalar_la timings")
-    ap.add_argument("--long-context", action="store_true",
-                    help="also run configuration 5: CyFA-1.4B, B=1, a 16384-token prefill, then 512 greedy "
+    ap.add_argument("--no-long-context", action="store_true",
+                    help="skip configuration 5: CyFA-1.4B, B=1, a 16384-token prefill, then 512 greedy "
                          "decode steps (reported under 'long_context')")
     ap.add_argument("--decode-kernel-only", action="store_true",
                     help="only time the fused decode kernel at the decode shape (for hardware-counter runs)")
@@ -118,9 +131,10 @@ def time_prefill(model, ids, steps, warmup):
                 out = model(ids, use_cache=True)
             torch.cuda.synchronize()
             elapsed = time.perf_counter() - start
+        first_row = out["logits"][0].float().cpu()
         del out
     res = timer.results()
-    return elapsed, res.get("cyfa_chunk_fwd_normed", []) + res.get("cyfa_chunk_fwd", [])
+    return elapsed, res.get("cyfa_chunk_fwd_normed", []) + res.get("cyfa_chunk_fwd", []), first_row
 
 
 def time_isolated_pass(K, V, B=8, H=4, T=4096, reps=20, warmup=3):
@@ -169,6 +183,54 @@ def time_decode(model, prompt, steps, warmup):
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - start
     return elapsed
+
+
+def decode_layer_kernel_ms(batch, heads, reps=24, replays=5):
+    """Average device time of one cyfa_decode_layer_step launch (the kernel the
+    model's graphed decode step runs: short convolution, gates, the decode op
+    and the gated output norm) at the decode shape, timed as decode_kernel_ms:
+    `reps` in-place launches on their own states captured in one graph,
+    replayed between HIP events on the launch stream."""
+    import torch
+
+    from cyclic_flow_attention import _native
+    from cyclic_flow_attention.ops.fused_recurrent import decode_layer_step
+
+    dev = torch.device("cuda:0")
+    H, D = heads, 3 * heads * 256
+    gen = torch.Generator().manual_seed(6)
+    qkv = torch.randn(batch, 1, D, generator=gen).bfloat16().to(dev)
+    wconv = (0.3 * torch.randn(D, 4, generator=gen)).bfloat16().to(dev)
+    abd = torch.randn(batch, 1, 3 * H, generator=gen).bfloat16().to(dev)
+    dt_bias, A_log = torch.randn(H, generator=gen).to(dev), torch.randn(H, generator=gen).to(dev)
+    gate = torch.randn(batch, 1, H * 256, generator=gen).bfloat16().to(dev)
+    ones = torch.ones(256, device=dev)
+    table = _native.readout_table(torch.eye(127, device=dev).expand(H, 127, 127).contiguous())
+    states = [(torch.randn(batch, heads, 256, 128, device=dev), torch.randn(batch, heads, 128, 256, device=dev),
+               torch.rand(batch, heads, device=dev),
+               (0.5 * torch.randn(batch, 3, D, device=dev)).bfloat16()) for _ in range(reps)]
+
+    def step(st):
+        decode_layer_step(qkv, st[3], st[3], wconv, abd, dt_bias, A_log, gate, ones, 1e-6, 127.0, table, ones, ones,
+                          1e-6, 1e-6, H, initial_state=st[:3], output_final_state=True, inplace=True)
+
+    with torch.no_grad():
+        step(states[0])
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for st in states:
+                step(st)
+        graph.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(replays):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+    return start.elapsed_time(end) / (reps * replays)
 
 
 def decode_kernel_ms(batch, heads, reps=24, replays=5, graphed=True):
@@ -222,9 +284,22 @@ def decode_kernel_ms(batch, heads, reps=24, replays=5, graphed=True):
     return start.elapsed_time(end) / (reps * replays)
 
 
-def cpu_baseline_prefill(model, config, seq_len):
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline_prefill(model, config, seq_len, gpu_logits=None, reps=3):
     """Oracle forward (float32, reference rounding points) of one whole
-    sequence of the prefill batch on the host cores."""
+    sequence of the prefill batch on the host cores: the median of `reps`
+    timed forwards after a warm-up forward. With the GPU's logits of the same
+    sequence (gpu_logits [T, V]), also reports how far they are from the
+    oracle's."""
     import torch
 
     from oracle import model_oracle
@@ -233,25 +308,40 @@ def cpu_baseline_prefill(model, config, seq_len):
     torch.set_num_threads(threads)
     params = {k: v.detach().cpu() for k, v in model.state_dict().items()}
     cfg = {k: getattr(config, k) for k in config.__dataclass_fields__}
-    gen = torch.Generator().manual_seed(1)
+    gen = torch.Generator().manual_seed(0)  # the prefill batch's ids: its first row
     ids = torch.randint(0, config.vocab_size, (1, seq_len), generator=gen)
+    times = []
     with torch.no_grad():
-        model_oracle.causal_lm(params, cfg, ids[:, :64], mode="mirror")  # warm-up
-        start = time.perf_counter()
-        model_oracle.causal_lm(params, cfg, ids, use_cache=True, mode="mirror")
-        elapsed = time.perf_counter() - start
-    return {
+        model_oracle.causal_lm(params, cfg, ids[:, :256], mode="mirror")  # warm-up
+        for _ in range(reps):
+            start = time.perf_counter()
+            logits, _ = model_oracle.causal_lm(params, cfg, ids, use_cache=True, mode="mirror")
+            times.append(time.perf_counter() - start)
+    elapsed = statistics.median(times)
+    out = {
         "value": round(seq_len / elapsed, 2),
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"CPU oracle (float32, bf16 rounding points) full 400M forward, B=1 x T={seq_len} "
-                  f"(one of the prefill batch's sequences), {elapsed:.1f} s",
+        "cpu": cpu_model(),
+        "sample": f"CPU oracle (float32, bf16 rounding points) full 400M forward of the prefill batch's first "
+                  f"sequence, B=1 x T={seq_len}: median of {reps} after a warm-up, {elapsed:.2f} s",
     }
+    if gpu_logits is not None:
+        a = gpu_logits.double().cpu()
+        b = logits[0].double()
+        diff = (a - b).abs()
+        out["parity"] = {"what": "GPU logits of that sequence vs the oracle's (mirror mode)",
+                         "max_abs": round(diff.max().item(), 4),
+                         "mean_rel": round((diff.mean() / b.abs().mean()).item(), 5),
+                         "top1_agree": round((a.argmax(-1) == b.argmax(-1)).double().mean().item(), 4)}
+    return out
 
 
-def cpu_baseline_decode(model, config, batch, steps=2):
-    """Oracle decode steps on the host, from a zero state (same per-step work)."""
+def cpu_baseline_decode(model, config, batch, steps=4, reps=3):
+    """Oracle decode steps on the host at the decode batch, from the state of
+    a short oracle prefill (the per-step work does not depend on the prompt
+    length): the median over `reps` runs of `steps` steps, after a warm-up step."""
     import torch
 
     from oracle import model_oracle
@@ -261,21 +351,27 @@ def cpu_baseline_decode(model, config, batch, steps=2):
     params = {k: v.detach().cpu() for k, v in model.state_dict().items()}
     cfg = {k: getattr(config, k) for k in config.__dataclass_fields__}
     gen = torch.Generator().manual_seed(2)
-    ids = torch.randint(0, config.vocab_size, (batch, 1), generator=gen)
-    cache = None
+    ids = torch.randint(0, config.vocab_size, (batch, 64), generator=gen)
+    times = []
     with torch.no_grad():
-        _, cache = model_oracle.causal_lm(params, cfg, ids, cache=None, use_cache=True, mode="mirror")
-        start = time.perf_counter()
-        for _ in range(steps):
-            logits, cache = model_oracle.causal_lm(params, cfg, ids, cache=cache, use_cache=True, mode="mirror")
-            ids = logits[:, -1].argmax(-1, keepdim=True)
-        elapsed = time.perf_counter() - start
+        logits, cache = model_oracle.causal_lm(params, cfg, ids, use_cache=True, mode="mirror")
+        tok = logits[:, -1].argmax(-1, keepdim=True)
+        logits, cache = model_oracle.causal_lm(params, cfg, tok, cache=cache, use_cache=True, mode="mirror")  # warm-up
+        for _ in range(reps):
+            start = time.perf_counter()
+            for _ in range(steps):
+                logits, cache = model_oracle.causal_lm(params, cfg, tok, cache=cache, use_cache=True, mode="mirror")
+                tok = logits[:, -1].argmax(-1, keepdim=True)
+            times.append(time.perf_counter() - start)
+    elapsed = statistics.median(times)
     return {
         "value": round(batch * steps / elapsed, 2),
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"CPU oracle (float32) {steps} decode steps of the 400M model at B={batch}, {elapsed:.1f} s",
+        "cpu": cpu_model(),
+        "sample": f"CPU oracle (float32) decode of the 400M model at B={batch} after a 64-token prompt: median of "
+                  f"{reps} runs of {steps} steps after a warm-up step, {elapsed:.2f} s per run",
     }
 
 
@@ -319,14 +415,16 @@ def main():
         del src, dst
 
     log(f"prefill B={args.batch} T={args.seq_len}: warmup {args.warmup}, timed {args.steps}")
-    elapsed, op_ms = time_prefill(model, ids, args.steps, args.warmup)
+    elapsed, op_ms, first_row_logits = time_prefill(model, ids, args.steps, args.warmup)
     tokens = args.batch * args.seq_len * args.steps
     value = tokens / elapsed
     op_avg = statistics.fmean(op_ms) if op_ms else float("nan")
     flop = FLOP_PER_TOKEN_HEAD * args.batch * args.seq_len * H
     achieved = flop / (op_avg * 1e-3) / 1e12
+    op_bytes = BYTES_PER_TOKEN_HEAD * args.batch * args.seq_len * H
+    op_gbs = op_bytes / (op_avg * 1e-3) / 1e9
     log(f"prefill {value:,.0f} tok/s; attention op {op_avg:.3f} ms/launch over {len(op_ms)} launches "
-        f"= {achieved:.1f} TFLOP/s")
+        f"= {achieved:.1f} TFLOP/s, {op_gbs:,.0f} GB/s algorithmic")
     result = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -358,6 +456,8 @@ def main():
             "traffic": TRAFFIC_PREFILL_BYTES if (args.batch, args.seq_len, H) == (8, 2048, 4) else None,
             "launch_ms": round(op_avg, 4),
             "flop_per_launch": flop,
+            "hbm": {"achieved": round(op_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(op_gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": op_bytes},
         },
     }
 
@@ -367,10 +467,13 @@ def main():
             f"timed {args.decode_steps}")
         d_elapsed = time_decode(model, prompt, args.decode_steps, args.decode_warmup)
         d_value = args.decode_batch * args.decode_steps / d_elapsed
-        d_avg = decode_kernel_ms(args.decode_batch, H)
         d_bytes = STATE_BYTES_PER_BH * args.decode_batch * H
+        l_avg = decode_layer_kernel_ms(args.decode_batch, H)
+        l_gbs = d_bytes / (l_avg * 1e-3) / 1e9
+        d_avg = decode_kernel_ms(args.decode_batch, H)
         d_gbs = d_bytes / (d_avg * 1e-3) / 1e9
-        log(f"decode {d_value:,.0f} tok/s; decode kernel {d_avg * 1e3:.1f} us/launch = {d_gbs:,.0f} GB/s")
+        log(f"decode {d_value:,.0f} tok/s; layer-step kernel {l_avg * 1e3:.1f} us/launch = {l_gbs:,.0f} GB/s; "
+            f"op kernel {d_avg * 1e3:.1f} us/launch = {d_gbs:,.0f} GB/s")
         result["decode"] = {
             "value": round(d_value, 1),
             "unit": "tok/s",
@@ -378,15 +481,23 @@ def main():
             "steps": args.decode_steps,
             "ms_per_step": round(d_elapsed / args.decode_steps * 1e3, 3),
             "roofline": {
-                "kernel": "cyfa_decode_step",
+                "kernel": "cyfa_decode_layer_step (the model's graphed step: short conv, gates, decode op, "
+                          "gated output norm)",
                 "bound": "hbm",
-                "achieved": round(d_gbs, 1),
+                "achieved": round(l_gbs, 1),
                 "peak": PEAK_HBM_GBS,
                 "unit": "GB/s",
+                "frac": round(l_gbs / PEAK_HBM_GBS, 4),
+                "traffic": TRAFFIC_LAYER_STEP_BYTES if (args.decode_batch, H) == (64, 4) else None,
+                "launch_us": round(l_avg * 1e3, 2),
+                "bytes_per_launch": d_bytes,
+            },
+            "op_kernel": {
+                "kernel": "cyfa_decode_step (fused_recurrent_cyfa alone)",
+                "achieved": round(d_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(d_gbs / PEAK_HBM_GBS, 4),
                 "traffic": TRAFFIC_DECODE_BYTES if (args.decode_batch, H) == (64, 4) else None,
                 "launch_us": round(d_avg * 1e3, 2),
-                "bytes_per_launch": d_bytes,
             },
         }
         del prompt
@@ -409,28 +520,40 @@ def main():
 
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle) ...")
-        result["cpu_baseline"] = cpu_baseline_prefill(model, config, args.seq_len)
+        result["cpu_baseline"] = cpu_baseline_prefill(model, config, args.seq_len, first_row_logits)
         log(f"cpu prefill {result['cpu_baseline']['value']} tok/s")
         if "decode" in result:
             result["decode"]["cpu_baseline"] = cpu_baseline_decode(model, config, args.decode_batch)
             log(f"cpu decode {result['decode']['cpu_baseline']['value']} tok/s")
 
-    if args.long_context:
+    if not args.no_long_context:
         del model
         torch.cuda.empty_cache()
         lc_config, lc_model = build_model("cyclic_flow_attention_1_4b.json", dev)
-        T5 = 16384
+        T5, H5 = 16384, lc_config.num_heads
         lc_ids = torch.randint(0, lc_config.vocab_size, (1, T5), generator=gen).to(dev)
         log(f"long context: CyFA-1.4B prefill B=1 T={T5}")
-        lc_elapsed, _ = time_prefill(lc_model, lc_ids, 2, 1)
+        lc_elapsed, lc_op_ms, _ = time_prefill(lc_model, lc_ids, 2, 1)
+        lc_op = statistics.fmean(lc_op_ms)
+        lc_flop = FLOP_PER_TOKEN_HEAD * T5 * H5
+        lc_bytes = BYTES_PER_TOKEN_HEAD * T5 * H5
         log(f"long context: decode B=1, 512 steps after the {T5}-token prompt")
         lc_dec = time_decode(lc_model, lc_ids, 512, 4)
+        lc_kernel = decode_layer_kernel_ms(1, H5)
+        lc_state = STATE_BYTES_PER_BH * H5
         result["long_context"] = {
             "workload": f"configuration 5: CyFA-1.4B, B=1, {T5}-token prefill, then 512 greedy decode steps",
-            "prefill": {"value": round(2 * T5 / lc_elapsed, 1), "unit": "tok/s", "ms_per_step": round(lc_elapsed / 2 * 1e3, 3)},
-            "decode": {"value": round(512 / lc_dec, 1), "unit": "tok/s", "ms_per_step": round(lc_dec / 512 * 1e3, 4)},
+            "prefill": {"value": round(2 * T5 / lc_elapsed, 1), "unit": "tok/s",
+                        "ms_per_step": round(lc_elapsed / 2 * 1e3, 3),
+                        "op_launch_ms": round(lc_op, 4),
+                        "mfma_frac": round(lc_flop / (lc_op * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                        "hbm_frac": round(lc_bytes / (lc_op * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+            "decode": {"value": round(512 / lc_dec, 1), "unit": "tok/s", "ms_per_step": round(lc_dec / 512 * 1e3, 4),
+                       "layer_kernel_us": round(lc_kernel * 1e3, 2),
+                       "layer_kernel_hbm_frac": round(lc_state / (lc_kernel * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
         }
-        log(f"long context: prefill {2 * T5 / lc_elapsed:,.0f} tok/s, decode {512 / lc_dec:,.1f} tok/s")
+        log(f"long context: prefill {2 * T5 / lc_elapsed:,.0f} tok/s (op {lc_op * 1e3:.1f} us), decode "
+            f"{512 / lc_dec:,.1f} tok/s (layer kernel {lc_kernel * 1e3:.1f} us)")
         del lc_model
 
     print(json.dumps(result), flush=True)

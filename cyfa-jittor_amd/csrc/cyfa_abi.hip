@@ -147,6 +147,11 @@ int decode_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* ly, void* hi
     p.hk_out = a->hk_out;
     p.hv_out = a->hv_out;
     p.clock_out = a->clock_out;
+    const size_t ws = cyfa::decode_workspace_bytes(a->B, a->H, a->K, a->V);
+    if (ws && a->workspace && a->workspace_bytes >= ws) {
+        if (!aligned(a->workspace, 16)) return fail(CYFA_ERR_ALIGN, "cyfa_decode_step: workspace needs 16-byte alignment");
+        p.part = (float*)a->workspace;
+    }
     if (ly) {
         p.qkv = (const __bf16*)ly->qkv;
         p.qkv_row = ly->qkv_row;
@@ -173,6 +178,11 @@ int decode_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* ly, void* hi
 }  // namespace
 
 int cyfa_decode_step(const CyfaDecodeArgs* a, void* hip_stream) { return decode_step(a, nullptr, hip_stream); }
+
+size_t cyfa_decode_workspace_bytes(int B, int H, int K, int V) {
+    if (!((K == 128 || K == 256) && (V == 128 || V == 256))) return 0;
+    return cyfa::decode_workspace_bytes(B, H, K, V);
+}
 
 int cyfa_decode_layer_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* layer, void* hip_stream) {
     if (!layer) return fail(CYFA_ERR_VALUE, "cyfa_decode_layer_step: null layer args");

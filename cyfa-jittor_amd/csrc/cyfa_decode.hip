@@ -1,12 +1,7 @@
 // cyfa_decode.hip -- fused constant-memory CyFA decode step for gfx950.
 //
-// One 1024-thread workgroup per (batch, head). The step is HBM-bound: it
-// streams the fp32 key state hk [K, M] and value state hv [M, V] in and out
-// once (512 KiB per (b, h) for K = V = 256). Both states are issued as
-// coalesced float4 loads at kernel entry. Both updated states are written
-// before the slot readout runs (the value-state update does not depend on the
-// readout; the updated hv stays in registers for o = hv'^T weights), so the
-// write stream drains while the readout computes.
+// The step is HBM-bound: it streams the fp32 key state hk [K, M] and value
+// state hv [M, V] in and out once (512 KiB per (b, h) for K = V = 256).
 //
 // Math (ops/fused_recurrent.py:57-188): q_hat = bf16(q rs_q w_q) * scale,
 // k_hat = bf16(k rs_k w_k); lam = clock + delta; alpha = e^g;
@@ -16,6 +11,20 @@
 // The readout is evaluated in fp32 (the reference rounds z, the table and p
 // to bf16 here); the write vector and the normalised q/k keep the reference's
 // bf16 rounding so decode and the chunkwise prefill see identical operands.
+//
+// Two launch forms with bit-identical results:
+//  * one 1024-thread workgroup per (b, h) (decode_step_kernel), when B H fills
+//    the chip (B H >= 64): both state streams are issued at entry and both
+//    updated states are written before the slot readout runs;
+//  * small batches (B H < 64, e.g. B = 1): eight workgroups per (b, h)
+//    (decode_split_a_kernel), each updating 32 rows of hk and 32 columns of
+//    hv (128-byte line-aligned slices), and writing its slice's partial sums
+//    of raw; then one workgroup per (b, h) (decode_split_b_kernel) sums the
+//    partials, runs the readout and forms o from the updated hv.
+// raw is always reduced in the same order: per 32-row slice s, each of 256
+// threads accumulates its four rows, the eight 32-thread groups are summed in
+// group order, and the slices in slice order; o is formed with the same
+// thread mapping in both forms.
 #include "cyfa_device.h"
 #include "cyfa_internal.h"
 
@@ -32,148 +41,67 @@ __device__ __forceinline__ void stream_store(float4* p, const float4& v) {
     __builtin_nontemporal_store(__builtin_bit_cast(f32x4, v), reinterpret_cast<f32x4*>(p));
 }
 
-// LAYER: the layer's one-token step around the op in the same kernel. The
-// width-4 causal short convolution of the projection row (layers/cyfa.py:138-233,
-// the arithmetic of short_conv_kernel) gives this head's q, k and v and the new
-// conv cache; the gate activations (layers/cyfa.py:323-326, as gates_kernel)
-// come from the a|b|d row; and o goes through the gated output norm
-// o_norm(o * prescale, gate) (layers/cyfa.py:349-350, as rms_norm_kernel<1>:
-// wave 0 holds four consecutive values per lane) before it is stored.
-template <int K, int V, bool LAYER>
-__global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
-    constexpr int NT = 1024;
-    constexpr int KJ = K / 32;      // float4 of hk per thread (row has 32 float4)
-    constexpr int VQ = V / 4;       // float4 per hv row
-    constexpr int VROWS = NT / VQ;  // hv rows covered per sweep
-    constexpr int VJ = kSlots / VROWS;
-    constexpr int NW = NT / 64;
-    const int bh = blockIdx.x, h = bh % p.H, tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+namespace {
 
-    __shared__ float s_q[K], s_k[K], s_w[kSlots], s_raw[kSlots], s_z[kSlots];
-    __shared__ float s_p[kSlots], s_om[kSlots], s_c[kPairs], s_s[kPairs];
-    __shared__ float s_part[NW][V > kSlots ? V : kSlots];
-    __shared__ float s_red[2][NW];
-    __shared__ float s_v[LAYER ? V : 1];
-    __shared__ __align__(16) float s_tab[kActive * kSlots];  // this head's readout table
+constexpr int SLICE = 32;  // hk rows / hv columns per slice
 
-    const bool has_state = p.hk_in != nullptr;
-    const float4* hk_in = reinterpret_cast<const float4*>(p.hk_in + (size_t)bh * K * kSlots);
-    const float4* hv_in = reinterpret_cast<const float4*>(p.hv_in + (size_t)bh * kSlots * V);
-    float4* hk_out = reinterpret_cast<float4*>(p.hk_out + (size_t)bh * K * kSlots);
-    float4* hv_out = reinterpret_cast<float4*>(p.hv_out + (size_t)bh * kSlots * V);
+// The one-token inputs of (b, h): q and k channel c (< K) or v channel c (< V)
+// of this head. LAYER: from the width-4 causal short convolution of the
+// projection row (layers/cyfa.py:138-233, the arithmetic of short_conv_kernel);
+// otherwise read from q, k, v. The convolution window (cache rows 0-2, then x)
+// and the weights of a channel are loaded by load_conv, used by conv_out.
+struct ConvIn {
+    float win[4], wt[4];
+};
 
-    // Layer step: the short-convolution inputs of this thread's channels (the
-    // q and k channel tid, the v channel tid) are loaded ahead of the state
-    // streams, so they arrive first. win[c][0..2] = cache rows, win[c][3] = x.
-    float cwin[3][4], cwt[3][4];
+__device__ __forceinline__ ConvIn load_conv(const DecodeParams& p, int b, int ch) {
+    ConvIn c;
+#pragma unroll
+    for (int w = 0; w < 3; w++)
+        c.win[w] = p.cache_in ? (float)p.cache_in[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch] : 0.f;
+    c.win[3] = (float)p.qkv[(size_t)b * p.qkv_row + ch];
+    const bf16x4 wt = *reinterpret_cast<const bf16x4*>(p.conv_w + (size_t)ch * 4);  // one 8-byte load
+#pragma unroll
+    for (int w = 0; w < 4; w++) c.wt[w] = (float)wt[w];
+    return c;
+}
+
+__device__ __forceinline__ float conv_out(const ConvIn& c) {
+    float acc = c.win[0] * c.wt[0];
+#pragma unroll
+    for (int w = 1; w < 4; w++) acc = fmaf(c.win[w], c.wt[w], acc);
+    return bf16_round(acc);
+}
+
+// The new conv cache of a channel: the last three rows of its window.
+__device__ __forceinline__ void store_conv_cache(const DecodeParams& p, int b, int ch, const ConvIn& c) {
+#pragma unroll
+    for (int w = 0; w < 3; w++)
+        p.cache_out[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch] = (bf16_t)c.win[w + 1];
+}
+
+// Gate activations of (b, h) (layers/cyfa.py:323-326, as gates_kernel) or the given gates.
+template <bool LAYER>
+__device__ __forceinline__ void load_gates(const DecodeParams& p, int bh, float& g, float& delta, float& beta) {
     if (LAYER) {
-        const int b = bh / p.H, HK = p.H * K;
-        const int ch[3] = {h * K + tid, HK + h * K + tid, 2 * HK + h * V + tid};
-#pragma unroll
-        for (int c = 0; c < 3; c++) {
-            if (tid < (c < 2 ? K : V)) {
-#pragma unroll
-                for (int w = 0; w < 3; w++)
-                    cwin[c][w] = p.cache_in ? (float)p.cache_in[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch[c]]
-                                            : 0.f;
-                cwin[c][3] = (float)p.qkv[(size_t)b * p.qkv_row + ch[c]];
-                const bf16x4 wt = *reinterpret_cast<const bf16x4*>(p.conv_w + (size_t)ch[c] * 4);  // one 8-byte load
-#pragma unroll
-                for (int w = 0; w < 4; w++) cwt[c][w] = (float)wt[w];
-            }
-        }
-    }
-
-    // Layer step: wave 0's norm weight and gate for the output norm at the
-    // end, loaded now so that their latency is not the kernel's last step.
-    constexpr int OJ = (V + 255) / 256;  // four consecutive values per lane and 256-wide block
-    float4 on_w4[OJ];
-    bf16x4 on_g4[OJ];
-    if (LAYER && wave == 0) {
-        const bf16_t* gt = p.gate + (size_t)(bh / p.H) * p.gate_row + (size_t)h * V;
-#pragma unroll
-        for (int j = 0; j < OJ; j++) {
-            on_w4[j] = *reinterpret_cast<const float4*>(p.on_w + 4 * lane + 256 * j);
-            on_g4[j] = *reinterpret_cast<const bf16x4*>(gt + 4 * lane + 256 * j);
-        }
-    }
-
-    // The readout table (L2-resident, 64 KB per head) is read into registers
-    // ahead of the state streams and staged in LDS during the prologue, so the
-    // readout after the state writes finds it on chip.
-    constexpr int TQ = kActive * kSlots / 4;  // float4 of the table: 3 per thread, 4 for the first 992
-    static_assert(NT == 1024 && TQ > 3 * NT && TQ <= 4 * NT, "table staging covers the table");
-    const float4* tb4 = reinterpret_cast<const float4*>(p.table + (size_t)h * kActive * kSlots);
-    const float4 tab0 = tb4[tid], tab1 = tb4[tid + NT], tab2 = tb4[tid + 2 * NT];
-    const float4 tab3 = tid + 3 * NT < TQ ? tb4[tid + 3 * NT] : float4{0.f, 0.f, 0.f, 0.f};
-
-    // Issue both state streams; everything below overlaps with them.
-    float4 hk_r[KJ], hv_r[VJ];
-    if (has_state) {
-#pragma unroll
-        for (int j = 0; j < KJ; j++) hk_r[j] = stream_load(hk_in + tid + NT * j);
-#pragma unroll
-        for (int j = 0; j < VJ; j++) hv_r[j] = stream_load(hv_in + tid + NT * j);
-    } else {
-#pragma unroll
-        for (int j = 0; j < KJ; j++) hk_r[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int j = 0; j < VJ; j++) hv_r[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-
-    // q/k RMS statistics (ops/fused_recurrent.py:62-89).
-    float qv = 0.f, kv = 0.f;
-    float g_in, delta_in, beta_in;
-    if (LAYER) {
-        const int b = bh / p.H;
-        const int HK = p.H * K;
-        // The arithmetic of short_conv_kernel; the new cache is the last three rows of the window.
-        auto conv = [&](int c, int ch) -> float {
-            float acc = cwin[c][0] * cwt[c][0];
-#pragma unroll
-            for (int w = 1; w < 4; w++) acc = fmaf(cwin[c][w], cwt[c][w], acc);
-#pragma unroll
-            for (int w = 0; w < 3; w++)
-                p.cache_out[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch] = (bf16_t)cwin[c][w + 1];
-            return bf16_round(acc);
-        };
-        if (tid < K) {
-            qv = conv(0, h * K + tid);
-            kv = conv(1, HK + h * K + tid);
-        }
-        if (tid < V) s_v[tid] = conv(2, 2 * HK + h * V + tid);
+        const int b = bh / p.H, h = bh % p.H;
         const bf16_t* row = p.abd + (size_t)b * p.abd_row;
         const float a = (float)row[h] + p.dt_bias[h];
         const float sp = a > 20.f ? a : log1pf(expf(a));
-        g_in = -expf(p.A_log[h]) * sp;
-        beta_in = sigmoidf((float)row[p.H + h]);
-        delta_in = sigmoidf((float)row[2 * p.H + h]);
+        g = -expf(p.A_log[h]) * sp;
+        beta = sigmoidf((float)row[p.H + h]);
+        delta = sigmoidf((float)row[2 * p.H + h]);
     } else {
-        if (tid < K) {
-            qv = (float)p.q[(size_t)bh * K + tid];
-            kv = (float)p.k[(size_t)bh * K + tid];
-        }
-        g_in = p.g[bh];
-        delta_in = p.delta[bh];
-        beta_in = p.beta[bh];
+        g = p.g[bh];
+        delta = p.delta[bh];
+        beta = p.beta[bh];
     }
-    const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
-    if (lane == 0 && wave < K / 64) {
-        s_red[0][wave] = sq;
-        s_red[1][wave] = sk;
-    }
-    {
-        float4* st4 = reinterpret_cast<float4*>(s_tab);
-        st4[tid] = tab0;
-        st4[tid + NT] = tab1;
-        st4[tid + 2 * NT] = tab2;
-        if (tid + 3 * NT < TQ) st4[tid + 3 * NT] = tab3;
-    }
-    const float clock = has_state ? p.clock_in[bh] : 0.f;
-    const float lam = clock + delta_in;
-    const float decay = expf(g_in);
-    const float beta = beta_in;
+}
+
+// Write vector w (bf16-rounded, ops/utils.py:664-702) and the phase of every
+// pair into LDS; threads 0..63 (one pair each).
+__device__ __forceinline__ void write_vector_lds(float lam, float beta, float* s_w, float* s_c, float* s_s) {
+    const int tid = threadIdx.x;
     if (tid < kPairs) {
         float s, c;
         pair_sincos(reduced_clock(lam), tid, s, c);
@@ -183,90 +111,49 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
         s_c[tid] = c;
         s_s[tid] = s;
     }
-    __syncthreads();
-    float tq = 0.f, tk = 0.f;
-#pragma unroll
-    for (int i = 0; i < K / 64; i++) {
-        tq += s_red[0][i];
-        tk += s_red[1][i];
-    }
-    if (tid < K) {
-        const float rq = rsqrtf(tq / K + p.q_eps), rk = rsqrtf(tk / K + p.k_eps);
-        s_q[tid] = bf16_round(qv * rq * p.q_w[tid]) * p.scale;
-        s_k[tid] = bf16_round(kv * rk * p.k_w[tid]);
-    }
-    __syncthreads();
-    if (tid == 0) p.clock_out[bh] = lam;  // after every thread has read clock_in
+}
 
-    // Key state: hk' = alpha hk + k_hat (x) w ; raw = hk'^T q_hat.
-    {
-        const int m4 = (tid & 31) * 4;
-        const float w0 = s_w[m4], w1 = s_w[m4 + 1], w2 = s_w[m4 + 2], w3 = s_w[m4 + 3];
-        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+// Key-state slice s for the 256 "slice threads" vt: float4 j (0..3) of thread
+// vt is element (row 32 s + vt / 32 + 8 j, columns 4 (vt % 32) ..) of hk, i.e.
+// float4 index 1024 s + vt + 256 j. Updates and stores the four float4 and
+// accumulates the thread's partial raw in row order j.
+__device__ __forceinline__ float4 key_slice_update(const float4 (&hk)[4], float4* hk_out, int s, int vt, float decay,
+                                                   const float* s_k, const float* s_q, const float* s_w) {
+    const int m4 = (vt & 31) * 4;
+    const float w0 = s_w[m4], w1 = s_w[m4 + 1], w2 = s_w[m4 + 2], w3 = s_w[m4 + 3];
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int j = 0; j < KJ; j++) {
-            const int d = (tid >> 5) + 32 * j;
-            const float kd = s_k[d], qd = s_q[d];
-            float4 n = hk_r[j];
-            n.x = fmaf(n.x, decay, kd * w0);
-            n.y = fmaf(n.y, decay, kd * w1);
-            n.z = fmaf(n.z, decay, kd * w2);
-            n.w = fmaf(n.w, decay, kd * w3);
-            stream_store(hk_out + tid + NT * j, n);
-            a0 = fmaf(n.x, qd, a0);
-            a1 = fmaf(n.y, qd, a1);
-            a2 = fmaf(n.z, qd, a2);
-            a3 = fmaf(n.w, qd, a3);
-        }
-        a0 += __shfl_xor(a0, 32);
-        a1 += __shfl_xor(a1, 32);
-        a2 += __shfl_xor(a2, 32);
-        a3 += __shfl_xor(a3, 32);
-        if (lane < 32) {
-            s_part[wave][m4] = a0;
-            s_part[wave][m4 + 1] = a1;
-            s_part[wave][m4 + 2] = a2;
-            s_part[wave][m4 + 3] = a3;
-        }
+    for (int j = 0; j < 4; j++) {
+        const int d = SLICE * s + (vt >> 5) + 8 * j;
+        const float kd = s_k[d], qd = s_q[d];
+        float4 n = hk[j];
+        n.x = fmaf(n.x, decay, kd * w0);
+        n.y = fmaf(n.y, decay, kd * w1);
+        n.z = fmaf(n.z, decay, kd * w2);
+        n.w = fmaf(n.w, decay, kd * w3);
+        stream_store(hk_out + 1024 * s + vt + 256 * j, n);
+        a.x = fmaf(n.x, qd, a.x);
+        a.y = fmaf(n.y, qd, a.y);
+        a.z = fmaf(n.z, qd, a.z);
+        a.w = fmaf(n.w, qd, a.w);
     }
-    // Value state: hv' = alpha hv + w (x) v, written now; kept in hv_r for o.
-    {
-        const int v4 = (tid % VQ) * 4, r0 = tid / VQ;
-        float v0, v1, v2, v3;
-        if (LAYER) {
-            v0 = s_v[v4];
-            v1 = s_v[v4 + 1];
-            v2 = s_v[v4 + 2];
-            v3 = s_v[v4 + 3];
-        } else {
-            const bf16x4 vb = *reinterpret_cast<const bf16x4*>(p.v + (size_t)bh * V + v4);
-            v0 = (float)vb[0];
-            v1 = (float)vb[1];
-            v2 = (float)vb[2];
-            v3 = (float)vb[3];
-        }
-#pragma unroll
-        for (int j = 0; j < VJ; j++) {
-            const float wm = s_w[r0 + VROWS * j];
-            float4 n = hv_r[j];
-            n.x = fmaf(n.x, decay, wm * v0);
-            n.y = fmaf(n.y, decay, wm * v1);
-            n.z = fmaf(n.z, decay, wm * v2);
-            n.w = fmaf(n.w, decay, wm * v3);
-            stream_store(hv_out + tid + NT * j, n);
-            hv_r[j] = n;
-        }
-    }
-    __syncthreads();
-    if (tid < kSlots) {
-        float r = 0.f;
-#pragma unroll
-        for (int w = 0; w < NW; w++) r += s_part[w][tid];
-        s_raw[tid] = r;
-    }
-    __syncthreads();
+    return a;
+}
 
-    // Slot readout (ops/fused_recurrent.py:114-175), fp32.
+// part[g][m] (g = vt / 32): a slice's eight group partials -> its partial raw
+// of slot m, summed in group order.
+__device__ __forceinline__ float slice_partial(const float* part, int m) {
+    float r = part[m];
+#pragma unroll
+    for (int g = 1; g < 8; g++) r += part[g * kSlots + m];
+    return r;
+}
+
+// Slot readout from raw (ops/fused_recurrent.py:114-175), fp32, 1024 threads;
+// the table of the head is in LDS. Leaves the weights in s_om.
+__device__ __forceinline__ void readout_1024(const float* s_raw, const float* s_c, const float* s_s, const float* tb,
+                                             float* s_z, float* s_p, float (*s_part)[256], float* s_om) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid < kPairs) {
         const float c = s_c[tid], s = s_s[tid];
         const float e = s_raw[2 * tid], o = s_raw[2 * tid + 1];
@@ -274,7 +161,6 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
         s_z[2 * tid + 1] = s * e + c * o;
     }
     __syncthreads();
-    const float* tb = s_tab;
     {
         const int r = tid >> 3, part = tid & 7;
         float lg = 0.f;
@@ -323,8 +209,19 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
         s_om[2 * tid + 1] = -s * ue + c * uo;
     }
     __syncthreads();
+}
 
-    // o = hv'^T weights, from the updated value state kept in registers.
+// o = hv'^T weights with 1024 threads: thread tid covers value columns
+// 4 (tid % VQ) .. and rows tid / VQ + VROWS j of hv' (hv_r), then the waves'
+// partials are summed in wave order. LAYER: the gated output norm
+// o_norm(o * prescale, gate) (layers/cyfa.py:349-350, as rms_norm_kernel<1>:
+// wave 0 holds four consecutive values per lane) before o is stored.
+template <int V, bool LAYER>
+__device__ __forceinline__ void output_1024(const DecodeParams& p, int bh, const float4* hv_r, const float* s_om,
+                                            float (*s_part)[256], float* s_v, const float4* on_w4,
+                                            const bf16x4* on_g4) {
+    constexpr int NT = 1024, VQ = V / 4, VROWS = NT / VQ, VJ = kSlots / VROWS;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     {
         const int v4 = (tid % VQ) * 4, r0 = tid / VQ;
         float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
@@ -354,7 +251,7 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
         if (tid < V) {
             float s = 0.f;
 #pragma unroll
-            for (int w = 0; w < NW; w++) s += s_part[w][tid];
+            for (int w = 0; w < NT / 64; w++) s += s_part[w][tid];
             p.o[(size_t)bh * V + tid] = (bf16_t)s;
         }
         return;
@@ -362,12 +259,12 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     if (tid < V) {
         float s = 0.f;
 #pragma unroll
-        for (int w = 0; w < NW; w++) s += s_part[w][tid];
+        for (int w = 0; w < NT / 64; w++) s += s_part[w][tid];
         s_v[tid] = (float)(bf16_t)s;  // o as the op would store it
     }
     __syncthreads();
     if (wave == 0) {
-        constexpr int J = OJ;
+        constexpr int J = (V + 255) / 256;
         float xs[J][4];
         float ss = 0.f;
 #pragma unroll
@@ -395,19 +292,390 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     }
 }
 
+// Wave 0's norm weight and gate for the output norm (LAYER), loaded early so
+// that their latency is not the kernel's last step.
+template <int V, bool LAYER>
+__device__ __forceinline__ void load_norm_inputs(const DecodeParams& p, int bh, float4* on_w4, bf16x4* on_g4) {
+    constexpr int OJ = (V + 255) / 256;
+    if (LAYER && (threadIdx.x >> 6) == 0) {
+        const int lane = threadIdx.x & 63;
+        const bf16_t* gt = p.gate + (size_t)(bh / p.H) * p.gate_row + (size_t)(bh % p.H) * V;
+#pragma unroll
+        for (int j = 0; j < OJ; j++) {
+            on_w4[j] = *reinterpret_cast<const float4*>(p.on_w + 4 * lane + 256 * j);
+            on_g4[j] = *reinterpret_cast<const bf16x4*>(gt + 4 * lane + 256 * j);
+        }
+    }
+}
+
+// q/k RMS norms (ops/fused_recurrent.py:62-89) from each thread's raw q, k
+// channel (threads < K), into s_q (scaled) and s_k; NW waves.
+template <int K, int NW>
+__device__ __forceinline__ void qk_norms(const DecodeParams& p, float qv, float kv, float (*s_red)[NW], float* s_q,
+                                         float* s_k) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
+    if (lane == 0 && wave < K / 64) {
+        s_red[0][wave] = sq;
+        s_red[1][wave] = sk;
+    }
+    __syncthreads();
+    float tq = 0.f, tk = 0.f;
+#pragma unroll
+    for (int i = 0; i < K / 64; i++) {
+        tq += s_red[0][i];
+        tk += s_red[1][i];
+    }
+    if (tid < K) {
+        const float rq = rsqrtf(tq / K + p.q_eps), rk = rsqrtf(tk / K + p.k_eps);
+        s_q[tid] = bf16_round(qv * rq * p.q_w[tid]) * p.scale;
+        s_k[tid] = bf16_round(kv * rk * p.k_w[tid]);
+    }
+}
+
+// The one-workgroup form. LAYER: the layer's one-token step around the op in
+// the same kernel: q, k and v from the short convolution and the new conv
+// cache, the gate activations from the a|b|d row, and o through the gated
+// output norm.
+template <int K, int V, bool LAYER>
+__global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
+    constexpr int NT = 1024;
+    constexpr int NS = K / SLICE;   // key-state slices
+    constexpr int RK = NS / 4;      // slices per thread (four 256-thread groups)
+    constexpr int VQ = V / 4;       // float4 per hv row
+    constexpr int VROWS = NT / VQ;  // hv rows covered per sweep
+    constexpr int VJ = kSlots / VROWS;
+    constexpr int NW = NT / 64;
+    const int bh = blockIdx.x, h = bh % p.H, tid = threadIdx.x, vt = tid & 255;
+
+    __shared__ float s_q[K], s_k[K], s_w[kSlots], s_raw[kSlots], s_z[kSlots];
+    __shared__ float s_p[kSlots], s_om[kSlots], s_c[kPairs], s_s[kPairs];
+    __shared__ float s_part[NW][256];
+    __shared__ float s_kpart[NS][8][kSlots];  // key-state slice partials of raw, per 32-thread group
+    __shared__ float s_red[2][NW];
+    __shared__ float s_v[LAYER ? V : 1];
+    __shared__ __align__(16) float s_tab[kActive * kSlots];  // this head's readout table
+
+    const bool has_state = p.hk_in != nullptr;
+    const float4* hk_in = reinterpret_cast<const float4*>(p.hk_in + (size_t)bh * K * kSlots);
+    const float4* hv_in = reinterpret_cast<const float4*>(p.hv_in + (size_t)bh * kSlots * V);
+    float4* hk_out = reinterpret_cast<float4*>(p.hk_out + (size_t)bh * K * kSlots);
+    float4* hv_out = reinterpret_cast<float4*>(p.hv_out + (size_t)bh * kSlots * V);
+
+    // Layer step: the short-convolution inputs of this thread's channels (the
+    // q and k channel tid, the v channel tid) are loaded ahead of the state
+    // streams, so they arrive first.
+    const int b = bh / p.H, HK = p.H * K;
+    ConvIn cq{}, ck{}, cv{};
+    if (LAYER) {
+        if (tid < K) {
+            cq = load_conv(p, b, h * K + tid);
+            ck = load_conv(p, b, HK + h * K + tid);
+        }
+        if (tid < V) cv = load_conv(p, b, 2 * HK + h * V + tid);
+    }
+    constexpr int OJ = (V + 255) / 256;
+    float4 on_w4[OJ];
+    bf16x4 on_g4[OJ];
+    load_norm_inputs<V, LAYER>(p, bh, on_w4, on_g4);
+
+    // The readout table (L2-resident, 64 KB per head) is read into registers
+    // ahead of the state streams and staged in LDS during the prologue, so the
+    // readout after the state writes finds it on chip.
+    constexpr int TQ = kActive * kSlots / 4;  // float4 of the table: 3 per thread, 4 for the first 992
+    static_assert(NT == 1024 && TQ > 3 * NT && TQ <= 4 * NT, "table staging covers the table");
+    const float4* tb4 = reinterpret_cast<const float4*>(p.table + (size_t)h * kActive * kSlots);
+    const float4 tab0 = tb4[tid], tab1 = tb4[tid + NT], tab2 = tb4[tid + 2 * NT];
+    const float4 tab3 = tid + 3 * NT < TQ ? tb4[tid + 3 * NT] : float4{0.f, 0.f, 0.f, 0.f};
+
+    // Issue both state streams; everything below overlaps with them. Key
+    // state: slices (tid >> 8) + 4 r, four float4 of slice thread vt each.
+    float4 hk_r[RK][4], hv_r[VJ];
+    if (has_state) {
+#pragma unroll
+        for (int r = 0; r < RK; r++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) hk_r[r][j] = stream_load(hk_in + 1024 * ((tid >> 8) + 4 * r) + vt + 256 * j);
+#pragma unroll
+        for (int j = 0; j < VJ; j++) hv_r[j] = stream_load(hv_in + tid + NT * j);
+    } else {
+#pragma unroll
+        for (int r = 0; r < RK; r++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) hk_r[r][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < VJ; j++) hv_r[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+
+    float qv = 0.f, kv = 0.f;
+    if (LAYER) {
+        if (tid < K) {
+            qv = conv_out(cq);
+            kv = conv_out(ck);
+            store_conv_cache(p, b, h * K + tid, cq);
+            store_conv_cache(p, b, HK + h * K + tid, ck);
+        }
+        if (tid < V) {
+            s_v[tid] = conv_out(cv);
+            store_conv_cache(p, b, 2 * HK + h * V + tid, cv);
+        }
+    } else if (tid < K) {
+        qv = (float)p.q[(size_t)bh * K + tid];
+        kv = (float)p.k[(size_t)bh * K + tid];
+    }
+    float g_in, delta_in, beta_in;
+    load_gates<LAYER>(p, bh, g_in, delta_in, beta_in);
+    {
+        float4* st4 = reinterpret_cast<float4*>(s_tab);
+        st4[tid] = tab0;
+        st4[tid + NT] = tab1;
+        st4[tid + 2 * NT] = tab2;
+        if (tid + 3 * NT < TQ) st4[tid + 3 * NT] = tab3;
+    }
+    const float clock = has_state ? p.clock_in[bh] : 0.f;
+    const float lam = clock + delta_in;
+    const float decay = expf(g_in);
+    write_vector_lds(lam, beta_in, s_w, s_c, s_s);
+    qk_norms<K, NW>(p, qv, kv, s_red, s_q, s_k);
+    __syncthreads();
+    if (tid == 0) p.clock_out[bh] = lam;  // after every thread has read clock_in
+
+    // Key state: hk' = alpha hk + k_hat (x) w ; raw = hk'^T q_hat, by slices.
+#pragma unroll
+    for (int r = 0; r < RK; r++) {
+        const int s = (tid >> 8) + 4 * r;
+        const float4 a = key_slice_update(hk_r[r], hk_out, s, vt, decay, s_k, s_q, s_w);
+        float* pt = &s_kpart[s][vt >> 5][(vt & 31) * 4];
+        pt[0] = a.x;
+        pt[1] = a.y;
+        pt[2] = a.z;
+        pt[3] = a.w;
+    }
+    // Value state: hv' = alpha hv + w (x) v, written now; kept in hv_r for o.
+    {
+        const int v4 = (tid % VQ) * 4, r0 = tid / VQ;
+        float v0, v1, v2, v3;
+        if (LAYER) {
+            v0 = s_v[v4];
+            v1 = s_v[v4 + 1];
+            v2 = s_v[v4 + 2];
+            v3 = s_v[v4 + 3];
+        } else {
+            const bf16x4 vb = *reinterpret_cast<const bf16x4*>(p.v + (size_t)bh * V + v4);
+            v0 = (float)vb[0];
+            v1 = (float)vb[1];
+            v2 = (float)vb[2];
+            v3 = (float)vb[3];
+        }
+#pragma unroll
+        for (int j = 0; j < VJ; j++) {
+            const float wm = s_w[r0 + VROWS * j];
+            float4 n = hv_r[j];
+            n.x = fmaf(n.x, decay, wm * v0);
+            n.y = fmaf(n.y, decay, wm * v1);
+            n.z = fmaf(n.z, decay, wm * v2);
+            n.w = fmaf(n.w, decay, wm * v3);
+            stream_store(hv_out + tid + NT * j, n);
+            hv_r[j] = n;
+        }
+    }
+    __syncthreads();
+    if (tid < kSlots) {
+        float r = slice_partial(&s_kpart[0][0][0], tid);
+#pragma unroll
+        for (int s = 1; s < NS; s++) r += slice_partial(&s_kpart[s][0][0], tid);
+        s_raw[tid] = r;
+    }
+    __syncthreads();
+    readout_1024(s_raw, s_c, s_s, s_tab, s_z, s_p, s_part, s_om);
+    output_1024<V, LAYER>(p, bh, hv_r, s_om, s_part, s_v, on_w4, on_g4);
+}
+
+// Small-batch form, part A: grid (NSL, B H), 256 threads; workgroup s updates
+// key-state slice s (rows 32 s ..) and value-state slice s (columns 32 s ..)
+// and writes its slice's partial raw to part_out[(bh NSL + s) 128 + m]. The
+// conv cache and the clock are left to part B, which runs after every
+// workgroup of part A has read them.
+template <int K, int V, bool LAYER>
+__global__ __launch_bounds__(256) void decode_split_a_kernel(DecodeParams p) {
+    constexpr int NT = 256, NW = NT / 64;
+    constexpr int NSL = (K > V ? K : V) / SLICE;
+    const int s = blockIdx.x, bh = blockIdx.y, h = bh % p.H, b = bh / p.H, tid = threadIdx.x;
+    const int HK = p.H * K;
+    __shared__ float s_q[K], s_k[K], s_w[kSlots], s_c[kPairs], s_s[kPairs];
+    __shared__ float s_kpart[8][kSlots];
+    __shared__ float s_v[SLICE];
+    __shared__ float s_red[2][NW];
+
+    const bool key = s < K / SLICE, val = s < V / SLICE;
+    const bool has_state = p.hk_in != nullptr;
+    const float4* hk_in = reinterpret_cast<const float4*>(p.hk_in + (size_t)bh * K * kSlots);
+    const float4* hv_in = reinterpret_cast<const float4*>(p.hv_in + (size_t)bh * kSlots * V);
+    float4* hk_out = reinterpret_cast<float4*>(p.hk_out + (size_t)bh * K * kSlots);
+    float4* hv_out = reinterpret_cast<float4*>(p.hv_out + (size_t)bh * kSlots * V);
+
+    ConvIn cq{}, ck{}, cv{};
+    if (LAYER) {
+        if (tid < K) {
+            cq = load_conv(p, b, h * K + tid);
+            ck = load_conv(p, b, HK + h * K + tid);
+        }
+        if (val && tid < SLICE) cv = load_conv(p, b, 2 * HK + h * V + SLICE * s + tid);
+    }
+    // This workgroup's slices of both states: hk float4 1024 s + tid + 256 j;
+    // hv row tid / 8 + 32 j, columns 32 s + 4 (tid % 8) ...
+    constexpr int VQ = V / 4;
+    float4 hk_r[4], hv_r[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        hk_r[j] = has_state && key ? stream_load(hk_in + 1024 * s + tid + 256 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+        hv_r[j] = has_state && val ? stream_load(hv_in + (size_t)((tid >> 3) + 32 * j) * VQ + 8 * s + (tid & 7))
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float qv = 0.f, kv = 0.f;
+    if (LAYER) {
+        if (tid < K) {
+            qv = conv_out(cq);
+            kv = conv_out(ck);
+        }
+        if (val && tid < SLICE) s_v[tid] = conv_out(cv);
+    } else {
+        if (tid < K) {
+            qv = (float)p.q[(size_t)bh * K + tid];
+            kv = (float)p.k[(size_t)bh * K + tid];
+        }
+        if (val && tid < SLICE) s_v[tid] = (float)p.v[(size_t)bh * V + SLICE * s + tid];
+    }
+    float g_in, delta_in, beta_in;
+    load_gates<LAYER>(p, bh, g_in, delta_in, beta_in);
+    const float lam = (has_state ? p.clock_in[bh] : 0.f) + delta_in;
+    const float decay = expf(g_in);
+    write_vector_lds(lam, beta_in, s_w, s_c, s_s);
+    qk_norms<K, NW>(p, qv, kv, s_red, s_q, s_k);
+    __syncthreads();
+    if (key) {
+        const float4 a = key_slice_update(hk_r, hk_out, s, tid, decay, s_k, s_q, s_w);
+        float* pt = &s_kpart[tid >> 5][(tid & 31) * 4];
+        pt[0] = a.x;
+        pt[1] = a.y;
+        pt[2] = a.z;
+        pt[3] = a.w;
+    }
+    if (val) {
+        const int c = 4 * (tid & 7);
+        const float v0 = s_v[c], v1 = s_v[c + 1], v2 = s_v[c + 2], v3 = s_v[c + 3];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int m = (tid >> 3) + 32 * j;
+            const float wm = s_w[m];
+            float4 n = hv_r[j];
+            n.x = fmaf(n.x, decay, wm * v0);
+            n.y = fmaf(n.y, decay, wm * v1);
+            n.z = fmaf(n.z, decay, wm * v2);
+            n.w = fmaf(n.w, decay, wm * v3);
+            stream_store(hv_out + (size_t)m * VQ + 8 * s + (tid & 7), n);
+        }
+    }
+    __syncthreads();
+    if (key && tid < kSlots) p.part[((size_t)bh * NSL + s) * kSlots + tid] = slice_partial(&s_kpart[0][0], tid);
+}
+
+// Small-batch form, part B: one 1024-thread workgroup per (b, h): raw from the
+// slices' partials (slice order), the readout, o from the updated value state
+// (read back, L2-resident), the conv cache and the clock.
+template <int K, int V, bool LAYER>
+__global__ __launch_bounds__(1024) void decode_split_b_kernel(DecodeParams p) {
+    constexpr int NT = 1024, NW = NT / 64;
+    constexpr int NS = K / SLICE, NSL = (K > V ? K : V) / SLICE;
+    constexpr int VQ = V / 4, VROWS = NT / VQ, VJ = kSlots / VROWS;
+    const int bh = blockIdx.x, h = bh % p.H, b = bh / p.H, tid = threadIdx.x;
+    const int HK = p.H * K;
+    __shared__ float s_raw[kSlots], s_z[kSlots], s_p[kSlots], s_om[kSlots], s_c[kPairs], s_s[kPairs], s_w[kSlots];
+    __shared__ float s_part[NW][256];
+    __shared__ float s_v[LAYER ? V : 1];
+    __shared__ __align__(16) float s_tab[kActive * kSlots];
+
+    constexpr int OJ = (V + 255) / 256;
+    float4 on_w4[OJ];
+    bf16x4 on_g4[OJ];
+    load_norm_inputs<V, LAYER>(p, bh, on_w4, on_g4);
+    constexpr int TQ = kActive * kSlots / 4;
+    const float4* tb4 = reinterpret_cast<const float4*>(p.table + (size_t)h * kActive * kSlots);
+    const float4 tab0 = tb4[tid], tab1 = tb4[tid + NT], tab2 = tb4[tid + 2 * NT];
+    const float4 tab3 = tid + 3 * NT < TQ ? tb4[tid + 3 * NT] : float4{0.f, 0.f, 0.f, 0.f};
+    const float4* hv_new = reinterpret_cast<const float4*>(p.hv_out + (size_t)bh * kSlots * V);
+    float4 hv_r[VJ];
+#pragma unroll
+    for (int j = 0; j < VJ; j++) hv_r[j] = hv_new[tid + NT * j];
+    float part_r = 0.f;
+    if (tid < kSlots) {
+        part_r = p.part[(size_t)bh * NSL * kSlots + tid];
+#pragma unroll
+        for (int s = 1; s < NS; s++) part_r += p.part[((size_t)bh * NSL + s) * kSlots + tid];
+        s_raw[tid] = part_r;
+    }
+    // The conv cache of this head's channels: the last three rows of each
+    // window (each channel read and written by one thread, so an in-place
+    // update needs no ordering between threads).
+    if (LAYER && tid < 2 * K + V) {
+        const int ch = tid < K ? h * K + tid : tid < 2 * K ? HK + h * K + (tid - K) : 2 * HK + h * V + (tid - 2 * K);
+        bf16_t win[3];
+#pragma unroll
+        for (int w = 1; w < 3; w++)
+            win[w - 1] = p.cache_in ? p.cache_in[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch] : (bf16_t)0.f;
+        win[2] = p.qkv[(size_t)b * p.qkv_row + ch];
+#pragma unroll
+        for (int w = 0; w < 3; w++) p.cache_out[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch] = win[w];
+    }
+    float g_in, delta_in, beta_in;
+    load_gates<LAYER>(p, bh, g_in, delta_in, beta_in);
+    (void)g_in;
+    const float lam = (p.hk_in != nullptr ? p.clock_in[bh] : 0.f) + delta_in;
+    write_vector_lds(lam, beta_in, s_w, s_c, s_s);
+    {
+        float4* st4 = reinterpret_cast<float4*>(s_tab);
+        st4[tid] = tab0;
+        st4[tid + NT] = tab1;
+        st4[tid + 2 * NT] = tab2;
+        if (tid + 3 * NT < TQ) st4[tid + 3 * NT] = tab3;
+    }
+    __syncthreads();
+    if (tid == 0) p.clock_out[bh] = lam;  // after every thread has read clock_in
+    readout_1024(s_raw, s_c, s_s, s_tab, s_z, s_p, s_part, s_om);
+    output_1024<V, LAYER>(p, bh, hv_r, s_om, s_part, s_v, on_w4, on_g4);
+}
+
+template <int K, int V, bool LAYER>
+void launch(const DecodeParams& p, hipStream_t stream) {
+    const int BH = p.B * p.H;
+    if (p.part && BH < DECODE_SPLIT_BH) {
+        constexpr int NSL = (K > V ? K : V) / SLICE;
+        hipLaunchKernelGGL((decode_split_a_kernel<K, V, LAYER>), dim3(NSL, BH), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((decode_split_b_kernel<K, V, LAYER>), dim3(BH), dim3(1024), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((decode_step_kernel<K, V, LAYER>), dim3(BH), dim3(1024), 0, stream, p);
+    }
+}
+
+}  // namespace
+
+size_t decode_workspace_bytes(int B, int H, int K, int V) {
+    if (B <= 0 || H <= 0 || (long long)B * H >= DECODE_SPLIT_BH) return 0;
+    return (size_t)B * H * ((K > V ? K : V) / SLICE) * kSlots * sizeof(float);
+}
+
 int launch_decode_step(const DecodeParams& p, int K, int V, hipStream_t stream) {
-    dim3 grid(p.B * p.H), block(1024);
     if (p.qkv) {  // the layer step: K = V = 256 only
         if (K != 256 || V != 256) return -1;
-        hipLaunchKernelGGL((decode_step_kernel<256, 256, true>), grid, block, 0, stream, p);
+        launch<256, 256, true>(p, stream);
     } else if (K == 256 && V == 256)
-        hipLaunchKernelGGL((decode_step_kernel<256, 256, false>), grid, block, 0, stream, p);
+        launch<256, 256, false>(p, stream);
     else if (K == 128 && V == 128)
-        hipLaunchKernelGGL((decode_step_kernel<128, 128, false>), grid, block, 0, stream, p);
+        launch<128, 128, false>(p, stream);
     else if (K == 256 && V == 128)
-        hipLaunchKernelGGL((decode_step_kernel<256, 128, false>), grid, block, 0, stream, p);
+        launch<256, 128, false>(p, stream);
     else if (K == 128 && V == 256)
-        hipLaunchKernelGGL((decode_step_kernel<128, 256, false>), grid, block, 0, stream, p);
+        launch<128, 256, false>(p, stream);
     else
         return -1;
     return 0;

@@ -31,7 +31,15 @@ struct DecodeParams {
     long long gate_row;
     const float* on_w;       // [V]
     float on_eps, on_prescale;
+    // Small batches (B H < DECODE_SPLIT_BH): the workspace for the slices'
+    // partial raw, [B H, max(K, V) / 32, 128] f32; null: one workgroup per (b, h).
+    float* part;
 };
+
+// B H below which a decode step is split across eight workgroups per (b, h).
+constexpr int DECODE_SPLIT_BH = 64;
+// Workspace bytes of the split decode step (0 when B H does not split).
+size_t decode_workspace_bytes(int B, int H, int K, int V);
 
 // Prefill: T is split into N = ceil(T / 64) chunks and every (batch, head)
 // sequence into P segments of L consecutive chunks. Segments run in parallel;

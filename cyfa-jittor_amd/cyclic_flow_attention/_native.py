@@ -14,7 +14,7 @@ import torch
 import torch.nn.functional as F
 
 LIB_PATH = Path(os.environ.get("CYFA_LIB", Path(__file__).with_name("libcyfa_hip.so")))
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 CYFA_OK = 0
 CYFA_ERR_VALUE = -1
@@ -62,6 +62,7 @@ class CyfaDecodeArgs(ctypes.Structure):
         ("q_norm_eps", _c_float), ("k_norm_eps", _c_float), ("scale", _c_float),
         ("hk_in", _c_void_p), ("hv_in", _c_void_p), ("clock_in", _c_void_p),
         ("o", _c_void_p), ("hk_out", _c_void_p), ("hv_out", _c_void_p), ("clock_out", _c_void_p),
+        ("workspace", _c_void_p), ("workspace_bytes", _c_size_t),
     ]
 
 
@@ -122,6 +123,7 @@ SIGNATURES = {
     "cyfa_scalar_la": (_c_int, [ctypes.POINTER(CyfaSlaArgs), _c_void_p]),
     "cyfa_scalar_la_workspace_bytes": (_c_size_t, [_c_int] * 5),
     "cyfa_decode_step": (_c_int, [ctypes.POINTER(CyfaDecodeArgs), _c_void_p]),
+    "cyfa_decode_workspace_bytes": (_c_size_t, [_c_int] * 4),
     "cyfa_decode_layer_step": (_c_int, [ctypes.POINTER(CyfaDecodeArgs), ctypes.POINTER(CyfaDecodeLayerArgs), _c_void_p]),
     "cyfa_readout_table": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "cyfa_rms_norm": (_c_int, [ctypes.POINTER(CyfaNormArgs), _c_void_p]),
@@ -281,6 +283,13 @@ def scalar_la(args: CyfaSlaArgs, device):
     rc = _timed("cyfa_scalar_la", lambda: lib.cyfa_scalar_la(ctypes.byref(args), stream_handle(device)))
     if rc != CYFA_OK:
         _raise(rc, "cyfa_scalar_la failed")
+
+
+def decode_workspace(B, H, K, V, device):
+    """The split decode step's workspace for these dimensions, or None when
+    the step runs one workgroup per (batch, head)."""
+    n = int(load_library().cyfa_decode_workspace_bytes(B, H, K, V))
+    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
 
 
 def decode_step(args: CyfaDecodeArgs, device):

@@ -30,6 +30,7 @@ def fused_recurrent_cyfa(
     *,
     table=None,
     inplace=False,
+    split=False,
 ):
     """Decode one token using constant-size key, value and clock states.
 
@@ -37,6 +38,11 @@ def fused_recurrent_cyfa(
     states are returned as new tensors; ``inplace=True`` (an extension) updates
     the given initial_state tensors instead and returns them. ``table`` (an
     extension) passes a precomputed readout @ Phi to skip rebuilding it.
+    ``split`` (an extension): with B H < 64 the step runs on eight
+    workgroups per (batch, head) in two launches instead of one workgroup per
+    (batch, head) in one. Both give bit-identical results; on MI355X the
+    one-workgroup form is 1-3 us faster at every B H < 64 measured, so it is
+    the default.
     """
     B, T, H, K = q.shape
     V = v.shape[-1]
@@ -84,8 +90,10 @@ def fused_recurrent_cyfa(
         hv_out = torch.empty(B, H, M, V, dtype=torch.float32, device=dev)
         c_out = torch.empty(B, H, dtype=torch.float32, device=dev)
     o = torch.empty(B, 1, H, V, dtype=torch.bfloat16, device=dev)
+    workspace = _native.decode_workspace(B, H, K, V, dev) if split else None  # alive until the launch
     args = _native.CyfaDecodeArgs(
         B=B, H=H, K=K, V=V, M=M,
+        workspace=_native.ptr(workspace), workspace_bytes=0 if workspace is None else workspace.numel(),
         q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(),
         g=g.data_ptr(), delta=delta.data_ptr(), beta=beta.data_ptr(),
         table=table.data_ptr(), q_norm_weight=qw.data_ptr(), k_norm_weight=kw.data_ptr(),
@@ -100,7 +108,7 @@ def fused_recurrent_cyfa(
 
 def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias, A_log, gate, norm_weight, norm_eps,
                       norm_prescale, table, q_norm_weight, k_norm_weight, q_norm_eps, k_norm_eps, num_heads,
-                      initial_state=None, output_final_state=False, inplace=False):
+                      initial_state=None, output_final_state=False, inplace=False, split=False):
     """The layer's one-token step around the op in one kernel (cyfa_decode_layer_step).
 
     qkv [B, 1, 3 H 256] is the projection before the short convolution (rows
@@ -109,7 +117,8 @@ def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias
     conv_cache), conv_weight [3 H 256, 4], abd [B, 1, 3H] the a|b|d projection
     with its biases, gate [B, 1, H 256]. Returns (o', states) with o' the gated
     output norm o_norm(o * norm_prescale, gate) of the op's output, [B, 1, H, 256],
-    and the states as fused_recurrent_cyfa returns them.
+    and the states as fused_recurrent_cyfa returns them. ``split``: as in
+    fused_recurrent_cyfa.
     """
     B = qkv.shape[0]
     H, K, V, M = num_heads, 256, 256, table.shape[-1]
@@ -156,8 +165,10 @@ def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias
         hv_out = torch.empty(B, H, M, V, dtype=torch.float32, device=dev)
         c_out = torch.empty(B, H, dtype=torch.float32, device=dev)
     o = torch.empty(B, 1, H, V, dtype=torch.bfloat16, device=dev)
+    workspace = _native.decode_workspace(B, H, K, V, dev) if split else None  # alive until the launch
     args = _native.CyfaDecodeArgs(
-        B=B, H=H, K=K, V=V, M=M, table=table.data_ptr(), q_norm_weight=qw.data_ptr(), k_norm_weight=kw.data_ptr(),
+        B=B, H=H, K=K, V=V, M=M, table=table.data_ptr(),
+        workspace=_native.ptr(workspace), workspace_bytes=0 if workspace is None else workspace.numel(), q_norm_weight=qw.data_ptr(), k_norm_weight=kw.data_ptr(),
         q_norm_eps=float(q_norm_eps), k_norm_eps=float(k_norm_eps), scale=float(K ** -0.5),
         hk_in=_native.ptr(hk_in), hv_in=_native.ptr(hv_in), clock_in=_native.ptr(c_in),
         o=o.data_ptr(), hk_out=hk_out.data_ptr(), hv_out=hv_out.data_ptr(), clock_out=c_out.data_ptr(),

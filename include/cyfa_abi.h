@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define CYFA_ABI_VERSION 2
+#define CYFA_ABI_VERSION 3
 
 enum {
     CYFA_OK = 0,
@@ -154,7 +154,17 @@ typedef struct CyfaDecodeArgs {
     const float *hk_in, *hv_in, *clock_in; /* nullable (all or none): zero state */
     void *o;                      /* bf16 [B,1,H,V] */
     float *hk_out, *hv_out, *clock_out;    /* required; may alias the inputs */
+    void *workspace;              /* nullable: >= cyfa_decode_workspace_bytes() bytes, 16-byte aligned */
+    size_t workspace_bytes;
 } CyfaDecodeArgs;
+
+/* Workspace bytes that let a decode step with B H < 64 split each (b, h)
+ * across eight workgroups (32 key-state rows and 32 value-state columns
+ * each); 0 when B H >= 64 (one workgroup per (b, h) fills the chip). Without
+ * the workspace the step runs one workgroup per (b, h); both forms give
+ * bit-identical results. No counterpart in the reference (its decode kernel
+ * runs one block per (b, h), ops/fused_recurrent.py:177-185). */
+size_t cyfa_decode_workspace_bytes(int B, int H, int K, int V);
 
 /* One fused constant-memory decode step: q/k RMS norm, clock and write
  * vector, key-state update and query, slot readout, value-state update and

@@ -206,3 +206,14 @@ def test_noalloc_entry_point_refuses_oversize_before_launch():
     assert b"scratch" in lib.cyfa_last_error()
     assert _native.chunk_workspace_bytes(8, 2048, 4, 256, 256) <= _native.NOALLOC_SCRATCH_BYTES
     assert _native.chunk_workspace_bytes(1, 16384, 8, 256, 256) <= _native.NOALLOC_SCRATCH_BYTES
+
+
+def test_decode_workspace_query():
+    """The small-batch decode split needs B H x 8 slices x 128 floats of
+    workspace below B H = 64 and none from there on (host-side query)."""
+    lib = _native.load_library()
+    assert lib.cyfa_decode_workspace_bytes(1, 8, 256, 256) == 8 * 8 * 128 * 4
+    assert lib.cyfa_decode_workspace_bytes(15, 4, 256, 256) == 60 * 8 * 128 * 4
+    assert lib.cyfa_decode_workspace_bytes(16, 4, 256, 256) == 0
+    assert lib.cyfa_decode_workspace_bytes(2, 2, 128, 128) == 4 * 4 * 128 * 4
+    assert lib.cyfa_decode_workspace_bytes(1, 1, 512, 256) == 0  # no kernel for K = 512

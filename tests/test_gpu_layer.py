@@ -343,12 +343,15 @@ def test_norm_linear_rows(M, residual, swiglu, K):
     assert rows <= max(1, M // 10), f"{rows} of {M} rows differ from rms_norm + linear"
 
 
-@pytest.mark.parametrize("B,state,inplace", [(3, True, False), (2, False, False), (4, True, True), (64, True, True)])
-def test_decode_layer_step_equals_separate_kernels(B, state, inplace):
+@pytest.mark.parametrize("B,state,inplace,split", [(3, True, False, True), (2, False, False, True),
+                                                   (4, True, True, True), (64, True, True, True),
+                                                   (3, True, True, False), (1, True, True, True)])
+def test_decode_layer_step_equals_separate_kernels(B, state, inplace, split):
     """cyfa_decode_layer_step (short convolution, gates, decode op and gated
-    output norm in one kernel) against the four separate kernels on the same
-    inputs: the same arithmetic in the same order, so outputs, states and the
-    new conv cache are bit-identical."""
+    output norm in one kernel, or in the two kernels of the small-batch split)
+    against the four separate kernels on the same inputs: the same arithmetic
+    in the same order, so outputs, states and the new conv cache are
+    bit-identical."""
     from cyclic_flow_attention import _native
     from cyclic_flow_attention.ops import fused_recurrent_cyfa
     from cyclic_flow_attention.ops.fused_recurrent import decode_layer_step
@@ -385,7 +388,7 @@ def test_decode_layer_step_equals_separate_kernels(B, state, inplace):
         st_in = None if init is None else tuple(t.clone() for t in init)
         got, st2 = decode_layer_step(qkv, cache_in, tail, wconv, abd, dt_bias, A_log, gate, nw, 1e-6, 127.0, table, qw,
                                      kw, 1e-6, 1e-6, H, initial_state=st_in, output_final_state=True,
-                                     inplace=inplace and st_in is not None)
+                                     inplace=inplace and st_in is not None, split=split)
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
     assert torch.equal(tail, tail_ref)

@@ -346,3 +346,28 @@ def test_decode_refuses_host_tensors_before_launch():
         fused_recurrent_cyfa(**xg, initial_state=init)
     with pytest.raises(ValueError):
         fused_recurrent_cyfa(**xg, table=torch.zeros(2, 127, 128, dtype=torch.bfloat16, device=DEV))
+
+
+@pytest.mark.parametrize("B,H,K,V", [(1, 8, 256, 256), (3, 2, 256, 256), (2, 3, 128, 256), (1, 4, 256, 128),
+                                     (5, 1, 128, 128), (15, 4, 256, 256)])
+def test_decode_split_equals_one_workgroup_form(B, H, K, V):
+    """Small batches (B H < 64) split each (b, h) across eight workgroups;
+    the split form and the one-workgroup form give bit-identical outputs and
+    states (raw and o are reduced in the same order in both), in place as
+    well, and match the oracle."""
+    from cyclic_flow_attention.ops import fused_recurrent_cyfa
+
+    x, init = _inputs(B, 1, H, K, V, seed=B * 7 + H, state=True, clock_scale=1e4)
+    xg, ig = _gpu(x, init)
+    with torch.no_grad():
+        o1, st1 = fused_recurrent_cyfa(**xg, initial_state=ig, output_final_state=True, split=False)
+        o2, st2 = fused_recurrent_cyfa(**xg, initial_state=ig, output_final_state=True, split=True)
+        buf = tuple(t.clone() for t in ig)
+        o3, st3 = fused_recurrent_cyfa(**xg, initial_state=buf, output_final_state=True, inplace=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(o1, o3)
+    for a, b, c in zip(st1, st2, st3):
+        assert torch.equal(a, b) and torch.equal(a, c)
+    ro, rst = O.fused_recurrent_cyfa(**_oracle(x, init)[0], initial_state=_oracle(x, init)[1], output_final_state=True)
+    assert_close(o2, ro, what=f"split decode o B{B} H{H}")
+    _check_states(st2, rst, "split decode")
