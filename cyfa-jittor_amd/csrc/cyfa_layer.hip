@@ -77,75 +77,95 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormParams p) {
 // modeling_cyfa.py). At these shapes a library GEMM tiles M into large blocks
 // and leaves most of the chip idle. Here a workgroup of 8 waves computes one
 // tile of RT x 16 rows by CT x 16 columns over the whole of K, on
-// v_mfma_f32_16x16x32_bf16 (A = x rows, B = W rows read straight from global
-// memory: lane (lr, lg) loads 8 consecutive k of row lr). Wave w takes a
-// contiguous run of the 32-deep k-steps, so its loads of a row cover whole
-// cache lines, with the loads of several steps in flight; the eight partial
-// tiles are summed in LDS in wave order. Every output element is therefore
-// summed in the same order whatever the tile shape, so the launcher may pick
-// the shape per call (launch_linear_rows) without changing a bit of y.
+// v_mfma_f32_16x16x32_bf16 (A = x rows, B = W rows). Wave w takes a contiguous
+// run of the 32-deep k-steps, with the loads of several steps in flight; the
+// eight partial tiles are summed in LDS in wave order. Every output element is
+// therefore summed in the same order whatever the tile shape, so the launcher
+// may pick the shape per call (launch_linear_rows) without changing a bit of y.
+//
+// Operand loads. An MFMA operand wants lane (lr, lg) to hold 8 consecutive k
+// of row lr, so a load in that layout touches 16 rows x 64 bytes; on MI355X
+// such loads move data at about half the rate of loads that cover whole
+// 128-byte lines (a 64-row x 1024 x 5632 tile read: 8.5 us against 4.9 us).
+// So a wave loads each pair of k-steps as whole lines, 8 rows x 128 bytes per
+// instruction, writes them to its own LDS region (rows LIN_STRIDE bytes apart,
+// so that the 16 rows of an operand read fall in 16 distinct bank groups) and
+// reads the operands back in MFMA layout. No other wave touches the region, so
+// no barrier is needed: a wave's LDS accesses complete in order.
 // Rows of x at or past M and rows of W at or past N read as zero (buffer
 // bounds).
 typedef __amdgpu_buffer_rsrc_t lin_rsrc_t;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int LIN_STRIDE = 144;  // staged row: 128 bytes (two k-steps) + 16 bytes of padding
+
+__device__ __forceinline__ float bf16_bits_to_float(unsigned short b) { return __uint_as_float((uint32_t)b << 16); }
 
 __device__ __forceinline__ lin_rsrc_t lin_rsrc(const void* base, size_t bytes) {
     const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
 }
 
-__device__ __forceinline__ bf16x8 lin_ld(lin_rsrc_t r, uint32_t off) {
-    return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
+// The most k-step pairs whose loads a wave has in flight together, about 24
+// loads per lane: P <= lin_pairs(RT, CT).
+__host__ __device__ constexpr int lin_pairs(int rt, int ct) { return rt + ct <= 2 ? 6 : rt + ct <= 3 ? 4 : rt + ct <= 4 ? 3 : 2; }
 
-// k-steps whose loads a wave has in flight together: about 24 loads per lane
-__host__ __device__ constexpr int lin_batch(int rt, int ct) { return rt + ct <= 2 ? 12 : rt + ct <= 3 ? 8 : rt + ct <= 4 ? 6 : 4; }
+// The offset of a load that must return zero: past the end of every buffer
+// the kernel reads (launch_linear_rows keeps each span below 2^31 bytes).
+// Loads are predicated through their offset rather than a branch, so that no
+// divergent branch sits among the loads: at such a branch the compiler waits
+// for every load in flight.
+constexpr uint32_t LIN_DEAD = 0x80000000u;
 
-template <int U, int RT, int CT>
-__device__ __forceinline__ void lin_issue_w(lin_rsrc_t rw, int s, int s1, uint32_t wrow, uint32_t wstride, int lg,
-                                           bf16x8 (&wf)[U][CT]) {
+// The loads of k-steps s and s + 1 for G groups of 16 rows (row stride rs
+// bytes), as whole lines: instruction i, lane l reads row 8 i + l / 8, the
+// 16-byte chunk l % 8 of the row's 128 bytes. Chunks of a step at or past s1
+// read zero.
+template <int G>
+__device__ __forceinline__ void lin_load_pair(lin_rsrc_t r, uint32_t rs, int s, int s1, int lane,
+                                              u32x4 (&raw)[2 * G]) {
+    const int cl = lane & 7;
+    // LIN_DEAD (bit 31) when the chunk's step is at or past s1: the sign bit of
+    // s + cl / 4 - s1 is set exactly when the step is live. Written as integer
+    // arithmetic; a select here was turned into a divergent branch per load.
+    const uint32_t dead = (~(uint32_t)(s + (cl >> 2) - s1)) & LIN_DEAD;
+    const uint32_t col = ((uint32_t)(32 * s + 8 * cl) * 2) | dead;
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-        if (s + u < s1) {
-            const uint32_t kb = (uint32_t)(32 * (s + u) + 8 * lg) * 2;
-#pragma unroll
-            for (int c = 0; c < CT; c++) wf[u][c] = lin_ld(rw, wrow + c * wstride + kb);
-        }
+    for (int i = 0; i < 2 * G; i++) {
+        const uint32_t row = 8 * i + (lane >> 3);
+        raw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, row * rs + col, 0, 0));
     }
 }
 
-template <int U, int RT>
-__device__ __forceinline__ void lin_issue_x(lin_rsrc_t rx, int s, int s1, uint32_t xrow, uint32_t xstride, int lg,
-                                            bf16x8 (&xf)[U][RT]) {
+// Writes the chunks of lin_load_pair to rows [0, 16 G) of a staging region.
+template <int G>
+__device__ __forceinline__ void lin_stage_pair(char* region, int lane, const u32x4 (&raw)[2 * G]) {
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-        if (s + u < s1) {
-            const uint32_t kb = (uint32_t)(32 * (s + u) + 8 * lg) * 2;
-#pragma unroll
-            for (int rt = 0; rt < RT; rt++) xf[u][rt] = lin_ld(rx, xrow + rt * xstride + kb);
-        }
-    }
+    for (int i = 0; i < 2 * G; i++)
+        *reinterpret_cast<u32x4*>(region + (8 * i + (lane >> 3)) * LIN_STRIDE + 16 * (lane & 7)) = raw[i];
 }
 
-template <int U, int RT, int CT>
-__device__ __forceinline__ void lin_mfma(int s, int s1, const bf16x8 (&wf)[U][CT], const bf16x8 (&xf)[U][RT],
-                                         f32x4 (&acc)[RT][CT]) {
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-        if (s + u < s1) {
-#pragma unroll
-            for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-                for (int c = 0; c < CT; c++)
-                    acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[u][rt], wf[u][c], acc[rt][c], 0, 0, 0);
-        }
-    }
+// The MFMA operand of staged step u (0 or 1) for rows 16 g .. 16 g + 15:
+// lane (lr, lg) gets row 16 g + lr, k = 8 lg .. 8 lg + 7 of the step.
+__device__ __forceinline__ bf16x8 lin_frag(const char* region, int g, int u, int lr, int lg) {
+    return *reinterpret_cast<const bf16x8*>(region + (16 * g + lr) * LIN_STRIDE + 16 * (4 * u + lg));
 }
 
-template <int RT, int CT, bool NORM>
+// A wave's k-run is processed in batches of P pairs of k-steps; every load of
+// a batch is issued, unconditionally, before the first is used (a load behind
+// a branch, even a uniform one, makes the compiler's wait counts assume the
+// worst and wait for loads issued later). The launcher picks P from the run's
+// length (linear_pairs), so few loads fall past the run.
+template <int RT, int CT, int P, bool NORM>
 __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
     constexpr int TM = 16 * RT, TN = 16 * CT, OUT = TM * TN, R = (OUT + 511) / 512;
-    constexpr int U = lin_batch(RT, CT);
-    __shared__ float part[8][TM][TN + 1];
+    constexpr int U = 2 * P;  // k-steps per batch
+    static_assert(P >= 1 && P <= lin_pairs(RT, CT), "loads in flight per lane");
+    constexpr int STAGE = (TM + TN) * LIN_STRIDE;  // one wave's staging region: x rows, then W rows
+    constexpr int PART = 8 * TM * (TN + 1) * 4;    // the eight waves' partial tiles, after the product
+    constexpr int LDS = 8 * STAGE > PART ? 8 * STAGE : PART;
+    __shared__ __align__(16) char lds[LDS];
+    float(*part)[TM][TN + 1] = reinterpret_cast<float(*)[TM][TN + 1]>(lds);
     __shared__ float sq[NORM ? 8 : 1][NORM ? TM : 1];
     __shared__ float4 snw[NORM ? LINEAR_NORM_MAX_K / 4 : 1];
     // The wave index comes from a scalar register, so the k-run bounds and
@@ -155,18 +175,12 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
     // build picked up stale operand registers (NaNs on MI355X).
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lr = lane & 15,
               lg = lane >> 4;
+    char* const xreg = lds + w * STAGE;
+    char* const wreg = xreg + TM * LIN_STRIDE;
     const int n0 = blockIdx.x * TN, m0 = blockIdx.y * TM;
     const int mrows = min(TM, p.M - m0);
     const lin_rsrc_t rx = lin_rsrc(p.x + (size_t)m0 * p.ldx, ((size_t)(mrows - 1) * p.ldx + p.K) * 2);
     const lin_rsrc_t rw = lin_rsrc(p.w + (size_t)n0 * p.K, (size_t)min(TN, p.N - n0) * p.K * 2);
-    // the bias and the residual of this thread's outputs, loaded with the operands
-    float bias[R], add[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const int idx = threadIdx.x + 512 * r, n = n0 + idx % TN, m = idx / TN;
-        bias[r] = p.bias && n < p.N ? (float)p.bias[n] : 0.f;
-        add[r] = p.add && n < p.N && idx < OUT && m < mrows ? (float)p.add[(size_t)(m0 + m) * p.ld_add + n] : 0.f;
-    }
     f32x4 acc[RT][CT];
 #pragma unroll
     for (int rt = 0; rt < RT; rt++)
@@ -174,35 +188,100 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
         for (int c = 0; c < CT; c++) acc[rt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int steps = p.K / 32, per = (steps + 7) / 8;
     const int s0 = min(steps, w * per), s1 = min(steps, s0 + per);
-    const uint32_t wrow = (uint32_t)lr * p.K * 2, xrow = (uint32_t)lr * (uint32_t)p.ldx * 2;
-    const uint32_t xstride = (uint32_t)(16 * p.ldx * 2), wstride = (uint32_t)(16 * p.K * 2);
-    bf16x8 wf[U][CT], xf[U][RT];
+    const uint32_t xrs = (uint32_t)p.ldx * 2, wrs = (uint32_t)p.K * 2;
+    // the bias and the residual of this thread's outputs, loaded first (a null
+    // pointer gets an empty buffer: every load of it reads zero)
+    const lin_rsrc_t rb = lin_rsrc(p.bias, p.bias ? (size_t)p.N * 2 : 0);
+    const lin_rsrc_t ra =
+        lin_rsrc(p.add ? p.add + (size_t)m0 * p.ld_add : nullptr, p.add ? ((size_t)(mrows - 1) * p.ld_add + p.N) * 2 : 0);
+    float bias[R], add[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int idx = threadIdx.x + 512 * r, n = n0 + idx % TN, m = idx / TN;
+        const uint32_t dead = (idx < OUT && m < mrows) ? 0u : LIN_DEAD;
+        bias[r] = bf16_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(rb, (uint32_t)n * 2, 0, 0));
+        add[r] = bf16_bits_to_float(
+            __builtin_amdgcn_raw_buffer_load_b16(ra, ((uint32_t)(m * p.ld_add + n) * 2) | dead, 0, 0));
+    }
     if constexpr (!NORM) {
         for (int s = s0; s < s1; s += U) {
-            lin_issue_w<U, RT, CT>(rw, s, s1, wrow, wstride, lg, wf);
-            lin_issue_x<U, RT>(rx, s, s1, xrow, xstride, lg, xf);
-            lin_mfma<U, RT, CT>(s, s1, wf, xf, acc);
+            u32x4 rawx[P][2 * RT], raww[P][2 * CT];
+#pragma unroll
+            for (int h = 0; h < P; h++) {
+                lin_load_pair<RT>(rx, xrs, s + 2 * h, s1, lane, rawx[h]);
+                lin_load_pair<CT>(rw, wrs, s + 2 * h, s1, lane, raww[h]);
+            }
+#pragma unroll
+            for (int h = 0; h < P; h++) {
+                if (s + 2 * h < s1) {
+                    lin_stage_pair<RT>(xreg, lane, rawx[h]);
+                    lin_stage_pair<CT>(wreg, lane, raww[h]);
+#pragma unroll
+                    for (int u = 0; u < 2; u++) {
+                        if (s + 2 * h + u < s1) {
+                            bf16x8 xf[RT], wf[CT];
+#pragma unroll
+                            for (int rt = 0; rt < RT; rt++) xf[rt] = lin_frag(xreg, rt, u, lr, lg);
+#pragma unroll
+                            for (int c = 0; c < CT; c++) wf[c] = lin_frag(wreg, c, u, lr, lg);
+#pragma unroll
+                            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                                for (int c = 0; c < CT; c++)
+                                    acc[rt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[rt], wf[c], acc[rt][c], 0, 0, 0);
+                        }
+                    }
+                }
+            }
         }
     } else {
-        // The row norm (the launcher guarantees one batch: K <= 256 U). Lane
+        // The row norm (the launcher guarantees one batch: per <= U). Lane
         // (lr, lg) holds 8 columns of row 16 rt + lr per k-step, the same
         // columns in every tile shape. Its sum of squares runs over its
         // k-steps in order, then over the row's four lanes (xor 16, xor 32)
         // and the eight waves in wave order.
-        // x (and the residual) first, then the norm weight, then W: loads
-        // complete in order, so the norm waits for x alone while W streams in.
+        // x and the norm weight first, then W, then (when given) the residual:
+        // loads complete in order, so the norm waits for x while W streams in.
         const bool res = p.norm_residual != nullptr;
-        lin_issue_x<U, RT>(rx, s0, s1, xrow, xstride, lg, xf);
-        bf16x8 rf[U][RT];
+        u32x4 rawx[P][2 * RT], rawr[P][2 * RT], raww[P][2 * CT];
+#pragma unroll
+        for (int h = 0; h < P; h++) lin_load_pair<RT>(rx, xrs, s0 + 2 * h, s1, lane, rawx[h]);
+        // the norm weight: K <= 2048, one float4 per thread (zero past K)
+        const float4 nwv = __builtin_bit_cast(
+            float4, __builtin_amdgcn_raw_buffer_load_b128(lin_rsrc(p.norm_weight, (size_t)p.K * 4), 16 * threadIdx.x, 0, 0));
+#pragma unroll
+        for (int h = 0; h < P; h++) lin_load_pair<CT>(rw, wrs, s0 + 2 * h, s1, lane, raww[h]);
         if (res) {
             const lin_rsrc_t rr =
                 lin_rsrc(p.norm_residual + (size_t)m0 * p.ldr, ((size_t)(mrows - 1) * p.ldr + p.K) * 2);
-            lin_issue_x<U, RT>(rr, s0, s1, (uint32_t)lr * (uint32_t)p.ldr * 2, (uint32_t)(16 * p.ldr * 2), lg, rf);
+#pragma unroll
+            for (int h = 0; h < P; h++) lin_load_pair<RT>(rr, (uint32_t)p.ldr * 2, s0 + 2 * h, s1, lane, rawr[h]);
         }
-        const bool has_nw = 4 * (int)threadIdx.x < p.K;  // K <= 2048: one float4 per thread at most
-        float4 nwv = float4{0.f, 0.f, 0.f, 0.f};
-        if (has_nw) nwv = reinterpret_cast<const float4*>(p.norm_weight)[threadIdx.x];
-        lin_issue_w<U, RT, CT>(rw, s0, s1, wrow, wstride, lg, wf);
+        bf16x8 xf[U][RT], rf[U][RT];
+#pragma unroll
+        for (int h = 0; h < P; h++) {
+            if (s0 + 2 * h < s1) {
+                lin_stage_pair<RT>(xreg, lane, rawx[h]);
+#pragma unroll
+                for (int u = 0; u < 2; u++)
+                    if (s0 + 2 * h + u < s1)
+#pragma unroll
+                        for (int rt = 0; rt < RT; rt++) xf[2 * h + u][rt] = lin_frag(xreg, rt, u, lr, lg);
+            }
+        }
+        if (res) {
+#pragma unroll
+            for (int h = 0; h < P; h++) {
+                if (s0 + 2 * h < s1) {
+                    lin_stage_pair<RT>(xreg, lane, rawr[h]);
+#pragma unroll
+                    for (int u = 0; u < 2; u++)
+                        if (s0 + 2 * h + u < s1)
+#pragma unroll
+                            for (int rt = 0; rt < RT; rt++) rf[2 * h + u][rt] = lin_frag(xreg, rt, u, lr, lg);
+                }
+            }
+        }
         if (res) {
             // s = bf16(x + residual); the first column of workgroups writes it out
 #pragma unroll
@@ -219,7 +298,7 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
                 }
             }
         }
-        if (has_nw) snw[threadIdx.x] = nwv;
+        snw[threadIdx.x] = nwv;
         float ss[RT];
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
@@ -253,8 +332,28 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
                 }
             }
         }
-        lin_mfma<U, RT, CT>(s0, s1, wf, xf, acc);
+#pragma unroll
+        for (int h = 0; h < P; h++) {
+            if (s0 + 2 * h < s1) {
+                lin_stage_pair<CT>(wreg, lane, raww[h]);
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    if (s0 + 2 * h + u < s1) {
+                        bf16x8 wf[CT];
+#pragma unroll
+                        for (int c = 0; c < CT; c++) wf[c] = lin_frag(wreg, c, u, lr, lg);
+#pragma unroll
+                        for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                            for (int c = 0; c < CT; c++)
+                                acc[rt][c] =
+                                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[2 * h + u][rt], wf[c], acc[rt][c], 0, 0, 0);
+                    }
+                }
+            }
+        }
     }
+    __syncthreads();  // the partial tiles overwrite the staging regions
     // acc[rt][c][i] = partial y[m0 + 16 rt + 4 lg + i][n0 + 16 c + lr]
 #pragma unroll
     for (int rt = 0; rt < RT; rt++)
@@ -490,6 +589,28 @@ int launch_rms_norm(const NormParams& p, hipStream_t stream) {
     return 0;
 }
 
+// linear_rows_kernel<RT, CT, P, NORM> for P pairs per batch, rounded up to
+// an instantiated count (1, 2, 3, 4, 6) within the shape's limit.
+template <int RT, int CT, bool NORM>
+static void launch_rows(const LinearParams& p, int pairs, dim3 grid, hipStream_t stream) {
+    constexpr int cap = lin_pairs(RT, CT);
+    const dim3 block(512);
+    if (pairs <= 1) {
+        hipLaunchKernelGGL((linear_rows_kernel<RT, CT, 1, NORM>), grid, block, 0, stream, p);
+    } else if (pairs == 2 || cap == 2) {
+        hipLaunchKernelGGL((linear_rows_kernel<RT, CT, 2, NORM>), grid, block, 0, stream, p);
+    } else if constexpr (cap >= 3) {
+        if (pairs == 3 || cap == 3) {
+            hipLaunchKernelGGL((linear_rows_kernel<RT, CT, 3, NORM>), grid, block, 0, stream, p);
+        } else if constexpr (cap >= 4) {
+            if (pairs == 4 || cap == 4)
+                hipLaunchKernelGGL((linear_rows_kernel<RT, CT, 4, NORM>), grid, block, 0, stream, p);
+            else if constexpr (cap >= 6)
+                hipLaunchKernelGGL((linear_rows_kernel<RT, CT, 6, NORM>), grid, block, 0, stream, p);
+        }
+    }
+}
+
 // The tile shape of linear_rows_kernel for one call. Each workgroup reads
 // 16 (RT + CT) rows of K (RT x 16 rows of x and CT x 16 rows of W), and at
 // these sizes a CU's read rate, not the chip's, is the limit; one workgroup
@@ -498,7 +619,7 @@ int launch_rms_norm(const NormParams& p, hipStream_t stream) {
 // (on MI355X: 28 -> 35 k tok/s for the 400M decode step at B=64 against a
 // fixed 4 x 2 tile). The SwiGLU epilogue needs CT = 2, the 16 gate and 16 up
 // columns of one interleaved group; the row norm needs each wave's k-steps in
-// one batch of loads (K <= 256 lin_batch). False when no shape qualifies.
+// one batch of loads (K <= 512 lin_pairs). False when no shape qualifies.
 static bool linear_tile(int M, int N, bool swiglu, int norm_k, int& rt_out, int& ct_out) {
     static const int shapes[][2] = {{4, 4}, {4, 2}, {2, 4}, {4, 1}, {2, 2}, {1, 4}, {2, 1}, {1, 2}, {1, 1}};
     long long best = -1;
@@ -508,7 +629,7 @@ static bool linear_tile(int M, int N, bool swiglu, int norm_k, int& rt_out, int&
         const int rt = sh[0], ct = sh[1];
         if (swiglu && ct != 2) continue;
         if (norm_k && rt * ct > 8) continue;  // no fused-norm build of the 64 x 64 tile (its registers would spill)
-        if (norm_k > 256 * lin_batch(rt, ct)) continue;  // the norm needs all of a row in one batch
+        if (norm_k > 512 * lin_pairs(rt, ct)) continue;  // the norm needs all of a row in one batch
         const long long groups = (long long)((M + 16 * rt - 1) / (16 * rt)) * ((N + 16 * ct - 1) / (16 * ct));
         const long long cost = (groups + 255) / 256 * (rt + ct);
         if (best < 0 || cost < best) {
@@ -522,20 +643,28 @@ static bool linear_tile(int M, int N, bool swiglu, int norm_k, int& rt_out, int&
 
 int launch_linear_rows(const LinearParams& p, hipStream_t stream) {
     if (p.M < 1 || p.M > 64 || (p.norm_weight && p.K > LINEAR_NORM_MAX_K)) return -1;
+    // every buffer the kernel reads spans less than LIN_DEAD bytes (so that
+    // offset reads zero) and every in-buffer offset fits 32 bits
+    const auto span = [&](long long ld, long long cols) { return ((unsigned long long)(p.M - 1) * ld + cols) * 2; };
+    if (p.K > (1 << 20) || span(p.ldx, p.K) >= LIN_DEAD || (p.add && span(p.ld_add, p.N) >= LIN_DEAD) ||
+        (p.norm_residual && span(p.ldr, p.K) >= LIN_DEAD) || (p.bias && (unsigned long long)p.N * 2 >= LIN_DEAD))
+        return -1;
     int rt, ct;
     if (!linear_tile(p.M, p.N, p.swiglu != 0, p.norm_weight ? p.K : 0, rt, ct)) return -1;
-    const dim3 grid((p.N + 16 * ct - 1) / (16 * ct), (p.M + 16 * rt - 1) / (16 * rt)), block(512);
+    const dim3 grid((p.N + 16 * ct - 1) / (16 * ct), (p.M + 16 * rt - 1) / (16 * rt));
+    // k-step pairs per batch: the whole of a wave's run when the shape allows it
+    const int per = (p.K / 32 + 7) / 8, pairs = min((per + 1) / 2, lin_pairs(rt, ct));
     const bool norm = p.norm_weight != nullptr;
 #define CYFA_LINEAR(RT_, CT_)                                                                                  \
     if (rt == RT_ && ct == CT_) {                                                                              \
         if (norm)                                                                                              \
-            hipLaunchKernelGGL((linear_rows_kernel<RT_, CT_, true>), grid, block, 0, stream, p);              \
+            launch_rows<RT_, CT_, true>(p, pairs, grid, stream);                                               \
         else                                                                                                   \
-            hipLaunchKernelGGL((linear_rows_kernel<RT_, CT_, false>), grid, block, 0, stream, p);             \
+            launch_rows<RT_, CT_, false>(p, pairs, grid, stream);                                              \
         return 0;                                                                                              \
     }
     if (rt == 4 && ct == 4 && !norm) {  // the lm_head's tile at 64 rows (N = 32000: 500 workgroups)
-        hipLaunchKernelGGL((linear_rows_kernel<4, 4, false>), grid, block, 0, stream, p);
+        launch_rows<4, 4, false>(p, pairs, grid, stream);
         return 0;
     }
     CYFA_LINEAR(4, 2)
