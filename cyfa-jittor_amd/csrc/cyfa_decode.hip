@@ -30,13 +30,6 @@
 
 namespace cyfa {
 
-// The states are touched exactly once per step: non-temporal loads and stores
-// keep them from displacing reusable lines in the caches (about 20% faster
-// at B = 64 with the state streaming from HBM).
-__device__ __forceinline__ float4 stream_load(const float4* p) {
-    return __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p)));
-}
-
 __device__ __forceinline__ void stream_store(float4* p, const float4& v) {
     __builtin_nontemporal_store(__builtin_bit_cast(f32x4, v), reinterpret_cast<f32x4*>(p));
 }
@@ -44,6 +37,44 @@ __device__ __forceinline__ void stream_store(float4* p, const float4& v) {
 namespace {
 
 constexpr int SLICE = 32;  // hk rows / hv columns per slice
+
+// Loads. Every load of a kernel is issued before the first is used, small
+// inputs first: loads complete in order, so the prologue waits for those
+// alone while the state streams are in flight. Loads go through buffer
+// resources and are predicated through their offset, never a branch: at a
+// branch among loads (even a uniform one) the compiler waits for every load
+// in flight. DEAD is an offset past the end of every buffer read here
+// (launch_decode_step keeps each span below 2^31 bytes), so its load returns
+// zero; a null base gets an empty buffer, whose every load returns zero.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t DEAD = 0x80000000u;
+
+__device__ __forceinline__ rsrc_t buf(const void* base, size_t bytes) {
+    const uint32_t n = base == nullptr ? 0u : bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
+
+// DEAD unless a < b (integer arithmetic: a select here can become a branch)
+__device__ __forceinline__ uint32_t dead_unless_below(int a, int b) { return (~(uint32_t)(a - b)) & DEAD; }
+
+__device__ __forceinline__ float ld_bf16(rsrc_t r, uint32_t off) {
+    return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0) << 16);
+}
+__device__ __forceinline__ float ld_f32(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ bf16x4 ld_bf16x4(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+__device__ __forceinline__ float4 ld_f32x4(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+// The states are touched exactly once per step: non-temporal loads and stores
+// keep them from displacing reusable lines in the caches (about 20% faster
+// at B = 64 with the state streaming from HBM).
+__device__ __forceinline__ float4 stream_load(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+}
 
 // The one-token inputs of (b, h): q and k channel c (< K) or v channel c (< V)
 // of this head. LAYER: from the width-4 causal short convolution of the
@@ -54,13 +85,29 @@ struct ConvIn {
     float win[4], wt[4];
 };
 
-__device__ __forceinline__ ConvIn load_conv(const DecodeParams& p, int b, int ch) {
+// The buffers of batch row b's conv inputs: the cache rows (empty without a
+// cache), the projection row and the conv weights; D = 2 H K + H V channels.
+struct ConvSrc {
+    rsrc_t cache, qkv, w;
+    uint32_t row;  // cache row stride, bytes
+};
+
+__device__ __forceinline__ ConvSrc conv_src(const DecodeParams& p, int b, int D) {
+    ConvSrc c;
+    c.cache = buf(p.cache_in ? p.cache_in + (size_t)b * p.cache_batch : nullptr, ((size_t)2 * p.cache_row + D) * 2);
+    c.qkv = buf(p.qkv + (size_t)b * p.qkv_row, (size_t)D * 2);
+    c.w = buf(p.conv_w, (size_t)D * 8);
+    c.row = (uint32_t)p.cache_row * 2;
+    return c;
+}
+
+// Channel ch's window and weights (all zero when dead is DEAD).
+__device__ __forceinline__ ConvIn load_conv(const ConvSrc& src, int ch, uint32_t dead) {
     ConvIn c;
 #pragma unroll
-    for (int w = 0; w < 3; w++)
-        c.win[w] = p.cache_in ? (float)p.cache_in[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch] : 0.f;
-    c.win[3] = (float)p.qkv[(size_t)b * p.qkv_row + ch];
-    const bf16x4 wt = *reinterpret_cast<const bf16x4*>(p.conv_w + (size_t)ch * 4);  // one 8-byte load
+    for (int w = 0; w < 3; w++) c.win[w] = ld_bf16(src.cache, (w * src.row + (uint32_t)ch * 2) | dead);
+    c.win[3] = ld_bf16(src.qkv, ((uint32_t)ch * 2) | dead);
+    const bf16x4 wt = ld_bf16x4(src.w, ((uint32_t)ch * 8) | dead);  // one 8-byte load
 #pragma unroll
     for (int w = 0; w < 4; w++) c.wt[w] = (float)wt[w];
     return c;
@@ -73,29 +120,100 @@ __device__ __forceinline__ float conv_out(const ConvIn& c) {
     return bf16_round(acc);
 }
 
-// The new conv cache of a channel: the last three rows of its window.
-__device__ __forceinline__ void store_conv_cache(const DecodeParams& p, int b, int ch, const ConvIn& c) {
-#pragma unroll
-    for (int w = 0; w < 3; w++)
-        p.cache_out[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch] = (bf16_t)c.win[w + 1];
+// The new conv cache of a channel: the last three rows of its window, through
+// the cache_out rows of batch row b (a store at a DEAD offset is dropped; the
+// stores are predicated like the loads, since a store behind a branch makes
+// later wait counts assume it was not issued and wait for loads past it).
+__device__ __forceinline__ rsrc_t conv_out_rows(const DecodeParams& p, int b, int D) {
+    return buf(p.cache_out + (size_t)b * p.cache_batch, ((size_t)2 * p.cache_row + D) * 2);
 }
 
-// Gate activations of (b, h) (layers/cyfa.py:323-326, as gates_kernel) or the given gates.
+__device__ __forceinline__ void store_conv_cache(rsrc_t out, uint32_t row, int ch, uint32_t dead, const ConvIn& c) {
+#pragma unroll
+    for (int w = 0; w < 3; w++)
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (bf16_t)c.win[w + 1]), out,
+                                              (w * row + (uint32_t)ch * 2) | dead, 0, 0);
+}
+
+// Gate inputs of (b, h): LAYER, the a, b, d projections (the activations
+// follow in gate_values); otherwise g, delta, beta themselves.
+struct GateIn {
+    float x0, x1, x2, dt_bias, A_log, clock;  // clock: the incoming clock (0 without a state)
+};
+
 template <bool LAYER>
-__device__ __forceinline__ void load_gates(const DecodeParams& p, int bh, float& g, float& delta, float& beta) {
+__device__ __forceinline__ GateIn load_gate_inputs(const DecodeParams& p, int bh) {
+    GateIn gi;
+    const int b = bh / p.H, h = bh % p.H;
     if (LAYER) {
-        const int b = bh / p.H, h = bh % p.H;
-        const bf16_t* row = p.abd + (size_t)b * p.abd_row;
-        const float a = (float)row[h] + p.dt_bias[h];
-        const float sp = a > 20.f ? a : log1pf(expf(a));
-        g = -expf(p.A_log[h]) * sp;
-        beta = sigmoidf((float)row[p.H + h]);
-        delta = sigmoidf((float)row[2 * p.H + h]);
+        const rsrc_t r = buf(p.abd + (size_t)b * p.abd_row, (size_t)3 * p.H * 2);
+        gi.x0 = ld_bf16(r, (uint32_t)h * 2);
+        gi.x1 = ld_bf16(r, (uint32_t)(p.H + h) * 2);
+        gi.x2 = ld_bf16(r, (uint32_t)(2 * p.H + h) * 2);
+        gi.dt_bias = ld_f32(buf(p.dt_bias, (size_t)p.H * 4), (uint32_t)h * 4);
+        gi.A_log = ld_f32(buf(p.A_log, (size_t)p.H * 4), (uint32_t)h * 4);
     } else {
-        g = p.g[bh];
-        delta = p.delta[bh];
-        beta = p.beta[bh];
+        gi.x0 = ld_f32(buf(p.g, (size_t)(bh + 1) * 4), (uint32_t)bh * 4);
+        gi.x1 = ld_f32(buf(p.delta, (size_t)(bh + 1) * 4), (uint32_t)bh * 4);
+        gi.x2 = ld_f32(buf(p.beta, (size_t)(bh + 1) * 4), (uint32_t)bh * 4);
+        gi.dt_bias = gi.A_log = 0.f;
     }
+    gi.clock = ld_f32(buf(p.hk_in != nullptr ? p.clock_in : nullptr, (size_t)(bh + 1) * 4), (uint32_t)bh * 4);
+    return gi;
+}
+
+// Gate activations (layers/cyfa.py:323-326, as gates_kernel) or the given gates.
+template <bool LAYER>
+__device__ __forceinline__ void gate_values(const DecodeParams& p, int bh, const GateIn& gi, float& g, float& delta,
+                                            float& beta) {
+    if (LAYER) {
+        const float a = gi.x0 + gi.dt_bias;
+        const float sp = a > 20.f ? a : log1pf(expf(a));
+        g = -expf(gi.A_log) * sp;
+        beta = sigmoidf(gi.x1);
+        delta = sigmoidf(gi.x2);
+    } else {
+        g = gi.x0;
+        delta = gi.x1;
+        beta = gi.x2;
+    }
+}
+
+// Wave 0's norm weight and gate for the output norm (LAYER): four
+// consecutive values per lane, as rms_norm_kernel<1> holds them.
+template <int V, bool LAYER>
+__device__ __forceinline__ void load_norm_inputs(const DecodeParams& p, int bh, float4* on_w4, bf16x4* on_g4) {
+    constexpr int OJ = (V + 255) / 256;
+    if (LAYER) {
+        const int lane = threadIdx.x & 63;
+        const uint32_t dead = dead_unless_below(threadIdx.x >> 6, 1);
+        const rsrc_t rn = buf(p.on_w, (size_t)V * 4);
+        const rsrc_t rg = buf(p.gate + (size_t)(bh / p.H) * p.gate_row + (size_t)(bh % p.H) * V, (size_t)V * 2);
+#pragma unroll
+        for (int j = 0; j < OJ; j++) {
+            on_w4[j] = ld_f32x4(rn, ((uint32_t)(4 * lane + 256 * j) * 4) | dead);
+            on_g4[j] = ld_bf16x4(rg, ((uint32_t)(4 * lane + 256 * j) * 2) | dead);
+        }
+    }
+}
+
+// The head's readout table, [kActive, kSlots] f32, 4 float4 per thread of a
+// 1024-thread workgroup (zero past its end); staged in LDS by stage_table.
+constexpr int TQ = kActive * kSlots / 4;
+static_assert(TQ > 3 * 1024 && TQ <= 4 * 1024, "table staging covers the table");
+
+__device__ __forceinline__ void load_table(const DecodeParams& p, int h, float4 (&tab)[4]) {
+    const rsrc_t r = buf(p.table + (size_t)h * kActive * kSlots, (size_t)kActive * kSlots * 4);
+#pragma unroll
+    for (int i = 0; i < 4; i++) tab[i] = ld_f32x4(r, (uint32_t)(threadIdx.x + 1024 * i) * 16);
+}
+
+__device__ __forceinline__ void stage_table(float* s_tab, const float4 (&tab)[4]) {
+    float4* st4 = reinterpret_cast<float4*>(s_tab);
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 3; i++) st4[tid + 1024 * i] = tab[i];
+    if (tid + 3 * 1024 < TQ) st4[tid + 3 * 1024] = tab[3];
 }
 
 // Write vector w (bf16-rounded, ops/utils.py:664-702) and the phase of every
@@ -173,9 +291,9 @@ __device__ __forceinline__ void readout_1024(const float* s_raw, const float* s_
                 lg += t.x * s_z[m] + t.y * s_z[m + 1] + t.z * s_z[m + 2] + t.w * s_z[m + 3];
             }
         }
-        lg += __shfl_xor(lg, 1);
-        lg += __shfl_xor(lg, 2);
-        lg += __shfl_xor(lg, 4);
+        lg += dpp_mov<0xB1>(lg);   // xor 1
+        lg += dpp_mov<0x4E>(lg);   // xor 2
+        lg += dpp_mov<0x141>(lg);  // the other quad of the octet (quads are uniform by now)
         if (part == 0) s_p[r] = r < kActive ? lg : -INFINITY;
     }
     __syncthreads();
@@ -292,27 +410,12 @@ __device__ __forceinline__ void output_1024(const DecodeParams& p, int bh, const
     }
 }
 
-// Wave 0's norm weight and gate for the output norm (LAYER), loaded early so
-// that their latency is not the kernel's last step.
-template <int V, bool LAYER>
-__device__ __forceinline__ void load_norm_inputs(const DecodeParams& p, int bh, float4* on_w4, bf16x4* on_g4) {
-    constexpr int OJ = (V + 255) / 256;
-    if (LAYER && (threadIdx.x >> 6) == 0) {
-        const int lane = threadIdx.x & 63;
-        const bf16_t* gt = p.gate + (size_t)(bh / p.H) * p.gate_row + (size_t)(bh % p.H) * V;
-#pragma unroll
-        for (int j = 0; j < OJ; j++) {
-            on_w4[j] = *reinterpret_cast<const float4*>(p.on_w + 4 * lane + 256 * j);
-            on_g4[j] = *reinterpret_cast<const bf16x4*>(gt + 4 * lane + 256 * j);
-        }
-    }
-}
-
 // q/k RMS norms (ops/fused_recurrent.py:62-89) from each thread's raw q, k
-// channel (threads < K), into s_q (scaled) and s_k; NW waves.
+// channel (threads < K) and its norm weights qw, kw (loaded with the other
+// small inputs), into s_q (scaled) and s_k; NW waves.
 template <int K, int NW>
-__device__ __forceinline__ void qk_norms(const DecodeParams& p, float qv, float kv, float (*s_red)[NW], float* s_q,
-                                         float* s_k) {
+__device__ __forceinline__ void qk_norms(const DecodeParams& p, float qv, float kv, float qw, float kw,
+                                         float (*s_red)[NW], float* s_q, float* s_k) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
     if (lane == 0 && wave < K / 64) {
@@ -328,15 +431,18 @@ __device__ __forceinline__ void qk_norms(const DecodeParams& p, float qv, float 
     }
     if (tid < K) {
         const float rq = rsqrtf(tq / K + p.q_eps), rk = rsqrtf(tk / K + p.k_eps);
-        s_q[tid] = bf16_round(qv * rq * p.q_w[tid]) * p.scale;
-        s_k[tid] = bf16_round(kv * rk * p.k_w[tid]);
+        s_q[tid] = bf16_round(qv * rq * qw) * p.scale;
+        s_k[tid] = bf16_round(kv * rk * kw);
     }
 }
 
 // The one-workgroup form. LAYER: the layer's one-token step around the op in
 // the same kernel: q, k and v from the short convolution and the new conv
 // cache, the gate activations from the a|b|d row, and o through the gated
-// output norm.
+// output norm. Phases: every load issued (small inputs, then hk, then hv);
+// prologue (conv, gates, write vector, q/k norms) while the states stream in;
+// key-state update as hk arrives; the slot readout while hv arrives; then the
+// value-state update and o.
 template <int K, int V, bool LAYER>
 __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     constexpr int NT = 1024;
@@ -346,99 +452,84 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     constexpr int VROWS = NT / VQ;  // hv rows covered per sweep
     constexpr int VJ = kSlots / VROWS;
     constexpr int NW = NT / 64;
-    const int bh = blockIdx.x, h = bh % p.H, tid = threadIdx.x, vt = tid & 255;
+    constexpr int OJ = (V + 255) / 256;
+    const int bh = blockIdx.x, h = bh % p.H, b = bh / p.H, tid = threadIdx.x, vt = tid & 255;
 
     __shared__ float s_q[K], s_k[K], s_w[kSlots], s_raw[kSlots], s_z[kSlots];
     __shared__ float s_p[kSlots], s_om[kSlots], s_c[kPairs], s_s[kPairs];
     __shared__ float s_part[NW][256];
     __shared__ float s_kpart[NS][8][kSlots];  // key-state slice partials of raw, per 32-thread group
     __shared__ float s_red[2][NW];
-    __shared__ float s_v[LAYER ? V : 1];
+    __shared__ float s_v[NT];  // v channel tid (tid < V); o in output_1024
     __shared__ __align__(16) float s_tab[kActive * kSlots];  // this head's readout table
 
     const bool has_state = p.hk_in != nullptr;
-    const float4* hk_in = reinterpret_cast<const float4*>(p.hk_in + (size_t)bh * K * kSlots);
-    const float4* hv_in = reinterpret_cast<const float4*>(p.hv_in + (size_t)bh * kSlots * V);
     float4* hk_out = reinterpret_cast<float4*>(p.hk_out + (size_t)bh * K * kSlots);
     float4* hv_out = reinterpret_cast<float4*>(p.hv_out + (size_t)bh * kSlots * V);
 
-    // Layer step: the short-convolution inputs of this thread's channels (the
-    // q and k channel tid, the v channel tid) are loaded ahead of the state
-    // streams, so they arrive first.
-    const int b = bh / p.H, HK = p.H * K;
+    // Small inputs: this thread's q and k channel tid and v channel tid (or
+    // the conv windows they come from), the gates, the q/k norm weights, the
+    // output norm inputs and the table.
+    const uint32_t dk = dead_unless_below(tid, K), dv = dead_unless_below(tid, V);
     ConvIn cq{}, ck{}, cv{};
+    float qv = 0.f, kv = 0.f, vv = 0.f;
     if (LAYER) {
-        if (tid < K) {
-            cq = load_conv(p, b, h * K + tid);
-            ck = load_conv(p, b, HK + h * K + tid);
-        }
-        if (tid < V) cv = load_conv(p, b, 2 * HK + h * V + tid);
+        const int HK = p.H * K;
+        const ConvSrc src = conv_src(p, b, 2 * HK + p.H * V);
+        cq = load_conv(src, h * K + tid, dk);
+        ck = load_conv(src, HK + h * K + tid, dk);
+        cv = load_conv(src, 2 * HK + h * V + tid, dv);
+    } else {
+        qv = ld_bf16(buf(p.q + (size_t)bh * K, (size_t)K * 2), ((uint32_t)tid * 2) | dk);
+        kv = ld_bf16(buf(p.k + (size_t)bh * K, (size_t)K * 2), ((uint32_t)tid * 2) | dk);
+        vv = ld_bf16(buf(p.v + (size_t)bh * V, (size_t)V * 2), ((uint32_t)tid * 2) | dv);
     }
-    constexpr int OJ = (V + 255) / 256;
+    const GateIn gi = load_gate_inputs<LAYER>(p, bh);
+    const float qw = ld_f32(buf(p.q_w, (size_t)K * 4), ((uint32_t)tid * 4) | dk);
+    const float kw = ld_f32(buf(p.k_w, (size_t)K * 4), ((uint32_t)tid * 4) | dk);
     float4 on_w4[OJ];
     bf16x4 on_g4[OJ];
     load_norm_inputs<V, LAYER>(p, bh, on_w4, on_g4);
+    float4 tab[4];
+    load_table(p, h, tab);
 
-    // The readout table (L2-resident, 64 KB per head) is read into registers
-    // ahead of the state streams and staged in LDS during the prologue, so the
-    // readout after the state writes finds it on chip.
-    constexpr int TQ = kActive * kSlots / 4;  // float4 of the table: 3 per thread, 4 for the first 992
-    static_assert(NT == 1024 && TQ > 3 * NT && TQ <= 4 * NT, "table staging covers the table");
-    const float4* tb4 = reinterpret_cast<const float4*>(p.table + (size_t)h * kActive * kSlots);
-    const float4 tab0 = tb4[tid], tab1 = tb4[tid + NT], tab2 = tb4[tid + 2 * NT];
-    const float4 tab3 = tid + 3 * NT < TQ ? tb4[tid + 3 * NT] : float4{0.f, 0.f, 0.f, 0.f};
+    // The key-state stream: slices (tid >> 8) + 4 r, four float4 of slice
+    // thread vt each.
+    const rsrc_t rk = buf(has_state ? p.hk_in + (size_t)bh * K * kSlots : nullptr, (size_t)K * kSlots * 4);
+    float4 hk_r[RK][4];
+#pragma unroll
+    for (int r = 0; r < RK; r++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) hk_r[r][j] = stream_load(rk, (uint32_t)(1024 * ((tid >> 8) + 4 * r) + vt + 256 * j) * 16);
 
-    // Issue both state streams; everything below overlaps with them. Key
-    // state: slices (tid >> 8) + 4 r, four float4 of slice thread vt each.
-    float4 hk_r[RK][4], hv_r[VJ];
-    if (has_state) {
-#pragma unroll
-        for (int r = 0; r < RK; r++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) hk_r[r][j] = stream_load(hk_in + 1024 * ((tid >> 8) + 4 * r) + vt + 256 * j);
-#pragma unroll
-        for (int j = 0; j < VJ; j++) hv_r[j] = stream_load(hv_in + tid + NT * j);
-    } else {
-#pragma unroll
-        for (int r = 0; r < RK; r++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) hk_r[r][j] = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int j = 0; j < VJ; j++) hv_r[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-
-    float qv = 0.f, kv = 0.f;
+    // Prologue.
     if (LAYER) {
-        if (tid < K) {
-            qv = conv_out(cq);
-            kv = conv_out(ck);
-            store_conv_cache(p, b, h * K + tid, cq);
-            store_conv_cache(p, b, HK + h * K + tid, ck);
-        }
-        if (tid < V) {
-            s_v[tid] = conv_out(cv);
-            store_conv_cache(p, b, 2 * HK + h * V + tid, cv);
-        }
-    } else if (tid < K) {
-        qv = (float)p.q[(size_t)bh * K + tid];
-        kv = (float)p.k[(size_t)bh * K + tid];
+        qv = conv_out(cq);
+        kv = conv_out(ck);
+        vv = conv_out(cv);
+        const rsrc_t co = conv_out_rows(p, b, 2 * p.H * K + p.H * V);
+        const uint32_t row = (uint32_t)p.cache_row * 2;
+        store_conv_cache(co, row, h * K + tid, dk, cq);
+        store_conv_cache(co, row, p.H * K + h * K + tid, dk, ck);
+        store_conv_cache(co, row, 2 * p.H * K + h * V + tid, dv, cv);
     }
+    s_v[tid] = vv;  // every thread: a store behind tid < V let the compiler sink cv's loads below the states'
     float g_in, delta_in, beta_in;
-    load_gates<LAYER>(p, bh, g_in, delta_in, beta_in);
-    {
-        float4* st4 = reinterpret_cast<float4*>(s_tab);
-        st4[tid] = tab0;
-        st4[tid + NT] = tab1;
-        st4[tid + 2 * NT] = tab2;
-        if (tid + 3 * NT < TQ) st4[tid + 3 * NT] = tab3;
-    }
-    const float clock = has_state ? p.clock_in[bh] : 0.f;
-    const float lam = clock + delta_in;
+    gate_values<LAYER>(p, bh, gi, g_in, delta_in, beta_in);
+    stage_table(s_tab, tab);
+    const float lam = gi.clock + delta_in;
     const float decay = expf(g_in);
     write_vector_lds(lam, beta_in, s_w, s_c, s_s);
-    qk_norms<K, NW>(p, qv, kv, s_red, s_q, s_k);
+    qk_norms<K, NW>(p, qv, kv, qw, kw, s_red, s_q, s_k);
     __syncthreads();
     if (tid == 0) p.clock_out[bh] = lam;  // after every thread has read clock_in
+
+    // The value-state stream, float4 tid + NT j, issued once the small
+    // inputs' registers are free; it is first needed after the readout.
+    const rsrc_t rv = buf(has_state ? p.hv_in + (size_t)bh * kSlots * V : nullptr, (size_t)kSlots * V * 4);
+    float4 hv_r[VJ];
+#pragma unroll
+    for (int j = 0; j < VJ; j++) hv_r[j] = stream_load(rv, (uint32_t)(tid + NT * j) * 16);
 
     // Key state: hk' = alpha hk + k_hat (x) w ; raw = hk'^T q_hat, by slices.
 #pragma unroll
@@ -451,22 +542,20 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
         pt[2] = a.z;
         pt[3] = a.w;
     }
+    __syncthreads();
+    if (tid < kSlots) {
+        float r = slice_partial(&s_kpart[0][0][0], tid);
+#pragma unroll
+        for (int s = 1; s < NS; s++) r += slice_partial(&s_kpart[s][0][0], tid);
+        s_raw[tid] = r;
+    }
+    __syncthreads();
+    readout_1024(s_raw, s_c, s_s, s_tab, s_z, s_p, s_part, s_om);
+
     // Value state: hv' = alpha hv + w (x) v, written now; kept in hv_r for o.
     {
         const int v4 = (tid % VQ) * 4, r0 = tid / VQ;
-        float v0, v1, v2, v3;
-        if (LAYER) {
-            v0 = s_v[v4];
-            v1 = s_v[v4 + 1];
-            v2 = s_v[v4 + 2];
-            v3 = s_v[v4 + 3];
-        } else {
-            const bf16x4 vb = *reinterpret_cast<const bf16x4*>(p.v + (size_t)bh * V + v4);
-            v0 = (float)vb[0];
-            v1 = (float)vb[1];
-            v2 = (float)vb[2];
-            v3 = (float)vb[3];
-        }
+        const float v0 = s_v[v4], v1 = s_v[v4 + 1], v2 = s_v[v4 + 2], v3 = s_v[v4 + 3];
 #pragma unroll
         for (int j = 0; j < VJ; j++) {
             const float wm = s_w[r0 + VROWS * j];
@@ -479,15 +568,6 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
             hv_r[j] = n;
         }
     }
-    __syncthreads();
-    if (tid < kSlots) {
-        float r = slice_partial(&s_kpart[0][0][0], tid);
-#pragma unroll
-        for (int s = 1; s < NS; s++) r += slice_partial(&s_kpart[s][0][0], tid);
-        s_raw[tid] = r;
-    }
-    __syncthreads();
-    readout_1024(s_raw, s_c, s_s, s_tab, s_z, s_p, s_part, s_om);
     output_1024<V, LAYER>(p, bh, hv_r, s_om, s_part, s_v, on_w4, on_g4);
 }
 
@@ -500,58 +580,58 @@ template <int K, int V, bool LAYER>
 __global__ __launch_bounds__(256) void decode_split_a_kernel(DecodeParams p) {
     constexpr int NT = 256, NW = NT / 64;
     constexpr int NSL = (K > V ? K : V) / SLICE;
+    constexpr int VQ = V / 4;
     const int s = blockIdx.x, bh = blockIdx.y, h = bh % p.H, b = bh / p.H, tid = threadIdx.x;
-    const int HK = p.H * K;
     __shared__ float s_q[K], s_k[K], s_w[kSlots], s_c[kPairs], s_s[kPairs];
     __shared__ float s_kpart[8][kSlots];
-    __shared__ float s_v[SLICE];
+    __shared__ float s_v[NT];  // v channel 32 s + tid (tid < 32)
     __shared__ float s_red[2][NW];
 
     const bool key = s < K / SLICE, val = s < V / SLICE;
     const bool has_state = p.hk_in != nullptr;
-    const float4* hk_in = reinterpret_cast<const float4*>(p.hk_in + (size_t)bh * K * kSlots);
-    const float4* hv_in = reinterpret_cast<const float4*>(p.hv_in + (size_t)bh * kSlots * V);
     float4* hk_out = reinterpret_cast<float4*>(p.hk_out + (size_t)bh * K * kSlots);
     float4* hv_out = reinterpret_cast<float4*>(p.hv_out + (size_t)bh * kSlots * V);
 
+    // small inputs first (q, k channel tid; v channel 32 s + tid), then the slices
+    const uint32_t dk = dead_unless_below(tid, K), dv = val ? dead_unless_below(tid, SLICE) : DEAD;
     ConvIn cq{}, ck{}, cv{};
+    float qv = 0.f, kv = 0.f, vv = 0.f;
     if (LAYER) {
-        if (tid < K) {
-            cq = load_conv(p, b, h * K + tid);
-            ck = load_conv(p, b, HK + h * K + tid);
-        }
-        if (val && tid < SLICE) cv = load_conv(p, b, 2 * HK + h * V + SLICE * s + tid);
+        const int HK = p.H * K;
+        const ConvSrc src = conv_src(p, b, 2 * HK + p.H * V);
+        cq = load_conv(src, h * K + tid, dk);
+        ck = load_conv(src, HK + h * K + tid, dk);
+        cv = load_conv(src, 2 * HK + h * V + SLICE * s + tid, dv);
+    } else {
+        qv = ld_bf16(buf(p.q + (size_t)bh * K, (size_t)K * 2), ((uint32_t)tid * 2) | dk);
+        kv = ld_bf16(buf(p.k + (size_t)bh * K, (size_t)K * 2), ((uint32_t)tid * 2) | dk);
+        vv = ld_bf16(buf(p.v + (size_t)bh * V, (size_t)V * 2), ((uint32_t)(SLICE * s + tid) * 2) | dv);
     }
+    const GateIn gi = load_gate_inputs<LAYER>(p, bh);
+    const float qw = ld_f32(buf(p.q_w, (size_t)K * 4), ((uint32_t)tid * 4) | dk);
+    const float kw = ld_f32(buf(p.k_w, (size_t)K * 4), ((uint32_t)tid * 4) | dk);
     // This workgroup's slices of both states: hk float4 1024 s + tid + 256 j;
     // hv row tid / 8 + 32 j, columns 32 s + 4 (tid % 8) ...
-    constexpr int VQ = V / 4;
+    const rsrc_t rk = buf(has_state && key ? p.hk_in + (size_t)bh * K * kSlots : nullptr, (size_t)K * kSlots * 4);
+    const rsrc_t rv = buf(has_state && val ? p.hv_in + (size_t)bh * kSlots * V : nullptr, (size_t)kSlots * V * 4);
     float4 hk_r[4], hv_r[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        hk_r[j] = has_state && key ? stream_load(hk_in + 1024 * s + tid + 256 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
-        hv_r[j] = has_state && val ? stream_load(hv_in + (size_t)((tid >> 3) + 32 * j) * VQ + 8 * s + (tid & 7))
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+        hk_r[j] = stream_load(rk, (uint32_t)(1024 * s + tid + 256 * j) * 16);
+        hv_r[j] = stream_load(rv, (uint32_t)(((tid >> 3) + 32 * j) * VQ + 8 * s + (tid & 7)) * 16);
     }
-    float qv = 0.f, kv = 0.f;
     if (LAYER) {
-        if (tid < K) {
-            qv = conv_out(cq);
-            kv = conv_out(ck);
-        }
-        if (val && tid < SLICE) s_v[tid] = conv_out(cv);
-    } else {
-        if (tid < K) {
-            qv = (float)p.q[(size_t)bh * K + tid];
-            kv = (float)p.k[(size_t)bh * K + tid];
-        }
-        if (val && tid < SLICE) s_v[tid] = (float)p.v[(size_t)bh * V + SLICE * s + tid];
+        qv = conv_out(cq);
+        kv = conv_out(ck);
+        vv = conv_out(cv);
     }
+    s_v[tid] = vv;  // every thread (see decode_step_kernel)
     float g_in, delta_in, beta_in;
-    load_gates<LAYER>(p, bh, g_in, delta_in, beta_in);
-    const float lam = (has_state ? p.clock_in[bh] : 0.f) + delta_in;
+    gate_values<LAYER>(p, bh, gi, g_in, delta_in, beta_in);
+    const float lam = gi.clock + delta_in;
     const float decay = expf(g_in);
     write_vector_lds(lam, beta_in, s_w, s_c, s_s);
-    qk_norms<K, NW>(p, qv, kv, s_red, s_q, s_k);
+    qk_norms<K, NW>(p, qv, kv, qw, kw, s_red, s_q, s_k);
     __syncthreads();
     if (key) {
         const float4 a = key_slice_update(hk_r, hk_out, s, tid, decay, s_k, s_q, s_w);
@@ -585,60 +665,63 @@ __global__ __launch_bounds__(256) void decode_split_a_kernel(DecodeParams p) {
 // (read back, L2-resident), the conv cache and the clock.
 template <int K, int V, bool LAYER>
 __global__ __launch_bounds__(1024) void decode_split_b_kernel(DecodeParams p) {
-    constexpr int NT = 1024, NW = NT / 64;
+    constexpr int NT = 1024;
     constexpr int NS = K / SLICE, NSL = (K > V ? K : V) / SLICE;
     constexpr int VQ = V / 4, VROWS = NT / VQ, VJ = kSlots / VROWS;
+    constexpr int NW = NT / 64;
+    constexpr int OJ = (V + 255) / 256;
     const int bh = blockIdx.x, h = bh % p.H, b = bh / p.H, tid = threadIdx.x;
-    const int HK = p.H * K;
     __shared__ float s_raw[kSlots], s_z[kSlots], s_p[kSlots], s_om[kSlots], s_c[kPairs], s_s[kPairs], s_w[kSlots];
     __shared__ float s_part[NW][256];
     __shared__ float s_v[LAYER ? V : 1];
     __shared__ __align__(16) float s_tab[kActive * kSlots];
 
-    constexpr int OJ = (V + 255) / 256;
     float4 on_w4[OJ];
     bf16x4 on_g4[OJ];
     load_norm_inputs<V, LAYER>(p, bh, on_w4, on_g4);
-    constexpr int TQ = kActive * kSlots / 4;
-    const float4* tb4 = reinterpret_cast<const float4*>(p.table + (size_t)h * kActive * kSlots);
-    const float4 tab0 = tb4[tid], tab1 = tb4[tid + NT], tab2 = tb4[tid + 2 * NT];
-    const float4 tab3 = tid + 3 * NT < TQ ? tb4[tid + 3 * NT] : float4{0.f, 0.f, 0.f, 0.f};
-    const float4* hv_new = reinterpret_cast<const float4*>(p.hv_out + (size_t)bh * kSlots * V);
-    float4 hv_r[VJ];
+    const GateIn gi = load_gate_inputs<LAYER>(p, bh);
+    // the slices' partials of raw (threads < 128, slice order)
+    const rsrc_t rp = buf(p.part + (size_t)bh * NSL * kSlots, (size_t)NSL * kSlots * 4);
+    const uint32_t dm = dead_unless_below(tid, kSlots);
+    float part_r[NS];
 #pragma unroll
-    for (int j = 0; j < VJ; j++) hv_r[j] = hv_new[tid + NT * j];
-    float part_r = 0.f;
-    if (tid < kSlots) {
-        part_r = p.part[(size_t)bh * NSL * kSlots + tid];
-#pragma unroll
-        for (int s = 1; s < NS; s++) part_r += p.part[((size_t)bh * NSL + s) * kSlots + tid];
-        s_raw[tid] = part_r;
-    }
+    for (int s = 0; s < NS; s++) part_r[s] = ld_f32(rp, ((uint32_t)(s * kSlots + tid) * 4) | dm);
     // The conv cache of this head's channels: the last three rows of each
     // window (each channel read and written by one thread, so an in-place
     // update needs no ordering between threads).
+    const int HK = p.H * K;
+    const int ch = tid < K ? h * K + tid : tid < 2 * K ? HK + h * K + (tid - K) : 2 * HK + h * V + (tid - 2 * K);
+    float win[3] = {0.f, 0.f, 0.f};
+    if (LAYER) {
+        const ConvSrc src = conv_src(p, b, 2 * HK + p.H * V);
+        const uint32_t dc = dead_unless_below(tid, 2 * K + V);
+#pragma unroll
+        for (int w = 1; w < 3; w++) win[w - 1] = ld_bf16(src.cache, (w * src.row + (uint32_t)ch * 2) | dc);
+        win[2] = ld_bf16(src.qkv, ((uint32_t)ch * 2) | dc);
+    }
+    float4 tab[4];
+    load_table(p, h, tab);
+    const rsrc_t rv = buf(p.hv_out + (size_t)bh * kSlots * V, (size_t)kSlots * V * 4);
+    float4 hv_r[VJ];
+#pragma unroll
+    for (int j = 0; j < VJ; j++) hv_r[j] = ld_f32x4(rv, (uint32_t)(tid + NT * j) * 16);
+    if (tid < kSlots) {
+        float r = part_r[0];
+#pragma unroll
+        for (int s = 1; s < NS; s++) r += part_r[s];
+        s_raw[tid] = r;
+    }
     if (LAYER && tid < 2 * K + V) {
-        const int ch = tid < K ? h * K + tid : tid < 2 * K ? HK + h * K + (tid - K) : 2 * HK + h * V + (tid - 2 * K);
-        bf16_t win[3];
 #pragma unroll
-        for (int w = 1; w < 3; w++)
-            win[w - 1] = p.cache_in ? p.cache_in[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch] : (bf16_t)0.f;
-        win[2] = p.qkv[(size_t)b * p.qkv_row + ch];
-#pragma unroll
-        for (int w = 0; w < 3; w++) p.cache_out[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch] = win[w];
+        for (int w = 0; w < 3; w++)
+            p.cache_out[(size_t)b * p.cache_batch + (size_t)w * p.cache_row + ch] = (bf16_t)win[w];
     }
     float g_in, delta_in, beta_in;
-    load_gates<LAYER>(p, bh, g_in, delta_in, beta_in);
+    gate_values<LAYER>(p, bh, gi, g_in, delta_in, beta_in);
     (void)g_in;
-    const float lam = (p.hk_in != nullptr ? p.clock_in[bh] : 0.f) + delta_in;
+    const float lam = gi.clock + delta_in;
     write_vector_lds(lam, beta_in, s_w, s_c, s_s);
-    {
-        float4* st4 = reinterpret_cast<float4*>(s_tab);
-        st4[tid] = tab0;
-        st4[tid + NT] = tab1;
-        st4[tid + 2 * NT] = tab2;
-        if (tid + 3 * NT < TQ) st4[tid + 3 * NT] = tab3;
-    }
+    stage_table(s_tab, tab);
     __syncthreads();
     if (tid == 0) p.clock_out[bh] = lam;  // after every thread has read clock_in
     readout_1024(s_raw, s_c, s_s, s_tab, s_z, s_p, s_part, s_om);
@@ -667,6 +750,10 @@ size_t decode_workspace_bytes(int B, int H, int K, int V) {
 int launch_decode_step(const DecodeParams& p, int K, int V, hipStream_t stream) {
     if (p.qkv) {  // the layer step: K = V = 256 only
         if (K != 256 || V != 256) return -1;
+        // every buffer the kernels read spans less than DEAD bytes
+        const long long D = (long long)p.H * (2 * K + V);
+        if (p.cache_in && (p.cache_row < 0 || (2 * p.cache_row + D) * 2 >= (long long)DEAD)) return -1;
+        if (D * 8 >= (long long)DEAD) return -1;
         launch<256, 256, true>(p, stream);
     } else if (K == 256 && V == 256)
         launch<256, 256, false>(p, stream);

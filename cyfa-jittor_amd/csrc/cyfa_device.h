@@ -130,18 +130,48 @@ __device__ __forceinline__ float sigmoidf(float x) {
     return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
 }
 
+// Wave reductions on the VALU. __shfl_xor is a ds_bpermute, an LDS round trip
+// per step (about 30 of them sat on the decode step's serial path): here DPP
+// moves reduce within rows of 16 lanes and v_readlane gathers the rows.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float lane_value(float x, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+
+// Sum (max) over aligned groups of W lanes, in every lane of the group; every
+// lane of the wave must be active. Fixed order: pairs (quad_perm [1,0,3,2]),
+// quads ([2,3,0,1]), octets (row_half_mirror), rows of 16 (row_mirror) - after
+// each step every lane of a group holds the same value, so a mirror reads the
+// value the matching xor lane holds - then rows (0 + 1) and (2 + 3), then
+// their sum.
 template <int W = 64>
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) x += __shfl_xor(x, o, W);
-    return x;
+    static_assert(W == 16 || W == 32 || W == 64, "group of 16, 32 or 64 lanes");
+    x += dpp_mov<0xB1>(x);
+    x += dpp_mov<0x4E>(x);
+    x += dpp_mov<0x141>(x);
+    x += dpp_mov<0x140>(x);
+    if (W == 16) return x;
+    const float lo = lane_value(x, 0) + lane_value(x, 16), hi = lane_value(x, 32) + lane_value(x, 48);
+    if (W == 32) return (threadIdx.x & 32) ? hi : lo;
+    return lo + hi;
 }
 
 template <int W = 64>
 __device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, W));
-    return x;
+    static_assert(W == 16 || W == 32 || W == 64, "group of 16, 32 or 64 lanes");
+    x = fmaxf(x, dpp_mov<0xB1>(x));
+    x = fmaxf(x, dpp_mov<0x4E>(x));
+    x = fmaxf(x, dpp_mov<0x141>(x));
+    x = fmaxf(x, dpp_mov<0x140>(x));
+    if (W == 16) return x;
+    const float lo = fmaxf(lane_value(x, 0), lane_value(x, 16)), hi = fmaxf(lane_value(x, 32), lane_value(x, 48));
+    if (W == 32) return (threadIdx.x & 32) ? hi : lo;
+    return fmaxf(lo, hi);
 }
 
 }  // namespace cyfa
