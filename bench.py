@@ -65,7 +65,7 @@ BYTES_PER_TOKEN_HEAD = 2 * 256 * 4 + 12 + 2 * 256
 # profiles/cyfa_decode_step_cfg4.md); they apply to the default shapes.
 TRAFFIC_PREFILL_BYTES = 343.2e6    # one cyfa_chunk_fwd_normed at B=8, T=2048, H=4
 TRAFFIC_DECODE_BYTES = 135.5e6     # one decode launch at B=64, H=4
-TRAFFIC_LAYER_STEP_BYTES = None    # one cyfa_decode_layer_step at B=64, H=4 (not yet counted)
+TRAFFIC_LAYER_STEP_BYTES = 138.1e6  # one cyfa_decode_layer_step at B=64, H=4 (69.6 MB read + 68.5 MB written)
 
 
 def parse():
@@ -87,6 +87,8 @@ def parse():
                          "decode steps (reported under 'long_context')")
     ap.add_argument("--decode-kernel-only", action="store_true",
                     help="only time the fused decode kernel at the decode shape (for hardware-counter runs)")
+    ap.add_argument("--layer-kernel-only", action="store_true",
+                    help="only run the decode layer-step kernel at the decode shape, eagerly (for hardware-counter runs)")
     ap.add_argument("--no-tuned-gemms", action="store_true",
                     help="leave the library GEMMs on their default solutions")
     ap.add_argument("--tune-gemms", metavar="FILE",
@@ -185,7 +187,7 @@ def time_decode(model, prompt, steps, warmup):
     return elapsed
 
 
-def decode_layer_kernel_ms(batch, heads, reps=24, replays=5):
+def decode_layer_kernel_ms(batch, heads, reps=24, replays=5, graphed=True):
     """Average device time of one cyfa_decode_layer_step launch (the kernel the
     model's graphed decode step runs: short convolution, gates, the decode op
     and the gated output norm) at the decode shape, timed as decode_kernel_ms:
@@ -217,6 +219,11 @@ def decode_layer_kernel_ms(batch, heads, reps=24, replays=5):
     with torch.no_grad():
         step(states[0])
         torch.cuda.synchronize()
+        if not graphed:  # one eager launch per state (hardware-counter runs attach per dispatch)
+            for st in states:
+                step(st)
+            torch.cuda.synchronize()
+            return None
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             for st in states:
@@ -391,6 +398,10 @@ def main():
         decode_kernel_ms(args.decode_batch, 4, graphed=False)
         log(f"decode kernel: 24 launches at B={args.decode_batch}, H=4, one state each")
         return 0
+    if args.layer_kernel_only:
+        decode_layer_kernel_ms(args.decode_batch, 4, graphed=False)
+        log(f"decode layer-step kernel: 25 launches at B={args.decode_batch}, H=4, one state each")
+        return 0
     log(f"device {torch.cuda.get_device_name(dev)}")
     from cyclic_flow_attention import gemm_tuning
 
@@ -468,8 +479,9 @@ def main():
         d_elapsed = time_decode(model, prompt, args.decode_steps, args.decode_warmup)
         d_value = args.decode_batch * args.decode_steps / d_elapsed
         d_bytes = STATE_BYTES_PER_BH * args.decode_batch * H
+        l_bytes = d_bytes
         l_avg = decode_layer_kernel_ms(args.decode_batch, H)
-        l_gbs = d_bytes / (l_avg * 1e-3) / 1e9
+        l_gbs = l_bytes / (l_avg * 1e-3) / 1e9
         d_avg = decode_kernel_ms(args.decode_batch, H)
         d_gbs = d_bytes / (d_avg * 1e-3) / 1e9
         log(f"decode {d_value:,.0f} tok/s; layer-step kernel {l_avg * 1e3:.1f} us/launch = {l_gbs:,.0f} GB/s; "
@@ -490,7 +502,7 @@ def main():
                 "frac": round(l_gbs / PEAK_HBM_GBS, 4),
                 "traffic": TRAFFIC_LAYER_STEP_BYTES if (args.decode_batch, H) == (64, 4) else None,
                 "launch_us": round(l_avg * 1e3, 2),
-                "bytes_per_launch": d_bytes,
+                "bytes_per_launch": l_bytes,
             },
             "op_kernel": {
                 "kernel": "cyfa_decode_step (fused_recurrent_cyfa alone)",

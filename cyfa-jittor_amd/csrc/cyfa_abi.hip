@@ -106,15 +106,18 @@ int decode_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* ly, void* hi
             return fail(CYFA_ERR_UNSUPPORTED, "cyfa_decode_layer_step: head dims K=%d V=%d, the layer step needs 256",
                         a->K, a->V);
         if (!ly->qkv || !ly->conv_cache_out || !ly->conv_weight || !ly->abd || !ly->dt_bias || !ly->A_log ||
-            !ly->gate || !ly->norm_weight)
+            !ly->norm_weight || (!ly->gate && (!ly->g0 || !ly->g_weight)))
             return fail(CYFA_ERR_VALUE, "cyfa_decode_layer_step: null required pointer");
         const long long D = 3LL * a->H * 256;
-        if (ly->qkv_row < D || ly->abd_row < 3LL * a->H || ly->gate_row < (long long)a->H * 256 || ly->gate_row % 4 ||
-            ly->cache_row < D || ly->cache_batch < 3 * ly->cache_row)
-            return fail(CYFA_ERR_VALUE, "cyfa_decode_layer_step: row strides too small");
-        if (!aligned(ly->gate, 8) || !aligned(ly->conv_weight, 8) || !aligned(ly->norm_weight, 16))
+        if (ly->qkv_row < D || ly->abd_row < 3LL * a->H || ly->cache_row < D || ly->cache_batch < 3 * ly->cache_row ||
+            (ly->gate && (ly->gate_row < (long long)a->H * 256 || ly->gate_row % 4)) ||
+            (!ly->gate && (ly->g0_row < 256 || ly->g0_row % 8)))
+            return fail(CYFA_ERR_VALUE, "cyfa_decode_layer_step: row strides too small or misaligned");
+        if (!aligned(ly->gate, 8) || !aligned(ly->conv_weight, 8) || !aligned(ly->norm_weight, 16) ||
+            (!ly->gate && (!aligned(ly->g0, 16) || !aligned(ly->g_weight, 16))))
             return fail(CYFA_ERR_ALIGN,
-                        "cyfa_decode_layer_step: gate and conv_weight need 8-byte, norm_weight 16-byte alignment");
+                        "cyfa_decode_layer_step: gate and conv_weight need 8-byte, norm_weight, g0 and g_weight "
+                        "16-byte alignment");
         if (!(ly->norm_eps >= 0.f) || !isfinite(ly->norm_prescale))
             return fail(CYFA_ERR_VALUE, "cyfa_decode_layer_step: norm_eps=%g prescale=%g", (double)ly->norm_eps,
                         (double)ly->norm_prescale);
@@ -166,6 +169,12 @@ int decode_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* ly, void* hi
         p.A_log = ly->A_log;
         p.gate = (const __bf16*)ly->gate;
         p.gate_row = ly->gate_row;
+        if (!ly->gate) {
+            p.g0 = (const __bf16*)ly->g0;
+            p.g0_row = ly->g0_row;
+            p.g1_w = (const __bf16*)ly->g_weight;
+            p.g1_b = (const __bf16*)ly->g_bias;
+        }
         p.on_w = ly->norm_weight;
         p.on_eps = ly->norm_eps;
         p.on_prescale = ly->norm_prescale;

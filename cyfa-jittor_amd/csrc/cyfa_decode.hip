@@ -216,6 +216,51 @@ __device__ __forceinline__ void stage_table(float* s_tab, const float4 (&tab)[4]
     if (tid + 3 * 1024 < TQ) st4[tid + 3 * 1024] = tab[3];
 }
 
+// The gate of (b, h) as the second projection of g_proj (layers/cyfa.py:
+// 211-214) when the caller passes g0 instead of the gate: gate = bf16(g0 W^T +
+// bias) for the head's V = 256 columns, in linear_rows_kernel's summation
+// order for K = 256 (eight 32-deep k-steps, one per wave there): each k-step
+// on one v_mfma_f32_16x16x32_bf16 from zero, with g0 in row 0 of A and the
+// other rows zero; the eight partials summed in k-step order, then the bias.
+// Wave c (0..15) forms columns 16 c .. 16 c + 15; lane (lr, lg) holds W row
+// 16 c + lr, k = 32 s + 8 lg .. 32 s + 8 lg + 7 of step s.
+struct GateW {
+    bf16x8 w[8];
+    float bias;
+};
+
+__device__ __forceinline__ GateW load_gate_weights(const DecodeParams& p, int h) {
+    constexpr int V = 256;
+    const int lane = threadIdx.x & 63, c = threadIdx.x >> 6, lr = lane & 15, lg = lane >> 4;
+    const rsrc_t r = buf(p.g1_w ? p.g1_w + ((size_t)h * V + 16 * c) * V : nullptr, (size_t)16 * V * 2);
+    GateW g;
+#pragma unroll
+    for (int st = 0; st < 8; st++)
+        g.w[st] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(lr * V + 32 * st + 8 * lg) * 2, 0, 0));
+    g.bias = ld_bf16(buf(p.g1_b ? p.g1_b + (size_t)h * V : nullptr, (size_t)V * 2), (uint32_t)(16 * c + lr) * 2);
+    return g;
+}
+
+// g0 of batch row b, 16 bytes per thread for threads 0..31 (zero elsewhere).
+__device__ __forceinline__ bf16x8 load_g0(const DecodeParams& p, int b) {
+    const rsrc_t r = buf(p.g0 ? p.g0 + (size_t)b * p.g0_row : nullptr, 512);
+    return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                          r, ((uint32_t)threadIdx.x * 16) | dead_unless_below(threadIdx.x, 32), 0, 0));
+}
+
+// s_gate[16 c + lr] = the gate's column 16 c + lr, bf16-rounded (s_g0: g0 as 32 bf16x8).
+__device__ __forceinline__ void gate_columns(const bf16x8* s_g0, const GateW& g, float* s_gate) {
+    const int lane = threadIdx.x & 63, c = threadIdx.x >> 6, lr = lane & 15, lg = lane >> 4;
+    float tot = 0.f;
+#pragma unroll
+    for (int st = 0; st < 8; st++) {
+        const bf16x8 a = lr == 0 ? s_g0[4 * st + lg] : bf16x8{};
+        const f32x4 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, g.w[st], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        tot += acc[0];  // row 0 of the tile (lanes lg = 0)
+    }
+    if (lg == 0) s_gate[16 * c + lr] = bf16_round(tot + g.bias);
+}
+
 // Write vector w (bf16-rounded, ops/utils.py:664-702) and the phase of every
 // pair into LDS; threads 0..63 (one pair each).
 __device__ __forceinline__ void write_vector_lds(float lam, float beta, float* s_w, float* s_c, float* s_s) {
@@ -337,7 +382,7 @@ __device__ __forceinline__ void readout_1024(const float* s_raw, const float* s_
 template <int V, bool LAYER>
 __device__ __forceinline__ void output_1024(const DecodeParams& p, int bh, const float4* hv_r, const float* s_om,
                                             float (*s_part)[256], float* s_v, const float4* on_w4,
-                                            const bf16x4* on_g4) {
+                                            const bf16x4* on_g4, const float* s_gate) {
     constexpr int NT = 1024, VQ = V / 4, VROWS = NT / VQ, VJ = kSlots / VROWS;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     {
@@ -404,7 +449,10 @@ __device__ __forceinline__ void output_1024(const DecodeParams& p, int bh, const
             const float wa[4] = {w.x, w.y, w.z, w.w};
             bf16x4 y;
 #pragma unroll
-            for (int i = 0; i < 4; i++) y[i] = (bf16_t)(xs[j][i] * rs * wa[i] * sigmoidf((float)g4[i]));
+            for (int i = 0; i < 4; i++) {
+                const float gv = s_gate ? s_gate[d0 + i] : (float)g4[i];  // formed in the kernel, or given
+                y[i] = (bf16_t)(xs[j][i] * rs * wa[i] * sigmoidf(gv));
+            }
             *reinterpret_cast<bf16x4*>(p.o + (size_t)bh * V + d0) = y;
         }
     }
@@ -462,8 +510,11 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     __shared__ float s_red[2][NW];
     __shared__ float s_v[NT];  // v channel tid (tid < V); o in output_1024
     __shared__ __align__(16) float s_tab[kActive * kSlots];  // this head's readout table
+    __shared__ bf16x8 s_g0[LAYER ? 32 : 1];                   // g0 (the gate formed in the kernel)
+    __shared__ float s_gate[LAYER ? V : 1];
 
     const bool has_state = p.hk_in != nullptr;
+    const bool own_gate = LAYER && p.g1_w != nullptr;
     float4* hk_out = reinterpret_cast<float4*>(p.hk_out + (size_t)bh * K * kSlots);
     float4* hv_out = reinterpret_cast<float4*>(p.hv_out + (size_t)bh * kSlots * V);
 
@@ -492,6 +543,7 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     load_norm_inputs<V, LAYER>(p, bh, on_w4, on_g4);
     float4 tab[4];
     load_table(p, h, tab);
+    const bf16x8 g0v = LAYER ? load_g0(p, b) : bf16x8{};
 
     // The key-state stream: slices (tid >> 8) + 4 r, four float4 of slice
     // thread vt each.
@@ -514,6 +566,7 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
         store_conv_cache(co, row, 2 * p.H * K + h * V + tid, dv, cv);
     }
     s_v[tid] = vv;  // every thread: a store behind tid < V let the compiler sink cv's loads below the states'
+    if (LAYER && tid < 32) s_g0[tid] = g0v;
     float g_in, delta_in, beta_in;
     gate_values<LAYER>(p, bh, gi, g_in, delta_in, beta_in);
     stage_table(s_tab, tab);
@@ -542,6 +595,10 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
         pt[2] = a.z;
         pt[3] = a.w;
     }
+    // the gate projection's weights (L2-resident), in the key state's registers;
+    // issued with the value state they would not fit beside it
+    GateW gw{};
+    if (LAYER) gw = load_gate_weights(p, h);
     __syncthreads();
     if (tid < kSlots) {
         float r = slice_partial(&s_kpart[0][0][0], tid);
@@ -568,7 +625,8 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
             hv_r[j] = n;
         }
     }
-    output_1024<V, LAYER>(p, bh, hv_r, s_om, s_part, s_v, on_w4, on_g4);
+    if (own_gate) gate_columns(s_g0, gw, s_gate);
+    output_1024<V, LAYER>(p, bh, hv_r, s_om, s_part, s_v, on_w4, on_g4, own_gate ? s_gate : nullptr);
 }
 
 // Small-batch form, part A: grid (NSL, B H), 256 threads; workgroup s updates
@@ -675,10 +733,16 @@ __global__ __launch_bounds__(1024) void decode_split_b_kernel(DecodeParams p) {
     __shared__ float s_part[NW][256];
     __shared__ float s_v[LAYER ? V : 1];
     __shared__ __align__(16) float s_tab[kActive * kSlots];
+    __shared__ bf16x8 s_g0[LAYER ? 32 : 1];
+    __shared__ float s_gate[LAYER ? V : 1];
 
+    const bool own_gate = LAYER && p.g1_w != nullptr;
     float4 on_w4[OJ];
     bf16x4 on_g4[OJ];
     load_norm_inputs<V, LAYER>(p, bh, on_w4, on_g4);
+    const bf16x8 g0v = LAYER ? load_g0(p, b) : bf16x8{};
+    GateW gw{};
+    if (LAYER) gw = load_gate_weights(p, h);
     const GateIn gi = load_gate_inputs<LAYER>(p, bh);
     // the slices' partials of raw (threads < 128, slice order)
     const rsrc_t rp = buf(p.part + (size_t)bh * NSL * kSlots, (size_t)NSL * kSlots * 4);
@@ -722,10 +786,12 @@ __global__ __launch_bounds__(1024) void decode_split_b_kernel(DecodeParams p) {
     const float lam = gi.clock + delta_in;
     write_vector_lds(lam, beta_in, s_w, s_c, s_s);
     stage_table(s_tab, tab);
+    if (LAYER && tid < 32) s_g0[tid] = g0v;
     __syncthreads();
     if (tid == 0) p.clock_out[bh] = lam;  // after every thread has read clock_in
     readout_1024(s_raw, s_c, s_s, s_tab, s_z, s_p, s_part, s_om);
-    output_1024<V, LAYER>(p, bh, hv_r, s_om, s_part, s_v, on_w4, on_g4);
+    if (own_gate) gate_columns(s_g0, gw, s_gate);
+    output_1024<V, LAYER>(p, bh, hv_r, s_om, s_part, s_v, on_w4, on_g4, own_gate ? s_gate : nullptr);
 }
 
 template <int K, int V, bool LAYER>

@@ -31,6 +31,11 @@ struct DecodeParams {
     long long gate_row;
     const float* on_w;       // [V]
     float on_eps, on_prescale;
+    // gate null: gate = bf16(g0 g1_w^T + g1_b) formed in the kernel, row b of
+    // g0 at g0 + b * g0_row ([V]), g1_w [H V, V], g1_b nullable [H V]
+    const __bf16* g0;
+    long long g0_row;
+    const __bf16 *g1_w, *g1_b;
     // Small batches (B H < DECODE_SPLIT_BH): the workspace for the slices'
     // partial raw, [B H, max(K, V) / 32, 128] f32; null: one workgroup per (b, h).
     float* part;

@@ -532,15 +532,21 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const bf16_t* x, long
             }
         }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o);
-        const int oi = __shfl_xor(bi, o);
+    // The wave's best (value, index): the comparison is associative and
+    // commutative, so any reduction order gives the same pair. DPP within rows
+    // of 16 lanes, then the four rows through v_readlane (no LDS round trips).
+    const auto take = [&](float ov, int oi) {
         if (argmax_better(ov, oi, bv, bi)) {
             bv = ov;
             bi = oi;
         }
-    }
+    };
+    take(dpp_mov<0xB1>(bv), __builtin_amdgcn_mov_dpp(bi, 0xB1, 0xF, 0xF, true));
+    take(dpp_mov<0x4E>(bv), __builtin_amdgcn_mov_dpp(bi, 0x4E, 0xF, 0xF, true));
+    take(dpp_mov<0x141>(bv), __builtin_amdgcn_mov_dpp(bi, 0x141, 0xF, 0xF, true));
+    take(dpp_mov<0x140>(bv), __builtin_amdgcn_mov_dpp(bi, 0x140, 0xF, 0xF, true));
+#pragma unroll
+    for (int r = 1; r < 4; r++) take(lane_value(bv, 16 * r), __builtin_amdgcn_readlane(bi, 16 * r));
     __shared__ float sv[NT / 64];
     __shared__ int si[NT / 64];
     if ((threadIdx.x & 63) == 0) {

@@ -14,7 +14,7 @@ import torch
 import torch.nn.functional as F
 
 LIB_PATH = Path(os.environ.get("CYFA_LIB", Path(__file__).with_name("libcyfa_hip.so")))
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 CYFA_OK = 0
 CYFA_ERR_VALUE = -1
@@ -74,6 +74,7 @@ class CyfaDecodeLayerArgs(ctypes.Structure):
         ("conv_weight", _c_void_p), ("abd", _c_void_p), ("abd_row", ctypes.c_longlong),
         ("dt_bias", _c_void_p), ("A_log", _c_void_p), ("gate", _c_void_p), ("gate_row", ctypes.c_longlong),
         ("norm_weight", _c_void_p), ("norm_eps", _c_float), ("norm_prescale", _c_float),
+        ("g0", _c_void_p), ("g0_row", ctypes.c_longlong), ("g_weight", _c_void_p), ("g_bias", _c_void_p),
     ]
 
 
@@ -452,17 +453,22 @@ def norm_linear(x, norm_weight, eps, weight, bias=None, residual=None, out_cols=
     return s, y.as_strided(lead + (out_w,), tuple(strides))
 
 
-def argmax_rows(x):
+def argmax_rows(x, out=None):
     """x.argmax(-1) for a bf16 CUDA tensor [..., n] (the first maximum, NaN
-    largest, as torch.argmax), one cyfa_argmax_rows launch; int64 [...]."""
-    require_device(x)
+    largest, as torch.argmax), one cyfa_argmax_rows launch; int64 [...].
+    ``out``: a contiguous int64 tensor of the result's size to write into (the
+    graphed decode step's token buffer), returned reshaped."""
+    require_device(x, out)
     if x.dtype != torch.bfloat16:
         raise ValueError("argmax_rows: bf16 input expected")
     n = x.shape[-1]
     x2 = x.reshape(-1, n)
     if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
         x2 = x2.contiguous()
-    out = torch.empty(x2.shape[0], dtype=torch.int64, device=x.device)
+    if out is None:
+        out = torch.empty(x2.shape[0], dtype=torch.int64, device=x.device)
+    elif out.dtype != torch.int64 or not out.is_contiguous() or out.numel() != x2.shape[0]:
+        raise ValueError(f"argmax_rows: out must be a contiguous int64 tensor of {x2.shape[0]} elements")
     _check(load_library().cyfa_argmax_rows(x2.data_ptr(), x2.stride(0), x2.shape[0], n, out.data_ptr(),
                                            stream_handle(x.device)), "cyfa_argmax_rows")
     return out.view(x.shape[:-1])

@@ -228,6 +228,12 @@ class CyclicFlowAttention(nn.Module):
         # When set, one-token steps update the cache's recurrent states in place
         # (the graphed decode loop); otherwise new state tensors are returned.
         self.decode_in_place = False
+        # When set, a one-token step forms the gate (g_proj[1]) inside the decode
+        # kernel instead of a separate projection launch. On MI355X it saves
+        # about 1.4% of the 400M step at B=64 (one launch per layer fewer) but
+        # costs the kernel 2.4 us of L2 reads (each workgroup reads its head's
+        # 128 KB weight slice) and loses at B=1, so it is off by default.
+        self.gate_projection_in_kernel = False
 
     def readout_table(self):
         """readout @ Phi, cached while the readout parameter is unchanged."""
@@ -364,13 +370,18 @@ class CyclicFlowAttention(nn.Module):
                                                               self.d_proj.weight), abd_bias)
             if g0_out is None:
                 g0_out = _native.linear(x, g0.weight)
-            gate = _native.linear(g0_out, g1.weight, g1.bias)
+            # g_proj[1] inside the kernel (the same bits as _native.linear) when asked and
+            # its operands are bf16; otherwise the gate is projected first
+            in_kernel = (self.gate_projection_in_kernel and g1.weight.dtype == torch.bfloat16
+                         and (g1.bias is None or g1.bias.dtype == torch.bfloat16))
+            gate = None if in_kernel else _native.linear(g0_out, g1.weight, g1.bias)
             o, state = decode_layer_step(
                 qkv, cat_cache, tail, wconv.reshape(-1, W).to(x.dtype), abd, self.dt_bias, self.A_log, gate,
                 self.o_norm.weight, self.o_norm.eps, float(self.num_slots - 1), self.readout_table(),
                 self.q_norm.weight, self.k_norm.weight, self.q_norm.eps, self.k_norm.eps, H,
                 initial_state=None if cache is None else cache["recurrent_state"], output_final_state=use_cache,
-                inplace=self.decode_in_place and cache is not None)
+                inplace=self.decode_in_place and cache is not None,
+                g_proj=(g0_out, g1.weight, g1.bias) if in_kernel else None)
             o = _native.linear(o.view(B, T, Dv), self.o_proj.weight, residual=block_in)
             cq, ck, cv = tail[..., :Dk], tail[..., Dk:2 * Dk], tail[..., 2 * Dk:]
             new_cache = {"recurrent_state": state, "conv_state": (cq, ck, cv)} if use_cache else None

@@ -258,7 +258,10 @@ class GraphedDecodeStep:
                             a.copy_(b)
                 self.logits = out["logits"]
                 last = out["logits"][:, -1:]
-                self.tokens.copy_(_native.argmax_rows(last) if inference_fast_path(last) else last.argmax(-1))
+                if inference_fast_path(last):
+                    _native.argmax_rows(last, out=self.tokens)  # straight into the token buffer
+                else:
+                    self.tokens.copy_(last.argmax(-1))
         finally:
             for attn in layers:
                 attn.decode_in_place = False

@@ -108,7 +108,7 @@ def fused_recurrent_cyfa(
 
 def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias, A_log, gate, norm_weight, norm_eps,
                       norm_prescale, table, q_norm_weight, k_norm_weight, q_norm_eps, k_norm_eps, num_heads,
-                      initial_state=None, output_final_state=False, inplace=False, split=False):
+                      initial_state=None, output_final_state=False, inplace=False, split=False, g_proj=None):
     """The layer's one-token step around the op in one kernel (cyfa_decode_layer_step).
 
     qkv [B, 1, 3 H 256] is the projection before the short convolution (rows
@@ -118,22 +118,38 @@ def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias
     with its biases, gate [B, 1, H 256]. Returns (o', states) with o' the gated
     output norm o_norm(o * norm_prescale, gate) of the op's output, [B, 1, H, 256],
     and the states as fused_recurrent_cyfa returns them. ``split``: as in
-    fused_recurrent_cyfa.
+    fused_recurrent_cyfa. ``g_proj`` (with gate None): (g0 [B, 1, 256], weight
+    [H 256, 256], bias [H 256] or None), and the kernel forms the gate as
+    linear(g0, weight, bias) - the second projection of g_proj - with the same
+    bits as _native.linear.
     """
     B = qkv.shape[0]
     H, K, V, M = num_heads, 256, 256, table.shape[-1]
     state_in = tuple(initial_state) if initial_state is not None else ()
+    if (gate is None) == (g_proj is None):
+        raise ValueError("decode_layer_step: pass exactly one of gate and g_proj")
+    g0, g_w, g_b = g_proj if g_proj is not None else (None, None, None)
     dev = _native.require_device(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias, A_log, gate, norm_weight,
-                                 table, q_norm_weight, k_norm_weight, *state_in)
+                                 table, q_norm_weight, k_norm_weight, g0, g_w, g_b, *state_in)
     D = 2 * H * K + H * V
     if qkv.shape[-1] != D or qkv.stride(-1) != 1 or conv_weight.shape != (D, 4) or not conv_weight.is_contiguous():
         raise ValueError("decode_layer_step: qkv must have 3 H 256 unit-stride columns and conv_weight [3 H 256, 4]")
-    for name, x in (("qkv", qkv), ("abd", abd), ("gate", gate), ("conv_weight", conv_weight),
-                    ("conv_cache_out", conv_cache_out)):
+    tensors = (("qkv", qkv), ("abd", abd), ("conv_weight", conv_weight), ("conv_cache_out", conv_cache_out))
+    tensors += (("gate", gate),) if gate is not None else (("g0", g0), ("g_proj weight", g_w))
+    tensors += (("g_proj bias", g_b),) if g_b is not None else ()
+    for name, x in tensors:
         if x.dtype != torch.bfloat16 or x.stride(-1) != 1:
             raise ValueError(f"decode_layer_step: {name} must be bfloat16 with unit last-dim stride")
-    if abd.shape[-1] != 3 * H or gate.shape[-1] != H * V:
+    if abd.shape[-1] != 3 * H or (gate is not None and gate.shape[-1] != H * V):
         raise ValueError(f"decode_layer_step: abd needs {3 * H} and gate {H * V} columns")
+    if g_proj is not None:
+        if g0.shape[-1] != V or g0.numel() != B * V or g_w.shape != (H * V, V) or (g_b is not None and g_b.shape != (H * V,)):
+            raise ValueError(f"decode_layer_step: g_proj needs g0 [{B}, 1, {V}], weight [{H * V}, {V}], bias [{H * V}]")
+        g0 = g0.reshape(B, V)  # a view for the layer's column slice of the input projection
+        if g0.stride(1) != 1 or g0.stride(0) % 8 or g0.data_ptr() % 16:
+            g0 = g0.contiguous()
+        g_w = g_w.detach().contiguous()
+        g_b = None if g_b is None else g_b.detach().contiguous()
     if conv_cache_out.dim() != 3 or tuple(conv_cache_out.shape) != (B, 3, D):
         raise ValueError(f"decode_layer_step: conv_cache_out must be [{B}, 3, {D}]")
     check_table(table, H, M)
@@ -177,9 +193,10 @@ def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias
         qkv=qkv.data_ptr(), qkv_row=qkv.stride(0), conv_cache=_native.ptr(conv_cache),
         conv_cache_out=conv_cache_out.data_ptr(), cache_row=conv_cache_out.stride(1),
         cache_batch=conv_cache_out.stride(0), conv_weight=conv_weight.data_ptr(), abd=abd.data_ptr(),
-        abd_row=abd.stride(0), dt_bias=db.data_ptr(), A_log=al.data_ptr(), gate=gate.data_ptr(),
-        gate_row=gate.stride(0), norm_weight=nw.data_ptr(), norm_eps=float(norm_eps),
-        norm_prescale=float(norm_prescale),
+        abd_row=abd.stride(0), dt_bias=db.data_ptr(), A_log=al.data_ptr(), gate=_native.ptr(gate),
+        gate_row=0 if gate is None else gate.stride(0), norm_weight=nw.data_ptr(), norm_eps=float(norm_eps),
+        norm_prescale=float(norm_prescale), g0=_native.ptr(g0), g0_row=0 if g0 is None else g0.stride(0),
+        g_weight=_native.ptr(g_w), g_bias=_native.ptr(g_b),
     )
     _native.decode_layer_step(args, layer, dev)
     return o, ((hk_out, hv_out, c_out) if output_final_state else None)

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define CYFA_ABI_VERSION 3
+#define CYFA_ABI_VERSION 4
 
 enum {
     CYFA_OK = 0,
@@ -186,10 +186,18 @@ typedef struct CyfaDecodeLayerArgs {
     const void *abd;              /* bf16 rows [B, abd_row]: a | b | d (H each), b and d biases added */
     long long abd_row;
     const float *dt_bias, *A_log; /* f32 [H] */
-    const void *gate;             /* bf16 rows [B, gate_row]: [H 256], 8-byte aligned */
+    const void *gate;             /* bf16 rows [B, gate_row]: [H 256], 8-byte aligned; or NULL, and
+                                     the gate is formed in the kernel from g0 (below) */
     long long gate_row;
     const float *norm_weight;     /* f32 [256] */
     float norm_eps, norm_prescale;
+    /* With gate NULL: gate = bf16(g0 g_weight^T + g_bias), the second projection
+       of g_proj (layers/cyfa.py:211-214), with the summation order of
+       cyfa_linear_rows, so both ways give the same bits. */
+    const void *g0;               /* bf16 rows [B, g0_row]: [256] (the output of g_proj[0]), 16-byte aligned */
+    long long g0_row;             /* a multiple of 8 */
+    const void *g_weight;         /* bf16 [H 256, 256], 16-byte aligned */
+    const void *g_bias;           /* nullable bf16 [H 256] */
 } CyfaDecodeLayerArgs;
 
 /* cyfa_decode_step with the layer around it in the same kernel: q, k and v

@@ -343,15 +343,18 @@ def test_norm_linear_rows(M, residual, swiglu, K):
     assert rows <= max(1, M // 10), f"{rows} of {M} rows differ from rms_norm + linear"
 
 
-@pytest.mark.parametrize("B,state,inplace,split", [(3, True, False, True), (2, False, False, True),
-                                                   (4, True, True, True), (64, True, True, True),
-                                                   (3, True, True, False), (1, True, True, True)])
-def test_decode_layer_step_equals_separate_kernels(B, state, inplace, split):
+@pytest.mark.parametrize("B,state,inplace,split,own_gate", [
+    (3, True, False, True, False), (2, False, False, True, False), (4, True, True, True, False),
+    (64, True, True, True, False), (3, True, True, False, False), (1, True, True, True, False),
+    (64, True, True, False, True), (3, True, True, True, True), (1, False, False, False, True),
+    (17, True, False, False, True)])
+def test_decode_layer_step_equals_separate_kernels(B, state, inplace, split, own_gate):
     """cyfa_decode_layer_step (short convolution, gates, decode op and gated
     output norm in one kernel, or in the two kernels of the small-batch split)
-    against the four separate kernels on the same inputs: the same arithmetic
-    in the same order, so outputs, states and the new conv cache are
-    bit-identical."""
+    against the separate kernels on the same inputs: the same arithmetic in
+    the same order, so outputs, states and the new conv cache are
+    bit-identical. own_gate: the kernel also forms the gate from g0 (the
+    second projection of g_proj), against _native.linear(g0, W, b)."""
     from cyclic_flow_attention import _native
     from cyclic_flow_attention.ops import fused_recurrent_cyfa
     from cyclic_flow_attention.ops.fused_recurrent import decode_layer_step
@@ -365,6 +368,12 @@ def test_decode_layer_step_equals_separate_kernels(B, state, inplace, split):
     abd = torch.randn(B, 1, 3 * H, generator=gen).bfloat16().to(DEV)
     dt_bias, A_log = torch.randn(H, generator=gen).to(DEV), torch.randn(H, generator=gen).to(DEV)
     gate = torch.randn(B, 1, H * 256, generator=gen).bfloat16().to(DEV)
+    g0_rows = torch.randn(B, 1, 256 + 24, generator=gen).bfloat16().to(DEV)
+    g0 = g0_rows[..., 8:264]  # a column slice, rows 280 apart (as in the layer's input projection)
+    g_w = (0.06 * torch.randn(H * 256, 256, generator=gen)).bfloat16().to(DEV)
+    g_b = (0.5 * torch.randn(H * 256, generator=gen)).bfloat16().to(DEV)
+    if own_gate:
+        gate = _native.linear(g0, g_w, g_b)
     nw = (1 + 0.1 * torch.randn(256, generator=gen)).to(DEV)
     qw, kw = (1 + 0.1 * torch.randn(256, generator=gen)).to(DEV), (1 + 0.1 * torch.randn(256, generator=gen)).to(DEV)
     readout = (torch.eye(127).expand(H, 127, 127) + 0.05 * torch.randn(H, 127, 127, generator=gen)).to(DEV)
@@ -386,9 +395,10 @@ def test_decode_layer_step_equals_separate_kernels(B, state, inplace, split):
         cache_in = None if cache is None else cache.clone()
         tail = cache_in if (inplace and cache_in is not None) else torch.empty(B, 3, D, dtype=torch.bfloat16, device=DEV)
         st_in = None if init is None else tuple(t.clone() for t in init)
-        got, st2 = decode_layer_step(qkv, cache_in, tail, wconv, abd, dt_bias, A_log, gate, nw, 1e-6, 127.0, table, qw,
-                                     kw, 1e-6, 1e-6, H, initial_state=st_in, output_final_state=True,
-                                     inplace=inplace and st_in is not None, split=split)
+        got, st2 = decode_layer_step(qkv, cache_in, tail, wconv, abd, dt_bias, A_log, None if own_gate else gate, nw,
+                                     1e-6, 127.0, table, qw, kw, 1e-6, 1e-6, H, initial_state=st_in,
+                                     output_final_state=True, inplace=inplace and st_in is not None, split=split,
+                                     g_proj=(g0, g_w, g_b) if own_gate else None)
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
     assert torch.equal(tail, tail_ref)
