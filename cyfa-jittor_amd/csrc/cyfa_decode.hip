@@ -217,7 +217,7 @@ __device__ __forceinline__ void stage_table(float* s_tab, const float4 (&tab)[4]
 }
 
 // The gate of (b, h) as the second projection of g_proj (layers/cyfa.py:
-// 211-214) when the caller passes g0 instead of the gate: gate = bf16(g0 W^T +
+// 292-295, 349) when the caller passes g0 instead of the gate: gate = bf16(g0 W^T +
 // bias) for the head's V = 256 columns, in linear_rows_kernel's summation
 // order for K = 256 (eight 32-deep k-steps, one per wave there): each k-step
 // on one v_mfma_f32_16x16x32_bf16 from zero, with g0 in row 0 of A and the

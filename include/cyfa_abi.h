@@ -192,7 +192,7 @@ typedef struct CyfaDecodeLayerArgs {
     const float *norm_weight;     /* f32 [256] */
     float norm_eps, norm_prescale;
     /* With gate NULL: gate = bf16(g0 g_weight^T + g_bias), the second projection
-       of g_proj (layers/cyfa.py:211-214), with the summation order of
+       of g_proj (layers/cyfa.py:292-295, 349), with the summation order of
        cyfa_linear_rows, so both ways give the same bits. */
     const void *g0;               /* bf16 rows [B, g0_row]: [256] (the output of g_proj[0]), 16-byte aligned */
     long long g0_row;             /* a multiple of 8 */
