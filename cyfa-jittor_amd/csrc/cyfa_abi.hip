@@ -297,6 +297,7 @@ int chunk_fwd(const CyfaChunkArgs* a, const CyfaOutNormArgs* on, void* hip_strea
     p.seg_decay = (float*)(base + ws.seg_decay);
     p.omega = (__bf16*)(base + ws.omega);
     p.tab_exp = (int*)(base + ws.tab_exp);
+    p.tab16 = (_Float16*)(base + ws.tab16);
     if (cyfa::launch_prefill(p, (hipStream_t)hip_stream) != 0)
         return fail(CYFA_ERR_UNSUPPORTED, "cyfa_chunk_fwd: launch refused");
     return check_launch(on ? "cyfa_chunk_fwd_normed" : "cyfa_chunk_fwd");

@@ -14,6 +14,7 @@ constexpr int kSlots = 128;   // stored slot coordinates M
 constexpr int kActive = 127;  // active slots R = M - 1
 constexpr int kPairs = 64;    // Fourier pairs M / 2
 constexpr int kChunk = 64;    // tokens per chunk
+constexpr int kMaxSegments = 8192;  // segments per sequence in a prefill sweep
 
 typedef __bf16 bf16_t;
 typedef _Float16 f16_t;

@@ -76,6 +76,7 @@ struct PrefillParams {
     float* seg_decay;  // [B*H, P] product of alpha over each segment
     __bf16* omega;     // [B*H, Tp, 128] slot weights between the two passes
     int* tab_exp;      // [B*H] power-of-two exponent e of the head's readout table: max |table| 2^-e < 2^14
+    _Float16* tab16;   // [H, 128, 128] table 2^-e in fp16, row 127 zero (written by segment_state)
 };
 
 // Isolated ScalarGatedLA, one pass (scalar_la): every operand read from memory.
@@ -129,7 +130,7 @@ struct ConvParams {
 };
 
 struct WorkspaceLayout {
-    size_t lam, gam, seg, seg_exp, seg_decay, omega, tab_exp, total;
+    size_t lam, gam, seg, seg_exp, seg_decay, omega, tab_exp, tab16, total;
 };
 
 // Largest byte span of one sequence's rows that the kernels' 32-bit buffer

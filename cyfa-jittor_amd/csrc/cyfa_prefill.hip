@@ -842,9 +842,9 @@ __device__ __forceinline__ void segment_state_body(const PrefillParams& p, int b
 }
 
 // Power-of-two exponent e of head h's readout table with max |table| 2^-e in
-// [2^13, 2^14) (0 for an all-zero or non-finite table): pass 1 stages the
-// table in fp16 as table 2^-e, so any finite table keeps fp16's full
-// precision and range.
+// [2^13, 2^14) (0 for an all-zero or non-finite table), and the table in fp16
+// as table 2^-e (workgroups of batch 0), which pass 1 stages: any finite table
+// keeps fp16's full precision and range.
 __device__ __forceinline__ void table_exponent(const PrefillParams& p, int h, int bh) {
     __shared__ float part[8];
     const int tid = threadIdx.x;
@@ -868,8 +868,21 @@ __device__ __forceinline__ void table_exponent(const PrefillParams& p, int h, in
             e -= 14;
         }
         p.tab_exp[bh] = e;
+        part[0] = ldexpf(1.f, -e);
     }
     __syncthreads();
+    // The fp16 table of head h, for every sequence's pass 1 (the exponent
+    // depends on the head only).
+    if (blockIdx.y == 0) {
+        const float ts = part[0];
+        const float* tb = p.table + (size_t)h * kActive * kSlots;
+        f16_t* dst = p.tab16 + (size_t)h * kSlots * kSlots;
+        for (int i = tid; i < kSlots * kSlots / 4; i += 512) {
+            const int r = i >> 5;
+            const float4 t = r < kActive ? *reinterpret_cast<const float4*>(tb + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            *reinterpret_cast<f16x4*>(dst + 4 * i) = f16x4{(f16_t)(t.x * ts), (f16_t)(t.y * ts), (f16_t)(t.z * ts), (f16_t)(t.w * ts)};
+        }
+    }
 }
 
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void segment_state_kernel(PrefillParams p) {
@@ -900,39 +913,95 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
 // hit that XCD's L2.
 // seg: E_0 of this sequence and part (E_i at seg + i * seg_stride elements);
 // seg_exp: its wave exponents (E_i's at seg_exp + i * exp_stride); decay: a_0.
-template <typename H0Index>
-__device__ __forceinline__ void load_start_state(const _Float16* seg, size_t seg_stride, const int* seg_exp,
-                                                 int exp_stride, const float* decay, int j, const float* h0,
-                                                 H0Index h0_index, f32x4 acc[8][2]) {
-    const int lane = threadIdx.x & 63, w = wave_id();
+//
+// The E_i go through the vector memory pipeline at one 1 KiB wave load per
+// 16 cycles of the CU, so the sum issues exactly the loads it uses: blocks of
+// at most SE_BLOCK states, each straight-line code (a compile-time count) with
+// SE_DEPTH states in flight. The first block's loads go out before the
+// caller's first-chunk loads (issue_first), so that adding E_{j-1} does not
+// wait for those; vector loads complete in issue order.
+constexpr int SE_DEPTH = 3;
+constexpr int SE_BLOCK = 8;
+constexpr uint32_t SE_DEAD = 0x80000000u;
+
+struct StartStates {
+    rsrc_t e, exps, decays;  // E_0 .. E_{j-1}; their exponents (exp_stride apart); a_0 ..
+    uint32_t lane_off, stride_b, exp_stride_b;
+    __device__ __forceinline__ uint32_t off(int i, int x) const { return lane_off + 1024u * x + (uint32_t)i * stride_b; }
+};
+
+// acc += (running decay product) 2^e_i E_i for i = i0, i0 - 1, .., i0 - NE + 1,
+// in that order; `a` carries the product of the decays already passed.
+template <int NE, int DEPTH, typename F>
+__device__ __forceinline__ void add_states(const StartStates& st, int i0, float& a, f32x4 acc[8][2], F&& after_first) {
+    constexpr int D = NE < DEPTH ? NE : DEPTH;
+    const int lane = threadIdx.x & 63;
+    // lane l < NE: exponent and decay of E_{i0 - l}
+    const int le = i0 - lane;
+    const uint32_t dm = ((uint32_t)(le | (NE - 1 - lane)) >> 31) * SE_DEAD;
+    const int expv = (int)__builtin_amdgcn_raw_buffer_load_b32(st.exps, ((uint32_t)le * st.exp_stride_b) | dm, 0, 0);
+    const int decv = (int)__builtin_amdgcn_raw_buffer_load_b32(st.decays, ((uint32_t)le * 4) | dm, 0, 0);
+    f16x8 v[D][8];
 #pragma unroll
-    for (int x = 0; x < 8; x++) acc[x][0] = acc[x][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    seg_exp += w;
-    // E_i for i = j - 1 down to 0; the loads of E_{i-1} are in flight while E_i is added.
-    f16x8 v[8];
-    if (j > 0) {
+    for (int d = 0; d < D; d++)
 #pragma unroll
         for (int x = 0; x < 8; x++)
-            v[x] = *reinterpret_cast<const f16x8*>(seg + (size_t)(j - 1) * seg_stride + frag_offset(w, x, lane));
-    }
-    float a = 1.f;
-    for (int i = j - 1; i >= 0; i--) {
-        f16x8 nv[8];
-        if (i > 0) {
+            v[d][x] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(st.e, st.off(i0 - d, x), 0, 0));
+    after_first();
 #pragma unroll
-            for (int x = 0; x < 8; x++)
-                nv[x] = *reinterpret_cast<const f16x8*>(seg + (size_t)(i - 1) * seg_stride + frag_offset(w, x, lane));
-        }
-        const float ai = ldexpf(a, seg_exp[i * exp_stride]);
+    for (int d = 0; d < NE; d++) {
+        const float ai = ldexpf(a, __builtin_amdgcn_readlane(expv, d));
 #pragma unroll
         for (int x = 0; x < 8; x++)
 #pragma unroll
             for (int c = 0; c < 2; c++)
 #pragma unroll
-                for (int q = 0; q < 4; q++) acc[x][c][q] = fmaf(ai, (float)v[x][4 * c + q], acc[x][c][q]);
-        a *= decay[i];
+                for (int q = 0; q < 4; q++) acc[x][c][q] = fmaf(ai, (float)v[d % D][x][4 * c + q], acc[x][c][q]);
+        a *= __builtin_bit_cast(float, __builtin_amdgcn_readlane(decv, d));
+        if (d + D < NE) {
 #pragma unroll
-        for (int x = 0; x < 8; x++) v[x] = nv[x];
+            for (int x = 0; x < 8; x++)
+                v[d % D][x] =
+                    __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(st.e, st.off(i0 - d - D, x), 0, 0));
+        }
+    }
+}
+
+// issue_first() is called exactly once, after the first states' loads.
+// DEPTH: states in flight (SE_DEPTH unless the caller's registers are short).
+template <int DEPTH = SE_DEPTH, typename H0Index, typename Issue>
+__device__ __forceinline__ void load_start_state(const _Float16* seg, size_t seg_stride, const int* seg_exp,
+                                                 int exp_stride, const float* decay, int j, const float* h0,
+                                                 H0Index h0_index, f32x4 acc[8][2], Issue&& issue_first) {
+    const int lane = threadIdx.x & 63, w = wave_id();
+#pragma unroll
+    for (int x = 0; x < 8; x++) acc[x][0] = acc[x][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float a = 1.f;
+    if (j == 0) {
+        issue_first();
+    } else {
+        // Host side: P <= kMaxSegments keeps j seg_stride 2 below 2^31.
+        StartStates st;
+        st.e = make_rsrc(seg, (size_t)j * seg_stride * 2);
+        st.exps = make_rsrc(seg_exp + w, (size_t)j * exp_stride * 4);
+        st.decays = make_rsrc(decay, (size_t)j * 4);
+        st.lane_off = (uint32_t)frag_offset(w, 0, lane) * 2;
+        st.stride_b = (uint32_t)seg_stride * 2;
+        st.exp_stride_b = (uint32_t)exp_stride * 4;
+        // The first block takes the remainder, so the later ones are full.
+        const int r = (j - 1) % SE_BLOCK + 1;
+        switch (r) {
+            case 1: add_states<1, DEPTH>(st, j - 1, a, acc, issue_first); break;
+            case 2: add_states<2, DEPTH>(st, j - 1, a, acc, issue_first); break;
+            case 3: add_states<3, DEPTH>(st, j - 1, a, acc, issue_first); break;
+            case 4: add_states<4, DEPTH>(st, j - 1, a, acc, issue_first); break;
+            case 5: add_states<5, DEPTH>(st, j - 1, a, acc, issue_first); break;
+            case 6: add_states<6, DEPTH>(st, j - 1, a, acc, issue_first); break;
+            case 7: add_states<7, DEPTH>(st, j - 1, a, acc, issue_first); break;
+            default: add_states<8, DEPTH>(st, j - 1, a, acc, issue_first); break;
+        }
+        static_assert(SE_BLOCK == 8, "the cases above cover 1 .. SE_BLOCK");
+        for (int i0 = j - 1 - r; i0 >= 0; i0 -= SE_BLOCK) add_states<SE_BLOCK, DEPTH>(st, i0, a, acc, [] {});
     }
     if (h0) {
 #pragma unroll
@@ -945,12 +1014,12 @@ __device__ __forceinline__ void load_start_state(const _Float16* seg, size_t seg
 }
 
 // The same for the two parts of a prefill call's segment states.
-template <typename H0Index>
+template <int DEPTH = SE_DEPTH, typename H0Index, typename Issue>
 __device__ __forceinline__ void load_start_state(const PrefillParams& p, int bh, int j, int part, const float* h0,
-                                                 H0Index h0_index, f32x4 acc[8][2]) {
-    load_start_state(p.seg + (size_t)bh * (p.P - 1) * SEG + part * SEG_K, SEG,
+                                                 H0Index h0_index, f32x4 acc[8][2], Issue&& issue_first) {
+    load_start_state<DEPTH>(p.seg + (size_t)bh * (p.P - 1) * SEG + part * SEG_K, SEG,
                      p.seg_exp + (size_t)bh * (p.P - 1) * 16 + part * 8, 16, p.seg_decay + bh * p.P, j, h0, h0_index,
-                     acc);
+                     acc, issue_first);
 }
 
 // ---------------------------------------------------------------------------
@@ -1147,51 +1216,49 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     const int y = w >> 2, mq = w & 3;
     const float log2_scale = p.log2_scale;
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
-    if (tid < KD) {
-        sQw[tid] = p.q_w[tid];
-        sKw[tid] = p.k_w[tid];
-    }
     const Seq sq = make_seq(p, b, h, bh);
     // Staging is split between the halves: every wave normalises its share of
     // q at the top of a chunk; the waves of the second half (u = tid - 256)
     // load and stage k_hat, the write-vector tile and the gates of the next
     // chunk while the first half runs the chunk's slot readout.
     const int u = tid - 256;
-    bf16x8 qraw[4], kraw[8];
-    GateRegs gr{};
-    // The first chunk's loads and the table's are issued before the start
-    // state is summed, so that their latency overlaps it.
-    issue_rows(sq, sq.q, p.T, n0 * 64, qraw);
-    if (y == 1) {
-        issue_rows_q(sq, sq.k, p.T, n0 * 64, u, kraw);
-        gr = issue_gates(sq, p.T, n0 * 64);
-    }
-    // The table goes to LDS in fp16 as table 2^-et (et from segment_state:
-    // max |table| 2^-et < 2^14); the readout undoes the factor.
+    // The table is staged in fp16 as table 2^-et (segment_state wrote it and
+    // et: max |table| 2^-et < 2^14); the readout undoes the factor.
     const int et = p.tab_exp[bh];
     const float tab_scale = ldexpf(1.f, et);
-    {
-        const float* tb = p.table + (size_t)h * kActive * kSlots;
-        const float ts = ldexpf(1.f, -et);
-        float4 tv[8];
+    // The first chunk's loads follow the start state's first loads (see
+    // load_start_state). kraw holds k rows in the second half and the table's
+    // rows in the first: the same eight loads per lane, with no branch among
+    // them (a branch would make the waits for the start state cover them).
+    bf16x8 qraw[4], kraw[8];
+    GateRegs gr;
+    float qw, kw;
+    f32x4 acc[8][2];
+    load_start_state<2>(p, bh, j, 0, p.h0_k ? p.h0_k + (size_t)bh * SEG_K : nullptr,
+                     [&](int kb, int c, int i) { return (HALF * y + state_row(kb, lg, i)) * kSlots + 32 * mq + 16 * c + lr; },
+                     acc, [&] {
+                         issue_rows(sq, sq.q, p.T, n0 * 64, qraw);
+                         const int t = min(n0 * 64 + (u >> 2), p.T - 1);
+                         const rsrc_t src = y ? sq.k : make_rsrc(p.tab16 + (size_t)h * kSlots * kSlots, kSlots * kSlots * 2);
+                         const uint32_t base = y ? (uint32_t)t * sq.row16 + 128 * (u & 3) : 16 * tid;
+                         const uint32_t step = y ? 16 : 4096;
 #pragma unroll
-        for (int it = 0; it < 8; it++) {
-            const int idx = tid + 512 * it, r = idx >> 5, m4 = (idx & 31) * 4;
-            tv[it] = r < kActive ? *reinterpret_cast<const float4*>(tb + r * kSlots + m4) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+                         for (int i = 0; i < 8; i++) kraw[i] = ld_b128(src, base + step * i);
+                         gr = issue_gates(sq, p.T, n0 * 64);
+                         qw = p.q_w[tid & (KD - 1)];
+                         kw = p.k_w[tid & (KD - 1)];
+                     });
+    if (tid < KD) {
+        sQw[tid] = qw;
+        sKw[tid] = kw;
+    }
+    if (y == 0) {  // table rows 16 i + (tid >> 4), columns 8 (tid & 15) ..
 #pragma unroll
-        for (int it = 0; it < 8; it++) {
-            const int idx = tid + 512 * it, r = idx >> 5, m4 = (idx & 31) * 4;
-            *reinterpret_cast<f16x4*>(sTab + r * RS + m4) =
-                f16x4{(f16_t)(tv[it].x * ts), (f16_t)(tv[it].y * ts), (f16_t)(tv[it].z * ts), (f16_t)(tv[it].w * ts)};
-        }
+        for (int i = 0; i < 8; i++)
+            *reinterpret_cast<bf16x8*>(reinterpret_cast<bf16_t*>(sTab) + (16 * i + (tid >> 4)) * RS + 8 * (tid & 15)) = kraw[i];
     }
     zero_scores(sP, 2);  // the two blocks above the diagonal that the intra product reads stay zero
     bf16_t* sPy = sP + y * (TileP::bytes / 2);
-    f32x4 acc[8][2];
-    load_start_state(p, bh, j, 0, p.h0_k ? p.h0_k + (size_t)bh * SEG_K : nullptr,
-                     [&](int kb, int c, int i) { return (HALF * y + state_row(kb, lg, i)) * kSlots + 32 * mq + 16 * c + lr; },
-                     acc);
     StateScale sc;
     __syncthreads();  // norm weights and table staged, score tiles zeroed
     if (y == 1) {
@@ -1353,19 +1420,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
     const int bh = cd.bh, j = cd.j, b = cd.b, h = cd.h;
     const int lane = threadIdx.x & 63, w = wave_id(), lr = lane & 15, lg = lane >> 4;
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
-    if (NORM && threadIdx.x < VD) sNw[threadIdx.x] = p.on_w[threadIdx.x];
     const Seq sq = make_seq(p, b, h, bh);
     const rsrc_t rom = make_rsrc(p.omega + (size_t)bh * p.Tp * kSlots, (size_t)p.Tp * kSlots * 2);
     const uint32_t o_lane = (uint32_t)lr * sq.row16 + 2 * (32 * w + 4 * lg);
-    // The first chunk's loads are issued before the start state is summed.
+    // The first chunk's loads follow the start state's first loads.
     bf16x8 vraw[4], om[2];
-    issue_rows(sq, sq.v, p.T, n0 * 64, vraw);
-    issue_omega(rom, n0 * 64, om);
-    GateRegs gr = issue_gates(sq, p.T, n0 * 64);
-    zero_scores(sP, 1);
+    GateRegs gr;
+    float nw = 0.f;
     f32x4 acc[8][2];
     load_start_state(p, bh, j, 1, p.h0_v ? p.h0_v + (size_t)bh * SEG_V : nullptr,
-                     [&](int mb, int c, int i) { return state_row(mb, lg, i) * VD + 32 * w + 16 * c + lr; }, acc);
+                     [&](int mb, int c, int i) { return state_row(mb, lg, i) * VD + 32 * w + 16 * c + lr; }, acc,
+                     [&] {
+                         issue_rows(sq, sq.v, p.T, n0 * 64, vraw);
+                         issue_omega(rom, n0 * 64, om);
+                         gr = issue_gates(sq, p.T, n0 * 64);
+                         if (NORM) nw = p.on_w[threadIdx.x & (VD - 1)];
+                     });
+    if (NORM && threadIdx.x < VD) sNw[threadIdx.x] = nw;
+    zero_scores(sP, 1);
     StateScale sc;
 
     for (int n = n0; n < n1; n++) {
@@ -1675,7 +1747,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void s
 template <typename H0Index>
 __device__ __forceinline__ void sla_start_state(const SlaParams& p, int bh, int j, H0Index h0_index, f32x4 acc[8][2]) {
     load_start_state(p.seg + (size_t)bh * (p.P - 1) * (KD * HALF), KD * HALF, p.seg_exp + (size_t)bh * (p.P - 1) * 8, 8,
-                     p.seg_decay + bh * p.P, j, p.h0 ? p.h0 + (size_t)bh * (KD * HALF) : nullptr, h0_index, acc);
+                     p.seg_decay + bh * p.P, j, p.h0 ? p.h0 + (size_t)bh * (KD * HALF) : nullptr, h0_index, acc, [] {});
 }
 
 // Shape A sweep (K = 256, V = 128), grid (H, B, P), 512 threads. Wave w works
@@ -2011,6 +2083,9 @@ void choose_segments(int BH, int N, int* P, int* L) {
         const int forced = atoi(env);
         if (forced > 0) l = forced < N ? forced : N;
     }
+    // At most kMaxSegments segments: the sweeps address the stored segment
+    // states of a sequence with 32-bit offsets below 2^31.
+    if ((N + l - 1) / l > kMaxSegments) l = (N + kMaxSegments - 1) / kMaxSegments;
     *L = l;
     *P = (N + l - 1) / l;
 }
@@ -2032,7 +2107,8 @@ WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V) {
     w.seg_decay = align256(w.seg_exp + nseg * 16 * sizeof(int));
     w.omega = align256(w.seg_decay + BH * P * sizeof(float));
     w.tab_exp = align256(w.omega + BH * Tp * kSlots * 2);
-    w.total = align256(w.tab_exp + BH * sizeof(int));
+    w.tab16 = align256(w.tab_exp + BH * sizeof(int));
+    w.total = align256(w.tab16 + (size_t)H * kSlots * kSlots * sizeof(_Float16));
     return w;
 }
 
