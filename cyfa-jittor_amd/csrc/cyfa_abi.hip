@@ -418,10 +418,11 @@ int cyfa_linear_rows(const CyfaLinearArgs* a, void* hip_stream) {
 int cyfa_norm_linear_rows(const CyfaLinearArgs* a, const CyfaRowNormArgs* n, void* hip_stream) {
     cyfa::LinearParams p;
     if (int rc = linear_params(a, "cyfa_norm_linear_rows", p)) return rc;
-    if (!n || !n->weight) return fail(CYFA_ERR_VALUE, "cyfa_norm_linear_rows: null norm args or weight");
+    if (!n) return fail(CYFA_ERR_VALUE, "cyfa_norm_linear_rows: null norm args");
     if (a->K > cyfa::LINEAR_NORM_MAX_K)
         return fail(CYFA_ERR_UNSUPPORTED, "cyfa_norm_linear_rows: K=%d above %d", a->K, cyfa::LINEAR_NORM_MAX_K);
-    if (!aligned(n->weight, 16)) return fail(CYFA_ERR_ALIGN, "cyfa_norm_linear_rows: norm weight needs 16-byte alignment");
+    if (n->weight && !aligned(n->weight, 16))
+        return fail(CYFA_ERR_ALIGN, "cyfa_norm_linear_rows: norm weight needs 16-byte alignment");
     if (n->residual) {
         if (!n->sum_out) return fail(CYFA_ERR_VALUE, "cyfa_norm_linear_rows: residual without sum_out");
         if (n->ldr < a->K || n->ldr % 8 != 0)
@@ -430,6 +431,7 @@ int cyfa_norm_linear_rows(const CyfaLinearArgs* a, const CyfaRowNormArgs* n, voi
             return fail(CYFA_ERR_ALIGN, "cyfa_norm_linear_rows: residual and sum_out need 16-byte alignment");
     }
     p.norm_weight = n->weight;
+    p.norm_folded = n->weight ? 0 : 1;  // NULL: the norm weight is folded into the projection's weight
     p.norm_eps = n->eps;
     p.norm_residual = (const __bf16*)n->residual;
     p.norm_sum_out = n->residual ? (__bf16*)n->sum_out : nullptr;

@@ -160,8 +160,12 @@ struct LinearParams {
     long long ld_add;
     // Optional RMS norm of the x rows before the product (over all K columns):
     //   s = norm_residual ? bf16(x + residual) : x   (norm_sum_out receives s)
-    //   the product reads bf16(s * rsqrt(mean(s^2) + norm_eps) * norm_weight)
-    const float* norm_weight;     // nullable: x is used as given
+    //   the product reads bf16(s * rsqrt(mean(s^2) + norm_eps) * norm_weight),
+    //   or, with norm_folded (norm_weight null; the caller has multiplied the
+    //   norm weight into w), y = rsqrt(mean(s^2) + norm_eps) (s W^T) + bias
+    //   with the row scale applied to the fp32 product
+    const float* norm_weight;     // nullable: x is used as given (unless norm_folded)
+    int norm_folded;
     const __bf16* norm_residual;  // nullable [M, K], rows ldr elements apart
     __bf16* norm_sum_out;         // [M, K], rows ldr apart; set with norm_residual; aliases no input
     long long ldr;

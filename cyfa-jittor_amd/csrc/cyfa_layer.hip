@@ -156,8 +156,11 @@ __device__ __forceinline__ bf16x8 lin_frag(const char* region, int g, int u, int
 // a branch, even a uniform one, makes the compiler's wait counts assume the
 // worst and wait for loads issued later). The launcher picks P from the run's
 // length (linear_pairs), so few loads fall past the run.
-template <int RT, int CT, int P, bool NORM>
+// NM: 0 no norm, 1 the row norm with its weight applied to the operand, 2 the
+// row norm folded (the weight is in W; the row scale multiplies the product).
+template <int RT, int CT, int P, int NM>
 __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
+    constexpr bool NORM = NM != 0;
     constexpr int TM = 16 * RT, TN = 16 * CT, OUT = TM * TN, R = (OUT + 511) / 512;
     constexpr int U = 2 * P;  // k-steps per batch
     static_assert(P >= 1 && P <= lin_pairs(RT, CT), "loads in flight per lane");
@@ -167,7 +170,8 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
     __shared__ __align__(16) char lds[LDS];
     float(*part)[TM][TN + 1] = reinterpret_cast<float(*)[TM][TN + 1]>(lds);
     __shared__ float sq[NORM ? 8 : 1][NORM ? TM : 1];
-    __shared__ float4 snw[NORM ? LINEAR_NORM_MAX_K / 4 : 1];
+    __shared__ float4 snw[NM == 1 ? LINEAR_NORM_MAX_K / 4 : 1];
+    __shared__ float srs[NM == 2 ? TM : 1];  // folded norm: the row scales
     // The wave index comes from a scalar register, so the k-run bounds and
     // every `s + u < s1` test are uniform branches. With a lane-divergent test
     // the compiler left one MFMA of the fused-norm variant to run under an
@@ -247,8 +251,10 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
 #pragma unroll
         for (int h = 0; h < P; h++) lin_load_pair<RT>(rx, xrs, s0 + 2 * h, s1, lane, rawx[h]);
         // the norm weight: K <= 2048, one float4 per thread (zero past K)
-        const float4 nwv = __builtin_bit_cast(
-            float4, __builtin_amdgcn_raw_buffer_load_b128(lin_rsrc(p.norm_weight, (size_t)p.K * 4), 16 * threadIdx.x, 0, 0));
+        float4 nwv = {};
+        if constexpr (NM == 1)
+            nwv = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 lin_rsrc(p.norm_weight, (size_t)p.K * 4), 16 * threadIdx.x, 0, 0));
 #pragma unroll
         for (int h = 0; h < P; h++) lin_load_pair<CT>(rw, wrs, s0 + 2 * h, s1, lane, raww[h]);
         if (res) {
@@ -298,7 +304,7 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
                 }
             }
         }
-        snw[threadIdx.x] = nwv;
+        if constexpr (NM == 1) snw[threadIdx.x] = nwv;
         float ss[RT];
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
@@ -306,8 +312,16 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 if (s0 + u < s1) {
+                    if constexpr (NM == 1) {
 #pragma unroll
-                    for (int e = 0; e < 8; e++) ss[rt] = fmaf((float)xf[u][rt][e], (float)xf[u][rt][e], ss[rt]);
+                        for (int e = 0; e < 8; e++) ss[rt] = fmaf((float)xf[u][rt][e], (float)xf[u][rt][e], ss[rt]);
+                    } else {  // bf16 pairs on the dot product
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const bf16x2 x2 = {xf[u][rt][2 * e], xf[u][rt][2 * e + 1]};
+                            ss[rt] = __builtin_amdgcn_fdot2_f32_bf16(x2, x2, ss[rt], false);
+                        }
+                    }
                 }
             }
             ss[rt] += __shfl_xor(ss[rt], 16);
@@ -322,6 +336,10 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
 #pragma unroll
             for (int ww = 0; ww < 8; ww++) t += sq[ww][16 * rt + lr];
             const float rs = rsqrtf(t / (float)p.K + p.norm_eps);
+            if constexpr (NM == 2) {  // the operand stays s; the scale goes to the epilogue
+                if (w == 0 && lg == 0) srs[16 * rt + lr] = rs;
+                continue;
+            }
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 if (s0 + u < s1) {
@@ -371,7 +389,8 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
                 sg += part[ww][m][f];
                 su += part[ww][m][16 + f];
             }
-            const float gf = (float)(bf16_t)sg, uf = (float)(bf16_t)su;
+            const float sc = NM == 2 ? srs[m] : 1.f;
+            const float gf = (float)(bf16_t)(sg * sc), uf = (float)(bf16_t)(su * sc);
             if (m < mrows && n0 + f < p.N)
                 p.y[(size_t)(m0 + m) * p.ldy + n0 / 2 + f] = (bf16_t)(gf * sigmoidf(gf) * uf);
         }
@@ -384,6 +403,7 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
             float s = 0.f;
 #pragma unroll
             for (int ww = 0; ww < 8; ww++) s += part[ww][m][n];
+            if constexpr (NM == 2) s *= srs[m];
             float v = s + bias[r];
             if (p.add) v = (float)(bf16_t)v + add[r];  // the block's residual add, x + bf16(y)
             if (m < mrows && n0 + n < p.N) p.y[(size_t)(m0 + m) * p.ldy + n0 + n] = (bf16_t)v;
@@ -595,24 +615,24 @@ int launch_rms_norm(const NormParams& p, hipStream_t stream) {
     return 0;
 }
 
-// linear_rows_kernel<RT, CT, P, NORM> for P pairs per batch, rounded up to
+// linear_rows_kernel<RT, CT, P, NM> for P pairs per batch, rounded up to
 // an instantiated count (1, 2, 3, 4, 6) within the shape's limit.
-template <int RT, int CT, bool NORM>
+template <int RT, int CT, int NM>
 static void launch_rows(const LinearParams& p, int pairs, dim3 grid, hipStream_t stream) {
     constexpr int cap = lin_pairs(RT, CT);
     const dim3 block(512);
     if (pairs <= 1) {
-        hipLaunchKernelGGL((linear_rows_kernel<RT, CT, 1, NORM>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((linear_rows_kernel<RT, CT, 1, NM>), grid, block, 0, stream, p);
     } else if (pairs == 2 || cap == 2) {
-        hipLaunchKernelGGL((linear_rows_kernel<RT, CT, 2, NORM>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((linear_rows_kernel<RT, CT, 2, NM>), grid, block, 0, stream, p);
     } else if constexpr (cap >= 3) {
         if (pairs == 3 || cap == 3) {
-            hipLaunchKernelGGL((linear_rows_kernel<RT, CT, 3, NORM>), grid, block, 0, stream, p);
+            hipLaunchKernelGGL((linear_rows_kernel<RT, CT, 3, NM>), grid, block, 0, stream, p);
         } else if constexpr (cap >= 4) {
             if (pairs == 4 || cap == 4)
-                hipLaunchKernelGGL((linear_rows_kernel<RT, CT, 4, NORM>), grid, block, 0, stream, p);
+                hipLaunchKernelGGL((linear_rows_kernel<RT, CT, 4, NM>), grid, block, 0, stream, p);
             else if constexpr (cap >= 6)
-                hipLaunchKernelGGL((linear_rows_kernel<RT, CT, 6, NORM>), grid, block, 0, stream, p);
+                hipLaunchKernelGGL((linear_rows_kernel<RT, CT, 6, NM>), grid, block, 0, stream, p);
         }
     }
 }
@@ -648,7 +668,8 @@ static bool linear_tile(int M, int N, bool swiglu, int norm_k, int& rt_out, int&
 }
 
 int launch_linear_rows(const LinearParams& p, hipStream_t stream) {
-    if (p.M < 1 || p.M > 64 || (p.norm_weight && p.K > LINEAR_NORM_MAX_K)) return -1;
+    const bool norm = p.norm_weight != nullptr || p.norm_folded;
+    if (p.M < 1 || p.M > 64 || (norm && p.K > LINEAR_NORM_MAX_K)) return -1;
     // every buffer the kernel reads spans less than LIN_DEAD bytes (so that
     // offset reads zero) and every in-buffer offset fits 32 bits
     const auto span = [&](long long ld, long long cols) { return ((unsigned long long)(p.M - 1) * ld + cols) * 2; };
@@ -656,21 +677,22 @@ int launch_linear_rows(const LinearParams& p, hipStream_t stream) {
         (p.norm_residual && span(p.ldr, p.K) >= LIN_DEAD) || (p.bias && (unsigned long long)p.N * 2 >= LIN_DEAD))
         return -1;
     int rt, ct;
-    if (!linear_tile(p.M, p.N, p.swiglu != 0, p.norm_weight ? p.K : 0, rt, ct)) return -1;
+    if (!linear_tile(p.M, p.N, p.swiglu != 0, norm ? p.K : 0, rt, ct)) return -1;
     const dim3 grid((p.N + 16 * ct - 1) / (16 * ct), (p.M + 16 * rt - 1) / (16 * rt));
     // k-step pairs per batch: the whole of a wave's run when the shape allows it
     const int per = (p.K / 32 + 7) / 8, pairs = min((per + 1) / 2, lin_pairs(rt, ct));
-    const bool norm = p.norm_weight != nullptr;
 #define CYFA_LINEAR(RT_, CT_)                                                                                  \
     if (rt == RT_ && ct == CT_) {                                                                              \
-        if (norm)                                                                                              \
-            launch_rows<RT_, CT_, true>(p, pairs, grid, stream);                                               \
+        if (p.norm_folded)                                                                                     \
+            launch_rows<RT_, CT_, 2>(p, pairs, grid, stream);                                                  \
+        else if (norm)                                                                                         \
+            launch_rows<RT_, CT_, 1>(p, pairs, grid, stream);                                                  \
         else                                                                                                   \
-            launch_rows<RT_, CT_, false>(p, pairs, grid, stream);                                              \
+            launch_rows<RT_, CT_, 0>(p, pairs, grid, stream);                                                  \
         return 0;                                                                                              \
     }
     if (rt == 4 && ct == 4 && !norm) {  // the lm_head's tile at 64 rows (N = 32000: 500 workgroups)
-        launch_rows<4, 4, false>(p, pairs, grid, stream);
+        launch_rows<4, 4, 0>(p, pairs, grid, stream);
         return 0;
     }
     CYFA_LINEAR(4, 2)

@@ -14,7 +14,7 @@ import torch
 import torch.nn.functional as F
 
 LIB_PATH = Path(os.environ.get("CYFA_LIB", Path(__file__).with_name("libcyfa_hip.so")))
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 CYFA_OK = 0
 CYFA_ERR_VALUE = -1
@@ -397,6 +397,12 @@ def linear(x, weight, bias=None, out_cols=None, residual=None):
 LINEAR_NORM_MAX_K = 2048
 
 
+def fold_norm_weight(weight, norm_weight):
+    """bf16(weight diag(norm_weight)): a projection's weight with the RMS norm
+    weight in front of it multiplied in, for norm_linear(norm_weight=None)."""
+    return (weight.detach().float() * norm_weight.detach().float()).to(weight.dtype)
+
+
 def norm_linear(x, norm_weight, eps, weight, bias=None, residual=None, out_cols=None, swiglu=False):
     """The block's pre-norm and its first projection in one cyfa_norm_linear_rows
     launch, for at most 64 bf16 rows of K <= 2048 columns:
@@ -404,7 +410,11 @@ def norm_linear(x, norm_weight, eps, weight, bias=None, residual=None, out_cols=
     y = linear(h, weight, bias) (linear_swiglu(h, weight) with ``swiglu``).
     Returns (s, y). Other shapes run rms_norm and the projection separately.
     h may differ from rms_norm's in the last bit: the sum of squares runs in
-    another order."""
+    another order.
+
+    norm_weight None: ``weight`` already carries the norm weight
+    (fold_norm_weight), and y = bf16(rsqrt(mean(s^2) + eps) (s weight^T) + bias)
+    with the row scale on the fp32 product (the shapes above only)."""
     K = weight.shape[-1]
     N = weight.shape[0]
     if x.shape[-1] != K:
@@ -414,6 +424,9 @@ def norm_linear(x, norm_weight, eps, weight, bias=None, residual=None, out_cols=
             or weight.dtype != torch.bfloat16 or (bias is not None and bias.dtype != torch.bfloat16)
             or (residual is not None and residual.dtype != torch.bfloat16) or not x.is_cuda
             or (swiglu and (bias is not None or N % 32)) or torch.is_grad_enabled()):
+        if norm_weight is None:
+            raise ValueError("norm_linear: a folded norm weight needs at most 64 bf16 rows of K <= 2048 "
+                             "on the GPU, without grad")
         if residual is None:
             s, h = x, rms_norm(x, norm_weight, eps)
         else:
@@ -426,7 +439,8 @@ def norm_linear(x, norm_weight, eps, weight, bias=None, residual=None, out_cols=
     w = weight.detach()
     if not w.is_contiguous():
         w = w.contiguous()
-    nw = norm_weight.detach().to(torch.float32).contiguous()
+    nw = None if norm_weight is None else norm_weight.detach().to(torch.float32).contiguous()
+    require_device(x, nw)
     s = x
     r2 = total = None
     if residual is not None:
@@ -441,7 +455,7 @@ def norm_linear(x, norm_weight, eps, weight, bias=None, residual=None, out_cols=
     args = CyfaLinearArgs(M=rows, N=N, K=K, x=x2.data_ptr(), ldx=x2.stride(0), weight=w.data_ptr(),
                           bias=ptr(None if bias is None else bias.detach().contiguous()), y=y.data_ptr(), ldy=ldy,
                           swiglu=1 if swiglu else 0)
-    nargs = CyfaRowNormArgs(weight=nw.data_ptr(), eps=float(eps), residual=ptr(r2), sum_out=ptr(total), ldr=K)
+    nargs = CyfaRowNormArgs(weight=ptr(nw), eps=float(eps), residual=ptr(r2), sum_out=ptr(total), ldr=K)
     _check(load_library().cyfa_norm_linear_rows(ctypes.byref(args), ctypes.byref(nargs), stream_handle(x.device)),
            "cyfa_norm_linear_rows")
     lead = tuple(x.shape[:-1])

@@ -31,6 +31,10 @@ from ..ops import chunk_cyfa, fused_recurrent_cyfa
 from ..ops.fused_recurrent import decode_layer_step
 from ..ops.utils import readout_table
 
+# A one-token step with at least this many (batch, head) workgroups forms
+# g_proj[1] inside the decode kernel by default (see gate_projection_in_kernel).
+GATE_IN_KERNEL_MIN_WORKGROUPS = 128
+
 
 def inference_fast_path(x):
     """bf16 GPU inference without gradients (the reference's `_inference` condition)."""
@@ -223,17 +227,30 @@ class CyclicFlowAttention(nn.Module):
         self._a_bias_zero = None  # a_proj has no bias: zeros in the fused a|b|d bias
         # decode steps: one [q | k | v | g_proj[0] | a | b | d] projection
         self._in_weight = FusedWeight()
+        self._in_weight_folded = FusedWeight()
+        # When set, a decode step with the block's norm fused into the input
+        # projection multiplies the norm weight into the projection's weight
+        # (cached) and applies the row scale to the product (cyfa_norm_linear_rows
+        # with a NULL norm weight): the kernel skips scaling every operand
+        # element, and the bf16 rounding of the normalised input moves to the
+        # folded weight. With MLPs folded too the 400M step at B=64 runs about
+        # 6% faster on MI355X, but the greedy tokens then follow the
+        # reference's rounding less closely (one of 130 decidable steps of the
+        # configuration-4 check differs), so it is off by default.
+        self.fold_prenorm_weight = False
         self._in_bias = FusedWeight()
         self._in_bias_zero = None
         # When set, one-token steps update the cache's recurrent states in place
         # (the graphed decode loop); otherwise new state tensors are returned.
         self.decode_in_place = False
-        # When set, a one-token step forms the gate (g_proj[1]) inside the decode
-        # kernel instead of a separate projection launch. On MI355X it saves
-        # about 1.4% of the 400M step at B=64 (one launch per layer fewer) but
-        # costs the kernel 2.4 us of L2 reads (each workgroup reads its head's
-        # 128 KB weight slice) and loses at B=1, so it is off by default.
-        self.gate_projection_in_kernel = False
+        # Whether a one-token step forms the gate (g_proj[1]) inside the decode
+        # kernel instead of a separate projection launch (same bits either way).
+        # On MI355X it saves about 1.4% of the 400M step at B=64 (one launch per
+        # layer fewer) but costs the kernel 2.4 us of L2 reads (each workgroup
+        # reads its head's 128 KB weight slice) and loses at B=1; None (the
+        # default) picks it when the step has at least
+        # GATE_IN_KERNEL_MIN_WORKGROUPS (batch, head) workgroups.
+        self.gate_projection_in_kernel = None
 
     def readout_table(self):
         """readout @ Phi, cached while the readout parameter is unchanged."""
@@ -340,7 +357,11 @@ class CyclicFlowAttention(nn.Module):
             w_in = self._in_weight.get(self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, g0.weight,
                                        self.a_proj.weight, self.b_proj.weight, self.d_proj.weight)
             b_in = self._in_bias.get(self._in_bias_zero, abd_bias)
-            if prenorm is not None:
+            if prenorm is not None and self.fold_prenorm_weight and x.shape[-1] <= _native.LINEAR_NORM_MAX_K:
+                w_f = self._in_weight_folded.get(w_in, prenorm.weight, build=_native.fold_norm_weight)
+                _, y_in = _native.norm_linear(x, None, prenorm.eps, w_f, b_in,
+                                              out_cols=(D3 + Dg + 3 * H + 7) // 8 * 8)
+            elif prenorm is not None:
                 _, y_in = _native.norm_linear(x, prenorm.weight, prenorm.eps, w_in, b_in,
                                               out_cols=(D3 + Dg + 3 * H + 7) // 8 * 8)
             else:
@@ -372,7 +393,10 @@ class CyclicFlowAttention(nn.Module):
                 g0_out = _native.linear(x, g0.weight)
             # g_proj[1] inside the kernel (the same bits as _native.linear) when asked and
             # its operands are bf16; otherwise the gate is projected first
-            in_kernel = (self.gate_projection_in_kernel and g1.weight.dtype == torch.bfloat16
+            want = self.gate_projection_in_kernel
+            if want is None:
+                want = B * H >= GATE_IN_KERNEL_MIN_WORKGROUPS
+            in_kernel = (want and g1.weight.dtype == torch.bfloat16
                          and (g1.bias is None or g1.bias.dtype == torch.bfloat16))
             gate = None if in_kernel else _native.linear(g0_out, g1.weight, g1.bias)
             o, state = decode_layer_step(

@@ -28,6 +28,10 @@ class GatedMLP(nn.Module):
         self.down_proj = nn.Linear(mid, config.hidden_size, bias=False)
         self._gate_up = FusedWeight()
         self._gate_up_il = FusedWeight()
+        self._gate_up_folded = FusedWeight()
+        # decode steps: mlp_norm's weight multiplied into the gate|up weight
+        # (off by default; see CyclicFlowAttention.fold_prenorm_weight)
+        self.fold_norm_weight = False
 
     def forward(self, x):
         rows = x.numel() // x.shape[-1]
@@ -52,7 +56,11 @@ class GatedMLP(nn.Module):
         if (inference_fast_path(x) and rows <= _native.LINEAR_ROWS_MAX and self.gate_proj.weight.shape[0] % 16 == 0
                 and x.shape[-1] % 32 == 0):
             w = self._gate_up_il.get(self.gate_proj.weight, self.up_proj.weight, build=_native.interleave_gate_up)
-            _, h = _native.norm_linear(x, norm.weight, norm.eps, w, swiglu=True)
+            if self.fold_norm_weight and x.shape[-1] <= _native.LINEAR_NORM_MAX_K:
+                w = self._gate_up_folded.get(w, norm.weight, build=_native.fold_norm_weight)
+                _, h = _native.norm_linear(x, None, norm.eps, w, swiglu=True)
+            else:
+                _, h = _native.norm_linear(x, norm.weight, norm.eps, w, swiglu=True)
             return _native.linear(h, self.down_proj.weight, residual=x)
         return x + self(norm(x))
 

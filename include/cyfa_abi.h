@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define CYFA_ABI_VERSION 4
+#define CYFA_ABI_VERSION 5
 
 enum {
     CYFA_OK = 0,
@@ -277,9 +277,14 @@ int cyfa_linear_rows(const CyfaLinearArgs *args, void *hip_stream);
 /* The RMS norm in front of a projection (K <= 2048 columns):
  *   s  = residual ? bf16(x + residual) : x        (sum_out receives s)
  *   xs = bf16(s * rsqrt(mean(s^2) + eps) * weight)
- * and the projection reads xs in place of x. */
+ * and the projection reads xs in place of x. With weight NULL the caller has
+ * multiplied the norm weight into the projection's weight (W' = bf16(W
+ * diag(weight))), and the row scale is applied to the fp32 product instead of
+ * the operand: y = bf16(rsqrt(mean(s^2) + eps) (s W'^T) + bias). That moves
+ * the bf16 rounding of the normalised input to W' (one rounding of each
+ * product term either way) and skips the per-element scaling of xs. */
 typedef struct CyfaRowNormArgs {
-    const float *weight;          /* f32 [K], 16-byte aligned */
+    const float *weight;          /* f32 [K], 16-byte aligned; NULL: folded into the weight (above) */
     float eps;
     const void *residual;         /* nullable bf16 [M, K], rows ldr elements apart */
     void *sum_out;                /* bf16 [M, K], rows ldr apart; required with residual; aliases no input */

@@ -343,6 +343,58 @@ def test_norm_linear_rows(M, residual, swiglu, K):
     assert rows <= max(1, M // 10), f"{rows} of {M} rows differ from rms_norm + linear"
 
 
+@pytest.mark.parametrize("M,residual,swiglu,K", [(1, False, False, 1024), (37, True, False, 1024),
+                                                 (64, False, False, 1024), (64, False, True, 1024),
+                                                 (5, True, True, 2048), (64, False, False, 512)])
+def test_norm_linear_rows_folded(M, residual, swiglu, K):
+    """cyfa_norm_linear_rows with the norm weight folded into the projection's
+    weight (NULL norm weight): y = bf16(rs (s W'^T) + bias) with W' =
+    bf16(W diag(w)), checked in float64 with the bound of the result's bf16
+    rounding plus the fp32 summation error (factor two to spare); with SwiGLU,
+    the gate and up values rounded to bf16 as the kernel rounds them, then the
+    product; s equals the separate residual add bit for bit."""
+    from cyclic_flow_attention import _native
+
+    gen = torch.Generator().manual_seed(M * 11 + K + 3 * residual + swiglu)
+    N = 2 * 1408 if swiglu else 3340
+    x = torch.randn(M, K, generator=gen).bfloat16()
+    r = torch.randn(M, K, generator=gen).bfloat16() if residual else None
+    nw = 1.0 + 0.1 * torch.randn(K, generator=gen)
+    w = (0.05 * torch.randn(N, K, generator=gen)).bfloat16()
+    b = None if swiglu else torch.randn(N, generator=gen).bfloat16()
+    wf = _native.fold_norm_weight(w, nw)
+    assert torch.equal(wf, (w.float() * nw).bfloat16())
+    d = lambda t: None if t is None else t.to(DEV)  # noqa: E731
+    with torch.no_grad():
+        s, y = _native.norm_linear(d(x), None, 1e-6, d(wf), d(b), residual=d(r), swiglu=swiglu)
+        s_ref = d(x) if r is None else (d(x).float() + d(r).float()).bfloat16()
+    torch.cuda.synchronize()
+    assert torch.equal(s, s_ref)
+    s64 = s.cpu().double()
+    rs = torch.rsqrt(s64.pow(2).mean(-1, keepdim=True) + 1e-6)
+    p64 = rs * (s64 @ wf.double().T)
+    mag = rs * (s64.abs() @ wf.double().abs().T)
+    if not swiglu:
+        y64 = p64 + b.double()
+        bound = 2 * (BF16_ULP / 2 * (y64.abs() + mag) + K * 2.0 ** -24 * mag) + 1e-30
+        err = (y.cpu().double() - y64).abs()
+        assert (err <= bound).all(), f"max err {err.max().item()}"
+    else:
+        # y = bf16(g sigmoid(g) u) of g, u rounded to bf16: propagate each one's
+        # rounding and summation error through the product, plus the last rounding
+        groups = N // 32
+        gi = (32 * torch.arange(groups)[:, None] + torch.arange(16)).reshape(-1)
+        g64, u64 = p64[:, gi], p64[:, gi + 16]
+        eg = BF16_ULP / 2 * g64.abs() + K * 2.0 ** -24 * mag[:, gi]
+        eu = BF16_ULP / 2 * u64.abs() + K * 2.0 ** -24 * mag[:, gi + 16]
+        sg = torch.sigmoid(g64)
+        y64 = g64 * sg * u64
+        dy_dg = (u64 * (sg + g64 * sg * (1 - sg))).abs()
+        bound = 2 * (dy_dg * eg + (g64 * sg).abs() * eu + BF16_ULP / 2 * y64.abs()) + 1e-30
+        err = (y.cpu().double() - y64).abs()
+        assert (err <= bound).all(), f"max err {err.max().item()}"
+
+
 @pytest.mark.parametrize("B,state,inplace,split,own_gate", [
     (3, True, False, True, False), (2, False, False, True, False), (4, True, True, True, False),
     (64, True, True, True, False), (3, True, True, False, False), (1, True, True, True, False),
