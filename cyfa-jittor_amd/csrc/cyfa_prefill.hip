@@ -588,12 +588,28 @@ __device__ __forceinline__ float dpp_shift(float x) {
 
 // clock0 + sum_{s < t_end} delta_s, summed in double by the workgroup (512
 // threads) in a fixed order, so every workgroup of a sequence gets the same bits.
-__device__ __forceinline__ double clock_before(const PrefillParams& p, int b, int h, int bh, int t_end) {
+// clock0 + sum of delta over tokens [0, t_end) of sequence sq, in double:
+// each thread adds tokens tid, tid + 512, .. in order, then the wave and
+// workgroup sums. The first four tokens' loads per thread go out before
+// issue_after(), the caller's own loads, so the sum does not wait for those
+// (vector loads complete in issue order); tokens past t_end load zero.
+template <typename F>
+__device__ __forceinline__ double clock_before(const PrefillParams& p, const Seq& sq, int bh, int t_end,
+                                               F&& issue_after) {
     __shared__ double part[8];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    double acc = 0.0;
     const int te = min(t_end, p.T);
-    for (int t = tid; t < te; t += 512) acc += (double)p.delta[tok_index(p, b, t, h)];
+    float d[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int t = tid + 512 * k;
+        d[k] = ld_f32(sq.delta, ((uint32_t)t * sq.row4) | ((uint32_t)((t - te) >> 31 ^ -1) & 0x80000000u));
+    }
+    issue_after();
+    double acc = 0.0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) acc += (double)d[k];  // zero past te
+    for (int t = tid + 2048; t < te; t += 512) acc += (double)ld_f32(sq.delta, (uint32_t)t * sq.row4);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
     if (lane == 0) part[w] = acc;
@@ -762,83 +778,86 @@ __device__ __forceinline__ void store_segment_state(const f32x4 acc[8][2], float
 }
 
 // ---------------------------------------------------------------------------
-// 1. Segment-local end states from a zero start. grid = (H, B, 2 (P-1)), 512
-// threads, blockIdx.z = 2 j + part; state blocks as in frag_offset. part 0: key state, rows 128 y ..,
-// y = w >> 2, columns 32 (w & 3) ..; part 1: value state, columns 32 w ...
-constexpr int SG_A = 0;                     // k_hat (key) or v (value), TileF
-constexpr int SG_B = SG_A + TileF::bytes;  // w, TileW
-constexpr int SG_G = SG_B + TileW::bytes;  // f32 [5][64] gates
+// 1. Segment-local end states from a zero start, both parts in one workgroup:
+// the gates, the clock and the write-vector tile are formed once for the key
+// state S_K += k_hat^T w' and the value state S_V += w^T v'. grid = (H, B, P),
+// 512 threads (blockIdx.z: see segment_state_kernel); state blocks as in
+// frag_offset: key state rows 128 y .., y = w >> 2, columns 32 (w & 3) ..;
+// value state columns 32 w ...
+constexpr int SG_K = 0;                     // k_hat, TileF
+constexpr int SG_V = SG_K + TileF::bytes;  // v, TileF
+constexpr int SG_W = SG_V + TileF::bytes;  // w, TileW
+constexpr int SG_G = SG_W + TileW::bytes;  // f32 [5][64] gates
 constexpr int SG_NW = SG_G + 5 * 64 * 4;   // f32 [256] k norm weight
 constexpr int SG_LDS = SG_NW + KD * 4;
-static_assert(2 * SG_LDS <= 160 * 1024, "two segment-state workgroups must fit in one CU's LDS");
+static_assert(SG_LDS <= 160 * 1024, "segment-state workgroup must fit in one CU's LDS");
 
-// key: S += k_hat^T w', A = k_hat columns (this wave's half), B = w columns 32 (w & 3) ..;
-// value: S += w^T v', A = w columns, B = v columns 32 w ...
-template <bool KEY>
 __device__ __forceinline__ void segment_state_body(const PrefillParams& p, int bh, int j, int b, int h,
                                                    unsigned char* smem) {
-    bf16_t* sA = reinterpret_cast<bf16_t*>(smem + SG_A);
-    bf16_t* sB = reinterpret_cast<bf16_t*>(smem + SG_B);
+    bf16_t* sK = reinterpret_cast<bf16_t*>(smem + SG_K);
+    bf16_t* sV = reinterpret_cast<bf16_t*>(smem + SG_V);
+    bf16_t* sW = reinterpret_cast<bf16_t*>(smem + SG_W);
     float* sLam = reinterpret_cast<float*>(smem + SG_G);
     float* sBeta = sLam + 64;
     float* sGam = sBeta + 64;
     float* sNw = reinterpret_cast<float*>(smem + SG_NW);
-    using LA = typename std::conditional<KEY, TileF, TileW>::type;
-    using LB = typename std::conditional<KEY, TileW, TileF>::type;
-    const bf16_t* sArow = KEY ? sA : sB;
-    const bf16_t* sBcol = KEY ? sB : sA;
     const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
     const int n0 = j * p.L, n1 = min(n0 + p.L, p.N);
-    const int a_col = KEY ? HALF * (w >> 2) : 0;
-    const int b_col = KEY ? 32 * (w & 3) : 32 * w;
-    f32x4 acc[8][2];
+    f32x4 acck[8][2], accv[8][2];
 #pragma unroll
-    for (int x = 0; x < 8; x++) acc[x][0] = acc[x][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int x = 0; x < 8; x++) acck[x][0] = acck[x][1] = accv[x][0] = accv[x][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     const Seq sq = make_seq(p, b, h, bh);
-    GateIn gin = load_gate_inputs(sq, p.T, n0 * 64);
-    bf16x8 raw[4];
-    issue_rows(sq, KEY ? sq.k : sq.v, p.T, n0 * 64, raw);
-    if (KEY && tid < KD) sNw[tid] = p.k_w[tid];
-    double clock = clock_before(p, b, h, bh, n0 * 64);  // its loads overlap the ones above
+    GateIn gin;
+    bf16x8 kraw[4], vraw[4];
+    float kwv;
+    // the clock prefix's loads first, then the first chunk's (see clock_before)
+    double clock = clock_before(p, sq, bh, n0 * 64, [&] {
+        gin = load_gate_inputs(sq, p.T, n0 * 64);
+        issue_rows(sq, sq.k, p.T, n0 * 64, kraw);
+        issue_rows(sq, sq.v, p.T, n0 * 64, vraw);
+        kwv = p.k_w[tid & (KD - 1)];
+    });
+    if (tid < KD) sNw[tid] = kwv;
     float logdecay = 0.f;
     StateScale sc;
     __syncthreads();
     for (int n = n0; n < n1; n++) {
         const int t0 = n * 64;
         const GateRegs gr = finish_gates(gin, clock);
-        // Both parts form the same clock and decay scan; the value part, whose
-        // chunks are shorter (no k_hat norm), writes them for the sweeps.
-        if (!KEY && w == 0) {
+        if (w == 0) {  // the clock and decay scan for the sweeps
             p.lam[(size_t)bh * p.Tp + t0 + lane] = gr.lamr;
             p.gam[(size_t)bh * p.Tp + t0 + lane] = gr.gam;
         }
         sc.begin_chunk(chunk_last_gam(gr));
         commit_gates(p.T, t0, gr, sLam, sBeta, sGam, sc.inv());
-        store_write_tile<TileW>(gr, p.T - t0, sB);
-        if (KEY)
-            norm_store_rows<TileF>(p, t0, raw, sNw, p.k_eps, sA);
-        else
-            store_rows<TileF>(raw, p.T - t0, sA);
+        store_write_tile<TileW>(gr, p.T - t0, sW);
+        norm_store_rows<TileF>(p, t0, kraw, sNw, p.k_eps, sK);
+        store_rows<TileF>(vraw, p.T - t0, sV);
         __syncthreads();
         if (n + 1 < n1) {
-            issue_rows(sq, KEY ? sq.k : sq.v, p.T, t0 + 64, raw);
+            issue_rows(sq, sq.k, p.T, t0 + 64, kraw);
+            issue_rows(sq, sq.v, p.T, t0 + 64, vraw);
             gin = load_gate_inputs(sq, p.T, t0 + 64);
         }
         logdecay += sGam[63];
         if (sc.fold != 1.f) {
 #pragma unroll
             for (int x = 0; x < 8; x++) {
-                acc[x][0] *= sc.fold;
-                acc[x][1] *= sc.fold;
+                acck[x][0] *= sc.fold;
+                acck[x][1] *= sc.fold;
+                accv[x][0] *= sc.fold;
+                accv[x][1] *= sc.fold;
             }
         }
-        chunk_state_update<LA, LB>(sArow, a_col, sBcol, b_col, sGam, acc);
+        chunk_state_update<TileF, TileW>(sK, HALF * (w >> 2), sW, 32 * (w & 3), sGam, acck);
+        chunk_state_update<TileW, TileF>(sW, 0, sV, 32 * w, sGam, accv);
         sc.sig = sc.next;
         __syncthreads();
     }
     const size_t slot = (size_t)bh * (p.P - 1) + j;
-    store_segment_state(acc, sc.sig, p.seg + slot * SEG + (KEY ? 0 : SEG_K), p.seg_exp + (slot * 2 + (KEY ? 0 : 1)) * 8);
-    if (KEY && tid == 0) p.seg_decay[bh * p.P + j] = exp2f(logdecay);
+    store_segment_state(acck, sc.sig, p.seg + slot * SEG, p.seg_exp + slot * 2 * 8);
+    store_segment_state(accv, sc.sig, p.seg + slot * SEG + SEG_K, p.seg_exp + (slot * 2 + 1) * 8);
+    if (tid == 0) p.seg_decay[bh * p.P + j] = exp2f(logdecay);
 }
 
 // Power-of-two exponent e of head h's readout table with max |table| 2^-e in
@@ -885,21 +904,23 @@ __device__ __forceinline__ void table_exponent(const PrefillParams& p, int h, in
     }
 }
 
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void segment_state_kernel(PrefillParams p) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void segment_state_kernel(PrefillParams p) {
     __shared__ __align__(16) unsigned char smem[SG_LDS];
+    // Workgroups are dispatched in block order; the later segments, whose
+    // clock prefix (clock_before) is longest, go first: z = 0 is the clock of
+    // the last segment, then segments P - 2 down to 0.
     const int z = blockIdx.z;
-    if (z == 2 * (p.P - 1)) {  // clock of the last segment and the table's exponent
+    if (z == 0) {  // clock of the last segment and the table's exponent
         const SegCoord cd = seg_coord(p.H, p.P - 1);
-        table_exponent(p, cd.h, cd.bh);
+        const Seq sq = make_seq(p, cd.b, cd.h, cd.bh);
         const int t_begin = (p.P - 1) * p.L * 64;
-        clock_scan(p, cd.bh, cd.b, cd.h, t_begin, clock_before(p, cd.b, cd.h, cd.bh, t_begin));
+        const double carry = clock_before(p, sq, cd.bh, t_begin, [] {});
+        table_exponent(p, cd.h, cd.bh);
+        clock_scan(p, cd.bh, cd.b, cd.h, t_begin, carry);
         return;
     }
-    const SegCoord cd = seg_coord(p.H, z >> 1);
-    if ((z & 1) == 0)
-        segment_state_body<true>(p, cd.bh, cd.j, cd.b, cd.h, smem);
-    else
-        segment_state_body<false>(p, cd.bh, cd.j, cd.b, cd.h, smem);
+    const SegCoord cd = seg_coord(p.H, p.P - 1 - z);
+    segment_state_body(p, cd.bh, cd.j, cd.b, cd.h, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -1684,12 +1705,18 @@ __device__ __forceinline__ void st_b128(rsrc_t r, uint32_t off, uint32_t soff, f
 
 // Segment-local end states, grid (H, B, P - 1), 512 threads; the state blocks of
 // the waves as in the prefill's key (shape A) or value (shape B) part.
+constexpr int SLS_F = 0;                      // the 256-wide operand, TileF
+constexpr int SLS_H = SLS_F + TileF::bytes;  // the 128-wide operand, TileW
+constexpr int SLS_G = SLS_H + TileW::bytes;  // f32 [5][64] gates
+constexpr int SLS_LDS = SLS_G + 5 * 64 * 4;
+static_assert(2 * SLS_LDS <= 160 * 1024, "two scalar_la segment workgroups must fit in one CU's LDS");
+
 template <bool SA>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void sla_segment_kernel(SlaParams p) {
-    __shared__ __align__(16) unsigned char smem[SG_NW];
-    bf16_t* sF = reinterpret_cast<bf16_t*>(smem + SG_A);  // the 256-wide operand: k (A) or v (B), TileF
-    bf16_t* sH = reinterpret_cast<bf16_t*>(smem + SG_B);  // the 128-wide operand: v (A) or k (B), TileW
-    float* sLam = reinterpret_cast<float*>(smem + SG_G);
+    __shared__ __align__(16) unsigned char smem[SLS_LDS];
+    bf16_t* sF = reinterpret_cast<bf16_t*>(smem + SLS_F);  // the 256-wide operand: k (A) or v (B), TileF
+    bf16_t* sH = reinterpret_cast<bf16_t*>(smem + SLS_H);  // the 128-wide operand: v (A) or k (B), TileW
+    float* sLam = reinterpret_cast<float*>(smem + SLS_G);
     float* sBeta = sLam + 64;
     float* sGam = sBeta + 64;
     using LA = typename std::conditional<SA, TileF, TileW>::type;
@@ -2113,7 +2140,7 @@ WorkspaceLayout workspace_layout(int B, int T, int H, int K, int V) {
 }
 
 int launch_prefill(const PrefillParams& p, hipStream_t stream) {
-    hipLaunchKernelGGL(segment_state_kernel, dim3(p.H, p.B, 2 * (p.P - 1) + 1), dim3(512), 0, stream, p);
+    hipLaunchKernelGGL(segment_state_kernel, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
     hipLaunchKernelGGL(pass1_kernel, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
     if (p.on_w)
         hipLaunchKernelGGL(pass2_kernel<true>, dim3(p.H, p.B, p.P), dim3(512), 0, stream, p);
