@@ -41,7 +41,8 @@ def chunk_cyfa(
 
     Inputs q, k and v use [batch, time, heads, channels]; g, delta and beta use
     [batch, time, heads]. The readout has [heads, slots-1, slots-1]. Returns
-    the output (bf16, [batch, time, heads, V]) and, when requested,
+    the output ([batch, time, heads, V], in q's dtype; bf16, fp16 and fp32 q, k,
+    v run the bf16 kernels) and, when requested,
     (key_state [B,H,K,M], value_state [B,H,M,V], clock [B,H]), all fp32.
     ``table`` (keyword only, not in the reference signature) is a precomputed
     readout @ Phi [H, M-1, M] fp32; when None it is formed from ``readout``.
@@ -67,11 +68,9 @@ def chunk_cyfa(
     for name, x in (("g", g), ("delta", delta), ("beta", beta)):
         if tuple(x.shape) != (B, T, H):
             raise ValueError(f"{name} must have shape {(B, T, H)}, got {tuple(x.shape)}")
-    for name, x in (("q", q), ("k", k), ("v", v)):
-        if x.dtype != torch.bfloat16:
-            raise NotImplementedError(f"the HIP prefill computes in bfloat16; {name} is {x.dtype}")
+    out_dtype = _operand_dtype("chunk_cyfa", q, k, v)
     dev = _native.require_device(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, table, *state_in)
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    q, k, v = (x.to(torch.bfloat16).contiguous() for x in (q, k, v))
     g, delta, beta = (x.to(torch.float32).contiguous() for x in (g, delta, beta))
     qw = q_norm_weight.to(torch.float32).contiguous()
     kw = k_norm_weight.to(torch.float32).contiguous()
@@ -119,9 +118,9 @@ def chunk_cyfa(
         if tuple(on_w.shape) != (V,):
             raise ValueError(f"output_norm weight must have shape ({V},), got {tuple(on_w.shape)}")
         on_gate = on_gate.reshape(B, T, H, V)
-        if on_gate.dtype != torch.bfloat16:
-            raise NotImplementedError(f"output_norm gate must be bfloat16, got {on_gate.dtype}")
-        on_gate = on_gate.contiguous()
+        if on_gate.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+            raise NotImplementedError(f"output_norm gate must be a float tensor, got {on_gate.dtype}")
+        on_gate = on_gate.to(torch.bfloat16).contiguous()
         _native.require_device(on_w, on_gate)
         norm = _native.CyfaOutNormArgs(weight=on_w.data_ptr(), gate=on_gate.data_ptr(), eps=float(on_eps),
                                        prescale=float(on_prescale))
@@ -129,7 +128,22 @@ def chunk_cyfa(
             _native.chunk_fwd_noalloc(args, norm, dev)
         else:
             _native.chunk_fwd_normed(args, norm, dev)
+    if out_dtype != torch.bfloat16:
+        o = o.to(out_dtype)
     return o, ((hk, hv, clock) if output_final_state else None)
+
+
+def _operand_dtype(what, *xs):
+    """The dtype of q, k, v (one float dtype). The kernels' MFMA operands are
+    bf16: fp32 and fp16 inputs are rounded to bf16 on entry (the bf16 path's
+    accuracy, not the reference's fp32 scalar path's, which computes without
+    intermediate rounding: ops/chunk.py:285-331) and the output is returned
+    in the input dtype."""
+    dt = xs[0].dtype
+    if any(x.dtype != dt for x in xs) or dt not in (torch.bfloat16, torch.float16, torch.float32):
+        raise NotImplementedError(f"{what}: q, k, v must share one of bf16, fp16, fp32; got "
+                                  + ", ".join(str(x.dtype) for x in xs))
+    return dt
 
 
 def scalar_la(q, k, v, g, initial, scale=1.0, raw_output=False, output_bth=False, v_bth=False):

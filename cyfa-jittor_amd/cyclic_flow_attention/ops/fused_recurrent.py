@@ -8,6 +8,7 @@ fused HBM-streaming kernel, ``cyfa_decode_step`` of libcyfa_hip.so.
 import torch
 
 from .. import _native
+from .chunk import _operand_dtype
 from .utils import check_table, readout_table
 
 
@@ -34,7 +35,8 @@ def fused_recurrent_cyfa(
 ):
     """Decode one token using constant-size key, value and clock states.
 
-    Uses the same input layout and return convention as chunk_cyfa. The new
+    Uses the same input layout and return convention as chunk_cyfa (q, k, v
+    of bf16, fp16 or fp32, rounded to bf16 for the kernel; o in their dtype). The new
     states are returned as new tensors; ``inplace=True`` (an extension) updates
     the given initial_state tensors instead and returns them. ``table`` (an
     extension) passes a precomputed readout @ Phi to skip rebuilding it.
@@ -58,12 +60,10 @@ def fused_recurrent_cyfa(
         raise NotImplementedError("native fused decode currently needs dense T=1")
     if M > 256 or K > 1024 or V > 1024:
         raise ValueError("decode shape exceeds block limits")
-    for name, x in (("q", q), ("k", k), ("v", v)):
-        if x.dtype != torch.bfloat16:
-            raise NotImplementedError(f"the HIP decode step computes in bfloat16; {name} is {x.dtype}")
+    out_dtype = _operand_dtype("fused_recurrent_cyfa", q, k, v)
     state_in = tuple(initial_state) if initial_state is not None else ()
     dev = _native.require_device(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, table, *state_in)
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    q, k, v = (x.to(torch.bfloat16).contiguous() for x in (q, k, v))
     g, delta, beta = (x.to(torch.float32).contiguous() for x in (g, delta, beta))
     qw = q_norm_weight.to(torch.float32).contiguous()
     kw = k_norm_weight.to(torch.float32).contiguous()
@@ -103,6 +103,8 @@ def fused_recurrent_cyfa(
         o=o.data_ptr(), hk_out=hk_out.data_ptr(), hv_out=hv_out.data_ptr(), clock_out=c_out.data_ptr(),
     )
     _native.decode_step(args, dev)
+    if out_dtype != torch.bfloat16:
+        o = o.to(out_dtype)
     return o, ((hk_out, hv_out, c_out) if output_final_state else None)
 
 

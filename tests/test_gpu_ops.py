@@ -371,3 +371,27 @@ def test_decode_split_equals_one_workgroup_form(B, H, K, V):
     ro, rst = O.fused_recurrent_cyfa(**_oracle(x, init)[0], initial_state=_oracle(x, init)[1], output_final_state=True)
     assert_close(o2, ro, what=f"split decode o B{B} H{H}")
     _check_states(st2, rst, "split decode")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_wide_operands_run_the_bf16_path(dtype):
+    """fp32 and fp16 q, k, v (the reference's scalar path, ops/chunk.py:285-331,
+    takes fp32) are rounded to bf16 on entry: the outputs equal the bf16 call's,
+    returned in the input dtype, for both the chunk op and the decode step."""
+    from cyclic_flow_attention.ops import chunk_cyfa, fused_recurrent_cyfa
+
+    x, init = _inputs(2, 130, 2, seed=11, state=True)
+    xg, ig = _gpu(x, init)
+    wide = dict(xg, q=xg["q"].to(dtype), k=xg["k"].to(dtype), v=xg["v"].to(dtype))
+    with torch.no_grad():
+        o_b, s_b = chunk_cyfa(**xg, initial_state=ig, output_final_state=True)
+        o_w, s_w = chunk_cyfa(**wide, initial_state=ig, output_final_state=True)
+        d = {k: (v[:, :1] if k in ("q", "k", "v", "g", "delta", "beta") else v) for k, v in xg.items()}
+        dw = {k: (v[:, :1] if k in ("q", "k", "v", "g", "delta", "beta") else v) for k, v in wide.items()}
+        r_b, _ = fused_recurrent_cyfa(**d, initial_state=ig)
+        r_w, _ = fused_recurrent_cyfa(**dw, initial_state=ig)
+    torch.cuda.synchronize()
+    assert o_w.dtype == dtype and r_w.dtype == dtype
+    assert torch.equal(o_w, o_b.to(dtype)) and torch.equal(r_w, r_b.to(dtype))
+    for a, b in zip(s_w, s_b):
+        assert torch.equal(a, b)
