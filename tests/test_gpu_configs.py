@@ -149,6 +149,9 @@ def test_config4_graphed_decode_and_greedy_tokens(model400, prompts):
                 undecidable += 1
             elif int(toks[r, i]) != int(top2.indices[0]):
                 mismatched += 1
+                d = mm_last[r] - me_last[r]
+                print(f"step {i} row {r}: token {int(toks[r, i])} vs {int(top2.indices[0])}; gap {gap:.4g}, "
+                      f"reference rounding moves the gap by {float(d[top2.indices[0]] - d[top2.indices[1]]):.4g}")
         if i == steps:
             break
         feed = toks[:, i:i + 1]
