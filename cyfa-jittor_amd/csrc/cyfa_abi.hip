@@ -527,6 +527,44 @@ int cyfa_argmax_rows(const void* x, long long ldx, int rows, int n, long long* o
     return check_launch("cyfa_argmax_rows");
 }
 
+int cyfa_gate_path(const CyfaGatePathArgs* a, void* hip_stream) {
+    if (!a) return fail(CYFA_ERR_VALUE, "cyfa_gate_path: null args");
+    if (a->M < 0 || a->K <= 0 || a->H <= 0 || a->Dv <= 0 || a->ldx < a->K || a->ldg < a->Dv)
+        return fail(CYFA_ERR_VALUE, "cyfa_gate_path: M=%d K=%d H=%d Dv=%d ldx=%lld ldg=%lld", a->M, a->K, a->H, a->Dv,
+                    a->ldx, a->ldg);
+    if (a->K % 64 || 3 * a->H > 32 || a->Dv % 256)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_gate_path: K=%d (multiple of 64), H=%d (3H <= 32), Dv=%d (multiple of 256)",
+                    a->K, a->H, a->Dv);
+    if (!a->x || !a->w1 || !a->abd_bias || !a->w2 || !a->dt_bias || !a->A_log || !a->gate || !a->g || !a->beta ||
+        !a->delta)
+        return fail(CYFA_ERR_VALUE, "cyfa_gate_path: null required pointer");
+    if (a->ldx % 8 || a->ldg % 8) return fail(CYFA_ERR_VALUE, "cyfa_gate_path: ldx, ldg must be multiples of 8");
+    if (!aligned(a->x, 16) || !aligned(a->w1, 16) || !aligned(a->w2, 16) || !aligned(a->gate, 16))
+        return fail(CYFA_ERR_ALIGN, "cyfa_gate_path: x, w1, w2 and gate need 16-byte alignment");
+    if (a->M == 0) return CYFA_OK;
+    cyfa::GatePathParams p;
+    p.M = a->M;
+    p.K = a->K;
+    p.H = a->H;
+    p.Dv = a->Dv;
+    p.x = (const __bf16*)a->x;
+    p.ldx = a->ldx;
+    p.w1 = (const __bf16*)a->w1;
+    p.abd_bias = (const __bf16*)a->abd_bias;
+    p.w2 = (const __bf16*)a->w2;
+    p.b2 = (const __bf16*)a->b2;
+    p.dt_bias = a->dt_bias;
+    p.A_log = a->A_log;
+    p.gate = (__bf16*)a->gate;
+    p.ldg = a->ldg;
+    p.g = a->g;
+    p.beta = a->beta;
+    p.delta = a->delta;
+    if (cyfa::launch_gate_path(p, (hipStream_t)hip_stream) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_gate_path: shape refused");
+    return check_launch("cyfa_gate_path");
+}
+
 int cyfa_gates(const void* abd, long long abd_row, const float* dt_bias, const float* A_log, float* g, float* beta,
                float* delta, int rows, int H, void* hip_stream) {
     if (!abd || !dt_bias || !A_log || !g || !beta || !delta || rows < 0 || H <= 0 || abd_row < 3LL * H)

@@ -167,9 +167,7 @@ template <bool LAYER>
 __device__ __forceinline__ void gate_values(const DecodeParams& p, int bh, const GateIn& gi, float& g, float& delta,
                                             float& beta) {
     if (LAYER) {
-        const float a = gi.x0 + gi.dt_bias;
-        const float sp = a > 20.f ? a : log1pf(expf(a));
-        g = -expf(gi.A_log) * sp;
+        g = decay_gate(gi.x0 + gi.dt_bias, gi.A_log);
         beta = sigmoidf(gi.x1);
         delta = sigmoidf(gi.x2);
     } else {

@@ -131,6 +131,13 @@ __device__ __forceinline__ float sigmoidf(float x) {
     return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
 }
 
+// The decay gate g = -exp(A_log) softplus(a + dt_bias) (layers/cyfa.py:323), of
+// x = a + dt_bias; softplus switches to the identity above 20 as F.softplus does.
+__device__ __forceinline__ float decay_gate(float x, float A_log) {
+    const float sp = x > 20.f ? x : log1pf(expf(x));
+    return -expf(A_log) * sp;
+}
+
 // Wave reductions on the VALU. __shfl_xor is a ds_bpermute, an LDS round trip
 // per step (about 30 of them sat on the decode step's serial path): here DPP
 // moves reduce within rows of 16 lanes and v_readlane gathers the rows.

@@ -174,11 +174,32 @@ struct LinearParams {
 
 constexpr int LINEAR_NORM_MAX_K = 2048;
 
+// The prefill gate path of a layer for rows of tokens x [M, K]:
+//   c = x [W_g0 | W_a | W_b | W_d]^T   (256 + 3H columns)
+//   g0 = bf16(c[:, :256]); abd = bf16(c[:, 256:] + abd_bias)
+//   g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b), delta = sigmoid(d)
+//   gate = bf16(g0 W_g1^T + b_g1)      (Dv columns)
+struct GatePathParams {
+    int M, K, H, Dv;
+    const __bf16* x;         // [M, K], rows ldx elements apart
+    long long ldx;
+    const __bf16* w1;        // [256 + 3H, K]: g_proj[0] rows, then a, b, d rows
+    const __bf16* abd_bias;  // [3H] (the a part zero)
+    const __bf16* w2;        // [Dv, 256] g_proj[1] weight
+    const __bf16* b2;        // nullable [Dv]
+    const float *dt_bias, *A_log;  // [H]
+    __bf16* gate;            // [M, Dv], rows ldg elements apart
+    long long ldg;
+    float *g, *beta, *delta;  // [M, H]
+};
+constexpr int GATE_PATH_G0 = 256;  // g_proj[0] width (head_v_dim) the kernel is built for
+
 int launch_rms_norm(const NormParams& p, hipStream_t stream);
 int launch_linear_rows(const LinearParams& p, hipStream_t stream);
 int launch_short_conv(const ConvParams& p, hipStream_t stream);
 int launch_silu_mul(const __bf16* gu, __bf16* out, int rows, int F, hipStream_t stream);
 int launch_argmax_rows(const __bf16* x, long long ldx, int rows, int n, long long* out, hipStream_t stream);
+int launch_gate_path(const GatePathParams& p, hipStream_t stream);
 int launch_gates(const __bf16* abd, long long abd_row, const float* dt_bias, const float* A_log, float* g, float* beta,
                  float* delta, int rows, int H, hipStream_t stream);
 

@@ -411,6 +411,214 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill gate path (layers/cyfa.py:292-295, 323-326, 349): the layer's
+// g_proj[0], a|b|d projections, gate activations and g_proj[1] for 64 token
+// rows per workgroup, 512 threads, in place of four launches that each read
+// the rows again. Stage 1 forms c = x [W_g0 | W_abd]^T over K in chunks of 64
+// (two 32-deep k-steps) staged in LDS as whole 128-byte lines and double
+// buffered (one barrier per chunk): wave w owns g_proj[0] columns 32 w .. + 31
+// of all 64 rows (eight accumulator blocks) and, for w < 4 AB, abd block w >> 2
+// of row block w & 3. g0 goes to LDS in bf16 and the gates straight to memory.
+// Stage 2 forms gate = g0 W_g1^T + b in rounds of 256 columns (wave w: round
+// columns 32 w .. + 31), W_g1 staged the same way, and writes each round's rows
+// through LDS as 16-byte pieces. Rows of x at or past M read as zero (buffer
+// bounds) and are not stored. Every product accumulates in fp32 and is
+// rounded to bf16 once, as the separate projections round it; the gates use
+// gates_kernel's formula on the rounded a|b|d values.
+constexpr int GP_ROWS = 64;
+constexpr int GP_KC = 64;                  // k per staged chunk
+constexpr int GP_LD = GP_KC + 8;           // staged row stride (elements): 144 bytes
+constexpr int GP_G0LD = GATE_PATH_G0 + 8;  // g0 row stride in LDS (elements)
+constexpr int GP_ROUND = 256;              // gate columns per stage-2 round
+constexpr int GP_OLD = GP_ROUND + 8;       // output tile row stride (elements)
+
+template <int AB>
+struct GpLayout {
+    static constexpr int NW1 = GATE_PATH_G0 + 16 * AB;  // staged stage-1 weight rows
+    static constexpr int XS = 0;                        // x chunks: 2 x [64][GP_LD]
+    static constexpr int WS = XS + 2 * GP_ROWS * GP_LD * 2;
+    static constexpr int S1_END = WS + 2 * NW1 * GP_LD * 2;  // weight chunks: 2 x [NW1][GP_LD]
+    static constexpr int G0 = 0;                              // g0: [64][GP_G0LD]
+    static constexpr int W2 = G0 + GP_ROWS * GP_G0LD * 2;     // W_g1 chunks 2 x [256][GP_LD], then the out tile
+    static constexpr int S2_END = W2 + 2 * GP_ROUND * GP_LD * 2;
+    static constexpr int BYTES = S1_END > S2_END ? S1_END : S2_END;
+    static_assert(GP_ROWS * GP_OLD * 2 <= 2 * GP_ROUND * GP_LD * 2, "the out tile fits the W_g1 buffers");
+    static_assert(BYTES <= 160 * 1024, "gate-path workgroup must fit in one CU's LDS");
+};
+
+template <int AB>
+__global__ __launch_bounds__(512) void gate_path_kernel(GatePathParams p) {
+    using L = GpLayout<AB>;
+    __shared__ __align__(16) char lds[L::BYTES];
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), lr = lane & 15,
+              lg = lane >> 4;
+    const int m0 = blockIdx.x * GP_ROWS, mrows = min(GP_ROWS, p.M - m0);
+    const int H = p.H, N1 = GATE_PATH_G0 + 3 * H;
+    const lin_rsrc_t rx = lin_rsrc(p.x + (size_t)m0 * p.ldx, ((size_t)(mrows - 1) * p.ldx + p.K) * 2);
+    const lin_rsrc_t rw1 = lin_rsrc(p.w1, (size_t)N1 * p.K * 2);  // rows past N1 read zero
+    const uint32_t xrs = (uint32_t)p.ldx * 2, krs = (uint32_t)p.K * 2, piece = 16 * (tid & 7);
+
+    // ---- stage 1: c = x [W_g0 | W_abd]^T ----
+    constexpr int NWL = (L::NW1 * 8 + 511) / 512;  // weight loads per thread per chunk
+    u32x4 rxv, rwv[NWL];
+    const auto issue1 = [&](int c) {
+        const uint32_t col = (uint32_t)c * GP_KC * 2 + piece;
+        rxv = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (tid >> 3) * xrs + col, 0, 0));
+#pragma unroll
+        for (int i = 0; i < NWL; i++)
+            rwv[i] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw1, ((tid + 512 * i) >> 3) * krs + col, 0, 0));
+    };
+    const auto store1 = [&](int buf) {
+        char* xs = lds + L::XS + buf * GP_ROWS * GP_LD * 2;
+        *reinterpret_cast<u32x4*>(xs + (tid >> 3) * GP_LD * 2 + piece) = rxv;
+        char* ws = lds + L::WS + buf * L::NW1 * GP_LD * 2;
+#pragma unroll
+        for (int i = 0; i < NWL; i++) {
+            const int idx = tid + 512 * i;
+            if (512 * NWL <= L::NW1 * 8 || idx < L::NW1 * 8)
+                *reinterpret_cast<u32x4*>(ws + (idx >> 3) * GP_LD * 2 + piece) = rwv[i];
+        }
+    };
+    f32x4 acc[4][2], accab = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int rb = 0; rb < 4; rb++) acc[rb][0] = acc[rb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const bool has_ab = w < 4 * AB;
+    const int ab_rb = w & 3, ab_cb = w >> 2;
+    const int nc = p.K / GP_KC;
+    issue1(0);
+    for (int c = 0; c < nc; c++) {
+        store1(c & 1);
+        __syncthreads();
+        if (c + 1 < nc) issue1(c + 1);
+        const bf16_t* xs = reinterpret_cast<const bf16_t*>(lds + L::XS + (c & 1) * GP_ROWS * GP_LD * 2);
+        const bf16_t* ws = reinterpret_cast<const bf16_t*>(lds + L::WS + (c & 1) * L::NW1 * GP_LD * 2);
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            bf16x8 xf[4], wf[2];
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++)
+                xf[rb] = *reinterpret_cast<const bf16x8*>(xs + (16 * rb + lr) * GP_LD + 32 * ks + 8 * lg);
+#pragma unroll
+            for (int cb = 0; cb < 2; cb++)
+                wf[cb] = *reinterpret_cast<const bf16x8*>(ws + (32 * w + 16 * cb + lr) * GP_LD + 32 * ks + 8 * lg);
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+                for (int cb = 0; cb < 2; cb++)
+                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[rb], wf[cb], acc[rb][cb], 0, 0, 0);
+            if (has_ab) {  // uniform; LDS reads only
+                const bf16x8 xa = *reinterpret_cast<const bf16x8*>(xs + (16 * ab_rb + lr) * GP_LD + 32 * ks + 8 * lg);
+                const bf16x8 wa =
+                    *reinterpret_cast<const bf16x8*>(ws + (GATE_PATH_G0 + 16 * ab_cb + lr) * GP_LD + 32 * ks + 8 * lg);
+                accab = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, wa, accab, 0, 0, 0);
+            }
+        }
+    }
+    // the first W_g1 chunk streams in while stage 1 is written out
+    const lin_rsrc_t rw2 = lin_rsrc(p.w2, (size_t)p.Dv * GATE_PATH_G0 * 2);
+    constexpr int NC2 = GATE_PATH_G0 / GP_KC;  // chunks per round
+    constexpr int NWL2 = GP_ROUND * 8 / 512;   // W_g1 loads per thread per chunk
+    u32x4 r2[NWL2];
+    const auto issue2 = [&](int n0, int c) {
+        const uint32_t col = (uint32_t)c * GP_KC * 2 + piece;
+#pragma unroll
+        for (int i = 0; i < NWL2; i++)
+            r2[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rw2, (uint32_t)(n0 + ((tid + 512 * i) >> 3)) * (GATE_PATH_G0 * 2) + col,
+                                                  0, 0));
+    };
+    const auto store2 = [&](int buf) {
+        char* ws = lds + L::W2 + buf * GP_ROUND * GP_LD * 2;
+#pragma unroll
+        for (int i = 0; i < NWL2; i++)
+            *reinterpret_cast<u32x4*>(ws + ((tid + 512 * i) >> 3) * GP_LD * 2 + piece) = r2[i];
+    };
+    issue2(0, 0);
+    // gates of the abd block: lane column 16 ab_cb + lr, rows 16 ab_rb + 4 lg + i
+    const lin_rsrc_t rab = lin_rsrc(p.abd_bias, (size_t)3 * H * 2);
+    const int acol = 16 * ab_cb + lr, ah = acol % H, akind = acol / H;
+    const float abias = bf16_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(rab, (uint32_t)acol * 2, 0, 0));
+    const float adt = p.dt_bias[ah], aal = p.A_log[ah];  // ah < H for every lane
+    __syncthreads();  // stage-1 tiles done with: g0 overwrites them
+    bf16_t* g0s = reinterpret_cast<bf16_t*>(lds + L::G0);
+#pragma unroll
+    for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+        for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                g0s[(16 * rb + 4 * lg + i) * GP_G0LD + 32 * w + 16 * cb + lr] = (bf16_t)acc[rb][cb][i];
+    if (has_ab && acol < 3 * H) {
+        float* dst = akind == 0 ? p.g : akind == 1 ? p.beta : p.delta;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int row = 16 * ab_rb + 4 * lg + i;
+            const float v = (float)(bf16_t)(accab[i] + abias);
+            if (row < mrows) dst[(size_t)(m0 + row) * H + ah] = akind == 0 ? decay_gate(v + adt, aal) : sigmoidf(v);
+        }
+    }
+
+    // ---- stage 2: gate = g0 W_g1^T + b, 256 columns per round ----
+    const lin_rsrc_t rb2 = lin_rsrc(p.b2, p.b2 ? (size_t)p.Dv * 2 : 0);
+    for (int n0 = 0; n0 < p.Dv; n0 += GP_ROUND) {
+        f32x4 acc2[4][2];
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++) acc2[rb][0] = acc2[rb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        float bias[2];  // loaded ahead of the round's later chunks (loads complete in order)
+#pragma unroll
+        for (int cb = 0; cb < 2; cb++)
+            bias[cb] = bf16_bits_to_float(
+                __builtin_amdgcn_raw_buffer_load_b16(rb2, (uint32_t)(n0 + 32 * w + 16 * cb + lr) * 2, 0, 0));
+        for (int c = 0; c < NC2; c++) {
+            store2(c & 1);
+            __syncthreads();  // (first chunk: g0 complete too)
+            if (c + 1 < NC2)
+                issue2(n0, c + 1);
+            else if (n0 + GP_ROUND < p.Dv)
+                issue2(n0 + GP_ROUND, 0);  // the next round's first chunk
+            const bf16_t* ws = reinterpret_cast<const bf16_t*>(lds + L::W2 + (c & 1) * GP_ROUND * GP_LD * 2);
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                bf16x8 xf[4], wf[2];
+#pragma unroll
+                for (int rb = 0; rb < 4; rb++)
+                    xf[rb] = *reinterpret_cast<const bf16x8*>(g0s + (16 * rb + lr) * GP_G0LD + GP_KC * c + 32 * ks +
+                                                              8 * lg);
+#pragma unroll
+                for (int cb = 0; cb < 2; cb++)
+                    wf[cb] =
+                        *reinterpret_cast<const bf16x8*>(ws + (32 * w + 16 * cb + lr) * GP_LD + 32 * ks + 8 * lg);
+#pragma unroll
+                for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+                    for (int cb = 0; cb < 2; cb++)
+                        acc2[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[rb], wf[cb], acc2[rb][cb], 0, 0, 0);
+            }
+        }
+        __syncthreads();  // the round's W_g1 chunks done with: the out tile overwrites them
+        bf16_t* ot = reinterpret_cast<bf16_t*>(lds + L::W2);
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+            for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    ot[(16 * rb + 4 * lg + i) * GP_OLD + 32 * w + 16 * cb + lr] = (bf16_t)(acc2[rb][cb][i] + bias[cb]);
+        __syncthreads();
+        // 64 rows x 32 pieces of 16 bytes
+#pragma unroll
+        for (int i = 0; i < GP_ROWS * (GP_ROUND / 8) / 512; i++) {
+            const int idx = tid + 512 * i, row = idx >> 5, pc = idx & 31;
+            if (row < mrows)
+                *reinterpret_cast<u32x4*>(p.gate + (size_t)(m0 + row) * p.ldg + n0 + 8 * pc) =
+                    *reinterpret_cast<const u32x4*>(ot + row * GP_OLD + 8 * pc);
+        }
+        __syncthreads();  // the out tile read before the next round's chunks land
+    }
+}
+
 // Causal depthwise convolution over time (layers/cyfa.py:138-233):
 //   y[b, t, c] = bias[c] + sum_{w < W} weight[c, w] * X[b, t + w - (W - 1), c]
 // where X[b, i] is x[b, i] for i >= 0, cache[b, W - 1 + i] for i < 0 when a
@@ -594,9 +802,7 @@ __global__ __launch_bounds__(256) void gates_kernel(const bf16_t* abd, long long
     if (i >= rows * H) return;
     const int r = i / H, h = i % H;
     const bf16_t* row = abd + (size_t)r * abd_row;
-    const float a = (float)row[h] + dt_bias[h];
-    const float sp = a > 20.f ? a : log1pf(expf(a));
-    g[i] = -expf(A_log[h]) * sp;
+    g[i] = decay_gate((float)row[h] + dt_bias[h], A_log[h]);
     beta[i] = sigmoidf((float)row[H + h]);
     delta[i] = sigmoidf((float)row[2 * H + h]);
 }
@@ -726,6 +932,22 @@ int launch_silu_mul(const bf16_t* gu, bf16_t* out, int rows, int F, hipStream_t 
 
 int launch_argmax_rows(const bf16_t* x, long long ldx, int rows, int n, long long* out, hipStream_t stream) {
     hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(1024), 0, stream, x, ldx, n, out);
+    return 0;
+}
+
+int launch_gate_path(const GatePathParams& p, hipStream_t stream) {
+    const int ab = (3 * p.H + 15) / 16;
+    if (p.M < 1 || p.K < GP_KC || p.K % GP_KC || p.H < 1 || ab > 2 || p.Dv < GP_ROUND || p.Dv % GP_ROUND) return -1;
+    // every buffer the kernel reads spans less than 2^31 bytes (32-bit offsets, LIN_DEAD unused here)
+    const unsigned long long xspan = ((unsigned long long)(min(p.M, GP_ROWS) - 1) * p.ldx + p.K) * 2;
+    if ((unsigned long long)(GATE_PATH_G0 + 3 * p.H) * p.K * 2 >= LIN_DEAD || xspan >= LIN_DEAD ||
+        (unsigned long long)p.Dv * GATE_PATH_G0 * 2 >= LIN_DEAD)
+        return -1;
+    const dim3 grid((p.M + GP_ROWS - 1) / GP_ROWS), block(512);
+    if (ab == 1)
+        hipLaunchKernelGGL(gate_path_kernel<1>, grid, block, 0, stream, p);
+    else
+        hipLaunchKernelGGL(gate_path_kernel<2>, grid, block, 0, stream, p);
     return 0;
 }
 

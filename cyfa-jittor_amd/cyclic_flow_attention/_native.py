@@ -14,7 +14,7 @@ import torch
 import torch.nn.functional as F
 
 LIB_PATH = Path(os.environ.get("CYFA_LIB", Path(__file__).with_name("libcyfa_hip.so")))
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 CYFA_OK = 0
 CYFA_ERR_VALUE = -1
@@ -115,6 +115,15 @@ class CyfaConvArgs(ctypes.Structure):
     ]
 
 
+class CyfaGatePathArgs(ctypes.Structure):
+    _fields_ = [
+        ("M", _c_int), ("K", _c_int), ("H", _c_int), ("Dv", _c_int),
+        ("x", _c_void_p), ("ldx", ctypes.c_longlong), ("w1", _c_void_p), ("abd_bias", _c_void_p),
+        ("w2", _c_void_p), ("b2", _c_void_p), ("dt_bias", _c_void_p), ("A_log", _c_void_p),
+        ("gate", _c_void_p), ("ldg", ctypes.c_longlong), ("g", _c_void_p), ("beta", _c_void_p), ("delta", _c_void_p),
+    ]
+
+
 # Every symbol include/cyfa_abi.h declares, with its ctypes signature.
 SIGNATURES = {
     "cyfa_chunk_fwd": (_c_int, [ctypes.POINTER(CyfaChunkArgs), _c_void_p]),
@@ -135,6 +144,7 @@ SIGNATURES = {
     "cyfa_argmax_rows": (_c_int, [_c_void_p, ctypes.c_longlong, _c_int, _c_int, _c_void_p, _c_void_p]),
     "cyfa_gates": (_c_int, [_c_void_p, ctypes.c_longlong, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                             _c_int, _c_int, _c_void_p]),
+    "cyfa_gate_path": (_c_int, [ctypes.POINTER(CyfaGatePathArgs), _c_void_p]),
     "cyfa_last_error": (ctypes.c_char_p, []),
     "cyfa_abi_version": (_c_int, []),
 }
@@ -555,6 +565,46 @@ def silu_mul(gu):
     _check(load_library().cyfa_silu_mul(ptr(gu), ptr(out), gu.numel() // F2, F2 // 2, stream_handle(dev)),
            "cyfa_silu_mul")
     return out
+
+
+GATE_PATH_G0 = 256
+
+
+def gate_path_ok(x, w1, w2, b2, H):
+    """Whether gate_path takes these operands (else the separate projections)."""
+    K = x.shape[-1]
+    return (x.is_cuda and x.dtype == torch.bfloat16 and w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16
+            and (b2 is None or b2.dtype == torch.bfloat16) and not torch.is_grad_enabled()
+            and K % 64 == 0 and 3 * H <= 32 and w1.shape == (GATE_PATH_G0 + 3 * H, K)
+            and w2.shape[1] == GATE_PATH_G0 and w2.shape[0] % 256 == 0)
+
+
+def gate_path(x, w1, abd_bias, w2, b2, dt_bias, A_log, H):
+    """The prefill gate path in one cyfa_gate_path launch: g0 = bf16(x W_g0^T),
+    abd = bf16(x [W_a|W_b|W_d]^T + abd_bias), the gate activations of abd and
+    gate = bf16(g0 W_g1^T + b2). w1 = [W_g0; W_a; W_b; W_d] [256 + 3H, K].
+    Returns (gate [..., Dv] bf16, g, beta, delta [..., H] fp32)."""
+    K = x.shape[-1]
+    Dv = w2.shape[0]
+    rows = x.numel() // K
+    dev = require_device(x, w1, abd_bias, w2, b2, dt_bias, A_log)
+    x2 = x.reshape(rows, K)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    w1c, w2c = w1.detach().contiguous(), w2.detach().contiguous()
+    ab = abd_bias.detach().to(torch.bfloat16).contiguous()
+    b2c = None if b2 is None else b2.detach().contiguous()
+    db = dt_bias.detach().to(torch.float32).contiguous()
+    al = A_log.detach().to(torch.float32).contiguous()
+    gate = torch.empty(rows, Dv, dtype=torch.bfloat16, device=dev)
+    g, beta, delta = (torch.empty(rows, H, dtype=torch.float32, device=dev) for _ in range(3))
+    args = CyfaGatePathArgs(M=rows, K=K, H=H, Dv=Dv, x=x2.data_ptr(), ldx=x2.stride(0), w1=w1c.data_ptr(),
+                            abd_bias=ab.data_ptr(), w2=w2c.data_ptr(), b2=ptr(b2c), dt_bias=db.data_ptr(),
+                            A_log=al.data_ptr(), gate=gate.data_ptr(), ldg=Dv, g=g.data_ptr(), beta=beta.data_ptr(),
+                            delta=delta.data_ptr())
+    _check(load_library().cyfa_gate_path(ctypes.byref(args), stream_handle(dev)), "cyfa_gate_path")
+    lead = tuple(x.shape[:-1])
+    return gate.view(lead + (Dv,)), g.view(lead + (H,)), beta.view(lead + (H,)), delta.view(lead + (H,))
 
 
 def gates(abd, dt_bias, A_log):

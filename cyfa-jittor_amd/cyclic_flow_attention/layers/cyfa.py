@@ -228,6 +228,7 @@ class CyclicFlowAttention(nn.Module):
         # decode steps: one [q | k | v | g_proj[0] | a | b | d] projection
         self._in_weight = FusedWeight()
         self._in_weight_folded = FusedWeight()
+        self._gp_weight = FusedWeight()
         # When set, a decode step with the block's norm fused into the input
         # projection multiplies the norm weight into the projection's weight
         # (cached) and applies the row scale to the product (cyfa_norm_linear_rows
@@ -417,10 +418,19 @@ class CyclicFlowAttention(nn.Module):
             (y,) = _native.short_conv(qkv, wconv.reshape(-1, W).to(x.dtype), None, cat_cache, cache_out=tail)
             q, k, v = y[..., :Dk].contiguous(), y[..., Dk:2 * Dk].contiguous(), y[..., 2 * Dk:].contiguous()
         cq, ck, cv = tail[..., :Dk], tail[..., Dk:2 * Dk], tail[..., 2 * Dk:]
-        if abd is None:
-            abd = _native.linear(x, self._abd_weight.get(self.a_proj.weight, self.b_proj.weight, self.d_proj.weight),
-                                 abd_bias)
-        g, beta, delta = _native.gates(abd, self.dt_bias, self.A_log)
+        gate = None
+        if abd is None and g0_out is None:
+            w1 = self._gp_weight.get(g0.weight, self.a_proj.weight, self.b_proj.weight, self.d_proj.weight)
+            if _native.gate_path_ok(x, w1, g1.weight, g1.bias, H):
+                # g_proj[0], a|b|d, the gates and g_proj[1] in one launch
+                gate, g, beta, delta = _native.gate_path(x, w1, abd_bias, g1.weight, g1.bias, self.dt_bias,
+                                                         self.A_log, H)
+                gate = gate.view(B, T, H, self.head_v_dim)
+        if gate is None:
+            if abd is None:
+                abd = _native.linear(x, self._abd_weight.get(self.a_proj.weight, self.b_proj.weight,
+                                                              self.d_proj.weight), abd_bias)
+            g, beta, delta = _native.gates(abd, self.dt_bias, self.A_log)
         kwargs = dict(
             q=q.view(B, T, H, self.head_k_dim),
             k=k.view(B, T, H, self.head_k_dim),
@@ -436,9 +446,10 @@ class CyclicFlowAttention(nn.Module):
             initial_state=None if cache is None else cache["recurrent_state"],
             output_final_state=use_cache,
         )
-        if g0_out is None:
-            g0_out = _native.linear(x, g0.weight)
-        gate = _native.linear(g0_out, g1.weight, g1.bias).view(B, T, H, self.head_v_dim)
+        if gate is None:
+            if g0_out is None:
+                g0_out = _native.linear(x, g0.weight)
+            gate = _native.linear(g0_out, g1.weight, g1.bias).view(B, T, H, self.head_v_dim)
         if not self.training and T == 1:
             o, state = fused_recurrent_cyfa(**kwargs, table=self.readout_table(),
                                             inplace=self.decode_in_place and cache is not None)

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define CYFA_ABI_VERSION 5
+#define CYFA_ABI_VERSION 6
 
 enum {
     CYFA_OK = 0,
@@ -298,6 +298,33 @@ typedef struct CyfaRowNormArgs {
  * layers/cyfa.py:62-135). The norm's sum of squares runs in another order than
  * cyfa_rms_norm's, so xs may differ from it in the last bit. */
 int cyfa_norm_linear_rows(const CyfaLinearArgs *args, const CyfaRowNormArgs *norm, void *hip_stream);
+
+/* The prefill gate path of CyclicFlowAttention.execute for M token rows x
+ * [M, K] (layers/cyfa.py:292-295, 323-326, 349): the g_proj[0] and a|b|d
+ * projections, the gate activations and g_proj[1] in one launch:
+ *   c  = x [W_g0 | W_a | W_b | W_d]^T          (256 + 3H columns)
+ *   g0 = bf16(c[:, :256]),  abd = bf16(c[:, 256:] + abd_bias)
+ *   g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b), delta = sigmoid(d)
+ *   gate = bf16(g0 W_g1^T + b_g1)
+ * with fp32 accumulation and the roundings of the separate projections (the
+ * summation order differs from a library GEMM's, so a value can differ from
+ * theirs in the last bit). K a multiple of 64, 3H <= 32, Dv a multiple of 256,
+ * g_proj[0] 256 wide. No reference counterpart as one entry point. */
+typedef struct CyfaGatePathArgs {
+    int M, K, H, Dv;
+    const void *x;                /* bf16 [M, K], rows ldx elements apart, 16-byte aligned */
+    long long ldx;                /* a multiple of 8, >= K */
+    const void *w1;               /* bf16 [256 + 3H, K]: g_proj[0] rows, then a, b, d rows; 16-byte aligned */
+    const void *abd_bias;         /* bf16 [3H] (zero for the a part) */
+    const void *w2;               /* bf16 [Dv, 256] g_proj[1] weight, 16-byte aligned */
+    const void *b2;               /* nullable bf16 [Dv] g_proj[1] bias */
+    const float *dt_bias, *A_log; /* f32 [H] */
+    void *gate;                   /* bf16 [M, Dv], rows ldg elements apart, 16-byte aligned */
+    long long ldg;                /* a multiple of 8, >= Dv */
+    float *g, *beta, *delta;      /* f32 [M, H] */
+} CyfaGatePathArgs;
+
+int cyfa_gate_path(const CyfaGatePathArgs *args, void *hip_stream);
 
 /* Arguments of one causal depthwise convolution over time of B x T rows of D
  * bf16 channels (D a multiple of 8, W in 2..4):

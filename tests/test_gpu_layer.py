@@ -532,3 +532,73 @@ def test_argmax_rows_equals_torch_argmax():
     assert torch.equal(got.cpu(), xd.argmax(-1).cpu())
     y = torch.randn(5, 104, generator=gen).bfloat16().to(DEV)[:, :100]  # rows 104 apart, 100 wide
     assert torch.equal(_native.argmax_rows(y).cpu(), y.argmax(-1).cpu())
+
+
+def _bf16_ulp(b):
+    """Spacing of bf16 values at b (bf16 keeps 8 significant bits)."""
+    _, e = torch.frexp(b.abs().clamp_min(2.0 ** -126))
+    return torch.ldexp(torch.ones_like(b), e - 8)
+
+
+def _near_rounding_edge(v64, err):
+    """Entries whose float64 value lies within err of a bf16 rounding edge: an
+    fp32 sum may round them to the neighbouring bf16 value."""
+    b = v64.bfloat16().double()
+    return (_bf16_ulp(b) / 2 - (v64 - b).abs()) < err
+
+
+@pytest.mark.parametrize("M,H,K", [(200, 4, 1024), (64, 4, 1024), (131, 8, 2048)])
+def test_gate_path_matches_float64(M, H, K):
+    """cyfa_gate_path (g_proj[0], a|b|d, the gate activations and g_proj[1] in
+    one launch) against float64 with the kernel's rounding points: g0 and abd
+    rounded to bf16 (where the float64 value lies within a statistical bound
+    of the fp32 summation error of a rounding edge, either neighbour), the gates of the rounded
+    a|b|d, and gate = bf16(g0 W_g1^T + b) within its last rounding plus the
+    fp32 summation error and the effect of any such neighbour in g0."""
+    from cyclic_flow_attention import _native
+
+    gen = torch.Generator().manual_seed(M + H + K)
+    Dv = 256 * H
+    x = torch.randn(M, K, generator=gen).bfloat16()
+    w1 = (0.03 * torch.randn(256 + 3 * H, K, generator=gen)).bfloat16()
+    abd_bias = torch.cat([torch.zeros(H), torch.randn(2 * H, generator=gen)]).bfloat16()
+    w2 = (0.05 * torch.randn(Dv, 256, generator=gen)).bfloat16()
+    b2 = torch.randn(Dv, generator=gen).bfloat16()
+    dt_bias = torch.randn(H, generator=gen)
+    A_log = torch.rand(H, generator=gen)
+    d = lambda t: t.to(DEV)  # noqa: E731
+    with torch.no_grad():
+        gate, g, beta, delta = _native.gate_path(d(x), d(w1), d(abd_bias), d(w2), d(b2), d(dt_bias), d(A_log), H)
+    torch.cuda.synchronize()
+    x64, w164 = x.double(), w1.double()
+    c64 = x64 @ w164.T
+    # fp32 summation error of the K exact bf16 products: each rounding errs by
+    # at most 2^-24 of its running sum, and as independent errors over sums
+    # that grow like a random walk they total a standard deviation near
+    # 2^-25 * sum|x w|; 8 * 2^-24 * sum|x w| is about 16 of them (the K * 2^-24
+    # worst case would mark most entries as near an edge)
+    e1 = 8 * 2.0 ** -24 * (x64.abs() @ w164.abs().T)
+    g0_64, abd64 = c64[:, :256], c64[:, 256:] + abd_bias.double()
+    g0b = g0_64.bfloat16().double()
+    near0 = _near_rounding_edge(g0_64, e1[:, :256])
+    assert near0.double().mean() < 0.05
+    w264 = w2.double()
+    p64 = g0b @ w264.T + b2.double()
+    mag2 = g0b.abs() @ w264.abs().T
+    flip = (near0.double() * _bf16_ulp(g0b)) @ w264.abs().T
+    bound = 2 * (BF16_ULP / 2 * (p64.abs() + mag2) + 256 * 2.0 ** -24 * mag2 + flip) + 1e-30
+    err = (gate.cpu().double() - p64).abs()
+    assert (err <= bound).all(), f"gate: max err {err.max().item()}"
+    ab = abd64.bfloat16().double()
+    nearab = _near_rounding_edge(abd64, e1[:, 256:] + 2.0 ** -24 * abd64.abs())
+    a, b, dd = ab[:, :H], ab[:, H:2 * H], ab[:, 2 * H:]
+    g64 = -torch.exp(A_log.double()) * torch.nn.functional.softplus(a + dt_bias.double())
+    for got, ref, deriv, nr, name in (
+        (g, g64, torch.exp(A_log.double()) * torch.sigmoid(a + dt_bias.double()), nearab[:, :H], "g"),
+        (beta, torch.sigmoid(b), torch.sigmoid(b) * (1 - torch.sigmoid(b)), nearab[:, H:2 * H], "beta"),
+        (delta, torch.sigmoid(dd), torch.sigmoid(dd) * (1 - torch.sigmoid(dd)), nearab[:, 2 * H:], "delta"),
+    ):
+        span = _bf16_ulp(ab[:, :H] if name == "g" else (b if name == "beta" else dd))
+        tol = 4e-6 * ref.abs() + nr.double() * deriv * span + 1e-7
+        e = (got.cpu().double() - ref).abs()
+        assert (e <= tol).all(), f"{name}: max err {e.max().item()}"
