@@ -532,9 +532,10 @@ int cyfa_gate_path(const CyfaGatePathArgs* a, void* hip_stream) {
     if (a->M < 0 || a->K <= 0 || a->H <= 0 || a->Dv <= 0 || a->ldx < a->K || a->ldg < a->Dv)
         return fail(CYFA_ERR_VALUE, "cyfa_gate_path: M=%d K=%d H=%d Dv=%d ldx=%lld ldg=%lld", a->M, a->K, a->H, a->Dv,
                     a->ldx, a->ldg);
-    if (a->K % 64 || 3 * a->H > 32 || a->Dv % 256)
-        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_gate_path: K=%d (multiple of 64), H=%d (3H <= 32), Dv=%d (multiple of 256)",
-                    a->K, a->H, a->Dv);
+    if (a->K % 64 || a->K > cyfa::GATE_PATH_MAX_K || 3 * a->H > 32 || a->Dv % 256 || a->Dv > cyfa::GATE_PATH_MAX_DV)
+        return fail(CYFA_ERR_UNSUPPORTED,
+                    "cyfa_gate_path: K=%d (a multiple of 64, <= %d), H=%d (3H <= 32), Dv=%d (a multiple of 256, <= %d)",
+                    a->K, cyfa::GATE_PATH_MAX_K, a->H, a->Dv, cyfa::GATE_PATH_MAX_DV);
     if (!a->x || !a->w1 || !a->abd_bias || !a->w2 || !a->dt_bias || !a->A_log || !a->gate || !a->g || !a->beta ||
         !a->delta)
         return fail(CYFA_ERR_VALUE, "cyfa_gate_path: null required pointer");

@@ -192,7 +192,9 @@ struct GatePathParams {
     long long ldg;
     float *g, *beta, *delta;  // [M, H]
 };
-constexpr int GATE_PATH_G0 = 256;  // g_proj[0] width (head_v_dim) the kernel is built for
+constexpr int GATE_PATH_G0 = 256;       // g_proj[0] width (head_v_dim) the kernel is built for
+constexpr int GATE_PATH_MAX_K = 2048;   // largest hidden size (its k-chunk loop is unrolled to this)
+constexpr int GATE_PATH_MAX_DV = 2048;  // largest H * head_v_dim (its column rounds, likewise)
 
 int launch_rms_norm(const NormParams& p, hipStream_t stream);
 int launch_linear_rows(const LinearParams& p, hipStream_t stream);

@@ -96,6 +96,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormParams p) {
 // bounds).
 typedef __amdgpu_buffer_rsrc_t lin_rsrc_t;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int LIN_STRIDE = 144;  // staged row: 128 bytes (two k-steps) + 16 bytes of padding
 
@@ -415,142 +416,173 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
 // Prefill gate path (layers/cyfa.py:292-295, 323-326, 349): the layer's
 // g_proj[0], a|b|d projections, gate activations and g_proj[1] for 64 token
 // rows per workgroup, 512 threads, in place of four launches that each read
-// the rows again. Stage 1 forms c = x [W_g0 | W_abd]^T over K in chunks of 64
-// (two 32-deep k-steps) staged in LDS as whole 128-byte lines and double
-// buffered (one barrier per chunk): wave w owns g_proj[0] columns 32 w .. + 31
-// of all 64 rows (eight accumulator blocks) and, for w < 4 AB, abd block w >> 2
-// of row block w & 3. g0 goes to LDS in bf16 and the gates straight to memory.
+// the rows again. Every operand streams in chunks of 64 k (one 128-byte line
+// per row) as whole-line loads into a ring of three register sets, three
+// chunks ahead; chunk c + 1 is written to one of two LDS buffers while chunk c
+// is multiplied from the other, with one barrier per chunk. In LDS, 16-byte
+// piece p of row r sits at piece p ^ (r & 7) of the row, so that the sixteen
+// rows of an MFMA operand read spread over the banks.
+// Stage 1 forms c = x [W_g0 | W_abd]^T: wave w owns g_proj[0] columns
+// 32 w .. + 31 of all 64 rows (eight accumulator blocks) and, for w < 4 AB,
+// abd block w >> 2 of row block w & 3. g0 is rounded to bf16 and passed
+// through LDS into registers, the A operand of every stage-2 product.
 // Stage 2 forms gate = g0 W_g1^T + b in rounds of 256 columns (wave w: round
-// columns 32 w .. + 31), W_g1 staged the same way, and writes each round's rows
-// through LDS as 16-byte pieces. Rows of x at or past M read as zero (buffer
-// bounds) and are not stored. Every product accumulates in fp32 and is
+// columns 32 w .. + 31); each wave writes its tile through its own LDS region
+// as 16-byte pieces. Rows of x at or past M read as zero (buffer bounds) and
+// are not stored. Every product accumulates in fp32 over k in order and is
 // rounded to bf16 once, as the separate projections round it; the gates use
 // gates_kernel's formula on the rounded a|b|d values.
+// The chunk sequences are written out (gp_unrolled): each ring slot is a
+// fixed set of registers, and no loop back edge remains (around one the
+// compiler waits for every load in flight).
 constexpr int GP_ROWS = 64;
-constexpr int GP_KC = 64;                  // k per staged chunk
-constexpr int GP_LD = GP_KC + 8;           // staged row stride (elements): 144 bytes
-constexpr int GP_G0LD = GATE_PATH_G0 + 8;  // g0 row stride in LDS (elements)
-constexpr int GP_ROUND = 256;              // gate columns per stage-2 round
-constexpr int GP_OLD = GP_ROUND + 8;       // output tile row stride (elements)
+constexpr int GP_ROUND = 256;  // gate columns per stage-2 round
+constexpr int GP_MAX_CHUNKS = GATE_PATH_MAX_K / 64;
+constexpr int GP_MAX_Q = 4 * (GATE_PATH_MAX_DV / GP_ROUND);  // stage-2 chunks: 4 per round
 
 template <int AB>
 struct GpLayout {
-    static constexpr int NW1 = GATE_PATH_G0 + 16 * AB;  // staged stage-1 weight rows
-    static constexpr int XS = 0;                        // x chunks: 2 x [64][GP_LD]
-    static constexpr int WS = XS + 2 * GP_ROWS * GP_LD * 2;
-    static constexpr int S1_END = WS + 2 * NW1 * GP_LD * 2;  // weight chunks: 2 x [NW1][GP_LD]
-    static constexpr int G0 = 0;                              // g0: [64][GP_G0LD]
-    static constexpr int W2 = G0 + GP_ROWS * GP_G0LD * 2;     // W_g1 chunks 2 x [256][GP_LD], then the out tile
-    static constexpr int S2_END = W2 + 2 * GP_ROUND * GP_LD * 2;
-    static constexpr int BYTES = S1_END > S2_END ? S1_END : S2_END;
-    static_assert(GP_ROWS * GP_OLD * 2 <= 2 * GP_ROUND * GP_LD * 2, "the out tile fits the W_g1 buffers");
-    static_assert(BYTES <= 160 * 1024, "gate-path workgroup must fit in one CU's LDS");
+    static constexpr int NW1 = GATE_PATH_G0 + 16 * AB;   // stage-1 weight rows
+    static constexpr int NWL = (NW1 + 63) / 64;          // weight loads per thread per chunk (8 rows per wave load)
+    static constexpr int BUF = (GP_ROWS + 64 * NWL) * 128;  // one stage-1 buffer: x rows, then weight rows
+    static_assert(GP_ROUND * 128 <= BUF && GP_ROWS * GATE_PATH_G0 * 2 <= BUF, "stage 2 fits a buffer");
 };
+constexpr int GP_OT = 8 * 16 * 64;  // per-wave output tiles: 16 rows x 32 columns of bf16
+static_assert(2 * GpLayout<2>::BUF + GP_OT + GATE_PATH_MAX_DV * 2 <= 160 * 1024, "gate-path LDS");
+
+// The MFMA operand piece of row R, k-step h of the chunk: k = 32 h + 8 lg .. + 7.
+__device__ __forceinline__ bf16x8 gp_frag(const char* buf, int R, int h, int lg) {
+    return *reinterpret_cast<const bf16x8*>(buf + R * 128 + 16 * ((4 * h + lg) ^ (R & 7)));
+}
+
+// f(integral_constant<int, i>) for i = C .. n - 1 (n <= MAX), written out.
+template <int C, int MAX, typename F>
+__device__ __forceinline__ void gp_unrolled(int n, F&& f) {
+    if constexpr (C < MAX) {
+        if (C >= n) return;
+        f(std::integral_constant<int, C>{});
+        gp_unrolled<C + 1, MAX>(n, f);
+    }
+}
 
 template <int AB>
 __global__ __launch_bounds__(512) void gate_path_kernel(GatePathParams p) {
     using L = GpLayout<AB>;
-    __shared__ __align__(16) char lds[L::BYTES];
+    constexpr int NWL = L::NWL;
+    __shared__ __align__(16) char buf[2][L::BUF];
+    __shared__ __align__(16) char sot[GP_OT];
+    __shared__ __align__(16) bf16_t sbias[GATE_PATH_MAX_DV];  // 512 threads x 4
+    static_assert(GATE_PATH_MAX_DV == 4 * 512, "one 8-byte bias load per thread");
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), lr = lane & 15,
               lg = lane >> 4;
     const int m0 = blockIdx.x * GP_ROWS, mrows = min(GP_ROWS, p.M - m0);
     const int H = p.H, N1 = GATE_PATH_G0 + 3 * H;
     const lin_rsrc_t rx = lin_rsrc(p.x + (size_t)m0 * p.ldx, ((size_t)(mrows - 1) * p.ldx + p.K) * 2);
     const lin_rsrc_t rw1 = lin_rsrc(p.w1, (size_t)N1 * p.K * 2);  // rows past N1 read zero
-    const uint32_t xrs = (uint32_t)p.ldx * 2, krs = (uint32_t)p.K * 2, piece = 16 * (tid & 7);
+    const lin_rsrc_t rw2 = lin_rsrc(p.w2, (size_t)p.Dv * GATE_PATH_G0 * 2);
+    const uint32_t xrs = (uint32_t)p.ldx * 2, krs = (uint32_t)p.K * 2;
+    // a load lane's row within its group of eight, the piece it fetches and
+    // where that piece goes in LDS
+    const int r8 = lane >> 3, pl = lane & 7, ps = 16 * (pl ^ r8);
+
+    // the gate inputs of this thread's abd column and the g_proj[1] bias (into
+    // LDS; past Dv: zero), loaded first
+    const int ab_rb = w & 3, ab_cb = w >> 2;
+    const lin_rsrc_t rab = lin_rsrc(p.abd_bias, (size_t)3 * H * 2);
+    const int acol = 16 * ab_cb + lr, ah = acol % H, akind = acol / H;
+    const float abias = bf16_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(rab, (uint32_t)acol * 2, 0, 0));
+    const float adt = p.dt_bias[ah], aal = p.A_log[ah];  // ah < H for every lane
+    {
+        const lin_rsrc_t rb2 = lin_rsrc(p.b2, p.b2 ? (size_t)p.Dv * 2 : 0);
+        *reinterpret_cast<u32x2*>(sbias + 4 * tid) =
+            __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rb2, 8 * tid, 0, 0));
+    }
 
     // ---- stage 1: c = x [W_g0 | W_abd]^T ----
-    constexpr int NWL = (L::NW1 * 8 + 511) / 512;  // weight loads per thread per chunk
-    u32x4 rxv, rwv[NWL];
-    const auto issue1 = [&](int c) {
-        const uint32_t col = (uint32_t)c * GP_KC * 2 + piece;
-        rxv = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (tid >> 3) * xrs + col, 0, 0));
+    const int nc = p.K / 64;
+    u32x4 r1[3][1 + NWL];  // ring: x piece, then the weight pieces (rows 64 i + 8 w + r8)
+    const auto issue1 = [&](int c, u32x4 (&r)[1 + NWL]) {
+        const uint32_t dead = ((uint32_t)(c - nc) & LIN_DEAD) ^ LIN_DEAD;  // chunks past K read zero
+        const uint32_t col = ((uint32_t)c * 128 + 16 * pl) | dead;
+        r[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(8 * w + r8) * xrs + col, 0, 0));
 #pragma unroll
         for (int i = 0; i < NWL; i++)
-            rwv[i] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw1, ((tid + 512 * i) >> 3) * krs + col, 0, 0));
+            r[1 + i] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw1, (uint32_t)(64 * i + 8 * w + r8) * krs + col, 0, 0));
     };
-    const auto store1 = [&](int buf) {
-        char* xs = lds + L::XS + buf * GP_ROWS * GP_LD * 2;
-        *reinterpret_cast<u32x4*>(xs + (tid >> 3) * GP_LD * 2 + piece) = rxv;
-        char* ws = lds + L::WS + buf * L::NW1 * GP_LD * 2;
+    const auto store1 = [&](char* b, const u32x4 (&r)[1 + NWL]) {
+        *reinterpret_cast<u32x4*>(b + (8 * w + r8) * 128 + ps) = r[0];
 #pragma unroll
-        for (int i = 0; i < NWL; i++) {
-            const int idx = tid + 512 * i;
-            if (512 * NWL <= L::NW1 * 8 || idx < L::NW1 * 8)
-                *reinterpret_cast<u32x4*>(ws + (idx >> 3) * GP_LD * 2 + piece) = rwv[i];
-        }
+        for (int i = 0; i < NWL; i++) *reinterpret_cast<u32x4*>(b + (GP_ROWS + 64 * i + 8 * w + r8) * 128 + ps) = r[1 + i];
     };
     f32x4 acc[4][2], accab = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int rb = 0; rb < 4; rb++) acc[rb][0] = acc[rb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const bool has_ab = w < 4 * AB;
-    const int ab_rb = w & 3, ab_cb = w >> 2;
-    const int nc = p.K / GP_KC;
-    issue1(0);
-    for (int c = 0; c < nc; c++) {
-        store1(c & 1);
-        __syncthreads();
-        if (c + 1 < nc) issue1(c + 1);
-        const bf16_t* xs = reinterpret_cast<const bf16_t*>(lds + L::XS + (c & 1) * GP_ROWS * GP_LD * 2);
-        const bf16_t* ws = reinterpret_cast<const bf16_t*>(lds + L::WS + (c & 1) * L::NW1 * GP_LD * 2);
+    issue1(0, r1[0]);
+    issue1(1, r1[1]);
+    issue1(2, r1[2]);
+    store1(buf[0], r1[0]);
+    issue1(3, r1[0]);
+    gp_unrolled<0, GP_MAX_CHUNKS>(nc, [&](auto cc) {
+        constexpr int c = decltype(cc)::value;
+        __syncthreads();  // chunk c is in buf[c & 1]; buf[(c + 1) & 1] is read by no one
+        const char* b = buf[c & 1];
+        store1(buf[(c + 1) & 1], r1[(c + 1) % 3]);
+        issue1(c + 4, r1[(c + 1) % 3]);
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
+        for (int h = 0; h < 2; h++) {
             bf16x8 xf[4], wf[2];
 #pragma unroll
-            for (int rb = 0; rb < 4; rb++)
-                xf[rb] = *reinterpret_cast<const bf16x8*>(xs + (16 * rb + lr) * GP_LD + 32 * ks + 8 * lg);
+            for (int rb = 0; rb < 4; rb++) xf[rb] = gp_frag(b, 16 * rb + lr, h, lg);
 #pragma unroll
-            for (int cb = 0; cb < 2; cb++)
-                wf[cb] = *reinterpret_cast<const bf16x8*>(ws + (32 * w + 16 * cb + lr) * GP_LD + 32 * ks + 8 * lg);
+            for (int cb = 0; cb < 2; cb++) wf[cb] = gp_frag(b, GP_ROWS + 32 * w + 16 * cb + lr, h, lg);
 #pragma unroll
             for (int rb = 0; rb < 4; rb++)
 #pragma unroll
                 for (int cb = 0; cb < 2; cb++)
                     acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[rb], wf[cb], acc[rb][cb], 0, 0, 0);
-            if (has_ab) {  // uniform; LDS reads only
-                const bf16x8 xa = *reinterpret_cast<const bf16x8*>(xs + (16 * ab_rb + lr) * GP_LD + 32 * ks + 8 * lg);
-                const bf16x8 wa =
-                    *reinterpret_cast<const bf16x8*>(ws + (GATE_PATH_G0 + 16 * ab_cb + lr) * GP_LD + 32 * ks + 8 * lg);
+            if (w < 4 * AB) {  // uniform; LDS reads only
+                const bf16x8 xa = gp_frag(b, 16 * ab_rb + lr, h, lg);
+                const bf16x8 wa = gp_frag(b, GP_ROWS + GATE_PATH_G0 + 16 * ab_cb + lr, h, lg);
                 accab = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, wa, accab, 0, 0, 0);
             }
         }
-    }
-    // the first W_g1 chunk streams in while stage 1 is written out
-    const lin_rsrc_t rw2 = lin_rsrc(p.w2, (size_t)p.Dv * GATE_PATH_G0 * 2);
-    constexpr int NC2 = GATE_PATH_G0 / GP_KC;  // chunks per round
-    constexpr int NWL2 = GP_ROUND * 8 / 512;   // W_g1 loads per thread per chunk
-    u32x4 r2[NWL2];
-    const auto issue2 = [&](int n0, int c) {
-        const uint32_t col = (uint32_t)c * GP_KC * 2 + piece;
+    });
+
+    // ---- stage 2: gate = g0 W_g1^T + b, 256 columns per round ----
+    const int nq = 4 * (p.Dv / GP_ROUND);  // chunk q: round q >> 2, k chunk q & 3
+    u32x4 r2[3][4];  // ring: W_g1 rows 256 (q >> 2) + 64 i + 8 w + r8 (rounds past Dv read zero)
+    const auto issue2 = [&](int q, u32x4 (&r)[4]) {
+        const int n0 = GP_ROUND * (q >> 2);
+        const uint32_t dead = ((uint32_t)(n0 - p.Dv) & LIN_DEAD) ^ LIN_DEAD;
+        const uint32_t col = ((uint32_t)(q & 3) * 128 + 16 * pl) | dead;
 #pragma unroll
-        for (int i = 0; i < NWL2; i++)
-            r2[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  rw2, (uint32_t)(n0 + ((tid + 512 * i) >> 3)) * (GATE_PATH_G0 * 2) + col,
-                                                  0, 0));
+        for (int i = 0; i < 4; i++)
+            r[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rw2, (uint32_t)(n0 + 64 * i + 8 * w + r8) * (GATE_PATH_G0 * 2) + col, 0, 0));
     };
-    const auto store2 = [&](int buf) {
-        char* ws = lds + L::W2 + buf * GP_ROUND * GP_LD * 2;
+    const auto store2 = [&](char* b, const u32x4 (&r)[4]) {
 #pragma unroll
-        for (int i = 0; i < NWL2; i++)
-            *reinterpret_cast<u32x4*>(ws + ((tid + 512 * i) >> 3) * GP_LD * 2 + piece) = r2[i];
+        for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4*>(b + (64 * i + 8 * w + r8) * 128 + ps) = r[i];
     };
-    issue2(0, 0);
-    // gates of the abd block: lane column 16 ab_cb + lr, rows 16 ab_rb + 4 lg + i
-    const lin_rsrc_t rab = lin_rsrc(p.abd_bias, (size_t)3 * H * 2);
-    const int acol = 16 * ab_cb + lr, ah = acol % H, akind = acol / H;
-    const float abias = bf16_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(rab, (uint32_t)acol * 2, 0, 0));
-    const float adt = p.dt_bias[ah], aal = p.A_log[ah];  // ah < H for every lane
-    __syncthreads();  // stage-1 tiles done with: g0 overwrites them
-    bf16_t* g0s = reinterpret_cast<bf16_t*>(lds + L::G0);
+    issue2(0, r2[0]);
+    issue2(1, r2[1]);
+    issue2(2, r2[2]);
+    __syncthreads();  // every wave is done with the stage-1 buffers
+    // g0 in bf16 into buf[1] (row r: 512 bytes, four lines of 64 k)
+    char* g0b = buf[1];
 #pragma unroll
     for (int rb = 0; rb < 4; rb++)
 #pragma unroll
         for (int cb = 0; cb < 2; cb++)
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                g0s[(16 * rb + 4 * lg + i) * GP_G0LD + 32 * w + 16 * cb + lr] = (bf16_t)acc[rb][cb][i];
-    if (has_ab && acol < 3 * H) {
+            for (int i = 0; i < 4; i++) {
+                const int row = 16 * rb + 4 * lg + i, col = 32 * w + 16 * cb + lr;
+                *reinterpret_cast<bf16_t*>(g0b + row * 512 + (col >> 6) * 128 + 16 * (((col >> 3) & 7) ^ (row & 7)) +
+                                           2 * (col & 7)) = (bf16_t)acc[rb][cb][i];
+            }
+    // the gates of the abd block: lane column 16 ab_cb + lr, rows 16 ab_rb + 4 lg + i
+    if (w < 4 * AB && acol < 3 * H) {
         float* dst = akind == 0 ? p.g : akind == 1 ? p.beta : p.delta;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -559,64 +591,69 @@ __global__ __launch_bounds__(512) void gate_path_kernel(GatePathParams p) {
             if (row < mrows) dst[(size_t)(m0 + row) * H + ah] = akind == 0 ? decay_gate(v + adt, aal) : sigmoidf(v);
         }
     }
-
-    // ---- stage 2: gate = g0 W_g1^T + b, 256 columns per round ----
-    const lin_rsrc_t rb2 = lin_rsrc(p.b2, p.b2 ? (size_t)p.Dv * 2 : 0);
-    for (int n0 = 0; n0 < p.Dv; n0 += GP_ROUND) {
-        f32x4 acc2[4][2];
+    store2(buf[0], r2[0]);
+    issue2(3, r2[0]);
+    __syncthreads();  // g0 and the first W_g1 chunk in LDS
+    // gf[rb][ks] = g0[16 rb + lr][32 ks + 8 lg .. + 7]
+    bf16x8 gf[4][GATE_PATH_G0 / 32];
 #pragma unroll
-        for (int rb = 0; rb < 4; rb++) acc2[rb][0] = acc2[rb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-        float bias[2];  // loaded ahead of the round's later chunks (loads complete in order)
+    for (int rb = 0; rb < 4; rb++)
 #pragma unroll
-        for (int cb = 0; cb < 2; cb++)
-            bias[cb] = bf16_bits_to_float(
-                __builtin_amdgcn_raw_buffer_load_b16(rb2, (uint32_t)(n0 + 32 * w + 16 * cb + lr) * 2, 0, 0));
-        for (int c = 0; c < NC2; c++) {
-            store2(c & 1);
-            __syncthreads();  // (first chunk: g0 complete too)
-            if (c + 1 < NC2)
-                issue2(n0, c + 1);
-            else if (n0 + GP_ROUND < p.Dv)
-                issue2(n0 + GP_ROUND, 0);  // the next round's first chunk
-            const bf16_t* ws = reinterpret_cast<const bf16_t*>(lds + L::W2 + (c & 1) * GP_ROUND * GP_LD * 2);
+        for (int ks = 0; ks < GATE_PATH_G0 / 32; ks++) {
+            const int R = 16 * rb + lr;
+            gf[rb][ks] =
+                *reinterpret_cast<const bf16x8*>(g0b + R * 512 + (ks >> 1) * 128 + 16 * ((4 * (ks & 1) + lg) ^ (R & 7)));
+        }
+    f32x4 acc2[4][2];
+    char* ot = sot + w * 1024;
+    gp_unrolled<0, GP_MAX_Q>(nq, [&](auto qq) {
+        constexpr int q = decltype(qq)::value, kq = q & 3;
+        // chunk q is in buf[q & 1]; buf[(q + 1) & 1] (for q = 0: g0) is read by no one
+        if constexpr (q > 0) __syncthreads();
+        const char* b = buf[q & 1];
+        if constexpr (q == 0) {
+            __syncthreads();  // every wave holds its g0 operands
+        }
+        store2(buf[(q + 1) & 1], r2[(q + 1) % 3]);
+        issue2(q + 4, r2[(q + 1) % 3]);
+        if constexpr (kq == 0) {
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                bf16x8 xf[4], wf[2];
+            for (int rb = 0; rb < 4; rb++) acc2[rb][0] = acc2[rb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
-                for (int rb = 0; rb < 4; rb++)
-                    xf[rb] = *reinterpret_cast<const bf16x8*>(g0s + (16 * rb + lr) * GP_G0LD + GP_KC * c + 32 * ks +
-                                                              8 * lg);
+        for (int h = 0; h < 2; h++) {
+            bf16x8 wf[2];
+#pragma unroll
+            for (int cb = 0; cb < 2; cb++) wf[cb] = gp_frag(b, 32 * w + 16 * cb + lr, h, lg);
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++)
 #pragma unroll
                 for (int cb = 0; cb < 2; cb++)
-                    wf[cb] =
-                        *reinterpret_cast<const bf16x8*>(ws + (32 * w + 16 * cb + lr) * GP_LD + 32 * ks + 8 * lg);
+                    acc2[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gf[rb][2 * kq + h], wf[cb], acc2[rb][cb], 0, 0, 0);
+        }
+        if constexpr (kq == 3) {  // the round's 64 x 32 tile, 16 rows at a time through the wave's LDS region
+            constexpr int rd = q >> 2;
+            const int n0 = GP_ROUND * rd + 32 * w;
+            float bias[2];
 #pragma unroll
-                for (int rb = 0; rb < 4; rb++)
+            for (int cb = 0; cb < 2; cb++) bias[cb] = (float)sbias[n0 + 16 * cb + lr];
 #pragma unroll
-                    for (int cb = 0; cb < 2; cb++)
-                        acc2[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[rb], wf[cb], acc2[rb][cb], 0, 0, 0);
+            for (int rb = 0; rb < 4; rb++) {
+#pragma unroll
+                for (int cb = 0; cb < 2; cb++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        *reinterpret_cast<bf16_t*>(ot + (4 * lg + i) * 64 + 2 * (16 * cb + lr)) =
+                            (bf16_t)(acc2[rb][cb][i] + bias[cb]);
+                // a wave's LDS accesses complete in order; the compiler keeps these in order too
+                asm volatile("" ::: "memory");
+                const int row = 16 * rb + (lane >> 2);
+                const u32x4 v = *reinterpret_cast<const u32x4*>(ot + (lane >> 2) * 64 + 16 * (lane & 3));
+                asm volatile("" ::: "memory");
+                if (row < mrows) *reinterpret_cast<u32x4*>(p.gate + (size_t)(m0 + row) * p.ldg + n0 + 8 * (lane & 3)) = v;
             }
         }
-        __syncthreads();  // the round's W_g1 chunks done with: the out tile overwrites them
-        bf16_t* ot = reinterpret_cast<bf16_t*>(lds + L::W2);
-#pragma unroll
-        for (int rb = 0; rb < 4; rb++)
-#pragma unroll
-            for (int cb = 0; cb < 2; cb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    ot[(16 * rb + 4 * lg + i) * GP_OLD + 32 * w + 16 * cb + lr] = (bf16_t)(acc2[rb][cb][i] + bias[cb]);
-        __syncthreads();
-        // 64 rows x 32 pieces of 16 bytes
-#pragma unroll
-        for (int i = 0; i < GP_ROWS * (GP_ROUND / 8) / 512; i++) {
-            const int idx = tid + 512 * i, row = idx >> 5, pc = idx & 31;
-            if (row < mrows)
-                *reinterpret_cast<u32x4*>(p.gate + (size_t)(m0 + row) * p.ldg + n0 + 8 * pc) =
-                    *reinterpret_cast<const u32x4*>(ot + row * GP_OLD + 8 * pc);
-        }
-        __syncthreads();  // the out tile read before the next round's chunks land
-    }
+    });
 }
 
 // Causal depthwise convolution over time (layers/cyfa.py:138-233):
@@ -937,7 +974,9 @@ int launch_argmax_rows(const bf16_t* x, long long ldx, int rows, int n, long lon
 
 int launch_gate_path(const GatePathParams& p, hipStream_t stream) {
     const int ab = (3 * p.H + 15) / 16;
-    if (p.M < 1 || p.K < GP_KC || p.K % GP_KC || p.H < 1 || ab > 2 || p.Dv < GP_ROUND || p.Dv % GP_ROUND) return -1;
+    if (p.M < 1 || p.K < 64 || p.K % 64 || p.K > GATE_PATH_MAX_K || p.H < 1 || ab > 2 || p.Dv < GP_ROUND ||
+        p.Dv % GP_ROUND || p.Dv > GATE_PATH_MAX_DV)
+        return -1;
     // every buffer the kernel reads spans less than 2^31 bytes (32-bit offsets, LIN_DEAD unused here)
     const unsigned long long xspan = ((unsigned long long)(min(p.M, GP_ROWS) - 1) * p.ldx + p.K) * 2;
     if ((unsigned long long)(GATE_PATH_G0 + 3 * p.H) * p.K * 2 >= LIN_DEAD || xspan >= LIN_DEAD ||

@@ -568,6 +568,7 @@ def silu_mul(gu):
 
 
 GATE_PATH_G0 = 256
+GATE_PATH_MAX = 2048  # largest K and Dv cyfa_gate_path takes
 
 
 def gate_path_ok(x, w1, w2, b2, H):
@@ -575,8 +576,8 @@ def gate_path_ok(x, w1, w2, b2, H):
     K = x.shape[-1]
     return (x.is_cuda and x.dtype == torch.bfloat16 and w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16
             and (b2 is None or b2.dtype == torch.bfloat16) and not torch.is_grad_enabled()
-            and K % 64 == 0 and 3 * H <= 32 and w1.shape == (GATE_PATH_G0 + 3 * H, K)
-            and w2.shape[1] == GATE_PATH_G0 and w2.shape[0] % 256 == 0)
+            and K % 64 == 0 and K <= GATE_PATH_MAX and 3 * H <= 32 and w1.shape == (GATE_PATH_G0 + 3 * H, K)
+            and w2.shape[1] == GATE_PATH_G0 and w2.shape[0] % 256 == 0 and w2.shape[0] <= GATE_PATH_MAX)
 
 
 def gate_path(x, w1, abd_bias, w2, b2, dt_bias, A_log, H):

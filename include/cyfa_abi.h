@@ -308,8 +308,9 @@ int cyfa_norm_linear_rows(const CyfaLinearArgs *args, const CyfaRowNormArgs *nor
  *   gate = bf16(g0 W_g1^T + b_g1)
  * with fp32 accumulation and the roundings of the separate projections (the
  * summation order differs from a library GEMM's, so a value can differ from
- * theirs in the last bit). K a multiple of 64, 3H <= 32, Dv a multiple of 256,
- * g_proj[0] 256 wide. No reference counterpart as one entry point. */
+ * theirs in the last bit). K a multiple of 64 up to 2048, 3H <= 32, Dv a
+ * multiple of 256 up to 2048, g_proj[0] 256 wide. No reference counterpart as
+ * one entry point. */
 typedef struct CyfaGatePathArgs {
     int M, K, H, Dv;
     const void *x;                /* bf16 [M, K], rows ldx elements apart, 16-byte aligned */
