@@ -63,7 +63,7 @@ BYTES_PER_TOKEN_HEAD = 2 * 256 * 4 + 12 + 2 * 256
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
 # scaled by a 1 GiB copy kernel (profiles/cyfa_chunk_fwd_cfg3_prefill.md,
 # profiles/cyfa_decode_step_cfg4.md); they apply to the default shapes.
-TRAFFIC_PREFILL_BYTES = 343.2e6    # one cyfa_chunk_fwd_normed at B=8, T=2048, H=4
+TRAFFIC_PREFILL_BYTES = 337.0e6    # one cyfa_chunk_fwd_normed at B=8, T=2048, H=4 (248.3 MB read + 88.7 MB written)
 TRAFFIC_DECODE_BYTES = 135.5e6     # one decode launch at B=64, H=4
 TRAFFIC_LAYER_STEP_BYTES = 138.1e6  # one cyfa_decode_layer_step at B=64, H=4 (69.6 MB read + 68.5 MB written)
 
