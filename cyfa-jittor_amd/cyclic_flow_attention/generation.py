@@ -45,8 +45,13 @@ def generate(model, ids, max_new_tokens=64, eos_token_id=None, temperature=0.0, 
         result = model(torch.tensor([current], dtype=torch.long, device=dev), cache=cache, use_cache=True)
         cache = result["cache"]
         last = result["logits"][0, -1]
-        scores = last.double().cpu().numpy()
-        token = int(scores.argmax()) if temperature == 0 else _nucleus(scores, temperature, top_p, rng)
+        if temperature == 0:
+            # greedy: the first largest logit, found on the device (one index
+            # crosses to the host, not the row); NaN counts as largest, as in
+            # numpy's argmax of the same values
+            token = int(last.argmax())
+        else:
+            token = _nucleus(last.double().cpu().numpy(), temperature, top_p, rng)
         generated.append(token)
         if on_token is not None and on_token(generated):
             break
