@@ -82,9 +82,15 @@ size_t cyfa_chunk_workspace_bytes(int B, int T, int H, int K, int V, int M, int 
 }
 
 int cyfa_readout_table(const float* readout, float* table, int H, int M, void* hip_stream) {
-    if (M != 128) return fail(CYFA_ERR_UNSUPPORTED, "cyfa_readout_table: num_slots must be 128, got %d", M);
+    if (M < 4 || M > 256 || M % 2)
+        return fail(CYFA_ERR_UNSUPPORTED, "cyfa_readout_table: num_slots must be even and in [4, 256], got %d", M);
     if (H <= 0) return fail(CYFA_ERR_VALUE, "cyfa_readout_table: H must be positive, got %d", H);
     if (!readout || !table) return fail(CYFA_ERR_VALUE, "cyfa_readout_table: null pointer");
+    if (M != 128) {  // the general path's table (any even M)
+        if (cyfa::launch_general_table(readout, table, H, M, (hipStream_t)hip_stream) != 0)
+            return fail(CYFA_ERR_UNSUPPORTED, "cyfa_readout_table: launch refused");
+        return check_launch("cyfa_readout_table");
+    }
     if (cyfa::launch_readout_table(readout, table, H, (hipStream_t)hip_stream) != 0)
         return fail(CYFA_ERR_UNSUPPORTED, "cyfa_readout_table: launch refused");
     return check_launch("cyfa_readout_table");
@@ -577,3 +583,129 @@ int cyfa_gates(const void* abd, long long abd_row, const float* dt_bias, const f
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// The general-shape path (cyfa_general.hip).
+
+size_t cyfa_chunk_general_workspace_bytes(int B, int T, int H, int K, int V, int M, int C) {
+    if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || M <= 0 || C <= 0) return 0;
+    return cyfa::general_workspace(B, T, H, K, V, M, C, nullptr).bytes;
+}
+
+namespace {
+
+// Shape limits of the general path, shared by the chunk and decode entries.
+int general_shape(const char* fn, int B, int H, int K, int V, int M, int dtype) {
+    if (dtype != CYFA_DTYPE_BF16 && dtype != CYFA_DTYPE_F32)
+        return fail(CYFA_ERR_VALUE, "%s: dtype must be CYFA_DTYPE_BF16 or CYFA_DTYPE_F32, got %d", fn, dtype);
+    if (B <= 0 || H <= 0) return fail(CYFA_ERR_VALUE, "%s: B=%d H=%d must be positive", fn, B, H);
+    if (K < 1 || K > 1024 || V < 1 || V > 1024)
+        return fail(CYFA_ERR_UNSUPPORTED, "%s: head dims K=%d V=%d must lie in [1, 1024]", fn, K, V);
+    if (M < 4 || M > 256 || M % 2)
+        return fail(CYFA_ERR_UNSUPPORTED, "%s: num_slots must be even and in [4, 256], got %d", fn, M);
+    return 0;
+}
+
+}  // namespace
+
+int cyfa_chunk_fwd_general(const CyfaChunkArgs* a, int dtype, void* hip_stream) {
+    const char* fn = "cyfa_chunk_fwd_general";
+    if (!a) return fail(CYFA_ERR_VALUE, "%s: null args", fn);
+    if (int rc = general_shape(fn, a->B, a->H, a->K, a->V, a->M, dtype)) return rc;
+    if (a->T <= 0) return fail(CYFA_ERR_VALUE, "%s: T=%d must be positive", fn, a->T);
+    if (!(a->C == 16 || a->C == 32 || a->C == 64))
+        return fail(CYFA_ERR_UNSUPPORTED, "%s: chunk_size must be 16, 32 or 64, got %d", fn, a->C);
+    if (!a->q || !a->k || !a->v || !a->g || !a->delta || !a->beta || !a->table || !a->q_norm_weight ||
+        !a->k_norm_weight || !a->o)
+        return fail(CYFA_ERR_VALUE, "%s: null required pointer", fn);
+    if (!(a->scale > 0.f) || !isfinite(a->scale))
+        return fail(CYFA_ERR_VALUE, "%s: scale must be positive and finite, got %g", fn, (double)a->scale);
+    const bool has_h0 = a->h0_k != nullptr;
+    if (has_h0 != (a->h0_v != nullptr) || has_h0 != (a->clock0 != nullptr))
+        return fail(CYFA_ERR_VALUE, "%s: h0_k, h0_v and clock0 must be all set or all null", fn);
+    const bool has_out = a->hk != nullptr;
+    if (has_out != (a->hv != nullptr) || has_out != (a->clock != nullptr))
+        return fail(CYFA_ERR_VALUE, "%s: hk, hv and clock must be all set or all null", fn);
+    // the kernels index rows (b, h, padded t) and their elements with 32-bit counts
+    const size_t Tp = (size_t)(a->T + a->C - 1) / a->C * a->C, rows = (size_t)a->B * a->H * Tp;
+    if (rows * 256 >= ((size_t)1 << 31))
+        return fail(CYFA_ERR_UNSUPPORTED, "%s: B * H * padded T = %zu rows is too many", fn, rows);
+    const size_t need = cyfa::general_workspace(a->B, a->T, a->H, a->K, a->V, a->M, a->C, nullptr).bytes;
+    if (!a->workspace || a->workspace_bytes < need)
+        return fail(CYFA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, got %zu", fn, need,
+                    a->workspace ? a->workspace_bytes : (size_t)0);
+    if (!aligned(a->workspace, 256)) return fail(CYFA_ERR_ALIGN, "%s: workspace needs 256-byte alignment", fn);
+    cyfa::GenChunkParams g{};
+    g.B = a->B;
+    g.T = a->T;
+    g.H = a->H;
+    g.K = a->K;
+    g.V = a->V;
+    g.M = a->M;
+    g.C = a->C;
+    g.bf16 = dtype == CYFA_DTYPE_BF16;
+    g.q = a->q;
+    g.k = a->k;
+    g.v = a->v;
+    g.g = a->g;
+    g.delta = a->delta;
+    g.beta = a->beta;
+    g.table = a->table;
+    g.q_w = a->q_norm_weight;
+    g.k_w = a->k_norm_weight;
+    g.q_eps = a->q_norm_eps;
+    g.k_eps = a->k_norm_eps;
+    g.scale = a->scale;
+    g.h0_k = a->h0_k;
+    g.h0_v = a->h0_v;
+    g.clock0 = a->clock0;
+    g.o = a->o;
+    g.hk = a->hk;
+    g.hv = a->hv;
+    g.clock = a->clock;
+    g.workspace = a->workspace;
+    if (cyfa::launch_general_chunk(g, (hipStream_t)hip_stream) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "%s: launch refused", fn);
+    return check_launch(fn);
+}
+
+int cyfa_decode_step_general(const CyfaDecodeArgs* a, int dtype, void* hip_stream) {
+    const char* fn = "cyfa_decode_step_general";
+    if (!a) return fail(CYFA_ERR_VALUE, "%s: null args", fn);
+    if (int rc = general_shape(fn, a->B, a->H, a->K, a->V, a->M, dtype)) return rc;
+    if (!a->q || !a->k || !a->v || !a->g || !a->delta || !a->beta || !a->table || !a->q_norm_weight ||
+        !a->k_norm_weight || !a->o || !a->hk_out || !a->hv_out || !a->clock_out)
+        return fail(CYFA_ERR_VALUE, "%s: null required pointer", fn);
+    const bool has_in = a->hk_in != nullptr;
+    if (has_in != (a->hv_in != nullptr) || has_in != (a->clock_in != nullptr))
+        return fail(CYFA_ERR_VALUE, "%s: hk_in, hv_in and clock_in must be all set or all null", fn);
+    if (!isfinite(a->scale)) return fail(CYFA_ERR_VALUE, "%s: scale must be finite", fn);
+    cyfa::GenDecodeParams p{};
+    p.B = a->B;
+    p.H = a->H;
+    p.K = a->K;
+    p.V = a->V;
+    p.M = a->M;
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.g = a->g;
+    p.delta = a->delta;
+    p.beta = a->beta;
+    p.table = a->table;
+    p.q_w = a->q_norm_weight;
+    p.k_w = a->k_norm_weight;
+    p.q_eps = a->q_norm_eps;
+    p.k_eps = a->k_norm_eps;
+    p.scale = a->scale;
+    p.hk_in = a->hk_in;
+    p.hv_in = a->hv_in;
+    p.clock_in = a->clock_in;
+    p.o = a->o;
+    p.hk_out = a->hk_out;
+    p.hv_out = a->hv_out;
+    p.clock_out = a->clock_out;
+    if (cyfa::launch_general_decode(p, dtype == CYFA_DTYPE_BF16, (hipStream_t)hip_stream) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "%s: launch refused", fn);
+    return check_launch(fn);
+}

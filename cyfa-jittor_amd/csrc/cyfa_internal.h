@@ -196,6 +196,77 @@ constexpr int GATE_PATH_G0 = 256;       // g_proj[0] width (head_v_dim) the kern
 constexpr int GATE_PATH_MAX_K = 2048;   // largest hidden size (its k-chunk loop is unrolled to this)
 constexpr int GATE_PATH_MAX_DV = 2048;  // largest H * head_v_dim (its column rounds, likewise)
 
+// The general-shape path (cyfa_general.hip): any K, V <= 1024, even M in
+// [4, 256], C in {16, 32, 64}, bf16 or fp32 q, k, v.
+struct GenSglaParams {
+    const float *q, *k, *v;  // head-major [B, H, Tp, Kq | Vd] fp32
+    const float* g;          // [B, T, H] natural-log gate (tokens past T: zero)
+    int B, T, Tp, H, Kq, Vd;
+    float scale;
+    const float* s0;  // nullable [B, H, Kq, Vd]
+    void* out;        // head-major fp32 [B, H, Tp, Vd], or [B, T, H, Vd] in the input dtype (out_bthd)
+    int out_bthd;
+    float* s_final;  // nullable [B, H, Kq, Vd]
+};
+
+struct GenChunkParams {
+    int B, T, H, K, V, M, C, bf16;
+    const void *q, *k, *v;
+    const float *g, *delta, *beta, *table, *q_w, *k_w;
+    float q_eps, k_eps, scale;
+    const float *h0_k, *h0_v, *clock0;
+    void* o;
+    float *hk, *hv, *clock;
+    void* workspace;
+};
+
+struct GenDecodeParams {
+    int B, H, K, V, M;
+    const void *q, *k, *v;
+    const float *g, *delta, *beta, *table, *q_w, *k_w;
+    float q_eps, k_eps, scale;
+    const float *hk_in, *hv_in, *clock_in;
+    void* o;
+    float *hk_out, *hv_out, *clock_out;
+};
+
+// The general chunk path's workspace: per (b, h, padded token) row the clock
+// (f64), q_hat and k_hat (K), v (V), the write vector, the pass-1 output and
+// the slot weights (M each) and the phases' cosines and sines (M / 2 each),
+// all fp32, each region 256-byte aligned. With base == nullptr only the size.
+struct GenWorkspace {
+    double* lam;
+    float *qh, *kh, *vh, *w, *cs, *sn, *raw, *wts;
+    size_t bytes;
+};
+
+inline GenWorkspace general_workspace(int B, int T, int H, int K, int V, int M, int C, void* base) {
+    const size_t Tp = (size_t)(T + C - 1) / C * C, rows = (size_t)B * H * Tp;
+    char* p = static_cast<char*>(base);
+    size_t off = 0;
+    const auto take = [&](size_t bytes) {
+        char* r = p ? p + off : nullptr;
+        off += (bytes + 255) / 256 * 256;
+        return r;
+    };
+    GenWorkspace w;
+    w.lam = reinterpret_cast<double*>(take(rows * 8));
+    w.qh = reinterpret_cast<float*>(take(rows * K * 4));
+    w.kh = reinterpret_cast<float*>(take(rows * K * 4));
+    w.vh = reinterpret_cast<float*>(take(rows * V * 4));
+    w.w = reinterpret_cast<float*>(take(rows * M * 4));
+    w.cs = reinterpret_cast<float*>(take(rows * (M / 2) * 4));
+    w.sn = reinterpret_cast<float*>(take(rows * (M / 2) * 4));
+    w.raw = reinterpret_cast<float*>(take(rows * M * 4));
+    w.wts = reinterpret_cast<float*>(take(rows * M * 4));
+    w.bytes = off;
+    return w;
+}
+
+int launch_general_table(const float* readout, float* table, int H, int M, hipStream_t stream);
+int launch_general_chunk(const GenChunkParams& p, hipStream_t stream);
+int launch_general_decode(const GenDecodeParams& p, int bf16, hipStream_t stream);
+
 int launch_rms_norm(const NormParams& p, hipStream_t stream);
 int launch_linear_rows(const LinearParams& p, hipStream_t stream);
 int launch_short_conv(const ConvParams& p, hipStream_t stream);

@@ -14,7 +14,7 @@ import torch
 import torch.nn.functional as F
 
 LIB_PATH = Path(os.environ.get("CYFA_LIB", Path(__file__).with_name("libcyfa_hip.so")))
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 CYFA_OK = 0
 CYFA_ERR_VALUE = -1
@@ -145,6 +145,9 @@ SIGNATURES = {
     "cyfa_gates": (_c_int, [_c_void_p, ctypes.c_longlong, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                             _c_int, _c_int, _c_void_p]),
     "cyfa_gate_path": (_c_int, [ctypes.POINTER(CyfaGatePathArgs), _c_void_p]),
+    "cyfa_chunk_general_workspace_bytes": (_c_size_t, [_c_int] * 7),
+    "cyfa_chunk_fwd_general": (_c_int, [ctypes.POINTER(CyfaChunkArgs), _c_int, _c_void_p]),
+    "cyfa_decode_step_general": (_c_int, [ctypes.POINTER(CyfaDecodeArgs), _c_int, _c_void_p]),
     "cyfa_last_error": (ctypes.c_char_p, []),
     "cyfa_abi_version": (_c_int, []),
 }
@@ -308,6 +311,35 @@ def decode_step(args: CyfaDecodeArgs, device):
     rc = _timed("cyfa_decode_step", lambda: lib.cyfa_decode_step(ctypes.byref(args), stream_handle(device)))
     if rc != CYFA_OK:
         _raise(rc, "cyfa_decode_step failed")
+
+
+CYFA_DTYPE_BF16, CYFA_DTYPE_F32 = 0, 1
+
+
+def general_dtype(x):
+    """The general path's element type for q, k, v of this dtype: bf16 stays
+    bf16; fp16 and fp32 run as fp32 (the caller converts fp16)."""
+    return CYFA_DTYPE_BF16 if x.dtype == torch.bfloat16 else CYFA_DTYPE_F32
+
+
+def chunk_general_workspace_bytes(B, T, H, K, V, M, C):
+    return int(load_library().cyfa_chunk_general_workspace_bytes(B, T, H, K, V, M, C))
+
+
+def chunk_fwd_general(args: CyfaChunkArgs, dtype, device):
+    lib = load_library()
+    rc = _timed("cyfa_chunk_fwd_general",
+                lambda: lib.cyfa_chunk_fwd_general(ctypes.byref(args), dtype, stream_handle(device)))
+    if rc != CYFA_OK:
+        _raise(rc, "cyfa_chunk_fwd_general failed")
+
+
+def decode_step_general(args: CyfaDecodeArgs, dtype, device):
+    lib = load_library()
+    rc = _timed("cyfa_decode_step_general",
+                lambda: lib.cyfa_decode_step_general(ctypes.byref(args), dtype, stream_handle(device)))
+    if rc != CYFA_OK:
+        _raise(rc, "cyfa_decode_step_general failed")
 
 
 def decode_layer_step(args: CyfaDecodeArgs, layer: CyfaDecodeLayerArgs, device):

@@ -41,9 +41,14 @@ def chunk_cyfa(
 
     Inputs q, k and v use [batch, time, heads, channels]; g, delta and beta use
     [batch, time, heads]. The readout has [heads, slots-1, slots-1]. Returns
-    the output ([batch, time, heads, V], in q's dtype; bf16, fp16 and fp32 q, k,
-    v run the bf16 kernels) and, when requested,
+    the output ([batch, time, heads, V], in q's dtype) and, when requested,
     (key_state [B,H,K,M], value_state [B,H,M,V], clock [B,H]), all fp32.
+    K = V = 256 with 128 slots and chunk_size 64 run the tuned kernels (fp16
+    and fp32 q, k, v rounded to bf16 for them); every other shape (K, V <=
+    1024, an even slot count up to 256, chunk_size 16, 32 or 64) runs the
+    general path, cyfa_chunk_fwd_general, which computes in fp32 (bf16
+    operands rounded where the reference casts; fp16 and fp32 operands in
+    fp32), like the reference's unfused fallback (ops/chunk.py:285-331).
     ``table`` (keyword only, not in the reference signature) is a precomputed
     readout @ Phi [H, M-1, M] fp32; when None it is formed from ``readout``.
     ``output_norm`` (keyword only, an extension) is ``(weight [V], gate
@@ -70,7 +75,13 @@ def chunk_cyfa(
             raise ValueError(f"{name} must have shape {(B, T, H)}, got {tuple(x.shape)}")
     out_dtype = _operand_dtype("chunk_cyfa", q, k, v)
     dev = _native.require_device(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, table, *state_in)
-    q, k, v = (x.to(torch.bfloat16).contiguous() for x in (q, k, v))
+    # the tuned kernels' shape; any other shape takes the general path, in
+    # bf16 for bf16 operands and in fp32 for fp16 and fp32 ones
+    fast = K == 256 and V == 256 and M == 128 and chunk_size == 64
+    if not fast and (output_norm is not None or no_alloc):
+        raise NotImplementedError("output_norm and no_alloc need K = V = 256, 128 slots and chunk_size 64")
+    io_dtype = torch.bfloat16 if fast or out_dtype == torch.bfloat16 else torch.float32
+    q, k, v = (x.to(io_dtype).contiguous() for x in (q, k, v))
     g, delta, beta = (x.to(torch.float32).contiguous() for x in (g, delta, beta))
     qw = q_norm_weight.to(torch.float32).contiguous()
     kw = k_norm_weight.to(torch.float32).contiguous()
@@ -84,7 +95,7 @@ def chunk_cyfa(
             raise ValueError("initial_state must be (hk [B,H,K,M], hv [B,H,M,V], clock [B,H])")
     else:
         h0k = h0v = c0 = None
-    o = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=dev)
+    o = torch.empty(B, T, H, V, dtype=io_dtype, device=dev)
     if output_final_state:
         hk = torch.empty(B, H, K, M, dtype=torch.float32, device=dev)
         hv = torch.empty(B, H, M, V, dtype=torch.float32, device=dev)
@@ -94,7 +105,8 @@ def chunk_cyfa(
     if no_alloc:
         ws_bytes, workspace = 0, None
     else:
-        ws_bytes = _native.chunk_workspace_bytes(B, T, H, K, V, M, chunk_size)
+        ws_bytes = (_native.chunk_workspace_bytes(B, T, H, K, V, M, chunk_size) if fast else
+                    _native.chunk_general_workspace_bytes(B, T, H, K, V, M, chunk_size))
         workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)  # alive until the launch
     args = _native.CyfaChunkArgs(
         B=B, T=T, H=H, K=K, V=V, M=M, C=chunk_size,
@@ -107,7 +119,9 @@ def chunk_cyfa(
         o=o.data_ptr(), hk=_native.ptr(hk), hv=_native.ptr(hv), clock=_native.ptr(clock),
         workspace=_native.ptr(workspace), workspace_bytes=ws_bytes,
     )
-    if output_norm is None:
+    if not fast:
+        _native.chunk_fwd_general(args, _native.general_dtype(q), dev)
+    elif output_norm is None:
         if no_alloc:
             _native.chunk_fwd_noalloc(args, None, dev)
         else:
@@ -128,7 +142,7 @@ def chunk_cyfa(
             _native.chunk_fwd_noalloc(args, norm, dev)
         else:
             _native.chunk_fwd_normed(args, norm, dev)
-    if out_dtype != torch.bfloat16:
+    if out_dtype != io_dtype:
         o = o.to(out_dtype)
     return o, ((hk, hv, clock) if output_final_state else None)
 

@@ -2,7 +2,8 @@
 
 Keeps the reference's signature, checks and return convention
 (ops/fused_recurrent.py:10-200 of Chyxx/CyFA-Jittor v0.1.2). One call runs one
-fused HBM-streaming kernel, ``cyfa_decode_step`` of libcyfa_hip.so.
+fused HBM-streaming kernel of libcyfa_hip.so: ``cyfa_decode_step`` at the tuned
+shapes, ``cyfa_decode_step_general`` at any other.
 """
 
 import torch
@@ -36,7 +37,11 @@ def fused_recurrent_cyfa(
     """Decode one token using constant-size key, value and clock states.
 
     Uses the same input layout and return convention as chunk_cyfa (q, k, v
-    of bf16, fp16 or fp32, rounded to bf16 for the kernel; o in their dtype). The new
+    of bf16, fp16 or fp32; o in their dtype). K, V in {128, 256} with 128
+    slots run the tuned kernel (fp16 and fp32 operands rounded to bf16 for
+    it); every other shape up to K, V <= 1024 and 256 slots runs the general
+    step (cyfa_decode_step_general: bf16 operands in bf16, fp16 and fp32 in
+    fp32). The new
     states are returned as new tensors; ``inplace=True`` (an extension) updates
     the given initial_state tensors instead and returns them. ``table`` (an
     extension) passes a precomputed readout @ Phi to skip rebuilding it.
@@ -63,7 +68,11 @@ def fused_recurrent_cyfa(
     out_dtype = _operand_dtype("fused_recurrent_cyfa", q, k, v)
     state_in = tuple(initial_state) if initial_state is not None else ()
     dev = _native.require_device(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, table, *state_in)
-    q, k, v = (x.to(torch.bfloat16).contiguous() for x in (q, k, v))
+    # the tuned kernel's shapes; any other shape takes the general step, in
+    # bf16 for bf16 operands and in fp32 for fp16 and fp32 ones
+    fast = K in (128, 256) and V in (128, 256) and M == 128
+    io_dtype = torch.bfloat16 if fast or out_dtype == torch.bfloat16 else torch.float32
+    q, k, v = (x.to(io_dtype).contiguous() for x in (q, k, v))
     g, delta, beta = (x.to(torch.float32).contiguous() for x in (g, delta, beta))
     qw = q_norm_weight.to(torch.float32).contiguous()
     kw = k_norm_weight.to(torch.float32).contiguous()
@@ -89,8 +98,8 @@ def fused_recurrent_cyfa(
         hk_out = torch.empty(B, H, K, M, dtype=torch.float32, device=dev)
         hv_out = torch.empty(B, H, M, V, dtype=torch.float32, device=dev)
         c_out = torch.empty(B, H, dtype=torch.float32, device=dev)
-    o = torch.empty(B, 1, H, V, dtype=torch.bfloat16, device=dev)
-    workspace = _native.decode_workspace(B, H, K, V, dev) if split else None  # alive until the launch
+    o = torch.empty(B, 1, H, V, dtype=io_dtype, device=dev)
+    workspace = _native.decode_workspace(B, H, K, V, dev) if split and fast else None  # alive until the launch
     args = _native.CyfaDecodeArgs(
         B=B, H=H, K=K, V=V, M=M,
         workspace=_native.ptr(workspace), workspace_bytes=0 if workspace is None else workspace.numel(),
@@ -102,8 +111,11 @@ def fused_recurrent_cyfa(
         hk_in=_native.ptr(hk_in), hv_in=_native.ptr(hv_in), clock_in=_native.ptr(c_in),
         o=o.data_ptr(), hk_out=hk_out.data_ptr(), hv_out=hv_out.data_ptr(), clock_out=c_out.data_ptr(),
     )
-    _native.decode_step(args, dev)
-    if out_dtype != torch.bfloat16:
+    if fast:
+        _native.decode_step(args, dev)
+    else:
+        _native.decode_step_general(args, _native.general_dtype(q), dev)
+    if out_dtype != io_dtype:
         o = o.to(out_dtype)
     return o, ((hk_out, hv_out, c_out) if output_final_state else None)
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define CYFA_ABI_VERSION 6
+#define CYFA_ABI_VERSION 7
 
 enum {
     CYFA_OK = 0,
@@ -212,8 +212,31 @@ int cyfa_decode_layer_step(const CyfaDecodeArgs *args, const CyfaDecodeLayerArgs
 
 /* table[h] = readout[h] @ Phi, with Phi the real-DFT slot basis [M-1, M].
  * Replaces _basis + jt.matmul (ops/chunk.py:82-103, 281;
- * ops/fused_recurrent.py:53). readout f32 [H, M-1, M-1]; table f32 [H, M-1, M]. */
+ * ops/fused_recurrent.py:53). readout f32 [H, M-1, M-1]; table f32 [H, M-1, M];
+ * M even in [4, 256]. */
 int cyfa_readout_table(const float *readout, float *table, int H, int M, void *hip_stream);
+
+/* Element type of q, k, v and o in the general-shape entry points. */
+enum { CYFA_DTYPE_BF16 = 0, CYFA_DTYPE_F32 = 1 };
+
+/* Workspace bytes of cyfa_chunk_fwd_general (0 for a non-positive argument). */
+size_t cyfa_chunk_general_workspace_bytes(int B, int T, int H, int K, int V, int M, int C);
+
+/* The chunkwise forward for shapes outside cyfa_chunk_fwd's (the
+ * reference's unfused fallback: _scalar_la, the affine scan over chunks, the
+ * modal readout and _rotate, ops/chunk.py:115-161, 285-331 and
+ * ops/utils.py:98-226, 779-929): K and V in [1, 1024], M even in [4, 256],
+ * C in {16, 32, 64}; q, k, v and o of `dtype` (bf16 or fp32), everything else
+ * as for cyfa_chunk_fwd. Computes in fp32; bf16 inputs are rounded to bf16
+ * where the reference casts to the input dtype. Plain kernels without matrix
+ * cores: no model configuration takes this path. */
+int cyfa_chunk_fwd_general(const CyfaChunkArgs *args, int dtype, void *hip_stream);
+
+/* One decode step for shapes outside cyfa_decode_step's, up to the
+ * reference's decode limits (ops/fused_recurrent.py:45-46): K and V in
+ * [1, 1024], M even in [4, 256]; q, k, v and o of `dtype`; states fp32; the
+ * workspace fields are ignored. One workgroup per (b, h). */
+int cyfa_decode_step_general(const CyfaDecodeArgs *args, int dtype, void *hip_stream);
 
 /* ---- Layer-side kernels around the op (layers/cyfa.py, modeling_cyfa.py) ---- */
 

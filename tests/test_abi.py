@@ -76,7 +76,42 @@ def test_unsupported_shapes_fail_before_launch():
     assert lib.cyfa_chunk_fwd(ctypes.byref(args), None) == _native.CYFA_ERR_VALUE  # null pointers
     dargs = _native.CyfaDecodeArgs(B=1, H=1, K=512, V=256, M=128)
     assert lib.cyfa_decode_step(ctypes.byref(dargs), None) == _native.CYFA_ERR_UNSUPPORTED
-    assert lib.cyfa_readout_table(None, None, 1, 64, None) == _native.CYFA_ERR_UNSUPPORTED
+    assert lib.cyfa_readout_table(None, None, 1, 63, None) == _native.CYFA_ERR_UNSUPPORTED  # odd slot count
+    assert lib.cyfa_readout_table(None, None, 1, 258, None) == _native.CYFA_ERR_UNSUPPORTED
+    assert lib.cyfa_readout_table(None, None, 1, 64, None) == _native.CYFA_ERR_VALUE  # the general table's M
+
+
+def test_general_path_checks_fail_before_launch():
+    """cyfa_chunk_fwd_general / cyfa_decode_step_general refuse what the
+    general kernels do not take, and a short workspace, before any launch."""
+    lib = _native.load_library()
+    bf, f32 = _native.CYFA_DTYPE_BF16, _native.CYFA_DTYPE_F32
+    dummy = 256  # a nonzero pointer value; nothing is dereferenced before the checks fail
+    args = _native.CyfaChunkArgs(B=1, T=100, H=2, K=128, V=64, M=64, C=32, scale=0.1)
+    for name in ("q", "k", "v", "g", "delta", "beta", "table", "q_norm_weight", "k_norm_weight", "o"):
+        setattr(args, name, dummy)
+    need = lib.cyfa_chunk_general_workspace_bytes(1, 100, 2, 128, 64, 64, 32)
+    Tp = 128  # 100 tokens padded to chunks of 32
+    assert need >= 2 * 128 * (8 + 4 * (2 * 128 + 64 + 4 * 64))
+    assert lib.cyfa_chunk_general_workspace_bytes(0, 100, 2, 128, 64, 64, 32) == 0
+    assert lib.cyfa_chunk_fwd_general(ctypes.byref(args), bf, None) == _native.CYFA_ERR_WORKSPACE
+    args.workspace, args.workspace_bytes = 4096, need - 1
+    assert lib.cyfa_chunk_fwd_general(ctypes.byref(args), bf, None) == _native.CYFA_ERR_WORKSPACE
+    assert lib.cyfa_chunk_fwd_general(ctypes.byref(args), 7, None) == _native.CYFA_ERR_VALUE
+    for field, bad in (("M", 63), ("M", 258), ("K", 2048), ("V", 0), ("C", 48)):
+        old = getattr(args, field)
+        setattr(args, field, bad)
+        assert lib.cyfa_chunk_fwd_general(ctypes.byref(args), f32, None) == _native.CYFA_ERR_UNSUPPORTED, field
+        setattr(args, field, old)
+    args.o = None
+    assert lib.cyfa_chunk_fwd_general(ctypes.byref(args), bf, None) == _native.CYFA_ERR_VALUE
+    args.o, args.hk = dummy, dummy  # final states all or none
+    assert lib.cyfa_chunk_fwd_general(ctypes.byref(args), bf, None) == _native.CYFA_ERR_VALUE
+    assert Tp % args.C == 0
+    dargs = _native.CyfaDecodeArgs(B=1, H=1, K=2048, V=64, M=64)
+    assert lib.cyfa_decode_step_general(ctypes.byref(dargs), bf, None) == _native.CYFA_ERR_UNSUPPORTED
+    dargs.K = 512
+    assert lib.cyfa_decode_step_general(ctypes.byref(dargs), bf, None) == _native.CYFA_ERR_VALUE  # null pointers
 
 
 def test_python_ops_reject_like_the_reference():
