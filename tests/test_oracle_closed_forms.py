@@ -160,3 +160,54 @@ def test_coherent_inputs_drive_the_readout_past_fp16():
     assert torch.isnan(torch.softmax(logits, -1)).any()
     logits_bf16 = torch.einsum("bhtm,hrm->bhtr", z.to(torch.bfloat16).double(), table)
     assert torch.isfinite(torch.softmax(logits_bf16, -1)).all()
+
+
+# The general-shape path runs the same oracle functions at other slot counts;
+# these pin them there by the same mathematics.
+GENERAL_M = [16, 64, 96, 256]
+
+
+@pytest.mark.parametrize("M", GENERAL_M)
+def test_basis_orthonormal_and_fft_any_slot_count(M):
+    Rg = M - 1
+    phi = O.basis(M)
+    assert phi.shape == (Rg, M) and torch.all(phi[:, 1] == 0)
+    torch.testing.assert_close(phi @ phi.T, torch.eye(Rg, dtype=torch.float64), atol=1e-12, rtol=0)
+    x = np.random.default_rng(M).standard_normal(Rg)
+    X = np.fft.fft(x)
+    sp = np.where(np.arange(M // 2) == 0, math.sqrt(1 / Rg), math.sqrt(2 / Rg))
+    expect = np.stack([sp * X[:M // 2].real, -sp * X[:M // 2].imag], axis=-1).reshape(M)
+    expect[1] = 0.0
+    np.testing.assert_allclose((phi.T @ torch.from_numpy(x)).numpy(), expect, atol=1e-12)
+
+
+def _u_matrix(d, M):
+    eye = torch.eye(M, dtype=torch.float64)
+    c, s = O.phase_cos_sin(torch.tensor([float(d)], dtype=torch.float64), M=M)
+    return O.rotate(eye, c.expand(M, M // 2), s.expand(M, M // 2)).T
+
+
+@pytest.mark.parametrize("M", GENERAL_M)
+@pytest.mark.parametrize("d", [1, 3, 200])
+def test_integer_clock_is_cyclic_roll_any_slot_count(M, d):
+    """U(d) for an integer clock moves slot r to slot r + d (mod R): the
+    phase's integer range reduction at this R."""
+    phi = O.basis(M)
+    expect = torch.from_numpy(np.roll(np.eye(M - 1), d, axis=0))
+    torch.testing.assert_close(phi @ _u_matrix(d, M) @ phi.T, expect, atol=1e-11, rtol=0)
+
+
+@pytest.mark.parametrize("M", GENERAL_M)
+def test_write_vector_and_readout_any_slot_count(M):
+    phi = O.basis(M)
+    beta = torch.tensor([0.3, 1.0], dtype=torch.float64)
+    w0 = O.write_vector(torch.zeros(2, dtype=torch.float64), beta, M=M)
+    torch.testing.assert_close(w0, beta[:, None] * phi[0][None, :], atol=1e-14, rtol=0)
+    lam = torch.tensor([0.37, 12.5, 999.9], dtype=torch.float64)
+    w = O.write_vector(lam, torch.full_like(lam, 0.7), M=M)
+    c, s = O.phase_cos_sin(lam, M=M)
+    torch.testing.assert_close(w, 0.7 * O.rotate(phi[0].expand(3, M), c, s, negative=True), atol=1e-12, rtol=0)
+    # at a zero clock the readout is softmax(raw Phi^T) Phi
+    raw = torch.randn(1, 1, 3, M, dtype=torch.float64, generator=torch.Generator().manual_seed(M))
+    weights = O.slot_readout(raw, torch.zeros(1, 1, 3, dtype=torch.float64), phi[None])
+    torch.testing.assert_close(weights, torch.softmax(raw @ phi.T, dim=-1) @ phi, atol=1e-14, rtol=0)
