@@ -166,7 +166,7 @@ struct LinearParams {
     //   with the row scale applied to the fp32 product
     const float* norm_weight;     // nullable: x is used as given (unless norm_folded)
     int norm_folded;
-    const __bf16* norm_residual;  // nullable [M, K], rows ldr elements apart
+    const __bf16* norm_residual;  // nullable [M, K], rows ldr elements apart (launch_linear_rows forms s first)
     __bf16* norm_sum_out;         // [M, K], rows ldr apart; set with norm_residual; aliases no input
     long long ldr;
     float norm_eps;

@@ -245,10 +245,15 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
         // columns in every tile shape. Its sum of squares runs over its
         // k-steps in order, then over the row's four lanes (xor 16, xor 32)
         // and the eight waves in wave order.
-        // x and the norm weight first, then W, then (when given) the residual:
-        // loads complete in order, so the norm waits for x while W streams in.
-        const bool res = p.norm_residual != nullptr;
-        u32x4 rawx[P][2 * RT], rawr[P][2 * RT], raww[P][2 * CT];
+        // x and the norm weight first, then W: loads complete in order, so the
+        // norm waits for x while W streams in. With four or more pairs (K =
+        // 2048) only the first PW pairs of W are issued here and the rest once
+        // x is in registers: all of a wave's run in flight at once takes more
+        // than 128 VGPRs, and then one workgroup fits a CU instead of two (at
+        // one row, the 1.4B model's gate|up launch of 352 workgroups ran in
+        // two rounds on 256 CUs).
+        constexpr int PW = P >= 4 ? P / 2 : P;
+        u32x4 rawx[P][2 * RT], raww[P][2 * CT];
 #pragma unroll
         for (int h = 0; h < P; h++) lin_load_pair<RT>(rx, xrs, s0 + 2 * h, s1, lane, rawx[h]);
         // the norm weight: K <= 2048, one float4 per thread (zero past K)
@@ -257,54 +262,23 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
             nwv = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                                                  lin_rsrc(p.norm_weight, (size_t)p.K * 4), 16 * threadIdx.x, 0, 0));
 #pragma unroll
-        for (int h = 0; h < P; h++) lin_load_pair<CT>(rw, wrs, s0 + 2 * h, s1, lane, raww[h]);
-        if (res) {
-            const lin_rsrc_t rr =
-                lin_rsrc(p.norm_residual + (size_t)m0 * p.ldr, ((size_t)(mrows - 1) * p.ldr + p.K) * 2);
-#pragma unroll
-            for (int h = 0; h < P; h++) lin_load_pair<RT>(rr, (uint32_t)p.ldr * 2, s0 + 2 * h, s1, lane, rawr[h]);
-        }
-        bf16x8 xf[U][RT], rf[U][RT];
+        for (int h = 0; h < PW; h++) lin_load_pair<CT>(rw, wrs, s0 + 2 * h, s1, lane, raww[h]);
+        // Every pair is staged, also one past the run (its loads read zero):
+        // with the staging under the run's test, the compiler moved the loads
+        // of the first pair behind that branch and waited there for every
+        // load in flight, W included.
+        bf16x8 xf[U][RT];
 #pragma unroll
         for (int h = 0; h < P; h++) {
-            if (s0 + 2 * h < s1) {
-                lin_stage_pair<RT>(xreg, lane, rawx[h]);
+            lin_stage_pair<RT>(xreg, lane, rawx[h]);
 #pragma unroll
-                for (int u = 0; u < 2; u++)
-                    if (s0 + 2 * h + u < s1)
+            for (int u = 0; u < 2; u++)
+                if (s0 + 2 * h + u < s1)
 #pragma unroll
-                        for (int rt = 0; rt < RT; rt++) xf[2 * h + u][rt] = lin_frag(xreg, rt, u, lr, lg);
-            }
+                    for (int rt = 0; rt < RT; rt++) xf[2 * h + u][rt] = lin_frag(xreg, rt, u, lr, lg);
         }
-        if (res) {
 #pragma unroll
-            for (int h = 0; h < P; h++) {
-                if (s0 + 2 * h < s1) {
-                    lin_stage_pair<RT>(xreg, lane, rawr[h]);
-#pragma unroll
-                    for (int u = 0; u < 2; u++)
-                        if (s0 + 2 * h + u < s1)
-#pragma unroll
-                            for (int rt = 0; rt < RT; rt++) rf[2 * h + u][rt] = lin_frag(xreg, rt, u, lr, lg);
-                }
-            }
-        }
-        if (res) {
-            // s = bf16(x + residual); the first column of workgroups writes it out
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                if (s0 + u < s1) {
-#pragma unroll
-                    for (int rt = 0; rt < RT; rt++) {
-#pragma unroll
-                        for (int e = 0; e < 8; e++) xf[u][rt][e] = (bf16_t)((float)xf[u][rt][e] + (float)rf[u][rt][e]);
-                        if (blockIdx.x == 0 && 16 * rt + lr < mrows)
-                            *reinterpret_cast<bf16x8*>(p.norm_sum_out + (size_t)(m0 + 16 * rt + lr) * p.ldr +
-                                                       32 * (s0 + u) + 8 * lg) = xf[u][rt];
-                    }
-                }
-            }
-        }
+        for (int h = PW; h < P; h++) lin_load_pair<CT>(rw, wrs, s0 + 2 * h, s1, lane, raww[h]);
         if constexpr (NM == 1) snw[threadIdx.x] = nwv;
         float ss[RT];
 #pragma unroll
@@ -844,6 +818,20 @@ __global__ __launch_bounds__(256) void gates_kernel(const bf16_t* abd, long long
     delta[i] = sigmoidf((float)row[2 * H + h]);
 }
 
+// s = bf16(x + residual) for the fused norm's rows (M rows of K columns, K a
+// multiple of 32), written to s rows ldr apart; one thread per 8 columns.
+__global__ __launch_bounds__(256) void add_rows_kernel(const bf16_t* x, long long ldx, const bf16_t* r, long long ldr,
+                                                       bf16_t* s, int K) {
+    const int c = 8 * (blockIdx.x * 256 + threadIdx.x), m = blockIdx.y;
+    if (c >= K) return;
+    const bf16x8 xv = *reinterpret_cast<const bf16x8*>(x + (size_t)m * ldx + c);
+    const bf16x8 rv = *reinterpret_cast<const bf16x8*>(r + (size_t)m * ldr + c);
+    bf16x8 sv;
+#pragma unroll
+    for (int e = 0; e < 8; e++) sv[e] = (bf16_t)((float)xv[e] + (float)rv[e]);
+    *reinterpret_cast<bf16x8*>(s + (size_t)m * ldr + c) = sv;
+}
+
 }  // namespace
 
 int launch_rms_norm(const NormParams& p, hipStream_t stream) {
@@ -910,7 +898,8 @@ static bool linear_tile(int M, int N, bool swiglu, int norm_k, int& rt_out, int&
     return best >= 0;
 }
 
-int launch_linear_rows(const LinearParams& p, hipStream_t stream) {
+int launch_linear_rows(const LinearParams& p_in, hipStream_t stream) {
+    LinearParams p = p_in;
     const bool norm = p.norm_weight != nullptr || p.norm_folded;
     if (p.M < 1 || p.M > 64 || (norm && p.K > LINEAR_NORM_MAX_K)) return -1;
     // every buffer the kernel reads spans less than LIN_DEAD bytes (so that
@@ -919,6 +908,16 @@ int launch_linear_rows(const LinearParams& p, hipStream_t stream) {
     if (p.K > (1 << 20) || span(p.ldx, p.K) >= LIN_DEAD || (p.add && span(p.ld_add, p.N) >= LIN_DEAD) ||
         (p.norm_residual && span(p.ldr, p.K) >= LIN_DEAD) || (p.bias && (unsigned long long)p.N * 2 >= LIN_DEAD))
         return -1;
+    if (norm && p.norm_residual) {
+        // s = bf16(x + residual) first, into norm_sum_out; the norm and the
+        // product then read s as x
+        hipLaunchKernelGGL(add_rows_kernel, dim3((p.K / 8 + 255) / 256, p.M), dim3(256), 0, stream, p.x, p.ldx,
+                           p.norm_residual, p.ldr, p.norm_sum_out, p.K);
+        p.x = p.norm_sum_out;
+        p.ldx = p.ldr;
+        p.norm_residual = nullptr;
+        p.norm_sum_out = nullptr;
+    }
     int rt, ct;
     if (!linear_tile(p.M, p.N, p.swiglu != 0, norm ? p.K : 0, rt, ct)) return -1;
     const dim3 grid((p.N + 16 * ct - 1) / (16 * ct), (p.M + 16 * rt - 1) / (16 * rt));
