@@ -709,3 +709,92 @@ int cyfa_decode_step_general(const CyfaDecodeArgs* a, int dtype, void* hip_strea
         return fail(CYFA_ERR_UNSUPPORTED, "%s: launch refused", fn);
     return check_launch(fn);
 }
+
+// ---------------------------------------------------------------------------
+// The backward pass of the chunk op (cyfa_backward.hip).
+
+size_t cyfa_chunk_bwd_workspace_bytes(int B, int T, int H, int K, int V, int M) {
+    if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || M <= 0) return 0;
+    return cyfa::bwd_workspace(B, T, H, K, V, M, nullptr).bytes;
+}
+
+int cyfa_chunk_bwd(const CyfaChunkArgs* a, int dtype, const CyfaChunkBwdArgs* d, void* hip_stream) {
+    const char* fn = "cyfa_chunk_bwd";
+    if (!a || !d) return fail(CYFA_ERR_VALUE, "%s: null args", fn);
+    if (dtype != CYFA_DTYPE_BF16 && dtype != CYFA_DTYPE_F32)
+        return fail(CYFA_ERR_VALUE, "%s: dtype must be CYFA_DTYPE_BF16 or CYFA_DTYPE_F32, got %d", fn, dtype);
+    if (a->B <= 0 || a->T <= 0 || a->H <= 0)
+        return fail(CYFA_ERR_VALUE, "%s: B=%d T=%d H=%d must be positive", fn, a->B, a->T, a->H);
+    if (a->K < 1 || a->K > 1024 || a->V < 1 || a->V > 1024)
+        return fail(CYFA_ERR_UNSUPPORTED, "%s: head dims K=%d V=%d must lie in [1, 1024]", fn, a->K, a->V);
+    if (a->M < 4 || a->M > cyfa::BWD_MAX_M || a->M % 2)
+        return fail(CYFA_ERR_UNSUPPORTED, "%s: num_slots must be even and in [4, %d], got %d", fn, cyfa::BWD_MAX_M,
+                    a->M);
+    if (!a->q || !a->k || !a->v || !a->g || !a->delta || !a->beta || !a->table || !a->q_norm_weight ||
+        !a->k_norm_weight)
+        return fail(CYFA_ERR_VALUE, "%s: null required forward input", fn);
+    if (!d->dq || !d->dk || !d->dv || !d->dg || !d->ddelta || !d->dbeta || !d->dtable || !d->dq_norm_weight ||
+        !d->dk_norm_weight)
+        return fail(CYFA_ERR_VALUE, "%s: null required gradient output", fn);
+    if (!(a->scale > 0.f) || !isfinite(a->scale))
+        return fail(CYFA_ERR_VALUE, "%s: scale must be positive and finite, got %g", fn, (double)a->scale);
+    const bool has_h0 = a->h0_k != nullptr;
+    if (has_h0 != (a->h0_v != nullptr) || has_h0 != (a->clock0 != nullptr))
+        return fail(CYFA_ERR_VALUE, "%s: h0_k, h0_v and clock0 must be all set or all null", fn);
+    const bool has_dh0 = d->dh0_k != nullptr;
+    if (has_dh0 != (d->dh0_v != nullptr) || has_dh0 != (d->dclock0 != nullptr))
+        return fail(CYFA_ERR_VALUE, "%s: dh0_k, dh0_v and dclock0 must be all set or all null", fn);
+    // the kernels index (b, h, padded t) rows and chunk states with 32-bit counts per row
+    const size_t Tp = (size_t)(a->T + 63) / 64 * 64, rows = (size_t)a->B * a->H * Tp;
+    if (rows * 1024 >= ((size_t)1 << 31))
+        return fail(CYFA_ERR_UNSUPPORTED, "%s: B * H * padded T = %zu rows is too many", fn, rows);
+    const size_t need = cyfa::bwd_workspace(a->B, a->T, a->H, a->K, a->V, a->M, nullptr).bytes;
+    if (!d->workspace || d->workspace_bytes < need)
+        return fail(CYFA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, got %zu", fn, need,
+                    d->workspace ? d->workspace_bytes : (size_t)0);
+    if (!aligned(d->workspace, 256)) return fail(CYFA_ERR_ALIGN, "%s: workspace needs 256-byte alignment", fn);
+    cyfa::BwdParams p{};
+    p.B = a->B;
+    p.T = a->T;
+    p.H = a->H;
+    p.K = a->K;
+    p.V = a->V;
+    p.M = a->M;
+    p.bf16 = dtype == CYFA_DTYPE_BF16;
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.d_o = d->d_o;
+    p.g = a->g;
+    p.delta = a->delta;
+    p.beta = a->beta;
+    p.table = a->table;
+    p.q_w = a->q_norm_weight;
+    p.k_w = a->k_norm_weight;
+    p.q_eps = a->q_norm_eps;
+    p.k_eps = a->k_norm_eps;
+    p.scale = a->scale;
+    p.h0_k = a->h0_k;
+    p.h0_v = a->h0_v;
+    p.clock0 = a->clock0;
+    p.d_hk = d->d_hk;
+    p.d_hv = d->d_hv;
+    p.d_clock = d->d_clock;
+    p.dq = d->dq;
+    p.dk = d->dk;
+    p.dv = d->dv;
+    p.dg = d->dg;
+    p.ddelta = d->ddelta;
+    p.dbeta = d->dbeta;
+    p.dtable = d->dtable;
+    p.dreadout = d->dreadout;
+    p.dq_w = d->dq_norm_weight;
+    p.dk_w = d->dk_norm_weight;
+    p.dh0_k = d->dh0_k;
+    p.dh0_v = d->dh0_v;
+    p.dclock0 = d->dclock0;
+    p.workspace = d->workspace;
+    if (cyfa::launch_chunk_bwd(p, (hipStream_t)hip_stream) != 0)
+        return fail(CYFA_ERR_UNSUPPORTED, "%s: launch refused", fn);
+    return check_launch(fn);
+}

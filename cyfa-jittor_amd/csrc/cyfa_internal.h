@@ -207,6 +207,7 @@ struct GenSglaParams {
     void* out;        // head-major fp32 [B, H, Tp, Vd], or [B, T, H, Vd] in the input dtype (out_bthd)
     int out_bthd;
     float* s_final;  // nullable [B, H, Kq, Vd]
+    float* states;   // nullable [B, H, Tp / C + 1, Kq, Vd]: the state before each chunk, then the final one
 };
 
 struct GenChunkParams {
@@ -263,8 +264,114 @@ inline GenWorkspace general_workspace(int B, int T, int H, int K, int V, int M, 
     return w;
 }
 
+// The forward recomputed for the backward pass (cyfa_general.hip), in fp32
+// with no intermediate rounding and the chunk length 64, from rows the caller
+// has already normalised: the clock, the write vector, pass 1 (keeping the
+// state before every chunk), the slot readout and pass 2 (likewise).
+struct GenRecomputeParams {
+    int B, T, Tp, H, K, V, M;
+    const float *qh, *kh, *vh;  // head-major [B*H, Tp, K | V]
+    const float *g, *delta, *beta, *table;
+    const float *clock0, *h0_k, *h0_v;  // nullable
+    float scale;
+    double* lam;                      // [B*H, Tp]
+    float *w, *cs, *sn, *raw, *wts;   // [B*H, Tp, M | M/2]
+    float *sk, *sv;                   // [B*H, Tp/64 + 1, K, M] and [B*H, Tp/64 + 1, M, V]
+    float* o;                         // head-major [B*H, Tp, V] (not used by the backward)
+};
+
+// The backward pass of the chunk op (cyfa_backward.hip): q, k, v and the
+// cotangent d_o are bf16 or fp32 (bf16 != 0 selects bf16), every other
+// tensor fp32; K, V <= 1024, an even M <= 128.
+struct BwdParams {
+    int B, T, H, K, V, M, bf16;
+    const void *q, *k, *v, *d_o;  // [B, T, H, K | V]; d_o nullable (zero)
+    const float *g, *delta, *beta, *table, *q_w, *k_w;
+    float q_eps, k_eps, scale;
+    const float *h0_k, *h0_v, *clock0;    // nullable
+    const float *d_hk, *d_hv, *d_clock;   // nullable cotangents of the final states
+    void *dq, *dk, *dv;                   // [B, T, H, K | V] in the operands' dtype
+    float *dg, *ddelta, *dbeta;           // [B, T, H]
+    float* dtable;                        // [H, M-1, M]
+    float* dreadout;                      // nullable [H, M-1, M-1]
+    float *dq_w, *dk_w;                   // [K]
+    float *dh0_k, *dh0_v, *dclock0;       // nullable
+    void* workspace;
+};
+constexpr int BWD_MAX_M = 128;
+
+// The backward pass's workspace (fp32 unless noted, each region 256-byte
+// aligned; rows = B*H*Tp head-major, Tp = T rounded up to 64, N = Tp / 64):
+// the recomputed forward (normalised rows and their norm factors, clock,
+// write vector and phases, pass-1 output, slot weights, the states before
+// every chunk of both passes) and the adjoints (cotangent rows, the state
+// cotangents before every chunk, the rows' cotangents of both passes, the
+// per-chunk boundary terms of the gate cotangent, per-block partial sums of
+// the table and norm-weight cotangents).
+struct BwdWorkspace {
+    double* lam;
+    float *qh, *kh, *rq, *rk, *vh, *w, *cs, *sn, *raw, *wts, *sk, *sv;
+    float *dO, *dsk, *dsv, *dwts, *dw2, *dvh, *draw, *dlam, *dqh, *dkh, *dw1, *bnd1, *bnd2, *dtab, *dnq, *dnk;
+    int N, nt1, nt2, ro_blocks, norm_blocks;
+    size_t bytes;
+};
+constexpr int BWD_RO_ROWS = 64;    // rows per readout-adjoint workgroup
+constexpr int BWD_NORM_ROWS = 64;  // rows per norm-adjoint workgroup
+
+inline BwdWorkspace bwd_workspace(int B, int T, int H, int K, int V, int M, void* base) {
+    const size_t Tp = (size_t)(T + 63) / 64 * 64, rows = (size_t)B * H * Tp, N = Tp / 64;
+    char* p = static_cast<char*>(base);
+    size_t off = 0;
+    const auto take = [&](size_t bytes) {
+        char* r = p ? p + off : nullptr;
+        off += (bytes + 255) / 256 * 256;
+        return r;
+    };
+    const auto f = [&](size_t n) { return reinterpret_cast<float*>(take(n * 4)); };
+    BwdWorkspace w;
+    w.N = (int)N;
+    w.nt1 = (M + 31) / 32;
+    w.nt2 = (V + 31) / 32;
+    w.ro_blocks = (int)((B * Tp + BWD_RO_ROWS - 1) / BWD_RO_ROWS);
+    w.norm_blocks = (int)(((size_t)B * T * H + BWD_NORM_ROWS - 1) / BWD_NORM_ROWS);
+    const size_t BH = (size_t)B * H;
+    w.lam = reinterpret_cast<double*>(take(rows * 8));
+    w.qh = f(rows * K);
+    w.kh = f(rows * K);
+    w.rq = f(rows);
+    w.rk = f(rows);
+    w.vh = f(rows * V);
+    w.w = f(rows * M);
+    w.cs = f(rows * (M / 2));
+    w.sn = f(rows * (M / 2));
+    w.raw = f(rows * M);
+    w.wts = f(rows * M);
+    w.sk = f(BH * (N + 1) * K * M);
+    w.sv = f(BH * (N + 1) * M * V);
+    w.dO = f(rows * V);
+    w.dsk = f(BH * (N + 1) * K * M);
+    w.dsv = f(BH * (N + 1) * M * V);
+    w.dwts = f(rows * M);
+    w.dw2 = f(rows * M);
+    w.dvh = f(rows * V);
+    w.draw = f(rows * M);
+    w.dlam = f(rows);
+    w.dqh = f(rows * K);
+    w.dkh = f(rows * K);
+    w.dw1 = f(rows * M);
+    w.bnd1 = f(BH * w.nt1 * N);
+    w.bnd2 = f(BH * w.nt2 * N);
+    w.dtab = f((size_t)H * w.ro_blocks * (M - 1) * M);
+    w.dnq = f((size_t)w.norm_blocks * K);
+    w.dnk = f((size_t)w.norm_blocks * K);
+    w.bytes = off;
+    return w;
+}
+
 int launch_general_table(const float* readout, float* table, int H, int M, hipStream_t stream);
 int launch_general_chunk(const GenChunkParams& p, hipStream_t stream);
+int launch_general_recompute(const GenRecomputeParams& p, hipStream_t stream);
+int launch_chunk_bwd(const BwdParams& p, hipStream_t stream);
 int launch_general_decode(const GenDecodeParams& p, int bf16, hipStream_t stream);
 
 int launch_rms_norm(const NormParams& p, hipStream_t stream);

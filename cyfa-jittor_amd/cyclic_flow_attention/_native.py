@@ -14,7 +14,7 @@ import torch
 import torch.nn.functional as F
 
 LIB_PATH = Path(os.environ.get("CYFA_LIB", Path(__file__).with_name("libcyfa_hip.so")))
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 CYFA_OK = 0
 CYFA_ERR_VALUE = -1
@@ -35,6 +35,18 @@ class CyfaChunkArgs(ctypes.Structure):
         ("q_norm_eps", _c_float), ("k_norm_eps", _c_float), ("scale", _c_float),
         ("h0_k", _c_void_p), ("h0_v", _c_void_p), ("clock0", _c_void_p),
         ("o", _c_void_p), ("hk", _c_void_p), ("hv", _c_void_p), ("clock", _c_void_p),
+        ("workspace", _c_void_p), ("workspace_bytes", _c_size_t),
+    ]
+
+
+class CyfaChunkBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("d_o", _c_void_p), ("d_hk", _c_void_p), ("d_hv", _c_void_p), ("d_clock", _c_void_p),
+        ("dq", _c_void_p), ("dk", _c_void_p), ("dv", _c_void_p),
+        ("dg", _c_void_p), ("ddelta", _c_void_p), ("dbeta", _c_void_p),
+        ("dtable", _c_void_p), ("dreadout", _c_void_p),
+        ("dq_norm_weight", _c_void_p), ("dk_norm_weight", _c_void_p),
+        ("dh0_k", _c_void_p), ("dh0_v", _c_void_p), ("dclock0", _c_void_p),
         ("workspace", _c_void_p), ("workspace_bytes", _c_size_t),
     ]
 
@@ -148,6 +160,8 @@ SIGNATURES = {
     "cyfa_chunk_general_workspace_bytes": (_c_size_t, [_c_int] * 7),
     "cyfa_chunk_fwd_general": (_c_int, [ctypes.POINTER(CyfaChunkArgs), _c_int, _c_void_p]),
     "cyfa_decode_step_general": (_c_int, [ctypes.POINTER(CyfaDecodeArgs), _c_int, _c_void_p]),
+    "cyfa_chunk_bwd_workspace_bytes": (_c_size_t, [_c_int] * 6),
+    "cyfa_chunk_bwd": (_c_int, [ctypes.POINTER(CyfaChunkArgs), _c_int, ctypes.POINTER(CyfaChunkBwdArgs), _c_void_p]),
     "cyfa_last_error": (ctypes.c_char_p, []),
     "cyfa_abi_version": (_c_int, []),
 }
@@ -332,6 +346,18 @@ def chunk_fwd_general(args: CyfaChunkArgs, dtype, device):
                 lambda: lib.cyfa_chunk_fwd_general(ctypes.byref(args), dtype, stream_handle(device)))
     if rc != CYFA_OK:
         _raise(rc, "cyfa_chunk_fwd_general failed")
+
+
+def chunk_bwd_workspace_bytes(B, T, H, K, V, M):
+    return int(load_library().cyfa_chunk_bwd_workspace_bytes(B, T, H, K, V, M))
+
+
+def chunk_bwd(args: CyfaChunkArgs, dtype, grads: CyfaChunkBwdArgs, device):
+    lib = load_library()
+    rc = _timed("cyfa_chunk_bwd",
+                lambda: lib.cyfa_chunk_bwd(ctypes.byref(args), dtype, ctypes.byref(grads), stream_handle(device)))
+    if rc != CYFA_OK:
+        _raise(rc, "cyfa_chunk_bwd failed")
 
 
 def decode_step_general(args: CyfaDecodeArgs, dtype, device):

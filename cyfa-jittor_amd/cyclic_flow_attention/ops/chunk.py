@@ -4,8 +4,10 @@ Keeps the reference's signature, argument meaning and error behaviour
 (ops/chunk.py:164-353 of Chyxx/CyFA-Jittor v0.1.2); the whole computation --
 q/k RMS norm, clock scan, write vector, both ScalarGatedLA passes, the fused
 slot readout and the final states -- runs inside ``cyfa_chunk_fwd`` of
-libcyfa_hip.so. Forward only: the reference's autograd adjoints are out of
-scope here, so gradients raise.
+libcyfa_hip.so. With inputs that require a gradient the op is an autograd
+function whose backward is ``cyfa_chunk_bwd`` (the reference's adjoints:
+ops/chunk.py:51-71, ops/chunk_bwd.py, ops/chunk_readout.py:13-621,
+ops/utils.py:589-754, ops/qk_norm.py:241-289).
 """
 
 import torch
@@ -58,13 +60,44 @@ def chunk_cyfa(
     ``no_alloc`` (keyword only, an extension) runs cyfa_chunk_fwd_noalloc: the
     intermediates live in the library's per-device scratch array instead of
     a workspace allocated here (calls on one GPU must not overlap).
+
+    When grad mode is on and q, k, v, g, delta, beta, the readout, a norm
+    weight or an initial state requires a gradient, the call is recorded for
+    autograd: the forward runs as above and the backward (cyfa_chunk_bwd)
+    returns the gradients of all of them (slot counts up to 128; ``table``,
+    ``output_norm`` and ``no_alloc`` are inference-only).
     """
     if cu_seqlens is not None:
         raise NotImplementedError("packed layout requires native segment dispatch")
     if checkpoint_level != 0:
         raise NotImplementedError("only saved-activation training is implemented")
     state_in = tuple(initial_state) if initial_state is not None else ()
-    check_forward_only("chunk_cyfa", (q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight) + state_in)
+    tracked = (q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight) + state_in
+    if torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in tracked):
+        if table is not None or output_norm is not None or no_alloc:
+            raise NotImplementedError("chunk_cyfa: table, output_norm and no_alloc are inference-only; "
+                                      "call it under torch.no_grad() or drop them")
+        M = readout.shape[-1] + 1
+        if M > BWD_MAX_SLOTS:
+            raise NotImplementedError(f"chunk_cyfa: the backward pass supports up to {BWD_MAX_SLOTS} slots, got {M}")
+        h0k, h0v, c0 = state_in if state_in else (None, None, None)
+        o, hk, hv, clock = _ChunkCyFA.apply(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, h0k, h0v,
+                                            c0, float(q_norm_eps), float(k_norm_eps), scale, int(chunk_size))
+        return o, ((hk, hv, clock) if output_final_state else None)
+    return _chunk_forward(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, q_norm_eps, k_norm_eps,
+                          scale, initial_state, output_final_state, chunk_size, table, output_norm, no_alloc)
+
+
+# Largest slot count of the backward pass (its readout adjoint keeps the
+# head's table and the table's gradient on chip).
+BWD_MAX_SLOTS = 128
+
+
+def _chunk_forward(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, q_norm_eps, k_norm_eps, scale,
+                   initial_state, output_final_state, chunk_size, table, output_norm, no_alloc):
+    """The forward op: the tuned kernels at K = V = 256, 128 slots and chunk
+    size 64, the general path at every other shape (see chunk_cyfa)."""
+    state_in = tuple(initial_state) if initial_state is not None else ()
     B, T, H, K = q.shape
     V = v.shape[-1]
     M = readout.shape[-1] + 1
@@ -145,6 +178,88 @@ def chunk_cyfa(
     if out_dtype != io_dtype:
         o = o.to(out_dtype)
     return o, ((hk, hv, clock) if output_final_state else None)
+
+
+class _ChunkCyFA(torch.autograd.Function):
+    """chunk_cyfa as an autograd function: the HIP forward, and the
+    gradients of every floating input from cyfa_chunk_bwd, which recomputes
+    the forward in fp32 from the saved inputs (so nothing but the inputs is
+    kept between the passes). Replaces the reference's jt.Function adjoints
+    behind chunk_cyfa (ops/chunk.py:51-71; ops/chunk_readout.py:776-786,
+    976-988; ops/utils.py:297-299, 589-641, 704-754; ops/qk_norm.py:241-289)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, h0k, h0v, c0, q_eps, k_eps,
+                scale, chunk_size):
+        init = (h0k, h0v, c0) if h0k is not None else None
+        o, (hk, hv, clock) = _chunk_forward(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, q_eps,
+                                            k_eps, scale, init, True, chunk_size, None, None, False)
+        ctx.save_for_backward(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, h0k, h0v, c0)
+        ctx.eps = (q_eps, k_eps)
+        ctx.scale = scale
+        ctx.set_materialize_grads(False)
+        return o, hk, hv, clock
+
+    @staticmethod
+    def backward(ctx, d_o, d_hk, d_hv, d_clock):
+        q, k, v, g, delta, beta, readout, q_w, k_w, h0k, h0v, c0 = ctx.saved_tensors
+        B, T, H, K = q.shape
+        V = v.shape[-1]
+        M = readout.shape[-1] + 1
+        dev = q.device
+        io = torch.bfloat16 if q.dtype == torch.bfloat16 else torch.float32
+        f32 = torch.float32
+
+        def c(x, dt=f32):
+            return None if x is None else x.detach().to(dt).contiguous()
+
+        qc, kc, vc = c(q, io), c(k, io), c(v, io)
+        gc, dc, bc, qwc, kwc = c(g), c(delta), c(beta), c(q_w), c(k_w)
+        table = readout_table(readout.detach())
+        has_h0 = h0k is not None
+        h0kc, h0vc, c0c = c(h0k), c(h0v), c(c0)
+        d_oc = c(d_o, io)
+        d_hkc, d_hvc, d_clc = c(d_hk), c(d_hv), c(d_clock)
+
+        def empty(shape, dt=f32):
+            return torch.empty(shape, dtype=dt, device=dev)
+
+        dq, dk, dv = empty((B, T, H, K), io), empty((B, T, H, K), io), empty((B, T, H, V), io)
+        dg, ddelta, dbeta = empty((B, T, H)), empty((B, T, H)), empty((B, T, H))
+        dtable, dreadout = empty((H, M - 1, M)), empty((H, M - 1, M - 1))
+        dqw, dkw = empty((K,)), empty((K,))
+        dh0k = dh0v = dc0 = None
+        if has_h0:
+            dh0k, dh0v, dc0 = empty((B, H, K, M)), empty((B, H, M, V)), empty((B, H))
+        ws_bytes = _native.chunk_bwd_workspace_bytes(B, T, H, K, V, M)
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        q_eps, k_eps = ctx.eps
+        args = _native.CyfaChunkArgs(
+            B=B, T=T, H=H, K=K, V=V, M=M, C=64,
+            q=qc.data_ptr(), k=kc.data_ptr(), v=vc.data_ptr(),
+            g=gc.data_ptr(), delta=dc.data_ptr(), beta=bc.data_ptr(),
+            table=table.data_ptr(), q_norm_weight=qwc.data_ptr(), k_norm_weight=kwc.data_ptr(),
+            q_norm_eps=float(q_eps), k_norm_eps=float(k_eps),
+            scale=float(K**-0.5 if ctx.scale is None else ctx.scale),
+            h0_k=_native.ptr(h0kc), h0_v=_native.ptr(h0vc), clock0=_native.ptr(c0c),
+        )
+        grads = _native.CyfaChunkBwdArgs(
+            d_o=_native.ptr(d_oc), d_hk=_native.ptr(d_hkc), d_hv=_native.ptr(d_hvc), d_clock=_native.ptr(d_clc),
+            dq=dq.data_ptr(), dk=dk.data_ptr(), dv=dv.data_ptr(),
+            dg=dg.data_ptr(), ddelta=ddelta.data_ptr(), dbeta=dbeta.data_ptr(),
+            dtable=dtable.data_ptr(), dreadout=dreadout.data_ptr(),
+            dq_norm_weight=dqw.data_ptr(), dk_norm_weight=dkw.data_ptr(),
+            dh0_k=_native.ptr(dh0k), dh0_v=_native.ptr(dh0v), dclock0=_native.ptr(dc0),
+            workspace=workspace.data_ptr(), workspace_bytes=ws_bytes,
+        )
+        _native.chunk_bwd(args, _native.general_dtype(qc), grads, dev)
+
+        def like(grad, x):
+            return None if x is None or grad is None else grad.to(x.dtype)
+
+        return (like(dq, q), like(dk, k), like(dv, v), like(dg, g), like(ddelta, delta), like(dbeta, beta),
+                like(dreadout, readout), like(dqw, q_w), like(dkw, k_w), like(dh0k, h0k), like(dh0v, h0v),
+                like(dc0, c0), None, None, None, None)
 
 
 def _operand_dtype(what, *xs):

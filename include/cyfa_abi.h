@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define CYFA_ABI_VERSION 7
+#define CYFA_ABI_VERSION 8
 
 enum {
     CYFA_OK = 0,
@@ -237,6 +237,44 @@ int cyfa_chunk_fwd_general(const CyfaChunkArgs *args, int dtype, void *hip_strea
  * [1, 1024], M even in [4, 256]; q, k, v and o of `dtype`; states fp32; the
  * workspace fields are ignored. One workgroup per (b, h). */
 int cyfa_decode_step_general(const CyfaDecodeArgs *args, int dtype, void *hip_stream);
+
+/* ---- Backward pass of the chunk op ---- */
+
+/* Cotangents in and gradients out of cyfa_chunk_bwd. Layouts as for
+ * CyfaChunkArgs; dq, dk, dv take the operands' dtype, the rest is f32. */
+typedef struct CyfaChunkBwdArgs {
+    const void *d_o;              /* nullable (zero) cotangent of o [B,T,H,V] */
+    const float *d_hk;            /* nullable cotangent of the final key state   [B,H,K,M] */
+    const float *d_hv;            /* nullable cotangent of the final value state [B,H,M,V] */
+    const float *d_clock;         /* nullable cotangent of the final clock       [B,H] */
+    void *dq, *dk, *dv;           /* [B,T,H,K], [B,T,H,K], [B,T,H,V] */
+    float *dg, *ddelta, *dbeta;   /* [B,T,H] */
+    float *dtable;                /* [H,M-1,M]: gradient of the readout table */
+    float *dreadout;              /* nullable [H,M-1,M-1]: dtable @ Phi^T, the readout's gradient */
+    float *dq_norm_weight;        /* [K] */
+    float *dk_norm_weight;        /* [K] */
+    float *dh0_k, *dh0_v, *dclock0; /* gradients of the initial states: all three or none */
+    void *workspace;              /* device scratch, >= cyfa_chunk_bwd_workspace_bytes() */
+    size_t workspace_bytes;
+} CyfaChunkBwdArgs;
+
+/* Workspace bytes of cyfa_chunk_bwd (0 for a non-positive argument). */
+size_t cyfa_chunk_bwd_workspace_bytes(int B, int T, int H, int K, int V, int M);
+
+/* Gradients of the chunkwise CyFA op with respect to q, k, v, g, delta, beta,
+ * the readout table (and readout), both q/k norm weights and the initial
+ * states, given the cotangents of o and of the final states. `fwd` holds the
+ * forward call's inputs (its o, hk, hv, clock and workspace fields are not
+ * read; its C is ignored: the backward works in 64-token chunks); q, k, v
+ * and d_o are of `dtype` (bf16 or fp32). K and V in [1, 1024], M even in
+ * [4, 128]. The forward is recomputed in fp32 without intermediate rounding,
+ * so the gradients are those of the op's exact arithmetic. Replaces the
+ * autograd adjoints behind chunk_cyfa: ScalarAttention.grad / scalar_grad
+ * (ops/chunk.py:51-71, ops/chunk_bwd.py:1008-1041), FirstReadout*.grad
+ * (ops/chunk_readout.py:13-621, 776-786, 976-988), PhaseWrite.grad and
+ * ClockScan.grad (ops/utils.py:297-299, 589-641, 704-754), HeadRMSNorm.grad
+ * (ops/qk_norm.py:241-289) and the table matmul's (ops/chunk.py:281). */
+int cyfa_chunk_bwd(const CyfaChunkArgs *fwd, int dtype, const CyfaChunkBwdArgs *bwd, void *hip_stream);
 
 /* ---- Layer-side kernels around the op (layers/cyfa.py, modeling_cyfa.py) ---- */
 

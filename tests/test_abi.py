@@ -51,7 +51,8 @@ def _c_layout(tmp_path, struct, fields):
                                       (_native.CyfaNormArgs, "CyfaNormArgs"),
                                       (_native.CyfaConvArgs, "CyfaConvArgs"),
                                       (_native.CyfaLinearArgs, "CyfaLinearArgs"),
-                                      (_native.CyfaRowNormArgs, "CyfaRowNormArgs")])
+                                      (_native.CyfaRowNormArgs, "CyfaRowNormArgs"),
+                                      (_native.CyfaChunkBwdArgs, "CyfaChunkBwdArgs")])
 def test_struct_layout_matches_header(tmp_path, cls, name):
     fields = [f for f, _ in cls._fields_]
     got = [ctypes.sizeof(cls)] + [getattr(cls, f).offset for f in fields]
@@ -112,6 +113,57 @@ def test_general_path_checks_fail_before_launch():
     assert lib.cyfa_decode_step_general(ctypes.byref(dargs), bf, None) == _native.CYFA_ERR_UNSUPPORTED
     dargs.K = 512
     assert lib.cyfa_decode_step_general(ctypes.byref(dargs), bf, None) == _native.CYFA_ERR_VALUE  # null pointers
+
+
+def test_backward_checks_fail_before_launch():
+    """cyfa_chunk_bwd refuses what its kernels do not take, missing outputs and
+    a short workspace, before any launch."""
+    lib = _native.load_library()
+    bf = _native.CYFA_DTYPE_BF16
+    dummy = 256  # a nonzero pointer value; nothing is dereferenced before the checks fail
+    args = _native.CyfaChunkArgs(B=2, T=100, H=2, K=256, V=256, M=128, C=64, scale=0.0625)
+    for name in ("q", "k", "v", "g", "delta", "beta", "table", "q_norm_weight", "k_norm_weight"):
+        setattr(args, name, dummy)
+    grads = _native.CyfaChunkBwdArgs()
+    for name in ("dq", "dk", "dv", "dg", "ddelta", "dbeta", "dtable", "dq_norm_weight", "dk_norm_weight"):
+        setattr(grads, name, dummy)
+    need = lib.cyfa_chunk_bwd_workspace_bytes(2, 100, 2, 256, 256, 128)
+    rows, chunks = 2 * 2 * 128, 2
+    # at least the saved states of both passes and their cotangents
+    assert need >= 4 * 4 * (2 * 2 * (chunks + 1) * 256 * 128) + 4 * rows * (2 * 256 + 256)
+    assert lib.cyfa_chunk_bwd_workspace_bytes(0, 100, 2, 256, 256, 128) == 0
+    assert lib.cyfa_chunk_bwd(ctypes.byref(args), bf, ctypes.byref(grads), None) == _native.CYFA_ERR_WORKSPACE
+    grads.workspace, grads.workspace_bytes = 4096, need - 1
+    assert lib.cyfa_chunk_bwd(ctypes.byref(args), bf, ctypes.byref(grads), None) == _native.CYFA_ERR_WORKSPACE
+    assert lib.cyfa_chunk_bwd(ctypes.byref(args), 7, ctypes.byref(grads), None) == _native.CYFA_ERR_VALUE
+    for field, bad in (("M", 130), ("M", 63), ("K", 2048), ("V", 0)):
+        old = getattr(args, field)
+        setattr(args, field, bad)
+        assert lib.cyfa_chunk_bwd(ctypes.byref(args), bf, ctypes.byref(grads), None) == _native.CYFA_ERR_UNSUPPORTED
+        setattr(args, field, old)
+    grads.dtable = None
+    assert lib.cyfa_chunk_bwd(ctypes.byref(args), bf, ctypes.byref(grads), None) == _native.CYFA_ERR_VALUE
+    grads.dtable, grads.dh0_k = dummy, dummy  # initial-state gradients all or none
+    assert lib.cyfa_chunk_bwd(ctypes.byref(args), bf, ctypes.byref(grads), None) == _native.CYFA_ERR_VALUE
+    grads.dh0_k = None
+    args.scale = 0.0
+    assert lib.cyfa_chunk_bwd(ctypes.byref(args), bf, ctypes.byref(grads), None) == _native.CYFA_ERR_VALUE
+
+
+def test_python_backward_refusals():
+    """What the backward does not cover is refused when the graph is built."""
+    from cyclic_flow_attention.ops import chunk_cyfa
+
+    q = torch.zeros(1, 2, 1, 256, dtype=torch.bfloat16, requires_grad=True)
+    g = torch.zeros(1, 2, 1)
+    w = torch.ones(256)
+    with pytest.raises(NotImplementedError):  # 256 slots: beyond the backward's 128
+        chunk_cyfa(q, q, q, g, g, g, torch.eye(255)[None], w, w)
+    ro = torch.eye(127)[None]
+    with pytest.raises(NotImplementedError):  # a precomputed table is inference-only
+        chunk_cyfa(q, q, q, g, g, g, ro, w, w, table=torch.zeros(1, 127, 128))
+    with pytest.raises(ValueError):  # CPU tensors: the HIP path has no CPU fallback, with or without grad
+        chunk_cyfa(q, q, q, g, g, g, ro, w, w)
 
 
 def test_python_ops_reject_like_the_reference():

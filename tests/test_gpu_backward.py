@@ -1,0 +1,155 @@
+"""GPU parity of the chunk op's backward pass (cyfa_chunk_bwd through
+chunk_cyfa's autograd function) against float64 autograd through the CPU
+oracle's exact mode.
+
+The reference gates its gradients by relative RMS error against another
+backend: < 0.01 for q, k, v and the table, < 0.02 for g, delta and beta
+(benchmarks/core.py:565-580). Those are the bars for bf16 operands here,
+whose gradients dq, dk, dv are returned in bf16 (a 2^-9 rounding alone is
+about 2e-3 rrms). The backward recomputes the forward in fp32 without
+intermediate rounding, so with fp32 operands every gradient must match the
+float64 gradient to rrms 1e-3.
+"""
+
+import pytest
+import torch
+
+from cyclic_flow_attention.ops import chunk_cyfa
+from oracle import cyfa_oracle as O
+from tolerance import metrics
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+NAMES = ("q", "k", "v", "g", "delta", "beta", "readout", "q_norm_weight", "k_norm_weight")
+GATE_NAMES = ("g", "delta", "beta")
+
+
+def _bar(name, dtype):
+    if dtype == torch.float32:
+        return 1e-3
+    return 0.02 if name in GATE_NAMES else 0.01
+
+
+def _inputs(B, T, H, K, V, M, seed, dtype, state):
+    gen = torch.Generator().manual_seed(seed)
+    R = M - 1
+    x = dict(
+        q=torch.randn(B, T, H, K, generator=gen),
+        k=torch.randn(B, T, H, K, generator=gen),
+        v=torch.randn(B, T, H, V, generator=gen),
+        g=torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=gen) + 3),
+        delta=torch.sigmoid(torch.randn(B, T, H, generator=gen)),
+        beta=torch.sigmoid(torch.randn(B, T, H, generator=gen)),
+        readout=torch.eye(R).expand(H, R, R) + 0.05 * torch.randn(H, R, R, generator=gen),
+        q_norm_weight=1 + 0.1 * torch.randn(K, generator=gen),
+        k_norm_weight=1 + 0.1 * torch.randn(K, generator=gen),
+    )
+    for name in ("q", "k", "v"):
+        x[name] = x[name].to(dtype)
+    init = None
+    if state:
+        init = (0.3 * torch.randn(B, H, K, M, generator=gen), 0.3 * torch.randn(B, H, M, V, generator=gen),
+                50.0 * torch.rand(B, H, generator=gen))
+    cot = dict(
+        o=torch.randn(B, T, H, V, generator=gen).to(dtype),
+        hk=torch.randn(B, H, K, M, generator=gen),
+        hv=torch.randn(B, H, M, V, generator=gen),
+        clock=torch.randn(B, H, generator=gen),
+    )
+    return x, init, cot
+
+
+def _loss(o, st, cot, with_state):
+    loss = (o.double() * cot["o"].double().to(o.device)).sum()
+    if with_state:
+        hk, hv, clock = st
+        dev = hk.device
+        loss = loss + (hk.double() * cot["hk"].double().to(dev)).sum() + (hv.double() * cot["hv"].double().to(dev)).sum()
+        loss = loss + (clock.double() * cot["clock"].double().to(dev)).sum()
+    return loss
+
+
+def _oracle_grads(x, init, cot, with_state, C):
+    xd = {k: v.double().requires_grad_(True) for k, v in x.items()}
+    initd = None if init is None else tuple(t.double().requires_grad_(True) for t in init)
+    o, st = O.chunk_cyfa(**xd, initial_state=initd, output_final_state=with_state, chunk_size=C)
+    _loss(o, st, cot, with_state).backward()
+    grads = {k: xd[k].grad for k in NAMES}
+    if initd is not None:
+        grads.update(h0k=initd[0].grad, h0v=initd[1].grad, clock0=initd[2].grad)
+    return grads
+
+
+def _gpu_grads(x, init, cot, with_state, C):
+    xg = {k: v.to(DEV).requires_grad_(True) for k, v in x.items()}
+    initg = None if init is None else tuple(t.to(DEV).requires_grad_(True) for t in init)
+    o, st = chunk_cyfa(**xg, initial_state=initg, output_final_state=with_state, chunk_size=C)
+    _loss(o, st, cot, with_state).backward()
+    torch.cuda.synchronize()
+    grads = {k: xg[k].grad for k in NAMES}
+    if initg is not None:
+        grads.update(h0k=initg[0].grad, h0v=initg[1].grad, clock0=initg[2].grad)
+    return grads
+
+
+# (B, T, H, K, V, M, C, dtype, initial state, final-state cotangents)
+CASES = [
+    (1, 64, 1, 256, 256, 128, 64, torch.bfloat16, False, False),   # the tuned forward, one chunk
+    (2, 150, 2, 256, 256, 128, 64, torch.bfloat16, True, True),    # ragged, carried states, all cotangents
+    (1, 256, 2, 256, 256, 128, 64, torch.float32, False, True),    # fp32 operands
+    (2, 100, 2, 64, 96, 16, 32, torch.float32, True, True),        # general shape, other slot count
+    (1, 77, 3, 128, 128, 64, 16, torch.bfloat16, True, False),     # general shape in bf16
+]
+
+
+@pytest.mark.parametrize("B,T,H,K,V,M,C,dtype,state,with_state", CASES)
+def test_chunk_backward_matches_oracle_autograd(B, T, H, K, V, M, C, dtype, state, with_state):
+    x, init, cot = _inputs(B, T, H, K, V, M, seed=B * 1000 + T + K, dtype=dtype, state=state)
+    ref = _oracle_grads(x, init, cot, with_state, C)
+    got = _gpu_grads(x, init, cot, with_state, C)
+    for name, r in ref.items():
+        gval = got[name]
+        assert gval is not None, f"{name}: no gradient"
+        assert gval.dtype == x.get(name, r).dtype or name in ("h0k", "h0v", "clock0"), f"{name}: dtype {gval.dtype}"
+        m = metrics(gval.float(), r)
+        bar = _bar(name, dtype)
+        assert torch.isfinite(gval.float()).all(), f"{name}: non-finite gradient"
+        print(f"grad {name} {tuple(x['q'].shape)} {dtype}: rrms {m['rrms']:.3e} (bar {bar})")
+        assert m["rrms"] < bar, f"{name} gradient rrms {m['rrms']:.3e} >= {bar} ({m})"
+
+
+def test_backward_state_only_cotangent():
+    """Only the final states feed the loss: o's cotangent is absent (None)."""
+    x, init, cot = _inputs(1, 96, 2, 256, 256, 128, seed=5, dtype=torch.float32, state=True)
+    xd = {k: v.double().requires_grad_(True) for k, v in x.items()}
+    initd = tuple(t.double().requires_grad_(True) for t in init)
+    _, st = O.chunk_cyfa(**xd, initial_state=initd, output_final_state=True)
+    (st[0] * cot["hk"].double()).sum().add((st[1] * cot["hv"].double()).sum()).backward()
+    xg = {k: v.to(DEV).requires_grad_(True) for k, v in x.items()}
+    initg = tuple(t.to(DEV).requires_grad_(True) for t in init)
+    _, sg = chunk_cyfa(**xg, initial_state=initg, output_final_state=True)
+    ((sg[0] * cot["hk"].to(DEV)).sum() + (sg[1] * cot["hv"].to(DEV)).sum()).backward()
+    for name in ("k", "v", "g", "delta", "beta", "k_norm_weight"):
+        m = metrics(xg[name].grad.float(), xd[name].grad)
+        assert m["rrms"] < 1e-3, f"{name}: {m}"
+    assert metrics(initg[0].grad, initd[0].grad)["rrms"] < 1e-3
+    assert metrics(initg[1].grad, initd[1].grad)["rrms"] < 1e-3
+    # q, its norm weight and the readout never reach the final states (autograd
+    # gives them no gradient at all); the backward returns exact zeros
+    for name in ("q", "q_norm_weight", "readout"):
+        assert xd[name].grad is None
+        assert float(xg[name].grad.abs().max()) == 0.0, name
+
+
+def test_backward_twice_is_deterministic():
+    """Two backward passes over the same graph give identical bits (partial
+    sums are added in a fixed order, no atomics)."""
+    x, init, cot = _inputs(2, 130, 2, 256, 256, 128, seed=9, dtype=torch.bfloat16, state=False)
+    xg = {k: v.to(DEV).requires_grad_(True) for k, v in x.items()}
+    o, _ = chunk_cyfa(**xg)
+    loss = (o.float() * cot["o"].float().to(DEV)).sum()
+    first = torch.autograd.grad(loss, [xg[n] for n in NAMES], retain_graph=True)
+    second = torch.autograd.grad(loss, [xg[n] for n in NAMES])
+    for name, a, b in zip(NAMES, first, second):
+        assert torch.equal(a, b), name
