@@ -10,18 +10,20 @@
 // table = readout @ Phi (ops/chunk.py:281).
 //
 // The forward is recomputed in fp32 with no intermediate rounding (the
-// general path's kernels, keeping the state before every 64-token chunk of
-// both passes), so the gradients are those of the op's exact arithmetic;
-// every adjoint accumulates in fp32. Per pass (o = SGLA(q, k, v, g, S0,
-// scale), in-chunk cumulative log-decay G):
+// general path's clock, write vector and readout; the states before every
+// 64-token chunk of both passes and the pass-1 output from the kernels
+// below), so the gradients are those of the op's exact arithmetic; every
+// adjoint accumulates in fp32. Per pass (o = SGLA(q, k, v, g, S0, scale),
+// in-chunk cumulative log-decay G):
 //   D_n  = e^{G_last} D_{n+1} + scale sum_t e^{G_t} q_t (x) dO_t      (state cotangent, reverse over chunks)
 //   dq_t = scale (e^{G_t} S_n dO_t + sum_{s<=t} e^{G_t-G_s} (dO_t.v_s) k_s)
 //   dk_s = scale sum_{t>=s} e^{G_t-G_s} (dO_t.v_s) q_t + e^{G_last-G_s} D_{n+1} v_s
 //   dv_s = scale sum_{t>=s} e^{G_t-G_s} (q_t.k_s) dO_t + e^{G_last-G_s} D_{n+1}^T k_s
 //   dL/dG_t = q_t.dq_t - k_t.dk_t + [t = last] <D_{n+1}, S_{n+1}>,  dg = in-chunk reverse cumsum
-// The state cotangents are one sweep per (32-column tile, b, h) that keeps
-// its tile of D in LDS; the rows' cotangents are then chunk-parallel, one
-// workgroup per (chunk, h, b), with no reduction across workgroups. The
+// The states and their cotangents are one sweep per (32-column tile, b, h)
+// that keeps its tile in LDS; outputs and the rows' cotangents are then
+// chunk-parallel, one workgroup per (chunk, h, b), with no reduction across
+// workgroups. The
 // readout adjoint runs per row (z = U(lam) raw, softmax of table z, u =
 // table^T p, weights = U(-lam) u) with the head's table and this
 // workgroup's share of the table cotangent on chip; partial sums (table,
@@ -111,81 +113,232 @@ __global__ __launch_bounds__(256) void bw_rows_kernel(const void* x, const float
     if (rs_out && lane == 0) rs_out[row] = rs;
 }
 
-// State cotangents of one pass: D_N = dS_final (or zero), then for n = N-1 .. 0
-// D_n = e^{G_last} D_{n+1} + scale sum_t e^{G_t} q_t (x) dO_t. D_n is kept for
-// every n (D_0 is the initial state's cotangent), and bnd[tile][n] = the
-// tile's part of <D_{n+1}, S_{n+1}>. Grid (ceil(Vd / 32), H, B), 256 threads;
-// the tile's [Kq][32] columns of D stay in LDS.
-struct ScanArgs {
-    const float* q;         // head-major [B*H, Tp, Kq]
-    const float* dO;        // head-major [B*H, Tp, Vd]
-    const float* g;         // [B, T, H]
-    const float* S;         // [B*H, N+1, Kq, Vd]
-    const float* dS_final;  // nullable [B*H, Kq, Vd]
-    float* D;               // [B*H, N+1, Kq, Vd]
-    float* bnd;             // [B*H, ntile, N]
-    float* dS0;             // nullable [B*H, Kq, Vd]
+// The chunk-to-chunk scan of one pass over a [Kq, Vd] matrix X, one 64 x 32
+// tile per workgroup (grid (ceil(Vd / 32), ceil(Kq / 64), B*H), 256
+// threads, each holding a 2 x 4 block of X in registers; every element's
+// recurrence is independent of the others):
+//   X <- e^{G_last} X + sum_t f_t a_t (x) b_t     (a rank-64 update per chunk)
+// Forward (BWD false): the states, n = 0 .. N-1, X_0 = x0 (or zero),
+//   f_t = e^{G_last - G_t}, a = k, b = v; xs[n] = the state before chunk n,
+//   xs[N] the final state.
+// Backward (BWD true): the state cotangents, n = N-1 .. 0, X_N = x0 (the
+//   final state's cotangent, or zero), f_t = scale e^{G_t}, a = q, b = dO;
+//   xs[n+1] = the cotangent after chunk n, xs[0] (and x_out) the initial
+//   state's; bnd[tile][n] = the tile's part of <xs[n+1], S[n+1]>.
+// Per chunk the f-scaled rows of a and the columns of b are staged in LDS
+// (two broadcast reads of a and one float4 of b per token feed eight FMAs).
+constexpr int SCAN_ROWS = 64;
+struct StateScanArgs {
+    const float *a, *b;  // head-major [B*H, Tp, Kq] and [B*H, Tp, Vd]
+    const float* g;      // [B, T, H]
+    const float* x0;     // nullable [B*H, Kq, Vd]
+    float* xs;           // [B*H, N+1, Kq, Vd]
+    const float* S;      // backward: the forward states [B*H, N+1, Kq, Vd]
+    float* bnd;          // backward: [B*H, ntiles, N], ntiles = ceil(Vd / 32) ceil(Kq / 64)
+    float* x_out;        // nullable [B*H, Kq, Vd]
     int B, T, Tp, H, Kq, Vd, N;
     float scale;
 };
 
-__global__ __launch_bounds__(256) void bw_scan_kernel(ScanArgs a) {
-    __shared__ float sD[BW_MAX_D * BW_TILE];
-    __shared__ float sdO[BC][BW_TILE];
-    __shared__ float sEq[BC];
+template <bool BWD>
+__global__ __launch_bounds__(256) void bw_state_scan_kernel(StateScanArgs p) {
+    __shared__ float sA[BC][SCAN_ROWS + 4];
+    __shared__ __align__(16) float sB[BC][BW_TILE];
+    __shared__ float sF[BC];
     __shared__ float sRed[4];
     __shared__ float sEl;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int tile = blockIdx.x, c0 = tile * BW_TILE, h = blockIdx.y, b = blockIdx.z;
-    const int Kq = a.Kq, Vd = a.Vd, N = a.N, nt = gridDim.x;
-    const size_t bh = (size_t)b * a.H + h, ssz = (size_t)Kq * Vd;
-    const float* S = a.S + bh * (N + 1) * ssz;
-    float* D = a.D + bh * (N + 1) * ssz;
-    const float* q = a.q + bh * a.Tp * Kq;
-    const float* dO = a.dO + bh * a.Tp * Vd;
-    for (int e = tid; e < Kq * BW_TILE; e += 256) {
-        const int r = e / BW_TILE, c = e % BW_TILE;
-        sD[e] = (a.dS_final && c0 + c < Vd) ? a.dS_final[bh * ssz + (size_t)r * Vd + c0 + c] : 0.f;
-    }
-    for (int n = N - 1; n >= 0; n--) {
-        // sD holds D_{n+1}: keep it, and its dot with S_{n+1} over the tile
-        float dot = 0.f;
-        for (int e = tid; e < Kq * BW_TILE; e += 256) {
-            const int r = e / BW_TILE, c = e % BW_TILE;
-            if (c0 + c < Vd) {
-                const size_t at = (size_t)(n + 1) * ssz + (size_t)r * Vd + c0 + c;
-                D[at] = sD[e];
-                dot = fmaf(sD[e], S[at], dot);
-            }
+    const int c0 = blockIdx.x * BW_TILE, r0 = blockIdx.y * SCAN_ROWS, bhi = blockIdx.z;
+    const int b = bhi / p.H, h = bhi % p.H, tile = blockIdx.y * gridDim.x + blockIdx.x;
+    const int nt = gridDim.x * gridDim.y;
+    const int Kq = p.Kq, Vd = p.Vd, N = p.N;
+    const size_t bh = bhi, ssz = (size_t)Kq * Vd;
+    float* xs = p.xs + bh * (N + 1) * ssz;
+    const float* A = p.a + bh * p.Tp * Kq;
+    const float* Bm = p.b + bh * p.Tp * Vd;
+    // this thread's block: rows r0 + rr, r0 + rr + 1; columns c0 + cc .. + 3
+    const int rr = 2 * (tid >> 3), cc = 4 * (tid & 7);
+    bool ok[2][4];
+    float x[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            ok[i][j] = r0 + rr + i < Kq && c0 + cc + j < Vd;
+            x[i][j] = ok[i][j] && p.x0 ? p.x0[bh * ssz + (size_t)(r0 + rr + i) * Vd + c0 + cc + j] : 0.f;
         }
-        dot = bw_wave_sum(dot);
-        if (lane == 0) sRed[wv] = dot;
+    const auto keep = [&](int n) {  // xs[n] = X; returns the block's part of <X, S[n]>
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (ok[i][j]) {
+                    const size_t at = (size_t)n * ssz + (size_t)(r0 + rr + i) * Vd + c0 + cc + j;
+                    xs[at] = x[i][j];
+                    if constexpr (BWD) dot = fmaf(x[i][j], p.S[bh * (N + 1) * ssz + at], dot);
+                }
+        return dot;
+    };
+    for (int step = 0; step < N; step++) {
+        const int n = BWD ? N - 1 - step : step;
+        const float dot = keep(BWD ? n + 1 : n);
         const int t0 = n * BC;
-        for (int e = tid; e < BC * BW_TILE; e += 256) {
-            const int t = e / BW_TILE, c = e % BW_TILE;
-            sdO[t][c] = c0 + c < Vd ? dO[(size_t)(t0 + t) * Vd + c0 + c] : 0.f;
+        __syncthreads();  // the previous chunk's tiles are done with
+        if constexpr (BWD) {
+            const float wsum = bw_wave_sum(dot);
+            if (lane == 0) sRed[wv] = wsum;
         }
         if (wv == 0) {
-            const float G = chunk_gam(a.g, b, h, a.T, a.H, n, lane);
-            sEq[lane] = expf(G);
-            if (lane == 63) sEl = expf(G);
+            const float G = chunk_gam(p.g, b, h, p.T, p.H, n, lane);
+            const float Gl = __shfl(G, 63);
+            sF[lane] = BWD ? p.scale * expf(G) : expf(Gl - G);
+            if (lane == 0) sEl = expf(Gl);
+        }
+        for (int e = tid; e < BC * BW_TILE; e += 256) {
+            const int t = e / BW_TILE, c = e % BW_TILE;
+            sB[t][c] = c0 + c < Vd ? Bm[(size_t)(t0 + t) * Vd + c0 + c] : 0.f;
+        }
+        __syncthreads();  // sF is read below
+        for (int e = tid; e < BC * SCAN_ROWS; e += 256) {
+            const int t = e / SCAN_ROWS, r = e % SCAN_ROWS;
+            sA[t][r] = r0 + r < Kq ? sF[t] * A[(size_t)(t0 + t) * Kq + r0 + r] : 0.f;
         }
         __syncthreads();
-        if (tid == 0) a.bnd[(bh * nt + tile) * N + n] = (sRed[0] + sRed[1]) + (sRed[2] + sRed[3]);
+        if constexpr (BWD) {
+            if (tid == 0) p.bnd[(bh * nt + tile) * N + n] = (sRed[0] + sRed[1]) + (sRed[2] + sRed[3]);
+        }
+        float acc[2][4] = {};
+        for (int t = 0; t < BC; t++) {
+            const float a0 = sA[t][rr], a1 = sA[t][rr + 1];
+            const float4 bv = *reinterpret_cast<const float4*>(&sB[t][cc]);
+            acc[0][0] = fmaf(a0, bv.x, acc[0][0]);
+            acc[0][1] = fmaf(a0, bv.y, acc[0][1]);
+            acc[0][2] = fmaf(a0, bv.z, acc[0][2]);
+            acc[0][3] = fmaf(a0, bv.w, acc[0][3]);
+            acc[1][0] = fmaf(a1, bv.x, acc[1][0]);
+            acc[1][1] = fmaf(a1, bv.y, acc[1][1]);
+            acc[1][2] = fmaf(a1, bv.z, acc[1][2]);
+            acc[1][3] = fmaf(a1, bv.w, acc[1][3]);
+        }
         const float el = sEl;
-        for (int e = tid; e < Kq * BW_TILE; e += 256) {
-            const int r = e / BW_TILE, c = e % BW_TILE;
-            float acc = 0.f;
-            for (int t = 0; t < BC; t++) acc = fmaf(sEq[t] * q[(size_t)(t0 + t) * Kq + r], sdO[t][c], acc);
-            sD[e] = fmaf(el, sD[e], a.scale * acc);
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) x[i][j] = fmaf(el, x[i][j], acc[i][j]);
+    }
+    keep(BWD ? 0 : N);
+    if (p.x_out) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (ok[i][j]) p.x_out[bh * ssz + (size_t)(r0 + rr + i) * Vd + c0 + cc + j] = x[i][j];
+    }
+}
+
+// Masked, decayed scores of one chunk into P: P[t][s] = [s <= t] e^{G_t - G_s}
+// sum_j X_t[j] Y_s[j] (X, Y: the chunk's 64 rows, D wide), from 64-wide
+// blocks of both staged in LDS; a thread forms a 4 x 4 block of (t, s).
+__device__ __forceinline__ void chunk_scores(const float* X, const float* Y, int D, const float* sG,
+                                             float (*sXs)[BC + 1], float (*sYs)[BC + 1], float (*P)[BC + 1]) {
+    const int tid = threadIdx.x, tb = 4 * (tid >> 4), sb = 4 * (tid & 15);
+    float acc[4][4] = {};
+    for (int d0 = 0; d0 < D; d0 += BC) {
+        __syncthreads();  // the staging tiles are free
+        for (int e = tid; e < BC * BC; e += 256) {
+            const int t = e / BC, d = e % BC;
+            const bool in = d0 + d < D;
+            sXs[t][d] = in ? X[(size_t)t * D + d0 + d] : 0.f;
+            sYs[t][d] = in ? Y[(size_t)t * D + d0 + d] : 0.f;
         }
         __syncthreads();
+        for (int d = 0; d < BC; d++) {
+            float xv[4], yv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                xv[i] = sXs[tb + i][d];
+                yv[i] = sYs[sb + i][d];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = fmaf(xv[i], yv[j], acc[i][j]);
+        }
     }
-    for (int e = tid; e < Kq * BW_TILE; e += 256) {
-        const int r = e / BW_TILE, c = e % BW_TILE;
-        if (c0 + c < Vd) {
-            D[(size_t)r * Vd + c0 + c] = sD[e];
-            if (a.dS0) a.dS0[bh * ssz + (size_t)r * Vd + c0 + c] = sD[e];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int t = tb + i, s = sb + j;
+            P[t][s] = s <= t ? acc[i][j] * expf(sG[t] - sG[s]) : 0.f;
+        }
+}
+
+// The pass-1 output of the recomputed forward, chunk-parallel (grid (N, H,
+// B), 256 threads): o_t = scale (e^{G_t} q_t S_n + sum_{s<=t} A[t][s] v_s),
+// A the masked decayed q.k scores. A thread owns one output column for
+// 64 / TV tokens.
+struct OutArgs {
+    const float *q, *k, *v;  // head-major [B*H, Tp, Kq | Vd]
+    const float* g;
+    const float* S;          // [B*H, N+1, Kq, Vd]
+    float* out;              // head-major [B*H, Tp, Vd]
+    int B, T, Tp, H, Kq, Vd, N;
+    float scale;
+};
+
+template <int TV>
+__global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
+    __shared__ float sA[BC][BC + 1];
+    __shared__ float sXs[BC][BC + 1], sYs[BC][BC + 1];
+    __shared__ float sX[BC][BW_STAGE];
+    __shared__ float sG[BC], sEq[BC];
+    const int tid = threadIdx.x, n = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int Kq = a.Kq, Vd = a.Vd, t0 = n * BC;
+    const size_t bh = (size_t)b * a.H + h, ssz = (size_t)Kq * Vd;
+    const float* q = a.q + (bh * a.Tp + t0) * Kq;
+    const float* k = a.k + (bh * a.Tp + t0) * Kq;
+    const float* v = a.v + (bh * a.Tp + t0) * Vd;
+    const float* S = a.S + (bh * (a.N + 1) + n) * ssz;
+    if (tid < 64) {
+        sG[tid] = chunk_gam(a.g, b, h, a.T, a.H, n, tid);
+        sEq[tid] = expf(sG[tid]);
+    }
+    chunk_scores(q, k, Kq, sG, sXs, sYs, sA);
+    constexpr int W = 256 / TV, NT = BC / TV;
+    const int cc = tid % W, tg = tid / W;
+    for (int c0 = 0; c0 < Vd; c0 += W) {
+        const int c = c0 + cc;
+        const bool live = c < Vd;
+        float acc[NT];
+#pragma unroll
+        for (int i = 0; i < NT; i++) acc[i] = 0.f;
+        for (int rb = 0; rb < Kq; rb += BW_STAGE) {
+            __syncthreads();
+            for (int e = tid; e < BC * BW_STAGE; e += 256) {
+                const int t = e / BW_STAGE, r = e % BW_STAGE;
+                sX[t][r] = rb + r < Kq ? q[(size_t)t * Kq + rb + r] : 0.f;
+            }
+            __syncthreads();
+            const int rw = min(BW_STAGE, Kq - rb);
+            if (live)
+                for (int r = 0; r < rw; r++) {
+                    const float sv = S[(size_t)(rb + r) * Vd + c];
+#pragma unroll
+                    for (int i = 0; i < NT; i++) acc[i] = fmaf(sv, sX[tg + TV * i][r], acc[i]);
+                }
+        }
+        if (live) {
+#pragma unroll
+            for (int i = 0; i < NT; i++) acc[i] *= sEq[tg + TV * i];
+            for (int s = 0; s < BC; s++) {
+                const float vv = v[(size_t)s * Vd + c];
+#pragma unroll
+                for (int i = 0; i < NT; i++) acc[i] = fmaf(sA[tg + TV * i][s], vv, acc[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < NT; i++) a.out[(bh * a.Tp + t0 + tg + TV * i) * Vd + c] = a.scale * acc[i];
         }
     }
 }
@@ -209,6 +362,7 @@ struct ChunkGradArgs {
 template <int TQ, int TV>
 __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     __shared__ float sA[BC][BC + 1], sB[BC][BC + 1];
+    __shared__ float sXs[BC][BC + 1], sYs[BC][BC + 1];
     __shared__ float sX[BC][BW_STAGE];
     __shared__ float sG[BC], sEq[BC], sEl[BC];
     const int tid = threadIdx.x, n = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -220,25 +374,14 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     const float* dO = a.dO + (bh * a.Tp + t0) * Vd;
     const float* S = a.S + (bh * (a.N + 1) + n) * ssz;
     const float* D = a.D + (bh * (a.N + 1) + n + 1) * ssz;
-    if (tid < 64) sG[tid] = chunk_gam(a.g, b, h, a.T, a.H, n, tid);
-    __syncthreads();
     if (tid < 64) {
-        sEq[tid] = expf(sG[tid]);
-        sEl[tid] = expf(sG[BC - 1] - sG[tid]);
+        const float G = chunk_gam(a.g, b, h, a.T, a.H, n, tid);
+        sG[tid] = G;
+        sEq[tid] = expf(G);
+        sEl[tid] = expf(__shfl(G, BC - 1) - G);
     }
-    for (int e = tid; e < BC * BC; e += 256) {
-        const int t = e / BC, s = e % BC;
-        float x = 0.f, y = 0.f;
-        if (s <= t) {
-            for (int j = 0; j < Kq; j++) x = fmaf(q[(size_t)t * Kq + j], k[(size_t)s * Kq + j], x);
-            for (int j = 0; j < Vd; j++) y = fmaf(dO[(size_t)t * Vd + j], v[(size_t)s * Vd + j], y);
-            const float d = expf(sG[t] - sG[s]);
-            x *= d;
-            y *= d;
-        }
-        sA[t][s] = x;
-        sB[t][s] = y;
-    }
+    chunk_scores(q, k, Kq, sG, sXs, sYs, sA);
+    chunk_scores(dO, v, Vd, sG, sXs, sYs, sB);
     // Stages row block [.][c0, c0 + 128) of a chunk matrix X (row stride ld, width wd) in sX.
     const auto stage = [&](const float* X, int ld, int wd, int c0) {
         __syncthreads();
@@ -341,14 +484,18 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     }
 }
 
-// The slot-readout adjoint, per row of one head (z = U(lam) raw, l = table z,
-// p = softmax(l), u = table^T p, weights = U(-lam) u):
+// The slot-readout adjoint for blocks of 32 rows of one head (z = U(lam) raw,
+// l = table z, p = softmax(l), u = table^T p, weights = U(-lam) u):
 //   du = U(lam) dweights, dp = table du, dl = p (dp - p.dp), dz = table^T dl,
 //   draw = U(-lam) dz, dtable += p du^T + dl z^T, and the clock's share
 //   dlam = sum_p kappa_p [dz . dU(lam)/dlam raw + dweights . dU(-lam)/dlam u]
-// with kappa_p = 2 pi p / (M - 1). Grid (row blocks, H), 256 threads; the
-// head's table (rows padded by one float against bank conflicts) and this
-// block's part of dtable (thread e owns entries e + 256 i) stay on chip.
+// with kappa_p = 2 pi p / (M - 1). Every product over the block is a small
+// GEMM against the head's table (staged once in LDS, rows padded by one
+// float against bank conflicts); a thread forms 4 x 4 output blocks. Grid
+// (ceil(B Tp / 256), H), 256 threads: a workgroup takes 256 rows, eight
+// blocks of 32, and keeps its part of dtable in registers (thread e owns the
+// 4 x 16 block of rows 4 (e / 8) .., columns 16 (e % 8) ..).
+constexpr int RO_BLK = 32;
 struct ReadoutGradArgs {
     const float *raw, *cs, *sn, *table, *dwts;  // head-major rows; table [H, M-1, M]
     float *draw, *dlam, *dtab;                  // dtab: [H, blocks, (M-1) M]
@@ -356,117 +503,171 @@ struct ReadoutGradArgs {
 };
 
 __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
-    constexpr int NE = ((BWD_MAX_M - 1) * BWD_MAX_M + 255) / 256;
-    __shared__ float sTab[(BWD_MAX_M - 1) * (BWD_MAX_M + 1)];
-    __shared__ float sz[BWD_MAX_M], sdu[BWD_MAX_M], sp[BWD_MAX_M], sdl[BWD_MAX_M], sdz[BWD_MAX_M], su[BWD_MAX_M];
-    __shared__ float sRed[2][4];
+    constexpr int LD = BWD_MAX_M + 1;
+    __shared__ float sTab[BWD_MAX_M * LD];  // rows R .. 127 zero
+    __shared__ float sZ[RO_BLK][LD], sDU[RO_BLK][LD], sP[RO_BLK][LD], sDL[RO_BLK][LD];
+    __shared__ float sLam[RO_BLK][32];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, blk = blockIdx.x, h = blockIdx.y;
-    const int M = a.M, R = M - 1, P = M / 2, LD = M + 1, RM = R * M;
-    const float* tb = a.table + (size_t)h * RM;
-    for (int e = tid; e < RM; e += 256) sTab[(e / M) * LD + e % M] = tb[e];
-    float acc[NE];
-#pragma unroll
-    for (int i = 0; i < NE; i++) acc[i] = 0.f;
-    // entry e = tid + 256 i is (r, m); stepping i adds 256 = dr rows and dm columns
-    const int dr = 256 / M, dm = 256 % M, r_first = tid / M, m_first = tid % M;
-    const float kap = tid < P ? (float)(kTwoPiBw * tid / R) : 0.f;
-    const int rows = a.B * a.Tp, rho0 = blk * BWD_RO_ROWS, rho1 = min(rho0 + BWD_RO_ROWS, rows);
-    __syncthreads();
-    for (int rho = rho0; rho < rho1; rho++) {
-        const int b = rho / a.Tp, t = rho % a.Tp;
-        const size_t row = ((size_t)b * a.H + h) * a.Tp + t;
-        float c = 0.f, s = 0.f, re = 0.f, ro = 0.f, de = 0.f, dd = 0.f;
-        if (tid < P) {
-            c = a.cs[row * P + tid];
-            s = a.sn[row * P + tid];
-            re = a.raw[row * M + 2 * tid];
-            ro = a.raw[row * M + 2 * tid + 1];
-            de = a.dwts[row * M + 2 * tid];
-            dd = a.dwts[row * M + 2 * tid + 1];
-            sz[2 * tid] = c * re - s * ro;
-            sz[2 * tid + 1] = s * re + c * ro;
-            sdu[2 * tid] = c * de - s * dd;
-            sdu[2 * tid + 1] = s * de + c * dd;
+    const int M = a.M, R = M - 1, P = M / 2, RM = R * M;
+    for (int e = tid; e < BWD_MAX_M * LD; e += 256) {  // the table, zero beyond R x M
+        const int r = e / LD, m = e % LD;
+        sTab[e] = (r < R && m < M) ? a.table[((size_t)h * R + r) * M + m] : 0.f;
+    }
+    // 4 x 4 blocks over (row, column): rows 4 (tid / 32) .., columns 4 (tid % 32) ..
+    const int br = 4 * (tid >> 5), bc = 4 * (tid & 31);
+    // dtable block: table rows 4 (tid / 8) .. + 4, columns 16 (tid % 8) .. + 16
+    const int tr = 4 * (tid >> 3), tc = 16 * (tid & 7);
+    float dt[4][16] = {};
+    const int rows = a.B * a.Tp;
+    for (int b0 = blk * 8 * RO_BLK; b0 < min(rows, (blk + 1) * 8 * RO_BLK); b0 += RO_BLK) {
+        __syncthreads();  // the previous block's tiles are done with
+        // z = U(lam) raw and du = U(lam) dweights, one (row, pair) per thread step
+        for (int e = tid; e < RO_BLK * (BWD_MAX_M / 2); e += 256) {
+            const int i = e / (BWD_MAX_M / 2), pr = e % (BWD_MAX_M / 2), rho = b0 + i;
+            float ze = 0.f, zo = 0.f, ue = 0.f, uo = 0.f;
+            if (rho < rows && pr < P) {
+                const size_t row = ((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp;
+                const float c = a.cs[row * P + pr], s = a.sn[row * P + pr];
+                const float re = a.raw[row * M + 2 * pr], ro = a.raw[row * M + 2 * pr + 1];
+                const float de = a.dwts[row * M + 2 * pr], dd = a.dwts[row * M + 2 * pr + 1];
+                ze = c * re - s * ro;
+                zo = s * re + c * ro;
+                ue = c * de - s * dd;
+                uo = s * de + c * dd;
+            }
+            sZ[i][2 * pr] = ze;
+            sZ[i][2 * pr + 1] = zo;
+            sDU[i][2 * pr] = ue;
+            sDU[i][2 * pr + 1] = uo;
         }
         __syncthreads();
-        float l = -INFINITY, dp = 0.f;
-        if (tid < R) {
-            float x = 0.f, y = 0.f;
+        // logits l = z table^T and dp = du table^T (into sP, sDL)
+        {
+            float l[4][4] = {}, d[4][4] = {};
             for (int m = 0; m < M; m++) {
-                const float tv = sTab[tid * LD + m];
-                x = fmaf(tv, sz[m], x);
-                y = fmaf(tv, sdu[m], y);
-            }
-            l = x;
-            dp = y;
-        }
-        const float wmx = bw_wave_max(l);
-        if (lane == 0) sRed[0][wv] = wmx;
-        __syncthreads();
-        const float mx = fmaxf(fmaxf(sRed[0][0], sRed[0][1]), fmaxf(sRed[0][2], sRed[0][3]));
-        const float ex = tid < R ? expf(l - mx) : 0.f;
-        const float wse = bw_wave_sum(ex);
-        if (lane == 0) sRed[1][wv] = wse;
-        __syncthreads();
-        const float pr = ex / ((sRed[1][0] + sRed[1][1]) + (sRed[1][2] + sRed[1][3]));
-        const float wpd = bw_wave_sum(pr * dp);
-        __syncthreads();  // sRed[0] read by every thread
-        if (lane == 0) sRed[0][wv] = wpd;
-        __syncthreads();
-        const float pdp = (sRed[0][0] + sRed[0][1]) + (sRed[0][2] + sRed[0][3]);
-        if (tid < M) {
-            sp[tid] = tid < R ? pr : 0.f;
-            sdl[tid] = tid < R ? pr * (dp - pdp) : 0.f;
-        }
-        __syncthreads();
-        if (tid < M) {
-            float x = 0.f, y = 0.f;
-            for (int r = 0; r < R; r++) {
-                const float tv = sTab[r * LD + tid];
-                x = fmaf(tv, sdl[r], x);
-                y = fmaf(tv, sp[r], y);
-            }
-            sdz[tid] = x;
-            su[tid] = y;
-        }
-        __syncthreads();
-        float dl = 0.f;
-        if (tid < P) {
-            const float ze = sdz[2 * tid], zo = sdz[2 * tid + 1], ue = su[2 * tid], uo = su[2 * tid + 1];
-            a.draw[row * M + 2 * tid] = c * ze + s * zo;
-            a.draw[row * M + 2 * tid + 1] = -s * ze + c * zo;
-            dl = kap * (ze * (-s * re - c * ro) + zo * (c * re - s * ro) + de * (-s * ue + c * uo) +
-                        dd * (-c * ue - s * uo));
-        }
-        if (wv == 0) {  // P <= 64: the pairs are all in wave 0
-            dl = bw_wave_sum(dl);
-            if (lane == 0) a.dlam[row] = dl;
-        }
-        int r = r_first, m = m_first;
+                float zv[4], uv[4], tv[4];
 #pragma unroll
-        for (int i = 0; i < NE; i++) {
-            if (r < R) acc[i] = fmaf(sp[r], sdu[m], fmaf(sdl[r], sz[m], acc[i]));
-            r += dr;
-            m += dm;
-            if (m >= M) {
-                m -= M;
-                r++;
+                for (int i = 0; i < 4; i++) {
+                    zv[i] = sZ[br + i][m];
+                    uv[i] = sDU[br + i][m];
+                    tv[i] = sTab[(bc + i) * LD + m];
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        l[i][j] = fmaf(zv[i], tv[j], l[i][j]);
+                        d[i][j] = fmaf(uv[i], tv[j], d[i][j]);
+                    }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    sP[br + i][bc + j] = l[i][j];
+                    sDL[br + i][bc + j] = d[i][j];
+                }
+        }
+        __syncthreads();
+        // softmax and dl per row: wave wv takes rows wv, wv + 4, ...; lanes take slots lane, lane + 64
+        for (int i = wv; i < RO_BLK; i += 4) {
+            const float l0 = lane < R ? sP[i][lane] : -INFINITY, l1 = lane + 64 < R ? sP[i][lane + 64] : -INFINITY;
+            const float mx = bw_wave_max(fmaxf(l0, l1));
+            const float e0 = lane < R ? expf(l0 - mx) : 0.f, e1 = lane + 64 < R ? expf(l1 - mx) : 0.f;
+            const float inv = 1.f / bw_wave_sum(e0 + e1);
+            const float p0 = e0 * inv, p1 = e1 * inv;
+            const float d0 = sDL[i][lane], d1 = sDL[i][lane + 64];
+            const float pdp = bw_wave_sum(p0 * d0 + p1 * d1);
+            sP[i][lane] = p0;
+            sP[i][lane + 64] = p1;
+            sDL[i][lane] = p0 * (d0 - pdp);
+            sDL[i][lane + 64] = p1 * (d1 - pdp);
+        }
+        __syncthreads();
+        // dz = dl table and u = p table: rows br .., columns (m) bc ..; then draw and the clock's share
+        {
+            float dz[4][4] = {}, u[4][4] = {};
+            for (int r = 0; r < R; r++) {
+                float lv[4], pv[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    lv[i] = sDL[br + i][r];
+                    pv[i] = sP[br + i][r];
+                }
+                float t4[4];  // the padded rows are not 16-byte aligned: four scalar reads
+#pragma unroll
+                for (int j = 0; j < 4; j++) t4[j] = sTab[r * LD + bc + j];
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        dz[i][j] = fmaf(lv[i], t4[j], dz[i][j]);
+                        u[i][j] = fmaf(pv[i], t4[j], u[i][j]);
+                    }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int rho = b0 + br + i;
+                float dl = 0.f;
+                if (rho < rows) {
+                    const size_t row = ((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp;
+#pragma unroll
+                    for (int j = 0; j < 4; j += 2) {
+                        const int pr = (bc + j) >> 1;
+                        if (pr < P) {
+                            const float c = a.cs[row * P + pr], s = a.sn[row * P + pr];
+                            const float re = a.raw[row * M + 2 * pr], ro = a.raw[row * M + 2 * pr + 1];
+                            const float de = a.dwts[row * M + 2 * pr], dd = a.dwts[row * M + 2 * pr + 1];
+                            const float ze = dz[i][j], zo = dz[i][j + 1], ue = u[i][j], uo = u[i][j + 1];
+                            a.draw[row * M + 2 * pr] = c * ze + s * zo;
+                            a.draw[row * M + 2 * pr + 1] = -s * ze + c * zo;
+                            dl += (float)(kTwoPiBw * pr / R) *
+                                  (ze * (-s * re - c * ro) + zo * (c * re - s * ro) + de * (-s * ue + c * uo) +
+                                   dd * (-c * ue - s * uo));
+                        }
+                    }
+                }
+                sLam[br + i][tid & 31] = dl;
             }
         }
-        __syncthreads();  // the row's vectors are replaced next
+        __syncthreads();
+        if (tid < RO_BLK && b0 + tid < rows) {  // the clock's share per row, summed in column order
+            float dl = 0.f;
+            for (int g = 0; g < 32; g++) dl += sLam[tid][g];
+            const int rho = b0 + tid;
+            a.dlam[((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp] = dl;
+        }
+        // dtable += p^T du + dl^T z over the block's rows
+        for (int i = 0; i < RO_BLK; i++) {
+            float pv[4], lv[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                pv[r] = sP[i][tr + r];
+                lv[r] = sDL[i][tr + r];
+            }
+#pragma unroll
+            for (int m = 0; m < 16; m++) {
+                const float du = sDU[i][tc + m], z = sZ[i][tc + m];
+#pragma unroll
+                for (int r = 0; r < 4; r++) dt[r][m] = fmaf(pv[r], du, fmaf(lv[r], z, dt[r][m]));
+            }
+        }
     }
     float* dst = a.dtab + ((size_t)h * gridDim.x + blk) * RM;
 #pragma unroll
-    for (int i = 0; i < NE; i++)
-        if (tid + 256 * i < RM) dst[tid + 256 * i] = acc[i];
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int m = 0; m < 16; m++)
+            if (tr + r < R && tc + m < M) dst[(tr + r) * M + tc + m] = dt[r][m];
 }
 
-// Per token of a chunk (lane = token): the gate cotangent of both passes
-// (dL/dG_t = q.dq - k.dk, plus <D_{n+1}, S_{n+1}> at the chunk's last token,
-// then the in-chunk reverse cumsum), and the write vector's (w = beta a(lam),
-// a[2p] = s_p cos theta_p, a[2p+1] = -s_p sin theta_p, dw = the pass-1 value
-// cotangent + the pass-2 key cotangent): dbeta = dw . a, and dlam = beta
-// dw . da/dlam + the readout's share. Grid (N, B*H), 64 threads.
+// Per chunk of (b, h): the gate cotangent of both passes (dL/dG_t = q.dq -
+// k.dk, plus <D_{n+1}, S_{n+1}> at the chunk's last token, then the in-chunk
+// reverse cumsum), and the write vector's (w = beta a(lam), a[2p] = s_p cos
+// theta_p, a[2p+1] = -s_p sin theta_p, dw = the pass-1 value cotangent + the
+// pass-2 key cotangent): dbeta = dw . a, and dlam = beta dw . da/dlam + the
+// readout's share. Grid (N, B*H), 256 threads: wave w forms tokens w, w + 4,
+// .. with its lanes across the row (coalesced), then wave 0 scans.
 struct TokenGradArgs {
     const float *qh, *kh, *dqh, *dkh;    // pass 1 rows [.., K]
     const float *wts, *w, *dwts, *dw2;   // pass 2 query and key rows [.., M]
@@ -479,38 +680,54 @@ struct TokenGradArgs {
     int B, T, Tp, H, K, M, N, nt1, nt2;
 };
 
-__global__ __launch_bounds__(64) void bw_token_kernel(TokenGradArgs a) {
-    const int lane = threadIdx.x, n = blockIdx.x, bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-    const int t = n * BC + lane, K = a.K, M = a.M, P = M / 2, R = M - 1;
-    const size_t row = (size_t)bh * a.Tp + t;
-    float dG = 0.f;
-    for (int j = 0; j < K; j++)
-        dG += a.qh[row * K + j] * a.dqh[row * K + j] - a.kh[row * K + j] * a.dkh[row * K + j];
-    for (int j = 0; j < M; j++)
-        dG += a.wts[row * M + j] * a.dwts[row * M + j] - a.w[row * M + j] * a.dw2[row * M + j];
-    if (lane == BC - 1) {
-        for (int i = 0; i < a.nt1; i++) dG += a.bnd1[((size_t)bh * a.nt1 + i) * a.N + n];
-        for (int i = 0; i < a.nt2; i++) dG += a.bnd2[((size_t)bh * a.nt2 + i) * a.N + n];
+__global__ __launch_bounds__(256) void bw_token_kernel(TokenGradArgs a) {
+    __shared__ float sdG[BC], sdB[BC], sdL[BC];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int n = blockIdx.x, bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+    const int K = a.K, M = a.M, P = M / 2, R = M - 1;
+    for (int i = wv; i < BC; i += 4) {
+        const size_t row = (size_t)bh * a.Tp + n * BC + i;
+        float dG = 0.f;
+        for (int j = lane; j < K; j += 64)
+            dG += a.qh[row * K + j] * a.dqh[row * K + j] - a.kh[row * K + j] * a.dkh[row * K + j];
+        for (int j = lane; j < M; j += 64)
+            dG += a.wts[row * M + j] * a.dwts[row * M + j] - a.w[row * M + j] * a.dw2[row * M + j];
+        float db = 0.f, dl = 0.f;
+        for (int p = lane; p < P; p += 64) {
+            const float c = a.cs[row * P + p], s = a.sn[row * P + p];
+            const float we = a.dw1[row * M + 2 * p] + a.dw2[row * M + 2 * p];
+            const float wo = a.dw1[row * M + 2 * p + 1] + a.dw2[row * M + 2 * p + 1];
+            const float sp = (float)sqrt((p == 0 ? 1.0 : 2.0) / R);
+            db = fmaf(sp, we * c - wo * s, db);
+            dl = fmaf(sp * (float)(kTwoPiBw * p / R), -we * s - wo * c, dl);
+        }
+        dG = bw_wave_sum(dG);
+        db = bw_wave_sum(db);
+        dl = bw_wave_sum(dl);
+        if (lane == 0) {
+            sdG[i] = dG;
+            sdB[i] = db;
+            sdL[i] = dl;
+        }
     }
-    float x = dG;
+    __syncthreads();
+    if (wv != 0) return;
+    const int t = n * BC + lane;
+    const size_t row = (size_t)bh * a.Tp + t;
+    float x = sdG[lane];
+    if (lane == BC - 1) {
+        for (int i = 0; i < a.nt1; i++) x += a.bnd1[((size_t)bh * a.nt1 + i) * a.N + n];
+        for (int i = 0; i < a.nt2; i++) x += a.bnd2[((size_t)bh * a.nt2 + i) * a.N + n];
+    }
     for (int o = 1; o < 64; o <<= 1) {
         const float y = __shfl_down(x, o);
         if (lane + o < 64) x += y;
     }
-    float db = 0.f, dl = 0.f;
-    for (int p = 0; p < P; p++) {
-        const float c = a.cs[row * P + p], s = a.sn[row * P + p];
-        const float we = a.dw1[row * M + 2 * p] + a.dw2[row * M + 2 * p];
-        const float wo = a.dw1[row * M + 2 * p + 1] + a.dw2[row * M + 2 * p + 1];
-        const float sp = (float)sqrt((p == 0 ? 1.0 : 2.0) / R);
-        db = fmaf(sp, we * c - wo * s, db);
-        dl = fmaf(sp * (float)(kTwoPiBw * p / R), -we * s - wo * c, dl);
-    }
     const float bt = t < a.T ? a.beta[((size_t)b * a.T + t) * a.H + h] : 0.f;
-    a.dlam[row] = fmaf(bt, dl, a.dlam[row]);
+    a.dlam[row] = fmaf(bt, sdL[lane], a.dlam[row]);
     if (t < a.T) {
         a.dg[((size_t)b * a.T + t) * a.H + h] = x;
-        a.dbeta[((size_t)b * a.T + t) * a.H + h] = db;
+        a.dbeta[((size_t)b * a.T + t) * a.H + h] = sdB[lane];
     }
 }
 
@@ -587,13 +804,16 @@ __global__ __launch_bounds__(256) void bw_norm_kernel(const void* x, const float
         dw_part[(size_t)blk * D + j] = (sdw[0][j] + sdw[1][j]) + (sdw[2][j] + sdw[3][j]);
 }
 
-// out[i] = sum_b part[b][i] for b in order (n columns, nb partial rows).
+// out[i] = sum over the nb partial rows of part[.][i]: one wave per column,
+// lane l adding rows l, l + 64, .. in order, then the wave's fixed-order sum.
 __global__ __launch_bounds__(256) void bw_reduce_kernel(const float* part, int nb, size_t n, float* out) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t i = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     if (i >= n) return;
     float s = 0.f;
-    for (int b = 0; b < nb; b++) s += part[(size_t)b * n + i];
-    out[i] = s;
+    for (int b = lane; b < nb; b += 64) s += part[(size_t)b * n + i];
+    s = bw_wave_sum(s);
+    if (lane == 0) out[i] = s;
 }
 
 // The table cotangent: per head, sum the readout blocks' partials in order.
@@ -636,6 +856,11 @@ __global__ __launch_bounds__(256) void bw_pack_kernel(const float* src, int B, i
     const size_t row = i / D;
     const int h = (int)(row % H), t = (int)((row / H) % T), b = (int)(row / ((size_t)H * T));
     bw_st<BF>(dst, i, src[(((size_t)b * H + h) * Tp + t) * D + j]);
+}
+
+// The scan's grid for a [Kq, Vd] matrix: (column tiles, row tiles, B*H).
+dim3 scan_grid(int Vd, int Kq, int BH) {
+    return dim3((Vd + BW_TILE - 1) / BW_TILE, (Kq + SCAN_ROWS - 1) / SCAN_ROWS, BH);
 }
 
 int token_groups(int width) { return width > 128 ? 1 : width > 64 ? 2 : 4; }
@@ -687,55 +912,66 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
         CYFA_BW_ROWS(false)
     }
 #undef CYFA_BW_ROWS
-    // the forward, recomputed in fp32, keeping the states before every chunk
-    GenRecomputeParams r{};
-    r.B = B;
-    r.T = T;
-    r.Tp = Tp;
-    r.H = H;
-    r.K = K;
-    r.V = V;
-    r.M = M;
-    r.qh = ws.qh;
-    r.kh = ws.kh;
-    r.vh = ws.vh;
-    r.g = p.g;
-    r.delta = p.delta;
-    r.beta = p.beta;
-    r.table = p.table;
-    r.clock0 = p.clock0;
-    r.h0_k = p.h0_k;
-    r.h0_v = p.h0_v;
-    r.scale = p.scale;
-    r.lam = ws.lam;
-    r.w = ws.w;
-    r.cs = ws.cs;
-    r.sn = ws.sn;
-    r.raw = ws.raw;
-    r.wts = ws.wts;
-    r.sk = ws.sk;
-    r.sv = ws.sv;
-    r.o = ws.dvh;  // overwritten by the pass-2 value cotangent below
-    if (launch_general_recompute(r, stream) != 0) return -1;
+    // the forward, recomputed in fp32: clock, write vector, the states before
+    // every chunk of both passes, the pass-1 output and the slot weights
+    if (launch_general_clock_write(p.delta, p.clock0, p.beta, B, T, Tp, H, M, ws.lam, ws.w, ws.cs, ws.sn, stream) != 0)
+        return -1;
+    StateScanArgs f1{};
+    f1.a = ws.kh;
+    f1.b = ws.w;
+    f1.g = p.g;
+    f1.x0 = p.h0_k;
+    f1.xs = ws.sk;
+    f1.B = B;
+    f1.T = T;
+    f1.Tp = Tp;
+    f1.H = H;
+    f1.Kq = K;
+    f1.Vd = M;
+    f1.N = N;
+    f1.scale = 1.f;
+    hipLaunchKernelGGL(bw_state_scan_kernel<false>, scan_grid(M, K, B * H), blk, 0, stream, f1);
+    OutArgs oa{};
+    oa.q = ws.qh;
+    oa.k = ws.kh;
+    oa.v = ws.w;
+    oa.g = p.g;
+    oa.S = ws.sk;
+    oa.out = ws.raw;
+    oa.B = B;
+    oa.T = T;
+    oa.Tp = Tp;
+    oa.H = H;
+    oa.Kq = K;
+    oa.Vd = M;
+    oa.N = N;
+    oa.scale = p.scale;
+    const dim3 cgrid(N, H, B);
+    if (token_groups(M) == 1)
+        hipLaunchKernelGGL(bw_out_kernel<1>, cgrid, blk, 0, stream, oa);
+    else if (token_groups(M) == 2)
+        hipLaunchKernelGGL(bw_out_kernel<2>, cgrid, blk, 0, stream, oa);
+    else
+        hipLaunchKernelGGL(bw_out_kernel<4>, cgrid, blk, 0, stream, oa);
+    if (launch_general_readout(ws.raw, ws.cs, ws.sn, p.table, (int)rows, Tp, H, M, ws.wts, stream) != 0) return -1;
+    StateScanArgs f2 = f1;
+    f2.a = ws.w;
+    f2.b = ws.vh;
+    f2.x0 = p.h0_v;
+    f2.xs = ws.sv;
+    f2.Kq = M;
+    f2.Vd = V;
+    hipLaunchKernelGGL(bw_state_scan_kernel<false>, scan_grid(V, M, B * H), blk, 0, stream, f2);
     // pass 2: state cotangents, then the rows' (slot weights, write vector, v)
-    ScanArgs s2{};
-    s2.q = ws.wts;
-    s2.dO = ws.dO;
-    s2.g = p.g;
+    StateScanArgs s2 = f2;
+    s2.a = ws.wts;
+    s2.b = ws.dO;
+    s2.x0 = p.d_hv;
+    s2.xs = ws.dsv;
     s2.S = ws.sv;
-    s2.dS_final = p.d_hv;
-    s2.D = ws.dsv;
     s2.bnd = ws.bnd2;
-    s2.dS0 = p.dh0_v;
-    s2.B = B;
-    s2.T = T;
-    s2.Tp = Tp;
-    s2.H = H;
-    s2.Kq = M;
-    s2.Vd = V;
-    s2.N = N;
-    s2.scale = 1.f;
-    hipLaunchKernelGGL(bw_scan_kernel, dim3(ws.nt2, H, B), blk, 0, stream, s2);
+    s2.x_out = p.dh0_v;
+    hipLaunchKernelGGL(bw_state_scan_kernel<true>, scan_grid(V, M, B * H), blk, 0, stream, s2);
     ChunkGradArgs c2{};
     c2.q = ws.wts;
     c2.k = ws.w;
@@ -772,18 +1008,16 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     ro.M = M;
     hipLaunchKernelGGL(bw_readout_kernel, dim3(ws.ro_blocks, H), blk, 0, stream, ro);
     // pass 1, with the pass-1 output's cotangent as dO
-    ScanArgs s1 = s2;
-    s1.q = ws.qh;
-    s1.dO = ws.draw;
+    StateScanArgs s1 = f1;
+    s1.a = ws.qh;
+    s1.b = ws.draw;
+    s1.x0 = p.d_hk;
+    s1.xs = ws.dsk;
     s1.S = ws.sk;
-    s1.dS_final = p.d_hk;
-    s1.D = ws.dsk;
     s1.bnd = ws.bnd1;
-    s1.dS0 = p.dh0_k;
-    s1.Kq = K;
-    s1.Vd = M;
+    s1.x_out = p.dh0_k;
     s1.scale = p.scale;
-    hipLaunchKernelGGL(bw_scan_kernel, dim3(ws.nt1, H, B), blk, 0, stream, s1);
+    hipLaunchKernelGGL(bw_state_scan_kernel<true>, scan_grid(M, K, B * H), blk, 0, stream, s1);
     ChunkGradArgs c1 = c2;
     c1.q = ws.qh;
     c1.k = ws.kh;
@@ -826,7 +1060,7 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     tg.N = N;
     tg.nt1 = ws.nt1;
     tg.nt2 = ws.nt2;
-    hipLaunchKernelGGL(bw_token_kernel, dim3(N, B * H), dim3(64), 0, stream, tg);
+    hipLaunchKernelGGL(bw_token_kernel, dim3(N, B * H), blk, 0, stream, tg);
     hipLaunchKernelGGL(bw_clock_kernel, dim3(B * H), dim3(64), 0, stream, ws.dlam, p.d_clock, B, T, Tp, H, p.ddelta,
                        p.dclock0);
     // the q/k norms, their weights, v's layout
@@ -842,7 +1076,7 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
         hipLaunchKernelGGL(bw_norm_kernel<false>, nb, blk, 0, stream, p.k, p.k_w, ws.rk, ws.dkh, B, T, Tp, H, K, p.dk,
                            ws.dnk);
     }
-    const dim3 kb((unsigned)((K + 255) / 256));
+    const dim3 kb((unsigned)((K + 3) / 4));
     hipLaunchKernelGGL(bw_reduce_kernel, kb, blk, 0, stream, ws.dnq, ws.norm_blocks, (size_t)K, p.dq_w);
     hipLaunchKernelGGL(bw_reduce_kernel, kb, blk, 0, stream, ws.dnk, ws.norm_blocks, (size_t)K, p.dk_w);
     const size_t nv = (size_t)B * T * H * V;

@@ -199,16 +199,7 @@ __global__ __launch_bounds__(256) void gen_sgla_kernel(GenSglaParams p) {
         const int r = e / GEN_COLS, c = e % GEN_COLS;
         sS[e] = (p.s0 && c0 + c < Vd) ? p.s0[(bh * Kq + r) * Vd + c0 + c] : 0.f;
     }
-    // The state before chunk n (and, n = Tp / C, the final state), for a backward pass.
-    const auto save_state = [&](int n) {
-        float* dst = p.states + ((bh * (p.Tp / C + 1) + n) * Kq) * Vd;
-        for (int e = tid; e < Kq * GEN_COLS; e += 256) {
-            const int r = e / GEN_COLS, c = e % GEN_COLS;
-            if (c0 + c < Vd) dst[(size_t)r * Vd + c0 + c] = sS[e];
-        }
-    };
     for (int t0 = 0; t0 < p.Tp; t0 += C) {
-        if (p.states) save_state(t0 / C);  // each thread writes the elements it updates
         for (int e = tid; e < C * GEN_COLS; e += 256) {
             const int s = e / GEN_COLS, c = e % GEN_COLS;
             sV[s][c] = c0 + c < Vd ? v[(size_t)(t0 + s) * Vd + c0 + c] : 0.f;
@@ -271,7 +262,6 @@ __global__ __launch_bounds__(256) void gen_sgla_kernel(GenSglaParams p) {
         }
         __syncthreads();  // the chunk's tiles are replaced next
     }
-    if (p.states) save_state(p.Tp / C);
     if (p.s_final) {
         for (int e = tid; e < Kq * GEN_COLS; e += 256) {
             const int r = e / GEN_COLS, c = e % GEN_COLS;
@@ -513,46 +503,22 @@ int launch_general_chunk(const GenChunkParams& g, hipStream_t stream) {
     return 0;
 }
 
-int launch_general_recompute(const GenRecomputeParams& r, hipStream_t stream) {
-    constexpr int C = 64;
-    if (r.Tp % C || r.K < 1 || r.K > GEN_MAX_K || r.V < 1 || r.V > GEN_MAX_K || r.M < 4 || r.M > 256 || r.M % 2)
-        return -1;
-    const dim3 blk(256);
-    hipLaunchKernelGGL(gen_clock_kernel, dim3(r.B * r.H), dim3(64), 0, stream, r.delta, r.clock0, r.B, r.T, r.Tp, r.H,
-                       r.lam, (float*)nullptr);
-    const size_t rows = (size_t)r.B * r.H * r.Tp, pairs = rows * (r.M / 2);
-    hipLaunchKernelGGL(gen_write_kernel<false>, dim3((unsigned)((pairs + 255) / 256)), blk, 0, stream, r.lam, r.beta,
-                       r.B, r.T, r.Tp, r.H, r.M, r.w, r.cs, r.sn);
-    GenSglaParams p1{};
-    p1.q = r.qh;
-    p1.k = r.kh;
-    p1.v = r.w;
-    p1.g = r.g;
-    p1.B = r.B;
-    p1.T = r.T;
-    p1.Tp = r.Tp;
-    p1.H = r.H;
-    p1.Kq = r.K;
-    p1.Vd = r.M;
-    p1.scale = r.scale;
-    p1.s0 = r.h0_k;
-    p1.out = r.raw;
-    p1.out_bthd = 0;
-    p1.states = r.sk;
-    hipLaunchKernelGGL((gen_sgla_kernel<C, false>), dim3((r.M + GEN_COLS - 1) / GEN_COLS, r.H, r.B), blk, 0, stream, p1);
-    hipLaunchKernelGGL(gen_readout_kernel<false>, dim3((unsigned)((rows + 3) / 4)), blk, 0, stream, r.raw, r.cs, r.sn,
-                       r.table, (int)rows, r.Tp, r.H, r.M, r.wts);
-    GenSglaParams p2 = p1;
-    p2.q = r.wts;
-    p2.k = r.w;
-    p2.v = r.vh;
-    p2.Kq = r.M;
-    p2.Vd = r.V;
-    p2.scale = 1.f;
-    p2.s0 = r.h0_v;
-    p2.out = r.o;
-    p2.states = r.sv;
-    hipLaunchKernelGGL((gen_sgla_kernel<C, false>), dim3((r.V + GEN_COLS - 1) / GEN_COLS, r.H, r.B), blk, 0, stream, p2);
+int launch_general_clock_write(const float* delta, const float* clock0, const float* beta, int B, int T, int Tp, int H,
+                               int M, double* lam, float* w, float* cs, float* sn, hipStream_t stream) {
+    if (M < 4 || M > 256 || M % 2) return -1;
+    hipLaunchKernelGGL(gen_clock_kernel, dim3(B * H), dim3(64), 0, stream, delta, clock0, B, T, Tp, H, lam,
+                       (float*)nullptr);
+    const size_t pairs = (size_t)B * H * Tp * (M / 2);
+    hipLaunchKernelGGL(gen_write_kernel<false>, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, stream, lam, beta,
+                       B, T, Tp, H, M, w, cs, sn);
+    return 0;
+}
+
+int launch_general_readout(const float* raw, const float* cs, const float* sn, const float* table, int rows, int Tp,
+                           int H, int M, float* weights, hipStream_t stream) {
+    if (M < 4 || M > 256 || M % 2) return -1;
+    hipLaunchKernelGGL(gen_readout_kernel<false>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, raw, cs, sn,
+                       table, rows, Tp, H, M, weights);
     return 0;
 }
 

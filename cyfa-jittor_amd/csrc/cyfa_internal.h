@@ -207,7 +207,6 @@ struct GenSglaParams {
     void* out;        // head-major fp32 [B, H, Tp, Vd], or [B, T, H, Vd] in the input dtype (out_bthd)
     int out_bthd;
     float* s_final;  // nullable [B, H, Kq, Vd]
-    float* states;   // nullable [B, H, Tp / C + 1, Kq, Vd]: the state before each chunk, then the final one
 };
 
 struct GenChunkParams {
@@ -264,22 +263,6 @@ inline GenWorkspace general_workspace(int B, int T, int H, int K, int V, int M, 
     return w;
 }
 
-// The forward recomputed for the backward pass (cyfa_general.hip), in fp32
-// with no intermediate rounding and the chunk length 64, from rows the caller
-// has already normalised: the clock, the write vector, pass 1 (keeping the
-// state before every chunk), the slot readout and pass 2 (likewise).
-struct GenRecomputeParams {
-    int B, T, Tp, H, K, V, M;
-    const float *qh, *kh, *vh;  // head-major [B*H, Tp, K | V]
-    const float *g, *delta, *beta, *table;
-    const float *clock0, *h0_k, *h0_v;  // nullable
-    float scale;
-    double* lam;                      // [B*H, Tp]
-    float *w, *cs, *sn, *raw, *wts;   // [B*H, Tp, M | M/2]
-    float *sk, *sv;                   // [B*H, Tp/64 + 1, K, M] and [B*H, Tp/64 + 1, M, V]
-    float* o;                         // head-major [B*H, Tp, V] (not used by the backward)
-};
-
 // The backward pass of the chunk op (cyfa_backward.hip): q, k, v and the
 // cotangent d_o are bf16 or fp32 (bf16 != 0 selects bf16), every other
 // tensor fp32; K, V <= 1024, an even M <= 128.
@@ -315,8 +298,8 @@ struct BwdWorkspace {
     int N, nt1, nt2, ro_blocks, norm_blocks;
     size_t bytes;
 };
-constexpr int BWD_RO_ROWS = 64;    // rows per readout-adjoint workgroup
-constexpr int BWD_NORM_ROWS = 64;  // rows per norm-adjoint workgroup
+constexpr int BWD_RO_ROWS = 256;    // rows per readout-adjoint workgroup
+constexpr int BWD_NORM_ROWS = 256;  // rows per norm-adjoint workgroup
 
 inline BwdWorkspace bwd_workspace(int B, int T, int H, int K, int V, int M, void* base) {
     const size_t Tp = (size_t)(T + 63) / 64 * 64, rows = (size_t)B * H * Tp, N = Tp / 64;
@@ -330,8 +313,8 @@ inline BwdWorkspace bwd_workspace(int B, int T, int H, int K, int V, int M, void
     const auto f = [&](size_t n) { return reinterpret_cast<float*>(take(n * 4)); };
     BwdWorkspace w;
     w.N = (int)N;
-    w.nt1 = (M + 31) / 32;
-    w.nt2 = (V + 31) / 32;
+    w.nt1 = (M + 31) / 32 * ((K + 63) / 64);  // the state scans' tiles (32 columns x 64 rows)
+    w.nt2 = (V + 31) / 32 * ((M + 63) / 64);
     w.ro_blocks = (int)((B * Tp + BWD_RO_ROWS - 1) / BWD_RO_ROWS);
     w.norm_blocks = (int)(((size_t)B * T * H + BWD_NORM_ROWS - 1) / BWD_NORM_ROWS);
     const size_t BH = (size_t)B * H;
@@ -370,7 +353,13 @@ inline BwdWorkspace bwd_workspace(int B, int T, int H, int K, int V, int M, void
 
 int launch_general_table(const float* readout, float* table, int H, int M, hipStream_t stream);
 int launch_general_chunk(const GenChunkParams& p, hipStream_t stream);
-int launch_general_recompute(const GenRecomputeParams& p, hipStream_t stream);
+// The general path's clock and unrounded fp32 write vector with its phases
+// (head-major [B*H, Tp] and [B*H, Tp, M | M/2]), and its unrounded fp32 slot
+// readout of rows raw -> weights; used by the backward pass's recompute.
+int launch_general_clock_write(const float* delta, const float* clock0, const float* beta, int B, int T, int Tp, int H,
+                               int M, double* lam, float* w, float* cs, float* sn, hipStream_t stream);
+int launch_general_readout(const float* raw, const float* cs, const float* sn, const float* table, int rows, int Tp,
+                           int H, int M, float* weights, hipStream_t stream);
 int launch_chunk_bwd(const BwdParams& p, hipStream_t stream);
 int launch_general_decode(const GenDecodeParams& p, int bf16, hipStream_t stream);
 

@@ -153,3 +153,48 @@ def test_backward_twice_is_deterministic():
     second = torch.autograd.grad(loss, [xg[n] for n in NAMES])
     for name, a, b in zip(NAMES, first, second):
         assert torch.equal(a, b), name
+
+
+def test_layer_backward_matches_oracle():
+    """Training through one CyclicFlowAttention layer (fp32 parameters, the
+    layer's general path around the op's autograd function): the gradients
+    of x and of every parameter against float64 autograd through the model
+    oracle. The op's forward rounds q, k, v to bf16 (the tuned kernels), so
+    the cotangents reaching the op carry bf16-level error: the reference's
+    gradient bars apply (0.02 for the gate parameters, 0.01 elsewhere)."""
+    from cyclic_flow_attention.layers import CyclicFlowAttention
+    from oracle import model_oracle as MO
+
+    B, T, hidden, H = 2, 150, 512, 2
+    torch.manual_seed(0)
+    layer = CyclicFlowAttention(hidden_size=hidden, num_heads=H, head_dim=256, num_slots=128).train()
+    gen = torch.Generator().manual_seed(1)
+    with torch.no_grad():
+        for name, p in layer.named_parameters():
+            if name.endswith(".weight") and "norm" not in name:
+                p.copy_(torch.randn(p.shape, generator=gen) * 0.02)
+            elif name.endswith(".bias"):
+                p.copy_(0.1 * torch.randn(p.shape, generator=gen))
+            elif "norm.weight" in name:
+                p.copy_(1 + 0.1 * torch.randn(p.shape, generator=gen))
+    x = torch.randn(B, T, hidden, generator=gen)
+    cot = torch.randn(B, T, hidden, generator=gen)
+    cfg = dict(hidden_size=hidden, num_heads=H, head_dim=256, num_slots=128, norm_eps=1e-6, use_short_conv=True)
+    sd = {"attn." + k: v.detach().double().requires_grad_(True) for k, v in layer.state_dict().items()}
+    xd = x.double().requires_grad_(True)
+    ry, _ = MO.attention_layer(sd, "attn.", xd, cfg, mode="exact")
+    (ry * cot.double()).sum().backward()
+
+    layer = layer.to(DEV)
+    xg = x.to(DEV).requires_grad_(True)
+    y, _ = layer(xg)
+    (y.double() * cot.to(DEV).double()).sum().backward()
+    torch.cuda.synchronize()
+    checks = [("x", xg.grad, xd.grad)]
+    checks += [(n, p.grad, sd["attn." + n].grad) for n, p in layer.named_parameters()]
+    for name, got, ref in checks:
+        assert got is not None and ref is not None, name
+        m = metrics(got.float(), ref)
+        bar = 0.02 if any(s in name for s in ("a_proj", "b_proj", "d_proj", "dt_bias", "A_log")) else 0.01
+        print(f"layer grad {name}: rrms {m['rrms']:.3e} (bar {bar})")
+        assert m["rrms"] < bar, f"layer {name} gradient: {m}"
