@@ -31,6 +31,10 @@ L2-normalised, log alpha = logsigmoid(N(3, 1)); HIP events around each launch;
 algorithmic bytes (q, k, v, g in, o out) against 8 TB/s.
 long_context: configuration 5 (CyFA-1.4B, B=1, a 16384-token prefill, 512
 greedy decode steps) with the op's and the decode layer kernel's fractions.
+backward: the chunk op's backward pass (cyfa_chunk_bwd: fp32 recompute and
+adjoints) at configuration 3's attention shape (B=8, T=2048, H=4, K=V=256,
+128 slots) with bf16 q, k, v and a bf16 cotangent of o; HIP events around each
+launch, next to the forward launch's duration.
 cpu_baseline: the CPU oracle (the restatement of the reference path; the
 reference itself has no CPU path) timed on this host, bounded sample, median
 of three after a warm-up, with the GPU's logits of the same sequence compared
@@ -85,6 +89,7 @@ def parse():
     ap.add_argument("--no-long-context", action="store_true",
                     help="skip configuration 5: CyFA-1.4B, B=1, a 16384-token prefill, then 512 greedy "
                          "decode steps (reported under 'long_context')")
+    ap.add_argument("--no-backward", action="store_true", help="skip the op's backward-pass timing")
     ap.add_argument("--decode-kernel-only", action="store_true",
                     help="only time the fused decode kernel at the decode shape (for hardware-counter runs)")
     ap.add_argument("--layer-kernel-only", action="store_true",
@@ -163,6 +168,41 @@ def time_isolated_pass(K, V, B=8, H=4, T=4096, reps=20, warmup=3):
             ms = timer.results().get("cyfa_scalar_la", [])
     per_th = 2 * K + 2 * K + 2 * V + 4 + (4 if raw else 2) * V  # q, k, v, g read; o written
     return statistics.fmean(ms), per_th * B * H * T, FLOP_PER_TOKEN_HEAD_PASS * B * H * T
+
+
+def time_backward(B=8, T=2048, H=4, reps=5, warmup=2):
+    """Average device durations (ms) of the chunk op's forward and backward
+    launches at configuration 3's attention shape."""
+    import torch
+
+    from cyclic_flow_attention import _native
+    from cyclic_flow_attention.ops import chunk_cyfa
+
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    K = V = 256
+    x = dict(
+        q=torch.randn(B, T, H, K, device="cuda", generator=gen).bfloat16(),
+        k=torch.randn(B, T, H, K, device="cuda", generator=gen).bfloat16(),
+        v=torch.randn(B, T, H, V, device="cuda", generator=gen).bfloat16(),
+        g=torch.nn.functional.logsigmoid(torch.randn(B, T, H, device="cuda", generator=gen) + 3),
+        delta=torch.sigmoid(torch.randn(B, T, H, device="cuda", generator=gen)),
+        beta=torch.sigmoid(torch.randn(B, T, H, device="cuda", generator=gen)),
+        readout=torch.eye(127, device="cuda").expand(H, 127, 127).contiguous(),
+        q_norm_weight=torch.ones(K, device="cuda"),
+        k_norm_weight=torch.ones(K, device="cuda"),
+    )
+    leaves = [t.requires_grad_(True) for t in x.values()]
+    d_o = torch.randn(B, T, H, V, device="cuda", generator=gen).bfloat16()
+    for _ in range(warmup):
+        o, _ = chunk_cyfa(**x)
+        torch.autograd.grad(o, leaves, d_o)
+    torch.cuda.synchronize()
+    with _native.LaunchTimer() as timer:
+        for _ in range(reps):
+            o, _ = chunk_cyfa(**x)
+            torch.autograd.grad(o, leaves, d_o)
+        res = timer.results()
+    return statistics.fmean(res["cyfa_chunk_fwd"]), statistics.fmean(res["cyfa_chunk_bwd"])
 
 
 def time_decode(model, prompt, steps, warmup):
@@ -529,6 +569,16 @@ def main():
             }
             log(f"scalar_la K={K} V={V}: {ms * 1e3:.1f} us/launch = {tflops:.1f} TFLOP/s, {gbs:,.0f} GB/s algorithmic")
         result["isolated_pass"] = iso
+
+    if not args.no_backward:
+        fwd_ms, bwd_ms = time_backward()
+        result["backward"] = {
+            "workload": "cyfa_chunk_bwd at configuration 3's attention shape: B=8, T=2048, H=4, K=V=256, 128 slots, "
+                        "bf16 q, k, v and cotangent; gradients of q, k, v, g, delta, beta, readout, norm weights",
+            "launch_ms": round(bwd_ms, 3), "forward_launch_ms": round(fwd_ms, 4),
+            "train_tok_per_s": round(8 * 2048 / ((fwd_ms + bwd_ms) * 1e-3), 1),
+        }
+        log(f"backward: {bwd_ms:.3f} ms per launch (forward {fwd_ms * 1e3:.1f} us)")
 
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle) ...")
