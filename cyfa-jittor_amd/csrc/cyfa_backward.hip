@@ -42,7 +42,6 @@ namespace {
 constexpr int BC = 64;           // chunk length of the recompute and the sweeps
 constexpr int BW_MAX_D = 1024;   // largest K and V
 constexpr int BW_TILE = 32;      // state columns per scan workgroup
-constexpr int BW_STAGE = 128;    // columns of a staged row block in the chunk kernel
 constexpr double kTwoPiBw = 6.283185307179586;
 
 __device__ __forceinline__ float bw_wave_sum(float x) {
@@ -180,31 +179,56 @@ __global__ __launch_bounds__(256) void bw_state_scan_kernel(StateScanArgs p) {
                 }
         return dot;
     };
+    // The next chunk's rows of a, columns of b and gate are loaded into
+    // registers while the current chunk's FMAs run.
+    constexpr int NA = BC * SCAN_ROWS / 256, NB = BC * BW_TILE / 256;
+    float ra[NA], rb[NB], rg = 0.f;
+    const auto fetch = [&](int n) {
+        const int t0 = n * BC;
+#pragma unroll
+        for (int i = 0; i < NA; i++) {
+            const int e = tid + 256 * i, t = e / SCAN_ROWS, r = e % SCAN_ROWS;
+            ra[i] = r0 + r < Kq ? A[(size_t)(t0 + t) * Kq + r0 + r] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int e = tid + 256 * i, t = e / BW_TILE, c = e % BW_TILE;
+            rb[i] = c0 + c < Vd ? Bm[(size_t)(t0 + t) * Vd + c0 + c] : 0.f;
+        }
+        if (wv == 0) rg = t0 + lane < p.T ? p.g[((size_t)b * p.T + t0 + lane) * p.H + h] : 0.f;
+    };
+    fetch(BWD ? N - 1 : 0);
     for (int step = 0; step < N; step++) {
         const int n = BWD ? N - 1 - step : step;
         const float dot = keep(BWD ? n + 1 : n);
-        const int t0 = n * BC;
         __syncthreads();  // the previous chunk's tiles are done with
         if constexpr (BWD) {
             const float wsum = bw_wave_sum(dot);
             if (lane == 0) sRed[wv] = wsum;
         }
-        if (wv == 0) {
-            const float G = chunk_gam(p.g, b, h, p.T, p.H, n, lane);
+        if (wv == 0) {  // G: the in-chunk inclusive cumsum of the prefetched gate
+            float G = rg;
+            for (int o = 1; o < 64; o <<= 1) {
+                const float y = __shfl_up(G, o);
+                if (lane >= o) G += y;
+            }
             const float Gl = __shfl(G, 63);
             sF[lane] = BWD ? p.scale * expf(G) : expf(Gl - G);
             if (lane == 0) sEl = expf(Gl);
         }
-        for (int e = tid; e < BC * BW_TILE; e += 256) {
-            const int t = e / BW_TILE, c = e % BW_TILE;
-            sB[t][c] = c0 + c < Vd ? Bm[(size_t)(t0 + t) * Vd + c0 + c] : 0.f;
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int e = tid + 256 * i;
+            sB[e / BW_TILE][e % BW_TILE] = rb[i];
         }
         __syncthreads();  // sF is read below
-        for (int e = tid; e < BC * SCAN_ROWS; e += 256) {
-            const int t = e / SCAN_ROWS, r = e % SCAN_ROWS;
-            sA[t][r] = r0 + r < Kq ? sF[t] * A[(size_t)(t0 + t) * Kq + r0 + r] : 0.f;
+#pragma unroll
+        for (int i = 0; i < NA; i++) {
+            const int e = tid + 256 * i, t = e / SCAN_ROWS;
+            sA[t][e % SCAN_ROWS] = sF[t] * ra[i];
         }
         __syncthreads();
+        if (step + 1 < N) fetch(BWD ? n - 1 : n + 1);
         if constexpr (BWD) {
             if (tid == 0) p.bnd[(bh * nt + tile) * N + n] = (sRed[0] + sRed[1]) + (sRed[2] + sRed[3]);
         }
@@ -275,10 +299,76 @@ __device__ __forceinline__ void chunk_scores(const float* X, const float* Y, int
         }
 }
 
+// acc[i][j] += sum_kk A(ti + i, kk) B(kk, tj + j) over kk in [0, Kd) for this
+// thread's 4 x 4 block (ti = 4 (tid / 16), tj = 4 (tid % 16)) of a 64 x 64
+// output tile: both operands staged through LDS in k-blocks of 32 (A
+// transposed, so a thread's four rows are one float4), 16 FMAs per two
+// float4 reads. fa(i, kk) and fb(kk, j) read the operands; B_KCONTIG says
+// whether fb is contiguous along kk (else along j), which picks the staging
+// order that keeps the reads coalesced. Every thread of the block calls it.
+constexpr int GT_K = 32, GT_LD = 68;
+template <bool B_KCONTIG, class FA, class FB>
+__device__ __forceinline__ void tile_gemm(FA fa, FB fb, int Kd, float (*sa)[GT_LD], float (*sb)[GT_LD],
+                                          float acc[4][4]) {
+    constexpr int NE = BC * GT_K / 256;  // staged elements of each operand per thread
+    const int tid = threadIdx.x, ti = 4 * (tid >> 4), tj = 4 * (tid & 15);
+    float ra[NE], rb[NE];
+    // the next k-block's operands go to registers while the current one is multiplied
+    const auto fetch = [&](int k0) {
+#pragma unroll
+        for (int x = 0; x < NE; x++) {
+            const int e = tid + 256 * x;
+            const int ka = e % GT_K, i = e / GT_K;
+            ra[x] = k0 + ka < Kd ? fa(i, k0 + ka) : 0.f;
+            const int kb = B_KCONTIG ? e % GT_K : e / BC, j = B_KCONTIG ? e / GT_K : e % BC;
+            rb[x] = k0 + kb < Kd ? fb(k0 + kb, j) : 0.f;
+        }
+    };
+    fetch(0);
+    for (int k0 = 0; k0 < Kd; k0 += GT_K) {
+        __syncthreads();  // the staging tiles are free
+#pragma unroll
+        for (int x = 0; x < NE; x++) {
+            const int e = tid + 256 * x;
+            sa[e % GT_K][e / GT_K] = ra[x];
+            if (B_KCONTIG)
+                sb[e % GT_K][e / GT_K] = rb[x];
+            else
+                sb[e / BC][e % BC] = rb[x];
+        }
+        __syncthreads();
+        if (k0 + GT_K < Kd) fetch(k0 + GT_K);
+#pragma unroll 8
+        for (int kk = 0; kk < GT_K; kk++) {
+            const float4 av = *reinterpret_cast<const float4*>(&sa[kk][ti]);
+            const float4 bv = *reinterpret_cast<const float4*>(&sb[kk][tj]);
+            const float ar[4] = {av.x, av.y, av.z, av.w}, br[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = fmaf(ar[i], br[j], acc[i][j]);
+        }
+    }
+}
+
+// Writes this thread's 4 x 4 block of a 64 x 64 tile (rows = the chunk's
+// tokens, columns d0 ..) into head-major rows dst [.., D], times the row
+// factor f(t) and a scale.
+template <class F>
+__device__ __forceinline__ void tile_store(float acc[4][4], float* dst, int D, int d0, F f) {
+    const int tid = threadIdx.x, ti = 4 * (tid >> 4), tj = 4 * (tid & 15);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float fr = f(ti + i);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (d0 + tj + j < D) dst[(size_t)(ti + i) * D + d0 + tj + j] = fr * acc[i][j];
+    }
+}
+
 // The pass-1 output of the recomputed forward, chunk-parallel (grid (N, H,
 // B), 256 threads): o_t = scale (e^{G_t} q_t S_n + sum_{s<=t} A[t][s] v_s),
-// A the masked decayed q.k scores. A thread owns one output column for
-// 64 / TV tokens.
+// A the masked decayed q.k scores, per 64-wide output tile as two tile GEMMs.
 struct OutArgs {
     const float *q, *k, *v;  // head-major [B*H, Tp, Kq | Vd]
     const float* g;
@@ -288,11 +378,14 @@ struct OutArgs {
     float scale;
 };
 
-template <int TV>
 __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
     __shared__ float sA[BC][BC + 1];
-    __shared__ float sXs[BC][BC + 1], sYs[BC][BC + 1];
-    __shared__ float sX[BC][BW_STAGE];
+    // staging: the score tiles first, then the GEMM tiles in the same bytes
+    __shared__ __align__(16) float sStage[2 * BC * (BC + 1)];
+    float(*sXs)[BC + 1] = reinterpret_cast<float(*)[BC + 1]>(sStage);
+    float(*sYs)[BC + 1] = reinterpret_cast<float(*)[BC + 1]>(sStage + BC * (BC + 1));
+    float(*sa)[GT_LD] = reinterpret_cast<float(*)[GT_LD]>(sStage);
+    float(*sb)[GT_LD] = reinterpret_cast<float(*)[GT_LD]>(sStage + GT_K * GT_LD);
     __shared__ float sG[BC], sEq[BC];
     const int tid = threadIdx.x, n = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int Kq = a.Kq, Vd = a.Vd, t0 = n * BC;
@@ -306,50 +399,28 @@ __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
         sEq[tid] = expf(sG[tid]);
     }
     chunk_scores(q, k, Kq, sG, sXs, sYs, sA);
-    constexpr int W = 256 / TV, NT = BC / TV;
-    const int cc = tid % W, tg = tid / W;
-    for (int c0 = 0; c0 < Vd; c0 += W) {
-        const int c = c0 + cc;
-        const bool live = c < Vd;
-        float acc[NT];
+    float* out = a.out + (bh * a.Tp + t0) * Vd;
+    for (int d0 = 0; d0 < Vd; d0 += BC) {
+        float acc[4][4] = {};
+        tile_gemm<false>([&](int i, int kk) { return q[(size_t)i * Kq + kk]; },
+                         [&](int kk, int j) { return d0 + j < Vd ? S[(size_t)kk * Vd + d0 + j] : 0.f; }, Kq, sa, sb,
+                         acc);
+        const int ti = 4 * (tid >> 4);
 #pragma unroll
-        for (int i = 0; i < NT; i++) acc[i] = 0.f;
-        for (int rb = 0; rb < Kq; rb += BW_STAGE) {
-            __syncthreads();
-            for (int e = tid; e < BC * BW_STAGE; e += 256) {
-                const int t = e / BW_STAGE, r = e % BW_STAGE;
-                sX[t][r] = rb + r < Kq ? q[(size_t)t * Kq + rb + r] : 0.f;
-            }
-            __syncthreads();
-            const int rw = min(BW_STAGE, Kq - rb);
-            if (live)
-                for (int r = 0; r < rw; r++) {
-                    const float sv = S[(size_t)(rb + r) * Vd + c];
+        for (int i = 0; i < 4; i++)
 #pragma unroll
-                    for (int i = 0; i < NT; i++) acc[i] = fmaf(sv, sX[tg + TV * i][r], acc[i]);
-                }
-        }
-        if (live) {
-#pragma unroll
-            for (int i = 0; i < NT; i++) acc[i] *= sEq[tg + TV * i];
-            for (int s = 0; s < BC; s++) {
-                const float vv = v[(size_t)s * Vd + c];
-#pragma unroll
-                for (int i = 0; i < NT; i++) acc[i] = fmaf(sA[tg + TV * i][s], vv, acc[i]);
-            }
-#pragma unroll
-            for (int i = 0; i < NT; i++) a.out[(bh * a.Tp + t0 + tg + TV * i) * Vd + c] = a.scale * acc[i];
-        }
+            for (int jj = 0; jj < 4; jj++) acc[i][jj] *= sEq[ti + i];
+        tile_gemm<false>([&](int i, int kk) { return sA[i][kk]; },
+                         [&](int kk, int j) { return d0 + j < Vd ? v[(size_t)kk * Vd + d0 + j] : 0.f; }, BC, sa, sb,
+                         acc);
+        tile_store(acc, out, Vd, d0, [&](int) { return a.scale; });
     }
 }
 
 // Cotangents of one chunk's rows: dq, dk (Kq) and dv (Vd) for its 64 tokens
 // from S_n (state before the chunk), D_{n+1} (cotangent after it) and the
-// two masked decayed score matrices A (q.k) and B (dO.v). Grid (N, H, B),
-// 256 threads. A thread owns one row coordinate (block width 256 / TQ of the
-// Kq dims, 256 / TV of the Vd dims) for 64 / T tokens, so every load of S,
-// D, k or q feeds as many FMAs as the thread has tokens; the other operand
-// is a staged row block read as an LDS broadcast.
+// two masked decayed score matrices A (q.k) and B (dO.v), each output tile
+// (64 tokens x 64 coordinates) as two tile GEMMs. Grid (N, H, B), 256 threads.
 struct ChunkGradArgs {
     const float *q, *k, *v, *dO;  // head-major [B*H, Tp, Kq | Vd]
     const float* g;               // [B, T, H]
@@ -359,11 +430,14 @@ struct ChunkGradArgs {
     float scale;
 };
 
-template <int TQ, int TV>
 __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     __shared__ float sA[BC][BC + 1], sB[BC][BC + 1];
-    __shared__ float sXs[BC][BC + 1], sYs[BC][BC + 1];
-    __shared__ float sX[BC][BW_STAGE];
+    // staging: the score tiles first, then the GEMM tiles in the same bytes
+    __shared__ __align__(16) float sStage[2 * BC * (BC + 1)];
+    float(*sXs)[BC + 1] = reinterpret_cast<float(*)[BC + 1]>(sStage);
+    float(*sYs)[BC + 1] = reinterpret_cast<float(*)[BC + 1]>(sStage + BC * (BC + 1));
+    float(*sa)[GT_LD] = reinterpret_cast<float(*)[GT_LD]>(sStage);
+    float(*sb)[GT_LD] = reinterpret_cast<float(*)[GT_LD]>(sStage + GT_K * GT_LD);
     __shared__ float sG[BC], sEq[BC], sEl[BC];
     const int tid = threadIdx.x, n = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int Kq = a.Kq, Vd = a.Vd, t0 = n * BC;
@@ -382,103 +456,142 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     }
     chunk_scores(q, k, Kq, sG, sXs, sYs, sA);
     chunk_scores(dO, v, Vd, sG, sXs, sYs, sB);
-    // Stages row block [.][c0, c0 + 128) of a chunk matrix X (row stride ld, width wd) in sX.
-    const auto stage = [&](const float* X, int ld, int wd, int c0) {
-        __syncthreads();
-        for (int e = tid; e < BC * BW_STAGE; e += 256) {
-            const int t = e / BW_STAGE, c = e % BW_STAGE;
-            sX[t][c] = c0 + c < wd ? X[(size_t)t * ld + c0 + c] : 0.f;
-        }
-        __syncthreads();
-    };
-    {
-        constexpr int W = 256 / TQ, NT = BC / TQ;
-        const int rr = tid % W, tg = tid / W;
-        for (int r0 = 0; r0 < Kq; r0 += W) {
-            const int r = r0 + rr;
-            const bool live = r < Kq;
-            float acc[NT];
-            // dq: e^{G_t} S_n dO_t, then + sum_s B[t][s] k_s
+    const int ti = 4 * (tid >> 4);
+    const float sc = a.scale;
+    for (int d0 = 0; d0 < Kq; d0 += BC) {
+        // dq = scale (e^{G_t} dO_t S_n^T + B k)
+        float acc[4][4] = {};
+        tile_gemm<true>([&](int i, int kk) { return dO[(size_t)i * Vd + kk]; },
+                        [&](int kk, int j) { return d0 + j < Kq ? S[(size_t)(d0 + j) * Vd + kk] : 0.f; }, Vd, sa, sb,
+                        acc);
 #pragma unroll
-            for (int i = 0; i < NT; i++) acc[i] = 0.f;
-            for (int cb = 0; cb < Vd; cb += BW_STAGE) {
-                stage(dO, Vd, Vd, cb);
-                const int cw = min(BW_STAGE, Vd - cb);
-                if (live)
-                    for (int c = 0; c < cw; c++) {
-                        const float sv = S[(size_t)r * Vd + cb + c];
+        for (int i = 0; i < 4; i++)
 #pragma unroll
-                        for (int i = 0; i < NT; i++) acc[i] = fmaf(sv, sX[tg + TQ * i][c], acc[i]);
-                    }
-            }
-            if (live) {
+            for (int jj = 0; jj < 4; jj++) acc[i][jj] *= sEq[ti + i];
+        tile_gemm<false>([&](int i, int kk) { return sB[i][kk]; },
+                         [&](int kk, int j) { return d0 + j < Kq ? k[(size_t)kk * Kq + d0 + j] : 0.f; }, BC, sa, sb,
+                         acc);
+        tile_store(acc, a.dq + (bh * a.Tp + t0) * Kq, Kq, d0, [&](int) { return sc; });
+        // dk = e^{G_last - G_s} v_s D_{n+1}^T + scale B^T q
 #pragma unroll
-                for (int i = 0; i < NT; i++) acc[i] *= sEq[tg + TQ * i];
-                for (int s = 0; s < BC; s++) {
-                    const float kv = k[(size_t)s * Kq + r];
+        for (int i = 0; i < 4; i++)
 #pragma unroll
-                    for (int i = 0; i < NT; i++) acc[i] = fmaf(sB[tg + TQ * i][s], kv, acc[i]);
-                }
+            for (int jj = 0; jj < 4; jj++) acc[i][jj] = 0.f;
+        tile_gemm<true>([&](int i, int kk) { return v[(size_t)i * Vd + kk]; },
+                        [&](int kk, int j) { return d0 + j < Kq ? D[(size_t)(d0 + j) * Vd + kk] : 0.f; }, Vd, sa, sb,
+                        acc);
 #pragma unroll
-                for (int i = 0; i < NT; i++)
-                    a.dq[(bh * a.Tp + t0 + tg + TQ * i) * Kq + r] = a.scale * acc[i];
-            }
-            // dk: e^{G_last - G_s} D_{n+1} v_s, then + scale sum_t B[t][s] q_t
+        for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int i = 0; i < NT; i++) acc[i] = 0.f;
-            for (int cb = 0; cb < Vd; cb += BW_STAGE) {
-                stage(v, Vd, Vd, cb);
-                const int cw = min(BW_STAGE, Vd - cb);
-                if (live)
-                    for (int c = 0; c < cw; c++) {
-                        const float dv = D[(size_t)r * Vd + cb + c];
-#pragma unroll
-                        for (int i = 0; i < NT; i++) acc[i] = fmaf(dv, sX[tg + TQ * i][c], acc[i]);
-                    }
-            }
-            if (live) {
-#pragma unroll
-                for (int i = 0; i < NT; i++) acc[i] *= sEl[tg + TQ * i];
-                for (int t = 0; t < BC; t++) {
-                    const float qv = a.scale * q[(size_t)t * Kq + r];
-#pragma unroll
-                    for (int i = 0; i < NT; i++) acc[i] = fmaf(sB[t][tg + TQ * i], qv, acc[i]);
-                }
-#pragma unroll
-                for (int i = 0; i < NT; i++) a.dk[(bh * a.Tp + t0 + tg + TQ * i) * Kq + r] = acc[i];
-            }
-        }
+            for (int jj = 0; jj < 4; jj++) acc[i][jj] *= sEl[ti + i];
+        tile_gemm<false>([&](int i, int kk) { return sc * sB[kk][i]; },
+                         [&](int kk, int j) { return d0 + j < Kq ? q[(size_t)kk * Kq + d0 + j] : 0.f; }, BC, sa, sb,
+                         acc);
+        tile_store(acc, a.dk + (bh * a.Tp + t0) * Kq, Kq, d0, [&](int) { return 1.f; });
     }
+    for (int d0 = 0; d0 < Vd; d0 += BC) {
+        // dv = e^{G_last - G_s} k_s D_{n+1} + scale A^T dO
+        float acc[4][4] = {};
+        tile_gemm<false>([&](int i, int kk) { return k[(size_t)i * Kq + kk]; },
+                         [&](int kk, int j) { return d0 + j < Vd ? D[(size_t)kk * Vd + d0 + j] : 0.f; }, Kq, sa, sb,
+                         acc);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) acc[i][jj] *= sEl[ti + i];
+        tile_gemm<false>([&](int i, int kk) { return sc * sA[kk][i]; },
+                         [&](int kk, int j) { return d0 + j < Vd ? dO[(size_t)kk * Vd + d0 + j] : 0.f; }, BC, sa, sb,
+                         acc);
+        tile_store(acc, a.dv + (bh * a.Tp + t0) * Vd, Vd, d0, [&](int) { return 1.f; });
+    }
+}
+
+// The slot readout of the recomputed forward (fp32, unrounded) for blocks of
+// 32 rows of one head: z = U(lam) raw, l = z table^T, p = softmax(l),
+// u = p table, weights = U(-lam) u; the two products as small GEMMs against
+// the staged table (4 x 4 per thread). Grid (ceil(B Tp / 32), H), 256 threads.
+__global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, const float* cs, const float* sn,
+                                                             const float* table, int B, int Tp, int H, int M,
+                                                             float* wts) {
+    constexpr int LD = BWD_MAX_M + 1, RB = 32;
+    __shared__ float sTab[BWD_MAX_M * LD];  // rows R .. 127 zero
+    __shared__ float sZ[RB][LD], sP[RB][LD];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, h = blockIdx.y;
+    const int R = M - 1, P = M / 2, rows = B * Tp, b0 = blockIdx.x * RB;
+    for (int e = tid; e < BWD_MAX_M * LD; e += 256) {
+        const int r = e / LD, m = e % LD;
+        sTab[e] = (r < R && m < M) ? table[((size_t)h * R + r) * M + m] : 0.f;
+    }
+    const auto row_of = [&](int rho) { return ((size_t)(rho / Tp) * H + h) * Tp + rho % Tp; };
+    for (int e = tid; e < RB * (BWD_MAX_M / 2); e += 256) {
+        const int i = e / (BWD_MAX_M / 2), pr = e % (BWD_MAX_M / 2), rho = b0 + i;
+        float ze = 0.f, zo = 0.f;
+        if (rho < rows && pr < P) {
+            const size_t row = row_of(rho);
+            const float c = cs[row * P + pr], s = sn[row * P + pr];
+            const float re = raw[row * M + 2 * pr], ro = raw[row * M + 2 * pr + 1];
+            ze = c * re - s * ro;
+            zo = s * re + c * ro;
+        }
+        sZ[i][2 * pr] = ze;
+        sZ[i][2 * pr + 1] = zo;
+    }
+    __syncthreads();
+    const int br = 4 * (tid >> 5), bc = 4 * (tid & 31);
     {
-        constexpr int W = 256 / TV, NT = BC / TV;
-        const int cc = tid % W, tg = tid / W;
-        for (int c0 = 0; c0 < Vd; c0 += W) {
-            const int c = c0 + cc;
-            const bool live = c < Vd;
-            // dv: e^{G_last - G_s} D_{n+1}^T k_s, then + scale sum_t A[t][s] dO_t
-            float acc[NT];
+        float l[4][4] = {};
+        for (int m = 0; m < M; m++) {
+            float zv[4], tv[4];
 #pragma unroll
-            for (int i = 0; i < NT; i++) acc[i] = 0.f;
-            for (int rb = 0; rb < Kq; rb += BW_STAGE) {
-                stage(k, Kq, Kq, rb);
-                const int rw = min(BW_STAGE, Kq - rb);
-                if (live)
-                    for (int r = 0; r < rw; r++) {
-                        const float dv = D[(size_t)(rb + r) * Vd + c];
-#pragma unroll
-                        for (int i = 0; i < NT; i++) acc[i] = fmaf(dv, sX[tg + TV * i][r], acc[i]);
-                    }
+            for (int i = 0; i < 4; i++) {
+                zv[i] = sZ[br + i][m];
+                tv[i] = sTab[(bc + i) * LD + m];
             }
-            if (live) {
 #pragma unroll
-                for (int i = 0; i < NT; i++) acc[i] *= sEl[tg + TV * i];
-                for (int t = 0; t < BC; t++) {
-                    const float ov = a.scale * dO[(size_t)t * Vd + c];
+            for (int i = 0; i < 4; i++)
 #pragma unroll
-                    for (int i = 0; i < NT; i++) acc[i] = fmaf(sA[t][tg + TV * i], ov, acc[i]);
-                }
+                for (int j = 0; j < 4; j++) l[i][j] = fmaf(zv[i], tv[j], l[i][j]);
+        }
 #pragma unroll
-                for (int i = 0; i < NT; i++) a.dv[(bh * a.Tp + t0 + tg + TV * i) * Vd + c] = acc[i];
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) sP[br + i][bc + j] = l[i][j];
+    }
+    __syncthreads();
+    for (int i = wv; i < RB; i += 4) {
+        const float l0 = lane < R ? sP[i][lane] : -INFINITY, l1 = lane + 64 < R ? sP[i][lane + 64] : -INFINITY;
+        const float mx = bw_wave_max(fmaxf(l0, l1));
+        const float e0 = lane < R ? expf(l0 - mx) : 0.f, e1 = lane + 64 < R ? expf(l1 - mx) : 0.f;
+        const float inv = 1.f / bw_wave_sum(e0 + e1);
+        sP[i][lane] = e0 * inv;
+        sP[i][lane + 64] = e1 * inv;
+    }
+    __syncthreads();
+    float u[4][4] = {};
+    for (int r = 0; r < R; r++) {
+        float pv[4], t4[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            pv[i] = sP[br + i][r];
+            t4[i] = sTab[r * LD + bc + i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) u[i][j] = fmaf(pv[i], t4[j], u[i][j]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int rho = b0 + br + i;
+        if (rho >= rows) continue;
+        const size_t row = row_of(rho);
+#pragma unroll
+        for (int j = 0; j < 4; j += 2) {
+            const int pr = (bc + j) >> 1;
+            if (pr < P) {
+                const float c = cs[row * P + pr], s = sn[row * P + pr];
+                wts[row * M + 2 * pr] = c * u[i][j] + s * u[i][j + 1];
+                wts[row * M + 2 * pr + 1] = -s * u[i][j] + c * u[i][j + 1];
             }
         }
     }
@@ -863,27 +976,8 @@ dim3 scan_grid(int Vd, int Kq, int BH) {
     return dim3((Vd + BW_TILE - 1) / BW_TILE, (Kq + SCAN_ROWS - 1) / SCAN_ROWS, BH);
 }
 
-int token_groups(int width) { return width > 128 ? 1 : width > 64 ? 2 : 4; }
-
-template <int TQ>
-void launch_chunk_grad_tv(const ChunkGradArgs& a, int tv, dim3 grid, hipStream_t stream) {
-    if (tv == 1)
-        hipLaunchKernelGGL((bw_chunk_kernel<TQ, 1>), grid, dim3(256), 0, stream, a);
-    else if (tv == 2)
-        hipLaunchKernelGGL((bw_chunk_kernel<TQ, 2>), grid, dim3(256), 0, stream, a);
-    else
-        hipLaunchKernelGGL((bw_chunk_kernel<TQ, 4>), grid, dim3(256), 0, stream, a);
-}
-
 void launch_chunk_grad(const ChunkGradArgs& a, hipStream_t stream) {
-    const dim3 grid(a.N, a.H, a.B);
-    const int tq = token_groups(a.Kq), tv = token_groups(a.Vd);
-    if (tq == 1)
-        launch_chunk_grad_tv<1>(a, tv, grid, stream);
-    else if (tq == 2)
-        launch_chunk_grad_tv<2>(a, tv, grid, stream);
-    else
-        launch_chunk_grad_tv<4>(a, tv, grid, stream);
+    hipLaunchKernelGGL(bw_chunk_kernel, dim3(a.N, a.H, a.B), dim3(256), 0, stream, a);
 }
 
 }  // namespace
@@ -946,14 +1040,9 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     oa.Vd = M;
     oa.N = N;
     oa.scale = p.scale;
-    const dim3 cgrid(N, H, B);
-    if (token_groups(M) == 1)
-        hipLaunchKernelGGL(bw_out_kernel<1>, cgrid, blk, 0, stream, oa);
-    else if (token_groups(M) == 2)
-        hipLaunchKernelGGL(bw_out_kernel<2>, cgrid, blk, 0, stream, oa);
-    else
-        hipLaunchKernelGGL(bw_out_kernel<4>, cgrid, blk, 0, stream, oa);
-    if (launch_general_readout(ws.raw, ws.cs, ws.sn, p.table, (int)rows, Tp, H, M, ws.wts, stream) != 0) return -1;
+    hipLaunchKernelGGL(bw_out_kernel, dim3(N, H, B), blk, 0, stream, oa);
+    hipLaunchKernelGGL(bw_fwd_readout_kernel, dim3((B * Tp + 31) / 32, H), blk, 0, stream, ws.raw, ws.cs, ws.sn,
+                       p.table, B, Tp, H, M, ws.wts);
     StateScanArgs f2 = f1;
     f2.a = ws.w;
     f2.b = ws.vh;

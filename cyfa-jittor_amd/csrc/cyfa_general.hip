@@ -514,14 +514,6 @@ int launch_general_clock_write(const float* delta, const float* clock0, const fl
     return 0;
 }
 
-int launch_general_readout(const float* raw, const float* cs, const float* sn, const float* table, int rows, int Tp,
-                           int H, int M, float* weights, hipStream_t stream) {
-    if (M < 4 || M > 256 || M % 2) return -1;
-    hipLaunchKernelGGL(gen_readout_kernel<false>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, raw, cs, sn,
-                       table, rows, Tp, H, M, weights);
-    return 0;
-}
-
 int launch_general_decode(const GenDecodeParams& p, int bf16, hipStream_t stream) {
     if (p.K < 1 || p.K > GEN_MAX_K || p.V < 1 || p.V > GEN_MAX_K || p.M < 4 || p.M > 256 || p.M % 2) return -1;
     if (bf16)

@@ -299,7 +299,7 @@ struct BwdWorkspace {
     size_t bytes;
 };
 constexpr int BWD_RO_ROWS = 256;    // rows per readout-adjoint workgroup
-constexpr int BWD_NORM_ROWS = 256;  // rows per norm-adjoint workgroup
+constexpr int BWD_NORM_ROWS = 64;   // rows per norm-adjoint workgroup
 
 inline BwdWorkspace bwd_workspace(int B, int T, int H, int K, int V, int M, void* base) {
     const size_t Tp = (size_t)(T + 63) / 64 * 64, rows = (size_t)B * H * Tp, N = Tp / 64;
@@ -354,12 +354,9 @@ inline BwdWorkspace bwd_workspace(int B, int T, int H, int K, int V, int M, void
 int launch_general_table(const float* readout, float* table, int H, int M, hipStream_t stream);
 int launch_general_chunk(const GenChunkParams& p, hipStream_t stream);
 // The general path's clock and unrounded fp32 write vector with its phases
-// (head-major [B*H, Tp] and [B*H, Tp, M | M/2]), and its unrounded fp32 slot
-// readout of rows raw -> weights; used by the backward pass's recompute.
+// (head-major [B*H, Tp] and [B*H, Tp, M | M/2]), for the backward pass's recompute.
 int launch_general_clock_write(const float* delta, const float* clock0, const float* beta, int B, int T, int Tp, int H,
                                int M, double* lam, float* w, float* cs, float* sn, hipStream_t stream);
-int launch_general_readout(const float* raw, const float* cs, const float* sn, const float* table, int rows, int Tp,
-                           int H, int M, float* weights, hipStream_t stream);
 int launch_chunk_bwd(const BwdParams& p, hipStream_t stream);
 int launch_general_decode(const GenDecodeParams& p, int bf16, hipStream_t stream);
 
