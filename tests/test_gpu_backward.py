@@ -198,3 +198,52 @@ def test_layer_backward_matches_oracle():
         bar = 0.02 if any(s in name for s in ("a_proj", "b_proj", "d_proj", "dt_bias", "A_log")) else 0.01
         print(f"layer grad {name}: rrms {m['rrms']:.3e} (bar {bar})")
         assert m["rrms"] < bar, f"layer {name} gradient: {m}"
+
+
+def test_chunk_backward_config1_size():
+    """The op's backward at configuration 1's attention shape (B=1, T=2048,
+    H=4, K=V=256, 128 slots, bf16), every gradient against float64 autograd."""
+    x, init, cot = _inputs(1, 2048, 4, 256, 256, 128, seed=11, dtype=torch.bfloat16, state=False)
+    ref = _oracle_grads(x, init, cot, False, 64)
+    got = _gpu_grads(x, init, cot, False, 64)
+    for name, r in ref.items():
+        m = metrics(got[name].float(), r)
+        print(f"config-1 grad {name}: rrms {m['rrms']:.3e}")
+        assert m["rrms"] < _bar(name, torch.bfloat16), f"{name}: {m}"
+
+
+def test_model_training_step_matches_oracle():
+    """One training step's gradients through CyclicFlowAttentionForCausalLM
+    (tiny config, fp32 parameters, the shifted cross-entropy of the model's
+    forward with labels) against float64 autograd through the model oracle:
+    the embedding, the block norms, every attention and MLP parameter and
+    the lm_head. The layer runs 32-token chunks, so its op takes the fp32
+    general forward (no bf16 rounding of q, k, v; the backward is the same
+    cyfa_chunk_bwd), and every gradient must match to rrms 1e-3 -- also the
+    one-element d_proj bias, whose gradient is a sum over tokens that cancels
+    to about 1/250 of its terms' magnitude, beyond what a bf16 forward can
+    resolve (the tuned bf16 forward under training is covered by
+    test_layer_backward_matches_oracle)."""
+    from cyclic_flow_attention.utils import initialize_model, read_config
+    from oracle import model_oracle as MO
+
+    config = read_config("tiny.json")
+    model = initialize_model(config, std=0.02, seed=2).float().to(DEV).train()
+    for layer in model.model.layers:
+        layer.attn.chunk_size = 32
+    cfg = {k: getattr(config, k) for k in config.__dataclass_fields__}
+    gen = torch.Generator().manual_seed(6)
+    ids = torch.randint(0, cfg["vocab_size"], (2, 100), generator=gen)
+    params = {k: v.detach().double().cpu().requires_grad_(True) for k, v in model.named_parameters()}
+    logits, _ = MO.causal_lm(params, cfg, ids, mode="exact", chunk_size=32)
+    loss = torch.nn.functional.cross_entropy(logits[:, :-1].reshape(-1, logits.shape[-1]), ids[:, 1:].reshape(-1))
+    loss.backward()
+    out = model(ids.to(DEV), labels=ids.to(DEV))
+    out["loss"].backward()
+    torch.cuda.synchronize()
+    assert abs(out["loss"].item() - loss.item()) < 1e-5 * abs(loss.item())
+    for name, p in model.named_parameters():
+        assert p.grad is not None, name
+        m = metrics(p.grad.float(), params[name].grad)
+        print(f"model grad {name}: rrms {m['rrms']:.3e}")
+        assert m["rrms"] < 1e-3, f"model {name} gradient: {m}"
