@@ -31,6 +31,9 @@ L2-normalised, log alpha = logsigmoid(N(3, 1)); HIP events around each launch;
 algorithmic bytes (q, k, v, g in, o out) against 8 TB/s.
 long_context: configuration 5 (CyFA-1.4B, B=1, a 16384-token prefill, 512
 greedy decode steps) with the op's and the decode layer kernel's fractions.
+measured_peaks: the box's achievable rates measured in the same run (a bf16
+8192^3 GEMM through hipBLASLt and a 1 GiB device copy); each roofline also
+gives its fraction of them (frac_of_measured) beside the vendor-peak frac.
 backward: the chunk op's backward pass (cyfa_chunk_bwd: fp32 recompute and
 adjoints) at configuration 3's attention shape (B=8, T=2048, H=4, K=V=256,
 128 slots) with bf16 q, k, v and a bf16 cotangent of o; HIP events around each
@@ -90,6 +93,8 @@ def parse():
                     help="skip configuration 5: CyFA-1.4B, B=1, a 16384-token prefill, then 512 greedy "
                          "decode steps (reported under 'long_context')")
     ap.add_argument("--no-backward", action="store_true", help="skip the op's backward-pass timing")
+    ap.add_argument("--no-measured-peaks", action="store_true",
+                    help="skip the bf16 GEMM and copy measurements of the box's achievable rates")
     ap.add_argument("--decode-kernel-only", action="store_true",
                     help="only time the fused decode kernel at the decode shape (for hardware-counter runs)")
     ap.add_argument("--layer-kernel-only", action="store_true",
@@ -203,6 +208,43 @@ def time_backward(B=8, T=2048, H=4, reps=5, warmup=2):
             torch.autograd.grad(o, leaves, d_o)
         res = timer.results()
     return statistics.fmean(res["cyfa_chunk_fwd"]), statistics.fmean(res["cyfa_chunk_bwd"])
+
+
+def measured_peaks(reps=10):
+    """The box's achievable rates, measured next to the results: a bf16 GEMM
+    of 8192 x 8192 x 8192 through the library (hipBLASLt, matrix cores) and a
+    device-to-device copy of 1 GiB (read + write), each the median of reps."""
+    import torch
+
+    a = torch.randn(8192, 8192, device="cuda").bfloat16()
+    b = torch.randn(8192, 8192, device="cuda").bfloat16()
+    src = torch.empty(1 << 28, device="cuda")  # 1 GiB of fp32
+    dst = torch.empty_like(src)
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        ms = []
+        for _ in range(reps):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            fn()
+            end.record()
+            end.synchronize()
+            ms.append(start.elapsed_time(end))
+        return statistics.median(ms)
+
+    gemm_ms = timed(lambda: torch.matmul(a, b))
+    copy_ms = timed(lambda: dst.copy_(src))
+    del a, b, src, dst
+    torch.cuda.empty_cache()
+    return {
+        "bf16_gemm": {"achieved": round(2 * 8192 ** 3 / (gemm_ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s",
+                      "what": "torch.matmul bf16 8192 x 8192 x 8192 (hipBLASLt), median of 10"},
+        "hbm_copy": {"achieved": round(2 * (1 << 30) / (copy_ms * 1e-3) / 1e9, 1), "unit": "GB/s",
+                     "what": "device copy of 1 GiB fp32 (read + write bytes), median of 10"},
+    }
 
 
 def time_decode(model, prompt, steps, warmup):
@@ -553,6 +595,16 @@ def main():
             },
         }
         del prompt
+
+    if not args.no_measured_peaks:
+        peaks = measured_peaks()
+        gemm, copy = peaks["bf16_gemm"]["achieved"], peaks["hbm_copy"]["achieved"]
+        result["measured_peaks"] = peaks
+        result["roofline"]["frac_of_measured"] = round(achieved / gemm, 4)
+        result["roofline"]["hbm"]["frac_of_measured"] = round(op_gbs / copy, 4)
+        if "decode" in result:
+            result["decode"]["roofline"]["frac_of_measured"] = round(result["decode"]["roofline"]["achieved"] / copy, 4)
+        log(f"measured peaks: bf16 GEMM {gemm:,.1f} TFLOP/s, copy {copy:,.0f} GB/s")
 
     if not args.no_isolated:
         iso = {"workload": "scalar_la, configuration 2: B=8, H=4, T=4096, zero initial state"}
