@@ -261,109 +261,178 @@ __global__ __launch_bounds__(256) void bw_state_scan_kernel(StateScanArgs p) {
     }
 }
 
-// Masked, decayed scores of one chunk into P: P[t][s] = [s <= t] e^{G_t - G_s}
-// sum_j X_t[j] Y_s[j] (X, Y: the chunk's 64 rows, D wide), from 64-wide
-// blocks of both staged in LDS; a thread forms a 4 x 4 block of (t, s).
-__device__ __forceinline__ void chunk_scores(const float* X, const float* Y, int D, const float* sG,
-                                             float (*sXs)[BC + 1], float (*sYs)[BC + 1], float (*P)[BC + 1]) {
-    const int tid = threadIdx.x, tb = 4 * (tid >> 4), sb = 4 * (tid & 15);
-    float acc[4][4] = {};
-    for (int d0 = 0; d0 < D; d0 += BC) {
-        __syncthreads();  // the staging tiles are free
-        for (int e = tid; e < BC * BC; e += 256) {
-            const int t = e / BC, d = e % BC;
-            const bool in = d0 + d < D;
-            sXs[t][d] = in ? X[(size_t)t * D + d0 + d] : 0.f;
-            sYs[t][d] = in ? Y[(size_t)t * D + d0 + d] : 0.f;
-        }
-        __syncthreads();
-        for (int d = 0; d < BC; d++) {
-            float xv[4], yv[4];
+// Tile GEMMs of the chunk kernels: a 64 x 64 output tile (rows = the chunk's
+// tokens, columns = 64 coordinates), acc[a][b] per thread at (TileMap<MF>::row,
+// TileMap<MF>::col), accumulated over a contraction of Kd in k-blocks of 32
+// staged through LDS, the next k-block's operands prefetched into registers
+// while the current one is multiplied. fa(i, kk) and fb(kk, j) read the
+// operands; B_KCONTIG says whether fb is contiguous along kk (else along j).
+//  - MF false (fp32 operands): fp32 FMA, a 4 x 4 block per thread (rows
+//    4 (tid / 16) .., columns 4 (tid % 16) ..), A staged transposed so a
+//    thread's four rows are one float4.
+//  - MF true (bf16 operands): matrix cores at near-fp32 accuracy: each fp32
+//    operand is split into hi = bf16(x) and lo = bf16(x - hi), staged in LDS,
+//    and a.b formed as lo_a hi_b + hi_a lo_b + hi_a hi_b on
+//    v_mfma_f32_16x16x32_bf16 with fp32 accumulation (about 16 mantissa
+//    bits; the dropped lo_a lo_b is 2^-16 relative): wave w forms rows 16 w
+//    .. + 16 as four 16 x 16 blocks, acc[nb][i] = tile[16 w + 4 (lane / 16) +
+//    i][16 nb + lane % 16]. The kernels are bound by the staging, not the
+//    matrix cores, so the three products cost about what one does.
+constexpr int GT_K = 32, GT_LD = 68;  // fp32 staging: [32][68] per operand
+constexpr int MT_LD = 40;             // bf16 staging: [64][40] per operand (32 k + 8 pad)
+constexpr int STAGE_BYTES = 4 * BC * MT_LD * 2;  // >= the fp32 staging's 2 * GT_K * GT_LD * 4
+static_assert(STAGE_BYTES >= 2 * GT_K * GT_LD * 4, "staging must hold either form");
+
+template <bool MF>
+struct TileMap {
+    __device__ static int row(int a, int b) {
+        if constexpr (MF)
+            return 16 * (threadIdx.x >> 6) + 4 * ((threadIdx.x & 63) >> 4) + b;
+        else
+            return 4 * (threadIdx.x >> 4) + a;
+    }
+    __device__ static int col(int a, int b) {
+        if constexpr (MF)
+            return 16 * a + (threadIdx.x & 15);
+        else
+            return 4 * (threadIdx.x & 15) + b;
+    }
+};
+
+template <bool MF, bool B_KCONTIG, class FA, class FB>
+__device__ __forceinline__ void tile_gemm(FA fa, FB fb, int Kd, unsigned char* stage, float acc[4][4]) {
+    const int tid = threadIdx.x;
+    if constexpr (!MF) {
+        float(*sa)[GT_LD] = reinterpret_cast<float(*)[GT_LD]>(stage);
+        float(*sb)[GT_LD] = reinterpret_cast<float(*)[GT_LD]>(stage + GT_K * GT_LD * 4);
+        constexpr int NE = BC * GT_K / 256;  // staged elements of each operand per thread
+        const int ti = 4 * (tid >> 4), tj = 4 * (tid & 15);
+        float ra[NE], rb[NE];
+        const auto fetch = [&](int k0) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                xv[i] = sXs[tb + i][d];
-                yv[i] = sYs[sb + i][d];
+            for (int x = 0; x < NE; x++) {
+                const int e = tid + 256 * x;
+                const int ka = e % GT_K, i = e / GT_K;
+                ra[x] = k0 + ka < Kd ? fa(i, k0 + ka) : 0.f;
+                const int kb = B_KCONTIG ? e % GT_K : e / BC, j = B_KCONTIG ? e / GT_K : e % BC;
+                rb[x] = k0 + kb < Kd ? fb(k0 + kb, j) : 0.f;
             }
+        };
+        fetch(0);
+        for (int k0 = 0; k0 < Kd; k0 += GT_K) {
+            __syncthreads();  // the staging tiles are free
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = fmaf(xv[i], yv[j], acc[i][j]);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int t = tb + i, s = sb + j;
-            P[t][s] = s <= t ? acc[i][j] * expf(sG[t] - sG[s]) : 0.f;
-        }
-}
-
-// acc[i][j] += sum_kk A(ti + i, kk) B(kk, tj + j) over kk in [0, Kd) for this
-// thread's 4 x 4 block (ti = 4 (tid / 16), tj = 4 (tid % 16)) of a 64 x 64
-// output tile: both operands staged through LDS in k-blocks of 32 (A
-// transposed, so a thread's four rows are one float4), 16 FMAs per two
-// float4 reads. fa(i, kk) and fb(kk, j) read the operands; B_KCONTIG says
-// whether fb is contiguous along kk (else along j), which picks the staging
-// order that keeps the reads coalesced. Every thread of the block calls it.
-constexpr int GT_K = 32, GT_LD = 68;
-template <bool B_KCONTIG, class FA, class FB>
-__device__ __forceinline__ void tile_gemm(FA fa, FB fb, int Kd, float (*sa)[GT_LD], float (*sb)[GT_LD],
-                                          float acc[4][4]) {
-    constexpr int NE = BC * GT_K / 256;  // staged elements of each operand per thread
-    const int tid = threadIdx.x, ti = 4 * (tid >> 4), tj = 4 * (tid & 15);
-    float ra[NE], rb[NE];
-    // the next k-block's operands go to registers while the current one is multiplied
-    const auto fetch = [&](int k0) {
-#pragma unroll
-        for (int x = 0; x < NE; x++) {
-            const int e = tid + 256 * x;
-            const int ka = e % GT_K, i = e / GT_K;
-            ra[x] = k0 + ka < Kd ? fa(i, k0 + ka) : 0.f;
-            const int kb = B_KCONTIG ? e % GT_K : e / BC, j = B_KCONTIG ? e / GT_K : e % BC;
-            rb[x] = k0 + kb < Kd ? fb(k0 + kb, j) : 0.f;
-        }
-    };
-    fetch(0);
-    for (int k0 = 0; k0 < Kd; k0 += GT_K) {
-        __syncthreads();  // the staging tiles are free
-#pragma unroll
-        for (int x = 0; x < NE; x++) {
-            const int e = tid + 256 * x;
-            sa[e % GT_K][e / GT_K] = ra[x];
-            if (B_KCONTIG)
-                sb[e % GT_K][e / GT_K] = rb[x];
-            else
-                sb[e / BC][e % BC] = rb[x];
-        }
-        __syncthreads();
-        if (k0 + GT_K < Kd) fetch(k0 + GT_K);
+            for (int x = 0; x < NE; x++) {
+                const int e = tid + 256 * x;
+                sa[e % GT_K][e / GT_K] = ra[x];
+                if (B_KCONTIG)
+                    sb[e % GT_K][e / GT_K] = rb[x];
+                else
+                    sb[e / BC][e % BC] = rb[x];
+            }
+            __syncthreads();
+            if (k0 + GT_K < Kd) fetch(k0 + GT_K);
 #pragma unroll 8
-        for (int kk = 0; kk < GT_K; kk++) {
-            const float4 av = *reinterpret_cast<const float4*>(&sa[kk][ti]);
-            const float4 bv = *reinterpret_cast<const float4*>(&sb[kk][tj]);
-            const float ar[4] = {av.x, av.y, av.z, av.w}, br[4] = {bv.x, bv.y, bv.z, bv.w};
+            for (int kk = 0; kk < GT_K; kk++) {
+                const float4 av = *reinterpret_cast<const float4*>(&sa[kk][ti]);
+                const float4 bv = *reinterpret_cast<const float4*>(&sb[kk][tj]);
+                const float ar[4] = {av.x, av.y, av.z, av.w}, br[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+                for (int i = 0; i < 4; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = fmaf(ar[i], br[j], acc[i][j]);
+                    for (int j = 0; j < 4; j++) acc[i][j] = fmaf(ar[i], br[j], acc[i][j]);
+            }
+        }
+    } else {
+        bf16_t* sah = reinterpret_cast<bf16_t*>(stage);  // hi and lo parts of A and of B
+        bf16_t* sal = sah + BC * MT_LD;
+        bf16_t* sbh = sal + BC * MT_LD;
+        bf16_t* sbl = sbh + BC * MT_LD;
+        const int l = tid & 63, w = tid >> 6, lr = l & 15, lg = l >> 4;
+        const int r = tid >> 2, kg = tid & 3;  // staging: row r, k-group kg (8 k)
+        float ra[8], rb[8];
+        const auto fetch = [&](int k0) {
+#pragma unroll
+            for (int x = 0; x < 8; x++) {
+                const int kk = k0 + 8 * kg + x;
+                ra[x] = kk < Kd ? fa(r, kk) : 0.f;
+                rb[x] = kk < Kd ? fb(kk, r) : 0.f;
+            }
+        };
+        fetch(0);
+        for (int k0 = 0; k0 < Kd; k0 += GT_K) {
+            __syncthreads();  // the staging tiles are free
+            bf16x8 vah, val, vbh, vbl;
+#pragma unroll
+            for (int x = 0; x < 8; x++) {
+                vah[x] = (bf16_t)ra[x];
+                val[x] = (bf16_t)(ra[x] - (float)vah[x]);
+                vbh[x] = (bf16_t)rb[x];
+                vbl[x] = (bf16_t)(rb[x] - (float)vbh[x]);
+            }
+            const int so = r * MT_LD + 8 * kg;
+            *reinterpret_cast<bf16x8*>(sah + so) = vah;
+            *reinterpret_cast<bf16x8*>(sal + so) = val;
+            *reinterpret_cast<bf16x8*>(sbh + so) = vbh;
+            *reinterpret_cast<bf16x8*>(sbl + so) = vbl;
+            __syncthreads();
+            if (k0 + GT_K < Kd) fetch(k0 + GT_K);
+            const int ao = (16 * w + lr) * MT_LD + 8 * lg;
+            const bf16x8 ah = *reinterpret_cast<const bf16x8*>(sah + ao);
+            const bf16x8 al = *reinterpret_cast<const bf16x8*>(sal + ao);
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++) {
+                const int bo = (16 * nb + lr) * MT_LD + 8 * lg;
+                const bf16x8 bh = *reinterpret_cast<const bf16x8*>(sbh + bo);
+                const bf16x8 bl = *reinterpret_cast<const bf16x8*>(sbl + bo);
+                f32x4 c = {acc[nb][0], acc[nb][1], acc[nb][2], acc[nb][3]};
+                c = mfma_bf16(al, bh, c);
+                c = mfma_bf16(ah, bl, c);
+                c = mfma_bf16(ah, bh, c);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[nb][i] = c[i];
+            }
         }
     }
 }
 
-// Writes this thread's 4 x 4 block of a 64 x 64 tile (rows = the chunk's
-// tokens, columns d0 ..) into head-major rows dst [.., D], times the row
-// factor f(t) and a scale.
-template <class F>
-__device__ __forceinline__ void tile_store(float acc[4][4], float* dst, int D, int d0, F f) {
-    const int tid = threadIdx.x, ti = 4 * (tid >> 4), tj = 4 * (tid & 15);
+// acc[a][b] *= f(row of (a, b)).
+template <bool MF, class F>
+__device__ __forceinline__ void tile_scale_rows(float acc[4][4], F f) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float fr = f(ti + i);
+    for (int a = 0; a < 4; a++)
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (d0 + tj + j < D) dst[(size_t)(ti + i) * D + d0 + tj + j] = fr * acc[i][j];
-    }
+        for (int b = 0; b < 4; b++) acc[a][b] *= f(TileMap<MF>::row(a, b));
+}
+
+// Writes this thread's part of a 64 x 64 tile (columns d0 ..) into head-major
+// rows dst [.., D], times a scale.
+template <bool MF>
+__device__ __forceinline__ void tile_store(float acc[4][4], float* dst, int D, int d0, float scale) {
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int t = TileMap<MF>::row(a, b), c = d0 + TileMap<MF>::col(a, b);
+            if (c < D) dst[(size_t)t * D + c] = scale * acc[a][b];
+        }
+}
+
+// Masked, decayed scores of one chunk into P: P[t][s] = [s <= t] e^{G_t - G_s}
+// sum_j X_t[j] Y_s[j] (X, Y: the chunk's 64 rows, D wide), as one tile GEMM.
+template <bool MF>
+__device__ __forceinline__ void chunk_scores(const float* X, const float* Y, int D, const float* sG,
+                                             unsigned char* stage, float (*P)[BC + 1]) {
+    float acc[4][4] = {};
+    tile_gemm<MF, true>([&](int i, int kk) { return X[(size_t)i * D + kk]; },
+                        [&](int kk, int j) { return Y[(size_t)j * D + kk]; }, D, stage, acc);
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int t = TileMap<MF>::row(a, b), s = TileMap<MF>::col(a, b);
+            P[t][s] = s <= t ? acc[a][b] * expf(sG[t] - sG[s]) : 0.f;
+        }
 }
 
 // The pass-1 output of the recomputed forward, chunk-parallel (grid (N, H,
@@ -378,14 +447,10 @@ struct OutArgs {
     float scale;
 };
 
+template <bool MF>
 __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
     __shared__ float sA[BC][BC + 1];
-    // staging: the score tiles first, then the GEMM tiles in the same bytes
-    __shared__ __align__(16) float sStage[2 * BC * (BC + 1)];
-    float(*sXs)[BC + 1] = reinterpret_cast<float(*)[BC + 1]>(sStage);
-    float(*sYs)[BC + 1] = reinterpret_cast<float(*)[BC + 1]>(sStage + BC * (BC + 1));
-    float(*sa)[GT_LD] = reinterpret_cast<float(*)[GT_LD]>(sStage);
-    float(*sb)[GT_LD] = reinterpret_cast<float(*)[GT_LD]>(sStage + GT_K * GT_LD);
+    __shared__ __align__(16) unsigned char sStage[STAGE_BYTES];
     __shared__ float sG[BC], sEq[BC];
     const int tid = threadIdx.x, n = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int Kq = a.Kq, Vd = a.Vd, t0 = n * BC;
@@ -398,22 +463,18 @@ __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
         sG[tid] = chunk_gam(a.g, b, h, a.T, a.H, n, tid);
         sEq[tid] = expf(sG[tid]);
     }
-    chunk_scores(q, k, Kq, sG, sXs, sYs, sA);
+    chunk_scores<MF>(q, k, Kq, sG, sStage, sA);
     float* out = a.out + (bh * a.Tp + t0) * Vd;
     for (int d0 = 0; d0 < Vd; d0 += BC) {
         float acc[4][4] = {};
-        tile_gemm<false>([&](int i, int kk) { return q[(size_t)i * Kq + kk]; },
-                         [&](int kk, int j) { return d0 + j < Vd ? S[(size_t)kk * Vd + d0 + j] : 0.f; }, Kq, sa, sb,
-                         acc);
-        const int ti = 4 * (tid >> 4);
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) acc[i][jj] *= sEq[ti + i];
-        tile_gemm<false>([&](int i, int kk) { return sA[i][kk]; },
-                         [&](int kk, int j) { return d0 + j < Vd ? v[(size_t)kk * Vd + d0 + j] : 0.f; }, BC, sa, sb,
-                         acc);
-        tile_store(acc, out, Vd, d0, [&](int) { return a.scale; });
+        tile_gemm<MF, false>([&](int i, int kk) { return q[(size_t)i * Kq + kk]; },
+                             [&](int kk, int j) { return d0 + j < Vd ? S[(size_t)kk * Vd + d0 + j] : 0.f; }, Kq,
+                             sStage, acc);
+        tile_scale_rows<MF>(acc, [&](int t) { return sEq[t]; });
+        tile_gemm<MF, false>([&](int i, int kk) { return sA[i][kk]; },
+                             [&](int kk, int j) { return d0 + j < Vd ? v[(size_t)kk * Vd + d0 + j] : 0.f; }, BC,
+                             sStage, acc);
+        tile_store<MF>(acc, out, Vd, d0, a.scale);
     }
 }
 
@@ -430,14 +491,10 @@ struct ChunkGradArgs {
     float scale;
 };
 
+template <bool MF>
 __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     __shared__ float sA[BC][BC + 1], sB[BC][BC + 1];
-    // staging: the score tiles first, then the GEMM tiles in the same bytes
-    __shared__ __align__(16) float sStage[2 * BC * (BC + 1)];
-    float(*sXs)[BC + 1] = reinterpret_cast<float(*)[BC + 1]>(sStage);
-    float(*sYs)[BC + 1] = reinterpret_cast<float(*)[BC + 1]>(sStage + BC * (BC + 1));
-    float(*sa)[GT_LD] = reinterpret_cast<float(*)[GT_LD]>(sStage);
-    float(*sb)[GT_LD] = reinterpret_cast<float(*)[GT_LD]>(sStage + GT_K * GT_LD);
+    __shared__ __align__(16) unsigned char sStage[STAGE_BYTES];
     __shared__ float sG[BC], sEq[BC], sEl[BC];
     const int tid = threadIdx.x, n = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int Kq = a.Kq, Vd = a.Vd, t0 = n * BC;
@@ -454,55 +511,45 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
         sEq[tid] = expf(G);
         sEl[tid] = expf(__shfl(G, BC - 1) - G);
     }
-    chunk_scores(q, k, Kq, sG, sXs, sYs, sA);
-    chunk_scores(dO, v, Vd, sG, sXs, sYs, sB);
-    const int ti = 4 * (tid >> 4);
+    chunk_scores<MF>(q, k, Kq, sG, sStage, sA);
+    chunk_scores<MF>(dO, v, Vd, sG, sStage, sB);
     const float sc = a.scale;
     for (int d0 = 0; d0 < Kq; d0 += BC) {
         // dq = scale (e^{G_t} dO_t S_n^T + B k)
         float acc[4][4] = {};
-        tile_gemm<true>([&](int i, int kk) { return dO[(size_t)i * Vd + kk]; },
-                        [&](int kk, int j) { return d0 + j < Kq ? S[(size_t)(d0 + j) * Vd + kk] : 0.f; }, Vd, sa, sb,
-                        acc);
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) acc[i][jj] *= sEq[ti + i];
-        tile_gemm<false>([&](int i, int kk) { return sB[i][kk]; },
-                         [&](int kk, int j) { return d0 + j < Kq ? k[(size_t)kk * Kq + d0 + j] : 0.f; }, BC, sa, sb,
-                         acc);
-        tile_store(acc, a.dq + (bh * a.Tp + t0) * Kq, Kq, d0, [&](int) { return sc; });
+        tile_gemm<MF, true>([&](int i, int kk) { return dO[(size_t)i * Vd + kk]; },
+                            [&](int kk, int j) { return d0 + j < Kq ? S[(size_t)(d0 + j) * Vd + kk] : 0.f; }, Vd,
+                            sStage, acc);
+        tile_scale_rows<MF>(acc, [&](int t) { return sEq[t]; });
+        tile_gemm<MF, false>([&](int i, int kk) { return sB[i][kk]; },
+                             [&](int kk, int j) { return d0 + j < Kq ? k[(size_t)kk * Kq + d0 + j] : 0.f; }, BC,
+                             sStage, acc);
+        tile_store<MF>(acc, a.dq + (bh * a.Tp + t0) * Kq, Kq, d0, sc);
         // dk = e^{G_last - G_s} v_s D_{n+1}^T + scale B^T q
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int x = 0; x < 4; x++)
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) acc[i][jj] = 0.f;
-        tile_gemm<true>([&](int i, int kk) { return v[(size_t)i * Vd + kk]; },
-                        [&](int kk, int j) { return d0 + j < Kq ? D[(size_t)(d0 + j) * Vd + kk] : 0.f; }, Vd, sa, sb,
-                        acc);
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) acc[i][jj] *= sEl[ti + i];
-        tile_gemm<false>([&](int i, int kk) { return sc * sB[kk][i]; },
-                         [&](int kk, int j) { return d0 + j < Kq ? q[(size_t)kk * Kq + d0 + j] : 0.f; }, BC, sa, sb,
-                         acc);
-        tile_store(acc, a.dk + (bh * a.Tp + t0) * Kq, Kq, d0, [&](int) { return 1.f; });
+            for (int y = 0; y < 4; y++) acc[x][y] = 0.f;
+        tile_gemm<MF, true>([&](int i, int kk) { return v[(size_t)i * Vd + kk]; },
+                            [&](int kk, int j) { return d0 + j < Kq ? D[(size_t)(d0 + j) * Vd + kk] : 0.f; }, Vd,
+                            sStage, acc);
+        tile_scale_rows<MF>(acc, [&](int t) { return sEl[t]; });
+        tile_gemm<MF, false>([&](int i, int kk) { return sc * sB[kk][i]; },
+                             [&](int kk, int j) { return d0 + j < Kq ? q[(size_t)kk * Kq + d0 + j] : 0.f; }, BC,
+                             sStage, acc);
+        tile_store<MF>(acc, a.dk + (bh * a.Tp + t0) * Kq, Kq, d0, 1.f);
     }
     for (int d0 = 0; d0 < Vd; d0 += BC) {
         // dv = e^{G_last - G_s} k_s D_{n+1} + scale A^T dO
         float acc[4][4] = {};
-        tile_gemm<false>([&](int i, int kk) { return k[(size_t)i * Kq + kk]; },
-                         [&](int kk, int j) { return d0 + j < Vd ? D[(size_t)kk * Vd + d0 + j] : 0.f; }, Kq, sa, sb,
-                         acc);
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) acc[i][jj] *= sEl[ti + i];
-        tile_gemm<false>([&](int i, int kk) { return sc * sA[kk][i]; },
-                         [&](int kk, int j) { return d0 + j < Vd ? dO[(size_t)kk * Vd + d0 + j] : 0.f; }, BC, sa, sb,
-                         acc);
-        tile_store(acc, a.dv + (bh * a.Tp + t0) * Vd, Vd, d0, [&](int) { return 1.f; });
+        tile_gemm<MF, false>([&](int i, int kk) { return k[(size_t)i * Kq + kk]; },
+                             [&](int kk, int j) { return d0 + j < Vd ? D[(size_t)kk * Vd + d0 + j] : 0.f; }, Kq,
+                             sStage, acc);
+        tile_scale_rows<MF>(acc, [&](int t) { return sEl[t]; });
+        tile_gemm<MF, false>([&](int i, int kk) { return sc * sA[kk][i]; },
+                             [&](int kk, int j) { return d0 + j < Vd ? dO[(size_t)kk * Vd + d0 + j] : 0.f; }, BC,
+                             sStage, acc);
+        tile_store<MF>(acc, a.dv + (bh * a.Tp + t0) * Vd, Vd, d0, 1.f);
     }
 }
 
@@ -976,8 +1023,11 @@ dim3 scan_grid(int Vd, int Kq, int BH) {
     return dim3((Vd + BW_TILE - 1) / BW_TILE, (Kq + SCAN_ROWS - 1) / SCAN_ROWS, BH);
 }
 
-void launch_chunk_grad(const ChunkGradArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(bw_chunk_kernel, dim3(a.N, a.H, a.B), dim3(256), 0, stream, a);
+void launch_chunk_grad(const ChunkGradArgs& a, bool mfma, hipStream_t stream) {
+    if (mfma)
+        hipLaunchKernelGGL(bw_chunk_kernel<true>, dim3(a.N, a.H, a.B), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(bw_chunk_kernel<false>, dim3(a.N, a.H, a.B), dim3(256), 0, stream, a);
 }
 
 }  // namespace
@@ -1040,7 +1090,10 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     oa.Vd = M;
     oa.N = N;
     oa.scale = p.scale;
-    hipLaunchKernelGGL(bw_out_kernel, dim3(N, H, B), blk, 0, stream, oa);
+    if (bf)
+        hipLaunchKernelGGL(bw_out_kernel<true>, dim3(N, H, B), blk, 0, stream, oa);
+    else
+        hipLaunchKernelGGL(bw_out_kernel<false>, dim3(N, H, B), blk, 0, stream, oa);
     hipLaunchKernelGGL(bw_fwd_readout_kernel, dim3((B * Tp + 31) / 32, H), blk, 0, stream, ws.raw, ws.cs, ws.sn,
                        p.table, B, Tp, H, M, ws.wts);
     StateScanArgs f2 = f1;
@@ -1080,7 +1133,7 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     c2.Vd = V;
     c2.N = N;
     c2.scale = 1.f;
-    launch_chunk_grad(c2, stream);
+    launch_chunk_grad(c2, bf, stream);
     // the readout: the pass-1 output's cotangent, the clock's share and the table's
     ReadoutGradArgs ro{};
     ro.raw = ws.raw;
@@ -1120,7 +1173,7 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     c1.Kq = K;
     c1.Vd = M;
     c1.scale = p.scale;
-    launch_chunk_grad(c1, stream);
+    launch_chunk_grad(c1, bf, stream);
     // gates, write vector and clock
     TokenGradArgs tg{};
     tg.qh = ws.qh;
