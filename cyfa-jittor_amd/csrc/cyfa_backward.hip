@@ -563,6 +563,7 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
     constexpr int LD = BWD_MAX_M + 1, RB = 32;
     __shared__ float sTab[BWD_MAX_M * LD];  // rows R .. 127 zero
     __shared__ float sZ[RB][LD], sP[RB][LD];
+    __shared__ float sCs[RB][BWD_MAX_M / 2], sSn[RB][BWD_MAX_M / 2];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, h = blockIdx.y;
     const int R = M - 1, P = M / 2, rows = B * Tp, b0 = blockIdx.x * RB;
     for (int e = tid; e < BWD_MAX_M * LD; e += 256) {
@@ -572,14 +573,17 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
     const auto row_of = [&](int rho) { return ((size_t)(rho / Tp) * H + h) * Tp + rho % Tp; };
     for (int e = tid; e < RB * (BWD_MAX_M / 2); e += 256) {
         const int i = e / (BWD_MAX_M / 2), pr = e % (BWD_MAX_M / 2), rho = b0 + i;
-        float ze = 0.f, zo = 0.f;
+        float ze = 0.f, zo = 0.f, c = 1.f, s = 0.f;
         if (rho < rows && pr < P) {
             const size_t row = row_of(rho);
-            const float c = cs[row * P + pr], s = sn[row * P + pr];
+            c = cs[row * P + pr];
+            s = sn[row * P + pr];
             const float re = raw[row * M + 2 * pr], ro = raw[row * M + 2 * pr + 1];
             ze = c * re - s * ro;
             zo = s * re + c * ro;
         }
+        sCs[i][pr] = c;
+        sSn[i][pr] = s;
         sZ[i][2 * pr] = ze;
         sZ[i][2 * pr + 1] = zo;
     }
@@ -636,7 +640,7 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
         for (int j = 0; j < 4; j += 2) {
             const int pr = (bc + j) >> 1;
             if (pr < P) {
-                const float c = cs[row * P + pr], s = sn[row * P + pr];
+                const float c = sCs[br + i][pr], s = sSn[br + i][pr];
                 wts[row * M + 2 * pr] = c * u[i][j] + s * u[i][j + 1];
                 wts[row * M + 2 * pr + 1] = -s * u[i][j] + c * u[i][j + 1];
             }
@@ -666,6 +670,7 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
     constexpr int LD = BWD_MAX_M + 1;
     __shared__ float sTab[BWD_MAX_M * LD];  // rows R .. 127 zero
     __shared__ float sZ[RO_BLK][LD], sDU[RO_BLK][LD], sP[RO_BLK][LD], sDL[RO_BLK][LD];
+    __shared__ float sCs[RO_BLK][BWD_MAX_M / 2], sSn[RO_BLK][BWD_MAX_M / 2];
     __shared__ float sLam[RO_BLK][32];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, blk = blockIdx.x, h = blockIdx.y;
     const int M = a.M, R = M - 1, P = M / 2, RM = R * M;
@@ -684,10 +689,11 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
         // z = U(lam) raw and du = U(lam) dweights, one (row, pair) per thread step
         for (int e = tid; e < RO_BLK * (BWD_MAX_M / 2); e += 256) {
             const int i = e / (BWD_MAX_M / 2), pr = e % (BWD_MAX_M / 2), rho = b0 + i;
-            float ze = 0.f, zo = 0.f, ue = 0.f, uo = 0.f;
+            float ze = 0.f, zo = 0.f, ue = 0.f, uo = 0.f, c = 1.f, s = 0.f;
             if (rho < rows && pr < P) {
                 const size_t row = ((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp;
-                const float c = a.cs[row * P + pr], s = a.sn[row * P + pr];
+                c = a.cs[row * P + pr];
+                s = a.sn[row * P + pr];
                 const float re = a.raw[row * M + 2 * pr], ro = a.raw[row * M + 2 * pr + 1];
                 const float de = a.dwts[row * M + 2 * pr], dd = a.dwts[row * M + 2 * pr + 1];
                 ze = c * re - s * ro;
@@ -695,6 +701,8 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
                 ue = c * de - s * dd;
                 uo = s * de + c * dd;
             }
+            sCs[i][pr] = c;
+            sSn[i][pr] = s;
             sZ[i][2 * pr] = ze;
             sZ[i][2 * pr + 1] = zo;
             sDU[i][2 * pr] = ue;
@@ -771,19 +779,21 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
                 float dl = 0.f;
                 if (rho < rows) {
                     const size_t row = ((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp;
+                    // With z = U(lam) raw and du = U(lam) dweights, the clock's share
+                    // kappa_p [dz . dU(lam)/dlam raw + dweights . dU(-lam)/dlam u] is
+                    // kappa_p [(z_e dz_o - z_o dz_e) + (du_e u_o - du_o u_e)] (a
+                    // rotation keeps the 2-d cross product), all from LDS and registers.
 #pragma unroll
                     for (int j = 0; j < 4; j += 2) {
                         const int pr = (bc + j) >> 1;
                         if (pr < P) {
-                            const float c = a.cs[row * P + pr], s = a.sn[row * P + pr];
-                            const float re = a.raw[row * M + 2 * pr], ro = a.raw[row * M + 2 * pr + 1];
-                            const float de = a.dwts[row * M + 2 * pr], dd = a.dwts[row * M + 2 * pr + 1];
-                            const float ze = dz[i][j], zo = dz[i][j + 1], ue = u[i][j], uo = u[i][j + 1];
-                            a.draw[row * M + 2 * pr] = c * ze + s * zo;
-                            a.draw[row * M + 2 * pr + 1] = -s * ze + c * zo;
-                            dl += (float)(kTwoPiBw * pr / R) *
-                                  (ze * (-s * re - c * ro) + zo * (c * re - s * ro) + de * (-s * ue + c * uo) +
-                                   dd * (-c * ue - s * uo));
+                            const float c = sCs[br + i][pr], s = sSn[br + i][pr];
+                            const float ge = dz[i][j], go = dz[i][j + 1], ue = u[i][j], uo = u[i][j + 1];
+                            a.draw[row * M + 2 * pr] = c * ge + s * go;
+                            a.draw[row * M + 2 * pr + 1] = -s * ge + c * go;
+                            const float ze = sZ[br + i][2 * pr], zo = sZ[br + i][2 * pr + 1];
+                            const float de = sDU[br + i][2 * pr], dd = sDU[br + i][2 * pr + 1];
+                            dl += (float)(kTwoPiBw * pr / R) * ((ze * go - zo * ge) + (de * uo - dd * ue));
                         }
                     }
                 }
