@@ -556,93 +556,97 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
 // The slot readout of the recomputed forward (fp32, unrounded) for blocks of
 // 32 rows of one head: z = U(lam) raw, l = z table^T, p = softmax(l),
 // u = p table, weights = U(-lam) u; the two products as small GEMMs against
-// the staged table (4 x 4 per thread). Grid (ceil(B Tp / 32), H), 256 threads.
+// the staged table (4 x 4 per thread). Grid (ceil(B Tp / (32 per_wg)), H),
+// 256 threads: a workgroup stages the table once and takes per_wg blocks.
 __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, const float* cs, const float* sn,
                                                              const float* table, int B, int Tp, int H, int M,
-                                                             float* wts) {
+                                                             int per_wg, float* wts) {
     constexpr int LD = BWD_MAX_M + 1, RB = 32;
     __shared__ float sTab[BWD_MAX_M * LD];  // rows R .. 127 zero
     __shared__ float sZ[RB][LD], sP[RB][LD];
     __shared__ float sCs[RB][BWD_MAX_M / 2], sSn[RB][BWD_MAX_M / 2];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, h = blockIdx.y;
-    const int R = M - 1, P = M / 2, rows = B * Tp, b0 = blockIdx.x * RB;
+    const int R = M - 1, P = M / 2, rows = B * Tp;
     for (int e = tid; e < BWD_MAX_M * LD; e += 256) {
         const int r = e / LD, m = e % LD;
         sTab[e] = (r < R && m < M) ? table[((size_t)h * R + r) * M + m] : 0.f;
     }
     const auto row_of = [&](int rho) { return ((size_t)(rho / Tp) * H + h) * Tp + rho % Tp; };
-    for (int e = tid; e < RB * (BWD_MAX_M / 2); e += 256) {
-        const int i = e / (BWD_MAX_M / 2), pr = e % (BWD_MAX_M / 2), rho = b0 + i;
-        float ze = 0.f, zo = 0.f, c = 1.f, s = 0.f;
-        if (rho < rows && pr < P) {
-            const size_t row = row_of(rho);
-            c = cs[row * P + pr];
-            s = sn[row * P + pr];
-            const float re = raw[row * M + 2 * pr], ro = raw[row * M + 2 * pr + 1];
-            ze = c * re - s * ro;
-            zo = s * re + c * ro;
-        }
-        sCs[i][pr] = c;
-        sSn[i][pr] = s;
-        sZ[i][2 * pr] = ze;
-        sZ[i][2 * pr + 1] = zo;
-    }
-    __syncthreads();
     const int br = 4 * (tid >> 5), bc = 4 * (tid & 31);
-    {
-        float l[4][4] = {};
-        for (int m = 0; m < M; m++) {
-            float zv[4], tv[4];
+    for (int b0 = blockIdx.x * per_wg * RB; b0 < min(rows, (blockIdx.x + 1) * per_wg * RB); b0 += RB) {
+        __syncthreads();  // the table is staged; the previous block's tiles are done with
+        for (int e = tid; e < RB * (BWD_MAX_M / 2); e += 256) {
+            const int i = e / (BWD_MAX_M / 2), pr = e % (BWD_MAX_M / 2), rho = b0 + i;
+            float ze = 0.f, zo = 0.f, c = 1.f, s = 0.f;
+            if (rho < rows && pr < P) {
+                const size_t row = row_of(rho);
+                c = cs[row * P + pr];
+                s = sn[row * P + pr];
+                const float re = raw[row * M + 2 * pr], ro = raw[row * M + 2 * pr + 1];
+                ze = c * re - s * ro;
+                zo = s * re + c * ro;
+            }
+            sCs[i][pr] = c;
+            sSn[i][pr] = s;
+            sZ[i][2 * pr] = ze;
+            sZ[i][2 * pr + 1] = zo;
+        }
+        __syncthreads();
+        {
+            float l[4][4] = {};
+            for (int m = 0; m < M; m++) {
+                float zv[4], tv[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                zv[i] = sZ[br + i][m];
-                tv[i] = sTab[(bc + i) * LD + m];
+                for (int i = 0; i < 4; i++) {
+                    zv[i] = sZ[br + i][m];
+                    tv[i] = sTab[(bc + i) * LD + m];
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) l[i][j] = fmaf(zv[i], tv[j], l[i][j]);
             }
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) l[i][j] = fmaf(zv[i], tv[j], l[i][j]);
+                for (int j = 0; j < 4; j++) sP[br + i][bc + j] = l[i][j];
         }
+        __syncthreads();
+        for (int i = wv; i < RB; i += 4) {
+            const float l0 = lane < R ? sP[i][lane] : -INFINITY, l1 = lane + 64 < R ? sP[i][lane + 64] : -INFINITY;
+            const float mx = bw_wave_max(fmaxf(l0, l1));
+            const float e0 = lane < R ? expf(l0 - mx) : 0.f, e1 = lane + 64 < R ? expf(l1 - mx) : 0.f;
+            const float inv = 1.f / bw_wave_sum(e0 + e1);
+            sP[i][lane] = e0 * inv;
+            sP[i][lane + 64] = e1 * inv;
+        }
+        __syncthreads();
+        float u[4][4] = {};
+        for (int r = 0; r < R; r++) {
+            float pv[4], t4[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+            for (int i = 0; i < 4; i++) {
+                pv[i] = sP[br + i][r];
+                t4[i] = sTab[r * LD + bc + i];
+            }
 #pragma unroll
-            for (int j = 0; j < 4; j++) sP[br + i][bc + j] = l[i][j];
-    }
-    __syncthreads();
-    for (int i = wv; i < RB; i += 4) {
-        const float l0 = lane < R ? sP[i][lane] : -INFINITY, l1 = lane + 64 < R ? sP[i][lane + 64] : -INFINITY;
-        const float mx = bw_wave_max(fmaxf(l0, l1));
-        const float e0 = lane < R ? expf(l0 - mx) : 0.f, e1 = lane + 64 < R ? expf(l1 - mx) : 0.f;
-        const float inv = 1.f / bw_wave_sum(e0 + e1);
-        sP[i][lane] = e0 * inv;
-        sP[i][lane + 64] = e1 * inv;
-    }
-    __syncthreads();
-    float u[4][4] = {};
-    for (int r = 0; r < R; r++) {
-        float pv[4], t4[4];
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) u[i][j] = fmaf(pv[i], t4[j], u[i][j]);
+        }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            pv[i] = sP[br + i][r];
-            t4[i] = sTab[r * LD + bc + i];
-        }
+            const int rho = b0 + br + i;
+            if (rho >= rows) continue;
+            const size_t row = row_of(rho);
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) u[i][j] = fmaf(pv[i], t4[j], u[i][j]);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int rho = b0 + br + i;
-        if (rho >= rows) continue;
-        const size_t row = row_of(rho);
-#pragma unroll
-        for (int j = 0; j < 4; j += 2) {
-            const int pr = (bc + j) >> 1;
-            if (pr < P) {
-                const float c = sCs[br + i][pr], s = sSn[br + i][pr];
-                wts[row * M + 2 * pr] = c * u[i][j] + s * u[i][j + 1];
-                wts[row * M + 2 * pr + 1] = -s * u[i][j] + c * u[i][j + 1];
+            for (int j = 0; j < 4; j += 2) {
+                const int pr = (bc + j) >> 1;
+                if (pr < P) {
+                    const float c = sCs[br + i][pr], s = sSn[br + i][pr];
+                    wts[row * M + 2 * pr] = c * u[i][j] + s * u[i][j + 1];
+                    wts[row * M + 2 * pr + 1] = -s * u[i][j] + c * u[i][j + 1];
+                }
             }
         }
     }
@@ -656,14 +660,15 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
 // with kappa_p = 2 pi p / (M - 1). Every product over the block is a small
 // GEMM against the head's table (staged once in LDS, rows padded by one
 // float against bank conflicts); a thread forms 4 x 4 output blocks. Grid
-// (ceil(B Tp / 256), H), 256 threads: a workgroup takes 256 rows, eight
-// blocks of 32, and keeps its part of dtable in registers (thread e owns the
-// 4 x 16 block of rows 4 (e / 8) .., columns 16 (e % 8) ..).
-constexpr int RO_BLK = 32;
+// (workgroups per head, H), 256 threads: a workgroup takes per_wg blocks of
+// 32 rows (bwd_ro_per_wg) and keeps its part of dtable in registers (thread e
+// owns the 4 x 16 block of rows 4 (e / 8) .., columns 16 (e % 8) ..).
+constexpr int RO_BLK = BWD_RO_BLOCK;
 struct ReadoutGradArgs {
     const float *raw, *cs, *sn, *table, *dwts;  // head-major rows; table [H, M-1, M]
-    float *draw, *dlam, *dtab;                  // dtab: [H, blocks, (M-1) M]
+    float *draw, *dlam, *dtab;                  // dtab: [H, workgroups, (M-1) M]
     int B, Tp, H, M;
+    int per_wg;                                 // blocks of 32 rows per workgroup
 };
 
 __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
@@ -684,7 +689,7 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
     const int tr = 4 * (tid >> 3), tc = 16 * (tid & 7);
     float dt[4][16] = {};
     const int rows = a.B * a.Tp;
-    for (int b0 = blk * 8 * RO_BLK; b0 < min(rows, (blk + 1) * 8 * RO_BLK); b0 += RO_BLK) {
+    for (int b0 = blk * a.per_wg * RO_BLK; b0 < min(rows, (blk + 1) * a.per_wg * RO_BLK); b0 += RO_BLK) {
         __syncthreads();  // the previous block's tiles are done with
         // z = U(lam) raw and du = U(lam) dweights, one (row, pair) per thread step
         for (int e = tid; e < RO_BLK * (BWD_MAX_M / 2); e += 256) {
@@ -1104,8 +1109,9 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
         hipLaunchKernelGGL(bw_out_kernel<true>, dim3(N, H, B), blk, 0, stream, oa);
     else
         hipLaunchKernelGGL(bw_out_kernel<false>, dim3(N, H, B), blk, 0, stream, oa);
-    hipLaunchKernelGGL(bw_fwd_readout_kernel, dim3((B * Tp + 31) / 32, H), blk, 0, stream, ws.raw, ws.cs, ws.sn,
-                       p.table, B, Tp, H, M, ws.wts);
+    const int ro_per_wg = bwd_ro_per_wg(B, Tp, H);
+    hipLaunchKernelGGL(bw_fwd_readout_kernel, dim3(ws.ro_blocks, H), blk, 0, stream, ws.raw, ws.cs, ws.sn, p.table, B,
+                       Tp, H, M, ro_per_wg, ws.wts);
     StateScanArgs f2 = f1;
     f2.a = ws.w;
     f2.b = ws.vh;
@@ -1158,6 +1164,7 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     ro.Tp = Tp;
     ro.H = H;
     ro.M = M;
+    ro.per_wg = ro_per_wg;
     hipLaunchKernelGGL(bw_readout_kernel, dim3(ws.ro_blocks, H), blk, 0, stream, ro);
     // pass 1, with the pass-1 output's cotangent as dO
     StateScanArgs s1 = f1;

@@ -298,8 +298,15 @@ struct BwdWorkspace {
     int N, nt1, nt2, ro_blocks, norm_blocks;
     size_t bytes;
 };
-constexpr int BWD_RO_ROWS = 256;    // rows per readout-adjoint workgroup
+constexpr int BWD_RO_BLOCK = 32;    // rows per block of the readout kernels
 constexpr int BWD_NORM_ROWS = 64;   // rows per norm-adjoint workgroup
+
+// Blocks of 32 rows per readout workgroup: up to eight (the head's table is
+// staged once per workgroup), as long as 512 or more workgroups remain.
+inline int bwd_ro_per_wg(int B, int Tp, int H) {
+    const int blocks = (B * Tp + BWD_RO_BLOCK - 1) / BWD_RO_BLOCK, per = blocks * H / 512;
+    return per < 1 ? 1 : per > 8 ? 8 : per;
+}
 
 inline BwdWorkspace bwd_workspace(int B, int T, int H, int K, int V, int M, void* base) {
     const size_t Tp = (size_t)(T + 63) / 64 * 64, rows = (size_t)B * H * Tp, N = Tp / 64;
@@ -315,7 +322,10 @@ inline BwdWorkspace bwd_workspace(int B, int T, int H, int K, int V, int M, void
     w.N = (int)N;
     w.nt1 = (M + 31) / 32 * ((K + 63) / 64);  // the state scans' tiles (32 columns x 64 rows)
     w.nt2 = (V + 31) / 32 * ((M + 63) / 64);
-    w.ro_blocks = (int)((B * Tp + BWD_RO_ROWS - 1) / BWD_RO_ROWS);
+    {
+        const int blocks = (int)((B * Tp + BWD_RO_BLOCK - 1) / BWD_RO_BLOCK), per = bwd_ro_per_wg(B, (int)Tp, H);
+        w.ro_blocks = (blocks + per - 1) / per;  // readout workgroups per head
+    }
     w.norm_blocks = (int)(((size_t)B * T * H + BWD_NORM_ROWS - 1) / BWD_NORM_ROWS);
     const size_t BH = (size_t)B * H;
     w.lam = reinterpret_cast<double*>(take(rows * 8));
