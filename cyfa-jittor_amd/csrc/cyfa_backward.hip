@@ -166,16 +166,25 @@ __global__ __launch_bounds__(256) void bw_state_scan_kernel(StateScanArgs p) {
             ok[i][j] = r0 + rr + i < Kq && c0 + cc + j < Vd;
             x[i][j] = ok[i][j] && p.x0 ? p.x0[bh * ssz + (size_t)(r0 + rr + i) * Vd + c0 + cc + j] : 0.f;
         }
-    const auto keep = [&](int n) {  // xs[n] = X; returns the block's part of <X, S[n]>
+    // backward: the forward state S[n] of this thread's block, loaded a chunk
+    // ahead (with the rows and columns below) for the boundary term <X, S[n]>
+    float sv[2][4] = {};
+    const auto fetch_state = [&](int n) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                sv[i][j] = ok[i][j] ? p.S[(bh * (N + 1) + n) * ssz + (size_t)(r0 + rr + i) * Vd + c0 + cc + j] : 0.f;
+    };
+    const auto keep = [&](int n) {  // xs[n] = X; returns the block's part of <X, S[n]> (backward)
         float dot = 0.f;
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 if (ok[i][j]) {
-                    const size_t at = (size_t)n * ssz + (size_t)(r0 + rr + i) * Vd + c0 + cc + j;
-                    xs[at] = x[i][j];
-                    if constexpr (BWD) dot = fmaf(x[i][j], p.S[bh * (N + 1) * ssz + at], dot);
+                    xs[(size_t)n * ssz + (size_t)(r0 + rr + i) * Vd + c0 + cc + j] = x[i][j];
+                    if constexpr (BWD) dot = fmaf(x[i][j], sv[i][j], dot);
                 }
         return dot;
     };
@@ -198,6 +207,7 @@ __global__ __launch_bounds__(256) void bw_state_scan_kernel(StateScanArgs p) {
         if (wv == 0) rg = t0 + lane < p.T ? p.g[((size_t)b * p.T + t0 + lane) * p.H + h] : 0.f;
     };
     fetch(BWD ? N - 1 : 0);
+    if constexpr (BWD) fetch_state(N);
     for (int step = 0; step < N; step++) {
         const int n = BWD ? N - 1 - step : step;
         const float dot = keep(BWD ? n + 1 : n);
@@ -229,6 +239,7 @@ __global__ __launch_bounds__(256) void bw_state_scan_kernel(StateScanArgs p) {
         }
         __syncthreads();
         if (step + 1 < N) fetch(BWD ? n - 1 : n + 1);
+        if constexpr (BWD) fetch_state(n);  // for the next step's keep(n)
         if constexpr (BWD) {
             if (tid == 0) p.bnd[(bh * nt + tile) * N + n] = (sRed[0] + sRed[1]) + (sRed[2] + sRed[3]);
         }
