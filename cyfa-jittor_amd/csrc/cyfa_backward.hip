@@ -112,10 +112,10 @@ __global__ __launch_bounds__(256) void bw_rows_kernel(const void* x, const float
     if (rs_out && lane == 0) rs_out[row] = rs;
 }
 
-// The chunk-to-chunk scan of one pass over a [Kq, Vd] matrix X, one 64 x 32
-// tile per workgroup (grid (ceil(Vd / 32), ceil(Kq / 64), B*H), 256
-// threads, each holding a 2 x 4 block of X in registers; every element's
-// recurrence is independent of the others):
+// The chunk-to-chunk scan of one pass over a [Kq, Vd] matrix X, one
+// SCAN_ROWS x 32 tile per workgroup (grid (ceil(Vd / 32), ceil(Kq /
+// SCAN_ROWS), B*H), 256 threads, each holding SCAN_RPT x 4 elements of X in
+// registers; every element's recurrence is independent of the others):
 //   X <- e^{G_last} X + sum_t f_t a_t (x) b_t     (a rank-64 update per chunk)
 // Forward (BWD false): the states, n = 0 .. N-1, X_0 = x0 (or zero),
 //   f_t = e^{G_last - G_t}, a = k, b = v; xs[n] = the state before chunk n,
@@ -126,7 +126,8 @@ __global__ __launch_bounds__(256) void bw_rows_kernel(const void* x, const float
 //   state's; bnd[tile][n] = the tile's part of <xs[n+1], S[n+1]>.
 // Per chunk the f-scaled rows of a and the columns of b are staged in LDS
 // (two broadcast reads of a and one float4 of b per token feed eight FMAs).
-constexpr int SCAN_ROWS = 64;
+constexpr int SCAN_ROWS = BWD_SCAN_ROWS;    // rows of a scan tile
+constexpr int SCAN_RPT = SCAN_ROWS / 32;    // rows per thread (8 threads across the 32 columns)
 struct StateScanArgs {
     const float *a, *b;  // head-major [B*H, Tp, Kq] and [B*H, Tp, Vd]
     const float* g;      // [B, T, H]
@@ -155,12 +156,12 @@ __global__ __launch_bounds__(256) void bw_state_scan_kernel(StateScanArgs p) {
     float* xs = p.xs + bh * (N + 1) * ssz;
     const float* A = p.a + bh * p.Tp * Kq;
     const float* Bm = p.b + bh * p.Tp * Vd;
-    // this thread's block: rows r0 + rr, r0 + rr + 1; columns c0 + cc .. + 3
-    const int rr = 2 * (tid >> 3), cc = 4 * (tid & 7);
-    bool ok[2][4];
-    float x[2][4];
+    // this thread's block: rows r0 + rr .. + SCAN_RPT; columns c0 + cc .. + 3
+    const int rr = SCAN_RPT * (tid >> 3), cc = 4 * (tid & 7);
+    bool ok[SCAN_RPT][4];
+    float x[SCAN_RPT][4];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < SCAN_RPT; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             ok[i][j] = r0 + rr + i < Kq && c0 + cc + j < Vd;
@@ -168,10 +169,10 @@ __global__ __launch_bounds__(256) void bw_state_scan_kernel(StateScanArgs p) {
         }
     // backward: the forward state S[n] of this thread's block, loaded a chunk
     // ahead (with the rows and columns below) for the boundary term <X, S[n]>
-    float sv[2][4] = {};
+    float sv[SCAN_RPT][4] = {};
     const auto fetch_state = [&](int n) {
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < SCAN_RPT; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 sv[i][j] = ok[i][j] ? p.S[(bh * (N + 1) + n) * ssz + (size_t)(r0 + rr + i) * Vd + c0 + cc + j] : 0.f;
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(256) void bw_state_scan_kernel(StateScanArgs p) {
     const auto keep = [&](int n) {  // xs[n] = X; returns the block's part of <X, S[n]> (backward)
         float dot = 0.f;
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < SCAN_RPT; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 if (ok[i][j]) {
@@ -243,29 +244,28 @@ __global__ __launch_bounds__(256) void bw_state_scan_kernel(StateScanArgs p) {
         if constexpr (BWD) {
             if (tid == 0) p.bnd[(bh * nt + tile) * N + n] = (sRed[0] + sRed[1]) + (sRed[2] + sRed[3]);
         }
-        float acc[2][4] = {};
+        float acc[SCAN_RPT][4] = {};
         for (int t = 0; t < BC; t++) {
-            const float a0 = sA[t][rr], a1 = sA[t][rr + 1];
             const float4 bv = *reinterpret_cast<const float4*>(&sB[t][cc]);
-            acc[0][0] = fmaf(a0, bv.x, acc[0][0]);
-            acc[0][1] = fmaf(a0, bv.y, acc[0][1]);
-            acc[0][2] = fmaf(a0, bv.z, acc[0][2]);
-            acc[0][3] = fmaf(a0, bv.w, acc[0][3]);
-            acc[1][0] = fmaf(a1, bv.x, acc[1][0]);
-            acc[1][1] = fmaf(a1, bv.y, acc[1][1]);
-            acc[1][2] = fmaf(a1, bv.z, acc[1][2]);
-            acc[1][3] = fmaf(a1, bv.w, acc[1][3]);
+#pragma unroll
+            for (int i = 0; i < SCAN_RPT; i++) {
+                const float av = sA[t][rr + i];
+                acc[i][0] = fmaf(av, bv.x, acc[i][0]);
+                acc[i][1] = fmaf(av, bv.y, acc[i][1]);
+                acc[i][2] = fmaf(av, bv.z, acc[i][2]);
+                acc[i][3] = fmaf(av, bv.w, acc[i][3]);
+            }
         }
         const float el = sEl;
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < SCAN_RPT; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++) x[i][j] = fmaf(el, x[i][j], acc[i][j]);
     }
     keep(BWD ? 0 : N);
     if (p.x_out) {
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < SCAN_RPT; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 if (ok[i][j]) p.x_out[bh * ssz + (size_t)(r0 + rr + i) * Vd + c0 + cc + j] = x[i][j];

@@ -299,6 +299,7 @@ struct BwdWorkspace {
     size_t bytes;
 };
 constexpr int BWD_RO_BLOCK = 32;    // rows per block of the readout kernels
+constexpr int BWD_SCAN_ROWS = 32;   // rows of a state-scan tile (its columns: 32)
 constexpr int BWD_NORM_ROWS = 64;   // rows per norm-adjoint workgroup
 
 // Blocks of 32 rows per readout workgroup: up to eight (the head's table is
@@ -320,8 +321,8 @@ inline BwdWorkspace bwd_workspace(int B, int T, int H, int K, int V, int M, void
     const auto f = [&](size_t n) { return reinterpret_cast<float*>(take(n * 4)); };
     BwdWorkspace w;
     w.N = (int)N;
-    w.nt1 = (M + 31) / 32 * ((K + 63) / 64);  // the state scans' tiles (32 columns x 64 rows)
-    w.nt2 = (V + 31) / 32 * ((M + 63) / 64);
+    w.nt1 = (M + 31) / 32 * ((K + BWD_SCAN_ROWS - 1) / BWD_SCAN_ROWS);  // the state scans' tiles
+    w.nt2 = (V + 31) / 32 * ((M + BWD_SCAN_ROWS - 1) / BWD_SCAN_ROWS);
     {
         const int blocks = (int)((B * Tp + BWD_RO_BLOCK - 1) / BWD_RO_BLOCK), per = bwd_ro_per_wg(B, (int)Tp, H);
         w.ro_blocks = (blocks + per - 1) / per;  // readout workgroups per head
