@@ -119,6 +119,26 @@ def test_chunk_backward_matches_oracle_autograd(B, T, H, K, V, M, C, dtype, stat
         assert m["rrms"] < bar, f"{name} gradient rrms {m['rrms']:.3e} >= {bar} ({m})"
 
 
+def test_backward_fp16_operands_and_scale():
+    """fp16 q, k, v run the backward in fp32 and get fp16 gradients; a
+    non-default pass-1 scale reaches every gradient."""
+    x, init, cot = _inputs(1, 130, 2, 256, 256, 128, seed=21, dtype=torch.float16, state=True)
+    xd = {k: v.double().requires_grad_(True) for k, v in x.items()}
+    initd = tuple(t.double().requires_grad_(True) for t in init)
+    o, _ = O.chunk_cyfa(**xd, initial_state=initd, scale=0.11)
+    (o * cot["o"].double()).sum().backward()
+    xg = {k: v.to(DEV).requires_grad_(True) for k, v in x.items()}
+    initg = tuple(t.to(DEV).requires_grad_(True) for t in init)
+    og, _ = chunk_cyfa(**xg, initial_state=initg, scale=0.11)
+    (og.double() * cot["o"].double().to(DEV)).sum().backward()
+    for name in NAMES:
+        assert xg[name].grad.dtype == x[name].dtype, name
+        m = metrics(xg[name].grad.float(), xd[name].grad)
+        assert m["rrms"] < _bar(name, torch.bfloat16), f"{name}: {m}"
+    for a, b in zip(initg, initd):
+        assert metrics(a.grad, b.grad)["rrms"] < 0.01
+
+
 def test_backward_state_only_cotangent():
     """Only the final states feed the loss: o's cotangent is absent (None)."""
     x, init, cot = _inputs(1, 96, 2, 256, 256, 128, seed=5, dtype=torch.float32, state=True)
