@@ -222,3 +222,41 @@ def test_layer_gates_wire_each_projection_to_its_gate():
         z = float(a[bi, t, h]) + float(p[pre + "dt_bias"][h])
         want = -math.exp(float(p[pre + "A_log"][h])) * math.log1p(math.exp(z))
         assert abs(float(g2[bi, t, h]) - want) < 1e-12
+
+
+def test_attention_layer_output_norm_is_per_head_and_scale_free():
+    """The layer normalises o per head before o_proj (layers/cyfa.py:349-350):
+    o is linear in v, so scaling one head's v projection leaves the layer's
+    output unchanged up to the norm's eps, while the other head's output is
+    not rescaled with it (a norm over all heads at once would move both)."""
+    p, pre, cfg = _layer_params(hidden=64, H=2, Dh=32, seed=6)
+    cfg["norm_eps"] = 1e-15  # (127 o)^2 is about 1e-4 at this scale: eps must not matter
+    gen = torch.Generator().manual_seed(7)
+    x = torch.randn(1, 50, cfg["hidden_size"], dtype=D64, generator=gen)
+    y, _ = MO.attention_layer(p, pre, x, cfg)
+    scaled = dict(p)
+    w = p[pre + "v_proj.weight"].clone()
+    w[:32] *= 10.0  # head 0's value channels
+    scaled[pre + "v_proj.weight"] = w
+    y10, _ = MO.attention_layer(scaled, pre, x, cfg)
+    torch.testing.assert_close(y10, y, atol=1e-9, rtol=1e-7)
+    unnormed = dict(p, **{pre + "o_norm.weight": 2 * p[pre + "o_norm.weight"]})
+    y2, _ = MO.attention_layer(unnormed, pre, x, cfg)
+    torch.testing.assert_close(y2, 2 * y, atol=1e-12, rtol=1e-12)  # the norm weight multiplies, after the norm
+
+
+def test_attention_layer_gate_is_sigmoid_of_g_proj():
+    """The output gate is sigmoid(g_proj(x)) multiplying the normalised o
+    before o_proj (layers/cyfa.py:292-295, 349-351): with a zero last g_proj
+    weight the gate is sigmoid(bias), and a bias that is one value c across
+    channels scales the whole output by sigmoid(c)."""
+    p, pre, cfg = _layer_params(seed=8)
+    gen = torch.Generator().manual_seed(9)
+    x = torch.randn(1, 30, cfg["hidden_size"], dtype=D64, generator=gen)
+    outs = []
+    for c in (0.0, 1.5):
+        q = dict(p, **{pre + "g_proj.1.weight": torch.zeros_like(p[pre + "g_proj.1.weight"]),
+                       pre + "g_proj.1.bias": torch.full_like(p[pre + "g_proj.1.bias"], c)})
+        outs.append(MO.attention_layer(q, pre, x, cfg)[0])
+    ratio = (1 / (1 + math.exp(-1.5))) / 0.5
+    torch.testing.assert_close(outs[1], ratio * outs[0], atol=1e-12, rtol=1e-12)
