@@ -575,8 +575,8 @@ def main():
             "steps": args.decode_steps,
             "ms_per_step": round(d_elapsed / args.decode_steps * 1e3, 3),
             "roofline": {
-                "kernel": "cyfa_decode_layer_step (the model's graphed step: short conv, gates, decode op, "
-                          "gated output norm)",
+                "kernel": "cyfa_decode_layer_step (the model's graphed-step kernel: short conv, gates, decode op, "
+                          "gated output norm; g_proj[1] precomputed)",
                 "bound": "hbm",
                 "achieved": round(l_gbs, 1),
                 "peak": PEAK_HBM_GBS,
