@@ -289,7 +289,9 @@ class CyclicFlowAttention(nn.Module):
         v = v.reshape(B, T, H, self.head_v_dim)
         a = self.a_proj(x).float() + self.dt_bias.float()
         g = -self.A_log.float().exp() * F.softplus(a)
-        delta = torch.sigmoid(self.d_proj(x).float())
+        # the clock branch trains d_proj but passes no gradient into x
+        # (reference layers/cyfa.py:325: d_proj(x.detach()))
+        delta = torch.sigmoid(self.d_proj(x.detach()).float())
         beta = torch.sigmoid(self.b_proj(x).float())
         if attention_mask is not None:
             valid = attention_mask.unsqueeze(-1).bool()

@@ -45,12 +45,15 @@ def chunk_cyfa(
     [batch, time, heads]. The readout has [heads, slots-1, slots-1]. Returns
     the output ([batch, time, heads, V], in q's dtype) and, when requested,
     (key_state [B,H,K,M], value_state [B,H,M,V], clock [B,H]), all fp32.
-    K = V = 256 with 128 slots and chunk_size 64 run the tuned kernels (fp16
-    and fp32 q, k, v rounded to bf16 for them); every other shape (K, V <=
-    1024, an even slot count up to 256, chunk_size 16, 32 or 64) runs the
-    general path, cyfa_chunk_fwd_general, which computes in fp32 (bf16
-    operands rounded where the reference casts; fp16 and fp32 operands in
-    fp32), like the reference's unfused fallback (ops/chunk.py:285-331).
+    bf16 q, k, v with K = V = 256, 128 slots and chunk_size 64 run the tuned
+    kernels, as the reference takes its fused bf16 kernels only for bf16
+    inputs (ops/chunk.py:209-223, 257-264). Every other call -- fp16 or fp32
+    operands at any shape, or any other shape (K, V <= 1024, an even slot
+    count up to 256, chunk_size 16, 32 or 64) -- runs the general path,
+    cyfa_chunk_fwd_general, which computes in fp32: fp16 and fp32 operands
+    without intermediate rounding, bf16 operands rounded where the reference
+    casts to the input dtype, like the reference's unfused fallback
+    (ops/chunk.py:285-331).
     ``table`` (keyword only, not in the reference signature) is a precomputed
     readout @ Phi [H, M-1, M] fp32; when None it is formed from ``readout``.
     ``output_norm`` (keyword only, an extension) is ``(weight [V], gate
@@ -80,6 +83,11 @@ def chunk_cyfa(
         M = readout.shape[-1] + 1
         if M > BWD_MAX_SLOTS:
             raise NotImplementedError(f"chunk_cyfa: the backward pass supports up to {BWD_MAX_SLOTS} slots, got {M}")
+        B, T, H = q.shape[:3]
+        rows = B * H * ((T + 63) // 64 * 64)
+        if rows * 1024 >= 1 << 31:  # cyfa_chunk_bwd's 32-bit row indexing: refuse before the forward runs
+            raise NotImplementedError(f"chunk_cyfa: the backward pass supports B * H * padded T below "
+                                      f"{(1 << 31) // 1024} rows, got {rows}")
         h0k, h0v, c0 = state_in if state_in else (None, None, None)
         o, hk, hv, clock = _ChunkCyFA.apply(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, h0k, h0v,
                                             c0, float(q_norm_eps), float(k_norm_eps), scale, int(chunk_size))
@@ -108,12 +116,13 @@ def _chunk_forward(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weigh
             raise ValueError(f"{name} must have shape {(B, T, H)}, got {tuple(x.shape)}")
     out_dtype = _operand_dtype("chunk_cyfa", q, k, v)
     dev = _native.require_device(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, table, *state_in)
-    # the tuned kernels' shape; any other shape takes the general path, in
-    # bf16 for bf16 operands and in fp32 for fp16 and fp32 ones
-    fast = K == 256 and V == 256 and M == 128 and chunk_size == 64
+    # bf16 operands at the tuned kernels' shape; everything else takes the
+    # general path, in bf16 for bf16 operands and in fp32 for fp16 and fp32 ones
+    io_dtype = torch.bfloat16 if out_dtype == torch.bfloat16 else torch.float32
+    fast = K == 256 and V == 256 and M == 128 and chunk_size == 64 and io_dtype == torch.bfloat16
     if not fast and (output_norm is not None or no_alloc):
-        raise NotImplementedError("output_norm and no_alloc need K = V = 256, 128 slots and chunk_size 64")
-    io_dtype = torch.bfloat16 if fast or out_dtype == torch.bfloat16 else torch.float32
+        raise NotImplementedError("output_norm and no_alloc need bf16 q, k, v with K = V = 256, 128 slots and "
+                                  "chunk_size 64")
     q, k, v = (x.to(io_dtype).contiguous() for x in (q, k, v))
     g, delta, beta = (x.to(torch.float32).contiguous() for x in (g, delta, beta))
     qw = q_norm_weight.to(torch.float32).contiguous()
@@ -263,11 +272,10 @@ class _ChunkCyFA(torch.autograd.Function):
 
 
 def _operand_dtype(what, *xs):
-    """The dtype of q, k, v (one float dtype). The kernels' MFMA operands are
-    bf16: fp32 and fp16 inputs are rounded to bf16 on entry (the bf16 path's
-    accuracy, not the reference's fp32 scalar path's, which computes without
-    intermediate rounding: ops/chunk.py:285-331) and the output is returned
-    in the input dtype."""
+    """The dtype of q, k, v (one float dtype). bf16 operands run the bf16
+    kernels; fp32 and fp16 operands run the general path in fp32 without
+    intermediate rounding (the reference's scalar path for non-bf16 inputs,
+    ops/chunk.py:285-331) and the output is returned in the input dtype."""
     dt = xs[0].dtype
     if any(x.dtype != dt for x in xs) or dt not in (torch.bfloat16, torch.float16, torch.float32):
         raise NotImplementedError(f"{what}: q, k, v must share one of bf16, fp16, fp32; got "

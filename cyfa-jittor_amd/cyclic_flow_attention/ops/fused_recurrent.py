@@ -37,11 +37,12 @@ def fused_recurrent_cyfa(
     """Decode one token using constant-size key, value and clock states.
 
     Uses the same input layout and return convention as chunk_cyfa (q, k, v
-    of bf16, fp16 or fp32; o in their dtype). K, V in {128, 256} with 128
-    slots run the tuned kernel (fp16 and fp32 operands rounded to bf16 for
-    it); every other shape up to K, V <= 1024 and 256 slots runs the general
-    step (cyfa_decode_step_general: bf16 operands in bf16, fp16 and fp32 in
-    fp32). The new
+    of bf16, fp16 or fp32; o in their dtype). bf16 operands with K, V in
+    {128, 256} and 128 slots run the tuned kernel; fp16 and fp32 operands
+    and every other shape up to K, V <= 1024 and 256 slots run the general
+    step (cyfa_decode_step_general: bf16 operands rounded where the
+    reference casts, fp16 and fp32 in fp32 without intermediate rounding, as
+    the reference's kernel computes in the input dtype). The new
     states are returned as new tensors; ``inplace=True`` (an extension) updates
     the given initial_state tensors instead and returns them. ``table`` (an
     extension) passes a precomputed readout @ Phi to skip rebuilding it.
@@ -68,10 +69,10 @@ def fused_recurrent_cyfa(
     out_dtype = _operand_dtype("fused_recurrent_cyfa", q, k, v)
     state_in = tuple(initial_state) if initial_state is not None else ()
     dev = _native.require_device(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, table, *state_in)
-    # the tuned kernel's shapes; any other shape takes the general step, in
-    # bf16 for bf16 operands and in fp32 for fp16 and fp32 ones
-    fast = K in (128, 256) and V in (128, 256) and M == 128
-    io_dtype = torch.bfloat16 if fast or out_dtype == torch.bfloat16 else torch.float32
+    # bf16 operands at the tuned kernel's shapes; everything else takes the
+    # general step, in bf16 for bf16 operands and in fp32 for fp16 and fp32 ones
+    io_dtype = torch.bfloat16 if out_dtype == torch.bfloat16 else torch.float32
+    fast = K in (128, 256) and V in (128, 256) and M == 128 and io_dtype == torch.bfloat16
     q, k, v = (x.to(io_dtype).contiguous() for x in (q, k, v))
     g, delta, beta = (x.to(torch.float32).contiguous() for x in (g, delta, beta))
     qw = q_norm_weight.to(torch.float32).contiguous()

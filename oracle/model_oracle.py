@@ -96,10 +96,12 @@ def gate_activations(a, b, d, dt_bias, A_log, mode="exact"):
 def layer_gates(p, pre, xin, mode="exact"):
     """(g, delta, beta) of the layer for the normed input xin: the a, b and d
     projections (layers/cyfa.py:323-326; a_proj has no bias, b_proj and
-    d_proj have one) through gate_activations."""
+    d_proj have one) through gate_activations. The d projection reads a
+    detached xin (layers/cyfa.py:325, ``self.d_proj(x.detach())``): delta
+    trains d_proj but sends no gradient into xin or anything before it."""
     a = linear(xin, p[pre + "a_proj.weight"], mode=mode)
     b = linear(xin, p[pre + "b_proj.weight"], p[pre + "b_proj.bias"], mode)
-    d = linear(xin, p[pre + "d_proj.weight"], p[pre + "d_proj.bias"], mode)
+    d = linear(xin.detach(), p[pre + "d_proj.weight"], p[pre + "d_proj.bias"], mode)
     g, beta, delta = gate_activations(a, b, d, p[pre + "dt_bias"], p[pre + "A_log"], mode)
     return g, delta, beta
 
@@ -181,9 +183,12 @@ def gated_mlp(p, pre, x, mode="exact"):
 
 
 def causal_lm(p, cfg, input_ids, cache=None, use_cache=False, attention_mask=None, mode="exact",
-              chunk_size=64, op_mode=None):
+              chunk_size=64, op_mode=None, last_logits_only=False, progress=None):
     """CyclicFlowAttentionForCausalLM.execute without the loss
-    (models/cyfa/modeling_cyfa.py:49-108). Returns (logits, cache)."""
+    (models/cyfa/modeling_cyfa.py:49-108). Returns (logits, cache).
+    ``last_logits_only`` returns the logits of the last position only
+    ([B, 1, vocab]; the final norm and lm_head act per row, so these equal the
+    last row of the full logits); ``progress(i)`` is called after layer i."""
     dt = _dt(mode)
     eps = cfg.get("norm_eps", 1e-6)
     x = p["model.embeddings.weight"].to(dt)[input_ids]
@@ -197,6 +202,10 @@ def causal_lm(p, cfg, input_ids, cache=None, use_cache=False, attention_mask=Non
         x = _cast(r + gated_mlp(p, pre + "mlp.", rms_norm(r, p[pre + "mlp_norm.weight"], eps, mode=mode), mode),
                   mode)
         new.append(c)
+        if progress is not None:
+            progress(i)
+    if last_logits_only:
+        x = x[:, -1:]
     hidden = rms_norm(x, p["model.norm.weight"], eps, mode=mode)
     logits = linear(hidden, p["lm_head.weight"], mode=mode)
     return logits, (new if use_cache else None)

@@ -395,12 +395,15 @@ def test_norm_linear_rows_folded(M, residual, swiglu, K):
         assert (err <= bound).all(), f"max err {err.max().item()}"
 
 
-@pytest.mark.parametrize("B,state,inplace,split,own_gate", [
-    (3, True, False, True, False), (2, False, False, True, False), (4, True, True, True, False),
-    (64, True, True, True, False), (3, True, True, False, False), (1, True, True, True, False),
-    (64, True, True, False, True), (3, True, True, True, True), (1, False, False, False, True),
-    (17, True, False, False, True)])
-def test_decode_layer_step_equals_separate_kernels(B, state, inplace, split, own_gate):
+@pytest.mark.parametrize("B,state,inplace,split,own_gate,H", [
+    (3, True, False, True, False, 4), (2, False, False, True, False, 4), (4, True, True, True, False, 4),
+    (64, True, True, True, False, 4), (3, True, True, False, False, 4), (1, True, True, True, False, 4),
+    (64, True, True, False, True, 4), (3, True, True, True, True, 4), (1, False, False, False, True, 4),
+    (17, True, False, False, True, 4),
+    # configuration 5's heads (the 1.4B model's single-sequence step), both forms and the in-kernel gate
+    (1, True, True, False, False, 8), (1, True, True, True, False, 8), (1, True, True, False, True, 8),
+    (16, True, True, False, True, 8)])
+def test_decode_layer_step_equals_separate_kernels(B, state, inplace, split, own_gate, H):
     """cyfa_decode_layer_step (short convolution, gates, decode op and gated
     output norm in one kernel, or in the two kernels of the small-batch split)
     against the separate kernels on the same inputs: the same arithmetic in
@@ -411,8 +414,8 @@ def test_decode_layer_step_equals_separate_kernels(B, state, inplace, split, own
     from cyclic_flow_attention.ops import fused_recurrent_cyfa
     from cyclic_flow_attention.ops.fused_recurrent import decode_layer_step
 
-    H, D = 4, 3 * 4 * 256
-    gen = torch.Generator().manual_seed(B + 10 * state + 100 * inplace)
+    D = 3 * H * 256
+    gen = torch.Generator().manual_seed(B + 10 * state + 100 * inplace + 1000 * H)
     qkv_rows = torch.randn(B, 1, D + 40, generator=gen).bfloat16().to(DEV)
     qkv = qkv_rows[..., :D]  # rows D + 40 apart
     cache = (0.5 * torch.randn(B, 3, D, generator=gen)).bfloat16().to(DEV) if state else None

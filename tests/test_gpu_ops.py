@@ -373,25 +373,45 @@ def test_decode_split_equals_one_workgroup_form(B, H, K, V):
     _check_states(st2, rst, "split decode")
 
 
+# fp32 operands: fp32 arithmetic throughout (5e-7 mean-rel observed on
+# MI355X); fp16: the same, with o returned in fp16, whose own rounding
+# (2^-11 relative) gives about 1.8e-4 mean-rel
+WIDE_BARS = {torch.float32: dict(max_abs=1e-4, mean_rel=1e-5), torch.float16: dict(max_abs=1e-3, mean_rel=5e-4)}
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
-def test_wide_operands_run_the_bf16_path(dtype):
-    """fp32 and fp16 q, k, v (the reference's scalar path, ops/chunk.py:285-331,
-    takes fp32) are rounded to bf16 on entry: the outputs equal the bf16 call's,
-    returned in the input dtype, for both the chunk op and the decode step."""
+def test_wide_operands_compute_in_fp32(dtype):
+    """fp32 and fp16 q, k, v at the tuned shape (K = V = 256, 128 slots,
+    chunk 64) are not rounded to bf16: like the reference, which takes its
+    fused bf16 kernels only for bf16 inputs and otherwise computes in the
+    input dtype (ops/chunk.py:209-223, 257-264, 285-331), they run in fp32.
+    The chunk op, its final states and a decode step from them match the
+    float64 oracle at fp32-level tolerance -- a bf16 rounding of q, k, v alone
+    would give about 3e-3 mean-rel -- and o comes back in the input dtype."""
     from cyclic_flow_attention.ops import chunk_cyfa, fused_recurrent_cyfa
 
     x, init = _inputs(2, 130, 2, seed=11, state=True)
+    gen = torch.Generator().manual_seed(12)
+    for name in ("q", "k", "v"):
+        x[name] = torch.randn(x[name].shape, generator=gen).to(dtype)
     xg, ig = _gpu(x, init)
-    wide = dict(xg, q=xg["q"].to(dtype), k=xg["k"].to(dtype), v=xg["v"].to(dtype))
+    xd, idd = _oracle(x, init)
+    seq = ("q", "k", "v", "g", "delta", "beta")
+    step = {k: (v[:, :1] if k in seq else v) for k, v in xg.items()}
     with torch.no_grad():
-        o_b, s_b = chunk_cyfa(**xg, initial_state=ig, output_final_state=True)
-        o_w, s_w = chunk_cyfa(**wide, initial_state=ig, output_final_state=True)
-        d = {k: (v[:, :1] if k in ("q", "k", "v", "g", "delta", "beta") else v) for k, v in xg.items()}
-        dw = {k: (v[:, :1] if k in ("q", "k", "v", "g", "delta", "beta") else v) for k, v in wide.items()}
-        r_b, _ = fused_recurrent_cyfa(**d, initial_state=ig)
-        r_w, _ = fused_recurrent_cyfa(**dw, initial_state=ig)
+        o, st = chunk_cyfa(**xg, initial_state=ig, output_final_state=True)
+        od, std = fused_recurrent_cyfa(**step, initial_state=st, output_final_state=True)
     torch.cuda.synchronize()
-    assert o_w.dtype == dtype and r_w.dtype == dtype
-    assert torch.equal(o_w, o_b.to(dtype)) and torch.equal(r_w, r_b.to(dtype))
-    for a, b in zip(s_w, s_b):
-        assert torch.equal(a, b)
+    assert o.dtype == dtype and od.dtype == dtype
+    ro, rst = O.chunk_cyfa(**xd, initial_state=idd, output_final_state=True, mode="exact")
+    stepd = {k: (v[:, :1] if k in seq else v) for k, v in xd.items()}
+    rod, rstd = O.fused_recurrent_cyfa(**stepd, initial_state=rst, output_final_state=True, mode="exact")
+    bar = WIDE_BARS[dtype]
+    f32 = WIDE_BARS[torch.float32]
+    assert_close(o, ro, what=f"{dtype} chunk o", **bar)
+    assert_close(st[0], rst[0], what=f"{dtype} chunk hk", **f32)
+    assert_close(st[1], rst[1], what=f"{dtype} chunk hv", **f32)
+    torch.testing.assert_close(st[2].double().cpu(), rst[2], atol=1e-4, rtol=1e-6)
+    assert_close(od, rod, what=f"{dtype} decode o", **bar)
+    assert_close(std[0], rstd[0], what=f"{dtype} decode hk", **f32)
+    assert_close(std[1], rstd[1], what=f"{dtype} decode hv", **f32)

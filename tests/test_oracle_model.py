@@ -123,6 +123,11 @@ def test_causal_lm_prefix_then_decode_equals_full_forward():
         logits, cache = MO.causal_lm(lm, cfg, ids[:, t:t + 1], cache=cache, use_cache=True)
         outs.append(logits)
     torch.testing.assert_close(torch.cat(outs, 1), full, atol=1e-10, rtol=0)
+    # the last-position form: the final norm and lm_head act per row
+    seen = []
+    last, _ = MO.causal_lm(lm, cfg, ids, last_logits_only=True, progress=seen.append)
+    assert last.shape == (1, 1, V) and seen == [0]
+    torch.testing.assert_close(last, full[:, -1:], atol=1e-12, rtol=0)  # one row: another BLAS blocking
 
 
 def test_gated_mlp_against_a_scalar_loop_and_its_special_cases():
@@ -260,3 +265,31 @@ def test_attention_layer_gate_is_sigmoid_of_g_proj():
         outs.append(MO.attention_layer(q, pre, x, cfg)[0])
     ratio = (1 / (1 + math.exp(-1.5))) / 0.5
     torch.testing.assert_close(outs[1], ratio * outs[0], atol=1e-12, rtol=1e-12)
+
+
+def test_clock_branch_sends_no_gradient_into_x():
+    """delta = sigmoid(d_proj(x.detach())) (layers/cyfa.py:325): the clock
+    branch trains d_proj but passes no gradient into x. With every other path
+    from x to the output cut (zero q/k/v, a, b and g_proj[0] weights; q, k, v
+    made constant by conv biases, beta and the gate by their biases) the
+    output still depends on x through delta -- a perturbation of x moves it --
+    yet x.grad is exactly zero while d_proj.weight.grad is not. Without the
+    detach x.grad would be the perturbation's slope."""
+    p, pre, cfg = _layer_params(hidden=48, H=2, Dh=32, seed=13)
+    H, Dh, hidden = 2, 32, 48
+    gen = torch.Generator().manual_seed(14)
+    for n in ("q_proj", "k_proj", "v_proj"):
+        p[pre + n + ".weight"] = torch.zeros(H * Dh, hidden, dtype=D64)
+        p[pre + n.replace("_proj", "_conv1d") + ".bias"] = torch.randn(H * Dh, dtype=D64, generator=gen)
+    for n in ("a_proj", "b_proj"):
+        p[pre + n + ".weight"] = torch.zeros(H, hidden, dtype=D64)
+    p[pre + "g_proj.0.weight"] = torch.zeros(Dh, hidden, dtype=D64)
+    p[pre + "d_proj.weight"] = (0.5 * torch.randn(H, hidden, dtype=D64, generator=gen)).requires_grad_(True)
+    x = torch.randn(1, 40, hidden, dtype=D64, generator=gen).requires_grad_(True)
+    y, _ = MO.attention_layer(p, pre, x, cfg)
+    y.pow(2).sum().backward()
+    assert x.grad is None or torch.count_nonzero(x.grad) == 0
+    assert p[pre + "d_proj.weight"].grad.abs().max() > 1e-6
+    with torch.no_grad():
+        y2, _ = MO.attention_layer(p, pre, x + 0.05 * torch.randn(x.shape, dtype=D64, generator=gen), cfg)
+    assert (y2 - y.detach()).abs().max() > 1e-6
