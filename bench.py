@@ -115,7 +115,30 @@ def log(msg):
 
 
 def cpu_threads():
+    """Threads of the CPU baseline: every core of the affinity set, capped at
+    16, the host share of one GPU on the MI355X boxes (whose affinity set
+    shows every core of the host)."""
     return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def cpu_cores_visible():
+    return len(os.sched_getaffinity(0))
+
+
+def decode_step_bytes(model, batch):
+    """HBM bytes one greedy decode step must move at least: every weight once
+    (the embedding table only for the batch's rows), the fp32 recurrent states
+    read and written, the conv caches read and written."""
+    import torch
+
+    cfg = model.config
+    weights = sum(p.numel() * p.element_size() for n, p in model.named_parameters() if "embeddings" not in n)
+    weights += batch * cfg.hidden_size * model.model.embeddings.weight.element_size()
+    layers = cfg.num_hidden_layers
+    H = cfg.num_heads
+    state = STATE_BYTES_PER_BH * batch * H * layers
+    conv = 2 * batch * (cfg.conv_size - 1) * 3 * H * 256 * 2 * layers
+    return weights, state + conv
 
 
 def build_model(cfg_name, device):
@@ -269,16 +292,23 @@ def time_decode(model, prompt, steps, warmup):
     return elapsed
 
 
-def decode_layer_kernel_ms(batch, heads, reps=24, replays=5, graphed=True):
+def decode_layer_kernel_ms(batch, heads, reps=24, replays=5, graphed=True, gate_in_kernel=None):
     """Average device time of one cyfa_decode_layer_step launch (the kernel the
     model's graphed decode step runs: short convolution, gates, the decode op
     and the gated output norm) at the decode shape, timed as decode_kernel_ms:
     `reps` in-place launches on their own states captured in one graph,
-    replayed between HIP events on the launch stream."""
+    replayed between HIP events on the launch stream. gate_in_kernel: the
+    kernel also forms the gate (g_proj[1]) from g0, as the model's step does
+    at GATE_IN_KERNEL_MIN_WORKGROUPS or more (batch, head) workgroups; None
+    picks the model's choice for this shape."""
     import torch
 
     from cyclic_flow_attention import _native
+    from cyclic_flow_attention.layers.cyfa import GATE_IN_KERNEL_MIN_WORKGROUPS
     from cyclic_flow_attention.ops.fused_recurrent import decode_layer_step
+
+    if gate_in_kernel is None:
+        gate_in_kernel = batch * heads >= GATE_IN_KERNEL_MIN_WORKGROUPS
 
     dev = torch.device("cuda:0")
     H, D = heads, 3 * heads * 256
@@ -288,6 +318,12 @@ def decode_layer_kernel_ms(batch, heads, reps=24, replays=5, graphed=True):
     abd = torch.randn(batch, 1, 3 * H, generator=gen).bfloat16().to(dev)
     dt_bias, A_log = torch.randn(H, generator=gen).to(dev), torch.randn(H, generator=gen).to(dev)
     gate = torch.randn(batch, 1, H * 256, generator=gen).bfloat16().to(dev)
+    g_proj = None
+    if gate_in_kernel:
+        g_proj = (torch.randn(batch, 1, 256, generator=gen).bfloat16().to(dev),
+                  (0.06 * torch.randn(H * 256, 256, generator=gen)).bfloat16().to(dev),
+                  (0.5 * torch.randn(H * 256, generator=gen)).bfloat16().to(dev))
+        gate = None
     ones = torch.ones(256, device=dev)
     table = _native.readout_table(torch.eye(127, device=dev).expand(H, 127, 127).contiguous())
     states = [(torch.randn(batch, heads, 256, 128, device=dev), torch.randn(batch, heads, 128, 256, device=dev),
@@ -296,7 +332,7 @@ def decode_layer_kernel_ms(batch, heads, reps=24, replays=5, graphed=True):
 
     def step(st):
         decode_layer_step(qkv, st[3], st[3], wconv, abd, dt_bias, A_log, gate, ones, 1e-6, 127.0, table, ones, ones,
-                          1e-6, 1e-6, H, initial_state=st[:3], output_final_state=True, inplace=True)
+                          1e-6, 1e-6, H, initial_state=st[:3], output_final_state=True, inplace=True, g_proj=g_proj)
 
     with torch.no_grad():
         step(states[0])
@@ -411,6 +447,7 @@ def cpu_baseline_prefill(model, config, seq_len, gpu_logits=None, reps=3):
         "value": round(seq_len / elapsed, 2),
         "unit": "tok/s",
         "cores": threads,
+        "cores_visible": cpu_cores_visible(),
         "kind": "port",
         "cpu": cpu_model(),
         "sample": f"CPU oracle (float32, bf16 rounding points) full 400M forward of the prefill batch's first "
@@ -457,6 +494,7 @@ def cpu_baseline_decode(model, config, batch, steps=4, reps=3):
         "value": round(batch * steps / elapsed, 2),
         "unit": "tok/s",
         "cores": threads,
+        "cores_visible": cpu_cores_visible(),
         "kind": "port",
         "cpu": cpu_model(),
         "sample": f"CPU oracle (float32) decode of the 400M model at B={batch} after a 64-token prompt: median of "
@@ -562,21 +600,32 @@ def main():
         d_value = args.decode_batch * args.decode_steps / d_elapsed
         d_bytes = STATE_BYTES_PER_BH * args.decode_batch * H
         l_bytes = d_bytes
+        # the kernel in the form the model's step runs it (g_proj[1] inside at
+        # this shape), then with a precomputed gate, then the op alone
         l_avg = decode_layer_kernel_ms(args.decode_batch, H)
         l_gbs = l_bytes / (l_avg * 1e-3) / 1e9
+        lp_avg = decode_layer_kernel_ms(args.decode_batch, H, gate_in_kernel=False)
+        lp_gbs = l_bytes / (lp_avg * 1e-3) / 1e9
         d_avg = decode_kernel_ms(args.decode_batch, H)
         d_gbs = d_bytes / (d_avg * 1e-3) / 1e9
-        log(f"decode {d_value:,.0f} tok/s; layer-step kernel {l_avg * 1e3:.1f} us/launch = {l_gbs:,.0f} GB/s; "
+        from cyclic_flow_attention.layers.cyfa import GATE_IN_KERNEL_MIN_WORKGROUPS
+
+        in_kernel = args.decode_batch * H >= GATE_IN_KERNEL_MIN_WORKGROUPS
+        w_bytes, s_bytes = decode_step_bytes(model, args.decode_batch)
+        step_ms = d_elapsed / args.decode_steps * 1e3
+        step_gbs = (w_bytes + s_bytes) / (step_ms * 1e-3) / 1e9
+        log(f"decode {d_value:,.0f} tok/s ({step_gbs:,.0f} GB/s of weights + states); layer-step kernel "
+            f"{l_avg * 1e3:.1f} us/launch = {l_gbs:,.0f} GB/s (gate precomputed {lp_avg * 1e3:.1f} us); "
             f"op kernel {d_avg * 1e3:.1f} us/launch = {d_gbs:,.0f} GB/s")
         result["decode"] = {
             "value": round(d_value, 1),
             "unit": "tok/s",
             "batch": args.decode_batch,
             "steps": args.decode_steps,
-            "ms_per_step": round(d_elapsed / args.decode_steps * 1e3, 3),
+            "ms_per_step": round(step_ms, 3),
             "roofline": {
-                "kernel": "cyfa_decode_layer_step (the model's graphed-step kernel: short conv, gates, decode op, "
-                          "gated output norm; g_proj[1] precomputed)",
+                "kernel": "cyfa_decode_layer_step as the model's graphed step runs it at this shape (short conv, "
+                          "gates, decode op, gated output norm" + (", g_proj[1] formed inside)" if in_kernel else ")"),
                 "bound": "hbm",
                 "achieved": round(l_gbs, 1),
                 "peak": PEAK_HBM_GBS,
@@ -586,12 +635,24 @@ def main():
                 "launch_us": round(l_avg * 1e3, 2),
                 "bytes_per_launch": l_bytes,
             },
+            "layer_kernel_gate_precomputed": {
+                "kernel": "cyfa_decode_layer_step with g_proj[1] precomputed",
+                "achieved": round(lp_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(lp_gbs / PEAK_HBM_GBS, 4), "launch_us": round(lp_avg * 1e3, 2),
+            },
             "op_kernel": {
                 "kernel": "cyfa_decode_step (fused_recurrent_cyfa alone)",
                 "achieved": round(d_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(d_gbs / PEAK_HBM_GBS, 4),
                 "traffic": TRAFFIC_DECODE_BYTES if (args.decode_batch, H) == (64, 4) else None,
                 "launch_us": round(d_avg * 1e3, 2),
+            },
+            "step_roofline": {
+                "what": "whole graphed decode step: every weight once (embedding rows only) plus the fp32 states and "
+                        "conv caches read and written, per step time",
+                "bound": "hbm", "achieved": round(step_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(step_gbs / PEAK_HBM_GBS, 4),
+                "weight_bytes": w_bytes, "state_bytes": s_bytes,
             },
         }
         del prompt
@@ -655,6 +716,8 @@ def main():
         lc_dec = time_decode(lc_model, lc_ids, 512, 4)
         lc_kernel = decode_layer_kernel_ms(1, H5)
         lc_state = STATE_BYTES_PER_BH * H5
+        lc_w, lc_s = decode_step_bytes(lc_model, 1)
+        lc_step_gbs = (lc_w + lc_s) / (lc_dec / 512) / 1e9
         result["long_context"] = {
             "workload": f"configuration 5: CyFA-1.4B, B=1, {T5}-token prefill, then 512 greedy decode steps",
             "prefill": {"value": round(2 * T5 / lc_elapsed, 1), "unit": "tok/s",
@@ -663,8 +726,13 @@ def main():
                         "mfma_frac": round(lc_flop / (lc_op * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                         "hbm_frac": round(lc_bytes / (lc_op * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
             "decode": {"value": round(512 / lc_dec, 1), "unit": "tok/s", "ms_per_step": round(lc_dec / 512 * 1e3, 4),
+                       "step_roofline": {
+                           "what": "whole graphed B=1 step: every weight once plus the fp32 states and conv caches "
+                                   "read and written, per step time",
+                           "bound": "hbm", "achieved": round(lc_step_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                           "frac": round(lc_step_gbs / PEAK_HBM_GBS, 4), "weight_bytes": lc_w, "state_bytes": lc_s},
                        "layer_kernel_us": round(lc_kernel * 1e3, 2),
-                       "layer_kernel_hbm_frac": round(lc_state / (lc_kernel * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+                       "layer_kernel_state_hbm_frac": round(lc_state / (lc_kernel * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
         }
         log(f"long context: prefill {2 * T5 / lc_elapsed:,.0f} tok/s (op {lc_op * 1e3:.1f} us), decode "
             f"{512 / lc_dec:,.1f} tok/s (layer kernel {lc_kernel * 1e3:.1f} us)")

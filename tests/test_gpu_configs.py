@@ -38,6 +38,9 @@ DEV = "cuda"
 T_PROMPT = 2048
 BF16_ULP = 2.0 ** -8
 BUDGET_FACTOR = 1.5  # GPU deviation from O_me allowed, relative to O_mm's
+# configuration 4's greedy check: 17 of its 130 steps are undecidable on
+# MI355X (none mismatched); the bound adds a slack of 7
+CFG4_MAX_UNDECIDABLE = 24
 
 
 def _budget_close(got, ref, spread_ref, what):
@@ -108,7 +111,10 @@ def test_config4_graphed_decode_and_greedy_tokens(model400, prompts):
     """Configuration 4: B=64 after a 2048-token chunkwise prompt. Replays of the
     graphed 24-layer step equal eager steps bit for bit for 8 steps; then 64
     greedy graphed steps, with rows 0 and 63 (the oracle's prompts) checked by
-    teacher forcing against O_me (undecidable steps counted and bounded)."""
+    teacher forcing against O_me: every decidable step picks O_me's token,
+    the undecidable ones are counted and bounded (17 of 130 observed), and at
+    every step the GPU's own logits prefer its token over O_me's by at most
+    twice the reference's own rounding noise on that difference."""
     model, params, cfg = model400
     ids2, (lg_me, c_me), (lg_mm, c_mm) = prompts
     B, steps = 64, 64
@@ -117,10 +123,12 @@ def test_config4_graphed_decode_and_greedy_tokens(model400, prompts):
     ids[0], ids[B - 1] = ids2[0], ids2[1]
     with torch.no_grad():
         hidden, cache = model.model(ids.to(DEV), use_cache=True)
-        tok = model.lm_head(hidden[:, -1:]).argmax(-1)
+        first = model.lm_head(hidden[:, -1:])
+        tok = first.argmax(-1)
         del hidden
         dec = model.graphed_decoder(cache, tok)
         tokens = [tok[[0, B - 1], 0].cpu()]
+        gpu_logits = [first[[0, B - 1], -1].float().cpu()]
         eager_tok = tok
         for step in range(8):
             eager = model(eager_tok, cache=cache, use_cache=True)
@@ -130,9 +138,11 @@ def test_config4_graphed_decode_and_greedy_tokens(model400, prompts):
             assert torch.equal(dec.logits, eager["logits"]), f"step {step}: graphed logits differ from eager"
             assert torch.equal(got, eager_tok), f"step {step}: graphed tokens differ from eager"
             tokens.append(got[[0, B - 1], 0].cpu())
+            gpu_logits.append(dec.logits[[0, B - 1], -1].float().cpu())
         del cache, eager
         for _ in range(steps - 8):
             tokens.append(dec.step()[[0, B - 1], 0].cpu())
+            gpu_logits.append(dec.logits[[0, B - 1], -1].float().cpu())
     torch.cuda.synchronize()
     toks = torch.stack(tokens, 1)  # [2, steps + 1]: the prefill's token, then one per step
     me_last, mm_last = lg_me[:, -1], lg_mm[:, -1]
@@ -145,6 +155,11 @@ def test_config4_graphed_decode_and_greedy_tokens(model400, prompts):
             gap = float(top2.values[0] - top2.values[1])
             decidable = (int(mm_last[r].argmax()) == int(top2.indices[0])
                          and gap > 2 * BF16_ULP * float(me_last[r].abs().max()))
+            # at every step the GPU prefers its token over O_me's by no more than
+            # twice the reference's own rounding noise on a logit difference
+            noise = 2 * 2 ** 0.5 * float((mm_last[r] - me_last[r]).pow(2).mean().sqrt())
+            pref = float(gpu_logits[i][r][int(toks[r, i])] - gpu_logits[i][r][top2.indices[0]])
+            assert pref <= noise, f"step {i} row {r}: the GPU prefers token {int(toks[r, i])} by {pref:.4f}"
             if not decidable:
                 undecidable += 1
             elif int(toks[r, i]) != int(top2.indices[0]):
@@ -163,7 +178,7 @@ def test_config4_graphed_decode_and_greedy_tokens(model400, prompts):
     print(f"cfg4 greedy tokens: {total - undecidable - mismatched} of {total} decidable steps match, "
           f"{undecidable} undecidable, {mismatched} mismatched")
     assert mismatched == 0, f"{mismatched} decidable greedy steps differ from the oracle's token"
-    assert undecidable <= total // 4, f"{undecidable} of {total} steps undecidable"
+    assert undecidable <= CFG4_MAX_UNDECIDABLE, f"{undecidable} of {total} steps undecidable"
 
 
 @pytest.mark.parametrize("name", ["tiny.json", "cyclic_flow_attention_400m.json"])
@@ -196,15 +211,18 @@ def test_model_prefix_then_decode_equals_full_forward(name):
         _budget_close(got, me[:, -1:], mm[:, -1:], f"{name} {what} vs oracle")
 
 
-def test_decode_layer_step_config4_matches_oracle():
-    """decode_layer_step at B=64, H=4 (configuration 4's 256 workgroups) against
-    the oracle's layer arithmetic: short convolution and conv cache, gate
-    activations, the exact decode op and the gated output norm."""
+@pytest.mark.parametrize("B,H", [(64, 4), (1, 8)])
+def test_decode_layer_step_matches_oracle(B, H):
+    """decode_layer_step at configuration 4's shape (B=64, H=4: 256
+    workgroups) and configuration 5's (B=1, H=8: the 1.4B model's
+    single-sequence step) against the oracle's layer arithmetic: short
+    convolution and conv cache, gate activations, the exact decode op and the
+    gated output norm."""
     from cyclic_flow_attention import _native
     from cyclic_flow_attention.ops.fused_recurrent import decode_layer_step
 
-    B, H, D = 64, 4, 3 * 4 * 256
-    gen = torch.Generator().manual_seed(64)
+    D = 3 * H * 256
+    gen = torch.Generator().manual_seed(64 + B + H)
     qkv = torch.randn(B, 1, D, generator=gen).bfloat16()
     cache = (0.5 * torch.randn(B, 3, D, generator=gen)).bfloat16()
     wconv = (0.3 * torch.randn(D, 4, generator=gen)).bfloat16()
@@ -245,8 +263,8 @@ def test_decode_layer_step_config4_matches_oracle():
     # bf16 ulp is 0.03): max-abs within the north-star bar or 1.5x the
     # reference's own rounding at this point, mean-rel within 5e-3
     assert_close(got.reshape(B, 1, H, 256), ref, max_abs=max(2e-2, 1.5 * own["max_abs"]),
-                 what="cfg4 layer step o'")
+                 what=f"B{B} H{H} layer step o'")
     for a_, b_, n in zip(st, rst, ("hk", "hv")):
-        assert_close(a_, b_, what=f"cfg4 layer step {n}")
+        assert_close(a_, b_, what=f"B{B} H{H} layer step {n}")
     torch.testing.assert_close(st[2].double().cpu(), rst[2], atol=5e-3, rtol=1e-6)
     assert torch.equal(tail.cpu(), new_cache.bfloat16())
