@@ -43,18 +43,35 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_base[kMaxDevices];  // device address of `scratch` per device, resolved on first use
 
-// Device address of the current device's scratch array (resolved once per
-// device, with that device current).
-int scratch_base(void** out, const char* what) {
-    int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+// Device address of the scratch array on the device the launch stream belongs
+// to (the current device for the null stream), resolved once per device with
+// that device current (made current for the call and restored after it when
+// the caller's current device is another one).
+int scratch_base(hipStream_t stream, void** out, const char* what) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess || cur < 0) {
         (void)hipGetLastError();
         return fail(CYFA_ERR_LAUNCH, "%s: no current HIP device", what);
     }
+    int dev = cur;
+    if (stream) {
+        hipDevice_t d = -1;
+        if (hipStreamGetDevice(stream, &d) != hipSuccess || d < 0) {
+            (void)hipGetLastError();
+            return fail(CYFA_ERR_LAUNCH, "%s: the stream's device is unknown", what);
+        }
+        dev = (int)d;
+    }
+    if (dev >= kMaxDevices) return fail(CYFA_ERR_LAUNCH, "%s: device %d beyond %d", what, dev, kMaxDevices);
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
     if (!g_scratch_base[dev]) {
+        if (dev != cur && hipSetDevice(dev) != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(CYFA_ERR_LAUNCH, "%s: cannot make device %d current", what, dev);
+        }
         void* p = nullptr;
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (dev != cur) (void)hipSetDevice(cur);
         if (e != hipSuccess || !p) {
             (void)hipGetLastError();
             return fail(CYFA_ERR_LAUNCH, "%s: hipGetSymbolAddress of the scratch array failed on device %d: %s", what,
@@ -184,6 +201,29 @@ int decode_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* ly, void* hi
         p.on_w = ly->norm_weight;
         p.on_eps = ly->norm_eps;
         p.on_prescale = ly->norm_prescale;
+        // Prefetch: at most CYFA_PREFETCH_MAX_BH step workgroups, the
+        // one-workgroup form, and workgroups on the compute units it leaves idle.
+        unsigned long long pf_total = 0;
+        for (int r = 0; r < CYFA_PREFETCH_RANGES; r++) {
+            const unsigned long long n = ly->prefetch_bytes[r];
+            if (n == 0) continue;
+            if (!ly->prefetch[r] || n >= (1ull << 31))
+                return fail(CYFA_ERR_VALUE, "cyfa_decode_layer_step: prefetch range %d: null or %llu bytes (below 2^31)",
+                            r, n);
+            if (!aligned(ly->prefetch[r], 16))
+                return fail(CYFA_ERR_ALIGN, "cyfa_decode_layer_step: prefetch range %d needs 16-byte alignment", r);
+            pf_total += n;
+        }
+        const long long bh = (long long)a->B * a->H;
+        const int idle = cyfa::device_cu_count() - (int)(bh < 1 << 20 ? bh : 1 << 20);
+        if (pf_total && bh <= CYFA_PREFETCH_MAX_BH && !p.part && idle > 0) {
+            for (int r = 0; r < CYFA_PREFETCH_RANGES; r++) {
+                p.pf[r] = ly->prefetch[r];
+                p.pf_bytes[r] = ly->prefetch_bytes[r];
+            }
+            const unsigned long long units = (pf_total + 16383) >> 14;  // 16 KiB per workgroup round
+            p.pf_wgs = (int)(units < (unsigned long long)idle ? units : (unsigned long long)idle);
+        }
     }
     if (cyfa::launch_decode_step(p, a->K, a->V, (hipStream_t)hip_stream) != 0)
         return fail(CYFA_ERR_UNSUPPORTED, "cyfa_decode_step: no kernel for K=%d V=%d", a->K, a->V);
@@ -293,7 +333,7 @@ int chunk_fwd(const CyfaChunkArgs* a, const CyfaOutNormArgs* on, void* hip_strea
     p.on_eps = on ? on->eps : 0.f;
     p.on_prescale = on ? on->prescale : 1.f;
     if (use_scratch) {
-        if (int rc = scratch_base(&workspace, "cyfa_chunk_fwd_noalloc")) return rc;
+        if (int rc = scratch_base((hipStream_t)hip_stream, &workspace, "cyfa_chunk_fwd_noalloc")) return rc;
     }
     char* base = (char*)workspace;
     p.lam = (float*)(base + ws.lam);

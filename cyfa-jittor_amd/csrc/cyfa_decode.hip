@@ -482,6 +482,35 @@ __device__ __forceinline__ void qk_norms(const DecodeParams& p, float qv, float 
     }
 }
 
+// The prefetch workgroups of the layer step (block ids B H onward, `nwg` of
+// them; this is number `wg`): the ranges p.pf[r] are read in units of 16 KiB
+// (one 16-byte load per thread), unit u by workgroup u mod nwg, eight units in
+// flight per workgroup, range after range, so that the first range is in the
+// caches first. The values are consumed by an empty asm statement (the loads
+// must not be dropped) and nothing is written. Loads past a range's end
+// return zero (the buffer's bounds).
+__device__ __forceinline__ void prefetch_ranges(const DecodeParams& p, int wg, int nwg) {
+#pragma unroll 1
+    for (int r = 0; r < 4; r++) {
+        const unsigned long long bytes = p.pf_bytes[r];
+        if (bytes == 0) continue;
+        const rsrc_t rs = buf(p.pf[r], (size_t)bytes);
+        const uint32_t units = (uint32_t)((bytes + 16383) >> 14);  // bytes < 2^31: no 32-bit overflow below
+#pragma unroll 1
+        for (uint32_t u0 = (uint32_t)wg; u0 < units; u0 += 8u * (uint32_t)nwg) {
+            f32x4 v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint32_t u = u0 + (uint32_t)i * (uint32_t)nwg;
+                const uint32_t off = (u << 14) + (uint32_t)threadIdx.x * 16u;
+                v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off | (u < units ? 0u : DEAD), 0, 0));
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) asm volatile("" ::"v"(v[i]));
+        }
+    }
+}
+
 // The one-workgroup form. LAYER: the layer's one-token step around the op in
 // the same kernel: q, k and v from the short convolution and the new conv
 // cache, the gate activations from the a|b|d row, and o through the gated
@@ -499,6 +528,10 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     constexpr int VJ = kSlots / VROWS;
     constexpr int NW = NT / 64;
     constexpr int OJ = (V + 255) / 256;
+    if (LAYER && (int)blockIdx.x >= p.B * p.H) {  // a prefetch workgroup (the whole workgroup exits here)
+        prefetch_ranges(p, (int)blockIdx.x - p.B * p.H, p.pf_wgs);
+        return;
+    }
     const int bh = blockIdx.x, h = bh % p.H, b = bh / p.H, tid = threadIdx.x, vt = tid & 255;
 
     __shared__ float s_q[K], s_k[K], s_w[kSlots], s_raw[kSlots], s_z[kSlots];
@@ -800,7 +833,10 @@ void launch(const DecodeParams& p, hipStream_t stream) {
         hipLaunchKernelGGL((decode_split_a_kernel<K, V, LAYER>), dim3(NSL, BH), dim3(256), 0, stream, p);
         hipLaunchKernelGGL((decode_split_b_kernel<K, V, LAYER>), dim3(BH), dim3(1024), 0, stream, p);
     } else {
-        hipLaunchKernelGGL((decode_step_kernel<K, V, LAYER>), dim3(BH), dim3(1024), 0, stream, p);
+        // the layer step's prefetch workgroups follow the B H step workgroups
+        // (dispatched after them, so they take the idle compute units)
+        const int extra = LAYER ? p.pf_wgs : 0;
+        hipLaunchKernelGGL((decode_step_kernel<K, V, LAYER>), dim3(BH + extra), dim3(1024), 0, stream, p);
     }
 }
 

@@ -39,6 +39,12 @@ struct DecodeParams {
     // Small batches (B H < DECODE_SPLIT_BH): the workspace for the slices'
     // partial raw, [B H, max(K, V) / 32, 128] f32; null: one workgroup per (b, h).
     float* part;
+    // Layer step, one-workgroup form: pf_wgs extra workgroups (block ids B H
+    // onward) read the ranges pf[r] of pf_bytes[r] bytes (each below 2^31,
+    // 16-byte aligned; 0: none) into the caches and exit.
+    const void* pf[4];
+    unsigned long long pf_bytes[4];
+    int pf_wgs;
 };
 
 // B H below which a decode step is split across eight workgroups per (b, h).

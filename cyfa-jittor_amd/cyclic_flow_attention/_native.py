@@ -14,7 +14,7 @@ import torch
 import torch.nn.functional as F
 
 LIB_PATH = Path(os.environ.get("CYFA_LIB", Path(__file__).with_name("libcyfa_hip.so")))
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 CYFA_OK = 0
 CYFA_ERR_VALUE = -1
@@ -24,6 +24,11 @@ CYFA_ERR_WORKSPACE = -4
 CYFA_ERR_LAUNCH = -5
 
 _c_int, _c_float, _c_void_p, _c_size_t = ctypes.c_int, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
+
+# cyfa_decode_layer_step's cache-prefetch ranges, and the largest B H with
+# which the kernel prefetches them (CYFA_PREFETCH_RANGES, CYFA_PREFETCH_MAX_BH)
+PREFETCH_RANGES = 4
+PREFETCH_MAX_BH = 64
 
 
 class CyfaChunkArgs(ctypes.Structure):
@@ -87,6 +92,7 @@ class CyfaDecodeLayerArgs(ctypes.Structure):
         ("dt_bias", _c_void_p), ("A_log", _c_void_p), ("gate", _c_void_p), ("gate_row", ctypes.c_longlong),
         ("norm_weight", _c_void_p), ("norm_eps", _c_float), ("norm_prescale", _c_float),
         ("g0", _c_void_p), ("g0_row", ctypes.c_longlong), ("g_weight", _c_void_p), ("g_bias", _c_void_p),
+        ("prefetch", _c_void_p * PREFETCH_RANGES), ("prefetch_bytes", ctypes.c_ulonglong * PREFETCH_RANGES),
     ]
 
 

@@ -48,6 +48,23 @@ class GatedMLP(nn.Module):
         u = self.up_proj(x)
         return self.down_proj((F.silu(g.float()) * u.float()).to(x.dtype))
 
+    def _step_gate_up(self, norm, K):
+        """The gate|up weight a decode step reads: interleaved, with the norm
+        weight folded in when fold_norm_weight is set."""
+        w = self._gate_up_il.get(self.gate_proj.weight, self.up_proj.weight, build=_native.interleave_gate_up)
+        if self.fold_norm_weight and K <= _native.LINEAR_NORM_MAX_K:
+            w = self._gate_up_folded.get(w, norm.weight, build=_native.fold_norm_weight)
+        return w
+
+    def step_weights(self, norm, x):
+        """The weights a decode step of forward_block(x, norm) reads, in the
+        order it reads them (gate|up, then down); () when it runs elsewhere."""
+        rows = x.numel() // x.shape[-1]
+        if (inference_fast_path(x) and rows <= _native.LINEAR_ROWS_MAX and self.gate_proj.weight.shape[0] % 16 == 0
+                and x.shape[-1] % 32 == 0):
+            return self._step_gate_up(norm, x.shape[-1]), self.down_proj.weight
+        return ()
+
     def forward_block(self, x, norm):
         """The MLP half of a decoder block, x + self(norm(x)). A decode step with
         at most 64 rows runs the norm inside the gate|up projection and the
@@ -55,9 +72,8 @@ class GatedMLP(nn.Module):
         rows = x.numel() // x.shape[-1]
         if (inference_fast_path(x) and rows <= _native.LINEAR_ROWS_MAX and self.gate_proj.weight.shape[0] % 16 == 0
                 and x.shape[-1] % 32 == 0):
-            w = self._gate_up_il.get(self.gate_proj.weight, self.up_proj.weight, build=_native.interleave_gate_up)
+            w = self._step_gate_up(norm, x.shape[-1])
             if self.fold_norm_weight and x.shape[-1] <= _native.LINEAR_NORM_MAX_K:
-                w = self._gate_up_folded.get(w, norm.weight, build=_native.fold_norm_weight)
                 _, h = _native.norm_linear(x, None, norm.eps, w, swiglu=True)
             else:
                 _, h = _native.norm_linear(x, norm.weight, norm.eps, w, swiglu=True)
@@ -111,7 +127,8 @@ class CyclicFlowAttentionModel(nn.Module):
             # it, each residual add inside the projection before it (x + y, as
             # CyFABlock.forward, bit for bit)
             for i, layer in enumerate(self.layers):
-                x, s = layer.attn.forward_block(x, layer.attn_norm, None if cache is None else cache[i], use_cache)
+                x, s = layer.attn.forward_block(x, layer.attn_norm, None if cache is None else cache[i], use_cache,
+                                                prefetch=layer.mlp.step_weights(layer.mlp_norm, x))
                 x = layer.mlp.forward_block(x, layer.mlp_norm)
                 new.append(s)
             return self.norm(x), (new if use_cache else None)

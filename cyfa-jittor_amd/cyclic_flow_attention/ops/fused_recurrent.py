@@ -123,7 +123,8 @@ def fused_recurrent_cyfa(
 
 def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias, A_log, gate, norm_weight, norm_eps,
                       norm_prescale, table, q_norm_weight, k_norm_weight, q_norm_eps, k_norm_eps, num_heads,
-                      initial_state=None, output_final_state=False, inplace=False, split=False, g_proj=None):
+                      initial_state=None, output_final_state=False, inplace=False, split=False, g_proj=None,
+                      prefetch=()):
     """The layer's one-token step around the op in one kernel (cyfa_decode_layer_step).
 
     qkv [B, 1, 3 H 256] is the projection before the short convolution (rows
@@ -136,7 +137,11 @@ def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias
     fused_recurrent_cyfa. ``g_proj`` (with gate None): (g0 [B, 1, 256], weight
     [H 256, 256], bias [H 256] or None), and the kernel forms the gate as
     linear(g0, weight, bias) - the second projection of g_proj - with the same
-    bits as _native.linear.
+    bits as _native.linear. ``prefetch``: up to four contiguous device tensors
+    (the weights of the projections that follow the step) that the launch
+    reads into the device's caches on the compute units the step leaves idle,
+    when B H <= _native.PREFETCH_MAX_BH and the one-workgroup form runs;
+    nothing depends on their values.
     """
     B = qkv.shape[0]
     H, K, V, M = num_heads, 256, 256, table.shape[-1]
@@ -213,5 +218,12 @@ def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias
         norm_prescale=float(norm_prescale), g0=_native.ptr(g0), g0_row=0 if g0 is None else g0.stride(0),
         g_weight=_native.ptr(g_w), g_bias=_native.ptr(g_b),
     )
+    if len(prefetch) > _native.PREFETCH_RANGES:
+        raise ValueError(f"decode_layer_step: at most {_native.PREFETCH_RANGES} prefetch tensors")
+    for i, t in enumerate(prefetch):
+        if not t.is_contiguous() or t.device != qkv.device:
+            raise ValueError("decode_layer_step: prefetch tensors must be contiguous, on the step's device")
+        layer.prefetch[i] = t.data_ptr()
+        layer.prefetch_bytes[i] = t.numel() * t.element_size()
     _native.decode_layer_step(args, layer, dev)
     return o, ((hk_out, hv_out, c_out) if output_final_state else None)

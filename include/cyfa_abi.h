@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define CYFA_ABI_VERSION 8
+#define CYFA_ABI_VERSION 9
 
 enum {
     CYFA_OK = 0,
@@ -98,7 +98,8 @@ int cyfa_chunk_fwd_normed(const CyfaChunkArgs *args, const CyfaOutNormArgs *norm
  * args->workspace_bytes are ignored, and the intermediates live in a device
  * array of CYFA_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds
  * until the process ends (its address is resolved on the first call on each
- * device). For callers that cannot allocate device memory: code under HIP
+ * device: the device of hip_stream, or the current device for the null
+ * stream). For callers that cannot allocate device memory: code under HIP
  * graph capture, serving loops that forbid allocation. No counterpart in the
  * reference. Calls whose workspace would exceed the array return
  * CYFA_ERR_UNSUPPORTED. Every call on one GPU uses that GPU's one array, so
@@ -173,6 +174,11 @@ size_t cyfa_decode_workspace_bytes(int B, int H, int K, int V);
  * (hk_out == hk_in, ...) is allowed. */
 int cyfa_decode_step(const CyfaDecodeArgs *args, void *hip_stream);
 
+/* Prefetch ranges of cyfa_decode_layer_step, and the largest B H with which
+ * it prefetches them. */
+#define CYFA_PREFETCH_RANGES 4
+#define CYFA_PREFETCH_MAX_BH 64
+
 /* The rest of the layer's one-token step, for the decode loop (K = V = 256,
  * conv width 4, no conv bias). */
 typedef struct CyfaDecodeLayerArgs {
@@ -198,6 +204,16 @@ typedef struct CyfaDecodeLayerArgs {
     long long g0_row;             /* a multiple of 8 */
     const void *g_weight;         /* bf16 [H 256, 256], 16-byte aligned */
     const void *g_bias;           /* nullable bf16 [H 256] */
+    /* Cache prefetch (no reference counterpart; all NULL / 0: none). At small
+       batches the step occupies one compute unit per (batch, head) and leaves
+       HBM almost idle; with B H <= CYFA_PREFETCH_MAX_BH the launch adds
+       workgroups on the idle compute units that read these device ranges --
+       the weights of the projections that follow the step -- into the
+       device's caches, so that those launches read them from the last-level
+       cache instead of HBM. The ranges are only read (16-byte aligned, each
+       below 4 GiB); no result depends on them. */
+    const void *prefetch[CYFA_PREFETCH_RANGES];
+    unsigned long long prefetch_bytes[CYFA_PREFETCH_RANGES];
 } CyfaDecodeLayerArgs;
 
 /* cyfa_decode_step with the layer around it in the same kernel: q, k and v
@@ -258,7 +274,13 @@ typedef struct CyfaChunkBwdArgs {
     size_t workspace_bytes;
 } CyfaChunkBwdArgs;
 
-/* Workspace bytes of cyfa_chunk_bwd (0 for a non-positive argument). */
+/* Workspace bytes of cyfa_chunk_bwd (0 for a non-positive argument): the
+ * recomputed fp32 rows (q_hat, k_hat, v, the cotangent of o), the states
+ * before every chunk of both passes and their cotangents (fp32,
+ * 4 B H (N + 1) K M bytes per stack, N = ceil(T / 64)) and the rows'
+ * cotangents; about 1.4 GB at B=8, T=2048, H=4, K=V=256, M=128.
+ * cyfa_chunk_bwd refuses B H ceil(T / 64) 64 >= 2^21 padded rows (its
+ * kernels index rows and chunk states with 32-bit counts). */
 size_t cyfa_chunk_bwd_workspace_bytes(int B, int T, int H, int K, int V, int M);
 
 /* Gradients of the chunkwise CyFA op with respect to q, k, v, g, delta, beta,

@@ -304,3 +304,25 @@ def test_decode_workspace_query():
     assert lib.cyfa_decode_workspace_bytes(16, 4, 256, 256) == 0
     assert lib.cyfa_decode_workspace_bytes(2, 2, 128, 128) == 4 * 4 * 128 * 4
     assert lib.cyfa_decode_workspace_bytes(1, 1, 512, 256) == 0  # no kernel for K = 512
+
+
+def test_decode_layer_prefetch_ranges_validated_before_launch():
+    """cyfa_decode_layer_step checks its cache-prefetch ranges before any launch:
+    a range with bytes needs a pointer, 16-byte alignment and fewer than 2^31
+    bytes (the pointers are never dereferenced here)."""
+    lib = _native.load_library()
+    H = 8
+    a = _native.CyfaDecodeArgs(B=1, H=H, K=256, V=256, M=128, table=0x10000, q_norm_weight=0x20000,
+                               k_norm_weight=0x30000, scale=0.0625, o=0x40000, hk_out=0x50000, hv_out=0x60000,
+                               clock_out=0x70000)
+    ly = _native.CyfaDecodeLayerArgs(qkv=0x80000, qkv_row=3 * H * 256, conv_cache_out=0x90000,
+                                     cache_row=3 * H * 256, cache_batch=9 * H * 256, conv_weight=0xa0000,
+                                     abd=0xb0000, abd_row=3 * H, dt_bias=0xc0000, A_log=0xd0000, gate=0xe0000,
+                                     gate_row=H * 256, norm_weight=0xf0000, norm_eps=1e-6, norm_prescale=127.0)
+    ly.prefetch_bytes[1] = 4096  # bytes without a pointer
+    assert lib.cyfa_decode_layer_step(ctypes.byref(a), ctypes.byref(ly), None) == _native.CYFA_ERR_VALUE
+    assert b"prefetch range 1" in lib.cyfa_last_error()
+    ly.prefetch[1] = 0x100008  # misaligned
+    assert lib.cyfa_decode_layer_step(ctypes.byref(a), ctypes.byref(ly), None) == _native.CYFA_ERR_ALIGN
+    ly.prefetch[1], ly.prefetch_bytes[1] = 0x100000, 1 << 31  # too large for the kernel's 32-bit offsets
+    assert lib.cyfa_decode_layer_step(ctypes.byref(a), ctypes.byref(ly), None) == _native.CYFA_ERR_VALUE

@@ -463,6 +463,67 @@ def test_decode_layer_step_equals_separate_kernels(B, state, inplace, split, own
         assert st2[0].data_ptr() == st_in[0].data_ptr()
 
 
+@pytest.mark.parametrize("B,H", [(1, 8), (4, 4), (16, 4), (64, 4)])
+def test_decode_layer_step_prefetch_changes_nothing(B, H):
+    """The layer step's cache prefetch (extra workgroups reading device ranges
+    at B H <= 64; ignored above) leaves every output bit as it is: o', the
+    states and the conv cache equal the step without it. The ranges have odd
+    sizes (a partial 16 KiB unit, a 16-byte one)."""
+    from cyclic_flow_attention import _native
+    from cyclic_flow_attention.ops.fused_recurrent import decode_layer_step
+
+    D = 3 * H * 256
+    gen = torch.Generator().manual_seed(77 + B + H)
+    qkv = torch.randn(B, 1, D, generator=gen).bfloat16().to(DEV)
+    cache = (0.5 * torch.randn(B, 3, D, generator=gen)).bfloat16().to(DEV)
+    wconv = (0.3 * torch.randn(D, 4, generator=gen)).bfloat16().to(DEV)
+    abd = torch.randn(B, 1, 3 * H, generator=gen).bfloat16().to(DEV)
+    dt_bias, A_log = torch.randn(H, generator=gen).to(DEV), torch.randn(H, generator=gen).to(DEV)
+    gate = torch.randn(B, 1, H * 256, generator=gen).bfloat16().to(DEV)
+    nw = (1 + 0.1 * torch.randn(256, generator=gen)).to(DEV)
+    qw, kw = (1 + 0.1 * torch.randn(256, generator=gen)).to(DEV), (1 + 0.1 * torch.randn(256, generator=gen)).to(DEV)
+    table = _native.readout_table((torch.eye(127).expand(H, 127, 127)
+                                   + 0.05 * torch.randn(H, 127, 127, generator=gen)).contiguous().to(DEV))
+    init = (0.3 * torch.randn(B, H, 256, 128, generator=gen).to(DEV),
+            0.3 * torch.randn(B, H, 128, 256, generator=gen).to(DEV), 50 * torch.rand(B, H, generator=gen).to(DEV))
+    ranges = (torch.randn(4_200_000, device=DEV).bfloat16(),
+              torch.randn(250_003, device=DEV), torch.randn(4, device=DEV))
+    outs = []
+    with torch.no_grad():
+        for pf in ((), tuple(r for r in ranges if r.numel())):
+            tail = torch.empty(B, 3, D, dtype=torch.bfloat16, device=DEV)
+            o, st = decode_layer_step(qkv, cache, tail, wconv, abd, dt_bias, A_log, gate, nw, 1e-6, 127.0, table, qw,
+                                      kw, 1e-6, 1e-6, H, initial_state=tuple(t.clone() for t in init),
+                                      output_final_state=True, prefetch=pf)
+            outs.append((o, st, tail))
+    torch.cuda.synchronize()
+    (o0, st0, t0), (o1, st1, t1) = outs
+    assert torch.equal(o0, o1) and torch.equal(t0, t1)
+    for a, b in zip(st0, st1):
+        assert torch.equal(a, b)
+
+
+def test_model_decode_prefetch_changes_nothing():
+    """A 400M-shape model (2 layers) decoding at B=2: the decode steps with
+    the layers' weight prefetch equal the steps without it, bit for bit."""
+    model, _, cfg = _model("cyclic_flow_attention_400m.json", seed=9, layers=2)
+    ids = torch.randint(0, cfg["vocab_size"], (2, 70), generator=torch.Generator().manual_seed(10)).to(DEV)
+    logits = []
+    with torch.no_grad():
+        for on in (False, True):
+            for blk in model.model.layers:
+                blk.attn.prefetch_weights = on
+            out = model(ids, use_cache=True)
+            cache, tok, run = out["cache"], out["logits"][:, -1:].argmax(-1), []
+            for _ in range(4):
+                out = model(tok, cache=cache, use_cache=True)
+                cache, tok = out["cache"], out["logits"][:, -1:].argmax(-1)
+                run.append(out["logits"])
+            logits.append(torch.cat(run, 1))
+    torch.cuda.synchronize()
+    assert torch.equal(logits[0], logits[1])
+
+
 @pytest.mark.parametrize("M", [1, 37, 64])
 def test_linear_swiglu_equals_projection_then_silu_mul(M):
     """The SwiGLU epilogue of cyfa_linear_rows (interleaved gate|up weight)
