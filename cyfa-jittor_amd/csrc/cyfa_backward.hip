@@ -26,7 +26,8 @@
 // workgroups. The
 // readout adjoint runs per row (z = U(lam) raw, softmax of table z, u =
 // table^T p, weights = U(-lam) u) with the head's table and this
-// workgroup's share of the table cotangent on chip; partial sums (table,
+// workgroup's share of the table cotangent on chip (up to 128 slots; above,
+// as tile GEMMs that stream the table); partial sums (table,
 // norm weights, per-column-tile boundary terms) are added in a fixed order,
 // so the result does not depend on scheduling. fp32 FMA loops over LDS
 // tiles, no matrix cores: a first, exact form of the training path.
@@ -572,13 +573,13 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
 __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, const float* cs, const float* sn,
                                                              const float* table, int B, int Tp, int H, int M,
                                                              int per_wg, float* wts) {
-    constexpr int LD = BWD_MAX_M + 1, RB = 32;
-    __shared__ float sTab[BWD_MAX_M * LD];  // rows R .. 127 zero
+    constexpr int TM = BWD_TABLE_M, LD = TM + 1, RB = 32;
+    __shared__ float sTab[TM * LD];  // rows R .. 127 zero
     __shared__ float sZ[RB][LD], sP[RB][LD];
-    __shared__ float sCs[RB][BWD_MAX_M / 2], sSn[RB][BWD_MAX_M / 2];
+    __shared__ float sCs[RB][TM / 2], sSn[RB][TM / 2];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, h = blockIdx.y;
     const int R = M - 1, P = M / 2, rows = B * Tp;
-    for (int e = tid; e < BWD_MAX_M * LD; e += 256) {
+    for (int e = tid; e < TM * LD; e += 256) {
         const int r = e / LD, m = e % LD;
         sTab[e] = (r < R && m < M) ? table[((size_t)h * R + r) * M + m] : 0.f;
     }
@@ -586,8 +587,8 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
     const int br = 4 * (tid >> 5), bc = 4 * (tid & 31);
     for (int b0 = blockIdx.x * per_wg * RB; b0 < min(rows, (blockIdx.x + 1) * per_wg * RB); b0 += RB) {
         __syncthreads();  // the table is staged; the previous block's tiles are done with
-        for (int e = tid; e < RB * (BWD_MAX_M / 2); e += 256) {
-            const int i = e / (BWD_MAX_M / 2), pr = e % (BWD_MAX_M / 2), rho = b0 + i;
+        for (int e = tid; e < RB * (TM / 2); e += 256) {
+            const int i = e / (TM / 2), pr = e % (TM / 2), rho = b0 + i;
             float ze = 0.f, zo = 0.f, c = 1.f, s = 0.f;
             if (rho < rows && pr < P) {
                 const size_t row = row_of(rho);
@@ -683,14 +684,14 @@ struct ReadoutGradArgs {
 };
 
 __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
-    constexpr int LD = BWD_MAX_M + 1;
-    __shared__ float sTab[BWD_MAX_M * LD];  // rows R .. 127 zero
+    constexpr int TM = BWD_TABLE_M, LD = TM + 1;
+    __shared__ float sTab[TM * LD];  // rows R .. 127 zero
     __shared__ float sZ[RO_BLK][LD], sDU[RO_BLK][LD], sP[RO_BLK][LD], sDL[RO_BLK][LD];
-    __shared__ float sCs[RO_BLK][BWD_MAX_M / 2], sSn[RO_BLK][BWD_MAX_M / 2];
+    __shared__ float sCs[RO_BLK][TM / 2], sSn[RO_BLK][TM / 2];
     __shared__ float sLam[RO_BLK][32];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, blk = blockIdx.x, h = blockIdx.y;
     const int M = a.M, R = M - 1, P = M / 2, RM = R * M;
-    for (int e = tid; e < BWD_MAX_M * LD; e += 256) {  // the table, zero beyond R x M
+    for (int e = tid; e < TM * LD; e += 256) {  // the table, zero beyond R x M
         const int r = e / LD, m = e % LD;
         sTab[e] = (r < R && m < M) ? a.table[((size_t)h * R + r) * M + m] : 0.f;
     }
@@ -703,8 +704,8 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
     for (int b0 = blk * a.per_wg * RO_BLK; b0 < min(rows, (blk + 1) * a.per_wg * RO_BLK); b0 += RO_BLK) {
         __syncthreads();  // the previous block's tiles are done with
         // z = U(lam) raw and du = U(lam) dweights, one (row, pair) per thread step
-        for (int e = tid; e < RO_BLK * (BWD_MAX_M / 2); e += 256) {
-            const int i = e / (BWD_MAX_M / 2), pr = e % (BWD_MAX_M / 2), rho = b0 + i;
+        for (int e = tid; e < RO_BLK * (TM / 2); e += 256) {
+            const int i = e / (TM / 2), pr = e % (TM / 2), rho = b0 + i;
             float ze = 0.f, zo = 0.f, ue = 0.f, uo = 0.f, c = 1.f, s = 0.f;
             if (rho < rows && pr < P) {
                 const size_t row = ((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp;
@@ -845,6 +846,208 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
 #pragma unroll
         for (int m = 0; m < 16; m++)
             if (tr + r < R && tc + m < M) dst[(tr + r) * M + tc + m] = dt[r][m];
+}
+
+// The readout and its adjoint for 128 < M <= 256 slots, where a head's table
+// (up to 255 x 256 fp32) does not fit in LDS beside the row blocks: every
+// product is a 64 x 64 fp32 tile GEMM (tile_gemm<false>) that streams the
+// table from memory, and the softmax and its adjoint run per row between
+// them. Token rows rho of head h are the B Tp rows (b, h, t), rho = b Tp + t,
+// at head-major row ((b H + h) Tp + t); X_lam(rho)[m] is U(lam) x (pairs
+// rotated by the row's phases, as z = U(lam) raw and du = U(lam) dweights).
+// Per-row intermediates have MW = 256 columns.
+constexpr int BW_WIDE_MW = BWD_WIDE_MW;        // columns of the wide path's per-row buffers
+constexpr int BW_WIDE_SPLIT = BWD_WIDE_SPLIT;  // token rows per dtable partial
+constexpr int BW_WIDE_CT = BW_WIDE_MW / BC;    // column tiles of a row (the clock's partials)
+
+struct WideArgs {
+    const float *raw, *cs, *sn, *table, *dwts;  // head-major rows; table [H, M-1, M]
+    float *lg, *dl;                             // [B H Tp, MW]: logits then p; dp then dl
+    float *wts, *draw, *dlp, *dlam;             // dlp [B H Tp, BW_WIDE_CT]: the clock's partials
+    float* dtab;                                // [H, splits, (M-1) M]
+    int B, Tp, H, M, splits;
+};
+
+__device__ __forceinline__ size_t wide_row(const WideArgs& a, int h, int rho) {
+    return ((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp;
+}
+
+// Element m of U(lam) x for head-major row `row` (x = raw or dweights).
+__device__ __forceinline__ float wide_rot(const WideArgs& a, const float* x, size_t row, int m) {
+    const int P = a.M / 2, pr = m >> 1;
+    const float c = a.cs[row * P + pr], s = a.sn[row * P + pr];
+    const float e = x[row * a.M + 2 * pr], o = x[row * a.M + 2 * pr + 1];
+    return (m & 1) ? s * e + c * o : c * e - s * o;
+}
+
+// out[row][r] = sum_m X_lam(rho)[m] table[h][r][m] for a 64-row block and 64
+// table rows (X = raw: the logits into lg; X = dweights: dp into dl).
+// Grid (ceil(B Tp / 64), ceil((M - 1) / 64), H).
+template <bool ADJ>
+__global__ __launch_bounds__(256) void bw_wide_logits_kernel(WideArgs a) {
+    __shared__ __align__(16) unsigned char sStage[STAGE_BYTES];
+    const int rho0 = blockIdx.x * BC, r0 = blockIdx.y * BC, h = blockIdx.z;
+    const int M = a.M, R = M - 1, rows = a.B * a.Tp;
+    const float* x = ADJ ? a.dwts : a.raw;
+    const float* tb = a.table + (size_t)h * R * M;
+    float acc[4][4] = {};
+    tile_gemm<false, true>(
+        [&](int i, int m) { return rho0 + i < rows ? wide_rot(a, x, wide_row(a, h, rho0 + i), m) : 0.f; },
+        [&](int m, int j) { return r0 + j < R ? tb[(size_t)(r0 + j) * M + m] : 0.f; }, M, sStage, acc);
+    float* out = ADJ ? a.dl : a.lg;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int rho = rho0 + TileMap<false>::row(i, 0);
+        if (rho >= rows) continue;
+        const size_t row = wide_row(a, h, rho);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = r0 + TileMap<false>::col(i, j);
+            if (r < R) out[row * BW_WIDE_MW + r] = acc[i][j];
+        }
+    }
+}
+
+// Per row, one wave: p = softmax(logits) over the R = M - 1 slots into lg;
+// ADJ: dl = p (dp - p.dp) into dl (p already in lg). Grid ceil(B H Tp / 4).
+template <bool ADJ>
+__global__ __launch_bounds__(256) void bw_wide_softmax_kernel(WideArgs a) {
+    const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, R = a.M - 1;
+    if (row >= (size_t)a.B * a.H * a.Tp) return;
+    float* lg = a.lg + row * BW_WIDE_MW;
+    float v[4];
+    if (!ADJ) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = lane + 64 * i;
+            v[i] = r < R ? lg[r] : -INFINITY;
+            mx = fmaxf(mx, v[i]);
+        }
+        mx = bw_wave_max(mx);
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            v[i] = lane + 64 * i < R ? expf(v[i] - mx) : 0.f;
+            sum += v[i];
+        }
+        const float inv = 1.f / bw_wave_sum(sum);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (lane + 64 * i < R) lg[lane + 64 * i] = v[i] * inv;
+    } else {
+        float* dl = a.dl + row * BW_WIDE_MW;
+        float pv[4], pdp = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = lane + 64 * i;
+            pv[i] = r < R ? lg[r] : 0.f;
+            v[i] = r < R ? dl[r] : 0.f;
+            pdp += pv[i] * v[i];
+        }
+        pdp = bw_wave_sum(pdp);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (lane + 64 * i < R) dl[lane + 64 * i] = pv[i] * (v[i] - pdp);
+    }
+}
+
+// u = p table for a 64-row block and 64 columns (m0 ..), then
+//   forward: weights = U(-lam) u into wts;
+//   ADJ: dz = dl table as well; draw = U(-lam) dz, and the clock's share of
+//   the block's pairs, kappa_p [(z_e dz_o - z_o dz_e) + (du_e u_o - du_o u_e)],
+//   summed over the tile's pairs in column order into dlp[row][m0 / 64].
+// Grid (ceil(B Tp / 64), ceil(M / 64), H).
+template <bool ADJ>
+__global__ __launch_bounds__(256) void bw_wide_u_kernel(WideArgs a) {
+    __shared__ __align__(16) unsigned char sStage[STAGE_BYTES];
+    __shared__ float sPart[BC][17];
+    const int tid = threadIdx.x, rho0 = blockIdx.x * BC, m0 = blockIdx.y * BC, h = blockIdx.z;
+    const int M = a.M, R = M - 1, P = M / 2, rows = a.B * a.Tp;
+    const float* tb = a.table + (size_t)h * R * M;
+    const auto tab = [&](int r, int j) { return m0 + j < M ? tb[(size_t)r * M + m0 + j] : 0.f; };
+    float u[4][4] = {}, dz[4][4] = {};
+    tile_gemm<false, false>(
+        [&](int i, int r) { return rho0 + i < rows ? a.lg[wide_row(a, h, rho0 + i) * BW_WIDE_MW + r] : 0.f; }, tab, R,
+        sStage, u);
+    if (ADJ)
+        tile_gemm<false, false>(
+            [&](int i, int r) { return rho0 + i < rows ? a.dl[wide_row(a, h, rho0 + i) * BW_WIDE_MW + r] : 0.f; },
+            tab, R, sStage, dz);
+    const int cg = tid & 15;  // this thread's four columns m0 + 4 cg ..: pairs (m0 + 4 cg) / 2 and + 1
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int ri = TileMap<false>::row(i, 0), rho = rho0 + ri;
+        float dls = 0.f;
+        if (rho < rows) {
+            const size_t row = wide_row(a, h, rho);
+#pragma unroll
+            for (int j = 0; j < 4; j += 2) {
+                const int m = m0 + TileMap<false>::col(i, j), pr = m >> 1;
+                if (pr >= P) continue;
+                const float c = a.cs[row * P + pr], s = a.sn[row * P + pr];
+                if (!ADJ) {
+                    a.wts[row * M + m] = c * u[i][j] + s * u[i][j + 1];
+                    a.wts[row * M + m + 1] = -s * u[i][j] + c * u[i][j + 1];
+                } else {
+                    const float ge = dz[i][j], go = dz[i][j + 1], ue = u[i][j], uo = u[i][j + 1];
+                    a.draw[row * M + m] = c * ge + s * go;
+                    a.draw[row * M + m + 1] = -s * ge + c * go;
+                    const float ze = wide_rot(a, a.raw, row, m), zo = wide_rot(a, a.raw, row, m + 1);
+                    const float de = wide_rot(a, a.dwts, row, m), dd = wide_rot(a, a.dwts, row, m + 1);
+                    dls += (float)(kTwoPiBw * pr / R) * ((ze * go - zo * ge) + (de * uo - dd * ue));
+                }
+            }
+        }
+        if (ADJ) sPart[ri][cg] = dls;
+    }
+    if (ADJ) {
+        __syncthreads();
+        if (tid < BC && rho0 + tid < rows) {
+            float t = 0.f;
+            for (int g = 0; g < 16; g++) t += sPart[tid][g];
+            a.dlp[wide_row(a, h, rho0 + tid) * BW_WIDE_CT + blockIdx.y] = t;
+        }
+    }
+}
+
+// The readout's share of the clock cotangent: the column tiles' partials in
+// order. One thread per head-major row.
+__global__ __launch_bounds__(256) void bw_wide_dlam_kernel(WideArgs a) {
+    const size_t row = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (row >= (size_t)a.B * a.H * a.Tp) return;
+    const int nt = (a.M + BC - 1) / BC;
+    float t = 0.f;
+    for (int c = 0; c < nt; c++) t += a.dlp[row * BW_WIDE_CT + c];
+    a.dlam[row] = t;
+}
+
+// dtable[h][r][m] partial over token rows [split BW_WIDE_SPLIT, + BW_WIDE_SPLIT):
+// sum_rho p[rho][r] du[rho][m] + dl[rho][r] z[rho][m], for 64 table rows and
+// 64 columns. Grid (ceil((M - 1) / 64), ceil(M / 64), H splits).
+__global__ __launch_bounds__(256) void bw_wide_dtable_kernel(WideArgs a) {
+    __shared__ __align__(16) unsigned char sStage[STAGE_BYTES];
+    const int r0 = blockIdx.x * BC, m0 = blockIdx.y * BC, h = blockIdx.z / a.splits, sp = blockIdx.z % a.splits;
+    const int M = a.M, R = M - 1, rows = a.B * a.Tp, k0 = sp * BW_WIDE_SPLIT;
+    const int Kd = min(BW_WIDE_SPLIT, rows - k0);
+    float acc[4][4] = {};
+    tile_gemm<false, false>(
+        [&](int i, int k) { return r0 + i < R ? a.lg[wide_row(a, h, k0 + k) * BW_WIDE_MW + r0 + i] : 0.f; },
+        [&](int k, int j) { return m0 + j < M ? wide_rot(a, a.dwts, wide_row(a, h, k0 + k), m0 + j) : 0.f; }, Kd,
+        sStage, acc);
+    tile_gemm<false, false>(
+        [&](int i, int k) { return r0 + i < R ? a.dl[wide_row(a, h, k0 + k) * BW_WIDE_MW + r0 + i] : 0.f; },
+        [&](int k, int j) { return m0 + j < M ? wide_rot(a, a.raw, wide_row(a, h, k0 + k), m0 + j) : 0.f; }, Kd,
+        sStage, acc);
+    float* dst = a.dtab + ((size_t)h * a.splits + sp) * R * M;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = r0 + TileMap<false>::row(i, j), m = m0 + TileMap<false>::col(i, j);
+            if (r < R && m < M) dst[(size_t)r * M + m] = acc[i][j];
+        }
 }
 
 // Per chunk of (b, h): the gate cotangent of both passes (dL/dG_t = q.dq -
@@ -1121,8 +1324,36 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     else
         hipLaunchKernelGGL(bw_out_kernel<false>, dim3(N, H, B), blk, 0, stream, oa);
     const int ro_per_wg = bwd_ro_per_wg(B, Tp, H);
-    hipLaunchKernelGGL(bw_fwd_readout_kernel, dim3(ws.ro_blocks, H), blk, 0, stream, ws.raw, ws.cs, ws.sn, p.table, B,
-                       Tp, H, M, ro_per_wg, ws.wts);
+    const bool wide = M > BWD_TABLE_M;
+    WideArgs wa{};
+    wa.raw = ws.raw;
+    wa.cs = ws.cs;
+    wa.sn = ws.sn;
+    wa.table = p.table;
+    wa.dwts = ws.dwts;
+    wa.lg = ws.lg;
+    wa.dl = ws.dlw;
+    wa.wts = ws.wts;
+    wa.draw = ws.draw;
+    wa.dlp = ws.dlp;
+    wa.dlam = ws.dlam;
+    wa.dtab = ws.dtab;
+    wa.B = B;
+    wa.Tp = Tp;
+    wa.H = H;
+    wa.M = M;
+    wa.splits = ws.ro_blocks;
+    const int rows_h = B * Tp;
+    const dim3 g_logits((rows_h + BC - 1) / BC, (M - 1 + BC - 1) / BC, H), g_u((rows_h + BC - 1) / BC, (M + BC - 1) / BC, H);
+    const dim3 g_rows((unsigned)((rows + 3) / 4));
+    if (wide) {  // logits, softmax, then the weights
+        hipLaunchKernelGGL(bw_wide_logits_kernel<false>, g_logits, blk, 0, stream, wa);
+        hipLaunchKernelGGL(bw_wide_softmax_kernel<false>, g_rows, blk, 0, stream, wa);
+        hipLaunchKernelGGL(bw_wide_u_kernel<false>, g_u, blk, 0, stream, wa);
+    } else {
+        hipLaunchKernelGGL(bw_fwd_readout_kernel, dim3(ws.ro_blocks, H), blk, 0, stream, ws.raw, ws.cs, ws.sn, p.table,
+                           B, Tp, H, M, ro_per_wg, ws.wts);
+    }
     StateScanArgs f2 = f1;
     f2.a = ws.w;
     f2.b = ws.vh;
@@ -1176,7 +1407,16 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     ro.H = H;
     ro.M = M;
     ro.per_wg = ro_per_wg;
-    hipLaunchKernelGGL(bw_readout_kernel, dim3(ws.ro_blocks, H), blk, 0, stream, ro);
+    if (wide) {  // dp, dl, then dz with draw and the clock's share, and the table cotangent's partials
+        hipLaunchKernelGGL(bw_wide_logits_kernel<true>, g_logits, blk, 0, stream, wa);
+        hipLaunchKernelGGL(bw_wide_softmax_kernel<true>, g_rows, blk, 0, stream, wa);
+        hipLaunchKernelGGL(bw_wide_u_kernel<true>, g_u, blk, 0, stream, wa);
+        hipLaunchKernelGGL(bw_wide_dlam_kernel, dim3((unsigned)((rows + 255) / 256)), blk, 0, stream, wa);
+        hipLaunchKernelGGL(bw_wide_dtable_kernel, dim3((M - 1 + BC - 1) / BC, (M + BC - 1) / BC, H * ws.ro_blocks), blk, 0,
+                           stream, wa);
+    } else {
+        hipLaunchKernelGGL(bw_readout_kernel, dim3(ws.ro_blocks, H), blk, 0, stream, ro);
+    }
     // pass 1, with the pass-1 output's cotangent as dO
     StateScanArgs s1 = f1;
     s1.a = ws.qh;

@@ -287,7 +287,11 @@ struct BwdParams {
     float *dh0_k, *dh0_v, *dclock0;       // nullable
     void* workspace;
 };
-constexpr int BWD_MAX_M = 128;
+// Largest slot count of the backward pass, and of its readout kernels that
+// stage a head's table in LDS; above BWD_TABLE_M the readout and its adjoint
+// run as tile GEMMs that stream the table (the "wide" readout).
+constexpr int BWD_MAX_M = 256;
+constexpr int BWD_TABLE_M = 128;
 
 // The backward pass's workspace (fp32 unless noted, each region 256-byte
 // aligned; rows = B*H*Tp head-major, Tp = T rounded up to 64, N = Tp / 64):
@@ -301,10 +305,13 @@ struct BwdWorkspace {
     double* lam;
     float *qh, *kh, *rq, *rk, *vh, *w, *cs, *sn, *raw, *wts, *sk, *sv;
     float *dO, *dsk, *dsv, *dwts, *dw2, *dvh, *draw, *dlam, *dqh, *dkh, *dw1, *bnd1, *bnd2, *dtab, *dnq, *dnk;
+    float *lg, *dlw, *dlp;  // the wide readout (M > BWD_TABLE_M): logits / p, dp / dl [rows, 256]; clock partials [rows, 4]
     int N, nt1, nt2, ro_blocks, norm_blocks;
     size_t bytes;
 };
 constexpr int BWD_RO_BLOCK = 32;    // rows per block of the readout kernels
+constexpr int BWD_WIDE_MW = 256;    // columns of the wide readout's per-row buffers
+constexpr int BWD_WIDE_SPLIT = 1024;  // token rows per table-cotangent partial of the wide readout
 constexpr int BWD_SCAN_ROWS = 32;   // rows of a state-scan tile (its columns: 32)
 constexpr int BWD_NORM_ROWS = 64;   // rows per norm-adjoint workgroup
 
@@ -329,7 +336,10 @@ inline BwdWorkspace bwd_workspace(int B, int T, int H, int K, int V, int M, void
     w.N = (int)N;
     w.nt1 = (M + 31) / 32 * ((K + BWD_SCAN_ROWS - 1) / BWD_SCAN_ROWS);  // the state scans' tiles
     w.nt2 = (V + 31) / 32 * ((M + BWD_SCAN_ROWS - 1) / BWD_SCAN_ROWS);
-    {
+    const bool wide = M > BWD_TABLE_M;
+    if (wide) {  // the table cotangent's partials: one per BWD_WIDE_SPLIT token rows of a head
+        w.ro_blocks = (int)((B * Tp + BWD_WIDE_SPLIT - 1) / BWD_WIDE_SPLIT);
+    } else {
         const int blocks = (int)((B * Tp + BWD_RO_BLOCK - 1) / BWD_RO_BLOCK), per = bwd_ro_per_wg(B, (int)Tp, H);
         w.ro_blocks = (blocks + per - 1) / per;  // readout workgroups per head
     }
@@ -364,6 +374,9 @@ inline BwdWorkspace bwd_workspace(int B, int T, int H, int K, int V, int M, void
     w.dtab = f((size_t)H * w.ro_blocks * (M - 1) * M);
     w.dnq = f((size_t)w.norm_blocks * K);
     w.dnk = f((size_t)w.norm_blocks * K);
+    w.lg = f(wide ? rows * BWD_WIDE_MW : 0);
+    w.dlw = f(wide ? rows * BWD_WIDE_MW : 0);
+    w.dlp = f(wide ? rows * (BWD_WIDE_MW / 64) : 0);
     w.bytes = off;
     return w;
 }

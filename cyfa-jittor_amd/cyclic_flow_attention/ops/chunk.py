@@ -67,7 +67,7 @@ def chunk_cyfa(
     When grad mode is on and q, k, v, g, delta, beta, the readout, a norm
     weight or an initial state requires a gradient, the call is recorded for
     autograd: the forward runs as above and the backward (cyfa_chunk_bwd)
-    returns the gradients of all of them (slot counts up to 128; ``table``,
+    returns the gradients of all of them (slot counts up to 256; ``table``,
     ``output_norm`` and ``no_alloc`` are inference-only).
     """
     if cu_seqlens is not None:
@@ -96,9 +96,10 @@ def chunk_cyfa(
                           scale, initial_state, output_final_state, chunk_size, table, output_norm, no_alloc)
 
 
-# Largest slot count of the backward pass (its readout adjoint keeps the
-# head's table and the table's gradient on chip).
-BWD_MAX_SLOTS = 128
+# Largest slot count of the backward pass (the reference's decode limit,
+# ops/fused_recurrent.py:45-46; up to 128 slots the readout adjoint keeps the
+# head's table on chip, above it streams the table through tile GEMMs).
+BWD_MAX_SLOTS = 256
 
 
 def _chunk_forward(q, k, v, g, delta, beta, readout, q_norm_weight, k_norm_weight, q_norm_eps, k_norm_eps, scale,

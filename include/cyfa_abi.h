@@ -278,7 +278,9 @@ typedef struct CyfaChunkBwdArgs {
  * recomputed fp32 rows (q_hat, k_hat, v, the cotangent of o), the states
  * before every chunk of both passes and their cotangents (fp32,
  * 4 B H (N + 1) K M bytes per stack, N = ceil(T / 64)) and the rows'
- * cotangents; about 1.4 GB at B=8, T=2048, H=4, K=V=256, M=128.
+ * cotangents (above 128 slots also the logits / probabilities and their
+ * cotangents, 2 x 1 KiB per row); about 1.4 GB at B=8, T=2048, H=4,
+ * K=V=256, M=128.
  * cyfa_chunk_bwd refuses B H ceil(T / 64) 64 >= 2^21 padded rows (its
  * kernels index rows and chunk states with 32-bit counts). */
 size_t cyfa_chunk_bwd_workspace_bytes(int B, int T, int H, int K, int V, int M);
@@ -289,7 +291,9 @@ size_t cyfa_chunk_bwd_workspace_bytes(int B, int T, int H, int K, int V, int M);
  * forward call's inputs (its o, hk, hv, clock and workspace fields are not
  * read; its C is ignored: the backward works in 64-token chunks); q, k, v
  * and d_o are of `dtype` (bf16 or fp32). K and V in [1, 1024], M even in
- * [4, 128]. The forward is recomputed in fp32 without intermediate rounding,
+ * [4, 256] (the reference's limit; above 128 slots the readout's adjoint
+ * streams the table through tile GEMMs instead of staging it on chip). The
+ * forward is recomputed in fp32 without intermediate rounding,
  * so the gradients are those of the op's exact arithmetic. Replaces the
  * autograd adjoints behind chunk_cyfa: ScalarAttention.grad / scalar_grad
  * (ops/chunk.py:51-71, ops/chunk_bwd.py:1008-1041), FirstReadout*.grad

@@ -136,7 +136,7 @@ def test_backward_checks_fail_before_launch():
     grads.workspace, grads.workspace_bytes = 4096, need - 1
     assert lib.cyfa_chunk_bwd(ctypes.byref(args), bf, ctypes.byref(grads), None) == _native.CYFA_ERR_WORKSPACE
     assert lib.cyfa_chunk_bwd(ctypes.byref(args), 7, ctypes.byref(grads), None) == _native.CYFA_ERR_VALUE
-    for field, bad in (("M", 130), ("M", 63), ("K", 2048), ("V", 0)):
+    for field, bad in (("M", 258), ("M", 63), ("K", 2048), ("V", 0)):
         old = getattr(args, field)
         setattr(args, field, bad)
         assert lib.cyfa_chunk_bwd(ctypes.byref(args), bf, ctypes.byref(grads), None) == _native.CYFA_ERR_UNSUPPORTED
@@ -157,8 +157,8 @@ def test_python_backward_refusals():
     q = torch.zeros(1, 2, 1, 256, dtype=torch.bfloat16, requires_grad=True)
     g = torch.zeros(1, 2, 1)
     w = torch.ones(256)
-    with pytest.raises(NotImplementedError):  # 256 slots: beyond the backward's 128
-        chunk_cyfa(q, q, q, g, g, g, torch.eye(255)[None], w, w)
+    with pytest.raises(NotImplementedError):  # 258 slots: beyond the backward's 256
+        chunk_cyfa(q, q, q, g, g, g, torch.eye(257)[None], w, w)
     ro = torch.eye(127)[None]
     with pytest.raises(NotImplementedError):  # a precomputed table is inference-only
         chunk_cyfa(q, q, q, g, g, g, ro, w, w, table=torch.zeros(1, 127, 128))

@@ -100,6 +100,10 @@ CASES = [
     (1, 256, 2, 256, 256, 128, 64, torch.float32, False, True),    # fp32 operands
     (2, 100, 2, 64, 96, 16, 32, torch.float32, True, True),        # general shape, other slot count
     (1, 77, 3, 128, 128, 64, 16, torch.bfloat16, True, False),     # general shape in bf16
+    # above 128 slots the readout and its adjoint run as tile GEMMs that stream the table
+    (2, 150, 2, 64, 96, 256, 32, torch.float32, True, True),       # 256 slots (the reference's limit)
+    (1, 70, 1, 128, 64, 200, 64, torch.bfloat16, True, True),      # 200 slots: ragged table tiles, bf16
+    (3, 400, 1, 64, 64, 256, 64, torch.float32, False, True),      # 1344 rows: two table-cotangent partials
 ]
 
 
@@ -162,10 +166,12 @@ def test_backward_state_only_cotangent():
         assert float(xg[name].grad.abs().max()) == 0.0, name
 
 
-def test_backward_twice_is_deterministic():
+@pytest.mark.parametrize("K,V,M", [(256, 256, 128), (64, 96, 256)])
+def test_backward_twice_is_deterministic(K, V, M):
     """Two backward passes over the same graph give identical bits (partial
-    sums are added in a fixed order, no atomics)."""
-    x, init, cot = _inputs(2, 130, 2, 256, 256, 128, seed=9, dtype=torch.bfloat16, state=False)
+    sums are added in a fixed order, no atomics), with the staged-table
+    readout adjoint (128 slots) and the streamed one (256 slots)."""
+    x, init, cot = _inputs(2, 130, 2, K, V, M, seed=9, dtype=torch.bfloat16, state=False)
     xg = {k: v.to(DEV).requires_grad_(True) for k, v in x.items()}
     o, _ = chunk_cyfa(**xg)
     loss = (o.float() * cot["o"].float().to(DEV)).sum()
@@ -175,20 +181,22 @@ def test_backward_twice_is_deterministic():
         assert torch.equal(a, b), name
 
 
-def test_layer_backward_matches_oracle():
+@pytest.mark.parametrize("slots", [128, 256])
+def test_layer_backward_matches_oracle(slots):
     """Training through one CyclicFlowAttention layer (fp32 parameters, the
     layer's general path around the op's autograd function): the gradients
     of x and of every parameter against float64 autograd through the model
     oracle. With fp32 q, k, v the op's forward runs the fp32 general path
     (no bf16 rounding, as the reference's fallback for non-bf16 inputs), so
     every gradient is fp32-class: rrms below 1e-3, with 2e-3 for the gate
-    parameters, whose gradients are sums over every token."""
+    parameters, whose gradients are sums over every token. 256 slots take
+    the backward's streamed readout adjoint."""
     from cyclic_flow_attention.layers import CyclicFlowAttention
     from oracle import model_oracle as MO
 
     B, T, hidden, H = 2, 150, 512, 2
     torch.manual_seed(0)
-    layer = CyclicFlowAttention(hidden_size=hidden, num_heads=H, head_dim=256, num_slots=128).train()
+    layer = CyclicFlowAttention(hidden_size=hidden, num_heads=H, head_dim=256, num_slots=slots).train()
     gen = torch.Generator().manual_seed(1)
     with torch.no_grad():
         for name, p in layer.named_parameters():
@@ -200,7 +208,7 @@ def test_layer_backward_matches_oracle():
                 p.copy_(1 + 0.1 * torch.randn(p.shape, generator=gen))
     x = torch.randn(B, T, hidden, generator=gen)
     cot = torch.randn(B, T, hidden, generator=gen)
-    cfg = dict(hidden_size=hidden, num_heads=H, head_dim=256, num_slots=128, norm_eps=1e-6, use_short_conv=True)
+    cfg = dict(hidden_size=hidden, num_heads=H, head_dim=256, num_slots=slots, norm_eps=1e-6, use_short_conv=True)
     sd = {"attn." + k: v.detach().double().requires_grad_(True) for k, v in layer.state_dict().items()}
     xd = x.double().requires_grad_(True)
     ry, _ = MO.attention_layer(sd, "attn.", xd, cfg, mode="exact")
