@@ -629,7 +629,7 @@ int cyfa_gates(const void* abd, long long abd_row, const float* dt_bias, const f
 
 size_t cyfa_chunk_general_workspace_bytes(int B, int T, int H, int K, int V, int M, int C) {
     if (B <= 0 || T <= 0 || H <= 0 || K <= 0 || V <= 0 || M <= 0 || C <= 0) return 0;
-    return cyfa::general_workspace(B, T, H, K, V, M, C, nullptr).bytes;
+    return cyfa::general_workspace(B, T, H, K, V, M, nullptr).bytes;
 }
 
 namespace {
@@ -666,11 +666,15 @@ int cyfa_chunk_fwd_general(const CyfaChunkArgs* a, int dtype, void* hip_stream) 
     const bool has_out = a->hk != nullptr;
     if (has_out != (a->hv != nullptr) || has_out != (a->clock != nullptr))
         return fail(CYFA_ERR_VALUE, "%s: hk, hv and clock must be all set or all null", fn);
-    // the kernels index rows (b, h, padded t) and their elements with 32-bit counts
-    const size_t Tp = (size_t)(a->T + a->C - 1) / a->C * a->C, rows = (size_t)a->B * a->H * Tp;
+    // the kernels index rows (b, h, padded t) and their elements with 32-bit
+    // counts, and the state scans take one grid row per (b, h)
+    const size_t Tp = (size_t)(a->T + cyfa::GEN_CHUNK - 1) / cyfa::GEN_CHUNK * cyfa::GEN_CHUNK;
+    const size_t rows = (size_t)a->B * a->H * Tp;
     if (rows * 256 >= ((size_t)1 << 31))
         return fail(CYFA_ERR_UNSUPPORTED, "%s: B * H * padded T = %zu rows is too many", fn, rows);
-    const size_t need = cyfa::general_workspace(a->B, a->T, a->H, a->K, a->V, a->M, a->C, nullptr).bytes;
+    if ((size_t)a->B * a->H > 65535)
+        return fail(CYFA_ERR_UNSUPPORTED, "%s: B * H = %zu is above 65535", fn, (size_t)a->B * a->H);
+    const size_t need = cyfa::general_workspace(a->B, a->T, a->H, a->K, a->V, a->M, nullptr).bytes;
     if (!a->workspace || a->workspace_bytes < need)
         return fail(CYFA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, got %zu", fn, need,
                     a->workspace ? a->workspace_bytes : (size_t)0);

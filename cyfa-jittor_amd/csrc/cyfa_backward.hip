@@ -447,14 +447,18 @@ __device__ __forceinline__ void chunk_scores(const float* X, const float* Y, int
         }
 }
 
-// The pass-1 output of the recomputed forward, chunk-parallel (grid (N, H,
-// B), 256 threads): o_t = scale (e^{G_t} q_t S_n + sum_{s<=t} A[t][s] v_s),
-// A the masked decayed q.k scores, per 64-wide output tile as two tile GEMMs.
+// The output of one pass, chunk-parallel (grid (N, H, B), 256 threads):
+// o_t = scale (e^{G_t} q_t S_n + sum_{s<=t} A[t][s] v_s), A the masked
+// decayed q.k scores, per 64-wide output tile as two tile GEMMs. The
+// backward's recompute writes pass 1 head-major and unrounded; the general
+// forward rounds to bf16 for bf16 inputs and writes pass 2 as [B, T, H, Vd].
 struct OutArgs {
     const float *q, *k, *v;  // head-major [B*H, Tp, Kq | Vd]
     const float* g;
     const float* S;          // [B*H, N+1, Kq, Vd]
-    float* out;              // head-major [B*H, Tp, Vd]
+    float* out;              // head-major [B*H, Tp, Vd], used when out_bthd is null
+    void* out_bthd;          // nullable [B, T, H, Vd], bf16 when bf16 else fp32
+    int bf16;                // round to bf16
     int B, T, Tp, H, Kq, Vd, N;
     float scale;
 };
@@ -486,7 +490,30 @@ __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
         tile_gemm<MF, false>([&](int i, int kk) { return sA[i][kk]; },
                              [&](int kk, int j) { return d0 + j < Vd ? v[(size_t)kk * Vd + d0 + j] : 0.f; }, BC,
                              sStage, acc);
-        tile_store<MF>(acc, out, Vd, d0, a.scale);
+        if (!a.out_bthd) {
+            if (a.bf16) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) acc[i][j] = (float)(bf16_t)(a.scale * acc[i][j]);
+                tile_store<MF>(acc, out, Vd, d0, 1.f);
+            } else {
+                tile_store<MF>(acc, out, Vd, d0, a.scale);
+            }
+            continue;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int t = t0 + TileMap<MF>::row(i, j), c = d0 + TileMap<MF>::col(i, j);
+                if (c >= Vd || t >= a.T) continue;
+                const size_t e = (((size_t)b * a.T + t) * a.H + h) * Vd + c;
+                if (a.bf16)
+                    reinterpret_cast<bf16_t*>(a.out_bthd)[e] = (bf16_t)(a.scale * acc[i][j]);
+                else
+                    reinterpret_cast<float*>(a.out_bthd)[e] = a.scale * acc[i][j];
+            }
     }
 }
 
@@ -565,11 +592,22 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     }
 }
 
-// The slot readout of the recomputed forward (fp32, unrounded) for blocks of
-// 32 rows of one head: z = U(lam) raw, l = z table^T, p = softmax(l),
-// u = p table, weights = U(-lam) u; the two products as small GEMMs against
-// the staged table (4 x 4 per thread). Grid (ceil(B Tp / (32 per_wg)), H),
-// 256 threads: a workgroup stages the table once and takes per_wg blocks.
+// The slot readout for blocks of 32 rows of one head: z = U(lam) raw,
+// l = z table^T, p = softmax(l), u = p table, weights = U(-lam) u; the two
+// products as small GEMMs against the staged table (4 x 4 per thread). BF
+// rounds z, the table, p and the weights to bf16 (the general forward's casts
+// to a bf16 input dtype, ops/utils.py:779-882); the backward's recompute is
+// unrounded. Grid (ceil(B Tp / (32 per_wg)), H), 256 threads: a workgroup
+// stages the table once and takes per_wg blocks.
+template <bool BF>
+__device__ __forceinline__ float bw_rnd(float x) {
+    if constexpr (BF)
+        return (float)(bf16_t)x;
+    else
+        return x;
+}
+
+template <bool BF>
 __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, const float* cs, const float* sn,
                                                              const float* table, int B, int Tp, int H, int M,
                                                              int per_wg, float* wts) {
@@ -581,7 +619,7 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
     const int R = M - 1, P = M / 2, rows = B * Tp;
     for (int e = tid; e < TM * LD; e += 256) {
         const int r = e / LD, m = e % LD;
-        sTab[e] = (r < R && m < M) ? table[((size_t)h * R + r) * M + m] : 0.f;
+        sTab[e] = (r < R && m < M) ? bw_rnd<BF>(table[((size_t)h * R + r) * M + m]) : 0.f;
     }
     const auto row_of = [&](int rho) { return ((size_t)(rho / Tp) * H + h) * Tp + rho % Tp; };
     const int br = 4 * (tid >> 5), bc = 4 * (tid & 31);
@@ -595,8 +633,8 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
                 c = cs[row * P + pr];
                 s = sn[row * P + pr];
                 const float re = raw[row * M + 2 * pr], ro = raw[row * M + 2 * pr + 1];
-                ze = c * re - s * ro;
-                zo = s * re + c * ro;
+                ze = bw_rnd<BF>(c * re - s * ro);
+                zo = bw_rnd<BF>(s * re + c * ro);
             }
             sCs[i][pr] = c;
             sSn[i][pr] = s;
@@ -629,8 +667,8 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
             const float mx = bw_wave_max(fmaxf(l0, l1));
             const float e0 = lane < R ? expf(l0 - mx) : 0.f, e1 = lane + 64 < R ? expf(l1 - mx) : 0.f;
             const float inv = 1.f / bw_wave_sum(e0 + e1);
-            sP[i][lane] = e0 * inv;
-            sP[i][lane + 64] = e1 * inv;
+            sP[i][lane] = bw_rnd<BF>(e0 * inv);
+            sP[i][lane + 64] = bw_rnd<BF>(e1 * inv);
         }
         __syncthreads();
         float u[4][4] = {};
@@ -656,8 +694,8 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
                 const int pr = (bc + j) >> 1;
                 if (pr < P) {
                     const float c = sCs[br + i][pr], s = sSn[br + i][pr];
-                    wts[row * M + 2 * pr] = c * u[i][j] + s * u[i][j + 1];
-                    wts[row * M + 2 * pr + 1] = -s * u[i][j] + c * u[i][j + 1];
+                    wts[row * M + 2 * pr] = bw_rnd<BF>(c * u[i][j] + s * u[i][j + 1]);
+                    wts[row * M + 2 * pr + 1] = bw_rnd<BF>(-s * u[i][j] + c * u[i][j + 1]);
                 }
             }
         }
@@ -866,7 +904,10 @@ struct WideArgs {
     float *wts, *draw, *dlp, *dlam;             // dlp [B H Tp, BW_WIDE_CT]: the clock's partials
     float* dtab;                                // [H, splits, (M-1) M]
     int B, Tp, H, M, splits;
+    int bf;                                     // forward: round z, the table, p and the weights to bf16
 };
+
+__device__ __forceinline__ float wide_rnd(const WideArgs& a, float x) { return a.bf ? (float)(bf16_t)x : x; }
 
 __device__ __forceinline__ size_t wide_row(const WideArgs& a, int h, int rho) {
     return ((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp;
@@ -892,8 +933,10 @@ __global__ __launch_bounds__(256) void bw_wide_logits_kernel(WideArgs a) {
     const float* tb = a.table + (size_t)h * R * M;
     float acc[4][4] = {};
     tile_gemm<false, true>(
-        [&](int i, int m) { return rho0 + i < rows ? wide_rot(a, x, wide_row(a, h, rho0 + i), m) : 0.f; },
-        [&](int m, int j) { return r0 + j < R ? tb[(size_t)(r0 + j) * M + m] : 0.f; }, M, sStage, acc);
+        [&](int i, int m) {
+            return rho0 + i < rows ? wide_rnd(a, wide_rot(a, x, wide_row(a, h, rho0 + i), m)) : 0.f;
+        },
+        [&](int m, int j) { return r0 + j < R ? wide_rnd(a, tb[(size_t)(r0 + j) * M + m]) : 0.f; }, M, sStage, acc);
     float* out = ADJ ? a.dl : a.lg;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -935,7 +978,7 @@ __global__ __launch_bounds__(256) void bw_wide_softmax_kernel(WideArgs a) {
         const float inv = 1.f / bw_wave_sum(sum);
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            if (lane + 64 * i < R) lg[lane + 64 * i] = v[i] * inv;
+            if (lane + 64 * i < R) lg[lane + 64 * i] = wide_rnd(a, v[i] * inv);
     } else {
         float* dl = a.dl + row * BW_WIDE_MW;
         float pv[4], pdp = 0.f;
@@ -966,7 +1009,7 @@ __global__ __launch_bounds__(256) void bw_wide_u_kernel(WideArgs a) {
     const int tid = threadIdx.x, rho0 = blockIdx.x * BC, m0 = blockIdx.y * BC, h = blockIdx.z;
     const int M = a.M, R = M - 1, P = M / 2, rows = a.B * a.Tp;
     const float* tb = a.table + (size_t)h * R * M;
-    const auto tab = [&](int r, int j) { return m0 + j < M ? tb[(size_t)r * M + m0 + j] : 0.f; };
+    const auto tab = [&](int r, int j) { return m0 + j < M ? wide_rnd(a, tb[(size_t)r * M + m0 + j]) : 0.f; };
     float u[4][4] = {}, dz[4][4] = {};
     tile_gemm<false, false>(
         [&](int i, int r) { return rho0 + i < rows ? a.lg[wide_row(a, h, rho0 + i) * BW_WIDE_MW + r] : 0.f; }, tab, R,
@@ -988,8 +1031,8 @@ __global__ __launch_bounds__(256) void bw_wide_u_kernel(WideArgs a) {
                 if (pr >= P) continue;
                 const float c = a.cs[row * P + pr], s = a.sn[row * P + pr];
                 if (!ADJ) {
-                    a.wts[row * M + m] = c * u[i][j] + s * u[i][j + 1];
-                    a.wts[row * M + m + 1] = -s * u[i][j] + c * u[i][j + 1];
+                    a.wts[row * M + m] = wide_rnd(a, c * u[i][j] + s * u[i][j + 1]);
+                    a.wts[row * M + m + 1] = wide_rnd(a, -s * u[i][j] + c * u[i][j + 1]);
                 } else {
                     const float ge = dz[i][j], go = dz[i][j + 1], ue = u[i][j], uo = u[i][j + 1];
                     a.draw[row * M + m] = c * ge + s * go;
@@ -1261,6 +1304,89 @@ void launch_chunk_grad(const ChunkGradArgs& a, bool mfma, hipStream_t stream) {
 
 }  // namespace
 
+int launch_chunk_pass(const ChunkPassParams& p, hipStream_t stream) {
+    if (p.B < 1 || p.H < 1 || p.T < 1 || p.Tp < p.T || p.Tp % BC || p.Kq < 1 || p.Kq > BW_MAX_D || p.Vd < 1 ||
+        p.Vd > BW_MAX_D || (!p.out && !p.out_bthd) || !p.states)
+        return -1;
+    const int N = p.Tp / BC;
+    StateScanArgs sa{};
+    sa.a = p.k;
+    sa.b = p.v;
+    sa.g = p.g;
+    sa.x0 = p.s0;
+    sa.xs = p.states;
+    sa.x_out = p.s_final;
+    sa.B = p.B;
+    sa.T = p.T;
+    sa.Tp = p.Tp;
+    sa.H = p.H;
+    sa.Kq = p.Kq;
+    sa.Vd = p.Vd;
+    sa.N = N;
+    sa.scale = 1.f;
+    hipLaunchKernelGGL(bw_state_scan_kernel<false>, scan_grid(p.Vd, p.Kq, p.B * p.H), dim3(256), 0, stream, sa);
+    OutArgs oa{};
+    oa.q = p.q;
+    oa.k = p.k;
+    oa.v = p.v;
+    oa.g = p.g;
+    oa.S = p.states;
+    oa.out = p.out;
+    oa.out_bthd = p.out_bthd;
+    oa.bf16 = p.bf16;
+    oa.B = p.B;
+    oa.T = p.T;
+    oa.Tp = p.Tp;
+    oa.H = p.H;
+    oa.Kq = p.Kq;
+    oa.Vd = p.Vd;
+    oa.N = N;
+    oa.scale = p.scale;
+    if (p.mfma)
+        hipLaunchKernelGGL(bw_out_kernel<true>, dim3(N, p.H, p.B), dim3(256), 0, stream, oa);
+    else
+        hipLaunchKernelGGL(bw_out_kernel<false>, dim3(N, p.H, p.B), dim3(256), 0, stream, oa);
+    return 0;
+}
+
+int launch_chunk_readout(const float* raw, const float* cs, const float* sn, const float* table, float* lg, int B,
+                         int Tp, int H, int M, int bf16, float* wts, hipStream_t stream) {
+    if (B < 1 || H < 1 || Tp < 1 || Tp % BC || M < 4 || M > BWD_MAX_M || M % 2) return -1;
+    const dim3 blk(256);
+    if (M > BWD_TABLE_M) {  // logits, softmax, then the weights, streaming the table
+        if (!lg) return -1;
+        WideArgs wa{};
+        wa.raw = raw;
+        wa.cs = cs;
+        wa.sn = sn;
+        wa.table = table;
+        wa.lg = lg;
+        wa.wts = wts;
+        wa.B = B;
+        wa.Tp = Tp;
+        wa.H = H;
+        wa.M = M;
+        wa.bf = bf16;
+        const int rows_h = B * Tp;
+        const size_t rows = (size_t)rows_h * H;
+        hipLaunchKernelGGL(bw_wide_logits_kernel<false>, dim3((rows_h + BC - 1) / BC, (M - 1 + BC - 1) / BC, H), blk,
+                           0, stream, wa);
+        hipLaunchKernelGGL(bw_wide_softmax_kernel<false>, dim3((unsigned)((rows + 3) / 4)), blk, 0, stream, wa);
+        hipLaunchKernelGGL(bw_wide_u_kernel<false>, dim3((rows_h + BC - 1) / BC, (M + BC - 1) / BC, H), blk, 0,
+                           stream, wa);
+        return 0;
+    }
+    const int per = bwd_ro_per_wg(B, Tp, H), blocks = (B * Tp + BWD_RO_BLOCK - 1) / BWD_RO_BLOCK;
+    const dim3 grid((blocks + per - 1) / per, H);
+    if (bf16)
+        hipLaunchKernelGGL(bw_fwd_readout_kernel<true>, grid, blk, 0, stream, raw, cs, sn, table, B, Tp, H, M, per,
+                           wts);
+    else
+        hipLaunchKernelGGL(bw_fwd_readout_kernel<false>, grid, blk, 0, stream, raw, cs, sn, table, B, Tp, H, M, per,
+                           wts);
+    return 0;
+}
+
 int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     const int B = p.B, T = p.T, H = p.H, K = p.K, V = p.V, M = p.M;
     if (B < 1 || T < 1 || H < 1 || K < 1 || K > BW_MAX_D || V < 1 || V > BW_MAX_D || M < 4 || M > BWD_MAX_M || M % 2)
@@ -1303,26 +1429,25 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     f1.Vd = M;
     f1.N = N;
     f1.scale = 1.f;
-    hipLaunchKernelGGL(bw_state_scan_kernel<false>, scan_grid(M, K, B * H), blk, 0, stream, f1);
-    OutArgs oa{};
-    oa.q = ws.qh;
-    oa.k = ws.kh;
-    oa.v = ws.w;
-    oa.g = p.g;
-    oa.S = ws.sk;
-    oa.out = ws.raw;
-    oa.B = B;
-    oa.T = T;
-    oa.Tp = Tp;
-    oa.H = H;
-    oa.Kq = K;
-    oa.Vd = M;
-    oa.N = N;
-    oa.scale = p.scale;
-    if (bf)
-        hipLaunchKernelGGL(bw_out_kernel<true>, dim3(N, H, B), blk, 0, stream, oa);
-    else
-        hipLaunchKernelGGL(bw_out_kernel<false>, dim3(N, H, B), blk, 0, stream, oa);
+    ChunkPassParams p1{};
+    p1.q = ws.qh;
+    p1.k = ws.kh;
+    p1.v = ws.w;
+    p1.g = p.g;
+    p1.s0 = p.h0_k;
+    p1.states = ws.sk;
+    p1.out = ws.raw;
+    p1.mfma = bf;
+    p1.B = B;
+    p1.T = T;
+    p1.Tp = Tp;
+    p1.H = H;
+    p1.Kq = K;
+    p1.Vd = M;
+    p1.scale = p.scale;
+    if (launch_chunk_pass(p1, stream) != 0 ||
+        launch_chunk_readout(ws.raw, ws.cs, ws.sn, p.table, ws.lg, B, Tp, H, M, 0, ws.wts, stream) != 0)
+        return -1;
     const int ro_per_wg = bwd_ro_per_wg(B, Tp, H);
     const bool wide = M > BWD_TABLE_M;
     WideArgs wa{};
@@ -1346,14 +1471,6 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     const int rows_h = B * Tp;
     const dim3 g_logits((rows_h + BC - 1) / BC, (M - 1 + BC - 1) / BC, H), g_u((rows_h + BC - 1) / BC, (M + BC - 1) / BC, H);
     const dim3 g_rows((unsigned)((rows + 3) / 4));
-    if (wide) {  // logits, softmax, then the weights
-        hipLaunchKernelGGL(bw_wide_logits_kernel<false>, g_logits, blk, 0, stream, wa);
-        hipLaunchKernelGGL(bw_wide_softmax_kernel<false>, g_rows, blk, 0, stream, wa);
-        hipLaunchKernelGGL(bw_wide_u_kernel<false>, g_u, blk, 0, stream, wa);
-    } else {
-        hipLaunchKernelGGL(bw_fwd_readout_kernel, dim3(ws.ro_blocks, H), blk, 0, stream, ws.raw, ws.cs, ws.sn, p.table,
-                           B, Tp, H, M, ro_per_wg, ws.wts);
-    }
     StateScanArgs f2 = f1;
     f2.a = ws.w;
     f2.b = ws.vh;

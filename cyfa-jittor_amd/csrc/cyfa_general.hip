@@ -171,104 +171,7 @@ __global__ __launch_bounds__(256) void gen_write_kernel(const double* lam, const
     sn[row * P + p] = s;
 }
 
-// One chunkwise ScalarGatedLA pass (ops/chunk.py:136-161; the state is the
-// state before each chunk, ops/chunk_h.py:238-327):
-//   o_t = scale (e^{G_t} q_t S + sum_{s <= t} e^{G_t - G_s} (q_t . k_s) v_s)
-//   S  <- e^{G_last} S + sum_s k_s^T e^{G_last - G_s} v_s
-// with G the in-chunk inclusive cumsum of the natural-log gate g [B, T, H].
-// Workgroup (32-column tile of V, h, b), 256 threads; the tile's state
-// columns [Kq][32] stay in LDS across the chunks. Each thread keeps the same
-// output elements (e = tid + 256 i) through a chunk.
 constexpr int GEN_MAX_K = 1024;
-constexpr int GEN_COLS = 32;
-
-template <int C, bool OUT_BF>
-__global__ __launch_bounds__(256) void gen_sgla_kernel(GenSglaParams p) {
-    constexpr int NO = C * GEN_COLS / 256;  // output elements per thread
-    __shared__ float sS[GEN_MAX_K * GEN_COLS];
-    __shared__ float sP[C][C + 1];
-    __shared__ float sV[C][GEN_COLS];
-    __shared__ float sG[C], sEq[C], sDv[C];
-    const int tid = threadIdx.x, c0 = blockIdx.x * GEN_COLS, h = blockIdx.y, b = blockIdx.z;
-    const int Kq = p.Kq, Vd = p.Vd;
-    const size_t bh = (size_t)b * p.H + h;
-    const float* q = p.q + bh * p.Tp * Kq;
-    const float* k = p.k + bh * p.Tp * Kq;
-    const float* v = p.v + bh * p.Tp * Vd;
-    for (int e = tid; e < Kq * GEN_COLS; e += 256) {
-        const int r = e / GEN_COLS, c = e % GEN_COLS;
-        sS[e] = (p.s0 && c0 + c < Vd) ? p.s0[(bh * Kq + r) * Vd + c0 + c] : 0.f;
-    }
-    for (int t0 = 0; t0 < p.Tp; t0 += C) {
-        for (int e = tid; e < C * GEN_COLS; e += 256) {
-            const int s = e / GEN_COLS, c = e % GEN_COLS;
-            sV[s][c] = c0 + c < Vd ? v[(size_t)(t0 + s) * Vd + c0 + c] : 0.f;
-        }
-        if (tid == 0) {
-            float G = 0.f;
-            for (int i = 0; i < C; i++) {
-                const int t = t0 + i;
-                G += t < p.T ? p.g[((size_t)b * p.T + t) * p.H + h] : 0.f;
-                sG[i] = G;
-            }
-            for (int i = 0; i < C; i++) {
-                sEq[i] = expf(sG[i]);
-                sDv[i] = expf(G - sG[i]);
-            }
-        }
-        __syncthreads();
-        // the masked, decayed scores and the inter-chunk part of this thread's outputs
-        for (int e = tid; e < C * C; e += 256) {
-            const int t = e / C, s = e % C;
-            float acc = 0.f;
-            if (s <= t) {
-                const float* qt = q + (size_t)(t0 + t) * Kq;
-                const float* ks = k + (size_t)(t0 + s) * Kq;
-                for (int j = 0; j < Kq; j++) acc = fmaf(qt[j], ks[j], acc);
-                acc *= expf(sG[t] - sG[s]);
-            }
-            sP[t][s] = acc;
-        }
-        float oi[NO];
-#pragma unroll
-        for (int i = 0; i < NO; i++) {
-            const int e = tid + 256 * i, t = e / GEN_COLS, c = e % GEN_COLS;
-            const float* qt = q + (size_t)(t0 + t) * Kq;
-            float acc = 0.f;
-            for (int j = 0; j < Kq; j++) acc = fmaf(qt[j], sS[j * GEN_COLS + c], acc);
-            oi[i] = acc;
-        }
-        __syncthreads();  // scores complete; every read of the old state done
-#pragma unroll
-        for (int i = 0; i < NO; i++) {
-            const int e = tid + 256 * i, t = e / GEN_COLS, c = e % GEN_COLS;
-            float acc = 0.f;
-            for (int s = 0; s <= t; s++) acc = fmaf(sP[t][s], sV[s][c], acc);
-            const float o = p.scale * (sEq[t] * oi[i] + acc);
-            const int tt = t0 + t;
-            if (c0 + c < Vd) {
-                if (!p.out_bthd)  // every padded row too (its values are exact zeros or unused)
-                    reinterpret_cast<float*>(p.out)[(bh * p.Tp + tt) * Vd + c0 + c] = OUT_BF ? gen_rnd<true>(o) : o;
-                else if (tt < p.T)
-                    gen_st<OUT_BF>(p.out, (((size_t)b * p.T + tt) * p.H + h) * Vd + c0 + c, o);
-            }
-        }
-        const float el = expf(sG[C - 1]);
-        for (int e = tid; e < Kq * GEN_COLS; e += 256) {
-            const int r = e / GEN_COLS, c = e % GEN_COLS;
-            float acc = 0.f;
-            for (int s = 0; s < C; s++) acc = fmaf(k[(size_t)(t0 + s) * Kq + r], sV[s][c] * sDv[s], acc);
-            sS[e] = el * sS[e] + acc;
-        }
-        __syncthreads();  // the chunk's tiles are replaced next
-    }
-    if (p.s_final) {
-        for (int e = tid; e < Kq * GEN_COLS; e += 256) {
-            const int r = e / GEN_COLS, c = e % GEN_COLS;
-            if (c0 + c < Vd) p.s_final[(bh * Kq + r) * Vd + c0 + c] = sS[e];
-        }
-    }
-}
 
 // The slot readout of one row (ops/utils.py:779-882): z = U(lam) raw cast to
 // the input dtype; logits_r = sum_m z_m table[r][m] (r < R, the table cast
@@ -322,19 +225,6 @@ __device__ __forceinline__ void gen_readout_row(const float* raw, const float* c
         wout[2 * pr] = gen_rnd<BF>(c * ue + s * uo);
         wout[2 * pr + 1] = gen_rnd<BF>(-s * ue + c * uo);
     }
-}
-
-// The readout of every (b, h, t) row, one wave per row.
-template <bool BF>
-__global__ __launch_bounds__(256) void gen_readout_kernel(const float* raw, const float* cs, const float* sn,
-                                                          const float* table, int rows, int Tp, int H, int M,
-                                                          float* weights) {
-    __shared__ float sz[4][256], sp[4][256];
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, row = blockIdx.x * 4 + wv;
-    if (row >= rows) return;
-    const int h = (row / Tp) % H, P = M / 2;
-    gen_readout_row<BF>(raw + (size_t)row * M, cs + (size_t)row * P, sn + (size_t)row * P,
-                        table + (size_t)h * (M - 1) * M, M, sz[wv], sp[wv], weights + (size_t)row * M, lane);
 }
 
 // One decode step of any shape (ops/fused_recurrent.py:10-200 with the
@@ -420,15 +310,20 @@ int launch_general_table(const float* readout, float* table, int H, int M, hipSt
     return 0;
 }
 
-// The chunk path: rows (q_hat, k_hat, v), the clock, the write vector, pass 1,
-// the readout and pass 2, in the workspace laid out by general_workspace.
+// The chunk path: rows (q_hat, k_hat, v), the clock, the write vector, then
+// pass 1, the readout and pass 2 (ops/chunk.py:136-161, 285-331), each pass
+// chunk-parallel (launch_chunk_pass: the states before every chunk by a scan,
+// then every chunk's output on tile products), in the workspace laid out by
+// general_workspace. bf16 inputs are cast where the reference casts to the
+// input dtype (q_hat, k_hat, w, the pass-1 output, the readout's z, table, p
+// and weights, o); fp32 inputs are not rounded.
 int launch_general_chunk(const GenChunkParams& g, hipStream_t stream) {
     const int B = g.B, T = g.T, H = g.H, K = g.K, V = g.V, M = g.M, C = g.C;
     if (K < 1 || K > GEN_MAX_K || V < 1 || V > GEN_MAX_K || M < 4 || M > 256 || M % 2 ||
         !(C == 16 || C == 32 || C == 64))
         return -1;
-    const int Tp = (T + C - 1) / C * C;
-    const GenWorkspace ws = general_workspace(B, T, H, K, V, M, C, g.workspace);
+    const GenWorkspace ws = general_workspace(B, T, H, K, V, M, g.workspace);
+    const int Tp = ws.Tp;
     const size_t rows = (size_t)B * H * Tp;
     const dim3 rb((unsigned)((rows + 3) / 4)), blk(256);
     if (g.bf16) {
@@ -448,12 +343,20 @@ int launch_general_chunk(const GenChunkParams& g, hipStream_t stream) {
         hipLaunchKernelGGL(gen_write_kernel<true>, wb, blk, 0, stream, ws.lam, g.beta, B, T, Tp, H, M, ws.w, ws.cs, ws.sn);
     else
         hipLaunchKernelGGL(gen_write_kernel<false>, wb, blk, 0, stream, ws.lam, g.beta, B, T, Tp, H, M, ws.w, ws.cs, ws.sn);
-    // pass 1: raw = sgla(q_hat, k_hat, w) over T padded (head-major fp32, cast like the input)
-    GenSglaParams p1{};
+    // pass 1: raw = sgla(q_hat, k_hat, w), head-major, cast like the input;
+    // bf16 inputs take the tile products on the matrix cores (their operands
+    // are bf16 values, the states and scores split into two bf16 parts)
+    ChunkPassParams p1{};
     p1.q = ws.qh;
     p1.k = ws.kh;
     p1.v = ws.w;
     p1.g = g.g;
+    p1.s0 = g.h0_k;
+    p1.states = ws.sk;
+    p1.s_final = g.hk;
+    p1.out = ws.raw;
+    p1.bf16 = g.bf16;
+    p1.mfma = g.bf16;
     p1.B = B;
     p1.T = T;
     p1.Tp = Tp;
@@ -461,46 +364,22 @@ int launch_general_chunk(const GenChunkParams& g, hipStream_t stream) {
     p1.Kq = K;
     p1.Vd = M;
     p1.scale = g.scale;
-    p1.s0 = g.h0_k;
-    p1.out = ws.raw;
-    p1.out_bthd = 0;
-    p1.s_final = g.hk;
+    if (launch_chunk_pass(p1, stream) != 0) return -1;
+    if (launch_chunk_readout(ws.raw, ws.cs, ws.sn, g.table, ws.lg, B, Tp, H, M, g.bf16, ws.wts, stream) != 0) return -1;
     // pass 2: o = sgla(weights, w, v), written as [B, T, H, V] in the input dtype
-    GenSglaParams p2 = p1;
+    ChunkPassParams p2 = p1;
     p2.q = ws.wts;
     p2.k = ws.w;
     p2.v = ws.vh;
+    p2.s0 = g.h0_v;
+    p2.states = ws.sv;
+    p2.s_final = g.hv;
+    p2.out = nullptr;
+    p2.out_bthd = g.o;
     p2.Kq = M;
     p2.Vd = V;
     p2.scale = 1.f;
-    p2.s0 = g.h0_v;
-    p2.out = g.o;
-    p2.out_bthd = 1;
-    p2.s_final = g.hv;
-    const auto sgla = [&](const GenSglaParams& sp, bool out_bf) {
-        const dim3 grid((sp.Vd + GEN_COLS - 1) / GEN_COLS, H, B);
-#define CYFA_GEN_SGLA(CC)                                                                     \
-    if (C == CC) {                                                                            \
-        if (out_bf)                                                                           \
-            hipLaunchKernelGGL((gen_sgla_kernel<CC, true>), grid, blk, 0, stream, sp);        \
-        else                                                                                  \
-            hipLaunchKernelGGL((gen_sgla_kernel<CC, false>), grid, blk, 0, stream, sp);       \
-    }
-        CYFA_GEN_SGLA(16)
-        CYFA_GEN_SGLA(32)
-        CYFA_GEN_SGLA(64)
-#undef CYFA_GEN_SGLA
-    };
-    sgla(p1, g.bf16 != 0);
-    const dim3 rr((unsigned)((rows + 3) / 4));
-    if (g.bf16)
-        hipLaunchKernelGGL(gen_readout_kernel<true>, rr, blk, 0, stream, ws.raw, ws.cs, ws.sn, g.table, (int)rows, Tp,
-                           H, M, ws.wts);
-    else
-        hipLaunchKernelGGL(gen_readout_kernel<false>, rr, blk, 0, stream, ws.raw, ws.cs, ws.sn, g.table, (int)rows, Tp,
-                           H, M, ws.wts);
-    sgla(p2, g.bf16 != 0);
-    return 0;
+    return launch_chunk_pass(p2, stream);
 }
 
 int launch_general_clock_write(const float* delta, const float* clock0, const float* beta, int B, int T, int Tp, int H,

@@ -202,17 +202,36 @@ constexpr int GATE_PATH_G0 = 256;       // g_proj[0] width (head_v_dim) the kern
 constexpr int GATE_PATH_MAX_K = 2048;   // largest hidden size (its k-chunk loop is unrolled to this)
 constexpr int GATE_PATH_MAX_DV = 2048;  // largest H * head_v_dim (its column rounds, likewise)
 
+// Largest slot count of the backward pass, and of its readout kernels that
+// stage a head's table in LDS; above BWD_TABLE_M the readout and its adjoint
+// run as tile GEMMs that stream the table (the "wide" readout).
+constexpr int BWD_MAX_M = 256;
+constexpr int BWD_TABLE_M = 128;
+
+constexpr int BWD_WIDE_MW = 256;    // columns of the wide readout's per-row buffers
+
 // The general-shape path (cyfa_general.hip): any K, V <= 1024, even M in
-// [4, 256], C in {16, 32, 64}, bf16 or fp32 q, k, v.
-struct GenSglaParams {
-    const float *q, *k, *v;  // head-major [B, H, Tp, Kq | Vd] fp32
-    const float* g;          // [B, T, H] natural-log gate (tokens past T: zero)
+// [4, 256], C in {16, 32, 64}, bf16 or fp32 q, k, v. It computes in chunks of
+// 64 tokens whatever C is (C changes no value beyond fp32 summation order).
+constexpr int GEN_CHUNK = 64;
+
+// One chunkwise ScalarGatedLA pass, chunk-parallel (cyfa_backward.hip): the
+// states before every chunk by a scan over the chunks, then every chunk's
+// output from its state and its own rows.
+//   o_t = scale (e^{G_t} q_t S_n + sum_{s <= t in chunk n} e^{G_t - G_s} (q_t . k_s) v_s)
+//   S_{n+1} = e^{G_last} S_n + sum_s k_s^T e^{G_last - G_s} v_s
+struct ChunkPassParams {
+    const float *q, *k, *v;  // head-major fp32 [B*H, Tp, Kq | Vd], Tp a multiple of 64, rows past T zero
+    const float* g;          // [B, T, H] natural-log gate (tokens past T add zero)
+    const float* s0;         // nullable [B*H, Kq, Vd]
+    float* states;           // workspace [B*H, Tp / 64 + 1, Kq, Vd]
+    float* s_final;          // nullable [B*H, Kq, Vd]
+    float* out;              // head-major fp32 [B*H, Tp, Vd] (nullable when out_bthd is set)
+    void* out_bthd;          // nullable [B, T, H, Vd], bf16 when bf16 else fp32
+    int bf16;                // round the output to bf16 (the input dtype's cast)
+    int mfma;                // tile products on the matrix cores (split bf16 operands, ~16 bits)
     int B, T, Tp, H, Kq, Vd;
     float scale;
-    const float* s0;  // nullable [B, H, Kq, Vd]
-    void* out;        // head-major fp32 [B, H, Tp, Vd], or [B, T, H, Vd] in the input dtype (out_bthd)
-    int out_bthd;
-    float* s_final;  // nullable [B, H, Kq, Vd]
 };
 
 struct GenChunkParams {
@@ -238,16 +257,21 @@ struct GenDecodeParams {
 
 // The general chunk path's workspace: per (b, h, padded token) row the clock
 // (f64), q_hat and k_hat (K), v (V), the write vector, the pass-1 output and
-// the slot weights (M each) and the phases' cosines and sines (M / 2 each),
-// all fp32, each region 256-byte aligned. With base == nullptr only the size.
+// the slot weights (M each) and the phases' cosines and sines (M / 2 each);
+// the states before every chunk of both passes; with M > 128 the readout's
+// per-row logits (BWD_WIDE_MW columns); all fp32, each region 256-byte
+// aligned, tokens padded to a multiple of GEN_CHUNK. With base == nullptr
+// only the size.
 struct GenWorkspace {
     double* lam;
-    float *qh, *kh, *vh, *w, *cs, *sn, *raw, *wts;
+    float *qh, *kh, *vh, *w, *cs, *sn, *raw, *wts, *sk, *sv, *lg;
+    int Tp;
     size_t bytes;
 };
 
-inline GenWorkspace general_workspace(int B, int T, int H, int K, int V, int M, int C, void* base) {
-    const size_t Tp = (size_t)(T + C - 1) / C * C, rows = (size_t)B * H * Tp;
+inline GenWorkspace general_workspace(int B, int T, int H, int K, int V, int M, void* base) {
+    const size_t Tp = (size_t)(T + GEN_CHUNK - 1) / GEN_CHUNK * GEN_CHUNK, rows = (size_t)B * H * Tp;
+    const size_t BH = (size_t)B * H, N1 = Tp / GEN_CHUNK + 1;
     char* p = static_cast<char*>(base);
     size_t off = 0;
     const auto take = [&](size_t bytes) {
@@ -255,16 +279,21 @@ inline GenWorkspace general_workspace(int B, int T, int H, int K, int V, int M, 
         off += (bytes + 255) / 256 * 256;
         return r;
     };
+    const auto f = [&](size_t n) { return reinterpret_cast<float*>(take(n * 4)); };
     GenWorkspace w;
+    w.Tp = (int)Tp;
     w.lam = reinterpret_cast<double*>(take(rows * 8));
-    w.qh = reinterpret_cast<float*>(take(rows * K * 4));
-    w.kh = reinterpret_cast<float*>(take(rows * K * 4));
-    w.vh = reinterpret_cast<float*>(take(rows * V * 4));
-    w.w = reinterpret_cast<float*>(take(rows * M * 4));
-    w.cs = reinterpret_cast<float*>(take(rows * (M / 2) * 4));
-    w.sn = reinterpret_cast<float*>(take(rows * (M / 2) * 4));
-    w.raw = reinterpret_cast<float*>(take(rows * M * 4));
-    w.wts = reinterpret_cast<float*>(take(rows * M * 4));
+    w.qh = f(rows * K);
+    w.kh = f(rows * K);
+    w.vh = f(rows * V);
+    w.w = f(rows * M);
+    w.cs = f(rows * (M / 2));
+    w.sn = f(rows * (M / 2));
+    w.raw = f(rows * M);
+    w.wts = f(rows * M);
+    w.sk = f(BH * N1 * K * M);
+    w.sv = f(BH * N1 * M * V);
+    w.lg = f(M > BWD_TABLE_M ? rows * BWD_WIDE_MW : 0);
     w.bytes = off;
     return w;
 }
@@ -287,12 +316,6 @@ struct BwdParams {
     float *dh0_k, *dh0_v, *dclock0;       // nullable
     void* workspace;
 };
-// Largest slot count of the backward pass, and of its readout kernels that
-// stage a head's table in LDS; above BWD_TABLE_M the readout and its adjoint
-// run as tile GEMMs that stream the table (the "wide" readout).
-constexpr int BWD_MAX_M = 256;
-constexpr int BWD_TABLE_M = 128;
-
 // The backward pass's workspace (fp32 unless noted, each region 256-byte
 // aligned; rows = B*H*Tp head-major, Tp = T rounded up to 64, N = Tp / 64):
 // the recomputed forward (normalised rows and their norm factors, clock,
@@ -310,7 +333,6 @@ struct BwdWorkspace {
     size_t bytes;
 };
 constexpr int BWD_RO_BLOCK = 32;    // rows per block of the readout kernels
-constexpr int BWD_WIDE_MW = 256;    // columns of the wide readout's per-row buffers
 constexpr int BWD_WIDE_SPLIT = 1024;  // token rows per table-cotangent partial of the wide readout
 constexpr int BWD_SCAN_ROWS = 32;   // rows of a state-scan tile (its columns: 32)
 constexpr int BWD_NORM_ROWS = 64;   // rows per norm-adjoint workgroup
@@ -383,6 +405,12 @@ inline BwdWorkspace bwd_workspace(int B, int T, int H, int K, int V, int M, void
 
 int launch_general_table(const float* readout, float* table, int H, int M, hipStream_t stream);
 int launch_general_chunk(const GenChunkParams& p, hipStream_t stream);
+int launch_chunk_pass(const ChunkPassParams& p, hipStream_t stream);
+// The slot readout of every head-major row (cyfa_backward.hip): z = U(lam) raw,
+// p = softmax(table z), weights = U(-lam) table^T p, rounded where the input
+// dtype is cast when bf16; lg: with M > 128 a [rows, 256] fp32 workspace.
+int launch_chunk_readout(const float* raw, const float* cs, const float* sn, const float* table, float* lg, int B,
+                         int Tp, int H, int M, int bf16, float* wts, hipStream_t stream);
 // The general path's clock and unrounded fp32 write vector with its phases
 // (head-major [B*H, Tp] and [B*H, Tp, M | M/2]), for the backward pass's recompute.
 int launch_general_clock_write(const float* delta, const float* clock0, const float* beta, int B, int T, int Tp, int H,

@@ -235,17 +235,23 @@ int cyfa_readout_table(const float *readout, float *table, int H, int M, void *h
 /* Element type of q, k, v and o in the general-shape entry points. */
 enum { CYFA_DTYPE_BF16 = 0, CYFA_DTYPE_F32 = 1 };
 
-/* Workspace bytes of cyfa_chunk_fwd_general (0 for a non-positive argument). */
+/* Workspace bytes of cyfa_chunk_fwd_general (0 for a non-positive argument):
+ * per (b, h, token padded to a multiple of 64) row the normalised rows, the
+ * clock, the write vector, both passes' row outputs and the phases, plus the
+ * fp32 states before every 64-token chunk of both passes,
+ * 4 B H (T/64 + 1)(K M + M V) bytes. C does not change it. */
 size_t cyfa_chunk_general_workspace_bytes(int B, int T, int H, int K, int V, int M, int C);
 
 /* The chunkwise forward for shapes outside cyfa_chunk_fwd's (the
  * reference's unfused fallback: _scalar_la, the affine scan over chunks, the
  * modal readout and _rotate, ops/chunk.py:115-161, 285-331 and
  * ops/utils.py:98-226, 779-929): K and V in [1, 1024], M even in [4, 256],
- * C in {16, 32, 64}; q, k, v and o of `dtype` (bf16 or fp32), everything else
- * as for cyfa_chunk_fwd. Computes in fp32; bf16 inputs are rounded to bf16
- * where the reference casts to the input dtype. Plain kernels without matrix
- * cores: no model configuration takes this path. */
+ * C in {16, 32, 64}, B * H <= 65535; q, k, v and o of `dtype` (bf16 or
+ * fp32), everything else as for cyfa_chunk_fwd. Computes in fp32; bf16 inputs
+ * are rounded to bf16 where the reference casts to the input dtype. Each pass
+ * runs chunk-parallel over 64-token chunks whatever C is (C changes no value
+ * beyond fp32 summation order): a scan forms the states before every chunk,
+ * then every chunk's output is formed from its state and its own rows. */
 int cyfa_chunk_fwd_general(const CyfaChunkArgs *args, int dtype, void *hip_stream);
 
 /* One decode step for shapes outside cyfa_decode_step's, up to the
