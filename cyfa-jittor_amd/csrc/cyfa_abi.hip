@@ -115,7 +115,9 @@ int cyfa_readout_table(const float* readout, float* table, int H, int M, void* h
 
 namespace {
 
-int decode_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* ly, void* hip_stream) {
+// f32: q, k, v and o are fp32 (cyfa_decode_step_general at the tuned shapes):
+// the same kernels without the bf16 rounding points, one workgroup per (b, h).
+int decode_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* ly, void* hip_stream, bool f32 = false) {
     if (!a) return fail(CYFA_ERR_VALUE, "cyfa_decode_step: null args");
     if (a->M != 128) return fail(CYFA_ERR_UNSUPPORTED, "cyfa_decode_step: num_slots must be 128, got %d", a->M);
     if (!((a->K == 128 || a->K == 256) && (a->V == 128 || a->V == 256)))
@@ -173,8 +175,9 @@ int decode_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* ly, void* hi
     p.hk_out = a->hk_out;
     p.hv_out = a->hv_out;
     p.clock_out = a->clock_out;
+    p.f32 = f32 ? 1 : 0;
     const size_t ws = cyfa::decode_workspace_bytes(a->B, a->H, a->K, a->V);
-    if (ws && a->workspace && a->workspace_bytes >= ws) {
+    if (!f32 && ws && a->workspace && a->workspace_bytes >= ws) {
         if (!aligned(a->workspace, 16)) return fail(CYFA_ERR_ALIGN, "cyfa_decode_step: workspace needs 16-byte alignment");
         p.part = (float*)a->workspace;
     }
@@ -724,6 +727,12 @@ int cyfa_decode_step_general(const CyfaDecodeArgs* a, int dtype, void* hip_strea
     if (has_in != (a->hv_in != nullptr) || has_in != (a->clock_in != nullptr))
         return fail(CYFA_ERR_VALUE, "%s: hk_in, hv_in and clock_in must be all set or all null", fn);
     if (!isfinite(a->scale)) return fail(CYFA_ERR_VALUE, "%s: scale must be finite", fn);
+    // fp32 at the tuned kernel's shapes: that kernel, without its bf16 rounding
+    // (its alignment needs met; the workspace fields stay ignored)
+    if (dtype == CYFA_DTYPE_F32 && a->M == 128 && (a->K == 128 || a->K == 256) && (a->V == 128 || a->V == 256) &&
+        aligned(a->v, 8) && aligned(a->table, 16) && aligned(a->hk_out, 16) && aligned(a->hv_out, 16) &&
+        (!has_in || (aligned(a->hk_in, 16) && aligned(a->hv_in, 16))))
+        return decode_step(a, nullptr, hip_stream, true);
     cyfa::GenDecodeParams p{};
     p.B = a->B;
     p.H = a->H;

@@ -76,6 +76,16 @@ __device__ __forceinline__ float4 stream_load(rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
 }
 
+// Element i of row `row` (n elements per row) of q, k or v: bf16, or fp32
+// (F32; the pointer then holds fp32 data).
+template <bool F32>
+__device__ __forceinline__ float ld_in(const __bf16* base, size_t row, int n, int i, uint32_t dead) {
+    if constexpr (F32)
+        return ld_f32(buf(reinterpret_cast<const float*>(base) + row * n, (size_t)n * 4), ((uint32_t)i * 4) | dead);
+    else
+        return ld_bf16(buf(base + row * n, (size_t)n * 2), ((uint32_t)i * 2) | dead);
+}
+
 // The one-token inputs of (b, h): q and k channel c (< K) or v channel c (< V)
 // of this head. LAYER: from the width-4 causal short convolution of the
 // projection row (layers/cyfa.py:138-233, the arithmetic of short_conv_kernel);
@@ -259,16 +269,24 @@ __device__ __forceinline__ void gate_columns(const bf16x8* s_g0, const GateW& g,
     if (lg == 0) s_gate[16 * c + lr] = bf16_round(tot + g.bias);
 }
 
-// Write vector w (bf16-rounded, ops/utils.py:664-702) and the phase of every
-// pair into LDS; threads 0..63 (one pair each).
+// Write vector w (ops/utils.py:664-702) and the phase of every pair into LDS;
+// threads 0..63 (one pair each). bf16 inputs: w rounded to bf16, the phase on
+// the hardware sine/cosine of the once-reduced clock. F32 (fp32 inputs, which
+// the reference computes without rounding): w unrounded, the phase from the
+// reference's integer range reduction of the clock and the full-precision
+// sincosf.
+template <bool F32 = false>
 __device__ __forceinline__ void write_vector_lds(float lam, float beta, float* s_w, float* s_c, float* s_s) {
     const int tid = threadIdx.x;
     if (tid < kPairs) {
         float s, c;
-        pair_sincos(reduced_clock(lam), tid, s, c);
+        if constexpr (F32)
+            sincosf(clock_phase(lam, tid), &s, &c);
+        else
+            pair_sincos(reduced_clock(lam), tid, s, c);
         const float a = beta * pair_scale(tid);
-        s_w[2 * tid] = bf16_round(a * c);
-        s_w[2 * tid + 1] = bf16_round(-a * s);
+        s_w[2 * tid] = F32 ? a * c : bf16_round(a * c);
+        s_w[2 * tid + 1] = F32 ? -a * s : bf16_round(-a * s);
         s_c[tid] = c;
         s_s[tid] = s;
     }
@@ -377,7 +395,7 @@ __device__ __forceinline__ void readout_1024(const float* s_raw, const float* s_
 // partials are summed in wave order. LAYER: the gated output norm
 // o_norm(o * prescale, gate) (layers/cyfa.py:349-350, as rms_norm_kernel<1>:
 // wave 0 holds four consecutive values per lane) before o is stored.
-template <int V, bool LAYER>
+template <int V, bool LAYER, bool F32 = false>
 __device__ __forceinline__ void output_1024(const DecodeParams& p, int bh, const float4* hv_r, const float* s_om,
                                             float (*s_part)[256], float* s_v, const float4* on_w4,
                                             const bf16x4* on_g4, const float* s_gate) {
@@ -413,7 +431,10 @@ __device__ __forceinline__ void output_1024(const DecodeParams& p, int bh, const
             float s = 0.f;
 #pragma unroll
             for (int w = 0; w < NT / 64; w++) s += s_part[w][tid];
-            p.o[(size_t)bh * V + tid] = (bf16_t)s;
+            if constexpr (F32)
+                reinterpret_cast<float*>(p.o)[(size_t)bh * V + tid] = s;
+            else
+                p.o[(size_t)bh * V + tid] = (bf16_t)s;
         }
         return;
     }
@@ -458,8 +479,9 @@ __device__ __forceinline__ void output_1024(const DecodeParams& p, int bh, const
 
 // q/k RMS norms (ops/fused_recurrent.py:62-89) from each thread's raw q, k
 // channel (threads < K) and its norm weights qw, kw (loaded with the other
-// small inputs), into s_q (scaled) and s_k; NW waves.
-template <int K, int NW>
+// small inputs), into s_q (scaled) and s_k; NW waves. Rounded to bf16 unless
+// F32 (fp32 inputs).
+template <int K, int NW, bool F32 = false>
 __device__ __forceinline__ void qk_norms(const DecodeParams& p, float qv, float kv, float qw, float kw,
                                          float (*s_red)[NW], float* s_q, float* s_k) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -477,8 +499,8 @@ __device__ __forceinline__ void qk_norms(const DecodeParams& p, float qv, float 
     }
     if (tid < K) {
         const float rq = rsqrtf(tq / K + p.q_eps), rk = rsqrtf(tk / K + p.k_eps);
-        s_q[tid] = bf16_round(qv * rq * qw) * p.scale;
-        s_k[tid] = bf16_round(kv * rk * kw);
+        s_q[tid] = (F32 ? qv * rq * qw : bf16_round(qv * rq * qw)) * p.scale;
+        s_k[tid] = F32 ? kv * rk * kw : bf16_round(kv * rk * kw);
     }
 }
 
@@ -518,7 +540,7 @@ __device__ __forceinline__ void prefetch_ranges(const DecodeParams& p, int wg, i
 // prologue (conv, gates, write vector, q/k norms) while the states stream in;
 // key-state update as hk arrives; the slot readout while hv arrives; then the
 // value-state update and o.
-template <int K, int V, bool LAYER>
+template <int K, int V, bool LAYER, bool F32 = false>
 __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     constexpr int NT = 1024;
     constexpr int NS = K / SLICE;   // key-state slices
@@ -562,9 +584,9 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
         ck = load_conv(src, HK + h * K + tid, dk);
         cv = load_conv(src, 2 * HK + h * V + tid, dv);
     } else {
-        qv = ld_bf16(buf(p.q + (size_t)bh * K, (size_t)K * 2), ((uint32_t)tid * 2) | dk);
-        kv = ld_bf16(buf(p.k + (size_t)bh * K, (size_t)K * 2), ((uint32_t)tid * 2) | dk);
-        vv = ld_bf16(buf(p.v + (size_t)bh * V, (size_t)V * 2), ((uint32_t)tid * 2) | dv);
+        qv = ld_in<F32>(p.q, bh, K, tid, dk);
+        kv = ld_in<F32>(p.k, bh, K, tid, dk);
+        vv = ld_in<F32>(p.v, bh, V, tid, dv);
     }
     const GateIn gi = load_gate_inputs<LAYER>(p, bh);
     const float qw = ld_f32(buf(p.q_w, (size_t)K * 4), ((uint32_t)tid * 4) | dk);
@@ -603,8 +625,8 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     stage_table(s_tab, tab);
     const float lam = gi.clock + delta_in;
     const float decay = expf(g_in);
-    write_vector_lds(lam, beta_in, s_w, s_c, s_s);
-    qk_norms<K, NW>(p, qv, kv, qw, kw, s_red, s_q, s_k);
+    write_vector_lds<F32>(lam, beta_in, s_w, s_c, s_s);
+    qk_norms<K, NW, F32>(p, qv, kv, qw, kw, s_red, s_q, s_k);
     __syncthreads();
     if (tid == 0) p.clock_out[bh] = lam;  // after every thread has read clock_in
 
@@ -657,7 +679,7 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
         }
     }
     if (own_gate) gate_columns(s_g0, gw, s_gate);
-    output_1024<V, LAYER>(p, bh, hv_r, s_om, s_part, s_v, on_w4, on_g4, own_gate ? s_gate : nullptr);
+    output_1024<V, LAYER, F32>(p, bh, hv_r, s_om, s_part, s_v, on_w4, on_g4, own_gate ? s_gate : nullptr);
 }
 
 // Small-batch form, part A: grid (NSL, B H), 256 threads; workgroup s updates
@@ -692,9 +714,9 @@ __global__ __launch_bounds__(256) void decode_split_a_kernel(DecodeParams p) {
         ck = load_conv(src, HK + h * K + tid, dk);
         cv = load_conv(src, 2 * HK + h * V + SLICE * s + tid, dv);
     } else {
-        qv = ld_bf16(buf(p.q + (size_t)bh * K, (size_t)K * 2), ((uint32_t)tid * 2) | dk);
-        kv = ld_bf16(buf(p.k + (size_t)bh * K, (size_t)K * 2), ((uint32_t)tid * 2) | dk);
-        vv = ld_bf16(buf(p.v + (size_t)bh * V, (size_t)V * 2), ((uint32_t)(SLICE * s + tid) * 2) | dv);
+        qv = ld_in<false>(p.q, bh, K, tid, dk);
+        kv = ld_in<false>(p.k, bh, K, tid, dk);
+        vv = ld_in<false>(p.v, bh, V, SLICE * s + tid, dv);
     }
     const GateIn gi = load_gate_inputs<LAYER>(p, bh);
     const float qw = ld_f32(buf(p.q_w, (size_t)K * 4), ((uint32_t)tid * 4) | dk);
@@ -840,6 +862,15 @@ void launch(const DecodeParams& p, hipStream_t stream) {
     }
 }
 
+// The op step; fp32 inputs always take the one-workgroup form.
+template <int K, int V>
+void launch_op(const DecodeParams& p, hipStream_t stream) {
+    if (p.f32)
+        hipLaunchKernelGGL((decode_step_kernel<K, V, false, true>), dim3(p.B * p.H), dim3(1024), 0, stream, p);
+    else
+        launch<K, V, false>(p, stream);
+}
+
 }  // namespace
 
 size_t decode_workspace_bytes(int B, int H, int K, int V) {
@@ -848,21 +879,21 @@ size_t decode_workspace_bytes(int B, int H, int K, int V) {
 }
 
 int launch_decode_step(const DecodeParams& p, int K, int V, hipStream_t stream) {
-    if (p.qkv) {  // the layer step: K = V = 256 only
-        if (K != 256 || V != 256) return -1;
+    if (p.qkv) {  // the layer step: K = V = 256 and bf16 only
+        if (K != 256 || V != 256 || p.f32) return -1;
         // every buffer the kernels read spans less than DEAD bytes
         const long long D = (long long)p.H * (2 * K + V);
         if (p.cache_in && (p.cache_row < 0 || (2 * p.cache_row + D) * 2 >= (long long)DEAD)) return -1;
         if (D * 8 >= (long long)DEAD) return -1;
         launch<256, 256, true>(p, stream);
     } else if (K == 256 && V == 256)
-        launch<256, 256, false>(p, stream);
+        launch_op<256, 256>(p, stream);
     else if (K == 128 && V == 128)
-        launch<128, 128, false>(p, stream);
+        launch_op<128, 128>(p, stream);
     else if (K == 256 && V == 128)
-        launch<256, 128, false>(p, stream);
+        launch_op<256, 128>(p, stream);
     else if (K == 128 && V == 256)
-        launch<128, 256, false>(p, stream);
+        launch_op<128, 256>(p, stream);
     else
         return -1;
     return 0;

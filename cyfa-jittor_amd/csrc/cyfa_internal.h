@@ -15,6 +15,7 @@ struct DecodeParams {
     const float *hk_in, *hv_in, *clock_in;
     __bf16* o;
     float *hk_out, *hv_out, *clock_out;
+    int f32;  // the op step with q, k, v and o in fp32 (computed without bf16 rounding)
     // Layer step (decode_step_kernel<.., true>): q, k, v come from the width-4
     // short convolution of the projection row qkv, the gates from abd, and o
     // receives the gated output norm instead of the op's output.

@@ -257,7 +257,9 @@ int cyfa_chunk_fwd_general(const CyfaChunkArgs *args, int dtype, void *hip_strea
 /* One decode step for shapes outside cyfa_decode_step's, up to the
  * reference's decode limits (ops/fused_recurrent.py:45-46): K and V in
  * [1, 1024], M even in [4, 256]; q, k, v and o of `dtype`; states fp32; the
- * workspace fields are ignored. One workgroup per (b, h). */
+ * workspace fields are ignored. One workgroup per (b, h). fp32 at
+ * cyfa_decode_step's shapes (K, V in {128, 256}, M = 128, with its alignment)
+ * runs that kernel without its bf16 rounding points. */
 int cyfa_decode_step_general(const CyfaDecodeArgs *args, int dtype, void *hip_stream);
 
 /* ---- Backward pass of the chunk op ---- */

@@ -97,6 +97,11 @@ DECODE_CASES = [
     (1, 3, 512, 384, 128, torch.float32, True),
     (2, 1, 1024, 1024, 256, torch.bfloat16, True),
     (3, 2, 128, 128, 32, torch.float32, False),
+    # fp32 at the tuned kernel's shapes (K, V in {128, 256}, 128 slots): that
+    # kernel without its bf16 rounding points
+    (3, 2, 128, 256, 128, torch.float32, True),
+    (1, 4, 256, 128, 128, torch.float32, False),
+    (64, 4, 256, 256, 128, torch.float32, True),
 ]
 
 
