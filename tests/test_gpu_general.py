@@ -68,6 +68,9 @@ CHUNK_CASES = [
     (1, 64, 3, 256, 128, 128, 64, torch.bfloat16, True),  # V = 128: outside the tuned kernels
     (1, 10, 2, 96, 80, 16, 64, torch.float32, True),      # T shorter than one chunk
     (1, 96, 1, 128, 128, 64, 32, torch.float16, True),    # fp16 operands run in fp32
+    (1, 70, 1, 1024, 1024, 256, 32, torch.bfloat16, True),  # the largest head dims and slot count
+    (1, 40, 2, 1, 1, 4, 16, torch.float32, True),          # the smallest
+    (2, 1, 2, 64, 64, 16, 64, torch.bfloat16, True),       # a one-token sequence
 ]
 
 
