@@ -76,21 +76,28 @@ __device__ __forceinline__ float gen_pair_scale(int p, int R) {
 
 // table[h][r][m] = sum_j readout[h][r][j] Phi[j][m] for any even M (the
 // basis of ops/chunk.py:82-103 with the angle 2 pi ((pair j) mod R) / R
-// reduced exactly in integers). One block per (h, r), one thread per m.
+// reduced exactly in integers: the R angles' sine and cosine are formed once
+// per block in LDS and indexed by k = (pair j) mod R, stepped by pair per j).
+// One block per (h, r), one thread per m.
 __global__ __launch_bounds__(256) void gen_table_kernel(const float* readout, float* table, int M) {
     const int R = M - 1, hr = blockIdx.x, m = threadIdx.x;
-    __shared__ float row[256];
-    for (int j = m; j < R; j += blockDim.x) row[j] = readout[(size_t)hr * R + j];
+    __shared__ float row[256], cos_k[256], sin_k[256];
+    for (int j = m; j < R; j += blockDim.x) {
+        row[j] = readout[(size_t)hr * R + j];
+        sincosf((float)((double)j * (kTwoPi / R)), &sin_k[j], &cos_k[j]);
+    }
     __syncthreads();
     if (m >= M) return;
     float acc = 0.f;
     if (m != 1) {
         const int pair = m >> 1;
         const float sc = gen_pair_scale(pair, R);
+        const float* basis = (m & 1) ? sin_k : cos_k;
+        int k = 0;  // (pair * j) mod R
         for (int j = 0; j < R; j++) {
-            float sn, cs;
-            sincosf((float)((double)((pair * j) % R) * (kTwoPi / R)), &sn, &cs);
-            acc = fmaf(row[j], sc * ((m & 1) ? sn : cs), acc);
+            acc = fmaf(row[j], sc * basis[k], acc);
+            k += pair;
+            k = k >= R ? k - R : k;
         }
     }
     table[(size_t)hr * M + m] = acc;

@@ -1634,20 +1634,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void p
 
 // ---------------------------------------------------------------------------
 // table[h] = readout[h] @ Phi (ops/chunk.py:82-103, 281). One block per
-// (h, r); Phi[j][m] is evaluated on the fly with the exact integer reduction
-// (pair * j) mod 127 of its angle.
+// (h, r); Phi[j][m] is taken from the 127 angles 2 pi k / 127 (sine and
+// cosine formed once per block in LDS) at the exact integer reduction
+// k = (pair * j) mod 127 of its angle, stepped by pair per j.
 __global__ __launch_bounds__(128) void readout_table_kernel(const float* readout, float* table) {
     const int hr = blockIdx.x, m = threadIdx.x, pair = m >> 1;
-    __shared__ float row[kActive];
-    if (m < kActive) row[m] = readout[(size_t)hr * kActive + m];
+    __shared__ float row[kActive], cos_k[kActive], sin_k[kActive];
+    if (m < kActive) {
+        row[m] = readout[(size_t)hr * kActive + m];
+        sincosf((float)m * 0.049473900056532176f, &sin_k[m], &cos_k[m]);
+    }
     __syncthreads();
     float acc = 0.f;
     if (m != 1) {
         const float sc = pair_scale(pair);
+        const float* basis = (m & 1) ? sin_k : cos_k;
+        int k = 0;  // (pair * jr) mod 127
         for (int jr = 0; jr < kActive; jr++) {
-            float sn, cs;
-            sincosf((float)((pair * jr) % kActive) * 0.049473900056532176f, &sn, &cs);
-            acc = fmaf(row[jr], sc * ((m & 1) ? sn : cs), acc);
+            acc = fmaf(row[jr], sc * basis[k], acc);
+            k += pair;
+            k = k >= kActive ? k - kActive : k;
         }
     }
     table[(size_t)hr * kSlots + m] = acc;
