@@ -32,11 +32,13 @@ from ..ops.fused_recurrent import decode_layer_step
 from ..ops.utils import readout_table
 
 # A one-token step with at least this many (batch, head) workgroups forms
-# g_proj[1] inside the decode kernel by default (see gate_projection_in_kernel).
+# g_proj[1] inside the decode kernel by default, as does a small-batch step
+# that prefetches (see gate_projection_in_kernel).
 GATE_IN_KERNEL_MIN_WORKGROUPS = 128
 # Bytes of weights a small-batch decode step reads into the caches while its
 # decode kernel runs (prefetch_weights): ranges are taken in the order the
-# step reads them, skipping any that would pass the budget. Measured on
+# step reads them (g_proj[1]'s weight when the kernel forms the gate, o_proj,
+# then the caller's), skipping any that would pass the budget. Measured on
 # MI355X (graphed steps): the 400M model's o_proj, gate|up and down (19 MB)
 # gain 3% at B=1 and 6% at B=16; the 1.4B model's o_proj (8 MB) gains 1.4% at
 # B=1, while its 77 MB outlast the decode kernel and cost 2.5%.
@@ -255,9 +257,12 @@ class CyclicFlowAttention(nn.Module):
         # kernel instead of a separate projection launch (same bits either way).
         # On MI355X it saves about 1.4% of the 400M step at B=64 (one launch per
         # layer fewer) but costs the kernel 2.4 us of L2 reads (each workgroup
-        # reads its head's 128 KB weight slice) and loses at B=1; None (the
-        # default) picks it when the step has at least
-        # GATE_IN_KERNEL_MIN_WORKGROUPS (batch, head) workgroups.
+        # reads its head's 128 KB weight slice), and without the weight in the
+        # caches it loses at B=1. None (the default) picks it when the step has
+        # at least GATE_IN_KERNEL_MIN_WORKGROUPS (batch, head) workgroups, or
+        # when the small-batch prefetch applies, which then reads the gate
+        # weight first (400M at B=1: 1025 -> 1035 tok/s; at B=16: 15.2k ->
+        # 15.4k; 1.4B at B=1: 711 -> 713).
         self.gate_projection_in_kernel = None
         # Whether a one-token step at small batch (B H <= _native.PREFETCH_MAX_BH)
         # has the decode kernel read o_proj's weight, and the weights forward_block
@@ -413,17 +418,18 @@ class CyclicFlowAttention(nn.Module):
             # g_proj[1] inside the kernel (the same bits as _native.linear) when asked and
             # its operands are bf16; otherwise the gate is projected first
             want = self.gate_projection_in_kernel
+            small = self.prefetch_weights and B * H <= _native.PREFETCH_MAX_BH
             if want is None:
-                want = B * H >= GATE_IN_KERNEL_MIN_WORKGROUPS
+                want = B * H >= GATE_IN_KERNEL_MIN_WORKGROUPS or small
             in_kernel = (want and g1.weight.dtype == torch.bfloat16
                          and (g1.bias is None or g1.bias.dtype == torch.bfloat16))
             gate = None if in_kernel else _native.linear(g0_out, g1.weight, g1.bias)
             # at small batches the decode kernel leaves most compute units and
             # HBM idle: it reads o_proj's weight and the caller's into the caches
             pf = ()
-            if self.prefetch_weights and B * H <= _native.PREFETCH_MAX_BH:
+            if small:
                 total = 0
-                for t in (self.o_proj.weight,) + tuple(prefetch):
+                for t in ((g1.weight,) if in_kernel else ()) + (self.o_proj.weight,) + tuple(prefetch):
                     n = t.numel() * t.element_size()
                     if total + n <= PREFETCH_BUDGET_BYTES and len(pf) < _native.PREFETCH_RANGES:
                         pf, total = pf + (t,), total + n
