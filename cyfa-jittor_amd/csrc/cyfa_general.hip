@@ -234,6 +234,40 @@ __device__ __forceinline__ void gen_readout_row(const float* raw, const float* c
     }
 }
 
+// One column of a state update, row by row: out[r ld] = alpha in[r ld] +
+// add(r) for r < rows (in == nullptr: a zero state), and use(r, value) in row
+// order. The rows are read in blocks of GEN_ROWS, the next block's loads
+// issued before the current block's stores: in and out may be the same
+// buffer (an in-place step), so the compiler cannot move a load above an
+// earlier store itself, and row-at-a-time code waits a full memory latency
+// per row. Every element is read before it is written, by the same thread.
+constexpr int GEN_ROWS = 16;
+
+template <class Add, class Use>
+__device__ __forceinline__ void gen_state_rows(const float* in, float* out, int ld, int rows, float alpha, Add add,
+                                               Use use) {
+    float cur[GEN_ROWS], nxt[GEN_ROWS];
+    const auto fetch = [&](int r0, float (&dst)[GEN_ROWS]) {
+#pragma unroll
+        for (int i = 0; i < GEN_ROWS; i++) dst[i] = in && r0 + i < rows ? in[(size_t)(r0 + i) * ld] : 0.f;
+    };
+    fetch(0, cur);
+    for (int r0 = 0; r0 < rows; r0 += GEN_ROWS) {
+        if (r0 + GEN_ROWS < rows) fetch(r0 + GEN_ROWS, nxt);
+#pragma unroll
+        for (int i = 0; i < GEN_ROWS; i++) {
+            const int r = r0 + i;
+            if (r < rows) {
+                const float hv = alpha * cur[i] + add(r);
+                out[(size_t)r * ld] = hv;
+                use(r, hv);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < GEN_ROWS; i++) cur[i] = nxt[i];
+    }
+}
+
 // One decode step of any shape (ops/fused_recurrent.py:10-200 with the
 // oracle's order): q_hat = cast(q rs w) scale, k_hat = cast(k rs w);
 // lam = clock + delta; hk' = e^g hk + k_hat (x) w; raw = hk'^T q_hat;
@@ -284,12 +318,9 @@ __global__ __launch_bounds__(256) void gen_decode_kernel(GenDecodeParams p) {
     // hk' and raw: thread m walks the key rows of column m
     for (int m = tid; m < M; m += 256) {
         float acc = 0.f;
-        for (int r = 0; r < K; r++) {
-            const size_t at = ((size_t)bh * K + r) * M + m;
-            const float hv = (p.hk_in ? alpha * p.hk_in[at] : 0.f) + sk[r] * sw[m];
-            p.hk_out[at] = hv;
-            acc = fmaf(hv, sq[r], acc);
-        }
+        const float wm = sw[m];
+        gen_state_rows(p.hk_in ? p.hk_in + (size_t)bh * K * M + m : nullptr, p.hk_out + (size_t)bh * K * M + m, M, K,
+                       alpha, [&](int r) { return sk[r] * wm; }, [&](int r, float hv) { acc = fmaf(hv, sq[r], acc); });
         sraw[m] = acc;
     }
     __syncthreads();
@@ -298,12 +329,9 @@ __global__ __launch_bounds__(256) void gen_decode_kernel(GenDecodeParams p) {
     // hv' and o: thread j walks the slot rows of value column j
     for (int j = tid; j < V; j += 256) {
         float acc = 0.f;
-        for (int m = 0; m < M; m++) {
-            const size_t at = ((size_t)bh * M + m) * V + j;
-            const float hv = (p.hv_in ? alpha * p.hv_in[at] : 0.f) + sw[m] * sv[j];
-            p.hv_out[at] = hv;
-            acc = fmaf(hv, swt[m], acc);
-        }
+        const float vj = sv[j];
+        gen_state_rows(p.hv_in ? p.hv_in + (size_t)bh * M * V + j : nullptr, p.hv_out + (size_t)bh * M * V + j, V, M,
+                       alpha, [&](int m) { return sw[m] * vj; }, [&](int m, float hv) { acc = fmaf(hv, swt[m], acc); });
         gen_st<BF>(p.o, xv + j, acc);
     }
     if (tid == 0) p.clock_out[bh] = (float)lam;
