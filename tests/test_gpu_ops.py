@@ -89,10 +89,16 @@ def test_decode_step_matches_oracle(B, H, K, V, state):
     _check_states(st, rst, "decode")
 
 
-def test_decode_step_inplace_equals_out_of_place():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_decode_step_inplace_equals_out_of_place(dtype):
+    """An in-place step (states updated in their own buffers) gives the bits
+    of an out-of-place one, for bf16 and for fp32 operands (the tuned kernel's
+    fp32 form)."""
     from cyclic_flow_attention.ops import fused_recurrent_cyfa
 
     x, init = _inputs(2, 1, 2, seed=5, state=True)
+    for name in ("q", "k", "v"):
+        x[name] = x[name].to(dtype)
     xg, ig = _gpu(x, init)
     with torch.no_grad():
         o1, st1 = fused_recurrent_cyfa(**xg, initial_state=ig, output_final_state=True)
