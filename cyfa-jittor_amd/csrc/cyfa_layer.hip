@@ -743,6 +743,10 @@ __device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) 
 __global__ __launch_bounds__(1024) void argmax_rows_kernel(const bf16_t* x, long long ldx, int n, long long* out) {
     constexpr int NT = 1024, DEPTH = 4;  // four 16-byte loads per thread in flight
     const bf16_t* xr = x + (size_t)blockIdx.x * ldx;
+    // The row as a buffer: a chunk of 8 not wholly inside it is loaded at the
+    // LIN_DEAD offset (zeros, its elements are read one by one below), so the
+    // loads sit behind no branch and all of them are in flight together.
+    const lin_rsrc_t r = lin_rsrc(xr, (size_t)n * 2);
     float bv = -INFINITY;
     int bi = 0x7fffffff;
     for (int base = 0; base < n; base += 8 * NT * DEPTH) {
@@ -750,7 +754,8 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const bf16_t* x, long
 #pragma unroll
         for (int d = 0; d < DEPTH; d++) {
             const int i0 = base + 8 * (threadIdx.x + NT * d);
-            if (i0 + 8 <= n) v[d] = *reinterpret_cast<const bf16x8*>(xr + i0);
+            const uint32_t dead = i0 + 8 <= n ? 0u : LIN_DEAD;
+            v[d] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, ((uint32_t)i0 * 2) | dead, 0, 0));
         }
 #pragma unroll
         for (int d = 0; d < DEPTH; d++) {
@@ -967,6 +972,7 @@ int launch_silu_mul(const bf16_t* gu, bf16_t* out, int rows, int F, hipStream_t 
 }
 
 int launch_argmax_rows(const bf16_t* x, long long ldx, int rows, int n, long long* out, hipStream_t stream) {
+    if ((unsigned long long)n * 2 >= LIN_DEAD) return -1;  // a row's byte offsets stay below the dead offset
     hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(1024), 0, stream, x, ldx, n, out);
     return 0;
 }
