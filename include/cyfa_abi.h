@@ -336,7 +336,8 @@ int cyfa_rms_norm(const CyfaNormArgs *args, void *hip_stream);
 /* Row-wise argmax of bf16 rows x[r * ldx .. + n) into out[r] (int64), with
  * torch.argmax's result: the index of the first maximum, NaN counting as the
  * largest value. Replaces the greedy token choice of a decode step
- * (logits.argmax, models/cyfa/modeling_cyfa.py:142-158; generation.py:43). */
+ * (logits.argmax, models/cyfa/modeling_cyfa.py:142-158; generation.py:43).
+ * x 16-byte aligned, ldx a multiple of 8, n below 2^30. */
 int cyfa_argmax_rows(const void *x, long long ldx, int rows, int n, long long *out, void *hip_stream);
 
 /* Arguments of one projection y = x W^T (+ bias) over at most 64 rows of x
