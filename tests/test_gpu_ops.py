@@ -121,6 +121,7 @@ CHUNK_CASES = [
     (2, 512, 2, True, "100"),    # one segment: no segment-state kernel
     (16, 1024, 4, False, None),  # 64 sequences, 4 chunks per segment
     (8, 2048, 4, True, None),    # configuration 3's attention shape: 8 segments of 4 chunks
+    (1, 65536, 2, True, None),   # four times configuration 5's length: 1024 chunks, the clock past 3e4
 ]
 
 
