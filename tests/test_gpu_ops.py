@@ -432,3 +432,46 @@ def test_wide_operands_compute_in_fp32(dtype):
     assert_close(od, rod, what=f"{dtype} decode o", **bar)
     assert_close(std[0], rstd[0], what=f"{dtype} decode hk", **f32)
     assert_close(std[1], rstd[1], what=f"{dtype} decode hv", **f32)
+
+
+@pytest.mark.parametrize("dtype,K,M", [(torch.bfloat16, 256, 128), (torch.float32, 256, 128),
+                                       (torch.bfloat16, 64, 96)])
+def test_forward_repeats_bit_for_bit_on_any_stream(dtype, K, M):
+    """The chunk op and a decode step give identical bits when run twice, and
+    when run on a side stream instead of the default one (every partial sum
+    in the kernels is added in a fixed order; the launches go on the caller's
+    current stream). Covers the tuned kernels (bf16, K = V = 256, 128 slots)
+    and the general path (fp32 operands; another head size and slot count)."""
+    from cyclic_flow_attention.ops import chunk_cyfa, fused_recurrent_cyfa
+
+    gen = torch.Generator().manual_seed(21)
+    B, T, H = 2, 300, 2
+    R = M - 1
+    x = dict(q=torch.randn(B, T, H, K, generator=gen).to(dtype), k=torch.randn(B, T, H, K, generator=gen).to(dtype),
+             v=torch.randn(B, T, H, K, generator=gen).to(dtype),
+             g=torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=gen) + 3),
+             delta=torch.sigmoid(torch.randn(B, T, H, generator=gen)),
+             beta=torch.sigmoid(torch.randn(B, T, H, generator=gen)),
+             readout=torch.eye(R).expand(H, R, R) + 0.05 * torch.randn(H, R, R, generator=gen),
+             q_norm_weight=1 + 0.1 * torch.randn(K, generator=gen), k_norm_weight=1 + 0.1 * torch.randn(K, generator=gen))
+    xg = {k: v.to(DEV) for k, v in x.items()}
+    seq = ("q", "k", "v", "g", "delta", "beta")
+    step = {k: (v[:, -1:] if k in seq else v) for k, v in xg.items()}
+
+    def run():
+        with torch.no_grad():
+            o, st = chunk_cyfa(**xg, output_final_state=True)
+            od, std = fused_recurrent_cyfa(**step, initial_state=st, output_final_state=True)
+        return (o,) + tuple(st) + (od,) + tuple(std)
+
+    first = run()
+    second = run()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        third = run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for a, b, c in zip(first, second, third):
+        assert torch.equal(a, b)
+        assert torch.equal(a, c)
