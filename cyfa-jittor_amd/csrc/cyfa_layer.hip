@@ -387,6 +387,154 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// One-row projections (M == 1, K >= 512: the projections of a B = 1 decode
+// step) with linear_rows_kernel's epilogues: the fused pre-norm (NM 1), the
+// SwiGLU pairing of interleaved gate and up rows, the bias and the residual
+// add. For one row the MFMA kernel uses one of the sixteen rows of each
+// operand block and stages every byte of W through LDS; here each wave
+// streams RW rows of W from memory with 16-byte loads and forms the dot
+// products on v_dot2_f32_bf16. Lane l covers elements 512 c + 8 l .. + 7 of
+// chunk c. A batch of D chunks is issued at once, x first, then the norm
+// weight, then W, so that the norm waits for x alone while W streams in; D
+// is 4 for K <= 2048 (always with the norm) and 12 above, so every K up to
+// 6144 is one batch. Each row's sum runs over the chunks
+// in order on the lane, then across the wave in wave_sum's fixed order: an
+// order other than linear_rows_kernel's, which can move an output across a
+// bf16 rounding boundary; every launch of a given shape takes the same path.
+template <int RW, int NM, bool SWIGLU, int D>
+__global__ __launch_bounds__(256) void gemv_row_kernel(LinearParams p) {
+    static_assert(!SWIGLU || RW % 2 == 0, "SwiGLU pairs gate and up rows");
+    static_assert(NM == 0 || D == 4, "the norm needs the whole row in one batch (K <= 2048)");
+    constexpr int F = SWIGLU ? RW / 2 : RW;  // outputs per wave
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int K = p.K, N = p.N, nch = (K + 511) / 512;
+    // this wave's W rows: SWIGLU, F gate rows 32 g + f0 .. and the matching up
+    // rows 32 g + 16 + f0 .. of group g (16 outputs per group)
+    int rows[RW];
+    const int per_group = 16 / F, g = wave / per_group, f0 = (wave % per_group) * F;
+    if constexpr (SWIGLU) {
+#pragma unroll
+        for (int i = 0; i < F; i++) {
+            rows[i] = 32 * g + f0 + i;
+            rows[F + i] = 32 * g + 16 + f0 + i;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < RW; i++) rows[i] = RW * wave + i;
+    }
+    lin_rsrc_t rw[RW];
+#pragma unroll
+    for (int i = 0; i < RW; i++)
+        rw[i] = lin_rsrc(rows[i] < N ? p.w + (size_t)rows[i] * K : nullptr, rows[i] < N ? (size_t)K * 2 : 0);
+    const lin_rsrc_t rx = lin_rsrc(p.x, (size_t)K * 2);
+    const lin_rsrc_t rn = lin_rsrc(NM == 1 ? p.norm_weight : nullptr, NM == 1 ? (size_t)K * 4 : 0);
+    // chunk c's 16-byte piece of this lane, or LIN_DEAD past K (K % 8 == 0:
+    // a lane's eight elements are all inside or all outside)
+    const auto piece = [&](int c) {
+        const int k = 512 * c + 8 * lane;
+        return ((uint32_t)k * 2) | (c < nch && k < K ? 0u : LIN_DEAD);
+    };
+    float acc[RW];
+#pragma unroll
+    for (int i = 0; i < RW; i++) acc[i] = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += D) {
+        bf16x8 xv[D];
+        float4 na[NM == 1 ? D : 1], nb[NM == 1 ? D : 1];
+        u32x4 wv[D][RW];
+#pragma unroll
+        for (int d = 0; d < D; d++) xv[d] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rx, piece(c0 + d), 0, 0));
+        if constexpr (NM == 1) {  // the norm weight's 8 floats: the same piece at twice the offset
+#pragma unroll
+            for (int d = 0; d < D; d++) {
+                const uint32_t off = piece(c0 + d), o2 = (off & ~LIN_DEAD) * 2 | (off & LIN_DEAD);
+                na[d] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rn, o2, 0, 0));
+                nb[d] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rn, o2 + 16, 0, 0));
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; d++)
+#pragma unroll
+            for (int i = 0; i < RW; i++)
+                wv[d][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw[i], piece(c0 + d), 0, 0));
+        // every load of the batch is issued before any is used: without the
+        // barrier the scheduler interleaves loads and uses to save registers
+        // and keeps only a few loads in flight
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (NM == 1) {
+            // rsqrt(mean x^2 + eps) over the whole row (one batch), on every
+            // wave; then bf16(x rs w), as the separate norm rounds it
+            float ss = 0.f;
+#pragma unroll
+            for (int d = 0; d < D; d++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const bf16x2 x2 = {xv[d][2 * e], xv[d][2 * e + 1]};
+                    ss = __builtin_amdgcn_fdot2_f32_bf16(x2, x2, ss, false);
+                }
+            const float rs = rsqrtf(wave_sum(ss) / (float)K + p.norm_eps);
+#pragma unroll
+            for (int d = 0; d < D; d++) {
+                const float wn[8] = {na[d].x, na[d].y, na[d].z, na[d].w, nb[d].x, nb[d].y, nb[d].z, nb[d].w};
+#pragma unroll
+                for (int e = 0; e < 8; e++) xv[d][e] = (bf16_t)((float)xv[d][e] * rs * wn[e]);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; d++)
+#pragma unroll
+            for (int i = 0; i < RW; i++) {
+                const bf16x8 wr = __builtin_bit_cast(bf16x8, wv[d][i]);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const bf16x2 a2 = {xv[d][2 * e], xv[d][2 * e + 1]}, b2 = {wr[2 * e], wr[2 * e + 1]};
+                    acc[i] = __builtin_amdgcn_fdot2_f32_bf16(a2, b2, acc[i], false);
+                }
+            }
+    }
+    float tot[RW];
+#pragma unroll
+    for (int i = 0; i < RW; i++) tot[i] = wave_sum(acc[i]);
+    if constexpr (SWIGLU) {
+#pragma unroll
+        for (int i = 0; i < F; i++) {
+            if (lane == i && rows[i] < N) {
+                const float gf = (float)(bf16_t)tot[i], uf = (float)(bf16_t)tot[F + i];
+                p.y[16 * g + f0 + i] = (bf16_t)(gf * sigmoidf(gf) * uf);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < RW; i++) {
+            if (lane == i && rows[i] < N) {
+                float v = tot[i] + (p.bias ? (float)p.bias[rows[i]] : 0.f);
+                if (p.add) v = (float)(bf16_t)v + (float)p.add[rows[i]];  // the block's residual add, x + bf16(y)
+                p.y[rows[i]] = (bf16_t)v;
+            }
+        }
+    }
+}
+
+// The one-row form for a call: RW rows per wave, the most that still gives
+// 256 or more workgroups; D chunks per batch.
+template <int NM, bool SWIGLU, int D>
+static void launch_gemv(const LinearParams& p, hipStream_t stream) {
+    const auto wgs = [&](int rw) {
+        const long long waves = SWIGLU ? (long long)(p.N / 32) * (16 / (rw / 2)) : (p.N + rw - 1) / rw;
+        return (unsigned)((waves + 3) / 4);
+    };
+    const dim3 block(256);
+    if (SWIGLU || wgs(4) >= 256) {
+        hipLaunchKernelGGL((gemv_row_kernel<4, NM, SWIGLU, D>), dim3(wgs(4)), block, 0, stream, p);
+    } else if constexpr (!SWIGLU) {
+        if (wgs(2) >= 256)
+            hipLaunchKernelGGL((gemv_row_kernel<2, NM, false, D>), dim3(wgs(2)), block, 0, stream, p);
+        else
+            hipLaunchKernelGGL((gemv_row_kernel<1, NM, false, D>), dim3(wgs(1)), block, 0, stream, p);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Prefill gate path (layers/cyfa.py:292-295, 323-326, 349): the layer's
 // g_proj[0], a|b|d projections, gate activations and g_proj[1] for 64 token
 // rows per workgroup, 512 threads, in place of four launches that each read
@@ -922,6 +1070,27 @@ int launch_linear_rows(const LinearParams& p_in, hipStream_t stream) {
         p.ldx = p.ldr;
         p.norm_residual = nullptr;
         p.norm_sum_out = nullptr;
+    }
+    // one row: the streaming form (K = 256, g_proj[1]'s, stays on the tile
+    // kernel, whose summation order the decode kernel's in-kernel gate repeats)
+    if (p.M == 1 && p.K >= 512 && !p.norm_folded && (!p.swiglu || p.N % 32 == 0)) {
+        // one batch of chunks for every K up to 6144 (the norm's K <= 2048)
+        const bool short_k = p.K <= 4 * 512;
+        if (p.swiglu) {
+            if (norm)
+                launch_gemv<1, true, 4>(p, stream);
+            else if (short_k)
+                launch_gemv<0, true, 4>(p, stream);
+            else
+                launch_gemv<0, true, 12>(p, stream);
+        } else if (norm) {
+            launch_gemv<1, false, 4>(p, stream);
+        } else if (short_k) {
+            launch_gemv<0, false, 4>(p, stream);
+        } else {
+            launch_gemv<0, false, 12>(p, stream);
+        }
+        return 0;
     }
     int rt, ct;
     if (!linear_tile(p.M, p.N, p.swiglu != 0, norm ? p.K : 0, rt, ct)) return -1;

@@ -239,11 +239,15 @@ def test_graphed_decode_matches_eager(name, layers, B):
                                             (17, 256, 1024, False, 1024), (64, 1024, 256, True, 256),
                                             (33, 1024, 2816, False, 2816), (64, 32000, 1024, False, 1024),
                                             (5, 100, 64, True, 3 * 64), (64, 3340, 1024, True, 1024),
-                                            (64, 1024, 2816, False, 2816), (40, 5000, 512, True, 512)])
+                                            (64, 1024, 2816, False, 2816), (40, 5000, 512, True, 512),
+                                            (1, 32000, 2048, False, 2048), (1, 2048, 5632, True, 5632),
+                                            (1, 6424, 2048, True, 3 * 2048), (1, 300, 544, True, 544)])
 def test_linear_rows_kernel(M, N, K, bias, ldx):
     """cyfa_linear_rows against x W^T + b in float64: one bf16 rounding of an
     fp32 sum (bound: half a bf16 ulp of the result plus the fp32 summation
-    error, K 2^-24 sum |x||w|, with a factor of two to spare)."""
+    error, K 2^-24 sum |x||w|, with a factor of two to spare). The one-row
+    cases with K >= 512 run the streaming kernel with four, two and one W rows
+    per wave, K a whole number of its 512-element chunks or not."""
     from cyclic_flow_attention import _native
 
     gen = torch.Generator().manual_seed(M * N + K)
@@ -263,9 +267,11 @@ def test_linear_rows_kernel(M, N, K, bias, ldx):
 
 @pytest.mark.parametrize("N,K", [(32000, 1024), (3340, 1024), (5000, 512)])
 def test_linear_rows_tile_shape_does_not_change_bits(N, K):
-    """The launcher picks the workgroup tile per call (64 rows and 1 row get
+    """The launcher picks the workgroup tile per call (64 rows and 2 rows get
     different tiles at these N); every output is the same fixed-order sum in
-    any tile, so a row's result does not depend on the other rows."""
+    any tile, so a row's result does not depend on the other rows. (A single
+    row with K >= 512 takes the streaming one-row kernel, whose sums run in
+    another order; its accuracy is checked against float64 above.)"""
     from cyclic_flow_attention import _native
 
     gen = torch.Generator().manual_seed(N + K)
@@ -274,10 +280,10 @@ def test_linear_rows_tile_shape_does_not_change_bits(N, K):
     b = torch.randn(N, generator=gen).bfloat16().to(DEV)
     with torch.no_grad():
         full = _native.linear(x, w, b)
-        rows = [_native.linear(x[m:m + 1], w, b) for m in (0, 17, 63)]
+        rows = [_native.linear(x[m:m + 2], w, b) for m in (0, 17, 62)]
     torch.cuda.synchronize()
-    for m, y in zip((0, 17, 63), rows):
-        assert torch.equal(y[0], full[m]), f"row {m}"
+    for m, y in zip((0, 17, 62), rows):
+        assert torch.equal(y, full[m:m + 2]), f"rows {m}, {m + 1}"
 
 
 
@@ -302,7 +308,9 @@ def test_linear_rows_residual_add(M, N, K):
 
 @pytest.mark.parametrize("M,residual,swiglu,K", [(1, False, False, 1024), (37, True, False, 1024),
                                                  (64, True, False, 1024), (64, True, True, 1024),
-                                                 (5, True, True, 2048), (64, False, False, 512)])
+                                                 (5, True, True, 2048), (64, False, False, 512),
+                                                 (1, True, False, 2048), (1, True, True, 2048),
+                                                 (1, False, True, 1024)])
 def test_norm_linear_rows(M, residual, swiglu, K):
     """cyfa_norm_linear_rows (the pre-norm inside the projection): s equals the
     separate residual add bit for bit; y against the norm and the projection
