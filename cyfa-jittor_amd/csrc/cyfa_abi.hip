@@ -219,12 +219,14 @@ int decode_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* ly, void* hi
         }
         const long long bh = (long long)a->B * a->H;
         const int idle = cyfa::device_cu_count() - (int)(bh < 1 << 20 ? bh : 1 << 20);
-        if (pf_total && bh <= CYFA_PREFETCH_MAX_BH && !p.part && idle > 0) {
+        p.self_pf = bh <= cyfa::DECODE_SELF_PREFETCH_MAX_BH && !p.part && idle > 0;
+        if ((pf_total || p.self_pf) && bh <= CYFA_PREFETCH_MAX_BH && !p.part && idle > 0) {
             for (int r = 0; r < CYFA_PREFETCH_RANGES; r++) {
                 p.pf[r] = ly->prefetch[r];
                 p.pf_bytes[r] = ly->prefetch_bytes[r];
             }
-            const unsigned long long units = (pf_total + 16383) >> 14;  // 16 KiB per workgroup round
+            // every idle compute unit for the self-prefetch (each XCD gets its share)
+            const unsigned long long units = p.self_pf ? (unsigned long long)idle : (pf_total + 16383) >> 14;
             p.pf_wgs = (int)(units < (unsigned long long)idle ? units : (unsigned long long)idle);
         }
     }

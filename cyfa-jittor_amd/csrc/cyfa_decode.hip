@@ -533,6 +533,56 @@ __device__ __forceinline__ void prefetch_ranges(const DecodeParams& p, int wg, i
     }
 }
 
+// The step workgroups' own inputs, read by the extra workgroups into the L2
+// of the XCD each step workgroup runs on (workgroups are dealt to the eight
+// XCDs round-robin by block id: step workgroup bh on XCD bh mod 8, extra
+// workgroup q, block id B H + q, on XCD (B H + q) mod 8). A step workgroup
+// pulls about 450 KB through one compute unit, whose misses in flight bound
+// it to a small fraction of the chip's rate; from its XCD's L2 the same loads
+// return several times sooner. Per step workgroup, 28 units of 16 KiB in the
+// order the step reads them: hk (8), the head's table (4), hv (8), the head's
+// g_proj[1] rows (8); unit k of the XCD's j-th step workgroup is number
+// k m + j of the XCD's list (m step workgroups on the XCD), taken by its
+// extra workgroups in turn, eight units in flight. Loads past an input's end
+// or of a null input read zero.
+template <int K, int V>
+__device__ __forceinline__ void prefetch_own_inputs(const DecodeParams& p, int q, int nwg) {
+    constexpr int NU = 28;
+    const int BH = p.B * p.H, x = (BH + q) & 7;
+    const int m = x < BH ? (BH - x + 7) >> 3 : 0;  // step workgroups x, x + 8, .. on this XCD
+    const int qi = q >> 3, nx = (nwg - (q & 7) + 7) >> 3;
+    const int units = NU * m;
+#pragma unroll 1
+    for (int u0 = qi; u0 < units; u0 += 8 * nx) {
+        f32x4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int u = u0 + i * nx, k = u / (m > 0 ? m : 1), bh = x + 8 * (u - k * (m > 0 ? m : 1)), h = bh % p.H;
+            const char* base = nullptr;
+            size_t bytes = 0;
+            if (u < units) {
+                if (k < 8) {
+                    base = p.hk_in ? reinterpret_cast<const char*>(p.hk_in + (size_t)bh * K * kSlots) + (size_t)k * 16384 : nullptr;
+                    bytes = 16384;
+                } else if (k < 12) {
+                    base = reinterpret_cast<const char*>(p.table + (size_t)h * kActive * kSlots) + (size_t)(k - 8) * 16384;
+                    bytes = (size_t)kActive * kSlots * 4 - (size_t)(k - 8) * 16384;
+                } else if (k < 20) {
+                    base = p.hv_in ? reinterpret_cast<const char*>(p.hv_in + (size_t)bh * kSlots * V) + (size_t)(k - 12) * 16384 : nullptr;
+                    bytes = 16384;
+                } else {
+                    base = p.g1_w ? reinterpret_cast<const char*>(p.g1_w + (size_t)h * V * V) + (size_t)(k - 20) * 16384 : nullptr;
+                    bytes = 16384;
+                }
+            }
+            v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(buf(base, base ? bytes : 0),
+                                                                                    (uint32_t)threadIdx.x * 16u, 0, 0));
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) asm volatile("" ::"v"(v[i]));
+    }
+}
+
 // The one-workgroup form. LAYER: the layer's one-token step around the op in
 // the same kernel: q, k and v from the short convolution and the new conv
 // cache, the gate activations from the a|b|d row, and o through the gated
@@ -551,6 +601,7 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     constexpr int NW = NT / 64;
     constexpr int OJ = (V + 255) / 256;
     if (LAYER && (int)blockIdx.x >= p.B * p.H) {  // a prefetch workgroup (the whole workgroup exits here)
+        if (p.self_pf) prefetch_own_inputs<K, V>(p, (int)blockIdx.x - p.B * p.H, p.pf_wgs);
         prefetch_ranges(p, (int)blockIdx.x - p.B * p.H, p.pf_wgs);
         return;
     }

@@ -46,7 +46,16 @@ struct DecodeParams {
     const void* pf[4];
     unsigned long long pf_bytes[4];
     int pf_wgs;
+    // With pf_wgs > 0: the extra workgroups first read the step workgroups'
+    // own inputs (hk, hv, the head's table and g_proj[1] rows) into the L2 of
+    // the XCD each step workgroup runs on.
+    int self_pf;
 };
+
+// B H up to which the layer step's extra workgroups prefetch the step
+// workgroups' own inputs (each XCD's L2 then holds about 450 KB per step
+// workgroup dealt to it, 3.6 MB at 64).
+constexpr int DECODE_SELF_PREFETCH_MAX_BH = 64;
 
 // B H below which a decode step is split across eight workgroups per (b, h).
 constexpr int DECODE_SPLIT_BH = 64;

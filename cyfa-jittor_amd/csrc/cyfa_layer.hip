@@ -435,6 +435,15 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(LinearParams p) {
         const int k = 512 * c + 8 * lane;
         return ((uint32_t)k * 2) | (c < nch && k < K ? 0u : LIN_DEAD);
     };
+    // lane i < RW: the bias and the residual of row RW wave + i, loaded first
+    // (a null pointer gets an empty buffer: its loads read zero)
+    float bias_l = 0.f, add_l = 0.f;
+    if constexpr (!SWIGLU) {
+        const int r = RW * wave + lane;
+        const uint32_t off = ((uint32_t)r * 2) | (lane < RW && r < N ? 0u : LIN_DEAD);
+        bias_l = bf16_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(lin_rsrc(p.bias, p.bias ? (size_t)N * 2 : 0), off, 0, 0));
+        add_l = bf16_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(lin_rsrc(p.add, p.add ? (size_t)N * 2 : 0), off, 0, 0));
+    }
     float acc[RW];
 #pragma unroll
     for (int i = 0; i < RW; i++) acc[i] = 0.f;
@@ -507,8 +516,8 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(LinearParams p) {
 #pragma unroll
         for (int i = 0; i < RW; i++) {
             if (lane == i && rows[i] < N) {
-                float v = tot[i] + (p.bias ? (float)p.bias[rows[i]] : 0.f);
-                if (p.add) v = (float)(bf16_t)v + (float)p.add[rows[i]];  // the block's residual add, x + bf16(y)
+                float v = tot[i] + bias_l;
+                if (p.add) v = (float)(bf16_t)v + add_l;  // the block's residual add, x + bf16(y)
                 p.y[rows[i]] = (bf16_t)v;
             }
         }

@@ -204,14 +204,16 @@ typedef struct CyfaDecodeLayerArgs {
     long long g0_row;             /* a multiple of 8 */
     const void *g_weight;         /* bf16 [H 256, 256], 16-byte aligned */
     const void *g_bias;           /* nullable bf16 [H 256] */
-    /* Cache prefetch (no reference counterpart; all NULL / 0: none). At small
-       batches the step occupies one compute unit per (batch, head) and leaves
-       HBM almost idle; with B H <= CYFA_PREFETCH_MAX_BH the launch adds
-       workgroups on the idle compute units that read these device ranges --
-       the weights of the projections that follow the step -- into the
-       device's caches, so that those launches read them from the last-level
-       cache instead of HBM. The ranges are only read (16-byte aligned, each
-       below 4 GiB); no result depends on them. */
+    /* Cache prefetch (no reference counterpart; all NULL / 0: no ranges). At
+       small batches the step occupies one compute unit per (batch, head), and
+       one compute unit's loads reach a small fraction of HBM's rate. With
+       B H <= CYFA_PREFETCH_MAX_BH the launch adds workgroups on the idle
+       compute units: they first read each step workgroup's own state, readout
+       table and g_weight rows into the L2 of the XCD that runs it, then these
+       device ranges -- the weights of the projections that follow the step --
+       into the caches. The extra workgroups write nothing and no result
+       depends on them. The ranges are only read (16-byte aligned, each below
+       2^31 bytes). */
     const void *prefetch[CYFA_PREFETCH_RANGES];
     unsigned long long prefetch_bytes[CYFA_PREFETCH_RANGES];
 } CyfaDecodeLayerArgs;

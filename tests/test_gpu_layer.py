@@ -511,6 +511,49 @@ def test_decode_layer_step_prefetch_changes_nothing(B, H):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("B,H,big", [(1, 8, 16), (4, 4, 32), (16, 4, 32)])
+def test_decode_layer_step_small_batch_equals_rows_of_a_large_batch(B, H, big):
+    """At B H <= 64 the layer step launches extra workgroups that read every
+    step workgroup's state, table and g_proj[1] rows into its XCD's L2 ahead
+    of it; above 64 there are none. Each (batch, head) is computed alone in
+    either case, so the first B rows of a batch of `big` (B H > 64) equal the
+    same rows stepped as a batch of B, bit for bit: o', both states, the
+    clock and the conv cache, with the gate formed in the kernel."""
+    from cyclic_flow_attention import _native
+    from cyclic_flow_attention.ops.fused_recurrent import decode_layer_step
+
+    D = 3 * H * 256
+    gen = torch.Generator().manual_seed(300 + B + H)
+    qkv = torch.randn(big, 1, D, generator=gen).bfloat16().to(DEV)
+    cache = (0.5 * torch.randn(big, 3, D, generator=gen)).bfloat16().to(DEV)
+    wconv = (0.3 * torch.randn(D, 4, generator=gen)).bfloat16().to(DEV)
+    abd = torch.randn(big, 1, 3 * H, generator=gen).bfloat16().to(DEV)
+    dt_bias, A_log = torch.randn(H, generator=gen).to(DEV), torch.randn(H, generator=gen).to(DEV)
+    g0 = torch.randn(big, 1, 256, generator=gen).bfloat16().to(DEV)
+    g_w = (0.06 * torch.randn(H * 256, 256, generator=gen)).bfloat16().to(DEV)
+    g_b = (0.5 * torch.randn(H * 256, generator=gen)).bfloat16().to(DEV)
+    nw = (1 + 0.1 * torch.randn(256, generator=gen)).to(DEV)
+    qw, kw = (1 + 0.1 * torch.randn(256, generator=gen)).to(DEV), (1 + 0.1 * torch.randn(256, generator=gen)).to(DEV)
+    table = _native.readout_table((torch.eye(127).expand(H, 127, 127)
+                                   + 0.05 * torch.randn(H, 127, 127, generator=gen)).contiguous().to(DEV))
+    init = (0.3 * torch.randn(big, H, 256, 128, generator=gen).to(DEV),
+            0.3 * torch.randn(big, H, 128, 256, generator=gen).to(DEV), 50 * torch.rand(big, H, generator=gen).to(DEV))
+    outs = []
+    with torch.no_grad():
+        for n in (big, B):
+            tail = torch.empty(n, 3, D, dtype=torch.bfloat16, device=DEV)
+            o, st = decode_layer_step(qkv[:n], cache[:n], tail, wconv, abd[:n], dt_bias, A_log, None, nw, 1e-6, 127.0,
+                                      table, qw, kw, 1e-6, 1e-6, H,
+                                      initial_state=tuple(t[:n].clone() for t in init), output_final_state=True,
+                                      g_proj=(g0[:n], g_w, g_b))
+            outs.append((o, st, tail))
+    torch.cuda.synchronize()
+    (o0, st0, t0), (o1, st1, t1) = outs
+    assert torch.equal(o0[:B], o1) and torch.equal(t0[:B], t1)
+    for a, b in zip(st0, st1):
+        assert torch.equal(a[:B], b)
+
+
 def test_model_decode_prefetch_changes_nothing():
     """A 400M-shape model (2 layers) decoding at B=2: the decode steps with
     the layers' weight prefetch equal the steps without it, bit for bit."""
