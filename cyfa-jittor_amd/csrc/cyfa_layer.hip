@@ -394,7 +394,10 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
 // operand block and stages every byte of W through LDS; here each wave
 // streams RW rows of W from memory with 16-byte loads and forms the dot
 // products on v_dot2_f32_bf16. Lane l covers elements 512 c + 8 l .. + 7 of
-// chunk c. A batch of D chunks is issued at once, x first, then the norm
+// chunk c. W is read once, with the non-temporal hint, so that its stream does
+// not displace the cache lines other kernels are about to reuse (the decode
+// step's prefetched state and weights, x). A batch of D chunks is issued at
+// once, x first, then the norm
 // weight, then W, so that the norm waits for x alone while W streams in; D
 // is 4 for K <= 2048 (always with the norm) and 12 above, so every K up to
 // 6144 is one batch. Each row's sum runs over the chunks
@@ -465,7 +468,7 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(LinearParams p) {
         for (int d = 0; d < D; d++)
 #pragma unroll
             for (int i = 0; i < RW; i++)
-                wv[d][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw[i], piece(c0 + d), 0, 0));
+                wv[d][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw[i], piece(c0 + d), 0, 2));
         // every load of the batch is issued before any is used: without the
         // barrier the scheduler interleaves loads and uses to save registers
         // and keeps only a few loads in flight
