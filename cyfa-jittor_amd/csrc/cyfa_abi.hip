@@ -215,6 +215,10 @@ int decode_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* ly, void* hi
                             r, n);
             if (!aligned(ly->prefetch[r], 16))
                 return fail(CYFA_ERR_ALIGN, "cyfa_decode_layer_step: prefetch range %d needs 16-byte alignment", r);
+            const unsigned long long span = ly->prefetch_span[r];
+            if (span % 16 != 0 || span >= (1ull << 31))
+                return fail(CYFA_ERR_VALUE, "cyfa_decode_layer_step: prefetch range %d: span %llu (a multiple of 16 "
+                            "below 2^31)", r, span);
             pf_total += n;
         }
         const long long bh = (long long)a->B * a->H;
@@ -224,6 +228,7 @@ int decode_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* ly, void* hi
             for (int r = 0; r < CYFA_PREFETCH_RANGES; r++) {
                 p.pf[r] = ly->prefetch[r];
                 p.pf_bytes[r] = ly->prefetch_bytes[r];
+                p.pf_span[r] = ly->prefetch_span[r];
             }
             // every idle compute unit for the self-prefetch (each XCD gets its share)
             const unsigned long long units = p.self_pf ? (unsigned long long)idle : (pf_total + 16383) >> 14;
@@ -464,6 +469,10 @@ int cyfa_linear_rows(const CyfaLinearArgs* a, void* hip_stream) {
     if (cyfa::launch_linear_rows(p, (hipStream_t)hip_stream) != 0)
         return fail(CYFA_ERR_UNSUPPORTED, "cyfa_linear_rows: no tile for M=%d N=%d K=%d", a->M, a->N, a->K);
     return check_launch("cyfa_linear_rows");
+}
+
+size_t cyfa_linear_rows_span(int M, int N, int K, int swiglu, int norm) {
+    return norm < 0 || norm > 2 ? 0 : cyfa::linear_rows_span(M, N, K, swiglu != 0, norm);
 }
 
 int cyfa_norm_linear_rows(const CyfaLinearArgs* a, const CyfaRowNormArgs* n, void* hip_stream) {

@@ -505,27 +505,46 @@ __device__ __forceinline__ void qk_norms(const DecodeParams& p, float qv, float 
 }
 
 // The prefetch workgroups of the layer step (block ids B H onward, `nwg` of
-// them; this is number `wg`): the ranges p.pf[r] are read in units of 16 KiB
-// (one 16-byte load per thread), unit u by workgroup u mod nwg, eight units in
-// flight per workgroup, range after range, so that the first range is in the
-// caches first. The values are consumed by an empty asm statement (the loads
-// must not be dropped) and nothing is written. Loads past a range's end
-// return zero (the buffer's bounds).
+// them; this is number `wg`, on XCD (B H + wg) mod 8 as workgroups are dealt
+// to the XCDs round-robin by block id): the ranges p.pf[r], range after
+// range, so that the first range is in the caches first, eight 16 KiB units
+// (one 16-byte load per thread) in flight per workgroup. A range with a span
+// is read for its consumer: the consumer's workgroup c reads the span's bytes
+// [c span, (c + 1) span) on XCD c mod 8, so this workgroup reads, in 16 KiB
+// pieces, the spans of the consumer workgroups on its own XCD, which land in
+// that XCD's L2; a range without one is read in units u = wg, wg + nwg, ...
+// The values are consumed by an empty asm statement (the loads must not be
+// dropped) and nothing is written. Loads past a range's end or a span's end
+// read zero or are skipped (the dead offset).
 __device__ __forceinline__ void prefetch_ranges(const DecodeParams& p, int wg, int nwg) {
+    const int x = (p.B * p.H + wg) & 7, qi = wg >> 3, nx = (nwg - (wg & 7) + 7) >> 3;
 #pragma unroll 1
     for (int r = 0; r < 4; r++) {
         const unsigned long long bytes = p.pf_bytes[r];
         if (bytes == 0) continue;
-        const rsrc_t rs = buf(p.pf[r], (size_t)bytes);
-        const uint32_t units = (uint32_t)((bytes + 16383) >> 14);  // bytes < 2^31: no 32-bit overflow below
+        const rsrc_t rs = buf(p.pf[r], (size_t)bytes);  // bytes < 2^31: no 32-bit overflow below
+        const uint32_t span = (uint32_t)p.pf_span[r];
+        // units of this workgroup: u = first, first + stride, ... < units
+        const uint32_t cpc = (span + 16383) >> 14;  // 16 KiB pieces per consumer span
+        const uint32_t ncons = span ? (uint32_t)((bytes + span - 1) / span) : 0u;
+        const uint32_t mine = span ? ((uint32_t)x < ncons ? (ncons - (uint32_t)x + 7) >> 3 : 0u) : 0u;
+        const uint32_t units = span ? mine * cpc : (uint32_t)((bytes + 16383) >> 14);
+        const uint32_t first = span ? (uint32_t)qi : (uint32_t)wg, stride = span ? (uint32_t)nx : (uint32_t)nwg;
 #pragma unroll 1
-        for (uint32_t u0 = (uint32_t)wg; u0 < units; u0 += 8u * (uint32_t)nwg) {
+        for (uint32_t u0 = first; u0 < units; u0 += 8u * stride) {
             f32x4 v[8];
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                const uint32_t u = u0 + (uint32_t)i * (uint32_t)nwg;
-                const uint32_t off = (u << 14) + (uint32_t)threadIdx.x * 16u;
-                v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off | (u < units ? 0u : DEAD), 0, 0));
+                const uint32_t u = u0 + (uint32_t)i * stride;
+                uint32_t off, live = u < units;
+                if (span) {  // piece j of consumer x + 8 (u / cpc)
+                    const uint32_t c = (uint32_t)x + 8u * (u / cpc), in = (u % cpc) * 16384u + (uint32_t)threadIdx.x * 16u;
+                    off = c * span + in;
+                    live &= in < span;
+                } else {
+                    off = (u << 14) + (uint32_t)threadIdx.x * 16u;
+                }
+                v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off | (live ? 0u : DEAD), 0, 0));
             }
 #pragma unroll
             for (int i = 0; i < 8; i++) asm volatile("" ::"v"(v[i]));

@@ -45,6 +45,9 @@ struct DecodeParams {
     // 16-byte aligned; 0: none) into the caches and exit.
     const void* pf[4];
     unsigned long long pf_bytes[4];
+    // 0, or the bytes of range r each workgroup of its consumer reads (the
+    // consumer's workgroup c reads [c span, (c + 1) span), on XCD c mod 8)
+    unsigned long long pf_span[4];
     int pf_wgs;
     // With pf_wgs > 0: the extra workgroups first read the step workgroups'
     // own inputs (hk, hv, the head's table and g_proj[1] rows) into the L2 of
@@ -189,6 +192,11 @@ struct LinearParams {
 };
 
 constexpr int LINEAR_NORM_MAX_K = 2048;
+
+// Bytes of W each workgroup of launch_linear_rows reads at this shape when
+// workgroup c reads exactly W bytes [c span, (c + 1) span); 0 otherwise
+// (norm: 0 none, 1 with the norm weight, 2 folded).
+unsigned long long linear_rows_span(int M, int N, int K, bool swiglu, int norm);
 
 // The prefill gate path of a layer for rows of tokens x [M, K]:
 //   c = x [W_g0 | W_a | W_b | W_d]^T   (256 + 3H columns)

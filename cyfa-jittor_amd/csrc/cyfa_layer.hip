@@ -527,22 +527,38 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(LinearParams p) {
     }
 }
 
-// The one-row form for a call: RW rows per wave, the most that still gives
-// 256 or more workgroups; D chunks per batch.
+// Whether a call takes the one-row form: one row, K >= 512 (K = 256,
+// g_proj[1]'s, stays on the tile kernel, whose summation order the decode
+// kernel's in-kernel gate repeats), not the folded norm.
+static bool gemv_applies(int M, int N, int K, bool swiglu, bool folded) {
+    return M == 1 && K >= 512 && !folded && (!swiglu || N % 32 == 0);
+}
+
+// Workgroups of the one-row form with RW rows per wave (four waves each).
+static unsigned gemv_workgroups(int N, bool swiglu, int rw) {
+    const long long waves = swiglu ? (long long)(N / 32) * (16 / (rw / 2)) : (N + rw - 1) / rw;
+    return (unsigned)((waves + 3) / 4);
+}
+
+// RW for a call: the most rows per wave that still give 256 or more
+// workgroups (SwiGLU: always 4, a gate and an up pair per output pair).
+static int gemv_rows_per_wave(int N, bool swiglu) {
+    if (swiglu || gemv_workgroups(N, false, 4) >= 256) return 4;
+    return gemv_workgroups(N, false, 2) >= 256 ? 2 : 1;
+}
+
+// The one-row form for a call; D chunks per batch.
 template <int NM, bool SWIGLU, int D>
 static void launch_gemv(const LinearParams& p, hipStream_t stream) {
-    const auto wgs = [&](int rw) {
-        const long long waves = SWIGLU ? (long long)(p.N / 32) * (16 / (rw / 2)) : (p.N + rw - 1) / rw;
-        return (unsigned)((waves + 3) / 4);
-    };
-    const dim3 block(256);
-    if (SWIGLU || wgs(4) >= 256) {
-        hipLaunchKernelGGL((gemv_row_kernel<4, NM, SWIGLU, D>), dim3(wgs(4)), block, 0, stream, p);
+    const int rw = gemv_rows_per_wave(p.N, SWIGLU);
+    const dim3 grid(gemv_workgroups(p.N, SWIGLU, rw)), block(256);
+    if (rw == 4) {
+        hipLaunchKernelGGL((gemv_row_kernel<4, NM, SWIGLU, D>), grid, block, 0, stream, p);
     } else if constexpr (!SWIGLU) {
-        if (wgs(2) >= 256)
-            hipLaunchKernelGGL((gemv_row_kernel<2, NM, false, D>), dim3(wgs(2)), block, 0, stream, p);
+        if (rw == 2)
+            hipLaunchKernelGGL((gemv_row_kernel<2, NM, false, D>), grid, block, 0, stream, p);
         else
-            hipLaunchKernelGGL((gemv_row_kernel<1, NM, false, D>), dim3(wgs(1)), block, 0, stream, p);
+            hipLaunchKernelGGL((gemv_row_kernel<1, NM, false, D>), grid, block, 0, stream, p);
     }
 }
 
@@ -1063,6 +1079,17 @@ static bool linear_tile(int M, int N, bool swiglu, int norm_k, int& rt_out, int&
     return best >= 0;
 }
 
+unsigned long long linear_rows_span(int M, int N, int K, bool swiglu, int norm) {
+    if (M < 1 || M > 64 || N < 1 || K < 32 || K % 32 || (norm && K > LINEAR_NORM_MAX_K) || (swiglu && N % 32))
+        return 0;
+    if (gemv_applies(M, N, K, swiglu, norm == 2))  // wave w reads rows RW w ..; SwiGLU's rows come in pieces
+        return swiglu ? 0 : 4ull * gemv_rows_per_wave(N, false) * K * 2;
+    int rt, ct;
+    if (!linear_tile(M, N, swiglu, norm ? K : 0, rt, ct)) return 0;
+    // workgroup (x, y) reads W rows 16 ct x ..; with one row tile, workgroup c is (c, 0)
+    return (M + 16 * rt - 1) / (16 * rt) == 1 ? 16ull * ct * K * 2 : 0;
+}
+
 int launch_linear_rows(const LinearParams& p_in, hipStream_t stream) {
     LinearParams p = p_in;
     const bool norm = p.norm_weight != nullptr || p.norm_folded;
@@ -1083,9 +1110,7 @@ int launch_linear_rows(const LinearParams& p_in, hipStream_t stream) {
         p.norm_residual = nullptr;
         p.norm_sum_out = nullptr;
     }
-    // one row: the streaming form (K = 256, g_proj[1]'s, stays on the tile
-    // kernel, whose summation order the decode kernel's in-kernel gate repeats)
-    if (p.M == 1 && p.K >= 512 && !p.norm_folded && (!p.swiglu || p.N % 32 == 0)) {
+    if (gemv_applies(p.M, p.N, p.K, p.swiglu != 0, p.norm_folded != 0)) {
         // one batch of chunks for every K up to 6144 (the norm's K <= 2048)
         const bool short_k = p.K <= 4 * 512;
         if (p.swiglu) {

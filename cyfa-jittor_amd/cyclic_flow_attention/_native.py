@@ -14,7 +14,7 @@ import torch
 import torch.nn.functional as F
 
 LIB_PATH = Path(os.environ.get("CYFA_LIB", Path(__file__).with_name("libcyfa_hip.so")))
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 CYFA_OK = 0
 CYFA_ERR_VALUE = -1
@@ -93,6 +93,7 @@ class CyfaDecodeLayerArgs(ctypes.Structure):
         ("norm_weight", _c_void_p), ("norm_eps", _c_float), ("norm_prescale", _c_float),
         ("g0", _c_void_p), ("g0_row", ctypes.c_longlong), ("g_weight", _c_void_p), ("g_bias", _c_void_p),
         ("prefetch", _c_void_p * PREFETCH_RANGES), ("prefetch_bytes", ctypes.c_ulonglong * PREFETCH_RANGES),
+        ("prefetch_span", ctypes.c_ulonglong * PREFETCH_RANGES),
     ]
 
 
@@ -157,6 +158,7 @@ SIGNATURES = {
     "cyfa_rms_norm": (_c_int, [ctypes.POINTER(CyfaNormArgs), _c_void_p]),
     "cyfa_short_conv": (_c_int, [ctypes.POINTER(CyfaConvArgs), _c_void_p]),
     "cyfa_linear_rows": (_c_int, [ctypes.POINTER(CyfaLinearArgs), _c_void_p]),
+    "cyfa_linear_rows_span": (_c_size_t, [_c_int] * 5),
     "cyfa_norm_linear_rows": (_c_int, [ctypes.POINTER(CyfaLinearArgs), ctypes.POINTER(CyfaRowNormArgs), _c_void_p]),
     "cyfa_silu_mul": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "cyfa_argmax_rows": (_c_int, [_c_void_p, ctypes.c_longlong, _c_int, _c_int, _c_void_p, _c_void_p]),
@@ -475,6 +477,15 @@ def fold_norm_weight(weight, norm_weight):
     """bf16(weight diag(norm_weight)): a projection's weight with the RMS norm
     weight in front of it multiplied in, for norm_linear(norm_weight=None)."""
     return (weight.detach().float() * norm_weight.detach().float()).to(weight.dtype)
+
+
+def linear_rows_span(M, N, K, swiglu=False, norm=0):
+    """Bytes of the weight each workgroup of a linear / norm_linear launch with
+    M rows reads, when workgroup c reads the bytes [c span, (c + 1) span) and
+    no other workgroup reads them; 0 otherwise (cyfa_linear_rows_span; norm:
+    0 none, 1 with the norm weight, 2 folded). For decode_layer_step's
+    prefetch spans; no GPU needed."""
+    return int(load_library().cyfa_linear_rows_span(int(M), int(N), int(K), int(bool(swiglu)), int(norm)))
 
 
 def norm_linear(x, norm_weight, eps, weight, bias=None, residual=None, out_cols=None, swiglu=False):

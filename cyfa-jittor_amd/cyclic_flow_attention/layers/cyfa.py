@@ -37,11 +37,14 @@ from ..ops.utils import readout_table
 GATE_IN_KERNEL_MIN_WORKGROUPS = 128
 # Bytes of weights a small-batch decode step reads into the caches while its
 # decode kernel runs (prefetch_weights): ranges are taken in the order the
-# step reads them (g_proj[1]'s weight when the kernel forms the gate, o_proj,
-# then the caller's), skipping any that would pass the budget. Measured on
-# MI355X (graphed steps): the 400M model's o_proj, gate|up and down (19 MB)
-# gain 3% at B=1 and 6% at B=16; the 1.4B model's o_proj (8 MB) gains 1.4% at
-# B=1, while its 77 MB outlast the decode kernel and cost 2.5%.
+# step reads them (o_proj, then the caller's: the MLP's gate|up and down),
+# skipping any that would pass the budget; a weight whose projection reads
+# one contiguous span per workgroup goes with that span, and its pieces land
+# in the L2 of the XCD that reads them. Measured on MI355X (graphed steps):
+# the 400M model's o_proj, gate|up and down (19 MB) gain 3% at B=1 and 6% at
+# B=16; the 1.4B model's o_proj (8 MB) gains 1.4% at B=1 (2.7% once its
+# pieces go to the XCDs that read them), while its 77 MB outlast the decode
+# kernel and cost 2.5%.
 PREFETCH_BUDGET_BYTES = 24 << 20
 
 
@@ -429,10 +432,17 @@ class CyclicFlowAttention(nn.Module):
             pf = ()
             if small:
                 total = 0
-                for t in ((g1.weight,) if in_kernel else ()) + (self.o_proj.weight,) + tuple(prefetch):
+                # (the kernel's extra workgroups read g_proj[1]'s rows into the
+                # L2 of each step workgroup themselves); o_proj's weight with
+                # the span each of its workgroups reads, so that every piece
+                # lands in the L2 of the XCD that reads it
+                w_o = self.o_proj.weight
+                span_o = _native.linear_rows_span(B * T, w_o.shape[0], w_o.shape[1])
+                for item in ((w_o, span_o),) + tuple(prefetch):
+                    t = item[0] if isinstance(item, tuple) else item
                     n = t.numel() * t.element_size()
                     if total + n <= PREFETCH_BUDGET_BYTES and len(pf) < _native.PREFETCH_RANGES:
-                        pf, total = pf + (t,), total + n
+                        pf, total = pf + (item,), total + n
             o, state = decode_layer_step(
                 qkv, cat_cache, tail, wconv.reshape(-1, W).to(x.dtype), abd, self.dt_bias, self.A_log, gate,
                 self.o_norm.weight, self.o_norm.eps, float(self.num_slots - 1), self.readout_table(),

@@ -58,11 +58,17 @@ class GatedMLP(nn.Module):
 
     def step_weights(self, norm, x):
         """The weights a decode step of forward_block(x, norm) reads, in the
-        order it reads them (gate|up, then down); () when it runs elsewhere."""
+        order it reads them (gate|up, then down), each with the span each
+        workgroup of its projection reads (_native.linear_rows_span); () when
+        it runs elsewhere."""
         rows = x.numel() // x.shape[-1]
         if (inference_fast_path(x) and rows <= _native.LINEAR_ROWS_MAX and self.gate_proj.weight.shape[0] % 16 == 0
                 and x.shape[-1] % 32 == 0):
-            return self._step_gate_up(norm, x.shape[-1]), self.down_proj.weight
+            K = x.shape[-1]
+            w_gu, w_d = self._step_gate_up(norm, K), self.down_proj.weight
+            folded = self.fold_norm_weight and K <= _native.LINEAR_NORM_MAX_K
+            return ((w_gu, _native.linear_rows_span(rows, w_gu.shape[0], K, swiglu=True, norm=2 if folded else 1)),
+                    (w_d, _native.linear_rows_span(rows, w_d.shape[0], w_d.shape[1])))
         return ()
 
     def forward_block(self, x, norm):

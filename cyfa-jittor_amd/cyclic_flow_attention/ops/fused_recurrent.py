@@ -138,10 +138,13 @@ def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias
     [H 256, 256], bias [H 256] or None), and the kernel forms the gate as
     linear(g0, weight, bias) - the second projection of g_proj - with the same
     bits as _native.linear. ``prefetch``: up to four contiguous device tensors
-    (the weights of the projections that follow the step) that the launch
-    reads into the device's caches on the compute units the step leaves idle,
-    when B H <= _native.PREFETCH_MAX_BH and the one-workgroup form runs;
-    nothing depends on their values.
+    (the weights of the projections that follow the step), each alone or as
+    (tensor, span) with span from _native.linear_rows_span for the projection
+    that reads it, that the launch reads into the device's caches on the
+    compute units the step leaves idle, when B H <= _native.PREFETCH_MAX_BH
+    and the one-workgroup form runs (a tensor with a span lands in the L2 of
+    the XCD whose workgroup will read each piece); nothing depends on their
+    values.
     """
     B = qkv.shape[0]
     H, K, V, M = num_heads, 256, 256, table.shape[-1]
@@ -220,10 +223,12 @@ def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias
     )
     if len(prefetch) > _native.PREFETCH_RANGES:
         raise ValueError(f"decode_layer_step: at most {_native.PREFETCH_RANGES} prefetch tensors")
-    for i, t in enumerate(prefetch):
+    for i, item in enumerate(prefetch):
+        t, span = item if isinstance(item, tuple) else (item, 0)
         if not t.is_contiguous() or t.device != qkv.device:
             raise ValueError("decode_layer_step: prefetch tensors must be contiguous, on the step's device")
         layer.prefetch[i] = t.data_ptr()
         layer.prefetch_bytes[i] = t.numel() * t.element_size()
+        layer.prefetch_span[i] = int(span)
     _native.decode_layer_step(args, layer, dev)
     return o, ((hk_out, hv_out, c_out) if output_final_state else None)

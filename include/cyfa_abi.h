@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define CYFA_ABI_VERSION 9
+#define CYFA_ABI_VERSION 10
 
 enum {
     CYFA_OK = 0,
@@ -213,9 +213,14 @@ typedef struct CyfaDecodeLayerArgs {
        device ranges -- the weights of the projections that follow the step --
        into the caches. The extra workgroups write nothing and no result
        depends on them. The ranges are only read (16-byte aligned, each below
-       2^31 bytes). */
+       2^31 bytes). prefetch_span[r]: 0, or the bytes of range r that each
+       workgroup of the projection reading it takes, workgroup c the bytes
+       [c span, (c + 1) span) (cyfa_linear_rows_span); each piece is then read
+       into the L2 of the XCD that workgroup c runs on (workgroups are dealt
+       to the eight XCDs by block id, c mod 8). A multiple of 16 below 2^31. */
     const void *prefetch[CYFA_PREFETCH_RANGES];
     unsigned long long prefetch_bytes[CYFA_PREFETCH_RANGES];
+    unsigned long long prefetch_span[CYFA_PREFETCH_RANGES];
 } CyfaDecodeLayerArgs;
 
 /* cyfa_decode_step with the layer around it in the same kernel: q, k and v
@@ -371,6 +376,15 @@ typedef struct CyfaLinearArgs {
  * the lm_head (models/cyfa/modeling_cyfa.py:80, 100). fp32 accumulation, one bf16
  * rounding. */
 int cyfa_linear_rows(const CyfaLinearArgs *args, void *hip_stream);
+
+/* The bytes of the weight that each workgroup of a cyfa_linear_rows (norm 0)
+ * or cyfa_norm_linear_rows (norm 1: with the norm weight, 2: folded) launch
+ * of this shape reads, when workgroup c reads the bytes [c span, (c + 1) span)
+ * of the weight and no other workgroup reads them; 0 when the launch's
+ * workgroups share weight rows or read them in separate pieces, and for
+ * shapes the launchers refuse. A host-side query for
+ * CyfaDecodeLayerArgs.prefetch_span. No reference counterpart. */
+size_t cyfa_linear_rows_span(int M, int N, int K, int swiglu, int norm);
 
 /* The RMS norm in front of a projection (K <= 2048 columns):
  *   s  = residual ? bf16(x + residual) : x        (sum_out receives s)

@@ -326,3 +326,33 @@ def test_decode_layer_prefetch_ranges_validated_before_launch():
     assert lib.cyfa_decode_layer_step(ctypes.byref(a), ctypes.byref(ly), None) == _native.CYFA_ERR_ALIGN
     ly.prefetch[1], ly.prefetch_bytes[1] = 0x100000, 1 << 31  # too large for the kernel's 32-bit offsets
     assert lib.cyfa_decode_layer_step(ctypes.byref(a), ctypes.byref(ly), None) == _native.CYFA_ERR_VALUE
+    ly.prefetch_bytes[1], ly.prefetch_span[1] = 4096, 24  # a span must be a multiple of 16
+    assert lib.cyfa_decode_layer_step(ctypes.byref(a), ctypes.byref(ly), None) == _native.CYFA_ERR_VALUE
+    assert b"span" in lib.cyfa_last_error()
+
+
+def test_linear_rows_span_query():
+    """cyfa_linear_rows_span, the bytes of W each workgroup of a projection
+    launch reads when workgroup c reads exactly the bytes [c span, (c + 1)
+    span): the one-row kernel's waves take RW rows each (four waves per
+    workgroup, RW the most of 4, 2, 1 that keeps 256 or more workgroups), the
+    tile kernel's workgroup x the rows 16 CT x .. when M fits one row tile;
+    0 where workgroups share rows (several row tiles), read them in pieces
+    (SwiGLU's interleaved gate and up rows in the one-row kernel) or the
+    launchers refuse the shape."""
+    span = _native.linear_rows_span
+    assert span(1, 2048, 2048) == 4 * 2 * 2048 * 2     # o_proj of the 1.4B step: RW 2, 256 workgroups
+    assert span(1, 2048, 5632) == 4 * 2 * 5632 * 2     # down
+    assert span(1, 6424, 2048, norm=1) == 4 * 4 * 2048 * 2  # the input projection: RW 4, 402 workgroups
+    assert span(1, 1024, 1024) == 4 * 1 * 1024 * 2     # RW 1: 256 workgroups of 4 rows
+    assert span(1, 11264, 2048, swiglu=True, norm=1) == 0
+    assert span(1, 2048, 2048, norm=2) != 4 * 2 * 2048 * 2  # the folded norm stays on the tile kernel
+    g1 = span(1, 2048, 256)                             # K = 256: the tile kernel, one row tile
+    assert g1 > 0 and g1 % (16 * 256 * 2) == 0
+    assert span(64, 1024, 1024) == 0                    # 1 x 1 tiles: four row tiles read each W tile
+    assert span(64, 5632, 1024, swiglu=True, norm=1) == 16 * 2 * 1024 * 2  # 4 x 2 tiles
+    assert span(64, 32000, 1024) == 16 * 4 * 1024 * 2   # the lm_head's 4 x 4 tiles
+    for bad in ((0, 64, 64), (65, 64, 64), (1, 64, 48), (1, 0, 64)):
+        assert span(*bad) == 0
+    assert span(1, 64, 4096, norm=1) == 0 and span(1, 48, 64, swiglu=True) == 0
+    assert _native.load_library().cyfa_linear_rows_span(1, 2048, 2048, 0, 3) == 0

@@ -476,7 +476,9 @@ def test_decode_layer_step_prefetch_changes_nothing(B, H):
     """The layer step's cache prefetch (extra workgroups reading device ranges
     at B H <= 64; ignored above) leaves every output bit as it is: o', the
     states and the conv cache equal the step without it. The ranges have odd
-    sizes (a partial 16 KiB unit, a 16-byte one)."""
+    sizes (a partial 16 KiB unit, a 16-byte one), and two are read per
+    consumer span (one a whole number of 16 KiB pieces, one not, with a
+    partial last span)."""
     from cyclic_flow_attention import _native
     from cyclic_flow_attention.ops.fused_recurrent import decode_layer_step
 
@@ -498,7 +500,7 @@ def test_decode_layer_step_prefetch_changes_nothing(B, H):
               torch.randn(250_003, device=DEV), torch.randn(4, device=DEV))
     outs = []
     with torch.no_grad():
-        for pf in ((), tuple(r for r in ranges if r.numel())):
+        for pf in ((), ((ranges[0], 32768), (ranges[1], 90112), ranges[2])):
             tail = torch.empty(B, 3, D, dtype=torch.bfloat16, device=DEV)
             o, st = decode_layer_step(qkv, cache, tail, wconv, abd, dt_bias, A_log, gate, nw, 1e-6, 127.0, table, qw,
                                       kw, 1e-6, 1e-6, H, initial_state=tuple(t.clone() for t in init),
