@@ -222,7 +222,14 @@ int decode_step(const CyfaDecodeArgs* a, const CyfaDecodeLayerArgs* ly, void* hi
             pf_total += n;
         }
         const long long bh = (long long)a->B * a->H;
-        const int idle = cyfa::device_cu_count() - (int)(bh < 1 << 20 ? bh : 1 << 20);
+        // Several step workgroups per (b, h) at small batches, each storing its
+        // share: only with every output apart from its input (in place, one
+        // workgroup's stores could reach another's loads)
+        const bool apart = p.hk_out != p.hk_in && p.hv_out != p.hv_in && p.clock_out != p.clock_in &&
+                           (!p.cache_in || (const void*)p.cache_in != (const void*)p.cache_out);
+        p.wpb = apart && !p.part ? (bh <= cyfa::DECODE_WPB4_MAX_BH ? 4 : bh <= cyfa::DECODE_WPB2_MAX_BH ? 2 : 1) : 1;
+        const long long steps = bh * p.wpb;
+        const int idle = cyfa::device_cu_count() - (int)(steps < 1 << 20 ? steps : 1 << 20);
         p.self_pf = bh <= cyfa::DECODE_SELF_PREFETCH_MAX_BH && !p.part && idle > 0;
         if ((pf_total || p.self_pf) && bh <= CYFA_PREFETCH_MAX_BH && !p.part && idle > 0) {
             for (int r = 0; r < CYFA_PREFETCH_RANGES; r++) {

@@ -237,10 +237,12 @@ struct GateW {
     float bias;
 };
 
-__device__ __forceinline__ GateW load_gate_weights(const DecodeParams& p, int h) {
+// live false: the wave's rows read zero (another step workgroup of the
+// (b, h) forms those columns).
+__device__ __forceinline__ GateW load_gate_weights(const DecodeParams& p, int h, bool live = true) {
     constexpr int V = 256;
     const int lane = threadIdx.x & 63, c = threadIdx.x >> 6, lr = lane & 15, lg = lane >> 4;
-    const rsrc_t r = buf(p.g1_w ? p.g1_w + ((size_t)h * V + 16 * c) * V : nullptr, (size_t)16 * V * 2);
+    const rsrc_t r = buf(p.g1_w && live ? p.g1_w + ((size_t)h * V + 16 * c) * V : nullptr, (size_t)16 * V * 2);
     GateW g;
 #pragma unroll
     for (int st = 0; st < 8; st++)
@@ -296,8 +298,11 @@ __device__ __forceinline__ void write_vector_lds(float lam, float beta, float* s
 // vt is element (row 32 s + vt / 32 + 8 j, columns 4 (vt % 32) ..) of hk, i.e.
 // float4 index 1024 s + vt + 256 j. Updates and stores the four float4 and
 // accumulates the thread's partial raw in row order j.
+// With `out` set (several step workgroups per (b, h)) the float4 go through
+// that buffer resource instead, at a DEAD offset (dropped) unless `dead` is 0.
 __device__ __forceinline__ float4 key_slice_update(const float4 (&hk)[4], float4* hk_out, int s, int vt, float decay,
-                                                   const float* s_k, const float* s_q, const float* s_w) {
+                                                   const float* s_k, const float* s_q, const float* s_w,
+                                                   const rsrc_t* out = nullptr, uint32_t dead = 0) {
     const int m4 = (vt & 31) * 4;
     const float w0 = s_w[m4], w1 = s_w[m4 + 1], w2 = s_w[m4 + 2], w3 = s_w[m4 + 3];
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -310,7 +315,11 @@ __device__ __forceinline__ float4 key_slice_update(const float4 (&hk)[4], float4
         n.y = fmaf(n.y, decay, kd * w1);
         n.z = fmaf(n.z, decay, kd * w2);
         n.w = fmaf(n.w, decay, kd * w3);
-        stream_store(hk_out + 1024 * s + vt + 256 * j, n);
+        if (out)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(f32x4, n), *out,
+                                                   ((uint32_t)(1024 * s + vt + 256 * j) * 16) | dead, 0, 2);
+        else
+            stream_store(hk_out + 1024 * s + vt + 256 * j, n);
         a.x = fmaf(n.x, qd, a.x);
         a.y = fmaf(n.y, qd, a.y);
         a.z = fmaf(n.z, qd, a.z);
@@ -395,10 +404,11 @@ __device__ __forceinline__ void readout_1024(const float* s_raw, const float* s_
 // partials are summed in wave order. LAYER: the gated output norm
 // o_norm(o * prescale, gate) (layers/cyfa.py:349-350, as rms_norm_kernel<1>:
 // wave 0 holds four consecutive values per lane) before o is stored.
-template <int V, bool LAYER, bool F32 = false>
+// S step workgroups per (b, h): workgroup sp stores columns [sp V / S, (sp + 1) V / S).
+template <int V, bool LAYER, bool F32 = false, int S = 1>
 __device__ __forceinline__ void output_1024(const DecodeParams& p, int bh, const float4* hv_r, const float* s_om,
                                             float (*s_part)[256], float* s_v, const float4* on_w4,
-                                            const bf16x4* on_g4, const float* s_gate) {
+                                            const bf16x4* on_g4, const float* s_gate, int sp = 0) {
     constexpr int NT = 1024, VQ = V / 4, VROWS = NT / VQ, VJ = kSlots / VROWS;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     {
@@ -472,7 +482,7 @@ __device__ __forceinline__ void output_1024(const DecodeParams& p, int bh, const
                 const float gv = s_gate ? s_gate[d0 + i] : (float)g4[i];  // formed in the kernel, or given
                 y[i] = (bf16_t)(xs[j][i] * rs * wa[i] * sigmoidf(gv));
             }
-            *reinterpret_cast<bf16x4*>(p.o + (size_t)bh * V + d0) = y;
+            if (S == 1 || d0 * S / V == sp) *reinterpret_cast<bf16x4*>(p.o + (size_t)bh * V + d0) = y;
         }
     }
 }
@@ -505,7 +515,8 @@ __device__ __forceinline__ void qk_norms(const DecodeParams& p, float qv, float 
 }
 
 // The prefetch workgroups of the layer step (block ids B H onward, `nwg` of
-// them; this is number `wg`, on XCD (B H + wg) mod 8 as workgroups are dealt
+// them after the nstep step workgroups; this is number `wg`, on XCD
+// (nstep + wg) mod 8 as workgroups are dealt
 // to the XCDs round-robin by block id): the ranges p.pf[r], range after
 // range, so that the first range is in the caches first, eight 16 KiB units
 // (one 16-byte load per thread) in flight per workgroup. A range with a span
@@ -516,8 +527,8 @@ __device__ __forceinline__ void qk_norms(const DecodeParams& p, float qv, float 
 // The values are consumed by an empty asm statement (the loads must not be
 // dropped) and nothing is written. Loads past a range's end or a span's end
 // read zero or are skipped (the dead offset).
-__device__ __forceinline__ void prefetch_ranges(const DecodeParams& p, int wg, int nwg) {
-    const int x = (p.B * p.H + wg) & 7, qi = wg >> 3, nx = (nwg - (wg & 7) + 7) >> 3;
+__device__ __forceinline__ void prefetch_ranges(const DecodeParams& p, int wg, int nwg, int nstep) {
+    const int x = (nstep + wg) & 7, qi = wg >> 3, nx = (nwg - (wg & 7) + 7) >> 3;
 #pragma unroll 1
     for (int r = 0; r < 4; r++) {
         const unsigned long long bytes = p.pf_bytes[r];
@@ -554,21 +565,21 @@ __device__ __forceinline__ void prefetch_ranges(const DecodeParams& p, int wg, i
 
 // The step workgroups' own inputs, read by the extra workgroups into the L2
 // of the XCD each step workgroup runs on (workgroups are dealt to the eight
-// XCDs round-robin by block id: step workgroup bh on XCD bh mod 8, extra
-// workgroup q, block id B H + q, on XCD (B H + q) mod 8). A step workgroup
-// pulls about 450 KB through one compute unit, whose misses in flight bound
-// it to a small fraction of the chip's rate; from its XCD's L2 the same loads
-// return several times sooner. Per step workgroup, 28 units of 16 KiB in the
-// order the step reads them: hk (8), the head's table (4), hv (8), the head's
-// g_proj[1] rows (8); unit k of the XCD's j-th step workgroup is number
-// k m + j of the XCD's list (m step workgroups on the XCD), taken by its
-// extra workgroups in turn, eight units in flight. Loads past an input's end
-// or of a null input read zero.
+// XCDs round-robin by block id: step workgroup i on XCD i mod 8, extra
+// workgroup q on XCD (nstep + q) mod 8, nstep = B H S step workgroups, S per
+// (b, h); step workgroup i serves (b, h) = i mod B H, part i / B H). A step
+// workgroup pulls about 450 KB through one compute unit, whose memory
+// pipeline bounds it to a small fraction of the chip's rate; from its XCD's
+// L2 the loads return sooner. Per step workgroup, 20 + 8 / S units of 16 KiB
+// in the order the step reads them: hk (8), the head's table (4), hv (8), the
+// part's g_proj[1] rows (8 / S); unit k of the XCD's j-th step workgroup is
+// number k m + j of the XCD's list (m step workgroups on the XCD), taken by
+// its extra workgroups in turn, eight units in flight. Loads past an input's
+// end or of a null input read zero.
 template <int K, int V>
-__device__ __forceinline__ void prefetch_own_inputs(const DecodeParams& p, int q, int nwg) {
-    constexpr int NU = 28;
-    const int BH = p.B * p.H, x = (BH + q) & 7;
-    const int m = x < BH ? (BH - x + 7) >> 3 : 0;  // step workgroups x, x + 8, .. on this XCD
+__device__ __forceinline__ void prefetch_own_inputs(const DecodeParams& p, int q, int nwg, int S) {
+    const int BH = p.B * p.H, nstep = BH * S, NU = 20 + 8 / S, x = (nstep + q) & 7;
+    const int m = x < nstep ? (nstep - x + 7) >> 3 : 0;  // step workgroups x, x + 8, .. on this XCD
     const int qi = q >> 3, nx = (nwg - (q & 7) + 7) >> 3;
     const int units = NU * m;
 #pragma unroll 1
@@ -576,7 +587,8 @@ __device__ __forceinline__ void prefetch_own_inputs(const DecodeParams& p, int q
         f32x4 v[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const int u = u0 + i * nx, k = u / (m > 0 ? m : 1), bh = x + 8 * (u - k * (m > 0 ? m : 1)), h = bh % p.H;
+            const int u = u0 + i * nx, mm = m > 0 ? m : 1, k = u / mm, wi = x + 8 * (u - k * mm);
+            const int bh = wi % BH, part = wi / BH, h = bh % p.H;
             const char* base = nullptr;
             size_t bytes = 0;
             if (u < units) {
@@ -590,7 +602,9 @@ __device__ __forceinline__ void prefetch_own_inputs(const DecodeParams& p, int q
                     base = p.hv_in ? reinterpret_cast<const char*>(p.hv_in + (size_t)bh * kSlots * V) + (size_t)(k - 12) * 16384 : nullptr;
                     bytes = 16384;
                 } else {
-                    base = p.g1_w ? reinterpret_cast<const char*>(p.g1_w + (size_t)h * V * V) + (size_t)(k - 20) * 16384 : nullptr;
+                    base = p.g1_w ? reinterpret_cast<const char*>(p.g1_w + (size_t)h * V * V) +
+                                        (size_t)(part * 8 / S + k - 20) * 16384
+                                  : nullptr;
                     bytes = 16384;
                 }
             }
@@ -609,7 +623,11 @@ __device__ __forceinline__ void prefetch_own_inputs(const DecodeParams& p, int q
 // prologue (conv, gates, write vector, q/k norms) while the states stream in;
 // key-state update as hk arrives; the slot readout while hv arrives; then the
 // value-state update and o.
-template <int K, int V, bool LAYER, bool F32 = false>
+// S: step workgroups per (b, h) (LAYER only, outputs apart from inputs): each
+// computes the whole step and stores its share of hk' (slices), hv' (rows) and
+// o (columns, with the gate columns it forms); workgroup 0 of the (b, h) also
+// the conv cache and the clock.
+template <int K, int V, bool LAYER, bool F32 = false, int S = 1>
 __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     constexpr int NT = 1024;
     constexpr int NS = K / SLICE;   // key-state slices
@@ -619,12 +637,15 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     constexpr int VJ = kSlots / VROWS;
     constexpr int NW = NT / 64;
     constexpr int OJ = (V + 255) / 256;
-    if (LAYER && (int)blockIdx.x >= p.B * p.H) {  // a prefetch workgroup (the whole workgroup exits here)
-        if (p.self_pf) prefetch_own_inputs<K, V>(p, (int)blockIdx.x - p.B * p.H, p.pf_wgs);
-        prefetch_ranges(p, (int)blockIdx.x - p.B * p.H, p.pf_wgs);
+    static_assert(S == 1 || (LAYER && !F32 && K == 256 && V == 256), "several workgroups per (b, h): the layer step");
+    const int BH = p.B * p.H;
+    if (LAYER && (int)blockIdx.x >= BH * S) {  // a prefetch workgroup (the whole workgroup exits here)
+        if (p.self_pf) prefetch_own_inputs<K, V>(p, (int)blockIdx.x - BH * S, p.pf_wgs, S);
+        prefetch_ranges(p, (int)blockIdx.x - BH * S, p.pf_wgs, BH * S);
         return;
     }
-    const int bh = blockIdx.x, h = bh % p.H, b = bh / p.H, tid = threadIdx.x, vt = tid & 255;
+    const int bh = S == 1 ? (int)blockIdx.x : (int)blockIdx.x % BH, sp = S == 1 ? 0 : (int)blockIdx.x / BH;
+    const int h = bh % p.H, b = bh / p.H, tid = threadIdx.x, vt = tid & 255;
 
     __shared__ float s_q[K], s_k[K], s_w[kSlots], s_raw[kSlots], s_z[kSlots];
     __shared__ float s_p[kSlots], s_om[kSlots], s_c[kPairs], s_s[kPairs];
@@ -683,10 +704,10 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
         kv = conv_out(ck);
         vv = conv_out(cv);
         const rsrc_t co = conv_out_rows(p, b, 2 * p.H * K + p.H * V);
-        const uint32_t row = (uint32_t)p.cache_row * 2;
-        store_conv_cache(co, row, h * K + tid, dk, cq);
-        store_conv_cache(co, row, p.H * K + h * K + tid, dk, ck);
-        store_conv_cache(co, row, 2 * p.H * K + h * V + tid, dv, cv);
+        const uint32_t row = (uint32_t)p.cache_row * 2, sd = sp == 0 ? 0u : DEAD;
+        store_conv_cache(co, row, h * K + tid, dk | sd, cq);
+        store_conv_cache(co, row, p.H * K + h * K + tid, dk | sd, ck);
+        store_conv_cache(co, row, 2 * p.H * K + h * V + tid, dv | sd, cv);
     }
     s_v[tid] = vv;  // every thread: a store behind tid < V let the compiler sink cv's loads below the states'
     if (LAYER && tid < 32) s_g0[tid] = g0v;
@@ -698,7 +719,7 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     write_vector_lds<F32>(lam, beta_in, s_w, s_c, s_s);
     qk_norms<K, NW, F32>(p, qv, kv, qw, kw, s_red, s_q, s_k);
     __syncthreads();
-    if (tid == 0) p.clock_out[bh] = lam;  // after every thread has read clock_in
+    if (tid == 0 && sp == 0) p.clock_out[bh] = lam;  // after every thread has read clock_in
 
     // The value-state stream, float4 tid + NT j, issued once the small
     // inputs' registers are free; it is first needed after the readout.
@@ -707,11 +728,14 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
 #pragma unroll
     for (int j = 0; j < VJ; j++) hv_r[j] = stream_load(rv, (uint32_t)(tid + NT * j) * 16);
 
-    // Key state: hk' = alpha hk + k_hat (x) w ; raw = hk'^T q_hat, by slices.
+    // Key state: hk' = alpha hk + k_hat (x) w ; raw = hk'^T q_hat, by slices
+    // (with S > 1, slice s stored by part s S / NS).
+    const rsrc_t hk_o = buf(p.hk_out + (size_t)bh * K * kSlots, (size_t)K * kSlots * 4);
 #pragma unroll
     for (int r = 0; r < RK; r++) {
         const int s = (tid >> 8) + 4 * r;
-        const float4 a = key_slice_update(hk_r[r], hk_out, s, vt, decay, s_k, s_q, s_w);
+        const float4 a = key_slice_update(hk_r[r], hk_out, s, vt, decay, s_k, s_q, s_w, S == 1 ? nullptr : &hk_o,
+                                          s * S / NS == sp ? 0u : DEAD);
         float* pt = &s_kpart[s][vt >> 5][(vt & 31) * 4];
         pt[0] = a.x;
         pt[1] = a.y;
@@ -721,7 +745,7 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
     // the gate projection's weights (L2-resident), in the key state's registers;
     // issued with the value state they would not fit beside it
     GateW gw{};
-    if (LAYER) gw = load_gate_weights(p, h);
+    if (LAYER) gw = load_gate_weights(p, h, S == 1 || (int)(tid >> 6) * S / NW == sp);
     __syncthreads();
     if (tid < kSlots) {
         float r = slice_partial(&s_kpart[0][0][0], tid);
@@ -744,12 +768,18 @@ __global__ __launch_bounds__(1024) void decode_step_kernel(DecodeParams p) {
             n.y = fmaf(n.y, decay, wm * v1);
             n.z = fmaf(n.z, decay, wm * v2);
             n.w = fmaf(n.w, decay, wm * v3);
-            stream_store(hv_out + tid + NT * j, n);
+            if constexpr (S == 1) {
+                stream_store(hv_out + tid + NT * j, n);
+            } else {  // rows of sweep j stored by part j S / VJ
+                const rsrc_t hv_o = buf(p.hv_out + (size_t)bh * kSlots * V, (size_t)kSlots * V * 4);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(f32x4, n), hv_o,
+                                                       ((uint32_t)(tid + NT * j) * 16) | (j * S / VJ == sp ? 0u : DEAD), 0, 2);
+            }
             hv_r[j] = n;
         }
     }
     if (own_gate) gate_columns(s_g0, gw, s_gate);
-    output_1024<V, LAYER, F32>(p, bh, hv_r, s_om, s_part, s_v, on_w4, on_g4, own_gate ? s_gate : nullptr);
+    output_1024<V, LAYER, F32, S>(p, bh, hv_r, s_om, s_part, s_v, on_w4, on_g4, own_gate ? s_gate : nullptr, sp);
 }
 
 // Small-batch form, part A: grid (NSL, B H), 256 threads; workgroup s updates
@@ -925,9 +955,19 @@ void launch(const DecodeParams& p, hipStream_t stream) {
         hipLaunchKernelGGL((decode_split_a_kernel<K, V, LAYER>), dim3(NSL, BH), dim3(256), 0, stream, p);
         hipLaunchKernelGGL((decode_split_b_kernel<K, V, LAYER>), dim3(BH), dim3(1024), 0, stream, p);
     } else {
-        // the layer step's prefetch workgroups follow the B H step workgroups
+        // the layer step's prefetch workgroups follow the B H S step workgroups
         // (dispatched after them, so they take the idle compute units)
         const int extra = LAYER ? p.pf_wgs : 0;
+        if constexpr (LAYER && K == 256 && V == 256) {
+            if (p.wpb == 4) {
+                hipLaunchKernelGGL((decode_step_kernel<K, V, true, false, 4>), dim3(4 * BH + extra), dim3(1024), 0, stream, p);
+                return;
+            }
+            if (p.wpb == 2) {
+                hipLaunchKernelGGL((decode_step_kernel<K, V, true, false, 2>), dim3(2 * BH + extra), dim3(1024), 0, stream, p);
+                return;
+            }
+        }
         hipLaunchKernelGGL((decode_step_kernel<K, V, LAYER>), dim3(BH + extra), dim3(1024), 0, stream, p);
     }
 }

@@ -53,12 +53,20 @@ struct DecodeParams {
     // own inputs (hk, hv, the head's table and g_proj[1] rows) into the L2 of
     // the XCD each step workgroup runs on.
     int self_pf;
+    // Layer step, one-workgroup form: step workgroups per (b, h), 1, 2 or 4
+    // (more than one only with every output apart from its input: each
+    // workgroup reads all of the (b, h)'s inputs and stores its share).
+    int wpb;
 };
 
 // B H up to which the layer step's extra workgroups prefetch the step
 // workgroups' own inputs (each XCD's L2 then holds about 450 KB per step
 // workgroup dealt to it, 3.6 MB at 64).
 constexpr int DECODE_SELF_PREFETCH_MAX_BH = 64;
+// B H up to which the layer step runs 4 (2) step workgroups per (b, h) when
+// its outputs are apart from its inputs.
+constexpr int DECODE_WPB4_MAX_BH = 16;
+constexpr int DECODE_WPB2_MAX_BH = 32;
 
 // B H below which a decode step is split across eight workgroups per (b, h).
 constexpr int DECODE_SPLIT_BH = 64;

@@ -253,9 +253,14 @@ class CyclicFlowAttention(nn.Module):
         self.fold_prenorm_weight = False
         self._in_bias = FusedWeight()
         self._in_bias_zero = None
-        # When set, one-token steps update the cache's recurrent states in place
-        # (the graphed decode loop); otherwise new state tensors are returned.
+        # When set, one-token steps update the cache's recurrent states in place;
+        # otherwise new state tensors are returned.
         self.decode_in_place = False
+        # When set (a layer cache of the input's layout), one-token steps of the
+        # fused path write the new states and conv cache into it: the graphed
+        # decode loop alternates two caches, so that no step updates in place
+        # and the decode kernel can run several workgroups per (batch, head).
+        self.decode_next = None
         # Whether a one-token step forms the gate (g_proj[1]) inside the decode
         # kernel instead of a separate projection launch (same bits either way).
         # On MI355X it saves about 1.4% of the 400M step at B=64 (one launch per
@@ -405,8 +410,17 @@ class CyclicFlowAttention(nn.Module):
                 cat_cache = torch.cat([c.to(x.dtype) for c in conv_cache], dim=-1)
         # the new caches are channel slices of one buffer the conv kernel writes
         # (the cache itself when a graphed decode step updates in place)
-        in_place = self.decode_in_place and cat_cache is not None and T <= 32
-        tail = cat_cache if in_place else torch.empty(B, W - 1, qkv.shape[-1], dtype=x.dtype, device=x.device)
+        nxt = self.decode_next if cache is not None and T == 1 else None
+        nxt_conv = None if nxt is None else shared_conv_cache(nxt["conv_state"])
+        if nxt_conv is not None and (nxt_conv.dtype != x.dtype or tuple(nxt_conv.shape) != (B, W - 1, qkv.shape[-1])):
+            nxt_conv = None
+        in_place = self.decode_in_place and cat_cache is not None and T <= 32 and nxt is None
+        if in_place:
+            tail = cat_cache
+        elif nxt_conv is not None:
+            tail = nxt_conv
+        else:
+            tail = torch.empty(B, W - 1, qkv.shape[-1], dtype=x.dtype, device=x.device)
         wconv = self._conv_weight.get(self.q_conv1d.weight, self.k_conv1d.weight, self.v_conv1d.weight)
         if (not self.training and T == 1 and W == 4 and self.head_k_dim == 256 and self.head_v_dim == 256
                 and all(c.bias is None for c in (self.q_conv1d, self.k_conv1d, self.v_conv1d))
@@ -448,8 +462,9 @@ class CyclicFlowAttention(nn.Module):
                 self.o_norm.weight, self.o_norm.eps, float(self.num_slots - 1), self.readout_table(),
                 self.q_norm.weight, self.k_norm.weight, self.q_norm.eps, self.k_norm.eps, H,
                 initial_state=None if cache is None else cache["recurrent_state"], output_final_state=use_cache,
-                inplace=self.decode_in_place and cache is not None,
-                g_proj=(g0_out, g1.weight, g1.bias) if in_kernel else None, prefetch=pf)
+                inplace=self.decode_in_place and cache is not None and nxt is None,
+                g_proj=(g0_out, g1.weight, g1.bias) if in_kernel else None, prefetch=pf,
+                out_state=None if nxt is None else nxt["recurrent_state"])
             o = _native.linear(o.view(B, T, Dv), self.o_proj.weight, residual=block_in)
             cq, ck, cv = tail[..., :Dk], tail[..., Dk:2 * Dk], tail[..., 2 * Dk:]
             new_cache = {"recurrent_state": state, "conv_state": (cq, ck, cv)} if use_cache else None

@@ -248,15 +248,19 @@ def _clone_cache(c):
 
 
 class GraphedDecodeStep:
-    """One greedy decode step of the whole model, captured once as a HIP graph.
+    """One greedy decode step of the whole model, captured as HIP graphs.
 
-    The step reads the token buffer, runs every layer's one-token path (the
-    fused decode kernel updates each layer's recurrent state in place), writes
-    the conv histories back into the cache buffers, and stores the argmax token
-    in the token buffer for the next replay. ``step()`` replays it and returns
-    the token buffer [B, 1] (valid until the next replay). The reference runs
-    the same step as separate launches with a host sync per token
-    (generation.py:23-62).
+    A step reads the token buffer, runs every layer's one-token path, writes
+    the new recurrent states and conv histories, and stores the argmax token
+    in the token buffer for the next replay. Two caches alternate: the step
+    captured from cache 0 writes cache 1 and the other one back, so that no
+    decode kernel updates a state in place (which lets it run several
+    workgroups per (batch, head) at small batches; see decode_next on the
+    attention layer). ``step()`` replays the graph of the current parity and
+    returns the token buffer [B, 1] (valid until the next replay); ``cache``
+    is the cache the next step reads, ``logits`` the last step's logits. The
+    reference runs the same step as separate launches with a host sync per
+    token (generation.py:23-62).
     """
 
     def __init__(self, model, cache, tokens):
@@ -264,39 +268,58 @@ class GraphedDecodeStep:
             raise ValueError("graphed decoding needs the model and tokens on a GPU")
         self.model = model
         self.tokens = tokens.detach().clone()
-        self.cache = [_clone_cache(c) for c in cache]
+        first = [_clone_cache(c) for c in cache]
+        self._caches = (first, [_clone_cache(c) for c in first])
         layers = [blk.attn for blk in model.model.layers]
-        for attn in layers:
-            attn.decode_in_place = True
+        self.graphs, self._logits = [], []
         try:
-            # one eager step on a copy warms up library handles and kernel selection
-            scratch = [_clone_cache(c) for c in self.cache]
+            # one eager step on copies warms up library handles and kernel selection
+            scratch = [_clone_cache(c) for c in first]
+            for attn, nxt in zip(layers, [_clone_cache(c) for c in first]):
+                attn.decode_next = nxt
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(side):
                 model(self.tokens.clone(), cache=scratch, use_cache=True)
             torch.cuda.current_stream().wait_stream(side)
             del scratch
-            self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph):
-                out = model(self.tokens, cache=self.cache, use_cache=True)
-                for dst, src in zip(self.cache, out["cache"]):
-                    for a, b in zip(dst["recurrent_state"], src["recurrent_state"]):
-                        if a.data_ptr() != b.data_ptr():
-                            a.copy_(b)
-                    for a, b in zip(dst["conv_state"], src["conv_state"]):
-                        if a.data_ptr() != b.data_ptr():
-                            a.copy_(b)
-                self.logits = out["logits"]
-                last = out["logits"][:, -1:]
-                if inference_fast_path(last):
-                    _native.argmax_rows(last, out=self.tokens)  # straight into the token buffer
-                else:
-                    self.tokens.copy_(last.argmax(-1))
+            for parity in (0, 1):
+                src, dst = self._caches[parity], self._caches[1 - parity]
+                for attn, nxt in zip(layers, dst):
+                    attn.decode_next = nxt
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    out = model(self.tokens, cache=src, use_cache=True)
+                    for d, o in zip(dst, out["cache"]):  # layers off the fused path return new tensors
+                        for a, b in zip(d["recurrent_state"], o["recurrent_state"]):
+                            if a.data_ptr() != b.data_ptr():
+                                a.copy_(b)
+                        for a, b in zip(d["conv_state"], o["conv_state"]):
+                            if a.data_ptr() != b.data_ptr():
+                                a.copy_(b)
+                    last = out["logits"][:, -1:]
+                    if inference_fast_path(last):
+                        _native.argmax_rows(last, out=self.tokens)  # straight into the token buffer
+                    else:
+                        self.tokens.copy_(last.argmax(-1))
+                self.graphs.append(graph)
+                self._logits.append(out["logits"])
         finally:
             for attn in layers:
-                attn.decode_in_place = False
+                attn.decode_next = None
+        self._parity = 0
+
+    @property
+    def cache(self):
+        """The layer caches the next step reads."""
+        return self._caches[self._parity]
+
+    @property
+    def logits(self):
+        """The logits of the last step (valid until the next replay)."""
+        return self._logits[1 - self._parity]
 
     def step(self):
-        self.graph.replay()
+        self.graphs[self._parity].replay()
+        self._parity ^= 1
         return self.tokens

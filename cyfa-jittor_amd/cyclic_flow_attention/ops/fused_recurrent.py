@@ -124,7 +124,7 @@ def fused_recurrent_cyfa(
 def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias, A_log, gate, norm_weight, norm_eps,
                       norm_prescale, table, q_norm_weight, k_norm_weight, q_norm_eps, k_norm_eps, num_heads,
                       initial_state=None, output_final_state=False, inplace=False, split=False, g_proj=None,
-                      prefetch=()):
+                      prefetch=(), out_state=None):
     """The layer's one-token step around the op in one kernel (cyfa_decode_layer_step).
 
     qkv [B, 1, 3 H 256] is the projection before the short convolution (rows
@@ -144,7 +144,10 @@ def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias
     compute units the step leaves idle, when B H <= _native.PREFETCH_MAX_BH
     and the one-workgroup form runs (a tensor with a span lands in the L2 of
     the XCD whose workgroup will read each piece); nothing depends on their
-    values.
+    values. ``out_state``: (hk, hv, clock) tensors that receive the new
+    states (contiguous fp32, apart from the inputs) instead of new ones; with
+    every output apart from its input (the states and the conv cache) and
+    B H <= 32 the kernel runs several workgroups per (b, h), the same bits.
     """
     B = qkv.shape[0]
     H, K, V, M = num_heads, 256, 256, table.shape[-1]
@@ -197,7 +200,14 @@ def decode_layer_step(qkv, conv_cache, conv_cache_out, conv_weight, abd, dt_bias
             hk_in, hv_in, c_in = (x.to(torch.float32).contiguous() for x in (hk_in, hv_in, c_in))
     else:
         hk_in = hv_in = c_in = None
-    if inplace and initial_state is not None:
+    if out_state is not None:
+        hk_out, hv_out, c_out = out_state
+        if (tuple(hk_out.shape) != (B, H, K, M) or tuple(hv_out.shape) != (B, H, M, V) or tuple(c_out.shape) != (B, H)
+                or any(x.dtype != torch.float32 or not x.is_contiguous() or x.device != dev
+                       for x in (hk_out, hv_out, c_out))):
+            raise ValueError("decode_layer_step: out_state must be contiguous fp32 (hk [B,H,K,M], hv [B,H,M,V], "
+                             "clock [B,H]) on the step's device")
+    elif inplace and initial_state is not None:
         hk_out, hv_out, c_out = hk_in, hv_in, c_in
     else:
         hk_out = torch.empty(B, H, K, M, dtype=torch.float32, device=dev)

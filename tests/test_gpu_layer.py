@@ -556,6 +556,54 @@ def test_decode_layer_step_small_batch_equals_rows_of_a_large_batch(B, H, big):
         assert torch.equal(a[:B], b)
 
 
+@pytest.mark.parametrize("B,H,gate_in_kernel", [(1, 8, True), (1, 4, False), (2, 8, True), (3, 8, False),
+                                                 (8, 4, True), (2, 16, True)])
+def test_decode_layer_step_split_workgroups_equal_one(B, H, gate_in_kernel):
+    """With its outputs apart from its inputs and B H <= 32 the layer step runs
+    4 (B H <= 16) or 2 step workgroups per (b, h), each computing the whole
+    step and storing its share of hk', hv', o and (workgroup 0) the conv cache
+    and the clock; in place it runs one. Both give the same bits: o', both
+    states, the clock and the conv cache."""
+    from cyclic_flow_attention import _native
+    from cyclic_flow_attention.ops.fused_recurrent import decode_layer_step
+
+    D = 3 * H * 256
+    gen = torch.Generator().manual_seed(500 + 10 * B + H)
+    qkv = torch.randn(B, 1, D, generator=gen).bfloat16().to(DEV)
+    cache = (0.5 * torch.randn(B, 3, D, generator=gen)).bfloat16().to(DEV)
+    wconv = (0.3 * torch.randn(D, 4, generator=gen)).bfloat16().to(DEV)
+    abd = torch.randn(B, 1, 3 * H, generator=gen).bfloat16().to(DEV)
+    dt_bias, A_log = torch.randn(H, generator=gen).to(DEV), torch.randn(H, generator=gen).to(DEV)
+    nw = (1 + 0.1 * torch.randn(256, generator=gen)).to(DEV)
+    qw, kw = (1 + 0.1 * torch.randn(256, generator=gen)).to(DEV), (1 + 0.1 * torch.randn(256, generator=gen)).to(DEV)
+    table = _native.readout_table((torch.eye(127).expand(H, 127, 127)
+                                   + 0.05 * torch.randn(H, 127, 127, generator=gen)).contiguous().to(DEV))
+    init = (0.3 * torch.randn(B, H, 256, 128, generator=gen).to(DEV),
+            0.3 * torch.randn(B, H, 128, 256, generator=gen).to(DEV), 50 * torch.rand(B, H, generator=gen).to(DEV))
+    if gate_in_kernel:
+        gate, g_proj = None, (torch.randn(B, 1, 256, generator=gen).bfloat16().to(DEV),
+                              (0.06 * torch.randn(H * 256, 256, generator=gen)).bfloat16().to(DEV),
+                              (0.5 * torch.randn(H * 256, generator=gen)).bfloat16().to(DEV))
+    else:
+        gate, g_proj = torch.randn(B, 1, H * 256, generator=gen).bfloat16().to(DEV), None
+    outs = []
+    with torch.no_grad():
+        for inplace in (False, True):
+            tail = torch.empty(B, 3, D, dtype=torch.bfloat16, device=DEV)
+            st_in = tuple(t.clone() for t in init)
+            o, st = decode_layer_step(qkv, cache, tail, wconv, abd, dt_bias, A_log, gate, nw, 1e-6, 127.0, table, qw,
+                                      kw, 1e-6, 1e-6, H, initial_state=st_in, output_final_state=True,
+                                      inplace=inplace, g_proj=g_proj)
+            if inplace:
+                assert st[0].data_ptr() == st_in[0].data_ptr()
+            outs.append((o, st, tail))
+    torch.cuda.synchronize()
+    (o0, st0, t0), (o1, st1, t1) = outs
+    assert torch.equal(o0, o1) and torch.equal(t0, t1)
+    for a, b in zip(st0, st1):
+        assert torch.equal(a, b)
+
+
 def test_model_decode_prefetch_changes_nothing():
     """A 400M-shape model (2 layers) decoding at B=2: the decode steps with
     the layers' weight prefetch equal the steps without it, bit for bit."""
