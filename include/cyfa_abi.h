@@ -230,7 +230,11 @@ typedef struct CyfaDecodeLayerArgs {
  * output norm o_norm(o * prescale, gate) (layers/cyfa.py:349-350) instead of
  * o. args->q, k, v, g, delta and beta are not read. Replaces those steps of
  * CyclicFlowAttention.execute for a one-token step together with
- * fused_recurrent_cyfa (ops/fused_recurrent.py:10-200). */
+ * fused_recurrent_cyfa (ops/fused_recurrent.py:10-200). With every output
+ * apart from its input (hk, hv, clock and conv cache; no partial overlap)
+ * and B H <= 32 the launch runs 4 (B H <= 16) or 2 workgroups per (b, h),
+ * each computing the whole step and storing its share: the same bits as the
+ * one-workgroup form, which in-place calls keep. */
 int cyfa_decode_layer_step(const CyfaDecodeArgs *args, const CyfaDecodeLayerArgs *layer, void *hip_stream);
 
 /* table[h] = readout[h] @ Phi, with Phi the real-DFT slot basis [M-1, M].
