@@ -396,11 +396,13 @@ __global__ __launch_bounds__(512) void linear_rows_kernel(LinearParams p) {
 // products on v_dot2_f32_bf16. Lane l covers elements 512 c + 8 l .. + 7 of
 // chunk c. W is read once, with the non-temporal hint, so that its stream does
 // not displace the cache lines other kernels are about to reuse (the decode
-// step's prefetched state and weights, x). A batch of D chunks is issued at
-// once, x first, then the norm
-// weight, then W, so that the norm waits for x alone while W streams in; D
-// is 4 for K <= 2048 (always with the norm) and 12 above, so every K up to
-// 6144 is one batch. Each row's sum runs over the chunks
+// step's prefetched state and weights, x). The workgroup's four waves share
+// one copy of x (normalised with the norm) in LDS, so each compute unit's
+// memory pipeline carries x once per workgroup rather than once per wave.
+// Every load is issued at once, x first, then the norm weight, then all of W
+// (D chunks per row: 4 for K <= 2048, always with the norm, 12 up to K =
+// 6144), so that the norm waits for x alone while W streams in. Each row's
+// sum runs over the chunks
 // in order on the lane, then across the wave in wave_sum's fixed order: an
 // order other than linear_rows_kernel's, which can move an output across a
 // bf16 rounding boundary; every launch of a given shape takes the same path.
@@ -409,9 +411,12 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(LinearParams p) {
     static_assert(!SWIGLU || RW % 2 == 0, "SwiGLU pairs gate and up rows");
     static_assert(NM == 0 || D == 4, "the norm needs the whole row in one batch (K <= 2048)");
     constexpr int F = SWIGLU ? RW / 2 : RW;  // outputs per wave
-    const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int K = p.K, N = p.N, nch = (K + 511) / 512;
+    constexpr int XP = D / 4;                // x pieces of 8 elements per thread (K <= 512 D = 2048 XP)
+    __shared__ bf16x8 s_x[64 * D];           // the row (normalised with NM 1), piece e = elements 8 e ..
+    __shared__ float s_ss[4];
+    const int tid = threadIdx.x, lane = tid & 63, wl = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave = blockIdx.x * 4 + wl;
+    const int K = p.K, N = p.N, nch = (K + 511) / 512;  // nch <= D: one batch
     // this wave's W rows: SWIGLU, F gate rows 32 g + f0 .. and the matching up
     // rows 32 g + 16 + f0 .. of group g (16 outputs per group)
     int rows[RW];
@@ -447,62 +452,71 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(LinearParams p) {
         bias_l = bf16_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(lin_rsrc(p.bias, p.bias ? (size_t)N * 2 : 0), off, 0, 0));
         add_l = bf16_bits_to_float(__builtin_amdgcn_raw_buffer_load_b16(lin_rsrc(p.add, p.add ? (size_t)N * 2 : 0), off, 0, 0));
     }
+    // The workgroup's four waves share one copy of the row in LDS: thread t
+    // loads pieces t + 256 i (and their norm weights), then W is issued.
+    bf16x8 xp[XP];
+    float4 na[NM == 1 ? XP : 1], nb[NM == 1 ? XP : 1];
+#pragma unroll
+    for (int i = 0; i < XP; i++) {
+        const int e = tid + 256 * i;
+        const uint32_t dead = 8 * e < K ? 0u : LIN_DEAD;
+        xp[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rx, ((uint32_t)e * 16) | dead, 0, 0));
+        if constexpr (NM == 1) {
+            na[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rn, ((uint32_t)e * 32) | dead, 0, 0));
+            nb[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rn, ((uint32_t)e * 32 + 16) | dead, 0, 0));
+        }
+    }
+    u32x4 wv[D][RW];
+#pragma unroll
+    for (int d = 0; d < D; d++)
+#pragma unroll
+        for (int i = 0; i < RW; i++)
+            wv[d][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw[i], piece(d), 0, 2));
+    // every load is issued before any is used: without the barrier the
+    // scheduler interleaves loads and uses to save registers and keeps only a
+    // few loads in flight
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NM == 1) {
+        // rsqrt(mean x^2 + eps) over the row: each thread's pieces in order,
+        // the wave's lanes (wave_sum), then the four waves in order; then
+        // bf16(x rs w), as the separate norm rounds it
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < XP; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const bf16x2 x2 = {xp[i][2 * e], xp[i][2 * e + 1]};
+                ss = __builtin_amdgcn_fdot2_f32_bf16(x2, x2, ss, false);
+            }
+        ss = wave_sum(ss);
+        if (lane == 0) s_ss[wl] = ss;
+        __syncthreads();
+        const float rs = rsqrtf((((s_ss[0] + s_ss[1]) + s_ss[2]) + s_ss[3]) / (float)K + p.norm_eps);
+#pragma unroll
+        for (int i = 0; i < XP; i++) {
+            const float wn[8] = {na[i].x, na[i].y, na[i].z, na[i].w, nb[i].x, nb[i].y, nb[i].z, nb[i].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) xp[i][e] = (bf16_t)((float)xp[i][e] * rs * wn[e]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < XP; i++) s_x[tid + 256 * i] = xp[i];
+    __syncthreads();
     float acc[RW];
 #pragma unroll
     for (int i = 0; i < RW; i++) acc[i] = 0.f;
-    for (int c0 = 0; c0 < nch; c0 += D) {
-        bf16x8 xv[D];
-        float4 na[NM == 1 ? D : 1], nb[NM == 1 ? D : 1];
-        u32x4 wv[D][RW];
 #pragma unroll
-        for (int d = 0; d < D; d++) xv[d] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rx, piece(c0 + d), 0, 0));
-        if constexpr (NM == 1) {  // the norm weight's 8 floats: the same piece at twice the offset
+    for (int d = 0; d < D; d++) {
+        const bf16x8 xs = s_x[64 * d + lane];
 #pragma unroll
-            for (int d = 0; d < D; d++) {
-                const uint32_t off = piece(c0 + d), o2 = (off & ~LIN_DEAD) * 2 | (off & LIN_DEAD);
-                na[d] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rn, o2, 0, 0));
-                nb[d] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rn, o2 + 16, 0, 0));
+        for (int i = 0; i < RW; i++) {
+            const bf16x8 wr = __builtin_bit_cast(bf16x8, wv[d][i]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const bf16x2 a2 = {xs[2 * e], xs[2 * e + 1]}, b2 = {wr[2 * e], wr[2 * e + 1]};
+                acc[i] = __builtin_amdgcn_fdot2_f32_bf16(a2, b2, acc[i], false);
             }
         }
-#pragma unroll
-        for (int d = 0; d < D; d++)
-#pragma unroll
-            for (int i = 0; i < RW; i++)
-                wv[d][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw[i], piece(c0 + d), 0, 2));
-        // every load of the batch is issued before any is used: without the
-        // barrier the scheduler interleaves loads and uses to save registers
-        // and keeps only a few loads in flight
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (NM == 1) {
-            // rsqrt(mean x^2 + eps) over the whole row (one batch), on every
-            // wave; then bf16(x rs w), as the separate norm rounds it
-            float ss = 0.f;
-#pragma unroll
-            for (int d = 0; d < D; d++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const bf16x2 x2 = {xv[d][2 * e], xv[d][2 * e + 1]};
-                    ss = __builtin_amdgcn_fdot2_f32_bf16(x2, x2, ss, false);
-                }
-            const float rs = rsqrtf(wave_sum(ss) / (float)K + p.norm_eps);
-#pragma unroll
-            for (int d = 0; d < D; d++) {
-                const float wn[8] = {na[d].x, na[d].y, na[d].z, na[d].w, nb[d].x, nb[d].y, nb[d].z, nb[d].w};
-#pragma unroll
-                for (int e = 0; e < 8; e++) xv[d][e] = (bf16_t)((float)xv[d][e] * rs * wn[e]);
-            }
-        }
-#pragma unroll
-        for (int d = 0; d < D; d++)
-#pragma unroll
-            for (int i = 0; i < RW; i++) {
-                const bf16x8 wr = __builtin_bit_cast(bf16x8, wv[d][i]);
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const bf16x2 a2 = {xv[d][2 * e], xv[d][2 * e + 1]}, b2 = {wr[2 * e], wr[2 * e + 1]};
-                    acc[i] = __builtin_amdgcn_fdot2_f32_bf16(a2, b2, acc[i], false);
-                }
-            }
     }
     float tot[RW];
 #pragma unroll
@@ -527,11 +541,11 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(LinearParams p) {
     }
 }
 
-// Whether a call takes the one-row form: one row, K >= 512 (K = 256,
+// Whether a call takes the one-row form: one row, 512 <= K <= 6144 (K = 256,
 // g_proj[1]'s, stays on the tile kernel, whose summation order the decode
 // kernel's in-kernel gate repeats), not the folded norm.
 static bool gemv_applies(int M, int N, int K, bool swiglu, bool folded) {
-    return M == 1 && K >= 512 && !folded && (!swiglu || N % 32 == 0);
+    return M == 1 && K >= 512 && K <= 12 * 512 && !folded && (!swiglu || N % 32 == 0);
 }
 
 // Workgroups of the one-row form with RW rows per wave (four waves each).
