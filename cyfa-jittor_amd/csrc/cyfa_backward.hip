@@ -594,7 +594,8 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
 
 // The slot readout for blocks of 32 rows of one head: z = U(lam) raw,
 // l = z table^T, p = softmax(l), u = p table, weights = U(-lam) u; the two
-// products as small GEMMs against the staged table (4 x 4 per thread). BF
+// products as small GEMMs against the staged table on the fp32 matrix cores
+// (mfma4 below). BF
 // rounds z, the table, p and the weights to bf16 (the general forward's casts
 // to a bf16 input dtype, ops/utils.py:779-882); the backward's recompute is
 // unrounded. Grid (ceil(B Tp / (32 per_wg)), H), 256 threads: a workgroup
@@ -607,22 +608,36 @@ __device__ __forceinline__ float bw_rnd(float x) {
         return x;
 }
 
+constexpr int RO_LD = BWD_TABLE_M + 4;  // staged table and row rows, 16-byte aligned
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+// v_mfma_f32_16x16x4_f32 (fp32 operands, fp32 accumulation): lane l holds
+// A[l % 16][l / 16] and B[l / 16][l % 16] of a 16 x 4 by 4 x 16 step and rows
+// 4 (l / 16) .. + 3 of column l % 16 of the 16 x 16 result.
+__device__ __forceinline__ f32x4v mfma4(float a, float b, f32x4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 template <bool BF>
 __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, const float* cs, const float* sn,
                                                              const float* table, int B, int Tp, int H, int M,
                                                              int per_wg, float* wts) {
-    constexpr int TM = BWD_TABLE_M, LD = TM + 1, RB = 32;
-    __shared__ float sTab[TM * LD];  // rows R .. 127 zero
+    constexpr int TM = BWD_TABLE_M, LD = RO_LD, RB = 32;
+    static_assert(TM == 128, "eight 16-wide tiles of slots");
+    __shared__ float sTab[TM * LD];  // rows R .. 127 and columns M .. 127 zero
     __shared__ float sZ[RB][LD], sP[RB][LD];
     __shared__ float sCs[RB][TM / 2], sSn[RB][TM / 2];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, h = blockIdx.y;
+    const int lr = lane & 15, lk = lane >> 4;
     const int R = M - 1, P = M / 2, rows = B * Tp;
     for (int e = tid; e < TM * LD; e += 256) {
         const int r = e / LD, m = e % LD;
         sTab[e] = (r < R && m < M) ? bw_rnd<BF>(table[((size_t)h * R + r) * M + m]) : 0.f;
     }
     const auto row_of = [&](int rho) { return ((size_t)(rho / Tp) * H + h) * Tp + rho % Tp; };
-    const int br = 4 * (tid >> 5), bc = 4 * (tid & 31);
+    // wave wv: row tile it = wv & 1, column tiles 4 (wv >> 1) .. + 3 (of r, then of m)
+    const int it = wv & 1, ct0 = 4 * (wv >> 1);
     for (int b0 = blockIdx.x * per_wg * RB; b0 < min(rows, (blockIdx.x + 1) * per_wg * RB); b0 += RB) {
         __syncthreads();  // the table is staged; the previous block's tiles are done with
         for (int e = tid; e < RB * (TM / 2); e += 256) {
@@ -642,24 +657,19 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
             sZ[i][2 * pr + 1] = zo;
         }
         __syncthreads();
-        {
-            float l[4][4] = {};
-            for (int m = 0; m < M; m++) {
-                float zv[4], tv[4];
+        {  // logits l[i][r] = sum_m z[i][m] table[r][m]
+            f32x4v acc[4];
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    zv[i] = sZ[br + i][m];
-                    tv[i] = sTab[(bc + i) * LD + m];
-                }
+            for (int t = 0; t < 4; t++) acc[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+            for (int k0 = 0; k0 < TM; k0 += 4) {
+                const float az = sZ[16 * it + lr][k0 + lk];
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++) l[i][j] = fmaf(zv[i], tv[j], l[i][j]);
+                for (int t = 0; t < 4; t++) acc[t] = mfma4(az, sTab[(16 * (ct0 + t) + lr) * LD + k0 + lk], acc[t]);
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int t = 0; t < 4; t++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) sP[br + i][bc + j] = l[i][j];
+                for (int q = 0; q < 4; q++) sP[16 * it + 4 * lk + q][16 * (ct0 + t) + lr] = acc[t][q];
         }
         __syncthreads();
         for (int i = wv; i < RB; i += 4) {
@@ -671,31 +681,29 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
             sP[i][lane + 64] = bw_rnd<BF>(e1 * inv);
         }
         __syncthreads();
-        float u[4][4] = {};
-        for (int r = 0; r < R; r++) {
-            float pv[4], t4[4];
+        // u[i][m] = sum_r p[i][r] table[r][m] (p and the table zero at r >= R); the
+        // weights' pair (2 pr, 2 pr + 1) sits in lanes (lr, lr ^ 1), swapped in by
+        // quad_perm [1,0,3,2]
+        f32x4v acc[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                pv[i] = sP[br + i][r];
-                t4[i] = sTab[r * LD + bc + i];
-            }
+        for (int t = 0; t < 4; t++) acc[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+        for (int k0 = 0; k0 < TM; k0 += 4) {
+            const float ap = sP[16 * it + lr][k0 + lk];
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) u[i][j] = fmaf(pv[i], t4[j], u[i][j]);
+            for (int t = 0; t < 4; t++) acc[t] = mfma4(ap, sTab[(k0 + lk) * LD + 16 * (ct0 + t) + lr], acc[t]);
         }
+        const bool odd = (lr & 1) != 0;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int rho = b0 + br + i;
-            if (rho >= rows) continue;
-            const size_t row = row_of(rho);
+        for (int t = 0; t < 4; t++) {
+            const int m = 16 * (ct0 + t) + lr, pr = m >> 1;
 #pragma unroll
-            for (int j = 0; j < 4; j += 2) {
-                const int pr = (bc + j) >> 1;
-                if (pr < P) {
-                    const float c = sCs[br + i][pr], s = sSn[br + i][pr];
-                    wts[row * M + 2 * pr] = bw_rnd<BF>(c * u[i][j] + s * u[i][j + 1]);
-                    wts[row * M + 2 * pr + 1] = bw_rnd<BF>(-s * u[i][j] + c * u[i][j + 1]);
+            for (int q = 0; q < 4; q++) {
+                const float un = acc[t][q], ux = dpp_mov<0xB1>(un);
+                const float ue = odd ? ux : un, uo = odd ? un : ux;
+                const int i = 16 * it + 4 * lk + q, rho = b0 + i;
+                if (rho < rows && pr < P) {
+                    const float c = sCs[i][pr], s = sSn[i][pr];
+                    wts[row_of(rho) * M + m] = bw_rnd<BF>(odd ? -s * ue + c * uo : c * ue + s * uo);
                 }
             }
         }
@@ -708,11 +716,14 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
 //   draw = U(-lam) dz, dtable += p du^T + dl z^T, and the clock's share
 //   dlam = sum_p kappa_p [dz . dU(lam)/dlam raw + dweights . dU(-lam)/dlam u]
 // with kappa_p = 2 pi p / (M - 1). Every product over the block is a small
-// GEMM against the head's table (staged once in LDS, rows padded by one
-// float against bank conflicts); a thread forms 4 x 4 output blocks. Grid
-// (workgroups per head, H), 256 threads: a workgroup takes per_wg blocks of
-// 32 rows (bwd_ro_per_wg) and keeps its part of dtable in registers (thread e
-// owns the 4 x 16 block of rows 4 (e / 8) .., columns 16 (e % 8) ..).
+// GEMM against the head's table (staged once in LDS, rows RO_LD floats apart)
+// on the fp32 matrix cores, v_mfma_f32_16x16x4_f32 (fp32 operands, fp32
+// accumulation): lane l holds A[l % 16][l / 16] and B[l / 16][l % 16] of a
+// 16 x 4 by 4 x 16 step and rows 4 (l / 16) .. + 3 of column l % 16 of the
+// 16 x 16 result. Grid (workgroups per head, H), 256 threads: a workgroup
+// takes per_wg blocks of 32 rows (bwd_ro_per_wg) and keeps its part of dtable
+// in the accumulators (wave w owns its 16 x 16 tiles (r, m) of columns
+// m in 32 w .. 32 w + 31).
 constexpr int RO_BLK = BWD_RO_BLOCK;
 struct ReadoutGradArgs {
     const float *raw, *cs, *sn, *table, *dwts;  // head-major rows; table [H, M-1, M]
@@ -722,22 +733,25 @@ struct ReadoutGradArgs {
 };
 
 __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
-    constexpr int TM = BWD_TABLE_M, LD = TM + 1;
-    __shared__ float sTab[TM * LD];  // rows R .. 127 zero
+    constexpr int TM = BWD_TABLE_M, LD = RO_LD;
+    static_assert(RO_BLK == 32 && TM == 128, "two 16-row tiles of rows, eight 16-wide tiles of slots");
+    __shared__ float sTab[TM * LD];  // rows R .. 127 and columns M .. 127 zero
     __shared__ float sZ[RO_BLK][LD], sDU[RO_BLK][LD], sP[RO_BLK][LD], sDL[RO_BLK][LD];
     __shared__ float sCs[RO_BLK][TM / 2], sSn[RO_BLK][TM / 2];
-    __shared__ float sLam[RO_BLK][32];
+    __shared__ float sLam[RO_BLK][2];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, blk = blockIdx.x, h = blockIdx.y;
+    const int lr = lane & 15, lk = lane >> 4;  // operand row / column and k of this lane
     const int M = a.M, R = M - 1, P = M / 2, RM = R * M;
     for (int e = tid; e < TM * LD; e += 256) {  // the table, zero beyond R x M
         const int r = e / LD, m = e % LD;
         sTab[e] = (r < R && m < M) ? a.table[((size_t)h * R + r) * M + m] : 0.f;
     }
-    // 4 x 4 blocks over (row, column): rows 4 (tid / 32) .., columns 4 (tid % 32) ..
-    const int br = 4 * (tid >> 5), bc = 4 * (tid & 31);
-    // dtable block: table rows 4 (tid / 8) .. + 4, columns 16 (tid % 8) .. + 16
-    const int tr = 4 * (tid >> 3), tc = 16 * (tid & 7);
-    float dt[4][16] = {};
+    // GEMMs over the block: wave wv takes row tile it = wv & 1 and the column
+    // tiles 4 (wv >> 1) .. + 3 of the logits (r) and of dz, u (m)
+    const int it = wv & 1, ct0 = 4 * (wv >> 1);
+    f32x4v dacc[8][2];  // dtable tiles (r tile, m tile 2 wv + mt)
+#pragma unroll
+    for (int rt = 0; rt < 8; rt++) dacc[rt][0] = dacc[rt][1] = f32x4v{0.f, 0.f, 0.f, 0.f};
     const int rows = a.B * a.Tp;
     for (int b0 = blk * a.per_wg * RO_BLK; b0 < min(rows, (blk + 1) * a.per_wg * RO_BLK); b0 += RO_BLK) {
         __syncthreads();  // the previous block's tiles are done with
@@ -764,31 +778,26 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
             sDU[i][2 * pr + 1] = uo;
         }
         __syncthreads();
-        // logits l = z table^T and dp = du table^T (into sP, sDL)
+        // logits l[i][r] = sum_m z[i][m] table[r][m] and dp[i][r] = sum_m du[i][m] table[r][m]
         {
-            float l[4][4] = {}, d[4][4] = {};
-            for (int m = 0; m < M; m++) {
-                float zv[4], uv[4], tv[4];
+            f32x4v accl[4], accd[4];
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    zv[i] = sZ[br + i][m];
-                    uv[i] = sDU[br + i][m];
-                    tv[i] = sTab[(bc + i) * LD + m];
+            for (int t = 0; t < 4; t++) accl[t] = accd[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+            for (int k0 = 0; k0 < TM; k0 += 4) {
+                const float az = sZ[16 * it + lr][k0 + lk], ad = sDU[16 * it + lr][k0 + lk];
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const float bt = sTab[(16 * (ct0 + t) + lr) * LD + k0 + lk];
+                    accl[t] = mfma4(az, bt, accl[t]);
+                    accd[t] = mfma4(ad, bt, accd[t]);
                 }
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        l[i][j] = fmaf(zv[i], tv[j], l[i][j]);
-                        d[i][j] = fmaf(uv[i], tv[j], d[i][j]);
-                    }
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int t = 0; t < 4; t++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    sP[br + i][bc + j] = l[i][j];
-                    sDL[br + i][bc + j] = d[i][j];
+                for (int q = 0; q < 4; q++) {
+                    sP[16 * it + 4 * lk + q][16 * (ct0 + t) + lr] = accl[t][q];
+                    sDL[16 * it + 4 * lk + q][16 * (ct0 + t) + lr] = accd[t][q];
                 }
         }
         __syncthreads();
@@ -807,83 +816,93 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
             sDL[i][lane + 64] = p1 * (d1 - pdp);
         }
         __syncthreads();
-        // dz = dl table and u = p table: rows br .., columns (m) bc ..; then draw and the clock's share
+        // dz[i][m] = sum_r dl[i][r] table[r][m] and u[i][m] = sum_r p[i][r] table[r][m]
+        // (p and dl are zero at r >= R, as is the table); then draw and the clock's share
         {
-            float dz[4][4] = {}, u[4][4] = {};
-            for (int r = 0; r < R; r++) {
-                float lv[4], pv[4];
+            f32x4v accz[4], accu[4];
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    lv[i] = sDL[br + i][r];
-                    pv[i] = sP[br + i][r];
+            for (int t = 0; t < 4; t++) accz[t] = accu[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+            for (int k0 = 0; k0 < TM; k0 += 4) {
+                const float al = sDL[16 * it + lr][k0 + lk], ap = sP[16 * it + lr][k0 + lk];
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const float bt = sTab[(k0 + lk) * LD + 16 * (ct0 + t) + lr];
+                    accz[t] = mfma4(al, bt, accz[t]);
+                    accu[t] = mfma4(ap, bt, accu[t]);
                 }
-                float t4[4];  // the padded rows are not 16-byte aligned: four scalar reads
-#pragma unroll
-                for (int j = 0; j < 4; j++) t4[j] = sTab[r * LD + bc + j];
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        dz[i][j] = fmaf(lv[i], t4[j], dz[i][j]);
-                        u[i][j] = fmaf(pv[i], t4[j], u[i][j]);
-                    }
             }
+            // lane holds rows i = 16 it + 4 lk + q of column m = 16 (ct0 + t) + lr; the pair
+            // (2 pr, 2 pr + 1) sits in lanes (lr, lr ^ 1), swapped in by quad_perm [1,0,3,2].
+            // With z = U(lam) raw and du = U(lam) dweights, the clock's share
+            // kappa_p [dz . dU(lam)/dlam raw + dweights . dU(-lam)/dlam u] is
+            // kappa_p [(z_e dz_o - z_o dz_e) + (du_e u_o - du_o u_e)] (a rotation keeps
+            // the 2-d cross product); the even lane of a pair forms it.
+            const bool odd = (lr & 1) != 0;
+            float dl[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int rho = b0 + br + i;
-                float dl = 0.f;
-                if (rho < rows) {
-                    const size_t row = ((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp;
-                    // With z = U(lam) raw and du = U(lam) dweights, the clock's share
-                    // kappa_p [dz . dU(lam)/dlam raw + dweights . dU(-lam)/dlam u] is
-                    // kappa_p [(z_e dz_o - z_o dz_e) + (du_e u_o - du_o u_e)] (a
-                    // rotation keeps the 2-d cross product), all from LDS and registers.
+            for (int t = 0; t < 4; t++) {
+                const int m = 16 * (ct0 + t) + lr, pr = m >> 1;
 #pragma unroll
-                    for (int j = 0; j < 4; j += 2) {
-                        const int pr = (bc + j) >> 1;
-                        if (pr < P) {
-                            const float c = sCs[br + i][pr], s = sSn[br + i][pr];
-                            const float ge = dz[i][j], go = dz[i][j + 1], ue = u[i][j], uo = u[i][j + 1];
-                            a.draw[row * M + 2 * pr] = c * ge + s * go;
-                            a.draw[row * M + 2 * pr + 1] = -s * ge + c * go;
-                            const float ze = sZ[br + i][2 * pr], zo = sZ[br + i][2 * pr + 1];
-                            const float de = sDU[br + i][2 * pr], dd = sDU[br + i][2 * pr + 1];
-                            dl += (float)(kTwoPiBw * pr / R) * ((ze * go - zo * ge) + (de * uo - dd * ue));
+                for (int q = 0; q < 4; q++) {
+                    const float gz = accz[t][q], gx = dpp_mov<0xB1>(gz);
+                    const float gu = accu[t][q], ux = dpp_mov<0xB1>(gu);
+                    const float ge = odd ? gx : gz, go = odd ? gz : gx, ue = odd ? ux : gu, uo = odd ? gu : ux;
+                    const int i = 16 * it + 4 * lk + q, rho = b0 + i;
+                    if (rho < rows && pr < P) {
+                        const size_t row = ((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp;
+                        const float c = sCs[i][pr], s = sSn[i][pr];
+                        a.draw[row * M + m] = odd ? -s * ge + c * go : c * ge + s * go;
+                        if (!odd) {
+                            const float ze = sZ[i][2 * pr], zo = sZ[i][2 * pr + 1];
+                            const float de = sDU[i][2 * pr], dd = sDU[i][2 * pr + 1];
+                            dl[q] += (float)(kTwoPiBw * pr / R) * ((ze * go - zo * ge) + (de * uo - dd * ue));
                         }
                     }
                 }
-                sLam[br + i][tid & 31] = dl;
+            }
+            // the row's share over this wave's 16 lanes (its four column tiles summed above,
+            // in tile order), then the two waves of the row tile in wave order
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float v = wave_sum<16>(dl[q]);
+                if (lr == 0) sLam[16 * it + 4 * lk + q][wv >> 1] = v;
             }
         }
         __syncthreads();
-        if (tid < RO_BLK && b0 + tid < rows) {  // the clock's share per row, summed in column order
-            float dl = 0.f;
-            for (int g = 0; g < 32; g++) dl += sLam[tid][g];
+        if (tid < RO_BLK && b0 + tid < rows) {  // the clock's share per row
             const int rho = b0 + tid;
-            a.dlam[((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp] = dl;
+            a.dlam[((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp] = sLam[tid][0] + sLam[tid][1];
         }
-        // dtable += p^T du + dl^T z over the block's rows
-        for (int i = 0; i < RO_BLK; i++) {
-            float pv[4], lv[4];
+        // dtable[r][m] += sum_i p[i][r] du[i][m] + dl[i][r] z[i][m] over the block's rows
+        for (int k0 = 0; k0 < RO_BLK; k0 += 4) {
+            float bu[2], bz[2];
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                pv[r] = sP[i][tr + r];
-                lv[r] = sDL[i][tr + r];
+            for (int mt = 0; mt < 2; mt++) {
+                bu[mt] = sDU[k0 + lk][16 * (2 * wv + mt) + lr];
+                bz[mt] = sZ[k0 + lk][16 * (2 * wv + mt) + lr];
             }
 #pragma unroll
-            for (int m = 0; m < 16; m++) {
-                const float du = sDU[i][tc + m], z = sZ[i][tc + m];
+            for (int rt = 0; rt < 8; rt++) {
+                const float ap = sP[k0 + lk][16 * rt + lr], al = sDL[k0 + lk][16 * rt + lr];
 #pragma unroll
-                for (int r = 0; r < 4; r++) dt[r][m] = fmaf(pv[r], du, fmaf(lv[r], z, dt[r][m]));
+                for (int mt = 0; mt < 2; mt++) {
+                    dacc[rt][mt] = mfma4(ap, bu[mt], dacc[rt][mt]);
+                    dacc[rt][mt] = mfma4(al, bz[mt], dacc[rt][mt]);
+                }
             }
         }
     }
+    // lane holds dtable rows 16 rt + 4 lk + q of column 16 (2 wv + mt) + lr
     float* dst = a.dtab + ((size_t)h * gridDim.x + blk) * RM;
 #pragma unroll
-    for (int r = 0; r < 4; r++)
+    for (int rt = 0; rt < 8; rt++)
 #pragma unroll
-        for (int m = 0; m < 16; m++)
-            if (tr + r < R && tc + m < M) dst[(tr + r) * M + tc + m] = dt[r][m];
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int r = 16 * rt + 4 * lk + q, m = 16 * (2 * wv + mt) + lr;
+                if (r < R && m < M) dst[r * M + m] = dacc[rt][mt][q];
+            }
 }
 
 // The readout and its adjoint for 128 < M <= 256 slots, where a head's table
