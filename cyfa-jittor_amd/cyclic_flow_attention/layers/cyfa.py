@@ -37,15 +37,22 @@ from ..ops.utils import readout_table
 GATE_IN_KERNEL_MIN_WORKGROUPS = 128
 # Bytes of weights a small-batch decode step reads into the caches while its
 # decode kernel runs (prefetch_weights): ranges are taken in the order the
-# step reads them (o_proj, then the caller's: the MLP's gate|up and down),
-# skipping any that would pass the budget; a weight whose projection reads
-# one contiguous span per workgroup goes with that span, and its pieces land
-# in the L2 of the XCD that reads them. Measured on MI355X (graphed steps):
-# the 400M model's o_proj, gate|up and down (19 MB) gain 3% at B=1 and 6% at
-# B=16; the 1.4B model's o_proj (8 MB) gains 1.4% at B=1 (2.7% once its
-# pieces go to the XCDs that read them), while its 77 MB outlast the decode
-# kernel and cost 2.5%.
-PREFETCH_BUDGET_BYTES = 24 << 20
+# step reads them (o_proj, then the caller's: the MLP's gate|up and down, then
+# the next layer's input projection), skipping any that would pass the budget
+# except a range marked as a prefix (the next layer's input weight), of which
+# the leading part that fits is read; a weight whose projection reads one
+# contiguous span per workgroup goes with that span, and its pieces land in
+# the L2 of the XCD that reads them. Measured on MI355X (graphed steps, 1.4B
+# at B=1): o_proj alone 957-970 tok/s, with down (31 MB) 990, with down and
+# the first 10-25% of the next input weight 999-1000 (the budget leaves it
+# 24%), with half of it 996, with all of it (58 MB) 958 - past what the L2s
+# hold until it is read.
+# (A prefix item is only taken up to PREFETCH_PREFIX_MAX_BH.)
+PREFETCH_BUDGET_BYTES = 36 << 20
+# Largest B H whose step takes (a prefix of) the next layer's input weight: from
+# B H = 64 the step workgroups' own prefetched inputs fill most of each XCD's
+# L2 (400M at B=16: 17.2 k tok/s without the prefix, 16.8 k with it).
+PREFETCH_PREFIX_MAX_BH = 16
 
 
 def inference_fast_path(x):
@@ -362,6 +369,23 @@ class CyclicFlowAttention(nn.Module):
         o, new_cache = self(norm(x), cache, use_cache)
         return x + o, new_cache
 
+    def step_input_weight(self, x, norm):
+        """The input projection's weight a one-token step of forward_block(x,
+        norm) reads first, as a prefetch range for the step before it:
+        ((weight, span, True),) - the span each workgroup of the projection
+        reads, and True: the leading part that fits the budget may be taken -
+        or () when the step runs elsewhere."""
+        rows = x.numel() // x.shape[-1]
+        if not self._fused_ok(x, None) or rows > _native.LINEAR_ROWS_MAX:
+            return ()
+        g0 = self.g_proj[0]
+        w = self._in_weight.get(self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, g0.weight,
+                                self.a_proj.weight, self.b_proj.weight, self.d_proj.weight)
+        folded = self.fold_prenorm_weight and x.shape[-1] <= _native.LINEAR_NORM_MAX_K
+        if folded:
+            w = self._in_weight_folded.get(w, norm.weight, build=_native.fold_norm_weight)
+        return ((w, _native.linear_rows_span(rows, w.shape[0], w.shape[1], norm=2 if folded else 1), True),)
+
     def _forward_fused(self, x, cache, use_cache, prenorm=None, prefetch=()):
         """bf16 inference: the same math as forward with fused launches. With
         ``prenorm`` (the block's norm), x is the block input and the result is
@@ -453,10 +477,15 @@ class CyclicFlowAttention(nn.Module):
                 w_o = self.o_proj.weight
                 span_o = _native.linear_rows_span(B * T, w_o.shape[0], w_o.shape[1])
                 for item in ((w_o, span_o),) + tuple(prefetch):
-                    t = item[0] if isinstance(item, tuple) else item
+                    t, span, prefix = (item + (False,))[:3] if isinstance(item, tuple) else (item, 0, False)
                     n = t.numel() * t.element_size()
-                    if total + n <= PREFETCH_BUDGET_BYTES and len(pf) < _native.PREFETCH_RANGES:
-                        pf, total = pf + (item,), total + n
+                    if len(pf) >= _native.PREFETCH_RANGES or (prefix and B * H > PREFETCH_PREFIX_MAX_BH):
+                        break
+                    if total + n <= PREFETCH_BUDGET_BYTES:
+                        pf, total = pf + ((t, span),), total + n
+                    elif prefix and PREFETCH_BUDGET_BYTES - total >= 1 << 20:
+                        k = (PREFETCH_BUDGET_BYTES - total) // t.element_size() // 8 * 8
+                        pf, total = pf + ((t.reshape(-1)[:k], span),), PREFETCH_BUDGET_BYTES
             o, state = decode_layer_step(
                 qkv, cat_cache, tail, wconv.reshape(-1, W).to(x.dtype), abd, self.dt_bias, self.A_log, gate,
                 self.o_norm.weight, self.o_norm.eps, float(self.num_slots - 1), self.readout_table(),

@@ -132,9 +132,15 @@ class CyclicFlowAttentionModel(nn.Module):
             # bf16 decode steps: each pre-norm runs inside the projection after
             # it, each residual add inside the projection before it (x + y, as
             # CyFABlock.forward, bit for bit)
+            # (a small-batch step's decode kernel reads the weights that follow
+            # it into the caches: the block's MLP, then the next layer's input
+            # projection, the first layer's after the last)
+            n = len(self.layers)
             for i, layer in enumerate(self.layers):
+                nxt = self.layers[(i + 1) % n]
+                pf = tuple(layer.mlp.step_weights(layer.mlp_norm, x)) + nxt.attn.step_input_weight(x, nxt.attn_norm)
                 x, s = layer.attn.forward_block(x, layer.attn_norm, None if cache is None else cache[i], use_cache,
-                                                prefetch=layer.mlp.step_weights(layer.mlp_norm, x))
+                                                prefetch=pf)
                 x = layer.mlp.forward_block(x, layer.mlp_norm)
                 new.append(s)
             return self.norm(x), (new if use_cache else None)
