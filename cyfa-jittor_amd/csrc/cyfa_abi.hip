@@ -467,8 +467,24 @@ static int linear_params(const CyfaLinearArgs* a, const char* name, cyfa::Linear
     p.swiglu = a->swiglu != 0;
     p.add = (const __bf16*)a->residual;
     p.ld_add = a->ldr;
+    static_assert(CYFA_LINEAR_PREFETCH_RANGES == cyfa::LINEAR_PREFETCH_RANGES, "prefetch ranges");
+    for (int r = 0; r < CYFA_LINEAR_PREFETCH_RANGES; r++) {
+        const unsigned long long n = a->prefetch_bytes[r], span = a->prefetch_span[r];
+        if (n == 0) continue;
+        if (!a->prefetch[r] || n >= (1ull << 31))
+            return fail(CYFA_ERR_VALUE, "%s: prefetch range %d: null or %llu bytes (below 2^31)", name, r, n);
+        if (!aligned(a->prefetch[r], 16))
+            return fail(CYFA_ERR_ALIGN, "%s: prefetch range %d needs 16-byte alignment", name, r);
+        if (span % 16 != 0 || span >= (1ull << 31))
+            return fail(CYFA_ERR_VALUE, "%s: prefetch range %d: span %llu (a multiple of 16 below 2^31)", name, r,
+                        span);
+        p.pf[r] = a->prefetch[r];
+        p.pf_bytes[r] = n;
+        p.pf_span[r] = span;
+    }
     return CYFA_OK;
 }
+
 
 int cyfa_linear_rows(const CyfaLinearArgs* a, void* hip_stream) {
     cyfa::LinearParams p;

@@ -173,6 +173,8 @@ int launch_decode_step(const DecodeParams& p, int K, int V, hipStream_t stream);
 int launch_prefill(const PrefillParams& p, hipStream_t stream);
 int launch_readout_table(const float* readout, float* table, int H, hipStream_t stream);
 // y = x W^T (+ bias) for at most 64 rows of x (the one-token decode step's projections).
+constexpr int LINEAR_PREFETCH_RANGES = 2;
+
 struct LinearParams {
     int M, N, K;
     const __bf16* x;     // [M, K], rows ldx elements apart
@@ -197,6 +199,14 @@ struct LinearParams {
     __bf16* norm_sum_out;         // [M, K], rows ldr apart; set with norm_residual; aliases no input
     long long ldr;
     float norm_eps;
+    // Cache prefetch for the launch after this one: the ranges pf[r] (pf_bytes[r]
+    // bytes, below 2^31; pf_span[r] as DecodeParams.pf_span) are read by pf_wgs
+    // extra workgroups after the tiles
+    const void* pf[LINEAR_PREFETCH_RANGES];
+    unsigned long long pf_bytes[LINEAR_PREFETCH_RANGES];
+    unsigned long long pf_span[LINEAR_PREFETCH_RANGES];
+    int pf_wgs;
+    int grid_x, grid_y;  // tiles along N (padded to a multiple of 8 when grid_y > 1) and along M; set by the launcher
 };
 
 constexpr int LINEAR_NORM_MAX_K = 2048;

@@ -14,7 +14,7 @@ import torch
 import torch.nn.functional as F
 
 LIB_PATH = Path(os.environ.get("CYFA_LIB", Path(__file__).with_name("libcyfa_hip.so")))
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 CYFA_OK = 0
 CYFA_ERR_VALUE = -1
@@ -28,6 +28,8 @@ _c_int, _c_float, _c_void_p, _c_size_t = ctypes.c_int, ctypes.c_float, ctypes.c_
 # cyfa_decode_layer_step's cache-prefetch ranges, and the largest B H with
 # which the kernel prefetches them (CYFA_PREFETCH_RANGES, CYFA_PREFETCH_MAX_BH)
 PREFETCH_RANGES = 4
+# cyfa_linear_rows' cache-prefetch ranges (CYFA_LINEAR_PREFETCH_RANGES)
+LINEAR_PREFETCH_RANGES = 2
 PREFETCH_MAX_BH = 64
 
 
@@ -113,6 +115,9 @@ class CyfaLinearArgs(ctypes.Structure):
         ("x", _c_void_p), ("ldx", ctypes.c_longlong), ("weight", _c_void_p), ("bias", _c_void_p),
         ("y", _c_void_p), ("ldy", ctypes.c_longlong), ("swiglu", _c_int),
         ("residual", _c_void_p), ("ldr", ctypes.c_longlong),
+        ("prefetch", _c_void_p * LINEAR_PREFETCH_RANGES),
+        ("prefetch_bytes", ctypes.c_ulonglong * LINEAR_PREFETCH_RANGES),
+        ("prefetch_span", ctypes.c_ulonglong * LINEAR_PREFETCH_RANGES),
     ]
 
 
@@ -425,13 +430,30 @@ def rms_norm(x, weight, eps, gate=None, residual=None, prescale=1.0):
 LINEAR_ROWS_MAX = 64
 
 
-def linear(x, weight, bias=None, out_cols=None, residual=None):
+def _set_linear_prefetch(args, prefetch, dev, what):
+    """Fill CyfaLinearArgs' prefetch ranges from (tensor, span) pairs (or bare
+    tensors, span 0)."""
+    if len(prefetch) > LINEAR_PREFETCH_RANGES:
+        raise ValueError(f"{what}: at most {LINEAR_PREFETCH_RANGES} prefetch tensors")
+    for i, item in enumerate(prefetch):
+        t, span = item if isinstance(item, tuple) else (item, 0)
+        if not t.is_contiguous() or t.device != dev:
+            raise ValueError(f"{what}: prefetch tensors must be contiguous, on the call's device")
+        args.prefetch[i] = t.data_ptr()
+        args.prefetch_bytes[i] = t.numel() * t.element_size()
+        args.prefetch_span[i] = int(span)
+
+
+def linear(x, weight, bias=None, out_cols=None, residual=None, prefetch=()):
     """x W^T (+ bias), bf16, like F.linear; with ``residual``, the block's
     residual add residual + bf16(x W^T + bias). Calls with at most 64 rows
     (the one-token decode step) run on cyfa_linear_rows, which streams W once
     across the whole chip; larger calls go to the library GEMM. ``out_cols``
     (>= N) pads the output rows, so that column slices of the result start
-    16-byte aligned."""
+    16-byte aligned. ``prefetch``: up to two contiguous device tensors, each
+    bare or as (tensor, span) with span from linear_rows_span, that extra
+    workgroups of the launch read into the caches for the projection after it
+    (ignored where the library GEMM runs)."""
     K = weight.shape[-1]
     N = weight.shape[0]
     width = K
@@ -460,6 +482,7 @@ def linear(x, weight, bias=None, out_cols=None, residual=None):
     args = CyfaLinearArgs(M=rows, N=N, K=K, x=x2.data_ptr(), ldx=x2.stride(0), weight=w.data_ptr(),
                           bias=ptr(None if bias is None else bias.detach().contiguous()), y=y.data_ptr(), ldy=ldy,
                           residual=ptr(residual), ldr=0 if residual is None else residual.stride(0))
+    _set_linear_prefetch(args, prefetch, x.device, "linear")
     _check(load_library().cyfa_linear_rows(ctypes.byref(args), stream_handle(x.device)), "cyfa_linear_rows")
     lead = tuple(x.shape[:-1])
     if not lead:
@@ -481,14 +504,14 @@ def fold_norm_weight(weight, norm_weight):
 
 def linear_rows_span(M, N, K, swiglu=False, norm=0):
     """Bytes of the weight each workgroup of a linear / norm_linear launch with
-    M rows reads, when workgroup c reads the bytes [c span, (c + 1) span) and
-    no other workgroup reads them; 0 otherwise (cyfa_linear_rows_span; norm:
-    0 none, 1 with the norm weight, 2 folded). For decode_layer_step's
-    prefetch spans; no GPU needed."""
+    M rows reads, when the workgroups that read the bytes [c span, (c + 1)
+    span) all run on XCD c mod 8; 0 otherwise (cyfa_linear_rows_span; norm:
+    0 none, 1 with the norm weight, 2 folded). For the prefetch spans of
+    decode_layer_step, linear and norm_linear; no GPU needed."""
     return int(load_library().cyfa_linear_rows_span(int(M), int(N), int(K), int(bool(swiglu)), int(norm)))
 
 
-def norm_linear(x, norm_weight, eps, weight, bias=None, residual=None, out_cols=None, swiglu=False):
+def norm_linear(x, norm_weight, eps, weight, bias=None, residual=None, out_cols=None, swiglu=False, prefetch=()):
     """The block's pre-norm and its first projection in one cyfa_norm_linear_rows
     launch, for at most 64 bf16 rows of K <= 2048 columns:
     s = bf16(x + residual) (x itself without a residual), h = rms_norm(s), and
@@ -499,7 +522,8 @@ def norm_linear(x, norm_weight, eps, weight, bias=None, residual=None, out_cols=
 
     norm_weight None: ``weight`` already carries the norm weight
     (fold_norm_weight), and y = bf16(rsqrt(mean(s^2) + eps) (s weight^T) + bias)
-    with the row scale on the fp32 product (the shapes above only)."""
+    with the row scale on the fp32 product (the shapes above only).
+    ``prefetch`` as in linear."""
     K = weight.shape[-1]
     N = weight.shape[0]
     if x.shape[-1] != K:
@@ -540,6 +564,7 @@ def norm_linear(x, norm_weight, eps, weight, bias=None, residual=None, out_cols=
     args = CyfaLinearArgs(M=rows, N=N, K=K, x=x2.data_ptr(), ldx=x2.stride(0), weight=w.data_ptr(),
                           bias=ptr(None if bias is None else bias.detach().contiguous()), y=y.data_ptr(), ldy=ldy,
                           swiglu=1 if swiglu else 0)
+    _set_linear_prefetch(args, prefetch, x.device, "norm_linear")
     nargs = CyfaRowNormArgs(weight=ptr(nw), eps=float(eps), residual=ptr(r2), sum_out=ptr(total), ldr=K)
     _check(load_library().cyfa_norm_linear_rows(ctypes.byref(args), ctypes.byref(nargs), stream_handle(x.device)),
            "cyfa_norm_linear_rows")

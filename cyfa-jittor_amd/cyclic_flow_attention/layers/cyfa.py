@@ -369,6 +369,12 @@ class CyclicFlowAttention(nn.Module):
         o, new_cache = self(norm(x), cache, use_cache)
         return x + o, new_cache
 
+    def step_prefetch_in_decode_kernel(self, x):
+        """Whether a one-token step of forward_block(x, ...) reads the weights
+        that follow it into the caches inside its decode kernel (small
+        batches); at larger batches the projections read the next one's."""
+        return self.prefetch_weights and x.numel() // x.shape[-1] * self.num_heads <= _native.PREFETCH_MAX_BH
+
     def step_input_weight(self, x, norm):
         """The input projection's weight a one-token step of forward_block(x,
         norm) reads first, as a prefetch range for the step before it:
@@ -494,7 +500,10 @@ class CyclicFlowAttention(nn.Module):
                 inplace=self.decode_in_place and cache is not None and nxt is None,
                 g_proj=(g0_out, g1.weight, g1.bias) if in_kernel else None, prefetch=pf,
                 out_state=None if nxt is None else nxt["recurrent_state"])
-            o = _native.linear(o.view(B, T, Dv), self.o_proj.weight, residual=block_in)
+            # at larger batches extra workgroups of o_proj read the weight of
+            # the projection after it (the MLP's gate|up) into the caches
+            o_pf = () if small else tuple(item[:2] for item in tuple(prefetch)[:1] if isinstance(item, tuple))
+            o = _native.linear(o.view(B, T, Dv), self.o_proj.weight, residual=block_in, prefetch=o_pf)
             cq, ck, cv = tail[..., :Dk], tail[..., Dk:2 * Dk], tail[..., 2 * Dk:]
             new_cache = {"recurrent_state": state, "conv_state": (cq, ck, cv)} if use_cache else None
             return o, new_cache

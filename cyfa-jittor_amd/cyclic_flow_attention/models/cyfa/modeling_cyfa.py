@@ -71,19 +71,28 @@ class GatedMLP(nn.Module):
                     (w_d, _native.linear_rows_span(rows, w_d.shape[0], w_d.shape[1])))
         return ()
 
-    def forward_block(self, x, norm):
+    def forward_block(self, x, norm, prefetch_next=None):
         """The MLP half of a decoder block, x + self(norm(x)). A decode step with
         at most 64 rows runs the norm inside the gate|up projection and the
-        residual add inside down_proj."""
+        residual add inside down_proj. With ``prefetch_next`` ((tensor, span)
+        items: the next layer's input weight, or ()), the gate|up launch also
+        reads down's weight into the caches and down reads those; nothing
+        depends on them."""
         rows = x.numel() // x.shape[-1]
         if (inference_fast_path(x) and rows <= _native.LINEAR_ROWS_MAX and self.gate_proj.weight.shape[0] % 16 == 0
                 and x.shape[-1] % 32 == 0):
-            w = self._step_gate_up(norm, x.shape[-1])
-            if self.fold_norm_weight and x.shape[-1] <= _native.LINEAR_NORM_MAX_K:
-                _, h = _native.norm_linear(x, None, norm.eps, w, swiglu=True)
+            K = x.shape[-1]
+            w = self._step_gate_up(norm, K)
+            w_d = self.down_proj.weight
+            gu_pf = d_pf = ()
+            if prefetch_next is not None:
+                gu_pf = ((w_d, _native.linear_rows_span(rows, w_d.shape[0], w_d.shape[1])),)
+                d_pf = tuple(item[:2] for item in prefetch_next)
+            if self.fold_norm_weight and K <= _native.LINEAR_NORM_MAX_K:
+                _, h = _native.norm_linear(x, None, norm.eps, w, swiglu=True, prefetch=gu_pf)
             else:
-                _, h = _native.norm_linear(x, norm.weight, norm.eps, w, swiglu=True)
-            return _native.linear(h, self.down_proj.weight, residual=x)
+                _, h = _native.norm_linear(x, norm.weight, norm.eps, w, swiglu=True, prefetch=gu_pf)
+            return _native.linear(h, w_d, residual=x, prefetch=d_pf)
         return x + self(norm(x))
 
 
@@ -138,10 +147,13 @@ class CyclicFlowAttentionModel(nn.Module):
             n = len(self.layers)
             for i, layer in enumerate(self.layers):
                 nxt = self.layers[(i + 1) % n]
-                pf = tuple(layer.mlp.step_weights(layer.mlp_norm, x)) + nxt.attn.step_input_weight(x, nxt.attn_norm)
+                nin = nxt.attn.step_input_weight(x, nxt.attn_norm)
+                pf = tuple(layer.mlp.step_weights(layer.mlp_norm, x)) + nin
                 x, s = layer.attn.forward_block(x, layer.attn_norm, None if cache is None else cache[i], use_cache,
                                                 prefetch=pf)
-                x = layer.mlp.forward_block(x, layer.mlp_norm)
+                # (larger batches: each projection reads the next one's weight)
+                x = layer.mlp.forward_block(x, layer.mlp_norm,
+                                            None if layer.attn.step_prefetch_in_decode_kernel(x) else nin)
                 new.append(s)
             return self.norm(x), (new if use_cache else None)
         # bf16 prefill: each residual add runs inside the following norm kernel

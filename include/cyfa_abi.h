@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define CYFA_ABI_VERSION 10
+#define CYFA_ABI_VERSION 11
 
 enum {
     CYFA_OK = 0,
@@ -359,6 +359,8 @@ int cyfa_argmax_rows(const void *x, long long ldx, int rows, int n, long long *o
  * (GatedMLP, models/cyfa/modeling_cyfa.py:22-27). With residual set, y is the
  * block's residual add around the projection (CyFABlock.execute,
  * models/cyfa/modeling_cyfa.py:48-51). */
+#define CYFA_LINEAR_PREFETCH_RANGES 2
+
 typedef struct CyfaLinearArgs {
     int M, N, K;
     const void *x;                /* bf16 [M, K], rows ldx elements apart (ldx >= K, ldx % 8 == 0) */
@@ -371,6 +373,17 @@ typedef struct CyfaLinearArgs {
     const void *residual;         /* nullable bf16 [M, N], rows ldr apart: y = bf16(residual + bf16(x W^T + b));
                                      not with swiglu; may be y itself */
     long long ldr;
+    /* Cache prefetch (no reference counterpart; all NULL / 0: none): extra
+       workgroups of the launch, on the compute units its tiles leave idle,
+       read prefetch[r] (prefetch_bytes[r] bytes, 16-byte aligned, below 2^31)
+       into the caches for the launch after this one, with prefetch_span[r] as
+       in CyfaDecodeLayerArgs (0, or the bytes each workgroup of that launch
+       reads, cyfa_linear_rows_span: each piece then lands in the L2 of the XCD
+       that reads it). Nothing is written; the projection's result does not
+       depend on it. */
+    const void *prefetch[CYFA_LINEAR_PREFETCH_RANGES];
+    unsigned long long prefetch_bytes[CYFA_LINEAR_PREFETCH_RANGES];
+    unsigned long long prefetch_span[CYFA_LINEAR_PREFETCH_RANGES];
 } CyfaLinearArgs;
 
 /* Replaces the Linear / BiasLinear projections (layers/cyfa.py:15-58) of the
@@ -383,11 +396,12 @@ int cyfa_linear_rows(const CyfaLinearArgs *args, void *hip_stream);
 
 /* The bytes of the weight that each workgroup of a cyfa_linear_rows (norm 0)
  * or cyfa_norm_linear_rows (norm 1: with the norm weight, 2: folded) launch
- * of this shape reads, when workgroup c reads the bytes [c span, (c + 1) span)
- * of the weight and no other workgroup reads them; 0 when the launch's
- * workgroups share weight rows or read them in separate pieces, and for
- * shapes the launchers refuse. A host-side query for
- * CyfaDecodeLayerArgs.prefetch_span. No reference counterpart. */
+ * of this shape reads, when the workgroups that read the bytes [c span,
+ * (c + 1) span) of the weight all run on XCD c mod 8 (workgroup c alone, or
+ * with several row tiles the row tiles of N tile c); 0 when a workgroup reads
+ * its weight rows in separate pieces, and for shapes the launchers refuse. A
+ * host-side query for the prefetch_span fields of CyfaDecodeLayerArgs and
+ * CyfaLinearArgs. No reference counterpart. */
 size_t cyfa_linear_rows_span(int M, int N, int K, int swiglu, int norm);
 
 /* The RMS norm in front of a projection (K <= 2048 columns):

@@ -331,15 +331,34 @@ def test_decode_layer_prefetch_ranges_validated_before_launch():
     assert b"span" in lib.cyfa_last_error()
 
 
+def test_linear_rows_prefetch_ranges_validated_before_launch():
+    """cyfa_linear_rows checks its cache-prefetch ranges before any launch, as
+    cyfa_decode_layer_step does (the pointers are never dereferenced here)."""
+    lib = _native.load_library()
+    a = _native.CyfaLinearArgs(M=64, N=1024, K=1024, x=0x10000, ldx=1024, weight=0x20000, y=0x30000, ldy=1024)
+    a.prefetch_bytes[1] = 4096  # bytes without a pointer
+    assert lib.cyfa_linear_rows(ctypes.byref(a), None) == _native.CYFA_ERR_VALUE
+    assert b"prefetch range 1" in lib.cyfa_last_error()
+    a.prefetch[1] = 0x100008  # misaligned
+    assert lib.cyfa_linear_rows(ctypes.byref(a), None) == _native.CYFA_ERR_ALIGN
+    a.prefetch[1], a.prefetch_bytes[1] = 0x100000, 1 << 31  # too large for the kernel's 32-bit offsets
+    assert lib.cyfa_linear_rows(ctypes.byref(a), None) == _native.CYFA_ERR_VALUE
+    a.prefetch_bytes[1], a.prefetch_span[1] = 4096, 24  # a span must be a multiple of 16
+    n = _native.CyfaRowNormArgs(weight=0x40000, eps=1e-6)
+    assert lib.cyfa_norm_linear_rows(ctypes.byref(a), ctypes.byref(n), None) == _native.CYFA_ERR_VALUE
+    assert b"span" in lib.cyfa_last_error()
+
+
 def test_linear_rows_span_query():
     """cyfa_linear_rows_span, the bytes of W each workgroup of a projection
-    launch reads when workgroup c reads exactly the bytes [c span, (c + 1)
-    span): the one-row kernel's waves take RW rows each (four waves per
-    workgroup, RW the most of 4, 2, 1 that keeps 256 or more workgroups), the
-    tile kernel's workgroup x the rows 16 CT x .. when M fits one row tile;
-    0 where workgroups share rows (several row tiles), read them in pieces
-    (SwiGLU's interleaved gate and up rows in the one-row kernel) or the
-    launchers refuse the shape."""
+    launch reads when the workgroups that read the bytes [c span, (c + 1)
+    span) all run on XCD c mod 8: the one-row kernel's waves take RW rows
+    each (four waves per workgroup, RW the most of 4, 2, 1 that keeps 256 or
+    more workgroups), the tile kernel's N tile x the rows 16 CT x .. (with
+    several row tiles the launcher pads the N tiles to a multiple of 8, so
+    that every row tile of N tile x runs on the same XCD); 0 where one
+    workgroup reads its rows in pieces (SwiGLU's interleaved gate and up rows
+    in the one-row kernel) or the launchers refuse the shape."""
     span = _native.linear_rows_span
     assert span(1, 2048, 2048) == 4 * 2 * 2048 * 2     # o_proj of the 1.4B step: RW 2, 256 workgroups
     assert span(1, 2048, 5632) == 4 * 2 * 5632 * 2     # down
@@ -349,7 +368,8 @@ def test_linear_rows_span_query():
     assert span(1, 2048, 2048, norm=2) != 4 * 2 * 2048 * 2  # the folded norm stays on the tile kernel
     g1 = span(1, 2048, 256)                             # K = 256: the tile kernel, one row tile
     assert g1 > 0 and g1 % (16 * 256 * 2) == 0
-    assert span(64, 1024, 1024) == 0                    # 1 x 1 tiles: four row tiles read each W tile
+    assert span(64, 1024, 1024) == 16 * 1 * 1024 * 2    # 1 x 1 tiles: four row tiles read each W tile
+    assert span(64, 3340, 1024, norm=1) == 16 * 2 * 1024 * 2  # 2 x 2 tiles, 105 N tiles padded to 112
     assert span(64, 5632, 1024, swiglu=True, norm=1) == 16 * 2 * 1024 * 2  # 4 x 2 tiles
     assert span(64, 32000, 1024) == 16 * 4 * 1024 * 2   # the lm_head's 4 x 4 tiles
     for bad in ((0, 64, 64), (65, 64, 64), (1, 64, 48), (1, 0, 64)):

@@ -286,6 +286,39 @@ def test_linear_rows_tile_shape_does_not_change_bits(N, K):
         assert torch.equal(y, full[m:m + 2]), f"rows {m}, {m + 1}"
 
 
+@pytest.mark.parametrize("M,N,K,kind", [(64, 5632, 1024, "swiglu"), (64, 3340, 1024, "norm"),
+                                        (64, 1024, 2816, "residual"), (32, 1024, 1024, "residual")])
+def test_linear_rows_prefetch_changes_no_bit(M, N, K, kind):
+    """The extra workgroups that read other weights into the caches for the
+    next launch (one range with the span its workgroups read, one without)
+    leave the projection's result unchanged, bit for bit; two calls in a
+    row, the second with fewer rows."""
+    from cyclic_flow_attention import _native
+
+    gen = torch.Generator().manual_seed(M + N + K)
+    w = (0.05 * torch.randn(N, K, generator=gen)).bfloat16().to(DEV)
+    nw = (1 + 0.1 * torch.randn(K, generator=gen)).to(DEV)
+    nxt = (0.05 * torch.randn(2048, 1024, generator=gen)).bfloat16().to(DEV)
+    other = torch.randn(1 << 20, generator=gen).to(DEV)[:777_777]  # 3.1 MB, no span
+    pf = ((nxt, _native.linear_rows_span(M, 2048, 1024, norm=1)), other)
+    assert pf[0][1] > 0
+
+    def run(x, prefetch):
+        if kind == "swiglu":
+            return _native.norm_linear(x, nw, 1e-6, w, swiglu=True, prefetch=prefetch)[1]
+        if kind == "norm":
+            return _native.norm_linear(x, nw, 1e-6, w, prefetch=prefetch)[1]
+        return _native.linear(x, w, residual=torch.ones(x.shape[0], N, dtype=torch.bfloat16, device=DEV),
+                              prefetch=prefetch)
+
+    for rows in (M, M // 2 + 1):
+        x = torch.randn(rows, K, generator=gen).bfloat16().to(DEV)
+        with torch.no_grad():
+            ref, got = run(x, ()), run(x, pf)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), rows
+
+
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 1024, 1024), (64, 1024, 2816), (17, 3340, 256)])
