@@ -32,6 +32,7 @@
 // so the result does not depend on scheduling. fp32 FMA loops over LDS
 // tiles, no matrix cores: a first, exact form of the training path.
 #include <cmath>
+#include <type_traits>
 
 #include "cyfa_device.h"
 #include "cyfa_internal.h"
@@ -113,6 +114,25 @@ __global__ __launch_bounds__(256) void bw_rows_kernel(const void* x, const float
     if (rs_out && lane == 0) rs_out[row] = rs;
 }
 
+// Global accesses of the backward kernels go through buffer resources over
+// regions below 2^31 bytes (a chunk's rows, one state), each out-of-range
+// element predicated through its offset: no branch among the loads, at which
+// the compiler would wait for every load in flight.
+typedef __amdgpu_buffer_rsrc_t bw_rsrc_t;
+constexpr uint32_t BW_DEAD = 0x80000000u;  // past every region below (each < 2^31 bytes)
+
+__device__ __forceinline__ bw_rsrc_t bw_rsrc(const float* base, size_t elems) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)(uint32_t)(elems * 4), 0x00020000);
+}
+
+// A buffer store that the range check drops when dead is set.
+__device__ __forceinline__ void bw_store(bw_rsrc_t r, uint32_t off, bool live, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off | (live ? 0u : BW_DEAD), 0, 0);
+}
+__device__ __forceinline__ float bw_load(bw_rsrc_t r, uint32_t off, bool live) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off | (live ? 0u : BW_DEAD), 0, 0));
+}
+
 // The chunk-to-chunk scan of one pass over a [Kq, Vd] matrix X, one
 // SCAN_ROWS x 32 tile per workgroup (grid (ceil(Vd / 32), ceil(Kq /
 // SCAN_ROWS), B*H), 256 threads, each holding SCAN_RPT x 4 elements of X in
@@ -159,54 +179,64 @@ __global__ __launch_bounds__(256) void bw_state_scan_kernel(StateScanArgs p) {
     const float* Bm = p.b + bh * p.Tp * Vd;
     // this thread's block: rows r0 + rr .. + SCAN_RPT; columns c0 + cc .. + 3
     const int rr = SCAN_RPT * (tid >> 3), cc = 4 * (tid & 7);
+    // Every global access below goes through a buffer resource, predicated
+    // through its offset (no branch among the loads); the states per chunk.
     bool ok[SCAN_RPT][4];
+    uint32_t off[SCAN_RPT][4];  // byte offset of this thread's elements in a [Kq, Vd] state
     float x[SCAN_RPT][4];
+    const bw_rsrc_t rx0 = bw_rsrc(p.x0 ? p.x0 + bh * ssz : nullptr, p.x0 ? ssz : 0);
 #pragma unroll
     for (int i = 0; i < SCAN_RPT; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             ok[i][j] = r0 + rr + i < Kq && c0 + cc + j < Vd;
-            x[i][j] = ok[i][j] && p.x0 ? p.x0[bh * ssz + (size_t)(r0 + rr + i) * Vd + c0 + cc + j] : 0.f;
+            off[i][j] = ((uint32_t)(r0 + rr + i) * (uint32_t)Vd + (uint32_t)(c0 + cc + j)) * 4u;
+            x[i][j] = bw_load(rx0, off[i][j], ok[i][j]);  // zero without x0 (empty buffer)
         }
     // backward: the forward state S[n] of this thread's block, loaded a chunk
     // ahead (with the rows and columns below) for the boundary term <X, S[n]>
     float sv[SCAN_RPT][4] = {};
     const auto fetch_state = [&](int n) {
+        const bw_rsrc_t rs = bw_rsrc(p.S + (bh * (N + 1) + n) * ssz, ssz);
 #pragma unroll
         for (int i = 0; i < SCAN_RPT; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                sv[i][j] = ok[i][j] ? p.S[(bh * (N + 1) + n) * ssz + (size_t)(r0 + rr + i) * Vd + c0 + cc + j] : 0.f;
+            for (int j = 0; j < 4; j++) sv[i][j] = bw_load(rs, off[i][j], ok[i][j]);
     };
     const auto keep = [&](int n) {  // xs[n] = X; returns the block's part of <X, S[n]> (backward)
+        const bw_rsrc_t rs = bw_rsrc(xs + (size_t)n * ssz, ssz);
         float dot = 0.f;
 #pragma unroll
         for (int i = 0; i < SCAN_RPT; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                if (ok[i][j]) {
-                    xs[(size_t)n * ssz + (size_t)(r0 + rr + i) * Vd + c0 + cc + j] = x[i][j];
-                    if constexpr (BWD) dot = fmaf(x[i][j], sv[i][j], dot);
-                }
+            for (int j = 0; j < 4; j++) {
+                bw_store(rs, off[i][j], ok[i][j], x[i][j]);
+                if constexpr (BWD) dot = fmaf(x[i][j], sv[i][j], dot);  // sv is zero where !ok
+            }
         return dot;
     };
     // The next chunk's rows of a, columns of b and gate are loaded into
     // registers while the current chunk's FMAs run.
     constexpr int NA = BC * SCAN_ROWS / 256, NB = BC * BW_TILE / 256;
     float ra[NA], rb[NB], rg = 0.f;
+    // (the host keeps B T H below 2^21: the gate's offsets fit 32 bits)
+    const bw_rsrc_t rgt = bw_rsrc(p.g, (size_t)p.B * p.T * p.H);
     const auto fetch = [&](int n) {
         const int t0 = n * BC;
+        const bw_rsrc_t rA = bw_rsrc(A + (size_t)t0 * Kq, (size_t)BC * Kq), rBm = bw_rsrc(Bm + (size_t)t0 * Vd, (size_t)BC * Vd);
 #pragma unroll
         for (int i = 0; i < NA; i++) {
             const int e = tid + 256 * i, t = e / SCAN_ROWS, r = e % SCAN_ROWS;
-            ra[i] = r0 + r < Kq ? A[(size_t)(t0 + t) * Kq + r0 + r] : 0.f;
+            ra[i] = bw_load(rA, ((uint32_t)t * (uint32_t)Kq + (uint32_t)(r0 + r)) * 4u, r0 + r < Kq);
         }
 #pragma unroll
         for (int i = 0; i < NB; i++) {
             const int e = tid + 256 * i, t = e / BW_TILE, c = e % BW_TILE;
-            rb[i] = c0 + c < Vd ? Bm[(size_t)(t0 + t) * Vd + c0 + c] : 0.f;
+            rb[i] = bw_load(rBm, ((uint32_t)t * (uint32_t)Vd + (uint32_t)(c0 + c)) * 4u, c0 + c < Vd);
         }
-        if (wv == 0) rg = t0 + lane < p.T ? p.g[((size_t)b * p.T + t0 + lane) * p.H + h] : 0.f;
+        // (every wave loads the gate; wave 0 uses it)
+        rg = bw_load(rgt, (((uint32_t)b * (uint32_t)p.T + (uint32_t)(t0 + lane)) * (uint32_t)p.H + (uint32_t)h) * 4u,
+                     t0 + lane < p.T);
     };
     fetch(BWD ? N - 1 : 0);
     if constexpr (BWD) fetch_state(N);
@@ -264,13 +294,224 @@ __global__ __launch_bounds__(256) void bw_state_scan_kernel(StateScanArgs p) {
             for (int j = 0; j < 4; j++) x[i][j] = fmaf(el, x[i][j], acc[i][j]);
     }
     keep(BWD ? 0 : N);
-    if (p.x_out) {
+    const bw_rsrc_t rxo = bw_rsrc(p.x_out ? p.x_out + bh * ssz : nullptr, p.x_out ? ssz : 0);
 #pragma unroll
-        for (int i = 0; i < SCAN_RPT; i++)
+    for (int i = 0; i < SCAN_RPT; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                if (ok[i][j]) p.x_out[bh * ssz + (size_t)(r0 + rr + i) * Vd + c0 + cc + j] = x[i][j];
+        for (int j = 0; j < 4; j++) bw_store(rxo, off[i][j], ok[i][j], x[i][j]);  // dropped without x_out
+}
+
+// The same scan for bf16 operands on the matrix cores: the rank-64 update
+// X += A^T B over the chunk's 64 tokens as split-bf16 products on
+// v_mfma_f32_16x16x32_bf16 (each fp32 operand as a bf16 high part and a bf16
+// remainder, lo_a hi_b + hi_a lo_b + hi_a hi_b: about 16 mantissa bits, as in
+// the chunk kernels' tile GEMMs). A workgroup takes a 32 T2 x 32 T2 tile,
+// wave w its 16 T2 x 16 T2 quarter (w >> 1, w & 1) as T2 x T2 accumulator
+// blocks: lane (lr, lg) of block (ib, jb) has rows 16 T2 (w >> 1) + 16 ib +
+// 4 lg + i, column 16 T2 (w & 1) + 16 jb + lr. The larger tile reads each
+// chunk's rows of a and b from fewer workgroups (the scans are bound by those
+// reads: every column tile reads the rows of a again, every row tile the
+// columns of b). Per chunk, thread (r, q) = (tid % 32 T2, tid / 32 T2) loads
+// tokens 8 T2 q .. + 8 T2 of row r of a and of column r of b and stages them
+// transposed (row = state coordinate, 64 tokens along the row), so that every
+// operand fragment is one 16-byte LDS read. The boundary terms go to bnd per
+// 32 x 32 tile, as the FMA form's: with T2 = 2 one per wave, with T2 = 1 one
+// per workgroup.
+constexpr int SCAN_LDT = BC + 8;  // staged row: 64 tokens + 8 of padding (bf16)
+
+__device__ __forceinline__ void split_bf16x8(const float* v, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+    for (int x = 0; x < 8; x++) {
+        hi[x] = (bf16_t)v[x];
+        lo[x] = (bf16_t)(v[x] - (float)hi[x]);
     }
+}
+
+template <bool BWD, int T2>
+__global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) {
+    static_assert(SCAN_ROWS == 32 && BW_TILE == 32 && (T2 == 1 || T2 == 2), "32 x 32 bnd tiles");
+    constexpr int TS = 32 * T2;     // tile side
+    constexpr int TPT = BC / (256 / TS);  // tokens per staging thread
+    __shared__ __align__(16) bf16_t sAh[TS][SCAN_LDT], sAl[TS][SCAN_LDT];
+    __shared__ __align__(16) bf16_t sBh[TS][SCAN_LDT], sBl[TS][SCAN_LDT];
+    __shared__ float sF[BC];
+    __shared__ float sRed[4];
+    __shared__ float sEl;
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lr = lane & 15, lg = lane >> 4;
+    const int c0 = blockIdx.x * TS, r0 = blockIdx.y * TS, bhi = blockIdx.z;
+    const int b = bhi / p.H, h = bhi % p.H;
+    const int Kq = p.Kq, Vd = p.Vd, N = p.N;
+    // bnd tiles of 32 x 32: nx across Vd, ny down Kq; this workgroup's (T2 = 1)
+    // or this wave's (T2 = 2)
+    const int nx = (Vd + 31) / 32, ny = (Kq + 31) / 32, nt = nx * ny;
+    const int ty = T2 == 1 ? (int)blockIdx.y : 2 * (int)blockIdx.y + (wv >> 1);
+    const int tx = T2 == 1 ? (int)blockIdx.x : 2 * (int)blockIdx.x + (wv & 1);
+    const size_t bh = bhi, ssz = (size_t)Kq * Vd;
+    float* xs = p.xs + bh * (N + 1) * ssz;
+    const float* A = p.a + bh * p.Tp * Kq;
+    const float* Bm = p.b + bh * p.Tp * Vd;
+    const int wr = 16 * T2 * (wv >> 1), wc = 16 * T2 * (wv & 1);  // the wave's quarter
+    bool ok[T2][T2][4];
+    uint32_t off[T2][T2][4];
+    f32x4 x[T2][T2];
+    const bw_rsrc_t rx0 = bw_rsrc(p.x0 ? p.x0 + bh * ssz : nullptr, p.x0 ? ssz : 0);
+#pragma unroll
+    for (int ib = 0; ib < T2; ib++)
+#pragma unroll
+        for (int jb = 0; jb < T2; jb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int xr = r0 + wr + 16 * ib + 4 * lg + i, xc = c0 + wc + 16 * jb + lr;
+                ok[ib][jb][i] = xr < Kq && xc < Vd;
+                off[ib][jb][i] = ((uint32_t)xr * (uint32_t)Vd + (uint32_t)xc) * 4u;
+                x[ib][jb][i] = bw_load(rx0, off[ib][jb][i], ok[ib][jb][i]);
+            }
+    float sv[T2][T2][4] = {};
+    const auto fetch_state = [&](int n) {
+        const bw_rsrc_t rs = bw_rsrc(p.S + (bh * (N + 1) + n) * ssz, ssz);
+#pragma unroll
+        for (int ib = 0; ib < T2; ib++)
+#pragma unroll
+            for (int jb = 0; jb < T2; jb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) sv[ib][jb][i] = bw_load(rs, off[ib][jb][i], ok[ib][jb][i]);
+    };
+    const auto keep = [&](int n) {  // xs[n] = X; returns the lane's part of <X, S[n]> (backward)
+        const bw_rsrc_t rs = bw_rsrc(xs + (size_t)n * ssz, ssz);
+        float dot = 0.f;
+#pragma unroll
+        for (int ib = 0; ib < T2; ib++)
+#pragma unroll
+            for (int jb = 0; jb < T2; jb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    bw_store(rs, off[ib][jb][i], ok[ib][jb][i], x[ib][jb][i]);
+                    if constexpr (BWD) dot = fmaf(x[ib][jb][i], sv[ib][jb][i], dot);
+                }
+        return dot;
+    };
+    const int sr = tid % TS, sq = tid / TS;  // staging: row / column sr, tokens TPT sq ..
+    const bw_rsrc_t rgt = bw_rsrc(p.g, (size_t)p.B * p.T * p.H);  // B T H < 2^21 (host)
+    // chunk n's rows of a, columns of b and gate into (ra, rb, rg)
+    const auto fetch = [&](int n, float* ra, float* rb, float& rg) {
+        const int t0 = n * BC;
+        const bw_rsrc_t rA = bw_rsrc(A + (size_t)t0 * Kq, (size_t)BC * Kq), rBm = bw_rsrc(Bm + (size_t)t0 * Vd, (size_t)BC * Vd);
+#pragma unroll
+        for (int i = 0; i < TPT; i++) {
+            const uint32_t t = TPT * sq + i;
+            ra[i] = bw_load(rA, (t * (uint32_t)Kq + (uint32_t)(r0 + sr)) * 4u, r0 + sr < Kq);
+            rb[i] = bw_load(rBm, (t * (uint32_t)Vd + (uint32_t)(c0 + sr)) * 4u, c0 + sr < Vd);
+        }
+        rg = bw_load(rgt, (((uint32_t)b * (uint32_t)p.T + (uint32_t)(t0 + lane)) * (uint32_t)p.H + (uint32_t)h) * 4u,
+                     t0 + lane < p.T);
+    };
+    const auto chunk_of = [&](int step) { return BWD ? N - 1 - step : step; };
+    // One chunk step from the registers (ra, rb, rg), which then receive the
+    // next chunk. (Two register sets, with the chunk two steps on in flight,
+    // were slower: 83 -> 93 us for the forward scan at configuration 3; the
+    // scan is bound by each compute unit's reads, not by their latency.)
+    const auto run_step = [&](int step, float* ra, float* rb, float& rg) {
+        const int n = chunk_of(step);
+        const float dot = keep(BWD ? n + 1 : n);
+        __syncthreads();  // the previous chunk's operands are done with
+        float wsum = 0.f;
+        if constexpr (BWD) {
+            wsum = bw_wave_sum(dot);
+            if (T2 == 1 && lane == 0) sRed[wv] = wsum;
+        }
+        if (wv == 0) {  // G: the in-chunk inclusive cumsum of the prefetched gate
+            float G = rg;
+            for (int o = 1; o < 64; o <<= 1) {
+                const float y = __shfl_up(G, o);
+                if (lane >= o) G += y;
+            }
+            const float Gl = __shfl(G, 63);
+            sF[lane] = BWD ? p.scale * expf(G) : expf(Gl - G);
+            if (lane == 0) sEl = expf(Gl);
+        }
+#pragma unroll
+        for (int u = 0; u < TPT / 8; u++) {
+            bf16x8 hi, lo;
+            split_bf16x8(rb + 8 * u, hi, lo);
+            *reinterpret_cast<bf16x8*>(&sBh[sr][TPT * sq + 8 * u]) = hi;
+            *reinterpret_cast<bf16x8*>(&sBl[sr][TPT * sq + 8 * u]) = lo;
+        }
+        __syncthreads();  // sF is read below
+#pragma unroll
+        for (int u = 0; u < TPT / 8; u++) {
+            float fa[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) fa[i] = sF[TPT * sq + 8 * u + i] * ra[8 * u + i];
+            bf16x8 hi, lo;
+            split_bf16x8(fa, hi, lo);
+            *reinterpret_cast<bf16x8*>(&sAh[sr][TPT * sq + 8 * u]) = hi;
+            *reinterpret_cast<bf16x8*>(&sAl[sr][TPT * sq + 8 * u]) = lo;
+        }
+        __syncthreads();
+        if (step + 1 < N) fetch(chunk_of(step + 1), ra, rb, rg);
+        if constexpr (BWD) fetch_state(n);  // for the next step's keep(n)
+        if constexpr (BWD) {
+            if (T2 == 1 && tid == 0)
+                p.bnd[(bh * nt + ty * nx + tx) * N + n] = (sRed[0] + sRed[1]) + (sRed[2] + sRed[3]);
+            if (T2 == 2 && lane == 0 && ty < ny && tx < nx) p.bnd[(bh * nt + ty * nx + tx) * N + n] = wsum;
+        }
+        const float el = sEl;
+#pragma unroll
+        for (int ib = 0; ib < T2; ib++)
+#pragma unroll
+            for (int jb = 0; jb < T2; jb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) x[ib][jb][i] *= el;
+#pragma unroll
+        for (int s = 0; s < BC / 32; s++) {
+            bf16x8 ah[T2], al[T2], bh8[T2], bl8[T2];
+#pragma unroll
+            for (int ib = 0; ib < T2; ib++) {
+                ah[ib] = *reinterpret_cast<const bf16x8*>(&sAh[wr + 16 * ib + lr][32 * s + 8 * lg]);
+                al[ib] = *reinterpret_cast<const bf16x8*>(&sAl[wr + 16 * ib + lr][32 * s + 8 * lg]);
+            }
+#pragma unroll
+            for (int jb = 0; jb < T2; jb++) {
+                bh8[jb] = *reinterpret_cast<const bf16x8*>(&sBh[wc + 16 * jb + lr][32 * s + 8 * lg]);
+                bl8[jb] = *reinterpret_cast<const bf16x8*>(&sBl[wc + 16 * jb + lr][32 * s + 8 * lg]);
+            }
+#pragma unroll
+            for (int ib = 0; ib < T2; ib++)
+#pragma unroll
+                for (int jb = 0; jb < T2; jb++) {
+                    x[ib][jb] = mfma_bf16(al[ib], bh8[jb], x[ib][jb]);
+                    x[ib][jb] = mfma_bf16(ah[ib], bl8[jb], x[ib][jb]);
+                    x[ib][jb] = mfma_bf16(ah[ib], bh8[jb], x[ib][jb]);
+                }
+        }
+    };
+    float ra[TPT], rb[TPT], rg;
+    fetch(chunk_of(0), ra, rb, rg);
+    if constexpr (BWD) fetch_state(N);
+    for (int step = 0; step < N; step++) run_step(step, ra, rb, rg);
+    keep(BWD ? 0 : N);
+    const bw_rsrc_t rxo = bw_rsrc(p.x_out ? p.x_out + bh * ssz : nullptr, p.x_out ? ssz : 0);
+#pragma unroll
+    for (int ib = 0; ib < T2; ib++)
+#pragma unroll
+        for (int jb = 0; jb < T2; jb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) bw_store(rxo, off[ib][jb][i], ok[ib][jb][i], x[ib][jb][i]);  // dropped without x_out
+}
+
+// Launches the scan over a [Kq, Vd] state (grid: the FMA form's 32 x 32
+// tiles): the matrix-core form for bf16 operands, with 64 x 64 tiles when
+// they still give a workgroup per compute unit.
+template <bool BWD>
+void launch_state_scan(const StateScanArgs& a, bool mfma, hipStream_t stream) {
+    const dim3 g32((a.Vd + 31) / 32, (a.Kq + 31) / 32, a.B * a.H), g64((a.Vd + 63) / 64, (a.Kq + 63) / 64, a.B * a.H);
+    if (!mfma)
+        hipLaunchKernelGGL(bw_state_scan_kernel<BWD>, g32, dim3(256), 0, stream, a);
+    else if ((long long)g64.x * g64.y * g64.z >= device_cu_count())
+        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, 2>), g64, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, 1>), g32, dim3(256), 0, stream, a);
 }
 
 // Tile GEMMs of the chunk kernels: a 64 x 64 output tile (rows = the chunk's
@@ -311,8 +552,61 @@ struct TileMap {
     }
 };
 
+// Global operands of tile_gemm, read through a buffer resource over the
+// operand's region with every out-of-range element predicated to zero through
+// its offset (so the next k-block's loads overlap the current one's products).
+//  RowsK: element (m, kk) = base[m ld + kk] for m < nm, kk < nk (the A
+//         operand, m = the tile row, and a B operand contiguous along kk,
+//         m = the tile column).
+//  RowsJ: element (kk, j) = base[kk ld + j] for kk < nk, j < nj (a B operand
+//         contiguous along j).
+struct RowsK {
+    bw_rsrc_t r;
+    uint32_t ld;
+    int nm, nk;
+    __device__ RowsK(const float* base, int ld_, int nm_, int nk_)
+        : r(bw_rsrc(base, nm_ > 0 ? (size_t)(nm_ - 1) * ld_ + nk_ : 0)), ld((uint32_t)ld_), nm(nm_), nk(nk_) {}
+    __device__ float load(int m, int kk) const {
+        const uint32_t dead = (m < nm && kk < nk) ? 0u : BW_DEAD;
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, ((uint32_t)m * ld + (uint32_t)kk) * 4u | dead, 0, 0));
+    }
+};
+
+struct RowsJ {
+    bw_rsrc_t r;
+    uint32_t ld;
+    int nk, nj;
+    __device__ RowsJ(const float* base, int ld_, int nk_, int nj_)
+        : r(bw_rsrc(base, nk_ > 0 ? (size_t)(nk_ - 1) * ld_ + nj_ : 0)), ld((uint32_t)ld_), nk(nk_), nj(nj_) {}
+    __device__ float load(int kk, int j) const {
+        const uint32_t dead = (kk < nk && j < nj) ? 0u : BW_DEAD;
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, ((uint32_t)kk * ld + (uint32_t)j) * 4u | dead, 0, 0));
+    }
+};
+
+// Element (i, kk) of A and (kk, j) of B, for a global operand or a callable
+// (LDS operands: read only at kk < Kd, contractions of BC tokens).
+template <class FA>
+__device__ __forceinline__ float opA(const FA& fa, int i, int kk, int Kd) {
+    if constexpr (std::is_same_v<FA, RowsK>)
+        return fa.load(i, kk);
+    else
+        return kk < Kd ? fa(i, kk) : 0.f;
+}
+template <class FB>
+__device__ __forceinline__ float opB(const FB& fb, int kk, int j, int Kd) {
+    if constexpr (std::is_same_v<FB, RowsK>)
+        return fb.load(j, kk);
+    else if constexpr (std::is_same_v<FB, RowsJ>)
+        return fb.load(kk, j);
+    else
+        return kk < Kd ? fb(kk, j) : 0.f;
+}
+
 template <bool MF, bool B_KCONTIG, class FA, class FB>
 __device__ __forceinline__ void tile_gemm(FA fa, FB fb, int Kd, unsigned char* stage, float acc[4][4]) {
+    static_assert(!std::is_same_v<FB, RowsK> || B_KCONTIG, "RowsK: B contiguous along kk");
+    static_assert(!std::is_same_v<FB, RowsJ> || !B_KCONTIG, "RowsJ: B contiguous along j");
     const int tid = threadIdx.x;
     if constexpr (!MF) {
         float(*sa)[GT_LD] = reinterpret_cast<float(*)[GT_LD]>(stage);
@@ -325,9 +619,9 @@ __device__ __forceinline__ void tile_gemm(FA fa, FB fb, int Kd, unsigned char* s
             for (int x = 0; x < NE; x++) {
                 const int e = tid + 256 * x;
                 const int ka = e % GT_K, i = e / GT_K;
-                ra[x] = k0 + ka < Kd ? fa(i, k0 + ka) : 0.f;
+                ra[x] = opA(fa, i, k0 + ka, Kd);
                 const int kb = B_KCONTIG ? e % GT_K : e / BC, j = B_KCONTIG ? e / GT_K : e % BC;
-                rb[x] = k0 + kb < Kd ? fb(k0 + kb, j) : 0.f;
+                rb[x] = opB(fb, k0 + kb, j, Kd);
             }
         };
         fetch(0);
@@ -367,8 +661,8 @@ __device__ __forceinline__ void tile_gemm(FA fa, FB fb, int Kd, unsigned char* s
 #pragma unroll
             for (int x = 0; x < 8; x++) {
                 const int kk = k0 + 8 * kg + x;
-                ra[x] = kk < Kd ? fa(r, kk) : 0.f;
-                rb[x] = kk < Kd ? fb(kk, r) : 0.f;
+                ra[x] = opA(fa, r, kk, Kd);
+                rb[x] = opB(fb, kk, r, Kd);
             }
         };
         fetch(0);
@@ -436,8 +730,7 @@ template <bool MF>
 __device__ __forceinline__ void chunk_scores(const float* X, const float* Y, int D, const float* sG,
                                              unsigned char* stage, float (*P)[BC + 1]) {
     float acc[4][4] = {};
-    tile_gemm<MF, true>([&](int i, int kk) { return X[(size_t)i * D + kk]; },
-                        [&](int kk, int j) { return Y[(size_t)j * D + kk]; }, D, stage, acc);
+    tile_gemm<MF, true>(RowsK(X, D, BC, D), RowsK(Y, D, BC, D), D, stage, acc);
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
@@ -483,13 +776,10 @@ __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
     float* out = a.out + (bh * a.Tp + t0) * Vd;
     for (int d0 = 0; d0 < Vd; d0 += BC) {
         float acc[4][4] = {};
-        tile_gemm<MF, false>([&](int i, int kk) { return q[(size_t)i * Kq + kk]; },
-                             [&](int kk, int j) { return d0 + j < Vd ? S[(size_t)kk * Vd + d0 + j] : 0.f; }, Kq,
-                             sStage, acc);
+        tile_gemm<MF, false>(RowsK(q, Kq, BC, Kq), RowsJ(S + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
         tile_scale_rows<MF>(acc, [&](int t) { return sEq[t]; });
-        tile_gemm<MF, false>([&](int i, int kk) { return sA[i][kk]; },
-                             [&](int kk, int j) { return d0 + j < Vd ? v[(size_t)kk * Vd + d0 + j] : 0.f; }, BC,
-                             sStage, acc);
+        tile_gemm<MF, false>([&](int i, int kk) { return sA[i][kk]; }, RowsJ(v + d0, Vd, BC, Vd - d0), BC, sStage,
+                             acc);
         if (!a.out_bthd) {
             if (a.bf16) {
 #pragma unroll
@@ -534,7 +824,9 @@ template <bool MF>
 __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     __shared__ float sA[BC][BC + 1], sB[BC][BC + 1];
     __shared__ __align__(16) unsigned char sStage[STAGE_BYTES];
-    __shared__ float sG[BC], sEq[BC], sEl[BC];
+    // (the row factors e^{G_t} and e^{G_last - G_t} are formed where used:
+    // without their two arrays the LDS allows three workgroups per CU)
+    __shared__ float sG[BC];
     const int tid = threadIdx.x, n = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int Kq = a.Kq, Vd = a.Vd, t0 = n * BC;
     const size_t bh = (size_t)b * a.H + h, ssz = (size_t)Kq * Vd;
@@ -547,8 +839,6 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     if (tid < 64) {
         const float G = chunk_gam(a.g, b, h, a.T, a.H, n, tid);
         sG[tid] = G;
-        sEq[tid] = expf(G);
-        sEl[tid] = expf(__shfl(G, BC - 1) - G);
     }
     chunk_scores<MF>(q, k, Kq, sG, sStage, sA);
     chunk_scores<MF>(dO, v, Vd, sG, sStage, sB);
@@ -556,37 +846,28 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     for (int d0 = 0; d0 < Kq; d0 += BC) {
         // dq = scale (e^{G_t} dO_t S_n^T + B k)
         float acc[4][4] = {};
-        tile_gemm<MF, true>([&](int i, int kk) { return dO[(size_t)i * Vd + kk]; },
-                            [&](int kk, int j) { return d0 + j < Kq ? S[(size_t)(d0 + j) * Vd + kk] : 0.f; }, Vd,
-                            sStage, acc);
-        tile_scale_rows<MF>(acc, [&](int t) { return sEq[t]; });
-        tile_gemm<MF, false>([&](int i, int kk) { return sB[i][kk]; },
-                             [&](int kk, int j) { return d0 + j < Kq ? k[(size_t)kk * Kq + d0 + j] : 0.f; }, BC,
-                             sStage, acc);
+        tile_gemm<MF, true>(RowsK(dO, Vd, BC, Vd), RowsK(S + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
+        tile_scale_rows<MF>(acc, [&](int t) { return expf(sG[t]); });
+        tile_gemm<MF, false>([&](int i, int kk) { return sB[i][kk]; }, RowsJ(k + d0, Kq, BC, Kq - d0), BC, sStage,
+                             acc);
         tile_store<MF>(acc, a.dq + (bh * a.Tp + t0) * Kq, Kq, d0, sc);
         // dk = e^{G_last - G_s} v_s D_{n+1}^T + scale B^T q
 #pragma unroll
         for (int x = 0; x < 4; x++)
 #pragma unroll
             for (int y = 0; y < 4; y++) acc[x][y] = 0.f;
-        tile_gemm<MF, true>([&](int i, int kk) { return v[(size_t)i * Vd + kk]; },
-                            [&](int kk, int j) { return d0 + j < Kq ? D[(size_t)(d0 + j) * Vd + kk] : 0.f; }, Vd,
-                            sStage, acc);
-        tile_scale_rows<MF>(acc, [&](int t) { return sEl[t]; });
-        tile_gemm<MF, false>([&](int i, int kk) { return sc * sB[kk][i]; },
-                             [&](int kk, int j) { return d0 + j < Kq ? q[(size_t)kk * Kq + d0 + j] : 0.f; }, BC,
+        tile_gemm<MF, true>(RowsK(v, Vd, BC, Vd), RowsK(D + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
+        tile_scale_rows<MF>(acc, [&](int t) { return expf(sG[BC - 1] - sG[t]); });
+        tile_gemm<MF, false>([&](int i, int kk) { return sc * sB[kk][i]; }, RowsJ(q + d0, Kq, BC, Kq - d0), BC,
                              sStage, acc);
         tile_store<MF>(acc, a.dk + (bh * a.Tp + t0) * Kq, Kq, d0, 1.f);
     }
     for (int d0 = 0; d0 < Vd; d0 += BC) {
         // dv = e^{G_last - G_s} k_s D_{n+1} + scale A^T dO
         float acc[4][4] = {};
-        tile_gemm<MF, false>([&](int i, int kk) { return k[(size_t)i * Kq + kk]; },
-                             [&](int kk, int j) { return d0 + j < Vd ? D[(size_t)kk * Vd + d0 + j] : 0.f; }, Kq,
-                             sStage, acc);
-        tile_scale_rows<MF>(acc, [&](int t) { return sEl[t]; });
-        tile_gemm<MF, false>([&](int i, int kk) { return sc * sA[kk][i]; },
-                             [&](int kk, int j) { return d0 + j < Vd ? dO[(size_t)kk * Vd + d0 + j] : 0.f; }, BC,
+        tile_gemm<MF, false>(RowsK(k, Kq, BC, Kq), RowsJ(D + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
+        tile_scale_rows<MF>(acc, [&](int t) { return expf(sG[BC - 1] - sG[t]); });
+        tile_gemm<MF, false>([&](int i, int kk) { return sc * sA[kk][i]; }, RowsJ(dO + d0, Vd, BC, Vd - d0), BC,
                              sStage, acc);
         tile_store<MF>(acc, a.dv + (bh * a.Tp + t0) * Vd, Vd, d0, 1.f);
     }
@@ -1309,11 +1590,6 @@ __global__ __launch_bounds__(256) void bw_pack_kernel(const float* src, int B, i
     bw_st<BF>(dst, i, src[(((size_t)b * H + h) * Tp + t) * D + j]);
 }
 
-// The scan's grid for a [Kq, Vd] matrix: (column tiles, row tiles, B*H).
-dim3 scan_grid(int Vd, int Kq, int BH) {
-    return dim3((Vd + BW_TILE - 1) / BW_TILE, (Kq + SCAN_ROWS - 1) / SCAN_ROWS, BH);
-}
-
 void launch_chunk_grad(const ChunkGradArgs& a, bool mfma, hipStream_t stream) {
     if (mfma)
         hipLaunchKernelGGL(bw_chunk_kernel<true>, dim3(a.N, a.H, a.B), dim3(256), 0, stream, a);
@@ -1343,7 +1619,7 @@ int launch_chunk_pass(const ChunkPassParams& p, hipStream_t stream) {
     sa.Vd = p.Vd;
     sa.N = N;
     sa.scale = 1.f;
-    hipLaunchKernelGGL(bw_state_scan_kernel<false>, scan_grid(p.Vd, p.Kq, p.B * p.H), dim3(256), 0, stream, sa);
+    launch_state_scan<false>(sa, p.mfma, stream);
     OutArgs oa{};
     oa.q = p.q;
     oa.k = p.k;
@@ -1497,7 +1773,7 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     f2.xs = ws.sv;
     f2.Kq = M;
     f2.Vd = V;
-    hipLaunchKernelGGL(bw_state_scan_kernel<false>, scan_grid(V, M, B * H), blk, 0, stream, f2);
+    launch_state_scan<false>(f2, bf, stream);
     // pass 2: state cotangents, then the rows' (slot weights, write vector, v)
     StateScanArgs s2 = f2;
     s2.a = ws.wts;
@@ -1507,7 +1783,7 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     s2.S = ws.sv;
     s2.bnd = ws.bnd2;
     s2.x_out = p.dh0_v;
-    hipLaunchKernelGGL(bw_state_scan_kernel<true>, scan_grid(V, M, B * H), blk, 0, stream, s2);
+    launch_state_scan<true>(s2, bf, stream);
     ChunkGradArgs c2{};
     c2.q = ws.wts;
     c2.k = ws.w;
@@ -1563,7 +1839,7 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     s1.bnd = ws.bnd1;
     s1.x_out = p.dh0_k;
     s1.scale = p.scale;
-    hipLaunchKernelGGL(bw_state_scan_kernel<true>, scan_grid(M, K, B * H), blk, 0, stream, s1);
+    launch_state_scan<true>(s1, bf, stream);
     ChunkGradArgs c1 = c2;
     c1.q = ws.qh;
     c1.k = ws.kh;
