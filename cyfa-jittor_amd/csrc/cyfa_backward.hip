@@ -100,6 +100,31 @@ __global__ __launch_bounds__(256) void bw_rows_kernel(const void* x, const float
         return;
     }
     const size_t src = (((size_t)b * T + t) * H + h) * D;
+    if (D == 256 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0) {
+        // the tuned head size (16-byte aligned rows): four consecutive
+        // elements per lane, one pass over x
+        float v[4];
+        if constexpr (BF) {
+            const bf16x4 xv = *reinterpret_cast<const bf16x4*>(reinterpret_cast<const bf16_t*>(x) + src + 4 * lane);
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] = (float)xv[e];
+        } else {
+            const float4 xv = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + src + 4 * lane);
+            v[0] = xv.x, v[1] = xv.y, v[2] = xv.z, v[3] = xv.w;
+        }
+        float4 o = {v[0], v[1], v[2], v[3]};
+        if (w) {
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) ss = fmaf(v[e], v[e], ss);
+            const float rs = rsqrtf(bw_wave_sum(ss) / (float)D + eps);
+            const float4 wv = *reinterpret_cast<const float4*>(w + 4 * lane);
+            o = float4{v[0] * rs * wv.x, v[1] * rs * wv.y, v[2] * rs * wv.z, v[3] * rs * wv.w};
+            if (rs_out && lane == 0) rs_out[row] = rs;
+        }
+        *reinterpret_cast<float4*>(dst + 4 * lane) = o;
+        return;
+    }
     if (!w) {
         for (int i = lane; i < D; i += 64) dst[i] = bw_ld<BF>(x, src + i);
         return;
@@ -1491,49 +1516,111 @@ __global__ __launch_bounds__(64) void bw_clock_kernel(const float* dlam, const f
 // eps)^-1/2): dx = rs w dx_hat - rs^3 / D (sum_i x_i w_i dx_hat_i) x, and
 // per block the partial dw = sum_rows dx_hat x rs. A workgroup takes 64 rows
 // (16 per wave, in order), lanes own coordinates j = lane + 64 jj.
-template <bool BF>
+template <bool BF, int NJ>
 __global__ __launch_bounds__(256) void bw_norm_kernel(const void* x, const float* w, const float* rs,
                                                       const float* dxh, int B, int T, int Tp, int H, int D, void* dx,
                                                       float* dw_part) {
-    constexpr int NJ = BW_MAX_D / 64;
-    __shared__ float sdw[4][BW_MAX_D];
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, blk = blockIdx.x;
+    // Lane l holds columns l + 64 jj (jj < NJ, NJ 64 >= D); the global
+    // accesses go through buffer resources over one row, columns past D
+    // predicated through the offset (no branch among the loads), and a wave
+    // takes its rows in groups of RB: every load of a group is issued before
+    // the first row's arithmetic, so the group waits for memory once.
+    constexpr int ES = BF ? 2 : 4;
+    constexpr int RPW = BWD_NORM_ROWS / 4;                   // rows per wave
+    constexpr int RB = 32 / NJ < RPW ? (32 / NJ > 0 ? 32 / NJ : 1) : RPW;
+    static_assert(RPW % RB == 0, "whole groups");
+    __shared__ float sdw[4][NJ * 64];
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, blk = blockIdx.x;
     const int total = B * T * H;
-    float dwa[NJ];
+    float dwa[NJ], wj[NJ];
+    const bw_rsrc_t rw = bw_rsrc(w, (size_t)D);
 #pragma unroll
-    for (int jj = 0; jj < NJ; jj++) dwa[jj] = 0.f;
-    for (int i = 0; i < BWD_NORM_ROWS / 4; i++) {
-        const int row = blk * BWD_NORM_ROWS + wv * (BWD_NORM_ROWS / 4) + i;
-        if (row >= total) break;
-        const int h = row % H, t = (row / H) % T, b = row / (H * T);
-        const size_t hm = ((size_t)b * H + h) * Tp + t;
-        const float r = rs[hm];
-        float sum = 0.f;
+    for (int jj = 0; jj < NJ; jj++) {
+        dwa[jj] = 0.f;
+        wj[jj] = bw_load(rw, (uint32_t)(lane + 64 * jj) * 4u, lane + 64 * jj < D);
+    }
+    const int row0 = blk * BWD_NORM_ROWS + wv * RPW;
+    for (int g = 0; g < RPW; g += RB) {
+        float xv[RB][NJ], dv[RB][NJ], r[RB];
+        bool live[RB];
 #pragma unroll
-        for (int jj = 0; jj < NJ; jj++) {
-            const int j = lane + 64 * jj;
-            if (j < D) {
-                const float xv = bw_ld<BF>(x, (size_t)row * D + j), dv = dxh[hm * D + j];
-                sum = fmaf(xv * w[j], dv, sum);
-                dwa[jj] = fmaf(dv * xv, r, dwa[jj]);
+        for (int k = 0; k < RB; k++) {
+            const int row = row0 + g + k;
+            live[k] = row < total;
+            // (the row and its coordinates through readfirstlane: in vector
+            // registers, every buffer access built on them would become a
+            // waterfall loop)
+            const int rr = __builtin_amdgcn_readfirstlane(live[k] ? row : 0);
+            const int h = __builtin_amdgcn_readfirstlane(rr % H), t = __builtin_amdgcn_readfirstlane((rr / H) % T),
+                      b = __builtin_amdgcn_readfirstlane(rr / (H * T));
+            const size_t hm = ((size_t)b * H + h) * Tp + t;
+            const bw_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<char*>(reinterpret_cast<const char*>(x)) + (size_t)rr * D * ES, (short)0, live[k] ? D * ES : 0,
+                0x00020000);
+            const bw_rsrc_t rd = bw_rsrc(dxh + hm * D, live[k] ? (size_t)D : 0);
+#pragma unroll
+            for (int jj = 0; jj < NJ; jj++) {
+                const int j = lane + 64 * jj;
+                const uint32_t dead = j < D ? 0u : BW_DEAD;
+                if constexpr (BF)
+                    xv[k][jj] = (float)__builtin_bit_cast(
+                        bf16_t, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rx, ((uint32_t)j * 2u) | dead, 0, 0));
+                else
+                    xv[k][jj] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, ((uint32_t)j * 4u) | dead, 0, 0));
+                dv[k][jj] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, ((uint32_t)j * 4u) | dead, 0, 0));
             }
+            r[k] = bw_load(bw_rsrc(rs + hm, 1), 0u, live[k]);
         }
-        const float cr = r * r * r * bw_wave_sum(sum) / (float)D;
 #pragma unroll
-        for (int jj = 0; jj < NJ; jj++) {
-            const int j = lane + 64 * jj;
-            if (j < D) {
-                const float xv = bw_ld<BF>(x, (size_t)row * D + j);
-                bw_st<BF>(dx, (size_t)row * D + j, r * w[j] * dxh[hm * D + j] - cr * xv);
+        for (int k = 0; k < RB; k++) {
+            const int row = row0 + g + k;
+            float sum = 0.f;
+#pragma unroll
+            for (int jj = 0; jj < NJ; jj++) {
+                sum = fmaf(xv[k][jj] * wj[jj], dv[k][jj], sum);
+                dwa[jj] = fmaf(dv[k][jj] * xv[k][jj], r[k], dwa[jj]);  // zero for a row past the end
+            }
+            const float cr = r[k] * r[k] * r[k] * bw_wave_sum(sum) / (float)D;
+            const bw_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<char*>(dx) + (size_t)(live[k] ? row : 0) * D * ES,
+                                                                   (short)0, live[k] ? D * ES : 0, 0x00020000);
+#pragma unroll
+            for (int jj = 0; jj < NJ; jj++) {
+                const int j = lane + 64 * jj;
+                const uint32_t dead = j < D ? 0u : BW_DEAD;
+                const float o = r[k] * wj[jj] * dv[k][jj] - cr * xv[k][jj];
+                if constexpr (BF)
+                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (bf16_t)o), ro,
+                                                          ((uint32_t)j * 2u) | dead, 0, 0);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, o), ro, ((uint32_t)j * 4u) | dead, 0, 0);
             }
         }
     }
 #pragma unroll
-    for (int jj = 0; jj < NJ; jj++)
-        if (lane + 64 * jj < D) sdw[wv][lane + 64 * jj] = dwa[jj];
+    for (int jj = 0; jj < NJ; jj++) sdw[wv][lane + 64 * jj] = dwa[jj];
     __syncthreads();
     for (int j = threadIdx.x; j < D; j += 256)
         dw_part[(size_t)blk * D + j] = (sdw[0][j] + sdw[1][j]) + (sdw[2][j] + sdw[3][j]);
+}
+
+// bw_norm_kernel for D columns: NJ the power of two with 64 NJ >= D.
+template <bool BF>
+void launch_norm_adjoint(dim3 nb, const void* x, const float* w, const float* rs, const float* dxh, int B, int T,
+                         int Tp, int H, int D, void* dx, float* dw_part, hipStream_t stream) {
+    const dim3 blk(256);
+#define CYFA_BW_NORM(NJ_) \
+    hipLaunchKernelGGL((bw_norm_kernel<BF, NJ_>), nb, blk, 0, stream, x, w, rs, dxh, B, T, Tp, H, D, dx, dw_part)
+    if (D <= 64)
+        CYFA_BW_NORM(1);
+    else if (D <= 128)
+        CYFA_BW_NORM(2);
+    else if (D <= 256)
+        CYFA_BW_NORM(4);
+    else if (D <= 512)
+        CYFA_BW_NORM(8);
+    else
+        CYFA_BW_NORM(16);
+#undef CYFA_BW_NORM
 }
 
 // out[i] = sum over the nb partial rows of part[.][i]: one wave per column,
@@ -1582,6 +1669,25 @@ __global__ __launch_bounds__(256) void bw_dreadout_kernel(const float* dtable, i
 // Head-major fp32 [B*H, Tp, D] rows into [B, T, H, D] in the operands' dtype.
 template <bool BF>
 __global__ __launch_bounds__(256) void bw_pack_kernel(const float* src, int B, int T, int Tp, int H, int D, void* dst) {
+    // four consecutive elements per thread (D % 4 == 0, the launcher checks;
+    // a row's four never straddle two rows)
+    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4, n = (size_t)B * T * H * D;
+    if (i >= n) return;
+    const int j = (int)(i % D);
+    const size_t row = i / D;
+    const int h = (int)(row % H), t = (int)((row / H) % T), b = (int)(row / ((size_t)H * T));
+    const float4 v = *reinterpret_cast<const float4*>(src + (((size_t)b * H + h) * Tp + t) * D + j);
+    if constexpr (BF) {
+        const bf16x4 o = {(bf16_t)v.x, (bf16_t)v.y, (bf16_t)v.z, (bf16_t)v.w};
+        *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16_t*>(dst) + i) = o;
+    } else {
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(dst) + i) = v;
+    }
+}
+
+// The same, one element per thread (any D, any alignment of dst).
+template <bool BF>
+__global__ __launch_bounds__(256) void bw_pack1_kernel(const float* src, int B, int T, int Tp, int H, int D, void* dst) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, n = (size_t)B * T * H * D;
     if (i >= n) return;
     const int j = (int)(i % D);
@@ -1888,25 +1994,26 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     // the q/k norms, their weights, v's layout
     const dim3 nb(ws.norm_blocks);
     if (bf) {
-        hipLaunchKernelGGL(bw_norm_kernel<true>, nb, blk, 0, stream, p.q, p.q_w, ws.rq, ws.dqh, B, T, Tp, H, K, p.dq,
-                           ws.dnq);
-        hipLaunchKernelGGL(bw_norm_kernel<true>, nb, blk, 0, stream, p.k, p.k_w, ws.rk, ws.dkh, B, T, Tp, H, K, p.dk,
-                           ws.dnk);
+        launch_norm_adjoint<true>(nb, p.q, p.q_w, ws.rq, ws.dqh, B, T, Tp, H, K, p.dq, ws.dnq, stream);
+        launch_norm_adjoint<true>(nb, p.k, p.k_w, ws.rk, ws.dkh, B, T, Tp, H, K, p.dk, ws.dnk, stream);
     } else {
-        hipLaunchKernelGGL(bw_norm_kernel<false>, nb, blk, 0, stream, p.q, p.q_w, ws.rq, ws.dqh, B, T, Tp, H, K, p.dq,
-                           ws.dnq);
-        hipLaunchKernelGGL(bw_norm_kernel<false>, nb, blk, 0, stream, p.k, p.k_w, ws.rk, ws.dkh, B, T, Tp, H, K, p.dk,
-                           ws.dnk);
+        launch_norm_adjoint<false>(nb, p.q, p.q_w, ws.rq, ws.dqh, B, T, Tp, H, K, p.dq, ws.dnq, stream);
+        launch_norm_adjoint<false>(nb, p.k, p.k_w, ws.rk, ws.dkh, B, T, Tp, H, K, p.dk, ws.dnk, stream);
     }
     const dim3 kb((unsigned)((K + 3) / 4));
     hipLaunchKernelGGL(bw_reduce_kernel, kb, blk, 0, stream, ws.dnq, ws.norm_blocks, (size_t)K, p.dq_w);
     hipLaunchKernelGGL(bw_reduce_kernel, kb, blk, 0, stream, ws.dnk, ws.norm_blocks, (size_t)K, p.dk_w);
     const size_t nv = (size_t)B * T * H * V;
-    const dim3 vb((unsigned)((nv + 255) / 256));
-    if (bf)
-        hipLaunchKernelGGL(bw_pack_kernel<true>, vb, blk, 0, stream, ws.dvh, B, T, Tp, H, V, p.dv);
+    const dim3 vb((unsigned)((nv + 255) / 256)), vb4((unsigned)((nv / 4 + 255) / 256));
+    const bool pack4 = V % 4 == 0 && ((uintptr_t)p.dv & (bf ? 7 : 15)) == 0;
+    if (bf && pack4)
+        hipLaunchKernelGGL(bw_pack_kernel<true>, vb4, blk, 0, stream, ws.dvh, B, T, Tp, H, V, p.dv);
+    else if (pack4)
+        hipLaunchKernelGGL(bw_pack_kernel<false>, vb4, blk, 0, stream, ws.dvh, B, T, Tp, H, V, p.dv);
+    else if (bf)
+        hipLaunchKernelGGL(bw_pack1_kernel<true>, vb, blk, 0, stream, ws.dvh, B, T, Tp, H, V, p.dv);
     else
-        hipLaunchKernelGGL(bw_pack_kernel<false>, vb, blk, 0, stream, ws.dvh, B, T, Tp, H, V, p.dv);
+        hipLaunchKernelGGL(bw_pack1_kernel<false>, vb, blk, 0, stream, ws.dvh, B, T, Tp, H, V, p.dv);
     const int RM = (M - 1) * M;
     hipLaunchKernelGGL(bw_table_reduce_kernel, dim3((RM + 255) / 256, H), blk, 0, stream, ws.dtab, ws.ro_blocks, RM,
                        p.dtable);
