@@ -597,6 +597,19 @@ struct RowsK {
     }
 };
 
+// RowsK with 16-byte loads of four consecutive kk: the caller guarantees a
+// 16-byte aligned base and ld, nk multiples of 4. In tile_gemm's matrix-core
+// staging, lane (r, kg) then loads kk = k0 + 4 kg .. + 3 and k0 + 16 + 4 kg ..
+// + 3, so that each load instruction covers 64 contiguous bytes of 16 rows
+// (with one 4-byte load per kk, eight instructions each touched 16 lines).
+struct RowsK4 : RowsK {
+    __device__ RowsK4(const float* base, int ld_, int nm_, int nk_) : RowsK(base, ld_, nm_, nk_) {}
+    __device__ f32x4 load4(int m, int kk0) const {
+        const uint32_t dead = (m < nm && kk0 < nk) ? 0u : BW_DEAD;
+        return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, ((uint32_t)m * ld + (uint32_t)kk0) * 4u | dead, 0, 0));
+    }
+};
+
 struct RowsJ {
     bw_rsrc_t r;
     uint32_t ld;
@@ -613,14 +626,14 @@ struct RowsJ {
 // (LDS operands: read only at kk < Kd, contractions of BC tokens).
 template <class FA>
 __device__ __forceinline__ float opA(const FA& fa, int i, int kk, int Kd) {
-    if constexpr (std::is_same_v<FA, RowsK>)
+    if constexpr (std::is_base_of_v<RowsK, FA>)
         return fa.load(i, kk);
     else
         return kk < Kd ? fa(i, kk) : 0.f;
 }
 template <class FB>
 __device__ __forceinline__ float opB(const FB& fb, int kk, int j, int Kd) {
-    if constexpr (std::is_same_v<FB, RowsK>)
+    if constexpr (std::is_base_of_v<RowsK, FB>)
         return fb.load(j, kk);
     else if constexpr (std::is_same_v<FB, RowsJ>)
         return fb.load(kk, j);
@@ -630,7 +643,7 @@ __device__ __forceinline__ float opB(const FB& fb, int kk, int j, int Kd) {
 
 template <bool MF, bool B_KCONTIG, class FA, class FB>
 __device__ __forceinline__ void tile_gemm(FA fa, FB fb, int Kd, unsigned char* stage, float acc[4][4]) {
-    static_assert(!std::is_same_v<FB, RowsK> || B_KCONTIG, "RowsK: B contiguous along kk");
+    static_assert(!std::is_base_of_v<RowsK, FB> || B_KCONTIG, "RowsK: B contiguous along kk");
     static_assert(!std::is_same_v<FB, RowsJ> || !B_KCONTIG, "RowsJ: B contiguous along j");
     const int tid = threadIdx.x;
     if constexpr (!MF) {
@@ -681,13 +694,35 @@ __device__ __forceinline__ void tile_gemm(FA fa, FB fb, int Kd, unsigned char* s
         bf16_t* sbl = sbh + BC * MT_LD;
         const int l = tid & 63, w = tid >> 6, lr = l & 15, lg = l >> 4;
         const int r = tid >> 2, kg = tid & 3;  // staging: row r, k-group kg (8 k)
+        // RowsK4 operands: lane (r, kg) holds kk = k0 + 4 kg .. + 3 and
+        // k0 + 16 + 4 kg .. + 3; the others kk = k0 + 8 kg .. + 7
+        constexpr bool VA = std::is_same_v<FA, RowsK4>, VB = std::is_same_v<FB, RowsK4>;
         float ra[8], rb[8];
         const auto fetch = [&](int k0) {
+            if constexpr (VA) {
+                const f32x4 lo4 = fa.load4(r, k0 + 4 * kg), hi4 = fa.load4(r, k0 + 16 + 4 * kg);
 #pragma unroll
-            for (int x = 0; x < 8; x++) {
-                const int kk = k0 + 8 * kg + x;
-                ra[x] = opA(fa, r, kk, Kd);
-                rb[x] = opB(fb, kk, r, Kd);
+                for (int x = 0; x < 4; x++) ra[x] = lo4[x], ra[4 + x] = hi4[x];
+            } else {
+#pragma unroll
+                for (int x = 0; x < 8; x++) ra[x] = opA(fa, r, k0 + 8 * kg + x, Kd);
+            }
+            if constexpr (VB) {
+                const f32x4 lo4 = fb.load4(r, k0 + 4 * kg), hi4 = fb.load4(r, k0 + 16 + 4 * kg);
+#pragma unroll
+                for (int x = 0; x < 4; x++) rb[x] = lo4[x], rb[4 + x] = hi4[x];
+            } else {
+#pragma unroll
+                for (int x = 0; x < 8; x++) rb[x] = opB(fb, k0 + 8 * kg + x, r, Kd);
+            }
+        };
+        // writes the 8 staged values of one operand in its lane order
+        const auto put = [&](bf16_t* base, bool split4, const bf16x8& v) {
+            if (split4) {
+                *reinterpret_cast<bf16x4*>(base + r * MT_LD + 4 * kg) = bf16x4{v[0], v[1], v[2], v[3]};
+                *reinterpret_cast<bf16x4*>(base + r * MT_LD + 16 + 4 * kg) = bf16x4{v[4], v[5], v[6], v[7]};
+            } else {
+                *reinterpret_cast<bf16x8*>(base + r * MT_LD + 8 * kg) = v;
             }
         };
         fetch(0);
@@ -701,11 +736,10 @@ __device__ __forceinline__ void tile_gemm(FA fa, FB fb, int Kd, unsigned char* s
                 vbh[x] = (bf16_t)rb[x];
                 vbl[x] = (bf16_t)(rb[x] - (float)vbh[x]);
             }
-            const int so = r * MT_LD + 8 * kg;
-            *reinterpret_cast<bf16x8*>(sah + so) = vah;
-            *reinterpret_cast<bf16x8*>(sal + so) = val;
-            *reinterpret_cast<bf16x8*>(sbh + so) = vbh;
-            *reinterpret_cast<bf16x8*>(sbl + so) = vbl;
+            put(sah, VA, vah);
+            put(sal, VA, val);
+            put(sbh, VB, vbh);
+            put(sbl, VB, vbl);
             __syncthreads();
             if (k0 + GT_K < Kd) fetch(k0 + GT_K);
             const int ao = (16 * w + lr) * MT_LD + 8 * lg;
@@ -751,11 +785,12 @@ __device__ __forceinline__ void tile_store(float acc[4][4], float* dst, int D, i
 
 // Masked, decayed scores of one chunk into P: P[t][s] = [s <= t] e^{G_t - G_s}
 // sum_j X_t[j] Y_s[j] (X, Y: the chunk's 64 rows, D wide), as one tile GEMM.
-template <bool MF>
+template <bool MF, bool V4>
 __device__ __forceinline__ void chunk_scores(const float* X, const float* Y, int D, const float* sG,
                                              unsigned char* stage, float (*P)[BC + 1]) {
+    using RK = std::conditional_t<V4, RowsK4, RowsK>;
     float acc[4][4] = {};
-    tile_gemm<MF, true>(RowsK(X, D, BC, D), RowsK(Y, D, BC, D), D, stage, acc);
+    tile_gemm<MF, true>(RK(X, D, BC, D), RK(Y, D, BC, D), D, stage, acc);
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
@@ -781,8 +816,9 @@ struct OutArgs {
     float scale;
 };
 
-template <bool MF>
+template <bool MF, bool V4>
 __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
+    using RK = std::conditional_t<V4, RowsK4, RowsK>;  // 16-byte row loads when aligned
     __shared__ float sA[BC][BC + 1];
     __shared__ __align__(16) unsigned char sStage[STAGE_BYTES];
     __shared__ float sG[BC], sEq[BC];
@@ -797,11 +833,11 @@ __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
         sG[tid] = chunk_gam(a.g, b, h, a.T, a.H, n, tid);
         sEq[tid] = expf(sG[tid]);
     }
-    chunk_scores<MF>(q, k, Kq, sG, sStage, sA);
+    chunk_scores<MF, V4>(q, k, Kq, sG, sStage, sA);
     float* out = a.out + (bh * a.Tp + t0) * Vd;
     for (int d0 = 0; d0 < Vd; d0 += BC) {
         float acc[4][4] = {};
-        tile_gemm<MF, false>(RowsK(q, Kq, BC, Kq), RowsJ(S + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
+        tile_gemm<MF, false>(RK(q, Kq, BC, Kq), RowsJ(S + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
         tile_scale_rows<MF>(acc, [&](int t) { return sEq[t]; });
         tile_gemm<MF, false>([&](int i, int kk) { return sA[i][kk]; }, RowsJ(v + d0, Vd, BC, Vd - d0), BC, sStage,
                              acc);
@@ -845,8 +881,9 @@ struct ChunkGradArgs {
     float scale;
 };
 
-template <bool MF>
+template <bool MF, bool V4>
 __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
+    using RK = std::conditional_t<V4, RowsK4, RowsK>;  // 16-byte row loads when aligned
     __shared__ float sA[BC][BC + 1], sB[BC][BC + 1];
     __shared__ __align__(16) unsigned char sStage[STAGE_BYTES];
     // (the row factors e^{G_t} and e^{G_last - G_t} are formed where used:
@@ -865,13 +902,13 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
         const float G = chunk_gam(a.g, b, h, a.T, a.H, n, tid);
         sG[tid] = G;
     }
-    chunk_scores<MF>(q, k, Kq, sG, sStage, sA);
-    chunk_scores<MF>(dO, v, Vd, sG, sStage, sB);
+    chunk_scores<MF, V4>(q, k, Kq, sG, sStage, sA);
+    chunk_scores<MF, V4>(dO, v, Vd, sG, sStage, sB);
     const float sc = a.scale;
     for (int d0 = 0; d0 < Kq; d0 += BC) {
         // dq = scale (e^{G_t} dO_t S_n^T + B k)
         float acc[4][4] = {};
-        tile_gemm<MF, true>(RowsK(dO, Vd, BC, Vd), RowsK(S + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
+        tile_gemm<MF, true>(RK(dO, Vd, BC, Vd), RK(S + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
         tile_scale_rows<MF>(acc, [&](int t) { return expf(sG[t]); });
         tile_gemm<MF, false>([&](int i, int kk) { return sB[i][kk]; }, RowsJ(k + d0, Kq, BC, Kq - d0), BC, sStage,
                              acc);
@@ -881,7 +918,7 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
         for (int x = 0; x < 4; x++)
 #pragma unroll
             for (int y = 0; y < 4; y++) acc[x][y] = 0.f;
-        tile_gemm<MF, true>(RowsK(v, Vd, BC, Vd), RowsK(D + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
+        tile_gemm<MF, true>(RK(v, Vd, BC, Vd), RK(D + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
         tile_scale_rows<MF>(acc, [&](int t) { return expf(sG[BC - 1] - sG[t]); });
         tile_gemm<MF, false>([&](int i, int kk) { return sc * sB[kk][i]; }, RowsJ(q + d0, Kq, BC, Kq - d0), BC,
                              sStage, acc);
@@ -890,7 +927,7 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     for (int d0 = 0; d0 < Vd; d0 += BC) {
         // dv = e^{G_last - G_s} k_s D_{n+1} + scale A^T dO
         float acc[4][4] = {};
-        tile_gemm<MF, false>(RowsK(k, Kq, BC, Kq), RowsJ(D + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
+        tile_gemm<MF, false>(RK(k, Kq, BC, Kq), RowsJ(D + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
         tile_scale_rows<MF>(acc, [&](int t) { return expf(sG[BC - 1] - sG[t]); });
         tile_gemm<MF, false>([&](int i, int kk) { return sc * sA[kk][i]; }, RowsJ(dO + d0, Vd, BC, Vd - d0), BC,
                              sStage, acc);
@@ -1697,10 +1734,15 @@ __global__ __launch_bounds__(256) void bw_pack1_kernel(const float* src, int B, 
 }
 
 void launch_chunk_grad(const ChunkGradArgs& a, bool mfma, hipStream_t stream) {
-    if (mfma)
-        hipLaunchKernelGGL(bw_chunk_kernel<true>, dim3(a.N, a.H, a.B), dim3(256), 0, stream, a);
+    // rows and states 16-byte aligned (workspace buffers, rows of Kq and Vd floats)
+    const bool v4 = a.Kq % 4 == 0 && a.Vd % 4 == 0;
+    const dim3 grid(a.N, a.H, a.B);
+    if (mfma && v4)
+        hipLaunchKernelGGL((bw_chunk_kernel<true, true>), grid, dim3(256), 0, stream, a);
+    else if (mfma)
+        hipLaunchKernelGGL((bw_chunk_kernel<true, false>), grid, dim3(256), 0, stream, a);
     else
-        hipLaunchKernelGGL(bw_chunk_kernel<false>, dim3(a.N, a.H, a.B), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((bw_chunk_kernel<false, false>), grid, dim3(256), 0, stream, a);
 }
 
 }  // namespace
@@ -1743,10 +1785,14 @@ int launch_chunk_pass(const ChunkPassParams& p, hipStream_t stream) {
     oa.Vd = p.Vd;
     oa.N = N;
     oa.scale = p.scale;
-    if (p.mfma)
-        hipLaunchKernelGGL(bw_out_kernel<true>, dim3(N, p.H, p.B), dim3(256), 0, stream, oa);
+    // rows and states 16-byte aligned (workspace buffers, rows of Kq and Vd floats)
+    const bool v4 = p.Kq % 4 == 0 && p.Vd % 4 == 0;
+    if (p.mfma && v4)
+        hipLaunchKernelGGL((bw_out_kernel<true, true>), dim3(N, p.H, p.B), dim3(256), 0, stream, oa);
+    else if (p.mfma)
+        hipLaunchKernelGGL((bw_out_kernel<true, false>), dim3(N, p.H, p.B), dim3(256), 0, stream, oa);
     else
-        hipLaunchKernelGGL(bw_out_kernel<false>, dim3(N, p.H, p.B), dim3(256), 0, stream, oa);
+        hipLaunchKernelGGL((bw_out_kernel<false, false>), dim3(N, p.H, p.B), dim3(256), 0, stream, oa);
     return 0;
 }
 
