@@ -981,24 +981,42 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
     const auto row_of = [&](int rho) { return ((size_t)(rho / Tp) * H + h) * Tp + rho % Tp; };
     // wave wv: row tile it = wv & 1, column tiles 4 (wv >> 1) .. + 3 (of r, then of m)
     const int it = wv & 1, ct0 = 4 * (wv >> 1);
-    for (int b0 = blockIdx.x * per_wg * RB; b0 < min(rows, (blockIdx.x + 1) * per_wg * RB); b0 += RB) {
+    // A block's inputs, element x of this thread = (row i, pair pr) = e / 64,
+    // e % 64, e = tid + 256 x: loaded one block ahead through buffer
+    // resources (rows < 2^21, M <= 128: offsets below 2^30), predicated
+    // through the offset, so that no block waits for its own loads.
+    constexpr int NX = RB * (TM / 2) / 256;
+    const int b_end = min(rows, (int)(blockIdx.x + 1) * per_wg * RB);
+    const bw_rsrc_t rcs = bw_rsrc(cs, (size_t)rows * H * P), rsn = bw_rsrc(sn, (size_t)rows * H * P),
+                    rraw = bw_rsrc(raw, (size_t)rows * H * M);  // every head's rows
+    float nc[NX], ns[NX], nre[NX], nro[NX];
+    const auto load_block = [&](int b0) {
+#pragma unroll
+        for (int x = 0; x < NX; x++) {
+            const int e = tid + 256 * x, i = e / (TM / 2), pr = e % (TM / 2), rho = b0 + i;
+            const bool live = rho < b_end && pr < P;
+            const uint32_t row = live ? (uint32_t)row_of(rho) : 0u;
+            nc[x] = bw_load(rcs, (row * (uint32_t)P + (uint32_t)pr) * 4u, live);
+            ns[x] = bw_load(rsn, (row * (uint32_t)P + (uint32_t)pr) * 4u, live);
+            nre[x] = bw_load(rraw, (row * (uint32_t)M + 2u * (uint32_t)pr) * 4u, live);
+            nro[x] = bw_load(rraw, (row * (uint32_t)M + 2u * (uint32_t)pr + 1u) * 4u, live);
+        }
+    };
+    const int b_first = blockIdx.x * per_wg * RB;
+    load_block(b_first);
+    for (int b0 = b_first; b0 < b_end; b0 += RB) {
         __syncthreads();  // the table is staged; the previous block's tiles are done with
-        for (int e = tid; e < RB * (TM / 2); e += 256) {
-            const int i = e / (TM / 2), pr = e % (TM / 2), rho = b0 + i;
-            float ze = 0.f, zo = 0.f, c = 1.f, s = 0.f;
-            if (rho < rows && pr < P) {
-                const size_t row = row_of(rho);
-                c = cs[row * P + pr];
-                s = sn[row * P + pr];
-                const float re = raw[row * M + 2 * pr], ro = raw[row * M + 2 * pr + 1];
-                ze = bw_rnd<BF>(c * re - s * ro);
-                zo = bw_rnd<BF>(s * re + c * ro);
-            }
+#pragma unroll
+        for (int x = 0; x < NX; x++) {
+            const int e = tid + 256 * x, i = e / (TM / 2), pr = e % (TM / 2);
+            const bool live = b0 + i < b_end && pr < P;
+            const float c = live ? nc[x] : 1.f, s = ns[x];
             sCs[i][pr] = c;
             sSn[i][pr] = s;
-            sZ[i][2 * pr] = ze;
-            sZ[i][2 * pr + 1] = zo;
+            sZ[i][2 * pr] = bw_rnd<BF>(c * nre[x] - s * nro[x]);  // zero where !live
+            sZ[i][2 * pr + 1] = bw_rnd<BF>(s * nre[x] + c * nro[x]);
         }
+        load_block(b0 + RB);  // the next block (past the end: dead loads)
         __syncthreads();
         {  // logits l[i][r] = sum_m z[i][m] table[r][m]
             f32x4v acc[4];
@@ -1096,30 +1114,47 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
 #pragma unroll
     for (int rt = 0; rt < 8; rt++) dacc[rt][0] = dacc[rt][1] = f32x4v{0.f, 0.f, 0.f, 0.f};
     const int rows = a.B * a.Tp;
-    for (int b0 = blk * a.per_wg * RO_BLK; b0 < min(rows, (blk + 1) * a.per_wg * RO_BLK); b0 += RO_BLK) {
+    // A block's inputs, element x of this thread = (row i, pair pr) = e / 64,
+    // e % 64, e = tid + 256 x: loaded one block ahead through buffer
+    // resources (rows < 2^21, M <= 128: offsets below 2^30), predicated
+    // through the offset, so that no block waits for its own loads.
+    constexpr int NX = RO_BLK * (TM / 2) / 256;
+    const int b_end = min(rows, (blk + 1) * a.per_wg * RO_BLK);
+    const bw_rsrc_t rcs = bw_rsrc(a.cs, (size_t)rows * a.H * P), rsn = bw_rsrc(a.sn, (size_t)rows * a.H * P),
+                    rraw = bw_rsrc(a.raw, (size_t)rows * a.H * M), rdw = bw_rsrc(a.dwts, (size_t)rows * a.H * M);
+    float nc[NX], ns[NX], nre[NX], nro[NX], nde[NX], ndd[NX];
+    const auto load_block = [&](int b0) {
+#pragma unroll
+        for (int x = 0; x < NX; x++) {
+            const int e = tid + 256 * x, i = e / (TM / 2), pr = e % (TM / 2), rho = b0 + i;
+            const bool live = rho < b_end && pr < P;
+            const uint32_t row = live ? (uint32_t)(((rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp) : 0u;
+            nc[x] = bw_load(rcs, (row * (uint32_t)P + (uint32_t)pr) * 4u, live);
+            ns[x] = bw_load(rsn, (row * (uint32_t)P + (uint32_t)pr) * 4u, live);
+            nre[x] = bw_load(rraw, (row * (uint32_t)M + 2u * (uint32_t)pr) * 4u, live);
+            nro[x] = bw_load(rraw, (row * (uint32_t)M + 2u * (uint32_t)pr + 1u) * 4u, live);
+            nde[x] = bw_load(rdw, (row * (uint32_t)M + 2u * (uint32_t)pr) * 4u, live);
+            ndd[x] = bw_load(rdw, (row * (uint32_t)M + 2u * (uint32_t)pr + 1u) * 4u, live);
+        }
+    };
+    const int b_first = blk * a.per_wg * RO_BLK;
+    load_block(b_first);
+    for (int b0 = b_first; b0 < b_end; b0 += RO_BLK) {
         __syncthreads();  // the previous block's tiles are done with
-        // z = U(lam) raw and du = U(lam) dweights, one (row, pair) per thread step
-        for (int e = tid; e < RO_BLK * (TM / 2); e += 256) {
-            const int i = e / (TM / 2), pr = e % (TM / 2), rho = b0 + i;
-            float ze = 0.f, zo = 0.f, ue = 0.f, uo = 0.f, c = 1.f, s = 0.f;
-            if (rho < rows && pr < P) {
-                const size_t row = ((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp;
-                c = a.cs[row * P + pr];
-                s = a.sn[row * P + pr];
-                const float re = a.raw[row * M + 2 * pr], ro = a.raw[row * M + 2 * pr + 1];
-                const float de = a.dwts[row * M + 2 * pr], dd = a.dwts[row * M + 2 * pr + 1];
-                ze = c * re - s * ro;
-                zo = s * re + c * ro;
-                ue = c * de - s * dd;
-                uo = s * de + c * dd;
-            }
+        // z = U(lam) raw and du = U(lam) dweights
+#pragma unroll
+        for (int x = 0; x < NX; x++) {
+            const int e = tid + 256 * x, i = e / (TM / 2), pr = e % (TM / 2);
+            const bool live = b0 + i < b_end && pr < P;
+            const float c = live ? nc[x] : 1.f, s = ns[x];  // zero inputs where !live
             sCs[i][pr] = c;
             sSn[i][pr] = s;
-            sZ[i][2 * pr] = ze;
-            sZ[i][2 * pr + 1] = zo;
-            sDU[i][2 * pr] = ue;
-            sDU[i][2 * pr + 1] = uo;
+            sZ[i][2 * pr] = c * nre[x] - s * nro[x];
+            sZ[i][2 * pr + 1] = s * nre[x] + c * nro[x];
+            sDU[i][2 * pr] = c * nde[x] - s * ndd[x];
+            sDU[i][2 * pr + 1] = s * nde[x] + c * ndd[x];
         }
+        load_block(b0 + RO_BLK);  // the next block (past the end: dead loads)
         __syncthreads();
         // logits l[i][r] = sum_m z[i][m] table[r][m] and dp[i][r] = sum_m du[i][m] table[r][m]
         {
@@ -1678,7 +1713,15 @@ __global__ __launch_bounds__(256) void bw_table_reduce_kernel(const float* part,
     if (e >= RM) return;
     const float* p = part + (size_t)h * nb * RM + e;
     float s = 0.f;
-    for (int b = 0; b < nb; b++) s += p[(size_t)b * RM];
+    int b = 0;
+    for (; b + 16 <= nb; b += 16) {  // sixteen loads in flight, then the sums in order
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = p[(size_t)(b + i) * RM];
+#pragma unroll
+        for (int i = 0; i < 16; i++) s += v[i];
+    }
+    for (; b < nb; b++) s += p[(size_t)b * RM];
     out[(size_t)h * RM + e] = s;
 }
 
