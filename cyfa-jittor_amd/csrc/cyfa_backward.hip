@@ -1728,20 +1728,24 @@ __global__ __launch_bounds__(256) void bw_table_reduce_kernel(const float* part,
 // dreadout[h][r][j] = sum_m dtable[h][r][m] Phi[j][m] (table = readout Phi,
 // ops/chunk.py:82-103, 281); Phi's angle 2 pi ((pair j) mod R) / R is reduced
 // exactly in integers. One block per (h, r), thread j.
+// The R angles' sine and cosine are formed once per block in LDS and indexed
+// by the exact integer reduction (pair j) mod R, stepped by j per pair: the
+// same values as a sincosf per term.
 __global__ __launch_bounds__(256) void bw_dreadout_kernel(const float* dtable, int M, float* dreadout) {
     const int R = M - 1, hr = blockIdx.x, j = threadIdx.x;
-    __shared__ float row[BWD_MAX_M];
+    __shared__ float row[BWD_MAX_M], sin_k[BWD_MAX_M], cos_k[BWD_MAX_M];
     if (j < M) row[j] = dtable[(size_t)hr * M + j];
+    if (j < R) sincosf((float)((double)j * (kTwoPiBw / R)), &sin_k[j], &cos_k[j]);
     __syncthreads();
     if (j >= R) return;
     float acc = 0.f;
-    for (int m = 0; m < M; m++) {
-        if (m == 1) continue;
-        const int pair = m >> 1;
+    int k = 0;  // (pair j) mod R
+    for (int pair = 0; pair < M / 2; pair++) {
         const float sc = (float)sqrt((pair == 0 ? 1.0 : 2.0) / R);
-        float sn, cs;
-        sincosf((float)((double)((pair * j) % R) * (kTwoPiBw / R)), &sn, &cs);
-        acc = fmaf(row[m], sc * ((m & 1) ? sn : cs), acc);
+        acc = fmaf(row[2 * pair], sc * cos_k[k], acc);
+        if (pair > 0) acc = fmaf(row[2 * pair + 1], sc * sin_k[k], acc);  // column 1 is not a basis vector
+        k += j;
+        k = k >= R ? k - R : k;
     }
     dreadout[(size_t)hr * R + j] = acc;
 }
