@@ -41,6 +41,8 @@ namespace cyfa {
 
 namespace {
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
 constexpr int BC = 64;           // chunk length of the recompute and the sweeps
 constexpr int BW_MAX_D = 1024;   // largest K and V
 constexpr int BW_TILE = 32;      // state columns per scan workgroup
@@ -622,6 +624,19 @@ struct RowsJ {
     }
 };
 
+// RowsJ with 16-byte loads of four consecutive j (16-byte aligned base, ld and
+// nj multiples of 4). In tile_gemm's matrix-core staging, lane (jq, kp) =
+// (tid % 16, tid / 16) loads j = 4 jq .. + 3 of rows kk = k0 + 2 kp and
+// k0 + 2 kp + 1 (each load instruction covers whole 256-byte row segments)
+// and writes the pairs (kk, kk + 1) of its four columns as 4-byte LDS stores.
+struct RowsJ4 : RowsJ {
+    __device__ RowsJ4(const float* base, int ld_, int nk_, int nj_) : RowsJ(base, ld_, nk_, nj_) {}
+    __device__ f32x4 load4(int kk, int j0) const {
+        const uint32_t dead = (kk < nk && j0 < nj) ? 0u : BW_DEAD;
+        return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, ((uint32_t)kk * ld + (uint32_t)j0) * 4u | dead, 0, 0));
+    }
+};
+
 // Element (i, kk) of A and (kk, j) of B, for a global operand or a callable
 // (LDS operands: read only at kk < Kd, contractions of BC tokens).
 template <class FA>
@@ -635,7 +650,7 @@ template <class FB>
 __device__ __forceinline__ float opB(const FB& fb, int kk, int j, int Kd) {
     if constexpr (std::is_base_of_v<RowsK, FB>)
         return fb.load(j, kk);
-    else if constexpr (std::is_same_v<FB, RowsJ>)
+    else if constexpr (std::is_base_of_v<RowsJ, FB>)
         return fb.load(kk, j);
     else
         return kk < Kd ? fb(kk, j) : 0.f;
@@ -644,7 +659,7 @@ __device__ __forceinline__ float opB(const FB& fb, int kk, int j, int Kd) {
 template <bool MF, bool B_KCONTIG, class FA, class FB>
 __device__ __forceinline__ void tile_gemm(FA fa, FB fb, int Kd, unsigned char* stage, float acc[4][4]) {
     static_assert(!std::is_base_of_v<RowsK, FB> || B_KCONTIG, "RowsK: B contiguous along kk");
-    static_assert(!std::is_same_v<FB, RowsJ> || !B_KCONTIG, "RowsJ: B contiguous along j");
+    static_assert(!std::is_base_of_v<RowsJ, FB> || !B_KCONTIG, "RowsJ: B contiguous along j");
     const int tid = threadIdx.x;
     if constexpr (!MF) {
         float(*sa)[GT_LD] = reinterpret_cast<float(*)[GT_LD]>(stage);
@@ -697,6 +712,8 @@ __device__ __forceinline__ void tile_gemm(FA fa, FB fb, int Kd, unsigned char* s
         // RowsK4 operands: lane (r, kg) holds kk = k0 + 4 kg .. + 3 and
         // k0 + 16 + 4 kg .. + 3; the others kk = k0 + 8 kg .. + 7
         constexpr bool VA = std::is_same_v<FA, RowsK4>, VB = std::is_same_v<FB, RowsK4>;
+        constexpr bool JB = std::is_same_v<FB, RowsJ4>;  // B: lane (jq, kp) as in RowsJ4
+        const int jq = tid & 15, kp = tid >> 4;
         float ra[8], rb[8];
         const auto fetch = [&](int k0) {
             if constexpr (VA) {
@@ -711,6 +728,10 @@ __device__ __forceinline__ void tile_gemm(FA fa, FB fb, int Kd, unsigned char* s
                 const f32x4 lo4 = fb.load4(r, k0 + 4 * kg), hi4 = fb.load4(r, k0 + 16 + 4 * kg);
 #pragma unroll
                 for (int x = 0; x < 4; x++) rb[x] = lo4[x], rb[4 + x] = hi4[x];
+            } else if constexpr (JB) {  // rb[c] = B(k0 + 2 kp, 4 jq + c), rb[4 + c] = B(k0 + 2 kp + 1, 4 jq + c)
+                const f32x4 r0 = fb.load4(k0 + 2 * kp, 4 * jq), r1 = fb.load4(k0 + 2 * kp + 1, 4 * jq);
+#pragma unroll
+                for (int x = 0; x < 4; x++) rb[x] = r0[x], rb[4 + x] = r1[x];
             } else {
 #pragma unroll
                 for (int x = 0; x < 8; x++) rb[x] = opB(fb, k0 + 8 * kg + x, r, Kd);
@@ -738,8 +759,16 @@ __device__ __forceinline__ void tile_gemm(FA fa, FB fb, int Kd, unsigned char* s
             }
             put(sah, VA, vah);
             put(sal, VA, val);
-            put(sbh, VB, vbh);
-            put(sbl, VB, vbl);
+            if constexpr (JB) {  // column 4 jq + c: the pair (k0 + 2 kp, + 1) as one 4-byte store
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    *reinterpret_cast<bf16x2*>(sbh + (4 * jq + c) * MT_LD + 2 * kp) = bf16x2{vbh[c], vbh[4 + c]};
+                    *reinterpret_cast<bf16x2*>(sbl + (4 * jq + c) * MT_LD + 2 * kp) = bf16x2{vbl[c], vbl[4 + c]};
+                }
+            } else {
+                put(sbh, VB, vbh);
+                put(sbl, VB, vbl);
+            }
             __syncthreads();
             if (k0 + GT_K < Kd) fetch(k0 + GT_K);
             const int ao = (16 * w + lr) * MT_LD + 8 * lg;
@@ -819,6 +848,7 @@ struct OutArgs {
 template <bool MF, bool V4>
 __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
     using RK = std::conditional_t<V4, RowsK4, RowsK>;  // 16-byte row loads when aligned
+    using RJ = std::conditional_t<V4, RowsJ4, RowsJ>;
     __shared__ float sA[BC][BC + 1];
     __shared__ __align__(16) unsigned char sStage[STAGE_BYTES];
     __shared__ float sG[BC], sEq[BC];
@@ -837,9 +867,9 @@ __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
     float* out = a.out + (bh * a.Tp + t0) * Vd;
     for (int d0 = 0; d0 < Vd; d0 += BC) {
         float acc[4][4] = {};
-        tile_gemm<MF, false>(RK(q, Kq, BC, Kq), RowsJ(S + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
+        tile_gemm<MF, false>(RK(q, Kq, BC, Kq), RJ(S + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
         tile_scale_rows<MF>(acc, [&](int t) { return sEq[t]; });
-        tile_gemm<MF, false>([&](int i, int kk) { return sA[i][kk]; }, RowsJ(v + d0, Vd, BC, Vd - d0), BC, sStage,
+        tile_gemm<MF, false>([&](int i, int kk) { return sA[i][kk]; }, RJ(v + d0, Vd, BC, Vd - d0), BC, sStage,
                              acc);
         if (!a.out_bthd) {
             if (a.bf16) {
@@ -884,6 +914,7 @@ struct ChunkGradArgs {
 template <bool MF, bool V4>
 __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     using RK = std::conditional_t<V4, RowsK4, RowsK>;  // 16-byte row loads when aligned
+    using RJ = std::conditional_t<V4, RowsJ4, RowsJ>;
     __shared__ float sA[BC][BC + 1], sB[BC][BC + 1];
     __shared__ __align__(16) unsigned char sStage[STAGE_BYTES];
     // (the row factors e^{G_t} and e^{G_last - G_t} are formed where used:
@@ -910,7 +941,7 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
         float acc[4][4] = {};
         tile_gemm<MF, true>(RK(dO, Vd, BC, Vd), RK(S + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
         tile_scale_rows<MF>(acc, [&](int t) { return expf(sG[t]); });
-        tile_gemm<MF, false>([&](int i, int kk) { return sB[i][kk]; }, RowsJ(k + d0, Kq, BC, Kq - d0), BC, sStage,
+        tile_gemm<MF, false>([&](int i, int kk) { return sB[i][kk]; }, RJ(k + d0, Kq, BC, Kq - d0), BC, sStage,
                              acc);
         tile_store<MF>(acc, a.dq + (bh * a.Tp + t0) * Kq, Kq, d0, sc);
         // dk = e^{G_last - G_s} v_s D_{n+1}^T + scale B^T q
@@ -920,16 +951,16 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
             for (int y = 0; y < 4; y++) acc[x][y] = 0.f;
         tile_gemm<MF, true>(RK(v, Vd, BC, Vd), RK(D + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
         tile_scale_rows<MF>(acc, [&](int t) { return expf(sG[BC - 1] - sG[t]); });
-        tile_gemm<MF, false>([&](int i, int kk) { return sc * sB[kk][i]; }, RowsJ(q + d0, Kq, BC, Kq - d0), BC,
+        tile_gemm<MF, false>([&](int i, int kk) { return sc * sB[kk][i]; }, RJ(q + d0, Kq, BC, Kq - d0), BC,
                              sStage, acc);
         tile_store<MF>(acc, a.dk + (bh * a.Tp + t0) * Kq, Kq, d0, 1.f);
     }
     for (int d0 = 0; d0 < Vd; d0 += BC) {
         // dv = e^{G_last - G_s} k_s D_{n+1} + scale A^T dO
         float acc[4][4] = {};
-        tile_gemm<MF, false>(RK(k, Kq, BC, Kq), RowsJ(D + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
+        tile_gemm<MF, false>(RK(k, Kq, BC, Kq), RJ(D + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
         tile_scale_rows<MF>(acc, [&](int t) { return expf(sG[BC - 1] - sG[t]); });
-        tile_gemm<MF, false>([&](int i, int kk) { return sc * sA[kk][i]; }, RowsJ(dO + d0, Vd, BC, Vd - d0), BC,
+        tile_gemm<MF, false>([&](int i, int kk) { return sc * sA[kk][i]; }, RJ(dO + d0, Vd, BC, Vd - d0), BC,
                              sStage, acc);
         tile_store<MF>(acc, a.dv + (bh * a.Tp + t0) * Vd, Vd, d0, 1.f);
     }
