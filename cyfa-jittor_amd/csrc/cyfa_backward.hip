@@ -48,15 +48,12 @@ constexpr int BW_MAX_D = 1024;   // largest K and V
 constexpr int BW_TILE = 32;      // state columns per scan workgroup
 constexpr double kTwoPiBw = 6.283185307179586;
 
-__device__ __forceinline__ float bw_wave_sum(float x) {
-    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-    return x;
-}
+// Whole-wave sum and max in every lane, on DPP moves and v_readlane (the
+// fixed order of wave_sum / wave_max); every call site has the whole wave
+// active. (With __shfl_xor each step was an LDS round trip.)
+__device__ __forceinline__ float bw_wave_sum(float x) { return wave_sum<64>(x); }
 
-__device__ __forceinline__ float bw_wave_max(float x) {
-    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-    return x;
-}
+__device__ __forceinline__ float bw_wave_max(float x) { return wave_max<64>(x); }
 
 template <bool BF>
 __device__ __forceinline__ float bw_ld(const void* p, size_t i) {
@@ -1102,6 +1099,158 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
     }
 }
 
+// The same readout with its two products as split-bf16 products on
+// v_mfma_f32_16x16x32_bf16 (every fp32 operand as a bf16 high part and a bf16
+// remainder, lo_a hi_b + hi_a lo_b + hi_a hi_b: about 16 mantissa bits; with
+// BF the operands are bf16 values and the products exact), for calls whose
+// tile products run on the matrix cores. The table sits in LDS once as its
+// two bf16 parts, row-major [r][m]: the logits read its rows as B fragments,
+// u gathers its columns. Waves and accumulator tiles as in
+// bw_fwd_readout_kernel; the softmax reductions on DPP moves.
+constexpr int RO_LDB = BWD_TABLE_M + 8;  // bf16 rows of the split table and row blocks
+
+// lane (lr, lg) gets X[r0 + lr][k0 + 8 lg .. + 7] of a row-major bf16 tile
+__device__ __forceinline__ bf16x8 ro_row(const bf16_t* X, int r0, int k0) {
+    const int l = threadIdx.x & 63;
+    return *reinterpret_cast<const bf16x8*>(X + (r0 + (l & 15)) * RO_LDB + k0 + 8 * (l >> 4));
+}
+
+// lane (lr, lg) gets X[s0 + 8 lg + j][c0 + lr], j = 0..7, of a row-major bf16
+// tile (a B fragment of the transpose), as eight 2-byte LDS reads
+__device__ __forceinline__ bf16x8 ro_col(const bf16_t* X, int s0, int c0) {
+    const int l = threadIdx.x & 63;
+    const bf16_t* p = X + (s0 + 8 * (l >> 4)) * RO_LDB + c0 + (l & 15);
+    bf16x8 r;
+#pragma unroll
+    for (int e = 0; e < 8; e++) r[e] = p[e * RO_LDB];
+    return r;
+}
+
+__device__ __forceinline__ void split_store(bf16_t* hi, bf16_t* lo, int idx, float v) {
+    const bf16_t h = (bf16_t)v;
+    hi[idx] = h;
+    lo[idx] = (bf16_t)(v - (float)h);
+}
+
+template <bool BF>
+__global__ __launch_bounds__(256) void bw_fwd_readout_mf_kernel(const float* raw, const float* cs, const float* sn,
+                                                                const float* table, int B, int Tp, int H, int M,
+                                                                int per_wg, float* wts) {
+    constexpr int TM = BWD_TABLE_M, LB = RO_LDB, RB = 32;
+    static_assert(TM == 128 && RB == 32, "eight 16-wide tiles of slots, two of rows");
+    __shared__ __align__(16) bf16_t sTh[TM * LB], sTl[TM * LB];  // rows R .. 127 and columns M .. 127 zero
+    __shared__ __align__(16) bf16_t sZh[RB * LB], sZl[RB * LB], sPh[RB * LB], sPl[RB * LB];
+    __shared__ float sL[RB][TM + 4];
+    __shared__ float sCs[RB][TM / 2], sSn[RB][TM / 2];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, h = blockIdx.y;
+    const int lr = lane & 15;
+    const int R = M - 1, P = M / 2, rows = B * Tp;
+    for (int e = tid; e < TM * TM; e += 256) {
+        const int r = e / TM, m = e % TM;
+        split_store(sTh, sTl, r * LB + m, (r < R && m < M) ? bw_rnd<BF>(table[((size_t)h * R + r) * M + m]) : 0.f);
+    }
+    const auto row_of = [&](int rho) { return ((size_t)(rho / Tp) * H + h) * Tp + rho % Tp; };
+    const int it = wv & 1, ct0 = 4 * (wv >> 1);
+    constexpr int NX = RB * (TM / 2) / 256;
+    const int b_end = min(rows, (int)(blockIdx.x + 1) * per_wg * RB);
+    const bw_rsrc_t rcs = bw_rsrc(cs, (size_t)rows * H * P), rsn = bw_rsrc(sn, (size_t)rows * H * P),
+                    rraw = bw_rsrc(raw, (size_t)rows * H * M);  // every head's rows
+    float nc[NX], ns[NX], nre[NX], nro[NX];
+    const auto load_block = [&](int b0) {
+#pragma unroll
+        for (int x = 0; x < NX; x++) {
+            const int e = tid + 256 * x, i = e / (TM / 2), pr = e % (TM / 2), rho = b0 + i;
+            const bool live = rho < b_end && pr < P;
+            const uint32_t row = live ? (uint32_t)row_of(rho) : 0u;
+            nc[x] = bw_load(rcs, (row * (uint32_t)P + (uint32_t)pr) * 4u, live);
+            ns[x] = bw_load(rsn, (row * (uint32_t)P + (uint32_t)pr) * 4u, live);
+            nre[x] = bw_load(rraw, (row * (uint32_t)M + 2u * (uint32_t)pr) * 4u, live);
+            nro[x] = bw_load(rraw, (row * (uint32_t)M + 2u * (uint32_t)pr + 1u) * 4u, live);
+        }
+    };
+    const int b_first = blockIdx.x * per_wg * RB;
+    load_block(b_first);
+    for (int b0 = b_first; b0 < b_end; b0 += RB) {
+        __syncthreads();  // the table is staged; the previous block's tiles are done with
+#pragma unroll
+        for (int x = 0; x < NX; x++) {
+            const int e = tid + 256 * x, i = e / (TM / 2), pr = e % (TM / 2);
+            const bool live = b0 + i < b_end && pr < P;
+            const float c = live ? nc[x] : 1.f, s = ns[x];
+            sCs[i][pr] = c;
+            sSn[i][pr] = s;
+            split_store(sZh, sZl, i * LB + 2 * pr, bw_rnd<BF>(c * nre[x] - s * nro[x]));  // zero where !live
+            split_store(sZh, sZl, i * LB + 2 * pr + 1, bw_rnd<BF>(s * nre[x] + c * nro[x]));
+        }
+        load_block(b0 + RB);  // the next block (past the end: dead loads)
+        __syncthreads();
+        {  // logits l[i][r] = sum_m z[i][m] table[r][m]
+            f32x4 acc[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k0 = 0; k0 < TM; k0 += 32) {
+                const bf16x8 ah = ro_row(sZh, 16 * it, k0), al = ro_row(sZl, 16 * it, k0);
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const bf16x8 bh = ro_row(sTh, 16 * (ct0 + t), k0), bl = ro_row(sTl, 16 * (ct0 + t), k0);
+                    acc[t] = mfma_bf16(al, bh, acc[t]);
+                    acc[t] = mfma_bf16(ah, bl, acc[t]);
+                    acc[t] = mfma_bf16(ah, bh, acc[t]);
+                }
+            }
+            const int lg = lane >> 4;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) sL[16 * it + 4 * lg + q][16 * (ct0 + t) + lr] = acc[t][q];
+        }
+        __syncthreads();
+        for (int i = wv; i < RB; i += 4) {
+            const float l0 = lane < R ? sL[i][lane] : -INFINITY, l1 = lane + 64 < R ? sL[i][lane + 64] : -INFINITY;
+            const float mx = bw_wave_max(fmaxf(l0, l1));
+            const float e0 = lane < R ? expf(l0 - mx) : 0.f, e1 = lane + 64 < R ? expf(l1 - mx) : 0.f;
+            const float inv = 1.f / bw_wave_sum(e0 + e1);
+            split_store(sPh, sPl, i * LB + lane, bw_rnd<BF>(e0 * inv));
+            split_store(sPh, sPl, i * LB + lane + 64, bw_rnd<BF>(e1 * inv));
+        }
+        __syncthreads();
+        // u[i][m] = sum_r p[i][r] table[r][m] (p and the table zero at r >= R); the
+        // weights' pair (2 pr, 2 pr + 1) sits in lanes (lr, lr ^ 1), swapped in by
+        // quad_perm [1,0,3,2]
+        f32x4 acc[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k0 = 0; k0 < TM; k0 += 32) {
+            const bf16x8 ah = ro_row(sPh, 16 * it, k0), al = ro_row(sPl, 16 * it, k0);
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const bf16x8 bh = ro_col(sTh, k0, 16 * (ct0 + t)), bl = ro_col(sTl, k0, 16 * (ct0 + t));
+                acc[t] = mfma_bf16(al, bh, acc[t]);
+                acc[t] = mfma_bf16(ah, bl, acc[t]);
+                acc[t] = mfma_bf16(ah, bh, acc[t]);
+            }
+        }
+        const bool odd = (lr & 1) != 0;
+        const int lk = lane >> 4;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int m = 16 * (ct0 + t) + lr, pr = m >> 1;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float un = acc[t][q], ux = dpp_mov<0xB1>(un);
+                const float ue = odd ? ux : un, uo = odd ? un : ux;
+                const int i = 16 * it + 4 * lk + q, rho = b0 + i;
+                if (rho < b_end && pr < P) {
+                    const float c = sCs[i][pr], s = sSn[i][pr];
+                    wts[row_of(rho) * M + m] = bw_rnd<BF>(odd ? -s * ue + c * uo : c * ue + s * uo);
+                }
+            }
+        }
+    }
+}
+
 // The slot-readout adjoint for blocks of 32 rows of one head (z = U(lam) raw,
 // l = table z, p = softmax(l), u = table^T p, weights = U(-lam) u):
 //   du = U(lam) dweights, dp = table du, dl = p (dp - p.dp), dz = table^T dl,
@@ -1875,7 +2024,7 @@ int launch_chunk_pass(const ChunkPassParams& p, hipStream_t stream) {
 }
 
 int launch_chunk_readout(const float* raw, const float* cs, const float* sn, const float* table, float* lg, int B,
-                         int Tp, int H, int M, int bf16, float* wts, hipStream_t stream) {
+                         int Tp, int H, int M, int bf16, int split, float* wts, hipStream_t stream) {
     if (B < 1 || H < 1 || Tp < 1 || Tp % BC || M < 4 || M > BWD_MAX_M || M % 2) return -1;
     const dim3 blk(256);
     if (M > BWD_TABLE_M) {  // logits, softmax, then the weights, streaming the table
@@ -1903,7 +2052,13 @@ int launch_chunk_readout(const float* raw, const float* cs, const float* sn, con
     }
     const int per = bwd_ro_per_wg(B, Tp, H), blocks = (B * Tp + BWD_RO_BLOCK - 1) / BWD_RO_BLOCK;
     const dim3 grid((blocks + per - 1) / per, H);
-    if (bf16)
+    if (split && bf16)
+        hipLaunchKernelGGL(bw_fwd_readout_mf_kernel<true>, grid, blk, 0, stream, raw, cs, sn, table, B, Tp, H, M, per,
+                           wts);
+    else if (split)
+        hipLaunchKernelGGL(bw_fwd_readout_mf_kernel<false>, grid, blk, 0, stream, raw, cs, sn, table, B, Tp, H, M, per,
+                           wts);
+    else if (bf16)
         hipLaunchKernelGGL(bw_fwd_readout_kernel<true>, grid, blk, 0, stream, raw, cs, sn, table, B, Tp, H, M, per,
                            wts);
     else
@@ -1971,7 +2126,7 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     p1.Vd = M;
     p1.scale = p.scale;
     if (launch_chunk_pass(p1, stream) != 0 ||
-        launch_chunk_readout(ws.raw, ws.cs, ws.sn, p.table, ws.lg, B, Tp, H, M, 0, ws.wts, stream) != 0)
+        launch_chunk_readout(ws.raw, ws.cs, ws.sn, p.table, ws.lg, B, Tp, H, M, 0, bf, ws.wts, stream) != 0)
         return -1;
     const int ro_per_wg = bwd_ro_per_wg(B, Tp, H);
     const bool wide = M > BWD_TABLE_M;

@@ -400,7 +400,7 @@ int launch_general_chunk(const GenChunkParams& g, hipStream_t stream) {
     p1.Vd = M;
     p1.scale = g.scale;
     if (launch_chunk_pass(p1, stream) != 0) return -1;
-    if (launch_chunk_readout(ws.raw, ws.cs, ws.sn, g.table, ws.lg, B, Tp, H, M, g.bf16, ws.wts, stream) != 0) return -1;
+    if (launch_chunk_readout(ws.raw, ws.cs, ws.sn, g.table, ws.lg, B, Tp, H, M, g.bf16, g.bf16, ws.wts, stream) != 0) return -1;
     // pass 2: o = sgla(weights, w, v), written as [B, T, H, V] in the input dtype
     ChunkPassParams p2 = p1;
     p2.q = ws.wts;

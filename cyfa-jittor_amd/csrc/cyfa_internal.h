@@ -444,9 +444,11 @@ int launch_general_chunk(const GenChunkParams& p, hipStream_t stream);
 int launch_chunk_pass(const ChunkPassParams& p, hipStream_t stream);
 // The slot readout of every head-major row (cyfa_backward.hip): z = U(lam) raw,
 // p = softmax(table z), weights = U(-lam) table^T p, rounded where the input
-// dtype is cast when bf16; lg: with M > 128 a [rows, 256] fp32 workspace.
+// dtype is cast when bf16; split: up to 128 slots, the products as split-bf16
+// products on the matrix cores (else fp32 ones); lg: with M > 128 a
+// [rows, 256] fp32 workspace.
 int launch_chunk_readout(const float* raw, const float* cs, const float* sn, const float* table, float* lg, int B,
-                         int Tp, int H, int M, int bf16, float* wts, hipStream_t stream);
+                         int Tp, int H, int M, int bf16, int split, float* wts, hipStream_t stream);
 // The general path's clock and unrounded fp32 write vector with its phases
 // (head-major [B*H, Tp] and [B*H, Tp, M | M/2]), for the backward pass's recompute.
 int launch_general_clock_write(const float* delta, const float* clock0, const float* beta, int B, int T, int Tp, int H,
