@@ -73,14 +73,27 @@ __device__ __forceinline__ void bw_st(void* p, size_t i, float v) {
 
 // The in-chunk inclusive cumsum G of the natural-log gate over chunk n of
 // (b, h), lane = token (tokens past T add zero); one wave.
+// Inclusive sum over the wave's 64 lanes on DPP moves: shifts by 1, 2, 4 and
+// 8 within rows of 16, then row 15's sum broadcast into the next row, and row
+// 31's into the upper half (every lane active). (__shfl_up made each step an
+// LDS round trip on the scans' serial path.)
+template <int CTRL>
+__device__ __forceinline__ float bw_dpp_shift(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float bw_wave_scan(float x) {
+    x += bw_dpp_shift<0x111>(x);
+    x += bw_dpp_shift<0x112>(x);
+    x += bw_dpp_shift<0x114>(x);
+    x += bw_dpp_shift<0x118>(x);
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x142, 0xA, 0xF, false));
+    x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x143, 0xC, 0xF, false));
+    return x;
+}
+
 __device__ __forceinline__ float chunk_gam(const float* g, int b, int h, int T, int H, int n, int lane) {
     const int t = n * BC + lane;
-    float x = t < T ? g[((size_t)b * T + t) * H + h] : 0.f;
-    for (int o = 1; o < 64; o <<= 1) {
-        const float y = __shfl_up(x, o);
-        if (lane >= o) x += y;
-    }
-    return x;
+    return bw_wave_scan(t < T ? g[((size_t)b * T + t) * H + h] : 0.f);
 }
 
 // Rows of x [B, T, H, D] into head-major fp32 [B*H, Tp, D]: with a norm
@@ -273,12 +286,8 @@ __global__ __launch_bounds__(256) void bw_state_scan_kernel(StateScanArgs p) {
             if (lane == 0) sRed[wv] = wsum;
         }
         if (wv == 0) {  // G: the in-chunk inclusive cumsum of the prefetched gate
-            float G = rg;
-            for (int o = 1; o < 64; o <<= 1) {
-                const float y = __shfl_up(G, o);
-                if (lane >= o) G += y;
-            }
-            const float Gl = __shfl(G, 63);
+            const float G = bw_wave_scan(rg);
+            const float Gl = lane_value(G, 63);
             sF[lane] = BWD ? p.scale * expf(G) : expf(Gl - G);
             if (lane == 0) sEl = expf(Gl);
         }
@@ -445,12 +454,8 @@ __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) 
             if (T2 == 1 && lane == 0) sRed[wv] = wsum;
         }
         if (wv == 0) {  // G: the in-chunk inclusive cumsum of the prefetched gate
-            float G = rg;
-            for (int o = 1; o < 64; o <<= 1) {
-                const float y = __shfl_up(G, o);
-                if (lane >= o) G += y;
-            }
-            const float Gl = __shfl(G, 63);
+            const float G = bw_wave_scan(rg);
+            const float Gl = lane_value(G, 63);
             sF[lane] = BWD ? p.scale * expf(G) : expf(Gl - G);
             if (lane == 0) sEl = expf(Gl);
         }
