@@ -100,6 +100,7 @@ CASES = [
     (1, 256, 2, 256, 256, 128, 64, torch.float32, False, True),    # fp32 operands
     (2, 100, 2, 64, 96, 16, 32, torch.float32, True, True),        # general shape, other slot count
     (1, 77, 3, 128, 128, 64, 16, torch.bfloat16, True, False),     # general shape in bf16
+    (2, 70, 2, 30, 18, 16, 16, torch.bfloat16, True, True),        # bf16, K and V not multiples of 4 (4-byte loads)
     # above 128 slots the readout and its adjoint run as tile GEMMs that stream the table
     (2, 150, 2, 64, 96, 256, 32, torch.float32, True, True),       # 256 slots (the reference's limit)
     (1, 70, 1, 128, 64, 200, 64, torch.bfloat16, True, True),      # 200 slots: ragged table tiles, bf16
