@@ -20,17 +20,18 @@
 //   dk_s = scale sum_{t>=s} e^{G_t-G_s} (dO_t.v_s) q_t + e^{G_last-G_s} D_{n+1} v_s
 //   dv_s = scale sum_{t>=s} e^{G_t-G_s} (q_t.k_s) dO_t + e^{G_last-G_s} D_{n+1}^T k_s
 //   dL/dG_t = q_t.dq_t - k_t.dk_t + [t = last] <D_{n+1}, S_{n+1}>,  dg = in-chunk reverse cumsum
-// The states and their cotangents are one sweep per (32-column tile, b, h)
-// that keeps its tile in LDS; outputs and the rows' cotangents are then
+// The states and their cotangents are one sweep per (state tile, b, h) that
+// keeps its tile in registers; outputs and the rows' cotangents are then
 // chunk-parallel, one workgroup per (chunk, h, b), with no reduction across
-// workgroups. The
-// readout adjoint runs per row (z = U(lam) raw, softmax of table z, u =
-// table^T p, weights = U(-lam) u) with the head's table and this
-// workgroup's share of the table cotangent on chip (up to 128 slots; above,
-// as tile GEMMs that stream the table); partial sums (table,
-// norm weights, per-column-tile boundary terms) are added in a fixed order,
-// so the result does not depend on scheduling. fp32 FMA loops over LDS
-// tiles, no matrix cores: a first, exact form of the training path.
+// workgroups. The readout adjoint runs per block of rows (z = U(lam) raw,
+// softmax of table z, u = table^T p, weights = U(-lam) u) with the head's
+// table and this workgroup's share of the table cotangent on chip (up to 128
+// slots; above, as tile GEMMs that stream the table); partial sums (table,
+// norm weights, per-tile boundary terms) are added in a fixed order, so the
+// result does not depend on scheduling. With bf16 operands the scans' and
+// chunk kernels' products and the recomputed readout's run on the matrix
+// cores with every fp32 operand split into two bf16 parts (about 16 mantissa
+// bits); with fp32 operands they are fp32 FMA loops, exact to fp32 rounding.
 #include <cmath>
 #include <type_traits>
 
