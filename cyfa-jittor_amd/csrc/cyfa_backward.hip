@@ -564,6 +564,7 @@ void launch_state_scan(const StateScanArgs& a, bool mfma, hipStream_t stream) {
 constexpr int GT_K = 32, GT_LD = 68;  // fp32 staging: [32][68] per operand
 constexpr int MT_LD = 40;             // bf16 staging: [64][40] per operand (32 k + 8 pad)
 constexpr int STAGE_BYTES = 4 * BC * MT_LD * 2;  // >= the fp32 staging's 2 * GT_K * GT_LD * 4
+constexpr int STAGE2_BYTES = 6 * BC * MT_LD * 2;  // tile_gemm_mf<2>: A and two B blocks, hi and lo
 static_assert(STAGE_BYTES >= 2 * GT_K * GT_LD * 4, "staging must hold either form");
 
 template <bool MF>
@@ -659,6 +660,115 @@ __device__ __forceinline__ float opB(const FB& fb, int kk, int j, int Kd) {
         return kk < Kd ? fb(kk, j) : 0.f;
 }
 
+// The matrix-core form of tile_gemm (above) for an output of 64 rows by
+// 64 NT columns in one pass over the contraction: A is staged once per
+// k-block and multiplied against NT B tiles, so that a row block feeding
+// several output tiles is read once (NT = 2 halves those reads against two
+// passes). acc[nb][i] = tile[16 w + 4 (lane / 16) + i][16 nb + lane % 16],
+// nb < 4 NT; the staging area holds (2 + 2 NT) 64-row blocks.
+template <int NT, class FA, class FB>
+__device__ __forceinline__ void tile_gemm_mf(FA fa, FB fb, int Kd, unsigned char* stage, float acc[4 * NT][4]) {
+    const int tid = threadIdx.x;
+    {
+        bf16_t* sah = reinterpret_cast<bf16_t*>(stage);  // hi and lo parts of A (64 rows) and of B (64 NT rows)
+        bf16_t* sal = sah + BC * MT_LD;
+        bf16_t* sbh = sal + BC * MT_LD;
+        bf16_t* sbl = sbh + NT * BC * MT_LD;
+        const int l = tid & 63, w = tid >> 6, lr = l & 15, lg = l >> 4;
+        const int r = tid >> 2, kg = tid & 3;  // staging: row r, k-group kg (8 k)
+        // RowsK4 operands: lane (r, kg) holds kk = k0 + 4 kg .. + 3 and
+        // k0 + 16 + 4 kg .. + 3; the others kk = k0 + 8 kg .. + 7
+        constexpr bool VA = std::is_same_v<FA, RowsK4>, VB = std::is_same_v<FB, RowsK4>;
+        constexpr bool JB = std::is_same_v<FB, RowsJ4>;  // B: lane (jq, kp) as in RowsJ4
+        const int jq = tid & 15, kp = tid >> 4;
+        float ra[8], rb[NT][8];
+        const auto fetch = [&](int k0) {
+            if constexpr (VA) {
+                const f32x4 lo4 = fa.load4(r, k0 + 4 * kg), hi4 = fa.load4(r, k0 + 16 + 4 * kg);
+#pragma unroll
+                for (int x = 0; x < 4; x++) ra[x] = lo4[x], ra[4 + x] = hi4[x];
+            } else {
+#pragma unroll
+                for (int x = 0; x < 8; x++) ra[x] = opA(fa, r, k0 + 8 * kg + x, Kd);
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {  // B's columns 64 nt ..
+                if constexpr (VB) {
+                    const f32x4 lo4 = fb.load4(64 * nt + r, k0 + 4 * kg), hi4 = fb.load4(64 * nt + r, k0 + 16 + 4 * kg);
+#pragma unroll
+                    for (int x = 0; x < 4; x++) rb[nt][x] = lo4[x], rb[nt][4 + x] = hi4[x];
+                } else if constexpr (JB) {  // rb[c] = B(k0 + 2 kp, 4 jq + c), rb[4 + c] = B(k0 + 2 kp + 1, 4 jq + c)
+                    const f32x4 r0 = fb.load4(k0 + 2 * kp, 64 * nt + 4 * jq), r1 = fb.load4(k0 + 2 * kp + 1, 64 * nt + 4 * jq);
+#pragma unroll
+                    for (int x = 0; x < 4; x++) rb[nt][x] = r0[x], rb[nt][4 + x] = r1[x];
+                } else {
+#pragma unroll
+                    for (int x = 0; x < 8; x++) rb[nt][x] = opB(fb, k0 + 8 * kg + x, 64 * nt + r, Kd);
+                }
+            }
+        };
+        // writes the 8 staged values of one operand in its lane order
+        const auto put = [&](bf16_t* base, bool split4, const bf16x8& v) {
+            if (split4) {
+                *reinterpret_cast<bf16x4*>(base + r * MT_LD + 4 * kg) = bf16x4{v[0], v[1], v[2], v[3]};
+                *reinterpret_cast<bf16x4*>(base + r * MT_LD + 16 + 4 * kg) = bf16x4{v[4], v[5], v[6], v[7]};
+            } else {
+                *reinterpret_cast<bf16x8*>(base + r * MT_LD + 8 * kg) = v;
+            }
+        };
+        fetch(0);
+        for (int k0 = 0; k0 < Kd; k0 += GT_K) {
+            __syncthreads();  // the staging tiles are free
+            bf16x8 vah, val;
+#pragma unroll
+            for (int x = 0; x < 8; x++) {
+                vah[x] = (bf16_t)ra[x];
+                val[x] = (bf16_t)(ra[x] - (float)vah[x]);
+            }
+            put(sah, VA, vah);
+            put(sal, VA, val);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                bf16x8 vbh, vbl;
+#pragma unroll
+                for (int x = 0; x < 8; x++) {
+                    vbh[x] = (bf16_t)rb[nt][x];
+                    vbl[x] = (bf16_t)(rb[nt][x] - (float)vbh[x]);
+                }
+                bf16_t* bh0 = sbh + 64 * nt * MT_LD;
+                bf16_t* bl0 = sbl + 64 * nt * MT_LD;
+                if constexpr (JB) {  // column 4 jq + c: the pair (k0 + 2 kp, + 1) as one 4-byte store
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        *reinterpret_cast<bf16x2*>(bh0 + (4 * jq + c) * MT_LD + 2 * kp) = bf16x2{vbh[c], vbh[4 + c]};
+                        *reinterpret_cast<bf16x2*>(bl0 + (4 * jq + c) * MT_LD + 2 * kp) = bf16x2{vbl[c], vbl[4 + c]};
+                    }
+                } else {
+                    put(bh0, VB, vbh);
+                    put(bl0, VB, vbl);
+                }
+            }
+            __syncthreads();
+            if (k0 + GT_K < Kd) fetch(k0 + GT_K);
+            const int ao = (16 * w + lr) * MT_LD + 8 * lg;
+            const bf16x8 ah = *reinterpret_cast<const bf16x8*>(sah + ao);
+            const bf16x8 al = *reinterpret_cast<const bf16x8*>(sal + ao);
+#pragma unroll
+            for (int nb = 0; nb < 4 * NT; nb++) {
+                const int bo = (16 * nb + lr) * MT_LD + 8 * lg;
+                const bf16x8 bh = *reinterpret_cast<const bf16x8*>(sbh + bo);
+                const bf16x8 bl = *reinterpret_cast<const bf16x8*>(sbl + bo);
+                f32x4 c = {acc[nb][0], acc[nb][1], acc[nb][2], acc[nb][3]};
+                c = mfma_bf16(al, bh, c);
+                c = mfma_bf16(ah, bl, c);
+                c = mfma_bf16(ah, bh, c);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[nb][i] = c[i];
+            }
+        }
+    }
+}
+
 template <bool MF, bool B_KCONTIG, class FA, class FB>
 __device__ __forceinline__ void tile_gemm(FA fa, FB fb, int Kd, unsigned char* stage, float acc[4][4]) {
     static_assert(!std::is_base_of_v<RowsK, FB> || B_KCONTIG, "RowsK: B contiguous along kk");
@@ -706,113 +816,42 @@ __device__ __forceinline__ void tile_gemm(FA fa, FB fb, int Kd, unsigned char* s
             }
         }
     } else {
-        bf16_t* sah = reinterpret_cast<bf16_t*>(stage);  // hi and lo parts of A and of B
-        bf16_t* sal = sah + BC * MT_LD;
-        bf16_t* sbh = sal + BC * MT_LD;
-        bf16_t* sbl = sbh + BC * MT_LD;
-        const int l = tid & 63, w = tid >> 6, lr = l & 15, lg = l >> 4;
-        const int r = tid >> 2, kg = tid & 3;  // staging: row r, k-group kg (8 k)
-        // RowsK4 operands: lane (r, kg) holds kk = k0 + 4 kg .. + 3 and
-        // k0 + 16 + 4 kg .. + 3; the others kk = k0 + 8 kg .. + 7
-        constexpr bool VA = std::is_same_v<FA, RowsK4>, VB = std::is_same_v<FB, RowsK4>;
-        constexpr bool JB = std::is_same_v<FB, RowsJ4>;  // B: lane (jq, kp) as in RowsJ4
-        const int jq = tid & 15, kp = tid >> 4;
-        float ra[8], rb[8];
-        const auto fetch = [&](int k0) {
-            if constexpr (VA) {
-                const f32x4 lo4 = fa.load4(r, k0 + 4 * kg), hi4 = fa.load4(r, k0 + 16 + 4 * kg);
-#pragma unroll
-                for (int x = 0; x < 4; x++) ra[x] = lo4[x], ra[4 + x] = hi4[x];
-            } else {
-#pragma unroll
-                for (int x = 0; x < 8; x++) ra[x] = opA(fa, r, k0 + 8 * kg + x, Kd);
-            }
-            if constexpr (VB) {
-                const f32x4 lo4 = fb.load4(r, k0 + 4 * kg), hi4 = fb.load4(r, k0 + 16 + 4 * kg);
-#pragma unroll
-                for (int x = 0; x < 4; x++) rb[x] = lo4[x], rb[4 + x] = hi4[x];
-            } else if constexpr (JB) {  // rb[c] = B(k0 + 2 kp, 4 jq + c), rb[4 + c] = B(k0 + 2 kp + 1, 4 jq + c)
-                const f32x4 r0 = fb.load4(k0 + 2 * kp, 4 * jq), r1 = fb.load4(k0 + 2 * kp + 1, 4 * jq);
-#pragma unroll
-                for (int x = 0; x < 4; x++) rb[x] = r0[x], rb[4 + x] = r1[x];
-            } else {
-#pragma unroll
-                for (int x = 0; x < 8; x++) rb[x] = opB(fb, k0 + 8 * kg + x, r, Kd);
-            }
-        };
-        // writes the 8 staged values of one operand in its lane order
-        const auto put = [&](bf16_t* base, bool split4, const bf16x8& v) {
-            if (split4) {
-                *reinterpret_cast<bf16x4*>(base + r * MT_LD + 4 * kg) = bf16x4{v[0], v[1], v[2], v[3]};
-                *reinterpret_cast<bf16x4*>(base + r * MT_LD + 16 + 4 * kg) = bf16x4{v[4], v[5], v[6], v[7]};
-            } else {
-                *reinterpret_cast<bf16x8*>(base + r * MT_LD + 8 * kg) = v;
-            }
-        };
-        fetch(0);
-        for (int k0 = 0; k0 < Kd; k0 += GT_K) {
-            __syncthreads();  // the staging tiles are free
-            bf16x8 vah, val, vbh, vbl;
-#pragma unroll
-            for (int x = 0; x < 8; x++) {
-                vah[x] = (bf16_t)ra[x];
-                val[x] = (bf16_t)(ra[x] - (float)vah[x]);
-                vbh[x] = (bf16_t)rb[x];
-                vbl[x] = (bf16_t)(rb[x] - (float)vbh[x]);
-            }
-            put(sah, VA, vah);
-            put(sal, VA, val);
-            if constexpr (JB) {  // column 4 jq + c: the pair (k0 + 2 kp, + 1) as one 4-byte store
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    *reinterpret_cast<bf16x2*>(sbh + (4 * jq + c) * MT_LD + 2 * kp) = bf16x2{vbh[c], vbh[4 + c]};
-                    *reinterpret_cast<bf16x2*>(sbl + (4 * jq + c) * MT_LD + 2 * kp) = bf16x2{vbl[c], vbl[4 + c]};
-                }
-            } else {
-                put(sbh, VB, vbh);
-                put(sbl, VB, vbl);
-            }
-            __syncthreads();
-            if (k0 + GT_K < Kd) fetch(k0 + GT_K);
-            const int ao = (16 * w + lr) * MT_LD + 8 * lg;
-            const bf16x8 ah = *reinterpret_cast<const bf16x8*>(sah + ao);
-            const bf16x8 al = *reinterpret_cast<const bf16x8*>(sal + ao);
-#pragma unroll
-            for (int nb = 0; nb < 4; nb++) {
-                const int bo = (16 * nb + lr) * MT_LD + 8 * lg;
-                const bf16x8 bh = *reinterpret_cast<const bf16x8*>(sbh + bo);
-                const bf16x8 bl = *reinterpret_cast<const bf16x8*>(sbl + bo);
-                f32x4 c = {acc[nb][0], acc[nb][1], acc[nb][2], acc[nb][3]};
-                c = mfma_bf16(al, bh, c);
-                c = mfma_bf16(ah, bl, c);
-                c = mfma_bf16(ah, bh, c);
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[nb][i] = c[i];
-            }
-        }
+        tile_gemm_mf<1>(fa, fb, Kd, stage, acc);
     }
 }
 
-// acc[a][b] *= f(row of (a, b)).
-template <bool MF, class F>
-__device__ __forceinline__ void tile_scale_rows(float acc[4][4], F f) {
+// acc[a][b] *= f(row of (a, b)); NA = 4 NT for a matrix-core tile of 64 NT
+// columns.
+template <bool MF, int NA = 4, class F>
+__device__ __forceinline__ void tile_scale_rows(float acc[NA][4], F f) {
 #pragma unroll
-    for (int a = 0; a < 4; a++)
+    for (int a = 0; a < NA; a++)
 #pragma unroll
         for (int b = 0; b < 4; b++) acc[a][b] *= f(TileMap<MF>::row(a, b));
 }
 
-// Writes this thread's part of a 64 x 64 tile (columns d0 ..) into head-major
-// rows dst [.., D], times a scale.
-template <bool MF>
-__device__ __forceinline__ void tile_store(float acc[4][4], float* dst, int D, int d0, float scale) {
+// Writes this thread's part of a 64 x 16 NA tile (columns d0 ..) into
+// head-major rows dst [.., D], times a scale.
+template <bool MF, int NA = 4>
+__device__ __forceinline__ void tile_store(float acc[NA][4], float* dst, int D, int d0, float scale) {
 #pragma unroll
-    for (int a = 0; a < 4; a++)
+    for (int a = 0; a < NA; a++)
 #pragma unroll
         for (int b = 0; b < 4; b++) {
             const int t = TileMap<MF>::row(a, b), c = d0 + TileMap<MF>::col(a, b);
             if (c < D) dst[(size_t)t * D + c] = scale * acc[a][b];
         }
+}
+
+// tile_gemm over 64 NT output columns: NT = 2 only on the matrix cores.
+template <bool MF, bool B_KCONTIG, int NT, class FA, class FB>
+__device__ __forceinline__ void tile_gemm_nt(FA fa, FB fb, int Kd, unsigned char* stage, float acc[4 * NT][4]) {
+    if constexpr (NT == 1) {
+        tile_gemm<MF, B_KCONTIG>(fa, fb, Kd, stage, acc);
+    } else {
+        static_assert(MF && NT == 2, "wide tiles on the matrix cores");
+        tile_gemm_mf<NT>(fa, fb, Kd, stage, acc);
+    }
 }
 
 // Masked, decayed scores of one chunk into P: P[t][s] = [s <= t] e^{G_t - G_s}
@@ -853,7 +892,10 @@ __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
     using RK = std::conditional_t<V4, RowsK4, RowsK>;  // 16-byte row loads when aligned
     using RJ = std::conditional_t<V4, RowsJ4, RowsJ>;
     __shared__ float sA[BC][BC + 1];
-    __shared__ __align__(16) unsigned char sStage[STAGE_BYTES];
+    // (output tiles of 64 columns: two at a time read q once instead of twice
+    // but measured slower here, 80 -> 84 us at configuration 3)
+    constexpr int NT = 1, NA = 4 * NT;
+    __shared__ __align__(16) unsigned char sStage[NT == 2 ? STAGE2_BYTES : STAGE_BYTES];
     __shared__ float sG[BC], sEq[BC];
     const int tid = threadIdx.x, n = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int Kq = a.Kq, Vd = a.Vd, t0 = n * BC;
@@ -868,26 +910,26 @@ __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
     }
     chunk_scores<MF, V4>(q, k, Kq, sG, sStage, sA);
     float* out = a.out + (bh * a.Tp + t0) * Vd;
-    for (int d0 = 0; d0 < Vd; d0 += BC) {
-        float acc[4][4] = {};
-        tile_gemm<MF, false>(RK(q, Kq, BC, Kq), RJ(S + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
-        tile_scale_rows<MF>(acc, [&](int t) { return sEq[t]; });
-        tile_gemm<MF, false>([&](int i, int kk) { return sA[i][kk]; }, RJ(v + d0, Vd, BC, Vd - d0), BC, sStage,
-                             acc);
+    for (int d0 = 0; d0 < Vd; d0 += BC * NT) {
+        float acc[NA][4] = {};
+        tile_gemm_nt<MF, false, NT>(RK(q, Kq, BC, Kq), RJ(S + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
+        tile_scale_rows<MF, NA>(acc, [&](int t) { return sEq[t]; });
+        tile_gemm_nt<MF, false, NT>([&](int i, int kk) { return sA[i][kk]; }, RJ(v + d0, Vd, BC, Vd - d0), BC,
+                                    sStage, acc);
         if (!a.out_bthd) {
             if (a.bf16) {
 #pragma unroll
-                for (int i = 0; i < 4; i++)
+                for (int i = 0; i < NA; i++)
 #pragma unroll
                     for (int j = 0; j < 4; j++) acc[i][j] = (float)(bf16_t)(a.scale * acc[i][j]);
-                tile_store<MF>(acc, out, Vd, d0, 1.f);
+                tile_store<MF, NA>(acc, out, Vd, d0, 1.f);
             } else {
-                tile_store<MF>(acc, out, Vd, d0, a.scale);
+                tile_store<MF, NA>(acc, out, Vd, d0, a.scale);
             }
             continue;
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < NA; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int t = t0 + TileMap<MF>::row(i, j), c = d0 + TileMap<MF>::col(i, j);
@@ -919,9 +961,13 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     using RK = std::conditional_t<V4, RowsK4, RowsK>;  // 16-byte row loads when aligned
     using RJ = std::conditional_t<V4, RowsJ4, RowsJ>;
     __shared__ float sA[BC][BC + 1], sB[BC][BC + 1];
-    __shared__ __align__(16) unsigned char sStage[STAGE_BYTES];
-    // (the row factors e^{G_t} and e^{G_last - G_t} are formed where used:
-    // without their two arrays the LDS allows three workgroups per CU)
+    // Output tiles of 64 NT columns: on the matrix cores two at a time, so that
+    // each row block a product reads (dO, v, k, and the other operands' rows)
+    // is read once per pair of tiles (the kernel reads HBM at its rate: 222 ->
+    // 184 us at configuration 3)
+    constexpr int NT = MF && V4 ? 2 : 1, NA = 4 * NT;
+    __shared__ __align__(16) unsigned char sStage[NT == 2 ? STAGE2_BYTES : STAGE_BYTES];
+    // (the row factors e^{G_t} and e^{G_last - G_t} are formed where used)
     __shared__ float sG[BC];
     const int tid = threadIdx.x, n = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int Kq = a.Kq, Vd = a.Vd, t0 = n * BC;
@@ -939,33 +985,33 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     chunk_scores<MF, V4>(q, k, Kq, sG, sStage, sA);
     chunk_scores<MF, V4>(dO, v, Vd, sG, sStage, sB);
     const float sc = a.scale;
-    for (int d0 = 0; d0 < Kq; d0 += BC) {
+    for (int d0 = 0; d0 < Kq; d0 += BC * NT) {
         // dq = scale (e^{G_t} dO_t S_n^T + B k)
-        float acc[4][4] = {};
-        tile_gemm<MF, true>(RK(dO, Vd, BC, Vd), RK(S + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
-        tile_scale_rows<MF>(acc, [&](int t) { return expf(sG[t]); });
-        tile_gemm<MF, false>([&](int i, int kk) { return sB[i][kk]; }, RJ(k + d0, Kq, BC, Kq - d0), BC, sStage,
+        float acc[NA][4] = {};
+        tile_gemm_nt<MF, true, NT>(RK(dO, Vd, BC, Vd), RK(S + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
+        tile_scale_rows<MF, NA>(acc, [&](int t) { return expf(sG[t]); });
+        tile_gemm_nt<MF, false, NT>([&](int i, int kk) { return sB[i][kk]; }, RJ(k + d0, Kq, BC, Kq - d0), BC, sStage,
                              acc);
-        tile_store<MF>(acc, a.dq + (bh * a.Tp + t0) * Kq, Kq, d0, sc);
+        tile_store<MF, NA>(acc, a.dq + (bh * a.Tp + t0) * Kq, Kq, d0, sc);
         // dk = e^{G_last - G_s} v_s D_{n+1}^T + scale B^T q
 #pragma unroll
-        for (int x = 0; x < 4; x++)
+        for (int x = 0; x < NA; x++)
 #pragma unroll
             for (int y = 0; y < 4; y++) acc[x][y] = 0.f;
-        tile_gemm<MF, true>(RK(v, Vd, BC, Vd), RK(D + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
-        tile_scale_rows<MF>(acc, [&](int t) { return expf(sG[BC - 1] - sG[t]); });
-        tile_gemm<MF, false>([&](int i, int kk) { return sc * sB[kk][i]; }, RJ(q + d0, Kq, BC, Kq - d0), BC,
+        tile_gemm_nt<MF, true, NT>(RK(v, Vd, BC, Vd), RK(D + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
+        tile_scale_rows<MF, NA>(acc, [&](int t) { return expf(sG[BC - 1] - sG[t]); });
+        tile_gemm_nt<MF, false, NT>([&](int i, int kk) { return sc * sB[kk][i]; }, RJ(q + d0, Kq, BC, Kq - d0), BC,
                              sStage, acc);
-        tile_store<MF>(acc, a.dk + (bh * a.Tp + t0) * Kq, Kq, d0, 1.f);
+        tile_store<MF, NA>(acc, a.dk + (bh * a.Tp + t0) * Kq, Kq, d0, 1.f);
     }
-    for (int d0 = 0; d0 < Vd; d0 += BC) {
+    for (int d0 = 0; d0 < Vd; d0 += BC * NT) {
         // dv = e^{G_last - G_s} k_s D_{n+1} + scale A^T dO
-        float acc[4][4] = {};
-        tile_gemm<MF, false>(RK(k, Kq, BC, Kq), RJ(D + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
-        tile_scale_rows<MF>(acc, [&](int t) { return expf(sG[BC - 1] - sG[t]); });
-        tile_gemm<MF, false>([&](int i, int kk) { return sc * sA[kk][i]; }, RJ(dO + d0, Vd, BC, Vd - d0), BC,
+        float acc[NA][4] = {};
+        tile_gemm_nt<MF, false, NT>(RK(k, Kq, BC, Kq), RJ(D + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
+        tile_scale_rows<MF, NA>(acc, [&](int t) { return expf(sG[BC - 1] - sG[t]); });
+        tile_gemm_nt<MF, false, NT>([&](int i, int kk) { return sc * sA[kk][i]; }, RJ(dO + d0, Vd, BC, Vd - d0), BC,
                              sStage, acc);
-        tile_store<MF>(acc, a.dv + (bh * a.Tp + t0) * Vd, Vd, d0, 1.f);
+        tile_store<MF, NA>(acc, a.dv + (bh * a.Tp + t0) * Vd, Vd, d0, 1.f);
     }
 }
 
