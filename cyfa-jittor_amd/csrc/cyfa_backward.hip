@@ -1157,9 +1157,12 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
 // BF the operands are bf16 values and the products exact), for calls whose
 // tile products run on the matrix cores. The table sits in LDS once as its
 // two bf16 parts, row-major [r][m]: the logits read its rows as B fragments,
-// u gathers its columns. Waves and accumulator tiles as in
-// bw_fwd_readout_kernel; the softmax reductions on DPP moves.
+// u gathers its columns. Wave w takes row tile w & 1 and the slot tiles
+// 2 (w >> 1), + 1 of both products; the softmax reductions on DPP moves.
 constexpr int RO_LDB = BWD_TABLE_M + 8;  // bf16 rows of the split table and row blocks
+// One workgroup per CU fits the LDS; eight waves put two on each SIMD, so
+// that one wave's LDS reads and softmax overlap the other's products.
+constexpr int RO_MF_THREADS = 512;
 
 // lane (lr, lg) gets X[r0 + lr][k0 + 8 lg .. + 7] of a row-major bf16 tile
 __device__ __forceinline__ bf16x8 ro_row(const bf16_t* X, int r0, int k0) {
@@ -1185,11 +1188,11 @@ __device__ __forceinline__ void split_store(bf16_t* hi, bf16_t* lo, int idx, flo
 }
 
 template <bool BF>
-__global__ __launch_bounds__(256) void bw_fwd_readout_mf_kernel(const float* raw, const float* cs, const float* sn,
+__global__ __launch_bounds__(RO_MF_THREADS) void bw_fwd_readout_mf_kernel(const float* raw, const float* cs, const float* sn,
                                                                 const float* table, int B, int Tp, int H, int M,
                                                                 int per_wg, float* wts) {
-    constexpr int TM = BWD_TABLE_M, LB = RO_LDB, RB = 32;
-    static_assert(TM == 128 && RB == 32, "eight 16-wide tiles of slots, two of rows");
+    constexpr int TM = BWD_TABLE_M, LB = RO_LDB, RB = 32, NT = RO_MF_THREADS, NW = NT / 64;
+    static_assert(TM == 128 && RB == 32 && NW == 8, "eight 16-wide tiles of slots, two of rows; two slot tiles per wave");
     __shared__ __align__(16) bf16_t sTh[TM * LB], sTl[TM * LB];  // rows R .. 127 and columns M .. 127 zero
     __shared__ __align__(16) bf16_t sZh[RB * LB], sZl[RB * LB], sPh[RB * LB], sPl[RB * LB];
     __shared__ float sL[RB][TM + 4];
@@ -1197,13 +1200,13 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_mf_kernel(const float* raw
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, h = blockIdx.y;
     const int lr = lane & 15;
     const int R = M - 1, P = M / 2, rows = B * Tp;
-    for (int e = tid; e < TM * TM; e += 256) {
+    for (int e = tid; e < TM * TM; e += NT) {
         const int r = e / TM, m = e % TM;
         split_store(sTh, sTl, r * LB + m, (r < R && m < M) ? bw_rnd<BF>(table[((size_t)h * R + r) * M + m]) : 0.f);
     }
     const auto row_of = [&](int rho) { return ((size_t)(rho / Tp) * H + h) * Tp + rho % Tp; };
-    const int it = wv & 1, ct0 = 4 * (wv >> 1);
-    constexpr int NX = RB * (TM / 2) / 256;
+    const int it = wv & 1, ct0 = 2 * (wv >> 1);
+    constexpr int NX = RB * (TM / 2) / NT;
     const int b_end = min(rows, (int)(blockIdx.x + 1) * per_wg * RB);
     const bw_rsrc_t rcs = bw_rsrc(cs, (size_t)rows * H * P), rsn = bw_rsrc(sn, (size_t)rows * H * P),
                     rraw = bw_rsrc(raw, (size_t)rows * H * M);  // every head's rows
@@ -1211,7 +1214,7 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_mf_kernel(const float* raw
     const auto load_block = [&](int b0) {
 #pragma unroll
         for (int x = 0; x < NX; x++) {
-            const int e = tid + 256 * x, i = e / (TM / 2), pr = e % (TM / 2), rho = b0 + i;
+            const int e = tid + NT * x, i = e / (TM / 2), pr = e % (TM / 2), rho = b0 + i;
             const bool live = rho < b_end && pr < P;
             const uint32_t row = live ? (uint32_t)row_of(rho) : 0u;
             nc[x] = bw_load(rcs, (row * (uint32_t)P + (uint32_t)pr) * 4u, live);
@@ -1226,7 +1229,7 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_mf_kernel(const float* raw
         __syncthreads();  // the table is staged; the previous block's tiles are done with
 #pragma unroll
         for (int x = 0; x < NX; x++) {
-            const int e = tid + 256 * x, i = e / (TM / 2), pr = e % (TM / 2);
+            const int e = tid + NT * x, i = e / (TM / 2), pr = e % (TM / 2);
             const bool live = b0 + i < b_end && pr < P;
             const float c = live ? nc[x] : 1.f, s = ns[x];
             sCs[i][pr] = c;
@@ -1237,14 +1240,14 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_mf_kernel(const float* raw
         load_block(b0 + RB);  // the next block (past the end: dead loads)
         __syncthreads();
         {  // logits l[i][r] = sum_m z[i][m] table[r][m]
-            f32x4 acc[4];
+            f32x4 acc[2];
 #pragma unroll
-            for (int t = 0; t < 4; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int t = 0; t < 2; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int k0 = 0; k0 < TM; k0 += 32) {
                 const bf16x8 ah = ro_row(sZh, 16 * it, k0), al = ro_row(sZl, 16 * it, k0);
 #pragma unroll
-                for (int t = 0; t < 4; t++) {
+                for (int t = 0; t < 2; t++) {
                     const bf16x8 bh = ro_row(sTh, 16 * (ct0 + t), k0), bl = ro_row(sTl, 16 * (ct0 + t), k0);
                     acc[t] = mfma_bf16(al, bh, acc[t]);
                     acc[t] = mfma_bf16(ah, bl, acc[t]);
@@ -1253,12 +1256,12 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_mf_kernel(const float* raw
             }
             const int lg = lane >> 4;
 #pragma unroll
-            for (int t = 0; t < 4; t++)
+            for (int t = 0; t < 2; t++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) sL[16 * it + 4 * lg + q][16 * (ct0 + t) + lr] = acc[t][q];
         }
         __syncthreads();
-        for (int i = wv; i < RB; i += 4) {
+        for (int i = wv; i < RB; i += NW) {
             const float l0 = lane < R ? sL[i][lane] : -INFINITY, l1 = lane + 64 < R ? sL[i][lane + 64] : -INFINITY;
             const float mx = bw_wave_max(fmaxf(l0, l1));
             const float e0 = lane < R ? expf(l0 - mx) : 0.f, e1 = lane + 64 < R ? expf(l1 - mx) : 0.f;
@@ -1270,14 +1273,14 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_mf_kernel(const float* raw
         // u[i][m] = sum_r p[i][r] table[r][m] (p and the table zero at r >= R); the
         // weights' pair (2 pr, 2 pr + 1) sits in lanes (lr, lr ^ 1), swapped in by
         // quad_perm [1,0,3,2]
-        f32x4 acc[4];
+        f32x4 acc[2];
 #pragma unroll
-        for (int t = 0; t < 4; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < 2; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int k0 = 0; k0 < TM; k0 += 32) {
             const bf16x8 ah = ro_row(sPh, 16 * it, k0), al = ro_row(sPl, 16 * it, k0);
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
+            for (int t = 0; t < 2; t++) {
                 const bf16x8 bh = ro_col(sTh, k0, 16 * (ct0 + t)), bl = ro_col(sTl, k0, 16 * (ct0 + t));
                 acc[t] = mfma_bf16(al, bh, acc[t]);
                 acc[t] = mfma_bf16(ah, bl, acc[t]);
@@ -1287,7 +1290,7 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_mf_kernel(const float* raw
         const bool odd = (lr & 1) != 0;
         const int lk = lane >> 4;
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
+        for (int t = 0; t < 2; t++) {
             const int m = 16 * (ct0 + t) + lr, pr = m >> 1;
 #pragma unroll
             for (int q = 0; q < 4; q++) {
@@ -1313,11 +1316,14 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_mf_kernel(const float* raw
 // on the fp32 matrix cores, v_mfma_f32_16x16x4_f32 (fp32 operands, fp32
 // accumulation): lane l holds A[l % 16][l / 16] and B[l / 16][l % 16] of a
 // 16 x 4 by 4 x 16 step and rows 4 (l / 16) .. + 3 of column l % 16 of the
-// 16 x 16 result. Grid (workgroups per head, H), 256 threads: a workgroup
+// 16 x 16 result. Grid (workgroups per head, H), 512 threads: a workgroup
 // takes per_wg blocks of 32 rows (bwd_ro_per_wg) and keeps its part of dtable
-// in the accumulators (wave w owns its 16 x 16 tiles (r, m) of columns
-// m in 32 w .. 32 w + 31).
+// in the accumulators (wave w owns the 16 x 16 tiles (r, m) of columns
+// m in 16 w .. 16 w + 15). The LDS holds one workgroup per CU; its eight
+// waves put two on each SIMD, so that one wave's LDS reads overlap the
+// other's matrix-core steps.
 constexpr int RO_BLK = BWD_RO_BLOCK;
+constexpr int RO_ADJ_THREADS = 512;
 struct ReadoutGradArgs {
     const float *raw, *cs, *sn, *table, *dwts;  // head-major rows; table [H, M-1, M]
     float *draw, *dlam, *dtab;                  // dtab: [H, workgroups, (M-1) M]
@@ -1325,32 +1331,33 @@ struct ReadoutGradArgs {
     int per_wg;                                 // blocks of 32 rows per workgroup
 };
 
-__global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
-    constexpr int TM = BWD_TABLE_M, LD = RO_LD;
+__global__ __launch_bounds__(RO_ADJ_THREADS) void bw_readout_kernel(ReadoutGradArgs a) {
+    constexpr int TM = BWD_TABLE_M, LD = RO_LD, NT = RO_ADJ_THREADS, NW = NT / 64;
+    static_assert(NW == 8, "two row tiles x four pairs of slot tiles; one 16-column dtable tile per wave");
     static_assert(RO_BLK == 32 && TM == 128, "two 16-row tiles of rows, eight 16-wide tiles of slots");
     __shared__ float sTab[TM * LD];  // rows R .. 127 and columns M .. 127 zero
     __shared__ float sZ[RO_BLK][LD], sDU[RO_BLK][LD], sP[RO_BLK][LD], sDL[RO_BLK][LD];
     __shared__ float sCs[RO_BLK][TM / 2], sSn[RO_BLK][TM / 2];
-    __shared__ float sLam[RO_BLK][2];
+    __shared__ float sLam[RO_BLK][NW / 2];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, blk = blockIdx.x, h = blockIdx.y;
     const int lr = lane & 15, lk = lane >> 4;  // operand row / column and k of this lane
     const int M = a.M, R = M - 1, P = M / 2, RM = R * M;
-    for (int e = tid; e < TM * LD; e += 256) {  // the table, zero beyond R x M
+    for (int e = tid; e < TM * LD; e += NT) {  // the table, zero beyond R x M
         const int r = e / LD, m = e % LD;
         sTab[e] = (r < R && m < M) ? a.table[((size_t)h * R + r) * M + m] : 0.f;
     }
     // GEMMs over the block: wave wv takes row tile it = wv & 1 and the column
-    // tiles 4 (wv >> 1) .. + 3 of the logits (r) and of dz, u (m)
-    const int it = wv & 1, ct0 = 4 * (wv >> 1);
-    f32x4v dacc[8][2];  // dtable tiles (r tile, m tile 2 wv + mt)
+    // tiles 2 (wv >> 1), + 1 of the logits (r) and of dz, u (m)
+    const int it = wv & 1, ct0 = 2 * (wv >> 1);
+    f32x4v dacc[8];  // dtable tiles (r tile, m tile wv)
 #pragma unroll
-    for (int rt = 0; rt < 8; rt++) dacc[rt][0] = dacc[rt][1] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    for (int rt = 0; rt < 8; rt++) dacc[rt] = f32x4v{0.f, 0.f, 0.f, 0.f};
     const int rows = a.B * a.Tp;
     // A block's inputs, element x of this thread = (row i, pair pr) = e / 64,
-    // e % 64, e = tid + 256 x: loaded one block ahead through buffer
+    // e % 64, e = tid + NT x: loaded one block ahead through buffer
     // resources (rows < 2^21, M <= 128: offsets below 2^30), predicated
     // through the offset, so that no block waits for its own loads.
-    constexpr int NX = RO_BLK * (TM / 2) / 256;
+    constexpr int NX = RO_BLK * (TM / 2) / NT;
     const int b_end = min(rows, (blk + 1) * a.per_wg * RO_BLK);
     const bw_rsrc_t rcs = bw_rsrc(a.cs, (size_t)rows * a.H * P), rsn = bw_rsrc(a.sn, (size_t)rows * a.H * P),
                     rraw = bw_rsrc(a.raw, (size_t)rows * a.H * M), rdw = bw_rsrc(a.dwts, (size_t)rows * a.H * M);
@@ -1358,7 +1365,7 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
     const auto load_block = [&](int b0) {
 #pragma unroll
         for (int x = 0; x < NX; x++) {
-            const int e = tid + 256 * x, i = e / (TM / 2), pr = e % (TM / 2), rho = b0 + i;
+            const int e = tid + NT * x, i = e / (TM / 2), pr = e % (TM / 2), rho = b0 + i;
             const bool live = rho < b_end && pr < P;
             const uint32_t row = live ? (uint32_t)(((rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp) : 0u;
             nc[x] = bw_load(rcs, (row * (uint32_t)P + (uint32_t)pr) * 4u, live);
@@ -1376,7 +1383,7 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
         // z = U(lam) raw and du = U(lam) dweights
 #pragma unroll
         for (int x = 0; x < NX; x++) {
-            const int e = tid + 256 * x, i = e / (TM / 2), pr = e % (TM / 2);
+            const int e = tid + NT * x, i = e / (TM / 2), pr = e % (TM / 2);
             const bool live = b0 + i < b_end && pr < P;
             const float c = live ? nc[x] : 1.f, s = ns[x];  // zero inputs where !live
             sCs[i][pr] = c;
@@ -1390,20 +1397,20 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
         __syncthreads();
         // logits l[i][r] = sum_m z[i][m] table[r][m] and dp[i][r] = sum_m du[i][m] table[r][m]
         {
-            f32x4v accl[4], accd[4];
+            f32x4v accl[2], accd[2];
 #pragma unroll
-            for (int t = 0; t < 4; t++) accl[t] = accd[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+            for (int t = 0; t < 2; t++) accl[t] = accd[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
             for (int k0 = 0; k0 < TM; k0 += 4) {
                 const float az = sZ[16 * it + lr][k0 + lk], ad = sDU[16 * it + lr][k0 + lk];
 #pragma unroll
-                for (int t = 0; t < 4; t++) {
+                for (int t = 0; t < 2; t++) {
                     const float bt = sTab[(16 * (ct0 + t) + lr) * LD + k0 + lk];
                     accl[t] = mfma4(az, bt, accl[t]);
                     accd[t] = mfma4(ad, bt, accd[t]);
                 }
             }
 #pragma unroll
-            for (int t = 0; t < 4; t++)
+            for (int t = 0; t < 2; t++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     sP[16 * it + 4 * lk + q][16 * (ct0 + t) + lr] = accl[t][q];
@@ -1411,8 +1418,8 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
                 }
         }
         __syncthreads();
-        // softmax and dl per row: wave wv takes rows wv, wv + 4, ...; lanes take slots lane, lane + 64
-        for (int i = wv; i < RO_BLK; i += 4) {
+        // softmax and dl per row: wave wv takes rows wv, wv + NW, ...; lanes take slots lane, lane + 64
+        for (int i = wv; i < RO_BLK; i += NW) {
             const float l0 = lane < R ? sP[i][lane] : -INFINITY, l1 = lane + 64 < R ? sP[i][lane + 64] : -INFINITY;
             const float mx = bw_wave_max(fmaxf(l0, l1));
             const float e0 = lane < R ? expf(l0 - mx) : 0.f, e1 = lane + 64 < R ? expf(l1 - mx) : 0.f;
@@ -1429,13 +1436,13 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
         // dz[i][m] = sum_r dl[i][r] table[r][m] and u[i][m] = sum_r p[i][r] table[r][m]
         // (p and dl are zero at r >= R, as is the table); then draw and the clock's share
         {
-            f32x4v accz[4], accu[4];
+            f32x4v accz[2], accu[2];
 #pragma unroll
-            for (int t = 0; t < 4; t++) accz[t] = accu[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+            for (int t = 0; t < 2; t++) accz[t] = accu[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
             for (int k0 = 0; k0 < TM; k0 += 4) {
                 const float al = sDL[16 * it + lr][k0 + lk], ap = sP[16 * it + lr][k0 + lk];
 #pragma unroll
-                for (int t = 0; t < 4; t++) {
+                for (int t = 0; t < 2; t++) {
                     const float bt = sTab[(k0 + lk) * LD + 16 * (ct0 + t) + lr];
                     accz[t] = mfma4(al, bt, accz[t]);
                     accu[t] = mfma4(ap, bt, accu[t]);
@@ -1450,7 +1457,7 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
             const bool odd = (lr & 1) != 0;
             float dl[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
+            for (int t = 0; t < 2; t++) {
                 const int m = 16 * (ct0 + t) + lr, pr = m >> 1;
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
@@ -1470,8 +1477,8 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
                     }
                 }
             }
-            // the row's share over this wave's 16 lanes (its four column tiles summed above,
-            // in tile order), then the two waves of the row tile in wave order
+            // the row's share over this wave's 16 lanes (its two column tiles summed above,
+            // in tile order), then the four waves of the row tile in wave order
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const float v = wave_sum<16>(dl[q]);
@@ -1481,38 +1488,29 @@ __global__ __launch_bounds__(256) void bw_readout_kernel(ReadoutGradArgs a) {
         __syncthreads();
         if (tid < RO_BLK && b0 + tid < rows) {  // the clock's share per row
             const int rho = b0 + tid;
-            a.dlam[((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp] = sLam[tid][0] + sLam[tid][1];
+            a.dlam[((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp] =
+                (sLam[tid][0] + sLam[tid][1]) + (sLam[tid][2] + sLam[tid][3]);
         }
         // dtable[r][m] += sum_i p[i][r] du[i][m] + dl[i][r] z[i][m] over the block's rows
         for (int k0 = 0; k0 < RO_BLK; k0 += 4) {
-            float bu[2], bz[2];
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
-                bu[mt] = sDU[k0 + lk][16 * (2 * wv + mt) + lr];
-                bz[mt] = sZ[k0 + lk][16 * (2 * wv + mt) + lr];
-            }
+            const float bu = sDU[k0 + lk][16 * wv + lr], bz = sZ[k0 + lk][16 * wv + lr];
 #pragma unroll
             for (int rt = 0; rt < 8; rt++) {
                 const float ap = sP[k0 + lk][16 * rt + lr], al = sDL[k0 + lk][16 * rt + lr];
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++) {
-                    dacc[rt][mt] = mfma4(ap, bu[mt], dacc[rt][mt]);
-                    dacc[rt][mt] = mfma4(al, bz[mt], dacc[rt][mt]);
-                }
+                dacc[rt] = mfma4(ap, bu, dacc[rt]);
+                dacc[rt] = mfma4(al, bz, dacc[rt]);
             }
         }
     }
-    // lane holds dtable rows 16 rt + 4 lk + q of column 16 (2 wv + mt) + lr
+    // lane holds dtable rows 16 rt + 4 lk + q of column 16 wv + lr
     float* dst = a.dtab + ((size_t)h * gridDim.x + blk) * RM;
 #pragma unroll
     for (int rt = 0; rt < 8; rt++)
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int r = 16 * rt + 4 * lk + q, m = 16 * (2 * wv + mt) + lr;
-                if (r < R && m < M) dst[r * M + m] = dacc[rt][mt][q];
-            }
+        for (int q = 0; q < 4; q++) {
+            const int r = 16 * rt + 4 * lk + q, m = 16 * wv + lr;
+            if (r < R && m < M) dst[r * M + m] = dacc[rt][q];
+        }
 }
 
 // The readout and its adjoint for 128 < M <= 256 slots, where a head's table
@@ -2105,10 +2103,10 @@ int launch_chunk_readout(const float* raw, const float* cs, const float* sn, con
     const int per = bwd_ro_per_wg(B, Tp, H), blocks = (B * Tp + BWD_RO_BLOCK - 1) / BWD_RO_BLOCK;
     const dim3 grid((blocks + per - 1) / per, H);
     if (split && bf16)
-        hipLaunchKernelGGL(bw_fwd_readout_mf_kernel<true>, grid, blk, 0, stream, raw, cs, sn, table, B, Tp, H, M, per,
+        hipLaunchKernelGGL(bw_fwd_readout_mf_kernel<true>, grid, dim3(RO_MF_THREADS), 0, stream, raw, cs, sn, table, B, Tp, H, M, per,
                            wts);
     else if (split)
-        hipLaunchKernelGGL(bw_fwd_readout_mf_kernel<false>, grid, blk, 0, stream, raw, cs, sn, table, B, Tp, H, M, per,
+        hipLaunchKernelGGL(bw_fwd_readout_mf_kernel<false>, grid, dim3(RO_MF_THREADS), 0, stream, raw, cs, sn, table, B, Tp, H, M, per,
                            wts);
     else if (bf16)
         hipLaunchKernelGGL(bw_fwd_readout_kernel<true>, grid, blk, 0, stream, raw, cs, sn, table, B, Tp, H, M, per,
@@ -2264,7 +2262,7 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
         hipLaunchKernelGGL(bw_wide_dtable_kernel, dim3((M - 1 + BC - 1) / BC, (M + BC - 1) / BC, H * ws.ro_blocks), blk, 0,
                            stream, wa);
     } else {
-        hipLaunchKernelGGL(bw_readout_kernel, dim3(ws.ro_blocks, H), blk, 0, stream, ro);
+        hipLaunchKernelGGL(bw_readout_kernel, dim3(ws.ro_blocks, H), dim3(RO_ADJ_THREADS), 0, stream, ro);
     }
     // pass 1, with the pass-1 output's cotangent as dO
     StateScanArgs s1 = f1;
