@@ -1158,11 +1158,12 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
 // tile products run on the matrix cores. The table sits in LDS once as its
 // two bf16 parts, row-major [r][m]: the logits read its rows as B fragments,
 // u gathers its columns. Wave w takes row tile w & 1 and the slot tiles
-// 2 (w >> 1), + 1 of both products; the softmax reductions on DPP moves.
+// CPW (w >> 1) .. + CPW - 1 of both products (CPW = 16 / waves); the softmax
+// reductions on DPP moves.
 constexpr int RO_LDB = BWD_TABLE_M + 8;  // bf16 rows of the split table and row blocks
-// One workgroup per CU fits the LDS; eight waves put two on each SIMD, so
-// that one wave's LDS reads and softmax overlap the other's products.
-constexpr int RO_MF_THREADS = 512;
+// One workgroup per CU fits the LDS; its waves put several on each SIMD, so
+// that one wave's LDS reads and softmax overlap another's products.
+constexpr int RO_MF_THREADS = 1024;
 
 // lane (lr, lg) gets X[r0 + lr][k0 + 8 lg .. + 7] of a row-major bf16 tile
 __device__ __forceinline__ bf16x8 ro_row(const bf16_t* X, int r0, int k0) {
@@ -1191,8 +1192,8 @@ template <bool BF>
 __global__ __launch_bounds__(RO_MF_THREADS) void bw_fwd_readout_mf_kernel(const float* raw, const float* cs, const float* sn,
                                                                 const float* table, int B, int Tp, int H, int M,
                                                                 int per_wg, float* wts) {
-    constexpr int TM = BWD_TABLE_M, LB = RO_LDB, RB = 32, NT = RO_MF_THREADS, NW = NT / 64;
-    static_assert(TM == 128 && RB == 32 && NW == 8, "eight 16-wide tiles of slots, two of rows; two slot tiles per wave");
+    constexpr int TM = BWD_TABLE_M, LB = RO_LDB, RB = 32, NT = RO_MF_THREADS, NW = NT / 64, CPW = 16 / NW;
+    static_assert(TM == 128 && RB == 32 && (NW == 8 || NW == 16), "eight 16-wide tiles of slots, two of rows");
     __shared__ __align__(16) bf16_t sTh[TM * LB], sTl[TM * LB];  // rows R .. 127 and columns M .. 127 zero
     __shared__ __align__(16) bf16_t sZh[RB * LB], sZl[RB * LB], sPh[RB * LB], sPl[RB * LB];
     __shared__ float sL[RB][TM + 4];
@@ -1205,7 +1206,7 @@ __global__ __launch_bounds__(RO_MF_THREADS) void bw_fwd_readout_mf_kernel(const 
         split_store(sTh, sTl, r * LB + m, (r < R && m < M) ? bw_rnd<BF>(table[((size_t)h * R + r) * M + m]) : 0.f);
     }
     const auto row_of = [&](int rho) { return ((size_t)(rho / Tp) * H + h) * Tp + rho % Tp; };
-    const int it = wv & 1, ct0 = 2 * (wv >> 1);
+    const int it = wv & 1, ct0 = CPW * (wv >> 1);
     constexpr int NX = RB * (TM / 2) / NT;
     const int b_end = min(rows, (int)(blockIdx.x + 1) * per_wg * RB);
     const bw_rsrc_t rcs = bw_rsrc(cs, (size_t)rows * H * P), rsn = bw_rsrc(sn, (size_t)rows * H * P),
@@ -1240,14 +1241,14 @@ __global__ __launch_bounds__(RO_MF_THREADS) void bw_fwd_readout_mf_kernel(const 
         load_block(b0 + RB);  // the next block (past the end: dead loads)
         __syncthreads();
         {  // logits l[i][r] = sum_m z[i][m] table[r][m]
-            f32x4 acc[2];
+            f32x4 acc[CPW];
 #pragma unroll
-            for (int t = 0; t < 2; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int t = 0; t < CPW; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int k0 = 0; k0 < TM; k0 += 32) {
                 const bf16x8 ah = ro_row(sZh, 16 * it, k0), al = ro_row(sZl, 16 * it, k0);
 #pragma unroll
-                for (int t = 0; t < 2; t++) {
+                for (int t = 0; t < CPW; t++) {
                     const bf16x8 bh = ro_row(sTh, 16 * (ct0 + t), k0), bl = ro_row(sTl, 16 * (ct0 + t), k0);
                     acc[t] = mfma_bf16(al, bh, acc[t]);
                     acc[t] = mfma_bf16(ah, bl, acc[t]);
@@ -1256,7 +1257,7 @@ __global__ __launch_bounds__(RO_MF_THREADS) void bw_fwd_readout_mf_kernel(const 
             }
             const int lg = lane >> 4;
 #pragma unroll
-            for (int t = 0; t < 2; t++)
+            for (int t = 0; t < CPW; t++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) sL[16 * it + 4 * lg + q][16 * (ct0 + t) + lr] = acc[t][q];
         }
@@ -1273,14 +1274,14 @@ __global__ __launch_bounds__(RO_MF_THREADS) void bw_fwd_readout_mf_kernel(const 
         // u[i][m] = sum_r p[i][r] table[r][m] (p and the table zero at r >= R); the
         // weights' pair (2 pr, 2 pr + 1) sits in lanes (lr, lr ^ 1), swapped in by
         // quad_perm [1,0,3,2]
-        f32x4 acc[2];
+        f32x4 acc[CPW];
 #pragma unroll
-        for (int t = 0; t < 2; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < CPW; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int k0 = 0; k0 < TM; k0 += 32) {
             const bf16x8 ah = ro_row(sPh, 16 * it, k0), al = ro_row(sPl, 16 * it, k0);
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
+            for (int t = 0; t < CPW; t++) {
                 const bf16x8 bh = ro_col(sTh, k0, 16 * (ct0 + t)), bl = ro_col(sTl, k0, 16 * (ct0 + t));
                 acc[t] = mfma_bf16(al, bh, acc[t]);
                 acc[t] = mfma_bf16(ah, bl, acc[t]);
@@ -1290,7 +1291,7 @@ __global__ __launch_bounds__(RO_MF_THREADS) void bw_fwd_readout_mf_kernel(const 
         const bool odd = (lr & 1) != 0;
         const int lk = lane >> 4;
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
+        for (int t = 0; t < CPW; t++) {
             const int m = 16 * (ct0 + t) + lr, pr = m >> 1;
 #pragma unroll
             for (int q = 0; q < 4; q++) {
@@ -1316,14 +1317,15 @@ __global__ __launch_bounds__(RO_MF_THREADS) void bw_fwd_readout_mf_kernel(const 
 // on the fp32 matrix cores, v_mfma_f32_16x16x4_f32 (fp32 operands, fp32
 // accumulation): lane l holds A[l % 16][l / 16] and B[l / 16][l % 16] of a
 // 16 x 4 by 4 x 16 step and rows 4 (l / 16) .. + 3 of column l % 16 of the
-// 16 x 16 result. Grid (workgroups per head, H), 512 threads: a workgroup
-// takes per_wg blocks of 32 rows (bwd_ro_per_wg) and keeps its part of dtable
-// in the accumulators (wave w owns the 16 x 16 tiles (r, m) of columns
-// m in 16 w .. 16 w + 15). The LDS holds one workgroup per CU; its eight
-// waves put two on each SIMD, so that one wave's LDS reads overlap the
-// other's matrix-core steps.
+// 16 x 16 result. Grid (workgroups per head, H), RO_ADJ_THREADS threads: a
+// workgroup takes per_wg blocks of 32 rows (bwd_ro_per_wg) and keeps its part
+// of dtable in the accumulators (wave w owns the 16 x 16 tiles (r, m) of
+// columns m in 16 (w % 8) .. + 15 and rows r in 16 DRT (w / 8) .. + 16 DRT - 1,
+// DRT = 64 / waves). The LDS holds one workgroup per CU; its waves put
+// several on each SIMD, so that one wave's LDS reads overlap another's
+// matrix-core steps.
 constexpr int RO_BLK = BWD_RO_BLOCK;
-constexpr int RO_ADJ_THREADS = 512;
+constexpr int RO_ADJ_THREADS = 1024;
 struct ReadoutGradArgs {
     const float *raw, *cs, *sn, *table, *dwts;  // head-major rows; table [H, M-1, M]
     float *draw, *dlam, *dtab;                  // dtab: [H, workgroups, (M-1) M]
@@ -1333,7 +1335,8 @@ struct ReadoutGradArgs {
 
 __global__ __launch_bounds__(RO_ADJ_THREADS) void bw_readout_kernel(ReadoutGradArgs a) {
     constexpr int TM = BWD_TABLE_M, LD = RO_LD, NT = RO_ADJ_THREADS, NW = NT / 64;
-    static_assert(NW == 8, "two row tiles x four pairs of slot tiles; one 16-column dtable tile per wave");
+    constexpr int CPW = 16 / NW, DRT = 64 / NW;  // slot tiles per wave in the block products; dtable row tiles
+    static_assert(NW == 8 || NW == 16, "two row tiles x eight slot tiles over the waves; eight dtable column tiles");
     static_assert(RO_BLK == 32 && TM == 128, "two 16-row tiles of rows, eight 16-wide tiles of slots");
     __shared__ float sTab[TM * LD];  // rows R .. 127 and columns M .. 127 zero
     __shared__ float sZ[RO_BLK][LD], sDU[RO_BLK][LD], sP[RO_BLK][LD], sDL[RO_BLK][LD];
@@ -1347,11 +1350,11 @@ __global__ __launch_bounds__(RO_ADJ_THREADS) void bw_readout_kernel(ReadoutGradA
         sTab[e] = (r < R && m < M) ? a.table[((size_t)h * R + r) * M + m] : 0.f;
     }
     // GEMMs over the block: wave wv takes row tile it = wv & 1 and the column
-    // tiles 2 (wv >> 1), + 1 of the logits (r) and of dz, u (m)
-    const int it = wv & 1, ct0 = 2 * (wv >> 1);
-    f32x4v dacc[8];  // dtable tiles (r tile, m tile wv)
+    // tiles CPW (wv >> 1) .. + CPW - 1 of the logits (r) and of dz, u (m)
+    const int it = wv & 1, ct0 = CPW * (wv >> 1), dm = wv & 7, dr0 = DRT * (wv >> 3);
+    f32x4v dacc[DRT];  // dtable tiles (r tile dr0 + rt, m tile dm)
 #pragma unroll
-    for (int rt = 0; rt < 8; rt++) dacc[rt] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    for (int rt = 0; rt < DRT; rt++) dacc[rt] = f32x4v{0.f, 0.f, 0.f, 0.f};
     const int rows = a.B * a.Tp;
     // A block's inputs, element x of this thread = (row i, pair pr) = e / 64,
     // e % 64, e = tid + NT x: loaded one block ahead through buffer
@@ -1397,20 +1400,20 @@ __global__ __launch_bounds__(RO_ADJ_THREADS) void bw_readout_kernel(ReadoutGradA
         __syncthreads();
         // logits l[i][r] = sum_m z[i][m] table[r][m] and dp[i][r] = sum_m du[i][m] table[r][m]
         {
-            f32x4v accl[2], accd[2];
+            f32x4v accl[CPW], accd[CPW];
 #pragma unroll
-            for (int t = 0; t < 2; t++) accl[t] = accd[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+            for (int t = 0; t < CPW; t++) accl[t] = accd[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
             for (int k0 = 0; k0 < TM; k0 += 4) {
                 const float az = sZ[16 * it + lr][k0 + lk], ad = sDU[16 * it + lr][k0 + lk];
 #pragma unroll
-                for (int t = 0; t < 2; t++) {
+                for (int t = 0; t < CPW; t++) {
                     const float bt = sTab[(16 * (ct0 + t) + lr) * LD + k0 + lk];
                     accl[t] = mfma4(az, bt, accl[t]);
                     accd[t] = mfma4(ad, bt, accd[t]);
                 }
             }
 #pragma unroll
-            for (int t = 0; t < 2; t++)
+            for (int t = 0; t < CPW; t++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     sP[16 * it + 4 * lk + q][16 * (ct0 + t) + lr] = accl[t][q];
@@ -1436,13 +1439,13 @@ __global__ __launch_bounds__(RO_ADJ_THREADS) void bw_readout_kernel(ReadoutGradA
         // dz[i][m] = sum_r dl[i][r] table[r][m] and u[i][m] = sum_r p[i][r] table[r][m]
         // (p and dl are zero at r >= R, as is the table); then draw and the clock's share
         {
-            f32x4v accz[2], accu[2];
+            f32x4v accz[CPW], accu[CPW];
 #pragma unroll
-            for (int t = 0; t < 2; t++) accz[t] = accu[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+            for (int t = 0; t < CPW; t++) accz[t] = accu[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
             for (int k0 = 0; k0 < TM; k0 += 4) {
                 const float al = sDL[16 * it + lr][k0 + lk], ap = sP[16 * it + lr][k0 + lk];
 #pragma unroll
-                for (int t = 0; t < 2; t++) {
+                for (int t = 0; t < CPW; t++) {
                     const float bt = sTab[(k0 + lk) * LD + 16 * (ct0 + t) + lr];
                     accz[t] = mfma4(al, bt, accz[t]);
                     accu[t] = mfma4(ap, bt, accu[t]);
@@ -1457,7 +1460,7 @@ __global__ __launch_bounds__(RO_ADJ_THREADS) void bw_readout_kernel(ReadoutGradA
             const bool odd = (lr & 1) != 0;
             float dl[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
+            for (int t = 0; t < CPW; t++) {
                 const int m = 16 * (ct0 + t) + lr, pr = m >> 1;
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
@@ -1477,8 +1480,8 @@ __global__ __launch_bounds__(RO_ADJ_THREADS) void bw_readout_kernel(ReadoutGradA
                     }
                 }
             }
-            // the row's share over this wave's 16 lanes (its two column tiles summed above,
-            // in tile order), then the four waves of the row tile in wave order
+            // the row's share over this wave's 16 lanes (its column tiles summed above,
+            // in tile order), then the waves of the row tile in wave order
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const float v = wave_sum<16>(dl[q]);
@@ -1488,27 +1491,29 @@ __global__ __launch_bounds__(RO_ADJ_THREADS) void bw_readout_kernel(ReadoutGradA
         __syncthreads();
         if (tid < RO_BLK && b0 + tid < rows) {  // the clock's share per row
             const int rho = b0 + tid;
-            a.dlam[((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp] =
-                (sLam[tid][0] + sLam[tid][1]) + (sLam[tid][2] + sLam[tid][3]);
+            float v = sLam[tid][0];
+#pragma unroll
+            for (int j = 1; j < NW / 2; j++) v += sLam[tid][j];
+            a.dlam[((size_t)(rho / a.Tp) * a.H + h) * a.Tp + rho % a.Tp] = v;
         }
         // dtable[r][m] += sum_i p[i][r] du[i][m] + dl[i][r] z[i][m] over the block's rows
         for (int k0 = 0; k0 < RO_BLK; k0 += 4) {
-            const float bu = sDU[k0 + lk][16 * wv + lr], bz = sZ[k0 + lk][16 * wv + lr];
+            const float bu = sDU[k0 + lk][16 * dm + lr], bz = sZ[k0 + lk][16 * dm + lr];
 #pragma unroll
-            for (int rt = 0; rt < 8; rt++) {
-                const float ap = sP[k0 + lk][16 * rt + lr], al = sDL[k0 + lk][16 * rt + lr];
+            for (int rt = 0; rt < DRT; rt++) {
+                const float ap = sP[k0 + lk][16 * (dr0 + rt) + lr], al = sDL[k0 + lk][16 * (dr0 + rt) + lr];
                 dacc[rt] = mfma4(ap, bu, dacc[rt]);
                 dacc[rt] = mfma4(al, bz, dacc[rt]);
             }
         }
     }
-    // lane holds dtable rows 16 rt + 4 lk + q of column 16 wv + lr
+    // lane holds dtable rows 16 (dr0 + rt) + 4 lk + q of column 16 dm + lr
     float* dst = a.dtab + ((size_t)h * gridDim.x + blk) * RM;
 #pragma unroll
-    for (int rt = 0; rt < 8; rt++)
+    for (int rt = 0; rt < DRT; rt++)
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const int r = 16 * rt + 4 * lk + q, m = 16 * wv + lr;
+            const int r = 16 * (dr0 + rt) + 4 * lk + q, m = 16 * dm + lr;
             if (r < R && m < M) dst[r * M + m] = dacc[rt][q];
         }
 }
