@@ -1021,8 +1021,9 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
 // (mfma4 below). BF
 // rounds z, the table, p and the weights to bf16 (the general forward's casts
 // to a bf16 input dtype, ops/utils.py:779-882); the backward's recompute is
-// unrounded. Grid (ceil(B Tp / (32 per_wg)), H), 256 threads: a workgroup
-// stages the table once and takes per_wg blocks.
+// unrounded. Grid (ceil(B Tp / (32 per_wg)), H), RO_FWD_THREADS threads: a
+// workgroup stages the table once and takes per_wg blocks; the LDS holds one
+// workgroup per CU, and its waves put several on each SIMD.
 template <bool BF>
 __device__ __forceinline__ float bw_rnd(float x) {
     if constexpr (BF)
@@ -1032,6 +1033,7 @@ __device__ __forceinline__ float bw_rnd(float x) {
 }
 
 constexpr int RO_LD = BWD_TABLE_M + 4;  // staged table and row rows, 16-byte aligned
+constexpr int RO_FWD_THREADS = 1024;
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
@@ -1043,29 +1045,29 @@ __device__ __forceinline__ f32x4v mfma4(float a, float b, f32x4v c) {
 }
 
 template <bool BF>
-__global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, const float* cs, const float* sn,
+__global__ __launch_bounds__(RO_FWD_THREADS) void bw_fwd_readout_kernel(const float* raw, const float* cs, const float* sn,
                                                              const float* table, int B, int Tp, int H, int M,
                                                              int per_wg, float* wts) {
-    constexpr int TM = BWD_TABLE_M, LD = RO_LD, RB = 32;
-    static_assert(TM == 128, "eight 16-wide tiles of slots");
+    constexpr int TM = BWD_TABLE_M, LD = RO_LD, RB = 32, NT = RO_FWD_THREADS, NW = NT / 64, CPW = 16 / NW;
+    static_assert(TM == 128 && (NW == 8 || NW == 16), "eight 16-wide tiles of slots, two of rows");
     __shared__ float sTab[TM * LD];  // rows R .. 127 and columns M .. 127 zero
     __shared__ float sZ[RB][LD], sP[RB][LD];
     __shared__ float sCs[RB][TM / 2], sSn[RB][TM / 2];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, h = blockIdx.y;
     const int lr = lane & 15, lk = lane >> 4;
     const int R = M - 1, P = M / 2, rows = B * Tp;
-    for (int e = tid; e < TM * LD; e += 256) {
+    for (int e = tid; e < TM * LD; e += NT) {
         const int r = e / LD, m = e % LD;
         sTab[e] = (r < R && m < M) ? bw_rnd<BF>(table[((size_t)h * R + r) * M + m]) : 0.f;
     }
     const auto row_of = [&](int rho) { return ((size_t)(rho / Tp) * H + h) * Tp + rho % Tp; };
-    // wave wv: row tile it = wv & 1, column tiles 4 (wv >> 1) .. + 3 (of r, then of m)
-    const int it = wv & 1, ct0 = 4 * (wv >> 1);
+    // wave wv: row tile it = wv & 1, column tiles CPW (wv >> 1) .. + CPW - 1 (of r, then of m)
+    const int it = wv & 1, ct0 = CPW * (wv >> 1);
     // A block's inputs, element x of this thread = (row i, pair pr) = e / 64,
-    // e % 64, e = tid + 256 x: loaded one block ahead through buffer
+    // e % 64, e = tid + NT x: loaded one block ahead through buffer
     // resources (rows < 2^21, M <= 128: offsets below 2^30), predicated
     // through the offset, so that no block waits for its own loads.
-    constexpr int NX = RB * (TM / 2) / 256;
+    constexpr int NX = RB * (TM / 2) / NT;
     const int b_end = min(rows, (int)(blockIdx.x + 1) * per_wg * RB);
     const bw_rsrc_t rcs = bw_rsrc(cs, (size_t)rows * H * P), rsn = bw_rsrc(sn, (size_t)rows * H * P),
                     rraw = bw_rsrc(raw, (size_t)rows * H * M);  // every head's rows
@@ -1073,7 +1075,7 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
     const auto load_block = [&](int b0) {
 #pragma unroll
         for (int x = 0; x < NX; x++) {
-            const int e = tid + 256 * x, i = e / (TM / 2), pr = e % (TM / 2), rho = b0 + i;
+            const int e = tid + NT * x, i = e / (TM / 2), pr = e % (TM / 2), rho = b0 + i;
             const bool live = rho < b_end && pr < P;
             const uint32_t row = live ? (uint32_t)row_of(rho) : 0u;
             nc[x] = bw_load(rcs, (row * (uint32_t)P + (uint32_t)pr) * 4u, live);
@@ -1088,7 +1090,7 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
         __syncthreads();  // the table is staged; the previous block's tiles are done with
 #pragma unroll
         for (int x = 0; x < NX; x++) {
-            const int e = tid + 256 * x, i = e / (TM / 2), pr = e % (TM / 2);
+            const int e = tid + NT * x, i = e / (TM / 2), pr = e % (TM / 2);
             const bool live = b0 + i < b_end && pr < P;
             const float c = live ? nc[x] : 1.f, s = ns[x];
             sCs[i][pr] = c;
@@ -1099,21 +1101,21 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
         load_block(b0 + RB);  // the next block (past the end: dead loads)
         __syncthreads();
         {  // logits l[i][r] = sum_m z[i][m] table[r][m]
-            f32x4v acc[4];
+            f32x4v acc[CPW];
 #pragma unroll
-            for (int t = 0; t < 4; t++) acc[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+            for (int t = 0; t < CPW; t++) acc[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
             for (int k0 = 0; k0 < TM; k0 += 4) {
                 const float az = sZ[16 * it + lr][k0 + lk];
 #pragma unroll
-                for (int t = 0; t < 4; t++) acc[t] = mfma4(az, sTab[(16 * (ct0 + t) + lr) * LD + k0 + lk], acc[t]);
+                for (int t = 0; t < CPW; t++) acc[t] = mfma4(az, sTab[(16 * (ct0 + t) + lr) * LD + k0 + lk], acc[t]);
             }
 #pragma unroll
-            for (int t = 0; t < 4; t++)
+            for (int t = 0; t < CPW; t++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) sP[16 * it + 4 * lk + q][16 * (ct0 + t) + lr] = acc[t][q];
         }
         __syncthreads();
-        for (int i = wv; i < RB; i += 4) {
+        for (int i = wv; i < RB; i += NW) {
             const float l0 = lane < R ? sP[i][lane] : -INFINITY, l1 = lane + 64 < R ? sP[i][lane + 64] : -INFINITY;
             const float mx = bw_wave_max(fmaxf(l0, l1));
             const float e0 = lane < R ? expf(l0 - mx) : 0.f, e1 = lane + 64 < R ? expf(l1 - mx) : 0.f;
@@ -1125,17 +1127,17 @@ __global__ __launch_bounds__(256) void bw_fwd_readout_kernel(const float* raw, c
         // u[i][m] = sum_r p[i][r] table[r][m] (p and the table zero at r >= R); the
         // weights' pair (2 pr, 2 pr + 1) sits in lanes (lr, lr ^ 1), swapped in by
         // quad_perm [1,0,3,2]
-        f32x4v acc[4];
+        f32x4v acc[CPW];
 #pragma unroll
-        for (int t = 0; t < 4; t++) acc[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < CPW; t++) acc[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
         for (int k0 = 0; k0 < TM; k0 += 4) {
             const float ap = sP[16 * it + lr][k0 + lk];
 #pragma unroll
-            for (int t = 0; t < 4; t++) acc[t] = mfma4(ap, sTab[(k0 + lk) * LD + 16 * (ct0 + t) + lr], acc[t]);
+            for (int t = 0; t < CPW; t++) acc[t] = mfma4(ap, sTab[(k0 + lk) * LD + 16 * (ct0 + t) + lr], acc[t]);
         }
         const bool odd = (lr & 1) != 0;
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
+        for (int t = 0; t < CPW; t++) {
             const int m = 16 * (ct0 + t) + lr, pr = m >> 1;
 #pragma unroll
             for (int q = 0; q < 4; q++) {
@@ -2114,10 +2116,10 @@ int launch_chunk_readout(const float* raw, const float* cs, const float* sn, con
         hipLaunchKernelGGL(bw_fwd_readout_mf_kernel<false>, grid, dim3(RO_MF_THREADS), 0, stream, raw, cs, sn, table, B, Tp, H, M, per,
                            wts);
     else if (bf16)
-        hipLaunchKernelGGL(bw_fwd_readout_kernel<true>, grid, blk, 0, stream, raw, cs, sn, table, B, Tp, H, M, per,
+        hipLaunchKernelGGL(bw_fwd_readout_kernel<true>, grid, dim3(RO_FWD_THREADS), 0, stream, raw, cs, sn, table, B, Tp, H, M, per,
                            wts);
     else
-        hipLaunchKernelGGL(bw_fwd_readout_kernel<false>, grid, blk, 0, stream, raw, cs, sn, table, B, Tp, H, M, per,
+        hipLaunchKernelGGL(bw_fwd_readout_kernel<false>, grid, dim3(RO_FWD_THREADS), 0, stream, raw, cs, sn, table, B, Tp, H, M, per,
                            wts);
     return 0;
 }
