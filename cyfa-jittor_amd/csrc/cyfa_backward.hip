@@ -1733,7 +1733,8 @@ __global__ __launch_bounds__(256) void bw_wide_dtable_kernel(WideArgs a) {
 // theta_p, a[2p+1] = -s_p sin theta_p, dw = the pass-1 value cotangent + the
 // pass-2 key cotangent): dbeta = dw . a, and dlam = beta dw . da/dlam + the
 // readout's share. Grid (N, B*H), 256 threads: wave w forms tokens w, w + 4,
-// .. with its lanes across the row (coalesced), then wave 0 scans.
+// .. (two at a time) with its lanes across the row (coalesced 16- and 8-byte
+// loads), then wave 0 scans.
 struct TokenGradArgs {
     const float *qh, *kh, *dqh, *dkh;    // pass 1 rows [.., K]
     const float *wts, *w, *dwts, *dw2;   // pass 2 query and key rows [.., M]
@@ -1746,34 +1747,82 @@ struct TokenGradArgs {
     int B, T, Tp, H, K, M, N, nt1, nt2;
 };
 
+template <bool V4>
 __global__ __launch_bounds__(256) void bw_token_kernel(TokenGradArgs a) {
     __shared__ float sdG[BC], sdB[BC], sdL[BC];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n = blockIdx.x, bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
     const int K = a.K, M = a.M, P = M / 2, R = M - 1;
-    for (int i = wv; i < BC; i += 4) {
-        const size_t row = (size_t)bh * a.Tp + n * BC + i;
-        float dG = 0.f;
-        for (int j = lane; j < K; j += 64)
-            dG += a.qh[row * K + j] * a.dqh[row * K + j] - a.kh[row * K + j] * a.dkh[row * K + j];
-        for (int j = lane; j < M; j += 64)
-            dG += a.wts[row * M + j] * a.dwts[row * M + j] - a.w[row * M + j] * a.dw2[row * M + j];
-        float db = 0.f, dl = 0.f;
-        for (int p = lane; p < P; p += 64) {
-            const float c = a.cs[row * P + p], s = a.sn[row * P + p];
-            const float we = a.dw1[row * M + 2 * p] + a.dw2[row * M + 2 * p];
-            const float wo = a.dw1[row * M + 2 * p + 1] + a.dw2[row * M + 2 * p + 1];
-            const float sp = (float)sqrt((p == 0 ? 1.0 : 2.0) / R);
-            db = fmaf(sp, we * c - wo * s, db);
-            dl = fmaf(sp * (float)(kTwoPiBw * p / R), -we * s - wo * c, dl);
+    // the write vector's per-pair factors: sqrt(1/R) for p = 0, sqrt(2/R) after;
+    // the phase derivative's 2 pi p / R for the lane's pairs p = lane, lane + 64
+    const float sp0 = (float)sqrt(1.0 / R), sp1 = (float)sqrt(2.0 / R);
+    const float kp[2] = {(float)(kTwoPiBw * lane / R), (float)(kTwoPiBw * (lane + 64) / R)};
+    // Wave wv forms the rows wv + 8 u and wv + 8 u + 4 together, so that both
+    // rows' loads are in flight at once. The lane reads four consecutive
+    // elements of the K-rows with V4 (K % 4 == 0), one otherwise, and the
+    // pair (2 p, 2 p + 1) of the M-rows.
+    for (int i0 = wv; i0 < BC; i0 += 8) {
+        size_t row[2];
+        float dG[2], db[2], dl[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            row[u] = (size_t)bh * a.Tp + n * BC + i0 + 4 * u;
+            dG[u] = db[u] = dl[u] = 0.f;
         }
-        dG = bw_wave_sum(dG);
-        db = bw_wave_sum(db);
-        dl = bw_wave_sum(dl);
-        if (lane == 0) {
-            sdG[i] = dG;
-            sdB[i] = db;
-            sdL[i] = dl;
+        if constexpr (!V4) {
+            for (int j = lane; j < K; j += 64)
+#pragma unroll
+                for (int u = 0; u < 2; u++)
+                    dG[u] += a.qh[row[u] * K + j] * a.dqh[row[u] * K + j] - a.kh[row[u] * K + j] * a.dkh[row[u] * K + j];
+        }
+        for (int j = 4 * lane; V4 && j < K; j += 256) {
+            float4 q[2], dq[2], k[2], dk[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                q[u] = *reinterpret_cast<const float4*>(a.qh + row[u] * K + j);
+                dq[u] = *reinterpret_cast<const float4*>(a.dqh + row[u] * K + j);
+                k[u] = *reinterpret_cast<const float4*>(a.kh + row[u] * K + j);
+                dk[u] = *reinterpret_cast<const float4*>(a.dkh + row[u] * K + j);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+                dG[u] += (q[u].x * dq[u].x + q[u].y * dq[u].y + q[u].z * dq[u].z + q[u].w * dq[u].w) -
+                         (k[u].x * dk[u].x + k[u].y * dk[u].y + k[u].z * dk[u].z + k[u].w * dk[u].w);
+        }
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int p = lane + 64 * c;
+            if (p >= P) break;
+            float2 wt[2], dwt[2], w[2], d2[2], d1[2];
+            float cs[2], sn[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const size_t e = row[u] * M + 2 * p;
+                wt[u] = *reinterpret_cast<const float2*>(a.wts + e);
+                dwt[u] = *reinterpret_cast<const float2*>(a.dwts + e);
+                w[u] = *reinterpret_cast<const float2*>(a.w + e);
+                d2[u] = *reinterpret_cast<const float2*>(a.dw2 + e);
+                d1[u] = *reinterpret_cast<const float2*>(a.dw1 + e);
+                cs[u] = a.cs[row[u] * P + p];
+                sn[u] = a.sn[row[u] * P + p];
+            }
+            const float sp = p == 0 ? sp0 : sp1;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                dG[u] += (wt[u].x * dwt[u].x + wt[u].y * dwt[u].y) - (w[u].x * d2[u].x + w[u].y * d2[u].y);
+                const float we = d1[u].x + d2[u].x, wo = d1[u].y + d2[u].y;
+                db[u] = fmaf(sp, we * cs[u] - wo * sn[u], db[u]);
+                dl[u] = fmaf(sp * kp[c], -we * sn[u] - wo * cs[u], dl[u]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const float g = bw_wave_sum(dG[u]), bb = bw_wave_sum(db[u]), ll = bw_wave_sum(dl[u]);
+            if (lane == 0) {
+                sdG[i0 + 4 * u] = g;
+                sdB[i0 + 4 * u] = bb;
+                sdL[i0 + 4 * u] = ll;
+            }
         }
     }
     __syncthreads();
@@ -2324,7 +2373,10 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     tg.N = N;
     tg.nt1 = ws.nt1;
     tg.nt2 = ws.nt2;
-    hipLaunchKernelGGL(bw_token_kernel, dim3(N, B * H), blk, 0, stream, tg);
+    if (K % 4 == 0)
+        hipLaunchKernelGGL(bw_token_kernel<true>, dim3(N, B * H), blk, 0, stream, tg);
+    else
+        hipLaunchKernelGGL(bw_token_kernel<false>, dim3(N, B * H), blk, 0, stream, tg);
     hipLaunchKernelGGL(bw_clock_kernel, dim3(B * H), dim3(64), 0, stream, ws.dlam, p.d_clock, B, T, Tp, H, p.ddelta,
                        p.dclock0);
     // the q/k norms, their weights, v's layout
