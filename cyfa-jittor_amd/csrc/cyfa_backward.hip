@@ -162,6 +162,9 @@ constexpr uint32_t BW_DEAD = 0x80000000u;  // past every region below (each < 2^
 __device__ __forceinline__ bw_rsrc_t bw_rsrc(const float* base, size_t elems) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)(uint32_t)(elems * 4), 0x00020000);
 }
+__device__ __forceinline__ bw_rsrc_t bw_rsrc(const bf16_t* base, size_t elems) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base), (short)0, (int)(uint32_t)(elems * 2), 0x00020000);
+}
 
 // A buffer store that the range check drops when dead is set.
 __device__ __forceinline__ void bw_store(bw_rsrc_t r, uint32_t off, bool live, float v) {
@@ -169,6 +172,19 @@ __device__ __forceinline__ void bw_store(bw_rsrc_t r, uint32_t off, bool live, f
 }
 __device__ __forceinline__ float bw_load(bw_rsrc_t r, uint32_t off, bool live) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off | (live ? 0u : BW_DEAD), 0, 0));
+}
+// The same for one bf16 element (off in bytes): stored rounded, loaded widened.
+__device__ __forceinline__ void bw_store_h(bw_rsrc_t r, uint32_t off, bool live, float v) {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (bf16_t)v), r, off | (live ? 0u : BW_DEAD), 0,
+                                          0);
+}
+__device__ __forceinline__ float bw_load_h(bw_rsrc_t r, uint32_t off, bool live) {
+    const unsigned short u = __builtin_amdgcn_raw_buffer_load_b16(r, off | (live ? 0u : BW_DEAD), 0, 0);
+    return __builtin_bit_cast(float, (uint32_t)u << 16);
+}
+__device__ __forceinline__ f32x4 bf16x4_bits_to_f32x4(uint32_t w0, uint32_t w1) {
+    return f32x4{__builtin_bit_cast(float, w0 << 16), __builtin_bit_cast(float, w0 & 0xffff0000u),
+                 __builtin_bit_cast(float, w1 << 16), __builtin_bit_cast(float, w1 & 0xffff0000u)};
 }
 
 // The chunk-to-chunk scan of one pass over a [Kq, Vd] matrix X, one
@@ -197,6 +213,7 @@ struct StateScanArgs {
     float* x_out;        // nullable [B*H, Kq, Vd]
     int B, T, Tp, H, Kq, Vd, N;
     float scale;
+    int sbf;             // matrix-core form: xs and S hold bf16 (bf16_t) states
 };
 
 template <bool BWD>
@@ -361,8 +378,9 @@ __device__ __forceinline__ void split_bf16x8(const float* v, bf16x8& hi, bf16x8&
     }
 }
 
-template <bool BWD, int T2>
+template <bool BWD, int T2, bool SB>
 __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) {
+    using SE = std::conditional_t<SB, bf16_t, float>;  // the stored states' element
     static_assert(SCAN_ROWS == 32 && BW_TILE == 32 && (T2 == 1 || T2 == 2), "32 x 32 bnd tiles");
     constexpr int TS = 32 * T2;     // tile side
     constexpr int TPT = BC / (256 / TS);  // tokens per staging thread
@@ -382,7 +400,8 @@ __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) 
     const int ty = T2 == 1 ? (int)blockIdx.y : 2 * (int)blockIdx.y + (wv >> 1);
     const int tx = T2 == 1 ? (int)blockIdx.x : 2 * (int)blockIdx.x + (wv & 1);
     const size_t bh = bhi, ssz = (size_t)Kq * Vd;
-    float* xs = p.xs + bh * (N + 1) * ssz;
+    SE* xs = reinterpret_cast<SE*>(p.xs) + bh * (N + 1) * ssz;
+    const SE* Sx = reinterpret_cast<const SE*>(p.S);
     const float* A = p.a + bh * p.Tp * Kq;
     const float* Bm = p.b + bh * p.Tp * Vd;
     const int wr = 16 * T2 * (wv >> 1), wc = 16 * T2 * (wv & 1);  // the wave's quarter
@@ -403,13 +422,15 @@ __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) 
             }
     float sv[T2][T2][4] = {};
     const auto fetch_state = [&](int n) {
-        const bw_rsrc_t rs = bw_rsrc(p.S + (bh * (N + 1) + n) * ssz, ssz);
+        const bw_rsrc_t rs = bw_rsrc(Sx + (bh * (N + 1) + n) * ssz, ssz);
 #pragma unroll
         for (int ib = 0; ib < T2; ib++)
 #pragma unroll
             for (int jb = 0; jb < T2; jb++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) sv[ib][jb][i] = bw_load(rs, off[ib][jb][i], ok[ib][jb][i]);
+                for (int i = 0; i < 4; i++)
+                    sv[ib][jb][i] = SB ? bw_load_h(rs, off[ib][jb][i] / 2u, ok[ib][jb][i])
+                                       : bw_load(rs, off[ib][jb][i], ok[ib][jb][i]);
     };
     const auto keep = [&](int n) {  // xs[n] = X; returns the lane's part of <X, S[n]> (backward)
         const bw_rsrc_t rs = bw_rsrc(xs + (size_t)n * ssz, ssz);
@@ -420,7 +441,10 @@ __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) 
             for (int jb = 0; jb < T2; jb++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    bw_store(rs, off[ib][jb][i], ok[ib][jb][i], x[ib][jb][i]);
+                    if constexpr (SB)
+                        bw_store_h(rs, off[ib][jb][i] / 2u, ok[ib][jb][i], x[ib][jb][i]);
+                    else
+                        bw_store(rs, off[ib][jb][i], ok[ib][jb][i], x[ib][jb][i]);
                     if constexpr (BWD) dot = fmaf(x[ib][jb][i], sv[ib][jb][i], dot);
                 }
         return dot;
@@ -539,9 +563,11 @@ void launch_state_scan(const StateScanArgs& a, bool mfma, hipStream_t stream) {
     if (!mfma)
         hipLaunchKernelGGL(bw_state_scan_kernel<BWD>, g32, dim3(256), 0, stream, a);
     else if ((long long)g64.x * g64.y * g64.z >= device_cu_count())
-        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, 2>), g64, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((a.sbf ? bw_state_scan_mf_kernel<BWD, 2, true> : bw_state_scan_mf_kernel<BWD, 2, false>), g64,
+                           dim3(256), 0, stream, a);
     else
-        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, 1>), g32, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((a.sbf ? bw_state_scan_mf_kernel<BWD, 1, true> : bw_state_scan_mf_kernel<BWD, 1, false>), g32,
+                           dim3(256), 0, stream, a);
 }
 
 // Tile GEMMs of the chunk kernels: a 64 x 64 output tile (rows = the chunk's
@@ -641,6 +667,59 @@ struct RowsJ4 : RowsJ {
     }
 };
 
+// RowsK, RowsK4, RowsJ and RowsJ4 over bf16 elements (the stored states and
+// state cotangents of bf16 calls): two-byte loads, and load4's four
+// consecutive elements in one 8-byte load (16-byte aligned base, ld and the
+// extent multiples of 4). The values widen to fp32 exactly.
+struct RowsKh : RowsK {
+    __device__ RowsKh(const bf16_t* base, int ld_, int nm_, int nk_) : RowsK(nullptr, ld_, nm_, nk_) {
+        r = bw_rsrc(base, nm_ > 0 ? (size_t)(nm_ - 1) * ld_ + nk_ : 0);
+    }
+    __device__ float load(int m, int kk) const {
+        return bw_load_h(r, ((uint32_t)m * ld + (uint32_t)kk) * 2u, m < nm && kk < nk);
+    }
+};
+struct RowsK4h : RowsK4 {
+    __device__ RowsK4h(const bf16_t* base, int ld_, int nm_, int nk_) : RowsK4(nullptr, ld_, nm_, nk_) {
+        r = bw_rsrc(base, nm_ > 0 ? (size_t)(nm_ - 1) * ld_ + nk_ : 0);
+    }
+    __device__ float load(int m, int kk) const {
+        return bw_load_h(r, ((uint32_t)m * ld + (uint32_t)kk) * 2u, m < nm && kk < nk);
+    }
+    __device__ f32x4 load4(int m, int kk0) const {
+        const uint32_t dead = (m < nm && kk0 < nk) ? 0u : BW_DEAD;
+        const auto w = __builtin_amdgcn_raw_buffer_load_b64(r, ((uint32_t)m * ld + (uint32_t)kk0) * 2u | dead, 0, 0);
+        return bf16x4_bits_to_f32x4(w[0], w[1]);
+    }
+};
+struct RowsJh : RowsJ {
+    __device__ RowsJh(const bf16_t* base, int ld_, int nk_, int nj_) : RowsJ(nullptr, ld_, nk_, nj_) {
+        r = bw_rsrc(base, nk_ > 0 ? (size_t)(nk_ - 1) * ld_ + nj_ : 0);
+    }
+    __device__ float load(int kk, int j) const {
+        return bw_load_h(r, ((uint32_t)kk * ld + (uint32_t)j) * 2u, kk < nk && j < nj);
+    }
+};
+struct RowsJ4h : RowsJ4 {
+    __device__ RowsJ4h(const bf16_t* base, int ld_, int nk_, int nj_) : RowsJ4(nullptr, ld_, nk_, nj_) {
+        r = bw_rsrc(base, nk_ > 0 ? (size_t)(nk_ - 1) * ld_ + nj_ : 0);
+    }
+    __device__ float load(int kk, int j) const {
+        return bw_load_h(r, ((uint32_t)kk * ld + (uint32_t)j) * 2u, kk < nk && j < nj);
+    }
+    __device__ f32x4 load4(int kk, int j0) const {
+        const uint32_t dead = (kk < nk && j0 < nj) ? 0u : BW_DEAD;
+        const auto w = __builtin_amdgcn_raw_buffer_load_b64(r, ((uint32_t)kk * ld + (uint32_t)j0) * 2u | dead, 0, 0);
+        return bf16x4_bits_to_f32x4(w[0], w[1]);
+    }
+};
+
+// The state operands' row types: fp32, or bf16 with SB.
+template <bool SB, bool V4>
+using StateRowsK = std::conditional_t<SB, std::conditional_t<V4, RowsK4h, RowsKh>, std::conditional_t<V4, RowsK4, RowsK>>;
+template <bool SB, bool V4>
+using StateRowsJ = std::conditional_t<SB, std::conditional_t<V4, RowsJ4h, RowsJh>, std::conditional_t<V4, RowsJ4, RowsJ>>;
+
 // Element (i, kk) of A and (kk, j) of B, for a global operand or a callable
 // (LDS operands: read only at kk < Kd, contractions of BC tokens).
 template <class FA>
@@ -678,8 +757,8 @@ __device__ __forceinline__ void tile_gemm_mf(FA fa, FB fb, int Kd, unsigned char
         const int r = tid >> 2, kg = tid & 3;  // staging: row r, k-group kg (8 k)
         // RowsK4 operands: lane (r, kg) holds kk = k0 + 4 kg .. + 3 and
         // k0 + 16 + 4 kg .. + 3; the others kk = k0 + 8 kg .. + 7
-        constexpr bool VA = std::is_same_v<FA, RowsK4>, VB = std::is_same_v<FB, RowsK4>;
-        constexpr bool JB = std::is_same_v<FB, RowsJ4>;  // B: lane (jq, kp) as in RowsJ4
+        constexpr bool VA = std::is_base_of_v<RowsK4, FA>, VB = std::is_base_of_v<RowsK4, FB>;
+        constexpr bool JB = std::is_base_of_v<RowsJ4, FB>;  // B: lane (jq, kp) as in RowsJ4
         const int jq = tid & 15, kp = tid >> 4;
         float ra[8], rb[NT][8];
         const auto fetch = [&](int k0) {
@@ -879,18 +958,21 @@ __device__ __forceinline__ void chunk_scores(const float* X, const float* Y, int
 struct OutArgs {
     const float *q, *k, *v;  // head-major [B*H, Tp, Kq | Vd]
     const float* g;
-    const float* S;          // [B*H, N+1, Kq, Vd]
+    const float* S;          // [B*H, N+1, Kq, Vd]: fp32, or bf16_t with sbf
     float* out;              // head-major [B*H, Tp, Vd], used when out_bthd is null
     void* out_bthd;          // nullable [B, T, H, Vd], bf16 when bf16 else fp32
     int bf16;                // round to bf16
     int B, T, Tp, H, Kq, Vd, N;
     float scale;
+    int sbf;                 // matrix-core form: S holds bf16 states
 };
 
-template <bool MF, bool V4>
+template <bool MF, bool V4, bool SB>
 __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
     using RK = std::conditional_t<V4, RowsK4, RowsK>;  // 16-byte row loads when aligned
     using RJ = std::conditional_t<V4, RowsJ4, RowsJ>;
+    using SJ = StateRowsJ<SB, V4>;
+    using SE = std::conditional_t<SB, bf16_t, float>;
     __shared__ float sA[BC][BC + 1];
     // (output tiles of 64 columns: two at a time read q once instead of twice
     // but measured slower here, 80 -> 84 us at configuration 3)
@@ -903,7 +985,7 @@ __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
     const float* q = a.q + (bh * a.Tp + t0) * Kq;
     const float* k = a.k + (bh * a.Tp + t0) * Kq;
     const float* v = a.v + (bh * a.Tp + t0) * Vd;
-    const float* S = a.S + (bh * (a.N + 1) + n) * ssz;
+    const SE* S = reinterpret_cast<const SE*>(a.S) + (bh * (a.N + 1) + n) * ssz;
     if (tid < 64) {
         sG[tid] = chunk_gam(a.g, b, h, a.T, a.H, n, tid);
         sEq[tid] = expf(sG[tid]);
@@ -912,7 +994,7 @@ __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
     float* out = a.out + (bh * a.Tp + t0) * Vd;
     for (int d0 = 0; d0 < Vd; d0 += BC * NT) {
         float acc[NA][4] = {};
-        tile_gemm_nt<MF, false, NT>(RK(q, Kq, BC, Kq), RJ(S + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
+        tile_gemm_nt<MF, false, NT>(RK(q, Kq, BC, Kq), SJ(S + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
         tile_scale_rows<MF, NA>(acc, [&](int t) { return sEq[t]; });
         tile_gemm_nt<MF, false, NT>([&](int i, int kk) { return sA[i][kk]; }, RJ(v + d0, Vd, BC, Vd - d0), BC,
                                     sStage, acc);
@@ -950,16 +1032,20 @@ __global__ __launch_bounds__(256) void bw_out_kernel(OutArgs a) {
 struct ChunkGradArgs {
     const float *q, *k, *v, *dO;  // head-major [B*H, Tp, Kq | Vd]
     const float* g;               // [B, T, H]
-    const float *S, *D;           // [B*H, N+1, Kq, Vd]
+    const float *S, *D;           // [B*H, N+1, Kq, Vd]: fp32, or bf16_t with sbf
     float *dq, *dk, *dv;          // head-major
     int B, T, Tp, H, Kq, Vd, N;
     float scale;
+    int sbf;                      // matrix-core form: S and D hold bf16 states
 };
 
-template <bool MF, bool V4>
+template <bool MF, bool V4, bool SB>
 __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     using RK = std::conditional_t<V4, RowsK4, RowsK>;  // 16-byte row loads when aligned
     using RJ = std::conditional_t<V4, RowsJ4, RowsJ>;
+    using SK = StateRowsK<SB, V4>;  // the states' rows
+    using SJ = StateRowsJ<SB, V4>;
+    using SE = std::conditional_t<SB, bf16_t, float>;
     __shared__ float sA[BC][BC + 1], sB[BC][BC + 1];
     // Output tiles of 64 NT columns: on the matrix cores two at a time, so that
     // each row block a product reads (dO, v, k, and the other operands' rows)
@@ -976,8 +1062,8 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     const float* k = a.k + (bh * a.Tp + t0) * Kq;
     const float* v = a.v + (bh * a.Tp + t0) * Vd;
     const float* dO = a.dO + (bh * a.Tp + t0) * Vd;
-    const float* S = a.S + (bh * (a.N + 1) + n) * ssz;
-    const float* D = a.D + (bh * (a.N + 1) + n + 1) * ssz;
+    const SE* S = reinterpret_cast<const SE*>(a.S) + (bh * (a.N + 1) + n) * ssz;
+    const SE* D = reinterpret_cast<const SE*>(a.D) + (bh * (a.N + 1) + n + 1) * ssz;
     if (tid < 64) {
         const float G = chunk_gam(a.g, b, h, a.T, a.H, n, tid);
         sG[tid] = G;
@@ -988,7 +1074,7 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     for (int d0 = 0; d0 < Kq; d0 += BC * NT) {
         // dq = scale (e^{G_t} dO_t S_n^T + B k)
         float acc[NA][4] = {};
-        tile_gemm_nt<MF, true, NT>(RK(dO, Vd, BC, Vd), RK(S + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
+        tile_gemm_nt<MF, true, NT>(RK(dO, Vd, BC, Vd), SK(S + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
         tile_scale_rows<MF, NA>(acc, [&](int t) { return expf(sG[t]); });
         tile_gemm_nt<MF, false, NT>([&](int i, int kk) { return sB[i][kk]; }, RJ(k + d0, Kq, BC, Kq - d0), BC, sStage,
                              acc);
@@ -998,7 +1084,7 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
         for (int x = 0; x < NA; x++)
 #pragma unroll
             for (int y = 0; y < 4; y++) acc[x][y] = 0.f;
-        tile_gemm_nt<MF, true, NT>(RK(v, Vd, BC, Vd), RK(D + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
+        tile_gemm_nt<MF, true, NT>(RK(v, Vd, BC, Vd), SK(D + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
         tile_scale_rows<MF, NA>(acc, [&](int t) { return expf(sG[BC - 1] - sG[t]); });
         tile_gemm_nt<MF, false, NT>([&](int i, int kk) { return sc * sB[kk][i]; }, RJ(q + d0, Kq, BC, Kq - d0), BC,
                              sStage, acc);
@@ -1007,7 +1093,7 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     for (int d0 = 0; d0 < Vd; d0 += BC * NT) {
         // dv = e^{G_last - G_s} k_s D_{n+1} + scale A^T dO
         float acc[NA][4] = {};
-        tile_gemm_nt<MF, false, NT>(RK(k, Kq, BC, Kq), RJ(D + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
+        tile_gemm_nt<MF, false, NT>(RK(k, Kq, BC, Kq), SJ(D + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
         tile_scale_rows<MF, NA>(acc, [&](int t) { return expf(sG[BC - 1] - sG[t]); });
         tile_gemm_nt<MF, false, NT>([&](int i, int kk) { return sc * sA[kk][i]; }, RJ(dO + d0, Vd, BC, Vd - d0), BC,
                              sStage, acc);
@@ -2071,11 +2157,13 @@ void launch_chunk_grad(const ChunkGradArgs& a, bool mfma, hipStream_t stream) {
     const bool v4 = a.Kq % 4 == 0 && a.Vd % 4 == 0;
     const dim3 grid(a.N, a.H, a.B);
     if (mfma && v4)
-        hipLaunchKernelGGL((bw_chunk_kernel<true, true>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((a.sbf ? bw_chunk_kernel<true, true, true> : bw_chunk_kernel<true, true, false>), grid,
+                           dim3(256), 0, stream, a);
     else if (mfma)
-        hipLaunchKernelGGL((bw_chunk_kernel<true, false>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((a.sbf ? bw_chunk_kernel<true, false, true> : bw_chunk_kernel<true, false, false>), grid,
+                           dim3(256), 0, stream, a);
     else
-        hipLaunchKernelGGL((bw_chunk_kernel<false, false>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((bw_chunk_kernel<false, false, false>), grid, dim3(256), 0, stream, a);
 }
 
 }  // namespace
@@ -2100,6 +2188,7 @@ int launch_chunk_pass(const ChunkPassParams& p, hipStream_t stream) {
     sa.Vd = p.Vd;
     sa.N = N;
     sa.scale = 1.f;
+    sa.sbf = p.mfma && p.sbf16;
     launch_state_scan<false>(sa, p.mfma, stream);
     OutArgs oa{};
     oa.q = p.q;
@@ -2118,14 +2207,18 @@ int launch_chunk_pass(const ChunkPassParams& p, hipStream_t stream) {
     oa.Vd = p.Vd;
     oa.N = N;
     oa.scale = p.scale;
+    oa.sbf = p.mfma && p.sbf16;
     // rows and states 16-byte aligned (workspace buffers, rows of Kq and Vd floats)
     const bool v4 = p.Kq % 4 == 0 && p.Vd % 4 == 0;
+    const dim3 og(N, p.H, p.B);
     if (p.mfma && v4)
-        hipLaunchKernelGGL((bw_out_kernel<true, true>), dim3(N, p.H, p.B), dim3(256), 0, stream, oa);
+        hipLaunchKernelGGL((oa.sbf ? bw_out_kernel<true, true, true> : bw_out_kernel<true, true, false>), og, dim3(256),
+                           0, stream, oa);
     else if (p.mfma)
-        hipLaunchKernelGGL((bw_out_kernel<true, false>), dim3(N, p.H, p.B), dim3(256), 0, stream, oa);
+        hipLaunchKernelGGL((oa.sbf ? bw_out_kernel<true, false, true> : bw_out_kernel<true, false, false>), og,
+                           dim3(256), 0, stream, oa);
     else
-        hipLaunchKernelGGL((bw_out_kernel<false, false>), dim3(N, p.H, p.B), dim3(256), 0, stream, oa);
+        hipLaunchKernelGGL((bw_out_kernel<false, false, false>), og, dim3(256), 0, stream, oa);
     return 0;
 }
 
@@ -2201,7 +2294,11 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     // every chunk of both passes, the pass-1 output and the slot weights
     if (launch_general_clock_write(p.delta, p.clock0, p.beta, B, T, Tp, H, M, ws.lam, ws.w, ws.cs, ws.sn, stream) != 0)
         return -1;
+    // The stored states and state cotangents of bf16 calls are bf16, as the
+    // reference stores its chunk states and their cotangents (the recurrence
+    // itself runs in fp32 registers; ops/chunk_h.py:212-214, 329-331).
     StateScanArgs f1{};
+    f1.sbf = bf;
     f1.a = ws.kh;
     f1.b = ws.w;
     f1.g = p.g;
@@ -2224,6 +2321,7 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     p1.states = ws.sk;
     p1.out = ws.raw;
     p1.mfma = bf;
+    p1.sbf16 = bf;
     p1.B = B;
     p1.T = T;
     p1.Tp = Tp;
@@ -2276,6 +2374,7 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     s2.x_out = p.dh0_v;
     launch_state_scan<true>(s2, bf, stream);
     ChunkGradArgs c2{};
+    c2.sbf = bf;
     c2.q = ws.wts;
     c2.k = ws.w;
     c2.v = ws.vh;

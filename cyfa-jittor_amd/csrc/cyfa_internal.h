@@ -266,6 +266,7 @@ struct ChunkPassParams {
     void* out_bthd;          // nullable [B, T, H, Vd], bf16 when bf16 else fp32
     int bf16;                // round the output to bf16 (the input dtype's cast)
     int mfma;                // tile products on the matrix cores (split bf16 operands, ~16 bits)
+    int sbf16;               // with mfma: states stored as bf16 (the workspace then holds bf16_t)
     int B, T, Tp, H, Kq, Vd;
     float scale;
 };
