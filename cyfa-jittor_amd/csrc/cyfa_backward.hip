@@ -100,15 +100,16 @@ __device__ __forceinline__ float chunk_gam(const float* g, int b, int h, int T, 
 // Rows of x [B, T, H, D] into head-major fp32 [B*H, Tp, D]: with a norm
 // weight the normalised row x rs w (ops/qk_norm.py:206-233, unrounded) and rs
 // per row; without, x itself; x == nullptr or t >= T gives zeros. One wave per row.
-template <bool BF>
+// O: the rows' element type (bf16_t only without w: a bf16 x's layout change).
+template <bool BF, class O = float>
 __global__ __launch_bounds__(256) void bw_rows_kernel(const void* x, const float* w, float eps, int B, int T, int Tp,
-                                                      int H, int D, float* out, float* rs_out) {
+                                                      int H, int D, O* out, float* rs_out) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= B * H * Tp) return;
     const int t = row % Tp, bh = row / Tp, b = bh / H, h = bh % H;
-    float* dst = out + (size_t)row * D;
+    O* dst = out + (size_t)row * D;
     if (!x || t >= T) {
-        for (int i = lane; i < D; i += 64) dst[i] = 0.f;
+        for (int i = lane; i < D; i += 64) dst[i] = (O)0.f;
         if (rs_out && lane == 0) rs_out[row] = 0.f;
         return;
     }
@@ -135,11 +136,14 @@ __global__ __launch_bounds__(256) void bw_rows_kernel(const void* x, const float
             o = float4{v[0] * rs * wv.x, v[1] * rs * wv.y, v[2] * rs * wv.z, v[3] * rs * wv.w};
             if (rs_out && lane == 0) rs_out[row] = rs;
         }
-        *reinterpret_cast<float4*>(dst + 4 * lane) = o;
+        if constexpr (std::is_same_v<O, bf16_t>)
+            *reinterpret_cast<bf16x4*>(dst + 4 * lane) = bf16x4{(bf16_t)o.x, (bf16_t)o.y, (bf16_t)o.z, (bf16_t)o.w};
+        else
+            *reinterpret_cast<float4*>(dst + 4 * lane) = o;
         return;
     }
     if (!w) {
-        for (int i = lane; i < D; i += 64) dst[i] = bw_ld<BF>(x, src + i);
+        for (int i = lane; i < D; i += 64) dst[i] = (O)bw_ld<BF>(x, src + i);
         return;
     }
     float ss = 0.f;
@@ -214,6 +218,7 @@ struct StateScanArgs {
     int B, T, Tp, H, Kq, Vd, N;
     float scale;
     int sbf;             // matrix-core form: xs and S hold bf16 (bf16_t) states
+    int bbf;             // matrix-core form: b holds bf16 (bf16_t) rows
 };
 
 template <bool BWD>
@@ -378,9 +383,10 @@ __device__ __forceinline__ void split_bf16x8(const float* v, bf16x8& hi, bf16x8&
     }
 }
 
-template <bool BWD, int T2, bool SB>
+template <bool BWD, int T2, bool SB, bool BB>
 __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) {
     using SE = std::conditional_t<SB, bf16_t, float>;  // the stored states' element
+    using BE = std::conditional_t<BB, bf16_t, float>;  // b's element
     static_assert(SCAN_ROWS == 32 && BW_TILE == 32 && (T2 == 1 || T2 == 2), "32 x 32 bnd tiles");
     constexpr int TS = 32 * T2;     // tile side
     constexpr int TPT = BC / (256 / TS);  // tokens per staging thread
@@ -403,7 +409,7 @@ __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) 
     SE* xs = reinterpret_cast<SE*>(p.xs) + bh * (N + 1) * ssz;
     const SE* Sx = reinterpret_cast<const SE*>(p.S);
     const float* A = p.a + bh * p.Tp * Kq;
-    const float* Bm = p.b + bh * p.Tp * Vd;
+    const BE* Bm = reinterpret_cast<const BE*>(p.b) + bh * p.Tp * Vd;
     const int wr = 16 * T2 * (wv >> 1), wc = 16 * T2 * (wv & 1);  // the wave's quarter
     bool ok[T2][T2][4];
     uint32_t off[T2][T2][4];
@@ -459,7 +465,8 @@ __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) 
         for (int i = 0; i < TPT; i++) {
             const uint32_t t = TPT * sq + i;
             ra[i] = bw_load(rA, (t * (uint32_t)Kq + (uint32_t)(r0 + sr)) * 4u, r0 + sr < Kq);
-            rb[i] = bw_load(rBm, (t * (uint32_t)Vd + (uint32_t)(c0 + sr)) * 4u, c0 + sr < Vd);
+            rb[i] = BB ? bw_load_h(rBm, (t * (uint32_t)Vd + (uint32_t)(c0 + sr)) * 2u, c0 + sr < Vd)
+                       : bw_load(rBm, (t * (uint32_t)Vd + (uint32_t)(c0 + sr)) * 4u, c0 + sr < Vd);
         }
         rg = bw_load(rgt, (((uint32_t)b * (uint32_t)p.T + (uint32_t)(t0 + lane)) * (uint32_t)p.H + (uint32_t)h) * 4u,
                      t0 + lane < p.T);
@@ -557,17 +564,27 @@ __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) 
 // Launches the scan over a [Kq, Vd] state (grid: the FMA form's 32 x 32
 // tiles): the matrix-core form for bf16 operands, with 64 x 64 tiles when
 // they still give a workgroup per compute unit.
+template <bool BWD, int T2>
+void launch_scan_mf(const StateScanArgs& a, dim3 grid, hipStream_t stream) {
+    if (a.sbf && a.bbf)
+        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, T2, true, true>), grid, dim3(256), 0, stream, a);
+    else if (a.sbf)
+        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, T2, true, false>), grid, dim3(256), 0, stream, a);
+    else if (a.bbf)
+        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, T2, false, true>), grid, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, T2, false, false>), grid, dim3(256), 0, stream, a);
+}
+
 template <bool BWD>
 void launch_state_scan(const StateScanArgs& a, bool mfma, hipStream_t stream) {
     const dim3 g32((a.Vd + 31) / 32, (a.Kq + 31) / 32, a.B * a.H), g64((a.Vd + 63) / 64, (a.Kq + 63) / 64, a.B * a.H);
     if (!mfma)
         hipLaunchKernelGGL(bw_state_scan_kernel<BWD>, g32, dim3(256), 0, stream, a);
     else if ((long long)g64.x * g64.y * g64.z >= device_cu_count())
-        hipLaunchKernelGGL((a.sbf ? bw_state_scan_mf_kernel<BWD, 2, true> : bw_state_scan_mf_kernel<BWD, 2, false>), g64,
-                           dim3(256), 0, stream, a);
+        launch_scan_mf<BWD, 2>(a, g64, stream);
     else
-        hipLaunchKernelGGL((a.sbf ? bw_state_scan_mf_kernel<BWD, 1, true> : bw_state_scan_mf_kernel<BWD, 1, false>), g32,
-                           dim3(256), 0, stream, a);
+        launch_scan_mf<BWD, 1>(a, g32, stream);
 }
 
 // Tile GEMMs of the chunk kernels: a 64 x 64 output tile (rows = the chunk's
@@ -935,10 +952,10 @@ __device__ __forceinline__ void tile_gemm_nt(FA fa, FB fb, int Kd, unsigned char
 
 // Masked, decayed scores of one chunk into P: P[t][s] = [s <= t] e^{G_t - G_s}
 // sum_j X_t[j] Y_s[j] (X, Y: the chunk's 64 rows, D wide), as one tile GEMM.
-template <bool MF, bool V4>
-__device__ __forceinline__ void chunk_scores(const float* X, const float* Y, int D, const float* sG,
-                                             unsigned char* stage, float (*P)[BC + 1]) {
-    using RK = std::conditional_t<V4, RowsK4, RowsK>;
+template <bool MF, bool V4, class E>
+__device__ __forceinline__ void chunk_scores(const E* X, const E* Y, int D, const float* sG, unsigned char* stage,
+                                             float (*P)[BC + 1]) {
+    using RK = StateRowsK<std::is_same_v<E, bf16_t>, V4>;  // fp32 or bf16 rows
     float acc[4][4] = {};
     tile_gemm<MF, true>(RK(X, D, BC, D), RK(Y, D, BC, D), D, stage, acc);
 #pragma unroll
@@ -1037,15 +1054,19 @@ struct ChunkGradArgs {
     int B, T, Tp, H, Kq, Vd, N;
     float scale;
     int sbf;                      // matrix-core form: S and D hold bf16 states
+    int rbf;                      // matrix-core form: v and dO hold bf16 rows
 };
 
-template <bool MF, bool V4, bool SB>
+template <bool MF, bool V4, bool SB, bool RB>
 __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     using RK = std::conditional_t<V4, RowsK4, RowsK>;  // 16-byte row loads when aligned
     using RJ = std::conditional_t<V4, RowsJ4, RowsJ>;
     using SK = StateRowsK<SB, V4>;  // the states' rows
     using SJ = StateRowsJ<SB, V4>;
     using SE = std::conditional_t<SB, bf16_t, float>;
+    using VK = StateRowsK<RB, V4>;  // v's and dO's rows
+    using VJ = StateRowsJ<RB, V4>;
+    using VE = std::conditional_t<RB, bf16_t, float>;
     __shared__ float sA[BC][BC + 1], sB[BC][BC + 1];
     // Output tiles of 64 NT columns: on the matrix cores two at a time, so that
     // each row block a product reads (dO, v, k, and the other operands' rows)
@@ -1060,8 +1081,8 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     const size_t bh = (size_t)b * a.H + h, ssz = (size_t)Kq * Vd;
     const float* q = a.q + (bh * a.Tp + t0) * Kq;
     const float* k = a.k + (bh * a.Tp + t0) * Kq;
-    const float* v = a.v + (bh * a.Tp + t0) * Vd;
-    const float* dO = a.dO + (bh * a.Tp + t0) * Vd;
+    const VE* v = reinterpret_cast<const VE*>(a.v) + (bh * a.Tp + t0) * Vd;
+    const VE* dO = reinterpret_cast<const VE*>(a.dO) + (bh * a.Tp + t0) * Vd;
     const SE* S = reinterpret_cast<const SE*>(a.S) + (bh * (a.N + 1) + n) * ssz;
     const SE* D = reinterpret_cast<const SE*>(a.D) + (bh * (a.N + 1) + n + 1) * ssz;
     if (tid < 64) {
@@ -1074,7 +1095,7 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
     for (int d0 = 0; d0 < Kq; d0 += BC * NT) {
         // dq = scale (e^{G_t} dO_t S_n^T + B k)
         float acc[NA][4] = {};
-        tile_gemm_nt<MF, true, NT>(RK(dO, Vd, BC, Vd), SK(S + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
+        tile_gemm_nt<MF, true, NT>(VK(dO, Vd, BC, Vd), SK(S + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
         tile_scale_rows<MF, NA>(acc, [&](int t) { return expf(sG[t]); });
         tile_gemm_nt<MF, false, NT>([&](int i, int kk) { return sB[i][kk]; }, RJ(k + d0, Kq, BC, Kq - d0), BC, sStage,
                              acc);
@@ -1084,7 +1105,7 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
         for (int x = 0; x < NA; x++)
 #pragma unroll
             for (int y = 0; y < 4; y++) acc[x][y] = 0.f;
-        tile_gemm_nt<MF, true, NT>(RK(v, Vd, BC, Vd), SK(D + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
+        tile_gemm_nt<MF, true, NT>(VK(v, Vd, BC, Vd), SK(D + (size_t)d0 * Vd, Vd, Kq - d0, Vd), Vd, sStage, acc);
         tile_scale_rows<MF, NA>(acc, [&](int t) { return expf(sG[BC - 1] - sG[t]); });
         tile_gemm_nt<MF, false, NT>([&](int i, int kk) { return sc * sB[kk][i]; }, RJ(q + d0, Kq, BC, Kq - d0), BC,
                              sStage, acc);
@@ -1095,7 +1116,7 @@ __global__ __launch_bounds__(256) void bw_chunk_kernel(ChunkGradArgs a) {
         float acc[NA][4] = {};
         tile_gemm_nt<MF, false, NT>(RK(k, Kq, BC, Kq), SJ(D + d0, Vd, Kq, Vd - d0), Kq, sStage, acc);
         tile_scale_rows<MF, NA>(acc, [&](int t) { return expf(sG[BC - 1] - sG[t]); });
-        tile_gemm_nt<MF, false, NT>([&](int i, int kk) { return sc * sA[kk][i]; }, RJ(dO + d0, Vd, BC, Vd - d0), BC,
+        tile_gemm_nt<MF, false, NT>([&](int i, int kk) { return sc * sA[kk][i]; }, VJ(dO + d0, Vd, BC, Vd - d0), BC,
                              sStage, acc);
         tile_store<MF, NA>(acc, a.dv + (bh * a.Tp + t0) * Vd, Vd, d0, 1.f);
     }
@@ -2156,14 +2177,19 @@ void launch_chunk_grad(const ChunkGradArgs& a, bool mfma, hipStream_t stream) {
     // rows and states 16-byte aligned (workspace buffers, rows of Kq and Vd floats)
     const bool v4 = a.Kq % 4 == 0 && a.Vd % 4 == 0;
     const dim3 grid(a.N, a.H, a.B);
-    if (mfma && v4)
-        hipLaunchKernelGGL((a.sbf ? bw_chunk_kernel<true, true, true> : bw_chunk_kernel<true, true, false>), grid,
-                           dim3(256), 0, stream, a);
+    // (the flags pair as the backward sets them: sbf for bf16 calls, rbf for pass 2's)
+    if (mfma && v4 && a.rbf)
+        hipLaunchKernelGGL((bw_chunk_kernel<true, true, true, true>), grid, dim3(256), 0, stream, a);
+    else if (mfma && v4)
+        hipLaunchKernelGGL((a.sbf ? bw_chunk_kernel<true, true, true, false> : bw_chunk_kernel<true, true, false, false>),
+                           grid, dim3(256), 0, stream, a);
+    else if (mfma && a.rbf)
+        hipLaunchKernelGGL((bw_chunk_kernel<true, false, true, true>), grid, dim3(256), 0, stream, a);
     else if (mfma)
-        hipLaunchKernelGGL((a.sbf ? bw_chunk_kernel<true, false, true> : bw_chunk_kernel<true, false, false>), grid,
-                           dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((a.sbf ? bw_chunk_kernel<true, false, true, false> : bw_chunk_kernel<true, false, false, false>),
+                           grid, dim3(256), 0, stream, a);
     else
-        hipLaunchKernelGGL((bw_chunk_kernel<false, false, false>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((bw_chunk_kernel<false, false, false, false>), grid, dim3(256), 0, stream, a);
 }
 
 }  // namespace
@@ -2280,13 +2306,17 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
 #define CYFA_BW_ROWS(BFV)                                                                                           \
     hipLaunchKernelGGL(bw_rows_kernel<BFV>, rb, blk, 0, stream, p.q, p.q_w, p.q_eps, B, T, Tp, H, K, ws.qh, ws.rq); \
     hipLaunchKernelGGL(bw_rows_kernel<BFV>, rb, blk, 0, stream, p.k, p.k_w, p.k_eps, B, T, Tp, H, K, ws.kh, ws.rk); \
-    hipLaunchKernelGGL(bw_rows_kernel<BFV>, rb, blk, 0, stream, p.v, (const float*)nullptr, 0.f, B, T, Tp, H, V,   \
-                       ws.vh, (float*)nullptr);                                                                    \
-    hipLaunchKernelGGL(bw_rows_kernel<BFV>, rb, blk, 0, stream, p.d_o, (const float*)nullptr, 0.f, B, T, Tp, H, V, \
-                       ws.dO, (float*)nullptr);
+    hipLaunchKernelGGL((bw_rows_kernel<BFV, RowT>), rb, blk, 0, stream, p.v, (const float*)nullptr, 0.f, B, T, Tp, H, \
+                       V, reinterpret_cast<RowT*>(ws.vh), (float*)nullptr);                                        \
+    hipLaunchKernelGGL((bw_rows_kernel<BFV, RowT>), rb, blk, 0, stream, p.d_o, (const float*)nullptr, 0.f, B, T, Tp, H, \
+                       V, reinterpret_cast<RowT*>(ws.dO), (float*)nullptr);
+    // v and dO of bf16 calls stay bf16 in the head-major rows (exact): the
+    // pass-2 scans and chunk kernels read half the bytes.
     if (bf) {
+        using RowT = bf16_t;
         CYFA_BW_ROWS(true)
     } else {
+        using RowT = float;
         CYFA_BW_ROWS(false)
     }
 #undef CYFA_BW_ROWS
@@ -2360,6 +2390,7 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     f2.b = ws.vh;
     f2.x0 = p.h0_v;
     f2.xs = ws.sv;
+    f2.bbf = bf;  // v's rows
     f2.Kq = M;
     f2.Vd = V;
     launch_state_scan<false>(f2, bf, stream);
@@ -2375,6 +2406,7 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     launch_state_scan<true>(s2, bf, stream);
     ChunkGradArgs c2{};
     c2.sbf = bf;
+    c2.rbf = bf;  // v's and dO's rows
     c2.q = ws.wts;
     c2.k = ws.w;
     c2.v = ws.vh;
@@ -2431,6 +2463,7 @@ int launch_chunk_bwd(const BwdParams& p, hipStream_t stream) {
     s1.scale = p.scale;
     launch_state_scan<true>(s1, bf, stream);
     ChunkGradArgs c1 = c2;
+    c1.rbf = 0;  // pass 1's rows (the write vector, draw) are fp32
     c1.q = ws.qh;
     c1.k = ws.kh;
     c1.v = ws.w;
