@@ -384,16 +384,20 @@ __device__ __forceinline__ void split_bf16x8(const float* v, bf16x8& hi, bf16x8&
 }
 
 template <bool BWD, int T2, bool SB, bool BB>
-__global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) {
+__global__ __launch_bounds__(T2 == 2 ? 512 : 256) void bw_state_scan_mf_kernel(StateScanArgs p) {
     using SE = std::conditional_t<SB, bf16_t, float>;  // the stored states' element
     using BE = std::conditional_t<BB, bf16_t, float>;  // b's element
     static_assert(SCAN_ROWS == 32 && BW_TILE == 32 && (T2 == 1 || T2 == 2), "32 x 32 bnd tiles");
     constexpr int TS = 32 * T2;     // tile side
-    constexpr int TPT = BC / (256 / TS);  // tokens per staging thread
+    // Waves: 8 for 64 x 64 tiles (one workgroup per CU at configuration 3's
+    // shapes, so that two waves share each SIMD), 4 for 32 x 32; wave w holds
+    // the 16 x 16 T2 block of rows 16 (w / 2) and columns 16 T2 (w % 2).
+    constexpr int NTH = T2 == 2 ? 512 : 256, NWV = NTH / 64, IB = 1;
+    constexpr int TPT = BC / (NTH / TS);  // tokens per staging thread
     __shared__ __align__(16) bf16_t sAh[TS][SCAN_LDT], sAl[TS][SCAN_LDT];
     __shared__ __align__(16) bf16_t sBh[TS][SCAN_LDT], sBl[TS][SCAN_LDT];
     __shared__ float sF[BC];
-    __shared__ float sRed[4];
+    __shared__ float sRed[NWV];
     __shared__ float sEl;
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lg = lane >> 4;
@@ -401,22 +405,22 @@ __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) 
     const int b = bhi / p.H, h = bhi % p.H;
     const int Kq = p.Kq, Vd = p.Vd, N = p.N;
     // bnd tiles of 32 x 32: nx across Vd, ny down Kq; this workgroup's (T2 = 1)
-    // or this wave's (T2 = 2)
+    // or this wave's and its partner's, wave w ^ 2 (T2 = 2)
     const int nx = (Vd + 31) / 32, ny = (Kq + 31) / 32, nt = nx * ny;
-    const int ty = T2 == 1 ? (int)blockIdx.y : 2 * (int)blockIdx.y + (wv >> 1);
+    const int ty = T2 == 1 ? (int)blockIdx.y : 2 * (int)blockIdx.y + (wv >> 2);
     const int tx = T2 == 1 ? (int)blockIdx.x : 2 * (int)blockIdx.x + (wv & 1);
     const size_t bh = bhi, ssz = (size_t)Kq * Vd;
     SE* xs = reinterpret_cast<SE*>(p.xs) + bh * (N + 1) * ssz;
     const SE* Sx = reinterpret_cast<const SE*>(p.S);
     const float* A = p.a + bh * p.Tp * Kq;
     const BE* Bm = reinterpret_cast<const BE*>(p.b) + bh * p.Tp * Vd;
-    const int wr = 16 * T2 * (wv >> 1), wc = 16 * T2 * (wv & 1);  // the wave's quarter
-    bool ok[T2][T2][4];
-    uint32_t off[T2][T2][4];
-    f32x4 x[T2][T2];
+    const int wr = 16 * IB * (wv >> 1), wc = 16 * T2 * (wv & 1);  // the wave's block
+    bool ok[IB][T2][4];
+    uint32_t off[IB][T2][4];
+    f32x4 x[IB][T2];
     const bw_rsrc_t rx0 = bw_rsrc(p.x0 ? p.x0 + bh * ssz : nullptr, p.x0 ? ssz : 0);
 #pragma unroll
-    for (int ib = 0; ib < T2; ib++)
+    for (int ib = 0; ib < IB; ib++)
 #pragma unroll
         for (int jb = 0; jb < T2; jb++)
 #pragma unroll
@@ -426,11 +430,11 @@ __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) 
                 off[ib][jb][i] = ((uint32_t)xr * (uint32_t)Vd + (uint32_t)xc) * 4u;
                 x[ib][jb][i] = bw_load(rx0, off[ib][jb][i], ok[ib][jb][i]);
             }
-    float sv[T2][T2][4] = {};
+    float sv[IB][T2][4] = {};
     const auto fetch_state = [&](int n) {
         const bw_rsrc_t rs = bw_rsrc(Sx + (bh * (N + 1) + n) * ssz, ssz);
 #pragma unroll
-        for (int ib = 0; ib < T2; ib++)
+        for (int ib = 0; ib < IB; ib++)
 #pragma unroll
             for (int jb = 0; jb < T2; jb++)
 #pragma unroll
@@ -442,7 +446,7 @@ __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) 
         const bw_rsrc_t rs = bw_rsrc(xs + (size_t)n * ssz, ssz);
         float dot = 0.f;
 #pragma unroll
-        for (int ib = 0; ib < T2; ib++)
+        for (int ib = 0; ib < IB; ib++)
 #pragma unroll
             for (int jb = 0; jb < T2; jb++)
 #pragma unroll
@@ -483,7 +487,7 @@ __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) 
         float wsum = 0.f;
         if constexpr (BWD) {
             wsum = bw_wave_sum(dot);
-            if (T2 == 1 && lane == 0) sRed[wv] = wsum;
+            if (lane == 0) sRed[wv] = wsum;
         }
         if (wv == 0) {  // G: the in-chunk inclusive cumsum of the prefetched gate
             const float G = bw_wave_scan(rg);
@@ -515,20 +519,21 @@ __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) 
         if constexpr (BWD) {
             if (T2 == 1 && tid == 0)
                 p.bnd[(bh * nt + ty * nx + tx) * N + n] = (sRed[0] + sRed[1]) + (sRed[2] + sRed[3]);
-            if (T2 == 2 && lane == 0 && ty < ny && tx < nx) p.bnd[(bh * nt + ty * nx + tx) * N + n] = wsum;
+            if (T2 == 2 && lane == 0 && (wv & 2) == 0 && ty < ny && tx < nx)  // the tile's two waves
+                p.bnd[(bh * nt + ty * nx + tx) * N + n] = sRed[wv] + sRed[wv + 2];
         }
         const float el = sEl;
 #pragma unroll
-        for (int ib = 0; ib < T2; ib++)
+        for (int ib = 0; ib < IB; ib++)
 #pragma unroll
             for (int jb = 0; jb < T2; jb++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) x[ib][jb][i] *= el;
 #pragma unroll
         for (int s = 0; s < BC / 32; s++) {
-            bf16x8 ah[T2], al[T2], bh8[T2], bl8[T2];
+            bf16x8 ah[IB], al[IB], bh8[T2], bl8[T2];
 #pragma unroll
-            for (int ib = 0; ib < T2; ib++) {
+            for (int ib = 0; ib < IB; ib++) {
                 ah[ib] = *reinterpret_cast<const bf16x8*>(&sAh[wr + 16 * ib + lr][32 * s + 8 * lg]);
                 al[ib] = *reinterpret_cast<const bf16x8*>(&sAl[wr + 16 * ib + lr][32 * s + 8 * lg]);
             }
@@ -538,7 +543,7 @@ __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) 
                 bl8[jb] = *reinterpret_cast<const bf16x8*>(&sBl[wc + 16 * jb + lr][32 * s + 8 * lg]);
             }
 #pragma unroll
-            for (int ib = 0; ib < T2; ib++)
+            for (int ib = 0; ib < IB; ib++)
 #pragma unroll
                 for (int jb = 0; jb < T2; jb++) {
                     x[ib][jb] = mfma_bf16(al[ib], bh8[jb], x[ib][jb]);
@@ -554,7 +559,7 @@ __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) 
     keep(BWD ? 0 : N);
     const bw_rsrc_t rxo = bw_rsrc(p.x_out ? p.x_out + bh * ssz : nullptr, p.x_out ? ssz : 0);
 #pragma unroll
-    for (int ib = 0; ib < T2; ib++)
+    for (int ib = 0; ib < IB; ib++)
 #pragma unroll
         for (int jb = 0; jb < T2; jb++)
 #pragma unroll
@@ -566,14 +571,15 @@ __global__ __launch_bounds__(256) void bw_state_scan_mf_kernel(StateScanArgs p) 
 // they still give a workgroup per compute unit.
 template <bool BWD, int T2>
 void launch_scan_mf(const StateScanArgs& a, dim3 grid, hipStream_t stream) {
+    const dim3 blk(T2 == 2 ? 512 : 256);
     if (a.sbf && a.bbf)
-        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, T2, true, true>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, T2, true, true>), grid, blk, 0, stream, a);
     else if (a.sbf)
-        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, T2, true, false>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, T2, true, false>), grid, blk, 0, stream, a);
     else if (a.bbf)
-        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, T2, false, true>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, T2, false, true>), grid, blk, 0, stream, a);
     else
-        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, T2, false, false>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((bw_state_scan_mf_kernel<BWD, T2, false, false>), grid, blk, 0, stream, a);
 }
 
 template <bool BWD>
